@@ -1,0 +1,242 @@
+#!/usr/bin/env python3
+"""Benchmark of the Leech-lattice quantization hot path on one MI355X.
+
+Headline (BASELINE.json metric): atoms/s of the fused per-step requantize of a
+Pollux-1152 layer (QKV 3456x1152, O 1152x1152, up 4608x1152,
+down 1152x4608 in torch (out, in) layout; fp32 N(0, 0.02) draws rounded to
+bf16 "master weights" and held as fp32 latents).  One step = for each of the
+four latents: row scale -> NN-B quantize -> 18-bit pack -> reconstructed fp32
+weight (pollux.py:874-884 + castor.pack_indices), inputs resident in HBM.
+
+The JSON line also carries
+  roofline      the scoring kernel (nn_kernel) against dense bf16 MFMA peak:
+                algorithmic flops 2*24*196,560 per atom over its HIP-event
+                kernel time inside the timed region;
+  cpu_baseline  the reference's own CPU path (autocast-bf16 matmul + max,
+                castor.py:544-557, plus its row scale and pack) restated with
+                the same torch ops (oracle/torch_ref.py) on a bounded sample
+                of the same workload, on this host's cores;
+  extras        pack / unpack / dequant HBM GB/s at BASELINE config-4 scale.
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "atoms/sec Leech NN quantize (+MFMA util %); dequant-GEMV GB/s at d=1920"
+FLOP_PER_ATOM = 2 * 24 * 196_560  # 9,434,880 algorithmic flops (origin free, K padding not counted)
+PEAK_BF16_FLOPS = 2.5e15  # MI355X dense bf16 MFMA
+PEAK_HBM_BPS = 8.0e12  # MI355X HBM3E
+C2_SHAPES = [(3456, 1152), (1152, 1152), (4608, 1152), (1152, 4608)]
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def make_c2(device, seed=2024):
+    import torch
+
+    g = torch.Generator().manual_seed(seed)
+    mats = []
+    for r, c in C2_SHAPES:
+        w = (torch.randn(r, c, generator=g) * 0.02).to(torch.bfloat16).float()
+        mats.append(w.to(device))
+    return mats
+
+
+def time_gpu(fn, iters, warmup):
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(iters):
+        fn()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / iters
+
+
+def cpu_baseline(mats, target_atoms):
+    """The reference's CPU path on the first rows of the QKV latent (a bounded sample)."""
+    import torch
+
+    from oracle import packing, torch_ref
+
+    cores = os.cpu_count() or 1
+    torch.set_num_threads(cores)
+    w = mats[0].cpu()
+    rows = max(1, target_atoms // (w.shape[1] // 24))
+    sample = w[:rows]
+    t0 = time.perf_counter()
+    x, sigma = torch_ref.lattice_input(sample)
+    idx = torch_ref.nn_b_indices(x)
+    packing.pack(idx.numpy())
+    center = torch_ref.codebook_tensor()[idx].reshape(sample.shape)
+    torch_ref.reconstruct(center, sigma)
+    dt = time.perf_counter() - t0
+    n = sample.numel() // 24
+    return {
+        "value": n / dt,
+        "unit": "atoms/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": f"first {rows} rows ({n} atoms) of the config-2 QKV latent: row scale, "
+        f"autocast-bf16 matmul + max (castor.py:549-557, chunk 4096), pack; {dt:.1f} s",
+    }
+
+
+def extras(device, iters=20):
+    import torch
+
+    from pollux_amd import castor, dequantize_h24
+
+    out = {}
+    n = 16_777_200  # config 4: 209,715 rows of 1920 = 80 atoms/row
+    g = torch.Generator(device=device).manual_seed(7)
+    idx = torch.randint(0, 196561, (n,), generator=g, device=device, dtype=torch.int64)
+    packed = castor.pack_indices(idx)
+    t = time_gpu(lambda: castor.pack_indices(idx), iters, 3)
+    out["pack_GBps"] = (8 + 2.25) * n / t / 1e9
+    t = time_gpu(lambda: castor.unpack_indices(packed, n), iters, 3)
+    out["unpack_GBps"] = (2.25 + 8) * n / t / 1e9
+    rows, cols = 209_715, 1920
+    sig = (torch.rand(rows, generator=g, device=device) * 0.045 + 0.005).half()
+    t = time_gpu(lambda: dequantize_h24(packed, sig, rows, cols), iters, 3)
+    out["dequant_GBps"] = (2.25 * n + 48 * n + 2 * rows) / t / 1e9
+    out["hbm_peak_GBps"] = PEAK_HBM_BPS / 1e9
+    for k in ("pack", "unpack", "dequant"):
+        out[f"{k}_hbm_frac"] = out[f"{k}_GBps"] * 1e9 / PEAK_HBM_BPS
+    out["scale"] = "16,777,200 indices / atoms (BASELINE config 4 size), rows of 1920"
+    return out
+
+
+def traffic_from_profiles():
+    p = ROOT / "profiles" / "nn_kernel_c2_traffic.json"
+    if p.exists():
+        try:
+            return json.loads(p.read_text()).get("hbm_bytes_per_launch")
+        except (ValueError, OSError):
+            return None
+    return None
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--cpu-atoms", type=int, default=24_576, help="CPU baseline sample size (atoms)")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-extras", action="store_true")
+    ap.add_argument("--mode", default="bf16", choices=["bf16", "fp32"])
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print(
+            "bench.py measures one GPU only: this build's hot path (Leech quantize / pack / dequant) is "
+            "benchmarked per device; multi-GPU sharding is described in DESIGN.md, not run.",
+            file=sys.stderr,
+        )
+        return 2
+
+    import torch
+
+    from pollux_amd import _lib, castor
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm device", file=sys.stderr)
+        return 2
+    dev = torch.device("cuda:0")
+    lib = _lib.lib()
+    with torch.cuda.device(dev):
+        _lib.check(lib.plx_device_init(), "plx_device_init")
+
+    mats = make_c2(dev)
+    atoms = sum(r * c // 24 for r, c in C2_SHAPES)
+
+    def step():
+        for w in mats:
+            castor.requantize_h24(w, mode=args.mode)
+
+    log(f"[bench] warmup {args.warmup} steps, workload config 2 ({atoms} atoms/step)")
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    _lib.check(lib.plx_profile_begin(), "plx_profile_begin")
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    import ctypes
+
+    tot_ms, launches = ctypes.c_double(), ctypes.c_int64()
+    _lib.check(lib.plx_profile_end(ctypes.byref(tot_ms), ctypes.byref(launches)), "plx_profile_end")
+    ms_per_step = elapsed / args.steps * 1e3
+    value = atoms * args.steps / elapsed
+    log(f"[bench] timed {args.steps} steps: {ms_per_step:.3f} ms/step, {value:.4g} atoms/s")
+
+    kernel_s = tot_ms.value / 1e3
+    flops = FLOP_PER_ATOM * atoms * args.steps
+    achieved = flops / kernel_s if kernel_s > 0 else 0.0
+    roofline = {
+        "bound": "mfma",
+        "achieved": achieved / 1e12,
+        "peak": PEAK_BF16_FLOPS / 1e12,
+        "unit": "TFLOP/s",
+        "frac": achieved / PEAK_BF16_FLOPS,
+        "traffic": traffic_from_profiles(),
+        "kernel": "nn_kernel (bf16 16x16x32 MFMA scoring + running max)",
+        "kernel_launches": int(launches.value),
+        "kernel_avg_ms": tot_ms.value / max(1, launches.value),
+        "flop_per_atom": FLOP_PER_ATOM,
+        "mfma_issue_frac": achieved * 32 / 24 / PEAK_BF16_FLOPS,
+    }
+
+    result = {
+        "metric": METRIC,
+        "value": value,
+        "unit": "atoms/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": "BASELINE config 2: Pollux-1152 single-layer requantize (row scale + NN-B quantize + "
+            "18-bit pack + reconstructed weight) of QKV 3456x1152, O 1152x1152, up 4608x1152, down 1152x4608",
+            "atoms_per_step": atoms,
+            "nn_mode": "NN-B (bf16 scores)" if args.mode == "bf16" else "NN-T (fp32 scores)",
+            "seed": 2024,
+        },
+        "roofline": roofline,
+    }
+    if not args.no_extras:
+        log("[bench] extras: pack / unpack / dequant at config-4 scale")
+        result["extras"] = extras(dev)
+    if not args.no_cpu_baseline:
+        log(f"[bench] CPU baseline on {args.cpu_atoms} atoms")
+        result["cpu_baseline"] = cpu_baseline(mats, args.cpu_atoms)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,147 @@
+/*
+ * pollux_amd.h -- C ABI of the MI355X (gfx950) Leech-lattice quantization library.
+ *
+ * Every entry point takes plain pointers, element counts and a hipStream_t
+ * (passed as void*; NULL = the legacy default stream) and returns an int
+ * status: PLX_OK (0) or one of the PLX_E* codes below, with a message
+ * retrievable from plx_last_error().  Device pointers must live on the
+ * current HIP device.  No entry point allocates its outputs: callers own all
+ * buffers.  Work is enqueued on the given stream and not synchronised.
+ *
+ * Each function names the reference interface it replaces
+ * (alavicka/pollux, file:line).
+ */
+#ifndef POLLUX_AMD_H
+#define POLLUX_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ------------------------------------------------------ */
+#define PLX_OK 0
+#define PLX_EINVAL 1  /* bad argument: shape, size, null pointer, mode */
+#define PLX_EHIP 2    /* a HIP runtime call or kernel launch failed */
+#define PLX_ENOMEM 3  /* a one-time device table allocation failed */
+
+/* ---- nearest-neighbour semantics -------------------------------------- */
+/* NN-B: bf16 operands, fp32 accumulation, score rounded to bf16, lowest index
+ *       among equal maxima, origin iff 2*max < 0x407FFFFF.  The reference's
+ *       non-Triton path, castor.py:544-557. */
+#define PLX_NN_BF16_SCORES 0
+/* NN-T: bf16 operands, fp32 accumulation and fp32 scores, lowest index among
+ *       equal maxima, same origin rule.  The reference's Triton kernel,
+ *       castor.py:407-460. */
+#define PLX_NN_FP32_SCORES 1
+
+/* ---- element types of plx_gather_codebook's output -------------------- */
+#define PLX_DTYPE_F32 0
+#define PLX_DTYPE_F16 1
+#define PLX_DTYPE_BF16 2
+
+/* ---- constants (castor.py:34-68) --------------------------------------- */
+#define PLX_H24_DIM 24
+#define PLX_KISSING_COUNT 196560
+#define PLX_CODEBOOK_COUNT 196561
+#define PLX_INDEX_BITS 18
+#define PLX_INDICES_PER_CHUNK 4
+#define PLX_BYTES_PER_CHUNK 9
+
+/* Message describing the last failed call on this host thread ("" if none). */
+const char *plx_last_error(void);
+
+/* Library ABI version (monotone). */
+int plx_version(void);
+
+/* ---- codebook (host) --------------------------------------------------- */
+/* Raw integer coordinates of the 196,561-row codebook, origin first, rows in
+ * the reference's lexicographic order; out: int8[196561*24].
+ * Replaces the generator of castor.py:74-190 (_build_codebook_cpu). */
+int plx_codebook_raw(int8_t *out, int64_t n_bytes);
+
+/* The reference's fp32 table raw*fp32(1/sqrt(8)); out: float[196561*24].
+ * Replaces castor._build_codebook_cpu() / get_h24_codebook (castor.py:146-199). */
+int plx_codebook_f32(float *out, int64_t n_floats);
+
+/* First 4x4 block of the fp32 codebook; out: float[16].
+ * Replaces castor.codebook_fingerprint (castor.py:263-266). */
+int plx_codebook_fingerprint(float *out16);
+
+/* Build (once per device) the device-resident codebook tables on the current
+ * device.  Every compute entry point calls it lazily; calling it up front
+ * moves the one-time upload out of the first timed call. */
+int plx_device_init(void);
+
+/* ---- 18-bit packing (castor.py:226-260) --------------------------------- */
+/* indices: int64[n] (idx_is_i64 = 1) or int32[n] (idx_is_i64 = 0).
+ * out: uint8[((n+3)/4)*9]; 72-bit big-endian groups of four 18-bit indices,
+ * zero padded.  Replaces castor.pack_indices (castor.py:226-246). */
+int plx_pack_indices(const void *indices, int idx_is_i64, int64_t n, uint8_t *out, void *stream);
+
+/* packed: uint8[n_packed_bytes], n_packed_bytes % 9 == 0; out: int64[num_indices]
+ * with num_indices <= 4*n_packed_bytes/9.  Replaces castor.unpack_indices
+ * (castor.py:249-260). */
+int plx_unpack_indices(const uint8_t *packed, int64_t n_packed_bytes, int64_t num_indices,
+                       int64_t *out, void *stream);
+
+/* ---- row scale (castor.py:309-339, pack.py:164) ------------------------ */
+/* sigma[r] = sqrt(mean(w[r,:]^2) + 1e-8) in fp32; w: float[rows*cols].
+ * Replaces castor.row_rms_from_matrix (castor.py:309-313). */
+int plx_row_rms(const float *w, int64_t rows, int64_t cols, float *sigma, void *stream);
+
+/* sigma16[r] = fp16(max(row_rms(w)[r] * fp32(sqrt 12), 1e-8)) as raw fp16 bits.
+ * Replaces the sigma line of pack._quantize_h24_layer (pack.py:164). */
+int plx_sigma16_pack(const float *w, int64_t rows, int64_t cols, uint16_t *sigma16, void *stream);
+
+/* ---- nearest-neighbour quantizer --------------------------------------- */
+/* Workspace (device bytes) plx_quantize / plx_requantize need for n_atoms. */
+size_t plx_quantize_workspace_bytes(int64_t n_atoms);
+
+/* x: float[n_atoms*24] lattice coordinates; idx_out: int32[n_atoms] codebook
+ * indices (0 = origin).  mode: PLX_NN_*.  Replaces the index computation of
+ * castor_quantize_leech (castor.py:487-560: _leech_nn_triton / the chunked
+ * fallback loop). */
+int plx_quantize(const float *x, int64_t n_atoms, int mode, int32_t *idx_out,
+                 void *workspace, size_t workspace_bytes, void *stream);
+
+/* out[i,:] = codebook[idx[i],:] cast (RNE) to out_dtype (PLX_DTYPE_*);
+ * indices outside 0..196560 read row 0.  Replaces
+ * codebook.to(dtype).index_select(0, indices) (castor.py:533,559). */
+int plx_gather_codebook(const int32_t *idx, int64_t n, int out_dtype, void *out, void *stream);
+
+/* The per-step requantize of one fp32 latent [rows, cols] (cols % 24 == 0):
+ *   sigma = row_rms(latent); x = (latent/sigma)/fp32(1/sqrt 2);
+ *   idx = NN(x); weight = (codebook[idx]*sigma)*fp32(1/sqrt 2)
+ * Outputs: sigma_out float[rows] and idx_out int32[rows*cols/24] (required);
+ * packed_out uint8[((N+3)/4)*9] and weight_out float[rows*cols] (nullable).
+ * Replaces pollux.py:874-884 (normalize_matrix_by_row_rms ->
+ * castor_quantize_leech -> scale_matrix_by_row_rms) followed by
+ * castor.pack_indices. */
+int plx_requantize(const float *latent, int64_t rows, int64_t cols, int mode,
+                   float *sigma_out, int32_t *idx_out, uint8_t *packed_out, float *weight_out,
+                   void *workspace, size_t workspace_bytes, void *stream);
+
+/* ---- dequantization (pollux.py:485-507) -------------------------------- */
+/* w16 = fp16(fp16(codebook16[unpack(packed)] * sigma16[row]) * fp32(1/sqrt 2)),
+ * shape [rows, cols] as raw fp16 bits.  Replaces PackedH24Linear.materialize
+ * (pollux.py:485-504). */
+int plx_dequant_f16(const uint8_t *packed, int64_t n_packed_bytes, const uint16_t *sigma16,
+                    int64_t rows, int64_t cols, uint16_t *w16_out, void *stream);
+
+/* ---- kernel timing (diagnostics; no counterpart in the reference) ------ */
+/* While enabled, every launch of the quantizer's scoring kernel (nn_kernel)
+ * is bracketed by HIP events recorded on its launch stream (up to 4096
+ * launches).  plx_profile_begin() clears and enables recording;
+ * plx_profile_end() disables it, waits for the recorded events and returns
+ * the summed kernel time (ms) and the number of launches.  Used by bench.py
+ * for the roofline's per-launch kernel duration. */
+int plx_profile_begin(void);
+int plx_profile_end(double *total_ms, int64_t *launches);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* POLLUX_AMD_H */

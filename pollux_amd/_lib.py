@@ -1,0 +1,92 @@
+"""ctypes binding of ``lib/libpollux_amd.so`` (the C ABI in include/pollux_amd.h).
+
+The library is built in-tree by ``pollux_amd.build`` for gfx950.  Loading
+fails loudly when it is missing: there is no CPU or PyTorch fallback for any
+compute entry point.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent / "lib" / "libpollux_amd.so"
+
+PLX_OK, PLX_EINVAL, PLX_EHIP, PLX_ENOMEM = 0, 1, 2, 3
+NN_BF16_SCORES, NN_FP32_SCORES = 0, 1
+DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
+
+_vp, _i64, _int, _sz = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_size_t
+
+# name -> (restype, argtypes); every symbol declared in include/pollux_amd.h
+SIGNATURES = {
+    "plx_last_error": (ctypes.c_char_p, []),
+    "plx_version": (_int, []),
+    "plx_codebook_raw": (_int, [_vp, _i64]),
+    "plx_codebook_f32": (_int, [_vp, _i64]),
+    "plx_codebook_fingerprint": (_int, [_vp]),
+    "plx_device_init": (_int, []),
+    "plx_pack_indices": (_int, [_vp, _int, _i64, _vp, _vp]),
+    "plx_unpack_indices": (_int, [_vp, _i64, _i64, _vp, _vp]),
+    "plx_row_rms": (_int, [_vp, _i64, _i64, _vp, _vp]),
+    "plx_sigma16_pack": (_int, [_vp, _i64, _i64, _vp, _vp]),
+    "plx_quantize_workspace_bytes": (_sz, [_i64]),
+    "plx_quantize": (_int, [_vp, _i64, _int, _vp, _vp, _sz, _vp]),
+    "plx_gather_codebook": (_int, [_vp, _i64, _int, _vp, _vp]),
+    "plx_requantize": (_int, [_vp, _i64, _i64, _int, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "plx_dequant_f16": (_int, [_vp, _i64, _vp, _i64, _i64, _vp, _vp]),
+    "plx_profile_begin": (_int, []),
+    "plx_profile_end": (_int, [_vp, _vp]),
+}
+
+_lock = threading.Lock()
+_lib: ctypes.CDLL | None = None
+
+
+def lib() -> ctypes.CDLL:
+    """The loaded library (raises if it has not been built)."""
+    global _lib
+    if _lib is None:
+        with _lock:
+            if _lib is None:
+                if not LIB_PATH.exists():
+                    raise RuntimeError(
+                        f"pollux_amd: HIP library {LIB_PATH} is missing; build it with "
+                        "`python -m pollux_amd.build` (hipcc, gfx950)."
+                    )
+                handle = ctypes.CDLL(str(LIB_PATH))
+                for name, (res, args) in SIGNATURES.items():
+                    fn = getattr(handle, name)
+                    fn.restype = res
+                    fn.argtypes = args
+                _lib = handle
+    return _lib
+
+
+def check(status: int, what: str) -> None:
+    """Map a PLX_* status to the reference's exception types."""
+    if status == PLX_OK:
+        return
+    msg = lib().plx_last_error().decode(errors="replace")
+    if status == PLX_EINVAL:
+        raise ValueError(msg or f"{what}: invalid argument")
+    raise RuntimeError(f"{what} failed ({status}): {msg}")
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def stream_of(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def require_device(t: torch.Tensor, name: str) -> None:
+    if t.device.type != "cuda":
+        raise ValueError(
+            f"pollux_amd: {name} must be on a ROCm device (torch 'cuda'); got {t.device}. "
+            "This library has no CPU path."
+        )

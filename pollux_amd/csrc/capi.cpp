@@ -1,0 +1,177 @@
+// extern "C" entry points: argument validation, error reporting, dispatch to
+// the kernel launchers.  Validation mirrors the reference's own checks so the
+// Python host layer can raise the same exception types (ValueError for shapes,
+// castor.py:272-295,311-312; RuntimeError for runtime failures).
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "plx_internal.h"
+
+namespace plx {
+namespace {
+thread_local std::string g_last_error;
+}
+
+int fail(int code, const char *fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  std::vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+int check_hip(hipError_t e, const char *what) {
+  if (e == hipSuccess) return PLX_OK;
+  return fail(PLX_EHIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+int check_launch(const char *what) { return check_hip(hipGetLastError(), what); }
+
+}  // namespace plx
+
+using namespace plx;
+
+#define PLX_REQUIRE(cond, ...) \
+  do {                         \
+    if (!(cond)) return fail(PLX_EINVAL, __VA_ARGS__); \
+  } while (0)
+
+static inline hipStream_t as_stream(void *s) { return static_cast<hipStream_t>(s); }
+
+extern "C" {
+
+const char *plx_last_error(void) { return g_last_error.c_str(); }
+
+int plx_version(void) { return 1; }
+
+int plx_codebook_raw(int8_t *out, int64_t n_bytes) {
+  PLX_REQUIRE(out != nullptr, "plx_codebook_raw: null output");
+  PLX_REQUIRE(n_bytes == static_cast<int64_t>(kCodebook) * kDim, "plx_codebook_raw: need %d bytes, got %lld",
+              kCodebook * kDim, static_cast<long long>(n_bytes));
+  const int8_t *raw = codebook_raw_host();
+  if (!raw) return fail(PLX_EINVAL, "codebook generator produced a wrong row count");
+  std::memcpy(out, raw, static_cast<size_t>(n_bytes));
+  return PLX_OK;
+}
+
+int plx_codebook_f32(float *out, int64_t n_floats) {
+  PLX_REQUIRE(out != nullptr, "plx_codebook_f32: null output");
+  PLX_REQUIRE(n_floats == static_cast<int64_t>(kCodebook) * kDim, "plx_codebook_f32: need %d floats, got %lld",
+              kCodebook * kDim, static_cast<long long>(n_floats));
+  const int8_t *raw = codebook_raw_host();
+  if (!raw) return fail(PLX_EINVAL, "codebook generator produced a wrong row count");
+  float val[9];
+  for (int k = -4; k <= 4; ++k) val[k + 4] = raw_to_f32(k);
+  for (int64_t i = 0; i < n_floats; ++i) out[i] = val[raw[i] + 4];
+  return PLX_OK;
+}
+
+int plx_codebook_fingerprint(float *out16) {
+  PLX_REQUIRE(out16 != nullptr, "plx_codebook_fingerprint: null output");
+  const int8_t *raw = codebook_raw_host();
+  if (!raw) return fail(PLX_EINVAL, "codebook generator produced a wrong row count");
+  for (int r = 0; r < 4; ++r)
+    for (int c = 0; c < 4; ++c) out16[r * 4 + c] = raw_to_f32(raw[r * kDim + c]);
+  return PLX_OK;
+}
+
+int plx_device_init(void) {
+  const DeviceTables *t = nullptr;
+  return get_tables(&t);
+}
+
+int plx_pack_indices(const void *indices, int idx_is_i64, int64_t n, uint8_t *out, void *stream) {
+  PLX_REQUIRE(n >= 0, "plx_pack_indices: negative count %lld", static_cast<long long>(n));
+  if (n == 0) return PLX_OK;
+  PLX_REQUIRE(indices != nullptr && out != nullptr, "plx_pack_indices: null pointer");
+  return launch_pack(indices, idx_is_i64, n, out, as_stream(stream));
+}
+
+int plx_unpack_indices(const uint8_t *packed, int64_t n_packed_bytes, int64_t num_indices, int64_t *out,
+                       void *stream) {
+  PLX_REQUIRE(n_packed_bytes >= 0 && n_packed_bytes % 9 == 0,
+              "plx_unpack_indices: packed length %lld is not a multiple of 9", static_cast<long long>(n_packed_bytes));
+  PLX_REQUIRE(num_indices >= 0 && num_indices <= (n_packed_bytes / 9) * 4,
+              "plx_unpack_indices: num_indices %lld exceeds the %lld indices held by %lld bytes",
+              static_cast<long long>(num_indices), static_cast<long long>((n_packed_bytes / 9) * 4),
+              static_cast<long long>(n_packed_bytes));
+  if (num_indices == 0) return PLX_OK;
+  PLX_REQUIRE(packed != nullptr && out != nullptr, "plx_unpack_indices: null pointer");
+  return launch_unpack(packed, num_indices, out, as_stream(stream));
+}
+
+int plx_row_rms(const float *w, int64_t rows, int64_t cols, float *sigma, void *stream) {
+  PLX_REQUIRE(rows >= 0 && cols > 0, "plx_row_rms: bad shape (%lld, %lld)", static_cast<long long>(rows),
+              static_cast<long long>(cols));
+  if (rows == 0) return PLX_OK;
+  PLX_REQUIRE(w != nullptr && sigma != nullptr, "plx_row_rms: null pointer");
+  return launch_row_rms(w, rows, cols, sigma, nullptr, as_stream(stream));
+}
+
+int plx_sigma16_pack(const float *w, int64_t rows, int64_t cols, uint16_t *sigma16, void *stream) {
+  PLX_REQUIRE(rows >= 0 && cols > 0, "plx_sigma16_pack: bad shape (%lld, %lld)", static_cast<long long>(rows),
+              static_cast<long long>(cols));
+  if (rows == 0) return PLX_OK;
+  PLX_REQUIRE(w != nullptr && sigma16 != nullptr, "plx_sigma16_pack: null pointer");
+  return launch_row_rms(w, rows, cols, nullptr, sigma16, as_stream(stream));
+}
+
+size_t plx_quantize_workspace_bytes(int64_t n_atoms) { return quantize_workspace_bytes(n_atoms < 0 ? 0 : n_atoms); }
+
+int plx_quantize(const float *x, int64_t n_atoms, int mode, int32_t *idx_out, void *workspace,
+                 size_t workspace_bytes, void *stream) {
+  PLX_REQUIRE(n_atoms >= 0, "plx_quantize: negative atom count");
+  PLX_REQUIRE(mode == PLX_NN_BF16_SCORES || mode == PLX_NN_FP32_SCORES, "plx_quantize: unknown mode %d", mode);
+  if (n_atoms == 0) return PLX_OK;
+  PLX_REQUIRE(x != nullptr && idx_out != nullptr, "plx_quantize: null pointer");
+  return launch_quantize(x, nullptr, n_atoms, kDim, n_atoms, mode, idx_out, nullptr, nullptr, workspace,
+                         workspace_bytes, as_stream(stream));
+}
+
+int plx_gather_codebook(const int32_t *idx, int64_t n, int out_dtype, void *out, void *stream) {
+  PLX_REQUIRE(n >= 0, "plx_gather_codebook: negative count");
+  PLX_REQUIRE(out_dtype == PLX_DTYPE_F32 || out_dtype == PLX_DTYPE_F16 || out_dtype == PLX_DTYPE_BF16,
+              "plx_gather_codebook: unknown dtype %d", out_dtype);
+  if (n == 0) return PLX_OK;
+  PLX_REQUIRE(idx != nullptr && out != nullptr, "plx_gather_codebook: null pointer");
+  PLX_REQUIRE((reinterpret_cast<uintptr_t>(out) & (out_dtype == PLX_DTYPE_F32 ? 15u : 7u)) == 0,
+              "plx_gather_codebook: output is not aligned");
+  return launch_gather(idx, n, out_dtype, out, as_stream(stream));
+}
+
+int plx_requantize(const float *latent, int64_t rows, int64_t cols, int mode, float *sigma_out, int32_t *idx_out,
+                   uint8_t *packed_out, float *weight_out, void *workspace, size_t workspace_bytes, void *stream) {
+  PLX_REQUIRE(rows >= 0 && cols > 0, "plx_requantize: bad shape (%lld, %lld)", static_cast<long long>(rows),
+              static_cast<long long>(cols));
+  PLX_REQUIRE(cols % kDim == 0, "Pollux requires in_features divisible by H24_DIM=24; got %lld.",
+              static_cast<long long>(cols));
+  PLX_REQUIRE(mode == PLX_NN_BF16_SCORES || mode == PLX_NN_FP32_SCORES, "plx_requantize: unknown mode %d", mode);
+  if (rows == 0) return PLX_OK;
+  PLX_REQUIRE(latent != nullptr && sigma_out != nullptr && idx_out != nullptr, "plx_requantize: null pointer");
+  const int64_t n_atoms = rows * (cols / kDim);
+  int st = launch_row_rms(latent, rows, cols, sigma_out, nullptr, as_stream(stream));
+  if (st != PLX_OK) return st;
+  return launch_quantize(latent, sigma_out, rows, cols, n_atoms, mode, idx_out, packed_out, weight_out, workspace,
+                         workspace_bytes, as_stream(stream));
+}
+
+int plx_dequant_f16(const uint8_t *packed, int64_t n_packed_bytes, const uint16_t *sigma16, int64_t rows,
+                    int64_t cols, uint16_t *w16_out, void *stream) {
+  PLX_REQUIRE(rows >= 0 && cols > 0 && cols % kDim == 0, "plx_dequant_f16: bad shape (%lld, %lld)",
+              static_cast<long long>(rows), static_cast<long long>(cols));
+  const int64_t n_atoms = rows * (cols / kDim);
+  PLX_REQUIRE(n_packed_bytes == ((n_atoms + 3) / 4) * 9,
+              "plx_dequant_f16: packed length %lld does not match %lld atoms (need %lld)",
+              static_cast<long long>(n_packed_bytes), static_cast<long long>(n_atoms),
+              static_cast<long long>(((n_atoms + 3) / 4) * 9));
+  if (rows == 0) return PLX_OK;
+  PLX_REQUIRE(packed != nullptr && sigma16 != nullptr && w16_out != nullptr, "plx_dequant_f16: null pointer");
+  return launch_dequant_f16(packed, sigma16, rows, cols, w16_out, as_stream(stream));
+}
+
+}  // extern "C"

@@ -1,0 +1,48 @@
+// Device helpers shared by the .hip translation units.
+#pragma once
+
+#include <hip/hip_fp16.h>
+
+#include "plx_internal.h"
+
+namespace plx {
+
+// fp32 -> bf16 bits, round to nearest even (finite inputs; the same rounding
+// the reference's bf16 casts use).
+__device__ __forceinline__ uint32_t bf16_rne_bits(float f) {
+  const uint32_t u = __float_as_uint(f);
+  return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+}
+
+__device__ __forceinline__ float bf16_bits_to_float(uint32_t b) { return __uint_as_float(b << 16); }
+
+// fp32 value of raw codebook coordinate k in -4..4: k * fp32(1/sqrt 8) rounded to fp32.
+__device__ __forceinline__ float raw_value_f32(int k) {
+  return static_cast<float>(k) * __uint_as_float(kLeechScaleBits);
+}
+
+// Four 18-bit indices -> one 9-byte big-endian group (castor.py:237-245).
+__device__ __forceinline__ void group_to_bytes(int32_t i0, int32_t i1, int32_t i2, int32_t i3, uint8_t *b) {
+  b[0] = static_cast<uint8_t>(i0 >> 10);
+  b[1] = static_cast<uint8_t>(i0 >> 2);
+  b[2] = static_cast<uint8_t>(((i0 & 0x03) << 6) | ((i1 >> 12) & 0x3F));
+  b[3] = static_cast<uint8_t>(i1 >> 4);
+  b[4] = static_cast<uint8_t>(((i1 & 0x0F) << 4) | ((i2 >> 14) & 0x0F));
+  b[5] = static_cast<uint8_t>(i2 >> 6);
+  b[6] = static_cast<uint8_t>(((i2 & 0x3F) << 2) | ((i3 >> 16) & 0x03));
+  b[7] = static_cast<uint8_t>(i3 >> 8);
+  b[8] = static_cast<uint8_t>(i3);
+}
+
+// One 9-byte group -> four indices (castor.py:254-257).
+__device__ __forceinline__ void bytes_to_group(const uint8_t *b, int32_t *v) {
+  const int32_t c0 = b[0], c1 = b[1], c2 = b[2], c3 = b[3], c4 = b[4], c5 = b[5], c6 = b[6], c7 = b[7], c8 = b[8];
+  v[0] = (c0 << 10) | (c1 << 2) | (c2 >> 6);
+  v[1] = ((c2 & 0x3F) << 12) | (c3 << 4) | (c4 >> 4);
+  v[2] = ((c4 & 0x0F) << 14) | (c5 << 6) | (c6 >> 2);
+  v[3] = ((c6 & 0x03) << 16) | (c7 << 8) | c8;
+}
+
+__device__ __forceinline__ bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace plx

@@ -1,0 +1,70 @@
+// Internal declarations shared by the library's translation units.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+#include "../../include/pollux_amd.h"
+
+namespace plx {
+
+constexpr int kDim = 24;
+constexpr int kKissing = 196560;
+constexpr int kCodebook = 196561;
+
+// MFMA codebook tiles: 16 kissing points per tile, stored as three K-planes
+// (coordinates 8p..8p+7) of 16 rows x 8 bf16, i.e. 768 bytes per tile.  The
+// tile array is padded with all-zero tiles to kPaddedTiles so that every
+// slice / stage / group split divides it evenly; a zero code scores exactly 0
+// and can never beat the origin threshold.
+constexpr int kTileCodes = 16;
+constexpr int kTileBytes = 768;
+constexpr int kRealTiles = kKissing / kTileCodes;  // 12285
+constexpr int kPaddedTiles = 12288;                // 2^12 * 3
+
+// fp32 constants of the reference (castor.py:47,50,68; castor.py:522; pack.py:164)
+constexpr uint32_t kLeechScaleBits = 0x3EB504F3u;  // fp32(1/sqrt 8)
+constexpr uint32_t kSLatticeBits = 0x3F3504F3u;    // fp32(1/sqrt 2)
+constexpr uint32_t kCSqNormBits = 0x407FFFFFu;     // fp32 |codebook[1]|^2
+constexpr uint32_t kEpsBits = 0x322BCC77u;         // fp32(1e-8)
+constexpr uint32_t kSqrt12Bits = 0x405DB3D7u;      // fp32(sqrt 12)
+
+struct DeviceTables {
+  int device = -1;
+  uint8_t *kp_bf16_tiles = nullptr;  // [kPaddedTiles][3][16][8] bf16 bits
+  int8_t *cb_raw = nullptr;          // [kCodebook][24] raw integer coordinates
+};
+
+// Host generator (codebook.cpp): raw coordinates, origin first, sorted.
+const int8_t *codebook_raw_host();
+// fp32 value of raw coordinate k (k in -4..4): k * fp32(1/sqrt 8), rounded to fp32.
+float raw_to_f32(int k);
+
+// Lazily built per-device tables for the current device (tables.cpp).
+int get_tables(const DeviceTables **out);
+
+// Error reporting (capi.cpp).
+int fail(int code, const char *fmt, ...);
+int check_hip(hipError_t e, const char *what);
+int check_launch(const char *what);
+
+// Event bracketing of the scoring kernel (profile.cpp); no-ops unless enabled.
+void profile_before(hipStream_t s);
+void profile_after(hipStream_t s);
+
+// Kernel launchers (one per .hip file); return PLX_* status.
+int launch_pack(const void *idx, int idx_is_i64, int64_t n, uint8_t *out, hipStream_t s);
+int launch_unpack(const uint8_t *packed, int64_t num_indices, int64_t *out, hipStream_t s);
+int launch_row_rms(const float *w, int64_t rows, int64_t cols, float *sigma, uint16_t *sigma16,
+                   hipStream_t s);
+int launch_quantize(const float *x, const float *sigma, int64_t rows, int64_t cols, int64_t n_atoms,
+                    int mode, int32_t *idx_out, uint8_t *packed_out, float *weight_out,
+                    void *workspace, size_t workspace_bytes, hipStream_t s);
+size_t quantize_workspace_bytes(int64_t n_atoms);
+int launch_gather(const int32_t *idx, int64_t n, int out_dtype, void *out, hipStream_t s);
+int launch_dequant_f16(const uint8_t *packed, const uint16_t *sigma16, int64_t rows, int64_t cols,
+                       uint16_t *w16, hipStream_t s);
+
+}  // namespace plx

@@ -1,0 +1,84 @@
+// Per-device codebook tables, built once per device and kept until exit.
+//
+// kp_bf16_tiles  the 196,560 kissing points (codebook rows 1..196560) rounded
+//                to bf16 exactly as the reference's bf16 casts round them
+//                (castor.py:437, autocast at castor.py:552), in the MFMA tile
+//                layout of quantize.hip; 12288 tiles x 768 B = 9,437,184 B.
+// cb_raw         the raw int8 coordinates of all 196,561 rows (4,717,464 B);
+//                decoded per value into fp32 / bf16 / fp16 by the kernels.
+
+#include <cstring>
+#include <mutex>
+#include <vector>
+
+#include "plx_internal.h"
+
+namespace plx {
+namespace {
+
+uint16_t f32_to_bf16_rne(float f) {
+  uint32_t u;
+  std::memcpy(&u, &f, 4);
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+std::mutex g_mu;
+DeviceTables g_tables[64];
+
+int build(int dev, DeviceTables *t) {
+  const int8_t *raw = codebook_raw_host();
+  if (!raw) return fail(PLX_EINVAL, "codebook generator produced a wrong row count");
+
+  uint16_t bf_of[9];
+  for (int k = -4; k <= 4; ++k) bf_of[k + 4] = f32_to_bf16_rne(raw_to_f32(k));
+
+  std::vector<uint16_t> tiles(static_cast<size_t>(kPaddedTiles) * (kTileBytes / 2), 0);
+  for (int tile = 0; tile < kRealTiles; ++tile)
+    for (int p = 0; p < 3; ++p)
+      for (int i = 0; i < kTileCodes; ++i)
+        for (int e = 0; e < 8; ++e) {
+          const int code = tile * kTileCodes + i + 1;  // codebook row (origin excluded)
+          const int k = raw[static_cast<size_t>(code) * kDim + 8 * p + e];
+          tiles[static_cast<size_t>(tile) * 384 + p * 128 + i * 8 + e] = bf_of[k + 4];
+        }
+
+  const size_t tile_bytes = tiles.size() * 2;
+  const size_t raw_bytes = static_cast<size_t>(kCodebook) * kDim;
+  void *dt = nullptr, *dr = nullptr;
+  if (hipMalloc(&dt, tile_bytes) != hipSuccess) return fail(PLX_ENOMEM, "hipMalloc(%zu) failed on device %d", tile_bytes, dev);
+  if (hipMalloc(&dr, raw_bytes) != hipSuccess) {
+    (void)hipFree(dt);
+    return fail(PLX_ENOMEM, "hipMalloc(%zu) failed on device %d", raw_bytes, dev);
+  }
+  int st = check_hip(hipMemcpy(dt, tiles.data(), tile_bytes, hipMemcpyHostToDevice), "upload codebook tiles");
+  if (st == PLX_OK) st = check_hip(hipMemcpy(dr, raw, raw_bytes, hipMemcpyHostToDevice), "upload raw codebook");
+  if (st != PLX_OK) {
+    (void)hipFree(dt);
+    (void)hipFree(dr);
+    return st;
+  }
+  t->kp_bf16_tiles = static_cast<uint8_t *>(dt);
+  t->cb_raw = static_cast<int8_t *>(dr);
+  t->device = dev;
+  return PLX_OK;
+}
+
+}  // namespace
+
+int get_tables(const DeviceTables **out) {
+  int dev = 0;
+  int st = check_hip(hipGetDevice(&dev), "hipGetDevice");
+  if (st != PLX_OK) return st;
+  if (dev < 0 || dev >= 64) return fail(PLX_EINVAL, "device ordinal %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_mu);
+  DeviceTables *t = &g_tables[dev];
+  if (t->device != dev) {
+    st = build(dev, t);
+    if (st != PLX_OK) return st;
+  }
+  *out = t;
+  return PLX_OK;
+}
+
+}  // namespace plx

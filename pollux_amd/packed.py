@@ -1,0 +1,71 @@
+"""Packed inference layer: PackedH24Linear with HIP dequantization (pollux.py:461-507).
+
+Same constructor, buffers (``packed_weights`` uint8, ``sigma_rows`` fp16),
+state-dict keys, ``materialize()`` and ``forward()`` as the reference, so
+``PolluxModel.from_packed_checkpoint`` (pollux.py:704-752) can build it
+unchanged.  ``materialize`` runs the fused unpack + LUT-gather + row-scale
+kernel (plx_dequant_f16) instead of unpack_indices -> index_select -> two
+broadcast multiplies.
+"""
+
+from __future__ import annotations
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from . import _lib
+from .castor import assert_row_aligned_in_features, h24_linear_atom_count, h24_linear_scale_row_count
+
+
+def dequantize_h24(packed: torch.Tensor, sigma16: torch.Tensor, out_features: int, in_features: int) -> torch.Tensor:
+    """fp16 [out, in] = fp16(fp16(cb16[unpack(packed)] * sigma16[row]) * s_lattice) (pollux.py:491-499)."""
+    _lib.require_device(packed, "dequantize_h24 packed input")
+    if packed.dtype != torch.uint8:
+        raise ValueError(f"packed weights must be uint8, got {packed.dtype}")
+    if sigma16.dtype != torch.float16:
+        raise ValueError(f"sigma rows must be float16, got {sigma16.dtype}")
+    assert_row_aligned_in_features(in_features)
+    pk = packed.reshape(-1).contiguous()
+    sg = sigma16.reshape(-1).contiguous()
+    if sg.numel() != out_features:
+        raise ValueError(f"expected {out_features} sigma rows, got {sg.numel()}")
+    out = torch.empty((out_features, in_features), dtype=torch.float16, device=pk.device)
+    with torch.cuda.device(pk.device):
+        st = _lib.lib().plx_dequant_f16(
+            _lib.ptr(pk), pk.numel(), _lib.ptr(sg), out_features, in_features, _lib.ptr(out), _lib.stream_of(pk.device)
+        )
+    _lib.check(st, "dequantize_h24")
+    return out
+
+
+class PackedH24Linear(nn.Module):
+    """uint8 packed 18-bit indices + fp16 row scale; dense fp16 weight after materialize()."""
+
+    def __init__(self, in_features: int, out_features: int, bias: bool = False) -> None:
+        super().__init__()
+        assert_row_aligned_in_features(in_features)
+        self.in_features = int(in_features)
+        self.out_features = int(out_features)
+        self.num_atoms = h24_linear_atom_count(self.out_features, self.in_features)
+        self.num_sigma_rows = h24_linear_scale_row_count(self.out_features)
+        packed_len = ((self.num_atoms + 3) // 4) * 9
+        self.register_buffer("packed_weights", torch.zeros(packed_len, dtype=torch.uint8))
+        self.register_buffer("sigma_rows", torch.ones(self.num_sigma_rows, dtype=torch.float16))
+        self._materialized = False
+        if bias:
+            self.bias = nn.Parameter(torch.zeros(self.out_features))
+        else:
+            self.register_parameter("bias", None)
+
+    def materialize(self) -> None:
+        if self._materialized:
+            return
+        weight = dequantize_h24(self.packed_weights, self.sigma_rows.to(torch.float16), self.out_features, self.in_features)
+        self.weight = nn.Parameter(weight, requires_grad=False)
+        del self.packed_weights
+        del self.sigma_rows
+        self._materialized = True
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return F.linear(x, self.weight.to(dtype=x.dtype), self.bias)
