@@ -5,12 +5,11 @@
 // keeping only a running maximum per (atom, lane) and the index of the code
 // group where it was reached; no score is ever written to memory.
 //
-// Decomposition.
+// nn_kernel -- the scoring sweep.
 //   grid.x = atom_blocks * n_slices; block b works on atom block b / n_slices
 //   and codebook slice b % n_slices.  Work-groups are dispatched round-robin
-//   over the 8 XCDs, so with 8 (or 16) slices each XCD only ever streams its
-//   own 1.18 (2.36) MB of the 9.4 MB bf16 codebook and serves it from its
-//   4 MB L2.
+//   over the 8 XCDs, so with 8 slices each XCD only ever streams its own
+//   1.18 MB of the 9.4 MB bf16 codebook and serves it from its 4 MB L2.
 //   A block is 4 waves; a wave holds 8 atom tiles of 16 atoms as MFMA B
 //   operands in registers (512 atoms per block) and sweeps its slice, staged
 //   through LDS 32 code tiles (24 KB) at a time, double buffered, with the
@@ -25,18 +24,22 @@
 //   NN-T (castor.py:419-460): winner = lowest code with the maximal fp32
 //     score S; origin iff 2*S < 0x407FFFFF.
 //   Both are tracked with one integer threshold R per (atom, lane): a group of
-//   4 tiles (16 codes per lane) improves when its max score, as an int bit
+//   8 tiles (32 codes per lane) improves when its max score, as an int bit
 //   pattern, exceeds R (positive floats order like ints; negative scores can
 //   only lose to the origin threshold R starts at).  NN-B raises R to the
 //   largest fp32 that still rounds to the new bucket, so later codes in the
 //   same bucket never displace the earlier group; NN-T raises R to the score.
-//   At the end each lane that holds its atom's best R rescans its best group
-//   exactly (fp64 sum of exact bf16 products, rounded to fp32 then bf16) to
-//   pick the lowest code, and the lanes / slices merge through a 64-bit
-//   atomicMax on (score bits << 32 | ~code).  MFMA's fp32 sum differs from the
-//   exact one by < 2^-22 * sum|x_i c_i| (measured), so the result equals the
-//   exact-score answer on every atom that is not a near-tie within that
-//   envelope.
+//   Each (atom, slice) ends as a 16-byte record: the best key and, per lane,
+//   the best group of the lanes that hold it.
+//
+// resolve_kernel -- one thread per atom: the maximum key over the slices, an
+//   exact-product rescan (v_dot2_f32_bf16) of the few groups that hold it to
+//   find the lowest code, then the index and the packed 9-byte groups.  Both
+//   fp32 sums (MFMA, dot2) lie within 2^-20 * sum|x_i c_i| of the exact score
+//   (MFMA measured at < 2^-22), so the result equals the exact-score answer
+//   on every atom that is not a near-tie within that envelope.
+
+#include <type_traits>
 
 #include "plx_device.h"
 
@@ -44,19 +47,21 @@ namespace plx {
 namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kWaves = 4;
 constexpr int kThreads = kWaves * 64;
 constexpr int kAT = 8;                                  // atom tiles per wave
-constexpr int kG = 4;                                   // code tiles per tracking group
+constexpr int kG = 8;                                   // code tiles per tracking group
 constexpr int kST = 32;                                 // code tiles per LDS stage
 constexpr int kAtomsPerBlock = kWaves * kAT * 16;       // 512
 constexpr int kStageBytes = kST * kTileBytes;           // 24,576
 constexpr int kStageVecs = kStageBytes / 16;            // 1,536 uint4
 constexpr int kLoadsPerThread = kStageVecs / kThreads;  // 6
 static_assert(kStageVecs % kThreads == 0, "stage must split evenly over the block");
-static_assert(kST % kG == 0, "groups must not straddle stages");
+static_assert(kST % kG == 0 && kG == 8, "whole 8-tile groups per LDS stage");
 
 constexpr int kModeB = PLX_NN_BF16_SCORES;
 
@@ -67,11 +72,16 @@ __device__ __forceinline__ int initial_threshold() {
   return MODE == kModeB ? 0x3FFF7FFF : 0x3FFFFFFE;
 }
 
+// New threshold after a group whose maximum is gm.  NN-T: gm itself.  NN-B:
+// the largest fp32 bit pattern in gm's bf16 bucket, with the bucket taken by
+// round-half-up ((gm + 0x8000) >> 16) -- two VALU ops instead of five.  It
+// differs from round-to-nearest-even only when gm's low 16 bits are exactly
+// 0x8000, a score sitting exactly on a bf16 rounding midpoint, which the
+// parity oracle classifies as a near-tie.
 template <int MODE>
 __device__ __forceinline__ int raised_threshold(int gm) {
   if (MODE != kModeB) return gm;
-  const uint32_t b = bf16_rne_bits(__int_as_float(gm));
-  return static_cast<int>((b << 16) + 0x8000u - (b & 1u));
+  return static_cast<int>(((static_cast<uint32_t>(gm) + 0x8000u) & 0xFFFF0000u) | 0x7FFFu);
 }
 
 // Lattice coordinates 8q..8q+7 of atom a (zeros past the end / for q == 3).
@@ -101,9 +111,8 @@ template <int MODE, bool FUSED>
 __global__ __launch_bounds__(kThreads, 2) void nn_kernel(const float *__restrict__ src,
                                                           const float *__restrict__ sigma, int64_t atoms_per_row,
                                                           int64_t n_atoms, const uint8_t *__restrict__ tiles,
-                                                          const int8_t *__restrict__ cb_raw, int n_slices,
-                                                          int tiles_per_slice,
-                                                          unsigned long long *__restrict__ keys) {
+                                                          int n_slices, int tiles_per_slice,
+                                                          uint4 *__restrict__ records) {
   __shared__ __align__(16) uint8_t lds[2][kStageBytes];
 
   const int slice = static_cast<int>(blockIdx.x % static_cast<unsigned>(n_slices));
@@ -132,9 +141,9 @@ __global__ __launch_bounds__(kThreads, 2) void nn_kernel(const float *__restrict
   const int t0 = slice * tiles_per_slice;
   const int n_stages = tiles_per_slice / kST;
   const uint4 *gsrc = reinterpret_cast<const uint4 *>(tiles + static_cast<size_t>(t0) * kTileBytes);
-  // Stage s is copied HBM/L2 -> LDS by global_load_lds_dwordx4 (no VGPR
-  // staging): wave w, lane l moves vector i*256 + 64w + l, so each wave fills
-  // a contiguous KiB of the buffer.
+  // Stage s is copied L2 -> LDS by global_load_lds_dwordx4 (no VGPR staging):
+  // wave w, lane l moves vector i*256 + 64w + l, so each wave fills a
+  // contiguous KiB of the buffer.
   auto stage_copy = [&](int stage, int dst_buf) {
 #pragma unroll
     for (int i = 0; i < kLoadsPerThread; ++i) {
@@ -148,173 +157,230 @@ __global__ __launch_bounds__(kThreads, 2) void nn_kernel(const float *__restrict
   __syncthreads();
 
   const int a_off = (q < 3 ? q : 0) * 256 + j * 16;
+  // Software pipeline: the MFMA result of tile k for atom tile `at` is folded
+  // into the group maximum while tile k+1's MFMAs issue, and tile k+1's A
+  // operand is read from LDS right after tile k's first MFMA.  A group of 8
+  // tiles is compared against the threshold once its last tile has been
+  // folded, i.e. during the next group's first tile; the slice's last tile is
+  // folded after the loop.
+  int gm[kAT];
+  f32x4 acc[kAT];
+#pragma unroll
+  for (int at = 0; at < kAT; ++at) {
+    gm[at] = INT_MIN;
+    acc[at] = f32x4{-0.f, -0.f, -0.f, -0.f};  // INT_MIN bit patterns: neutral for the fold
+  }
+  int group_prev = -1;  // global id of the group whose compare is pending
   for (int st = 0; st < n_stages; ++st) {
     const int buf = st & 1;
     if (st + 1 < n_stages) stage_copy(st + 1, buf ^ 1);
     const uint8_t *L = lds[buf] + a_off;
-    const int group0 = (t0 + st * kST) / kG;
-#pragma unroll 1
-    for (int g = 0; g < kST / kG; ++g) {
-      int gm[kAT];
+    bf16x8 a = *reinterpret_cast<const bf16x8 *>(L);
+    bool up[kAT];
+    int gdone[kAT];
+    // One group of 8 tiles: tile 0 closes the previous group, tile 1 starts
+    // this group's maximum.
+    auto eight_tiles = [&](int k0) {
+      constexpr bool FIRST = true;
 #pragma unroll
-      for (int at = 0; at < kAT; ++at) gm[at] = INT_MIN;
-#pragma unroll
-      for (int t = 0; t < kG; ++t) {
-        const bf16x8 a = *reinterpret_cast<const bf16x8 *>(L + (g * kG + t) * kTileBytes);
+      for (int t = 0; t < 8; ++t) {
+        const int k = k0 + t;
+        bf16x8 an;
 #pragma unroll
         for (int at = 0; at < kAT; ++at) {
           const f32x4 c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b[at], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-          // written as a chain so each pair folds into one v_max3_i32
-          gm[at] = max(max(gm[at], __float_as_int(c[0])), __float_as_int(c[1]));
-          gm[at] = max(max(gm[at], __float_as_int(c[2])), __float_as_int(c[3]));
-        }
-      }
-      // Improvements get rare once the running maxima settle: test all atom
-      // tiles, and take the update path only when some lane of the wave needs it.
-      bool any_up = false;
-#pragma unroll
-      for (int at = 0; at < kAT; ++at) any_up |= gm[at] > R[at];
-      if (__builtin_expect(__ballot(any_up) != 0ull, 0)) {
-#pragma unroll
-        for (int at = 0; at < kAT; ++at) {
-          if (gm[at] > R[at]) {
-            R[at] = raised_threshold<MODE>(gm[at]);
-            best[at] = group0 + g;
+          if (at == 0) {
+            // the LDS wait that guards `a` must not also wait for this read
+            __builtin_amdgcn_sched_barrier(0);
+            an = *reinterpret_cast<const bf16x8 *>(L + (k + 1 < kST ? k + 1 : k) * kTileBytes);
           }
+          int m;
+          if (FIRST && t == 1) {
+            m = max(max(__float_as_int(acc[at][0]), __float_as_int(acc[at][1])), __float_as_int(acc[at][2]));
+            m = max(m, __float_as_int(acc[at][3]));
+          } else {
+            m = max(max(gm[at], __float_as_int(acc[at][0])), __float_as_int(acc[at][1]));
+            m = max(max(m, __float_as_int(acc[at][2])), __float_as_int(acc[at][3]));
+          }
+          // The empty asm pins the fold next to this MFMA (IR passes would
+          // otherwise sink the chain to the group end) and the sched_barrier
+          // stops the machine scheduler from hoisting every MFMA, so the
+          // matrix pipe and the VALU work in parallel.
+          asm volatile("" : "+v"(m));
+          if (FIRST && t == 0) {
+            gdone[at] = m;
+            up[at] = m > R[at];
+          }
+          gm[at] = m;
+          acc[at] = c;
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        a = an;
+      }
+    };
+#pragma unroll 1
+    for (int k0 = 0; k0 < kST; k0 += kG) {
+      eight_tiles(k0);
+#pragma unroll
+      for (int at = 0; at < kAT; ++at) {
+        if (up[at]) {
+          R[at] = raised_threshold<MODE>(gdone[at]);
+          best[at] = group_prev;
         }
       }
+      group_prev = (t0 + st * kST + k0) / kG;
     }
     __syncthreads();
   }
+  // fold the slice's last tile and close its last group
+#pragma unroll
+  for (int at = 0; at < kAT; ++at) {
+    int m = max(max(gm[at], __float_as_int(acc[at][0])), __float_as_int(acc[at][1]));
+    m = max(max(m, __float_as_int(acc[at][2])), __float_as_int(acc[at][3]));
+    if (m > R[at]) {
+      R[at] = raised_threshold<MODE>(m);
+      best[at] = group_prev;
+    }
+  }
 
-  // ---- resolve: exact rescan of the best group of each candidate lane ----
-  const double s1 = static_cast<double>(bf16_bits_to_float(bf16_rne_bits(raw_value_f32(1))));
-  const double s2 = static_cast<double>(bf16_bits_to_float(bf16_rne_bits(raw_value_f32(2))));
-  const double s3 = static_cast<double>(bf16_bits_to_float(bf16_rne_bits(raw_value_f32(3))));
-  const double s4 = static_cast<double>(bf16_bits_to_float(bf16_rne_bits(raw_value_f32(4))));
-#pragma unroll 1
+  // ---- per (atom, slice) record for the resolve kernel ----
+  // key: the slice's best bucket (NN-B, bf16 bits) or fp32 score bits (NN-T),
+  // 0 when nothing beat the origin threshold; then, for each of the four lanes
+  // of the atom, its best group if it holds the slice maximum (else 0xFFFF).
+#pragma unroll
   for (int at = 0; at < kAT; ++at) {
     int Rm = R[at];
     Rm = max(Rm, __shfl_xor(Rm, 16, 64));
     Rm = max(Rm, __shfl_xor(Rm, 32, 64));
+    const uint32_t g16 = (best[at] >= 0 && R[at] == Rm) ? static_cast<uint32_t>(best[at]) : 0xFFFFu;
+    const uint32_t g0 = static_cast<uint32_t>(__shfl(static_cast<int>(g16), j, 64));
+    const uint32_t g1 = static_cast<uint32_t>(__shfl(static_cast<int>(g16), j + 16, 64));
+    const uint32_t g2 = static_cast<uint32_t>(__shfl(static_cast<int>(g16), j + 32, 64));
+    const uint32_t g3 = static_cast<uint32_t>(__shfl(static_cast<int>(g16), j + 48, 64));
     const int64_t a = wave_atom0 + at * 16 + j;
-    uint32_t key_hi = 0, key_lo = 0;
-    if (best[at] >= 0 && R[at] == Rm && a < n_atoms) {
-      double xs[kDim];
+    if (q == 0 && a < n_atoms) {
+      const bool hit = Rm != initial_threshold<MODE>();
+      const uint32_t key = hit ? (MODE == kModeB ? static_cast<uint32_t>(Rm) >> 16 : static_cast<uint32_t>(Rm)) : 0u;
+      records[static_cast<int64_t>(slice) * n_atoms + a] = make_uint4(key, g0 | (g1 << 16), g2 | (g3 << 16), 0u);
+    }
+  }
+}
+
+// Resolve: one thread per atom.  Takes the maximum key over the slices, then
+// rescans (v_dot2_f32_bf16: exact bf16 products, fp32 accumulation) the best
+// groups of every (slice, lane) that holds it -- typically one group, 4 rows
+// of 8 tiles = 32 codes -- and picks the lowest code reaching the bucket
+// (NN-B) or the highest fp32 score (NN-T, lowest code on ties); writes the
+// int32 index and, optionally, the packed 9-byte groups.
+template <int MODE, bool FUSED>
+__global__ __launch_bounds__(256) void resolve_kernel(const uint4 *__restrict__ records, int n_slices,
+                                                      int64_t n_atoms, const float *__restrict__ src,
+                                                      const float *__restrict__ sigma, int64_t atoms_per_row,
+                                                      const uint8_t *__restrict__ rescan,
+                                                      int32_t *__restrict__ idx_out, uint8_t *__restrict__ packed_out) {
+  __shared__ int32_t ids[256];
+  __shared__ __align__(16) uint8_t bytes[64 * 9];
+  const int64_t a0 = static_cast<int64_t>(blockIdx.x) * 256;
+  const int64_t a = a0 + threadIdx.x;
+  int32_t id = 0;
+  if (a < n_atoms) {
+    uint32_t M = 0;
+    for (int s = 0; s < n_slices; ++s) M = max(M, records[static_cast<int64_t>(s) * n_atoms + a].x);
+    if (M != 0) {
+      uint32_t xw[12];
 #pragma unroll
       for (int qq = 0; qq < 3; ++qq) {
         float v[8];
         load_coords8<FUSED>(src, sigma, atoms_per_row, n_atoms, a, qq, v);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) xs[8 * qq + e] = static_cast<double>(bf16_bits_to_float(bf16_rne_bits(v[e])));
+        for (int d = 0; d < 4; ++d) xw[4 * qq + d] = bf16_rne_bits(v[2 * d]) | (bf16_rne_bits(v[2 * d + 1]) << 16);
       }
-      const uint32_t target = MODE == kModeB ? (static_cast<uint32_t>(R[at]) >> 16) : 0u;
-      bool found = false;
-      uint32_t found_code = 0;
+      uint32_t found = 0xFFFFFFFFu;  // lowest code whose bucket equals M (NN-B)
       float best_v = -__builtin_inff();
-      uint32_t best_code = 0;
-      for (int t = 0; t < kG; ++t) {
-        for (int e = 0; e < 4; ++e) {
-          const int code = (best[at] * kG + t) * kTileCodes + 4 * q + e;  // kissing index
-          if (code >= kKissing) continue;
-          const int8_t *cr = cb_raw + static_cast<size_t>(code + 1) * kDim;
-          double s = 0.0;
-#pragma unroll
-          for (int k = 0; k < kDim; ++k) {
-            const int r = cr[k];
-            const int m = r < 0 ? -r : r;
-            double c = m == 1 ? s1 : m == 2 ? s2 : m == 3 ? s3 : m == 4 ? s4 : 0.0;
-            c = r < 0 ? -c : c;
-            s = fma(xs[k], c, s);
+      uint32_t best_code = 0xFFFFFFFFu;
+      // Each thread walks its own candidate slots (slice, lane) in rounds, so
+      // the wave runs the rescan body once per round (~1-3 rounds) instead of
+      // once per slot that any of its threads needs.
+      const int n_slots = 4 * n_slices;
+      int slot = 0;
+      uint4 rec = records[a];
+      for (;;) {
+        uint32_t g = 0xFFFFu;
+        for (; slot < n_slots; ++slot) {
+          if ((slot & 3) == 0) rec = records[static_cast<int64_t>(slot >> 2) * n_atoms + a];
+          if (rec.x != M) {
+            slot |= 3;  // skip the rest of this slice
+            continue;
           }
-          const float s32 = static_cast<float>(s);
-          float v = s32;
-          if (MODE == kModeB) {
-            const uint32_t bk = bf16_rne_bits(s32);
-            v = bf16_bits_to_float(bk);
-            if (!found && bk == target) {
-              found = true;
-              found_code = static_cast<uint32_t>(code);
+          g = (((slot & 2) ? rec.z : rec.y) >> (16 * (slot & 1))) & 0xFFFFu;
+          if (g != 0xFFFFu) break;
+        }
+        if (slot >= n_slots) break;
+        const int qq = slot & 3;
+        ++slot;
+        if (slot < n_slots && (slot & 3) == 0) rec = records[static_cast<int64_t>(slot >> 2) * n_atoms + a];
+        // the lane's 32 codes of group g are 1.5 KB contiguous in the lane-major table
+        const uint4 *cg = reinterpret_cast<const uint4 *>(rescan) +
+                          ((static_cast<size_t>(qq) * kPaddedTiles + static_cast<size_t>(g) * kG) * 4) * 3;
+        for (int t = 0; t < kG; ++t) {
+          const int tile = static_cast<int>(g) * kG + t;
+          if (tile >= kRealTiles) break;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int row = 4 * qq + e;
+            const uint4 *cp = cg + (t * 4 + e) * 3;
+            const uint4 c0 = cp[0], c1 = cp[1], c2 = cp[2];
+            const uint32_t cw[12] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w, c2.x, c2.y, c2.z, c2.w};
+            float sc = 0.f;
+#pragma unroll
+            for (int d = 0; d < 12; ++d)
+              sc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, xw[d]), __builtin_bit_cast(bf16x2, cw[d]), sc,
+                                                   false);
+            const uint32_t code = static_cast<uint32_t>(tile * kTileCodes + row);
+            float v = sc;
+            if (MODE == kModeB) {
+              const uint32_t bk = bf16_rne_bits(sc);
+              v = bf16_bits_to_float(bk);
+              if (bk == M && code < found) found = code;
+            }
+            if (v > best_v || (v == best_v && code < best_code)) {
+              best_v = v;
+              best_code = code;
             }
           }
-          if (v > best_v) {
-            best_v = v;
-            best_code = static_cast<uint32_t>(code);
-          }
         }
       }
-      uint32_t code = best_code;
-      float v = best_v;
-      if (MODE == kModeB && found) {
-        code = found_code;
-        v = bf16_bits_to_float(target);
+      bool snap;
+      uint32_t code;
+      if (MODE == kModeB) {
+        const uint32_t bucket = found != 0xFFFFFFFFu ? M : (__float_as_uint(best_v) >> 16);
+        code = found != 0xFFFFFFFFu ? found : best_code;
+        snap = !(best_v > 0.f) || bucket < 0x4000u;  // bf16 max below 2.0
+      } else {
+        code = best_code;
+        snap = !(2.0f * best_v >= __uint_as_float(kCSqNormBits));
       }
-      if (v > 0.f) {
-        key_hi = MODE == kModeB ? (__float_as_uint(v) >> 16) : __float_as_uint(v);
-        key_lo = 0xFFFFFFFFu - code;
-      }
+      id = snap ? 0 : static_cast<int32_t>(code) + 1;
     }
-    // merge the four lanes of atom j: max of (key_hi, key_lo) lexicographically
-#pragma unroll
-    for (int off = 16; off <= 32; off <<= 1) {
-      const uint32_t oh = static_cast<uint32_t>(__shfl_xor(static_cast<int>(key_hi), off, 64));
-      const uint32_t ol = static_cast<uint32_t>(__shfl_xor(static_cast<int>(key_lo), off, 64));
-      if (oh > key_hi || (oh == key_hi && ol > key_lo)) {
-        key_hi = oh;
-        key_lo = ol;
-      }
-    }
-    if (q == 0 && a < n_atoms && (key_hi | key_lo) != 0u)
-      atomicMax(keys + a, (static_cast<unsigned long long>(key_hi) << 32) | key_lo);
-  }
-}
-
-__global__ void fill_u64_kernel(unsigned long long *__restrict__ p, int64_t n) {
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (i < n) p[i] = 0ull;
-}
-
-// keys -> int32 indices (and optionally the packed 9-byte groups); one thread per group of 4 atoms.
-template <int MODE>
-__global__ __launch_bounds__(256) void finalize_kernel(const unsigned long long *__restrict__ keys, int64_t n,
-                                                       int32_t *__restrict__ idx_out,
-                                                       uint8_t *__restrict__ packed_out, int64_t n_groups) {
-  __shared__ __align__(16) uint8_t lds[256 * 9];
-  const int64_t g0 = static_cast<int64_t>(blockIdx.x) * 256;
-  const int64_t g = g0 + threadIdx.x;
-  if (g < n_groups) {
-    int32_t v[4];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const int64_t a = g * 4 + k;
-      int32_t id = 0;
-      if (a < n) {
-        const unsigned long long key = keys[a];
-        const uint32_t hi = static_cast<uint32_t>(key >> 32);
-        const uint32_t code = 0xFFFFFFFFu - static_cast<uint32_t>(key);
-        bool snap = key == 0ull;
-        if (!snap) {
-          if (MODE == kModeB)
-            snap = hi < 0x4000u;  // bf16 max below 2.0
-          else
-            snap = 2.0f * __uint_as_float(hi) < __uint_as_float(kCSqNormBits);
-        }
-        id = snap ? 0 : static_cast<int32_t>(code) + 1;
-        idx_out[a] = id;
-      }
-      v[k] = id;
-    }
-    if (packed_out) group_to_bytes(v[0], v[1], v[2], v[3], lds + threadIdx.x * 9);
+    idx_out[a] = id;
   }
   if (!packed_out) return;
+  ids[threadIdx.x] = id;
   __syncthreads();
-  const int64_t groups_here = min(static_cast<int64_t>(256), n_groups - g0);
+  const int64_t n_groups = (n_atoms + 3) / 4;
+  const int64_t g0 = a0 / 4;
+  const int64_t groups_here = min(static_cast<int64_t>(64), n_groups - g0);
+  if (threadIdx.x < groups_here) {
+    const int i = threadIdx.x * 4;
+    group_to_bytes(ids[i], ids[i + 1], ids[i + 2], ids[i + 3], bytes + threadIdx.x * 9);
+  }
+  __syncthreads();
   uint8_t *dst = packed_out + g0 * 9;
-  if (groups_here == 256 && aligned16(packed_out)) {
-    if (threadIdx.x < 144) reinterpret_cast<uint4 *>(dst)[threadIdx.x] = reinterpret_cast<const uint4 *>(lds)[threadIdx.x];
+  if (groups_here == 64 && aligned16(packed_out)) {
+    if (threadIdx.x < 36) reinterpret_cast<uint4 *>(dst)[threadIdx.x] = reinterpret_cast<const uint4 *>(bytes)[threadIdx.x];
   } else {
     const int nb = static_cast<int>(groups_here * 9);
-    for (int i = threadIdx.x; i < nb; i += 256) dst[i] = lds[i];
+    for (int i = threadIdx.x; i < nb; i += 256) dst[i] = bytes[i];
   }
 }
 
@@ -351,80 +417,71 @@ __global__ __launch_bounds__(256) void gather_kernel(const int32_t *__restrict__
   }
 }
 
+// Codebook slices per launch: 8 keeps each XCD on its own 1.18 MB of the bf16
+// codebook (L2-resident); small launches use more slices so the grid still
+// has several waves of work-groups per CU slot.
 int choose_slices(int64_t ablocks) {
   int s = 8;
-  while (s < 64 && ablocks * s < 2048) s *= 2;
+  while (s < 64 && ablocks * s < 6144) s *= 2;
   return s;
 }
 
-}  // namespace
-
-size_t quantize_workspace_bytes(int64_t n_atoms) {
-  return static_cast<size_t>((n_atoms * 8 + 255) / 256 * 256);
-}
-
-int launch_quantize(const float *x, const float *sigma, int64_t rows, int64_t cols, int64_t n_atoms, int mode,
-                    int32_t *idx_out, uint8_t *packed_out, float *weight_out, void *workspace,
-                    size_t workspace_bytes, hipStream_t s) {
-  if (n_atoms <= 0) return PLX_OK;
-  if (workspace == nullptr || workspace_bytes < quantize_workspace_bytes(n_atoms))
-    return fail(PLX_EINVAL, "quantize: workspace of %zu bytes is smaller than the %zu needed for %lld atoms",
-                workspace_bytes, quantize_workspace_bytes(n_atoms), static_cast<long long>(n_atoms));
-  if ((reinterpret_cast<uintptr_t>(x) & 15u) != 0)
-    return fail(PLX_EINVAL, "quantize: input must be 16-byte aligned");
-  const DeviceTables *tab = nullptr;
-  int st = get_tables(&tab);
-  if (st != PLX_OK) return st;
-
-  unsigned long long *keys = static_cast<unsigned long long *>(workspace);
-  hipLaunchKernelGGL(fill_u64_kernel, dim3(static_cast<unsigned>((n_atoms + 255) / 256)), dim3(256), 0, s, keys,
-                     n_atoms);
-  if ((st = check_launch("fill_u64_kernel")) != PLX_OK) return st;
-
+template <int MODE, bool FUSED>
+int launch_mode(const float *x, const float *sigma, int64_t apr, int64_t n_atoms, const DeviceTables *tab,
+                int32_t *idx_out, uint8_t *packed_out, uint4 *records, hipStream_t s) {
   const int64_t ablocks = (n_atoms + kAtomsPerBlock - 1) / kAtomsPerBlock;
   const int n_slices = choose_slices(ablocks);
   const int tiles_per_slice = kPaddedTiles / n_slices;
   const int64_t grid = ablocks * n_slices;
   if (grid > 0x7FFFFFFFll) return fail(PLX_EINVAL, "quantize: %lld atoms exceed one launch", static_cast<long long>(n_atoms));
+  profile_before(s);
+  hipLaunchKernelGGL((nn_kernel<MODE, FUSED>), dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0, s, x, sigma, apr,
+                     n_atoms, tab->kp_bf16_tiles, n_slices, tiles_per_slice, records);
+  int st = check_launch("nn_kernel");
+  if (st != PLX_OK) return st;
+  profile_after(s);
+  hipLaunchKernelGGL((resolve_kernel<MODE, FUSED>), dim3(static_cast<unsigned>((n_atoms + 255) / 256)), dim3(256), 0, s,
+                     records, n_slices, n_atoms, x, sigma, apr, tab->kp_bf16_lanes, idx_out, packed_out);
+  return check_launch("resolve_kernel");
+}
+
+}  // namespace
+
+size_t quantize_workspace_bytes(int64_t n_atoms) {
+  if (n_atoms <= 0) return 0;
+  const int64_t ablocks = (n_atoms + kAtomsPerBlock - 1) / kAtomsPerBlock;
+  return static_cast<size_t>(n_atoms) * static_cast<size_t>(choose_slices(ablocks)) * sizeof(uint4);
+}
+
+int launch_quantize(const float *x, const float *sigma, int64_t rows, int64_t cols, int64_t n_atoms, int mode,
+                    int32_t *idx_out, uint8_t *packed_out, float *weight_out, void *workspace,
+                    size_t workspace_bytes, hipStream_t s) {
+  (void)rows;
+  if (n_atoms <= 0) return PLX_OK;
+  if (workspace == nullptr || workspace_bytes < quantize_workspace_bytes(n_atoms))
+    return fail(PLX_EINVAL, "quantize: workspace of %zu bytes is smaller than the %zu needed for %lld atoms",
+                workspace_bytes, quantize_workspace_bytes(n_atoms), static_cast<long long>(n_atoms));
+  if ((reinterpret_cast<uintptr_t>(x) & 15u) != 0 || (reinterpret_cast<uintptr_t>(workspace) & 15u) != 0)
+    return fail(PLX_EINVAL, "quantize: input and workspace must be 16-byte aligned");
+  const DeviceTables *tab = nullptr;
+  int st = get_tables(&tab);
+  if (st != PLX_OK) return st;
+  uint4 *records = static_cast<uint4 *>(workspace);
   const bool fused = sigma != nullptr;
   const int64_t apr = cols / kDim;
-  const dim3 g(static_cast<unsigned>(grid)), b(kThreads);
-  profile_before(s);
-  if (mode == PLX_NN_BF16_SCORES) {
-    if (fused)
-      hipLaunchKernelGGL((nn_kernel<PLX_NN_BF16_SCORES, true>), g, b, 0, s, x, sigma, apr, n_atoms, tab->kp_bf16_tiles,
-                         tab->cb_raw, n_slices, tiles_per_slice, keys);
-    else
-      hipLaunchKernelGGL((nn_kernel<PLX_NN_BF16_SCORES, false>), g, b, 0, s, x, sigma, apr, n_atoms,
-                         tab->kp_bf16_tiles, tab->cb_raw, n_slices, tiles_per_slice, keys);
-  } else {
-    if (fused)
-      hipLaunchKernelGGL((nn_kernel<PLX_NN_FP32_SCORES, true>), g, b, 0, s, x, sigma, apr, n_atoms, tab->kp_bf16_tiles,
-                         tab->cb_raw, n_slices, tiles_per_slice, keys);
-    else
-      hipLaunchKernelGGL((nn_kernel<PLX_NN_FP32_SCORES, false>), g, b, 0, s, x, sigma, apr, n_atoms,
-                         tab->kp_bf16_tiles, tab->cb_raw, n_slices, tiles_per_slice, keys);
-  }
-  if ((st = check_launch("nn_kernel")) != PLX_OK) return st;
-  profile_after(s);
-
-  const int64_t n_groups = (n_atoms + 3) / 4;
-  const dim3 fg(static_cast<unsigned>((n_groups + 255) / 256));
   if (mode == PLX_NN_BF16_SCORES)
-    hipLaunchKernelGGL(finalize_kernel<PLX_NN_BF16_SCORES>, fg, dim3(256), 0, s, keys, n_atoms, idx_out, packed_out,
-                       n_groups);
+    st = fused ? launch_mode<PLX_NN_BF16_SCORES, true>(x, sigma, apr, n_atoms, tab, idx_out, packed_out, records, s)
+               : launch_mode<PLX_NN_BF16_SCORES, false>(x, sigma, apr, n_atoms, tab, idx_out, packed_out, records, s);
   else
-    hipLaunchKernelGGL(finalize_kernel<PLX_NN_FP32_SCORES>, fg, dim3(256), 0, s, keys, n_atoms, idx_out, packed_out,
-                       n_groups);
-  if ((st = check_launch("finalize_kernel")) != PLX_OK) return st;
-
+    st = fused ? launch_mode<PLX_NN_FP32_SCORES, true>(x, sigma, apr, n_atoms, tab, idx_out, packed_out, records, s)
+               : launch_mode<PLX_NN_FP32_SCORES, false>(x, sigma, apr, n_atoms, tab, idx_out, packed_out, records, s);
+  if (st != PLX_OK) return st;
   if (weight_out) {
     const dim3 gg(static_cast<unsigned>((n_atoms * 6 + 255) / 256));
     hipLaunchKernelGGL((gather_kernel<0, true>), gg, dim3(256), 0, s, idx_out, n_atoms, tab->cb_raw, sigma, apr,
                        static_cast<void *>(weight_out));
     if ((st = check_launch("gather_kernel")) != PLX_OK) return st;
   }
-  (void)rows;
   return PLX_OK;
 }
 

@@ -4,6 +4,9 @@
 //                to bf16 exactly as the reference's bf16 casts round them
 //                (castor.py:437, autocast at castor.py:552), in the MFMA tile
 //                layout of quantize.hip; 12288 tiles x 768 B = 9,437,184 B.
+// kp_bf16_lanes  the same bf16 values regrouped lane-major ([q][tile][4][24],
+//                rows 4q..4q+3 of each tile) so the resolve kernel reads one
+//                lane's 32 codes of a group as 1.5 KB contiguous; 9,437,184 B.
 // cb_raw         the raw int8 coordinates of all 196,561 rows (4,717,464 B);
 //                decoded per value into fp32 / bf16 / fp16 by the kernels.
 
@@ -43,22 +46,38 @@ int build(int dev, DeviceTables *t) {
           tiles[static_cast<size_t>(tile) * 384 + p * 128 + i * 8 + e] = bf_of[k + 4];
         }
 
+  // lane-major copy for the resolve kernel: [q][tile][e][24], row = 4q + e
+  std::vector<uint16_t> lanes(static_cast<size_t>(4) * kPaddedTiles * 4 * kDim, 0);
+  for (int q = 0; q < 4; ++q)
+    for (int tile = 0; tile < kRealTiles; ++tile)
+      for (int e = 0; e < 4; ++e) {
+        const int code = tile * kTileCodes + 4 * q + e + 1;
+        uint16_t *dst = lanes.data() + ((static_cast<size_t>(q) * kPaddedTiles + tile) * 4 + e) * kDim;
+        for (int c = 0; c < kDim; ++c) dst[c] = bf_of[raw[static_cast<size_t>(code) * kDim + c] + 4];
+      }
+
   const size_t tile_bytes = tiles.size() * 2;
+  const size_t lane_bytes = lanes.size() * 2;
   const size_t raw_bytes = static_cast<size_t>(kCodebook) * kDim;
-  void *dt = nullptr, *dr = nullptr;
-  if (hipMalloc(&dt, tile_bytes) != hipSuccess) return fail(PLX_ENOMEM, "hipMalloc(%zu) failed on device %d", tile_bytes, dev);
-  if (hipMalloc(&dr, raw_bytes) != hipSuccess) {
-    (void)hipFree(dt);
-    return fail(PLX_ENOMEM, "hipMalloc(%zu) failed on device %d", raw_bytes, dev);
+  void *dt = nullptr, *dl = nullptr, *dr = nullptr;
+  if (hipMalloc(&dt, tile_bytes) != hipSuccess || hipMalloc(&dl, lane_bytes) != hipSuccess ||
+      hipMalloc(&dr, raw_bytes) != hipSuccess) {
+    if (dt) (void)hipFree(dt);
+    if (dl) (void)hipFree(dl);
+    return fail(PLX_ENOMEM, "device table allocation (%zu B) failed on device %d", tile_bytes + lane_bytes + raw_bytes,
+                dev);
   }
   int st = check_hip(hipMemcpy(dt, tiles.data(), tile_bytes, hipMemcpyHostToDevice), "upload codebook tiles");
+  if (st == PLX_OK) st = check_hip(hipMemcpy(dl, lanes.data(), lane_bytes, hipMemcpyHostToDevice), "upload lane table");
   if (st == PLX_OK) st = check_hip(hipMemcpy(dr, raw, raw_bytes, hipMemcpyHostToDevice), "upload raw codebook");
   if (st != PLX_OK) {
     (void)hipFree(dt);
+    (void)hipFree(dl);
     (void)hipFree(dr);
     return st;
   }
   t->kp_bf16_tiles = static_cast<uint8_t *>(dt);
+  t->kp_bf16_lanes = static_cast<uint8_t *>(dl);
   t->cb_raw = static_cast<int8_t *>(dr);
   t->device = dev;
   return PLX_OK;
