@@ -141,6 +141,12 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true")
     ap.add_argument("--mode", default="bf16", choices=["bf16", "fp32"])
+    ap.add_argument(
+        "--pmc-workload",
+        action="store_true",
+        help="for rocprofv3 --pmc runs: 5 copies of a 256 MiB fp32 tensor (HBM-counter calibration), then "
+        "--steps config-2 steps; prints nothing",
+    )
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -169,6 +175,16 @@ def main() -> int:
     def step():
         for w in mats:
             castor.requantize_h24(w, mode=args.mode)
+
+    if args.pmc_workload:
+        src = torch.ones(64 * 1024 * 1024, dtype=torch.float32, device=dev)  # 256 MiB
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        for _ in range(args.steps):
+            step()
+        torch.cuda.synchronize()
+        return 0
 
     log(f"[bench] warmup {args.warmup} steps, workload config 2 ({atoms} atoms/step)")
     for _ in range(args.warmup):
