@@ -122,6 +122,46 @@ def extras(device, iters=20):
     return out
 
 
+def gemv_extras(device, copies=200, m_gemm=64):
+    """Config 5: fused dequant-GEMV (M=1) and dequant-GEMM (M=64) on [7680,1920] and [1920,7680].
+
+    Each timing cycles through `copies` distinct packed weights (>= 256 MB in
+    total, above the 256 MB Infinity Cache) so the compressed stream is read
+    from HBM; HIP events on the launch stream bracket the whole loop.
+    """
+    import torch
+
+    from pollux_amd import dequant_linear
+
+    out = {}
+    for name, (of, inf) in (("up_7680x1920", (7680, 1920)), ("down_1920x7680", (1920, 7680))):
+        g = torch.Generator(device=device).manual_seed(of)
+        n_atoms = of * inf // 24
+        nbytes = (n_atoms + 3) // 4 * 9
+        pk = torch.randint(0, 256, (copies, nbytes), generator=g, device=device, dtype=torch.uint8)
+        sg = (torch.rand(copies, of, generator=g, device=device) * 0.045 + 0.005).half()
+        for m in (1, m_gemm):
+            x = torch.randn(m, inf, generator=g, device=device).to(torch.bfloat16)
+            for i in range(3):
+                dequant_linear(pk[i], sg[i], of, inf, x)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for i in range(copies):
+                dequant_linear(pk[i], sg[i], of, inf, x)
+            e1.record()
+            e1.synchronize()
+            t = e0.elapsed_time(e1) / 1e3 / copies
+            comp = nbytes + 2 * of + 2 * m * inf + 4 * m * of
+            key = f"{name}_M{m}"
+            out[f"{key}_us"] = t * 1e6
+            out[f"{key}_compressed_GBps"] = comp / t / 1e9
+            out[f"{key}_dense_equiv_GBps"] = (2 * of * inf) / t / 1e9
+            out[f"{key}_TFLOPs"] = 2 * m * of * inf / t / 1e12
+    out["note"] = (f"{copies} rotating packed copies per matrix ({copies} x 1.38 MB); compressed bytes = packed + "
+                   "sigma16 + x bf16 + y fp32; dense-equivalent = fp16 weight bytes")
+    return out
+
+
 def traffic_from_profiles():
     p = ROOT / "profiles" / "nn_kernel_c2_traffic.json"
     if p.exists():
@@ -245,8 +285,9 @@ def main() -> int:
         "roofline": roofline,
     }
     if not args.no_extras:
-        log("[bench] extras: pack / unpack / dequant at config-4 scale")
+        log("[bench] extras: pack / unpack / dequant at config-4 scale; dequant-GEMV/GEMM at config 5")
         result["extras"] = extras(dev)
+        result["extras"]["dequant_linear"] = gemv_extras(dev)
     if not args.no_cpu_baseline:
         log(f"[bench] CPU baseline on {args.cpu_atoms} atoms")
         result["cpu_baseline"] = cpu_baseline(mats, args.cpu_atoms)

@@ -131,6 +131,15 @@ int plx_requantize(const float *latent, int64_t rows, int64_t cols, int mode,
 int plx_dequant_f16(const uint8_t *packed, int64_t n_packed_bytes, const uint16_t *sigma16,
                     int64_t rows, int64_t cols, uint16_t *w16_out, void *stream);
 
+/* y[m, r] = sum_i x[m, i] * W[r, i] for m < m_rows, with W the fp16
+ * materialisation of (packed, sigma16) above, never stored: x is bf16
+ * (x_is_f32 = 0) or fp32 (x_is_f32 = 1) [m_rows, cols], y fp32 [m_rows, rows],
+ * fp32 accumulation.  Replaces PackedH24Linear.forward after materialize
+ * (pollux.py:506-507: F.linear(x, weight.to(x.dtype))), evaluated in fp32. */
+int plx_dequant_linear(const uint8_t *packed, int64_t n_packed_bytes, const uint16_t *sigma16,
+                       int64_t rows, int64_t cols, const void *x, int x_is_f32, int64_t m_rows,
+                       float *y, void *stream);
+
 /* ---- kernel timing (diagnostics; no counterpart in the reference) ------ */
 /* While enabled, every launch of the quantizer's scoring kernel (nn_kernel)
  * is bracketed by HIP events recorded on its launch stream (up to 4096

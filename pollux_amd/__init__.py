@@ -9,6 +9,6 @@ build    builds lib/libpollux_amd.so (hipcc, gfx950) in-tree
 """
 
 from . import castor  # noqa: F401
-from .packed import PackedH24Linear, dequantize_h24  # noqa: F401
+from .packed import PackedH24Linear, dequant_linear, dequantize_h24  # noqa: F401
 
-__all__ = ["castor", "PackedH24Linear", "dequantize_h24"]
+__all__ = ["castor", "PackedH24Linear", "dequant_linear", "dequantize_h24"]

@@ -174,4 +174,18 @@ int plx_dequant_f16(const uint8_t *packed, int64_t n_packed_bytes, const uint16_
   return launch_dequant_f16(packed, sigma16, rows, cols, w16_out, as_stream(stream));
 }
 
+int plx_dequant_linear(const uint8_t *packed, int64_t n_packed_bytes, const uint16_t *sigma16, int64_t rows,
+                       int64_t cols, const void *x, int x_is_f32, int64_t m_rows, float *y, void *stream) {
+  PLX_REQUIRE(rows >= 0 && cols > 0 && cols % kDim == 0, "plx_dequant_linear: bad shape (%lld, %lld)",
+              static_cast<long long>(rows), static_cast<long long>(cols));
+  PLX_REQUIRE(m_rows >= 0, "plx_dequant_linear: negative batch");
+  const int64_t n_atoms = rows * (cols / kDim);
+  PLX_REQUIRE(n_packed_bytes == ((n_atoms + 3) / 4) * 9,
+              "plx_dequant_linear: packed length %lld does not match %lld atoms", static_cast<long long>(n_packed_bytes),
+              static_cast<long long>(n_atoms));
+  if (rows == 0 || m_rows == 0) return PLX_OK;
+  PLX_REQUIRE(packed != nullptr && sigma16 != nullptr && x != nullptr && y != nullptr, "plx_dequant_linear: null pointer");
+  return launch_dequant_linear(packed, sigma16, rows, cols, x, x_is_f32, m_rows, y, as_stream(stream));
+}
+
 }  // extern "C"

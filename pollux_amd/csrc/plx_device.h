@@ -21,6 +21,23 @@ __device__ __forceinline__ float raw_value_f32(int k) {
   return static_cast<float>(k) * __uint_as_float(kLeechScaleBits);
 }
 
+// fp16 bits of the materialised weight for raw coordinate k and row scale sig
+// (pollux.py:492-499): fp16(fp32(fp16(cb16[k] * sig)) * fp32(1/sqrt 2)), both
+// products in fp32 then rounded to fp16, cb16 = fp16(k * fp32(1/sqrt 8)).
+__device__ __forceinline__ uint32_t dq_value(int k, float sig, float sl) {
+  const float c16 = __half2float(__float2half_rn(raw_value_f32(k)));
+  const float t = __half2float(__float2half_rn(c16 * sig));
+  return __half_as_ushort(__float2half_rn(t * sl));
+}
+
+// Index n of a packed stream: 18 bits at bit 18*(n%4) of group n/4, read as
+// the 24-bit big-endian window starting at byte 9*(n/4) + 2*(n%4).
+__device__ __forceinline__ int32_t packed_index(const uint8_t *__restrict__ packed, int64_t n) {
+  const uint8_t *b = packed + (n >> 2) * 9 + 2 * (n & 3);
+  const uint32_t v = (static_cast<uint32_t>(b[0]) << 16) | (static_cast<uint32_t>(b[1]) << 8) | b[2];
+  return static_cast<int32_t>((v >> (6 - 2 * (n & 3))) & 0x3FFFFu);
+}
+
 // Four 18-bit indices -> one 9-byte big-endian group (castor.py:237-245).
 __device__ __forceinline__ void group_to_bytes(int32_t i0, int32_t i1, int32_t i2, int32_t i3, uint8_t *b) {
   b[0] = static_cast<uint8_t>(i0 >> 10);

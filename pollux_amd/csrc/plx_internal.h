@@ -36,6 +36,7 @@ struct DeviceTables {
   uint8_t *kp_bf16_tiles = nullptr;  // [kPaddedTiles][3][16][8] bf16 bits (MFMA A-operand layout)
   uint8_t *kp_bf16_lanes = nullptr;  // [4][kPaddedTiles][4][24] bf16 bits (rows 4q..4q+3 of each tile, lane-major)
   int8_t *cb_raw = nullptr;          // [kCodebook][24] raw integer coordinates
+  uint8_t *kp_gemv = nullptr;        // [kCodebook] x 16 B: 24 signed nibbles + (type | pos << 8)
 };
 
 // Host generator (codebook.cpp): raw coordinates, origin first, sorted.
@@ -67,5 +68,7 @@ size_t quantize_workspace_bytes(int64_t n_atoms);
 int launch_gather(const int32_t *idx, int64_t n, int out_dtype, void *out, hipStream_t s);
 int launch_dequant_f16(const uint8_t *packed, const uint16_t *sigma16, int64_t rows, int64_t cols,
                        uint16_t *w16, hipStream_t s);
+int launch_dequant_linear(const uint8_t *packed, const uint16_t *sigma16, int64_t rows, int64_t cols, const void *x,
+                          int x_is_f32, int64_t m, float *y, hipStream_t s);
 
 }  // namespace plx

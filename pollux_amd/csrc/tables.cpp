@@ -9,6 +9,10 @@
 //                lane's 32 codes of a group as 1.5 KB contiguous; 9,437,184 B.
 // cb_raw         the raw int8 coordinates of all 196,561 rows (4,717,464 B);
 //                decoded per value into fp32 / bf16 / fp16 by the kernels.
+// kp_gemv        per code 16 B for the fused dequant-linear: the 24 raw
+//                coordinates as signed 4-bit fields, then type (0 origin,
+//                1 = +-4 pair, 2 = +-2 octad, 3 = one -3) | position of -3 << 8
+//                (3,144,976 B).
 
 #include <cstring>
 #include <mutex>
@@ -56,29 +60,49 @@ int build(int dev, DeviceTables *t) {
         for (int c = 0; c < kDim; ++c) dst[c] = bf_of[raw[static_cast<size_t>(code) * kDim + c] + 4];
       }
 
+  // dequant-linear entries: 24 signed 4-bit coordinates, then type | pos << 8
+  std::vector<uint32_t> gemv(static_cast<size_t>(kCodebook) * 4, 0);
+  for (int code = 0; code < kCodebook; ++code) {
+    const int8_t *r = raw + static_cast<size_t>(code) * kDim;
+    uint32_t *e = gemv.data() + static_cast<size_t>(code) * 4;
+    int nz = 0, pos = 0;
+    for (int c = 0; c < kDim; ++c) {
+      e[c / 8] |= (static_cast<uint32_t>(r[c]) & 0xFu) << (4 * (c % 8));
+      nz += r[c] != 0;
+      if (r[c] == -3) pos = c;
+    }
+    const uint32_t type = nz == 0 ? 0u : nz == 2 ? 1u : nz == 8 ? 2u : 3u;
+    e[3] = type | (static_cast<uint32_t>(pos) << 8);
+  }
+
   const size_t tile_bytes = tiles.size() * 2;
   const size_t lane_bytes = lanes.size() * 2;
+  const size_t gemv_bytes = gemv.size() * 4;
   const size_t raw_bytes = static_cast<size_t>(kCodebook) * kDim;
-  void *dt = nullptr, *dl = nullptr, *dr = nullptr;
+  void *dt = nullptr, *dl = nullptr, *dr = nullptr, *dg = nullptr;
   if (hipMalloc(&dt, tile_bytes) != hipSuccess || hipMalloc(&dl, lane_bytes) != hipSuccess ||
-      hipMalloc(&dr, raw_bytes) != hipSuccess) {
+      hipMalloc(&dr, raw_bytes) != hipSuccess || hipMalloc(&dg, gemv_bytes) != hipSuccess) {
     if (dt) (void)hipFree(dt);
     if (dl) (void)hipFree(dl);
-    return fail(PLX_ENOMEM, "device table allocation (%zu B) failed on device %d", tile_bytes + lane_bytes + raw_bytes,
-                dev);
+    if (dr) (void)hipFree(dr);
+    return fail(PLX_ENOMEM, "device table allocation (%zu B) failed on device %d",
+                tile_bytes + lane_bytes + raw_bytes + gemv_bytes, dev);
   }
   int st = check_hip(hipMemcpy(dt, tiles.data(), tile_bytes, hipMemcpyHostToDevice), "upload codebook tiles");
   if (st == PLX_OK) st = check_hip(hipMemcpy(dl, lanes.data(), lane_bytes, hipMemcpyHostToDevice), "upload lane table");
   if (st == PLX_OK) st = check_hip(hipMemcpy(dr, raw, raw_bytes, hipMemcpyHostToDevice), "upload raw codebook");
+  if (st == PLX_OK) st = check_hip(hipMemcpy(dg, gemv.data(), gemv_bytes, hipMemcpyHostToDevice), "upload gemv table");
   if (st != PLX_OK) {
     (void)hipFree(dt);
     (void)hipFree(dl);
     (void)hipFree(dr);
+    (void)hipFree(dg);
     return st;
   }
   t->kp_bf16_tiles = static_cast<uint8_t *>(dt);
   t->kp_bf16_lanes = static_cast<uint8_t *>(dl);
   t->cb_raw = static_cast<int8_t *>(dr);
+  t->kp_gemv = static_cast<uint8_t *>(dg);
   t->device = dev;
   return PLX_OK;
 }

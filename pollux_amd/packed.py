@@ -5,7 +5,8 @@ state-dict keys, ``materialize()`` and ``forward()`` as the reference, so
 ``PolluxModel.from_packed_checkpoint`` (pollux.py:704-752) can build it
 unchanged.  ``materialize`` runs the fused unpack + LUT-gather + row-scale
 kernel (plx_dequant_f16) instead of unpack_indices -> index_select -> two
-broadcast multiplies.
+broadcast multiplies.  Before ``materialize`` (or without it), ``forward``
+runs the fused dequant-linear kernel on the packed weights directly.
 """
 
 from __future__ import annotations
@@ -39,6 +40,40 @@ def dequantize_h24(packed: torch.Tensor, sigma16: torch.Tensor, out_features: in
     return out
 
 
+def dequant_linear(
+    packed: torch.Tensor, sigma16: torch.Tensor, out_features: int, in_features: int, x: torch.Tensor
+) -> torch.Tensor:
+    """F.linear(x, materialize(W).float()) in fp32 without materialising W (pollux.py:491-507).
+
+    x: [..., in] bf16 or fp32 (other float dtypes are cast to fp32); returns fp32 [..., out].
+    """
+    _lib.require_device(packed, "dequant_linear packed input")
+    if packed.dtype != torch.uint8 or sigma16.dtype != torch.float16:
+        raise ValueError("packed weights must be uint8 and sigma rows float16")
+    assert_row_aligned_in_features(in_features)
+    if x.shape[-1] != in_features:
+        raise ValueError(f"x has {x.shape[-1]} features, layer expects {in_features}")
+    lead = x.shape[:-1]
+    xx = x.reshape(-1, in_features)
+    if xx.dtype not in (torch.bfloat16, torch.float32):
+        xx = xx.float()
+    xx = xx.contiguous()
+    pk = packed.reshape(-1).contiguous()
+    if pk.data_ptr() % 16:
+        pk = pk.clone()  # the kernel streams the packed bytes as aligned 16-byte vectors
+    if xx.data_ptr() % 16:
+        xx = xx.clone()
+    sg = sigma16.reshape(-1).contiguous()
+    y = torch.empty((xx.shape[0], out_features), dtype=torch.float32, device=pk.device)
+    with torch.cuda.device(pk.device):
+        st = _lib.lib().plx_dequant_linear(
+            _lib.ptr(pk), pk.numel(), _lib.ptr(sg), out_features, in_features, _lib.ptr(xx),
+            int(xx.dtype == torch.float32), xx.shape[0], _lib.ptr(y), _lib.stream_of(pk.device),
+        )
+    _lib.check(st, "dequant_linear")
+    return y.reshape(*lead, out_features)
+
+
 class PackedH24Linear(nn.Module):
     """uint8 packed 18-bit indices + fp16 row scale; dense fp16 weight after materialize()."""
 
@@ -68,4 +103,8 @@ class PackedH24Linear(nn.Module):
         self._materialized = True
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if not self._materialized:
+            # fused path: weights stay packed (0.76 bits/param); fp32 result cast to x's dtype
+            y = dequant_linear(self.packed_weights, self.sigma_rows, self.out_features, self.in_features, x).to(x.dtype)
+            return y if self.bias is None else y + self.bias.to(x.dtype)
         return F.linear(x, self.weight.to(dtype=x.dtype), self.bias)
