@@ -15,6 +15,7 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kBlockBytes = kThreads * 9;  // 2304 = 144 * 16
+typedef int64_t i64x2_t __attribute__((ext_vector_type(2)));
 
 template <bool I64>
 __global__ __launch_bounds__(kThreads) void pack_kernel(const void *__restrict__ idx, int64_t n,
@@ -83,20 +84,25 @@ __global__ __launch_bounds__(kThreads) void unpack_kernel(const uint8_t *__restr
     for (int i = threadIdx.x; i < nb; i += kThreads) lds[i] = src[i];
   }
   __syncthreads();
-  const int64_t g = g0 + threadIdx.x;
-  if (g >= n_groups) return;
-  int32_t iv[4];
-  bytes_to_group(lds + threadIdx.x * 9, iv);
-  const int64_t i0 = iv[0], i1 = iv[1], i2 = iv[2], i3 = iv[3];
-  const int64_t base = g * 4;
-  if (base + 4 <= num_indices && vec_ok) {
-    longlong2 *p = reinterpret_cast<longlong2 *>(out + base);
-    p[0] = make_longlong2(i0, i1);
-    p[1] = make_longlong2(i2, i3);
-  } else {
-    const int64_t v[4] = {i0, i1, i2, i3};
-    for (int k = 0; k < 4; ++k)
-      if (base + k < num_indices) out[base + k] = v[k];
+  // Thread t writes index pairs t and t + 256 of the block (16 B each), so
+  // every store instruction covers 1 KiB contiguous; non-temporal, since the
+  // int64 stream is not read back by this kernel.
+  const int64_t i_blk = g0 * 4;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int pr = h * kThreads + threadIdx.x;
+    const int64_t base = i_blk + 2 * pr;
+    if (base >= num_indices) break;
+    int32_t iv[4];
+    bytes_to_group(lds + (pr >> 1) * 9, iv);
+    const int64_t lo = (pr & 1) ? iv[2] : iv[0], hi = (pr & 1) ? iv[3] : iv[1];
+    if (base + 2 <= num_indices && vec_ok) {
+      const i64x2_t v = {lo, hi};
+      __builtin_nontemporal_store(v, reinterpret_cast<i64x2_t *>(out + base));
+    } else {
+      out[base] = lo;
+      if (base + 1 < num_indices) out[base + 1] = hi;
+    }
   }
 }
 

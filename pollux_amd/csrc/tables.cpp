@@ -13,6 +13,13 @@
 //                coordinates as signed 4-bit fields, then type (0 origin,
 //                1 = +-4 pair, 2 = +-2 octad, 3 = one -3) | position of -3 << 8
 //                (3,144,976 B).
+// kp_dq          per code 3 words for the dequant kernel: the raw alphabet
+//                {0,1,2,4,-4,-3,-2,-1} (there is no +3) as value ids 0..7,
+//                word p byte i = id(coord 8p+i) | id(coord 8p+4+i) << 4, the
+//                order v_perm_b32 lookups want (2,358,732 B).
+// kp_raw_tiles   the raw integer coordinates (exact in bf16) in the MFMA tile
+//                layout of kp_bf16_tiles, for the fp32-exact NN-P scoring
+//                (9,437,184 B).
 
 #include <cstring>
 #include <mutex>
@@ -60,49 +67,75 @@ int build(int dev, DeviceTables *t) {
         for (int c = 0; c < kDim; ++c) dst[c] = bf_of[raw[static_cast<size_t>(code) * kDim + c] + 4];
       }
 
+  // raw-integer tiles (NN-P): same layout, value k as bf16
+  std::vector<uint16_t> raw_tiles(tiles.size(), 0);
+  for (int tile = 0; tile < kRealTiles; ++tile)
+    for (int p = 0; p < 3; ++p)
+      for (int i = 0; i < kTileCodes; ++i)
+        for (int e = 0; e < 8; ++e) {
+          const int code = tile * kTileCodes + i + 1;
+          const float k = static_cast<float>(raw[static_cast<size_t>(code) * kDim + 8 * p + e]);
+          raw_tiles[static_cast<size_t>(tile) * 384 + p * 128 + i * 8 + e] = f32_to_bf16_rne(k);
+        }
+
   // dequant-linear entries: 24 signed 4-bit coordinates, then type | pos << 8
   std::vector<uint32_t> gemv(static_cast<size_t>(kCodebook) * 4, 0);
+  // dequant value ids (raw k -> id): 0->0 1->1 2->2 4->3 -4->4 -3->5 -2->6 -1->7
+  static const uint32_t kId[9] = {4, 5, 6, 7, 0, 1, 2, 0xFF, 3};
+  std::vector<uint32_t> dq(static_cast<size_t>(kCodebook) * 3, 0);
   for (int code = 0; code < kCodebook; ++code) {
     const int8_t *r = raw + static_cast<size_t>(code) * kDim;
     uint32_t *e = gemv.data() + static_cast<size_t>(code) * 4;
+    uint32_t *d = dq.data() + static_cast<size_t>(code) * 3;
     int nz = 0, pos = 0;
     for (int c = 0; c < kDim; ++c) {
       e[c / 8] |= (static_cast<uint32_t>(r[c]) & 0xFu) << (4 * (c % 8));
       nz += r[c] != 0;
       if (r[c] == -3) pos = c;
+      const uint32_t id = kId[r[c] + 4];
+      if (id > 7) return fail(PLX_EINVAL, "codebook coordinate %d outside the dequant alphabet", r[c]);
+      const int p = c / 8, w = c % 8;
+      d[p] |= id << (8 * (w % 4) + 4 * (w / 4));
     }
     const uint32_t type = nz == 0 ? 0u : nz == 2 ? 1u : nz == 8 ? 2u : 3u;
     e[3] = type | (static_cast<uint32_t>(pos) << 8);
   }
 
-  const size_t tile_bytes = tiles.size() * 2;
-  const size_t lane_bytes = lanes.size() * 2;
-  const size_t gemv_bytes = gemv.size() * 4;
-  const size_t raw_bytes = static_cast<size_t>(kCodebook) * kDim;
-  void *dt = nullptr, *dl = nullptr, *dr = nullptr, *dg = nullptr;
-  if (hipMalloc(&dt, tile_bytes) != hipSuccess || hipMalloc(&dl, lane_bytes) != hipSuccess ||
-      hipMalloc(&dr, raw_bytes) != hipSuccess || hipMalloc(&dg, gemv_bytes) != hipSuccess) {
-    if (dt) (void)hipFree(dt);
-    if (dl) (void)hipFree(dl);
-    if (dr) (void)hipFree(dr);
-    return fail(PLX_ENOMEM, "device table allocation (%zu B) failed on device %d",
-                tile_bytes + lane_bytes + raw_bytes + gemv_bytes, dev);
+  struct Upload {
+    const void *host;
+    size_t bytes;
+    void **dev;
+  };
+  void *dt = nullptr, *dl = nullptr, *dr = nullptr, *dg = nullptr, *dd = nullptr, *drt = nullptr;
+  const Upload ups[] = {
+      {tiles.data(), tiles.size() * 2, &dt},
+      {lanes.data(), lanes.size() * 2, &dl},
+      {raw, static_cast<size_t>(kCodebook) * kDim, &dr},
+      {gemv.data(), gemv.size() * 4, &dg},
+      {dq.data(), dq.size() * 4, &dd},
+      {raw_tiles.data(), raw_tiles.size() * 2, &drt},
+  };
+  int st = PLX_OK;
+  for (const Upload &u : ups) {
+    if (hipMalloc(u.dev, u.bytes) != hipSuccess) {
+      *u.dev = nullptr;
+      st = fail(PLX_ENOMEM, "device table allocation (%zu B) failed on device %d", u.bytes, dev);
+      break;
+    }
+    st = check_hip(hipMemcpy(*u.dev, u.host, u.bytes, hipMemcpyHostToDevice), "upload codebook table");
+    if (st != PLX_OK) break;
   }
-  int st = check_hip(hipMemcpy(dt, tiles.data(), tile_bytes, hipMemcpyHostToDevice), "upload codebook tiles");
-  if (st == PLX_OK) st = check_hip(hipMemcpy(dl, lanes.data(), lane_bytes, hipMemcpyHostToDevice), "upload lane table");
-  if (st == PLX_OK) st = check_hip(hipMemcpy(dr, raw, raw_bytes, hipMemcpyHostToDevice), "upload raw codebook");
-  if (st == PLX_OK) st = check_hip(hipMemcpy(dg, gemv.data(), gemv_bytes, hipMemcpyHostToDevice), "upload gemv table");
   if (st != PLX_OK) {
-    (void)hipFree(dt);
-    (void)hipFree(dl);
-    (void)hipFree(dr);
-    (void)hipFree(dg);
+    for (const Upload &u : ups)
+      if (*u.dev) (void)hipFree(*u.dev);
     return st;
   }
   t->kp_bf16_tiles = static_cast<uint8_t *>(dt);
   t->kp_bf16_lanes = static_cast<uint8_t *>(dl);
   t->cb_raw = static_cast<int8_t *>(dr);
   t->kp_gemv = static_cast<uint8_t *>(dg);
+  t->kp_dq = static_cast<uint32_t *>(dd);
+  t->kp_raw_tiles = static_cast<uint8_t *>(drt);
   t->device = dev;
   return PLX_OK;
 }
