@@ -36,6 +36,11 @@ extern "C" {
  *       equal maxima, same origin rule.  The reference's Triton kernel,
  *       castor.py:407-460. */
 #define PLX_NN_FP32_SCORES 1
+/* NN-P: fp32 atoms against the fp32 codebook, first (lowest-index) maximum of
+ *       the fp32 scores, origin iff ||atom||_2 < 1e-8 (no score threshold;
+ *       invariant under positive scaling of the atom).  The reference's
+ *       pack-time search, pack._quantize_h24_layer (pack.py:167-177). */
+#define PLX_NN_PACK_FP32 2
 
 /* ---- element types of plx_gather_codebook's output -------------------- */
 #define PLX_DTYPE_F32 0
@@ -123,6 +128,15 @@ int plx_gather_codebook(const int32_t *idx, int64_t n, int out_dtype, void *out,
 int plx_requantize(const float *latent, int64_t rows, int64_t cols, int mode,
                    float *sigma_out, int32_t *idx_out, uint8_t *packed_out, float *weight_out,
                    void *workspace, size_t workspace_bytes, void *stream);
+
+/* Pack-time quantization of one weight [rows, cols] (cols % 24 == 0):
+ *   idx = NN-P(w atoms); packed_out = pack(idx) (uint8[((N+3)/4)*9]);
+ *   sigma16_out[r] = fp16(max(row_rms(w)[r] * fp32(sqrt 12), 1e-8)) (raw bits);
+ * idx_out int32[N] is nullable.  Replaces pack._quantize_h24_layer
+ * (pack.py:139-180) including its castor.pack_indices call. */
+int plx_quantize_layer_pack(const float *w, int64_t rows, int64_t cols, uint8_t *packed_out,
+                            uint16_t *sigma16_out, int32_t *idx_out, void *workspace,
+                            size_t workspace_bytes, void *stream);
 
 /* ---- dequantization (pollux.py:485-507) -------------------------------- */
 /* w16 = fp16(fp16(codebook16[unpack(packed)] * sigma16[row]) * fp32(1/sqrt 2)),

@@ -16,7 +16,7 @@ import torch
 LIB_PATH = Path(__file__).resolve().parent / "lib" / "libpollux_amd.so"
 
 PLX_OK, PLX_EINVAL, PLX_EHIP, PLX_ENOMEM = 0, 1, 2, 3
-NN_BF16_SCORES, NN_FP32_SCORES = 0, 1
+NN_BF16_SCORES, NN_FP32_SCORES, NN_PACK_FP32 = 0, 1, 2
 DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
 
 _vp, _i64, _int, _sz = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_size_t
@@ -37,6 +37,7 @@ SIGNATURES = {
     "plx_quantize": (_int, [_vp, _i64, _int, _vp, _vp, _sz, _vp]),
     "plx_gather_codebook": (_int, [_vp, _i64, _int, _vp, _vp]),
     "plx_requantize": (_int, [_vp, _i64, _i64, _int, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "plx_quantize_layer_pack": (_int, [_vp, _i64, _i64, _vp, _vp, _vp, _vp, _sz, _vp]),
     "plx_dequant_f16": (_int, [_vp, _i64, _vp, _i64, _i64, _vp, _vp]),
     "plx_dequant_linear": (_int, [_vp, _i64, _vp, _i64, _i64, _vp, _int, _i64, _vp, _vp]),
     "plx_profile_begin": (_int, []),

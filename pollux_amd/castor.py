@@ -54,6 +54,8 @@ BYTES_PER_CHUNK = 9
 LEECH_SCALE: float = 1.0 / math.sqrt(8.0)
 
 _MODES = {"bf16": _lib.NN_BF16_SCORES, "fp32": _lib.NN_FP32_SCORES}
+# quantize_indices also takes "pack": the pack-time NN-P search (pack.py:167-177)
+_INDEX_MODES = {**_MODES, "pack": _lib.NN_PACK_FP32}
 _mode_lock = threading.Lock()
 _nn_mode = os.environ.get("POLLUX_AMD_NN_MODE", "bf16")
 if _nn_mode not in _MODES:
@@ -255,14 +257,20 @@ def _workspace(n_atoms: int, device: torch.device) -> torch.Tensor:
 
 
 def quantize_indices(x: torch.Tensor, mode: str | None = None) -> torch.Tensor:
-    """int32 codebook indices of the atoms of ``x`` ([..., 24], any float dtype)."""
+    """int32 codebook indices of the atoms of ``x`` ([..., 24], any float dtype).
+
+    mode: "bf16" (NN-B), "fp32" (NN-T) or "pack" (NN-P); default: the module mode.
+    """
     _lib.require_device(x, "quantize input")
     xf = x.reshape(-1, H24_DIM).float().contiguous()
     n = xf.shape[0]
     idx = torch.empty(n, dtype=torch.int32, device=xf.device)
     if n == 0:
         return idx
-    code = _MODES[mode or _nn_mode]
+    m = mode or _nn_mode
+    if m not in _INDEX_MODES:
+        raise ValueError(f"nn mode must be one of {sorted(_INDEX_MODES)}, got {m!r}")
+    code = _INDEX_MODES[m]
     ws = _workspace(n, xf.device)
     with torch.cuda.device(xf.device):
         st = _lib.lib().plx_quantize(

@@ -126,7 +126,8 @@ size_t plx_quantize_workspace_bytes(int64_t n_atoms) { return quantize_workspace
 int plx_quantize(const float *x, int64_t n_atoms, int mode, int32_t *idx_out, void *workspace,
                  size_t workspace_bytes, void *stream) {
   PLX_REQUIRE(n_atoms >= 0, "plx_quantize: negative atom count");
-  PLX_REQUIRE(mode == PLX_NN_BF16_SCORES || mode == PLX_NN_FP32_SCORES, "plx_quantize: unknown mode %d", mode);
+  PLX_REQUIRE(mode == PLX_NN_BF16_SCORES || mode == PLX_NN_FP32_SCORES || mode == PLX_NN_PACK_FP32,
+              "plx_quantize: unknown mode %d", mode);
   if (n_atoms == 0) return PLX_OK;
   PLX_REQUIRE(x != nullptr && idx_out != nullptr, "plx_quantize: null pointer");
   return launch_quantize(x, nullptr, n_atoms, kDim, n_atoms, mode, idx_out, nullptr, nullptr, workspace,
@@ -157,6 +158,21 @@ int plx_requantize(const float *latent, int64_t rows, int64_t cols, int mode, fl
   int st = launch_row_rms(latent, rows, cols, sigma_out, nullptr, as_stream(stream));
   if (st != PLX_OK) return st;
   return launch_quantize(latent, sigma_out, rows, cols, n_atoms, mode, idx_out, packed_out, weight_out, workspace,
+                         workspace_bytes, as_stream(stream));
+}
+
+int plx_quantize_layer_pack(const float *w, int64_t rows, int64_t cols, uint8_t *packed_out, uint16_t *sigma16_out,
+                            int32_t *idx_out, void *workspace, size_t workspace_bytes, void *stream) {
+  PLX_REQUIRE(rows >= 0 && cols > 0, "plx_quantize_layer_pack: bad shape (%lld, %lld)", static_cast<long long>(rows),
+              static_cast<long long>(cols));
+  PLX_REQUIRE(cols % kDim == 0, "Pollux requires in_features divisible by H24_DIM=24; got %lld.",
+              static_cast<long long>(cols));
+  if (rows == 0) return PLX_OK;
+  PLX_REQUIRE(w != nullptr && packed_out != nullptr && sigma16_out != nullptr, "plx_quantize_layer_pack: null pointer");
+  const int64_t n_atoms = rows * (cols / kDim);
+  int st = launch_row_rms(w, rows, cols, nullptr, sigma16_out, as_stream(stream));
+  if (st != PLX_OK) return st;
+  return launch_quantize(w, nullptr, rows, cols, n_atoms, PLX_NN_PACK_FP32, idx_out, packed_out, nullptr, workspace,
                          workspace_bytes, as_stream(stream));
 }
 

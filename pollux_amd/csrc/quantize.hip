@@ -23,6 +23,13 @@
 //     with the maximal bucket M; origin iff 2*M < 0x407FFFFF, i.e. M < 2.0.
 //   NN-T (castor.py:419-460): winner = lowest code with the maximal fp32
 //     score S; origin iff 2*S < 0x407FFFFF.
+//   NN-P (pack.py:167-177): fp32 atom against the fp32 codebook, winner =
+//     lowest code with the maximal score; origin iff |x|_2 < 1e-8.  The atom
+//     is split exactly into three bf16 parts (x = h + m + l up to 2^-27|x|)
+//     and scored against the raw integer codes (exact in bf16) by three
+//     chained MFMAs per tile; the fp32 codebook is the raw table times
+//     fp32(1/sqrt 8) (3s rounded), so these scores order the codes like the
+//     fp32 ones up to 2^-21 * sum|x_i c_i|, inside the near-tie envelope.
 //   Both are tracked with one integer threshold R per (atom, lane): a group of
 //   8 tiles (32 codes per lane) improves when its max score, as an int bit
 //   pattern, exceeds R (positive floats order like ints; negative scores can
@@ -33,8 +40,10 @@
 //   the best group of the lanes that hold it.
 //
 // resolve_kernel -- one thread per atom: the maximum key over the slices, an
-//   exact-product rescan (v_dot2_f32_bf16) of the few groups that hold it to
-//   find the lowest code, then the index and the packed 9-byte groups.  Both
+//   exact-product rescan (v_dot2_f32_bf16; NN-P: fp64 dot products of the
+//   fp32 atom and the fp32 codebook rows, exact up to 2^-48) of the few
+//   groups that hold it to find the lowest code, then the index and the
+//   packed 9-byte groups.  Both
 //   fp32 sums (MFMA, dot2) lie within 2^-20 * sum|x_i c_i| of the exact score
 //   (MFMA measured at < 2^-22), so the result equals the exact-score answer
 //   on every atom that is not a near-tie within that envelope.
@@ -64,12 +73,21 @@ static_assert(kStageVecs % kThreads == 0, "stage must split evenly over the bloc
 static_assert(kST % kG == 0 && kG == 8, "whole 8-tile groups per LDS stage");
 
 constexpr int kModeB = PLX_NN_BF16_SCORES;
+constexpr int kModeP = PLX_NN_PACK_FP32;
+
+// bf16 parts per atom coordinate: NN-P carries the fp32 value as h + m + l.
+template <int MODE>
+constexpr int n_splits() {
+  return MODE == kModeP ? 3 : 1;
+}
 
 template <int MODE>
 __device__ __forceinline__ int initial_threshold() {
   // NN-B: largest fp32 whose bf16 rounding is below 2.0 (bf16 0x3FFF is odd).
   // NN-T: largest fp32 s with 2*s < 0x407FFFFF.
-  return MODE == kModeB ? 0x3FFF7FFF : 0x3FFFFFFE;
+  // NN-P: +0.0 -- no score threshold (every nonzero atom has a positive
+  //       maximum: the best +-4 pair scores 4s(|x_i| + |x_j|)).
+  return MODE == kModeB ? 0x3FFF7FFF : MODE == kModeP ? 0 : 0x3FFFFFFE;
 }
 
 // New threshold after a group whose maximum is gm.  NN-T: gm itself.  NN-B:
@@ -121,14 +139,26 @@ __global__ __launch_bounds__(kThreads, 2) void nn_kernel(const float *__restrict
   const int wave = tid >> 6, lane = tid & 63, q = lane >> 4, j = lane & 15;
   const int64_t wave_atom0 = ablock * kAtomsPerBlock + static_cast<int64_t>(wave) * (kAT * 16);
 
-  // B operands: 8 atom tiles, lane holds coordinates 8q..8q+7 of atom j.
-  bf16x8 b[kAT];
+  // B operands: 8 atom tiles, lane holds coordinates 8q..8q+7 of atom j
+  // (NN-P: as three bf16 parts, b[0] + b[1] + b[2]).
+  constexpr int NS = n_splits<MODE>();
+  bf16x8 b[NS][kAT];
 #pragma unroll
   for (int at = 0; at < kAT; ++at) {
     float v[8];
     load_coords8<FUSED>(src, sigma, atoms_per_row, n_atoms, wave_atom0 + at * 16 + j, q, v);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) b[at][e] = __builtin_bit_cast(__bf16, static_cast<uint16_t>(bf16_rne_bits(v[e])));
+    for (int e = 0; e < 8; ++e) {
+      const uint32_t h = bf16_rne_bits(v[e]);
+      b[0][at][e] = __builtin_bit_cast(__bf16, static_cast<uint16_t>(h));
+      if constexpr (NS == 3) {
+        const float r1 = v[e] - bf16_bits_to_float(h);  // exact
+        const uint32_t m = bf16_rne_bits(r1);
+        const float r2 = r1 - bf16_bits_to_float(m);    // exact
+        b[1][at][e] = __builtin_bit_cast(__bf16, static_cast<uint16_t>(m));
+        b[2][at][e] = __builtin_bit_cast(__bf16, static_cast<uint16_t>(bf16_rne_bits(r2)));
+      }
+    }
   }
 
   int R[kAT], best[kAT];
@@ -164,7 +194,7 @@ __global__ __launch_bounds__(kThreads, 2) void nn_kernel(const float *__restrict
   // folded, i.e. during the next group's first tile; the slice's last tile is
   // folded after the loop.
   int gm[kAT];
-  f32x4 acc[kAT];
+  f32x4 acc[kAT], part[kAT];
 #pragma unroll
   for (int at = 0; at < kAT; ++at) {
     gm[at] = INT_MIN;
@@ -188,7 +218,7 @@ __global__ __launch_bounds__(kThreads, 2) void nn_kernel(const float *__restrict
         bf16x8 an;
 #pragma unroll
         for (int at = 0; at < kAT; ++at) {
-          const f32x4 c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b[at], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+          const f32x4 c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b[0][at], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
           if (at == 0) {
             // the LDS wait that guards `a` must not also wait for this read
             __builtin_amdgcn_sched_barrier(0);
@@ -212,8 +242,19 @@ __global__ __launch_bounds__(kThreads, 2) void nn_kernel(const float *__restrict
             up[at] = m > R[at];
           }
           gm[at] = m;
-          acc[at] = c;
+          if constexpr (NS == 1)
+            acc[at] = c;
+          else
+            part[at] = c;
           __builtin_amdgcn_sched_barrier(0);
+        }
+        if constexpr (NS == 3) {
+#pragma unroll
+          for (int at = 0; at < kAT; ++at)
+            part[at] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b[1][at], part[at], 0, 0, 0);
+#pragma unroll
+          for (int at = 0; at < kAT; ++at)
+            acc[at] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b[2][at], part[at], 0, 0, 0);
         }
         a = an;
       }
@@ -286,17 +327,31 @@ __global__ __launch_bounds__(256) void resolve_kernel(const uint4 *__restrict__ 
   if (a < n_atoms) {
     uint32_t M = 0;
     for (int s = 0; s < n_slices; ++s) M = max(M, records[static_cast<int64_t>(s) * n_atoms + a].x);
-    if (M != 0) {
-      uint32_t xw[12];
+    // NN-B/T: bf16 pairs of the atom; NN-P: the fp32 atom in fp64 and |x|^2
+    uint32_t xw[MODE == kModeP ? 1 : 12];
+    double xd[MODE == kModeP ? kDim : 1];
+    double nrm2 = 0.0;
 #pragma unroll
-      for (int qq = 0; qq < 3; ++qq) {
-        float v[8];
-        load_coords8<FUSED>(src, sigma, atoms_per_row, n_atoms, a, qq, v);
+    for (int qq = 0; qq < 3; ++qq) {
+      float v[8];
+      load_coords8<FUSED>(src, sigma, atoms_per_row, n_atoms, a, qq, v);
+      if constexpr (MODE == kModeP) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          xd[8 * qq + e] = static_cast<double>(v[e]);
+          nrm2 = fma(xd[8 * qq + e], xd[8 * qq + e], nrm2);
+        }
+      } else {
 #pragma unroll
         for (int d = 0; d < 4; ++d) xw[4 * qq + d] = bf16_rne_bits(v[2 * d]) | (bf16_rne_bits(v[2 * d + 1]) << 16);
       }
+    }
+    // NN-P's origin rule (pack.py:174): |x|_2 < fp32(1e-8); no scan needed
+    const bool p_snap = MODE == kModeP && sqrt(nrm2) < static_cast<double>(__uint_as_float(kEpsBits));
+    if (M != 0 && !p_snap) {
       uint32_t found = 0xFFFFFFFFu;  // lowest code whose bucket equals M (NN-B)
       float best_v = -__builtin_inff();
+      double best_d = -__builtin_inf();
       uint32_t best_code = 0xFFFFFFFFu;
       // Each thread walks its own candidate slots (slice, lane) in rounds, so
       // the wave runs the rescan body once per round (~1-3 rounds) instead of
@@ -319,7 +374,9 @@ __global__ __launch_bounds__(256) void resolve_kernel(const uint4 *__restrict__ 
         const int qq = slot & 3;
         ++slot;
         if (slot < n_slots && (slot & 3) == 0) rec = records[static_cast<int64_t>(slot >> 2) * n_atoms + a];
-        // the lane's 32 codes of group g are 1.5 KB contiguous in the lane-major table
+        // NN-B/T: the lane's 32 codes of group g are 1.5 KB contiguous in the
+        // lane-major table; NN-P: rows of the raw int8 codebook (4 consecutive
+        // codes = 96 B per tile)
         const uint4 *cg = reinterpret_cast<const uint4 *>(rescan) +
                           ((static_cast<size_t>(qq) * kPaddedTiles + static_cast<size_t>(g) * kG) * 4) * 3;
         for (int t = 0; t < kG; ++t) {
@@ -328,6 +385,23 @@ __global__ __launch_bounds__(256) void resolve_kernel(const uint4 *__restrict__ 
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const int row = 4 * qq + e;
+            const uint32_t code = static_cast<uint32_t>(tile * kTileCodes + row);
+            if constexpr (MODE == kModeP) {
+              const uint2 *cr = reinterpret_cast<const uint2 *>(rescan + (static_cast<size_t>(code) + 1) * kDim);
+              const uint2 r0 = cr[0], r1 = cr[1], r2 = cr[2];
+              const uint32_t rw[6] = {r0.x, r0.y, r1.x, r1.y, r2.x, r2.y};
+              double sc = 0.0;
+#pragma unroll
+              for (int c = 0; c < kDim; ++c) {
+                const int k = static_cast<int32_t>(rw[c / 4] << (24 - 8 * (c % 4))) >> 24;
+                sc = fma(xd[c], static_cast<double>(raw_value_f32(k)), sc);
+              }
+              if (sc > best_d || (sc == best_d && code < best_code)) {
+                best_d = sc;
+                best_code = code;
+              }
+              continue;
+            }
             const uint4 *cp = cg + (t * 4 + e) * 3;
             const uint4 c0 = cp[0], c1 = cp[1], c2 = cp[2];
             const uint32_t cw[12] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w, c2.x, c2.y, c2.z, c2.w};
@@ -336,7 +410,6 @@ __global__ __launch_bounds__(256) void resolve_kernel(const uint4 *__restrict__ 
             for (int d = 0; d < 12; ++d)
               sc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, xw[d]), __builtin_bit_cast(bf16x2, cw[d]), sc,
                                                    false);
-            const uint32_t code = static_cast<uint32_t>(tile * kTileCodes + row);
             float v = sc;
             if (MODE == kModeB) {
               const uint32_t bk = bf16_rne_bits(sc);
@@ -352,7 +425,10 @@ __global__ __launch_bounds__(256) void resolve_kernel(const uint4 *__restrict__ 
       }
       bool snap;
       uint32_t code;
-      if (MODE == kModeB) {
+      if (MODE == kModeP) {
+        code = best_code;
+        snap = best_code == 0xFFFFFFFFu;  // non-finite atom: no score compared
+      } else if (MODE == kModeB) {
         const uint32_t bucket = found != 0xFFFFFFFFu ? M : (__float_as_uint(best_v) >> 16);
         code = found != 0xFFFFFFFFu ? found : best_code;
         snap = !(best_v > 0.f) || bucket < 0x4000u;  // bf16 max below 2.0
@@ -362,7 +438,7 @@ __global__ __launch_bounds__(256) void resolve_kernel(const uint4 *__restrict__ 
       }
       id = snap ? 0 : static_cast<int32_t>(code) + 1;
     }
-    idx_out[a] = id;
+    if (idx_out) idx_out[a] = id;
   }
   if (!packed_out) return;
   ids[threadIdx.x] = id;
@@ -435,13 +511,15 @@ int launch_mode(const float *x, const float *sigma, int64_t apr, int64_t n_atoms
   const int64_t grid = ablocks * n_slices;
   if (grid > 0x7FFFFFFFll) return fail(PLX_EINVAL, "quantize: %lld atoms exceed one launch", static_cast<long long>(n_atoms));
   profile_before(s);
+  const uint8_t *tiles = MODE == kModeP ? tab->kp_raw_tiles : tab->kp_bf16_tiles;
+  const uint8_t *rescan = MODE == kModeP ? reinterpret_cast<const uint8_t *>(tab->cb_raw) : tab->kp_bf16_lanes;
   hipLaunchKernelGGL((nn_kernel<MODE, FUSED>), dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0, s, x, sigma, apr,
-                     n_atoms, tab->kp_bf16_tiles, n_slices, tiles_per_slice, records);
+                     n_atoms, tiles, n_slices, tiles_per_slice, records);
   int st = check_launch("nn_kernel");
   if (st != PLX_OK) return st;
   profile_after(s);
   hipLaunchKernelGGL((resolve_kernel<MODE, FUSED>), dim3(static_cast<unsigned>((n_atoms + 255) / 256)), dim3(256), 0, s,
-                     records, n_slices, n_atoms, x, sigma, apr, tab->kp_bf16_lanes, idx_out, packed_out);
+                     records, n_slices, n_atoms, x, sigma, apr, rescan, idx_out, packed_out);
   return check_launch("resolve_kernel");
 }
 
@@ -469,7 +547,9 @@ int launch_quantize(const float *x, const float *sigma, int64_t rows, int64_t co
   uint4 *records = static_cast<uint4 *>(workspace);
   const bool fused = sigma != nullptr;
   const int64_t apr = cols / kDim;
-  if (mode == PLX_NN_BF16_SCORES)
+  if (mode == PLX_NN_PACK_FP32)
+    st = launch_mode<PLX_NN_PACK_FP32, false>(x, nullptr, apr, n_atoms, tab, idx_out, packed_out, records, s);
+  else if (mode == PLX_NN_BF16_SCORES)
     st = fused ? launch_mode<PLX_NN_BF16_SCORES, true>(x, sigma, apr, n_atoms, tab, idx_out, packed_out, records, s)
                : launch_mode<PLX_NN_BF16_SCORES, false>(x, sigma, apr, n_atoms, tab, idx_out, packed_out, records, s);
   else
