@@ -154,6 +154,19 @@ int plx_dequant_linear(const uint8_t *packed, int64_t n_packed_bytes, const uint
                        int64_t rows, int64_t cols, const void *x, int x_is_f32, int64_t m_rows,
                        float *y, void *stream);
 
+/* ---- per-row INT8 periphery (embeddings / LM head in .plx files) ------- */
+/* q_out int8[rows*cols] = int8(clamp(rint((w / mu) * 127), -128, 127)),
+ * mu16_out[r] = fp16(mu) with mu = max(max_j |w[r,j]|, 1e-8); all fp32 IEEE ops.
+ * Replaces pack._quantize_int8 (pack.py:124-136). */
+int plx_quantize_int8_rows(const float *w, int64_t rows, int64_t cols, int8_t *q_out,
+                           uint16_t *mu16_out, void *stream);
+
+/* w16_out[r,j] = fp16(q[r,j] * fp16(mu16[r] * fp32(1/127))) as raw fp16 bits.
+ * Replaces PackedInt8Embedding/PackedInt8Linear.materialize (pollux.py:521-530,
+ * 551-560) as torch evaluates it on fp16 device tensors. */
+int plx_dequant_int8_rows(const int8_t *q, const uint16_t *mu16, int64_t rows, int64_t cols,
+                          uint16_t *w16_out, void *stream);
+
 /* ---- kernel timing (diagnostics; no counterpart in the reference) ------ */
 /* While enabled, every launch of the quantizer's scoring kernel (nn_kernel)
  * is bracketed by HIP events recorded on its launch stream (up to 4096

@@ -3,12 +3,26 @@
 Modules
 -------
 castor   castor.py-compatible API: codebook, 18-bit pack/unpack, row scale,
-         nearest-neighbour quantizer, fused requantize
-packed   PackedH24Linear with HIP dequantization
+         nearest-neighbour quantizer (NN-B / NN-T / NN-P), fused requantize
+packed   PackedH24Linear (HIP dequantization, fused dequant-GEMV/GEMM) and the
+         INT8 periphery layers PackedInt8Embedding / PackedInt8Linear
+pack     pack.py-compatible pack-time quantization (_quantize_h24_layer,
+         _quantize_int8, the state-dict packing loop)
+plx      the .plx container: byte-exact writer, reader, memory-mapped loader
 build    builds lib/libpollux_amd.so (hipcc, gfx950) in-tree
 """
 
-from . import castor  # noqa: F401
-from .packed import PackedH24Linear, dequant_linear, dequantize_h24  # noqa: F401
+from . import castor, pack, plx  # noqa: F401
+from .packed import (  # noqa: F401
+    PackedH24Linear,
+    PackedInt8Embedding,
+    PackedInt8Linear,
+    dequant_linear,
+    dequantize_h24,
+    dequantize_int8_rows,
+)
 
-__all__ = ["castor", "PackedH24Linear", "dequant_linear", "dequantize_h24"]
+__all__ = [
+    "castor", "pack", "plx", "PackedH24Linear", "PackedInt8Embedding", "PackedInt8Linear",
+    "dequant_linear", "dequantize_h24", "dequantize_int8_rows",
+]

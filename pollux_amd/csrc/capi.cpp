@@ -204,4 +204,22 @@ int plx_dequant_linear(const uint8_t *packed, int64_t n_packed_bytes, const uint
   return launch_dequant_linear(packed, sigma16, rows, cols, x, x_is_f32, m_rows, y, as_stream(stream));
 }
 
+int plx_quantize_int8_rows(const float *w, int64_t rows, int64_t cols, int8_t *q_out, uint16_t *mu16_out,
+                           void *stream) {
+  PLX_REQUIRE(rows >= 0 && cols > 0, "plx_quantize_int8_rows: bad shape (%lld, %lld)", static_cast<long long>(rows),
+              static_cast<long long>(cols));
+  if (rows == 0) return PLX_OK;
+  PLX_REQUIRE(w != nullptr && q_out != nullptr && mu16_out != nullptr, "plx_quantize_int8_rows: null pointer");
+  return launch_int8_quant(w, rows, cols, q_out, mu16_out, as_stream(stream));
+}
+
+int plx_dequant_int8_rows(const int8_t *q, const uint16_t *mu16, int64_t rows, int64_t cols, uint16_t *w16_out,
+                          void *stream) {
+  PLX_REQUIRE(rows >= 0 && cols > 0, "plx_dequant_int8_rows: bad shape (%lld, %lld)", static_cast<long long>(rows),
+              static_cast<long long>(cols));
+  if (rows == 0) return PLX_OK;
+  PLX_REQUIRE(q != nullptr && mu16 != nullptr && w16_out != nullptr, "plx_dequant_int8_rows: null pointer");
+  return launch_int8_dequant(q, mu16, rows, cols, w16_out, as_stream(stream));
+}
+
 }  // extern "C"

@@ -108,3 +108,76 @@ class PackedH24Linear(nn.Module):
             y = dequant_linear(self.packed_weights, self.sigma_rows, self.out_features, self.in_features, x).to(x.dtype)
             return y if self.bias is None else y + self.bias.to(x.dtype)
         return F.linear(x, self.weight.to(dtype=x.dtype), self.bias)
+
+
+def dequantize_int8_rows(q: torch.Tensor, mu16: torch.Tensor) -> torch.Tensor:
+    """fp16 weight = q * (mu / 127) per row, as torch evaluates it on fp16 device tensors (pollux.py:526)."""
+    _lib.require_device(q, "dequantize_int8_rows input")
+    if q.dtype != torch.int8 or mu16.dtype != torch.float16:
+        raise ValueError("INT8 rows need int8 values and float16 mu_rows")
+    if q.dim() < 1:
+        raise ValueError("INT8 rows need at least one dimension")
+    cols = q.shape[-1]
+    rows = q.numel() // cols if cols else 0
+    if mu16.numel() != rows:
+        raise ValueError(f"expected {rows} mu rows, got {mu16.numel()}")
+    qq = q.contiguous()
+    mu = mu16.reshape(-1).contiguous()
+    out = torch.empty(q.shape, dtype=torch.float16, device=q.device)
+    if rows and cols:
+        with torch.cuda.device(q.device):
+            st = _lib.lib().plx_dequant_int8_rows(
+                _lib.ptr(qq), _lib.ptr(mu), rows, cols, _lib.ptr(out), _lib.stream_of(q.device)
+            )
+        _lib.check(st, "dequantize_int8_rows")
+    return out
+
+
+class _PackedInt8Rows(nn.Module):
+    """Shared buffers / materialize of the INT8 periphery layers (pollux.py:508-563)."""
+
+    def _init_rows(self, rows: int, cols: int) -> None:
+        self.register_buffer("weight_int8", torch.zeros(rows, cols, dtype=torch.int8))
+        self.register_buffer("mu_rows", torch.ones(rows, dtype=torch.float16))
+        self._materialized = False
+
+    def materialize(self) -> None:
+        if self._materialized:
+            return
+        weight = dequantize_int8_rows(self.weight_int8, self.mu_rows.to(torch.float16))
+        self.weight = nn.Parameter(weight, requires_grad=False)
+        del self.weight_int8
+        del self.mu_rows
+        self._materialized = True
+
+
+class PackedInt8Embedding(_PackedInt8Rows):
+    """Token embedding with INT8 weights and per-row fp16 scales (pollux.py:508-532)."""
+
+    def __init__(self, num_embeddings: int, embedding_dim: int) -> None:
+        super().__init__()
+        self.num_embeddings = int(num_embeddings)
+        self.embedding_dim = int(embedding_dim)
+        self._init_rows(self.num_embeddings, self.embedding_dim)
+
+    def forward(self, idx: torch.Tensor) -> torch.Tensor:
+        self.materialize()
+        return F.embedding(idx, self.weight.to(dtype=torch.float32))
+
+
+class PackedInt8Linear(_PackedInt8Rows):
+    """Output projection with INT8 weights and per-row fp16 scales (pollux.py:535-563)."""
+
+    def __init__(self, in_features: int, out_features: int, bias: bool = False) -> None:
+        super().__init__()
+        self.in_features = int(in_features)
+        self.out_features = int(out_features)
+        self._init_rows(self.out_features, self.in_features)
+        if bias:
+            self.bias = nn.Parameter(torch.zeros(out_features))
+        else:
+            self.register_parameter("bias", None)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        self.materialize()
+        return F.linear(x, self.weight.to(dtype=x.dtype), self.bias)
