@@ -145,14 +145,19 @@ int plx_quantize_layer_pack(const float *w, int64_t rows, int64_t cols, uint8_t 
 int plx_dequant_f16(const uint8_t *packed, int64_t n_packed_bytes, const uint16_t *sigma16,
                     int64_t rows, int64_t cols, uint16_t *w16_out, void *stream);
 
+/* Workspace (device bytes, 16-byte aligned) plx_dequant_linear needs for
+ * this shape, batch and activation type (0 when none). */
+size_t plx_dequant_linear_workspace_bytes(int64_t rows, int64_t cols, int64_t m_rows, int x_is_f32);
+
 /* y[m, r] = sum_i x[m, i] * W[r, i] for m < m_rows, with W the fp16
  * materialisation of (packed, sigma16) above, never stored: x is bf16
  * (x_is_f32 = 0) or fp32 (x_is_f32 = 1) [m_rows, cols], y fp32 [m_rows, rows],
- * fp32 accumulation.  Replaces PackedH24Linear.forward after materialize
- * (pollux.py:506-507: F.linear(x, weight.to(x.dtype))), evaluated in fp32. */
+ * fp32 accumulation; results are deterministic (fixed summation order).
+ * Replaces PackedH24Linear.forward after materialize (pollux.py:506-507:
+ * F.linear(x, weight.to(x.dtype))), evaluated in fp32. */
 int plx_dequant_linear(const uint8_t *packed, int64_t n_packed_bytes, const uint16_t *sigma16,
                        int64_t rows, int64_t cols, const void *x, int x_is_f32, int64_t m_rows,
-                       float *y, void *stream);
+                       float *y, void *workspace, size_t workspace_bytes, void *stream);
 
 /* ---- per-row INT8 periphery (embeddings / LM head in .plx files) ------- */
 /* q_out int8[rows*cols] = int8(clamp(rint((w / mu) * 127), -128, 127)),

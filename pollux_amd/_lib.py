@@ -41,7 +41,8 @@ SIGNATURES = {
     "plx_quantize_int8_rows": (_int, [_vp, _i64, _i64, _vp, _vp, _vp]),
     "plx_dequant_int8_rows": (_int, [_vp, _vp, _i64, _i64, _vp, _vp]),
     "plx_dequant_f16": (_int, [_vp, _i64, _vp, _i64, _i64, _vp, _vp]),
-    "plx_dequant_linear": (_int, [_vp, _i64, _vp, _i64, _i64, _vp, _int, _i64, _vp, _vp]),
+    "plx_dequant_linear_workspace_bytes": (_sz, [_i64, _i64, _i64, _int]),
+    "plx_dequant_linear": (_int, [_vp, _i64, _vp, _i64, _i64, _vp, _int, _i64, _vp, _vp, _sz, _vp]),
     "plx_profile_begin": (_int, []),
     "plx_profile_end": (_int, [_vp, _vp]),
 }

@@ -190,8 +190,14 @@ int plx_dequant_f16(const uint8_t *packed, int64_t n_packed_bytes, const uint16_
   return launch_dequant_f16(packed, sigma16, rows, cols, w16_out, as_stream(stream));
 }
 
+size_t plx_dequant_linear_workspace_bytes(int64_t rows, int64_t cols, int64_t m_rows, int x_is_f32) {
+  if (rows <= 0 || cols <= 0 || cols % kDim != 0 || m_rows <= 0) return 0;
+  return dequant_linear_workspace_bytes(rows, cols, m_rows, x_is_f32);
+}
+
 int plx_dequant_linear(const uint8_t *packed, int64_t n_packed_bytes, const uint16_t *sigma16, int64_t rows,
-                       int64_t cols, const void *x, int x_is_f32, int64_t m_rows, float *y, void *stream) {
+                       int64_t cols, const void *x, int x_is_f32, int64_t m_rows, float *y, void *workspace,
+                       size_t workspace_bytes, void *stream) {
   PLX_REQUIRE(rows >= 0 && cols > 0 && cols % kDim == 0, "plx_dequant_linear: bad shape (%lld, %lld)",
               static_cast<long long>(rows), static_cast<long long>(cols));
   PLX_REQUIRE(m_rows >= 0, "plx_dequant_linear: negative batch");
@@ -201,7 +207,8 @@ int plx_dequant_linear(const uint8_t *packed, int64_t n_packed_bytes, const uint
               static_cast<long long>(n_atoms));
   if (rows == 0 || m_rows == 0) return PLX_OK;
   PLX_REQUIRE(packed != nullptr && sigma16 != nullptr && x != nullptr && y != nullptr, "plx_dequant_linear: null pointer");
-  return launch_dequant_linear(packed, sigma16, rows, cols, x, x_is_f32, m_rows, y, as_stream(stream));
+  return launch_dequant_linear(packed, sigma16, rows, cols, x, x_is_f32, m_rows, y, workspace, workspace_bytes,
+                               as_stream(stream));
 }
 
 int plx_quantize_int8_rows(const float *w, int64_t rows, int64_t cols, int8_t *q_out, uint16_t *mu16_out,

@@ -334,198 +334,421 @@ int launch_dql(const uint8_t *packed, int64_t packed_bytes, const uint16_t *sigm
 }
 
 // ---------------------------------------------------------------------------
-// dequant-GEMM for larger batches: y[m, r] = sum_i x[m, i] W[r, i] on MFMA.
+// dequant-GEMM: y[m, r] = sum_i x[m, i] W[r, i] on MFMA for bf16 activations.
 //
 // W[r, i] = +-v_|k| (fp16, 11 significant bits) is split exactly into two bf16
-// values, W = hi + lo (hi = bf16_rne(W), lo = W - hi has <= 4 significant
+// values, W = hi + lo (hi = bf16_rne(W); lo = W - hi has <= 3 significant
 // bits), so two v_mfma_f32_16x16x32_bf16 per tile give exact products of the
 // bf16 activations with the fp16 weights, accumulated in fp32.
-// Block = KW waves x 64 lanes, 16 output rows (MFMA B columns) x all tokens in
-// tiles of 16 (MFMA A rows); the waves split the row's atoms (K) and reduce
-// their partial tiles through LDS.  The block's packed bytes are staged in
-// LDS; each lane decodes its B operand (row l%16, 8 consecutive K = one plane
-// of one atom) from the 16-byte code entry.
+//
+// Block: 4 waves, 128 output rows (32 per wave = two MFMA B tiles of 16) x
+// 16*MT tokens (MFMA A tiles), over a range of SPB stages of 8 atoms (K = 192)
+// of the row; the grid splits K into `splits` such ranges so that the chip
+// is full, and a second kernel sums the split partials in a fixed order.
+//   prologue: decode the block's 128 x 8*SPB codes from the packed stream and
+//             fetch their kp_dq words (3 per code) into LDS; every lane builds
+//             the 8-entry hi / lo byte tables of its two rows' weight values;
+//   stage s:  the x tile [16*MT tokens][192] bf16 sits in LDS (rows padded to
+//             400 B: conflict-free 16-byte reads); stage s+1's tile is loaded
+//             into registers meanwhile.  Per K step of 32 a lane decodes its
+//             B fragments (8 weights of one row = one plane of one atom) with
+//             v_perm_b32 byte lookups and issues 4*MT MFMAs.
+// Tokens >= m and columns >= cols are zero-filled (so no NaN from outside the
+// operands can reach a valid output); atoms >= atoms_per_row decode as the
+// origin (weight 0).
 // ---------------------------------------------------------------------------
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
-__device__ __forceinline__ uint32_t hi_lo_pack(uint32_t h16, float v) {
-  // returns (hi bf16 | lo bf16 << 16) for the fp16 value with bits h16 (as float v)
-  (void)h16;
+constexpr int kMmRows = 128;              // output rows per block
+constexpr int kMmStageAtoms = 8;          // atoms (of every row) per stage
+constexpr int kMmStageK = kMmStageAtoms * kDim;  // 192
+constexpr int kMmXStride = 400;           // bytes per token row of the LDS x tile (384 + 16 pad)
+constexpr int kMmMaxSpb = 2;              // stages per block (LDS: 55 KB at 64 tokens)
+
+__device__ __forceinline__ uint32_t hi_lo_pack(float v) {
+  // (hi bf16 | lo bf16 << 16) with hi + lo == v exactly for an fp16 value v
   if (!(fabsf(v) <= 3.0e38f)) return bf16_rne_bits(v);  // inf / nan: carried by hi alone
   const uint32_t hb = bf16_rne_bits(v);
   const float lo = v - __uint_as_float(hb << 16);
   return hb | (bf16_rne_bits(lo) << 16);
 }
 
-template <int KW, int MT>  // KW waves split K; MT token tiles of 16
-__global__ __launch_bounds__(KW * 64) void dqgemm_kernel(const uint8_t *__restrict__ packed, int64_t packed_bytes,
-                                                         const uint16_t *__restrict__ sigma16, int64_t rows,
-                                                         int64_t atoms_per_row, const uint16_t *__restrict__ x,
-                                                         int64_t m_total, float *__restrict__ y,
-                                                         const uint4 *__restrict__ kp_gemv) {
+// 24-bit big-endian window of atom n read as two aligned dwords (bounds-checked
+// at the stream's tail), then the 18-bit index.
+__device__ __forceinline__ int32_t packed_index_dw(const uint8_t *__restrict__ packed, int64_t packed_bytes,
+                                                   int64_t n) {
+  const int64_t b = (n >> 2) * 9 + 2 * (n & 3);
+  const int64_t b4 = b & ~static_cast<int64_t>(3);
+  uint32_t v;
+  if (b4 + 8 <= packed_bytes) {
+    const uint32_t w0 = *reinterpret_cast<const uint32_t *>(packed + b4);
+    const uint32_t w1 = *reinterpret_cast<const uint32_t *>(packed + b4 + 4);
+    const uint32_t o = static_cast<uint32_t>(b & 3);
+    v = __builtin_amdgcn_perm(w1, w0, (o + 2) | ((o + 1) << 8) | (o << 16) | 0x0C000000u);
+  } else {
+    v = 0;
+    for (int k = 0; k < 3; ++k) v = (v << 8) | (b + k < packed_bytes ? packed[b + k] : 0u);
+  }
+  return static_cast<int32_t>((v >> (6 - 2 * (n & 3))) & 0x3FFFFu);
+}
+
+// 8 bf16 of one plane from a kp_dq word and a row's 4-word byte table.
+__device__ __forceinline__ bf16x8_t perm_decode(uint32_t w, uint32_t t0, uint32_t t1, uint32_t t2, uint32_t t3) {
+  const uint32_t s_lo = w & 0x0F0F0F0Fu, s_hi = (w >> 4) & 0x0F0F0F0Fu;
+  const uint32_t l_lo = __builtin_amdgcn_perm(t1, t0, s_lo), h_lo = __builtin_amdgcn_perm(t3, t2, s_lo);
+  const uint32_t l_hi = __builtin_amdgcn_perm(t1, t0, s_hi), h_hi = __builtin_amdgcn_perm(t3, t2, s_hi);
+  typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+  const u4 r = {__builtin_amdgcn_perm(h_lo, l_lo, 0x05010400u), __builtin_amdgcn_perm(h_lo, l_lo, 0x07030602u),
+                __builtin_amdgcn_perm(h_hi, l_hi, 0x05010400u), __builtin_amdgcn_perm(h_hi, l_hi, 0x07030602u)};
+  return __builtin_bit_cast(bf16x8_t, r);
+}
+
+// Four codes of one 9-byte packed group from the three dwords covering it
+// (o = byte offset of the group in the first dword).
+__device__ __forceinline__ void group_codes(uint32_t d0, uint32_t d1, uint32_t d2, uint32_t o, int32_t *c) {
+  const uint32_t sel = (o + 3) | ((o + 2) << 8) | ((o + 1) << 16) | (o << 24);
+  const uint32_t hi = __builtin_amdgcn_perm(d1, d0, sel);  // B0 B1 B2 B3, big-endian
+  const uint32_t lo = __builtin_amdgcn_perm(d2, d1, sel);  // B4 B5 B6 B7
+  const uint32_t b8 = (d2 >> (8 * o)) & 0xFFu;
+  c[0] = static_cast<int32_t>(hi >> 14);
+  c[1] = static_cast<int32_t>(((hi & 0x3FFFu) << 4) | (lo >> 28));
+  c[2] = static_cast<int32_t>((lo >> 10) & 0x3FFFFu);
+  c[3] = static_cast<int32_t>(((lo & 0x3FFu) << 8) | b8);
+}
+
+template <int MT, int SPB>  // token tiles of 16; stages of 8 atoms per block
+__global__ __launch_bounds__(256, 2) void dqmm_kernel(const uint8_t *__restrict__ packed, int64_t packed_bytes,
+                                                      const uint16_t *__restrict__ sigma16, int64_t rows,
+                                                      int64_t atoms_per_row, const uint16_t *__restrict__ x,
+                                                      int64_t m_total, int splits,
+                                                      const uint32_t *__restrict__ kp_dq, float *__restrict__ y,
+                                                      float *__restrict__ partial) {
   extern __shared__ __align__(16) uint8_t smem[];
-  constexpr int NT = KW * 64;
+  constexpr int TOK = 16 * MT;
+  constexpr int NA = kMmStageAtoms * SPB;     // atoms of every row in this block
+  constexpr int WS = NA * 3 + 4;              // words per row in LDS (16-byte multiple; 16 rows hit 16 banks)
+  uint8_t *xs = smem;                                                        // [TOK][400 B]
+  uint32_t *wt = reinterpret_cast<uint32_t *>(smem + TOK * kMmXStride);      // [128][WS]
+  uint4 *rtab = reinterpret_cast<uint4 *>(wt + kMmRows * WS);               // [128][2] row byte tables
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, j = lane & 15, q = lane >> 4;
+  const int64_t row_block = blockIdx.x / static_cast<unsigned>(splits);
+  const int split = static_cast<int>(blockIdx.x % static_cast<unsigned>(splits));
+  const int64_t row0 = row_block * kMmRows;
+  const int64_t tok0 = static_cast<int64_t>(blockIdx.y) * 64;
   const int64_t cols = atoms_per_row * kDim;
-  const int64_t row0 = static_cast<int64_t>(blockIdx.x) * 16;
-  const int64_t rows_here = min(static_cast<int64_t>(16), rows - row0);
-  const int64_t atom0 = row0 * atoms_per_row;
-  const int64_t g_lo = atom0 >> 2, g_hi = (atom0 + rows_here * atoms_per_row + 3) >> 2;
-  const int64_t start = g_lo * 9, end = g_hi * 9, base16 = start & ~static_cast<int64_t>(15);
-  const int nvec = static_cast<int>((end - base16 + 15) >> 4);
-  const uint8_t *pb = smem + (start - base16);
-  float *red = reinterpret_cast<float *>(smem + static_cast<int64_t>(nvec) * 16);  // [KW][MT][256] partial tiles
-  for (int i = threadIdx.x; i < nvec; i += NT) {
-    const int64_t gb = base16 + 16 * static_cast<int64_t>(i);
-    if (gb + 16 <= packed_bytes)
-      reinterpret_cast<uint4 *>(smem)[i] = *reinterpret_cast<const uint4 *>(packed + gb);
-    else
-      for (int k = 0; k < 16 && gb + k < packed_bytes; ++k) smem[16 * i + k] = packed[gb + k];
-  }
-  __syncthreads();
+  const int64_t a_begin = static_cast<int64_t>(split) * NA;
+  const int n_stages = static_cast<int>(min(static_cast<int64_t>(SPB), (atoms_per_row - a_begin + kMmStageAtoms - 1) / kMmStageAtoms));
 
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int j = lane & 15, q = lane >> 4;
-  const int64_t row = row0 + j;
-  const bool row_live = j < rows_here;
-  // per-row hi/lo bf16 pairs of the magnitudes |k| = 1..4
-  uint32_t mag[5];
-  mag[0] = 0u;
-  {
-    const float sig = row_live ? __half2float(__ushort_as_half(sigma16[row])) : 0.f;
-    const float sl = __uint_as_float(kSLatticeBits);
+  // ---- x stage tiles: TOK x 192 bf16 = TOK*24 vectors of 16 B ----
+  constexpr int kVec = TOK * 24;
+  constexpr int kVecPerThread = (kVec + 255) / 256;
+  uint4 xr[kVecPerThread];
+  auto load_x = [&](int st) {
+    const int64_t k0 = (a_begin + static_cast<int64_t>(st) * kMmStageAtoms) * kDim;
 #pragma unroll
-    for (int k = 1; k <= 4; ++k) {
-      const uint32_t h = dq_value(k, sig, sl);
-      mag[k] = hi_lo_pack(h, __half2float(__ushort_as_half(static_cast<uint16_t>(h))));
+    for (int u = 0; u < kVecPerThread; ++u) {
+      const int v = u * 256 + tid;
+      const int t = v / 24, kv = v - t * 24;
+      const int64_t tok = tok0 + t, k = k0 + 8 * kv;
+      xr[u] = make_uint4(0u, 0u, 0u, 0u);
+      if (v < kVec && tok < m_total && k < cols) xr[u] = *reinterpret_cast<const uint4 *>(x + tok * cols + k);
     }
-  }
-  f32x4_t acc[MT];
+  };
+  auto store_x = [&]() {
 #pragma unroll
-  for (int t = 0; t < MT; ++t) acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int u = 0; u < kVecPerThread; ++u) {
+      const int v = u * 256 + tid;
+      const int t = v / 24, kv = v - t * 24;
+      if (v < kVec) *reinterpret_cast<uint4 *>(xs + t * kMmXStride + 16 * kv) = xr[u];
+    }
+  };
+  load_x(0);  // in flight during the whole prologue
 
-  // K = 24 * atoms_per_row; this wave's share of 96-wide chunks (4 atoms).
-  // Two-deep pipeline: chunk ch+KW's code words and activation tiles are
-  // loaded while chunk ch is decoded and multiplied.
-  const int64_t n_chunks = (atoms_per_row + 3) / 4;
-  auto load_chunk = [&](int64_t ch, uint32_t (&w)[3], bf16x8_t (&av)[3][MT]) {
+  // ---- per-row byte tables (threads 0..127, one row each): hi low/high, lo low/high bytes ----
+  auto build_row_tables = [&]() {
+    if (tid >= kMmRows) return;
+    const int64_t row = row0 + tid;
+    const float sl = __uint_as_float(kSLatticeBits);
+    const float sig = row < rows ? __half2float(__ushort_as_half(sigma16[row])) : 0.f;
+    const uint32_t v0 = dq_value(0, sig, sl), v1 = dq_value(1, sig, sl), v2 = dq_value(2, sig, sl);
+    const uint32_t v3 = dq_value(3, sig, sl), v4 = dq_value(4, sig, sl);
+    const uint32_t h[8] = {v0, v1, v2, v4, v4 ^ 0x8000u, v3 ^ 0x8000u, v2 ^ 0x8000u, v1 ^ 0x8000u};
+    uint32_t hl[8];
 #pragma unroll
-    for (int ks = 0; ks < 3; ++ks) {
-      const int kk = 32 * ks + 8 * q;
-      const int64_t a = ch * 4 + kk / 24;
-      const int plane = (kk % 24) / 8;
-      w[ks] = 0u;
-      if (ch < n_chunks && row_live && a < atoms_per_row) {
-        const int64_t n = row * atoms_per_row + a - g_lo * 4;
-        const uint8_t *bp = pb + (n >> 2) * 9 + 2 * (n & 3);
-        const uint32_t v = (static_cast<uint32_t>(bp[0]) << 16) | (static_cast<uint32_t>(bp[1]) << 8) | bp[2];
-        int32_t code = static_cast<int32_t>((v >> (6 - 2 * (n & 3))) & 0x3FFFFu);
-        if (code > kKissing) code = 0;
-        const uint32_t *ep = reinterpret_cast<const uint32_t *>(kp_gemv + code);
-        w[ks] = ep[plane];
+    for (int e = 0; e < 8; ++e) hl[e] = hi_lo_pack(__half2float(__ushort_as_half(static_cast<uint16_t>(h[e]))));
+    uint32_t t[8];
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      uint32_t lb0 = 0, lb1 = 0, hb0 = 0, hb1 = 0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t b0 = hl[e] >> (16 * half), b1 = hl[e + 4] >> (16 * half);
+        lb0 |= (b0 & 0xFFu) << (8 * e);
+        lb1 |= (b1 & 0xFFu) << (8 * e);
+        hb0 |= ((b0 >> 8) & 0xFFu) << (8 * e);
+        hb1 |= ((b1 >> 8) & 0xFFu) << (8 * e);
       }
-      const int64_t kcol = ch * 96 + kk;
+      t[4 * half + 0] = lb0;
+      t[4 * half + 1] = lb1;
+      t[4 * half + 2] = hb0;
+      t[4 * half + 3] = hb1;
+    }
+    rtab[2 * tid] = make_uint4(t[0], t[1], t[2], t[3]);
+    rtab[2 * tid + 1] = make_uint4(t[4], t[5], t[6], t[7]);
+  };
+
+  // ---- codes -> kp_dq words in LDS ----
+  // Rows holding a multiple of 4 atoms: a thread decodes whole 9-byte groups
+  // (4 codes from 3 dwords); the row tables are built while those loads are
+  // in flight, then all table loads are issued before any LDS store.
+  constexpr int GPR = NA / 4;                               // groups per row in this block
+  constexpr int NG = (kMmRows * GPR + 255) / 256;           // groups per thread
+  if ((atoms_per_row & 3) == 0) {
+    uint32_t dw[NG][3], off[NG];
+    bool live[NG];
 #pragma unroll
-      for (int t = 0; t < MT; ++t) {
-        const int64_t tok = t * 16 + j;
-        if (ch < n_chunks && tok < m_total && kcol < cols) {
-          av[ks][t] = *reinterpret_cast<const bf16x8_t *>(x + tok * cols + kcol);
-        } else {
-#pragma unroll
-          for (int c = 0; c < 8; ++c) av[ks][t][c] = __builtin_bit_cast(__bf16, static_cast<uint16_t>(0));
+    for (int u = 0; u < NG; ++u) {
+      const int g = u * 256 + tid;
+      const int r = g / GPR, k = g - r * GPR;
+      const int64_t row = row0 + r;
+      const int64_t a = a_begin + 4 * k;
+      live[u] = g < kMmRows * GPR && row < rows && a < atoms_per_row;
+      dw[u][0] = dw[u][1] = dw[u][2] = 0u;
+      off[u] = 0;
+      if (live[u]) {
+        const int64_t b = (row * atoms_per_row + a) / 4 * 9;
+        const int64_t b4 = b & ~static_cast<int64_t>(3);
+        off[u] = static_cast<uint32_t>(b & 3);
+        const uint32_t *pw = reinterpret_cast<const uint32_t *>(packed + b4);
+        if (b4 + 12 <= packed_bytes) {
+          dw[u][0] = pw[0];
+          dw[u][1] = pw[1];
+          dw[u][2] = pw[2];
+        } else {  // the stream's last group: byte loads inside the stream
+          uint32_t t[3] = {0u, 0u, 0u};
+          for (int e = 0; e < 12 && b4 + e < packed_bytes; ++e) t[e / 4] |= static_cast<uint32_t>(packed[b4 + e]) << (8 * (e % 4));
+          dw[u][0] = t[0];
+          dw[u][1] = t[1];
+          dw[u][2] = t[2];
         }
       }
     }
-  };
-  uint32_t w_cur[3], w_nxt[3];
-  bf16x8_t a_cur[3][MT], a_nxt[3][MT];
-  load_chunk(wave, w_cur, a_cur);
-  for (int64_t ch = wave; ch < n_chunks; ch += KW) {
-    load_chunk(ch + KW, w_nxt, a_nxt);
+    build_row_tables();
+    uint3 e[NG][4];
 #pragma unroll
-    for (int ks = 0; ks < 3; ++ks) {
-      bf16x8_t bh, bl;
+    for (int u = 0; u < NG; ++u) {
+      int32_t c[4] = {0, 0, 0, 0};
+      if (live[u]) group_codes(dw[u][0], dw[u][1], dw[u][2], off[u], c);
 #pragma unroll
-      for (int c = 0; c < 8; ++c) {
-        const int k = static_cast<int>(static_cast<int32_t>(w_cur[ks] << (28 - 4 * c)) >> 28);
-        const int m = k < 0 ? -k : k;
-        uint32_t hl = m == 0 ? mag[0] : m == 1 ? mag[1] : m == 2 ? mag[2] : m == 3 ? mag[3] : mag[4];
-        if (k < 0) hl ^= 0x80008000u;  // W = hi + lo, both negated
-        bh[c] = __builtin_bit_cast(__bf16, static_cast<uint16_t>(hl & 0xFFFFu));
-        bl[c] = __builtin_bit_cast(__bf16, static_cast<uint16_t>(hl >> 16));
-      }
-#pragma unroll
-      for (int t = 0; t < MT; ++t) {
-        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_cur[ks][t], bh, acc[t], 0, 0, 0);
-        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_cur[ks][t], bl, acc[t], 0, 0, 0);
+      for (int i = 0; i < 4; ++i) {
+        const int32_t code = c[i] > kKissing ? 0 : c[i];
+        e[u][i] = *reinterpret_cast<const uint3 *>(kp_dq + static_cast<int64_t>(code) * 3);
       }
     }
 #pragma unroll
-    for (int ks = 0; ks < 3; ++ks) {
-      w_cur[ks] = w_nxt[ks];
-#pragma unroll
-      for (int t = 0; t < MT; ++t) a_cur[ks][t] = a_nxt[ks][t];
+    for (int u = 0; u < NG; ++u) {
+      const int g = u * 256 + tid;
+      if (g < kMmRows * GPR) {
+        const int r = g / GPR, k = g - r * GPR;
+        uint4 *d = reinterpret_cast<uint4 *>(wt + r * WS + 12 * k);   // 48 B, 16-byte aligned
+        d[0] = make_uint4(e[u][0].x, e[u][0].y, e[u][0].z, e[u][1].x);
+        d[1] = make_uint4(e[u][1].y, e[u][1].z, e[u][2].x, e[u][2].y);
+        d[2] = make_uint4(e[u][2].z, e[u][3].x, e[u][3].y, e[u][3].z);
+      }
+    }
+  } else {
+    // general rows: one code per (row, atom)
+    build_row_tables();
+    for (int c = tid; c < kMmRows * NA; c += 256) {
+      const int r = c / NA, a = c - r * NA;
+      const int64_t row = row0 + r, atom = a_begin + a;
+      int32_t code = 0;
+      if (row < rows && atom < atoms_per_row) {
+        code = packed_index_dw(packed, packed_bytes, row * atoms_per_row + atom);
+        if (code > kKissing) code = 0;
+      }
+      const uint3 e = *reinterpret_cast<const uint3 *>(kp_dq + static_cast<int64_t>(code) * 3);
+      uint32_t *d = wt + r * WS + 3 * a;
+      d[0] = e.x;
+      d[1] = e.y;
+      d[2] = e.z;
     }
   }
-  // reduce the KW partial tiles: C[token 4q'+e][row j] lives in lane j + 16 q', element e
+
+  f32x4_t acc[MT][2];
 #pragma unroll
   for (int t = 0; t < MT; ++t)
 #pragma unroll
-    for (int e = 0; e < 4; ++e) red[(wave * MT + t) * 256 + e * 64 + lane] = acc[t][e];
+    for (int rt = 0; rt < 2; ++rt) acc[t][rt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  store_x();
   __syncthreads();
-  for (int i = threadIdx.x; i < MT * 256; i += NT) {
-    const int t = i / 256, e = (i % 256) / 64, l = i % 64;
-    float sum = 0.f;
+  const int r0l = 32 * wave + j, r1l = 32 * wave + 16 + j;
+  const uint4 ta0 = rtab[2 * r0l], tb0 = rtab[2 * r0l + 1], ta1 = rtab[2 * r1l], tb1 = rtab[2 * r1l + 1];
+  const uint32_t *wrow0 = wt + r0l * WS;
+  const uint32_t *wrow1 = wt + r1l * WS;
 #pragma unroll
-    for (int w = 0; w < KW; ++w) sum += red[(w * MT + t) * 256 + e * 64 + l];
-    const int64_t tok = t * 16 + 4 * (l >> 4) + e;
-    const int64_t r = row0 + (l & 15);
-    if (tok < m_total && r < rows) y[tok * rows + r] = sum;
+  for (int st = 0; st < SPB; ++st) {
+    if (st >= n_stages) break;
+    if (st + 1 < n_stages) load_x(st + 1);
+#pragma unroll
+    for (int ks = 0; ks < 6; ++ks) {
+      const int kk = 32 * ks + 8 * q;
+      const int a = st * kMmStageAtoms + kk / 24, pl = (kk % 24) / 8;
+      const uint32_t w0 = wrow0[a * 3 + pl], w1 = wrow1[a * 3 + pl];
+      const bf16x8_t bh0 = perm_decode(w0, ta0.x, ta0.y, ta0.z, ta0.w);
+      const bf16x8_t bl0 = perm_decode(w0, tb0.x, tb0.y, tb0.z, tb0.w);
+      const bf16x8_t bh1 = perm_decode(w1, ta1.x, ta1.y, ta1.z, ta1.w);
+      const bf16x8_t bl1 = perm_decode(w1, tb1.x, tb1.y, tb1.z, tb1.w);
+#pragma unroll
+      for (int t = 0; t < MT; ++t) {
+        const bf16x8_t av = *reinterpret_cast<const bf16x8_t *>(xs + (16 * t + j) * kMmXStride + 2 * kk);
+        acc[t][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bh0, acc[t][0], 0, 0, 0);
+        acc[t][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bh1, acc[t][1], 0, 0, 0);
+        acc[t][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bl0, acc[t][0], 0, 0, 0);
+        acc[t][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bl1, acc[t][1], 0, 0, 0);
+      }
+    }
+    if (st + 1 < n_stages) {
+      __syncthreads();
+      store_x();
+      __syncthreads();
+    }
   }
+
+  // ---- epilogue: C[token 16t + 4q + e][row 32*wave + 16rt + j] ----
+  float *dst = splits == 1 ? y : partial + (static_cast<int64_t>(blockIdx.y) * splits + split) * 64 * rows;
+  const int64_t tok_base = splits == 1 ? tok0 : 0;   // partial tiles are indexed per slab
+#pragma unroll
+  for (int t = 0; t < MT; ++t)
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+      const int64_t row = row0 + 32 * wave + 16 * rt + j;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int64_t tl = 16 * t + 4 * q + e;
+        if (row < rows && tok0 + tl < m_total) dst[(tok_base + tl) * rows + row] = acc[t][rt][e];
+      }
+    }
 }
 
-template <int KW>
-int launch_dqg(const uint8_t *packed, int64_t packed_bytes, const uint16_t *sigma16, int64_t rows, int64_t apr,
-               const uint16_t *x, int64_t m, float *y, const uint4 *tab, hipStream_t s) {
-  const int64_t pbytes = (16 * apr + 8) / 4 * 9 + 32;
-  const size_t p16 = ((static_cast<size_t>(pbytes) + 15) & ~static_cast<size_t>(15)) + 16;
-  const dim3 g(static_cast<unsigned>((rows + 15) / 16));
-  const int mt = static_cast<int>((m + 15) / 16);
-  const size_t shm = p16 + static_cast<size_t>(KW) * (mt <= 2 ? 2 : 4) * 256 * 4;
-  if (shm > 64 * 1024) return fail(PLX_EINVAL, "dequant_linear: rows of %lld atoms are too long", static_cast<long long>(apr));
-  if (mt <= 2)
-    hipLaunchKernelGGL((dqgemm_kernel<KW, 2>), g, dim3(KW * 64), shm, s, packed, packed_bytes, sigma16, rows, apr, x, m,
-                       y, tab);
-  else
-    hipLaunchKernelGGL((dqgemm_kernel<KW, 4>), g, dim3(KW * 64), shm, s, packed, packed_bytes, sigma16, rows, apr, x, m,
-                       y, tab);
-  return check_launch("dqgemm_kernel");
+// y[tok, r] = sum over splits (ascending) of the partial tiles; 4 outputs per
+// thread (rows % 4 == 0) or 1, loads of 4 splits issued together.
+template <bool VEC>
+__global__ __launch_bounds__(256) void dqmm_reduce_kernel(const float *__restrict__ partial, int splits, int64_t rows,
+                                                          int64_t m_total, float *__restrict__ y) {
+  constexpr int W = VEC ? 4 : 1;
+  const int64_t i = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * W;
+  if (i >= m_total * rows) return;
+  const int64_t tok = i / rows, row = i - tok * rows;
+  const int64_t slab = tok / 64, tl = tok - slab * 64;
+  const int64_t stride = 64 * rows;
+  const float *p = partial + (slab * splits) * stride + tl * rows + row;
+  typedef float f4 __attribute__((ext_vector_type(4)));
+  typedef float fw __attribute__((ext_vector_type(W)));
+  fw s = {};
+  int k = 0;
+  for (; k + 4 <= splits; k += 4) {
+    fw v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) v[u] = *reinterpret_cast<const fw *>(p + static_cast<int64_t>(k + u) * stride);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) s += v[u];
+  }
+  for (; k < splits; ++k) s += *reinterpret_cast<const fw *>(p + static_cast<int64_t>(k) * stride);
+  *reinterpret_cast<fw *>(y + i) = s;
+  (void)sizeof(f4);
 }
+
+struct MmPlan {
+  int spb = 1, splits = 1;
+};
+
+// Stages per block and K splits: 2 stages per block, or 1 when that leaves
+// fewer than 256 blocks.
+MmPlan mm_plan(int64_t rows, int64_t apr) {
+  MmPlan p;
+  const int64_t stages = (apr + kMmStageAtoms - 1) / kMmStageAtoms;
+  const int64_t row_blocks = (rows + kMmRows - 1) / kMmRows;
+  int64_t spb = 2;
+  if (row_blocks * ((stages + 1) / 2) < 256) spb = 1;
+  if (spb > stages) spb = stages;
+  if (spb < 1) spb = 1;
+  p.spb = static_cast<int>(spb);
+  p.splits = static_cast<int>((stages + spb - 1) / spb);
+  if (p.splits < 1) p.splits = 1;
+  return p;
+}
+
+template <int MT, int SPB>
+int launch_dqmm_t(const uint8_t *packed, int64_t pb, const uint16_t *sigma16, int64_t rows, int64_t apr,
+                  const uint16_t *x, int64_t m, float *y, float *partial, int splits, const uint32_t *kp_dq,
+                  hipStream_t s) {
+  const int64_t row_blocks = (rows + kMmRows - 1) / kMmRows;
+  const int64_t slabs = (m + 63) / 64;
+  constexpr int WS = kMmStageAtoms * SPB * 3 + 4;
+  const size_t shm = static_cast<size_t>(16 * MT) * kMmXStride + static_cast<size_t>(kMmRows) * WS * 4 +
+                     static_cast<size_t>(kMmRows) * 32;
+  const dim3 g(static_cast<unsigned>(row_blocks * splits), static_cast<unsigned>(slabs));
+  hipLaunchKernelGGL((dqmm_kernel<MT, SPB>), g, dim3(256), shm, s, packed, pb, sigma16, rows, apr, x, m, splits, kp_dq,
+                     y, partial);
+  return check_launch("dqmm_kernel");
+}
+
+template <int MT>
+int launch_dqmm(const uint8_t *packed, int64_t pb, const uint16_t *sigma16, int64_t rows, int64_t apr,
+                const uint16_t *x, int64_t m, float *y, float *partial, const MmPlan &pl, const uint32_t *kp_dq,
+                hipStream_t s) {
+  if (pl.spb == 1) return launch_dqmm_t<MT, 1>(packed, pb, sigma16, rows, apr, x, m, y, partial, pl.splits, kp_dq, s);
+  return launch_dqmm_t<MT, 2>(packed, pb, sigma16, rows, apr, x, m, y, partial, pl.splits, kp_dq, s);
+}
+
+bool uses_mfma(int x_is_f32, int64_t m) { return !x_is_f32 && m > 16; }
 
 }  // namespace
 
+size_t dequant_linear_workspace_bytes(int64_t rows, int64_t cols, int64_t m, int x_is_f32) {
+  if (!uses_mfma(x_is_f32, m) || rows <= 0) return 0;
+  const MmPlan pl = mm_plan(rows, cols / kDim);
+  if (pl.splits == 1) return 0;
+  return static_cast<size_t>((m + 63) / 64) * pl.splits * 64 * static_cast<size_t>(rows) * sizeof(float);
+}
+
 int launch_dequant_linear(const uint8_t *packed, const uint16_t *sigma16, int64_t rows, int64_t cols, const void *x,
-                          int x_is_f32, int64_t m, float *y, hipStream_t s) {
+                          int x_is_f32, int64_t m, float *y, void *workspace, size_t workspace_bytes, hipStream_t s) {
   if ((reinterpret_cast<uintptr_t>(x) & 15u) != 0 || (reinterpret_cast<uintptr_t>(packed) & 15u) != 0)
     return fail(PLX_EINVAL, "dequant_linear: x and packed must be 16-byte aligned");
+  const size_t need = dequant_linear_workspace_bytes(rows, cols, m, x_is_f32);
+  if (workspace_bytes < need || (need && workspace == nullptr))
+    return fail(PLX_EINVAL, "dequant_linear: workspace of %zu bytes is smaller than the %zu needed", workspace_bytes, need);
+  if (need && (reinterpret_cast<uintptr_t>(workspace) & 15u) != 0)
+    return fail(PLX_EINVAL, "dequant_linear: workspace must be 16-byte aligned");
   const DeviceTables *tab = nullptr;
   int st = get_tables(&tab);
   if (st != PLX_OK) return st;
   const int64_t apr = cols / kDim;
   const int64_t pb = ((rows * apr + 3) / 4) * 9;  // packed stream length
-  const uint4 *kp = reinterpret_cast<const uint4 *>(tab->kp_gemv);
-  // bf16 batches of 17..64 tokens: MFMA dequant-GEMM (larger batches loop over 64-token slabs)
-  if (!x_is_f32 && m > 16) {
+  if (uses_mfma(x_is_f32, m)) {
+    // bf16 batches above 16 tokens: MFMA dequant-GEMM in slabs of 64 tokens
+    const MmPlan pl = mm_plan(rows, apr);
     const uint16_t *xb = static_cast<const uint16_t *>(x);
-    for (int64_t m0 = 0; m0 < m; m0 += 64) {
-      const int64_t mm = m - m0 < 64 ? m - m0 : 64;
-      const int st2 = rows >= 4096 ? launch_dqg<4>(packed, pb, sigma16, rows, apr, xb + m0 * cols, mm, y + m0 * rows, kp, s)
-                                   : launch_dqg<8>(packed, pb, sigma16, rows, apr, xb + m0 * cols, mm, y + m0 * rows, kp, s);
-      if (st2 != PLX_OK) return st2;
-    }
-    return PLX_OK;
+    float *part = static_cast<float *>(workspace);
+    const int mt = m >= 64 ? 4 : m > 32 ? 4 : 2;
+    st = mt == 4 ? launch_dqmm<4>(packed, pb, sigma16, rows, apr, xb, m, y, part, pl, tab->kp_dq, s)
+                 : launch_dqmm<2>(packed, pb, sigma16, rows, apr, xb, m, y, part, pl, tab->kp_dq, s);
+    if (st != PLX_OK || pl.splits == 1) return st;
+    const int64_t n = m * rows;
+    if (rows % 4 == 0 && (reinterpret_cast<uintptr_t>(y) & 15u) == 0)
+      hipLaunchKernelGGL((dqmm_reduce_kernel<true>), dim3(static_cast<unsigned>((n / 4 + 255) / 256)), dim3(256), 0, s,
+                         part, pl.splits, rows, m, y);
+    else
+      hipLaunchKernelGGL((dqmm_reduce_kernel<false>), dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s,
+                         part, pl.splits, rows, m, y);
+    return check_launch("dqmm_reduce_kernel");
   }
+  const uint4 *kp = reinterpret_cast<const uint4 *>(tab->kp_gemv);
   // lanes per row: about 2-5 atoms per lane
   if (apr >= 160)
     return x_is_f32 ? launch_dql<64, true>(packed, pb, sigma16, rows, apr, x, m, y, kp, s)

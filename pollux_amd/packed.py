@@ -65,10 +65,14 @@ def dequant_linear(
         xx = xx.clone()
     sg = sigma16.reshape(-1).contiguous()
     y = torch.empty((xx.shape[0], out_features), dtype=torch.float32, device=pk.device)
+    x_f32 = int(xx.dtype == torch.float32)
+    lib = _lib.lib()
+    nws = int(lib.plx_dequant_linear_workspace_bytes(out_features, in_features, xx.shape[0], x_f32))
+    ws = torch.empty(max(nws, 16), dtype=torch.uint8, device=pk.device) if nws else None
     with torch.cuda.device(pk.device):
-        st = _lib.lib().plx_dequant_linear(
+        st = lib.plx_dequant_linear(
             _lib.ptr(pk), pk.numel(), _lib.ptr(sg), out_features, in_features, _lib.ptr(xx),
-            int(xx.dtype == torch.float32), xx.shape[0], _lib.ptr(y), _lib.stream_of(pk.device),
+            x_f32, xx.shape[0], _lib.ptr(y), _lib.ptr(ws), nws, _lib.stream_of(pk.device),
         )
     _lib.check(st, "dequant_linear")
     return y.reshape(*lead, out_features)
