@@ -39,11 +39,11 @@
 //   Each (atom, slice) ends as a 16-byte record: the best key and, per lane,
 //   the best group of the lanes that hold it.
 //
-// resolve_kernel -- one thread per atom: the maximum key over the slices, an
+// resolve_kernel -- per atom the maximum key over the slices, then an
 //   exact-product rescan (v_dot2_f32_bf16; NN-P: fp64 dot products of the
 //   fp32 atom and the fp32 codebook rows, exact up to 2^-48) of the few
-//   groups that hold it to find the lowest code, then the index and the
-//   packed 9-byte groups.  Both
+//   groups that hold it to find the lowest code, 8 lanes per group with
+//   coalesced table reads, then the index and the packed 9-byte groups.  Both
 //   fp32 sums (MFMA, dot2) lie within 2^-20 * sum|x_i c_i| of the exact score
 //   (MFMA measured at < 2^-22), so the result equals the exact-score answer
 //   on every atom that is not a near-tie within that envelope.
@@ -83,11 +83,12 @@ constexpr int n_splits() {
 
 template <int MODE>
 __device__ __forceinline__ int initial_threshold() {
-  // NN-B: largest fp32 whose bf16 rounding is below 2.0 (bf16 0x3FFF is odd).
+  // NN-B: the largest group key of bucket 0x3FFF (bf16 max below 2.0); any
+  //       group reaching bucket 0x4000 has a larger key (group_key).
   // NN-T: largest fp32 s with 2*s < 0x407FFFFF.
   // NN-P: +0.0 -- no score threshold (every nonzero atom has a positive
   //       maximum: the best +-4 pair scores 4s(|x_i| + |x_j|)).
-  return MODE == kModeB ? 0x3FFF7FFF : MODE == kModeP ? 0 : 0x3FFFFFFE;
+  return MODE == kModeB ? 0x3FFFFFFF : MODE == kModeP ? 0 : 0x3FFFFFFE;
 }
 
 // New threshold after a group whose maximum is gm.  NN-T: gm itself.  NN-B:
@@ -125,12 +126,39 @@ __device__ __forceinline__ void load_coords8(const float *__restrict__ src, cons
   }
 }
 
-template <int MODE, bool FUSED>
-__global__ __launch_bounds__(kThreads, 2) void nn_kernel(const float *__restrict__ src,
-                                                          const float *__restrict__ sigma, int64_t atoms_per_row,
-                                                          int64_t n_atoms, const uint8_t *__restrict__ tiles,
-                                                          int n_slices, int tiles_per_slice,
-                                                          uint4 *__restrict__ records) {
+// bf16 lattice coordinates of every atom, row-major [n_atoms][24] (one
+// 16-byte plane of 8 per thread), written once per launch so the scoring
+// blocks of all slices load ready-made MFMA B operands instead of each
+// repeating the row-scale divisions.  NN-B / NN-T only.
+template <bool FUSED>
+__global__ __launch_bounds__(256) void prep_kernel(const float *__restrict__ src, const float *__restrict__ sigma,
+                                                   int64_t atoms_per_row, int64_t n_atoms, uint4 *__restrict__ xb) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;  // plane i % 3 of atom i / 3
+  if (i >= n_atoms * 3) return;
+  const int64_t a = i / 3;
+  float v[8];
+  load_coords8<FUSED>(src, sigma, atoms_per_row, n_atoms, a, static_cast<int>(i - 3 * a), v);
+  uint4 w;
+  w.x = bf16_rne_bits(v[0]) | (bf16_rne_bits(v[1]) << 16);
+  w.y = bf16_rne_bits(v[2]) | (bf16_rne_bits(v[3]) << 16);
+  w.z = bf16_rne_bits(v[4]) | (bf16_rne_bits(v[5]) << 16);
+  w.w = bf16_rne_bits(v[6]) | (bf16_rne_bits(v[7]) << 16);
+  xb[i] = w;
+}
+
+// NN-B tracking key of a group: bucket (round-half-up, see raised_threshold)
+// in the high half, 0xFFFF - group in the low half, so one signed max keeps
+// the highest bucket and, within it, the earliest group.
+__device__ __forceinline__ int group_key(int gm, int group) {
+  return static_cast<int>(((static_cast<uint32_t>(gm) + 0x8000u) & 0xFFFF0000u) |
+                          (static_cast<uint32_t>(0xFFFF - group) & 0xFFFFu));
+}
+
+// src: NN-P: the fp32 atoms; NN-B / NN-T: xb, the bf16 planes of prep_kernel.
+template <int MODE>
+__global__ __launch_bounds__(kThreads, 2) void nn_kernel(const void *__restrict__ src, int64_t n_atoms,
+                                                          const uint8_t *__restrict__ tiles, int n_slices,
+                                                          int tiles_per_slice, uint4 *__restrict__ records) {
   __shared__ __align__(16) uint8_t lds[2][kStageBytes];
 
   const int slice = static_cast<int>(blockIdx.x % static_cast<unsigned>(n_slices));
@@ -145,8 +173,15 @@ __global__ __launch_bounds__(kThreads, 2) void nn_kernel(const float *__restrict
   bf16x8 b[NS][kAT];
 #pragma unroll
   for (int at = 0; at < kAT; ++at) {
+    const int64_t a = wave_atom0 + at * 16 + j;
+    if constexpr (NS == 1) {
+      uint4 w = make_uint4(0u, 0u, 0u, 0u);
+      if (a < n_atoms && q < 3) w = static_cast<const uint4 *>(src)[a * 3 + q];
+      b[0][at] = __builtin_bit_cast(bf16x8, w);
+      continue;
+    }
     float v[8];
-    load_coords8<FUSED>(src, sigma, atoms_per_row, n_atoms, wave_atom0 + at * 16 + j, q, v);
+    load_coords8<false>(static_cast<const float *>(src), nullptr, 1, n_atoms, a, q, v);
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const uint32_t h = bf16_rne_bits(v[e]);
@@ -191,8 +226,8 @@ __global__ __launch_bounds__(kThreads, 2) void nn_kernel(const float *__restrict
   // into the group maximum while tile k+1's MFMAs issue, and tile k+1's A
   // operand is read from LDS right after tile k's first MFMA.  A group of 8
   // tiles is compared against the threshold once its last tile has been
-  // folded, i.e. during the next group's first tile; the slice's last tile is
-  // folded after the loop.
+  // folded, i.e. during the next group's first tile (NN-B: the next group's
+  // tile at % 8); the slice's last tile is folded after the loop.
   int gm[kAT];
   f32x4 acc[kAT], part[kAT];
 #pragma unroll
@@ -239,8 +274,12 @@ __global__ __launch_bounds__(kThreads, 2) void nn_kernel(const float *__restrict
           asm volatile("" : "+v"(m));
           if (FIRST && t == 0) {
             gdone[at] = m;
-            up[at] = m > R[at];
+            if constexpr (MODE != kModeB) up[at] = m > R[at];
           }
+          // NN-B: the closed group's key enters R in tile at % 8 of the next
+          // group, one atom tile per code tile, so the key's VALU work is
+          // spread evenly under the MFMAs instead of piling up in tile 0.
+          if (MODE == kModeB && at % 8 == t) R[at] = max(R[at], group_key(gdone[at], group_prev));
           gm[at] = m;
           if constexpr (NS == 1)
             acc[at] = c;
@@ -262,11 +301,13 @@ __global__ __launch_bounds__(kThreads, 2) void nn_kernel(const float *__restrict
 #pragma unroll 1
     for (int k0 = 0; k0 < kST; k0 += kG) {
       eight_tiles(k0);
+      if constexpr (MODE != kModeB) {
 #pragma unroll
-      for (int at = 0; at < kAT; ++at) {
-        if (up[at]) {
-          R[at] = raised_threshold<MODE>(gdone[at]);
-          best[at] = group_prev;
+        for (int at = 0; at < kAT; ++at) {
+          if (up[at]) {
+            R[at] = raised_threshold<MODE>(gdone[at]);
+            best[at] = group_prev;
+          }
         }
       }
       group_prev = (t0 + st * kST + k0) / kG;
@@ -278,7 +319,9 @@ __global__ __launch_bounds__(kThreads, 2) void nn_kernel(const float *__restrict
   for (int at = 0; at < kAT; ++at) {
     int m = max(max(gm[at], __float_as_int(acc[at][0])), __float_as_int(acc[at][1]));
     m = max(max(m, __float_as_int(acc[at][2])), __float_as_int(acc[at][3]));
-    if (m > R[at]) {
+    if constexpr (MODE == kModeB) {
+      R[at] = max(R[at], group_key(m, group_prev));
+    } else if (m > R[at]) {
       R[at] = raised_threshold<MODE>(m);
       best[at] = group_prev;
     }
@@ -288,12 +331,19 @@ __global__ __launch_bounds__(kThreads, 2) void nn_kernel(const float *__restrict
   // key: the slice's best bucket (NN-B, bf16 bits) or fp32 score bits (NN-T),
   // 0 when nothing beat the origin threshold; then, for each of the four lanes
   // of the atom, its best group if it holds the slice maximum (else 0xFFFF).
+  // NN-B: only the lanes whose earliest group at that bucket is the slice's
+  // earliest -- the lowest code of the bucket lies in that group.
 #pragma unroll
   for (int at = 0; at < kAT; ++at) {
     int Rm = R[at];
     Rm = max(Rm, __shfl_xor(Rm, 16, 64));
     Rm = max(Rm, __shfl_xor(Rm, 32, 64));
-    const uint32_t g16 = (best[at] >= 0 && R[at] == Rm) ? static_cast<uint32_t>(best[at]) : 0xFFFFu;
+    uint32_t g16;
+    if constexpr (MODE == kModeB)
+      g16 = (R[at] == Rm && Rm != initial_threshold<MODE>()) ? 0xFFFFu - (static_cast<uint32_t>(R[at]) & 0xFFFFu)
+                                                              : 0xFFFFu;
+    else
+      g16 = (best[at] >= 0 && R[at] == Rm) ? static_cast<uint32_t>(best[at]) : 0xFFFFu;
     const uint32_t g0 = static_cast<uint32_t>(__shfl(static_cast<int>(g16), j, 64));
     const uint32_t g1 = static_cast<uint32_t>(__shfl(static_cast<int>(g16), j + 16, 64));
     const uint32_t g2 = static_cast<uint32_t>(__shfl(static_cast<int>(g16), j + 32, 64));
@@ -307,156 +357,282 @@ __global__ __launch_bounds__(kThreads, 2) void nn_kernel(const float *__restrict
   }
 }
 
-// Resolve: one thread per atom.  Takes the maximum key over the slices, then
-// rescans (v_dot2_f32_bf16: exact bf16 products, fp32 accumulation) the best
-// groups of every (slice, lane) that holds it -- typically one group, 4 rows
-// of 8 tiles = 32 codes -- and picks the lowest code reaching the bucket
-// (NN-B) or the highest fp32 score (NN-T, lowest code on ties); writes the
-// int32 index and, optionally, the packed 9-byte groups.
+// Resolve: per block 256 atoms, in rounds.
+//   scan     thread per atom: the maximum key M over the slices, the atom's
+//            coordinates into LDS (bf16 pairs; NN-P: fp32), then up to
+//            kRsPerRound candidate slots (slice, lane) whose record holds M,
+//            each naming a group of 8 tiles x 4 codes of that lane;
+//   compact  a block-wide prefix sum packs the candidates into one list;
+//   rescan   8 lanes per candidate, lane t scoring the 4 codes of tile t of
+//            the group (NN-B/T: 192 B contiguous in the lane-major bf16
+//            table, v_dot2_f32_bf16 = exact bf16 products, fp32 sums; NN-P:
+//            4 consecutive rows of the raw int8 codebook, fp64 dot products of
+//            the fp32 atom with the fp32 codebook values, exact to 2^-48),
+//            then a 3-step shuffle reduction per candidate;
+//   merge    thread per atom folds its candidates' results in list order.
+// An atom with more than kRsPerRound candidates continues in the next round.
+// NN-B picks the lowest code whose bf16 score bucket equals M (falling back to
+// the best rounded score, lowest code on ties, if the fp32 sums disagree with
+// the sweep's); NN-T the highest fp32 score, lowest code on ties; NN-P the
+// highest fp64 score, lowest code on ties.  Then the int32 index and,
+// optionally, the packed 9-byte groups.
+constexpr int kRsPerRound = 4;
+constexpr int kRsCap = 256 * kRsPerRound;
+
+template <int MODE>
+struct RsScore {  // per-candidate / per-atom running result
+  typedef typename std::conditional<MODE == kModeP, double, float>::type T;
+};
+
 template <int MODE, bool FUSED>
 __global__ __launch_bounds__(256) void resolve_kernel(const uint4 *__restrict__ records, int n_slices,
                                                       int64_t n_atoms, const float *__restrict__ src,
                                                       const float *__restrict__ sigma, int64_t atoms_per_row,
-                                                      const uint8_t *__restrict__ rescan,
+                                                      const uint4 *__restrict__ xb, const uint8_t *__restrict__ rescan,
                                                       int32_t *__restrict__ idx_out, uint8_t *__restrict__ packed_out) {
+  typedef typename RsScore<MODE>::T score_t;
+  constexpr int XW = MODE == kModeP ? kDim : 12;  // words of one atom's coordinates in LDS
+  __shared__ __align__(16) uint32_t xs[256 * XW];
+  __shared__ uint32_t tmp[kRsPerRound * 256];     // per-thread candidates before compaction
+  __shared__ uint32_t cand[kRsCap];               // atom | lane << 8 | group << 10
+  __shared__ score_t res_v[kRsCap];
+  __shared__ uint32_t res_code[kRsCap];
+  __shared__ uint32_t res_found[MODE == kModeB ? kRsCap : 1];
+  __shared__ uint32_t Ms[256];                    // per atom: the maximum key
+  __shared__ int wave_sum[4];
   __shared__ int32_t ids[256];
   __shared__ __align__(16) uint8_t bytes[64 * 9];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t a0 = static_cast<int64_t>(blockIdx.x) * 256;
-  const int64_t a = a0 + threadIdx.x;
-  int32_t id = 0;
+  const int64_t a = a0 + tid;
+
+  // ---- scan: M and the slices holding it, coordinates, origin rules ----
+  // Only the 4-byte keys are read here, 8 slices' loads in flight at a time.
+  uint32_t M = 0;
+  uint64_t mask = 0;  // slices whose key equals M (n_slices <= 64)
+  bool active = false;
   if (a < n_atoms) {
-    uint32_t M = 0;
-    for (int s = 0; s < n_slices; ++s) M = max(M, records[static_cast<int64_t>(s) * n_atoms + a].x);
-    // NN-B/T: bf16 pairs of the atom; NN-P: the fp32 atom in fp64 and |x|^2
-    uint32_t xw[MODE == kModeP ? 1 : 12];
-    double xd[MODE == kModeP ? kDim : 1];
+    const uint32_t *keys = reinterpret_cast<const uint32_t *>(records);
+    for (int s0 = 0; s0 < n_slices; s0 += 8) {
+      uint32_t k[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) k[i] = s0 + i < n_slices ? keys[4 * (static_cast<int64_t>(s0 + i) * n_atoms + a)] : 0u;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        if (k[i] > M) {
+          M = k[i];
+          mask = 0;
+        }
+        if (k[i] == M) mask |= uint64_t{1} << (s0 + i);
+      }
+    }
     double nrm2 = 0.0;
 #pragma unroll
     for (int qq = 0; qq < 3; ++qq) {
-      float v[8];
-      load_coords8<FUSED>(src, sigma, atoms_per_row, n_atoms, a, qq, v);
       if constexpr (MODE == kModeP) {
+        float v[8];
+        load_coords8<FUSED>(src, sigma, atoms_per_row, n_atoms, a, qq, v);
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          xd[8 * qq + e] = static_cast<double>(v[e]);
-          nrm2 = fma(xd[8 * qq + e], xd[8 * qq + e], nrm2);
+          xs[tid * XW + 8 * qq + e] = __float_as_uint(v[e]);
+          nrm2 = fma(static_cast<double>(v[e]), static_cast<double>(v[e]), nrm2);
         }
       } else {
-#pragma unroll
-        for (int d = 0; d < 4; ++d) xw[4 * qq + d] = bf16_rne_bits(v[2 * d]) | (bf16_rne_bits(v[2 * d + 1]) << 16);
+        *reinterpret_cast<uint4 *>(xs + tid * XW + 4 * qq) = xb[a * 3 + qq];  // bf16 pairs from prep_kernel
       }
     }
     // NN-P's origin rule (pack.py:174): |x|_2 < fp32(1e-8); no scan needed
     const bool p_snap = MODE == kModeP && sqrt(nrm2) < static_cast<double>(__uint_as_float(kEpsBits));
-    if (M != 0 && !p_snap) {
-      uint32_t found = 0xFFFFFFFFu;  // lowest code whose bucket equals M (NN-B)
-      float best_v = -__builtin_inff();
-      double best_d = -__builtin_inf();
-      uint32_t best_code = 0xFFFFFFFFu;
-      // Each thread walks its own candidate slots (slice, lane) in rounds, so
-      // the wave runs the rescan body once per round (~1-3 rounds) instead of
-      // once per slot that any of its threads needs.
-      const int n_slots = 4 * n_slices;
-      int slot = 0;
-      uint4 rec = records[a];
-      for (;;) {
-        uint32_t g = 0xFFFFu;
-        for (; slot < n_slots; ++slot) {
-          if ((slot & 3) == 0) rec = records[static_cast<int64_t>(slot >> 2) * n_atoms + a];
-          if (rec.x != M) {
-            slot |= 3;  // skip the rest of this slice
-            continue;
-          }
-          g = (((slot & 2) ? rec.z : rec.y) >> (16 * (slot & 1))) & 0xFFFFu;
-          if (g != 0xFFFFu) break;
+    active = M != 0 && !p_snap;
+  }
+  Ms[tid] = M;
+
+  uint32_t found = 0xFFFFFFFFu;  // NN-B: lowest code whose bucket equals M
+  score_t best_v = -__builtin_inf();
+  uint32_t best_code = 0xFFFFFFFFu;
+  int qpos = 0;  // next lane of the lowest slice left in mask
+  for (;;) {
+    // ---- this thread's next candidates: lanes (in order) of the slices in mask ----
+    int nm = 0;
+    if (active) {
+      int loaded = -1;
+      uint4 rec = make_uint4(0u, 0u, 0u, 0u);
+      while (mask != 0 && nm < kRsPerRound) {
+        const int s = __builtin_ctzll(mask);
+        if (s != loaded) {
+          rec = records[static_cast<int64_t>(s) * n_atoms + a];
+          loaded = s;
         }
-        if (slot >= n_slots) break;
-        const int qq = slot & 3;
-        ++slot;
-        if (slot < n_slots && (slot & 3) == 0) rec = records[static_cast<int64_t>(slot >> 2) * n_atoms + a];
-        // NN-B/T: the lane's 32 codes of group g are 1.5 KB contiguous in the
-        // lane-major table; NN-P: rows of the raw int8 codebook (4 consecutive
-        // codes = 96 B per tile)
-        const uint4 *cg = reinterpret_cast<const uint4 *>(rescan) +
-                          ((static_cast<size_t>(qq) * kPaddedTiles + static_cast<size_t>(g) * kG) * 4) * 3;
-        for (int t = 0; t < kG; ++t) {
-          const int tile = static_cast<int>(g) * kG + t;
-          if (tile >= kRealTiles) break;
+        const int qq = qpos;
+        const uint32_t g = (((qq & 2) ? rec.z : rec.y) >> (16 * (qq & 1))) & 0xFFFFu;
+        if (++qpos == 4) {
+          qpos = 0;
+          mask &= mask - 1;
+        }
+        if (g != 0xFFFFu) tmp[nm++ * 256 + tid] = static_cast<uint32_t>(tid) | static_cast<uint32_t>(qq) << 8 | g << 10;
+      }
+    }
+    const bool more = nm == kRsPerRound && mask != 0;
+
+    // ---- compact: exclusive prefix sum of nm over the block ----
+    int incl = nm;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int t = __shfl_up(incl, d, 64);
+      if (lane >= d) incl += t;
+    }
+    if (lane == 63) wave_sum[wave] = incl;
+    __syncthreads();
+    int off = incl - nm, total = 0;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const int ws = wave_sum[w];
+      if (w < wave) off += ws;
+      total += ws;
+    }
+    for (int i = 0; i < nm; ++i) cand[off + i] = tmp[i * 256 + tid];
+    __syncthreads();
+
+    // ---- rescan: 8 lanes per candidate ----
+    for (int task = tid; task < total * 8; task += 256) {
+      const int c = task >> 3, t = task & 7;
+      const uint32_t cd = cand[c];
+      const int al = static_cast<int>(cd & 0xFFu), qq = static_cast<int>((cd >> 8) & 3u);
+      const int tile = static_cast<int>(cd >> 10) * kG + t;
+      uint32_t f = 0xFFFFFFFFu, bc = 0xFFFFFFFFu;
+      score_t bv = -__builtin_inf();
+      if (tile < kRealTiles) {
+        if constexpr (MODE == kModeP) {
+          double xd[kDim];
+#pragma unroll
+          for (int k = 0; k < kDim; ++k) xd[k] = static_cast<double>(__uint_as_float(xs[al * XW + k]));
+          const uint32_t code0 = static_cast<uint32_t>(tile * kTileCodes + 4 * qq);
+          const uint2 *cr = reinterpret_cast<const uint2 *>(rescan + (static_cast<size_t>(code0) + 1) * kDim);
+          uint2 rw[12];
+#pragma unroll
+          for (int k = 0; k < 12; ++k) rw[k] = cr[k];
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            const int row = 4 * qq + e;
-            const uint32_t code = static_cast<uint32_t>(tile * kTileCodes + row);
-            if constexpr (MODE == kModeP) {
-              const uint2 *cr = reinterpret_cast<const uint2 *>(rescan + (static_cast<size_t>(code) + 1) * kDim);
-              const uint2 r0 = cr[0], r1 = cr[1], r2 = cr[2];
-              const uint32_t rw[6] = {r0.x, r0.y, r1.x, r1.y, r2.x, r2.y};
-              double sc = 0.0;
+            const uint32_t w6[6] = {rw[3 * e].x, rw[3 * e].y, rw[3 * e + 1].x, rw[3 * e + 1].y, rw[3 * e + 2].x,
+                                    rw[3 * e + 2].y};
+            double sc = 0.0;
 #pragma unroll
-              for (int c = 0; c < kDim; ++c) {
-                const int k = static_cast<int32_t>(rw[c / 4] << (24 - 8 * (c % 4))) >> 24;
-                sc = fma(xd[c], static_cast<double>(raw_value_f32(k)), sc);
-              }
-              if (sc > best_d || (sc == best_d && code < best_code)) {
-                best_d = sc;
-                best_code = code;
-              }
-              continue;
+            for (int k = 0; k < kDim; ++k) {
+              const int r = static_cast<int32_t>(w6[k / 4] << (24 - 8 * (k % 4))) >> 24;
+              sc = fma(xd[k], static_cast<double>(raw_value_f32(r)), sc);
             }
-            const uint4 *cp = cg + (t * 4 + e) * 3;
-            const uint4 c0 = cp[0], c1 = cp[1], c2 = cp[2];
-            const uint32_t cw[12] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w, c2.x, c2.y, c2.z, c2.w};
+            if (sc > bv) {  // codes ascend with e: the first maximum is kept
+              bv = sc;
+              bc = code0 + e;
+            }
+          }
+        } else {
+          const uint4 *xq = reinterpret_cast<const uint4 *>(xs + al * XW);
+          const uint4 x0 = xq[0], x1 = xq[1], x2 = xq[2];
+          const uint32_t xw[12] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w, x2.x, x2.y, x2.z, x2.w};
+          const uint4 *cp = reinterpret_cast<const uint4 *>(rescan) +
+                            ((static_cast<size_t>(qq) * kPaddedTiles + static_cast<size_t>(tile)) * 4) * 3;
+          uint4 cw4[12];
+#pragma unroll
+          for (int k = 0; k < 12; ++k) cw4[k] = cp[k];
+          const uint32_t Mk = Ms[al];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const uint32_t cw[12] = {cw4[3 * e].x, cw4[3 * e].y, cw4[3 * e].z, cw4[3 * e].w,
+                                     cw4[3 * e + 1].x, cw4[3 * e + 1].y, cw4[3 * e + 1].z, cw4[3 * e + 1].w,
+                                     cw4[3 * e + 2].x, cw4[3 * e + 2].y, cw4[3 * e + 2].z, cw4[3 * e + 2].w};
             float sc = 0.f;
 #pragma unroll
             for (int d = 0; d < 12; ++d)
-              sc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, xw[d]), __builtin_bit_cast(bf16x2, cw[d]), sc,
-                                                   false);
+              sc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, xw[d]), __builtin_bit_cast(bf16x2, cw[d]),
+                                                   sc, false);
+            const uint32_t code = static_cast<uint32_t>(tile * kTileCodes + 4 * qq + e);
             float v = sc;
             if (MODE == kModeB) {
               const uint32_t bk = bf16_rne_bits(sc);
               v = bf16_bits_to_float(bk);
-              if (bk == M && code < found) found = code;
+              if (bk == Mk && code < f) f = code;
             }
-            if (v > best_v || (v == best_v && code < best_code)) {
-              best_v = v;
-              best_code = code;
+            if (v > bv) {
+              bv = v;
+              bc = code;
             }
           }
         }
       }
-      bool snap;
-      uint32_t code;
-      if (MODE == kModeP) {
-        code = best_code;
-        snap = best_code == 0xFFFFFFFFu;  // non-finite atom: no score compared
-      } else if (MODE == kModeB) {
-        const uint32_t bucket = found != 0xFFFFFFFFu ? M : (__float_as_uint(best_v) >> 16);
-        code = found != 0xFFFFFFFFu ? found : best_code;
-        snap = !(best_v > 0.f) || bucket < 0x4000u;  // bf16 max below 2.0
-      } else {
-        code = best_code;
-        snap = !(2.0f * best_v >= __uint_as_float(kCSqNormBits));
+      // reduce over the candidate's 8 lanes: lowest found code; best score, lowest code on ties
+#pragma unroll
+      for (int d = 1; d < 8; d <<= 1) {
+        const uint32_t of = static_cast<uint32_t>(__shfl_xor(static_cast<int>(f), d, 64));
+        const uint32_t oc = static_cast<uint32_t>(__shfl_xor(static_cast<int>(bc), d, 64));
+        score_t ov;
+        if constexpr (MODE == kModeP)
+          ov = __longlong_as_double(__shfl_xor(__double_as_longlong(bv), d, 64));
+        else
+          ov = __shfl_xor(bv, d, 64);
+        f = min(f, of);
+        if (ov > bv || (ov == bv && oc < bc)) {
+          bv = ov;
+          bc = oc;
+        }
       }
-      id = snap ? 0 : static_cast<int32_t>(code) + 1;
+      if (t == 0) {
+        res_v[c] = bv;
+        res_code[c] = bc;
+        if constexpr (MODE == kModeB) res_found[c] = f;
+      }
     }
-    if (idx_out) idx_out[a] = id;
+    __syncthreads();
+
+    // ---- merge this thread's candidates ----
+    for (int i = 0; i < nm; ++i) {
+      const score_t v = res_v[off + i];
+      const uint32_t code = res_code[off + i];
+      if (v > best_v || (v == best_v && code < best_code)) {
+        best_v = v;
+        best_code = code;
+      }
+      if constexpr (MODE == kModeB) found = min(found, res_found[off + i]);
+    }
+    if (!__syncthreads_or(more)) break;
   }
+
+  int32_t id = 0;
+  if (active) {
+    bool snap;
+    uint32_t code;
+    if (MODE == kModeP) {
+      code = best_code;
+      snap = best_code == 0xFFFFFFFFu;  // non-finite atom: no score compared
+    } else if (MODE == kModeB) {
+      const uint32_t bucket = found != 0xFFFFFFFFu ? M : (__float_as_uint(static_cast<float>(best_v)) >> 16);
+      code = found != 0xFFFFFFFFu ? found : best_code;
+      snap = !(best_v > 0.f) || bucket < 0x4000u;  // bf16 max below 2.0
+    } else {
+      code = best_code;
+      snap = !(2.0f * static_cast<float>(best_v) >= __uint_as_float(kCSqNormBits));
+    }
+    id = snap ? 0 : static_cast<int32_t>(code) + 1;
+  }
+  if (idx_out && a < n_atoms) idx_out[a] = id;
   if (!packed_out) return;
-  ids[threadIdx.x] = id;
+  ids[tid] = id;
   __syncthreads();
   const int64_t n_groups = (n_atoms + 3) / 4;
   const int64_t g0 = a0 / 4;
   const int64_t groups_here = min(static_cast<int64_t>(64), n_groups - g0);
-  if (threadIdx.x < groups_here) {
-    const int i = threadIdx.x * 4;
-    group_to_bytes(ids[i], ids[i + 1], ids[i + 2], ids[i + 3], bytes + threadIdx.x * 9);
+  if (tid < groups_here) {
+    const int i = tid * 4;
+    group_to_bytes(ids[i], ids[i + 1], ids[i + 2], ids[i + 3], bytes + tid * 9);
   }
   __syncthreads();
   uint8_t *dst = packed_out + g0 * 9;
   if (groups_here == 64 && aligned16(packed_out)) {
-    if (threadIdx.x < 36) reinterpret_cast<uint4 *>(dst)[threadIdx.x] = reinterpret_cast<const uint4 *>(bytes)[threadIdx.x];
+    if (tid < 36) reinterpret_cast<uint4 *>(dst)[tid] = reinterpret_cast<const uint4 *>(bytes)[tid];
   } else {
     const int nb = static_cast<int>(groups_here * 9);
-    for (int i = threadIdx.x; i < nb; i += 256) dst[i] = bytes[i];
+    for (int i = tid; i < nb; i += 256) dst[i] = bytes[i];
   }
 }
 
@@ -502,24 +678,38 @@ int choose_slices(int64_t ablocks) {
   return s;
 }
 
+size_t records_bytes(int64_t n_atoms) {
+  const int64_t ablocks = (n_atoms + kAtomsPerBlock - 1) / kAtomsPerBlock;
+  return static_cast<size_t>(n_atoms) * static_cast<size_t>(choose_slices(ablocks)) * sizeof(uint4);
+}
+
+// workspace = per-(atom, slice) records, then (NN-B / NN-T) the bf16 planes
 template <int MODE, bool FUSED>
 int launch_mode(const float *x, const float *sigma, int64_t apr, int64_t n_atoms, const DeviceTables *tab,
-                int32_t *idx_out, uint8_t *packed_out, uint4 *records, hipStream_t s) {
+                int32_t *idx_out, uint8_t *packed_out, uint8_t *workspace, hipStream_t s) {
   const int64_t ablocks = (n_atoms + kAtomsPerBlock - 1) / kAtomsPerBlock;
   const int n_slices = choose_slices(ablocks);
   const int tiles_per_slice = kPaddedTiles / n_slices;
   const int64_t grid = ablocks * n_slices;
   if (grid > 0x7FFFFFFFll) return fail(PLX_EINVAL, "quantize: %lld atoms exceed one launch", static_cast<long long>(n_atoms));
+  uint4 *records = reinterpret_cast<uint4 *>(workspace);
+  uint4 *xb = reinterpret_cast<uint4 *>(workspace + ((records_bytes(n_atoms) + 255) & ~static_cast<size_t>(255)));
+  int st;
+  if (MODE != kModeP) {
+    hipLaunchKernelGGL((prep_kernel<FUSED>), dim3(static_cast<unsigned>((n_atoms * 3 + 255) / 256)), dim3(256), 0, s, x,
+                       sigma, apr, n_atoms, xb);
+    if ((st = check_launch("prep_kernel")) != PLX_OK) return st;
+  }
   profile_before(s);
   const uint8_t *tiles = MODE == kModeP ? tab->kp_raw_tiles : tab->kp_bf16_tiles;
   const uint8_t *rescan = MODE == kModeP ? reinterpret_cast<const uint8_t *>(tab->cb_raw) : tab->kp_bf16_lanes;
-  hipLaunchKernelGGL((nn_kernel<MODE, FUSED>), dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0, s, x, sigma, apr,
-                     n_atoms, tiles, n_slices, tiles_per_slice, records);
-  int st = check_launch("nn_kernel");
-  if (st != PLX_OK) return st;
+  const void *operand = MODE == kModeP ? static_cast<const void *>(x) : static_cast<const void *>(xb);
+  hipLaunchKernelGGL((nn_kernel<MODE>), dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0, s, operand, n_atoms, tiles,
+                     n_slices, tiles_per_slice, records);
+  if ((st = check_launch("nn_kernel")) != PLX_OK) return st;
   profile_after(s);
   hipLaunchKernelGGL((resolve_kernel<MODE, FUSED>), dim3(static_cast<unsigned>((n_atoms + 255) / 256)), dim3(256), 0, s,
-                     records, n_slices, n_atoms, x, sigma, apr, rescan, idx_out, packed_out);
+                     records, n_slices, n_atoms, x, sigma, apr, xb, rescan, idx_out, packed_out);
   return check_launch("resolve_kernel");
 }
 
@@ -527,8 +717,7 @@ int launch_mode(const float *x, const float *sigma, int64_t apr, int64_t n_atoms
 
 size_t quantize_workspace_bytes(int64_t n_atoms) {
   if (n_atoms <= 0) return 0;
-  const int64_t ablocks = (n_atoms + kAtomsPerBlock - 1) / kAtomsPerBlock;
-  return static_cast<size_t>(n_atoms) * static_cast<size_t>(choose_slices(ablocks)) * sizeof(uint4);
+  return ((records_bytes(n_atoms) + 255) & ~static_cast<size_t>(255)) + static_cast<size_t>(n_atoms) * 48;
 }
 
 int launch_quantize(const float *x, const float *sigma, int64_t rows, int64_t cols, int64_t n_atoms, int mode,
@@ -544,17 +733,17 @@ int launch_quantize(const float *x, const float *sigma, int64_t rows, int64_t co
   const DeviceTables *tab = nullptr;
   int st = get_tables(&tab);
   if (st != PLX_OK) return st;
-  uint4 *records = static_cast<uint4 *>(workspace);
+  uint8_t *ws = static_cast<uint8_t *>(workspace);
   const bool fused = sigma != nullptr;
   const int64_t apr = cols / kDim;
   if (mode == PLX_NN_PACK_FP32)
-    st = launch_mode<PLX_NN_PACK_FP32, false>(x, nullptr, apr, n_atoms, tab, idx_out, packed_out, records, s);
+    st = launch_mode<PLX_NN_PACK_FP32, false>(x, nullptr, apr, n_atoms, tab, idx_out, packed_out, ws, s);
   else if (mode == PLX_NN_BF16_SCORES)
-    st = fused ? launch_mode<PLX_NN_BF16_SCORES, true>(x, sigma, apr, n_atoms, tab, idx_out, packed_out, records, s)
-               : launch_mode<PLX_NN_BF16_SCORES, false>(x, sigma, apr, n_atoms, tab, idx_out, packed_out, records, s);
+    st = fused ? launch_mode<PLX_NN_BF16_SCORES, true>(x, sigma, apr, n_atoms, tab, idx_out, packed_out, ws, s)
+               : launch_mode<PLX_NN_BF16_SCORES, false>(x, sigma, apr, n_atoms, tab, idx_out, packed_out, ws, s);
   else
-    st = fused ? launch_mode<PLX_NN_FP32_SCORES, true>(x, sigma, apr, n_atoms, tab, idx_out, packed_out, records, s)
-               : launch_mode<PLX_NN_FP32_SCORES, false>(x, sigma, apr, n_atoms, tab, idx_out, packed_out, records, s);
+    st = fused ? launch_mode<PLX_NN_FP32_SCORES, true>(x, sigma, apr, n_atoms, tab, idx_out, packed_out, ws, s)
+               : launch_mode<PLX_NN_FP32_SCORES, false>(x, sigma, apr, n_atoms, tab, idx_out, packed_out, ws, s);
   if (st != PLX_OK) return st;
   if (weight_out) {
     const dim3 gg(static_cast<unsigned>((n_atoms * 6 + 255) / 256));
