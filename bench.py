@@ -55,17 +55,30 @@ def make_c2(device, seed=2024):
     return mats
 
 
-def time_gpu(fn, iters, warmup):
+def time_gpu(fn, iters, warmup, rounds=1, warm_s=0.0):
+    """Seconds per call: median over `rounds` of the mean over `iters` back-to-back calls.
+
+    Warmup: `warmup` calls, continued until `warm_s` seconds have passed (an
+    HBM-bound kernel reaches its steady memory clock only after a sustained load).
+    """
     import torch
 
-    for _ in range(warmup):
+    t_end = time.perf_counter() + warm_s
+    k = 0
+    while k < warmup or time.perf_counter() < t_end:
         fn()
+        k += 1
+        if k % 8 == 0:
+            torch.cuda.synchronize()
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(iters):
-        fn()
-    torch.cuda.synchronize()
-    return (time.perf_counter() - t0) / iters
+    per = []
+    for _ in range(rounds):
+        t0 = time.perf_counter()
+        for _ in range(iters):
+            fn()
+        torch.cuda.synchronize()
+        per.append((time.perf_counter() - t0) / iters)
+    return sorted(per)[len(per) // 2]
 
 
 def cpu_baseline(mats, target_atoms):
@@ -107,27 +120,31 @@ def extras(device, iters=20):
     g = torch.Generator(device=device).manual_seed(7)
     idx = torch.randint(0, 196561, (n,), generator=g, device=device, dtype=torch.int64)
     packed = castor.pack_indices(idx)
-    t = time_gpu(lambda: castor.pack_indices(idx), iters, 3)
+    t = time_gpu(lambda: castor.pack_indices(idx), iters, 10, 5, 0.3)
     out["pack_GBps"] = (8 + 2.25) * n / t / 1e9
-    t = time_gpu(lambda: castor.unpack_indices(packed, n), iters, 3)
+    t = time_gpu(lambda: castor.unpack_indices(packed, n), iters, 10, 5, 0.3)
     out["unpack_GBps"] = (2.25 + 8) * n / t / 1e9
     rows, cols = 209_715, 1920
     sig = (torch.rand(rows, generator=g, device=device) * 0.045 + 0.005).half()
-    t = time_gpu(lambda: dequantize_h24(packed, sig, rows, cols), iters, 3)
+    t = time_gpu(lambda: dequantize_h24(packed, sig, rows, cols), iters, 10, 5, 0.3)
     out["dequant_GBps"] = (2.25 * n + 48 * n + 2 * rows) / t / 1e9
     out["hbm_peak_GBps"] = PEAK_HBM_BPS / 1e9
     for k in ("pack", "unpack", "dequant"):
         out[f"{k}_hbm_frac"] = out[f"{k}_GBps"] * 1e9 / PEAK_HBM_BPS
-    out["scale"] = "16,777,200 indices / atoms (BASELINE config 4 size), rows of 1920"
+    out["scale"] = ("16,777,200 indices / atoms (BASELINE config 4 size), rows of 1920; median of 5 rounds of "
+                    f"{iters} back-to-back calls after >= 0.3 s of warmup calls")
     return out
 
 
-def gemv_extras(device, copies=200, m_gemm=64):
+def gemv_extras(device, copies=200, m_gemm=64, replays=5):
     """Config 5: fused dequant-GEMV (M=1) and dequant-GEMM (M=64) on [7680,1920] and [1920,7680].
 
-    Each timing cycles through `copies` distinct packed weights (>= 256 MB in
-    total, above the 256 MB Infinity Cache) so the compressed stream is read
-    from HBM; HIP events on the launch stream bracket the whole loop.
+    `copies` calls, each on a distinct packed weight (>= 256 MB in total, above
+    the 256 MB Infinity Cache, so the compressed stream is read from HBM), are
+    captured in one HIP graph; the graph is replayed and HIP events on the
+    replay stream give the device time per call (kernel plus graph dispatch,
+    without the Python call overhead).  Replay outputs are checked against an
+    eager call.
     """
     import torch
 
@@ -142,23 +159,36 @@ def gemv_extras(device, copies=200, m_gemm=64):
         sg = (torch.rand(copies, of, generator=g, device=device) * 0.045 + 0.005).half()
         for m in (1, m_gemm):
             x = torch.randn(m, inf, generator=g, device=device).to(torch.bfloat16)
-            for i in range(3):
-                dequant_linear(pk[i], sg[i], of, inf, x)
+            eager = [dequant_linear(pk[i], sg[i], of, inf, x) for i in (0, copies - 1)]
+            side = torch.cuda.Stream(device)
+            side.wait_stream(torch.cuda.current_stream(device))
+            with torch.cuda.stream(side):
+                for i in range(3):
+                    dequant_linear(pk[i], sg[i], of, inf, x)
+            torch.cuda.current_stream(device).wait_stream(side)
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                ys = [dequant_linear(pk[i], sg[i], of, inf, x) for i in range(copies)]
+            graph.replay()
+            torch.cuda.synchronize()
+            if not (torch.equal(ys[0], eager[0]) and torch.equal(ys[-1], eager[1])):
+                raise RuntimeError(f"dequant_linear graph replay differs from the eager call ({name}, M={m})")
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             e0.record()
-            for i in range(copies):
-                dequant_linear(pk[i], sg[i], of, inf, x)
+            for _ in range(replays):
+                graph.replay()
             e1.record()
             e1.synchronize()
-            t = e0.elapsed_time(e1) / 1e3 / copies
+            t = e0.elapsed_time(e1) / 1e3 / (replays * copies)
+            del graph, ys
             comp = nbytes + 2 * of + 2 * m * inf + 4 * m * of
             key = f"{name}_M{m}"
             out[f"{key}_us"] = t * 1e6
             out[f"{key}_compressed_GBps"] = comp / t / 1e9
             out[f"{key}_dense_equiv_GBps"] = (2 * of * inf) / t / 1e9
             out[f"{key}_TFLOPs"] = 2 * m * of * inf / t / 1e12
-    out["note"] = (f"{copies} rotating packed copies per matrix ({copies} x 1.38 MB); compressed bytes = packed + "
-                   "sigma16 + x bf16 + y fp32; dense-equivalent = fp16 weight bytes")
+    out["note"] = (f"HIP graph of {copies} calls on distinct packed copies ({copies} x 1.38 MB), replayed {replays}x; "
+                   "compressed bytes = packed + sigma16 + x bf16 + y fp32; dense-equivalent = fp16 weight bytes")
     return out
 
 
@@ -177,7 +207,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--cpu-atoms", type=int, default=24_576, help="CPU baseline sample size (atoms)")
+    ap.add_argument("--cpu-atoms", type=int, default=165_888, help="CPU baseline sample size (atoms)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true")
     ap.add_argument("--mode", default="bf16", choices=["bf16", "fp32"])

@@ -11,15 +11,17 @@
 // fp16 values; every step of the formula is an odd function of the code
 // value, so the negative entries are the positive ones with the sign flipped.
 //
-// Layout of the work: a block covers 1,024 atoms = 3,072 output chunks of 16 B
-// (8 coordinates); thread t of the block writes chunks t, t+256, ... so each
-// store instruction writes 1 KiB contiguous.  Per block the packed bytes are
-// staged in LDS and decoded once per atom, and each row met by the block gets
-// its 8-entry value table (low bytes, high bytes: 4 words) in LDS; a chunk is
-// then one 4-byte kp_dq load (3-bit value ids, L2-resident) and 6 v_perm_b32
-// byte lookups.  The output is written with non-temporal stores: as
-// ordinary stores its 48 B/atom stream evicts kp_dq from L2 and the gathers
-// then miss (measured: 41% of HBM peak instead of 70%).
+// Layout of the work: a block covers 256 atoms = 768 output chunks of 16 B
+// (8 coordinates); thread t of the block writes chunks t, t+256, t+512, so each
+// store instruction writes 4 KiB contiguous.  Few stores per thread matter on
+// MI355X: with 3 chunks per thread the kernel sustains ~82% of HBM peak, with
+// 12 (1,024-atom blocks) ~72%.  Per block the packed bytes are staged in LDS
+// and decoded once per atom, and each row met by the block gets its 8-entry
+// value table (low bytes, high bytes: 4 words) in LDS; a chunk is then one
+// 4-byte kp_dq load (3-bit value ids, L2-resident) and 6 v_perm_b32 byte
+// lookups.  The output is written with non-temporal stores: as ordinary
+// stores its 48 B/atom stream evicts kp_dq from L2 and the gathers then miss
+// (measured: 30-40% of HBM peak).
 //
 // Indices above 196,560 (not produced by the reference packer) decode as the
 // origin, so corrupt input can never read outside the table.
@@ -32,9 +34,9 @@ namespace plx {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kDqAtoms = 1024;                     // atoms per block
+constexpr int kDqAtoms = 256;                      // atoms per block
 constexpr int kDqChunks = kDqAtoms * 3;            // 16-byte output chunks per block
-constexpr int kDqPackedBytes = kDqAtoms / 4 * 9;   // 2,304
+constexpr int kDqPackedBytes = kDqAtoms / 4 * 9;   // 576
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
 __global__ __launch_bounds__(kThreads) void dequant_kernel(const uint8_t *__restrict__ packed, int64_t packed_bytes,
@@ -85,7 +87,7 @@ __global__ __launch_bounds__(kThreads) void dequant_kernel(const uint8_t *__rest
 
   u32x4_t *dst = reinterpret_cast<u32x4_t *>(w16 + a0 * kDim);
   const int n_chunks = atoms_here * 3;
-#pragma unroll 2
+#pragma unroll
   for (int c = tid; c < n_chunks; c += kThreads) {
     const int atom = c / 3, plane = c - 3 * atom;
     const uint32_t en = ent[atom];
