@@ -10,8 +10,8 @@
 //   and codebook slice b % n_slices.  Work-groups are dispatched round-robin
 //   over the 8 XCDs, so with 8 slices each XCD only ever streams its own
 //   1.18 MB of the 9.4 MB bf16 codebook and serves it from its 4 MB L2.
-//   A block is 4 waves; a wave holds 8 atom tiles of 16 atoms as MFMA B
-//   operands in registers (512 atoms per block) and sweeps its slice, staged
+//   A block is 4 waves; a wave holds 12 atom tiles of 16 atoms as MFMA B
+//   operands in registers (768 atoms per block) and sweeps its slice, staged
 //   through LDS 32 code tiles (24 KB) at a time, double buffered, with the
 //   next stage streamed by global_load_lds while the current one is scored.
 //   MFMA A operand = 16 codes x 32 K from LDS (lanes 48-63 re-read plane 0:
@@ -31,7 +31,7 @@
 //     fp32(1/sqrt 8) (3s rounded), so these scores order the codes like the
 //     fp32 ones up to 2^-21 * sum|x_i c_i|, inside the near-tie envelope.
 //   Both are tracked with one integer threshold R per (atom, lane): a group of
-//   8 tiles (32 codes per lane) improves when its max score, as an int bit
+//   kG tiles (4 kG codes per lane) improves when its max score, as an int bit
 //   pattern, exceeds R (positive floats order like ints; negative scores can
 //   only lose to the origin threshold R starts at).  NN-B raises R to the
 //   largest fp32 that still rounds to the new bucket, so later codes in the
@@ -42,7 +42,7 @@
 // resolve_kernel -- per atom the maximum key over the slices, then an
 //   exact-product rescan (v_dot2_f32_bf16; NN-P: fp64 dot products of the
 //   fp32 atom and the fp32 codebook rows, exact up to 2^-48) of the few
-//   groups that hold it to find the lowest code, 8 lanes per group with
+//   groups that hold it to find the lowest code, kG lanes per group with
 //   coalesced table reads, then the index and the packed 9-byte groups.  Both
 //   fp32 sums (MFMA, dot2) lie within 2^-20 * sum|x_i c_i| of the exact score
 //   (MFMA measured at < 2^-22), so the result equals the exact-score answer
@@ -62,15 +62,15 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kWaves = 4;
 constexpr int kThreads = kWaves * 64;
-constexpr int kAT = 8;                                  // atom tiles per wave
-constexpr int kG = 8;                                   // code tiles per tracking group
+constexpr int kAT = 12;                                 // atom tiles per wave
+constexpr int kG = 16;                                  // code tiles per tracking group
 constexpr int kST = 32;                                 // code tiles per LDS stage
-constexpr int kAtomsPerBlock = kWaves * kAT * 16;       // 512
+constexpr int kAtomsPerBlock = kWaves * kAT * 16;       // 768
 constexpr int kStageBytes = kST * kTileBytes;           // 24,576
 constexpr int kStageVecs = kStageBytes / 16;            // 1,536 uint4
 constexpr int kLoadsPerThread = kStageVecs / kThreads;  // 6
 static_assert(kStageVecs % kThreads == 0, "stage must split evenly over the block");
-static_assert(kST % kG == 0 && kG == 8, "whole 8-tile groups per LDS stage");
+static_assert(kST % kG == 0 && kG >= 8 && kG <= 64 && (kG & (kG - 1)) == 0, "whole groups per LDS stage");
 
 constexpr int kModeB = PLX_NN_BF16_SCORES;
 constexpr int kModeP = PLX_NN_PACK_FP32;
@@ -149,9 +149,11 @@ __global__ __launch_bounds__(256) void prep_kernel(const float *__restrict__ src
 // NN-B tracking key of a group: bucket (round-half-up, see raised_threshold)
 // in the high half, 0xFFFF - group in the low half, so one signed max keeps
 // the highest bucket and, within it, the earliest group.
+// v_perm_b32 takes bytes 2-3 of the rounded score and bytes 0-1 of the
+// (uniform) group field in one instruction.
 __device__ __forceinline__ int group_key(int gm, int group) {
-  return static_cast<int>(((static_cast<uint32_t>(gm) + 0x8000u) & 0xFFFF0000u) |
-                          (static_cast<uint32_t>(0xFFFF - group) & 0xFFFFu));
+  return static_cast<int>(__builtin_amdgcn_perm(static_cast<uint32_t>(gm) + 0x8000u,
+                                                static_cast<uint32_t>(0xFFFF - group) & 0xFFFFu, 0x07060100u));
 }
 
 // src: NN-P: the fp32 atoms; NN-B / NN-T: xb, the bf16 planes of prep_kernel.
@@ -167,7 +169,7 @@ __global__ __launch_bounds__(kThreads, 2) void nn_kernel(const void *__restrict_
   const int wave = tid >> 6, lane = tid & 63, q = lane >> 4, j = lane & 15;
   const int64_t wave_atom0 = ablock * kAtomsPerBlock + static_cast<int64_t>(wave) * (kAT * 16);
 
-  // B operands: 8 atom tiles, lane holds coordinates 8q..8q+7 of atom j
+  // B operands: kAT atom tiles, lane holds coordinates 8q..8q+7 of atom j
   // (NN-P: as three bf16 parts, b[0] + b[1] + b[2]).
   constexpr int NS = n_splits<MODE>();
   bf16x8 b[NS][kAT];
@@ -224,7 +226,7 @@ __global__ __launch_bounds__(kThreads, 2) void nn_kernel(const void *__restrict_
   const int a_off = (q < 3 ? q : 0) * 256 + j * 16;
   // Software pipeline: the MFMA result of tile k for atom tile `at` is folded
   // into the group maximum while tile k+1's MFMAs issue, and tile k+1's A
-  // operand is read from LDS right after tile k's first MFMA.  A group of 8
+  // operand is read from LDS right after tile k's first MFMA.  A group of kG
   // tiles is compared against the threshold once its last tile has been
   // folded, i.e. during the next group's first tile (NN-B: the next group's
   // tile at % 8); the slice's last tile is folded after the loop.
@@ -243,12 +245,12 @@ __global__ __launch_bounds__(kThreads, 2) void nn_kernel(const void *__restrict_
     bf16x8 a = *reinterpret_cast<const bf16x8 *>(L);
     bool up[kAT];
     int gdone[kAT];
-    // One group of 8 tiles: tile 0 closes the previous group, tile 1 starts
+    // One group of kG tiles: tile 0 closes the previous group, tile 1 starts
     // this group's maximum.
-    auto eight_tiles = [&](int k0) {
+    auto group_tiles = [&](int k0) {
       constexpr bool FIRST = true;
 #pragma unroll
-      for (int t = 0; t < 8; ++t) {
+      for (int t = 0; t < kG; ++t) {
         const int k = k0 + t;
         bf16x8 an;
 #pragma unroll
@@ -300,7 +302,7 @@ __global__ __launch_bounds__(kThreads, 2) void nn_kernel(const void *__restrict_
     };
 #pragma unroll 1
     for (int k0 = 0; k0 < kST; k0 += kG) {
-      eight_tiles(k0);
+      group_tiles(k0);
       if constexpr (MODE != kModeB) {
 #pragma unroll
         for (int at = 0; at < kAT; ++at) {
@@ -361,9 +363,9 @@ __global__ __launch_bounds__(kThreads, 2) void nn_kernel(const void *__restrict_
 //   scan     thread per atom: the maximum key M over the slices, the atom's
 //            coordinates into LDS (bf16 pairs; NN-P: fp32), then up to
 //            kRsPerRound candidate slots (slice, lane) whose record holds M,
-//            each naming a group of 8 tiles x 4 codes of that lane;
+//            each naming a group of kG tiles x 4 codes of that lane;
 //   compact  a block-wide prefix sum packs the candidates into one list;
-//   rescan   8 lanes per candidate, lane t scoring the 4 codes of tile t of
+//   rescan   kG lanes per candidate, lane t scoring the 4 codes of tile t of
 //            the group (NN-B/T: 192 B contiguous in the lane-major bf16
 //            table, v_dot2_f32_bf16 = exact bf16 products, fp32 sums; NN-P:
 //            4 consecutive rows of the raw int8 codebook, fp64 dot products of
@@ -494,9 +496,9 @@ __global__ __launch_bounds__(256) void resolve_kernel(const uint4 *__restrict__ 
     for (int i = 0; i < nm; ++i) cand[off + i] = tmp[i * 256 + tid];
     __syncthreads();
 
-    // ---- rescan: 8 lanes per candidate ----
-    for (int task = tid; task < total * 8; task += 256) {
-      const int c = task >> 3, t = task & 7;
+    // ---- rescan: kG lanes per candidate ----
+    for (int task = tid; task < total * kG; task += 256) {
+      const int c = task / kG, t = task % kG;
       const uint32_t cd = cand[c];
       const int al = static_cast<int>(cd & 0xFFu), qq = static_cast<int>((cd >> 8) & 3u);
       const int tile = static_cast<int>(cd >> 10) * kG + t;
@@ -561,9 +563,9 @@ __global__ __launch_bounds__(256) void resolve_kernel(const uint4 *__restrict__ 
           }
         }
       }
-      // reduce over the candidate's 8 lanes: lowest found code; best score, lowest code on ties
+      // reduce over the candidate's kG lanes: lowest found code; best score, lowest code on ties
 #pragma unroll
-      for (int d = 1; d < 8; d <<= 1) {
+      for (int d = 1; d < kG; d <<= 1) {
         const uint32_t of = static_cast<uint32_t>(__shfl_xor(static_cast<int>(f), d, 64));
         const uint32_t oc = static_cast<uint32_t>(__shfl_xor(static_cast<int>(bc), d, 64));
         score_t ov;
