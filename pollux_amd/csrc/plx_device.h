@@ -60,6 +60,33 @@ __device__ __forceinline__ void bytes_to_group(const uint8_t *b, int32_t *v) {
   v[3] = ((c6 & 0x03) << 16) | (c7 << 8) | c8;
 }
 
+// Byte tables of the bf16 codebook values by 3-bit value id (ids 0..7 = raw
+// coordinates {0, 1, 2, 4, -4, -3, -2, -1}, the id order of the kp_dq table):
+// x = low bytes of ids 0-3, y = low bytes of ids 4-7, z / w = high bytes.
+__device__ __forceinline__ uint4 bf16_value_table() {
+  const int kv[8] = {0, 1, 2, 4, -4, -3, -2, -1};
+  uint32_t e[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) e[i] = bf16_rne_bits(raw_value_f32(kv[i]));
+  uint4 t;
+  t.x = (e[0] & 0xFFu) | (e[1] & 0xFFu) << 8 | (e[2] & 0xFFu) << 16 | (e[3] & 0xFFu) << 24;
+  t.y = (e[4] & 0xFFu) | (e[5] & 0xFFu) << 8 | (e[6] & 0xFFu) << 16 | (e[7] & 0xFFu) << 24;
+  t.z = (e[0] >> 8) | (e[1] >> 8) << 8 | (e[2] >> 8) << 16 | (e[3] >> 8) << 24;
+  t.w = (e[4] >> 8) | (e[5] >> 8) << 8 | (e[6] >> 8) << 16 | (e[7] >> 8) << 24;
+  return t;
+}
+
+// One kp_dq word (byte i = id of coordinate i | id of coordinate 4+i << 4)
+// -> the 8 16-bit values as pairs (coordinates 0,1 | 2,3 | 4,5 | 6,7), low
+// half first, through 6 v_perm_b32 byte lookups in a 4-word table t.
+__device__ __forceinline__ uint4 ids_to_pairs(uint32_t w, uint4 t) {
+  const uint32_t s_lo = w & 0x0F0F0F0Fu, s_hi = (w >> 4) & 0x0F0F0F0Fu;
+  const uint32_t l_lo = __builtin_amdgcn_perm(t.y, t.x, s_lo), h_lo = __builtin_amdgcn_perm(t.w, t.z, s_lo);
+  const uint32_t l_hi = __builtin_amdgcn_perm(t.y, t.x, s_hi), h_hi = __builtin_amdgcn_perm(t.w, t.z, s_hi);
+  return make_uint4(__builtin_amdgcn_perm(h_lo, l_lo, 0x05010400u), __builtin_amdgcn_perm(h_lo, l_lo, 0x07030602u),
+                    __builtin_amdgcn_perm(h_hi, l_hi, 0x05010400u), __builtin_amdgcn_perm(h_hi, l_hi, 0x07030602u));
+}
+
 __device__ __forceinline__ bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 }  // namespace plx

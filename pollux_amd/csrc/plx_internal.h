@@ -34,7 +34,6 @@ constexpr uint32_t kSqrt12Bits = 0x405DB3D7u;      // fp32(sqrt 12)
 struct DeviceTables {
   int device = -1;
   uint8_t *kp_bf16_tiles = nullptr;  // [kPaddedTiles][3][16][8] bf16 bits (MFMA A-operand layout)
-  uint8_t *kp_bf16_lanes = nullptr;  // [4][kPaddedTiles][4][24] bf16 bits (rows 4q..4q+3 of each tile, lane-major)
   int8_t *cb_raw = nullptr;          // [kCodebook][24] raw integer coordinates
   uint8_t *kp_gemv = nullptr;        // [kCodebook] x 16 B: 24 signed nibbles + (type | pos << 8)
   uint32_t *kp_dq = nullptr;         // [kCodebook][3] words: 3-bit value ids of 8 coordinates per word

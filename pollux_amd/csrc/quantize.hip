@@ -160,7 +160,8 @@ __device__ __forceinline__ int group_key(int gm, int group) {
 template <int MODE>
 __global__ __launch_bounds__(kThreads, 2) void nn_kernel(const void *__restrict__ src, int64_t n_atoms,
                                                           const uint8_t *__restrict__ tiles, int n_slices,
-                                                          int tiles_per_slice, uint4 *__restrict__ records) {
+                                                          int tiles_per_slice, uint32_t *__restrict__ keys,
+                                                          uint2 *__restrict__ groups) {
   __shared__ __align__(16) uint8_t lds[2][kStageBytes];
 
   const int slice = static_cast<int>(blockIdx.x % static_cast<unsigned>(n_slices));
@@ -354,7 +355,8 @@ __global__ __launch_bounds__(kThreads, 2) void nn_kernel(const void *__restrict_
     if (q == 0 && a < n_atoms) {
       const bool hit = Rm != initial_threshold<MODE>();
       const uint32_t key = hit ? (MODE == kModeB ? static_cast<uint32_t>(Rm) >> 16 : static_cast<uint32_t>(Rm)) : 0u;
-      records[static_cast<int64_t>(slice) * n_atoms + a] = make_uint4(key, g0 | (g1 << 16), g2 | (g3 << 16), 0u);
+      keys[static_cast<int64_t>(slice) * n_atoms + a] = key;
+      groups[static_cast<int64_t>(slice) * n_atoms + a] = make_uint2(g0 | (g1 << 16), g2 | (g3 << 16));
     }
   }
 }
@@ -387,7 +389,8 @@ struct RsScore {  // per-candidate / per-atom running result
 };
 
 template <int MODE, bool FUSED>
-__global__ __launch_bounds__(256) void resolve_kernel(const uint4 *__restrict__ records, int n_slices,
+__global__ __launch_bounds__(256) void resolve_kernel(const uint32_t *__restrict__ keys,
+                                                      const uint2 *__restrict__ groups, int n_slices,
                                                       int64_t n_atoms, const float *__restrict__ src,
                                                       const float *__restrict__ sigma, int64_t atoms_per_row,
                                                       const uint4 *__restrict__ xb, const uint8_t *__restrict__ rescan,
@@ -415,11 +418,10 @@ __global__ __launch_bounds__(256) void resolve_kernel(const uint4 *__restrict__ 
   uint64_t mask = 0;  // slices whose key equals M (n_slices <= 64)
   bool active = false;
   if (a < n_atoms) {
-    const uint32_t *keys = reinterpret_cast<const uint32_t *>(records);
     for (int s0 = 0; s0 < n_slices; s0 += 8) {
       uint32_t k[8];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) k[i] = s0 + i < n_slices ? keys[4 * (static_cast<int64_t>(s0 + i) * n_atoms + a)] : 0u;
+      for (int i = 0; i < 8; ++i) k[i] = s0 + i < n_slices ? keys[static_cast<int64_t>(s0 + i) * n_atoms + a] : 0u;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         if (k[i] > M) {
@@ -459,15 +461,15 @@ __global__ __launch_bounds__(256) void resolve_kernel(const uint4 *__restrict__ 
     int nm = 0;
     if (active) {
       int loaded = -1;
-      uint4 rec = make_uint4(0u, 0u, 0u, 0u);
+      uint2 rec = make_uint2(0u, 0u);
       while (mask != 0 && nm < kRsPerRound) {
         const int s = __builtin_ctzll(mask);
         if (s != loaded) {
-          rec = records[static_cast<int64_t>(s) * n_atoms + a];
+          rec = groups[static_cast<int64_t>(s) * n_atoms + a];
           loaded = s;
         }
         const int qq = qpos;
-        const uint32_t g = (((qq & 2) ? rec.z : rec.y) >> (16 * (qq & 1))) & 0xFFFFu;
+        const uint32_t g = (((qq & 2) ? rec.y : rec.x) >> (16 * (qq & 1))) & 0xFFFFu;
         if (++qpos == 4) {
           qpos = 0;
           mask &= mask - 1;
@@ -497,6 +499,7 @@ __global__ __launch_bounds__(256) void resolve_kernel(const uint4 *__restrict__ 
     __syncthreads();
 
     // ---- rescan: kG lanes per candidate ----
+    const uint4 bt = bf16_value_table();
     for (int task = tid; task < total * kG; task += 256) {
       const int c = task / kG, t = task % kG;
       const uint32_t cd = cand[c];
@@ -533,17 +536,25 @@ __global__ __launch_bounds__(256) void resolve_kernel(const uint4 *__restrict__ 
           const uint4 *xq = reinterpret_cast<const uint4 *>(xs + al * XW);
           const uint4 x0 = xq[0], x1 = xq[1], x2 = xq[2];
           const uint32_t xw[12] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w, x2.x, x2.y, x2.z, x2.w};
-          const uint4 *cp = reinterpret_cast<const uint4 *>(rescan) +
-                            ((static_cast<size_t>(qq) * kPaddedTiles + static_cast<size_t>(tile)) * 4) * 3;
-          uint4 cw4[12];
+          // 4 consecutive codebook rows (code + 1): 12 words of 3-bit value
+          // ids, expanded to bf16 pairs by byte lookups
+          const uint32_t code0 = static_cast<uint32_t>(tile * kTileCodes + 4 * qq);
+          const uint32_t *cp = reinterpret_cast<const uint32_t *>(rescan) + (static_cast<size_t>(code0) + 1) * 3;
+          uint32_t idw[12];
 #pragma unroll
-          for (int k = 0; k < 12; ++k) cw4[k] = cp[k];
+          for (int k = 0; k < 12; ++k) idw[k] = cp[k];
           const uint32_t Mk = Ms[al];
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            const uint32_t cw[12] = {cw4[3 * e].x, cw4[3 * e].y, cw4[3 * e].z, cw4[3 * e].w,
-                                     cw4[3 * e + 1].x, cw4[3 * e + 1].y, cw4[3 * e + 1].z, cw4[3 * e + 1].w,
-                                     cw4[3 * e + 2].x, cw4[3 * e + 2].y, cw4[3 * e + 2].z, cw4[3 * e + 2].w};
+            uint32_t cw[12];
+#pragma unroll
+            for (int p = 0; p < 3; ++p) {
+              const uint4 o = ids_to_pairs(idw[3 * e + p], bt);
+              cw[4 * p] = o.x;
+              cw[4 * p + 1] = o.y;
+              cw[4 * p + 2] = o.z;
+              cw[4 * p + 3] = o.w;
+            }
             float sc = 0.f;
 #pragma unroll
             for (int d = 0; d < 12; ++d)
@@ -680,9 +691,11 @@ int choose_slices(int64_t ablocks) {
   return s;
 }
 
+// per-(atom, slice) records as two arrays: 4-byte keys, then the 8-byte lane groups
 size_t records_bytes(int64_t n_atoms) {
   const int64_t ablocks = (n_atoms + kAtomsPerBlock - 1) / kAtomsPerBlock;
-  return static_cast<size_t>(n_atoms) * static_cast<size_t>(choose_slices(ablocks)) * sizeof(uint4);
+  const size_t n_rec = static_cast<size_t>(n_atoms) * static_cast<size_t>(choose_slices(ablocks));
+  return ((n_rec * 4 + 255) & ~static_cast<size_t>(255)) + n_rec * 8;
 }
 
 // workspace = per-(atom, slice) records, then (NN-B / NN-T) the bf16 planes
@@ -694,7 +707,9 @@ int launch_mode(const float *x, const float *sigma, int64_t apr, int64_t n_atoms
   const int tiles_per_slice = kPaddedTiles / n_slices;
   const int64_t grid = ablocks * n_slices;
   if (grid > 0x7FFFFFFFll) return fail(PLX_EINVAL, "quantize: %lld atoms exceed one launch", static_cast<long long>(n_atoms));
-  uint4 *records = reinterpret_cast<uint4 *>(workspace);
+  const size_t n_rec = static_cast<size_t>(n_atoms) * static_cast<size_t>(n_slices);
+  uint32_t *keys = reinterpret_cast<uint32_t *>(workspace);
+  uint2 *groups = reinterpret_cast<uint2 *>(workspace + ((n_rec * 4 + 255) & ~static_cast<size_t>(255)));
   uint4 *xb = reinterpret_cast<uint4 *>(workspace + ((records_bytes(n_atoms) + 255) & ~static_cast<size_t>(255)));
   int st;
   if (MODE != kModeP) {
@@ -704,14 +719,15 @@ int launch_mode(const float *x, const float *sigma, int64_t apr, int64_t n_atoms
   }
   profile_before(s);
   const uint8_t *tiles = MODE == kModeP ? tab->kp_raw_tiles : tab->kp_bf16_tiles;
-  const uint8_t *rescan = MODE == kModeP ? reinterpret_cast<const uint8_t *>(tab->cb_raw) : tab->kp_bf16_lanes;
+  const uint8_t *rescan =
+      MODE == kModeP ? reinterpret_cast<const uint8_t *>(tab->cb_raw) : reinterpret_cast<const uint8_t *>(tab->kp_dq);
   const void *operand = MODE == kModeP ? static_cast<const void *>(x) : static_cast<const void *>(xb);
   hipLaunchKernelGGL((nn_kernel<MODE>), dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0, s, operand, n_atoms, tiles,
-                     n_slices, tiles_per_slice, records);
+                     n_slices, tiles_per_slice, keys, groups);
   if ((st = check_launch("nn_kernel")) != PLX_OK) return st;
   profile_after(s);
   hipLaunchKernelGGL((resolve_kernel<MODE, FUSED>), dim3(static_cast<unsigned>((n_atoms + 255) / 256)), dim3(256), 0, s,
-                     records, n_slices, n_atoms, x, sigma, apr, xb, rescan, idx_out, packed_out);
+                     keys, groups, n_slices, n_atoms, x, sigma, apr, xb, rescan, idx_out, packed_out);
   return check_launch("resolve_kernel");
 }
 

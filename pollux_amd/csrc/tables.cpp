@@ -4,16 +4,14 @@
 //                to bf16 exactly as the reference's bf16 casts round them
 //                (castor.py:437, autocast at castor.py:552), in the MFMA tile
 //                layout of quantize.hip; 12288 tiles x 768 B = 9,437,184 B.
-// kp_bf16_lanes  the same bf16 values regrouped lane-major ([q][tile][4][24],
-//                rows 4q..4q+3 of each tile) so the resolve kernel reads one
-//                lane's 32 codes of a group as 1.5 KB contiguous; 9,437,184 B.
 // cb_raw         the raw int8 coordinates of all 196,561 rows (4,717,464 B);
 //                decoded per value into fp32 / bf16 / fp16 by the kernels.
 // kp_gemv        per code 16 B for the fused dequant-linear: the 24 raw
 //                coordinates as signed 4-bit fields, then type (0 origin,
 //                1 = +-4 pair, 2 = +-2 octad, 3 = one -3) | position of -3 << 8
 //                (3,144,976 B).
-// kp_dq          per code 3 words for the dequant kernel: the raw alphabet
+// kp_dq          per code 3 words for the dequant kernel and the quantizer's
+//                NN-B / NN-T rescans: the raw alphabet
 //                {0,1,2,4,-4,-3,-2,-1} (there is no +3) as value ids 0..7,
 //                word p byte i = id(coord 8p+i) | id(coord 8p+4+i) << 4, the
 //                order v_perm_b32 lookups want (2,358,732 B).
@@ -57,16 +55,6 @@ int build(int dev, DeviceTables *t) {
           tiles[static_cast<size_t>(tile) * 384 + p * 128 + i * 8 + e] = bf_of[k + 4];
         }
 
-  // lane-major copy for the resolve kernel: [q][tile][e][24], row = 4q + e
-  std::vector<uint16_t> lanes(static_cast<size_t>(4) * kPaddedTiles * 4 * kDim, 0);
-  for (int q = 0; q < 4; ++q)
-    for (int tile = 0; tile < kRealTiles; ++tile)
-      for (int e = 0; e < 4; ++e) {
-        const int code = tile * kTileCodes + 4 * q + e + 1;
-        uint16_t *dst = lanes.data() + ((static_cast<size_t>(q) * kPaddedTiles + tile) * 4 + e) * kDim;
-        for (int c = 0; c < kDim; ++c) dst[c] = bf_of[raw[static_cast<size_t>(code) * kDim + c] + 4];
-      }
-
   // raw-integer tiles (NN-P): same layout, value k as bf16
   std::vector<uint16_t> raw_tiles(tiles.size(), 0);
   for (int tile = 0; tile < kRealTiles; ++tile)
@@ -106,10 +94,9 @@ int build(int dev, DeviceTables *t) {
     size_t bytes;
     void **dev;
   };
-  void *dt = nullptr, *dl = nullptr, *dr = nullptr, *dg = nullptr, *dd = nullptr, *drt = nullptr;
+  void *dt = nullptr, *dr = nullptr, *dg = nullptr, *dd = nullptr, *drt = nullptr;
   const Upload ups[] = {
       {tiles.data(), tiles.size() * 2, &dt},
-      {lanes.data(), lanes.size() * 2, &dl},
       {raw, static_cast<size_t>(kCodebook) * kDim, &dr},
       {gemv.data(), gemv.size() * 4, &dg},
       {dq.data(), dq.size() * 4, &dd},
@@ -131,7 +118,6 @@ int build(int dev, DeviceTables *t) {
     return st;
   }
   t->kp_bf16_tiles = static_cast<uint8_t *>(dt);
-  t->kp_bf16_lanes = static_cast<uint8_t *>(dl);
   t->cb_raw = static_cast<int8_t *>(dr);
   t->kp_gemv = static_cast<uint8_t *>(dg);
   t->kp_dq = static_cast<uint32_t *>(dd);
