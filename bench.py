@@ -192,6 +192,42 @@ def gemv_extras(device, copies=200, m_gemm=64, replays=5):
     return out
 
 
+def optim_extras(device, mats, iters=10):
+    """Fused optimiser step + requantize (pollux.py:836-884) of the config-2 latents.
+
+    One step = plx_pollux_step_h24 on each of the four matrices: the Adam /
+    speed-cap / decay update (one HBM pass: grad, m, v, latent read, m, v,
+    latent written = 28 B per element) followed by the requantize.
+    """
+    import torch
+
+    from pollux_amd import optim
+
+    g = torch.Generator(device=device).manual_seed(11)
+    state = []
+    for w in mats:
+        state.append((torch.randn(w.shape, generator=g, device=device) * 1e-3,
+                      torch.zeros_like(w), torch.zeros_like(w), w.clone(), torch.empty_like(w)))
+    heat = torch.tensor(0.5, device=device)
+    inertia = optim.width_inertia(1152)
+    counter = torch.zeros((), dtype=torch.int64, device=device)  # the optimiser's device-resident step counter
+
+    def step():
+        sc = optim.step_scalars(heat, counter, inertia, device)  # once per step, as pollux.py:815-820
+        for grad, m, v, lat, p in state:
+            optim.pollux_h24_step_(p, grad, m, v, lat, heat=heat, step=counter, width_inertia=inertia, scalars=sc)
+        counter.add_(1)
+
+    t = time_gpu(step, iters, 3)
+    n_el = sum(w.numel() for w in mats)
+    return {
+        "step_ms": t * 1e3,
+        "atoms_per_s": n_el / 24 / t,
+        "note": "4 x plx_pollux_step_h24 (fused Adam/speed-cap/decay update + requantize) on the config-2 latents",
+        "update_bytes_per_element": 28,
+    }
+
+
 def traffic_from_profiles():
     p = ROOT / "profiles" / "nn_kernel_c2_traffic.json"
     if p.exists():
@@ -318,6 +354,7 @@ def main() -> int:
         log("[bench] extras: pack / unpack / dequant at config-4 scale; dequant-GEMV/GEMM at config 5")
         result["extras"] = extras(dev)
         result["extras"]["dequant_linear"] = gemv_extras(dev)
+        result["extras"]["optimizer_step"] = optim_extras(dev, mats)
     if not args.no_cpu_baseline:
         log(f"[bench] CPU baseline on {args.cpu_atoms} atoms")
         result["cpu_baseline"] = cpu_baseline(mats, args.cpu_atoms)

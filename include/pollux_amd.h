@@ -138,6 +138,31 @@ int plx_quantize_layer_pack(const float *w, int64_t rows, int64_t cols, uint8_t 
                             uint16_t *sigma16_out, int32_t *idx_out, void *workspace,
                             size_t workspace_bytes, void *stream);
 
+/* ---- fused optimiser step + requantize (pollux.py:836-884) ------------ */
+/* Workspace (device bytes) plx_pollux_step_h24 needs for a [rows, cols] parameter. */
+size_t plx_pollux_step_workspace_bytes(int64_t rows, int64_t cols);
+
+/* One optimiser step of one H24 parameter [rows, cols] (cols % 24 == 0), all
+ * fp32 and 16-byte aligned, m / v / latent updated in place:
+ *   m = fma(g, 1-b1, m*b1);  v = fma((1-b2)*g, g, v*b2);
+ *   s = neg_scale * ((m/bc1) / (sqrt(v/bc2) + 1e-8));
+ *   per 24-element atom: s *= min(reciprocal(|s|_2 + 1e-8) * cap, 1);
+ *   latent = latent*wdf + s;
+ * then the requantize of plx_requantize on the new latent (sigma_out, idx_out
+ * required; packed_out, weight_out nullable; weight_out is the parameter's
+ * new data), and, if adam_norm_out is not NULL, adam_norm_out[0] = |s|_2 over
+ * the whole parameter.  scalars: DEVICE float[9] = {b1, 1-b1, b2, 1-b2,
+ * max(bc1, 1e-8), max(bc2, 1e-8), neg_scale, wdf, cap} as the reference's
+ * 0-dim fp32 tensors evaluate them (bc = 1 - b^(step+1); neg_scale =
+ * -(heat*gamma/C / width_inertia); wdf = 1 - heat*gamma^2; cap =
+ * KINEMATIC_LIMIT*s_lattice), so no host synchronisation is needed.
+ * Replaces the H24 branch of pollux_step (pollux.py:836-884) and its
+ * vector_norm contribution to adam_energy_sum (pollux.py:886-888). */
+int plx_pollux_step_h24(const float *grad, float *m, float *v, float *latent, int64_t rows, int64_t cols,
+                        const float *scalars, int mode, float *sigma_out, int32_t *idx_out,
+                        uint8_t *packed_out, float *weight_out, float *adam_norm_out,
+                        void *workspace, size_t workspace_bytes, void *stream);
+
 /* ---- dequantization (pollux.py:485-507) -------------------------------- */
 /* w16 = fp16(fp16(codebook16[unpack(packed)] * sigma16[row]) * fp32(1/sqrt 2)),
  * shape [rows, cols] as raw fp16 bits.  Replaces PackedH24Linear.materialize

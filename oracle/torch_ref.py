@@ -106,3 +106,38 @@ def materialize(indices: torch.Tensor, sigma16: torch.Tensor, out_features: int,
 def linear_fp32(x: torch.Tensor, w16: torch.Tensor) -> torch.Tensor:
     """The fp32 reference for the packed layer: F.linear(x.float(), W.float()) (pollux.py:507 with fp32 x)."""
     return torch.nn.functional.linear(x.float(), w16.float())
+
+
+def pollux_h24_update(grad, m, v, latent, heat, step, width_inertia):
+    """pollux.py:815-878 for one H24 parameter with the reference's torch ops on the CPU (sqrt correctly rounded).
+
+    m, v, latent are updated in place (as the reference does); returns the capped step.
+    heat: 0-dim fp32 tensor; step: the step counter before the update (int).
+    """
+    gamma = 0.065771
+    c_f = math.sqrt(2.0)
+    kinematic_limit = (c_f - 1.0) / 2.0
+    beta_2 = 1.0 - float(gamma)
+    beta_1 = 1.0 - math.sqrt(float(gamma))
+    step_f = torch.tensor(float(step), dtype=torch.float32) + 1.0
+    bc1 = 1.0 - (torch.as_tensor(beta_1, dtype=torch.float32) ** step_f)
+    bc2 = 1.0 - (torch.as_tensor(beta_2, dtype=torch.float32) ** step_f)
+    m.mul_(beta_1).add_(grad, alpha=1.0 - beta_1)
+    v.mul_(beta_2).addcmul_(grad, grad, value=1.0 - beta_2)
+    m_unbiased = m / torch.clamp(bc1, min=NUMERICAL_EPSILON)
+    v_unbiased = v / torch.clamp(bc2, min=NUMERICAL_EPSILON)
+    # torch's vectorised CPU sqrt is faithful, not correctly rounded (1 ulp off on
+    # ~0.7% of fp32 inputs); the reference runs this step on its GPU, where sqrtf
+    # is correctly rounded.  sqrt in float64 then rounded to fp32 is the
+    # correctly rounded fp32 sqrt (53 >= 2*24 + 2 bits).
+    denom = torch.sqrt(v_unbiased.double()).float() + NUMERICAL_EPSILON
+    kinetic_scale = heat * float(gamma) / float(c_f)
+    adam_step = -(kinetic_scale / width_inertia) * (m_unbiased / denom)
+    adam_h24 = adam_step.reshape(-1, 24)
+    step_norm = torch.linalg.vector_norm(adam_h24, dim=-1, keepdim=True)
+    speed_cap = float(kinematic_limit) * float(S_LATTICE)
+    adam_step = (adam_h24 * torch.clamp(speed_cap / (step_norm + NUMERICAL_EPSILON), max=1.0)).reshape_as(adam_step)
+    weight_decay_factor = 1.0 - (heat * (float(gamma) ** 2))
+    latent.mul_(weight_decay_factor)
+    latent.add_(adam_step)
+    return adam_step

@@ -9,10 +9,11 @@ packed   PackedH24Linear (HIP dequantization, fused dequant-GEMV/GEMM) and the
 pack     pack.py-compatible pack-time quantization (_quantize_h24_layer,
          _quantize_int8, the state-dict packing loop)
 plx      the .plx container: byte-exact writer, reader, memory-mapped loader
+optim    the fused optimiser step + requantize of an H24 parameter (pollux_step's H24 branch)
 build    builds lib/libpollux_amd.so (hipcc, gfx950) in-tree
 """
 
-from . import castor, pack, plx  # noqa: F401
+from . import castor, optim, pack, plx  # noqa: F401
 from .packed import (  # noqa: F401
     PackedH24Linear,
     PackedInt8Embedding,
@@ -23,6 +24,6 @@ from .packed import (  # noqa: F401
 )
 
 __all__ = [
-    "castor", "pack", "plx", "PackedH24Linear", "PackedInt8Embedding", "PackedInt8Linear",
+    "castor", "optim", "pack", "plx", "PackedH24Linear", "PackedInt8Embedding", "PackedInt8Linear",
     "dequant_linear", "dequantize_h24", "dequantize_int8_rows",
 ]

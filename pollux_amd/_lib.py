@@ -38,6 +38,8 @@ SIGNATURES = {
     "plx_gather_codebook": (_int, [_vp, _i64, _int, _vp, _vp]),
     "plx_requantize": (_int, [_vp, _i64, _i64, _int, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
     "plx_quantize_layer_pack": (_int, [_vp, _i64, _i64, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "plx_pollux_step_workspace_bytes": (_sz, [_i64, _i64]),
+    "plx_pollux_step_h24": (_int, [_vp, _vp, _vp, _vp, _i64, _i64, _vp, _int, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
     "plx_quantize_int8_rows": (_int, [_vp, _i64, _i64, _vp, _vp, _vp]),
     "plx_dequant_int8_rows": (_int, [_vp, _vp, _i64, _i64, _vp, _vp]),
     "plx_dequant_f16": (_int, [_vp, _i64, _vp, _i64, _i64, _vp, _vp]),

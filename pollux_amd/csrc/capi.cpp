@@ -161,6 +161,38 @@ int plx_requantize(const float *latent, int64_t rows, int64_t cols, int mode, fl
                          workspace_bytes, as_stream(stream));
 }
 
+size_t plx_pollux_step_workspace_bytes(int64_t rows, int64_t cols) {
+  if (rows <= 0 || cols <= 0 || cols % kDim != 0) return 0;
+  const int64_t n_atoms = rows * (cols / kDim);
+  return ((quantize_workspace_bytes(n_atoms) + 255) & ~static_cast<size_t>(255)) + adam_h24_workspace_bytes(n_atoms);
+}
+
+int plx_pollux_step_h24(const float *grad, float *m, float *v, float *latent, int64_t rows, int64_t cols,
+                        const float *scalars, int mode, float *sigma_out, int32_t *idx_out, uint8_t *packed_out,
+                        float *weight_out, float *adam_norm_out, void *workspace, size_t workspace_bytes, void *stream) {
+  PLX_REQUIRE(rows >= 0 && cols > 0, "plx_pollux_step_h24: bad shape (%lld, %lld)", static_cast<long long>(rows),
+              static_cast<long long>(cols));
+  PLX_REQUIRE(cols % kDim == 0, "Pollux requires in_features divisible by H24_DIM=24; got %lld.",
+              static_cast<long long>(cols));
+  PLX_REQUIRE(mode == PLX_NN_BF16_SCORES || mode == PLX_NN_FP32_SCORES, "plx_pollux_step_h24: unknown mode %d", mode);
+  if (rows == 0) return PLX_OK;
+  PLX_REQUIRE(grad != nullptr && m != nullptr && v != nullptr && latent != nullptr && scalars != nullptr &&
+                  sigma_out != nullptr && idx_out != nullptr,
+              "plx_pollux_step_h24: null pointer");
+  const size_t need = plx_pollux_step_workspace_bytes(rows, cols);
+  PLX_REQUIRE(workspace != nullptr && workspace_bytes >= need,
+              "plx_pollux_step_h24: workspace of %zu bytes is smaller than the %zu needed", workspace_bytes, need);
+  const int64_t n_atoms = rows * (cols / kDim);
+  const size_t qws = (quantize_workspace_bytes(n_atoms) + 255) & ~static_cast<size_t>(255);
+  int st = launch_adam_h24(grad, m, v, latent, n_atoms, scalars, adam_norm_out, static_cast<uint8_t *>(workspace) + qws,
+                           as_stream(stream));
+  if (st != PLX_OK) return st;
+  st = launch_row_rms(latent, rows, cols, sigma_out, nullptr, as_stream(stream));
+  if (st != PLX_OK) return st;
+  return launch_quantize(latent, sigma_out, rows, cols, n_atoms, mode, idx_out, packed_out, weight_out, workspace, qws,
+                         as_stream(stream));
+}
+
 int plx_quantize_layer_pack(const float *w, int64_t rows, int64_t cols, uint8_t *packed_out, uint16_t *sigma16_out,
                             int32_t *idx_out, void *workspace, size_t workspace_bytes, void *stream) {
   PLX_REQUIRE(rows >= 0 && cols > 0, "plx_quantize_layer_pack: bad shape (%lld, %lld)", static_cast<long long>(rows),
