@@ -228,6 +228,21 @@ def optim_extras(device, mats, iters=10):
     }
 
 
+def pack_time_extras(mats, iters=5):
+    """Pack-time NN-P quantizer (pack.py:139-180) on the config-2 weights: atoms/s.
+
+    NN-P scores fp32 atoms exactly (three bf16 MFMA parts per tile) and
+    rescans its candidates in fp64, so it does ~3x the MFMA work of NN-B.
+    """
+    from pollux_amd import pack
+
+    t = time_gpu(lambda: [pack.quantize_h24_layer(w) for w in mats], iters, 2)
+    n = sum(w.numel() for w in mats) // 24
+    return {"atoms_per_s": n / t, "ms_per_layer": t * 1e3,
+            "mfma_issue_frac_of_bf16_peak": 3 * 32 * 196_608 * 16 * 2 * n / 16 / t / PEAK_BF16_FLOPS,
+            "note": "quantize_h24_layer (NN-P + sigma16 + 18-bit pack) on the four config-2 weights"}
+
+
 def traffic_from_profiles():
     p = ROOT / "profiles" / "nn_kernel_c2_traffic.json"
     if p.exists():
@@ -355,6 +370,7 @@ def main() -> int:
         result["extras"] = extras(dev)
         result["extras"]["dequant_linear"] = gemv_extras(dev)
         result["extras"]["optimizer_step"] = optim_extras(dev, mats)
+        result["extras"]["pack_time_nn_p"] = pack_time_extras(mats)
     if not args.no_cpu_baseline:
         log(f"[bench] CPU baseline on {args.cpu_atoms} atoms")
         result["cpu_baseline"] = cpu_baseline(mats, args.cpu_atoms)
