@@ -297,6 +297,10 @@ def main() -> int:
         for w in mats:
             castor.requantize_h24(w, mode=args.mode)
 
+    def step_batched():
+        # one scoring sweep over the layer's four latents (plx_requantize_batch)
+        castor.requantize_h24_many(mats, mode=args.mode)
+
     if args.pmc_workload:
         src = torch.ones(64 * 1024 * 1024, dtype=torch.float32, device=dev)  # 256 MiB
         dst = torch.empty_like(src)
@@ -360,6 +364,7 @@ def main() -> int:
             "workload": "BASELINE config 2: Pollux-1152 single-layer requantize (row scale + NN-B quantize + "
             "18-bit pack + reconstructed weight) of QKV 3456x1152, O 1152x1152, up 4608x1152, down 1152x4608",
             "atoms_per_step": atoms,
+            "call": "castor.requantize_h24 per latent, as the reference's per-parameter loop (pollux.py:828-884)",
             "nn_mode": "NN-B (bf16 scores)" if args.mode == "bf16" else "NN-T (fp32 scores)",
             "seed": 2024,
         },
@@ -368,6 +373,10 @@ def main() -> int:
     if not args.no_extras:
         log("[bench] extras: pack / unpack / dequant at config-4 scale; dequant-GEMV/GEMM at config 5")
         result["extras"] = extras(dev)
+        t_b = time_gpu(step_batched, args.steps, 2)
+        result["extras"]["requantize_batched"] = {
+            "ms_per_step": t_b * 1e3, "atoms_per_s": atoms / t_b,
+            "note": "the same step as one requantize_h24_many call (plx_requantize_batch, one sweep for all four)"}
         result["extras"]["dequant_linear"] = gemv_extras(dev)
         result["extras"]["optimizer_step"] = optim_extras(dev, mats)
         result["extras"]["pack_time_nn_p"] = pack_time_extras(mats)

@@ -129,6 +129,25 @@ int plx_requantize(const float *latent, int64_t rows, int64_t cols, int mode,
                    float *sigma_out, int32_t *idx_out, uint8_t *packed_out, float *weight_out,
                    void *workspace, size_t workspace_bytes, void *stream);
 
+/* One matrix of plx_requantize_batch: the arguments of plx_requantize. */
+typedef struct plx_requantize_item {
+  const float *latent;   /* float[rows*cols], 16-byte aligned */
+  int64_t rows, cols;    /* cols % 24 == 0 */
+  float *sigma_out;      /* float[rows] */
+  int32_t *idx_out;      /* int32[rows*cols/24] */
+  uint8_t *packed_out;   /* uint8[((N+3)/4)*9] or NULL */
+  float *weight_out;     /* float[rows*cols] or NULL */
+} plx_requantize_item;
+
+/* plx_requantize of n_items latents with one scoring sweep over all their
+ * atoms (a layer's matrices, or every parameter of an optimiser step): the
+ * results equal n_items separate plx_requantize calls (up to near-ties).
+ * items is a HOST array; workspace: plx_quantize_workspace_bytes(total atoms).
+ * Replaces the per-parameter requantize of the pollux_step loop
+ * (pollux.py:828-884) for the H24 parameters of one step. */
+int plx_requantize_batch(const plx_requantize_item *items, int n_items, int mode,
+                         void *workspace, size_t workspace_bytes, void *stream);
+
 /* Pack-time quantization of one weight [rows, cols] (cols % 24 == 0):
  *   idx = NN-P(w atoms); packed_out = pack(idx) (uint8[((N+3)/4)*9]);
  *   sigma16_out[r] = fp16(max(row_rms(w)[r] * fp32(sqrt 12), 1e-8)) (raw bits);

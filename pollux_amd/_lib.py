@@ -38,6 +38,7 @@ SIGNATURES = {
     "plx_gather_codebook": (_int, [_vp, _i64, _int, _vp, _vp]),
     "plx_requantize": (_int, [_vp, _i64, _i64, _int, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
     "plx_quantize_layer_pack": (_int, [_vp, _i64, _i64, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "plx_requantize_batch": (_int, [_vp, _int, _int, _vp, _sz, _vp]),
     "plx_pollux_step_workspace_bytes": (_sz, [_i64, _i64]),
     "plx_pollux_step_h24": (_int, [_vp, _vp, _vp, _vp, _i64, _i64, _vp, _int, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
     "plx_quantize_int8_rows": (_int, [_vp, _i64, _i64, _vp, _vp, _vp]),
@@ -48,6 +49,15 @@ SIGNATURES = {
     "plx_profile_begin": (_int, []),
     "plx_profile_end": (_int, [_vp, _vp]),
 }
+
+class RequantizeItem(ctypes.Structure):
+    """plx_requantize_item (include/pollux_amd.h)."""
+
+    _fields_ = [
+        ("latent", _vp), ("rows", _i64), ("cols", _i64), ("sigma_out", _vp),
+        ("idx_out", _vp), ("packed_out", _vp), ("weight_out", _vp),
+    ]
+
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

@@ -364,6 +364,50 @@ def requantize_h24(latent: torch.Tensor, *, mode: str | None = None, pack: bool 
     return {"sigma": sigma, "indices": idx, "packed": packed, "weight": w}
 
 
+def requantize_h24_many(
+    latents: list[torch.Tensor], *, mode: str | None = None, pack: bool = True, weight: bool = True
+) -> list[dict]:
+    """requantize_h24 on several fp32 latents with one scoring sweep over all their atoms.
+
+    The per-step requantize of pollux.py:828-884 for a group of parameters
+    (e.g. a layer's matrices) on one device; returns one dict per latent, as
+    requantize_h24 does.  Indices equal separate requantize_h24 calls except
+    possibly on near-tie atoms.
+    """
+    if not latents:
+        return []
+    dev = latents[0].device
+    lats, outs, items = [], [], []
+    for t in latents:
+        if t.dim() != 2:
+            raise ValueError(f"requantize_h24_many expects 2D latents, got {t.dim()}D.")
+        _lib.require_device(t, "requantize_h24_many input")
+        if t.device != dev:
+            raise ValueError("requantize_h24_many: all latents must be on one device")
+        rows, cols = t.shape
+        assert_row_aligned_in_features(cols)
+        lat = t.detach().float().contiguous()
+        n = rows * (cols // H24_DIM)
+        o = {
+            "sigma": torch.empty(rows, dtype=torch.float32, device=dev),
+            "indices": torch.empty(n, dtype=torch.int32, device=dev),
+            "packed": torch.empty(((n + 3) // 4) * BYTES_PER_CHUNK, dtype=torch.uint8, device=dev) if pack else None,
+            "weight": torch.empty_like(lat) if weight else None,
+        }
+        lats.append(lat)
+        outs.append(o)
+        items.append(_lib.RequantizeItem(_lib.ptr(lat), rows, cols, _lib.ptr(o["sigma"]), _lib.ptr(o["indices"]),
+                                         _lib.ptr(o["packed"]), _lib.ptr(o["weight"])))
+    total = sum(o["indices"].numel() for o in outs)
+    ws = _workspace(total, dev)
+    arr = (_lib.RequantizeItem * len(items))(*items)
+    with torch.cuda.device(dev):
+        st = _lib.lib().plx_requantize_batch(arr, len(items), _MODES[mode or _nn_mode], _lib.ptr(ws), ws.numel(),
+                                             _lib.stream_of(dev))
+    _lib.check(st, "requantize_h24_many")
+    return outs
+
+
 def sigma16_pack(weight: torch.Tensor) -> torch.Tensor:
     """fp16(clamp(row_rms(w) * sqrt(12), 1e-8)) per row (pack.py:164)."""
     if weight.dim() != 2:

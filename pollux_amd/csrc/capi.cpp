@@ -7,6 +7,7 @@
 #include <cstdio>
 #include <cstring>
 #include <string>
+#include <vector>
 
 #include "plx_internal.h"
 
@@ -159,6 +160,26 @@ int plx_requantize(const float *latent, int64_t rows, int64_t cols, int mode, fl
   if (st != PLX_OK) return st;
   return launch_quantize(latent, sigma_out, rows, cols, n_atoms, mode, idx_out, packed_out, weight_out, workspace,
                          workspace_bytes, as_stream(stream));
+}
+
+int plx_requantize_batch(const plx_requantize_item *items, int n_items, int mode, void *workspace,
+                         size_t workspace_bytes, void *stream) {
+  PLX_REQUIRE(n_items >= 0 && n_items <= 4096, "plx_requantize_batch: bad item count %d", n_items);
+  PLX_REQUIRE(mode == PLX_NN_BF16_SCORES || mode == PLX_NN_FP32_SCORES, "plx_requantize_batch: unknown mode %d", mode);
+  if (n_items == 0) return PLX_OK;
+  PLX_REQUIRE(items != nullptr, "plx_requantize_batch: null item array");
+  std::vector<RequantItem> its(static_cast<size_t>(n_items));
+  for (int i = 0; i < n_items; ++i) {
+    const plx_requantize_item &x = items[i];
+    PLX_REQUIRE(x.rows >= 0 && x.cols > 0, "plx_requantize_batch: item %d has a bad shape (%lld, %lld)", i,
+                static_cast<long long>(x.rows), static_cast<long long>(x.cols));
+    PLX_REQUIRE(x.cols % kDim == 0, "Pollux requires in_features divisible by H24_DIM=24; got %lld (item %d).",
+                static_cast<long long>(x.cols), i);
+    PLX_REQUIRE(x.rows == 0 || (x.latent != nullptr && x.sigma_out != nullptr && x.idx_out != nullptr),
+                "plx_requantize_batch: item %d has a null pointer", i);
+    its[static_cast<size_t>(i)] = RequantItem{x.latent, x.rows, x.cols, x.sigma_out, x.idx_out, x.packed_out, x.weight_out};
+  }
+  return launch_requantize_batch(its.data(), n_items, mode, workspace, workspace_bytes, as_stream(stream));
 }
 
 size_t plx_pollux_step_workspace_bytes(int64_t rows, int64_t cols) {

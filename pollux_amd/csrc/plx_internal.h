@@ -66,6 +66,18 @@ int launch_quantize(const float *x, const float *sigma, int64_t rows, int64_t co
                     int mode, int32_t *idx_out, uint8_t *packed_out, float *weight_out,
                     void *workspace, size_t workspace_bytes, hipStream_t s);
 size_t quantize_workspace_bytes(int64_t n_atoms);
+// One matrix of a batched requantize (the latent's row scale, indices, packed
+// bytes and reconstructed weight; packed and weight may be null).
+struct RequantItem {
+  const float *latent;
+  int64_t rows, cols;
+  float *sigma;
+  int32_t *idx;
+  uint8_t *packed;
+  float *weight;
+};
+int launch_requantize_batch(const RequantItem *items, int n_items, int mode, void *workspace, size_t workspace_bytes,
+                            hipStream_t s);
 int launch_gather(const int32_t *idx, int64_t n, int out_dtype, void *out, hipStream_t s);
 int launch_dequant_f16(const uint8_t *packed, const uint16_t *sigma16, int64_t rows, int64_t cols,
                        uint16_t *w16, hipStream_t s);

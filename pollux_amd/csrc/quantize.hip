@@ -375,6 +375,9 @@ __global__ __launch_bounds__(kThreads, 2) void nn_kernel(const void *__restrict_
 //            then a 3-step shuffle reduction per candidate;
 //   merge    thread per atom folds its candidates' results in list order.
 // An atom with more than kRsPerRound candidates continues in the next round.
+// keys / groups / xb point at this call's first atom; the records of slice s
+// start rec_stride atoms apart (the atom count of the sweep, which may cover
+// several matrices).
 // NN-B picks the lowest code whose bf16 score bucket equals M (falling back to
 // the best rounded score, lowest code on ties, if the fp32 sums disagree with
 // the sweep's); NN-T the highest fp32 score, lowest code on ties; NN-P the
@@ -391,7 +394,8 @@ struct RsScore {  // per-candidate / per-atom running result
 template <int MODE, bool FUSED>
 __global__ __launch_bounds__(256) void resolve_kernel(const uint32_t *__restrict__ keys,
                                                       const uint2 *__restrict__ groups, int n_slices,
-                                                      int64_t n_atoms, const float *__restrict__ src,
+                                                      int64_t rec_stride, int64_t n_atoms,
+                                                      const float *__restrict__ src,
                                                       const float *__restrict__ sigma, int64_t atoms_per_row,
                                                       const uint4 *__restrict__ xb, const uint8_t *__restrict__ rescan,
                                                       int32_t *__restrict__ idx_out, uint8_t *__restrict__ packed_out) {
@@ -421,7 +425,7 @@ __global__ __launch_bounds__(256) void resolve_kernel(const uint32_t *__restrict
     for (int s0 = 0; s0 < n_slices; s0 += 8) {
       uint32_t k[8];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) k[i] = s0 + i < n_slices ? keys[static_cast<int64_t>(s0 + i) * n_atoms + a] : 0u;
+      for (int i = 0; i < 8; ++i) k[i] = s0 + i < n_slices ? keys[static_cast<int64_t>(s0 + i) * rec_stride + a] : 0u;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         if (k[i] > M) {
@@ -465,7 +469,7 @@ __global__ __launch_bounds__(256) void resolve_kernel(const uint32_t *__restrict
       while (mask != 0 && nm < kRsPerRound) {
         const int s = __builtin_ctzll(mask);
         if (s != loaded) {
-          rec = groups[static_cast<int64_t>(s) * n_atoms + a];
+          rec = groups[static_cast<int64_t>(s) * rec_stride + a];
           loaded = s;
         }
         const int qq = qpos;
@@ -727,7 +731,7 @@ int launch_mode(const float *x, const float *sigma, int64_t apr, int64_t n_atoms
   if ((st = check_launch("nn_kernel")) != PLX_OK) return st;
   profile_after(s);
   hipLaunchKernelGGL((resolve_kernel<MODE, FUSED>), dim3(static_cast<unsigned>((n_atoms + 255) / 256)), dim3(256), 0, s,
-                     keys, groups, n_slices, n_atoms, x, sigma, apr, xb, rescan, idx_out, packed_out);
+                     keys, groups, n_slices, n_atoms, n_atoms, x, sigma, apr, xb, rescan, idx_out, packed_out);
   return check_launch("resolve_kernel");
 }
 
@@ -770,6 +774,85 @@ int launch_quantize(const float *x, const float *sigma, int64_t rows, int64_t co
     if ((st = check_launch("gather_kernel")) != PLX_OK) return st;
   }
   return PLX_OK;
+}
+
+namespace {
+
+// Several latents in one scoring sweep: row scale and operand planes per
+// matrix, one nn_kernel launch over all their atoms (fewer codebook slices per
+// atom block and no per-matrix tail of the grid), then per matrix the resolve
+// (index + pack) and the scaled gather of the reconstructed weight.
+template <int MODE>
+int launch_batch_mode(const RequantItem *items, int n_items, const DeviceTables *tab, uint8_t *workspace,
+                      hipStream_t s) {
+  int64_t total = 0;
+  for (int i = 0; i < n_items; ++i) total += items[i].rows * (items[i].cols / kDim);
+  if (total == 0) return PLX_OK;
+  const int64_t ablocks = (total + kAtomsPerBlock - 1) / kAtomsPerBlock;
+  const int n_slices = choose_slices(ablocks);
+  const int tiles_per_slice = kPaddedTiles / n_slices;
+  const int64_t grid = ablocks * n_slices;
+  if (grid > 0x7FFFFFFFll) return fail(PLX_EINVAL, "requantize_batch: %lld atoms exceed one launch", static_cast<long long>(total));
+  const size_t n_rec = static_cast<size_t>(total) * static_cast<size_t>(n_slices);
+  uint32_t *keys = reinterpret_cast<uint32_t *>(workspace);
+  uint2 *groups = reinterpret_cast<uint2 *>(workspace + ((n_rec * 4 + 255) & ~static_cast<size_t>(255)));
+  uint4 *xb = reinterpret_cast<uint4 *>(workspace + ((records_bytes(total) + 255) & ~static_cast<size_t>(255)));
+  int st;
+  int64_t off = 0;
+  for (int i = 0; i < n_items; ++i) {
+    const RequantItem &it = items[i];
+    const int64_t apr = it.cols / kDim, n = it.rows * apr;
+    if (n == 0) continue;
+    if ((st = launch_row_rms(it.latent, it.rows, it.cols, it.sigma, nullptr, s)) != PLX_OK) return st;
+    hipLaunchKernelGGL((prep_kernel<true>), dim3(static_cast<unsigned>((n * 3 + 255) / 256)), dim3(256), 0, s, it.latent,
+                       it.sigma, apr, n, xb + off * 3);
+    if ((st = check_launch("prep_kernel")) != PLX_OK) return st;
+    off += n;
+  }
+  profile_before(s);
+  hipLaunchKernelGGL((nn_kernel<MODE>), dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0, s,
+                     static_cast<const void *>(xb), total, tab->kp_bf16_tiles, n_slices, tiles_per_slice, keys, groups);
+  if ((st = check_launch("nn_kernel")) != PLX_OK) return st;
+  profile_after(s);
+  off = 0;
+  for (int i = 0; i < n_items; ++i) {
+    const RequantItem &it = items[i];
+    const int64_t apr = it.cols / kDim, n = it.rows * apr;
+    if (n == 0) continue;
+    hipLaunchKernelGGL((resolve_kernel<MODE, true>), dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s,
+                       keys + off, groups + off, n_slices, total, n, it.latent, it.sigma, apr, xb + off * 3,
+                       reinterpret_cast<const uint8_t *>(tab->kp_dq), it.idx, it.packed);
+    if ((st = check_launch("resolve_kernel")) != PLX_OK) return st;
+    if (it.weight) {
+      hipLaunchKernelGGL((gather_kernel<0, true>), dim3(static_cast<unsigned>((n * 6 + 255) / 256)), dim3(256), 0, s,
+                         it.idx, n, tab->cb_raw, it.sigma, apr, static_cast<void *>(it.weight));
+      if ((st = check_launch("gather_kernel")) != PLX_OK) return st;
+    }
+    off += n;
+  }
+  return PLX_OK;
+}
+
+}  // namespace
+
+int launch_requantize_batch(const RequantItem *items, int n_items, int mode, void *workspace, size_t workspace_bytes,
+                            hipStream_t s) {
+  int64_t total = 0;
+  for (int i = 0; i < n_items; ++i) total += items[i].rows * (items[i].cols / kDim);
+  if (total == 0) return PLX_OK;
+  if (workspace == nullptr || workspace_bytes < quantize_workspace_bytes(total))
+    return fail(PLX_EINVAL, "requantize_batch: workspace of %zu bytes is smaller than the %zu needed for %lld atoms",
+                workspace_bytes, quantize_workspace_bytes(total), static_cast<long long>(total));
+  if ((reinterpret_cast<uintptr_t>(workspace) & 15u) != 0) return fail(PLX_EINVAL, "requantize_batch: workspace must be 16-byte aligned");
+  for (int i = 0; i < n_items; ++i)
+    if ((reinterpret_cast<uintptr_t>(items[i].latent) & 15u) != 0)
+      return fail(PLX_EINVAL, "requantize_batch: latent %d must be 16-byte aligned", i);
+  const DeviceTables *tab = nullptr;
+  int st = get_tables(&tab);
+  if (st != PLX_OK) return st;
+  uint8_t *ws = static_cast<uint8_t *>(workspace);
+  return mode == PLX_NN_BF16_SCORES ? launch_batch_mode<PLX_NN_BF16_SCORES>(items, n_items, tab, ws, s)
+                                    : launch_batch_mode<PLX_NN_FP32_SCORES>(items, n_items, tab, ws, s);
 }
 
 int launch_gather(const int32_t *idx, int64_t n, int out_dtype, void *out, hipStream_t s) {

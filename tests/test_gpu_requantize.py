@@ -63,3 +63,27 @@ def test_sigma16_pack(dev):
     d = (got.view(torch.int16).long() - want.view(torch.int16).long()).abs()
     assert d.max() <= 1
     print(f"[sigma16] exact {float((d == 0).float().mean()):.4f}", flush=True)
+
+
+def test_batched_requantize_equals_separate_calls(dev):
+    # plx_requantize_batch: one scoring sweep over the atoms of several latents
+    # (BASELINE config-2 layer + a ragged small matrix); every output equals the
+    # separate requantize_h24 calls, except indices that differ only on
+    # near-tie atoms (checked against the oracle).
+    g = torch.Generator().manual_seed(77)
+    shapes = [(3456, 1152), (1152, 1152), (4608, 1152), (1152, 4608), (5, 24), (0, 48), (3, 72)]
+    lats = [((torch.randn(r, c, generator=g) * 0.02).to(torch.bfloat16).float()).to(dev) for r, c in shapes]
+    many = castor.requantize_h24_many(lats)
+    for lat, got in zip(lats, many):
+        one = castor.requantize_h24(lat)
+        assert torch.equal(got["sigma"], one["sigma"])
+        diff = (got["indices"] != one["indices"]).nonzero().flatten().cpu().numpy()
+        if len(diff):
+            x, _ = torch_ref.lattice_input(lat.cpu(), one["sigma"].cpu())
+            r = nn.quantize(x.reshape(-1, 24)[torch.from_numpy(diff)].numpy(), "B")
+            assert r["near_tie"].all(), diff[~r["near_tie"]][:10]
+            assert len(diff) <= max(3, got["indices"].numel() // 1000)
+        else:
+            assert torch.equal(got["packed"], one["packed"])
+            assert torch.equal(got["weight"], one["weight"])
+        assert np.array_equal(got["packed"].cpu().numpy(), packing.pack(got["indices"].cpu().numpy().astype(np.int64)))
