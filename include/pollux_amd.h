@@ -194,9 +194,13 @@ int plx_dequant_f16(const uint8_t *packed, int64_t n_packed_bytes, const uint16_
 size_t plx_dequant_linear_workspace_bytes(int64_t rows, int64_t cols, int64_t m_rows, int x_is_f32);
 
 /* y[m, r] = sum_i x[m, i] * W[r, i] for m < m_rows, with W the fp16
- * materialisation of (packed, sigma16) above, never stored: x is bf16
- * (x_is_f32 = 0) or fp32 (x_is_f32 = 1) [m_rows, cols], y fp32 [m_rows, rows],
- * fp32 accumulation; results are deterministic (fixed summation order).
+ * materialisation of (packed, sigma16) above cast to x's dtype as the reference
+ * does, never stored: x is bf16 (x_is_f32 = 0; W is rounded to bf16, RNE) or
+ * fp32 (x_is_f32 = 1; W exact) [m_rows, cols], y fp32 [m_rows, rows], exact
+ * products with fp32 accumulation; results are deterministic (fixed summation
+ * order).  bf16 batches above 16 tokens need the workspace sized by
+ * plx_dequant_linear_workspace_bytes (a fragment-order copy of x, plus split
+ * partial tiles for narrow layers); cols <= 2^23.
  * Replaces PackedH24Linear.forward after materialize (pollux.py:506-507:
  * F.linear(x, weight.to(x.dtype))), evaluated in fp32. */
 int plx_dequant_linear(const uint8_t *packed, int64_t n_packed_bytes, const uint16_t *sigma16,

@@ -108,6 +108,17 @@ def linear_fp32(x: torch.Tensor, w16: torch.Tensor) -> torch.Tensor:
     return torch.nn.functional.linear(x.float(), w16.float())
 
 
+def linear_as_reference(x: torch.Tensor, w16: torch.Tensor) -> torch.Tensor:
+    """pollux.py:507, F.linear(x, W.to(x.dtype)), evaluated in fp32 on the CPU.
+
+    The weight is first rounded to x's dtype as the reference does (bf16 RNE for
+    bf16 activations, exact for fp32); the products of two bf16 values are
+    exact in fp32, so this differs from the reference's GEMM only in the
+    summation order (and in not rounding the output back to x's dtype).
+    """
+    return torch.nn.functional.linear(x.float(), w16.to(x.dtype).float())
+
+
 def pollux_h24_update(grad, m, v, latent, heat, step, width_inertia):
     """pollux.py:815-878 for one H24 parameter with the reference's torch ops on the CPU (sqrt correctly rounded).
 

@@ -136,8 +136,10 @@ namespace {
 //   type 3 (+-1, one -3 at coordinate p) v1 * (D + 3 x_p) - v3 * x_p
 //   origin                              0
 // The row keeps four fp32 partial sums and applies the magnitudes once at the
-// end: the same products as the reference's fp32 F.linear on the fp16 W,
-// regrouped (fp32 rounding differs at the 1e-7 relative level).
+// end: the same products as the reference's F.linear(x, W.to(x.dtype))
+// (pollux.py:507), regrouped (fp32 rounding differs at the 1e-7 relative
+// level).  W.to(x.dtype) is the fp16 value for fp32 activations and its bf16
+// RNE rounding for bf16 activations, so the magnitudes are rounded likewise.
 //
 // Per code the kernel reads one 16-byte entry of kp_gemv (24 signed 4-bit
 // coordinates + type/position byte; 3.1 MB, L2-resident per XCD).
@@ -299,11 +301,17 @@ __global__ __launch_bounds__(256) void dqlinear_kernel(const uint8_t *__restrict
       const float v2 = __half2float(__ushort_as_half(static_cast<uint16_t>(dq_value(2, sig, sl))));
       const float v3 = __half2float(__ushort_as_half(static_cast<uint16_t>(dq_value(3, sig, sl))));
       const float v4 = __half2float(__ushort_as_half(static_cast<uint16_t>(dq_value(4, sig, sl))));
+      // bf16 activations: the reference multiplies by W.to(bf16) (pollux.py:507), an RNE
+      // rounding of each magnitude (RNE is odd, so the signed weights follow)
+      const float m1 = XF32 ? v1 : bf16_bits_to_float(bf16_rne_bits(v1));
+      const float m2 = XF32 ? v2 : bf16_bits_to_float(bf16_rne_bits(v2));
+      const float m3 = XF32 ? v3 : bf16_bits_to_float(bf16_rne_bits(v3));
+      const float m4 = XF32 ? v4 : bf16_bits_to_float(bf16_rne_bits(v4));
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb)
         if (mb < mb_here)
           y[(m0 + mb) * rows + row] =
-              v4 * (acc[mb][0] * 0.25f) + v2 * (acc[mb][1] * 0.5f) + v1 * acc[mb][2] - v3 * acc[mb][3];
+              m4 * (acc[mb][0] * 0.25f) + m2 * (acc[mb][1] * 0.5f) + m1 * acc[mb][2] - m3 * acc[mb][3];
     }
   }
 }
@@ -336,46 +344,60 @@ int launch_dql(const uint8_t *packed, int64_t packed_bytes, const uint16_t *sigm
 }
 
 // ---------------------------------------------------------------------------
-// dequant-GEMM: y[m, r] = sum_i x[m, i] W[r, i] on MFMA for bf16 activations.
+// dequant-GEMM: y[m, r] = sum_i x[m, i] bf16(W[r, i]) on MFMA for bf16 activations.
 //
-// W[r, i] = +-v_|k| (fp16, 11 significant bits) is split exactly into two bf16
-// values, W = hi + lo (hi = bf16_rne(W); lo = W - hi has <= 3 significant
-// bits), so two v_mfma_f32_16x16x32_bf16 per tile give exact products of the
-// bf16 activations with the fp16 weights, accumulated in fp32.
+// The reference evaluates F.linear(x, W.to(x.dtype)) (pollux.py:507): with
+// bf16 activations the fp16 weight is rounded to bf16 (RNE) first.  Every
+// weight of row r is +-v_|k| and RNE is odd, so the row's 8-entry table holds
+// bf16(v_|k|) with the signs; v_mfma_f32_16x16x32_bf16 then forms the same
+// exact products as the reference's bf16 GEMM, accumulated in fp32.
 //
-// Block: 4 waves, 128 output rows (32 per wave = two MFMA B tiles of 16) x
-// 16*MT tokens (MFMA A tiles), over a range of SPB stages of 8 atoms (K = 192)
-// of the row; the grid splits K into `splits` such ranges so that the chip
-// is full, and a second kernel sums the split partials in a fixed order.
-//   prologue: decode the block's 128 x 8*SPB codes from the packed stream and
-//             fetch their kp_dq words (3 per code) into LDS; every lane builds
-//             the 8-entry hi / lo byte tables of its two rows' weight values;
-//   stage s:  the x tile [16*MT tokens][192] bf16 sits in LDS (rows padded to
-//             400 B: conflict-free 16-byte reads); stage s+1's tile is loaded
-//             into registers meanwhile.  Per K step of 32 a lane decodes its
-//             B fragments (8 weights of one row = one plane of one atom) with
-//             v_perm_b32 byte lookups and issues 4*MT MFMAs.
+// Block: WV waves, 32 output rows (two MFMA B tiles of 16) x 16*MT tokens
+// (MFMA A tiles), over `apb` atoms of every row (the whole row when that
+// fills the chip; otherwise the grid splits K into `splits` ranges and
+// dqmm_reduce_kernel sums the split partial tiles in split order).
+//   prologue: decode the block's 32 x apb codes from the packed stream and
+//             fetch their kp_dq words (3 per code) into LDS; 32 lanes build
+//             the 8-entry bf16 byte tables of the block's rows;
+//   k loop:   each wave takes a contiguous share of the block's atoms in
+//             quads of 4 (= 3 K steps of 32) and reads its activation
+//             fragments from a fragment-order copy of x that a small kernel
+//             writes first (L2-resident: every block reads all of it), PD
+//             quads ahead in registers; per K step a
+//             lane decodes its B fragments (8 weights of one row = one plane
+//             of one atom) from one LDS word with v_perm_b32 byte lookups and
+//             issues 2*MT MFMAs.  No block barrier inside the loop.
+//   epilogue: the waves' fp32 tiles are summed through LDS in wave order.
+// xfrag_kernel runs first and writes the fragment-order copy of x into the
+// caller's workspace.
+// Summing the splits inside this kernel instead (the last split block of a row
+// block adds the others' tiles) measured slower both ways it can be made
+// coherent across XCDs: with a device fence (which writes back and
+// invalidates the XCD's whole L2) 3x, with device-scope atomic stores and
+// loads of the tiles 1.35x.
+// One block per 32 rows keeps the decode of every weight in one lane and
+// fills the chip without a K split for wide layers (7680 rows: 240 blocks);
+// the cost is that each block reads all of x from L2.
 // Tokens >= m and columns >= cols are zero-filled (so no NaN from outside the
-// operands can reach a valid output); atoms >= atoms_per_row decode as the
-// origin (weight 0).
+// operands can reach a valid output); atoms >= atoms_per_row and rows >= rows
+// decode as the origin (weight 0).
 // ---------------------------------------------------------------------------
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
-constexpr int kMmRows = 128;              // output rows per block
-constexpr int kMmStageAtoms = 8;          // atoms (of every row) per stage
-constexpr int kMmStageK = kMmStageAtoms * kDim;  // 192
-constexpr int kMmXStride = 400;           // bytes per token row of the LDS x tile (384 + 16 pad)
-constexpr int kMmMaxSpb = 2;              // stages per block (LDS: 55 KB at 64 tokens)
+constexpr int kMmRows = 32;             // output rows per block
+constexpr int kMmMaxApb = 128;          // atoms of a row per block (kp_dq tile: 32 x 388 words = 49.7 KB)
+constexpr int kMmTargetBlocks = 192;    // K is split until the grid holds about this many blocks
+constexpr int kMmRedStride = 36;        // floats per token in the cross-wave sum (conflict-free writes)
+constexpr int kXfQuadBytes = 3 * 4 * 1024;       // fragment-order x: 3 K steps x 4 token tiles x 64 lanes x 16 B
+constexpr int64_t kMmMaxCols = 1 << 23;           // a slab of fragment-order x stays far below 2^31 bytes
+constexpr int kBufferFlags = 0x00020000;          // raw buffer descriptor word 3 on gfx9 (gfx950)
+constexpr int kBufferOutOfRange = 0x7FFFFFF0;     // a byte offset past every buffer range used here
 
-__device__ __forceinline__ uint32_t hi_lo_pack(float v) {
-  // (hi bf16 | lo bf16 << 16) with hi + lo == v exactly for an fp16 value v
-  if (!(fabsf(v) <= 3.0e38f)) return bf16_rne_bits(v);  // inf / nan: carried by hi alone
-  const uint32_t hb = bf16_rne_bits(v);
-  const float lo = v - __uint_as_float(hb << 16);
-  return hb | (bf16_rne_bits(lo) << 16);
-}
+// Words per row of the block's kp_dq tile: 3 per atom, padded to 4 mod 8 so the
+// 16 rows of a B tile read by one instruction fall into distinct banks.
+__host__ __device__ constexpr int mm_row_words(int apb) { return ((3 * apb + 7) & ~7) + 4; }
 
 // 24-bit big-endian window of atom n read as two aligned dwords (bounds-checked
 // at the stream's tail), then the 18-bit index.
@@ -420,55 +442,79 @@ __device__ __forceinline__ void group_codes(uint32_t d0, uint32_t d1, uint32_t d
   c[3] = static_cast<int32_t>(((lo & 0x3FFu) << 8) | b8);
 }
 
-template <int MT, int SPB>  // token tiles of 16; stages of 8 atoms per block
-__global__ __launch_bounds__(256, 2) void dqmm_kernel(const uint8_t *__restrict__ packed, int64_t packed_bytes,
-                                                      const uint16_t *__restrict__ sigma16, int64_t rows,
-                                                      int64_t atoms_per_row, const uint16_t *__restrict__ x,
-                                                      int64_t m_total, int splits,
-                                                      const uint32_t *__restrict__ kp_dq, float *__restrict__ y,
-                                                      float *__restrict__ partial) {
+// Fragment-order copy of the bf16 activations for dqmm_kernel, one 16-byte
+// fragment per thread: xf[slab][Q][s][t][lane] = x[64 slab + 16t + (lane & 15)]
+// [96Q + 32s + 8(lane >> 4) .. +8), zero for tokens >= m and columns >= cols.
+__global__ __launch_bounds__(256) void xfrag_kernel(const uint16_t *__restrict__ x, int64_t m_total, int64_t cols,
+                                                    int64_t n_quads_row, uint4 *__restrict__ xf) {
+  const int64_t per_slab = n_quads_row * (kXfQuadBytes / 16);
+  const int64_t f = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;  // fragment within the slab
+  if (f >= per_slab) return;
+  const int lane = static_cast<int>(f & 63);
+  const int64_t rest = f >> 6;  // (3Q + s) * 4 + t
+  const int t = static_cast<int>(rest & 3);
+  const int64_t tok = static_cast<int64_t>(blockIdx.y) * 64 + 16 * t + (lane & 15);
+  const int64_t col = 32 * (rest >> 2) + 8 * (lane >> 4);
+  uint4 v = make_uint4(0u, 0u, 0u, 0u);
+  if (tok < m_total && col < cols) v = *reinterpret_cast<const uint4 *>(x + tok * cols + col);
+  xf[static_cast<int64_t>(blockIdx.y) * per_slab + f] = v;
+}
+
+template <int MT, int WV, int PD>  // token tiles of 16; waves per block; quads of x in flight per wave
+__global__ __launch_bounds__(64 * WV, WV <= 4 ? 2 : 1) void dqmm_kernel(
+    const uint8_t *__restrict__ packed, int64_t packed_bytes, const uint16_t *__restrict__ sigma16, int64_t rows,
+    int64_t atoms_per_row, const uint4 *__restrict__ xf, int64_t n_quads_row, int64_t m_total, int splits, int apb,
+    const uint32_t *__restrict__ kp_dq, float *__restrict__ y, float *__restrict__ partial) {
   extern __shared__ __align__(16) uint8_t smem[];
+  constexpr int NT = 64 * WV;
   constexpr int TOK = 16 * MT;
-  constexpr int NA = kMmStageAtoms * SPB;     // atoms of every row in this block
-  constexpr int WS = NA * 3 + 4;              // words per row in LDS (16-byte multiple; 16 rows hit 16 banks)
-  uint8_t *xs = smem;                                                        // [TOK][400 B]
-  uint32_t *wt = reinterpret_cast<uint32_t *>(smem + TOK * kMmXStride);      // [128][WS]
-  uint4 *rtab = reinterpret_cast<uint4 *>(wt + kMmRows * WS);               // [128][2] row byte tables
+  const int ws = mm_row_words(apb);
+  const int region = max(kMmRows * ws, WV * TOK * kMmRedStride) * 4;
+  uint32_t *wt = reinterpret_cast<uint32_t *>(smem);          // [32][ws] kp_dq words
+  float *red = reinterpret_cast<float *>(smem);               // after the k loop: [WV][TOK][kMmRedStride]
+  uint4 *rtab = reinterpret_cast<uint4 *>(smem + region);     // [32] row byte tables
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, j = lane & 15, q = lane >> 4;
   const int64_t row_block = blockIdx.x / static_cast<unsigned>(splits);
   const int split = static_cast<int>(blockIdx.x % static_cast<unsigned>(splits));
   const int64_t row0 = row_block * kMmRows;
   const int64_t tok0 = static_cast<int64_t>(blockIdx.y) * 64;
-  const int64_t cols = atoms_per_row * kDim;
-  const int64_t a_begin = static_cast<int64_t>(split) * NA;
-  const int n_stages = static_cast<int>(min(static_cast<int64_t>(SPB), (atoms_per_row - a_begin + kMmStageAtoms - 1) / kMmStageAtoms));
+  const int64_t a_begin = static_cast<int64_t>(split) * apb;
+  const int n_atoms = static_cast<int>(min(static_cast<int64_t>(apb), atoms_per_row - a_begin));  // >= 1
+  const int n_quads = (n_atoms + 3) >> 2;
+  // this wave's quads: a contiguous share of the block's
+  const int qbase = n_quads / WV, qextra = n_quads % WV;
+  const int wq0 = wave * qbase + min(wave, qextra);
+  const int wqn = qbase + (wave < qextra ? 1 : 0);
 
-  // ---- x stage tiles: TOK x 192 bf16 = TOK*24 vectors of 16 B ----
-  constexpr int kVec = TOK * 24;
-  constexpr int kVecPerThread = (kVec + 255) / 256;
-  uint4 xr[kVecPerThread];
-  auto load_x = [&](int st) {
-    const int64_t k0 = (a_begin + static_cast<int64_t>(st) * kMmStageAtoms) * kDim;
+  // ---- activation fragments, from the fragment-order copy of x (xfrag_kernel) ----
+  // Quad Q of the row, K step s, token tile t: 64 lanes x 16 B contiguous, so
+  // one wave load reads 1 KB (8 whole cache lines; read straight from x, the
+  // same fragments touch 16 half lines per load, measured ~30% slower).  Raw
+  // buffer loads over the slab's part: a quad past this wave's share takes an
+  // out-of-range offset, which returns zeros without touching memory, so the
+  // loads need no branches (the compiler can then wait for one quad's loads
+  // while the next quads' stay in flight).
+  const int slab_bytes = static_cast<int>(n_quads_row * kXfQuadBytes);
+  const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint4 *>(xf + static_cast<int64_t>(blockIdx.y) * (slab_bytes / 16)), static_cast<short>(0), slab_bytes,
+      kBufferFlags);
+  const int xbase = static_cast<int>(a_begin / 4 + wq0) * kXfQuadBytes + 16 * lane;
+  auto load_quad = [&](uint4 (&xa)[3][MT], int qd) {
 #pragma unroll
-    for (int u = 0; u < kVecPerThread; ++u) {
-      const int v = u * 256 + tid;
-      const int t = v / 24, kv = v - t * 24;
-      const int64_t tok = tok0 + t, k = k0 + 8 * kv;
-      xr[u] = make_uint4(0u, 0u, 0u, 0u);
-      if (v < kVec && tok < m_total && k < cols) xr[u] = *reinterpret_cast<const uint4 *>(x + tok * cols + k);
+    for (int s = 0; s < 3; ++s) {
+#pragma unroll
+      for (int t = 0; t < MT; ++t) {
+        int off = qd < wqn ? xbase + qd * kXfQuadBytes + (4 * s + t) * 1024 : kBufferOutOfRange;
+        asm("" : "+v"(off));  // one unconditional load (not one per select outcome under branches)
+        xa[s][t] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(xrs, off, 0, 0));
+      }
     }
   };
-  auto store_x = [&]() {
+  uint4 xa[PD][3][MT];
 #pragma unroll
-    for (int u = 0; u < kVecPerThread; ++u) {
-      const int v = u * 256 + tid;
-      const int t = v / 24, kv = v - t * 24;
-      if (v < kVec) *reinterpret_cast<uint4 *>(xs + t * kMmXStride + 16 * kv) = xr[u];
-    }
-  };
-  load_x(0);  // in flight during the whole prologue
+  for (int u = 0; u < PD; ++u) load_quad(xa[u], u);  // in flight during the prologue
 
-  // ---- per-row byte tables (threads 0..127, one row each): hi low/high, lo low/high bytes ----
+  // ---- per-row byte tables (threads 0..31, one row each): bf16 of the fp16 values, low / high bytes ----
   auto build_row_tables = [&]() {
     if (tid >= kMmRows) return;
     const int64_t row = row0 + tid;
@@ -477,50 +523,38 @@ __global__ __launch_bounds__(256, 2) void dqmm_kernel(const uint8_t *__restrict_
     const uint32_t v0 = dq_value(0, sig, sl), v1 = dq_value(1, sig, sl), v2 = dq_value(2, sig, sl);
     const uint32_t v3 = dq_value(3, sig, sl), v4 = dq_value(4, sig, sl);
     const uint32_t h[8] = {v0, v1, v2, v4, v4 ^ 0x8000u, v3 ^ 0x8000u, v2 ^ 0x8000u, v1 ^ 0x8000u};
-    uint32_t hl[8];
+    uint32_t lb0 = 0, lb1 = 0, hb0 = 0, hb1 = 0;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) hl[e] = hi_lo_pack(__half2float(__ushort_as_half(static_cast<uint16_t>(h[e]))));
-    uint32_t t[8];
-#pragma unroll
-    for (int half = 0; half < 2; ++half) {
-      uint32_t lb0 = 0, lb1 = 0, hb0 = 0, hb1 = 0;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const uint32_t b0 = hl[e] >> (16 * half), b1 = hl[e + 4] >> (16 * half);
-        lb0 |= (b0 & 0xFFu) << (8 * e);
-        lb1 |= (b1 & 0xFFu) << (8 * e);
-        hb0 |= ((b0 >> 8) & 0xFFu) << (8 * e);
-        hb1 |= ((b1 >> 8) & 0xFFu) << (8 * e);
-      }
-      t[4 * half + 0] = lb0;
-      t[4 * half + 1] = lb1;
-      t[4 * half + 2] = hb0;
-      t[4 * half + 3] = hb1;
+    for (int e = 0; e < 4; ++e) {
+      const uint32_t b0 = bf16_rne_bits(__half2float(__ushort_as_half(static_cast<uint16_t>(h[e]))));
+      const uint32_t b1 = bf16_rne_bits(__half2float(__ushort_as_half(static_cast<uint16_t>(h[e + 4]))));
+      lb0 |= (b0 & 0xFFu) << (8 * e);
+      lb1 |= (b1 & 0xFFu) << (8 * e);
+      hb0 |= ((b0 >> 8) & 0xFFu) << (8 * e);
+      hb1 |= ((b1 >> 8) & 0xFFu) << (8 * e);
     }
-    rtab[2 * tid] = make_uint4(t[0], t[1], t[2], t[3]);
-    rtab[2 * tid + 1] = make_uint4(t[4], t[5], t[6], t[7]);
+    rtab[tid] = make_uint4(lb0, lb1, hb0, hb1);
   };
 
   // ---- codes -> kp_dq words in LDS ----
   // Rows holding a multiple of 4 atoms: a thread decodes whole 9-byte groups
   // (4 codes from 3 dwords); the row tables are built while those loads are
   // in flight, then all table loads are issued before any LDS store.
-  constexpr int GPR = NA / 4;                               // groups per row in this block
-  constexpr int NG = (kMmRows * GPR + 255) / 256;           // groups per thread
   if ((atoms_per_row & 3) == 0) {
+    constexpr int NG = (kMmRows * kMmMaxApb / 4 + NT - 1) / NT;  // groups per thread at most
+    const int gpr = n_quads;                                     // groups per row in this block
     uint32_t dw[NG][3], off[NG];
     bool live[NG];
 #pragma unroll
     for (int u = 0; u < NG; ++u) {
-      const int g = u * 256 + tid;
-      const int r = g / GPR, k = g - r * GPR;
+      const int g = u * NT + tid;
+      const int r = g / gpr, k = g - r * gpr;
       const int64_t row = row0 + r;
-      const int64_t a = a_begin + 4 * k;
-      live[u] = g < kMmRows * GPR && row < rows && a < atoms_per_row;
+      live[u] = g < kMmRows * gpr && row < rows;
       dw[u][0] = dw[u][1] = dw[u][2] = 0u;
       off[u] = 0;
       if (live[u]) {
-        const int64_t b = (row * atoms_per_row + a) / 4 * 9;
+        const int64_t b = (row * atoms_per_row + a_begin + 4 * k) / 4 * 9;
         const int64_t b4 = b & ~static_cast<int64_t>(3);
         off[u] = static_cast<uint32_t>(b & 3);
         const uint32_t *pw = reinterpret_cast<const uint32_t *>(packed + b4);
@@ -551,20 +585,21 @@ __global__ __launch_bounds__(256, 2) void dqmm_kernel(const uint8_t *__restrict_
     }
 #pragma unroll
     for (int u = 0; u < NG; ++u) {
-      const int g = u * 256 + tid;
-      if (g < kMmRows * GPR) {
-        const int r = g / GPR, k = g - r * GPR;
-        uint4 *d = reinterpret_cast<uint4 *>(wt + r * WS + 12 * k);   // 48 B, 16-byte aligned
-        d[0] = make_uint4(e[u][0].x, e[u][0].y, e[u][0].z, e[u][1].x);
-        d[1] = make_uint4(e[u][1].y, e[u][1].z, e[u][2].x, e[u][2].y);
-        d[2] = make_uint4(e[u][2].z, e[u][3].x, e[u][3].y, e[u][3].z);
+      const int g = u * NT + tid;
+      if (g < kMmRows * gpr) {
+        const int r = g / gpr, k = g - r * gpr;
+        uint32_t *d = wt + r * ws + 12 * k;   // 48 B at a 16-byte multiple (ws % 4 == 0)
+        reinterpret_cast<uint4 *>(d)[0] = make_uint4(e[u][0].x, e[u][0].y, e[u][0].z, e[u][1].x);
+        reinterpret_cast<uint4 *>(d)[1] = make_uint4(e[u][1].y, e[u][1].z, e[u][2].x, e[u][2].y);
+        reinterpret_cast<uint4 *>(d)[2] = make_uint4(e[u][2].z, e[u][3].x, e[u][3].y, e[u][3].z);
       }
     }
   } else {
-    // general rows: one code per (row, atom)
+    // general rows: one code per (row, atom), atoms up to the end of the last quad
     build_row_tables();
-    for (int c = tid; c < kMmRows * NA; c += 256) {
-      const int r = c / NA, a = c - r * NA;
+    const int na = 4 * n_quads;
+    for (int c = tid; c < kMmRows * na; c += NT) {
+      const int r = c / na, a = c - r * na;
       const int64_t row = row0 + r, atom = a_begin + a;
       int32_t code = 0;
       if (row < rows && atom < atoms_per_row) {
@@ -572,68 +607,92 @@ __global__ __launch_bounds__(256, 2) void dqmm_kernel(const uint8_t *__restrict_
         if (code > kKissing) code = 0;
       }
       const uint3 e = *reinterpret_cast<const uint3 *>(kp_dq + static_cast<int64_t>(code) * 3);
-      uint32_t *d = wt + r * WS + 3 * a;
+      uint32_t *d = wt + r * ws + 3 * a;
       d[0] = e.x;
       d[1] = e.y;
       d[2] = e.z;
     }
   }
+  __syncthreads();
 
   f32x4_t acc[MT][2];
 #pragma unroll
   for (int t = 0; t < MT; ++t)
 #pragma unroll
     for (int rt = 0; rt < 2; ++rt) acc[t][rt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-
-  store_x();
-  __syncthreads();
-  const int r0l = 32 * wave + j, r1l = 32 * wave + 16 + j;
-  const uint4 ta0 = rtab[2 * r0l], tb0 = rtab[2 * r0l + 1], ta1 = rtab[2 * r1l], tb1 = rtab[2 * r1l + 1];
-  const uint32_t *wrow0 = wt + r0l * WS;
-  const uint32_t *wrow1 = wt + r1l * WS;
+  const uint4 ta0 = rtab[j], ta1 = rtab[16 + j];
+  // word of (row, block atom a, plane p) = 3a + p; K step s of quad Q, lane group q: 12Q + 4s + q
+  const uint32_t *wrow0 = wt + j * ws + 12 * wq0 + q;
+  const uint32_t *wrow1 = wt + (16 + j) * ws + 12 * wq0 + q;
+  auto compute_quad = [&](const uint4 (&xa_q)[3][MT], int qd) {
 #pragma unroll
-  for (int st = 0; st < SPB; ++st) {
-    if (st >= n_stages) break;
-    if (st + 1 < n_stages) load_x(st + 1);
-#pragma unroll
-    for (int ks = 0; ks < 6; ++ks) {
-      const int kk = 32 * ks + 8 * q;
-      const int a = st * kMmStageAtoms + kk / 24, pl = (kk % 24) / 8;
-      const uint32_t w0 = wrow0[a * 3 + pl], w1 = wrow1[a * 3 + pl];
-      const bf16x8_t bh0 = perm_decode(w0, ta0.x, ta0.y, ta0.z, ta0.w);
-      const bf16x8_t bl0 = perm_decode(w0, tb0.x, tb0.y, tb0.z, tb0.w);
-      const bf16x8_t bh1 = perm_decode(w1, ta1.x, ta1.y, ta1.z, ta1.w);
-      const bf16x8_t bl1 = perm_decode(w1, tb1.x, tb1.y, tb1.z, tb1.w);
+    for (int s = 0; s < 3; ++s) {
+      const uint32_t w0 = wrow0[12 * qd + 4 * s], w1 = wrow1[12 * qd + 4 * s];
+      const bf16x8_t b0 = perm_decode(w0, ta0.x, ta0.y, ta0.z, ta0.w);
+      const bf16x8_t b1 = perm_decode(w1, ta1.x, ta1.y, ta1.z, ta1.w);
 #pragma unroll
       for (int t = 0; t < MT; ++t) {
-        const bf16x8_t av = *reinterpret_cast<const bf16x8_t *>(xs + (16 * t + j) * kMmXStride + 2 * kk);
-        acc[t][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bh0, acc[t][0], 0, 0, 0);
-        acc[t][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bh1, acc[t][1], 0, 0, 0);
-        acc[t][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bl0, acc[t][0], 0, 0, 0);
-        acc[t][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bl1, acc[t][1], 0, 0, 0);
+        const bf16x8_t av = __builtin_bit_cast(bf16x8_t, xa_q[s][t]);
+        acc[t][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, b0, acc[t][0], 0, 0, 0);
+        acc[t][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, b1, acc[t][1], 0, 0, 0);
       }
     }
-    if (st + 1 < n_stages) {
-      __syncthreads();
-      store_x();
-      __syncthreads();
+    // keep the fragments in their registers until the slot is refilled, so no
+    // MFMA result is allocated there (that made the loop wait for every load)
+#pragma unroll
+    for (int s = 0; s < 3; ++s)
+#pragma unroll
+      for (int t = 0; t < MT; ++t) asm volatile("" : : "v"(__builtin_bit_cast(u32x4_t, xa_q[s][t])));
+  };
+  // Whole rounds of PD quads without branches, then the last < PD quads.  The
+  // first round is peeled: the loop header then sees the same loads in flight
+  // (PD slots, oldest first) from both of its predecessors, so the compiler
+  // waits for one slot at a time instead of for every load.
+  auto round = [&](int q0) {
+#pragma unroll
+    for (int u = 0; u < PD; ++u) {
+      compute_quad(xa[u], q0 + u);
+      __builtin_amdgcn_sched_barrier(0);  // slot u is refilled right after its MFMAs, not at the round's end
+      load_quad(xa[u], q0 + u + PD);
+      __builtin_amdgcn_sched_barrier(0);
     }
+  };
+  int qd = 0;
+  if (PD <= wqn) {
+    round(0);
+    for (qd = PD; qd + PD <= wqn; qd += PD) round(qd);
   }
+#pragma unroll
+  for (int u = 0; u < PD - 1; ++u)
+    if (qd + u < wqn) compute_quad(xa[u], qd + u);
 
-  // ---- epilogue: C[token 16t + 4q + e][row 32*wave + 16rt + j] ----
-  float *dst = splits == 1 ? y : partial + (static_cast<int64_t>(blockIdx.y) * splits + split) * 64 * rows;
-  const int64_t tok_base = splits == 1 ? tok0 : 0;   // partial tiles are indexed per slab
+  // ---- epilogue: the waves' tiles summed in wave order; C[token 16t + 4q + e][row 16rt + j] ----
+  __syncthreads();  // every wave is done with the kp_dq tile
+  float *rw = red + wave * (TOK * kMmRedStride);
 #pragma unroll
   for (int t = 0; t < MT; ++t)
 #pragma unroll
-    for (int rt = 0; rt < 2; ++rt) {
-      const int64_t row = row0 + 32 * wave + 16 * rt + j;
+    for (int rt = 0; rt < 2; ++rt)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int64_t tl = 16 * t + 4 * q + e;
-        if (row < rows && tok0 + tl < m_total) dst[(tok_base + tl) * rows + row] = acc[t][rt][e];
-      }
+      for (int e = 0; e < 4; ++e) rw[(16 * t + 4 * q + e) * kMmRedStride + 16 * rt + j] = acc[t][rt][e];
+  __syncthreads();
+  float *dst = splits == 1 ? y : partial + (static_cast<int64_t>(blockIdx.y) * splits + split) * 64 * rows;
+  const int64_t tok_base = splits == 1 ? tok0 : 0;  // partial tiles are indexed per slab
+  const bool vec = (rows & 3) == 0 && (reinterpret_cast<uintptr_t>(dst) & 15u) == 0;
+  for (int i = tid; i < TOK * (kMmRows / 4); i += NT) {
+    const int tl = i / (kMmRows / 4), g = i - tl * (kMmRows / 4);
+    f32x4_t sum = *reinterpret_cast<const f32x4_t *>(red + tl * kMmRedStride + 4 * g);
+#pragma unroll
+    for (int w = 1; w < WV; ++w) sum += *reinterpret_cast<const f32x4_t *>(red + (w * TOK + tl) * kMmRedStride + 4 * g);
+    const int64_t row = row0 + 4 * g;
+    if (tok0 + tl >= m_total || row >= rows) continue;
+    float *d = dst + (tok_base + tl) * rows + row;
+    if (vec) {
+      *reinterpret_cast<f32x4_t *>(d) = sum;
+    } else {
+      for (int c = 0; c < 4 && row + c < rows; ++c) d[c] = sum[c];
     }
+  }
 }
 
 // y[tok, r] = sum over splits (ascending) of the partial tiles; 4 outputs per
@@ -665,46 +724,60 @@ __global__ __launch_bounds__(256) void dqmm_reduce_kernel(const float *__restric
 }
 
 struct MmPlan {
-  int spb = 1, splits = 1;
+  int apb = 4, splits = 1;
 };
 
-// Stages per block and K splits: 2 stages per block, or 1 when that leaves
-// fewer than 256 blocks.
+// Atoms per block (a multiple of 4, at most kMmMaxApb) and K splits: the fewest
+// splits that keep the block's atoms within kMmMaxApb and give the grid about
+// kMmTargetBlocks blocks.
 MmPlan mm_plan(int64_t rows, int64_t apr) {
   MmPlan p;
-  const int64_t stages = (apr + kMmStageAtoms - 1) / kMmStageAtoms;
   const int64_t row_blocks = (rows + kMmRows - 1) / kMmRows;
-  int64_t spb = 2;
-  if (row_blocks * ((stages + 1) / 2) < 256) spb = 1;
-  if (spb > stages) spb = stages;
-  if (spb < 1) spb = 1;
-  p.spb = static_cast<int>(spb);
-  p.splits = static_cast<int>((stages + spb - 1) / spb);
-  if (p.splits < 1) p.splits = 1;
+  int64_t s = max((apr + kMmMaxApb - 1) / kMmMaxApb, (kMmTargetBlocks + row_blocks - 1) / row_blocks);
+  s = max(static_cast<int64_t>(1), min(s, (apr + 3) / 4));
+  const int64_t apb = (((apr + s - 1) / s) + 3) & ~static_cast<int64_t>(3);
+  p.apb = static_cast<int>(apb);
+  p.splits = static_cast<int>((apr + apb - 1) / apb);
   return p;
 }
 
-template <int MT, int SPB>
+template <int MT, int WV, int PD>
 int launch_dqmm_t(const uint8_t *packed, int64_t pb, const uint16_t *sigma16, int64_t rows, int64_t apr,
-                  const uint16_t *x, int64_t m, float *y, float *partial, int splits, const uint32_t *kp_dq,
+                  const uint4 *xf, int64_t m, float *y, float *partial, const MmPlan &pl, const uint32_t *kp_dq,
                   hipStream_t s) {
   const int64_t row_blocks = (rows + kMmRows - 1) / kMmRows;
   const int64_t slabs = (m + 63) / 64;
-  constexpr int WS = kMmStageAtoms * SPB * 3 + 4;
-  const size_t shm = static_cast<size_t>(16 * MT) * kMmXStride + static_cast<size_t>(kMmRows) * WS * 4 +
-                     static_cast<size_t>(kMmRows) * 32;
-  const dim3 g(static_cast<unsigned>(row_blocks * splits), static_cast<unsigned>(slabs));
-  hipLaunchKernelGGL((dqmm_kernel<MT, SPB>), g, dim3(256), shm, s, packed, pb, sigma16, rows, apr, x, m, splits, kp_dq,
-                     y, partial);
+  const int64_t nq = (apr + 3) / 4;
+  const size_t region = static_cast<size_t>(max(kMmRows * mm_row_words(pl.apb), WV * 16 * MT * kMmRedStride)) * 4;
+  const size_t shm = region + static_cast<size_t>(kMmRows) * 16;
+  const dim3 g(static_cast<unsigned>(row_blocks * pl.splits), static_cast<unsigned>(slabs));
+  hipLaunchKernelGGL((dqmm_kernel<MT, WV, PD>), g, dim3(64 * WV), shm, s, packed, pb, sigma16, rows, apr, xf, nq, m,
+                     pl.splits, pl.apb, kp_dq, y, partial);
   return check_launch("dqmm_kernel");
 }
 
 template <int MT>
 int launch_dqmm(const uint8_t *packed, int64_t pb, const uint16_t *sigma16, int64_t rows, int64_t apr,
-                const uint16_t *x, int64_t m, float *y, float *partial, const MmPlan &pl, const uint32_t *kp_dq,
+                const uint4 *xf, int64_t m, float *y, float *partial, const MmPlan &pl, const uint32_t *kp_dq,
                 hipStream_t s) {
-  if (pl.spb == 1) return launch_dqmm_t<MT, 1>(packed, pb, sigma16, rows, apr, x, m, y, partial, pl.splits, kp_dq, s);
-  return launch_dqmm_t<MT, 2>(packed, pb, sigma16, rows, apr, x, m, y, partial, pl.splits, kp_dq, s);
+  // 8 waves (two per SIMD cover each other's load latency), one quad of x in
+  // flight per wave; 4 waves with 2 quads in flight measured within 3%
+  return launch_dqmm_t<MT, 8, 1>(packed, pb, sigma16, rows, apr, xf, m, y, partial, pl, kp_dq, s);
+}
+
+// Workspace of the batched path: the fragment-order x copy (a multiple of 256
+// bytes), then, with a K split, the split partial tiles [slab][split][64][rows] fp32.
+struct MmWorkspace {
+  size_t xf = 0, partial = 0;
+  size_t total() const { return xf + partial; }
+};
+
+MmWorkspace mm_workspace(int64_t rows, int64_t cols, int64_t m, const MmPlan &pl) {
+  MmWorkspace w;
+  const size_t slabs = static_cast<size_t>((m + 63) / 64);
+  w.xf = slabs * static_cast<size_t>((cols / kDim + 3) / 4) * kXfQuadBytes;
+  if (pl.splits > 1) w.partial = slabs * pl.splits * 64 * static_cast<size_t>(rows) * sizeof(float);
+  return w;
 }
 
 bool uses_mfma(int x_is_f32, int64_t m) { return !x_is_f32 && m > 16; }
@@ -712,10 +785,8 @@ bool uses_mfma(int x_is_f32, int64_t m) { return !x_is_f32 && m > 16; }
 }  // namespace
 
 size_t dequant_linear_workspace_bytes(int64_t rows, int64_t cols, int64_t m, int x_is_f32) {
-  if (!uses_mfma(x_is_f32, m) || rows <= 0) return 0;
-  const MmPlan pl = mm_plan(rows, cols / kDim);
-  if (pl.splits == 1) return 0;
-  return static_cast<size_t>((m + 63) / 64) * pl.splits * 64 * static_cast<size_t>(rows) * sizeof(float);
+  if (!uses_mfma(x_is_f32, m) || rows <= 0 || cols <= 0) return 0;
+  return mm_workspace(rows, cols, m, mm_plan(rows, cols / kDim)).total();
 }
 
 int launch_dequant_linear(const uint8_t *packed, const uint16_t *sigma16, int64_t rows, int64_t cols, const void *x,
@@ -734,12 +805,21 @@ int launch_dequant_linear(const uint8_t *packed, const uint16_t *sigma16, int64_
   const int64_t pb = ((rows * apr + 3) / 4) * 9;  // packed stream length
   if (uses_mfma(x_is_f32, m)) {
     // bf16 batches above 16 tokens: MFMA dequant-GEMM in slabs of 64 tokens
+    if (cols > kMmMaxCols)
+      return fail(PLX_EINVAL, "dequant_linear: %lld columns exceed the batched path's %lld", static_cast<long long>(cols),
+                  static_cast<long long>(kMmMaxCols));
     const MmPlan pl = mm_plan(rows, apr);
-    const uint16_t *xb = static_cast<const uint16_t *>(x);
-    float *part = static_cast<float *>(workspace);
-    const int mt = m >= 64 ? 4 : m > 32 ? 4 : 2;
-    st = mt == 4 ? launch_dqmm<4>(packed, pb, sigma16, rows, apr, xb, m, y, part, pl, tab->kp_dq, s)
-                 : launch_dqmm<2>(packed, pb, sigma16, rows, apr, xb, m, y, part, pl, tab->kp_dq, s);
+    const MmWorkspace w = mm_workspace(rows, cols, m, pl);
+    uint8_t *wsb = static_cast<uint8_t *>(workspace);
+    uint4 *xf = reinterpret_cast<uint4 *>(wsb);
+    float *part = reinterpret_cast<float *>(wsb + w.xf);
+    const int64_t slabs = (m + 63) / 64, nq = (apr + 3) / 4;
+    hipLaunchKernelGGL(xfrag_kernel, dim3(static_cast<unsigned>(nq * 3), static_cast<unsigned>(slabs)), dim3(256), 0, s,
+                       static_cast<const uint16_t *>(x), m, cols, nq, xf);
+    st = check_launch("xfrag_kernel");
+    if (st != PLX_OK) return st;
+    st = m > 32 ? launch_dqmm<4>(packed, pb, sigma16, rows, apr, xf, m, y, part, pl, tab->kp_dq, s)
+                : launch_dqmm<2>(packed, pb, sigma16, rows, apr, xf, m, y, part, pl, tab->kp_dq, s);
     if (st != PLX_OK || pl.splits == 1) return st;
     const int64_t n = m * rows;
     if (rows % 4 == 0 && (reinterpret_cast<uintptr_t>(y) & 15u) == 0)

@@ -43,8 +43,11 @@ def dequantize_h24(packed: torch.Tensor, sigma16: torch.Tensor, out_features: in
 def dequant_linear(
     packed: torch.Tensor, sigma16: torch.Tensor, out_features: int, in_features: int, x: torch.Tensor
 ) -> torch.Tensor:
-    """F.linear(x, materialize(W).float()) in fp32 without materialising W (pollux.py:491-507).
+    """F.linear(x, materialize(W).to(x.dtype)) in fp32 without materialising W (pollux.py:491-507).
 
+    As in the reference, the fp16 weight is cast to x's dtype: bf16 activations
+    multiply bf16-rounded weights, fp32 activations the exact fp16 values; the
+    products are exact and accumulated in fp32.
     x: [..., in] bf16 or fp32 (other float dtypes are cast to fp32); returns fp32 [..., out].
     """
     _lib.require_device(packed, "dequant_linear packed input")

@@ -1,11 +1,16 @@
-"""Fused dequant-linear (PackedH24Linear.forward, pollux.py:485-507) against the reference's fp32 F.linear.
+"""Fused dequant-linear (PackedH24Linear.forward, pollux.py:485-507) against the reference's F.linear.
 
 packed [7680, 1920] and [1920, 7680] (torch (out, in) layout),
 indices uniform over 0..196560, sigma16 ~ U(0.005, 0.05), bf16 activations
 N(0, 1) at batch 1 (GEMV) and 64 (GEMM), fp32 accumulation.
-Tolerance (stated): relative L2 error <= 1e-5 against F.linear(x.float(),
-W16.float()), and per element |dy| <= 1e-5 * sum_i |x_i W_i| (the products are
-exact in fp32; only the summation order differs).
+The reference computes F.linear(x, W16.to(x.dtype)) (pollux.py:507): with bf16
+activations the fp16 weight is rounded to bf16 first.  The expected value is
+that expression evaluated in fp32 (oracle.torch_ref.linear_as_reference).
+Tolerance (stated): relative L2 error <= 1e-5, and per element |dy| <= 1e-5 *
+sum_i |x_i W_i| (the products are exact in fp32; only the summation order
+differs).  For bf16 activations the test also checks that the result is far
+(> 1e-4 relative) from the product with the unrounded fp16 weight, so it tells
+the reference's rounding from its absence.
 """
 
 import pytest
@@ -30,14 +35,19 @@ def _layer(out_f, in_f, seed):
 
 
 def _check(y, x, w16):
-    ref = torch_ref.linear_fp32(x, w16)
+    """y against F.linear(x, w16.to(x.dtype)) evaluated in fp32 (x in its own dtype)."""
+    ref = torch_ref.linear_as_reference(x, w16)
+    w = w16.to(x.dtype).double()
     err = (y.double() - ref.double())
     rel = err.norm() / ref.double().norm()
-    bound = ELEM * (x.double().abs() @ w16.double().abs().t())
+    bound = ELEM * (x.double().abs() @ w.abs().t())
     worst = (err.abs() / bound).max().item()
     print(f"[dql] rel_l2 {rel:.3e} worst elem/bound {worst:.3f}", flush=True)
     assert rel <= REL_L2
     assert worst <= 1.0
+    if x.dtype == torch.bfloat16:
+        exact16 = torch_ref.linear_fp32(x, w16).double()
+        assert (y.double() - exact16).norm() / exact16.norm() > 1e-4  # the bf16 rounding of W is applied
 
 
 @pytest.mark.parametrize("shape", [(7680, 1920), (1920, 7680)])
@@ -49,17 +59,32 @@ def test_config5_bf16_activations(dev, shape, m):
     w16 = torch_ref.materialize(idx, sig, out_f, in_f)
     y = dequant_linear(packed.to(dev), sig.to(dev), out_f, in_f, x.to(dev)).cpu()
     assert y.dtype == torch.float32 and y.shape == (m, out_f)
-    _check(y, x.float(), w16)
+    _check(y, x, w16)
 
 
-@pytest.mark.parametrize("shape,m", [((1152, 1152), 17), ((37, 1920), 33), ((4608, 1152), 100), ((20, 240), 64)])
+# cases: K split with partials (1152 x 1152), 2-tile token slab (m <= 32), rows % 4 != 0 (37),
+# two token slabs (m = 100), rows of a non-multiple of 4 atoms in one block (1176 = 49 atoms)
+# and over several blocks (240 = 10 atoms), one atom per row (24)
+@pytest.mark.parametrize("shape,m", [((1152, 1152), 17), ((37, 1920), 33), ((4608, 1152), 100), ((20, 240), 64),
+                                     ((64, 1176), 40), ((130, 24), 20)])
 def test_mfma_gemm_batches_bf16(dev, shape, m):
     out_f, in_f = shape
     idx, sig, packed, g = _layer(out_f, in_f, 3 * out_f + m)
     x = (torch.randn(m, in_f, generator=g) * 2.0).to(torch.bfloat16)
     w16 = torch_ref.materialize(idx, sig, out_f, in_f)
     y = dequant_linear(packed.to(dev), sig.to(dev), out_f, in_f, x.to(dev)).cpu()
-    _check(y, x.float(), w16)
+    _check(y, x, w16)
+
+
+@pytest.mark.parametrize("shape,m", [((1152, 1152), 7), ((37, 48), 2), ((100, 4608), 16)])
+def test_gemv_bf16_small_batches(dev, shape, m):
+    # batches of up to 16 tokens take the GEMV kernel, which rounds the magnitudes to bf16
+    out_f, in_f = shape
+    idx, sig, packed, g = _layer(out_f, in_f, 5 * out_f + m)
+    x = torch.randn(m, in_f, generator=g).to(torch.bfloat16)
+    w16 = torch_ref.materialize(idx, sig, out_f, in_f)
+    y = dequant_linear(packed.to(dev), sig.to(dev), out_f, in_f, x.to(dev)).cpu()
+    _check(y, x, w16)
 
 
 @pytest.mark.parametrize("shape,m", [((37, 48), 3), ((1152, 1152), 5), ((100, 4608), 2), ((24, 24), 1)])
