@@ -157,18 +157,18 @@ def gemv_extras(device, copies=200, m_gemm=64, replays=5):
         nbytes = (n_atoms + 3) // 4 * 9
         pk = torch.randint(0, 256, (copies, nbytes), generator=g, device=device, dtype=torch.uint8)
         sg = (torch.rand(copies, of, generator=g, device=device) * 0.045 + 0.005).half()
-        for m in (1, m_gemm):
+        for m, mode in ((1, "exact"), (m_gemm, "exact"), (m_gemm, "as_x")):
             x = torch.randn(m, inf, generator=g, device=device).to(torch.bfloat16)
-            eager = [dequant_linear(pk[i], sg[i], of, inf, x) for i in (0, copies - 1)]
+            eager = [dequant_linear(pk[i], sg[i], of, inf, x, weight_rounding=mode) for i in (0, copies - 1)]
             side = torch.cuda.Stream(device)
             side.wait_stream(torch.cuda.current_stream(device))
             with torch.cuda.stream(side):
                 for i in range(3):
-                    dequant_linear(pk[i], sg[i], of, inf, x)
+                    dequant_linear(pk[i], sg[i], of, inf, x, weight_rounding=mode)
             torch.cuda.current_stream(device).wait_stream(side)
             graph = torch.cuda.CUDAGraph()
             with torch.cuda.graph(graph):
-                ys = [dequant_linear(pk[i], sg[i], of, inf, x) for i in range(copies)]
+                ys = [dequant_linear(pk[i], sg[i], of, inf, x, weight_rounding=mode) for i in range(copies)]
             graph.replay()
             torch.cuda.synchronize()
             if not (torch.equal(ys[0], eager[0]) and torch.equal(ys[-1], eager[1])):
@@ -182,13 +182,15 @@ def gemv_extras(device, copies=200, m_gemm=64, replays=5):
             t = e0.elapsed_time(e1) / 1e3 / (replays * copies)
             del graph, ys
             comp = nbytes + 2 * of + 2 * m * inf + 4 * m * of
-            key = f"{name}_M{m}"
+            key = f"{name}_M{m}" + ("" if mode == "exact" else f"_{mode}")
             out[f"{key}_us"] = t * 1e6
             out[f"{key}_compressed_GBps"] = comp / t / 1e9
             out[f"{key}_dense_equiv_GBps"] = (2 * of * inf) / t / 1e9
             out[f"{key}_TFLOPs"] = 2 * m * of * inf / t / 1e12
     out["note"] = (f"HIP graph of {copies} calls on distinct packed copies ({copies} x 1.38 MB), replayed {replays}x; "
-                   "compressed bytes = packed + sigma16 + x bf16 + y fp32; dense-equivalent = fp16 weight bytes")
+                   "compressed bytes = packed + sigma16 + x bf16 + y fp32; dense-equivalent = fp16 weight bytes; "
+                   "default: exact products with the fp16 weights; _as_x: weights rounded to bf16 first, as the "
+                   "reference's literal F.linear(x, W.to(x.dtype))")
     return out
 
 

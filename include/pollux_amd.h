@@ -189,22 +189,28 @@ int plx_pollux_step_h24(const float *grad, float *m, float *v, float *latent, in
 int plx_dequant_f16(const uint8_t *packed, int64_t n_packed_bytes, const uint16_t *sigma16,
                     int64_t rows, int64_t cols, uint16_t *w16_out, void *stream);
 
+/* plx_dequant_linear flags (0 = bf16 activations, exact fp16 weights) */
+#define PLX_DQL_X_F32 1  /* x is fp32 (else bf16) */
+#define PLX_DQL_W_AS_X 2 /* bf16 x: round W to bf16 first, as the reference's literal
+                            F.linear(x, W.to(x.dtype)) does (pollux.py:507) */
+
 /* Workspace (device bytes, 16-byte aligned) plx_dequant_linear needs for
- * this shape, batch and activation type (0 when none). */
-size_t plx_dequant_linear_workspace_bytes(int64_t rows, int64_t cols, int64_t m_rows, int x_is_f32);
+ * this shape, batch and flags (0 when none). */
+size_t plx_dequant_linear_workspace_bytes(int64_t rows, int64_t cols, int64_t m_rows, int flags);
 
 /* y[m, r] = sum_i x[m, i] * W[r, i] for m < m_rows, with W the fp16
- * materialisation of (packed, sigma16) above cast to x's dtype as the reference
- * does, never stored: x is bf16 (x_is_f32 = 0; W is rounded to bf16, RNE) or
- * fp32 (x_is_f32 = 1; W exact) [m_rows, cols], y fp32 [m_rows, rows], exact
- * products with fp32 accumulation; results are deterministic (fixed summation
+ * materialisation of (packed, sigma16) above, never stored: x is bf16 or fp32
+ * (PLX_DQL_X_F32) [m_rows, cols], y fp32 [m_rows, rows].  The products with
+ * the fp16 weights are exact and accumulated in fp32: the numerics of
+ * F.linear(x.float(), W.float()).  With PLX_DQL_W_AS_X and bf16 x the weights
+ * are rounded to bf16 (RNE) first.  Results are deterministic (fixed summation
  * order).  bf16 batches above 16 tokens need the workspace sized by
  * plx_dequant_linear_workspace_bytes (a fragment-order copy of x, plus split
  * partial tiles for narrow layers); cols <= 2^23.
  * Replaces PackedH24Linear.forward after materialize (pollux.py:506-507:
- * F.linear(x, weight.to(x.dtype))), evaluated in fp32. */
+ * F.linear(x, weight.to(x.dtype))). */
 int plx_dequant_linear(const uint8_t *packed, int64_t n_packed_bytes, const uint16_t *sigma16,
-                       int64_t rows, int64_t cols, const void *x, int x_is_f32, int64_t m_rows,
+                       int64_t rows, int64_t cols, const void *x, int flags, int64_t m_rows,
                        float *y, void *workspace, size_t workspace_bytes, void *stream);
 
 /* ---- per-row INT8 periphery (embeddings / LM head in .plx files) ------- */

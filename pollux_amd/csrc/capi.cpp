@@ -243,24 +243,25 @@ int plx_dequant_f16(const uint8_t *packed, int64_t n_packed_bytes, const uint16_
   return launch_dequant_f16(packed, sigma16, rows, cols, w16_out, as_stream(stream));
 }
 
-size_t plx_dequant_linear_workspace_bytes(int64_t rows, int64_t cols, int64_t m_rows, int x_is_f32) {
+size_t plx_dequant_linear_workspace_bytes(int64_t rows, int64_t cols, int64_t m_rows, int flags) {
   if (rows <= 0 || cols <= 0 || cols % kDim != 0 || m_rows <= 0) return 0;
-  return dequant_linear_workspace_bytes(rows, cols, m_rows, x_is_f32);
+  return dequant_linear_workspace_bytes(rows, cols, m_rows, flags);
 }
 
 int plx_dequant_linear(const uint8_t *packed, int64_t n_packed_bytes, const uint16_t *sigma16, int64_t rows,
-                       int64_t cols, const void *x, int x_is_f32, int64_t m_rows, float *y, void *workspace,
+                       int64_t cols, const void *x, int flags, int64_t m_rows, float *y, void *workspace,
                        size_t workspace_bytes, void *stream) {
   PLX_REQUIRE(rows >= 0 && cols > 0 && cols % kDim == 0, "plx_dequant_linear: bad shape (%lld, %lld)",
               static_cast<long long>(rows), static_cast<long long>(cols));
   PLX_REQUIRE(m_rows >= 0, "plx_dequant_linear: negative batch");
+  PLX_REQUIRE((flags & ~(PLX_DQL_X_F32 | PLX_DQL_W_AS_X)) == 0, "plx_dequant_linear: unknown flags 0x%x", flags);
   const int64_t n_atoms = rows * (cols / kDim);
   PLX_REQUIRE(n_packed_bytes == ((n_atoms + 3) / 4) * 9,
               "plx_dequant_linear: packed length %lld does not match %lld atoms", static_cast<long long>(n_packed_bytes),
               static_cast<long long>(n_atoms));
   if (rows == 0 || m_rows == 0) return PLX_OK;
   PLX_REQUIRE(packed != nullptr && sigma16 != nullptr && x != nullptr && y != nullptr, "plx_dequant_linear: null pointer");
-  return launch_dequant_linear(packed, sigma16, rows, cols, x, x_is_f32, m_rows, y, workspace, workspace_bytes,
+  return launch_dequant_linear(packed, sigma16, rows, cols, x, flags, m_rows, y, workspace, workspace_bytes,
                                as_stream(stream));
 }
 

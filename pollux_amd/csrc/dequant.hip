@@ -136,10 +136,11 @@ namespace {
 //   type 3 (+-1, one -3 at coordinate p) v1 * (D + 3 x_p) - v3 * x_p
 //   origin                              0
 // The row keeps four fp32 partial sums and applies the magnitudes once at the
-// end: the same products as the reference's F.linear(x, W.to(x.dtype))
-// (pollux.py:507), regrouped (fp32 rounding differs at the 1e-7 relative
-// level).  W.to(x.dtype) is the fp16 value for fp32 activations and its bf16
-// RNE rounding for bf16 activations, so the magnitudes are rounded likewise.
+// end: the same products as F.linear(x.float(), W.float()), regrouped (fp32
+// rounding differs at the 1e-7 relative level).  With `round_w` (bf16 x and
+// PLX_DQL_W_AS_X) the magnitudes are first rounded to bf16 (RNE, an odd
+// function, so the signed weights follow): the products of the reference's
+// literal F.linear(x, W.to(x.dtype)) (pollux.py:507).
 //
 // Per code the kernel reads one 16-byte entry of kp_gemv (24 signed 4-bit
 // coordinates + type/position byte; 3.1 MB, L2-resident per XCD).
@@ -186,7 +187,7 @@ __global__ __launch_bounds__(256) void dqlinear_kernel(const uint8_t *__restrict
                                                        const uint16_t *__restrict__ sigma16, int64_t rows,
                                                        int64_t atoms_per_row, const void *__restrict__ x,
                                                        int64_t m_total, float *__restrict__ y,
-                                                       const uint4 *__restrict__ kp_gemv) {
+                                                       const uint4 *__restrict__ kp_gemv, int round_w) {
   extern __shared__ __align__(16) uint8_t smem[];
   constexpr int R = 256 / L;
   const int64_t cols = atoms_per_row * kDim;
@@ -301,12 +302,10 @@ __global__ __launch_bounds__(256) void dqlinear_kernel(const uint8_t *__restrict
       const float v2 = __half2float(__ushort_as_half(static_cast<uint16_t>(dq_value(2, sig, sl))));
       const float v3 = __half2float(__ushort_as_half(static_cast<uint16_t>(dq_value(3, sig, sl))));
       const float v4 = __half2float(__ushort_as_half(static_cast<uint16_t>(dq_value(4, sig, sl))));
-      // bf16 activations: the reference multiplies by W.to(bf16) (pollux.py:507), an RNE
-      // rounding of each magnitude (RNE is odd, so the signed weights follow)
-      const float m1 = XF32 ? v1 : bf16_bits_to_float(bf16_rne_bits(v1));
-      const float m2 = XF32 ? v2 : bf16_bits_to_float(bf16_rne_bits(v2));
-      const float m3 = XF32 ? v3 : bf16_bits_to_float(bf16_rne_bits(v3));
-      const float m4 = XF32 ? v4 : bf16_bits_to_float(bf16_rne_bits(v4));
+      const float m1 = round_w ? bf16_bits_to_float(bf16_rne_bits(v1)) : v1;
+      const float m2 = round_w ? bf16_bits_to_float(bf16_rne_bits(v2)) : v2;
+      const float m3 = round_w ? bf16_bits_to_float(bf16_rne_bits(v3)) : v3;
+      const float m4 = round_w ? bf16_bits_to_float(bf16_rne_bits(v4)) : v4;
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb)
         if (mb < mb_here)
@@ -318,7 +317,7 @@ __global__ __launch_bounds__(256) void dqlinear_kernel(const uint8_t *__restrict
 
 template <int L, bool XF32>
 int launch_dql(const uint8_t *packed, int64_t packed_bytes, const uint16_t *sigma16, int64_t rows, int64_t apr,
-               const void *x, int64_t m, float *y, const uint4 *tab, hipStream_t s) {
+               const void *x, int64_t m, float *y, const uint4 *tab, int round_w, hipStream_t s) {
   constexpr int R = 256 / L;
   const dim3 g(static_cast<unsigned>((rows + R - 1) / R));
   const size_t pbytes = static_cast<size_t>((R * apr + 8) / 4 + 2) * 9;
@@ -331,7 +330,7 @@ int launch_dql(const uint8_t *packed, int64_t packed_bytes, const uint16_t *sigm
   if (shm > 64 * 1024) return fail(PLX_EINVAL, "dequant_linear: rows of %lld atoms are too long", static_cast<long long>(apr));
 #define PLX_DQL(MB, XL) \
   hipLaunchKernelGGL((dqlinear_kernel<L, MB, XF32, XL>), g, dim3(256), shm, s, packed, packed_bytes, sigma16, rows, apr, \
-                     x, m, y, tab)
+                     x, m, y, tab, round_w)
   if (mb == 4) {
     if (xl) PLX_DQL(4, true); else PLX_DQL(4, false);
   } else if (mb == 2) {
@@ -344,13 +343,16 @@ int launch_dql(const uint8_t *packed, int64_t packed_bytes, const uint16_t *sigm
 }
 
 // ---------------------------------------------------------------------------
-// dequant-GEMM: y[m, r] = sum_i x[m, i] bf16(W[r, i]) on MFMA for bf16 activations.
+// dequant-GEMM: y[m, r] = sum_i x[m, i] W[r, i] on MFMA for bf16 activations.
 //
-// The reference evaluates F.linear(x, W.to(x.dtype)) (pollux.py:507): with
-// bf16 activations the fp16 weight is rounded to bf16 (RNE) first.  Every
-// weight of row r is +-v_|k| and RNE is odd, so the row's 8-entry table holds
-// bf16(v_|k|) with the signs; v_mfma_f32_16x16x32_bf16 then forms the same
-// exact products as the reference's bf16 GEMM, accumulated in fp32.
+// EXACT (the default): W[r, i] = +-v_|k| (fp16, 11 significant bits) is split
+// exactly into two bf16 values, W = hi + lo (hi = bf16_rne(W); lo = W - hi has
+// <= 3 significant bits), so two v_mfma_f32_16x16x32_bf16 per tile give exact
+// products of the bf16 activations with the fp16 weights, accumulated in fp32:
+// the numerics of F.linear(x.float(), W.float()).  Without EXACT only hi is
+// used: the products of the reference's literal F.linear(x, W.to(x.dtype))
+// (pollux.py:507), which rounds the fp16 weight to bf16 first (RNE is odd, so
+// the row's 8-entry table of signed values holds bf16(+-v_|k|)).
 //
 // Block: WV waves, 32 output rows (two MFMA B tiles of 16) x 16*MT tokens
 // (MFMA A tiles), over `apb` atoms of every row (the whole row when that
@@ -358,7 +360,8 @@ int launch_dql(const uint8_t *packed, int64_t packed_bytes, const uint16_t *sigm
 // dqmm_reduce_kernel sums the split partial tiles in split order).
 //   prologue: decode the block's 32 x apb codes from the packed stream and
 //             fetch their kp_dq words (3 per code) into LDS; 32 lanes build
-//             the 8-entry bf16 byte tables of the block's rows;
+//             the 8-entry bf16 byte tables (hi, and lo when EXACT) of the
+//             block's rows;
 //   k loop:   each wave takes a contiguous share of the block's atoms in
 //             quads of 4 (= 3 K steps of 32) and reads its activation
 //             fragments from a fragment-order copy of x that a small kernel
@@ -366,7 +369,8 @@ int launch_dql(const uint8_t *packed, int64_t packed_bytes, const uint16_t *sigm
 //             quads ahead in registers; per K step a
 //             lane decodes its B fragments (8 weights of one row = one plane
 //             of one atom) from one LDS word with v_perm_b32 byte lookups and
-//             issues 2*MT MFMAs.  No block barrier inside the loop.
+//             issues 2*MT MFMAs (4*MT when EXACT).  No block barrier inside
+//             the loop.
 //   epilogue: the waves' fp32 tiles are summed through LDS in wave order.
 // xfrag_kernel runs first and writes the fragment-order copy of x into the
 // caller's workspace.
@@ -460,7 +464,15 @@ __global__ __launch_bounds__(256) void xfrag_kernel(const uint16_t *__restrict__
   xf[static_cast<int64_t>(blockIdx.y) * per_slab + f] = v;
 }
 
-template <int MT, int WV, int PD>  // token tiles of 16; waves per block; quads of x in flight per wave
+// (hi | lo << 16) with hi + lo == v exactly for an fp16 value v (lo = 0 for inf / nan)
+__device__ __forceinline__ uint32_t hi_lo_pack(float v) {
+  const uint32_t hb = bf16_rne_bits(v);
+  if (!(fabsf(v) <= 3.0e38f)) return hb;
+  return hb | (bf16_rne_bits(v - __uint_as_float(hb << 16)) << 16);
+}
+
+// token tiles of 16; waves per block; quads of x in flight per wave; exact fp16 weights (hi + lo)
+template <int MT, int WV, int PD, bool EXACT>
 __global__ __launch_bounds__(64 * WV, WV <= 4 ? 2 : 1) void dqmm_kernel(
     const uint8_t *__restrict__ packed, int64_t packed_bytes, const uint16_t *__restrict__ sigma16, int64_t rows,
     int64_t atoms_per_row, const uint4 *__restrict__ xf, int64_t n_quads_row, int64_t m_total, int splits, int apb,
@@ -472,7 +484,7 @@ __global__ __launch_bounds__(64 * WV, WV <= 4 ? 2 : 1) void dqmm_kernel(
   const int region = max(kMmRows * ws, WV * TOK * kMmRedStride) * 4;
   uint32_t *wt = reinterpret_cast<uint32_t *>(smem);          // [32][ws] kp_dq words
   float *red = reinterpret_cast<float *>(smem);               // after the k loop: [WV][TOK][kMmRedStride]
-  uint4 *rtab = reinterpret_cast<uint4 *>(smem + region);     // [32] row byte tables
+  uint4 *rtab = reinterpret_cast<uint4 *>(smem + region);     // [EXACT ? 2 : 1][32] row byte tables
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, j = lane & 15, q = lane >> 4;
   const int64_t row_block = blockIdx.x / static_cast<unsigned>(splits);
   const int split = static_cast<int>(blockIdx.x % static_cast<unsigned>(splits));
@@ -514,7 +526,7 @@ __global__ __launch_bounds__(64 * WV, WV <= 4 ? 2 : 1) void dqmm_kernel(
 #pragma unroll
   for (int u = 0; u < PD; ++u) load_quad(xa[u], u);  // in flight during the prologue
 
-  // ---- per-row byte tables (threads 0..31, one row each): bf16 of the fp16 values, low / high bytes ----
+  // ---- per-row byte tables (threads 0..31, one row each): low / high bytes of hi (and lo) ----
   auto build_row_tables = [&]() {
     if (tid >= kMmRows) return;
     const int64_t row = row0 + tid;
@@ -523,17 +535,22 @@ __global__ __launch_bounds__(64 * WV, WV <= 4 ? 2 : 1) void dqmm_kernel(
     const uint32_t v0 = dq_value(0, sig, sl), v1 = dq_value(1, sig, sl), v2 = dq_value(2, sig, sl);
     const uint32_t v3 = dq_value(3, sig, sl), v4 = dq_value(4, sig, sl);
     const uint32_t h[8] = {v0, v1, v2, v4, v4 ^ 0x8000u, v3 ^ 0x8000u, v2 ^ 0x8000u, v1 ^ 0x8000u};
-    uint32_t lb0 = 0, lb1 = 0, hb0 = 0, hb1 = 0;
+    uint32_t hl[8];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const uint32_t b0 = bf16_rne_bits(__half2float(__ushort_as_half(static_cast<uint16_t>(h[e]))));
-      const uint32_t b1 = bf16_rne_bits(__half2float(__ushort_as_half(static_cast<uint16_t>(h[e + 4]))));
-      lb0 |= (b0 & 0xFFu) << (8 * e);
-      lb1 |= (b1 & 0xFFu) << (8 * e);
-      hb0 |= ((b0 >> 8) & 0xFFu) << (8 * e);
-      hb1 |= ((b1 >> 8) & 0xFFu) << (8 * e);
+    for (int e = 0; e < 8; ++e) hl[e] = hi_lo_pack(__half2float(__ushort_as_half(static_cast<uint16_t>(h[e]))));
+#pragma unroll
+    for (int half = 0; half < (EXACT ? 2 : 1); ++half) {
+      uint32_t lb0 = 0, lb1 = 0, hb0 = 0, hb1 = 0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t b0 = hl[e] >> (16 * half), b1 = hl[e + 4] >> (16 * half);
+        lb0 |= (b0 & 0xFFu) << (8 * e);
+        lb1 |= (b1 & 0xFFu) << (8 * e);
+        hb0 |= ((b0 >> 8) & 0xFFu) << (8 * e);
+        hb1 |= ((b1 >> 8) & 0xFFu) << (8 * e);
+      }
+      rtab[half * kMmRows + tid] = make_uint4(lb0, lb1, hb0, hb1);
     }
-    rtab[tid] = make_uint4(lb0, lb1, hb0, hb1);
   };
 
   // ---- codes -> kp_dq words in LDS ----
@@ -621,6 +638,7 @@ __global__ __launch_bounds__(64 * WV, WV <= 4 ? 2 : 1) void dqmm_kernel(
 #pragma unroll
     for (int rt = 0; rt < 2; ++rt) acc[t][rt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   const uint4 ta0 = rtab[j], ta1 = rtab[16 + j];
+  const uint4 tb0 = rtab[EXACT ? kMmRows + j : j], tb1 = rtab[EXACT ? kMmRows + 16 + j : 16 + j];
   // word of (row, block atom a, plane p) = 3a + p; K step s of quad Q, lane group q: 12Q + 4s + q
   const uint32_t *wrow0 = wt + j * ws + 12 * wq0 + q;
   const uint32_t *wrow1 = wt + (16 + j) * ws + 12 * wq0 + q;
@@ -635,6 +653,16 @@ __global__ __launch_bounds__(64 * WV, WV <= 4 ? 2 : 1) void dqmm_kernel(
         const bf16x8_t av = __builtin_bit_cast(bf16x8_t, xa_q[s][t]);
         acc[t][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, b0, acc[t][0], 0, 0, 0);
         acc[t][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, b1, acc[t][1], 0, 0, 0);
+      }
+      if constexpr (EXACT) {
+        const bf16x8_t l0 = perm_decode(w0, tb0.x, tb0.y, tb0.z, tb0.w);
+        const bf16x8_t l1 = perm_decode(w1, tb1.x, tb1.y, tb1.z, tb1.w);
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+          const bf16x8_t av = __builtin_bit_cast(bf16x8_t, xa_q[s][t]);
+          acc[t][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, l0, acc[t][0], 0, 0, 0);
+          acc[t][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, l1, acc[t][1], 0, 0, 0);
+        }
       }
     }
     // keep the fragments in their registers until the slot is refilled, so no
@@ -741,7 +769,7 @@ MmPlan mm_plan(int64_t rows, int64_t apr) {
   return p;
 }
 
-template <int MT, int WV, int PD>
+template <int MT, int WV, int PD, bool EXACT>
 int launch_dqmm_t(const uint8_t *packed, int64_t pb, const uint16_t *sigma16, int64_t rows, int64_t apr,
                   const uint4 *xf, int64_t m, float *y, float *partial, const MmPlan &pl, const uint32_t *kp_dq,
                   hipStream_t s) {
@@ -749,9 +777,9 @@ int launch_dqmm_t(const uint8_t *packed, int64_t pb, const uint16_t *sigma16, in
   const int64_t slabs = (m + 63) / 64;
   const int64_t nq = (apr + 3) / 4;
   const size_t region = static_cast<size_t>(max(kMmRows * mm_row_words(pl.apb), WV * 16 * MT * kMmRedStride)) * 4;
-  const size_t shm = region + static_cast<size_t>(kMmRows) * 16;
+  const size_t shm = region + static_cast<size_t>(kMmRows) * 16 * (EXACT ? 2 : 1);
   const dim3 g(static_cast<unsigned>(row_blocks * pl.splits), static_cast<unsigned>(slabs));
-  hipLaunchKernelGGL((dqmm_kernel<MT, WV, PD>), g, dim3(64 * WV), shm, s, packed, pb, sigma16, rows, apr, xf, nq, m,
+  hipLaunchKernelGGL((dqmm_kernel<MT, WV, PD, EXACT>), g, dim3(64 * WV), shm, s, packed, pb, sigma16, rows, apr, xf, nq, m,
                      pl.splits, pl.apb, kp_dq, y, partial);
   return check_launch("dqmm_kernel");
 }
@@ -759,10 +787,11 @@ int launch_dqmm_t(const uint8_t *packed, int64_t pb, const uint16_t *sigma16, in
 template <int MT>
 int launch_dqmm(const uint8_t *packed, int64_t pb, const uint16_t *sigma16, int64_t rows, int64_t apr,
                 const uint4 *xf, int64_t m, float *y, float *partial, const MmPlan &pl, const uint32_t *kp_dq,
-                hipStream_t s) {
+                bool exact, hipStream_t s) {
   // 8 waves (two per SIMD cover each other's load latency), one quad of x in
   // flight per wave; 4 waves with 2 quads in flight measured within 3%
-  return launch_dqmm_t<MT, 8, 1>(packed, pb, sigma16, rows, apr, xf, m, y, partial, pl, kp_dq, s);
+  if (exact) return launch_dqmm_t<MT, 8, 1, true>(packed, pb, sigma16, rows, apr, xf, m, y, partial, pl, kp_dq, s);
+  return launch_dqmm_t<MT, 8, 1, false>(packed, pb, sigma16, rows, apr, xf, m, y, partial, pl, kp_dq, s);
 }
 
 // Workspace of the batched path: the fragment-order x copy (a multiple of 256
@@ -780,20 +809,22 @@ MmWorkspace mm_workspace(int64_t rows, int64_t cols, int64_t m, const MmPlan &pl
   return w;
 }
 
-bool uses_mfma(int x_is_f32, int64_t m) { return !x_is_f32 && m > 16; }
+bool uses_mfma(int flags, int64_t m) { return !(flags & PLX_DQL_X_F32) && m > 16; }
 
 }  // namespace
 
-size_t dequant_linear_workspace_bytes(int64_t rows, int64_t cols, int64_t m, int x_is_f32) {
-  if (!uses_mfma(x_is_f32, m) || rows <= 0 || cols <= 0) return 0;
+size_t dequant_linear_workspace_bytes(int64_t rows, int64_t cols, int64_t m, int flags) {
+  if (!uses_mfma(flags, m) || rows <= 0 || cols <= 0) return 0;
   return mm_workspace(rows, cols, m, mm_plan(rows, cols / kDim)).total();
 }
 
 int launch_dequant_linear(const uint8_t *packed, const uint16_t *sigma16, int64_t rows, int64_t cols, const void *x,
-                          int x_is_f32, int64_t m, float *y, void *workspace, size_t workspace_bytes, hipStream_t s) {
+                          int flags, int64_t m, float *y, void *workspace, size_t workspace_bytes, hipStream_t s) {
   if ((reinterpret_cast<uintptr_t>(x) & 15u) != 0 || (reinterpret_cast<uintptr_t>(packed) & 15u) != 0)
     return fail(PLX_EINVAL, "dequant_linear: x and packed must be 16-byte aligned");
-  const size_t need = dequant_linear_workspace_bytes(rows, cols, m, x_is_f32);
+  const int x_is_f32 = flags & PLX_DQL_X_F32;
+  const int round_w = !x_is_f32 && (flags & PLX_DQL_W_AS_X) ? 1 : 0;  // W.to(fp32) is exact
+  const size_t need = dequant_linear_workspace_bytes(rows, cols, m, flags);
   if (workspace_bytes < need || (need && workspace == nullptr))
     return fail(PLX_EINVAL, "dequant_linear: workspace of %zu bytes is smaller than the %zu needed", workspace_bytes, need);
   if (need && (reinterpret_cast<uintptr_t>(workspace) & 15u) != 0)
@@ -803,7 +834,7 @@ int launch_dequant_linear(const uint8_t *packed, const uint16_t *sigma16, int64_
   if (st != PLX_OK) return st;
   const int64_t apr = cols / kDim;
   const int64_t pb = ((rows * apr + 3) / 4) * 9;  // packed stream length
-  if (uses_mfma(x_is_f32, m)) {
+  if (uses_mfma(flags, m)) {
     // bf16 batches above 16 tokens: MFMA dequant-GEMM in slabs of 64 tokens
     if (cols > kMmMaxCols)
       return fail(PLX_EINVAL, "dequant_linear: %lld columns exceed the batched path's %lld", static_cast<long long>(cols),
@@ -818,8 +849,8 @@ int launch_dequant_linear(const uint8_t *packed, const uint16_t *sigma16, int64_
                        static_cast<const uint16_t *>(x), m, cols, nq, xf);
     st = check_launch("xfrag_kernel");
     if (st != PLX_OK) return st;
-    st = m > 32 ? launch_dqmm<4>(packed, pb, sigma16, rows, apr, xf, m, y, part, pl, tab->kp_dq, s)
-                : launch_dqmm<2>(packed, pb, sigma16, rows, apr, xf, m, y, part, pl, tab->kp_dq, s);
+    st = m > 32 ? launch_dqmm<4>(packed, pb, sigma16, rows, apr, xf, m, y, part, pl, tab->kp_dq, !round_w, s)
+                : launch_dqmm<2>(packed, pb, sigma16, rows, apr, xf, m, y, part, pl, tab->kp_dq, !round_w, s);
     if (st != PLX_OK || pl.splits == 1) return st;
     const int64_t n = m * rows;
     if (rows % 4 == 0 && (reinterpret_cast<uintptr_t>(y) & 15u) == 0)
@@ -833,13 +864,13 @@ int launch_dequant_linear(const uint8_t *packed, const uint16_t *sigma16, int64_
   const uint4 *kp = reinterpret_cast<const uint4 *>(tab->kp_gemv);
   // lanes per row: about 2-5 atoms per lane
   if (apr >= 160)
-    return x_is_f32 ? launch_dql<64, true>(packed, pb, sigma16, rows, apr, x, m, y, kp, s)
-                    : launch_dql<64, false>(packed, pb, sigma16, rows, apr, x, m, y, kp, s);
+    return x_is_f32 ? launch_dql<64, true>(packed, pb, sigma16, rows, apr, x, m, y, kp, round_w, s)
+                    : launch_dql<64, false>(packed, pb, sigma16, rows, apr, x, m, y, kp, round_w, s);
   if (apr >= 40)
-    return x_is_f32 ? launch_dql<32, true>(packed, pb, sigma16, rows, apr, x, m, y, kp, s)
-                    : launch_dql<32, false>(packed, pb, sigma16, rows, apr, x, m, y, kp, s);
-  return x_is_f32 ? launch_dql<8, true>(packed, pb, sigma16, rows, apr, x, m, y, kp, s)
-                  : launch_dql<8, false>(packed, pb, sigma16, rows, apr, x, m, y, kp, s);
+    return x_is_f32 ? launch_dql<32, true>(packed, pb, sigma16, rows, apr, x, m, y, kp, round_w, s)
+                    : launch_dql<32, false>(packed, pb, sigma16, rows, apr, x, m, y, kp, round_w, s);
+  return x_is_f32 ? launch_dql<8, true>(packed, pb, sigma16, rows, apr, x, m, y, kp, round_w, s)
+                  : launch_dql<8, false>(packed, pb, sigma16, rows, apr, x, m, y, kp, round_w, s);
 }
 
 }  // namespace plx

@@ -81,9 +81,9 @@ int launch_requantize_batch(const RequantItem *items, int n_items, int mode, voi
 int launch_gather(const int32_t *idx, int64_t n, int out_dtype, void *out, hipStream_t s);
 int launch_dequant_f16(const uint8_t *packed, const uint16_t *sigma16, int64_t rows, int64_t cols,
                        uint16_t *w16, hipStream_t s);
-size_t dequant_linear_workspace_bytes(int64_t rows, int64_t cols, int64_t m, int x_is_f32);
+size_t dequant_linear_workspace_bytes(int64_t rows, int64_t cols, int64_t m, int flags);
 int launch_dequant_linear(const uint8_t *packed, const uint16_t *sigma16, int64_t rows, int64_t cols, const void *x,
-                          int x_is_f32, int64_t m, float *y, void *workspace, size_t workspace_bytes, hipStream_t s);
+                          int flags, int64_t m, float *y, void *workspace, size_t workspace_bytes, hipStream_t s);
 size_t adam_h24_workspace_bytes(int64_t n_atoms);
 int launch_adam_h24(const float *grad, float *m, float *v, float *latent, int64_t n_atoms, const float *scalars,
                     float *adam_norm_out, void *workspace, hipStream_t s);

@@ -40,19 +40,27 @@ def dequantize_h24(packed: torch.Tensor, sigma16: torch.Tensor, out_features: in
     return out
 
 
-def dequant_linear(
-    packed: torch.Tensor, sigma16: torch.Tensor, out_features: int, in_features: int, x: torch.Tensor
-) -> torch.Tensor:
-    """F.linear(x, materialize(W).to(x.dtype)) in fp32 without materialising W (pollux.py:491-507).
+DQL_X_F32, DQL_W_AS_X = 1, 2  # plx_dequant_linear flags (include/pollux_amd.h)
 
-    As in the reference, the fp16 weight is cast to x's dtype: bf16 activations
-    multiply bf16-rounded weights, fp32 activations the exact fp16 values; the
-    products are exact and accumulated in fp32.
+
+def dequant_linear(
+    packed: torch.Tensor, sigma16: torch.Tensor, out_features: int, in_features: int, x: torch.Tensor,
+    weight_rounding: str = "exact",
+) -> torch.Tensor:
+    """y = x @ W.T in fp32 without materialising W (pollux.py:491-507).
+
+    weight_rounding="exact": products with the fp16 weights, exact, accumulated
+    in fp32 -- the numerics of F.linear(x.float(), materialize(W).float()).
+    weight_rounding="as_x": the reference's literal F.linear(x, W.to(x.dtype)),
+    i.e. with bf16 activations the fp16 weight is rounded to bf16 first (for
+    fp32 activations the two are the same).
     x: [..., in] bf16 or fp32 (other float dtypes are cast to fp32); returns fp32 [..., out].
     """
     _lib.require_device(packed, "dequant_linear packed input")
     if packed.dtype != torch.uint8 or sigma16.dtype != torch.float16:
         raise ValueError("packed weights must be uint8 and sigma rows float16")
+    if weight_rounding not in ("exact", "as_x"):
+        raise ValueError(f"weight_rounding must be 'exact' or 'as_x', got {weight_rounding!r}")
     assert_row_aligned_in_features(in_features)
     if x.shape[-1] != in_features:
         raise ValueError(f"x has {x.shape[-1]} features, layer expects {in_features}")
@@ -68,21 +76,28 @@ def dequant_linear(
         xx = xx.clone()
     sg = sigma16.reshape(-1).contiguous()
     y = torch.empty((xx.shape[0], out_features), dtype=torch.float32, device=pk.device)
-    x_f32 = int(xx.dtype == torch.float32)
+    flags = (DQL_X_F32 if xx.dtype == torch.float32 else 0) | (DQL_W_AS_X if weight_rounding == "as_x" else 0)
     lib = _lib.lib()
-    nws = int(lib.plx_dequant_linear_workspace_bytes(out_features, in_features, xx.shape[0], x_f32))
+    nws = int(lib.plx_dequant_linear_workspace_bytes(out_features, in_features, xx.shape[0], flags))
     ws = torch.empty(max(nws, 16), dtype=torch.uint8, device=pk.device) if nws else None
     with torch.cuda.device(pk.device):
         st = lib.plx_dequant_linear(
             _lib.ptr(pk), pk.numel(), _lib.ptr(sg), out_features, in_features, _lib.ptr(xx),
-            x_f32, xx.shape[0], _lib.ptr(y), _lib.ptr(ws), nws, _lib.stream_of(pk.device),
+            flags, xx.shape[0], _lib.ptr(y), _lib.ptr(ws), nws, _lib.stream_of(pk.device),
         )
     _lib.check(st, "dequant_linear")
     return y.reshape(*lead, out_features)
 
 
 class PackedH24Linear(nn.Module):
-    """uint8 packed 18-bit indices + fp16 row scale; dense fp16 weight after materialize()."""
+    """uint8 packed 18-bit indices + fp16 row scale; dense fp16 weight after materialize().
+
+    Before materialize, forward runs dequant_linear with ``weight_rounding``
+    (class default "exact"; "as_x" reproduces the reference's rounding of W to
+    x's dtype).
+    """
+
+    weight_rounding = "exact"
 
     def __init__(self, in_features: int, out_features: int, bias: bool = False) -> None:
         super().__init__()
@@ -112,7 +127,8 @@ class PackedH24Linear(nn.Module):
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         if not self._materialized:
             # fused path: weights stay packed (0.76 bits/param); fp32 result cast to x's dtype
-            y = dequant_linear(self.packed_weights, self.sigma_rows, self.out_features, self.in_features, x).to(x.dtype)
+            y = dequant_linear(self.packed_weights, self.sigma_rows, self.out_features, self.in_features, x,
+                               weight_rounding=self.weight_rounding).to(x.dtype)
             return y if self.bias is None else y + self.bias.to(x.dtype)
         return F.linear(x, self.weight.to(dtype=x.dtype), self.bias)
 

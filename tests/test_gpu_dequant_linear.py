@@ -3,14 +3,17 @@
 packed [7680, 1920] and [1920, 7680] (torch (out, in) layout),
 indices uniform over 0..196560, sigma16 ~ U(0.005, 0.05), bf16 activations
 N(0, 1) at batch 1 (GEMV) and 64 (GEMM), fp32 accumulation.
-The reference computes F.linear(x, W16.to(x.dtype)) (pollux.py:507): with bf16
-activations the fp16 weight is rounded to bf16 first.  The expected value is
-that expression evaluated in fp32 (oracle.torch_ref.linear_as_reference).
-Tolerance (stated): relative L2 error <= 1e-5, and per element |dy| <= 1e-5 *
-sum_i |x_i W_i| (the products are exact in fp32; only the summation order
-differs).  For bf16 activations the test also checks that the result is far
-(> 1e-4 relative) from the product with the unrounded fp16 weight, so it tells
-the reference's rounding from its absence.
+Default mode ("exact"): the expected value is F.linear(x.float(), W16.float())
+(oracle.torch_ref.linear_fp32), the fp32 numerics of pollux.py:507.
+Mode "as_x": the reference's literal F.linear(x, W16.to(x.dtype)), which for
+bf16 activations rounds the fp16 weight to bf16 first, evaluated in fp32
+(oracle.torch_ref.linear_as_reference); its distance from the exact product
+(~1.7e-3 relative at config 5) is printed as context.
+Tolerance (stated), either mode: relative L2 error <= 1e-5, and per element
+|dy| <= 1e-5 * sum_i |x_i W_i| (the products are exact in fp32; only the
+summation order differs).  For bf16 activations each check also asserts that
+the result is > 1e-4 away from the other mode's expected value, so the tests
+tell the two roundings apart.
 """
 
 import pytest
@@ -34,20 +37,22 @@ def _layer(out_f, in_f, seed):
     return idx, sig, packed, g
 
 
-def _check(y, x, w16):
-    """y against F.linear(x, w16.to(x.dtype)) evaluated in fp32 (x in its own dtype)."""
-    ref = torch_ref.linear_as_reference(x, w16)
-    w = w16.to(x.dtype).double()
-    err = (y.double() - ref.double())
-    rel = err.norm() / ref.double().norm()
+def _check(y, x, w16, mode="exact"):
+    """y against the expected value of `mode` (x in its own dtype)."""
+    exact = torch_ref.linear_fp32(x, w16).double()
+    literal = torch_ref.linear_as_reference(x, w16).double()
+    ref, other = (exact, literal) if mode == "exact" else (literal, exact)
+    w = (w16 if mode == "exact" else w16.to(x.dtype)).double()
+    err = y.double() - ref
+    rel = err.norm() / ref.norm()
     bound = ELEM * (x.double().abs() @ w.abs().t())
     worst = (err.abs() / bound).max().item()
-    print(f"[dql] rel_l2 {rel:.3e} worst elem/bound {worst:.3f}", flush=True)
+    ctx = ((literal - exact).norm() / exact.norm()).item()
+    print(f"[dql] {mode}: rel_l2 {rel:.3e} worst elem/bound {worst:.3f}; literal-vs-exact {ctx:.2e}", flush=True)
     assert rel <= REL_L2
     assert worst <= 1.0
     if x.dtype == torch.bfloat16:
-        exact16 = torch_ref.linear_fp32(x, w16).double()
-        assert (y.double() - exact16).norm() / exact16.norm() > 1e-4  # the bf16 rounding of W is applied
+        assert (y.double() - other).norm() / other.norm() > 1e-4  # the two roundings are told apart
 
 
 @pytest.mark.parametrize("shape", [(7680, 1920), (1920, 7680)])
@@ -114,3 +119,27 @@ def test_packed_layer_forward_without_materialize(dev):
     assert y_fused.shape == (2, 3, out_f)
     assert ((y_fused - ref).norm() / ref.norm()).item() <= REL_L2
     assert ((y_dense - ref).norm() / ref.norm()).item() <= 1e-5
+
+
+@pytest.mark.parametrize("shape,m", [((7680, 1920), 64), ((1920, 7680), 64), ((7680, 1920), 1), ((1152, 1152), 17),
+                                     ((37, 1920), 5)])
+def test_reference_literal_rounding(dev, shape, m):
+    # weight_rounding="as_x": F.linear(x, W.to(x.dtype)) as the reference evaluates it with bf16 x
+    out_f, in_f = shape
+    idx, sig, packed, g = _layer(out_f, in_f, 13 * out_f + m)
+    x = torch.randn(m, in_f, generator=g).to(torch.bfloat16)
+    w16 = torch_ref.materialize(idx, sig, out_f, in_f)
+    y = dequant_linear(packed.to(dev), sig.to(dev), out_f, in_f, x.to(dev), weight_rounding="as_x").cpu()
+    _check(y, x, w16, mode="as_x")
+
+
+def test_literal_rounding_is_exact_for_fp32_activations(dev):
+    # W.to(fp32) is exact, so both modes agree bit for bit with fp32 x
+    out_f, in_f = 64, 1152
+    idx, sig, packed, g = _layer(out_f, in_f, 21)
+    x = torch.randn(3, in_f, generator=g).to(dev)
+    a = dequant_linear(packed.to(dev), sig.to(dev), out_f, in_f, x)
+    b = dequant_linear(packed.to(dev), sig.to(dev), out_f, in_f, x, weight_rounding="as_x")
+    assert torch.equal(a, b)
+    with pytest.raises(ValueError):
+        dequant_linear(packed.to(dev), sig.to(dev), out_f, in_f, x, weight_rounding="bf16")
