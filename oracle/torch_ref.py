@@ -152,3 +152,56 @@ def pollux_h24_update(grad, m, v, latent, heat, step, width_inertia):
     latent.mul_(weight_decay_factor)
     latent.add_(adam_step)
     return adam_step
+
+
+def int8_materialize(q: torch.Tensor, mu16: torch.Tensor) -> torch.Tensor:
+    """PackedInt8Embedding/Linear.materialize (pollux.py:521-530): int8 * (mu / 127.0) in fp16."""
+    return q.to(torch.float16) * (mu16.unsqueeze(-1).to(torch.float16) / 127.0)
+
+
+def _rms_norm(x: torch.Tensor, w: torch.Tensor, eps: float = 1e-8) -> torch.Tensor:
+    """RMSNorm.forward (pollux.py:580-582)."""
+    return x * torch.rsqrt(x.pow(2).mean(dim=-1, keepdim=True) + eps) * w
+
+
+def pollux_packed_forward(state: dict, cfg: dict, idx: torch.Tensor) -> torch.Tensor:
+    """PolluxModel.forward with packed_inference after from_packed_checkpoint (pollux.py:566-702, 704-758).
+
+    ``state``: a packed state dict (the .plx tensors); every packed weight is
+    materialised the reference's way (unpack, fp16 codebook gather, * sigma16,
+    * s_lattice; int8 * (mu / 127)) and the forward runs in fp32 on the CPU:
+    embeddings, pre-norm blocks with per-head Q/K RMS norms, causal SDPA, GELU
+    MLP, final norm, head.  Returns logits [b, t, vocab] (fp32).
+    """
+    from . import packing
+
+    n_layers, n_heads, d_head = int(cfg["n_layers"]), int(cfg["n_heads"]), int(cfg["d_head"])
+    f = torch.nn.functional
+
+    n_embd = int(cfg["n_embd"])
+    in_features = {"q_proj": n_embd, "k_proj": n_embd, "v_proj": n_embd, "o_proj": n_embd,
+                   "fc1": n_embd, "fc2": 4 * n_embd}
+
+    def h24(name: str) -> torch.Tensor:
+        sig = state[name + ".sigma_rows"]
+        out_f, in_f = sig.numel(), in_features[name.rsplit(".", 1)[1]]
+        ids = packing.unpack(state[name + ".packed_weights"].numpy(), out_f * in_f // 24)
+        return materialize(torch.from_numpy(ids.astype(np.int64)), sig, out_f, in_f).float()
+
+    emb = int8_materialize(state["tok_emb.weight_int8"], state["tok_emb.mu_rows"])
+    head = int8_materialize(state["head.weight_int8"], state["head.mu_rows"]).float()
+    b, t = idx.shape
+    x = f.embedding(idx, emb.float()) + state["pos_emb.weight"].float()[:t].unsqueeze(0)
+    for i in range(n_layers):
+        p = f"blocks.{i}."
+        h = _rms_norm(x, state[p + "ln1.weight"].float())
+        q = f.linear(h, h24(p + "attn.q_proj")).view(b, t, n_heads, d_head)
+        k = f.linear(h, h24(p + "attn.k_proj")).view(b, t, n_heads, d_head)
+        v = f.linear(h, h24(p + "attn.v_proj")).view(b, t, n_heads, d_head).transpose(1, 2)
+        q = _rms_norm(q, state[p + "attn.q_ln.weight"].float()).transpose(1, 2)
+        k = _rms_norm(k, state[p + "attn.k_ln.weight"].float()).transpose(1, 2)
+        a = f.scaled_dot_product_attention(q, k, v, is_causal=True)
+        x = x + f.linear(a.transpose(1, 2).contiguous().view(b, t, n_heads * d_head), h24(p + "attn.o_proj"))
+        h = _rms_norm(x, state[p + "ln2.weight"].float())
+        x = x + f.linear(f.gelu(f.linear(h, h24(p + "mlp.fc1"))), h24(p + "mlp.fc2"))
+    return f.linear(_rms_norm(x, state["ln_f.weight"].float()), head)

@@ -1,0 +1,357 @@
+"""Packed Pollux decoder for inference, with a KV cache (pollux.py:566-758, generate.py:280-336).
+
+The reference loads a .plx checkpoint into ``PolluxModel`` with packed layers
+(``from_packed_checkpoint``, pollux.py:704-758), materialises every packed
+weight to fp16 and then, for every generated token, recomputes the whole
+prefix (``generate``, generate.py:313-327).  Here:
+
+* ``PackedPolluxModel`` has the reference's module tree and state-dict keys
+  (``tok_emb``, ``pos_emb``, ``blocks.{i}.{ln1,attn,ln2,mlp}``, ``ln_f``,
+  ``head``), so a .plx state dict loads with ``strict=True``;
+* the H24 projections stay packed (0.76 bits per weight) and run the fused
+  dequant-GEMV/GEMM kernels (``PackedH24Linear.forward``); ``materialize=True``
+  gives the reference's dense fp16 path instead;
+* ``prefill`` / ``decode`` keep each layer's keys and values in a ``KVCache``,
+  so a new token costs one position instead of the whole prefix.
+
+Activations are fp32, as in the reference's packed inference (no autocast):
+the INT8 embedding rows are cast to fp32 (pollux.py:532-533), the packed
+linears see fp32 x (exact products with the fp16 weights), the head multiplies
+by its fp16 weight cast to fp32 (pollux.py:562-563).
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Any
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from .castor import H24_DIM, assert_row_aligned_width
+from .packed import PackedH24Linear, PackedInt8Embedding, PackedInt8Linear
+from .plx import check_fingerprint, load_plx
+
+# pollux.py:258-278: the config fields and their aliases
+CONFIG_FIELDS = (
+    "n_layers", "n_heads", "d_head", "n_embd", "tokenizer_vocab_size", "vocab_size", "batch_size",
+    "seq_len", "grad_accum_steps", "use_compile", "use_gradient_checkpointing", "target_tokens",
+    "tokenizer_dir",
+)
+CONFIG_ALIASES = {"d_model": "n_embd", "n_layer": "n_layers", "n_head": "n_heads"}
+CONFIG_DEFAULTS = {  # pollux.py:283-295
+    "n_layers": 18, "n_heads": 80, "d_head": 24, "n_embd": 1920, "tokenizer_vocab_size": 50257,
+    "vocab_size": 50688, "batch_size": 2, "seq_len": 1024, "grad_accum_steps": 128, "use_compile": False,
+    "use_gradient_checkpointing": False, "target_tokens": 9_953_989_333, "tokenizer_dir": "",
+}
+
+
+class PolluxConfig:
+    """PolluxConfig (pollux.py:280-356): architecture fields, dict round trip, validation."""
+
+    def __init__(self, **overrides: Any) -> None:
+        for name in CONFIG_FIELDS:
+            setattr(self, name, overrides.get(name, CONFIG_DEFAULTS[name]))
+
+    @classmethod
+    def from_dict(cls, raw: dict[str, Any] | None) -> PolluxConfig:
+        values = {}
+        for key, value in (raw or {}).items():
+            target = CONFIG_ALIASES.get(str(key), str(key))
+            if target in CONFIG_FIELDS:
+                values[target] = value
+        cfg = cls(**values)
+        cfg.validate_instance()
+        return cfg
+
+    def to_dict(self) -> dict[str, Any]:
+        return {name: getattr(self, name) for name in CONFIG_FIELDS}
+
+    def validate_instance(self) -> None:
+        """pollux.py:324-349."""
+        d_head, n_heads, n_embd = int(self.d_head), int(self.n_heads), int(self.n_embd)
+        if d_head != H24_DIM:
+            raise ValueError(
+                f"d_head must equal H24_DIM ({H24_DIM}): each attention head is one "
+                "24-dimensional Leech lattice atom."
+            )
+        if n_embd != n_heads * d_head:
+            raise ValueError(
+                "n_embd must equal n_heads * d_head: embedding width is an integer "
+                "multiple of the 24D packing unit."
+            )
+        assert_row_aligned_width(n_embd)
+        vocab, tok_vocab = int(self.vocab_size), int(self.tokenizer_vocab_size)
+        if vocab % H24_DIM != 0:
+            raise ValueError(f"vocab_size ({vocab}) must be divisible by H24_DIM ({H24_DIM}).")
+        if vocab < tok_vocab:
+            raise ValueError(f"vocab_size ({vocab}) must cover tokenizer_vocab_size ({tok_vocab}).")
+
+
+class RMSNorm(nn.Module):
+    """x * rsqrt(mean(x^2) + eps) * weight over the last dimension (pollux.py:566-582)."""
+
+    def __init__(self, dim: int, eps: float = 1e-8) -> None:
+        super().__init__()
+        self.eps = eps
+        self.weight = nn.Parameter(torch.ones(dim))
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return x * torch.rsqrt(x.pow(2).mean(dim=-1, keepdim=True) + self.eps) * self.weight
+
+
+@dataclass
+class KVCache:
+    """Keys and values of every layer, [batch, heads, max_len, d_head] fp32, filled up to ``length``."""
+
+    k: list[torch.Tensor]
+    v: list[torch.Tensor]
+    length: int = 0
+
+    @classmethod
+    def allocate(cls, cfg: PolluxConfig, batch: int, max_len: int, device) -> KVCache:
+        shape = (batch, int(cfg.n_heads), max_len, int(cfg.d_head))
+        n = int(cfg.n_layers)
+        return cls([torch.zeros(shape, device=device) for _ in range(n)],
+                   [torch.zeros(shape, device=device) for _ in range(n)])
+
+    @property
+    def max_len(self) -> int:
+        return self.k[0].shape[2]
+
+
+class PackedCausalAttention(nn.Module):
+    """PolluxCausalAttention (pollux.py:585-626) on packed projections, with an optional KV cache."""
+
+    def __init__(self, cfg: PolluxConfig) -> None:
+        super().__init__()
+        self.n_heads, self.d_head, self.n_embd = int(cfg.n_heads), int(cfg.d_head), int(cfg.n_embd)
+        self.q_proj = PackedH24Linear(self.n_embd, self.n_embd)
+        self.k_proj = PackedH24Linear(self.n_embd, self.n_embd)
+        self.v_proj = PackedH24Linear(self.n_embd, self.n_embd)
+        self.o_proj = PackedH24Linear(self.n_embd, self.n_embd)
+        self.q_ln = RMSNorm(self.d_head)  # per-head Q/K norms on the 24-d atom
+        self.k_ln = RMSNorm(self.d_head)
+
+    def forward(self, x: torch.Tensor, cache: KVCache | None = None, layer: int = 0) -> torch.Tensor:
+        b, t, c = x.shape
+        q = self.q_ln(self.q_proj(x).view(b, t, self.n_heads, self.d_head)).transpose(1, 2)
+        k = self.k_ln(self.k_proj(x).view(b, t, self.n_heads, self.d_head)).transpose(1, 2)
+        v = self.v_proj(x).view(b, t, self.n_heads, self.d_head).transpose(1, 2)
+        if cache is None:
+            attn = F.scaled_dot_product_attention(q, k, v, is_causal=True)
+        else:
+            p0 = cache.length
+            cache.k[layer][:, :, p0:p0 + t] = k
+            cache.v[layer][:, :, p0:p0 + t] = v
+            keys, vals = cache.k[layer][:, :, :p0 + t], cache.v[layer][:, :, :p0 + t]
+            if p0 == 0:
+                attn = F.scaled_dot_product_attention(q, keys, vals, is_causal=True)
+            elif t == 1:
+                attn = F.scaled_dot_product_attention(q, keys, vals)  # every cached position is visible
+            else:
+                # query i sits at position p0 + i and sees positions <= p0 + i
+                allowed = torch.ones(t, p0 + t, dtype=torch.bool, device=x.device).tril(diagonal=p0)
+                attn = F.scaled_dot_product_attention(q, keys, vals, attn_mask=allowed)
+        return self.o_proj(attn.transpose(1, 2).contiguous().view(b, t, c))
+
+
+class PackedMLP(nn.Module):
+    """PolluxMLP (pollux.py:629-645): fc2(gelu(fc1(x))), 4x expansion."""
+
+    def __init__(self, cfg: PolluxConfig) -> None:
+        super().__init__()
+        n_embd = int(cfg.n_embd)
+        self.fc1 = PackedH24Linear(n_embd, 4 * n_embd)
+        self.fc2 = PackedH24Linear(4 * n_embd, n_embd)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return self.fc2(F.gelu(self.fc1(x)))
+
+
+class PackedBlock(nn.Module):
+    """PolluxBlock (pollux.py:648-662): pre-norm attention and MLP residuals."""
+
+    def __init__(self, cfg: PolluxConfig) -> None:
+        super().__init__()
+        self.ln1 = RMSNorm(int(cfg.n_embd))
+        self.attn = PackedCausalAttention(cfg)
+        self.ln2 = RMSNorm(int(cfg.n_embd))
+        self.mlp = PackedMLP(cfg)
+
+    def forward(self, x: torch.Tensor, cache: KVCache | None = None, layer: int = 0) -> torch.Tensor:
+        x = x + self.attn(self.ln1(x), cache, layer)
+        return x + self.mlp(self.ln2(x))
+
+
+class PackedPolluxModel(nn.Module):
+    """PolluxModel with ``packed_inference`` (pollux.py:665-702): INT8 embedding / head, packed H24 blocks."""
+
+    def __init__(self, cfg: PolluxConfig) -> None:
+        super().__init__()
+        cfg.validate_instance()
+        self.cfg = cfg
+        n_embd = int(cfg.n_embd)
+        self.tok_emb = PackedInt8Embedding(int(cfg.vocab_size), n_embd)
+        self.pos_emb = nn.Embedding(int(cfg.seq_len), n_embd)
+        self.blocks = nn.ModuleList([PackedBlock(cfg) for _ in range(int(cfg.n_layers))])
+        self.ln_f = RMSNorm(n_embd)
+        self.head = PackedInt8Linear(n_embd, int(cfg.vocab_size), bias=False)
+
+    def _run(self, idx: torch.Tensor, pos0: int, cache: KVCache | None) -> torch.Tensor:
+        t = idx.shape[1]
+        pos = torch.arange(pos0, pos0 + t, device=idx.device).unsqueeze(0)
+        x = self.tok_emb(idx) + self.pos_emb(pos)
+        for i, block in enumerate(self.blocks):
+            x = block(x, cache, i)
+        if cache is not None:
+            cache.length = pos0 + t
+        return self.head(self.ln_f(x))
+
+    def forward(self, idx: torch.Tensor) -> torch.Tensor:
+        """Logits [b, t, vocab] of the full prefix, positions 0..t-1 (pollux.py:691-702)."""
+        if idx.shape[1] > int(self.cfg.seq_len):
+            raise ValueError(f"sequence of {idx.shape[1]} tokens exceeds seq_len {self.cfg.seq_len}")
+        return self._run(idx, 0, None)
+
+    def new_cache(self, batch: int = 1, max_len: int | None = None) -> KVCache:
+        device = self.pos_emb.weight.device
+        return KVCache.allocate(self.cfg, batch, int(max_len or self.cfg.seq_len), device)
+
+    def prefill(self, idx: torch.Tensor, cache: KVCache) -> torch.Tensor:
+        """Logits of ``idx`` appended at the cache's current length; the cache then holds them too."""
+        if cache.length + idx.shape[1] > min(cache.max_len, int(self.cfg.seq_len)):
+            raise ValueError("the cache (or seq_len) is too short for these tokens")
+        return self._run(idx, cache.length, cache)
+
+    def decode(self, next_ids: torch.Tensor, cache: KVCache) -> torch.Tensor:
+        """Logits [b, vocab] of one new token per sequence (next_ids [b] or [b, 1])."""
+        return self.prefill(next_ids.reshape(-1, 1), cache)[:, -1]
+
+    @classmethod
+    def from_packed_checkpoint(cls, source: str | dict, device: torch.device | str, *,
+                               materialize: bool = False) -> PackedPolluxModel:
+        """PolluxModel.from_packed_checkpoint (pollux.py:704-758) for a .plx path or a loaded payload.
+
+        The fingerprint check and the per-key dtype normalisation are the
+        reference's; the packed H24 layers stay packed unless ``materialize``.
+        The INT8 periphery is expanded to fp16 once (as the reference does).
+        """
+        if isinstance(source, dict):
+            check_fingerprint(source)
+            payload = source
+            state = {}
+            for key, t in payload["state_dict"].items():
+                if key.endswith(".packed_weights"):
+                    t = t.to(dtype=torch.uint8)
+                elif key.endswith(".weight_int8"):
+                    t = t.to(dtype=torch.int8)
+                elif key.endswith(".sigma_rows") or key.endswith(".mu_rows"):
+                    t = t.to(dtype=torch.float16)
+                elif t.is_floating_point():
+                    t = t.to(dtype=torch.float32)
+                state[key] = t.to(device)
+        else:
+            payload = load_plx(source, device)
+            state = payload["state_dict"]
+        cfg = PolluxConfig.from_dict(payload.get("config"))
+        with torch.device("meta"):
+            model = cls(cfg)
+        model = model.to_empty(device=device)
+        model.load_state_dict(state, strict=True)
+        model.eval()
+        for module in model.modules():
+            if isinstance(module, (PackedInt8Embedding, PackedInt8Linear)):
+                module.materialize()
+            elif materialize and isinstance(module, PackedH24Linear):
+                module.materialize()
+        return model
+
+
+# ---- sampling (generate.py:228-278) ------------------------------------------------
+
+
+def mask_inactive_vocab(logits: torch.Tensor, active_vocab: int) -> torch.Tensor:
+    """Logits beyond the tokenizer vocabulary set to -inf (generate.py:228-233)."""
+    if logits.size(-1) <= active_vocab:
+        return logits
+    mask = torch.arange(logits.size(-1), device=logits.device) >= active_vocab
+    return logits.masked_fill(mask, float("-inf"))
+
+
+def apply_repetition_penalty(logits: torch.Tensor, ids: torch.Tensor, penalty: float) -> None:
+    """In place: seen tokens' positive logits divided by the penalty, negative ones multiplied (generate.py:240-253)."""
+    if penalty <= 1.0:
+        return
+    seen = torch.unique(ids)
+    seen = seen[(seen >= 0) & (seen < logits.numel())]
+    if seen.numel() == 0:
+        return
+    vals = logits[seen]
+    logits[seen] = torch.where(vals > 0, vals / penalty, vals * penalty)
+
+
+def apply_top_k(logits: torch.Tensor, k: int) -> torch.Tensor:
+    """Keep the k largest logits (generate.py:256-262)."""
+    if k <= 0 or k >= logits.numel():
+        return logits
+    _, keep = torch.topk(logits, k)
+    drop = torch.ones_like(logits, dtype=torch.bool)
+    drop.scatter_(0, keep, False)
+    return logits.masked_fill(drop, float("-inf"))
+
+
+def apply_top_p(logits: torch.Tensor, p: float) -> torch.Tensor:
+    """Nucleus filter: keep the smallest prefix of the sorted distribution reaching p (generate.py:265-278)."""
+    if p <= 0.0 or p >= 1.0:
+        return logits
+    sorted_logits, order = torch.sort(logits, descending=True)
+    cumulative = torch.cumsum(torch.softmax(sorted_logits, dim=-1), dim=-1)
+    remove = cumulative > p
+    remove[1:] = remove[:-1].clone()
+    remove[0] = False
+    drop = torch.zeros_like(logits, dtype=torch.bool)
+    drop.scatter_(0, order, remove)
+    return logits.masked_fill(drop, float("-inf"))
+
+
+@torch.inference_mode()
+def generate(model: PackedPolluxModel, ids: list[int], *, max_new_tokens: int = 80, temperature: float = 0.6,
+             top_k: int = 50, top_p: float = 0.9, repetition_penalty: float = 1.1, active_vocab: int | None = None,
+             eos_id: int = 50256, generator: torch.Generator | None = None, use_cache: bool = True) -> list[int]:
+    """The token loop of generate.generate (generate.py:286-336) on token ids.
+
+    Sampling follows the reference step for step (vocabulary mask, repetition
+    penalty, temperature, top-k, top-p, multinomial).  With ``use_cache`` the
+    prompt is prefilled once and each new token is one ``decode`` position;
+    once the sequence is longer than seq_len the reference's window
+    ``idx[:, -seq_len:]`` restarts the positions at 0, so from then on every
+    step recomputes the window, exactly as the reference does.
+    """
+    device = model.pos_emb.weight.device
+    seq_len = int(model.cfg.seq_len)
+    v_active = active_vocab or eos_id + 1
+    ids = [t for t in ids if 0 <= t < v_active] or [eos_id]
+    idx = torch.tensor([ids], device=device, dtype=torch.long)
+    cache = model.new_cache(1, seq_len) if use_cache else None
+    logits = None
+    for _ in range(max_new_tokens):
+        if cache is not None and idx.shape[1] <= seq_len:
+            if cache.length == 0:
+                logits = model.prefill(idx, cache)[:, -1]
+            else:
+                logits = model.decode(idx[:, -1], cache)
+        else:
+            logits = model(idx[:, -seq_len:])[:, -1]
+        logits = mask_inactive_vocab(logits.float()[0], v_active)
+        apply_repetition_penalty(logits, idx[0], repetition_penalty)
+        if temperature > 0:
+            logits = logits / max(float(temperature), 1e-8)
+        logits = apply_top_p(apply_top_k(logits, top_k), top_p)
+        probs = torch.softmax(logits, dim=-1)
+        next_id = int(torch.multinomial(probs, num_samples=1, generator=generator).item())
+        idx = torch.cat([idx, torch.tensor([[next_id]], device=device)], dim=1)
+        if next_id == eos_id:
+            break
+    return idx[0].tolist()

@@ -185,7 +185,9 @@ class PackedInt8Embedding(_PackedInt8Rows):
 
     def forward(self, idx: torch.Tensor) -> torch.Tensor:
         self.materialize()
-        return F.embedding(idx, self.weight.to(dtype=torch.float32))
+        # rows gathered, then cast: the same values as F.embedding(idx, weight.float())
+        # (pollux.py:532-533) without casting the whole table per call
+        return F.embedding(idx, self.weight).to(dtype=torch.float32)
 
 
 class PackedInt8Linear(_PackedInt8Rows):
@@ -203,4 +205,14 @@ class PackedInt8Linear(_PackedInt8Rows):
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         self.materialize()
-        return F.linear(x, self.weight.to(dtype=x.dtype), self.bias)
+        return F.linear(x, self._weight_as(x.dtype), self.bias)
+
+    def _weight_as(self, dtype: torch.dtype) -> torch.Tensor:
+        """weight.to(dtype) (pollux.py:562-563), cast once per dtype and kept (the weights are frozen)."""
+        if self.weight.dtype == dtype:
+            return self.weight
+        cache = self.__dict__.setdefault("_cast", {})
+        w = cache.get(dtype)
+        if w is None or w.device != self.weight.device:
+            w = cache[dtype] = self.weight.detach().to(dtype=dtype)
+        return w

@@ -1,0 +1,66 @@
+"""Host-side parts of the packed Pollux decoder: config rules, module tree, sampling helpers (no GPU)."""
+
+import math
+
+import pytest
+import torch
+
+from pollux_amd.model import (
+    PackedPolluxModel,
+    PolluxConfig,
+    apply_repetition_penalty,
+    apply_top_k,
+    apply_top_p,
+    mask_inactive_vocab,
+)
+
+
+def test_config_defaults_aliases_and_rules():
+    cfg = PolluxConfig.from_dict({})
+    assert (cfg.n_layers, cfg.n_heads, cfg.d_head, cfg.n_embd, cfg.vocab_size, cfg.seq_len) == (18, 80, 24, 1920, 50688, 1024)
+    cfg = PolluxConfig.from_dict({"d_model": 48, "n_head": 2, "n_layer": 3, "vocab_size": 96,
+                                  "tokenizer_vocab_size": 90, "unknown": 1})
+    assert (cfg.n_embd, cfg.n_heads, cfg.n_layers) == (48, 2, 3)
+    assert cfg.to_dict()["n_embd"] == 48 and "unknown" not in cfg.to_dict()
+    bad = [
+        {"d_head": 12, "n_heads": 4, "n_embd": 48},                       # d_head must be 24
+        {"n_heads": 3, "n_embd": 48},                                      # n_embd = n_heads * d_head
+        {"n_heads": 2, "n_embd": 48, "vocab_size": 100, "tokenizer_vocab_size": 90},  # vocab % 24
+        {"n_heads": 2, "n_embd": 48, "vocab_size": 48, "tokenizer_vocab_size": 90},   # vocab covers tokenizer
+    ]
+    for raw in bad:
+        with pytest.raises(ValueError):
+            PolluxConfig.from_dict(raw)
+
+
+def test_state_dict_keys_are_the_reference_packed_keys():
+    cfg = PolluxConfig(n_layers=2, n_heads=2, n_embd=48, vocab_size=96, tokenizer_vocab_size=90, seq_len=16)
+    keys = set(PackedPolluxModel(cfg).state_dict())
+    want = {"tok_emb.weight_int8", "tok_emb.mu_rows", "pos_emb.weight", "ln_f.weight", "head.weight_int8",
+            "head.mu_rows"}
+    for i in range(2):
+        p = f"blocks.{i}."
+        want |= {p + "ln1.weight", p + "ln2.weight", p + "attn.q_ln.weight", p + "attn.k_ln.weight"}
+        for name in ("attn.q_proj", "attn.k_proj", "attn.v_proj", "attn.o_proj", "mlp.fc1", "mlp.fc2"):
+            want |= {p + name + ".packed_weights", p + name + ".sigma_rows"}
+    assert keys == want
+    sd = PackedPolluxModel(cfg).state_dict()
+    assert sd["blocks.0.mlp.fc1.packed_weights"].numel() == (192 * 48 // 24 + 3) // 4 * 9
+    assert sd["blocks.0.mlp.fc2.sigma_rows"].shape == (48,)
+    assert sd["head.weight_int8"].shape == (96, 48) and sd["head.weight_int8"].dtype == torch.int8
+
+
+def test_sampling_helpers_hand_computed():
+    x = torch.tensor([1.0, 5.0, 3.0, 4.0])
+    assert apply_top_k(x, 2).tolist() == [-math.inf, 5.0, -math.inf, 4.0]
+    assert apply_top_k(x, 0).tolist() == x.tolist()
+    # softmax of (3, 2, 1, 0) = (0.644, 0.237, 0.087, 0.032): cumulative 0.644, 0.881, 0.968 -> with
+    # p = 0.9 the token that crosses p (logit 1) is kept, logit 0 is dropped
+    y = torch.tensor([0.0, 1.0, 2.0, 3.0])
+    assert apply_top_p(y, 0.9).tolist() == [-math.inf, 1.0, 2.0, 3.0]
+    assert apply_top_p(y, 0.5).tolist() == [-math.inf, -math.inf, -math.inf, 3.0]
+    z = torch.tensor([2.0, -2.0, 1.0])
+    apply_repetition_penalty(z, torch.tensor([0, 1, 1]), 2.0)
+    assert z.tolist() == [1.0, -4.0, 1.0]
+    m = mask_inactive_vocab(torch.zeros(5), 3)
+    assert m.tolist() == [0.0, 0.0, 0.0, -math.inf, -math.inf]
