@@ -255,6 +255,96 @@ def traffic_from_profiles():
     return None
 
 
+def decode_extras(device, prompt_len=64, new_tokens=128):
+    """Packed Pollux-1920 decoder (18 layers, d 1920, vocab 50,688; random packed weights): tokens/s at batch 1.
+
+    graph: GraphDecoder (KV cache, one HIP graph replay per token, greedy
+    argmax on the device); eager: the same cached decode as plain module
+    calls; recompute: the reference's loop (generate.py:313-315), the full
+    prefix per token, once with the packed layers fused and once the
+    reference's way (materialised fp16 weights cast to fp32 by every
+    F.linear call, pollux.py:507).
+    """
+    import torch
+
+    from pollux_amd import castor
+    from pollux_amd.model import GraphDecoder, PackedPolluxModel
+    from pollux_amd.plx import PLX_FORMAT
+
+    cfg = {"n_layers": 18, "n_heads": 80, "d_head": 24, "n_embd": 1920, "vocab_size": 50688,
+           "tokenizer_vocab_size": 50257, "seq_len": 1024}
+    g = torch.Generator(device=device).manual_seed(1920)
+    d, v = cfg["n_embd"], cfg["vocab_size"]
+    state = {"pos_emb.weight": torch.randn(cfg["seq_len"], d, generator=g, device=device) * 0.02,
+             "ln_f.weight": torch.ones(d, device=device)}
+    for name, rows in (("tok_emb", v), ("head", v)):
+        state[name + ".weight_int8"] = torch.randint(-127, 128, (rows, d), generator=g, device=device,
+                                                     dtype=torch.int8)
+        state[name + ".mu_rows"] = (torch.rand(rows, generator=g, device=device) * 0.1 + 0.01).half()
+    shapes = {"attn.q_proj": (d, d), "attn.k_proj": (d, d), "attn.v_proj": (d, d), "attn.o_proj": (d, d),
+              "mlp.fc1": (4 * d, d), "mlp.fc2": (d, 4 * d)}
+    for i in range(cfg["n_layers"]):
+        p = f"blocks.{i}."
+        for k in ("ln1.weight", "ln2.weight"):
+            state[p + k] = torch.ones(d, device=device)
+        state[p + "attn.q_ln.weight"] = torch.ones(24, device=device)
+        state[p + "attn.k_ln.weight"] = torch.ones(24, device=device)
+        for name, (o, i_) in shapes.items():
+            idx = torch.randint(0, 196561, (o * i_ // 24,), generator=g, device=device)
+            state[p + name + ".packed_weights"] = castor.pack_indices(idx)
+            state[p + name + ".sigma_rows"] = (torch.rand(o, generator=g, device=device) * 0.045 + 0.005).half()
+    payload = {"format": PLX_FORMAT, "config": cfg, "codebook_fingerprint": castor.codebook_fingerprint(),
+               "state_dict": state}
+    model = PackedPolluxModel.from_packed_checkpoint(payload, device)
+    prompt = torch.randint(0, 50257, (1, prompt_len), generator=g, device=device)
+
+    def timed(fn, n):
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        fn(n)
+        e1.record()
+        e1.synchronize()
+        return e0.elapsed_time(e1) / 1e3 / n
+
+    out = {}
+    with torch.inference_mode():
+        dec = GraphDecoder(model, batch=1)
+        nxt = dec.prefill(prompt).argmax(-1)
+
+        def run_graph(n):
+            t = nxt
+            for _ in range(n):
+                t = dec.decode(t).argmax(-1)
+
+        run_graph(4)
+        dec.prefill(prompt)
+        t_graph = timed(run_graph, new_tokens)
+        cache = model.new_cache(1)
+        first = model.prefill(prompt, cache)[:, -1].argmax(-1)
+
+        def run_eager(n):
+            t = first
+            for _ in range(n):
+                t = model.decode(t, cache).argmax(-1)
+
+        t_eager = timed(run_eager, 32)
+        seq = torch.cat([prompt, prompt[:, :1]], dim=1)
+        t_recompute = timed(lambda n: [model(seq)[:, -1].argmax(-1) for _ in range(n)], 4)
+        del dec, cache
+        dense = PackedPolluxModel.from_packed_checkpoint(payload, device, materialize=True)
+        t_dense = timed(lambda n: [dense(seq)[:, -1].argmax(-1) for _ in range(n)], 4)
+        del dense
+    out["graph_cached_tokens_per_s"] = 1.0 / t_graph
+    out["graph_cached_ms_per_token"] = t_graph * 1e3
+    out["eager_cached_tokens_per_s"] = 1.0 / t_eager
+    out["recompute_fused_tokens_per_s"] = 1.0 / t_recompute
+    out["recompute_reference_dense_tokens_per_s"] = 1.0 / t_dense
+    out["note"] = (f"batch 1, prompt {prompt_len} tokens, {new_tokens} greedy tokens (graph); recompute rows at a "
+                   f"{prompt_len + 1}-token prefix; random packed weights (valid indices), fp32 activations")
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -382,6 +472,7 @@ def main() -> int:
         result["extras"]["dequant_linear"] = gemv_extras(dev)
         result["extras"]["optimizer_step"] = optim_extras(dev, mats)
         result["extras"]["pack_time_nn_p"] = pack_time_extras(mats)
+        result["extras"]["packed_decode"] = decode_extras(dev)
     if not args.no_cpu_baseline:
         log(f"[bench] CPU baseline on {args.cpu_atoms} atoms")
         result["cpu_baseline"] = cpu_baseline(mats, args.cpu_atoms)

@@ -213,6 +213,27 @@ int plx_dequant_linear(const uint8_t *packed, int64_t n_packed_bytes, const uint
                        int64_t rows, int64_t cols, const void *x, int flags, int64_t m_rows,
                        float *y, void *workspace, size_t workspace_bytes, void *stream);
 
+/* ---- packed decoder steps ------------------------------------------------
+ * No counterpart in the reference's FFI: the reference runs these steps as
+ * torch ops.  They serve the KV-cached decode of the packed Pollux decoder
+ * (pollux_amd.model), one kernel each instead of a chain of elementwise and
+ * reduction kernels. */
+/* y[r, :] = x[r, :] * rsqrt(mean(x[r, :]^2) + eps) * w, fp32 x, y [rows, d] and
+ * w [d], d % 4 == 0, 16-byte aligned, y not overlapping x (RMSNorm.forward,
+ * pollux.py:580-582). */
+int plx_rms_norm(const float *x, const float *w, float *y, int64_t rows, int64_t d, float eps, void *stream);
+
+/* The attention of one new token per sequence (pollux.py:615-626 at the last
+ * position).  q, k, v: fp32 [n, 24] projections of the new token, n = sequences
+ * x heads; q_norm_w, k_norm_w: fp32 [24] (q_ln, k_ln weights); caches fp32
+ * [n, max_len, 24] (16-byte aligned); *pos: the new token's position (device
+ * int64).  Writes RMSNorm(k) and v at position *pos, then out fp32 [n, 24] =
+ * softmax_{j <= pos}(RMSNorm(q) . K_j / sqrt 24) V_j.  A position outside
+ * 0..max_len-1 writes nothing to the caches and sets out to NaN. */
+int plx_decode_attention(const float *q, const float *k, const float *v, const float *q_norm_w,
+                         const float *k_norm_w, float eps, float *k_cache, float *v_cache,
+                         const int64_t *pos, int64_t n, int64_t max_len, float *out, void *stream);
+
 /* ---- per-row INT8 periphery (embeddings / LM head in .plx files) ------- */
 /* q_out int8[rows*cols] = int8(clamp(rint((w / mu) * 127), -128, 127)),
  * mu16_out[r] = fp16(mu) with mu = max(max_j |w[r,j]|, 1e-8); all fp32 IEEE ops.

@@ -243,6 +243,25 @@ int plx_dequant_f16(const uint8_t *packed, int64_t n_packed_bytes, const uint16_
   return launch_dequant_f16(packed, sigma16, rows, cols, w16_out, as_stream(stream));
 }
 
+int plx_rms_norm(const float *x, const float *w, float *y, int64_t rows, int64_t d, float eps, void *stream) {
+  PLX_REQUIRE(rows >= 0 && d > 0, "plx_rms_norm: bad shape (%lld, %lld)", static_cast<long long>(rows),
+              static_cast<long long>(d));
+  if (rows == 0) return PLX_OK;
+  PLX_REQUIRE(x != nullptr && w != nullptr && y != nullptr, "plx_rms_norm: null pointer");
+  return launch_rms_norm(x, w, y, rows, d, eps, as_stream(stream));
+}
+
+int plx_decode_attention(const float *q, const float *k, const float *v, const float *q_norm_w,
+                         const float *k_norm_w, float eps, float *k_cache, float *v_cache, const int64_t *pos,
+                         int64_t n, int64_t max_len, float *out, void *stream) {
+  PLX_REQUIRE(n >= 0, "plx_decode_attention: negative head count");
+  if (n == 0) return PLX_OK;
+  PLX_REQUIRE(q && k && v && q_norm_w && k_norm_w && k_cache && v_cache && pos && out,
+              "plx_decode_attention: null pointer");
+  return launch_decode_attention(q, k, v, q_norm_w, k_norm_w, eps, k_cache, v_cache, pos, n, max_len, out,
+                                 as_stream(stream));
+}
+
 size_t plx_dequant_linear_workspace_bytes(int64_t rows, int64_t cols, int64_t m_rows, int flags) {
   if (rows <= 0 || cols <= 0 || cols % kDim != 0 || m_rows <= 0) return 0;
   return dequant_linear_workspace_bytes(rows, cols, m_rows, flags);

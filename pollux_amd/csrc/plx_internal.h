@@ -81,6 +81,10 @@ int launch_requantize_batch(const RequantItem *items, int n_items, int mode, voi
 int launch_gather(const int32_t *idx, int64_t n, int out_dtype, void *out, hipStream_t s);
 int launch_dequant_f16(const uint8_t *packed, const uint16_t *sigma16, int64_t rows, int64_t cols,
                        uint16_t *w16, hipStream_t s);
+int launch_rms_norm(const float *x, const float *w, float *y, int64_t rows, int64_t d, float eps, hipStream_t s);
+int launch_decode_attention(const float *q, const float *k, const float *v, const float *q_w, const float *k_w,
+                            float eps, float *k_cache, float *v_cache, const int64_t *pos, int64_t seqs_heads,
+                            int64_t max_len, float *out, hipStream_t s);
 size_t dequant_linear_workspace_bytes(int64_t rows, int64_t cols, int64_t m, int flags);
 int launch_dequant_linear(const uint8_t *packed, const uint16_t *sigma16, int64_t rows, int64_t cols, const void *x,
                           int flags, int64_t m, float *y, void *workspace, size_t workspace_bytes, hipStream_t s);

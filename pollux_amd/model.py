@@ -29,6 +29,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
+from . import _lib
 from .castor import H24_DIM, assert_row_aligned_width
 from .packed import PackedH24Linear, PackedInt8Embedding, PackedInt8Linear
 from .plx import check_fingerprint, load_plx
@@ -89,8 +90,44 @@ class PolluxConfig:
             raise ValueError(f"vocab_size ({vocab}) must cover tokenizer_vocab_size ({tok_vocab}).")
 
 
+def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
+    """x * rsqrt(mean(x^2) + eps) * weight over the last dimension, one HIP kernel (plx_rms_norm)."""
+    _lib.require_device(x, "rms_norm input")
+    if x.dtype != torch.float32 or weight.dtype != torch.float32:
+        raise ValueError("rms_norm runs on fp32 activations and weights")
+    xx = x.contiguous()
+    w = weight.detach().contiguous()
+    y = torch.empty_like(xx)
+    d = xx.shape[-1]
+    with torch.cuda.device(xx.device):
+        st = _lib.lib().plx_rms_norm(_lib.ptr(xx), _lib.ptr(w), _lib.ptr(y), xx.numel() // d if d else 0, d,
+                                     float(eps), _lib.stream_of(xx.device))
+    _lib.check(st, "rms_norm")
+    return y
+
+
+def decode_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q_ln: RMSNorm, k_ln: RMSNorm,
+                     k_cache: torch.Tensor, v_cache: torch.Tensor, pos: torch.Tensor) -> torch.Tensor:
+    """Attention of one new token per sequence over the cache (plx_decode_attention).
+
+    q, k, v: [b, 1, H*24] projections; caches [b, H, max_len, 24]; pos: 0-dim
+    int64 device tensor.  Writes k_ln(k) and v at ``pos``; returns [b, 1, H*24].
+    """
+    b, t, c = q.shape
+    n = b * (c // H24_DIM)
+    out = torch.empty_like(q)
+    qq, kk, vv = q.contiguous(), k.contiguous(), v.contiguous()
+    with torch.cuda.device(q.device):
+        st = _lib.lib().plx_decode_attention(
+            _lib.ptr(qq), _lib.ptr(kk), _lib.ptr(vv), _lib.ptr(q_ln.weight.detach()), _lib.ptr(k_ln.weight.detach()),
+            float(q_ln.eps), _lib.ptr(k_cache), _lib.ptr(v_cache), _lib.ptr(pos), n, k_cache.shape[2], _lib.ptr(out),
+            _lib.stream_of(q.device))
+    _lib.check(st, "decode_attention")
+    return out
+
+
 class RMSNorm(nn.Module):
-    """x * rsqrt(mean(x^2) + eps) * weight over the last dimension (pollux.py:566-582)."""
+    """x * rsqrt(mean(x^2) + eps) * weight over the last dimension (pollux.py:566-582), fused on the device."""
 
     def __init__(self, dim: int, eps: float = 1e-8) -> None:
         super().__init__()
@@ -98,7 +135,7 @@ class RMSNorm(nn.Module):
         self.weight = nn.Parameter(torch.ones(dim))
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        return x * torch.rsqrt(x.pow(2).mean(dim=-1, keepdim=True) + self.eps) * self.weight
+        return rms_norm(x, self.weight, self.eps)
 
 
 @dataclass
@@ -134,8 +171,16 @@ class PackedCausalAttention(nn.Module):
         self.q_ln = RMSNorm(self.d_head)  # per-head Q/K norms on the 24-d atom
         self.k_ln = RMSNorm(self.d_head)
 
-    def forward(self, x: torch.Tensor, cache: KVCache | None = None, layer: int = 0) -> torch.Tensor:
+    def forward(self, x: torch.Tensor, cache: KVCache | None = None, layer: int = 0,
+                pos: torch.Tensor | None = None) -> torch.Tensor:
         b, t, c = x.shape
+        if cache is not None and t == 1:
+            # one new token per sequence: norms, cache write and attention in one kernel at device position pos
+            if pos is None:
+                pos = torch.full((), cache.length, dtype=torch.long, device=x.device)
+            o = decode_attention(self.q_proj(x), self.k_proj(x), self.v_proj(x), self.q_ln, self.k_ln,
+                                 cache.k[layer], cache.v[layer], pos)
+            return self.o_proj(o)
         q = self.q_ln(self.q_proj(x).view(b, t, self.n_heads, self.d_head)).transpose(1, 2)
         k = self.k_ln(self.k_proj(x).view(b, t, self.n_heads, self.d_head)).transpose(1, 2)
         v = self.v_proj(x).view(b, t, self.n_heads, self.d_head).transpose(1, 2)
@@ -148,8 +193,6 @@ class PackedCausalAttention(nn.Module):
             keys, vals = cache.k[layer][:, :, :p0 + t], cache.v[layer][:, :, :p0 + t]
             if p0 == 0:
                 attn = F.scaled_dot_product_attention(q, keys, vals, is_causal=True)
-            elif t == 1:
-                attn = F.scaled_dot_product_attention(q, keys, vals)  # every cached position is visible
             else:
                 # query i sits at position p0 + i and sees positions <= p0 + i
                 allowed = torch.ones(t, p0 + t, dtype=torch.bool, device=x.device).tril(diagonal=p0)
@@ -180,8 +223,9 @@ class PackedBlock(nn.Module):
         self.ln2 = RMSNorm(int(cfg.n_embd))
         self.mlp = PackedMLP(cfg)
 
-    def forward(self, x: torch.Tensor, cache: KVCache | None = None, layer: int = 0) -> torch.Tensor:
-        x = x + self.attn(self.ln1(x), cache, layer)
+    def forward(self, x: torch.Tensor, cache: KVCache | None = None, layer: int = 0,
+                pos: torch.Tensor | None = None) -> torch.Tensor:
+        x = x + self.attn(self.ln1(x), cache, layer, pos)
         return x + self.mlp(self.ln2(x))
 
 
@@ -203,8 +247,9 @@ class PackedPolluxModel(nn.Module):
         t = idx.shape[1]
         pos = torch.arange(pos0, pos0 + t, device=idx.device).unsqueeze(0)
         x = self.tok_emb(idx) + self.pos_emb(pos)
+        step_pos = pos.view(()) if (cache is not None and t == 1) else None
         for i, block in enumerate(self.blocks):
-            x = block(x, cache, i)
+            x = block(x, cache, i, step_pos)
         if cache is not None:
             cache.length = pos0 + t
         return self.head(self.ln_f(x))
@@ -267,6 +312,78 @@ class PackedPolluxModel(nn.Module):
             elif materialize and isinstance(module, PackedH24Linear):
                 module.materialize()
         return model
+
+
+class GraphDecoder:
+    """One-token decode steps of ``model`` replayed from a captured HIP graph.
+
+    Static buffers: the token ids [batch], the position (a 0-dim device
+    tensor the graph advances itself), the KV cache at its full length, and
+    the logits.  The step is the eager modules' one-token path (fused packed
+    linears, RMS norms and attention kernels, which read the position from
+    the device), captured once.
+    Usage: ``dec.prefill(prompt_ids)`` then ``logits = dec.decode(next_ids)``
+    per token; the returned logits tensor is reused by the next replay.
+    """
+
+    def __init__(self, model: PackedPolluxModel, batch: int = 1, max_len: int | None = None) -> None:
+        self.model = model
+        cfg = model.cfg
+        self.max_len = int(min(max_len or cfg.seq_len, cfg.seq_len))
+        device = model.pos_emb.weight.device
+        self.cache = model.new_cache(batch, self.max_len)
+        self.ids = torch.zeros(batch, dtype=torch.long, device=device)
+        self.pos = torch.zeros((), dtype=torch.long, device=device)
+        self.length = 0
+        self.graph = None
+        self.logits = None
+
+    def _step(self) -> torch.Tensor:
+        m = self.model
+        b = self.ids.shape[0]
+        x = m.tok_emb(self.ids.view(b, 1)) + m.pos_emb(self.pos.view(1, 1))
+        for i, blk in enumerate(m.blocks):
+            x = blk(x, self.cache, i, self.pos)
+        self.pos += 1
+        return m.head(m.ln_f(x))[:, -1]
+
+    @torch.inference_mode()
+    def prefill(self, idx: torch.Tensor) -> torch.Tensor:
+        """Eager prefill of ``idx`` [batch, t] from position 0; returns the logits of its last position."""
+        self.cache.length = 0
+        out = self.model.prefill(idx, self.cache)[:, -1]
+        self.length = idx.shape[1]
+        self.pos.fill_(self.length)
+        if self.graph is None:
+            self._capture()
+        return out
+
+    def _capture(self) -> None:
+        saved = self.length
+        side = torch.cuda.Stream(self.pos.device)
+        side.wait_stream(torch.cuda.current_stream(self.pos.device))
+        with torch.cuda.stream(side):
+            for _ in range(2):  # warm-up (lazy casts, allocator); writes only positions >= length
+                self.pos.fill_(saved)
+                self._step()
+        torch.cuda.current_stream(self.pos.device).wait_stream(side)
+        self.pos.fill_(saved)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self.logits = self._step()
+        self.pos.fill_(saved)  # capture does not run the step
+
+    @torch.inference_mode()
+    def decode(self, next_ids: torch.Tensor) -> torch.Tensor:
+        """Logits [batch, vocab] of one new token per sequence at the next position."""
+        if self.graph is None:
+            raise RuntimeError("GraphDecoder.decode before prefill")
+        if self.length >= self.max_len:
+            raise ValueError(f"the cache holds {self.max_len} positions")
+        self.ids.copy_(next_ids.reshape(-1))
+        self.graph.replay()
+        self.length += 1
+        return self.logits
 
 
 # ---- sampling (generate.py:228-278) ------------------------------------------------

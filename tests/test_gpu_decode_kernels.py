@@ -1,0 +1,94 @@
+"""plx_rms_norm and plx_decode_attention (the packed decoder's fused steps) against torch fp32 references.
+
+Bars (stated): RMS norm within 2e-6 relative per element of the torch
+expression x * rsqrt(mean(x^2) + eps) * w (pollux.py:580-582); decode
+attention within 1e-5 relative (L2) of scaled_dot_product_attention over the
+cache with the new row appended, the written cache row within 2e-6 of the
+normalised k and v bit-exact, every other cache row untouched; a position
+outside the cache writes nothing and returns NaN.
+"""
+
+import math
+
+import pytest
+import torch
+
+from pollux_amd.model import RMSNorm, decode_attention, rms_norm
+
+pytestmark = pytest.mark.gpu
+
+
+def _ref_norm(x, w, eps=1e-8):
+    return x * torch.rsqrt(x.pow(2).mean(dim=-1, keepdim=True) + eps) * w
+
+
+@pytest.mark.parametrize("rows,d", [(37, 1920), (80, 24), (1, 7680), (513, 48)])
+def test_rms_norm(dev, rows, d):
+    g = torch.Generator().manual_seed(rows + d)
+    x = (torch.randn(rows, d, generator=g) * 3.0).to(dev)
+    w = (1.0 + 0.1 * torch.randn(d, generator=g)).to(dev)
+    y = rms_norm(x, w, 1e-8)
+    ref = _ref_norm(x.double(), w.double())
+    err = ((y.double() - ref).abs() / ref.abs().clamp_min(1e-30)).max().item()
+    print(f"[dec] rms_norm {rows}x{d}: max rel {err:.2e}", flush=True)
+    assert err <= 2e-6
+    with pytest.raises(ValueError):
+        rms_norm(x.double(), w.double(), 1e-8)
+
+
+def test_rms_norm_zero_row_and_module(dev):
+    x = torch.zeros(2, 48, device=dev)
+    x[1] = 1.0
+    m = RMSNorm(48).to(dev)
+    y = m(x)
+    assert torch.equal(y[0], torch.zeros(48, device=dev))  # eps keeps the zero row finite
+    assert torch.allclose(y[1], torch.ones(48, device=dev), rtol=1e-6)
+
+
+@pytest.mark.parametrize("b,heads,max_len,pos", [(1, 80, 1024, 64), (2, 3, 16, 0), (1, 5, 300, 299), (3, 2, 8, 5)])
+def test_decode_attention(dev, b, heads, max_len, pos):
+    g = torch.Generator().manual_seed(b * 1000 + heads + pos)
+    c = heads * 24
+    q = torch.randn(b, 1, c, generator=g).to(dev)
+    k = torch.randn(b, 1, c, generator=g).to(dev)
+    v = torch.randn(b, 1, c, generator=g).to(dev)
+    q_ln, k_ln = RMSNorm(24).to(dev), RMSNorm(24).to(dev)
+    with torch.no_grad():
+        q_ln.weight.copy_(1.0 + 0.1 * torch.randn(24, generator=g))
+        k_ln.weight.copy_(1.0 + 0.1 * torch.randn(24, generator=g))
+    kc = torch.randn(b, heads, max_len, 24, generator=g).to(dev)
+    vc = torch.randn(b, heads, max_len, 24, generator=g).to(dev)
+    kc0, vc0 = kc.clone(), vc.clone()
+    p = torch.tensor(pos, dtype=torch.long, device=dev)
+    with torch.no_grad():
+        out = decode_attention(q, k, v, q_ln, k_ln, kc, vc, p)
+    # reference: the new row appended at pos, causal attention of the last query
+    qn = _ref_norm(q.view(b, heads, 24).double(), q_ln.weight.detach().double())
+    kn = _ref_norm(k.view(b, heads, 24).double(), k_ln.weight.detach().double())
+    keys = kc0.double().clone()
+    vals = vc0.double().clone()
+    keys[:, :, pos] = kn
+    vals[:, :, pos] = v.view(b, heads, 24).double()
+    s = torch.einsum("bhc,bhjc->bhj", qn, keys[:, :, :pos + 1]) / math.sqrt(24)
+    ref = torch.einsum("bhj,bhjc->bhc", torch.softmax(s, dim=-1), vals[:, :, :pos + 1]).reshape(b, 1, c)
+    rel = ((out.double() - ref).norm() / ref.norm()).item()
+    print(f"[dec] decode_attention b={b} H={heads} L={max_len} pos={pos}: rel {rel:.2e}", flush=True)
+    assert rel <= 1e-5
+    assert ((kc[:, :, pos].double() - kn).abs() / kn.abs().clamp_min(1e-30)).max().item() <= 2e-6
+    assert torch.equal(vc[:, :, pos], v.view(b, heads, 24))
+    rest = [j for j in range(max_len) if j != pos]
+    assert torch.equal(kc[:, :, rest], kc0[:, :, rest]) and torch.equal(vc[:, :, rest], vc0[:, :, rest])
+
+
+def test_decode_attention_position_outside_cache(dev):
+    b, heads, max_len = 1, 2, 8
+    q = torch.randn(b, 1, 48, device=dev)
+    kc = torch.randn(b, heads, max_len, 24, device=dev)
+    vc = torch.randn(b, heads, max_len, 24, device=dev)
+    kc0, vc0 = kc.clone(), vc.clone()
+    ln = RMSNorm(24).to(dev)
+    for bad in (max_len, -1):
+        with torch.no_grad():
+            out = decode_attention(q, q, q, ln, ln, kc, vc, torch.tensor(bad, dtype=torch.long, device=dev))
+        assert torch.isnan(out).all()
+        assert torch.equal(kc, kc0) and torch.equal(vc, vc0)

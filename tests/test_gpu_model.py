@@ -136,3 +136,28 @@ def test_config_from_plx_payload(dev, packed):
         a = model(idx)
         b = PackedPolluxModel.from_packed_checkpoint(str(packed[0]), dev)(idx)
     assert torch.equal(a, b)
+
+
+def test_graph_decoder_matches_eager_decode(dev, packed):
+    # every replay of the captured step against the eager decode, across two prompts
+    from pollux_amd.model import GraphDecoder
+
+    model = PackedPolluxModel.from_packed_checkpoint(str(packed[0]), dev)
+    dec = GraphDecoder(model, batch=1)
+    g = torch.Generator().manual_seed(4)
+    worst = 0.0
+    for prompt_len in (3, 6):
+        idx = torch.randint(0, 90, (1, 16), generator=g).to(dev)
+        with torch.inference_mode():
+            first = dec.prefill(idx[:, :prompt_len])
+            cache = model.new_cache(1)
+            assert _rel(first, model.prefill(idx[:, :prompt_len], cache)[:, -1]) <= 1e-6
+            for s in range(prompt_len, 16):
+                got = dec.decode(idx[:, s]).clone()
+                torch.cuda.synchronize()
+                want = model.decode(idx[:, s], cache)
+                worst = max(worst, _rel(got, want))
+        with pytest.raises(ValueError):
+            dec.decode(idx[:, 0])  # the cache is full
+    print(f"[model] graph decode vs eager decode, worst rel {worst:.2e}", flush=True)
+    assert worst <= 1e-5
