@@ -204,9 +204,10 @@ size_t plx_dequant_linear_workspace_bytes(int64_t rows, int64_t cols, int64_t m_
  * the fp16 weights are exact and accumulated in fp32: the numerics of
  * F.linear(x.float(), W.float()).  With PLX_DQL_W_AS_X and bf16 x the weights
  * are rounded to bf16 (RNE) first.  Results are deterministic (fixed summation
- * order).  bf16 batches above 16 tokens need the workspace sized by
+ * order).  Batches above 16 tokens run on MFMA (fp32 x split exactly into
+ * three bf16 parts) and need the workspace sized by
  * plx_dequant_linear_workspace_bytes (a fragment-order copy of x, plus split
- * partial tiles for narrow layers); cols <= 2^23.
+ * partial tiles for narrow layers); cols <= 2^22.
  * Replaces PackedH24Linear.forward after materialize (pollux.py:506-507:
  * F.linear(x, weight.to(x.dtype))). */
 int plx_dequant_linear(const uint8_t *packed, int64_t n_packed_bytes, const uint16_t *sigma16,

@@ -395,7 +395,7 @@ constexpr int kMmMaxApb = 128;          // atoms of a row per block (kp_dq tile:
 constexpr int kMmTargetBlocks = 192;    // K is split until the grid holds about this many blocks
 constexpr int kMmRedStride = 36;        // floats per token in the cross-wave sum (conflict-free writes)
 constexpr int kXfQuadBytes = 3 * 4 * 1024;       // fragment-order x: 3 K steps x 4 token tiles x 64 lanes x 16 B
-constexpr int64_t kMmMaxCols = 1 << 23;           // a slab of fragment-order x stays far below 2^31 bytes
+constexpr int64_t kMmMaxCols = 1 << 22;           // a slab of fragment-order x (3 parts) stays below 2^31 bytes
 constexpr int kBufferFlags = 0x00020000;          // raw buffer descriptor word 3 on gfx9 (gfx950)
 constexpr int kBufferOutOfRange = 0x7FFFFFF0;     // a byte offset past every buffer range used here
 
@@ -446,22 +446,64 @@ __device__ __forceinline__ void group_codes(uint32_t d0, uint32_t d1, uint32_t d
   c[3] = static_cast<int32_t>(((lo & 0x3FFu) << 8) | b8);
 }
 
-// Fragment-order copy of the bf16 activations for dqmm_kernel, one 16-byte
-// fragment per thread: xf[slab][Q][s][t][lane] = x[64 slab + 16t + (lane & 15)]
-// [96Q + 32s + 8(lane >> 4) .. +8), zero for tokens >= m and columns >= cols.
-__global__ __launch_bounds__(256) void xfrag_kernel(const uint16_t *__restrict__ x, int64_t m_total, int64_t cols,
+// Fragment-order copy of the activations for dqmm_kernel.  One thread per
+// 16-byte fragment position (slab, quad Q, K step s, token tile t, lane):
+// x[64 slab + 16t + (lane & 15)][96Q + 32s + 8(lane >> 4) .. +8), zero for
+// tokens >= m and columns >= cols, stored at xf[slab][Q][part][s][t][lane].
+// bf16 x is one part.  fp32 x is split exactly into three bf16 parts, x = h +
+// m + l (h = bf16(x), m = bf16(x - h), l = x - h - m, exact while the parts
+// stay normal, |x| >= ~2^-110; inf / nan go to h alone), so that bf16 MFMAs
+// form the products of the fp32 activations.
+template <bool XF32>
+__global__ __launch_bounds__(256) void xfrag_kernel(const void *__restrict__ x, int64_t m_total, int64_t cols,
                                                     int64_t n_quads_row, uint4 *__restrict__ xf) {
-  const int64_t per_slab = n_quads_row * (kXfQuadBytes / 16);
-  const int64_t f = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;  // fragment within the slab
+  constexpr int XP = XF32 ? 3 : 1;
+  constexpr int kQuadFrags = kXfQuadBytes / 16;  // 768 per part
+  const int64_t per_slab = n_quads_row * kQuadFrags;
+  const int64_t f = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;  // fragment position within the slab
   if (f >= per_slab) return;
   const int lane = static_cast<int>(f & 63);
   const int64_t rest = f >> 6;  // (3Q + s) * 4 + t
   const int t = static_cast<int>(rest & 3);
+  const int64_t qs = rest >> 2;  // 3Q + s
+  const int64_t quad = qs / 3, within = f - quad * kQuadFrags;
   const int64_t tok = static_cast<int64_t>(blockIdx.y) * 64 + 16 * t + (lane & 15);
-  const int64_t col = 32 * (rest >> 2) + 8 * (lane >> 4);
-  uint4 v = make_uint4(0u, 0u, 0u, 0u);
-  if (tok < m_total && col < cols) v = *reinterpret_cast<const uint4 *>(x + tok * cols + col);
-  xf[static_cast<int64_t>(blockIdx.y) * per_slab + f] = v;
+  const int64_t col = 32 * qs + 8 * (lane >> 4);
+  uint4 *dst = xf + static_cast<int64_t>(blockIdx.y) * per_slab * XP + quad * XP * kQuadFrags + within;
+  const bool live = tok < m_total && col < cols;
+  if constexpr (!XF32) {
+    uint4 v = make_uint4(0u, 0u, 0u, 0u);
+    if (live) v = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(x) + tok * cols + col);
+    dst[0] = v;
+  } else {
+    float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    if (live) {
+      const float4 *src = reinterpret_cast<const float4 *>(static_cast<const float *>(x) + tok * cols + col);
+      const float4 a = src[0], b = src[1];
+      v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    }
+    uint32_t part[3][4];
+#pragma unroll
+    for (int e = 0; e < 8; e += 2) {
+      uint32_t hb[2], mb[2], lb[2];
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const float xv = v[e + u];
+        hb[u] = bf16_rne_bits(xv);
+        mb[u] = lb[u] = 0u;
+        if (fabsf(xv) <= 3.0e38f) {
+          const float r1 = xv - __uint_as_float(hb[u] << 16);
+          mb[u] = bf16_rne_bits(r1);
+          lb[u] = bf16_rne_bits(r1 - __uint_as_float(mb[u] << 16));
+        }
+      }
+      part[0][e / 2] = hb[0] | (hb[1] << 16);
+      part[1][e / 2] = mb[0] | (mb[1] << 16);
+      part[2][e / 2] = lb[0] | (lb[1] << 16);
+    }
+#pragma unroll
+    for (int pp = 0; pp < 3; ++pp) dst[pp * kQuadFrags] = make_uint4(part[pp][0], part[pp][1], part[pp][2], part[pp][3]);
+  }
 }
 
 // (hi | lo << 16) with hi + lo == v exactly for an fp16 value v (lo = 0 for inf / nan)
@@ -471,8 +513,9 @@ __device__ __forceinline__ uint32_t hi_lo_pack(float v) {
   return hb | (bf16_rne_bits(v - __uint_as_float(hb << 16)) << 16);
 }
 
-// token tiles of 16; waves per block; quads of x in flight per wave; exact fp16 weights (hi + lo)
-template <int MT, int WV, int PD, bool EXACT>
+// token tiles of 16; waves per block; quads of x in flight per wave; exact fp16 weights (hi + lo);
+// bf16 parts per activation (1: bf16 x; 3: fp32 x, see xfrag_kernel)
+template <int MT, int WV, int PD, bool EXACT, int XP>
 __global__ __launch_bounds__(64 * WV, WV <= 4 ? 2 : 1) void dqmm_kernel(
     const uint8_t *__restrict__ packed, int64_t packed_bytes, const uint16_t *__restrict__ sigma16, int64_t rows,
     int64_t atoms_per_row, const uint4 *__restrict__ xf, int64_t n_quads_row, int64_t m_total, int splits, int apb,
@@ -506,23 +549,26 @@ __global__ __launch_bounds__(64 * WV, WV <= 4 ? 2 : 1) void dqmm_kernel(
   // out-of-range offset, which returns zeros without touching memory, so the
   // loads need no branches (the compiler can then wait for one quad's loads
   // while the next quads' stay in flight).
-  const int slab_bytes = static_cast<int>(n_quads_row * kXfQuadBytes);
+  const int slab_bytes = static_cast<int>(n_quads_row * XP * kXfQuadBytes);
   const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint4 *>(xf + static_cast<int64_t>(blockIdx.y) * (slab_bytes / 16)), static_cast<short>(0), slab_bytes,
       kBufferFlags);
-  const int xbase = static_cast<int>(a_begin / 4 + wq0) * kXfQuadBytes + 16 * lane;
-  auto load_quad = [&](uint4 (&xa)[3][MT], int qd) {
+  const int xbase = static_cast<int>(a_begin / 4 + wq0) * XP * kXfQuadBytes + 16 * lane;
+  auto load_quad = [&](uint4 (&xa)[3][XP][MT], int qd) {
 #pragma unroll
     for (int s = 0; s < 3; ++s) {
 #pragma unroll
-      for (int t = 0; t < MT; ++t) {
-        int off = qd < wqn ? xbase + qd * kXfQuadBytes + (4 * s + t) * 1024 : kBufferOutOfRange;
-        asm("" : "+v"(off));  // one unconditional load (not one per select outcome under branches)
-        xa[s][t] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(xrs, off, 0, 0));
+      for (int pp = 0; pp < XP; ++pp) {
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+          int off = qd < wqn ? xbase + (qd * XP + pp) * kXfQuadBytes + (4 * s + t) * 1024 : kBufferOutOfRange;
+          asm("" : "+v"(off));  // one unconditional load (not one per select outcome under branches)
+          xa[s][pp][t] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(xrs, off, 0, 0));
+        }
       }
     }
   };
-  uint4 xa[PD][3][MT];
+  uint4 xa[PD][3][XP][MT];
 #pragma unroll
   for (int u = 0; u < PD; ++u) load_quad(xa[u], u);  // in flight during the prologue
 
@@ -642,27 +688,32 @@ __global__ __launch_bounds__(64 * WV, WV <= 4 ? 2 : 1) void dqmm_kernel(
   // word of (row, block atom a, plane p) = 3a + p; K step s of quad Q, lane group q: 12Q + 4s + q
   const uint32_t *wrow0 = wt + j * ws + 12 * wq0 + q;
   const uint32_t *wrow1 = wt + (16 + j) * ws + 12 * wq0 + q;
-  auto compute_quad = [&](const uint4 (&xa_q)[3][MT], int qd) {
+  auto compute_quad = [&](const uint4 (&xa_q)[3][XP][MT], int qd) {
 #pragma unroll
     for (int s = 0; s < 3; ++s) {
       const uint32_t w0 = wrow0[12 * qd + 4 * s], w1 = wrow1[12 * qd + 4 * s];
       const bf16x8_t b0 = perm_decode(w0, ta0.x, ta0.y, ta0.z, ta0.w);
       const bf16x8_t b1 = perm_decode(w1, ta1.x, ta1.y, ta1.z, ta1.w);
 #pragma unroll
-      for (int t = 0; t < MT; ++t) {
-        const bf16x8_t av = __builtin_bit_cast(bf16x8_t, xa_q[s][t]);
-        acc[t][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, b0, acc[t][0], 0, 0, 0);
-        acc[t][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, b1, acc[t][1], 0, 0, 0);
-      }
+      for (int pp = 0; pp < XP; ++pp)
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+          const bf16x8_t av = __builtin_bit_cast(bf16x8_t, xa_q[s][pp][t]);
+          acc[t][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, b0, acc[t][0], 0, 0, 0);
+          acc[t][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, b1, acc[t][1], 0, 0, 0);
+        }
       if constexpr (EXACT) {
         const bf16x8_t l0 = perm_decode(w0, tb0.x, tb0.y, tb0.z, tb0.w);
         const bf16x8_t l1 = perm_decode(w1, tb1.x, tb1.y, tb1.z, tb1.w);
+        // the third activation part times the weights' low part is below 2^-25 of the product: skipped
 #pragma unroll
-        for (int t = 0; t < MT; ++t) {
-          const bf16x8_t av = __builtin_bit_cast(bf16x8_t, xa_q[s][t]);
-          acc[t][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, l0, acc[t][0], 0, 0, 0);
-          acc[t][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, l1, acc[t][1], 0, 0, 0);
-        }
+        for (int pp = 0; pp < (XP == 3 ? 2 : XP); ++pp)
+#pragma unroll
+          for (int t = 0; t < MT; ++t) {
+            const bf16x8_t av = __builtin_bit_cast(bf16x8_t, xa_q[s][pp][t]);
+            acc[t][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, l0, acc[t][0], 0, 0, 0);
+            acc[t][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, l1, acc[t][1], 0, 0, 0);
+          }
       }
     }
     // keep the fragments in their registers until the slot is refilled, so no
@@ -670,7 +721,9 @@ __global__ __launch_bounds__(64 * WV, WV <= 4 ? 2 : 1) void dqmm_kernel(
 #pragma unroll
     for (int s = 0; s < 3; ++s)
 #pragma unroll
-      for (int t = 0; t < MT; ++t) asm volatile("" : : "v"(__builtin_bit_cast(u32x4_t, xa_q[s][t])));
+      for (int pp = 0; pp < XP; ++pp)
+#pragma unroll
+        for (int t = 0; t < MT; ++t) asm volatile("" : : "v"(__builtin_bit_cast(u32x4_t, xa_q[s][pp][t])));
   };
   // Whole rounds of PD quads without branches, then the last < PD quads.  The
   // first round is peeled: the loop header then sees the same loads in flight
@@ -769,7 +822,7 @@ MmPlan mm_plan(int64_t rows, int64_t apr) {
   return p;
 }
 
-template <int MT, int WV, int PD, bool EXACT>
+template <int MT, int WV, int PD, bool EXACT, int XP>
 int launch_dqmm_t(const uint8_t *packed, int64_t pb, const uint16_t *sigma16, int64_t rows, int64_t apr,
                   const uint4 *xf, int64_t m, float *y, float *partial, const MmPlan &pl, const uint32_t *kp_dq,
                   hipStream_t s) {
@@ -779,7 +832,7 @@ int launch_dqmm_t(const uint8_t *packed, int64_t pb, const uint16_t *sigma16, in
   const size_t region = static_cast<size_t>(max(kMmRows * mm_row_words(pl.apb), WV * 16 * MT * kMmRedStride)) * 4;
   const size_t shm = region + static_cast<size_t>(kMmRows) * 16 * (EXACT ? 2 : 1);
   const dim3 g(static_cast<unsigned>(row_blocks * pl.splits), static_cast<unsigned>(slabs));
-  hipLaunchKernelGGL((dqmm_kernel<MT, WV, PD, EXACT>), g, dim3(64 * WV), shm, s, packed, pb, sigma16, rows, apr, xf, nq, m,
+  hipLaunchKernelGGL((dqmm_kernel<MT, WV, PD, EXACT, XP>), g, dim3(64 * WV), shm, s, packed, pb, sigma16, rows, apr, xf, nq, m,
                      pl.splits, pl.apb, kp_dq, y, partial);
   return check_launch("dqmm_kernel");
 }
@@ -787,11 +840,12 @@ int launch_dqmm_t(const uint8_t *packed, int64_t pb, const uint16_t *sigma16, in
 template <int MT>
 int launch_dqmm(const uint8_t *packed, int64_t pb, const uint16_t *sigma16, int64_t rows, int64_t apr,
                 const uint4 *xf, int64_t m, float *y, float *partial, const MmPlan &pl, const uint32_t *kp_dq,
-                bool exact, hipStream_t s) {
+                bool exact, bool x_f32, hipStream_t s) {
   // 8 waves (two per SIMD cover each other's load latency), one quad of x in
   // flight per wave; 4 waves with 2 quads in flight measured within 3%
-  if (exact) return launch_dqmm_t<MT, 8, 1, true>(packed, pb, sigma16, rows, apr, xf, m, y, partial, pl, kp_dq, s);
-  return launch_dqmm_t<MT, 8, 1, false>(packed, pb, sigma16, rows, apr, xf, m, y, partial, pl, kp_dq, s);
+  if (x_f32) return launch_dqmm_t<MT, 8, 1, true, 3>(packed, pb, sigma16, rows, apr, xf, m, y, partial, pl, kp_dq, s);
+  if (exact) return launch_dqmm_t<MT, 8, 1, true, 1>(packed, pb, sigma16, rows, apr, xf, m, y, partial, pl, kp_dq, s);
+  return launch_dqmm_t<MT, 8, 1, false, 1>(packed, pb, sigma16, rows, apr, xf, m, y, partial, pl, kp_dq, s);
 }
 
 // Workspace of the batched path: the fragment-order x copy (a multiple of 256
@@ -801,21 +855,21 @@ struct MmWorkspace {
   size_t total() const { return xf + partial; }
 };
 
-MmWorkspace mm_workspace(int64_t rows, int64_t cols, int64_t m, const MmPlan &pl) {
+MmWorkspace mm_workspace(int64_t rows, int64_t cols, int64_t m, const MmPlan &pl, bool x_f32) {
   MmWorkspace w;
   const size_t slabs = static_cast<size_t>((m + 63) / 64);
-  w.xf = slabs * static_cast<size_t>((cols / kDim + 3) / 4) * kXfQuadBytes;
+  w.xf = slabs * static_cast<size_t>((cols / kDim + 3) / 4) * kXfQuadBytes * (x_f32 ? 3 : 1);
   if (pl.splits > 1) w.partial = slabs * pl.splits * 64 * static_cast<size_t>(rows) * sizeof(float);
   return w;
 }
 
-bool uses_mfma(int flags, int64_t m) { return !(flags & PLX_DQL_X_F32) && m > 16; }
+bool uses_mfma(int /*flags*/, int64_t m) { return m > 16; }
 
 }  // namespace
 
 size_t dequant_linear_workspace_bytes(int64_t rows, int64_t cols, int64_t m, int flags) {
   if (!uses_mfma(flags, m) || rows <= 0 || cols <= 0) return 0;
-  return mm_workspace(rows, cols, m, mm_plan(rows, cols / kDim)).total();
+  return mm_workspace(rows, cols, m, mm_plan(rows, cols / kDim), (flags & PLX_DQL_X_F32) != 0).total();
 }
 
 int launch_dequant_linear(const uint8_t *packed, const uint16_t *sigma16, int64_t rows, int64_t cols, const void *x,
@@ -835,22 +889,25 @@ int launch_dequant_linear(const uint8_t *packed, const uint16_t *sigma16, int64_
   const int64_t apr = cols / kDim;
   const int64_t pb = ((rows * apr + 3) / 4) * 9;  // packed stream length
   if (uses_mfma(flags, m)) {
-    // bf16 batches above 16 tokens: MFMA dequant-GEMM in slabs of 64 tokens
+    // batches above 16 tokens: MFMA dequant-GEMM in slabs of 64 tokens
     if (cols > kMmMaxCols)
       return fail(PLX_EINVAL, "dequant_linear: %lld columns exceed the batched path's %lld", static_cast<long long>(cols),
                   static_cast<long long>(kMmMaxCols));
     const MmPlan pl = mm_plan(rows, apr);
-    const MmWorkspace w = mm_workspace(rows, cols, m, pl);
+    const MmWorkspace w = mm_workspace(rows, cols, m, pl, x_is_f32 != 0);
     uint8_t *wsb = static_cast<uint8_t *>(workspace);
     uint4 *xf = reinterpret_cast<uint4 *>(wsb);
     float *part = reinterpret_cast<float *>(wsb + w.xf);
     const int64_t slabs = (m + 63) / 64, nq = (apr + 3) / 4;
-    hipLaunchKernelGGL(xfrag_kernel, dim3(static_cast<unsigned>(nq * 3), static_cast<unsigned>(slabs)), dim3(256), 0, s,
-                       static_cast<const uint16_t *>(x), m, cols, nq, xf);
+    const dim3 gx(static_cast<unsigned>(nq * 3), static_cast<unsigned>(slabs));
+    if (x_is_f32)
+      hipLaunchKernelGGL((xfrag_kernel<true>), gx, dim3(256), 0, s, x, m, cols, nq, xf);
+    else
+      hipLaunchKernelGGL((xfrag_kernel<false>), gx, dim3(256), 0, s, x, m, cols, nq, xf);
     st = check_launch("xfrag_kernel");
     if (st != PLX_OK) return st;
-    st = m > 32 ? launch_dqmm<4>(packed, pb, sigma16, rows, apr, xf, m, y, part, pl, tab->kp_dq, !round_w, s)
-                : launch_dqmm<2>(packed, pb, sigma16, rows, apr, xf, m, y, part, pl, tab->kp_dq, !round_w, s);
+    st = m > 32 ? launch_dqmm<4>(packed, pb, sigma16, rows, apr, xf, m, y, part, pl, tab->kp_dq, !round_w, x_is_f32, s)
+                : launch_dqmm<2>(packed, pb, sigma16, rows, apr, xf, m, y, part, pl, tab->kp_dq, !round_w, x_is_f32, s);
     if (st != PLX_OK || pl.splits == 1) return st;
     const int64_t n = m * rows;
     if (rows % 4 == 0 && (reinterpret_cast<uintptr_t>(y) & 15u) == 0)

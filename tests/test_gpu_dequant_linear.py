@@ -92,8 +92,11 @@ def test_gemv_bf16_small_batches(dev, shape, m):
     _check(y, x, w16)
 
 
-@pytest.mark.parametrize("shape,m", [((37, 48), 3), ((1152, 1152), 5), ((100, 4608), 2), ((24, 24), 1)])
+@pytest.mark.parametrize("shape,m", [((37, 48), 3), ((1152, 1152), 5), ((100, 4608), 2), ((24, 24), 1),
+                                     ((7680, 1920), 64), ((1920, 7680), 64), ((37, 1920), 33), ((64, 1176), 40),
+                                     ((4608, 1152), 100), ((130, 24), 20)])
 def test_ragged_shapes_fp32_activations(dev, shape, m):
+    # m > 16 runs the MFMA GEMM with each fp32 activation split into three bf16 parts
     out_f, in_f = shape
     idx, sig, packed, g = _layer(out_f, in_f, 7 * out_f + m)
     x = torch.randn(m, in_f, generator=g) * 3.0
@@ -137,9 +140,22 @@ def test_literal_rounding_is_exact_for_fp32_activations(dev):
     # W.to(fp32) is exact, so both modes agree bit for bit with fp32 x
     out_f, in_f = 64, 1152
     idx, sig, packed, g = _layer(out_f, in_f, 21)
-    x = torch.randn(3, in_f, generator=g).to(dev)
-    a = dequant_linear(packed.to(dev), sig.to(dev), out_f, in_f, x)
-    b = dequant_linear(packed.to(dev), sig.to(dev), out_f, in_f, x, weight_rounding="as_x")
-    assert torch.equal(a, b)
+    for m in (3, 40):
+        x = torch.randn(m, in_f, generator=g).to(dev)
+        a = dequant_linear(packed.to(dev), sig.to(dev), out_f, in_f, x)
+        b = dequant_linear(packed.to(dev), sig.to(dev), out_f, in_f, x, weight_rounding="as_x")
+        assert torch.equal(a, b)
     with pytest.raises(ValueError):
         dequant_linear(packed.to(dev), sig.to(dev), out_f, in_f, x, weight_rounding="bf16")
+
+
+def test_fp32_activations_wide_dynamic_range(dev):
+    # activations spanning 2^-60..2^60 (and exact zeros): the three-part split keeps every product
+    out_f, in_f, m = 96, 1152, 24
+    idx, sig, packed, g = _layer(out_f, in_f, 31)
+    mag = torch.pow(2.0, torch.randint(-60, 61, (m, in_f), generator=g).float())
+    x = torch.randn(m, in_f, generator=g) * mag
+    x[:, ::7] = 0.0
+    w16 = torch_ref.materialize(idx, sig, out_f, in_f)
+    y = dequant_linear(packed.to(dev), sig.to(dev), out_f, in_f, x.to(dev)).cpu()
+    _check(y, x, w16)
