@@ -144,7 +144,7 @@ namespace {
 //
 // Per code the kernel reads one 16-byte entry of kp_gemv (24 signed 4-bit
 // coordinates + type/position byte; 3.1 MB, L2-resident per XCD).
-// L lanes share a row and stride over its atoms; a block is 256 threads.
+// L lanes share a row and stride over its atoms; a block is NT threads.
 // ---------------------------------------------------------------------------
 
 template <bool XF32>
@@ -182,14 +182,14 @@ __device__ __forceinline__ float x_at(const void *__restrict__ x, int64_t off) {
 // fp32) are staged in LDS first; each lane then handles atoms sub, sub+L, ...
 // of its row in chunks of 4, issuing the chunk's four table gathers before
 // scoring any of them.
-template <int L, int MB, bool XF32, bool XL>
-__global__ __launch_bounds__(256) void dqlinear_kernel(const uint8_t *__restrict__ packed, int64_t packed_bytes,
+template <int L, int MB, bool XF32, bool XL, int NT>
+__global__ __launch_bounds__(NT) void dqlinear_kernel(const uint8_t *__restrict__ packed, int64_t packed_bytes,
                                                        const uint16_t *__restrict__ sigma16, int64_t rows,
                                                        int64_t atoms_per_row, const void *__restrict__ x,
                                                        int64_t m_total, float *__restrict__ y,
                                                        const uint4 *__restrict__ kp_gemv, int round_w) {
   extern __shared__ __align__(16) uint8_t smem[];
-  constexpr int R = 256 / L;
+  constexpr int R = NT / L;
   const int64_t cols = atoms_per_row * kDim;
   const int64_t row0 = static_cast<int64_t>(blockIdx.x) * R;
   const int64_t rows_here = min(static_cast<int64_t>(R), rows - row0);
@@ -203,7 +203,7 @@ __global__ __launch_bounds__(256) void dqlinear_kernel(const uint8_t *__restrict
   const int nvec = static_cast<int>((end - base16 + 15) >> 4);
   const uint8_t *pb = smem + (start - base16);
   float *xs = reinterpret_cast<float *>(smem + static_cast<int64_t>(nvec) * 16);
-  for (int i = threadIdx.x; i < nvec; i += 256) {
+  for (int i = threadIdx.x; i < nvec; i += NT) {
     const int64_t gb = base16 + 16 * static_cast<int64_t>(i);
     if (gb + 16 <= packed_bytes) {
       reinterpret_cast<uint4 *>(smem)[i] = *reinterpret_cast<const uint4 *>(packed + gb);
@@ -221,7 +221,7 @@ __global__ __launch_bounds__(256) void dqlinear_kernel(const uint8_t *__restrict
     if (XL) {
       __syncthreads();
       // token rows are whole multiples of 8 elements (cols = 24 * apr): 8 per thread-step
-      for (int64_t i = threadIdx.x; i < mb_here * cols / 8; i += 256) {
+      for (int64_t i = threadIdx.x; i < mb_here * cols / 8; i += NT) {
         float v[8];
         load_x8<XF32>(x, m0 * cols + 8 * i, v);
         float4 *d = reinterpret_cast<float4 *>(xs + 8 * i);
@@ -315,10 +315,10 @@ __global__ __launch_bounds__(256) void dqlinear_kernel(const uint8_t *__restrict
   }
 }
 
-template <int L, bool XF32>
+template <int L, bool XF32, int NT>
 int launch_dql(const uint8_t *packed, int64_t packed_bytes, const uint16_t *sigma16, int64_t rows, int64_t apr,
                const void *x, int64_t m, float *y, const uint4 *tab, int round_w, hipStream_t s) {
-  constexpr int R = 256 / L;
+  constexpr int R = NT / L;
   const dim3 g(static_cast<unsigned>((rows + R - 1) / R));
   const size_t pbytes = static_cast<size_t>((R * apr + 8) / 4 + 2) * 9;
   const size_t p16 = ((pbytes + 15) & ~static_cast<size_t>(15)) + 16;  // + one vector of alignment slack
@@ -329,7 +329,7 @@ int launch_dql(const uint8_t *packed, int64_t packed_bytes, const uint16_t *sigm
   const size_t shm = xl ? p16 + xbytes : p16;
   if (shm > 64 * 1024) return fail(PLX_EINVAL, "dequant_linear: rows of %lld atoms are too long", static_cast<long long>(apr));
 #define PLX_DQL(MB, XL) \
-  hipLaunchKernelGGL((dqlinear_kernel<L, MB, XF32, XL>), g, dim3(256), shm, s, packed, packed_bytes, sigma16, rows, apr, \
+  hipLaunchKernelGGL((dqlinear_kernel<L, MB, XF32, XL, NT>), g, dim3(NT), shm, s, packed, packed_bytes, sigma16, rows, apr, \
                      x, m, y, tab, round_w)
   if (mb == 4) {
     if (xl) PLX_DQL(4, true); else PLX_DQL(4, false);
@@ -919,15 +919,19 @@ int launch_dequant_linear(const uint8_t *packed, const uint16_t *sigma16, int64_
     return check_launch("dqmm_reduce_kernel");
   }
   const uint4 *kp = reinterpret_cast<const uint4 *>(tab->kp_gemv);
-  // lanes per row: about 2-5 atoms per lane
+  // lanes per row: about 3-5 atoms per lane (7680 x 1920 at M = 1: 16 lanes 6% faster than 32, 8 slower);
+  // 512-thread blocks (4% faster than 256 at M = 1, 1,024 slower), 256 for rows too long to stage 8 in LDS
+  if (apr >= 3072)
+    return x_is_f32 ? launch_dql<64, true, 256>(packed, pb, sigma16, rows, apr, x, m, y, kp, round_w, s)
+                    : launch_dql<64, false, 256>(packed, pb, sigma16, rows, apr, x, m, y, kp, round_w, s);
   if (apr >= 160)
-    return x_is_f32 ? launch_dql<64, true>(packed, pb, sigma16, rows, apr, x, m, y, kp, round_w, s)
-                    : launch_dql<64, false>(packed, pb, sigma16, rows, apr, x, m, y, kp, round_w, s);
-  if (apr >= 40)
-    return x_is_f32 ? launch_dql<32, true>(packed, pb, sigma16, rows, apr, x, m, y, kp, round_w, s)
-                    : launch_dql<32, false>(packed, pb, sigma16, rows, apr, x, m, y, kp, round_w, s);
-  return x_is_f32 ? launch_dql<8, true>(packed, pb, sigma16, rows, apr, x, m, y, kp, round_w, s)
-                  : launch_dql<8, false>(packed, pb, sigma16, rows, apr, x, m, y, kp, round_w, s);
+    return x_is_f32 ? launch_dql<64, true, 512>(packed, pb, sigma16, rows, apr, x, m, y, kp, round_w, s)
+                    : launch_dql<64, false, 512>(packed, pb, sigma16, rows, apr, x, m, y, kp, round_w, s);
+  if (apr >= 16)
+    return x_is_f32 ? launch_dql<16, true, 512>(packed, pb, sigma16, rows, apr, x, m, y, kp, round_w, s)
+                    : launch_dql<16, false, 512>(packed, pb, sigma16, rows, apr, x, m, y, kp, round_w, s);
+  return x_is_f32 ? launch_dql<8, true, 512>(packed, pb, sigma16, rows, apr, x, m, y, kp, round_w, s)
+                  : launch_dql<8, false, 512>(packed, pb, sigma16, rows, apr, x, m, y, kp, round_w, s);
 }
 
 }  // namespace plx

@@ -94,7 +94,7 @@ def test_gemv_bf16_small_batches(dev, shape, m):
 
 @pytest.mark.parametrize("shape,m", [((37, 48), 3), ((1152, 1152), 5), ((100, 4608), 2), ((24, 24), 1),
                                      ((7680, 1920), 64), ((1920, 7680), 64), ((37, 1920), 33), ((64, 1176), 40),
-                                     ((4608, 1152), 100), ((130, 24), 20)])
+                                     ((4608, 1152), 100), ((130, 24), 20), ((5, 73728), 1), ((3, 73728), 20)])
 def test_ragged_shapes_fp32_activations(dev, shape, m):
     # m > 16 runs the MFMA GEMM with each fp32 activation split into three bf16 parts
     out_f, in_f = shape
