@@ -193,6 +193,7 @@ int plx_dequant_f16(const uint8_t *packed, int64_t n_packed_bytes, const uint16_
 #define PLX_DQL_X_F32 1  /* x is fp32 (else bf16) */
 #define PLX_DQL_W_AS_X 2 /* bf16 x: round W to bf16 first, as the reference's literal
                             F.linear(x, W.to(x.dtype)) does (pollux.py:507) */
+#define PLX_DQL_GELU 4   /* y = gelu(x W^T), torch's erf form (pollux.py:645) */
 
 /* Workspace (device bytes, 16-byte aligned) plx_dequant_linear needs for
  * this shape, batch and flags (0 when none). */
@@ -203,8 +204,8 @@ size_t plx_dequant_linear_workspace_bytes(int64_t rows, int64_t cols, int64_t m_
  * (PLX_DQL_X_F32) [m_rows, cols], y fp32 [m_rows, rows].  The products with
  * the fp16 weights are exact and accumulated in fp32: the numerics of
  * F.linear(x.float(), W.float()).  With PLX_DQL_W_AS_X and bf16 x the weights
- * are rounded to bf16 (RNE) first.  Results are deterministic (fixed summation
- * order).  Batches above 16 tokens run on MFMA (fp32 x split exactly into
+ * are rounded to bf16 (RNE) first; with PLX_DQL_GELU, y = gelu(x W^T) (torch's
+ * erf form).  Results are deterministic (fixed summation order).  Batches above 16 tokens run on MFMA (fp32 x split exactly into
  * three bf16 parts) and need the workspace sized by
  * plx_dequant_linear_workspace_bytes (a fragment-order copy of x, plus split
  * partial tiles for narrow layers); cols <= 2^22.
@@ -213,6 +214,27 @@ size_t plx_dequant_linear_workspace_bytes(int64_t rows, int64_t cols, int64_t m_
 int plx_dequant_linear(const uint8_t *packed, int64_t n_packed_bytes, const uint16_t *sigma16,
                        int64_t rows, int64_t cols, const void *x, int flags, int64_t m_rows,
                        float *y, void *workspace, size_t workspace_bytes, void *stream);
+
+/* Several packed weights that share one x (e.g. the q, k and v projections,
+ * pollux.py:616-621) in one call: for each target i,
+ * y_i = [residual_i +] act(x W_i^T) with W_i [rows_i, cols] as in
+ * plx_dequant_linear (act = GELU with PLX_DQL_GELU, else identity; residual_i
+ * may be NULL: the residual adds of pollux.py:660-661).  Up to 16 targets; at
+ * m_rows <= 16 up to four of them run in one GEMV launch.  No counterpart in
+ * the reference's FFI (separate F.linear calls there); results equal separate
+ * plx_dequant_linear calls followed by the epilogue. */
+typedef struct {
+  const uint8_t *packed;     /* ((rows*cols/24 + 3)/4)*9 bytes, 16-byte aligned */
+  const uint16_t *sigma16;   /* [rows] fp16 bits */
+  int64_t rows;
+  float *y;                  /* [m_rows, rows] fp32 */
+  const float *residual;     /* [m_rows, rows] fp32 or NULL */
+} plx_dql_target;
+
+size_t plx_dequant_linear_multi_workspace_bytes(const plx_dql_target *targets, int n_targets, int64_t cols,
+                                                int64_t m_rows, int flags);
+int plx_dequant_linear_multi(const plx_dql_target *targets, int n_targets, int64_t cols, const void *x,
+                             int flags, int64_t m_rows, void *workspace, size_t workspace_bytes, void *stream);
 
 /* ---- packed decoder steps ------------------------------------------------
  * No counterpart in the reference's FFI: the reference runs these steps as

@@ -46,6 +46,8 @@ SIGNATURES = {
     "plx_dequant_f16": (_int, [_vp, _i64, _vp, _i64, _i64, _vp, _vp]),
     "plx_dequant_linear_workspace_bytes": (_sz, [_i64, _i64, _i64, _int]),
     "plx_dequant_linear": (_int, [_vp, _i64, _vp, _i64, _i64, _vp, _int, _i64, _vp, _vp, _sz, _vp]),
+    "plx_dequant_linear_multi_workspace_bytes": (_sz, [_vp, _int, _i64, _i64, _int]),
+    "plx_dequant_linear_multi": (_int, [_vp, _int, _i64, _vp, _int, _i64, _vp, _sz, _vp]),
     "plx_rms_norm": (_int, [_vp, _vp, _vp, _i64, _i64, ctypes.c_float, _vp]),
     "plx_decode_attention": (_int, [_vp, _vp, _vp, _vp, _vp, ctypes.c_float, _vp, _vp, _vp, _i64, _i64, _vp, _vp]),
     "plx_profile_begin": (_int, []),
@@ -59,6 +61,12 @@ class RequantizeItem(ctypes.Structure):
         ("latent", _vp), ("rows", _i64), ("cols", _i64), ("sigma_out", _vp),
         ("idx_out", _vp), ("packed_out", _vp), ("weight_out", _vp),
     ]
+
+
+class DqlTarget(ctypes.Structure):
+    """plx_dql_target (include/pollux_amd.h)."""
+
+    _fields_ = [("packed", _vp), ("sigma16", _vp), ("rows", _i64), ("y", _vp), ("residual", _vp)]
 
 
 _lock = threading.Lock()

@@ -243,6 +243,38 @@ int plx_dequant_f16(const uint8_t *packed, int64_t n_packed_bytes, const uint16_
   return launch_dequant_f16(packed, sigma16, rows, cols, w16_out, as_stream(stream));
 }
 
+static_assert(sizeof(plx_dql_target) == sizeof(DqlTarget), "plx_dql_target mirrors DqlTarget");
+
+size_t plx_dequant_linear_multi_workspace_bytes(const plx_dql_target *targets, int n, int64_t cols, int64_t m_rows,
+                                                int flags) {
+  if (targets == nullptr || n < 1 || n > 16 || cols <= 0 || cols % kDim != 0 || m_rows <= 0) return 0;
+  int64_t rows[16];
+  for (int i = 0; i < n; ++i) rows[i] = targets[i].rows;
+  return dequant_linear_workspace_bytes_multi(rows, n, cols, m_rows, flags);
+}
+
+int plx_dequant_linear_multi(const plx_dql_target *targets, int n, int64_t cols, const void *x, int flags,
+                             int64_t m_rows, void *workspace, size_t workspace_bytes, void *stream) {
+  PLX_REQUIRE(targets != nullptr && n >= 1 && n <= 16, "plx_dequant_linear_multi: %d targets (1..16)", n);
+  PLX_REQUIRE(cols > 0 && cols % kDim == 0, "plx_dequant_linear_multi: bad column count %lld",
+              static_cast<long long>(cols));
+  PLX_REQUIRE(m_rows >= 0, "plx_dequant_linear_multi: negative batch");
+  PLX_REQUIRE((flags & ~(PLX_DQL_X_F32 | PLX_DQL_W_AS_X | PLX_DQL_GELU)) == 0,
+              "plx_dequant_linear_multi: unknown flags 0x%x", flags);
+  DqlTarget t[16];
+  int live = 0;
+  for (int i = 0; i < n; ++i) {
+    PLX_REQUIRE(targets[i].rows >= 0, "plx_dequant_linear_multi: negative rows in target %d", i);
+    if (targets[i].rows == 0) continue;
+    PLX_REQUIRE(targets[i].packed && targets[i].sigma16 && targets[i].y, "plx_dequant_linear_multi: null pointer in target %d",
+                i);
+    t[live++] = DqlTarget{targets[i].packed, targets[i].sigma16, targets[i].rows, targets[i].y, targets[i].residual};
+  }
+  if (live == 0 || m_rows == 0) return PLX_OK;
+  PLX_REQUIRE(x != nullptr, "plx_dequant_linear_multi: null x");
+  return launch_dequant_linear_multi(t, live, cols, x, flags, m_rows, workspace, workspace_bytes, as_stream(stream));
+}
+
 int plx_rms_norm(const float *x, const float *w, float *y, int64_t rows, int64_t d, float eps, void *stream) {
   PLX_REQUIRE(rows >= 0 && d > 0, "plx_rms_norm: bad shape (%lld, %lld)", static_cast<long long>(rows),
               static_cast<long long>(d));
@@ -273,7 +305,8 @@ int plx_dequant_linear(const uint8_t *packed, int64_t n_packed_bytes, const uint
   PLX_REQUIRE(rows >= 0 && cols > 0 && cols % kDim == 0, "plx_dequant_linear: bad shape (%lld, %lld)",
               static_cast<long long>(rows), static_cast<long long>(cols));
   PLX_REQUIRE(m_rows >= 0, "plx_dequant_linear: negative batch");
-  PLX_REQUIRE((flags & ~(PLX_DQL_X_F32 | PLX_DQL_W_AS_X)) == 0, "plx_dequant_linear: unknown flags 0x%x", flags);
+  PLX_REQUIRE((flags & ~(PLX_DQL_X_F32 | PLX_DQL_W_AS_X | PLX_DQL_GELU)) == 0, "plx_dequant_linear: unknown flags 0x%x",
+              flags);
   const int64_t n_atoms = rows * (cols / kDim);
   PLX_REQUIRE(n_packed_bytes == ((n_atoms + 3) / 4) * 9,
               "plx_dequant_linear: packed length %lld does not match %lld atoms", static_cast<long long>(n_packed_bytes),

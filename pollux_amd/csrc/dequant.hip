@@ -147,6 +147,38 @@ namespace {
 // L lanes share a row and stride over its atoms; a block is NT threads.
 // ---------------------------------------------------------------------------
 
+// Output epilogue of the dequant-linear kernels: GELU in torch's erf form
+// (F.gelu: x * 0.5 * (1 + erf(x * sqrt(1/2))), pollux.py:645) and / or a
+// residual added after it (x + linear(h), pollux.py:660-661).
+__device__ __forceinline__ float dql_epilogue(float v, const float *__restrict__ residual, int64_t i, int gelu) {
+  if (gelu) v = (v * 0.5f) * (1.0f + erff(v * __uint_as_float(kSLatticeBits)));  // fp32(1/sqrt 2)
+  if (residual) v = residual[i] + v;
+  return v;
+}
+
+// Up to kDqlMaxTargets weights sharing one x in one GEMV launch: block b works
+// on the target whose cumulative row-block range holds b.
+constexpr int kDqlMaxTargets = 4;
+struct DqlTargets {
+  const uint8_t *packed[kDqlMaxTargets];
+  int64_t packed_bytes[kDqlMaxTargets];
+  const uint16_t *sigma16[kDqlMaxTargets];
+  int64_t rows[kDqlMaxTargets];
+  float *y[kDqlMaxTargets];
+  const float *residual[kDqlMaxTargets];
+  int64_t block_end[kDqlMaxTargets];
+  int n;
+};
+
+// element ti of a kernel-argument array by wave-uniform selects (no dynamic indexing of the argument block)
+template <typename T>
+__device__ __forceinline__ T pick(const T (&a)[kDqlMaxTargets], int ti) {
+  T v = a[0];
+#pragma unroll
+  for (int i = 1; i < kDqlMaxTargets; ++i) v = ti == i ? a[i] : v;
+  return v;
+}
+
 template <bool XF32>
 __device__ __forceinline__ void load_x8(const void *__restrict__ x, int64_t off, float *v) {
   if (XF32) {
@@ -183,15 +215,24 @@ __device__ __forceinline__ float x_at(const void *__restrict__ x, int64_t off) {
 // of its row in chunks of 4, issuing the chunk's four table gathers before
 // scoring any of them.
 template <int L, int MB, bool XF32, bool XL, int NT>
-__global__ __launch_bounds__(NT) void dqlinear_kernel(const uint8_t *__restrict__ packed, int64_t packed_bytes,
-                                                       const uint16_t *__restrict__ sigma16, int64_t rows,
-                                                       int64_t atoms_per_row, const void *__restrict__ x,
-                                                       int64_t m_total, float *__restrict__ y,
-                                                       const uint4 *__restrict__ kp_gemv, int round_w) {
+__global__ __launch_bounds__(NT) void dqlinear_kernel(const DqlTargets targets, int64_t atoms_per_row,
+                                                       const void *__restrict__ x, int64_t m_total,
+                                                       const uint4 *__restrict__ kp_gemv, int round_w, int gelu) {
   extern __shared__ __align__(16) uint8_t smem[];
   constexpr int R = NT / L;
+  int ti = 0;
+#pragma unroll
+  for (int i = 0; i + 1 < kDqlMaxTargets; ++i)
+    ti += (i + 1 < targets.n && static_cast<int64_t>(blockIdx.x) >= targets.block_end[i]) ? 1 : 0;
+  const uint8_t *__restrict__ packed = pick(targets.packed, ti);
+  const int64_t packed_bytes = pick(targets.packed_bytes, ti);
+  const uint16_t *__restrict__ sigma16 = pick(targets.sigma16, ti);
+  const int64_t rows = pick(targets.rows, ti);
+  float *__restrict__ y = pick(targets.y, ti);
+  const float *__restrict__ residual = pick(targets.residual, ti);
+  const int64_t first_block = ti == 0 ? 0 : pick(targets.block_end, ti - 1);
   const int64_t cols = atoms_per_row * kDim;
-  const int64_t row0 = static_cast<int64_t>(blockIdx.x) * R;
+  const int64_t row0 = (static_cast<int64_t>(blockIdx.x) - first_block) * R;
   const int64_t rows_here = min(static_cast<int64_t>(R), rows - row0);
   // packed bytes of atoms [row0*apr, (row0+rows_here)*apr): whole 9-byte groups
   const int64_t atom0 = row0 * atoms_per_row;
@@ -308,18 +349,27 @@ __global__ __launch_bounds__(NT) void dqlinear_kernel(const uint8_t *__restrict_
       const float m4 = round_w ? bf16_bits_to_float(bf16_rne_bits(v4)) : v4;
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb)
-        if (mb < mb_here)
-          y[(m0 + mb) * rows + row] =
-              m4 * (acc[mb][0] * 0.25f) + m2 * (acc[mb][1] * 0.5f) + m1 * acc[mb][2] - m3 * acc[mb][3];
+        if (mb < mb_here) {
+          const int64_t i = (m0 + mb) * rows + row;
+          y[i] = dql_epilogue(m4 * (acc[mb][0] * 0.25f) + m2 * (acc[mb][1] * 0.5f) + m1 * acc[mb][2] - m3 * acc[mb][3],
+                              residual, i, gelu);
+        }
     }
   }
 }
 
 template <int L, bool XF32, int NT>
-int launch_dql(const uint8_t *packed, int64_t packed_bytes, const uint16_t *sigma16, int64_t rows, int64_t apr,
-               const void *x, int64_t m, float *y, const uint4 *tab, int round_w, hipStream_t s) {
+int launch_dql(DqlTargets t, int64_t apr, const void *x, int64_t m, const uint4 *tab, int round_w, int gelu,
+               hipStream_t s) {
   constexpr int R = NT / L;
-  const dim3 g(static_cast<unsigned>((rows + R - 1) / R));
+  int64_t blocks = 0;
+  for (int i = 0; i < kDqlMaxTargets; ++i) {
+    if (i < t.n) blocks += (t.rows[i] + R - 1) / R;
+    t.block_end[i] = blocks;
+  }
+  if (blocks == 0) return PLX_OK;
+  if (blocks > 0x7FFFFFFFll) return fail(PLX_EINVAL, "dequant_linear: too many rows");
+  const dim3 g(static_cast<unsigned>(blocks));
   const size_t pbytes = static_cast<size_t>((R * apr + 8) / 4 + 2) * 9;
   const size_t p16 = ((pbytes + 15) & ~static_cast<size_t>(15)) + 16;  // + one vector of alignment slack
   const int64_t cols = apr * kDim;
@@ -329,8 +379,7 @@ int launch_dql(const uint8_t *packed, int64_t packed_bytes, const uint16_t *sigm
   const size_t shm = xl ? p16 + xbytes : p16;
   if (shm > 64 * 1024) return fail(PLX_EINVAL, "dequant_linear: rows of %lld atoms are too long", static_cast<long long>(apr));
 #define PLX_DQL(MB, XL) \
-  hipLaunchKernelGGL((dqlinear_kernel<L, MB, XF32, XL, NT>), g, dim3(NT), shm, s, packed, packed_bytes, sigma16, rows, apr, \
-                     x, m, y, tab, round_w)
+  hipLaunchKernelGGL((dqlinear_kernel<L, MB, XF32, XL, NT>), g, dim3(NT), shm, s, t, apr, x, m, tab, round_w, gelu)
   if (mb == 4) {
     if (xl) PLX_DQL(4, true); else PLX_DQL(4, false);
   } else if (mb == 2) {
@@ -519,7 +568,8 @@ template <int MT, int WV, int PD, bool EXACT, int XP>
 __global__ __launch_bounds__(64 * WV, WV <= 4 ? 2 : 1) void dqmm_kernel(
     const uint8_t *__restrict__ packed, int64_t packed_bytes, const uint16_t *__restrict__ sigma16, int64_t rows,
     int64_t atoms_per_row, const uint4 *__restrict__ xf, int64_t n_quads_row, int64_t m_total, int splits, int apb,
-    const uint32_t *__restrict__ kp_dq, float *__restrict__ y, float *__restrict__ partial) {
+    const uint32_t *__restrict__ kp_dq, float *__restrict__ y, float *__restrict__ partial,
+    const float *__restrict__ residual, int gelu) {
   extern __shared__ __align__(16) uint8_t smem[];
   constexpr int NT = 64 * WV;
   constexpr int TOK = 16 * MT;
@@ -768,6 +818,11 @@ __global__ __launch_bounds__(64 * WV, WV <= 4 ? 2 : 1) void dqmm_kernel(
     const int64_t row = row0 + 4 * g;
     if (tok0 + tl >= m_total || row >= rows) continue;
     float *d = dst + (tok_base + tl) * rows + row;
+    if (splits == 1) {  // the final output: epilogue here (with a K split, in dqmm_reduce_kernel)
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        if (row + c < rows) sum[c] = dql_epilogue(sum[c], residual, (tok0 + tl) * rows + row + c, gelu);
+    }
     if (vec) {
       *reinterpret_cast<f32x4_t *>(d) = sum;
     } else {
@@ -780,7 +835,8 @@ __global__ __launch_bounds__(64 * WV, WV <= 4 ? 2 : 1) void dqmm_kernel(
 // thread (rows % 4 == 0) or 1, loads of 4 splits issued together.
 template <bool VEC>
 __global__ __launch_bounds__(256) void dqmm_reduce_kernel(const float *__restrict__ partial, int splits, int64_t rows,
-                                                          int64_t m_total, float *__restrict__ y) {
+                                                          int64_t m_total, float *__restrict__ y,
+                                                          const float *__restrict__ residual, int gelu) {
   constexpr int W = VEC ? 4 : 1;
   const int64_t i = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * W;
   if (i >= m_total * rows) return;
@@ -800,6 +856,8 @@ __global__ __launch_bounds__(256) void dqmm_reduce_kernel(const float *__restric
     for (int u = 0; u < 4; ++u) s += v[u];
   }
   for (; k < splits; ++k) s += *reinterpret_cast<const fw *>(p + static_cast<int64_t>(k) * stride);
+#pragma unroll
+  for (int c = 0; c < W; ++c) s[c] = dql_epilogue(s[c], residual, i + c, gelu);
   *reinterpret_cast<fw *>(y + i) = s;
   (void)sizeof(f4);
 }
@@ -825,7 +883,7 @@ MmPlan mm_plan(int64_t rows, int64_t apr) {
 template <int MT, int WV, int PD, bool EXACT, int XP>
 int launch_dqmm_t(const uint8_t *packed, int64_t pb, const uint16_t *sigma16, int64_t rows, int64_t apr,
                   const uint4 *xf, int64_t m, float *y, float *partial, const MmPlan &pl, const uint32_t *kp_dq,
-                  hipStream_t s) {
+                  const float *residual, int gelu, hipStream_t s) {
   const int64_t row_blocks = (rows + kMmRows - 1) / kMmRows;
   const int64_t slabs = (m + 63) / 64;
   const int64_t nq = (apr + 3) / 4;
@@ -833,19 +891,24 @@ int launch_dqmm_t(const uint8_t *packed, int64_t pb, const uint16_t *sigma16, in
   const size_t shm = region + static_cast<size_t>(kMmRows) * 16 * (EXACT ? 2 : 1);
   const dim3 g(static_cast<unsigned>(row_blocks * pl.splits), static_cast<unsigned>(slabs));
   hipLaunchKernelGGL((dqmm_kernel<MT, WV, PD, EXACT, XP>), g, dim3(64 * WV), shm, s, packed, pb, sigma16, rows, apr, xf, nq, m,
-                     pl.splits, pl.apb, kp_dq, y, partial);
+                     pl.splits, pl.apb, kp_dq, y, partial, residual, gelu);
   return check_launch("dqmm_kernel");
 }
 
 template <int MT>
 int launch_dqmm(const uint8_t *packed, int64_t pb, const uint16_t *sigma16, int64_t rows, int64_t apr,
                 const uint4 *xf, int64_t m, float *y, float *partial, const MmPlan &pl, const uint32_t *kp_dq,
-                bool exact, bool x_f32, hipStream_t s) {
+                bool exact, bool x_f32, const float *residual, int gelu, hipStream_t s) {
   // 8 waves (two per SIMD cover each other's load latency), one quad of x in
   // flight per wave; 4 waves with 2 quads in flight measured within 3%
-  if (x_f32) return launch_dqmm_t<MT, 8, 1, true, 3>(packed, pb, sigma16, rows, apr, xf, m, y, partial, pl, kp_dq, s);
-  if (exact) return launch_dqmm_t<MT, 8, 1, true, 1>(packed, pb, sigma16, rows, apr, xf, m, y, partial, pl, kp_dq, s);
-  return launch_dqmm_t<MT, 8, 1, false, 1>(packed, pb, sigma16, rows, apr, xf, m, y, partial, pl, kp_dq, s);
+  if (x_f32)
+    return launch_dqmm_t<MT, 8, 1, true, 3>(packed, pb, sigma16, rows, apr, xf, m, y, partial, pl, kp_dq, residual,
+                                            gelu, s);
+  if (exact)
+    return launch_dqmm_t<MT, 8, 1, true, 1>(packed, pb, sigma16, rows, apr, xf, m, y, partial, pl, kp_dq, residual,
+                                            gelu, s);
+  return launch_dqmm_t<MT, 8, 1, false, 1>(packed, pb, sigma16, rows, apr, xf, m, y, partial, pl, kp_dq, residual,
+                                           gelu, s);
 }
 
 // Workspace of the batched path: the fragment-order x copy (a multiple of 256
@@ -867,18 +930,36 @@ bool uses_mfma(int /*flags*/, int64_t m) { return m > 16; }
 
 }  // namespace
 
-size_t dequant_linear_workspace_bytes(int64_t rows, int64_t cols, int64_t m, int flags) {
-  if (!uses_mfma(flags, m) || rows <= 0 || cols <= 0) return 0;
-  return mm_workspace(rows, cols, m, mm_plan(rows, cols / kDim), (flags & PLX_DQL_X_F32) != 0).total();
+size_t dequant_linear_workspace_bytes_multi(const int64_t *rows, int n, int64_t cols, int64_t m, int flags) {
+  if (!uses_mfma(flags, m) || cols <= 0 || n <= 0) return 0;
+  // one fragment-order copy of x for every target, one partial buffer reused by them in stream order
+  size_t xf = 0, partial = 0;
+  for (int i = 0; i < n; ++i) {
+    if (rows[i] <= 0) continue;
+    const MmWorkspace w = mm_workspace(rows[i], cols, m, mm_plan(rows[i], cols / kDim), (flags & PLX_DQL_X_F32) != 0);
+    xf = w.xf;
+    partial = partial > w.partial ? partial : w.partial;
+  }
+  return xf + partial;
 }
 
-int launch_dequant_linear(const uint8_t *packed, const uint16_t *sigma16, int64_t rows, int64_t cols, const void *x,
-                          int flags, int64_t m, float *y, void *workspace, size_t workspace_bytes, hipStream_t s) {
-  if ((reinterpret_cast<uintptr_t>(x) & 15u) != 0 || (reinterpret_cast<uintptr_t>(packed) & 15u) != 0)
-    return fail(PLX_EINVAL, "dequant_linear: x and packed must be 16-byte aligned");
+size_t dequant_linear_workspace_bytes(int64_t rows, int64_t cols, int64_t m, int flags) {
+  return dequant_linear_workspace_bytes_multi(&rows, 1, cols, m, flags);
+}
+
+int launch_dequant_linear_multi(const DqlTarget *targets, int n, int64_t cols, const void *x, int flags, int64_t m,
+                                void *workspace, size_t workspace_bytes, hipStream_t s) {
+  if (n < 1 || n > 16) return fail(PLX_EINVAL, "dequant_linear: %d targets (1..16)", n);
+  if ((reinterpret_cast<uintptr_t>(x) & 15u) != 0) return fail(PLX_EINVAL, "dequant_linear: x must be 16-byte aligned");
+  for (int i = 0; i < n; ++i)
+    if ((reinterpret_cast<uintptr_t>(targets[i].packed) & 15u) != 0)
+      return fail(PLX_EINVAL, "dequant_linear: packed weights must be 16-byte aligned");
   const int x_is_f32 = flags & PLX_DQL_X_F32;
   const int round_w = !x_is_f32 && (flags & PLX_DQL_W_AS_X) ? 1 : 0;  // W.to(fp32) is exact
-  const size_t need = dequant_linear_workspace_bytes(rows, cols, m, flags);
+  const int gelu = (flags & PLX_DQL_GELU) ? 1 : 0;
+  int64_t rows_list[16];
+  for (int i = 0; i < n; ++i) rows_list[i] = targets[i].rows;
+  const size_t need = dequant_linear_workspace_bytes_multi(rows_list, n, cols, m, flags);
   if (workspace_bytes < need || (need && workspace == nullptr))
     return fail(PLX_EINVAL, "dequant_linear: workspace of %zu bytes is smaller than the %zu needed", workspace_bytes, need);
   if (need && (reinterpret_cast<uintptr_t>(workspace) & 15u) != 0)
@@ -887,17 +968,13 @@ int launch_dequant_linear(const uint8_t *packed, const uint16_t *sigma16, int64_
   int st = get_tables(&tab);
   if (st != PLX_OK) return st;
   const int64_t apr = cols / kDim;
-  const int64_t pb = ((rows * apr + 3) / 4) * 9;  // packed stream length
   if (uses_mfma(flags, m)) {
-    // batches above 16 tokens: MFMA dequant-GEMM in slabs of 64 tokens
+    // batches above 16 tokens: MFMA dequant-GEMM in slabs of 64 tokens, one launch (+ split sum) per target
     if (cols > kMmMaxCols)
       return fail(PLX_EINVAL, "dequant_linear: %lld columns exceed the batched path's %lld", static_cast<long long>(cols),
                   static_cast<long long>(kMmMaxCols));
-    const MmPlan pl = mm_plan(rows, apr);
-    const MmWorkspace w = mm_workspace(rows, cols, m, pl, x_is_f32 != 0);
     uint8_t *wsb = static_cast<uint8_t *>(workspace);
     uint4 *xf = reinterpret_cast<uint4 *>(wsb);
-    float *part = reinterpret_cast<float *>(wsb + w.xf);
     const int64_t slabs = (m + 63) / 64, nq = (apr + 3) / 4;
     const dim3 gx(static_cast<unsigned>(nq * 3), static_cast<unsigned>(slabs));
     if (x_is_f32)
@@ -905,33 +982,64 @@ int launch_dequant_linear(const uint8_t *packed, const uint16_t *sigma16, int64_
     else
       hipLaunchKernelGGL((xfrag_kernel<false>), gx, dim3(256), 0, s, x, m, cols, nq, xf);
     st = check_launch("xfrag_kernel");
-    if (st != PLX_OK) return st;
-    st = m > 32 ? launch_dqmm<4>(packed, pb, sigma16, rows, apr, xf, m, y, part, pl, tab->kp_dq, !round_w, x_is_f32, s)
-                : launch_dqmm<2>(packed, pb, sigma16, rows, apr, xf, m, y, part, pl, tab->kp_dq, !round_w, x_is_f32, s);
-    if (st != PLX_OK || pl.splits == 1) return st;
-    const int64_t n = m * rows;
-    if (rows % 4 == 0 && (reinterpret_cast<uintptr_t>(y) & 15u) == 0)
-      hipLaunchKernelGGL((dqmm_reduce_kernel<true>), dim3(static_cast<unsigned>((n / 4 + 255) / 256)), dim3(256), 0, s,
-                         part, pl.splits, rows, m, y);
-    else
-      hipLaunchKernelGGL((dqmm_reduce_kernel<false>), dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s,
-                         part, pl.splits, rows, m, y);
-    return check_launch("dqmm_reduce_kernel");
+    for (int i = 0; i < n && st == PLX_OK; ++i) {
+      const DqlTarget &t = targets[i];
+      if (t.rows <= 0) continue;
+      const MmPlan pl = mm_plan(t.rows, apr);
+      float *part = reinterpret_cast<float *>(wsb + mm_workspace(t.rows, cols, m, pl, x_is_f32 != 0).xf);
+      const int64_t pb = ((t.rows * apr + 3) / 4) * 9;  // packed stream length
+      st = m > 32 ? launch_dqmm<4>(t.packed, pb, t.sigma16, t.rows, apr, xf, m, t.y, part, pl, tab->kp_dq, !round_w,
+                                   x_is_f32, t.residual, gelu, s)
+                  : launch_dqmm<2>(t.packed, pb, t.sigma16, t.rows, apr, xf, m, t.y, part, pl, tab->kp_dq, !round_w,
+                                   x_is_f32, t.residual, gelu, s);
+      if (st != PLX_OK || pl.splits == 1) continue;
+      const int64_t cnt = m * t.rows;
+      if (t.rows % 4 == 0 && (reinterpret_cast<uintptr_t>(t.y) & 15u) == 0)
+        hipLaunchKernelGGL((dqmm_reduce_kernel<true>), dim3(static_cast<unsigned>((cnt / 4 + 255) / 256)), dim3(256), 0,
+                           s, part, pl.splits, t.rows, m, t.y, t.residual, gelu);
+      else
+        hipLaunchKernelGGL((dqmm_reduce_kernel<false>), dim3(static_cast<unsigned>((cnt + 255) / 256)), dim3(256), 0, s,
+                           part, pl.splits, t.rows, m, t.y, t.residual, gelu);
+      st = check_launch("dqmm_reduce_kernel");
+    }
+    return st;
   }
   const uint4 *kp = reinterpret_cast<const uint4 *>(tab->kp_gemv);
-  // lanes per row: about 3-5 atoms per lane (7680 x 1920 at M = 1: 16 lanes 6% faster than 32, 8 slower);
-  // 512-thread blocks (4% faster than 256 at M = 1, 1,024 slower), 256 for rows too long to stage 8 in LDS
-  if (apr >= 3072)
-    return x_is_f32 ? launch_dql<64, true, 256>(packed, pb, sigma16, rows, apr, x, m, y, kp, round_w, s)
-                    : launch_dql<64, false, 256>(packed, pb, sigma16, rows, apr, x, m, y, kp, round_w, s);
-  if (apr >= 160)
-    return x_is_f32 ? launch_dql<64, true, 512>(packed, pb, sigma16, rows, apr, x, m, y, kp, round_w, s)
-                    : launch_dql<64, false, 512>(packed, pb, sigma16, rows, apr, x, m, y, kp, round_w, s);
-  if (apr >= 16)
-    return x_is_f32 ? launch_dql<16, true, 512>(packed, pb, sigma16, rows, apr, x, m, y, kp, round_w, s)
-                    : launch_dql<16, false, 512>(packed, pb, sigma16, rows, apr, x, m, y, kp, round_w, s);
-  return x_is_f32 ? launch_dql<8, true, 512>(packed, pb, sigma16, rows, apr, x, m, y, kp, round_w, s)
-                  : launch_dql<8, false, 512>(packed, pb, sigma16, rows, apr, x, m, y, kp, round_w, s);
+  // up to kDqlMaxTargets targets per GEMV launch
+  for (int i0 = 0; i0 < n && st == PLX_OK; i0 += kDqlMaxTargets) {
+    DqlTargets t{};
+    t.n = n - i0 < kDqlMaxTargets ? n - i0 : kDqlMaxTargets;
+    for (int i = 0; i < kDqlMaxTargets; ++i) {
+      const DqlTarget &src = targets[i0 + (i < t.n ? i : 0)];
+      t.packed[i] = src.packed;
+      t.packed_bytes[i] = ((src.rows * apr + 3) / 4) * 9;
+      t.sigma16[i] = src.sigma16;
+      t.rows[i] = i < t.n ? src.rows : 0;
+      t.y[i] = src.y;
+      t.residual[i] = src.residual;
+    }
+    // lanes per row: about 3-5 atoms per lane (7680 x 1920 at M = 1: 16 lanes 6% faster than 32, 8 slower);
+    // 512-thread blocks (4% faster than 256 at M = 1, 1,024 slower), 256 for rows too long to stage 8 in LDS
+    if (apr >= 3072)
+      st = x_is_f32 ? launch_dql<64, true, 256>(t, apr, x, m, kp, round_w, gelu, s)
+                    : launch_dql<64, false, 256>(t, apr, x, m, kp, round_w, gelu, s);
+    else if (apr >= 160)
+      st = x_is_f32 ? launch_dql<64, true, 512>(t, apr, x, m, kp, round_w, gelu, s)
+                    : launch_dql<64, false, 512>(t, apr, x, m, kp, round_w, gelu, s);
+    else if (apr >= 16)
+      st = x_is_f32 ? launch_dql<16, true, 512>(t, apr, x, m, kp, round_w, gelu, s)
+                    : launch_dql<16, false, 512>(t, apr, x, m, kp, round_w, gelu, s);
+    else
+      st = x_is_f32 ? launch_dql<8, true, 512>(t, apr, x, m, kp, round_w, gelu, s)
+                    : launch_dql<8, false, 512>(t, apr, x, m, kp, round_w, gelu, s);
+  }
+  return st;
+}
+
+int launch_dequant_linear(const uint8_t *packed, const uint16_t *sigma16, int64_t rows, int64_t cols, const void *x,
+                          int flags, int64_t m, float *y, void *workspace, size_t workspace_bytes, hipStream_t s) {
+  const DqlTarget t{packed, sigma16, rows, y, nullptr};
+  return launch_dequant_linear_multi(&t, 1, cols, x, flags, m, workspace, workspace_bytes, s);
 }
 
 }  // namespace plx

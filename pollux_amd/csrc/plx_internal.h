@@ -85,6 +85,17 @@ int launch_rms_norm(const float *x, const float *w, float *y, int64_t rows, int6
 int launch_decode_attention(const float *q, const float *k, const float *v, const float *q_w, const float *k_w,
                             float eps, float *k_cache, float *v_cache, const int64_t *pos, int64_t seqs_heads,
                             int64_t max_len, float *out, hipStream_t s);
+// One weight of a multi-target dequant-linear call (all share x and cols).
+struct DqlTarget {
+  const uint8_t *packed;
+  const uint16_t *sigma16;
+  int64_t rows;
+  float *y;
+  const float *residual;  // y = residual + (x W^T) when not null
+};
+size_t dequant_linear_workspace_bytes_multi(const int64_t *rows, int n, int64_t cols, int64_t m, int flags);
+int launch_dequant_linear_multi(const DqlTarget *targets, int n, int64_t cols, const void *x, int flags, int64_t m,
+                                void *workspace, size_t workspace_bytes, hipStream_t s);
 size_t dequant_linear_workspace_bytes(int64_t rows, int64_t cols, int64_t m, int flags);
 int launch_dequant_linear(const uint8_t *packed, const uint16_t *sigma16, int64_t rows, int64_t cols, const void *x,
                           int flags, int64_t m, float *y, void *workspace, size_t workspace_bytes, hipStream_t s);

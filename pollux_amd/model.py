@@ -31,7 +31,7 @@ import torch.nn.functional as F
 
 from . import _lib
 from .castor import H24_DIM, assert_row_aligned_width
-from .packed import PackedH24Linear, PackedInt8Embedding, PackedInt8Linear
+from .packed import PackedH24Linear, PackedInt8Embedding, PackedInt8Linear, packed_linear_group
 from .plx import check_fingerprint, load_plx
 
 # pollux.py:258-278: the config fields and their aliases
@@ -172,18 +172,19 @@ class PackedCausalAttention(nn.Module):
         self.k_ln = RMSNorm(self.d_head)
 
     def forward(self, x: torch.Tensor, cache: KVCache | None = None, layer: int = 0,
-                pos: torch.Tensor | None = None) -> torch.Tensor:
+                pos: torch.Tensor | None = None, residual: torch.Tensor | None = None) -> torch.Tensor:
+        """[residual +] o_proj(attention(x)); the q, k, v projections share one dequant-linear call."""
         b, t, c = x.shape
+        q, k, v = packed_linear_group([self.q_proj, self.k_proj, self.v_proj], x)
         if cache is not None and t == 1:
             # one new token per sequence: norms, cache write and attention in one kernel at device position pos
             if pos is None:
                 pos = torch.full((), cache.length, dtype=torch.long, device=x.device)
-            o = decode_attention(self.q_proj(x), self.k_proj(x), self.v_proj(x), self.q_ln, self.k_ln,
-                                 cache.k[layer], cache.v[layer], pos)
-            return self.o_proj(o)
-        q = self.q_ln(self.q_proj(x).view(b, t, self.n_heads, self.d_head)).transpose(1, 2)
-        k = self.k_ln(self.k_proj(x).view(b, t, self.n_heads, self.d_head)).transpose(1, 2)
-        v = self.v_proj(x).view(b, t, self.n_heads, self.d_head).transpose(1, 2)
+            o = decode_attention(q, k, v, self.q_ln, self.k_ln, cache.k[layer], cache.v[layer], pos)
+            return packed_linear_group([self.o_proj], o, residuals=[residual])[0]
+        q = self.q_ln(q.view(b, t, self.n_heads, self.d_head)).transpose(1, 2)
+        k = self.k_ln(k.view(b, t, self.n_heads, self.d_head)).transpose(1, 2)
+        v = v.view(b, t, self.n_heads, self.d_head).transpose(1, 2)
         if cache is None:
             attn = F.scaled_dot_product_attention(q, k, v, is_causal=True)
         else:
@@ -197,7 +198,8 @@ class PackedCausalAttention(nn.Module):
                 # query i sits at position p0 + i and sees positions <= p0 + i
                 allowed = torch.ones(t, p0 + t, dtype=torch.bool, device=x.device).tril(diagonal=p0)
                 attn = F.scaled_dot_product_attention(q, keys, vals, attn_mask=allowed)
-        return self.o_proj(attn.transpose(1, 2).contiguous().view(b, t, c))
+        return packed_linear_group([self.o_proj], attn.transpose(1, 2).contiguous().view(b, t, c),
+                                   residuals=[residual])[0]
 
 
 class PackedMLP(nn.Module):
@@ -209,8 +211,10 @@ class PackedMLP(nn.Module):
         self.fc1 = PackedH24Linear(n_embd, 4 * n_embd)
         self.fc2 = PackedH24Linear(4 * n_embd, n_embd)
 
-    def forward(self, x: torch.Tensor) -> torch.Tensor:
-        return self.fc2(F.gelu(self.fc1(x)))
+    def forward(self, x: torch.Tensor, residual: torch.Tensor | None = None) -> torch.Tensor:
+        """[residual +] fc2(gelu(fc1(x))), with the GELU and the residual add in the dequant-linear epilogues."""
+        h = packed_linear_group([self.fc1], x, gelu=True)[0]
+        return packed_linear_group([self.fc2], h, residuals=[residual])[0]
 
 
 class PackedBlock(nn.Module):
@@ -225,8 +229,8 @@ class PackedBlock(nn.Module):
 
     def forward(self, x: torch.Tensor, cache: KVCache | None = None, layer: int = 0,
                 pos: torch.Tensor | None = None) -> torch.Tensor:
-        x = x + self.attn(self.ln1(x), cache, layer, pos)
-        return x + self.mlp(self.ln2(x))
+        x = self.attn(self.ln1(x), cache, layer, pos, residual=x)  # x + attn(ln1(x))
+        return self.mlp(self.ln2(x), residual=x)                    # x + mlp(ln2(x))
 
 
 class PackedPolluxModel(nn.Module):

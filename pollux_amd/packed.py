@@ -40,7 +40,7 @@ def dequantize_h24(packed: torch.Tensor, sigma16: torch.Tensor, out_features: in
     return out
 
 
-DQL_X_F32, DQL_W_AS_X = 1, 2  # plx_dequant_linear flags (include/pollux_amd.h)
+DQL_X_F32, DQL_W_AS_X, DQL_GELU = 1, 2, 4  # plx_dequant_linear flags (include/pollux_amd.h)
 
 
 def dequant_linear(
@@ -87,6 +87,90 @@ def dequant_linear(
         )
     _lib.check(st, "dequant_linear")
     return y.reshape(*lead, out_features)
+
+
+def dequant_linear_multi(
+    weights: list[tuple[torch.Tensor, torch.Tensor, int]], in_features: int, x: torch.Tensor, *,
+    residuals: list[torch.Tensor | None] | None = None, gelu: bool = False, weight_rounding: str = "exact",
+) -> list[torch.Tensor]:
+    """Several packed weights sharing x in one call: [residual_i +] act(x @ W_i.T), fp32 [..., out_i] each.
+
+    ``weights``: (packed, sigma16, out_features) per target; act = GELU (erf
+    form, as F.gelu) when ``gelu``; ``residuals``: fp32 [..., out_i] tensors
+    added after the activation (or None).  At up to 16 tokens, four targets
+    share one GEMV launch.  Results equal separate dequant_linear calls
+    followed by the same epilogue.
+    """
+    if weight_rounding not in ("exact", "as_x"):
+        raise ValueError(f"weight_rounding must be 'exact' or 'as_x', got {weight_rounding!r}")
+    if not 1 <= len(weights) <= 16:
+        raise ValueError("dequant_linear_multi takes 1..16 weights")
+    assert_row_aligned_in_features(in_features)
+    if x.shape[-1] != in_features:
+        raise ValueError(f"x has {x.shape[-1]} features, layer expects {in_features}")
+    lead = x.shape[:-1]
+    xx = x.reshape(-1, in_features)
+    if xx.dtype not in (torch.bfloat16, torch.float32):
+        xx = xx.float()
+    xx = xx.contiguous()
+    if xx.data_ptr() % 16:
+        xx = xx.clone()
+    _lib.require_device(xx, "dequant_linear_multi x")
+    m = xx.shape[0]
+    residuals = residuals or [None] * len(weights)
+    arr = (_lib.DqlTarget * len(weights))()
+    ys, keep = [], []
+    for i, (pk, sg, out_f) in enumerate(weights):
+        _lib.require_device(pk, "dequant_linear_multi packed input")
+        if pk.dtype != torch.uint8 or sg.dtype != torch.float16:
+            raise ValueError("packed weights must be uint8 and sigma rows float16")
+        pk = pk.reshape(-1).contiguous()
+        if pk.data_ptr() % 16:
+            pk = pk.clone()
+        sg = sg.reshape(-1).contiguous()
+        if sg.numel() != out_f or pk.numel() != ((out_f * in_features // 24 + 3) // 4) * 9:
+            raise ValueError(f"target {i}: packed / sigma sizes do not match [{out_f}, {in_features}]")
+        y = torch.empty((m, out_f), dtype=torch.float32, device=xx.device)
+        r = residuals[i]
+        if r is not None:
+            if r.dtype != torch.float32 or r.numel() != m * out_f:
+                raise ValueError(f"target {i}: residual must be float32 with {m * out_f} elements")
+            r = r.reshape(m, out_f).contiguous()
+        arr[i] = _lib.DqlTarget(pk.data_ptr(), sg.data_ptr(), out_f, y.data_ptr(), _lib.ptr(r))
+        keep += [pk, sg, r]
+        ys.append(y)
+    flags = (DQL_X_F32 if xx.dtype == torch.float32 else 0) | (DQL_W_AS_X if weight_rounding == "as_x" else 0) | (
+        DQL_GELU if gelu else 0)
+    lib = _lib.lib()
+    nws = int(lib.plx_dequant_linear_multi_workspace_bytes(arr, len(weights), in_features, m, flags))
+    ws = torch.empty(max(nws, 16), dtype=torch.uint8, device=xx.device) if nws else None
+    with torch.cuda.device(xx.device):
+        st = lib.plx_dequant_linear_multi(arr, len(weights), in_features, _lib.ptr(xx), flags, m, _lib.ptr(ws), nws,
+                                          _lib.stream_of(xx.device))
+    _lib.check(st, "dequant_linear_multi")
+    return [y.reshape(*lead, y.shape[1]) for y in ys]
+
+
+def packed_linear_group(layers: list, x: torch.Tensor, *, residuals: list | None = None,
+                        gelu: bool = False) -> list[torch.Tensor]:
+    """[residual +] act(layer(x)) for PackedH24Linear layers sharing x, fused when they are all packed.
+
+    Materialised layers take the reference's ops instead (F.linear on the
+    weight cast to x's dtype, F.gelu, then the residual add).
+    """
+    residuals = residuals or [None] * len(layers)
+    if all(isinstance(l, PackedH24Linear) and not l._materialized and l.bias is None for l in layers):
+        ys = dequant_linear_multi([(l.packed_weights, l.sigma_rows, l.out_features) for l in layers],
+                                  layers[0].in_features, x, residuals=residuals, gelu=gelu,
+                                  weight_rounding=layers[0].weight_rounding)
+        return [y.to(x.dtype) for y in ys]
+    outs = []
+    for layer, r in zip(layers, residuals):
+        y = layer(x)
+        if gelu:
+            y = F.gelu(y)
+        outs.append(y if r is None else r + y)
+    return outs
 
 
 class PackedH24Linear(nn.Module):

@@ -159,3 +159,54 @@ def test_fp32_activations_wide_dynamic_range(dev):
     w16 = torch_ref.materialize(idx, sig, out_f, in_f)
     y = dequant_linear(packed.to(dev), sig.to(dev), out_f, in_f, x.to(dev)).cpu()
     _check(y, x, w16)
+
+
+@pytest.mark.parametrize("m,dtype", [(1, torch.bfloat16), (5, torch.float32), (40, torch.bfloat16), (33, torch.float32)])
+def test_multi_target_equals_separate_calls(dev, m, dtype):
+    # q/k/v-style targets sharing x (plus one with other rows, a zero-row one, and more than four in all)
+    from pollux_amd.packed import dequant_linear_multi
+
+    in_f = 1152
+    shapes = [1152, 1152, 1152, 96, 0, 600]
+    layers = [_layer(max(o, 1), in_f, 40 + i) for i, o in enumerate(shapes)]
+    g = torch.Generator().manual_seed(m)
+    x = torch.randn(m, in_f, generator=g).to(dtype).to(dev)
+    weights = [(pk.to(dev) if o else pk[:0].to(dev), sig.to(dev) if o else sig[:0].to(dev), o)
+               for (idx, sig, pk, _), o in zip(layers, shapes)]
+    ys = dequant_linear_multi(weights, in_f, x)
+    for (pk, sg, o), y in zip(weights, ys):
+        assert y.shape == (m, o)
+        if o:
+            assert torch.equal(y, dequant_linear(pk, sg, o, in_f, x))
+
+
+@pytest.mark.parametrize("m", [1, 7, 64])
+def test_multi_target_epilogues(dev, m):
+    from pollux_amd.packed import dequant_linear_multi
+
+    out_f, in_f = 1920, 1920
+    idx, sig, packed, g = _layer(out_f, in_f, 77 + m)
+    x = torch.randn(m, in_f, generator=g).to(dev)
+    pk, sg = packed.to(dev), sig.to(dev)
+    plain = dequant_linear(pk, sg, out_f, in_f, x)
+    r = torch.randn(m, out_f, generator=g).to(dev)
+    (with_res,) = dequant_linear_multi([(pk, sg, out_f)], in_f, x, residuals=[r])
+    assert torch.equal(with_res, r + plain)  # the reference's x + linear(h)
+    (act,) = dequant_linear_multi([(pk, sg, out_f)], in_f, x, gelu=True)
+    want = torch.nn.functional.gelu(plain)
+    ulp = (act.view(torch.int32).long() - want.view(torch.int32).long()).abs().max().item()
+    print(f"[dql] gelu epilogue vs F.gelu: max {ulp} ulp", flush=True)
+    assert ulp <= 2
+
+
+def test_multi_target_bad_arguments(dev):
+    from pollux_amd.packed import dequant_linear_multi
+
+    idx, sig, packed, g = _layer(48, 48, 5)
+    x = torch.randn(2, 48, device=dev)
+    with pytest.raises(ValueError):
+        dequant_linear_multi([(packed.to(dev), sig.to(dev), 48)] * 17, 48, x)
+    with pytest.raises(ValueError):
+        dequant_linear_multi([(packed.to(dev)[:-9], sig.to(dev), 48)], 48, x)
+    with pytest.raises(ValueError):
+        dequant_linear_multi([(packed.to(dev), sig.to(dev), 48)], 48, x, residuals=[torch.zeros(3, device=dev)])
