@@ -28,6 +28,8 @@
 
 #include <hip/hip_fp16.h>
 
+#include <type_traits>
+
 #include "plx_device.h"
 
 namespace plx {
@@ -156,8 +158,9 @@ __device__ __forceinline__ float dql_epilogue(float v, const float *__restrict__
   return v;
 }
 
-// Up to kDqlMaxTargets weights sharing one x in one GEMV launch: block b works
-// on the target whose cumulative row-block range holds b.
+// Up to kDqlMaxTargets weights sharing one x in one GEMV launch: blockIdx.y is
+// the target, blockIdx.x the row block (blocks past a shorter target's rows
+// return at once).
 constexpr int kDqlMaxTargets = 4;
 struct DqlTargets {
   const uint8_t *packed[kDqlMaxTargets];
@@ -166,17 +169,28 @@ struct DqlTargets {
   int64_t rows[kDqlMaxTargets];
   float *y[kDqlMaxTargets];
   const float *residual[kDqlMaxTargets];
-  int64_t block_end[kDqlMaxTargets];
   int n;
 };
 
+// One target without epilogue: the plain call (selecting a target and the
+// epilogue's checks cost ~0.7 us per launch at M = 1, measured).
+struct DqlOne {
+  const uint8_t *packed;
+  int64_t packed_bytes;
+  const uint16_t *sigma16;
+  int64_t rows;
+  float *y;
+};
+
 // element ti of a kernel-argument array by wave-uniform selects (no dynamic indexing of the argument block)
+// (the loaded values are made opaque: otherwise the compiler turns the selects
+// into a kernel-argument load at a computed offset, a dependent round trip)
 template <typename T>
 __device__ __forceinline__ T pick(const T (&a)[kDqlMaxTargets], int ti) {
-  T v = a[0];
-#pragma unroll
-  for (int i = 1; i < kDqlMaxTargets; ++i) v = ti == i ? a[i] : v;
-  return v;
+  static_assert(kDqlMaxTargets == 4 && sizeof(T) == 8, "pick: four 64-bit values");
+  T v0 = a[0], v1 = a[1], v2 = a[2], v3 = a[3];
+  asm volatile("" : "+s"(v0), "+s"(v1), "+s"(v2), "+s"(v3));
+  return ti == 1 ? v1 : ti == 2 ? v2 : ti == 3 ? v3 : v0;
 }
 
 template <bool XF32>
@@ -214,25 +228,39 @@ __device__ __forceinline__ float x_at(const void *__restrict__ x, int64_t off) {
 // fp32) are staged in LDS first; each lane then handles atoms sub, sub+L, ...
 // of its row in chunks of 4, issuing the chunk's four table gathers before
 // scoring any of them.
-template <int L, int MB, bool XF32, bool XL, int NT>
-__global__ __launch_bounds__(NT) void dqlinear_kernel(const DqlTargets targets, int64_t atoms_per_row,
+template <bool GEN>
+using DqlArgs = typename std::conditional<GEN, DqlTargets, DqlOne>::type;
+
+// GEN: several targets and the epilogue (DqlTargets); else one target, no epilogue (DqlOne)
+template <int L, int MB, bool XF32, bool XL, int NT, bool GEN>
+__global__ __launch_bounds__(NT) void dqlinear_kernel(const DqlArgs<GEN> targets, int64_t atoms_per_row,
                                                        const void *__restrict__ x, int64_t m_total,
                                                        const uint4 *__restrict__ kp_gemv, int round_w, int gelu) {
   extern __shared__ __align__(16) uint8_t smem[];
   constexpr int R = NT / L;
-  int ti = 0;
-#pragma unroll
-  for (int i = 0; i + 1 < kDqlMaxTargets; ++i)
-    ti += (i + 1 < targets.n && static_cast<int64_t>(blockIdx.x) >= targets.block_end[i]) ? 1 : 0;
-  const uint8_t *__restrict__ packed = pick(targets.packed, ti);
-  const int64_t packed_bytes = pick(targets.packed_bytes, ti);
-  const uint16_t *__restrict__ sigma16 = pick(targets.sigma16, ti);
-  const int64_t rows = pick(targets.rows, ti);
-  float *__restrict__ y = pick(targets.y, ti);
-  const float *__restrict__ residual = pick(targets.residual, ti);
-  const int64_t first_block = ti == 0 ? 0 : pick(targets.block_end, ti - 1);
+  const uint8_t *__restrict__ packed;
+  const uint16_t *__restrict__ sigma16;
+  float *__restrict__ y;
+  const float *__restrict__ residual = nullptr;
+  int64_t packed_bytes, rows;
+  if constexpr (GEN) {
+    const int ti = static_cast<int>(blockIdx.y);
+    packed = pick(targets.packed, ti);
+    packed_bytes = pick(targets.packed_bytes, ti);
+    sigma16 = pick(targets.sigma16, ti);
+    rows = pick(targets.rows, ti);
+    y = pick(targets.y, ti);
+    residual = pick(targets.residual, ti);
+    if (static_cast<int64_t>(blockIdx.x) * R >= rows) return;  // the whole block: before any barrier
+  } else {
+    packed = targets.packed;
+    packed_bytes = targets.packed_bytes;
+    sigma16 = targets.sigma16;
+    rows = targets.rows;
+    y = targets.y;
+  }
   const int64_t cols = atoms_per_row * kDim;
-  const int64_t row0 = (static_cast<int64_t>(blockIdx.x) - first_block) * R;
+  const int64_t row0 = static_cast<int64_t>(blockIdx.x) * R;
   const int64_t rows_here = min(static_cast<int64_t>(R), rows - row0);
   // packed bytes of atoms [row0*apr, (row0+rows_here)*apr): whole 9-byte groups
   const int64_t atom0 = row0 * atoms_per_row;
@@ -351,8 +379,11 @@ __global__ __launch_bounds__(NT) void dqlinear_kernel(const DqlTargets targets, 
       for (int mb = 0; mb < MB; ++mb)
         if (mb < mb_here) {
           const int64_t i = (m0 + mb) * rows + row;
-          y[i] = dql_epilogue(m4 * (acc[mb][0] * 0.25f) + m2 * (acc[mb][1] * 0.5f) + m1 * acc[mb][2] - m3 * acc[mb][3],
-                              residual, i, gelu);
+          const float v = m4 * (acc[mb][0] * 0.25f) + m2 * (acc[mb][1] * 0.5f) + m1 * acc[mb][2] - m3 * acc[mb][3];
+          if constexpr (GEN)
+            y[i] = dql_epilogue(v, residual, i, gelu);
+          else
+            y[i] = v;
         }
     }
   }
@@ -363,13 +394,12 @@ int launch_dql(DqlTargets t, int64_t apr, const void *x, int64_t m, const uint4 
                hipStream_t s) {
   constexpr int R = NT / L;
   int64_t blocks = 0;
-  for (int i = 0; i < kDqlMaxTargets; ++i) {
-    if (i < t.n) blocks += (t.rows[i] + R - 1) / R;
-    t.block_end[i] = blocks;
-  }
+  for (int i = 0; i < t.n; ++i) blocks = max(blocks, (t.rows[i] + R - 1) / R);
   if (blocks == 0) return PLX_OK;
   if (blocks > 0x7FFFFFFFll) return fail(PLX_EINVAL, "dequant_linear: too many rows");
-  const dim3 g(static_cast<unsigned>(blocks));
+  const bool gen = t.n > 1 || t.residual[0] != nullptr || gelu;
+  const dim3 g(static_cast<unsigned>(blocks), static_cast<unsigned>(gen ? t.n : 1));
+  const DqlOne one{t.packed[0], t.packed_bytes[0], t.sigma16[0], t.rows[0], t.y[0]};
   const size_t pbytes = static_cast<size_t>((R * apr + 8) / 4 + 2) * 9;
   const size_t p16 = ((pbytes + 15) & ~static_cast<size_t>(15)) + 16;  // + one vector of alignment slack
   const int64_t cols = apr * kDim;
@@ -379,7 +409,14 @@ int launch_dql(DqlTargets t, int64_t apr, const void *x, int64_t m, const uint4 
   const size_t shm = xl ? p16 + xbytes : p16;
   if (shm > 64 * 1024) return fail(PLX_EINVAL, "dequant_linear: rows of %lld atoms are too long", static_cast<long long>(apr));
 #define PLX_DQL(MB, XL) \
-  hipLaunchKernelGGL((dqlinear_kernel<L, MB, XF32, XL, NT>), g, dim3(NT), shm, s, t, apr, x, m, tab, round_w, gelu)
+  do {                                                                                                        \
+    if (gen)                                                                                                  \
+      hipLaunchKernelGGL((dqlinear_kernel<L, MB, XF32, XL, NT, true>), g, dim3(NT), shm, s, t, apr, x, m, tab,  \
+                         round_w, gelu);                                                                       \
+    else                                                                                                      \
+      hipLaunchKernelGGL((dqlinear_kernel<L, MB, XF32, XL, NT, false>), g, dim3(NT), shm, s, one, apr, x, m,    \
+                         tab, round_w, 0);                                                                     \
+  } while (0)
   if (mb == 4) {
     if (xl) PLX_DQL(4, true); else PLX_DQL(4, false);
   } else if (mb == 2) {
