@@ -194,6 +194,8 @@ int plx_dequant_f16(const uint8_t *packed, int64_t n_packed_bytes, const uint16_
 #define PLX_DQL_W_AS_X 2 /* bf16 x: round W to bf16 first, as the reference's literal
                             F.linear(x, W.to(x.dtype)) does (pollux.py:507) */
 #define PLX_DQL_GELU 4   /* y = gelu(x W^T), torch's erf form (pollux.py:645) */
+#define PLX_DQL_RMS_NORM 8 /* plx_dequant_linear_multi only: RMS-normalise each fp32 x
+                              row first (pre-norm of pollux.py:660-661) */
 
 /* Workspace (device bytes, 16-byte aligned) plx_dequant_linear needs for
  * this shape, batch and flags (0 when none). */
@@ -217,12 +219,17 @@ int plx_dequant_linear(const uint8_t *packed, int64_t n_packed_bytes, const uint
 
 /* Several packed weights that share one x (e.g. the q, k and v projections,
  * pollux.py:616-621) in one call: for each target i,
- * y_i = [residual_i +] act(x W_i^T) with W_i [rows_i, cols] as in
+ * y_i = [residual_i +] act(n(x) W_i^T) with W_i [rows_i, cols] as in
  * plx_dequant_linear (act = GELU with PLX_DQL_GELU, else identity; residual_i
- * may be NULL: the residual adds of pollux.py:660-661).  Up to 16 targets; at
- * m_rows <= 16 up to four of them run in one GEMV launch.  No counterpart in
- * the reference's FFI (separate F.linear calls there); results equal separate
- * plx_dequant_linear calls followed by the epilogue. */
+ * may be NULL: the residual adds of pollux.py:660-661).  n(x) = x, or with
+ * PLX_DQL_RMS_NORM (fp32 x; norm_weight fp32 [cols], 16-byte aligned)
+ * x * rsqrt(mean(x^2) + norm_eps) * norm_weight per row, the block's ln1 /
+ * ln2 (pollux.py:580-582); norm_weight is NULL without the flag.  Up to 16
+ * targets; at m_rows <= 16 up to four of them run in one GEMV launch, which
+ * normalises x in LDS.  No counterpart in the reference's FFI (separate
+ * RMSNorm and F.linear calls there); results equal plx_rms_norm followed by
+ * separate plx_dequant_linear calls and the epilogue, up to the summation
+ * order of the norm's sum of squares. */
 typedef struct {
   const uint8_t *packed;     /* ((rows*cols/24 + 3)/4)*9 bytes, 16-byte aligned */
   const uint16_t *sigma16;   /* [rows] fp16 bits */
@@ -234,7 +241,8 @@ typedef struct {
 size_t plx_dequant_linear_multi_workspace_bytes(const plx_dql_target *targets, int n_targets, int64_t cols,
                                                 int64_t m_rows, int flags);
 int plx_dequant_linear_multi(const plx_dql_target *targets, int n_targets, int64_t cols, const void *x,
-                             int flags, int64_t m_rows, void *workspace, size_t workspace_bytes, void *stream);
+                             int flags, int64_t m_rows, const float *norm_weight, float norm_eps,
+                             void *workspace, size_t workspace_bytes, void *stream);
 
 /* ---- packed decoder steps ------------------------------------------------
  * No counterpart in the reference's FFI: the reference runs these steps as

@@ -254,13 +254,18 @@ size_t plx_dequant_linear_multi_workspace_bytes(const plx_dql_target *targets, i
 }
 
 int plx_dequant_linear_multi(const plx_dql_target *targets, int n, int64_t cols, const void *x, int flags,
-                             int64_t m_rows, void *workspace, size_t workspace_bytes, void *stream) {
+                             int64_t m_rows, const float *norm_weight, float norm_eps, void *workspace,
+                             size_t workspace_bytes, void *stream) {
   PLX_REQUIRE(targets != nullptr && n >= 1 && n <= 16, "plx_dequant_linear_multi: %d targets (1..16)", n);
   PLX_REQUIRE(cols > 0 && cols % kDim == 0, "plx_dequant_linear_multi: bad column count %lld",
               static_cast<long long>(cols));
   PLX_REQUIRE(m_rows >= 0, "plx_dequant_linear_multi: negative batch");
-  PLX_REQUIRE((flags & ~(PLX_DQL_X_F32 | PLX_DQL_W_AS_X | PLX_DQL_GELU)) == 0,
+  PLX_REQUIRE((flags & ~(PLX_DQL_X_F32 | PLX_DQL_W_AS_X | PLX_DQL_GELU | PLX_DQL_RMS_NORM)) == 0,
               "plx_dequant_linear_multi: unknown flags 0x%x", flags);
+  PLX_REQUIRE(((flags & PLX_DQL_RMS_NORM) != 0) == (norm_weight != nullptr),
+              "plx_dequant_linear_multi: PLX_DQL_RMS_NORM needs a norm weight, and a norm weight the flag");
+  PLX_REQUIRE(!(flags & PLX_DQL_RMS_NORM) || (flags & PLX_DQL_X_F32),
+              "plx_dequant_linear_multi: PLX_DQL_RMS_NORM takes fp32 x");
   DqlTarget t[16];
   int live = 0;
   for (int i = 0; i < n; ++i) {
@@ -272,7 +277,8 @@ int plx_dequant_linear_multi(const plx_dql_target *targets, int n, int64_t cols,
   }
   if (live == 0 || m_rows == 0) return PLX_OK;
   PLX_REQUIRE(x != nullptr, "plx_dequant_linear_multi: null x");
-  return launch_dequant_linear_multi(t, live, cols, x, flags, m_rows, workspace, workspace_bytes, as_stream(stream));
+  return launch_dequant_linear_multi(t, live, cols, x, flags, m_rows, norm_weight, norm_eps, workspace, workspace_bytes,
+                                     as_stream(stream));
 }
 
 int plx_rms_norm(const float *x, const float *w, float *y, int64_t rows, int64_t d, float eps, void *stream) {

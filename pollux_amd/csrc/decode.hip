@@ -3,7 +3,8 @@
 //
 // rmsnorm_kernel: y = x * rsqrt(mean(x^2) + eps) * w over rows of d fp32
 //   values (RMSNorm.forward, pollux.py:580-582); one wave per row, float4
-//   loads, the sum of squares reduced across the wave with shuffles.
+//   loads (all of a row's issued at once up to 2,048 values), the sum of
+//   squares reduced across the wave with shuffles.
 //
 // decode_attention_kernel: one block per (sequence, head).  For the new token
 //   it RMS-normalises q and k over the head's 24 values (q_ln / k_ln,
@@ -22,6 +23,7 @@ namespace plx {
 namespace {
 
 constexpr int kNormRowsPerBlock = 4;  // one wave per row
+constexpr int kNormRegVec = 8;        // float4 per lane held in registers (rows of <= 2,048 values)
 constexpr int kAttnThreads = 256;
 
 __device__ __forceinline__ float wave_sum(float v) {
@@ -30,6 +32,10 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// REG: rows of up to kNormRegVec float4 per lane (d <= 2,048) are held in
+// registers, so every load of the row is in flight before the reduction (a
+// loop of dependent trips through memory costs ~1 us per trip at one row).
+template <bool REG>
 __global__ __launch_bounds__(64 * kNormRowsPerBlock) void rmsnorm_kernel(const float *__restrict__ x,
                                                                         const float *__restrict__ w,
                                                                         float *__restrict__ y, int64_t rows, int d,
@@ -42,18 +48,43 @@ __global__ __launch_bounds__(64 * kNormRowsPerBlock) void rmsnorm_kernel(const f
   float4 *yr = reinterpret_cast<float4 *>(y + row * d);
   const int n4 = d >> 2;
   float ss = 0.f;
-  for (int i = lane; i < n4; i += 64) {
-    const float4 v = xr[i];
-    ss = fmaf(v.x, v.x, ss);
-    ss = fmaf(v.y, v.y, ss);
-    ss = fmaf(v.z, v.z, ss);
-    ss = fmaf(v.w, v.w, ss);
-  }
-  ss = wave_sum(ss);
-  const float r = 1.0f / sqrtf(ss / static_cast<float>(d) + eps);
-  for (int i = lane; i < n4; i += 64) {
-    const float4 v = xr[i], g = wr[i];
-    yr[i] = make_float4(v.x * r * g.x, v.y * r * g.y, v.z * r * g.z, v.w * r * g.w);
+  if constexpr (REG) {
+    float4 v[kNormRegVec], g[kNormRegVec];
+#pragma unroll
+    for (int k = 0; k < kNormRegVec; ++k) {
+      const int i = lane + 64 * k;
+      v[k] = i < n4 ? xr[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+      g[k] = i < n4 ? wr[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (int k = 0; k < kNormRegVec; ++k) {
+      ss = fmaf(v[k].x, v[k].x, ss);
+      ss = fmaf(v[k].y, v[k].y, ss);
+      ss = fmaf(v[k].z, v[k].z, ss);
+      ss = fmaf(v[k].w, v[k].w, ss);
+    }
+    ss = wave_sum(ss);
+    const float r = 1.0f / sqrtf(ss / static_cast<float>(d) + eps);
+#pragma unroll
+    for (int k = 0; k < kNormRegVec; ++k) {
+      const int i = lane + 64 * k;
+      if (i < n4)
+        yr[i] = make_float4(v[k].x * r * g[k].x, v[k].y * r * g[k].y, v[k].z * r * g[k].z, v[k].w * r * g[k].w);
+    }
+  } else {
+    for (int i = lane; i < n4; i += 64) {
+      const float4 v = xr[i];
+      ss = fmaf(v.x, v.x, ss);
+      ss = fmaf(v.y, v.y, ss);
+      ss = fmaf(v.z, v.z, ss);
+      ss = fmaf(v.w, v.w, ss);
+    }
+    ss = wave_sum(ss);
+    const float r = 1.0f / sqrtf(ss / static_cast<float>(d) + eps);
+    for (int i = lane; i < n4; i += 64) {
+      const float4 v = xr[i], g = wr[i];
+      yr[i] = make_float4(v.x * r * g.x, v.y * r * g.y, v.z * r * g.z, v.w * r * g.w);
+    }
   }
 }
 
@@ -174,8 +205,12 @@ int launch_rms_norm(const float *x, const float *w, float *y, int64_t rows, int6
   if ((al & 15u) != 0) return fail(PLX_EINVAL, "rms_norm: x, w and y must be 16-byte aligned");
   const int64_t blocks = (rows + kNormRowsPerBlock - 1) / kNormRowsPerBlock;
   if (blocks > 0x7FFFFFFFll) return fail(PLX_EINVAL, "rms_norm: too many rows");
-  hipLaunchKernelGGL(rmsnorm_kernel, dim3(static_cast<unsigned>(blocks)), dim3(64 * kNormRowsPerBlock), 0, s, x, w, y,
-                     rows, static_cast<int>(d), eps);
+  if (d <= 64 * 4 * kNormRegVec)
+    hipLaunchKernelGGL((rmsnorm_kernel<true>), dim3(static_cast<unsigned>(blocks)), dim3(64 * kNormRowsPerBlock), 0, s,
+                       x, w, y, rows, static_cast<int>(d), eps);
+  else
+    hipLaunchKernelGGL((rmsnorm_kernel<false>), dim3(static_cast<unsigned>(blocks)), dim3(64 * kNormRowsPerBlock), 0, s,
+                       x, w, y, rows, static_cast<int>(d), eps);
   return check_launch("rmsnorm_kernel");
 }
 

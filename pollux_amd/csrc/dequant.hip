@@ -169,6 +169,8 @@ struct DqlTargets {
   int64_t rows[kDqlMaxTargets];
   float *y[kDqlMaxTargets];
   const float *residual[kDqlMaxTargets];
+  const float *norm_w;  // fp32 x is RMS-normalised per token row in LDS first (or NULL)
+  float norm_eps;
   int n;
 };
 
@@ -237,6 +239,7 @@ __global__ __launch_bounds__(NT) void dqlinear_kernel(const DqlArgs<GEN> targets
                                                        const void *__restrict__ x, int64_t m_total,
                                                        const uint4 *__restrict__ kp_gemv, int round_w, int gelu) {
   extern __shared__ __align__(16) uint8_t smem[];
+  __shared__ float norm_red[NT / 64][MB];  // per-wave sums of squares (GEN with norm_w)
   constexpr int R = NT / L;
   const uint8_t *__restrict__ packed;
   const uint16_t *__restrict__ sigma16;
@@ -289,6 +292,9 @@ __global__ __launch_bounds__(NT) void dqlinear_kernel(const DqlArgs<GEN> targets
     const int mb_here = static_cast<int>(min(static_cast<int64_t>(MB), m_total - m0));
     if (XL) {
       __syncthreads();
+      float ss[MB];
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) ss[mb] = 0.f;
       // token rows are whole multiples of 8 elements (cols = 24 * apr): 8 per thread-step
       for (int64_t i = threadIdx.x; i < mb_here * cols / 8; i += NT) {
         float v[8];
@@ -296,6 +302,51 @@ __global__ __launch_bounds__(NT) void dqlinear_kernel(const DqlArgs<GEN> targets
         float4 *d = reinterpret_cast<float4 *>(xs + 8 * i);
         d[0] = make_float4(v[0], v[1], v[2], v[3]);
         d[1] = make_float4(v[4], v[5], v[6], v[7]);
+        if constexpr (GEN) {
+          if (targets.norm_w) {
+            float s = 0.f;
+#pragma unroll
+            for (int c = 0; c < 8; ++c) s = fmaf(v[c], v[c], s);
+            const int tr = static_cast<int>(8 * i / cols);
+#pragma unroll
+            for (int mb = 0; mb < MB; ++mb) ss[mb] += tr == mb ? s : 0.f;
+          }
+        }
+      }
+      if constexpr (GEN) {
+        // RMSNorm of each staged token row (pollux.py:580-582): every block
+        // sums the squares in the same order, so all blocks scale alike
+        if (targets.norm_w) {
+#pragma unroll
+          for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) ss[mb] += __shfl_xor(ss[mb], off, 64);
+          if (lane == 0)
+#pragma unroll
+            for (int mb = 0; mb < MB; ++mb) norm_red[threadIdx.x >> 6][mb] = ss[mb];
+          __syncthreads();
+          float rs[MB];
+#pragma unroll
+          for (int mb = 0; mb < MB; ++mb) {
+            float t = 0.f;
+#pragma unroll
+            for (int w = 0; w < NT / 64; ++w) t += norm_red[w][mb];
+            rs[mb] = 1.0f / sqrtf(t / static_cast<float>(cols) + targets.norm_eps);
+          }
+          const float4 *nw = reinterpret_cast<const float4 *>(targets.norm_w);
+          for (int64_t i = threadIdx.x; i < mb_here * cols / 8; i += NT) {
+            const int tr = static_cast<int>(8 * i / cols);
+            const int64_t c8 = 8 * i - static_cast<int64_t>(tr) * cols;
+            float r = rs[0];
+#pragma unroll
+            for (int mb = 1; mb < MB; ++mb) r = tr == mb ? rs[mb] : r;
+            float4 *d = reinterpret_cast<float4 *>(xs + 8 * i);
+            const float4 g0 = nw[c8 / 4], g1 = nw[c8 / 4 + 1];
+            const float4 a = d[0], b = d[1];
+            d[0] = make_float4(a.x * r * g0.x, a.y * r * g0.y, a.z * r * g0.z, a.w * r * g0.w);
+            d[1] = make_float4(b.x * r * g1.x, b.y * r * g1.y, b.z * r * g1.z, b.w * r * g1.w);
+          }
+        }
       }
     }
     __syncthreads();
@@ -389,16 +440,17 @@ __global__ __launch_bounds__(NT) void dqlinear_kernel(const DqlArgs<GEN> targets
   }
 }
 
+// t.norm_w (fp32 x only): x is normalised in the kernel when its rows fit in
+// LDS, else by rmsnorm into xnorm ([m, cols] fp32) first.
 template <int L, bool XF32, int NT>
 int launch_dql(DqlTargets t, int64_t apr, const void *x, int64_t m, const uint4 *tab, int round_w, int gelu,
-               hipStream_t s) {
+               float *xnorm, hipStream_t s) {
   constexpr int R = NT / L;
   int64_t blocks = 0;
   for (int i = 0; i < t.n; ++i) blocks = max(blocks, (t.rows[i] + R - 1) / R);
   if (blocks == 0) return PLX_OK;
   if (blocks > 0x7FFFFFFFll) return fail(PLX_EINVAL, "dequant_linear: too many rows");
-  const bool gen = t.n > 1 || t.residual[0] != nullptr || gelu;
-  const dim3 g(static_cast<unsigned>(blocks), static_cast<unsigned>(gen ? t.n : 1));
+  const dim3 g(static_cast<unsigned>(blocks), static_cast<unsigned>(t.n));
   const DqlOne one{t.packed[0], t.packed_bytes[0], t.sigma16[0], t.rows[0], t.y[0]};
   const size_t pbytes = static_cast<size_t>((R * apr + 8) / 4 + 2) * 9;
   const size_t p16 = ((pbytes + 15) & ~static_cast<size_t>(15)) + 16;  // + one vector of alignment slack
@@ -408,6 +460,13 @@ int launch_dql(DqlTargets t, int64_t apr, const void *x, int64_t m, const uint4 
   const bool xl = p16 + xbytes <= 48 * 1024;
   const size_t shm = xl ? p16 + xbytes : p16;
   if (shm > 64 * 1024) return fail(PLX_EINVAL, "dequant_linear: rows of %lld atoms are too long", static_cast<long long>(apr));
+  if (t.norm_w && !xl) {
+    const int st = launch_rms_norm(static_cast<const float *>(x), t.norm_w, xnorm, m, cols, t.norm_eps, s);
+    if (st != PLX_OK) return st;
+    x = xnorm;
+    t.norm_w = nullptr;
+  }
+  const bool gen = t.n > 1 || t.residual[0] != nullptr || gelu || t.norm_w != nullptr;
 #define PLX_DQL(MB, XL) \
   do {                                                                                                        \
     if (gen)                                                                                                  \
@@ -967,8 +1026,9 @@ bool uses_mfma(int /*flags*/, int64_t m) { return m > 16; }
 
 }  // namespace
 
-size_t dequant_linear_workspace_bytes_multi(const int64_t *rows, int n, int64_t cols, int64_t m, int flags) {
-  if (!uses_mfma(flags, m) || cols <= 0 || n <= 0) return 0;
+// MFMA part (fragment-order x + split partials) of the workspace
+size_t mm_workspace_bytes_multi(const int64_t *rows, int n, int64_t cols, int64_t m, int flags) {
+  if (!uses_mfma(flags, m)) return 0;
   // one fragment-order copy of x for every target, one partial buffer reused by them in stream order
   size_t xf = 0, partial = 0;
   for (int i = 0; i < n; ++i) {
@@ -980,12 +1040,21 @@ size_t dequant_linear_workspace_bytes_multi(const int64_t *rows, int n, int64_t 
   return xf + partial;
 }
 
+// Layout: [MFMA part | normalised x (PLX_DQL_RMS_NORM), 256-byte aligned]
+size_t dequant_linear_workspace_bytes_multi(const int64_t *rows, int n, int64_t cols, int64_t m, int flags) {
+  if (cols <= 0 || n <= 0 || m <= 0) return 0;
+  size_t total = mm_workspace_bytes_multi(rows, n, cols, m, flags);
+  if (flags & PLX_DQL_RMS_NORM) total = ((total + 255) & ~static_cast<size_t>(255)) + static_cast<size_t>(m * cols) * 4;
+  return total;
+}
+
 size_t dequant_linear_workspace_bytes(int64_t rows, int64_t cols, int64_t m, int flags) {
   return dequant_linear_workspace_bytes_multi(&rows, 1, cols, m, flags);
 }
 
 int launch_dequant_linear_multi(const DqlTarget *targets, int n, int64_t cols, const void *x, int flags, int64_t m,
-                                void *workspace, size_t workspace_bytes, hipStream_t s) {
+                                const float *norm_w, float norm_eps, void *workspace, size_t workspace_bytes,
+                                hipStream_t s) {
   if (n < 1 || n > 16) return fail(PLX_EINVAL, "dequant_linear: %d targets (1..16)", n);
   if ((reinterpret_cast<uintptr_t>(x) & 15u) != 0) return fail(PLX_EINVAL, "dequant_linear: x must be 16-byte aligned");
   for (int i = 0; i < n; ++i)
@@ -994,6 +1063,11 @@ int launch_dequant_linear_multi(const DqlTarget *targets, int n, int64_t cols, c
   const int x_is_f32 = flags & PLX_DQL_X_F32;
   const int round_w = !x_is_f32 && (flags & PLX_DQL_W_AS_X) ? 1 : 0;  // W.to(fp32) is exact
   const int gelu = (flags & PLX_DQL_GELU) ? 1 : 0;
+  const bool norm = (flags & PLX_DQL_RMS_NORM) != 0;
+  if (norm != (norm_w != nullptr))
+    return fail(PLX_EINVAL, "dequant_linear: PLX_DQL_RMS_NORM and a norm weight go together");
+  if (norm && (!x_is_f32 || (reinterpret_cast<uintptr_t>(norm_w) & 15u) != 0))
+    return fail(PLX_EINVAL, "dequant_linear: the RMS norm takes fp32 x and a 16-byte aligned weight");
   int64_t rows_list[16];
   for (int i = 0; i < n; ++i) rows_list[i] = targets[i].rows;
   const size_t need = dequant_linear_workspace_bytes_multi(rows_list, n, cols, m, flags);
@@ -1005,6 +1079,10 @@ int launch_dequant_linear_multi(const DqlTarget *targets, int n, int64_t cols, c
   int st = get_tables(&tab);
   if (st != PLX_OK) return st;
   const int64_t apr = cols / kDim;
+  float *xnorm = norm ? reinterpret_cast<float *>(static_cast<uint8_t *>(workspace) +
+                                                  ((mm_workspace_bytes_multi(rows_list, n, cols, m, flags) + 255) &
+                                                   ~static_cast<size_t>(255)))
+                      : nullptr;
   if (uses_mfma(flags, m)) {
     // batches above 16 tokens: MFMA dequant-GEMM in slabs of 64 tokens, one launch (+ split sum) per target
     if (cols > kMmMaxCols)
@@ -1014,6 +1092,11 @@ int launch_dequant_linear_multi(const DqlTarget *targets, int n, int64_t cols, c
     uint4 *xf = reinterpret_cast<uint4 *>(wsb);
     const int64_t slabs = (m + 63) / 64, nq = (apr + 3) / 4;
     const dim3 gx(static_cast<unsigned>(nq * 3), static_cast<unsigned>(slabs));
+    if (norm) {
+      st = launch_rms_norm(static_cast<const float *>(x), norm_w, xnorm, m, cols, norm_eps, s);
+      if (st != PLX_OK) return st;
+      x = xnorm;
+    }
     if (x_is_f32)
       hipLaunchKernelGGL((xfrag_kernel<true>), gx, dim3(256), 0, s, x, m, cols, nq, xf);
     else
@@ -1055,20 +1138,22 @@ int launch_dequant_linear_multi(const DqlTarget *targets, int n, int64_t cols, c
       t.y[i] = src.y;
       t.residual[i] = src.residual;
     }
+    t.norm_w = norm_w;
+    t.norm_eps = norm_eps;
     // lanes per row: about 3-5 atoms per lane (7680 x 1920 at M = 1: 16 lanes 6% faster than 32, 8 slower);
     // 512-thread blocks (4% faster than 256 at M = 1, 1,024 slower), 256 for rows too long to stage 8 in LDS
     if (apr >= 3072)
-      st = x_is_f32 ? launch_dql<64, true, 256>(t, apr, x, m, kp, round_w, gelu, s)
-                    : launch_dql<64, false, 256>(t, apr, x, m, kp, round_w, gelu, s);
+      st = x_is_f32 ? launch_dql<64, true, 256>(t, apr, x, m, kp, round_w, gelu, xnorm, s)
+                    : launch_dql<64, false, 256>(t, apr, x, m, kp, round_w, gelu, xnorm, s);
     else if (apr >= 160)
-      st = x_is_f32 ? launch_dql<64, true, 512>(t, apr, x, m, kp, round_w, gelu, s)
-                    : launch_dql<64, false, 512>(t, apr, x, m, kp, round_w, gelu, s);
+      st = x_is_f32 ? launch_dql<64, true, 512>(t, apr, x, m, kp, round_w, gelu, xnorm, s)
+                    : launch_dql<64, false, 512>(t, apr, x, m, kp, round_w, gelu, xnorm, s);
     else if (apr >= 16)
-      st = x_is_f32 ? launch_dql<16, true, 512>(t, apr, x, m, kp, round_w, gelu, s)
-                    : launch_dql<16, false, 512>(t, apr, x, m, kp, round_w, gelu, s);
+      st = x_is_f32 ? launch_dql<16, true, 512>(t, apr, x, m, kp, round_w, gelu, xnorm, s)
+                    : launch_dql<16, false, 512>(t, apr, x, m, kp, round_w, gelu, xnorm, s);
     else
-      st = x_is_f32 ? launch_dql<8, true, 512>(t, apr, x, m, kp, round_w, gelu, s)
-                    : launch_dql<8, false, 512>(t, apr, x, m, kp, round_w, gelu, s);
+      st = x_is_f32 ? launch_dql<8, true, 512>(t, apr, x, m, kp, round_w, gelu, xnorm, s)
+                    : launch_dql<8, false, 512>(t, apr, x, m, kp, round_w, gelu, xnorm, s);
   }
   return st;
 }
@@ -1076,7 +1161,7 @@ int launch_dequant_linear_multi(const DqlTarget *targets, int n, int64_t cols, c
 int launch_dequant_linear(const uint8_t *packed, const uint16_t *sigma16, int64_t rows, int64_t cols, const void *x,
                           int flags, int64_t m, float *y, void *workspace, size_t workspace_bytes, hipStream_t s) {
   const DqlTarget t{packed, sigma16, rows, y, nullptr};
-  return launch_dequant_linear_multi(&t, 1, cols, x, flags, m, workspace, workspace_bytes, s);
+  return launch_dequant_linear_multi(&t, 1, cols, x, flags, m, nullptr, 0.f, workspace, workspace_bytes, s);
 }
 
 }  // namespace plx

@@ -95,7 +95,8 @@ struct DqlTarget {
 };
 size_t dequant_linear_workspace_bytes_multi(const int64_t *rows, int n, int64_t cols, int64_t m, int flags);
 int launch_dequant_linear_multi(const DqlTarget *targets, int n, int64_t cols, const void *x, int flags, int64_t m,
-                                void *workspace, size_t workspace_bytes, hipStream_t s);
+                                const float *norm_w, float norm_eps, void *workspace, size_t workspace_bytes,
+                                hipStream_t s);
 size_t dequant_linear_workspace_bytes(int64_t rows, int64_t cols, int64_t m, int flags);
 int launch_dequant_linear(const uint8_t *packed, const uint16_t *sigma16, int64_t rows, int64_t cols, const void *x,
                           int flags, int64_t m, float *y, void *workspace, size_t workspace_bytes, hipStream_t s);

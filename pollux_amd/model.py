@@ -172,10 +172,12 @@ class PackedCausalAttention(nn.Module):
         self.k_ln = RMSNorm(self.d_head)
 
     def forward(self, x: torch.Tensor, cache: KVCache | None = None, layer: int = 0,
-                pos: torch.Tensor | None = None, residual: torch.Tensor | None = None) -> torch.Tensor:
-        """[residual +] o_proj(attention(x)); the q, k, v projections share one dequant-linear call."""
+                pos: torch.Tensor | None = None, residual: torch.Tensor | None = None,
+                norm: RMSNorm | None = None) -> torch.Tensor:
+        """[residual +] o_proj(attention(norm(x))); norm and the q, k, v projections share one dequant-linear call."""
         b, t, c = x.shape
-        q, k, v = packed_linear_group([self.q_proj, self.k_proj, self.v_proj], x)
+        q, k, v = packed_linear_group([self.q_proj, self.k_proj, self.v_proj], x,
+                                      norm=None if norm is None else (norm.weight, norm.eps))
         if cache is not None and t == 1:
             # one new token per sequence: norms, cache write and attention in one kernel at device position pos
             if pos is None:
@@ -211,9 +213,10 @@ class PackedMLP(nn.Module):
         self.fc1 = PackedH24Linear(n_embd, 4 * n_embd)
         self.fc2 = PackedH24Linear(4 * n_embd, n_embd)
 
-    def forward(self, x: torch.Tensor, residual: torch.Tensor | None = None) -> torch.Tensor:
-        """[residual +] fc2(gelu(fc1(x))), with the GELU and the residual add in the dequant-linear epilogues."""
-        h = packed_linear_group([self.fc1], x, gelu=True)[0]
+    def forward(self, x: torch.Tensor, residual: torch.Tensor | None = None,
+                norm: RMSNorm | None = None) -> torch.Tensor:
+        """[residual +] fc2(gelu(fc1(norm(x)))): the norm is fc1's prologue, the GELU and the residual add epilogues."""
+        h = packed_linear_group([self.fc1], x, gelu=True, norm=None if norm is None else (norm.weight, norm.eps))[0]
         return packed_linear_group([self.fc2], h, residuals=[residual])[0]
 
 
@@ -229,8 +232,8 @@ class PackedBlock(nn.Module):
 
     def forward(self, x: torch.Tensor, cache: KVCache | None = None, layer: int = 0,
                 pos: torch.Tensor | None = None) -> torch.Tensor:
-        x = self.attn(self.ln1(x), cache, layer, pos, residual=x)  # x + attn(ln1(x))
-        return self.mlp(self.ln2(x), residual=x)                    # x + mlp(ln2(x))
+        x = self.attn(x, cache, layer, pos, residual=x, norm=self.ln1)  # x + attn(ln1(x))
+        return self.mlp(x, residual=x, norm=self.ln2)                    # x + mlp(ln2(x))
 
 
 class PackedPolluxModel(nn.Module):

@@ -40,7 +40,7 @@ def dequantize_h24(packed: torch.Tensor, sigma16: torch.Tensor, out_features: in
     return out
 
 
-DQL_X_F32, DQL_W_AS_X, DQL_GELU = 1, 2, 4  # plx_dequant_linear flags (include/pollux_amd.h)
+DQL_X_F32, DQL_W_AS_X, DQL_GELU, DQL_RMS_NORM = 1, 2, 4, 8  # plx_dequant_linear flags (include/pollux_amd.h)
 
 
 def dequant_linear(
@@ -92,14 +92,16 @@ def dequant_linear(
 def dequant_linear_multi(
     weights: list[tuple[torch.Tensor, torch.Tensor, int]], in_features: int, x: torch.Tensor, *,
     residuals: list[torch.Tensor | None] | None = None, gelu: bool = False, weight_rounding: str = "exact",
+    norm: tuple[torch.Tensor, float] | None = None,
 ) -> list[torch.Tensor]:
-    """Several packed weights sharing x in one call: [residual_i +] act(x @ W_i.T), fp32 [..., out_i] each.
+    """Several packed weights sharing x in one call: [residual_i +] act(n(x) @ W_i.T), fp32 [..., out_i] each.
 
     ``weights``: (packed, sigma16, out_features) per target; act = GELU (erf
     form, as F.gelu) when ``gelu``; ``residuals``: fp32 [..., out_i] tensors
-    added after the activation (or None).  At up to 16 tokens, four targets
-    share one GEMV launch.  Results equal separate dequant_linear calls
-    followed by the same epilogue.
+    added after the activation (or None); ``norm``: (weight, eps) of an
+    RMSNorm applied to x first (fp32 x; n = identity when None).  At up to 16
+    tokens, four targets share one GEMV launch, which also normalises x.
+    Results equal separate dequant_linear calls followed by the same epilogue.
     """
     if weight_rounding not in ("exact", "as_x"):
         raise ValueError(f"weight_rounding must be 'exact' or 'as_x', got {weight_rounding!r}")
@@ -141,29 +143,43 @@ def dequant_linear_multi(
         ys.append(y)
     flags = (DQL_X_F32 if xx.dtype == torch.float32 else 0) | (DQL_W_AS_X if weight_rounding == "as_x" else 0) | (
         DQL_GELU if gelu else 0)
+    nw, eps = None, 0.0
+    if norm is not None:
+        nw, eps = norm[0].detach(), float(norm[1])
+        if xx.dtype != torch.float32 or nw.dtype != torch.float32 or nw.numel() != in_features:
+            raise ValueError(f"norm: fp32 x and an fp32 weight of {in_features} values")
+        _lib.require_device(nw, "dequant_linear_multi norm weight")
+        nw = nw.reshape(-1).contiguous()
+        if nw.data_ptr() % 16:
+            nw = nw.clone()
+        flags |= DQL_RMS_NORM
     lib = _lib.lib()
     nws = int(lib.plx_dequant_linear_multi_workspace_bytes(arr, len(weights), in_features, m, flags))
     ws = torch.empty(max(nws, 16), dtype=torch.uint8, device=xx.device) if nws else None
     with torch.cuda.device(xx.device):
-        st = lib.plx_dequant_linear_multi(arr, len(weights), in_features, _lib.ptr(xx), flags, m, _lib.ptr(ws), nws,
-                                          _lib.stream_of(xx.device))
+        st = lib.plx_dequant_linear_multi(arr, len(weights), in_features, _lib.ptr(xx), flags, m, _lib.ptr(nw), eps,
+                                          _lib.ptr(ws), nws, _lib.stream_of(xx.device))
     _lib.check(st, "dequant_linear_multi")
     return [y.reshape(*lead, y.shape[1]) for y in ys]
 
 
 def packed_linear_group(layers: list, x: torch.Tensor, *, residuals: list | None = None,
-                        gelu: bool = False) -> list[torch.Tensor]:
-    """[residual +] act(layer(x)) for PackedH24Linear layers sharing x, fused when they are all packed.
+                        gelu: bool = False, norm: tuple[torch.Tensor, float] | None = None) -> list[torch.Tensor]:
+    """[residual +] act(layer(n(x))) for PackedH24Linear layers sharing x, fused when they are all packed.
 
-    Materialised layers take the reference's ops instead (F.linear on the
-    weight cast to x's dtype, F.gelu, then the residual add).
+    ``norm``: (weight, eps) of an RMSNorm applied to x first (fp32 x), or None.
+    Materialised layers take the reference's ops instead (the RMSNorm
+    expression of pollux.py:580-582, F.linear on the weight cast to x's dtype,
+    F.gelu, then the residual add).
     """
     residuals = residuals or [None] * len(layers)
     if all(isinstance(l, PackedH24Linear) and not l._materialized and l.bias is None for l in layers):
         ys = dequant_linear_multi([(l.packed_weights, l.sigma_rows, l.out_features) for l in layers],
                                   layers[0].in_features, x, residuals=residuals, gelu=gelu,
-                                  weight_rounding=layers[0].weight_rounding)
+                                  weight_rounding=layers[0].weight_rounding, norm=norm)
         return [y.to(x.dtype) for y in ys]
+    if norm is not None:
+        x = x * torch.rsqrt(x.pow(2).mean(dim=-1, keepdim=True) + norm[1]) * norm[0]
     outs = []
     for layer, r in zip(layers, residuals):
         y = layer(x)

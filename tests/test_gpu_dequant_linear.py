@@ -210,3 +210,63 @@ def test_multi_target_bad_arguments(dev):
         dequant_linear_multi([(packed.to(dev)[:-9], sig.to(dev), 48)], 48, x)
     with pytest.raises(ValueError):
         dequant_linear_multi([(packed.to(dev), sig.to(dev), 48)], 48, x, residuals=[torch.zeros(3, device=dev)])
+
+
+# in-kernel norm: m = 1, 3 (two token chunks of 2), 7 (chunks of 4 and 3) at 1920 columns;
+# x too wide to stage in LDS (5 x 3072: the norm runs as plx_rms_norm into the workspace first);
+# the MFMA batch path (40 tokens)
+@pytest.mark.parametrize("m,in_f", [(1, 1920), (3, 1920), (7, 1920), (5, 3072), (40, 1920)])
+def test_multi_target_rms_norm_prologue(dev, m, in_f):
+    from pollux_amd.model import rms_norm
+    from pollux_amd.packed import dequant_linear_multi
+
+    shapes = [1920, 96]
+    layers = [_layer(o, in_f, 300 + i + m) for i, o in enumerate(shapes)]
+    g = torch.Generator().manual_seed(m * 7 + in_f)
+    x = (torch.randn(m, in_f, generator=g) * 3.0 + 0.5).to(dev)
+    nw = (1.0 + 0.1 * torch.randn(in_f, generator=g)).to(dev)
+    r = torch.randn(m, shapes[0], generator=g).to(dev)
+    weights = [(pk.to(dev), sig.to(dev), o) for (idx, sig, pk, _), o in zip(layers, shapes)]
+    ys = dequant_linear_multi(weights, in_f, x, residuals=[r, None], norm=(nw, 1e-8))
+    xn = rms_norm(x, nw, 1e-8)
+    in_lds = m <= 16 and in_f == 1920
+    for i, ((pk, sg, o), y) in enumerate(zip(weights, ys)):
+        sep = dequant_linear(pk, sg, o, in_f, xn) + (r if i == 0 else 0.0)
+        if in_lds:  # the sum of squares is taken in another order than plx_rms_norm's
+            rel = ((y - sep).double().norm() / sep.double().norm()).item()
+            print(f"[dql] norm prologue m={m} target {i}: rel vs rms_norm + dequant_linear {rel:.2e}", flush=True)
+            assert rel <= 1e-6
+        else:
+            assert torch.equal(y, sep)
+    # against the reference's expressions in fp64 (RMSNorm.forward, F.linear on the fp16 weight)
+    idx, sig, _, _ = layers[1]
+    w16 = torch_ref.materialize(idx, sig, shapes[1], in_f)
+    xd = x.double().cpu()
+    xn_ref = (xd * torch.rsqrt(xd.pow(2).mean(dim=-1, keepdim=True) + 1e-8) * nw.double().cpu()).float()
+    _check(ys[1].cpu(), xn_ref, w16)
+
+
+def test_rms_norm_flag_and_weight_go_together(dev):
+    from pollux_amd import _lib
+    from pollux_amd.packed import DQL_RMS_NORM, DQL_X_F32, dequant_linear_multi
+
+    idx, sig, packed, g = _layer(48, 48, 6)
+    pk, sg = packed.to(dev), sig.to(dev)
+    x = torch.randn(2, 48, device=dev)
+    with pytest.raises(ValueError):  # bf16 x
+        dequant_linear_multi([(pk, sg, 48)], 48, x.bfloat16(), norm=(torch.ones(48, device=dev), 1e-8))
+    with pytest.raises(ValueError):  # weight of the wrong length
+        dequant_linear_multi([(pk, sg, 48)], 48, x, norm=(torch.ones(24, device=dev), 1e-8))
+    y = torch.zeros(2, 48, device=dev)
+    arr = (_lib.DqlTarget * 1)()
+    arr[0] = _lib.DqlTarget(pk.data_ptr(), sg.data_ptr(), 48, y.data_ptr(), None)
+    lib = _lib.lib()
+    w = torch.ones(48, device=dev)
+    s = _lib.stream_of(x.device)
+    # flag without weight, weight without flag, flag with bf16 x: refused before any launch
+    assert lib.plx_dequant_linear_multi(arr, 1, 48, x.data_ptr(), DQL_X_F32 | DQL_RMS_NORM, 2, None, 1e-8, None, 0, s) != 0
+    assert lib.plx_dequant_linear_multi(arr, 1, 48, x.data_ptr(), DQL_X_F32, 2, w.data_ptr(), 1e-8, None, 0, s) != 0
+    xb = x.bfloat16()
+    assert lib.plx_dequant_linear_multi(arr, 1, 48, xb.data_ptr(), DQL_RMS_NORM, 2, w.data_ptr(), 1e-8, None, 0, s) != 0
+    torch.cuda.synchronize()
+    assert torch.equal(y, torch.zeros(2, 48, device=dev))
