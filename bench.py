@@ -255,20 +255,12 @@ def traffic_from_profiles():
     return None
 
 
-def decode_extras(device, prompt_len=64, new_tokens=128):
-    """Packed Pollux-1920 decoder (18 layers, d 1920, vocab 50,688; random packed weights): tokens/s at batch 1.
-
-    graph: GraphDecoder (KV cache, one HIP graph replay per token, greedy
-    argmax on the device); eager: the same cached decode as plain module
-    calls; recompute: the reference's loop (generate.py:313-315), the full
-    prefix per token, once with the packed layers fused and once the
-    reference's way (materialised fp16 weights cast to fp32 by every
-    F.linear call, pollux.py:507).
-    """
+def random_packed_pollux(device):
+    """(model, generator): packed Pollux-1920 (18 layers, d 1920, vocab 50,688), random packed weights (valid indices)."""
     import torch
 
     from pollux_amd import castor
-    from pollux_amd.model import GraphDecoder, PackedPolluxModel
+    from pollux_amd.model import PackedPolluxModel
     from pollux_amd.plx import PLX_FORMAT
 
     cfg = {"n_layers": 18, "n_heads": 80, "d_head": 24, "n_embd": 1920, "vocab_size": 50688,
@@ -295,7 +287,24 @@ def decode_extras(device, prompt_len=64, new_tokens=128):
             state[p + name + ".sigma_rows"] = (torch.rand(o, generator=g, device=device) * 0.045 + 0.005).half()
     payload = {"format": PLX_FORMAT, "config": cfg, "codebook_fingerprint": castor.codebook_fingerprint(),
                "state_dict": state}
-    model = PackedPolluxModel.from_packed_checkpoint(payload, device)
+    return PackedPolluxModel.from_packed_checkpoint(payload, device), g
+
+
+def decode_extras(device, prompt_len=64, new_tokens=128):
+    """Packed Pollux-1920 decoder (18 layers, d 1920, vocab 50,688; random packed weights): tokens/s at batch 1.
+
+    graph: GraphDecoder (KV cache, one HIP graph replay per token, greedy
+    argmax on the device); eager: the same cached decode as plain module
+    calls; recompute: the reference's loop (generate.py:313-315), the full
+    prefix per token, once with the packed layers fused and once the
+    reference's way (materialised fp16 weights cast to fp32 by every
+    F.linear call, pollux.py:507).
+    """
+    import torch
+
+    from pollux_amd.model import GraphDecoder
+
+    model, g = random_packed_pollux(device)
     prompt = torch.randint(0, 50257, (1, prompt_len), generator=g, device=device)
 
     def timed(fn, n):

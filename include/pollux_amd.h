@@ -278,6 +278,29 @@ int plx_quantize_int8_rows(const float *w, int64_t rows, int64_t cols, int8_t *q
 int plx_dequant_int8_rows(const int8_t *q, const uint16_t *mu16, int64_t rows, int64_t cols,
                           uint16_t *w16_out, void *stream);
 
+/* y[m, r] = sum_j n(x)[m, j] * w16[r, j] for m < m_rows (fp32 x [m_rows, cols],
+ * y fp32 [m_rows, rows]), with w16 = the materialisation above, never stored:
+ * exact products accumulated in fp32, the numerics of PackedInt8Linear.forward
+ * (pollux.py:562-563, F.linear(x, W.to(x.dtype))).  n(x) = x, or with a
+ * norm_weight (fp32 [cols]) x * rsqrt(mean(x^2) + norm_eps) * norm_weight per
+ * token (the final norm ln_f before the head, pollux.py:699-700).
+ * cols % 16 == 0 and <= 4,096; q, x, norm_weight 16-byte aligned.  Streams the
+ * INT8 rows once per 4 tokens (meant for decode batches of a few tokens). */
+int plx_int8_linear(const int8_t *q, const uint16_t *mu16, int64_t rows, int64_t cols, const float *x,
+                    int64_t m_rows, const float *norm_weight, float norm_eps, float *y, void *stream);
+
+/* out[b, i, :] = fp32(w16[ids[b, i], :]) + pos_weight[*pos0 + i, :] for b < batch,
+ * i < t (fp32 out [batch, t, cols]): PackedInt8Embedding.forward plus the
+ * position embedding (pollux.py:532-533, 691-693) in one kernel.  pos_weight
+ * fp32 [pos_rows, cols] or NULL (no position term); pos0: device int64 start
+ * position (NULL = 0), read at run time.  An id outside 0..vocab-1 or a
+ * position outside 0..pos_rows-1 yields a NaN row.  cols % 4 == 0; q 4-byte,
+ * pos_weight and out 16-byte aligned.  No counterpart in the reference's FFI
+ * (embedding gather, cast and add are separate torch ops there). */
+int plx_int8_embed(const int8_t *q, const uint16_t *mu16, int64_t vocab, int64_t cols, const int64_t *ids,
+                   int64_t batch, int64_t t, const float *pos_weight, int64_t pos_rows, const int64_t *pos0,
+                   float *out, void *stream);
+
 /* ---- kernel timing (diagnostics; no counterpart in the reference) ------ */
 /* While enabled, every launch of the quantizer's scoring kernel (nn_kernel)
  * is bracketed by HIP events recorded on its launch stream (up to 4096

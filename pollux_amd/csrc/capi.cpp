@@ -323,6 +323,24 @@ int plx_dequant_linear(const uint8_t *packed, int64_t n_packed_bytes, const uint
                                as_stream(stream));
 }
 
+int plx_int8_linear(const int8_t *q, const uint16_t *mu16, int64_t rows, int64_t cols, const float *x, int64_t m_rows,
+                    const float *norm_weight, float norm_eps, float *y, void *stream) {
+  PLX_REQUIRE(rows >= 0 && cols > 0 && m_rows >= 0, "plx_int8_linear: bad shape (%lld, %lld) x %lld tokens",
+              static_cast<long long>(rows), static_cast<long long>(cols), static_cast<long long>(m_rows));
+  if (rows == 0 || m_rows == 0) return PLX_OK;
+  PLX_REQUIRE(q != nullptr && mu16 != nullptr && x != nullptr && y != nullptr, "plx_int8_linear: null pointer");
+  return launch_int8_linear(q, mu16, rows, cols, x, m_rows, norm_weight, norm_eps, y, as_stream(stream));
+}
+
+int plx_int8_embed(const int8_t *q, const uint16_t *mu16, int64_t vocab, int64_t cols, const int64_t *ids,
+                   int64_t batch, int64_t t, const float *pos_weight, int64_t pos_rows, const int64_t *pos0, float *out,
+                   void *stream) {
+  PLX_REQUIRE(vocab >= 0 && cols > 0 && batch >= 0 && t >= 0 && pos_rows >= 0, "plx_int8_embed: bad shape");
+  if (batch == 0 || t == 0) return PLX_OK;
+  PLX_REQUIRE(q != nullptr && mu16 != nullptr && ids != nullptr && out != nullptr, "plx_int8_embed: null pointer");
+  return launch_int8_embed(q, mu16, vocab, cols, ids, batch * t, t, pos_weight, pos_rows, pos0, out, as_stream(stream));
+}
+
 int plx_quantize_int8_rows(const float *w, int64_t rows, int64_t cols, int8_t *q_out, uint16_t *mu16_out,
                            void *stream) {
   PLX_REQUIRE(rows >= 0 && cols > 0, "plx_quantize_int8_rows: bad shape (%lld, %lld)", static_cast<long long>(rows),

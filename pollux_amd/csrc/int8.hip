@@ -12,6 +12,23 @@
 //
 // One wave per row; both kernels stream the row with 16-byte accesses when
 // the row is 16-byte aligned, else element-wise.
+//
+// int8_linear_kernel: y[m, r] = sum_j n(x)[m, j] * w_j of row r, fp32
+//   accumulation of exact products with the fp16 weights above, never stored
+//   (PackedInt8Linear.forward, pollux.py:562-563: F.linear(x, W.to(x.dtype)),
+//   W fp16 and x fp32); n = identity or the final RMSNorm ln_f
+//   (pollux.py:699-700) applied to x in registers.  One wave per run of rows;
+//   lane l holds x of the 16-column chunks l, l + 64, ... for MB tokens in
+//   registers and streams the same chunks of 4 rows at a time (16-byte loads).
+//   Weights: the 4 bytes of a dword, offset by 128 (xor 0x80), become the low
+//   bytes of fp16 values 1024 + u (v_perm_b32 with 0x64 high bytes), minus
+//   1152 gives q exactly, and one fp16 multiply by s16 rounds q * s16 once -
+//   the same value as fp16(fp32(q) * fp32(s16)), whose fp32 product is exact.
+//
+// int8_embed_kernel: out[b, i, :] = fp32(w[idx[b, i], :]) + pos_w[p0 + i, :]
+//   (PackedInt8Embedding.forward + the position embedding, pollux.py:532-533,
+//   691-693), p0 read from device memory (a captured graph replays it while
+//   the position advances); an id or position out of range yields a NaN row.
 
 #include <hip/hip_fp16.h>
 
@@ -85,6 +102,173 @@ __global__ __launch_bounds__(256) void int8_dequant_kernel(const int8_t *__restr
   }
 }
 
+constexpr int kLinWaves = 4;  // waves per block of int8_linear_kernel
+
+__device__ __forceinline__ float wave_sum64(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+// s16 of a row as fp32 (fp16(fp32(mu16) * fp32(1/127)))
+__device__ __forceinline__ float int8_row_scale(uint16_t mu) {
+  return __half2float(__float2half_rn(__half2float(__ushort_as_half(mu)) * (1.0f / 127.0f)));
+}
+
+// the fp16 weights of bytes 0,1 (lo) and 2,3 (hi) of d, each pair times s2
+__device__ __forceinline__ void int8x4_weights(uint32_t d, __half2 s2, __half2 &lo, __half2 &hi) {
+  const uint32_t u = d ^ 0x80808080u;
+  const uint32_t a = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);  // 1024 + u0, 1024 + u1
+  const uint32_t b = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);  // 1024 + u2, 1024 + u3
+  const __half2 off = __halves2half2(__ushort_as_half(0x6480), __ushort_as_half(0x6480));  // 1152
+  lo = __hmul2(__hsub2(*reinterpret_cast<const __half2 *>(&a), off), s2);
+  hi = __hmul2(__hsub2(*reinterpret_cast<const __half2 *>(&b), off), s2);
+}
+
+template <int CPL, int MB, bool NORM>
+__global__ __launch_bounds__(64 * kLinWaves) void int8_linear_kernel(
+    const int8_t *__restrict__ q, const uint16_t *__restrict__ mu16, int64_t rows, int cols,
+    const float *__restrict__ x, int64_t m_total, const float *__restrict__ norm_w, float eps, int rows_per_wave,
+    float *__restrict__ y) {
+  const int lane = threadIdx.x & 63;
+  const int64_t wave = static_cast<int64_t>(blockIdx.x) * kLinWaves + (threadIdx.x >> 6);
+  const int64_t r_begin = wave * rows_per_wave;
+  if (r_begin >= rows) return;  // the whole wave (no block barriers here)
+  const int64_t r_end = min(rows, r_begin + rows_per_wave);
+  const int nch = cols >> 4;
+  for (int64_t m0 = 0; m0 < m_total; m0 += MB) {
+    const int mb_here = static_cast<int>(min(static_cast<int64_t>(MB), m_total - m0));
+    float xr[MB][CPL][16];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) {
+        const int c = lane + 64 * j;
+        const bool ok = c < nch && mb < mb_here;
+        const float4 *src = reinterpret_cast<const float4 *>(x + (m0 + mb) * cols + 16 * c);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const float4 v = ok ? src[k] : make_float4(0.f, 0.f, 0.f, 0.f);
+          xr[mb][j][4 * k] = v.x;
+          xr[mb][j][4 * k + 1] = v.y;
+          xr[mb][j][4 * k + 2] = v.z;
+          xr[mb][j][4 * k + 3] = v.w;
+        }
+      }
+    if constexpr (NORM) {
+      // x * rsqrt(mean(x^2) + eps) * w per token (pollux.py:580-582); every wave sums alike
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) {
+        float ss = 0.f;
+#pragma unroll
+        for (int j = 0; j < CPL; ++j)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) ss = fmaf(xr[mb][j][e], xr[mb][j][e], ss);
+        ss = wave_sum64(ss);
+        const float r = 1.0f / sqrtf(ss / static_cast<float>(cols) + eps);
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) {
+          const int c = lane + 64 * j;
+          if (c >= nch) continue;
+          const float4 *g4 = reinterpret_cast<const float4 *>(norm_w + 16 * c);
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            const float4 g = g4[k];
+            xr[mb][j][4 * k] = xr[mb][j][4 * k] * r * g.x;
+            xr[mb][j][4 * k + 1] = xr[mb][j][4 * k + 1] * r * g.y;
+            xr[mb][j][4 * k + 2] = xr[mb][j][4 * k + 2] * r * g.z;
+            xr[mb][j][4 * k + 3] = xr[mb][j][4 * k + 3] * r * g.w;
+          }
+        }
+      }
+    }
+    for (int64_t r0 = r_begin; r0 < r_end; r0 += 4) {
+      uint4 qv[4][CPL];
+      float sc[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int64_t row = r0 + i;
+        const bool rv = row < r_end;
+        sc[i] = rv ? int8_row_scale(mu16[row]) : 0.f;
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) {
+          const int c = lane + 64 * j;
+          qv[i][j] = rv && c < nch ? *reinterpret_cast<const uint4 *>(q + row * cols + 16 * c) : make_uint4(0, 0, 0, 0);
+        }
+      }
+      float acc[4][MB];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) acc[i][mb] = 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const __half2 s2 = __float2half2_rn(sc[i]);  // exact: sc is an fp16 value
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) {
+          if (lane + 64 * j >= nch) continue;
+          const uint32_t d[4] = {qv[i][j].x, qv[i][j].y, qv[i][j].z, qv[i][j].w};
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            __half2 lo, hi;
+            int8x4_weights(d[k], s2, lo, hi);
+            const float w0 = __low2float(lo), w1 = __high2float(lo), w2 = __low2float(hi), w3 = __high2float(hi);
+#pragma unroll
+            for (int mb = 0; mb < MB; ++mb) {
+              float a = acc[i][mb];
+              a = fmaf(w0, xr[mb][j][4 * k], a);
+              a = fmaf(w1, xr[mb][j][4 * k + 1], a);
+              a = fmaf(w2, xr[mb][j][4 * k + 2], a);
+              a = fmaf(w3, xr[mb][j][4 * k + 3], a);
+              acc[i][mb] = a;
+            }
+          }
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) {
+          const float v = wave_sum64(acc[i][mb]);
+          if (lane == i * MB + mb && r0 + i < r_end && mb < mb_here) y[(m0 + mb) * rows + r0 + i] = v;
+        }
+    }
+  }
+}
+
+// one wave per token; cols % 4 == 0, q rows 4-byte aligned, pos_w / out 16-byte aligned
+__global__ __launch_bounds__(256) void int8_embed_kernel(const int8_t *__restrict__ q,
+                                                         const uint16_t *__restrict__ mu16, int64_t vocab, int cols,
+                                                         const int64_t *__restrict__ idx, int64_t n, int64_t t,
+                                                         const float *__restrict__ pos_w, int64_t pos_rows,
+                                                         const int64_t *__restrict__ pos0, float *__restrict__ out) {
+  const int lane = threadIdx.x & 63;
+  const int64_t tok = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (tok >= n) return;
+  const int64_t id = idx[tok];
+  const int64_t p = pos_w ? (pos0 ? *pos0 : 0) + tok % t : 0;
+  float4 *o = reinterpret_cast<float4 *>(out + tok * cols);
+  if (id < 0 || id >= vocab || (pos_w && (p < 0 || p >= pos_rows))) {
+    const float nan = __builtin_nanf("");
+    for (int i = lane; i < cols / 4; i += 64) o[i] = make_float4(nan, nan, nan, nan);
+    return;
+  }
+  const float s = int8_row_scale(mu16[id]);
+  const uint32_t *qr = reinterpret_cast<const uint32_t *>(q + id * cols);
+  const float4 *pr = pos_w ? reinterpret_cast<const float4 *>(pos_w + p * cols) : nullptr;
+  for (int i = lane; i < cols / 4; i += 64) {
+    const uint32_t b = qr[i];
+    auto one = [&](int8_t v) { return __half2float(__float2half_rn(static_cast<float>(v) * s)); };
+    float4 v = make_float4(one(static_cast<int8_t>(b)), one(static_cast<int8_t>(b >> 8)),
+                           one(static_cast<int8_t>(b >> 16)), one(static_cast<int8_t>(b >> 24)));
+    if (pr) {
+      const float4 g = pr[i];
+      v = make_float4(v.x + g.x, v.y + g.y, v.z + g.z, v.w + g.w);
+    }
+    o[i] = v;
+  }
+}
+
 }  // namespace
 
 int launch_int8_quant(const float *w, int64_t rows, int64_t cols, int8_t *q, uint16_t *mu16, hipStream_t s) {
@@ -103,6 +287,69 @@ int launch_int8_dequant(const int8_t *q, const uint16_t *mu16, int64_t rows, int
   hipLaunchKernelGGL(int8_dequant_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, q, mu16, rows, cols,
                      w16, vec4);
   return check_launch("int8_dequant_kernel");
+}
+
+int launch_int8_linear(const int8_t *q, const uint16_t *mu16, int64_t rows, int64_t cols, const float *x, int64_t m,
+                       const float *norm_w, float eps, float *y, hipStream_t s) {
+  if (rows == 0 || m == 0) return PLX_OK;
+  if (cols <= 0 || cols % 16 != 0 || cols > 64 * 16 * 4)
+    return fail(PLX_EINVAL, "int8_linear: %lld columns (a multiple of 16 up to 4,096)", static_cast<long long>(cols));
+  const uintptr_t al = reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(x) |
+                       reinterpret_cast<uintptr_t>(norm_w);
+  if ((al & 15u) != 0) return fail(PLX_EINVAL, "int8_linear: q, x and the norm weight must be 16-byte aligned");
+  // about 8 waves of 4-row groups per SIMD over the chip (1,024 SIMDs)
+  int64_t rpw = (rows + 8 * 1024 - 1) / (8 * 1024);
+  rpw = rpw < 4 ? 4 : (rpw + 3) / 4 * 4;
+  const int64_t waves = (rows + rpw - 1) / rpw;
+  const int64_t blocks = (waves + kLinWaves - 1) / kLinWaves;
+  if (blocks > 0x7FFFFFFFll) return fail(PLX_EINVAL, "int8_linear: too many rows");
+  const int cpl = static_cast<int>((cols / 16 + 63) / 64);
+  const int mb = m >= 4 ? 4 : m >= 2 ? 2 : 1;
+  const dim3 g(static_cast<unsigned>(blocks)), b(64 * kLinWaves);
+  const int ci = static_cast<int>(cols);
+  const int ri = static_cast<int>(rpw);
+#define PLX_I8L(CPL, MB)                                                                                         \
+  do {                                                                                                           \
+    if (norm_w)                                                                                                  \
+      hipLaunchKernelGGL((int8_linear_kernel<CPL, MB, true>), g, b, 0, s, q, mu16, rows, ci, x, m, norm_w, eps, ri, y); \
+    else                                                                                                         \
+      hipLaunchKernelGGL((int8_linear_kernel<CPL, MB, false>), g, b, 0, s, q, mu16, rows, ci, x, m, norm_w, eps, ri, y); \
+  } while (0)
+#define PLX_I8L_MB(CPL)  \
+  do {                   \
+    if (mb == 4)         \
+      PLX_I8L(CPL, 4);   \
+    else if (mb == 2)    \
+      PLX_I8L(CPL, 2);   \
+    else                 \
+      PLX_I8L(CPL, 1);   \
+  } while (0)
+  if (cpl == 1)
+    PLX_I8L_MB(1);
+  else if (cpl == 2)
+    PLX_I8L_MB(2);
+  else
+    PLX_I8L_MB(4);
+#undef PLX_I8L_MB
+#undef PLX_I8L
+  return check_launch("int8_linear_kernel");
+}
+
+int launch_int8_embed(const int8_t *q, const uint16_t *mu16, int64_t vocab, int64_t cols, const int64_t *idx,
+                      int64_t n, int64_t t, const float *pos_w, int64_t pos_rows, const int64_t *pos0, float *out,
+                      hipStream_t s) {
+  if (n == 0) return PLX_OK;
+  if (cols <= 0 || cols % 4 != 0 || cols > (1 << 24) || t <= 0)
+    return fail(PLX_EINVAL, "int8_embed: %lld columns (a positive multiple of 4), %lld tokens per row",
+                static_cast<long long>(cols), static_cast<long long>(t));
+  const uintptr_t al = reinterpret_cast<uintptr_t>(pos_w) | reinterpret_cast<uintptr_t>(out);
+  if ((reinterpret_cast<uintptr_t>(q) & 3u) != 0 || (al & 15u) != 0)
+    return fail(PLX_EINVAL, "int8_embed: q must be 4-byte and pos_w / out 16-byte aligned");
+  const int64_t blocks = (n + 3) / 4;
+  if (blocks > 0x7FFFFFFFll) return fail(PLX_EINVAL, "int8_embed: too many tokens");
+  hipLaunchKernelGGL(int8_embed_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, q, mu16, vocab,
+                     static_cast<int>(cols), idx, n, t, pos_w, pos_rows, pos0, out);
+  return check_launch("int8_embed_kernel");
 }
 
 }  // namespace plx

@@ -81,6 +81,11 @@ int launch_requantize_batch(const RequantItem *items, int n_items, int mode, voi
 int launch_gather(const int32_t *idx, int64_t n, int out_dtype, void *out, hipStream_t s);
 int launch_dequant_f16(const uint8_t *packed, const uint16_t *sigma16, int64_t rows, int64_t cols,
                        uint16_t *w16, hipStream_t s);
+int launch_int8_linear(const int8_t *q, const uint16_t *mu16, int64_t rows, int64_t cols, const float *x, int64_t m,
+                       const float *norm_w, float eps, float *y, hipStream_t s);
+int launch_int8_embed(const int8_t *q, const uint16_t *mu16, int64_t vocab, int64_t cols, const int64_t *idx,
+                      int64_t n, int64_t t, const float *pos_w, int64_t pos_rows, const int64_t *pos0, float *out,
+                      hipStream_t s);
 int launch_rms_norm(const float *x, const float *w, float *y, int64_t rows, int64_t d, float eps, hipStream_t s);
 int launch_decode_attention(const float *q, const float *k, const float *v, const float *q_w, const float *k_w,
                             float eps, float *k_cache, float *v_cache, const int64_t *pos, int64_t seqs_heads,

@@ -31,7 +31,7 @@ import torch.nn.functional as F
 
 from . import _lib
 from .castor import H24_DIM, assert_row_aligned_width
-from .packed import PackedH24Linear, PackedInt8Embedding, PackedInt8Linear, packed_linear_group
+from .packed import PackedH24Linear, PackedInt8Embedding, PackedInt8Linear, int8_embed, packed_linear_group
 from .plx import check_fingerprint, load_plx
 
 # pollux.py:258-278: the config fields and their aliases
@@ -253,13 +253,25 @@ class PackedPolluxModel(nn.Module):
     def _run(self, idx: torch.Tensor, pos0: int, cache: KVCache | None) -> torch.Tensor:
         t = idx.shape[1]
         pos = torch.arange(pos0, pos0 + t, device=idx.device).unsqueeze(0)
-        x = self.tok_emb(idx) + self.pos_emb(pos)
+        x = self.embed(idx, pos[:, 0])
         step_pos = pos.view(()) if (cache is not None and t == 1) else None
         for i, block in enumerate(self.blocks):
             x = block(x, cache, i, step_pos)
         if cache is not None:
             cache.length = pos0 + t
-        return self.head(self.ln_f(x))
+        return self.logits(x)
+
+    def embed(self, idx: torch.Tensor, pos0: torch.Tensor) -> torch.Tensor:
+        """tok_emb(idx) + pos_emb(positions pos0 .. pos0 + t - 1) (pollux.py:691-693); pos0 a device int64 tensor."""
+        if not self.tok_emb._materialized:
+            return int8_embed(self.tok_emb.weight_int8, self.tok_emb.mu_rows, idx, pos_weight=self.pos_emb.weight,
+                              pos0=pos0)
+        pos = pos0.reshape(1, 1) + torch.arange(idx.shape[1], device=idx.device).unsqueeze(0)
+        return self.tok_emb(idx) + self.pos_emb(pos)
+
+    def logits(self, x: torch.Tensor) -> torch.Tensor:
+        """head(ln_f(x)) (pollux.py:699-700), the norm fused into the INT8 head where that runs."""
+        return self.head(x, norm=(self.ln_f.weight, self.ln_f.eps))
 
     def forward(self, idx: torch.Tensor) -> torch.Tensor:
         """Logits [b, t, vocab] of the full prefix, positions 0..t-1 (pollux.py:691-702)."""
@@ -287,8 +299,9 @@ class PackedPolluxModel(nn.Module):
         """PolluxModel.from_packed_checkpoint (pollux.py:704-758) for a .plx path or a loaded payload.
 
         The fingerprint check and the per-key dtype normalisation are the
-        reference's; the packed H24 layers stay packed unless ``materialize``.
-        The INT8 periphery is expanded to fp16 once (as the reference does).
+        reference's.  Unless ``materialize`` (the reference's expansion of every
+        packed layer to fp16), the H24 layers stay packed and the INT8 periphery
+        stays INT8 (fused gather and GEMV kernels).
         """
         if isinstance(source, dict):
             check_fingerprint(source)
@@ -313,11 +326,10 @@ class PackedPolluxModel(nn.Module):
         model = model.to_empty(device=device)
         model.load_state_dict(state, strict=True)
         model.eval()
-        for module in model.modules():
-            if isinstance(module, (PackedInt8Embedding, PackedInt8Linear)):
-                module.materialize()
-            elif materialize and isinstance(module, PackedH24Linear):
-                module.materialize()
+        if materialize:
+            for module in model.modules():
+                if isinstance(module, (PackedInt8Embedding, PackedInt8Linear, PackedH24Linear)):
+                    module.materialize()
         return model
 
 
@@ -348,11 +360,11 @@ class GraphDecoder:
     def _step(self) -> torch.Tensor:
         m = self.model
         b = self.ids.shape[0]
-        x = m.tok_emb(self.ids.view(b, 1)) + m.pos_emb(self.pos.view(1, 1))
+        x = m.embed(self.ids.view(b, 1), self.pos)
         for i, blk in enumerate(m.blocks):
             x = blk(x, self.cache, i, self.pos)
         self.pos += 1
-        return m.head(m.ln_f(x))[:, -1]
+        return m.logits(x)[:, -1]
 
     @torch.inference_mode()
     def prefill(self, idx: torch.Tensor) -> torch.Tensor:

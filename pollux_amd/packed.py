@@ -256,6 +256,70 @@ def dequantize_int8_rows(q: torch.Tensor, mu16: torch.Tensor) -> torch.Tensor:
     return out
 
 
+def int8_linear(q: torch.Tensor, mu16: torch.Tensor, x: torch.Tensor, *,
+                norm: tuple[torch.Tensor, float] | None = None) -> torch.Tensor:
+    """fp32 [..., rows] = n(x) @ W.T with W = q * (mu / 127) in fp16 (never stored), one HIP kernel (plx_int8_linear).
+
+    Exact products, fp32 sums: F.linear(x, W.float()) up to summation order
+    (PackedInt8Linear.forward, pollux.py:562-563).  ``norm``: (weight, eps) of
+    an RMSNorm applied to x first, or None.  x fp32 with a multiple of 16 up to
+    4,096 features.
+    """
+    _lib.require_device(x, "int8_linear input")
+    if q.dtype != torch.int8 or mu16.dtype != torch.float16 or x.dtype != torch.float32:
+        raise ValueError("int8_linear: int8 q, float16 mu and float32 x")
+    rows, cols = q.shape
+    if x.shape[-1] != cols or mu16.numel() != rows:
+        raise ValueError(f"int8_linear: x has {x.shape[-1]} features, weight [{rows}, {cols}], {mu16.numel()} mu rows")
+    xx = x.reshape(-1, cols).contiguous()
+    if xx.data_ptr() % 16:
+        xx = xx.clone()
+    qq = q.contiguous()
+    nw, eps = None, 0.0
+    if norm is not None:
+        nw, eps = norm[0].detach().reshape(-1).contiguous(), float(norm[1])
+        if nw.dtype != torch.float32 or nw.numel() != cols:
+            raise ValueError(f"int8_linear: the norm weight must be fp32 with {cols} values")
+        if nw.data_ptr() % 16:
+            nw = nw.clone()
+    y = torch.empty((xx.shape[0], rows), dtype=torch.float32, device=x.device)
+    with torch.cuda.device(x.device):
+        st = _lib.lib().plx_int8_linear(_lib.ptr(qq), _lib.ptr(mu16.contiguous()), rows, cols, _lib.ptr(xx),
+                                        xx.shape[0], _lib.ptr(nw), eps, _lib.ptr(y), _lib.stream_of(x.device))
+    _lib.check(st, "int8_linear")
+    return y.reshape(*x.shape[:-1], rows)
+
+
+def int8_embed(q: torch.Tensor, mu16: torch.Tensor, ids: torch.Tensor, *, pos_weight: torch.Tensor | None = None,
+               pos0: torch.Tensor | None = None) -> torch.Tensor:
+    """fp32 [b, t, cols] = W[ids] (+ pos_weight[p0 + i] at step i), one HIP kernel (plx_int8_embed).
+
+    W = q * (mu / 127) in fp16 (PackedInt8Embedding.forward, pollux.py:532-533);
+    the position term is the model's pos_emb (pollux.py:691-693), p0 a 0-dim
+    int64 device tensor (0 when None).  Ids or positions out of range give NaN rows.
+    """
+    _lib.require_device(ids, "int8_embed ids")
+    if q.dtype != torch.int8 or mu16.dtype != torch.float16:
+        raise ValueError("int8_embed: int8 q and float16 mu")
+    ii = ids.reshape(ids.shape[0] if ids.dim() > 1 else 1, -1).to(torch.int64).contiguous()
+    vocab, cols = q.shape
+    pw = None
+    if pos_weight is not None:
+        pw = pos_weight.detach().contiguous()
+        if pw.dtype != torch.float32 or pw.shape[-1] != cols:
+            raise ValueError("int8_embed: the position table must be fp32 [positions, cols]")
+    p0 = None
+    if pos0 is not None:
+        p0 = pos0.reshape(()).to(torch.int64)
+    out = torch.empty((*ii.shape, cols), dtype=torch.float32, device=ids.device)
+    with torch.cuda.device(ids.device):
+        st = _lib.lib().plx_int8_embed(_lib.ptr(q.contiguous()), _lib.ptr(mu16.contiguous()), vocab, cols, _lib.ptr(ii),
+                                       ii.shape[0], ii.shape[1], _lib.ptr(pw), 0 if pw is None else pw.shape[0],
+                                       _lib.ptr(p0), _lib.ptr(out), _lib.stream_of(ids.device))
+    _lib.check(st, "int8_embed")
+    return out.reshape(*ids.shape, cols)
+
+
 class _PackedInt8Rows(nn.Module):
     """Shared buffers / materialize of the INT8 periphery layers (pollux.py:508-563)."""
 
@@ -284,7 +348,9 @@ class PackedInt8Embedding(_PackedInt8Rows):
         self._init_rows(self.num_embeddings, self.embedding_dim)
 
     def forward(self, idx: torch.Tensor) -> torch.Tensor:
-        self.materialize()
+        if not self._materialized:
+            # gathered and dequantised in one kernel: the values of F.embedding(idx, weight.float())
+            return int8_embed(self.weight_int8, self.mu_rows, idx)
         # rows gathered, then cast: the same values as F.embedding(idx, weight.float())
         # (pollux.py:532-533) without casting the whole table per call
         return F.embedding(idx, self.weight).to(dtype=torch.float32)
@@ -303,16 +369,32 @@ class PackedInt8Linear(_PackedInt8Rows):
         else:
             self.register_parameter("bias", None)
 
-    def forward(self, x: torch.Tensor) -> torch.Tensor:
-        self.materialize()
+    # token counts up to which the INT8 GEMV runs (it streams the rows once per 4 tokens)
+    gemv_max_tokens = 16
+
+    def forward(self, x: torch.Tensor, norm: tuple[torch.Tensor, float] | None = None) -> torch.Tensor:
+        """F.linear(n(x), W.to(x.dtype), bias) (pollux.py:562-563); ``norm``: (weight, eps) of an RMSNorm on x, or None.
+
+        Until materialize(), fp32 batches of up to ``gemv_max_tokens`` tokens
+        run the INT8 GEMV (norm fused in); others take the reference's
+        F.linear on the fp16 weight cast to x's dtype (kept for reuse).
+        """
+        if (not self._materialized and self.bias is None and x.dtype == torch.float32
+                and x.numel() // max(self.in_features, 1) <= self.gemv_max_tokens
+                and self.in_features % 16 == 0 and self.in_features <= 4096):
+            return int8_linear(self.weight_int8, self.mu_rows, x, norm=norm)
+        if norm is not None:
+            x = x * torch.rsqrt(x.pow(2).mean(dim=-1, keepdim=True) + norm[1]) * norm[0]
         return F.linear(x, self._weight_as(x.dtype), self.bias)
 
     def _weight_as(self, dtype: torch.dtype) -> torch.Tensor:
         """weight.to(dtype) (pollux.py:562-563), cast once per dtype and kept (the weights are frozen)."""
-        if self.weight.dtype == dtype:
+        if self._materialized and self.weight.dtype == dtype:
             return self.weight
         cache = self.__dict__.setdefault("_cast", {})
         w = cache.get(dtype)
-        if w is None or w.device != self.weight.device:
-            w = cache[dtype] = self.weight.detach().to(dtype=dtype)
+        dev = (self.weight if self._materialized else self.weight_int8).device
+        if w is None or w.device != dev:
+            w16 = self.weight if self._materialized else dequantize_int8_rows(self.weight_int8, self.mu_rows)
+            w = cache[dtype] = w16.detach().to(dtype=dtype)
         return w

@@ -69,7 +69,75 @@ def test_packed_int8_layers(dev):
     x = torch.randn(4, 48, generator=g).to(dev)
     wq = _ref_int8_materialize(q, mu)
     assert torch.equal(emb(ids), torch.nn.functional.embedding(ids, wq.float()))
-    assert torch.equal(lin(x), torch.nn.functional.linear(x, wq.float()))
+    # fused INT8 GEMV: exact products, another summation order than F.linear
+    want = torch.nn.functional.linear(x, wq.float())
+    _check_int8_linear(lin(x), x, wq)
+    big = torch.randn(20, 48, generator=g).to(dev)  # beyond the GEMV's token limit: the reference's F.linear
+    assert torch.equal(lin(big), torch.nn.functional.linear(big, wq.float()))
+    for m in (emb, lin):
+        m.materialize()
+    assert torch.equal(emb(ids), torch.nn.functional.embedding(ids, wq.float()))
+    assert torch.equal(lin(x), want)
+
+
+def _check_int8_linear(y, x, w16, bound=1e-5):
+    """y against fp64 x @ w16.T: |err| <= bound * sum |x||w| per element (fp32 accumulation)."""
+    xd, wd = x.double().cpu(), w16.double().cpu()
+    ref = xd @ wd.t()
+    scale = xd.abs() @ wd.abs().t()
+    err = (y.double().cpu() - ref).abs()
+    worst = (err / scale.clamp_min(1e-300)).max().item()
+    print(f"[int8] linear {tuple(y.shape)}: worst err / sum|x||w| {worst:.2e}", flush=True)
+    assert worst <= bound
+
+
+# rows % 4 != 0, 16 columns (one chunk), 1,040 columns (a second chunk on one lane only),
+# 1,920 (the Pollux head), 4,096 (four chunks per lane); 1..16 tokens (chunks of 4, 2, 1)
+@pytest.mark.parametrize("rows,cols,m", [(4103, 1920, 1), (4103, 1920, 2), (4103, 1920, 7), (513, 16, 3),
+                                         (999, 1040, 5), (257, 4096, 4), (130, 4096, 16), (61, 48, 1)])
+def test_int8_linear_matches_fp64(dev, rows, cols, m):
+    from pollux_amd.packed import int8_linear
+
+    g = torch.Generator().manual_seed(rows + cols + m)
+    q = torch.randint(-128, 128, (rows, cols), dtype=torch.int8, generator=g)
+    q[0, :] = -128  # the int8 range's end
+    mu = (torch.rand(rows, generator=g) * 0.2 + 1e-3).to(torch.float16)
+    mu[1] = 1.3e-4  # s16 ~ 1e-6 is an fp16 subnormal; the row's weights round on both sides of 2^-14
+    x = (torch.randn(m, cols, generator=g) * 2.0).to(dev)
+    qd, mud = q.to(dev), mu.to(dev)
+    wq = _ref_int8_materialize(qd, mud)
+    y = int8_linear(qd, mud, x)
+    assert y.shape == (m, rows)
+    _check_int8_linear(y, x, wq)
+    assert torch.isfinite(y).all() and (wq[1] != 0).any() and (wq[1].abs() < 2.0 ** -14).any()
+    nw = (1.0 + 0.1 * torch.randn(cols, generator=g)).to(dev)
+    yn = int8_linear(qd, mud, x, norm=(nw, 1e-8))
+    xd = x.double()
+    xn = (xd * torch.rsqrt(xd.pow(2).mean(dim=-1, keepdim=True) + 1e-8) * nw.double()).float()
+    _check_int8_linear(yn, xn, wq, bound=2e-5)  # + the norm's rounding (a few ulp of x)
+
+
+def test_int8_embed_with_positions(dev):
+    from pollux_amd.packed import int8_embed
+
+    g = torch.Generator().manual_seed(21)
+    q = torch.randint(-128, 128, (300, 72), dtype=torch.int8, generator=g).to(dev)
+    mu = (torch.rand(300, generator=g) * 0.2 + 1e-3).to(torch.float16).to(dev)
+    pos_w = torch.randn(40, 72, generator=g).to(dev)
+    ids = torch.randint(0, 300, (3, 7), generator=g).to(dev)
+    wq = _ref_int8_materialize(q, mu).float()
+    p0 = torch.tensor(5, device=dev)
+    got = int8_embed(q, mu, ids, pos_weight=pos_w, pos0=p0)
+    want = torch.nn.functional.embedding(ids, wq) + pos_w[5:12].unsqueeze(0)
+    assert torch.equal(got, want)
+    assert torch.equal(int8_embed(q, mu, ids), torch.nn.functional.embedding(ids, wq))
+    # an id out of range, then positions past the table: NaN rows, nothing else touched
+    bad = ids.clone()
+    bad[1, 2] = 300
+    out = int8_embed(q, mu, bad, pos_weight=pos_w, pos0=p0)
+    assert torch.isnan(out[1, 2]).all() and torch.equal(out[0], want[0])
+    out = int8_embed(q, mu, ids, pos_weight=pos_w, pos0=torch.tensor(36, device=dev))
+    assert torch.isnan(out[:, 4:]).all() and torch.isfinite(out[:, :4]).all()
 
 
 def _state(g, d=96, hidden=384, vocab=200):
