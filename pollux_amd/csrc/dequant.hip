@@ -195,6 +195,28 @@ __device__ __forceinline__ T pick(const T (&a)[kDqlMaxTargets], int ti) {
   return ti == 1 ? v1 : ti == 2 ? v2 : ti == 3 ? v3 : v0;
 }
 
+// Accesses through pointers the compiler cannot trace to a kernel argument
+// (those pick() returns) as global memory operations: flat ones would also
+// count against the scalar loads' wait counter, so every kernel-argument load
+// would wait for them.
+template <typename T>
+__device__ __forceinline__ T gload(const T *p) {
+  return *(const __attribute__((address_space(1))) T *)(p);
+}
+template <typename T>
+__device__ __forceinline__ void gstore(T *p, T v) {
+  *(__attribute__((address_space(1))) T *)(p) = v;
+}
+// 16 bytes as a native vector (a struct copy would be lowered to flat loads)
+__device__ __forceinline__ uint4 gload16(const void *p) {
+  const u32x4_t v = *(const __attribute__((address_space(1))) u32x4_t *)(p);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ float4 gload16f(const float *p) {
+  const uint4 v = gload16(p);
+  return make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w));
+}
+
 template <bool XF32>
 __device__ __forceinline__ void load_x8(const void *__restrict__ x, int64_t off, float *v) {
   if (XF32) {
@@ -225,16 +247,26 @@ __device__ __forceinline__ float x_at(const void *__restrict__ x, int64_t off) {
   return __uint_as_float(static_cast<uint32_t>(static_cast<const uint16_t *>(x)[off]) << 16);
 }
 
-// One pass over the packed rows for MB tokens.  Block = 256 threads = R = 256/L
+// One pass over the packed rows for MB tokens.  Block = NT threads = R = NT/L
 // rows; the block's packed bytes (and, when XL, the MB token rows of x as
 // fp32) are staged in LDS first; each lane then handles atoms sub, sub+L, ...
-// of its row in chunks of 4, issuing the chunk's four table gathers before
-// scoring any of them.
+// of its row in chunks of kDqlGather, issuing the chunk's table gathers before
+// scoring any of them.  At one token the kernel is a chain of memory round
+// trips, so everything that does not depend on the staged data is requested
+// before the first barrier (which waits for all of it): x and the norm weights
+// into registers when each thread holds at most one 8-value piece of the first
+// MB token rows, the packed bytes, the row's sigma16 and residual values.
 template <bool GEN>
 using DqlArgs = typename std::conditional<GEN, DqlTargets, DqlOne>::type;
 
-// GEN: several targets and the epilogue (DqlTargets); else one target, no epilogue (DqlOne)
-template <int L, int MB, bool XF32, bool XL, int NT, bool GEN>
+constexpr int kDqlGather = 4;  // table gathers in flight per lane (a larger unrolled chunk measured slower)
+
+// GEN: several targets and the epilogue (DqlTargets); else one target, no epilogue (DqlOne).
+// XREG (with XL, m_total <= MB and MB token rows of at most 8 * NT values): x
+// goes through registers into LDS and the general staging loop is compiled
+// out - at one token these kernels are short enough that their code size
+// shows in the time (cold instruction fetch).
+template <int L, int MB, bool XF32, bool XL, int NT, bool GEN, bool XREG>
 __global__ __launch_bounds__(NT) void dqlinear_kernel(const DqlArgs<GEN> targets, int64_t atoms_per_row,
                                                        const void *__restrict__ x, int64_t m_total,
                                                        const uint4 *__restrict__ kp_gemv, int round_w, int gelu) {
@@ -245,6 +277,7 @@ __global__ __launch_bounds__(NT) void dqlinear_kernel(const DqlArgs<GEN> targets
   const uint16_t *__restrict__ sigma16;
   float *__restrict__ y;
   const float *__restrict__ residual = nullptr;
+  const float *__restrict__ norm_w = nullptr;
   int64_t packed_bytes, rows;
   if constexpr (GEN) {
     const int ti = static_cast<int>(blockIdx.y);
@@ -254,6 +287,7 @@ __global__ __launch_bounds__(NT) void dqlinear_kernel(const DqlArgs<GEN> targets
     rows = pick(targets.rows, ti);
     y = pick(targets.y, ti);
     residual = pick(targets.residual, ti);
+    norm_w = targets.norm_w;
     if (static_cast<int64_t>(blockIdx.x) * R >= rows) return;  // the whole block: before any barrier
   } else {
     packed = targets.packed;
@@ -265,6 +299,12 @@ __global__ __launch_bounds__(NT) void dqlinear_kernel(const DqlArgs<GEN> targets
   const int64_t cols = atoms_per_row * kDim;
   const int64_t row0 = static_cast<int64_t>(blockIdx.x) * R;
   const int64_t rows_here = min(static_cast<int64_t>(R), rows - row0);
+  const int lane = threadIdx.x & 63;
+  const int sub = lane % L;
+  const int64_t row = row0 + threadIdx.x / L;
+  const bool live = row < rows;
+  const bool writer = live && sub == 0;
+
   // packed bytes of atoms [row0*apr, (row0+rows_here)*apr): whole 9-byte groups
   const int64_t atom0 = row0 * atoms_per_row;
   const int64_t g_lo = atom0 >> 2, g_hi = (atom0 + rows_here * atoms_per_row + 3) >> 2;
@@ -275,76 +315,155 @@ __global__ __launch_bounds__(NT) void dqlinear_kernel(const DqlArgs<GEN> targets
   const int nvec = static_cast<int>((end - base16 + 15) >> 4);
   const uint8_t *pb = smem + (start - base16);
   float *xs = reinterpret_cast<float *>(smem + static_cast<int64_t>(nvec) * 16);
-  for (int i = threadIdx.x; i < nvec; i += NT) {
-    const int64_t gb = base16 + 16 * static_cast<int64_t>(i);
-    if (gb + 16 <= packed_bytes) {
-      reinterpret_cast<uint4 *>(smem)[i] = *reinterpret_cast<const uint4 *>(packed + gb);
-    } else {
-      for (int k = 0; k < 16 && gb + k < packed_bytes; ++k) smem[16 * i + k] = packed[gb + k];
+  // the thread's first vector is requested before anything else (from a
+  // clamped address, so no branch holds the load)
+  const int64_t gb0 = base16 + 16 * static_cast<int64_t>(threadIdx.x);
+  const bool v0ok = static_cast<int>(threadIdx.x) < nvec && gb0 + 16 <= packed_bytes;
+  uint4 pk0 = make_uint4(0u, 0u, 0u, 0u);
+  if (packed_bytes >= 16) pk0 = gload16(packed + (v0ok ? gb0 : 0));
+
+  // requests that need nothing staged: sigma16, residuals and (first MB tokens) x and norm weights;
+  // every lane loads its (clamped) row: a load under a divergent branch would be
+  // waited for at once (the other path writes the same register)
+  const int64_t rrow = live ? row : rows - 1;
+  const uint16_t sig_bits = gload(sigma16 + rrow);
+  const int mb0 = static_cast<int>(min(static_cast<int64_t>(MB), m_total));
+  float res0[MB];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) res0[mb] = 0.f;
+  if constexpr (GEN) {
+    if (residual) {
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+        if (mb < mb0) res0[mb] = gload(residual + static_cast<int64_t>(mb) * rows + rrow);
+    }
+  }
+  const int64_t items0 = mb0 * cols / 8;  // 8-value pieces of the first MB token rows
+  constexpr bool xreg = XL && XREG;
+  float xv0[8], nv0[8];
+  if (xreg && threadIdx.x < items0) {
+    load_x8<XF32>(x, 8 * static_cast<int64_t>(threadIdx.x), xv0);
+    if constexpr (GEN) {
+      if (norm_w) {
+        const int64_t c8 = 8 * static_cast<int64_t>(threadIdx.x) % cols;
+        const float4 g0 = gload16f(norm_w + c8);
+        const float4 g1 = gload16f(norm_w + c8 + 4);
+        nv0[0] = g0.x; nv0[1] = g0.y; nv0[2] = g0.z; nv0[3] = g0.w;
+        nv0[4] = g1.x; nv0[5] = g1.y; nv0[6] = g1.z; nv0[7] = g1.w;
+      }
     }
   }
 
-  const int lane = threadIdx.x & 63;
-  const int sub = lane % L;
-  const int64_t row = row0 + threadIdx.x / L;
-  const bool live = row < rows;
+  for (int i = threadIdx.x; i < nvec; i += NT) {
+    const int64_t gb = base16 + 16 * static_cast<int64_t>(i);
+    if (i == static_cast<int>(threadIdx.x) && v0ok) {
+      reinterpret_cast<uint4 *>(smem)[i] = pk0;
+    } else if (gb + 16 <= packed_bytes) {
+      reinterpret_cast<uint4 *>(smem)[i] = gload16(packed + gb);
+    } else {
+      for (int k = 0; k < 16 && gb + k < packed_bytes; ++k) smem[16 * i + k] = gload(packed + gb + k);
+    }
+  }
+
   for (int64_t m0 = 0; m0 < m_total; m0 += MB) {
     const int mb_here = static_cast<int>(min(static_cast<int64_t>(MB), m_total - m0));
     if (XL) {
-      __syncthreads();
-      float ss[MB];
-#pragma unroll
-      for (int mb = 0; mb < MB; ++mb) ss[mb] = 0.f;
-      // token rows are whole multiples of 8 elements (cols = 24 * apr): 8 per thread-step
-      for (int64_t i = threadIdx.x; i < mb_here * cols / 8; i += NT) {
-        float v[8];
-        load_x8<XF32>(x, m0 * cols + 8 * i, v);
-        float4 *d = reinterpret_cast<float4 *>(xs + 8 * i);
-        d[0] = make_float4(v[0], v[1], v[2], v[3]);
-        d[1] = make_float4(v[4], v[5], v[6], v[7]);
+      if (m0 > 0) __syncthreads();  // the previous tokens' reads of xs are done
+      if constexpr (xreg) {
+        const bool mine = threadIdx.x < items0;
         if constexpr (GEN) {
-          if (targets.norm_w) {
+          // RMSNorm of each token row (pollux.py:580-582) from the registers:
+          // every block sums the squares in the same order, so all blocks scale alike
+          if (norm_w) {
+            const int tr = mine ? static_cast<int>(8 * static_cast<int64_t>(threadIdx.x) / cols) : MB;
             float s = 0.f;
+            if (mine) {
 #pragma unroll
-            for (int c = 0; c < 8; ++c) s = fmaf(v[c], v[c], s);
-            const int tr = static_cast<int>(8 * i / cols);
+              for (int c = 0; c < 8; ++c) s = fmaf(xv0[c], xv0[c], s);
+            }
+            float ss[MB];
 #pragma unroll
-            for (int mb = 0; mb < MB; ++mb) ss[mb] += tr == mb ? s : 0.f;
+            for (int mb = 0; mb < MB; ++mb) {
+              ss[mb] = tr == mb ? s : 0.f;
+#pragma unroll
+              for (int off = 32; off > 0; off >>= 1) ss[mb] += __shfl_xor(ss[mb], off, 64);
+            }
+            if (lane == 0)
+#pragma unroll
+              for (int mb = 0; mb < MB; ++mb) norm_red[threadIdx.x >> 6][mb] = ss[mb];
+            __syncthreads();
+            float r = 0.f;
+#pragma unroll
+            for (int mb = 0; mb < MB; ++mb) {
+              float t = 0.f;
+#pragma unroll
+              for (int w = 0; w < NT / 64; ++w) t += norm_red[w][mb];
+              const float rm = 1.0f / sqrtf(t / static_cast<float>(cols) + targets.norm_eps);
+              r = tr == mb ? rm : r;
+            }
+            if (mine) {
+#pragma unroll
+              for (int c = 0; c < 8; ++c) xv0[c] = xv0[c] * r * nv0[c];
+            }
           }
         }
-      }
-      if constexpr (GEN) {
-        // RMSNorm of each staged token row (pollux.py:580-582): every block
-        // sums the squares in the same order, so all blocks scale alike
-        if (targets.norm_w) {
+        if (mine) {
+          float4 *d = reinterpret_cast<float4 *>(xs + 8 * static_cast<int64_t>(threadIdx.x));
+          d[0] = make_float4(xv0[0], xv0[1], xv0[2], xv0[3]);
+          d[1] = make_float4(xv0[4], xv0[5], xv0[6], xv0[7]);
+        }
+      } else {
+        float ss[MB];
 #pragma unroll
-          for (int mb = 0; mb < MB; ++mb)
+        for (int mb = 0; mb < MB; ++mb) ss[mb] = 0.f;
+        // token rows are whole multiples of 8 elements (cols = 24 * apr): 8 per thread-step
+        for (int64_t i = threadIdx.x; i < mb_here * cols / 8; i += NT) {
+          float v[8];
+          load_x8<XF32>(x, m0 * cols + 8 * i, v);
+          float4 *d = reinterpret_cast<float4 *>(xs + 8 * i);
+          d[0] = make_float4(v[0], v[1], v[2], v[3]);
+          d[1] = make_float4(v[4], v[5], v[6], v[7]);
+          if constexpr (GEN) {
+            if (norm_w) {
+              float s = 0.f;
 #pragma unroll
-            for (int off = 32; off > 0; off >>= 1) ss[mb] += __shfl_xor(ss[mb], off, 64);
-          if (lane == 0)
+              for (int c = 0; c < 8; ++c) s = fmaf(v[c], v[c], s);
+              const int tr = static_cast<int>(8 * i / cols);
 #pragma unroll
-            for (int mb = 0; mb < MB; ++mb) norm_red[threadIdx.x >> 6][mb] = ss[mb];
-          __syncthreads();
-          float rs[MB];
-#pragma unroll
-          for (int mb = 0; mb < MB; ++mb) {
-            float t = 0.f;
-#pragma unroll
-            for (int w = 0; w < NT / 64; ++w) t += norm_red[w][mb];
-            rs[mb] = 1.0f / sqrtf(t / static_cast<float>(cols) + targets.norm_eps);
+              for (int mb = 0; mb < MB; ++mb) ss[mb] += tr == mb ? s : 0.f;
+            }
           }
-          const float4 *nw = reinterpret_cast<const float4 *>(targets.norm_w);
-          for (int64_t i = threadIdx.x; i < mb_here * cols / 8; i += NT) {
-            const int tr = static_cast<int>(8 * i / cols);
-            const int64_t c8 = 8 * i - static_cast<int64_t>(tr) * cols;
-            float r = rs[0];
+        }
+        if constexpr (GEN) {
+          if (norm_w) {
 #pragma unroll
-            for (int mb = 1; mb < MB; ++mb) r = tr == mb ? rs[mb] : r;
-            float4 *d = reinterpret_cast<float4 *>(xs + 8 * i);
-            const float4 g0 = nw[c8 / 4], g1 = nw[c8 / 4 + 1];
-            const float4 a = d[0], b = d[1];
-            d[0] = make_float4(a.x * r * g0.x, a.y * r * g0.y, a.z * r * g0.z, a.w * r * g0.w);
-            d[1] = make_float4(b.x * r * g1.x, b.y * r * g1.y, b.z * r * g1.z, b.w * r * g1.w);
+            for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+              for (int off = 32; off > 0; off >>= 1) ss[mb] += __shfl_xor(ss[mb], off, 64);
+            if (lane == 0)
+#pragma unroll
+              for (int mb = 0; mb < MB; ++mb) norm_red[threadIdx.x >> 6][mb] = ss[mb];
+            __syncthreads();
+            float rs[MB];
+#pragma unroll
+            for (int mb = 0; mb < MB; ++mb) {
+              float t = 0.f;
+#pragma unroll
+              for (int w = 0; w < NT / 64; ++w) t += norm_red[w][mb];
+              rs[mb] = 1.0f / sqrtf(t / static_cast<float>(cols) + targets.norm_eps);
+            }
+            for (int64_t i = threadIdx.x; i < mb_here * cols / 8; i += NT) {
+              const int tr = static_cast<int>(8 * i / cols);
+              const int64_t c8 = 8 * i - static_cast<int64_t>(tr) * cols;
+              float r = rs[0];
+#pragma unroll
+              for (int mb = 1; mb < MB; ++mb) r = tr == mb ? rs[mb] : r;
+              float4 *d = reinterpret_cast<float4 *>(xs + 8 * i);
+              const float4 g0 = gload16f(norm_w + c8), g1 = gload16f(norm_w + c8 + 4);
+              const float4 a = d[0], b = d[1];
+              d[0] = make_float4(a.x * r * g0.x, a.y * r * g0.y, a.z * r * g0.z, a.w * r * g0.w);
+              d[1] = make_float4(b.x * r * g1.x, b.y * r * g1.y, b.z * r * g1.z, b.w * r * g1.w);
+            }
           }
         }
       }
@@ -356,10 +475,10 @@ __global__ __launch_bounds__(NT) void dqlinear_kernel(const DqlArgs<GEN> targets
 #pragma unroll
       for (int t = 0; t < 4; ++t) acc[mb][t] = 0.f;
     if (live) {
-      for (int64_t a0 = sub; a0 < atoms_per_row; a0 += 4 * L) {
-        uint4 e[4];
+      for (int64_t a0 = sub; a0 < atoms_per_row; a0 += kDqlGather * L) {
+        uint4 e[kDqlGather];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < kDqlGather; ++i) {
           const int64_t a = a0 + i * L;
           int32_t code = 0;
           if (a < atoms_per_row) {
@@ -372,7 +491,7 @@ __global__ __launch_bounds__(NT) void dqlinear_kernel(const DqlArgs<GEN> targets
           e[i] = kp_gemv[code];
         }
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < kDqlGather; ++i) {
           const int64_t a = a0 + i * L;
           if (a >= atoms_per_row) break;
           const uint32_t type = e[i].w & 3u;
@@ -415,8 +534,8 @@ __global__ __launch_bounds__(NT) void dqlinear_kernel(const DqlArgs<GEN> targets
       for (int t = 0; t < 4; ++t)
 #pragma unroll
         for (int off = L / 2; off > 0; off >>= 1) acc[mb][t] += __shfl_xor(acc[mb][t], off, 64);
-    if (live && sub == 0) {
-      const float sig = __half2float(__ushort_as_half(sigma16[row]));
+    if (writer) {
+      const float sig = __half2float(__ushort_as_half(sig_bits));
       const float sl = __uint_as_float(kSLatticeBits);
       const float v1 = __half2float(__ushort_as_half(static_cast<uint16_t>(dq_value(1, sig, sl))));
       const float v2 = __half2float(__ushort_as_half(static_cast<uint16_t>(dq_value(2, sig, sl))));
@@ -430,11 +549,13 @@ __global__ __launch_bounds__(NT) void dqlinear_kernel(const DqlArgs<GEN> targets
       for (int mb = 0; mb < MB; ++mb)
         if (mb < mb_here) {
           const int64_t i = (m0 + mb) * rows + row;
-          const float v = m4 * (acc[mb][0] * 0.25f) + m2 * (acc[mb][1] * 0.5f) + m1 * acc[mb][2] - m3 * acc[mb][3];
-          if constexpr (GEN)
-            y[i] = dql_epilogue(v, residual, i, gelu);
-          else
-            y[i] = v;
+          float v = m4 * (acc[mb][0] * 0.25f) + m2 * (acc[mb][1] * 0.5f) + m1 * acc[mb][2] - m3 * acc[mb][3];
+          if constexpr (GEN) {
+            // GELU (torch's erf form), then the residual (prefetched for the first tokens)
+            if (gelu) v = (v * 0.5f) * (1.0f + erff(v * __uint_as_float(kSLatticeBits)));
+            if (residual) v = (m0 == 0 ? res0[mb] : gload(residual + i)) + v;
+          }
+          gstore(y + i, v);
         }
     }
   }
@@ -460,6 +581,8 @@ int launch_dql(DqlTargets t, int64_t apr, const void *x, int64_t m, const uint4 
   const bool xl = p16 + xbytes <= 48 * 1024;
   const size_t shm = xl ? p16 + xbytes : p16;
   if (shm > 64 * 1024) return fail(PLX_EINVAL, "dequant_linear: rows of %lld atoms are too long", static_cast<long long>(apr));
+  // x through registers: one pass over all tokens, at most one 8-value piece per thread
+  const bool xreg = xl && m <= mb && m * cols <= 8 * NT;
   if (t.norm_w && !xl) {
     const int st = launch_rms_norm(static_cast<const float *>(x), t.norm_w, xnorm, m, cols, t.norm_eps, s);
     if (st != PLX_OK) return st;
@@ -467,21 +590,21 @@ int launch_dql(DqlTargets t, int64_t apr, const void *x, int64_t m, const uint4 
     t.norm_w = nullptr;
   }
   const bool gen = t.n > 1 || t.residual[0] != nullptr || gelu || t.norm_w != nullptr;
-#define PLX_DQL(MB, XL) \
-  do {                                                                                                        \
-    if (gen)                                                                                                  \
-      hipLaunchKernelGGL((dqlinear_kernel<L, MB, XF32, XL, NT, true>), g, dim3(NT), shm, s, t, apr, x, m, tab,  \
-                         round_w, gelu);                                                                       \
-    else                                                                                                      \
-      hipLaunchKernelGGL((dqlinear_kernel<L, MB, XF32, XL, NT, false>), g, dim3(NT), shm, s, one, apr, x, m,    \
-                         tab, round_w, 0);                                                                     \
+#define PLX_DQL(MB, XL, XR) \
+  do {                                                                                                          \
+    if (gen)                                                                                                    \
+      hipLaunchKernelGGL((dqlinear_kernel<L, MB, XF32, XL, NT, true, XR>), g, dim3(NT), shm, s, t, apr, x, m, tab, \
+                         round_w, gelu);                                                                         \
+    else                                                                                                        \
+      hipLaunchKernelGGL((dqlinear_kernel<L, MB, XF32, XL, NT, false, XR>), g, dim3(NT), shm, s, one, apr, x, m,  \
+                         tab, round_w, 0);                                                                       \
   } while (0)
   if (mb == 4) {
-    if (xl) PLX_DQL(4, true); else PLX_DQL(4, false);
+    if (xreg) PLX_DQL(4, true, true); else if (xl) PLX_DQL(4, true, false); else PLX_DQL(4, false, false);
   } else if (mb == 2) {
-    if (xl) PLX_DQL(2, true); else PLX_DQL(2, false);
+    if (xreg) PLX_DQL(2, true, true); else if (xl) PLX_DQL(2, true, false); else PLX_DQL(2, false, false);
   } else {
-    if (xl) PLX_DQL(1, true); else PLX_DQL(1, false);
+    if (xreg) PLX_DQL(1, true, true); else if (xl) PLX_DQL(1, true, false); else PLX_DQL(1, false, false);
   }
 #undef PLX_DQL
   return check_launch("dqlinear_kernel");
