@@ -11,8 +11,8 @@
 //   pollux.py:615-620), writes k and v into the caches at the position read
 //   from device memory, then computes softmax_j<=pos(q . K_j / sqrt 24) V_j
 //   over the cached positions (the causal scaled_dot_product_attention of
-//   pollux.py:624 for the last query): scores in LDS, block max and sum, the
-//   24 outputs accumulated per thread over its positions and reduced in LDS.
+//   pollux.py:624 for the last query): an online softmax per thread over its
+//   positions, combined across the block at the end.
 //   Reading the position from device memory lets a captured graph replay the
 //   step while the position advances on the device; a position outside the
 //   cache writes nothing and yields NaN outputs.
@@ -26,11 +26,7 @@ constexpr int kNormRowsPerBlock = 4;  // one wave per row
 constexpr int kNormRegVec = 8;        // float4 per lane held in registers (rows of <= 2,048 values)
 constexpr int kAttnThreads = 256;
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-  return v;
-}
+__device__ __forceinline__ float wave_sum(float v) { return wave_reduce_sum(v); }
 
 // REG: rows of up to kNormRegVec float4 per lane (d <= 2,048) are held in
 // registers, so every load of the row is in flight before the reduction (a
@@ -89,109 +85,130 @@ __global__ __launch_bounds__(64 * kNormRowsPerBlock) void rmsnorm_kernel(const f
 }
 
 // q, k, v: [b, H, 24] projections of the new token; caches [b, H, max_len, 24];
-// out [b, H, 24].  Dynamic LDS: max_len floats of scores.
+// out [b, H, 24].  Thread t takes the cached positions t, t + 256, ... below
+// pos with an online softmax (running max, sum and the 24 weighted-V sums);
+// the new position's normalised k and its v go through LDS (they are written
+// to the caches, not read back).  Every load that does not depend on the
+// position (q, k, v, norm weights) is issued before it, every row load for the
+// first 256 positions right after it, from clamped addresses (no branch holds a
+// load).
 __global__ __launch_bounds__(kAttnThreads) void decode_attention_kernel(
     const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v,
     const float *__restrict__ q_w, const float *__restrict__ k_w, float eps, float *__restrict__ k_cache,
     float *__restrict__ v_cache, const int64_t *__restrict__ pos_ptr, int64_t max_len, float scale,
     float *__restrict__ out) {
-  extern __shared__ float scores[];
-  __shared__ float qn[kDim];
+  __shared__ float qn[kDim], kn[kDim], vn[kDim];
   __shared__ float red[kAttnThreads / 64][kDim + 1];
-  __shared__ float stat[2];
-  const int tid = threadIdx.x;
+  __shared__ float stat[kAttnThreads / 64];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t bh = blockIdx.x;  // sequence * H + head
+  const int c = tid < kDim ? tid : 0;
+  const float qv = q[bh * kDim + c], kv = k[bh * kDim + c], vv = v[bh * kDim + c];
+  const float qw = q_w[c], kw = k_w[c];
   const int64_t pos = *pos_ptr;
   if (pos < 0 || pos >= max_len) {  // the caller's position is outside the cache: write nothing
     if (tid < kDim) out[bh * kDim + tid] = __builtin_nanf("");
     return;
   }
-  const float *qh = q + bh * kDim;
   float *kc = k_cache + bh * max_len * kDim;
   float *vc = v_cache + bh * max_len * kDim;
+  // this thread's first cached position (row 0 stands in when there is none: loaded, never used)
+  const int64_t j0 = tid < pos ? tid : 0;
+  float kr[kDim], vr[kDim];
+#pragma unroll
+  for (int i = 0; i < kDim / 4; ++i) {
+    const float4 a = reinterpret_cast<const float4 *>(kc + j0 * kDim)[i];
+    const float4 b = reinterpret_cast<const float4 *>(vc + j0 * kDim)[i];
+    kr[4 * i] = a.x; kr[4 * i + 1] = a.y; kr[4 * i + 2] = a.z; kr[4 * i + 3] = a.w;
+    vr[4 * i] = b.x; vr[4 * i + 1] = b.y; vr[4 * i + 2] = b.z; vr[4 * i + 3] = b.w;
+  }
 
-  // wave 0: per-head RMS norms of q and k (24 values each), write k and v at pos
-  if (tid < 64) {
-    const int c = tid < kDim ? tid : 0;
-    const float qv = tid < kDim ? qh[c] : 0.f, kv = tid < kDim ? k[bh * kDim + c] : 0.f;
-    const float qs = wave_sum(qv * qv), ks = wave_sum(kv * kv);
+  // wave 0: per-head RMS norms of q and k (24 values each); the new row into LDS and the caches
+  if (wave == 0) {
+    const bool on = lane < kDim;
+    float sq[2] = {on ? qv * qv : 0.f, on ? kv * kv : 0.f};
+    group_reduce<64>(sq);
+    const float qs = sq[0], ks = sq[1];
     const float rq = 1.0f / sqrtf(qs / static_cast<float>(kDim) + eps);
     const float rk = 1.0f / sqrtf(ks / static_cast<float>(kDim) + eps);
-    if (tid < kDim) {
-      qn[c] = qv * rq * q_w[c];
-      kc[pos * kDim + c] = kv * rk * k_w[c];
-      vc[pos * kDim + c] = v[bh * kDim + c];
+    if (on) {
+      const float kk = kv * rk * kw;
+      qn[lane] = qv * rq * qw;
+      kn[lane] = kk;
+      vn[lane] = vv;
+      kc[pos * kDim + lane] = kk;
+      vc[pos * kDim + lane] = vv;
     }
   }
-  __syncthreads();  // the new row is visible to the block (global and LDS)
+  __syncthreads();
 
-  // scores of positions 0..pos
   float qr[kDim];
 #pragma unroll
-  for (int c = 0; c < kDim; ++c) qr[c] = qn[c];
-  float mx = -INFINITY;
-  for (int64_t j = tid; j <= pos; j += kAttnThreads) {
-    const float4 *kr = reinterpret_cast<const float4 *>(kc + j * kDim);
+  for (int i = 0; i < kDim; ++i) qr[i] = qn[i];
+  float m = -INFINITY, l = 0.f, acc[kDim];
+#pragma unroll
+  for (int i = 0; i < kDim; ++i) acc[i] = 0.f;
+  // online softmax step with key row kk and value row vv
+  auto step = [&](const float *kk, const float *vrow) {
     float s = 0.f;
 #pragma unroll
-    for (int i = 0; i < kDim / 4; ++i) {
-      const float4 t = kr[i];
-      s = fmaf(qr[4 * i], t.x, s);
-      s = fmaf(qr[4 * i + 1], t.y, s);
-      s = fmaf(qr[4 * i + 2], t.z, s);
-      s = fmaf(qr[4 * i + 3], t.w, s);
-    }
+    for (int i = 0; i < kDim; ++i) s = fmaf(qr[i], kk[i], s);
     s *= scale;
-    scores[j] = s;
-    mx = fmaxf(mx, s);
-  }
-  // block max
+    const float mn = fmaxf(m, s);
+    const float a = expf(m - mn), p = expf(s - mn);  // m = -inf at the first step: a = 0
+    l = fmaf(l, a, p);
 #pragma unroll
-  for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
-  if ((tid & 63) == 0) red[tid >> 6][0] = mx;
-  __syncthreads();
-  if (tid == 0) {
-    float m = red[0][0];
-    for (int w = 1; w < kAttnThreads / 64; ++w) m = fmaxf(m, red[w][0]);
-    stat[0] = m;
-  }
-  __syncthreads();
-  const float m = stat[0];
-  // exp, weighted V sum per thread
-  float acc[kDim];
-#pragma unroll
-  for (int c = 0; c < kDim; ++c) acc[c] = 0.f;
-  float se = 0.f;
-  for (int64_t j = tid; j <= pos; j += kAttnThreads) {
-    const float p = expf(scores[j] - m);
-    se += p;
-    const float4 *vr = reinterpret_cast<const float4 *>(vc + j * kDim);
+    for (int i = 0; i < kDim; ++i) acc[i] = fmaf(acc[i], a, p * vrow[i]);
+    m = mn;
+  };
+  if (tid < pos) step(kr, vr);
+  for (int64_t j = tid + kAttnThreads; j < pos; j += kAttnThreads) {
 #pragma unroll
     for (int i = 0; i < kDim / 4; ++i) {
-      const float4 t = vr[i];
-      acc[4 * i] = fmaf(p, t.x, acc[4 * i]);
-      acc[4 * i + 1] = fmaf(p, t.y, acc[4 * i + 1]);
-      acc[4 * i + 2] = fmaf(p, t.z, acc[4 * i + 2]);
-      acc[4 * i + 3] = fmaf(p, t.w, acc[4 * i + 3]);
+      const float4 a = reinterpret_cast<const float4 *>(kc + j * kDim)[i];
+      const float4 b = reinterpret_cast<const float4 *>(vc + j * kDim)[i];
+      kr[4 * i] = a.x; kr[4 * i + 1] = a.y; kr[4 * i + 2] = a.z; kr[4 * i + 3] = a.w;
+      vr[4 * i] = b.x; vr[4 * i + 1] = b.y; vr[4 * i + 2] = b.z; vr[4 * i + 3] = b.w;
     }
+    step(kr, vr);
   }
-  __syncthreads();  // red[] is reused
-  se = wave_sum(se);
+  if (tid == pos % kAttnThreads) {  // the new position
 #pragma unroll
-  for (int c = 0; c < kDim; ++c) acc[c] = wave_sum(acc[c]);
-  if ((tid & 63) == 0) {
+    for (int i = 0; i < kDim; ++i) {
+      kr[i] = kn[i];
+      vr[i] = vn[i];
+    }
+    step(kr, vr);
+  }
+
+  // block max of the running maxima, then every thread's state rescaled to it
+  float bmv[1] = {m};
+  group_reduce<64, true>(bmv);
+  float bm = bmv[0];
+  if (lane == 0) stat[wave] = bm;
+  __syncthreads();
+  bm = stat[0];
 #pragma unroll
-    for (int c = 0; c < kDim; ++c) red[tid >> 6][c] = acc[c];
-    red[tid >> 6][kDim] = se;
+  for (int w = 1; w < kAttnThreads / 64; ++w) bm = fmaxf(bm, stat[w]);
+  const float f = m == -INFINITY ? 0.f : expf(m - bm);
+  float part[kDim + 1];
+#pragma unroll
+  for (int i = 0; i < kDim; ++i) part[i] = acc[i] * f;
+  part[kDim] = l * f;
+  group_reduce<64>(part);
+  if (lane == 0) {
+#pragma unroll
+    for (int i = 0; i <= kDim; ++i) red[wave][i] = part[i];
   }
   __syncthreads();
   if (tid < kDim) {
-    float s = 0.f, e = 0.f;
+    float sacc = 0.f, sl = 0.f;
+#pragma unroll
     for (int w = 0; w < kAttnThreads / 64; ++w) {
-      s += red[w][tid];
-      e += red[w][kDim];
+      sacc += red[w][tid];
+      sl += red[w][kDim];
     }
-    out[bh * kDim + tid] = s / e;
+    out[bh * kDim + tid] = sacc / sl;
   }
 }
 
@@ -218,14 +235,13 @@ int launch_decode_attention(const float *q, const float *k, const float *v, cons
                             float eps, float *k_cache, float *v_cache, const int64_t *pos, int64_t seqs_heads,
                             int64_t max_len, float *out, hipStream_t s) {
   if (seqs_heads <= 0) return PLX_OK;
-  if (max_len <= 0 || max_len > 16384)
-    return fail(PLX_EINVAL, "decode_attention: cache length %lld outside 1..16384", static_cast<long long>(max_len));
+  if (max_len <= 0 || max_len > (1 << 24))
+    return fail(PLX_EINVAL, "decode_attention: cache length %lld outside 1..2^24", static_cast<long long>(max_len));
   if (seqs_heads > 0x7FFFFFFFll) return fail(PLX_EINVAL, "decode_attention: too many heads");
   const uintptr_t al = reinterpret_cast<uintptr_t>(k_cache) | reinterpret_cast<uintptr_t>(v_cache);
   if ((al & 15u) != 0) return fail(PLX_EINVAL, "decode_attention: caches must be 16-byte aligned");
-  hipLaunchKernelGGL(decode_attention_kernel, dim3(static_cast<unsigned>(seqs_heads)), dim3(kAttnThreads),
-                     static_cast<size_t>(max_len) * sizeof(float), s, q, k, v, q_w, k_w, eps, k_cache, v_cache, pos,
-                     max_len, 1.0f / sqrtf(static_cast<float>(kDim)), out);
+  hipLaunchKernelGGL(decode_attention_kernel, dim3(static_cast<unsigned>(seqs_heads)), dim3(kAttnThreads), 0, s, q, k,
+                     v, q_w, k_w, eps, k_cache, v_cache, pos, max_len, 1.0f / sqrtf(static_cast<float>(kDim)), out);
   return check_launch("decode_attention_kernel");
 }
 

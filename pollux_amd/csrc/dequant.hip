@@ -383,11 +383,8 @@ __global__ __launch_bounds__(NT) void dqlinear_kernel(const DqlArgs<GEN> targets
             }
             float ss[MB];
 #pragma unroll
-            for (int mb = 0; mb < MB; ++mb) {
-              ss[mb] = tr == mb ? s : 0.f;
-#pragma unroll
-              for (int off = 32; off > 0; off >>= 1) ss[mb] += __shfl_xor(ss[mb], off, 64);
-            }
+            for (int mb = 0; mb < MB; ++mb) ss[mb] = tr == mb ? s : 0.f;
+            group_reduce<64>(ss);
             if (lane == 0)
 #pragma unroll
               for (int mb = 0; mb < MB; ++mb) norm_red[threadIdx.x >> 6][mb] = ss[mb];
@@ -436,10 +433,7 @@ __global__ __launch_bounds__(NT) void dqlinear_kernel(const DqlArgs<GEN> targets
         }
         if constexpr (GEN) {
           if (norm_w) {
-#pragma unroll
-            for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-              for (int off = 32; off > 0; off >>= 1) ss[mb] += __shfl_xor(ss[mb], off, 64);
+            group_reduce<64>(ss);
             if (lane == 0)
 #pragma unroll
               for (int mb = 0; mb < MB; ++mb) norm_red[threadIdx.x >> 6][mb] = ss[mb];
@@ -528,12 +522,18 @@ __global__ __launch_bounds__(NT) void dqlinear_kernel(const DqlArgs<GEN> targets
       }
     }
     // reduce the L lanes of each row
+    {
+      float flat[MB * 4];
 #pragma unroll
-    for (int mb = 0; mb < MB; ++mb)
+      for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
-      for (int t = 0; t < 4; ++t)
+        for (int t = 0; t < 4; ++t) flat[4 * mb + t] = acc[mb][t];
+      group_reduce<L>(flat);
 #pragma unroll
-        for (int off = L / 2; off > 0; off >>= 1) acc[mb][t] += __shfl_xor(acc[mb][t], off, 64);
+      for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) acc[mb][t] = flat[4 * mb + t];
+    }
     if (writer) {
       const float sig = __half2float(__ushort_as_half(sig_bits));
       const float sl = __uint_as_float(kSLatticeBits);

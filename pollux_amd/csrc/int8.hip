@@ -102,13 +102,10 @@ __global__ __launch_bounds__(256) void int8_dequant_kernel(const int8_t *__restr
   }
 }
 
-constexpr int kLinWaves = 4;  // waves per block of int8_linear_kernel
+constexpr int kLinWaves = 4;   // waves per block of int8_linear_kernel
+constexpr int kEmbedRegs = 8;  // 4-byte pieces per lane held in registers by int8_embed_kernel (rows <= 2,048)
 
-__device__ __forceinline__ float wave_sum64(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-  return v;
-}
+__device__ __forceinline__ float wave_sum64(float v) { return wave_reduce_sum(v); }
 
 // s16 of a row as fp32 (fp16(fp32(mu16) * fp32(1/127)))
 __device__ __forceinline__ float int8_row_scale(uint16_t mu) {
@@ -225,13 +222,17 @@ __global__ __launch_bounds__(64 * kLinWaves) void int8_linear_kernel(
           }
         }
       }
+      float flat[4 * MB];
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int mb = 0; mb < MB; ++mb) {
-          const float v = wave_sum64(acc[i][mb]);
-          if (lane == i * MB + mb && r0 + i < r_end && mb < mb_here) y[(m0 + mb) * rows + r0 + i] = v;
-        }
+        for (int mb = 0; mb < MB; ++mb) flat[i * MB + mb] = acc[i][mb];
+      group_reduce<64>(flat);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+          if (lane == i * MB + mb && r0 + i < r_end && mb < mb_here) y[(m0 + mb) * rows + r0 + i] = flat[i * MB + mb];
     }
   }
 }
@@ -253,19 +254,34 @@ __global__ __launch_bounds__(256) void int8_embed_kernel(const int8_t *__restric
     for (int i = lane; i < cols / 4; i += 64) o[i] = make_float4(nan, nan, nan, nan);
     return;
   }
-  const float s = int8_row_scale(mu16[id]);
+  const uint16_t mu = mu16[id];
   const uint32_t *qr = reinterpret_cast<const uint32_t *>(q + id * cols);
   const float4 *pr = pos_w ? reinterpret_cast<const float4 *>(pos_w + p * cols) : nullptr;
-  for (int i = lane; i < cols / 4; i += 64) {
-    const uint32_t b = qr[i];
+  const int n4 = cols / 4;
+  auto emit = [&](int i, uint32_t b, float4 g, float s) {
     auto one = [&](int8_t v) { return __half2float(__float2half_rn(static_cast<float>(v) * s)); };
     float4 v = make_float4(one(static_cast<int8_t>(b)), one(static_cast<int8_t>(b >> 8)),
                            one(static_cast<int8_t>(b >> 16)), one(static_cast<int8_t>(b >> 24)));
-    if (pr) {
-      const float4 g = pr[i];
-      v = make_float4(v.x + g.x, v.y + g.y, v.z + g.z, v.w + g.w);
-    }
+    if (pr) v = make_float4(v.x + g.x, v.y + g.y, v.z + g.z, v.w + g.w);
     o[i] = v;
+  };
+  if (n4 <= 64 * kEmbedRegs) {
+    // the whole row's loads in flight at once (clamped indices: no branch holds a load)
+    uint32_t b[kEmbedRegs];
+    float4 g[kEmbedRegs];
+#pragma unroll
+    for (int k = 0; k < kEmbedRegs; ++k) {
+      const int i = lane + 64 * k < n4 ? lane + 64 * k : 0;
+      b[k] = qr[i];
+      g[k] = pr ? pr[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    const float s = int8_row_scale(mu);
+#pragma unroll
+    for (int k = 0; k < kEmbedRegs; ++k)
+      if (lane + 64 * k < n4) emit(lane + 64 * k, b[k], g[k], s);
+  } else {
+    const float s = int8_row_scale(mu);
+    for (int i = lane; i < n4; i += 64) emit(i, qr[i], pr ? pr[i] : make_float4(0.f, 0.f, 0.f, 0.f), s);
   }
 }
 

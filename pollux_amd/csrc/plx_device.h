@@ -30,6 +30,52 @@ __device__ __forceinline__ uint32_t dq_value(int k, float sig, float sl) {
   return __half_as_ushort(__float2half_rn(t * sl));
 }
 
+// Lane exchange within rows of 16 lanes by DPP (no trip through the LDS
+// crossbar): CTRL 0xB1 = quad_perm [1,0,3,2] (lane ^ 1), 0x4E = quad_perm
+// [2,3,0,1] (lane ^ 2), 0x141 = half-row mirror (lane i of 8 reads 7 - i),
+// 0x140 = row mirror (lane i of 16 reads 15 - i).  All lanes must be active.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+// Sums (MAX: maxima) of N values over groups of G consecutive lanes (G = 8,
+// 16, 32 or 64), every lane of a group ending with its group's result, in
+// the same order in every group.  Within a row of 16 the steps are DPP moves
+// (xor 1, xor 2, then the two mirrors, which pair quads and half-rows that
+// already hold equal values), across rows shuffles; each step is taken for
+// all N values before the next, so their latencies overlap (a shuffle chain
+// per value waits for every step).  All lanes must be active.
+template <int G, bool MAX = false, int N>
+__device__ __forceinline__ void group_reduce(float (&v)[N]) {
+  static_assert(G == 8 || G == 16 || G == 32 || G == 64, "groups of 8, 16, 32 or 64 lanes");
+  auto op = [](float a, float b) { return MAX ? fmaxf(a, b) : a + b; };
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] = op(v[i], dpp_f32<0xB1>(v[i]));
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] = op(v[i], dpp_f32<0x4E>(v[i]));
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] = op(v[i], dpp_f32<0x141>(v[i]));
+  if constexpr (G >= 16) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] = op(v[i], dpp_f32<0x140>(v[i]));
+  }
+  if constexpr (G >= 32) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] = op(v[i], __shfl_xor(v[i], 16, 64));
+  }
+  if constexpr (G >= 64) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] = op(v[i], __shfl_xor(v[i], 32, 64));
+  }
+}
+
+__device__ __forceinline__ float wave_reduce_sum(float v) {
+  float a[1] = {v};
+  group_reduce<64>(a);
+  return a[0];
+}
+
 // Index n of a packed stream: 18 bits at bit 18*(n%4) of group n/4, read as
 // the 24-bit big-endian window starting at byte 9*(n/4) + 2*(n%4).
 __device__ __forceinline__ int32_t packed_index(const uint8_t *__restrict__ packed, int64_t n) {

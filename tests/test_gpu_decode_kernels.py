@@ -45,7 +45,9 @@ def test_rms_norm_zero_row_and_module(dev):
     assert torch.allclose(y[1], torch.ones(48, device=dev), rtol=1e-6)
 
 
-@pytest.mark.parametrize("b,heads,max_len,pos", [(1, 80, 1024, 64), (2, 3, 16, 0), (1, 5, 300, 299), (3, 2, 8, 5)])
+# positions below one block's width, several passes of it (299, 1500), the first position (0)
+@pytest.mark.parametrize("b,heads,max_len,pos", [(1, 80, 1024, 64), (2, 3, 16, 0), (1, 5, 300, 299), (3, 2, 8, 5),
+                                                 (1, 4, 2048, 1500)])
 def test_decode_attention(dev, b, heads, max_len, pos):
     g = torch.Generator().manual_seed(b * 1000 + heads + pos)
     c = heads * 24
