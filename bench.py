@@ -256,7 +256,7 @@ def traffic_from_profiles():
 
 
 def random_packed_pollux(device):
-    """(model, generator): packed Pollux-1920 (18 layers, d 1920, vocab 50,688), random packed weights (valid indices)."""
+    """(model, generator, payload): packed Pollux-1920 (18 layers, d 1920, vocab 50,688), random packed weights."""
     import torch
 
     from pollux_amd import castor
@@ -287,7 +287,31 @@ def random_packed_pollux(device):
             state[p + name + ".sigma_rows"] = (torch.rand(o, generator=g, device=device) * 0.045 + 0.005).half()
     payload = {"format": PLX_FORMAT, "config": cfg, "codebook_fingerprint": castor.codebook_fingerprint(),
                "state_dict": state}
-    return PackedPolluxModel.from_packed_checkpoint(payload, device), g
+    return PackedPolluxModel.from_packed_checkpoint(payload, device), g, payload
+
+
+def decode_workload(device, n_tokens, prompt_len=64):
+    """Greedy graph decode of n_tokens after a prompt (random packed Pollux-1920); returns a summary line."""
+    import torch
+
+    from pollux_amd.model import GraphDecoder
+
+    model, g, _ = random_packed_pollux(device)
+    prompt = torch.randint(0, 50257, (1, prompt_len), generator=g, device=device)
+    with torch.inference_mode():
+        dec = GraphDecoder(model, batch=1)
+        t = dec.prefill(prompt).argmax(-1)
+        for _ in range(8):
+            t = dec.decode(t).argmax(-1)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(n_tokens):
+            t = dec.decode(t).argmax(-1)
+        e1.record()
+        e1.synchronize()
+    ms = e0.elapsed_time(e1) / n_tokens
+    return f"packed decode (graph, batch 1, prompt {prompt_len}): {ms:.4f} ms/token over {n_tokens} tokens"
 
 
 def decode_extras(device, prompt_len=64, new_tokens=128):
@@ -302,9 +326,9 @@ def decode_extras(device, prompt_len=64, new_tokens=128):
     """
     import torch
 
-    from pollux_amd.model import GraphDecoder
+    from pollux_amd.model import GraphDecoder, PackedPolluxModel
 
-    model, g = random_packed_pollux(device)
+    model, g, payload = random_packed_pollux(device)
     prompt = torch.randint(0, 50257, (1, prompt_len), generator=g, device=device)
 
     def timed(fn, n):
@@ -369,6 +393,14 @@ def main() -> int:
         help="for rocprofv3 --pmc runs: 5 copies of a 256 MiB fp32 tensor (HBM-counter calibration), then "
         "--steps config-2 steps; prints nothing",
     )
+    ap.add_argument(
+        "--decode-workload",
+        type=int,
+        default=0,
+        metavar="N",
+        help="for rocprofv3 runs: the packed Pollux-1920 decoder only (prefill 64 tokens, then N greedy tokens "
+        "replayed from its HIP graph); prints one line with ms/token",
+    )
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -390,6 +422,10 @@ def main() -> int:
     lib = _lib.lib()
     with torch.cuda.device(dev):
         _lib.check(lib.plx_device_init(), "plx_device_init")
+
+    if args.decode_workload:
+        print(decode_workload(dev, args.decode_workload), flush=True)
+        return 0
 
     mats = make_c2(dev)
     atoms = sum(r * c // 24 for r, c in C2_SHAPES)
