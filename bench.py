@@ -255,6 +255,102 @@ def traffic_from_profiles():
     return None
 
 
+def _nn_profiled(fn, iters):
+    """(seconds per call, nn_kernel ms per launch) of fn over iters calls, nn_kernel timed by HIP events."""
+    import ctypes
+
+    import torch
+
+    from pollux_amd import _lib
+
+    lib = _lib.lib()
+    torch.cuda.synchronize()
+    _lib.check(lib.plx_profile_begin(), "plx_profile_begin")
+    t = time_gpu(fn, iters, 0)
+    tot_ms, launches = ctypes.c_double(), ctypes.c_int64()
+    _lib.check(lib.plx_profile_end(ctypes.byref(tot_ms), ctypes.byref(launches)), "plx_profile_end")
+    return t, tot_ms.value / max(1, launches.value)
+
+
+def sweep_extras(device):
+    """The bulk quantizer at BASELINE config 4 and the Pollux-1920 layer of config 3.
+
+    config 4: 16,777,200 atoms (209,715 rows of 1920) with directions on S^23
+    and radius U(0, 2) * sqrt(32), fed to quantize_indices (NN-B).  config 3:
+    the fused requantize (as the headline step) of the four Pollux-1920
+    latents, then quantize_indices on their lattice-unit atoms with 5% replaced
+    by midpoints of code pairs at raw inner product 16 (+ N(0, 1e-3) noise)
+    and 5% by random directions at norm sqrt 2 (the origin boundary).
+    """
+    import numpy as np
+    import torch
+
+    from pollux_amd import castor
+
+    out = {}
+    n = 209_715 * 80
+    g = torch.Generator(device=device).manual_seed(404)
+    d = torch.randn(n, 24, generator=g, device=device)
+    x = d / d.norm(dim=1, keepdim=True) * (torch.rand(n, 1, generator=g, device=device) * 2.0 * np.sqrt(32.0))
+    del d
+    castor.quantize_indices(x, mode="bf16")
+    t, k_ms = _nn_profiled(lambda: castor.quantize_indices(x, mode="bf16"), 3)
+    out["config4_quantize"] = {
+        "atoms": n, "ms": t * 1e3, "atoms_per_s": n / t, "nn_kernel_ms": k_ms,
+        "nn_kernel_mfma_frac": FLOP_PER_ATOM * n / (k_ms / 1e3) / PEAK_BF16_FLOPS,
+        "note": "quantize_indices (NN-B: bf16 scores, lowest index) on uniform-sphere atoms"}
+    del x
+    torch.cuda.empty_cache()
+
+    shapes = [(5760, 1920), (1920, 1920), (7680, 1920), (1920, 7680)]
+    g = torch.Generator(device=device).manual_seed(303)
+    mats = [(torch.randn(r, c, generator=g, device=device) * 0.02).to(torch.bfloat16).float() for r, c in shapes]
+    atoms = sum(r * c // 24 for r, c in shapes)
+
+    def step():
+        for w in mats:
+            castor.requantize_h24(w, mode="bf16")
+
+    step()
+    t, k_ms = _nn_profiled(step, 5)
+    out["config3_requantize"] = {
+        "atoms": atoms, "ms_per_step": t * 1e3, "atoms_per_s": atoms / t, "nn_kernel_ms_avg": k_ms,
+        "note": "fused row scale + NN-B + pack + reconstructed weight of QKV 5760x1920, O 1920x1920, up 7680x1920, "
+                "down 1920x7680 (bf16-rounded N(0, 0.02) master weights)"}
+
+    # lattice-unit atoms (pollux.py:876-882) with the boundary stress
+    xs = []
+    for w in mats:
+        sigma = castor.row_rms_from_matrix(w)
+        xs.append((w / sigma.unsqueeze(1) / castor.s_lattice).reshape(-1, 24))
+    x = torch.cat(xs)
+    rng = torch.Generator(device=device).manual_seed(304)
+    perm = torch.randperm(atoms, generator=rng, device=device)
+    mid_at, near_at = perm[: atoms // 20], perm[atoms // 20: atoms // 10]
+    cb = castor.get_h24_codebook(device, torch.float32)
+    raw = torch.round(cb * np.sqrt(8.0)).to(torch.int32)
+    a = torch.randint(1, 196561, (mid_at.numel(),), generator=rng, device=device)
+    b = torch.zeros_like(a)
+    todo = torch.arange(a.numel(), device=device)
+    while todo.numel():  # a partner at raw inner product 16 (the true-Leech contact)
+        cand = torch.randint(1, 196561, (todo.numel(), 64), generator=rng, device=device)
+        ip = (raw[cand] * raw[a[todo]].unsqueeze(1)).sum(-1)
+        hit = ip == 16
+        ok = hit.any(dim=1)
+        b[todo[ok]] = cand[ok].gather(1, hit[ok].int().argmax(dim=1, keepdim=True)).squeeze(1)
+        todo = todo[~ok]
+    x[mid_at] = 0.5 * (cb[a] + cb[b]) + torch.randn(a.numel(), 24, generator=rng, device=device) * 1e-3
+    dirs = torch.randn(near_at.numel(), 24, generator=rng, device=device)
+    x[near_at] = dirs / dirs.norm(dim=1, keepdim=True) * np.sqrt(2.0)
+    castor.quantize_indices(x, mode="bf16")
+    t, k_ms = _nn_profiled(lambda: castor.quantize_indices(x, mode="bf16"), 5)
+    out["config3_stress_quantize"] = {
+        "atoms": atoms, "ms": t * 1e3, "atoms_per_s": atoms / t, "nn_kernel_ms": k_ms,
+        "note": "quantize_indices (NN-B) on the config-3 lattice atoms with 5% contact-pair midpoints and 5% "
+                "near-origin atoms (more near-ties for the exact rescoring pass)"}
+    return out
+
+
 def random_packed_pollux(device):
     """(model, generator, payload): packed Pollux-1920 (18 layers, d 1920, vocab 50,688), random packed weights."""
     import torch
@@ -518,6 +614,7 @@ def main() -> int:
         result["extras"]["optimizer_step"] = optim_extras(dev, mats)
         result["extras"]["pack_time_nn_p"] = pack_time_extras(mats)
         result["extras"]["packed_decode"] = decode_extras(dev)
+        result["extras"]["quantizer_sweeps"] = sweep_extras(dev)
     if not args.no_cpu_baseline:
         log(f"[bench] CPU baseline on {args.cpu_atoms} atoms")
         result["cpu_baseline"] = cpu_baseline(mats, args.cpu_atoms)
