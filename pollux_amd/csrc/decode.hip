@@ -102,7 +102,7 @@ __global__ __launch_bounds__(kAttnThreads) void decode_attention_kernel(
   __shared__ float stat[kAttnThreads / 64];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t bh = blockIdx.x;  // sequence * H + head
-  const int c = tid < kDim ? tid : 0;
+  const int c = lane < kDim ? lane : 0;  // every wave loads the head's 24 values (lanes 0..23)
   const float qv = q[bh * kDim + c], kv = k[bh * kDim + c], vv = v[bh * kDim + c];
   const float qw = q_w[c], kw = k_w[c];
   const int64_t pos = *pos_ptr;
@@ -123,16 +123,17 @@ __global__ __launch_bounds__(kAttnThreads) void decode_attention_kernel(
     vr[4 * i] = b.x; vr[4 * i + 1] = b.y; vr[4 * i + 2] = b.z; vr[4 * i + 3] = b.w;
   }
 
-  // wave 0: per-head RMS norms of q and k (24 values each); the new row into LDS and the caches
-  if (wave == 0) {
+  // per-head RMS norms of q and k (24 values each), computed by every wave (no
+  // branch around the loads above, which the compiler would otherwise sink into
+  // it and wait for one by one); wave 0 stores the new row in LDS and the caches
+  {
     const bool on = lane < kDim;
     float sq[2] = {on ? qv * qv : 0.f, on ? kv * kv : 0.f};
     group_reduce<64>(sq);
-    const float qs = sq[0], ks = sq[1];
-    const float rq = 1.0f / sqrtf(qs / static_cast<float>(kDim) + eps);
-    const float rk = 1.0f / sqrtf(ks / static_cast<float>(kDim) + eps);
-    if (on) {
-      const float kk = kv * rk * kw;
+    const float rq = 1.0f / sqrtf(sq[0] / static_cast<float>(kDim) + eps);
+    const float rk = 1.0f / sqrtf(sq[1] / static_cast<float>(kDim) + eps);
+    const float kk = kv * rk * kw;
+    if (tid < kDim) {
       qn[lane] = qv * rq * qw;
       kn[lane] = kk;
       vn[lane] = vv;

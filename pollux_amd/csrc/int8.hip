@@ -135,6 +135,9 @@ __global__ __launch_bounds__(64 * kLinWaves) void int8_linear_kernel(
   const int nch = cols >> 4;
   for (int64_t m0 = 0; m0 < m_total; m0 += MB) {
     const int mb_here = static_cast<int>(min(static_cast<int64_t>(MB), m_total - m0));
+    // Every load below comes from a clamped address with no branch around it
+    // (a load under a divergent branch is waited for at once when the other
+    // path writes the same register); out-of-range values are zeroed after.
     float xr[MB][CPL][16];
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb)
@@ -142,14 +145,15 @@ __global__ __launch_bounds__(64 * kLinWaves) void int8_linear_kernel(
       for (int j = 0; j < CPL; ++j) {
         const int c = lane + 64 * j;
         const bool ok = c < nch && mb < mb_here;
-        const float4 *src = reinterpret_cast<const float4 *>(x + (m0 + mb) * cols + 16 * c);
+        const float4 *src =
+            reinterpret_cast<const float4 *>(x + (m0 + (mb < mb_here ? mb : 0)) * cols + 16 * (c < nch ? c : 0));
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-          const float4 v = ok ? src[k] : make_float4(0.f, 0.f, 0.f, 0.f);
-          xr[mb][j][4 * k] = v.x;
-          xr[mb][j][4 * k + 1] = v.y;
-          xr[mb][j][4 * k + 2] = v.z;
-          xr[mb][j][4 * k + 3] = v.w;
+          const float4 v = src[k];
+          xr[mb][j][4 * k] = ok ? v.x : 0.f;
+          xr[mb][j][4 * k + 1] = ok ? v.y : 0.f;
+          xr[mb][j][4 * k + 2] = ok ? v.z : 0.f;
+          xr[mb][j][4 * k + 3] = ok ? v.w : 0.f;
         }
       }
     if constexpr (NORM) {
@@ -166,11 +170,10 @@ __global__ __launch_bounds__(64 * kLinWaves) void int8_linear_kernel(
 #pragma unroll
         for (int j = 0; j < CPL; ++j) {
           const int c = lane + 64 * j;
-          if (c >= nch) continue;
-          const float4 *g4 = reinterpret_cast<const float4 *>(norm_w + 16 * c);
+          const float4 *g4 = reinterpret_cast<const float4 *>(norm_w + 16 * (c < nch ? c : 0));
 #pragma unroll
           for (int k = 0; k < 4; ++k) {
-            const float4 g = g4[k];
+            const float4 g = g4[k];  // lanes past the row scale zeros
             xr[mb][j][4 * k] = xr[mb][j][4 * k] * r * g.x;
             xr[mb][j][4 * k + 1] = xr[mb][j][4 * k + 1] * r * g.y;
             xr[mb][j][4 * k + 2] = xr[mb][j][4 * k + 2] * r * g.z;
@@ -184,13 +187,12 @@ __global__ __launch_bounds__(64 * kLinWaves) void int8_linear_kernel(
       float sc[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int64_t row = r0 + i;
-        const bool rv = row < r_end;
-        sc[i] = rv ? int8_row_scale(mu16[row]) : 0.f;
+        const int64_t row = r0 + i < r_end ? r0 + i : r_end - 1;  // rows past the end: loaded, never stored
+        sc[i] = int8_row_scale(mu16[row]);
 #pragma unroll
         for (int j = 0; j < CPL; ++j) {
-          const int c = lane + 64 * j;
-          qv[i][j] = rv && c < nch ? *reinterpret_cast<const uint4 *>(q + row * cols + 16 * c) : make_uint4(0, 0, 0, 0);
+          const int c = lane + 64 * j;  // chunks past the row: loaded, never used
+          qv[i][j] = *reinterpret_cast<const uint4 *>(q + row * cols + 16 * (c < nch ? c : 0));
         }
       }
       float acc[4][MB];
