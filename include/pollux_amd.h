@@ -265,6 +265,12 @@ int plx_decode_attention(const float *q, const float *k, const float *v, const f
                          const float *k_norm_w, float eps, float *k_cache, float *v_cache,
                          const int64_t *pos, int64_t n, int64_t max_len, float *out, void *stream);
 
+/* out[r] = the index of the maximum of x[r, :] (fp32 [rows, cols], int64 out):
+ * torch.argmax's rule (the first index among equal maxima; a NaN counts as the
+ * maximum).  Greedy decoding's token choice (generate.py:313-320, top_k = 1)
+ * inside a captured decode step. */
+int plx_argmax_rows(const float *x, int64_t rows, int64_t cols, int64_t *out, void *stream);
+
 /* ---- per-row INT8 periphery (embeddings / LM head in .plx files) ------- */
 /* q_out int8[rows*cols] = int8(clamp(rint((w / mu) * 127), -128, 127)),
  * mu16_out[r] = fp16(mu) with mu = max(max_j |w[r,j]|, 1e-8); all fp32 IEEE ops.

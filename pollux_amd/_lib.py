@@ -50,6 +50,7 @@ SIGNATURES = {
     "plx_dequant_linear_multi": (_int, [_vp, _int, _i64, _vp, _int, _i64, _vp, ctypes.c_float, _vp, _sz, _vp]),
     "plx_int8_linear": (_int, [_vp, _vp, _i64, _i64, _vp, _i64, _vp, ctypes.c_float, _vp, _vp]),
     "plx_int8_embed": (_int, [_vp, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _vp, _vp, _vp]),
+    "plx_argmax_rows": (_int, [_vp, _i64, _i64, _vp, _vp]),
     "plx_rms_norm": (_int, [_vp, _vp, _vp, _i64, _i64, ctypes.c_float, _vp]),
     "plx_decode_attention": (_int, [_vp, _vp, _vp, _vp, _vp, ctypes.c_float, _vp, _vp, _vp, _i64, _i64, _vp, _vp]),
     "plx_profile_begin": (_int, []),

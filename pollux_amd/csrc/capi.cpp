@@ -289,6 +289,14 @@ int plx_rms_norm(const float *x, const float *w, float *y, int64_t rows, int64_t
   return launch_rms_norm(x, w, y, rows, d, eps, as_stream(stream));
 }
 
+int plx_argmax_rows(const float *x, int64_t rows, int64_t cols, int64_t *out, void *stream) {
+  PLX_REQUIRE(rows >= 0 && cols > 0, "plx_argmax_rows: bad shape (%lld, %lld)", static_cast<long long>(rows),
+              static_cast<long long>(cols));
+  if (rows == 0) return PLX_OK;
+  PLX_REQUIRE(x != nullptr && out != nullptr, "plx_argmax_rows: null pointer");
+  return launch_argmax_rows(x, rows, cols, out, as_stream(stream));
+}
+
 int plx_decode_attention(const float *q, const float *k, const float *v, const float *q_norm_w,
                          const float *k_norm_w, float eps, float *k_cache, float *v_cache, const int64_t *pos,
                          int64_t n, int64_t max_len, float *out, void *stream) {

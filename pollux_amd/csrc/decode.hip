@@ -25,6 +25,8 @@ namespace {
 constexpr int kNormRowsPerBlock = 4;  // one wave per row
 constexpr int kNormRegVec = 8;        // float4 per lane held in registers (rows of <= 2,048 values)
 constexpr int kAttnThreads = 256;
+constexpr int kArgThreads = 1024;
+constexpr int kArgRegs = 16;  // float4 per thread held in registers (rows of <= 65,536 values)
 
 __device__ __forceinline__ float wave_sum(float v) { return wave_reduce_sum(v); }
 
@@ -213,7 +215,89 @@ __global__ __launch_bounds__(kAttnThreads) void decode_attention_kernel(
   }
 }
 
+// torch.argmax's order: a NaN beats every number; among equal values (or
+// NaNs) the lowest index wins.
+__device__ __forceinline__ bool arg_better(float v, int i, float bv, int bi) {
+  const bool vn = v != v, bn = bv != bv;
+  if (vn || bn) return vn && (!bn || i < bi);
+  return v > bv || (v == bv && i < bi);
+}
+
+// One block per row of cols values; each thread scans its strided share
+// (increasing indices), then the block reduces (value, index) pairs.
+template <bool VEC>
+__global__ __launch_bounds__(kArgThreads) void argmax_rows_kernel(const float *__restrict__ x, int cols,
+                                                                  int64_t *__restrict__ out) {
+  __shared__ float sv[kArgThreads / 64];
+  __shared__ int si[kArgThreads / 64];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const float *r = x + static_cast<int64_t>(blockIdx.x) * cols;
+  float bv = -INFINITY;
+  int bi = cols;  // beyond every index: the first -inf wins when all are -inf
+  if constexpr (VEC) {
+    const float4 *r4 = reinterpret_cast<const float4 *>(r);
+    const int n4 = cols / 4;
+    auto take = [&](const float4 &v, int i) {
+      if (arg_better(v.x, 4 * i, bv, bi)) { bv = v.x; bi = 4 * i; }
+      if (arg_better(v.y, 4 * i + 1, bv, bi)) { bv = v.y; bi = 4 * i + 1; }
+      if (arg_better(v.z, 4 * i + 2, bv, bi)) { bv = v.z; bi = 4 * i + 2; }
+      if (arg_better(v.w, 4 * i + 3, bv, bi)) { bv = v.w; bi = 4 * i + 3; }
+    };
+    if (n4 <= kArgThreads * kArgRegs) {
+      // the whole row in flight at once (clamped indices: no branch holds a load)
+      float4 v[kArgRegs];
+#pragma unroll
+      for (int k = 0; k < kArgRegs; ++k) {
+        const int i = tid + kArgThreads * k;
+        v[k] = r4[i < n4 ? i : 0];
+      }
+#pragma unroll
+      for (int k = 0; k < kArgRegs; ++k)
+        if (tid + kArgThreads * k < n4) take(v[k], tid + kArgThreads * k);
+    } else {
+#pragma unroll 4
+      for (int i = tid; i < n4; i += kArgThreads) take(r4[i], i);
+    }
+  } else {
+#pragma unroll 4
+    for (int i = tid; i < cols; i += kArgThreads) {
+      const float v = r[i];
+      if (arg_better(v, i, bv, bi)) { bv = v; bi = i; }
+    }
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const float ov = __shfl_xor(bv, off, 64);
+    const int oi = __shfl_xor(bi, off, 64);
+    if (arg_better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+  }
+  if (lane == 0) {
+    sv[wave] = bv;
+    si[wave] = bi;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    for (int w = 1; w < kArgThreads / 64; ++w)
+      if (arg_better(sv[w], si[w], bv, bi)) { bv = sv[w]; bi = si[w]; }
+    out[blockIdx.x] = bi < cols ? bi : 0;
+  }
+}
+
 }  // namespace
+
+int launch_argmax_rows(const float *x, int64_t rows, int64_t cols, int64_t *out, hipStream_t s) {
+  if (rows <= 0) return PLX_OK;
+  if (cols <= 0 || cols > 0x7FFFFFFFll || rows > 0x7FFFFFFFll)
+    return fail(PLX_EINVAL, "argmax_rows: shape (%lld, %lld)", static_cast<long long>(rows), static_cast<long long>(cols));
+  const bool vec = cols % 4 == 0 && (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
+  if (vec)
+    hipLaunchKernelGGL((argmax_rows_kernel<true>), dim3(static_cast<unsigned>(rows)), dim3(kArgThreads), 0, s, x,
+                       static_cast<int>(cols), out);
+  else
+    hipLaunchKernelGGL((argmax_rows_kernel<false>), dim3(static_cast<unsigned>(rows)), dim3(kArgThreads), 0, s, x,
+                       static_cast<int>(cols), out);
+  return check_launch("argmax_rows_kernel");
+}
 
 int launch_rms_norm(const float *x, const float *w, float *y, int64_t rows, int64_t d, float eps, hipStream_t s) {
   if (rows <= 0) return PLX_OK;

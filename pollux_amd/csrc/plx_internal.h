@@ -86,6 +86,7 @@ int launch_int8_linear(const int8_t *q, const uint16_t *mu16, int64_t rows, int6
 int launch_int8_embed(const int8_t *q, const uint16_t *mu16, int64_t vocab, int64_t cols, const int64_t *idx,
                       int64_t n, int64_t t, const float *pos_w, int64_t pos_rows, const int64_t *pos0, float *out,
                       hipStream_t s);
+int launch_argmax_rows(const float *x, int64_t rows, int64_t cols, int64_t *out, hipStream_t s);
 int launch_rms_norm(const float *x, const float *w, float *y, int64_t rows, int64_t d, float eps, hipStream_t s);
 int launch_decode_attention(const float *q, const float *k, const float *v, const float *q_w, const float *k_w,
                             float eps, float *k_cache, float *v_cache, const int64_t *pos, int64_t seqs_heads,

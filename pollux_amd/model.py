@@ -106,6 +106,25 @@ def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
     return y
 
 
+def argmax_rows(x: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """torch.argmax(x, dim=-1) for fp32 x, one HIP kernel (plx_argmax_rows): int64 [...] (into ``out`` if given)."""
+    _lib.require_device(x, "argmax_rows input")
+    if x.dtype != torch.float32:
+        raise ValueError("argmax_rows runs on fp32 values")
+    cols = x.shape[-1]
+    if cols == 0:
+        raise ValueError("argmax_rows of an empty dimension")
+    xx = x.reshape(-1, cols).contiguous()
+    if out is None:
+        out = torch.empty(x.shape[:-1], dtype=torch.long, device=x.device)
+    if out.dtype != torch.long or out.numel() != xx.shape[0] or not out.is_contiguous() or out.device != x.device:
+        raise ValueError("argmax_rows: out must be a contiguous int64 tensor with one element per row")
+    with torch.cuda.device(x.device):
+        st = _lib.lib().plx_argmax_rows(_lib.ptr(xx), xx.shape[0], cols, _lib.ptr(out), _lib.stream_of(x.device))
+    _lib.check(st, "argmax_rows")
+    return out
+
+
 def decode_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q_ln: RMSNorm, k_ln: RMSNorm,
                      k_cache: torch.Tensor, v_cache: torch.Tensor, pos: torch.Tensor) -> torch.Tensor:
     """Attention of one new token per sequence over the cache (plx_decode_attention).
@@ -343,9 +362,14 @@ class GraphDecoder:
     the device), captured once.
     Usage: ``dec.prefill(prompt_ids)`` then ``logits = dec.decode(next_ids)``
     per token; the returned logits tensor is reused by the next replay.
+    With ``greedy=True`` the captured step also takes the argmax of its
+    logits (generate.py:313-320 with top_k = 1), records it at its position
+    and feeds it to the next replay: ``dec.decode_greedy(first_ids, n)`` then
+    decodes n tokens without the host in the loop.
     """
 
-    def __init__(self, model: PackedPolluxModel, batch: int = 1, max_len: int | None = None) -> None:
+    def __init__(self, model: PackedPolluxModel, batch: int = 1, max_len: int | None = None,
+                 greedy: bool = False) -> None:
         self.model = model
         cfg = model.cfg
         self.max_len = int(min(max_len or cfg.seq_len, cfg.seq_len))
@@ -353,6 +377,9 @@ class GraphDecoder:
         self.cache = model.new_cache(batch, self.max_len)
         self.ids = torch.zeros(batch, dtype=torch.long, device=device)
         self.pos = torch.zeros((), dtype=torch.long, device=device)
+        self.greedy = bool(greedy)
+        # token chosen at each position (greedy); one slot past the cache for the last step's choice
+        self.history = torch.zeros(batch, self.max_len + 1, dtype=torch.long, device=device) if greedy else None
         self.length = 0
         self.graph = None
         self.logits = None
@@ -364,7 +391,11 @@ class GraphDecoder:
         for i, blk in enumerate(m.blocks):
             x = blk(x, self.cache, i, self.pos)
         self.pos += 1
-        return m.logits(x)[:, -1]
+        logits = m.logits(x)[:, -1]
+        if self.greedy:
+            argmax_rows(logits, out=self.ids)  # the next replay's input
+            self.history.index_copy_(1, self.pos.view(1), self.ids.view(b, 1))  # at the new token's position
+        return logits
 
     @torch.inference_mode()
     def prefill(self, idx: torch.Tensor) -> torch.Tensor:
@@ -403,6 +434,22 @@ class GraphDecoder:
         self.graph.replay()
         self.length += 1
         return self.logits
+
+    @torch.inference_mode()
+    def decode_greedy(self, next_ids: torch.Tensor, n: int) -> torch.Tensor:
+        """Token ids [batch, n]: n greedy steps from ``next_ids``, each replay feeding its argmax to the next."""
+        if not self.greedy:
+            raise RuntimeError("decode_greedy needs GraphDecoder(..., greedy=True)")
+        if self.graph is None:
+            raise RuntimeError("GraphDecoder.decode_greedy before prefill")
+        if n < 0 or self.length + n > self.max_len:
+            raise ValueError(f"{n} steps from position {self.length} exceed the cache's {self.max_len} positions")
+        start = self.length + 1  # position of the first chosen token
+        self.ids.copy_(next_ids.reshape(-1))
+        for _ in range(n):
+            self.graph.replay()
+        self.length += n
+        return self.history[:, start:start + n].clone()
 
 
 # ---- sampling (generate.py:228-278) ------------------------------------------------

@@ -94,3 +94,38 @@ def test_decode_attention_position_outside_cache(dev):
             out = decode_attention(q, q, q, ln, ln, kc, vc, torch.tensor(bad, dtype=torch.long, device=dev))
         assert torch.isnan(out).all()
         assert torch.equal(kc, kc0) and torch.equal(vc, vc0)
+
+
+@pytest.mark.parametrize("rows,cols", [(1, 50688), (3, 1000), (2, 7), (5, 4096), (1, 1)])
+def test_argmax_rows_matches_torch(dev, rows, cols):
+    from pollux_amd.model import argmax_rows
+
+    g = torch.Generator().manual_seed(rows * 31 + cols)
+    x = torch.randn(rows, cols, generator=g)
+    if cols > 10:
+        x[0, cols // 3] = x[0].max() + 1.0
+        x[0, cols // 2] = x[0, cols // 3]  # a tie: the lower index wins
+    x = x.to(dev)
+    assert torch.equal(argmax_rows(x), torch.argmax(x, dim=-1))
+    if cols > 10:
+        y = x.clone()
+        y[-1, 5] = float("nan")
+        y[-1, 9] = float("nan")  # NaN counts as the maximum; the first NaN wins
+        y[0] = float("-inf")      # all -inf: index 0
+        assert torch.equal(argmax_rows(y), torch.argmax(y, dim=-1))
+        # a row start that is not 16-byte aligned (element-wise loads)
+        z = x.reshape(-1)[1:1 + (rows * cols - 1) // (cols - 1) * (cols - 1)].reshape(-1, cols - 1)
+        assert torch.equal(argmax_rows(z), torch.argmax(z, dim=-1))
+
+
+def test_argmax_rows_long_rows_and_out(dev):
+    # rows past the register path (> 65,536 values) and the out= form
+    from pollux_amd.model import argmax_rows
+
+    x = torch.randn(2, 70_000, generator=torch.Generator().manual_seed(5)).to(dev)
+    x[1, 69_999] = 100.0
+    out = torch.full((2,), -1, dtype=torch.long, device=dev)
+    assert argmax_rows(x, out=out) is out
+    assert torch.equal(out, torch.argmax(x, dim=-1))
+    with pytest.raises(ValueError):
+        argmax_rows(x, out=torch.empty(3, dtype=torch.long, device=dev))

@@ -161,3 +161,27 @@ def test_graph_decoder_matches_eager_decode(dev, packed):
             dec.decode(idx[:, 0])  # the cache is full
     print(f"[model] graph decode vs eager decode, worst rel {worst:.2e}", flush=True)
     assert worst <= 1e-5
+
+
+def test_graph_greedy_decode_matches_eager_argmax(dev, packed):
+    # the captured step's own argmax and token feedback against an eager KV-cached greedy loop
+    from pollux_amd.model import GraphDecoder
+
+    model = PackedPolluxModel.from_packed_checkpoint(str(packed[0]), dev)
+    dec = GraphDecoder(model, batch=2, greedy=True)
+    idx = torch.randint(0, 90, (2, 4), generator=torch.Generator().manual_seed(9)).to(dev)
+    with torch.inference_mode():
+        first = dec.prefill(idx).argmax(-1)
+        got = dec.decode_greedy(first, 12)  # inputs at positions 4..15 fill the cache; choices for 5..16
+        cache = model.new_cache(2)
+        t = model.prefill(idx, cache)[:, -1].argmax(-1)
+        want = []
+        for _ in range(12):
+            t = model.decode(t, cache).argmax(-1)
+            want.append(t)
+        want = torch.stack(want, dim=1)
+        with pytest.raises(ValueError):
+            dec.decode_greedy(first, 1)  # the cache is full
+    print(f"[model] greedy graph tokens {got.tolist()}", flush=True)
+    assert got.shape == (2, 12)
+    assert torch.equal(got, want)
