@@ -1263,7 +1263,8 @@ int launch_dequant_linear_multi(const DqlTarget *targets, int n, int64_t cols, c
     }
     t.norm_w = norm_w;
     t.norm_eps = norm_eps;
-    // lanes per row: about 3-5 atoms per lane (7680 x 1920 at M = 1: 16 lanes 6% faster than 32, 8 slower);
+    // lanes per row: about 3-5 atoms per lane (7680 x 1920 at M = 1: 16 lanes as fast as 32, 8 slower; the
+    // 1920-row q/k/v and o_proj launches of the decode step 3% faster with 32, from the doubled grid);
     // 512-thread blocks (4% faster than 256 at M = 1, 1,024 slower), 256 for rows too long to stage 8 in LDS
     if (apr >= 3072)
       st = x_is_f32 ? launch_dql<64, true, 256>(t, apr, x, m, kp, round_w, gelu, xnorm, s)
@@ -1271,9 +1272,17 @@ int launch_dequant_linear_multi(const DqlTarget *targets, int n, int64_t cols, c
     else if (apr >= 160)
       st = x_is_f32 ? launch_dql<64, true, 512>(t, apr, x, m, kp, round_w, gelu, xnorm, s)
                     : launch_dql<64, false, 512>(t, apr, x, m, kp, round_w, gelu, xnorm, s);
-    else if (apr >= 16)
-      st = x_is_f32 ? launch_dql<16, true, 512>(t, apr, x, m, kp, round_w, gelu, xnorm, s)
-                    : launch_dql<16, false, 512>(t, apr, x, m, kp, round_w, gelu, xnorm, s);
+    else if (apr >= 16) {
+      // 32 lanes per row (16 rows per block) when 16 would leave the grid under 192 blocks
+      int64_t mrows = 0;
+      for (int i = 0; i < t.n; ++i) mrows = t.rows[i] > mrows ? t.rows[i] : mrows;
+      if ((mrows + 31) / 32 * t.n < 192)
+        st = x_is_f32 ? launch_dql<32, true, 512>(t, apr, x, m, kp, round_w, gelu, xnorm, s)
+                      : launch_dql<32, false, 512>(t, apr, x, m, kp, round_w, gelu, xnorm, s);
+      else
+        st = x_is_f32 ? launch_dql<16, true, 512>(t, apr, x, m, kp, round_w, gelu, xnorm, s)
+                      : launch_dql<16, false, 512>(t, apr, x, m, kp, round_w, gelu, xnorm, s);
+    }
     else
       st = x_is_f32 ? launch_dql<8, true, 512>(t, apr, x, m, kp, round_w, gelu, xnorm, s)
                     : launch_dql<8, false, 512>(t, apr, x, m, kp, round_w, gelu, xnorm, s);
