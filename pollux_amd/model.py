@@ -269,7 +269,7 @@ class PackedPolluxModel(nn.Module):
         self.ln_f = RMSNorm(n_embd)
         self.head = PackedInt8Linear(n_embd, int(cfg.vocab_size), bias=False)
 
-    def _run(self, idx: torch.Tensor, pos0: int, cache: KVCache | None) -> torch.Tensor:
+    def _run(self, idx: torch.Tensor, pos0: int, cache: KVCache | None, last_only: bool = False) -> torch.Tensor:
         t = idx.shape[1]
         pos = torch.arange(pos0, pos0 + t, device=idx.device).unsqueeze(0)
         x = self.embed(idx, pos[:, 0])
@@ -278,7 +278,7 @@ class PackedPolluxModel(nn.Module):
             x = block(x, cache, i, step_pos)
         if cache is not None:
             cache.length = pos0 + t
-        return self.logits(x)
+        return self.logits(x[:, -1:] if last_only else x)
 
     def embed(self, idx: torch.Tensor, pos0: torch.Tensor) -> torch.Tensor:
         """tok_emb(idx) + pos_emb(positions pos0 .. pos0 + t - 1) (pollux.py:691-693); pos0 a device int64 tensor."""
@@ -292,21 +292,28 @@ class PackedPolluxModel(nn.Module):
         """head(ln_f(x)) (pollux.py:699-700), the norm fused into the INT8 head where that runs."""
         return self.head(x, norm=(self.ln_f.weight, self.ln_f.eps))
 
-    def forward(self, idx: torch.Tensor) -> torch.Tensor:
-        """Logits [b, t, vocab] of the full prefix, positions 0..t-1 (pollux.py:691-702)."""
+    def forward(self, idx: torch.Tensor, last_only: bool = False) -> torch.Tensor:
+        """Logits [b, t, vocab] of the full prefix, positions 0..t-1 (pollux.py:691-702).
+
+        ``last_only``: logits [b, 1, vocab] of the last position only (the head,
+        the largest layer, then runs on one row per sequence).
+        """
         if idx.shape[1] > int(self.cfg.seq_len):
             raise ValueError(f"sequence of {idx.shape[1]} tokens exceeds seq_len {self.cfg.seq_len}")
-        return self._run(idx, 0, None)
+        return self._run(idx, 0, None, last_only)
 
     def new_cache(self, batch: int = 1, max_len: int | None = None) -> KVCache:
         device = self.pos_emb.weight.device
         return KVCache.allocate(self.cfg, batch, int(max_len or self.cfg.seq_len), device)
 
-    def prefill(self, idx: torch.Tensor, cache: KVCache) -> torch.Tensor:
-        """Logits of ``idx`` appended at the cache's current length; the cache then holds them too."""
+    def prefill(self, idx: torch.Tensor, cache: KVCache, last_only: bool = False) -> torch.Tensor:
+        """Logits of ``idx`` appended at the cache's current length (``last_only``: of its last position only).
+
+        The cache then holds the new positions too.
+        """
         if cache.length + idx.shape[1] > min(cache.max_len, int(self.cfg.seq_len)):
             raise ValueError("the cache (or seq_len) is too short for these tokens")
-        return self._run(idx, cache.length, cache)
+        return self._run(idx, cache.length, cache, last_only)
 
     def decode(self, next_ids: torch.Tensor, cache: KVCache) -> torch.Tensor:
         """Logits [b, vocab] of one new token per sequence (next_ids [b] or [b, 1])."""
@@ -401,7 +408,7 @@ class GraphDecoder:
     def prefill(self, idx: torch.Tensor) -> torch.Tensor:
         """Eager prefill of ``idx`` [batch, t] from position 0; returns the logits of its last position."""
         self.cache.length = 0
-        out = self.model.prefill(idx, self.cache)[:, -1]
+        out = self.model.prefill(idx, self.cache, last_only=True)[:, -1]
         self.length = idx.shape[1]
         self.pos.fill_(self.length)
         if self.graph is None:
@@ -522,11 +529,11 @@ def generate(model: PackedPolluxModel, ids: list[int], *, max_new_tokens: int = 
     for _ in range(max_new_tokens):
         if cache is not None and idx.shape[1] <= seq_len:
             if cache.length == 0:
-                logits = model.prefill(idx, cache)[:, -1]
+                logits = model.prefill(idx, cache, last_only=True)[:, -1]
             else:
                 logits = model.decode(idx[:, -1], cache)
         else:
-            logits = model(idx[:, -seq_len:])[:, -1]
+            logits = model(idx[:, -seq_len:], last_only=True)[:, -1]
         logits = mask_inactive_vocab(logits.float()[0], v_active)
         apply_repetition_penalty(logits, idx[0], repetition_penalty)
         if temperature > 0:

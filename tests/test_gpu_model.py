@@ -185,3 +185,17 @@ def test_graph_greedy_decode_matches_eager_argmax(dev, packed):
     print(f"[model] greedy graph tokens {got.tolist()}", flush=True)
     assert got.shape == (2, 12)
     assert torch.equal(got, want)
+
+
+def test_last_only_logits(dev, packed):
+    # the head on the last position only (INT8 GEMV) against the last row of the full logits (F.linear)
+    model = PackedPolluxModel.from_packed_checkpoint(str(packed[0]), dev)
+    idx = torch.randint(0, 90, (2, 10), generator=torch.Generator().manual_seed(6)).to(dev)
+    with torch.inference_mode():
+        full = model(idx)
+        last = model(idx, last_only=True)
+        cache = model.new_cache(2)
+        pre = model.prefill(idx, cache, last_only=True)
+    assert last.shape == (2, 1, 96) and pre.shape == (2, 1, 96)
+    assert _rel(last[:, 0], full[:, -1]) <= 1e-5
+    assert _rel(pre[:, 0], full[:, -1]) <= 1e-5
