@@ -167,10 +167,11 @@ class KVCache:
 
     @classmethod
     def allocate(cls, cfg: PolluxConfig, batch: int, max_len: int, device) -> KVCache:
+        # uninitialised: positions are only ever read after they are written (positions < length)
         shape = (batch, int(cfg.n_heads), max_len, int(cfg.d_head))
         n = int(cfg.n_layers)
-        return cls([torch.zeros(shape, device=device) for _ in range(n)],
-                   [torch.zeros(shape, device=device) for _ in range(n)])
+        return cls([torch.empty(shape, device=device) for _ in range(n)],
+                   [torch.empty(shape, device=device) for _ in range(n)])
 
     @property
     def max_len(self) -> int:
