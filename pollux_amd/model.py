@@ -270,7 +270,8 @@ class PackedPolluxModel(nn.Module):
         self.ln_f = RMSNorm(n_embd)
         self.head = PackedInt8Linear(n_embd, int(cfg.vocab_size), bias=False)
 
-    def _run(self, idx: torch.Tensor, pos0: int, cache: KVCache | None, last_only: bool = False) -> torch.Tensor:
+    def _run(self, idx: torch.Tensor, pos0: int, cache: KVCache | None, last_only: bool = False,
+             pick: torch.Tensor | None = None) -> torch.Tensor:
         t = idx.shape[1]
         pos = torch.arange(pos0, pos0 + t, device=idx.device).unsqueeze(0)
         x = self.embed(idx, pos[:, 0])
@@ -279,6 +280,8 @@ class PackedPolluxModel(nn.Module):
             x = block(x, cache, i, step_pos)
         if cache is not None:
             cache.length = pos0 + t
+        if pick is not None:  # one position given by a device index (graph-captured prefill of a padded prompt)
+            return self.logits(x.index_select(1, pick.view(1)))
         return self.logits(x[:, -1:] if last_only else x)
 
     def embed(self, idx: torch.Tensor, pos0: torch.Tensor) -> torch.Tensor:
@@ -391,6 +394,7 @@ class GraphDecoder:
         self.length = 0
         self.graph = None
         self.logits = None
+        self._prefills = {}  # padded prompt length -> (graph, ids [batch, T], last position, logits)
 
     def _step(self) -> torch.Tensor:
         m = self.model
@@ -407,14 +411,55 @@ class GraphDecoder:
 
     @torch.inference_mode()
     def prefill(self, idx: torch.Tensor) -> torch.Tensor:
-        """Eager prefill of ``idx`` [batch, t] from position 0; returns the logits of its last position."""
-        self.cache.length = 0
-        out = self.model.prefill(idx, self.cache, last_only=True)[:, -1]
-        self.length = idx.shape[1]
-        self.pos.fill_(self.length)
+        """Prefill of ``idx`` [batch, t] from position 0; returns the logits of its last position.
+
+        Replayed from a graph captured per padded length (powers of two from
+        16, at most the cache length; captured on first use): the prompt is
+        padded at its end, which causal attention makes exact -- no real
+        position sees the padding, the logits come from position t - 1, and
+        the padding's cache rows are overwritten by the decode steps before
+        they are read.
+        """
+        b, t = idx.shape
+        if b != self.ids.shape[0]:
+            raise ValueError(f"prefill of {b} sequences for a decoder of batch {self.ids.shape[0]}")
+        if not 1 <= t <= self.max_len:
+            raise ValueError(f"a prompt of {t} tokens does not fit the cache's {self.max_len} positions")
+        T = min(max(16, 1 << (t - 1).bit_length()), self.max_len)
+        entry = self._prefills.get(T)
+        if entry is None:
+            entry = self._prefills[T] = self._capture_prefill(T)
+        graph, ids, last, logits = entry
+        ids[:, :t].copy_(idx)
+        ids[:, t:].zero_()
+        last.fill_(t - 1)
+        graph.replay()
+        self.cache.length = t
+        self.length = t
+        self.pos.fill_(t)
         if self.graph is None:
             self._capture()
-        return out
+        return logits[:, 0].clone()
+
+    def _capture_prefill(self, T: int):
+        device = self.pos.device
+        ids = torch.zeros(self.ids.shape[0], T, dtype=torch.long, device=device)
+        last = torch.full((), T - 1, dtype=torch.long, device=device)
+
+        def run():
+            self.cache.length = 0
+            return self.model._run(ids, 0, self.cache, pick=last)
+
+        side = torch.cuda.Stream(device)
+        side.wait_stream(torch.cuda.current_stream(device))
+        with torch.cuda.stream(side):
+            for _ in range(2):  # warm-up: lazy casts, allocator
+                run()
+        torch.cuda.current_stream(device).wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            logits = run()
+        return graph, ids, last, logits
 
     def _capture(self) -> None:
         saved = self.length

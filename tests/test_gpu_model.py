@@ -199,3 +199,30 @@ def test_last_only_logits(dev, packed):
     assert last.shape == (2, 1, 96) and pre.shape == (2, 1, 96)
     assert _rel(last[:, 0], full[:, -1]) <= 1e-5
     assert _rel(pre[:, 0], full[:, -1]) <= 1e-5
+
+
+def test_graph_prefill_buckets_match_eager(dev, tmp_path):
+    # prompts padded to 16 / 32 / 64 positions (graphs captured per bucket), across the GEMV / GEMM
+    # switch at 16 tokens, against the eager prefill; decoding continues from the padded prefill
+    from pollux_amd.model import GraphDecoder
+
+    cfg = dict(CFG, seq_len=64)
+    state, _ = pack.pack_state_dict(_dense_state(cfg, 11), dev)
+    path = tmp_path / "s64.plx"
+    plx.write_plx(path, pack.pack_config(cfg), state)
+    model = PackedPolluxModel.from_packed_checkpoint(str(path), dev)
+    dec = GraphDecoder(model, batch=1)
+    g = torch.Generator().manual_seed(12)
+    for t in (1, 16, 17, 33, 64):
+        idx = torch.randint(0, 90, (1, t), generator=g).to(dev)
+        with torch.inference_mode():
+            got = dec.prefill(idx)
+            cache = model.new_cache(1)
+            want = model.prefill(idx, cache)[:, -1]
+            assert _rel(got, want) <= 1e-5, t
+            if t < 64:
+                nxt = torch.tensor([5], device=dev)
+                assert _rel(dec.decode(nxt), model.decode(nxt, cache)) <= 1e-5, t
+    assert sorted(dec._prefills) == [16, 32, 64]
+    with pytest.raises(ValueError):
+        dec.prefill(torch.zeros(1, 65, dtype=torch.long, device=dev))
