@@ -207,7 +207,7 @@ size_t plx_dequant_linear_workspace_bytes(int64_t rows, int64_t cols, int64_t m_
  * the fp16 weights are exact and accumulated in fp32: the numerics of
  * F.linear(x.float(), W.float()).  With PLX_DQL_W_AS_X and bf16 x the weights
  * are rounded to bf16 (RNE) first; with PLX_DQL_GELU, y = gelu(x W^T) (torch's
- * erf form).  Results are deterministic (fixed summation order).  Batches above 16 tokens run on MFMA (fp32 x split exactly into
+ * erf form).  Results are deterministic (fixed summation order).  Batches above 4 tokens run on MFMA (fp32 x split exactly into
  * three bf16 parts) and need the workspace sized by
  * plx_dequant_linear_workspace_bytes (a fragment-order copy of x, plus split
  * partial tiles for narrow layers); cols <= 2^22.
@@ -225,7 +225,7 @@ int plx_dequant_linear(const uint8_t *packed, int64_t n_packed_bytes, const uint
  * PLX_DQL_RMS_NORM (fp32 x; norm_weight fp32 [cols], 16-byte aligned)
  * x * rsqrt(mean(x^2) + norm_eps) * norm_weight per row, the block's ln1 /
  * ln2 (pollux.py:580-582); norm_weight is NULL without the flag.  Up to 16
- * targets; at m_rows <= 16 up to four of them run in one GEMV launch, which
+ * targets; at m_rows <= 4 up to four of them run in one GEMV launch, which
  * normalises x in LDS.  No counterpart in the reference's FFI (separate
  * RMSNorm and F.linear calls there); results equal plx_rms_norm followed by
  * separate plx_dequant_linear calls and the epilogue, up to the summation

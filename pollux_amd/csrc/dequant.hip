@@ -1145,7 +1145,11 @@ MmWorkspace mm_workspace(int64_t rows, int64_t cols, int64_t m, const MmPlan &pl
   return w;
 }
 
-bool uses_mfma(int /*flags*/, int64_t m) { return m > 16; }
+// GEMV up to 4 tokens, MFMA GEMM above: the GEMV streams the packed rows and
+// repeats its codebook gathers once per 4 tokens, the GEMM's cost barely
+// changes between 5 and 64 tokens (measured per call: 7680x1920 GEMV 9.6 us at
+// 4 tokens, 13.9 at 6; GEMM 13.0 at 17; 1920x7680 16.6 / 23.7 against 16.0)
+bool uses_mfma(int /*flags*/, int64_t m) { return m > 4; }
 
 }  // namespace
 
@@ -1207,7 +1211,7 @@ int launch_dequant_linear_multi(const DqlTarget *targets, int n, int64_t cols, c
                                                    ~static_cast<size_t>(255)))
                       : nullptr;
   if (uses_mfma(flags, m)) {
-    // batches above 16 tokens: MFMA dequant-GEMM in slabs of 64 tokens, one launch (+ split sum) per target
+    // batches above 4 tokens: MFMA dequant-GEMM in slabs of 64 tokens, one launch (+ split sum) per target
     if (cols > kMmMaxCols)
       return fail(PLX_EINVAL, "dequant_linear: %lld columns exceed the batched path's %lld", static_cast<long long>(cols),
                   static_cast<long long>(kMmMaxCols));

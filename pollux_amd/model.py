@@ -413,8 +413,8 @@ class GraphDecoder:
     def prefill(self, idx: torch.Tensor) -> torch.Tensor:
         """Prefill of ``idx`` [batch, t] from position 0; returns the logits of its last position.
 
-        Replayed from a graph captured per padded length (powers of two from
-        16, at most the cache length; captured on first use): the prompt is
+        Replayed from a graph captured per padded length (4, then powers of
+        two from 16, at most the cache length; captured on first use): the prompt is
         padded at its end, which causal attention makes exact -- no real
         position sees the padding, the logits come from position t - 1, and
         the padding's cache rows are overwritten by the decode steps before
@@ -425,7 +425,9 @@ class GraphDecoder:
             raise ValueError(f"prefill of {b} sequences for a decoder of batch {self.ids.shape[0]}")
         if not 1 <= t <= self.max_len:
             raise ValueError(f"a prompt of {t} tokens does not fit the cache's {self.max_len} positions")
-        T = min(max(16, 1 << (t - 1).bit_length()), self.max_len)
+        # 4, then 16, 32, 64, ...: the edge at 4 is the dequant-linear's GEMV / GEMM switch, so the real
+        # tokens take the same kernels as without padding
+        T = min(4 if t <= 4 else max(16, 1 << (t - 1).bit_length()), self.max_len)
         entry = self._prefills.get(T)
         if entry is None:
             entry = self._prefills[T] = self._capture_prefill(T)

@@ -99,7 +99,7 @@ def dequant_linear_multi(
     ``weights``: (packed, sigma16, out_features) per target; act = GELU (erf
     form, as F.gelu) when ``gelu``; ``residuals``: fp32 [..., out_i] tensors
     added after the activation (or None); ``norm``: (weight, eps) of an
-    RMSNorm applied to x first (fp32 x; n = identity when None).  At up to 16
+    RMSNorm applied to x first (fp32 x; n = identity when None).  At up to 4
     tokens, four targets share one GEMV launch, which also normalises x.
     Results equal separate dequant_linear calls followed by the same epilogue.
     """

@@ -202,8 +202,8 @@ def test_last_only_logits(dev, packed):
 
 
 def test_graph_prefill_buckets_match_eager(dev, tmp_path):
-    # prompts padded to 16 / 32 / 64 positions (graphs captured per bucket), across the GEMV / GEMM
-    # switch at 16 tokens, against the eager prefill; decoding continues from the padded prefill
+    # prompts padded to 4 / 16 / 32 / 64 positions (graphs captured per bucket), on both sides of the
+    # GEMV / GEMM switch at 4 tokens, against the eager prefill; decoding continues from the padded prefill
     from pollux_amd.model import GraphDecoder
 
     cfg = dict(CFG, seq_len=64)
@@ -213,7 +213,7 @@ def test_graph_prefill_buckets_match_eager(dev, tmp_path):
     model = PackedPolluxModel.from_packed_checkpoint(str(path), dev)
     dec = GraphDecoder(model, batch=1)
     g = torch.Generator().manual_seed(12)
-    for t in (1, 16, 17, 33, 64):
+    for t in (1, 4, 5, 16, 17, 33, 64):
         idx = torch.randint(0, 90, (1, t), generator=g).to(dev)
         with torch.inference_mode():
             got = dec.prefill(idx)
@@ -223,6 +223,6 @@ def test_graph_prefill_buckets_match_eager(dev, tmp_path):
             if t < 64:
                 nxt = torch.tensor([5], device=dev)
                 assert _rel(dec.decode(nxt), model.decode(nxt, cache)) <= 1e-5, t
-    assert sorted(dec._prefills) == [16, 32, 64]
+    assert sorted(dec._prefills) == [4, 16, 32, 64]
     with pytest.raises(ValueError):
         dec.prefill(torch.zeros(1, 65, dtype=torch.long, device=dev))
