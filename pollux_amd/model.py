@@ -557,7 +557,8 @@ def apply_top_p(logits: torch.Tensor, p: float) -> torch.Tensor:
 @torch.inference_mode()
 def generate(model: PackedPolluxModel, ids: list[int], *, max_new_tokens: int = 80, temperature: float = 0.6,
              top_k: int = 50, top_p: float = 0.9, repetition_penalty: float = 1.1, active_vocab: int | None = None,
-             eos_id: int = 50256, generator: torch.Generator | None = None, use_cache: bool = True) -> list[int]:
+             eos_id: int = 50256, generator: torch.Generator | None = None, use_cache: bool = True,
+             use_graph: bool = False) -> list[int]:
     """The token loop of generate.generate (generate.py:286-336) on token ids.
 
     Sampling follows the reference step for step (vocabulary mask, repetition
@@ -566,16 +567,24 @@ def generate(model: PackedPolluxModel, ids: list[int], *, max_new_tokens: int = 
     once the sequence is longer than seq_len the reference's window
     ``idx[:, -seq_len:]`` restarts the positions at 0, so from then on every
     step recomputes the window, exactly as the reference does.
+    ``use_graph`` (with ``use_cache``): the prefill and the decode steps are
+    replayed from a ``GraphDecoder``'s graphs (captured once per call, worth it
+    for long generations); the sampling stays on the host's stream.
     """
     device = model.pos_emb.weight.device
     seq_len = int(model.cfg.seq_len)
     v_active = active_vocab or eos_id + 1
     ids = [t for t in ids if 0 <= t < v_active] or [eos_id]
     idx = torch.tensor([ids], device=device, dtype=torch.long)
-    cache = model.new_cache(1, seq_len) if use_cache else None
+    dec = GraphDecoder(model, batch=1) if (use_cache and use_graph) else None
+    cache = model.new_cache(1, seq_len) if (use_cache and dec is None) else None
+    started = False
     logits = None
     for _ in range(max_new_tokens):
-        if cache is not None and idx.shape[1] <= seq_len:
+        if dec is not None and idx.shape[1] <= seq_len:
+            logits = dec.decode(idx[:, -1]) if started else dec.prefill(idx)
+            started = True
+        elif cache is not None and idx.shape[1] <= seq_len:
             if cache.length == 0:
                 logits = model.prefill(idx, cache, last_only=True)[:, -1]
             else:

@@ -117,12 +117,13 @@ def test_generate_with_and_without_cache(dev, packed, top_k, temperature):
     model = PackedPolluxModel.from_packed_checkpoint(str(packed[0]), dev)
     prompt = [3, 14, 15, 9, 26]
     runs = []
-    for use_cache in (True, False):
+    for use_cache, use_graph in ((True, False), (False, False), (True, True)):
         g = torch.Generator(device=dev).manual_seed(7)
         runs.append(generate(model, prompt, max_new_tokens=20, top_k=top_k, temperature=temperature, top_p=0.95,
-                             repetition_penalty=1.1, active_vocab=90, eos_id=89, generator=g, use_cache=use_cache))
+                             repetition_penalty=1.1, active_vocab=90, eos_id=89, generator=g, use_cache=use_cache,
+                             use_graph=use_graph))
     print(f"[model] generated {runs[0]}", flush=True)
-    assert runs[0] == runs[1]
+    assert runs[0] == runs[1] == runs[2]
     assert runs[0][:5] == prompt and len(runs[0]) > 16  # went past seq_len unless eos came first
 
 
