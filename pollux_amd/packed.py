@@ -163,6 +163,30 @@ def dequant_linear_multi(
     return [y.reshape(*lead, y.shape[1]) for y in ys]
 
 
+# fused packed streams of layer groups (q/k/v), keyed by the layers' identities and buffer addresses
+_FUSED: dict = {}
+
+
+def _fused_group(layers: list) -> tuple[torch.Tensor, torch.Tensor, int, list[int]]:
+    """(packed, sigma16, rows, row offsets) of ``layers`` stacked along their output rows.
+
+    Valid when every layer holds a whole number of 9-byte groups (rows * in_features / 24 % 4 == 0):
+    the streams then concatenate byte for byte.  Rebuilt when a layer's buffers change.
+    """
+    key = tuple((id(l), l.packed_weights.data_ptr(), l.sigma_rows.data_ptr()) for l in layers)
+    hit = _FUSED.get(key)
+    if hit is None:
+        if len(_FUSED) > 256:
+            _FUSED.clear()
+        offs, r = [], 0
+        for l in layers:
+            offs.append(r)
+            r += l.out_features
+        hit = _FUSED[key] = (torch.cat([l.packed_weights.reshape(-1) for l in layers]),
+                             torch.cat([l.sigma_rows.reshape(-1) for l in layers]), r, offs)
+    return hit
+
+
 def packed_linear_group(layers: list, x: torch.Tensor, *, residuals: list | None = None,
                         gelu: bool = False, norm: tuple[torch.Tensor, float] | None = None) -> list[torch.Tensor]:
     """[residual +] act(layer(n(x))) for PackedH24Linear layers sharing x, fused when they are all packed.
@@ -174,6 +198,16 @@ def packed_linear_group(layers: list, x: torch.Tensor, *, residuals: list | None
     """
     residuals = residuals or [None] * len(layers)
     if all(isinstance(l, PackedH24Linear) and not l._materialized and l.bias is None for l in layers):
+        in_f = layers[0].in_features
+        if (len(layers) > 1 and x.numel() // max(in_f, 1) > 4 and all(r is None for r in residuals)
+                and all(l.in_features == in_f and (l.out_features * in_f // 24) % 4 == 0 for l in layers)
+                and len({l.weight_rounding for l in layers}) == 1):
+            # above 4 tokens the weights run as separate GEMM launches: one stacked weight takes one
+            packed, sigma, rows, offs = _fused_group(layers)
+            (y,) = dequant_linear_multi([(packed, sigma, rows)], in_f, x, gelu=gelu,
+                                        weight_rounding=layers[0].weight_rounding, norm=norm)
+            y = y.to(x.dtype)
+            return [y[..., o:o + l.out_features] for l, o in zip(layers, offs)]
         ys = dequant_linear_multi([(l.packed_weights, l.sigma_rows, l.out_features) for l in layers],
                                   layers[0].in_features, x, residuals=residuals, gelu=gelu,
                                   weight_rounding=layers[0].weight_rounding, norm=norm)

@@ -270,3 +270,32 @@ def test_rms_norm_flag_and_weight_go_together(dev):
     assert lib.plx_dequant_linear_multi(arr, 1, 48, xb.data_ptr(), DQL_RMS_NORM, 2, w.data_ptr(), 1e-8, None, 0, s) != 0
     torch.cuda.synchronize()
     assert torch.equal(y, torch.zeros(2, 48, device=dev))
+
+
+@pytest.mark.parametrize("m", [3, 8, 40])
+def test_packed_linear_group_stacked_qkv(dev, m):
+    # above 4 tokens q / k / v run as one stacked weight (one GEMM launch); at or below, as one GEMV launch
+    from pollux_amd.packed import _FUSED, PackedH24Linear, packed_linear_group
+
+    in_f = 1920
+    layers = []
+    for i in range(3):
+        idx, sig, packed, g = _layer(1920, in_f, 500 + i)
+        lyr = PackedH24Linear(in_f, 1920).to(dev)
+        lyr.packed_weights.copy_(packed.to(dev))
+        lyr.sigma_rows.copy_(sig.to(dev))
+        layers.append(lyr)
+    x = torch.randn(2, (m + 1) // 2, in_f, generator=torch.Generator().manual_seed(m)).to(dev)
+    nw = (1.0 + 0.1 * torch.randn(in_f, generator=torch.Generator().manual_seed(m + 1))).to(dev)
+    with torch.inference_mode():
+        got = packed_linear_group(layers, x, norm=(nw, 1e-8))
+        sep = [packed_linear_group([l], x, norm=(nw, 1e-8))[0] for l in layers]
+        again = packed_linear_group(layers, x, norm=(nw, 1e-8))
+    for a, b, c in zip(got, sep, again):
+        assert a.shape == b.shape == (2, (m + 1) // 2, 1920)
+        rel = ((a - b).double().norm() / b.double().norm()).item()
+        assert rel <= 1e-6, rel
+        assert torch.equal(a, c)
+    stacked = x.shape[0] * x.shape[1] > 4
+    key = tuple((id(l), l.packed_weights.data_ptr(), l.sigma_rows.data_ptr()) for l in layers)
+    assert (key in _FUSED) == stacked
