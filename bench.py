@@ -481,10 +481,22 @@ def decode_extras(device, prompt_len=64, new_tokens=128):
         dense = PackedPolluxModel.from_packed_checkpoint(payload, device, materialize=True)
         t_dense = timed(lambda n: [dense(seq)[:, -1].argmax(-1) for _ in range(n)], 4)
         del dense
+        # last: the batch-16 decoder's cache (4.5 GB) and graph pools stay with the allocator afterwards
+        prompts16 = torch.randint(0, 50257, (16, prompt_len), generator=g, device=device)
+        bdec = GraphDecoder(model, batch=16, greedy=True)
+        b_first = bdec.prefill(prompts16).argmax(-1)
+        bdec.decode_greedy(b_first, 4)
+        bdec.prefill(prompts16)
+        t_batch16 = timed(lambda n: bdec.decode_greedy(b_first, n), new_tokens)
+        del bdec
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
     out["graph_cached_tokens_per_s"] = 1.0 / t_graph
     out["graph_cached_ms_per_token"] = t_graph * 1e3
     out["graph_greedy_tokens_per_s"] = 1.0 / t_greedy
     out["graph_greedy_ms_per_token"] = t_greedy * 1e3
+    out["graph_greedy_batch16_tokens_per_s"] = 16.0 / t_batch16
+    out["graph_greedy_batch16_ms_per_step"] = t_batch16 * 1e3
     out["eager_cached_tokens_per_s"] = 1.0 / t_eager
     out["prefill_graph_ms"] = t_prefill_graph * 1e3
     out["prefill_eager_ms"] = t_prefill * 1e3
@@ -492,7 +504,8 @@ def decode_extras(device, prompt_len=64, new_tokens=128):
     out["recompute_reference_dense_tokens_per_s"] = 1.0 / t_dense
     out["note"] = (f"batch 1, prompt {prompt_len} tokens, {new_tokens} greedy tokens (graph: one replay per token, "
                    f"torch argmax on the host's stream between replays; graph_greedy: the argmax and the token "
-                   f"feedback inside the captured step, no host work per token); prefill: the prompt into the "
+                   f"feedback inside the captured step, no host work per token; batch16: 16 sequences per "
+                   f"step); prefill: the prompt into the "
                    f"cache with the last position's logits (time to first token), replayed from GraphDecoder's "
                    f"graph for the padded length or run eagerly into a new cache; recompute rows at a "
                    f"{prompt_len + 1}-token prefix; random packed weights (valid indices), fp32 activations")
