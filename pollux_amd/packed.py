@@ -163,28 +163,29 @@ def dequant_linear_multi(
     return [y.reshape(*lead, y.shape[1]) for y in ys]
 
 
-# fused packed streams of layer groups (q/k/v), keyed by the layers' identities and buffer addresses
-_FUSED: dict = {}
-
-
 def _fused_group(layers: list) -> tuple[torch.Tensor, torch.Tensor, int, list[int]]:
     """(packed, sigma16, rows, row offsets) of ``layers`` stacked along their output rows.
 
     Valid when every layer holds a whole number of 9-byte groups (rows * in_features / 24 % 4 == 0):
-    the streams then concatenate byte for byte.  Rebuilt when a layer's buffers change.
+    the streams then concatenate byte for byte.  Kept on the first layer; rebuilt when any layer's
+    buffers are replaced (the entry holds the tensors themselves, compared by identity) or
+    modified in place (their version counters; tensors created under ``torch.inference_mode``
+    keep none, so an in-place write to those is not seen: replace such buffers instead).
     """
-    key = tuple((id(l), l.packed_weights.data_ptr(), l.sigma_rows.data_ptr()) for l in layers)
-    hit = _FUSED.get(key)
-    if hit is None:
-        if len(_FUSED) > 256:
-            _FUSED.clear()
-        offs, r = [], 0
-        for l in layers:
-            offs.append(r)
-            r += l.out_features
-        hit = _FUSED[key] = (torch.cat([l.packed_weights.reshape(-1) for l in layers]),
-                             torch.cat([l.sigma_rows.reshape(-1) for l in layers]), r, offs)
-    return hit
+    bufs = tuple(t for l in layers for t in (l.packed_weights, l.sigma_rows))
+    versions = tuple(None if t.is_inference() else t._version for t in bufs)
+    hit = layers[0].__dict__.get("_stacked")
+    if hit is not None and len(hit[0]) == len(bufs) and all(a is b for a, b in zip(hit[0], bufs)) \
+            and hit[1] == versions:
+        return hit[2]
+    offs, r = [], 0
+    for l in layers:
+        offs.append(r)
+        r += l.out_features
+    fused = (torch.cat([l.packed_weights.reshape(-1) for l in layers]),
+             torch.cat([l.sigma_rows.reshape(-1) for l in layers]), r, offs)
+    layers[0].__dict__["_stacked"] = (bufs, versions, fused)
+    return fused
 
 
 def packed_linear_group(layers: list, x: torch.Tensor, *, residuals: list | None = None,

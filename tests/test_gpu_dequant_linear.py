@@ -275,7 +275,7 @@ def test_rms_norm_flag_and_weight_go_together(dev):
 @pytest.mark.parametrize("m", [3, 8, 40])
 def test_packed_linear_group_stacked_qkv(dev, m):
     # above 4 tokens q / k / v run as one stacked weight (one GEMM launch); at or below, as one GEMV launch
-    from pollux_amd.packed import _FUSED, PackedH24Linear, packed_linear_group
+    from pollux_amd.packed import PackedH24Linear, packed_linear_group
 
     in_f = 1920
     layers = []
@@ -297,5 +297,13 @@ def test_packed_linear_group_stacked_qkv(dev, m):
         assert rel <= 1e-6, rel
         assert torch.equal(a, c)
     stacked = x.shape[0] * x.shape[1] > 4
-    key = tuple((id(l), l.packed_weights.data_ptr(), l.sigma_rows.data_ptr()) for l in layers)
-    assert (key in _FUSED) == stacked
+    assert ("_stacked" in layers[0].__dict__) == stacked
+    if stacked:
+        # an in-place update of one layer's weights rebuilds the stacked copy
+        idx, sig, packed, _ = _layer(1920, in_f, 777)
+        with torch.inference_mode():
+            layers[1].packed_weights.copy_(packed.to(dev))
+            layers[1].sigma_rows.copy_(sig.to(dev))
+            new = packed_linear_group(layers, x, norm=(nw, 1e-8))[1]
+            want = packed_linear_group([layers[1]], x, norm=(nw, 1e-8))[0]
+        assert ((new - want).double().norm() / want.double().norm()).item() <= 1e-6

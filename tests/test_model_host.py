@@ -64,3 +64,22 @@ def test_sampling_helpers_hand_computed():
     assert z.tolist() == [1.0, -4.0, 1.0]
     m = mask_inactive_vocab(torch.zeros(5), 3)
     assert m.tolist() == [0.0, 0.0, 0.0, -math.inf, -math.inf]
+
+
+def test_stacked_qkv_cache_follows_the_layers_buffers():
+    """The stacked q/k/v copy is rebuilt when a layer's buffer is replaced or written in place."""
+    from pollux_amd.packed import PackedH24Linear, _fused_group
+
+    layers = [PackedH24Linear(48, 24), PackedH24Linear(48, 48)]
+    for i, l in enumerate(layers):
+        l.packed_weights.copy_(torch.randint(0, 256, l.packed_weights.shape, dtype=torch.uint8))
+        l.sigma_rows.fill_(i + 1)
+    a = _fused_group(layers)
+    assert _fused_group(layers) is a and (a[2], a[3]) == (72, [0, 24])
+    assert a[0].equal(torch.cat([l.packed_weights.reshape(-1) for l in layers]))
+    layers[1].packed_weights.add_(1)                                   # in place
+    b = _fused_group(layers)
+    assert b is not a and b[0][layers[0].packed_weights.numel():].equal(layers[1].packed_weights.reshape(-1))
+    layers[1].sigma_rows = torch.full_like(layers[1].sigma_rows, 7)    # replaced
+    c = _fused_group(layers)
+    assert c is not b and (c[1][24:] == 7).all() and (c[1][:24] == 1).all()
