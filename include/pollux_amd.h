@@ -295,6 +295,23 @@ int plx_dequant_int8_rows(const int8_t *q, const uint16_t *mu16, int64_t rows, i
 int plx_int8_linear(const int8_t *q, const uint16_t *mu16, int64_t rows, int64_t cols, const float *x,
                     int64_t m_rows, const float *norm_weight, float norm_eps, float *y, void *stream);
 
+/* plx_int8_linear with greedy decoding's token choice fused in: y as above,
+ * then ids[t] = the index of the maximum of y[t, :] (int64 [m_rows]) by
+ * torch.argmax's rule (the first index among equal maxima; a NaN counts as
+ * the maximum) -- generate.py:313-320 with top_k = 1 after the head
+ * (pollux.py:699-702).  With pos (device int64): history[t, *pos + 1] = ids[t]
+ * (int64 [m_rows, hist_len], written when *pos + 1 lies in [0, hist_len);
+ * history may be null), then *pos += 1 -- the token record and position
+ * advance of a greedy decode step.  Each block of the GEMV keeps its best
+ * (value, index) per token in the workspace (the size below, 8-byte
+ * aligned; nothing needs clearing) and one more block picks the winner: two
+ * launches instead of the GEMV, an argmax and the bookkeeping. */
+size_t plx_int8_linear_argmax_workspace_bytes(int64_t rows, int64_t m_rows);
+int plx_int8_linear_argmax(const int8_t *q, const uint16_t *mu16, int64_t rows, int64_t cols, const float *x,
+                           int64_t m_rows, const float *norm_weight, float norm_eps, float *y, int64_t *ids,
+                           int64_t *history, int64_t hist_len, int64_t *pos, void *workspace, size_t workspace_bytes,
+                           void *stream);
+
 /* out[b, i, :] = fp32(w16[ids[b, i], :]) + pos_weight[*pos0 + i, :] for b < batch,
  * i < t (fp32 out [batch, t, cols]): PackedInt8Embedding.forward plus the
  * position embedding (pollux.py:532-533, 691-693) in one kernel.  pos_weight

@@ -49,6 +49,9 @@ SIGNATURES = {
     "plx_dequant_linear_multi_workspace_bytes": (_sz, [_vp, _int, _i64, _i64, _int]),
     "plx_dequant_linear_multi": (_int, [_vp, _int, _i64, _vp, _int, _i64, _vp, ctypes.c_float, _vp, _sz, _vp]),
     "plx_int8_linear": (_int, [_vp, _vp, _i64, _i64, _vp, _i64, _vp, ctypes.c_float, _vp, _vp]),
+    "plx_int8_linear_argmax_workspace_bytes": (ctypes.c_size_t, [_i64, _i64]),
+    "plx_int8_linear_argmax": (_int, [_vp, _vp, _i64, _i64, _vp, _i64, _vp, ctypes.c_float, _vp, _vp, _vp, _i64,
+                                      _vp, _vp, ctypes.c_size_t, _vp]),
     "plx_int8_embed": (_int, [_vp, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _vp, _vp, _vp]),
     "plx_argmax_rows": (_int, [_vp, _i64, _i64, _vp, _vp]),
     "plx_rms_norm": (_int, [_vp, _vp, _vp, _i64, _i64, ctypes.c_float, _vp]),

@@ -337,7 +337,26 @@ int plx_int8_linear(const int8_t *q, const uint16_t *mu16, int64_t rows, int64_t
               static_cast<long long>(rows), static_cast<long long>(cols), static_cast<long long>(m_rows));
   if (rows == 0 || m_rows == 0) return PLX_OK;
   PLX_REQUIRE(q != nullptr && mu16 != nullptr && x != nullptr && y != nullptr, "plx_int8_linear: null pointer");
-  return launch_int8_linear(q, mu16, rows, cols, x, m_rows, norm_weight, norm_eps, y, as_stream(stream));
+  return launch_int8_linear(q, mu16, rows, cols, x, m_rows, norm_weight, norm_eps, y, nullptr, as_stream(stream));
+}
+
+size_t plx_int8_linear_argmax_workspace_bytes(int64_t rows, int64_t m_rows) {
+  return int8_linear_argmax_workspace_bytes(rows, m_rows);
+}
+
+int plx_int8_linear_argmax(const int8_t *q, const uint16_t *mu16, int64_t rows, int64_t cols, const float *x,
+                           int64_t m_rows, const float *norm_weight, float norm_eps, float *y, int64_t *ids,
+                           int64_t *history, int64_t hist_len, int64_t *pos, void *workspace, size_t workspace_bytes,
+                           void *stream) {
+  PLX_REQUIRE(rows > 0 && cols > 0 && m_rows >= 0 && hist_len >= 0,
+              "plx_int8_linear_argmax: bad shape (%lld, %lld) x %lld tokens", static_cast<long long>(rows),
+              static_cast<long long>(cols), static_cast<long long>(m_rows));
+  if (m_rows == 0) return PLX_OK;
+  PLX_REQUIRE(q != nullptr && mu16 != nullptr && x != nullptr && y != nullptr && ids != nullptr,
+              "plx_int8_linear_argmax: null pointer");
+  PLX_REQUIRE(history == nullptr || pos != nullptr, "plx_int8_linear_argmax: a history needs the position");
+  return launch_int8_linear_argmax(q, mu16, rows, cols, x, m_rows, norm_weight, norm_eps, y, ids, history, hist_len,
+                                   pos, workspace, workspace_bytes, as_stream(stream));
 }
 
 int plx_int8_embed(const int8_t *q, const uint16_t *mu16, int64_t vocab, int64_t cols, const int64_t *ids,

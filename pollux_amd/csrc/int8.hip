@@ -30,6 +30,7 @@
 //   691-693), p0 read from device memory (a captured graph replays it while
 //   the position advances); an id or position out of range yields a NaN row.
 
+#include <algorithm>
 #include <hip/hip_fp16.h>
 
 #include "plx_device.h"
@@ -122,18 +123,41 @@ __device__ __forceinline__ void int8x4_weights(uint32_t d, __half2 s2, __half2 &
   hi = __hmul2(__hsub2(*reinterpret_cast<const __half2 *>(&b), off), s2);
 }
 
-template <int CPL, int MB, bool NORM>
+// The argmax key of value v at index i: unsigned order of the keys is
+// torch.argmax's order (a NaN above every number, +0 and -0 equal, the lower
+// index winning among equal values): the value's bits made monotone in the
+// high word (NaNs as one positive quiet NaN, -0 as +0), ~i in the low word.
+// No key is 0.
+__device__ __forceinline__ uint64_t arg_key(float v, uint32_t i) {
+  uint32_t b = __float_as_uint(v);
+  b = v != v ? 0x7FC00000u : v == 0.0f ? 0u : b;
+  b ^= (b & 0x80000000u) ? 0xFFFFFFFFu : 0x80000000u;
+  return (static_cast<uint64_t>(b) << 32) | static_cast<uint64_t>(~i);
+}
+
+__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
+  const uint32_t lo = __shfl_xor(static_cast<uint32_t>(v), m, 64);
+  const uint32_t hi = __shfl_xor(static_cast<uint32_t>(v >> 32), m, 64);
+  return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+
+// ARG: also the block's largest arg_key per token into keys[m, gridDim.x]
+// (every wave then runs the token loop, the ones past the rows with no rows,
+// for the block barrier each token group ends with).
+template <int CPL, int MB, bool NORM, bool ARG>
 __global__ __launch_bounds__(64 * kLinWaves) void int8_linear_kernel(
     const int8_t *__restrict__ q, const uint16_t *__restrict__ mu16, int64_t rows, int cols,
     const float *__restrict__ x, int64_t m_total, const float *__restrict__ norm_w, float eps, int rows_per_wave,
-    float *__restrict__ y) {
+    float *__restrict__ y, uint64_t *__restrict__ keys) {
   const int lane = threadIdx.x & 63;
   const int64_t wave = static_cast<int64_t>(blockIdx.x) * kLinWaves + (threadIdx.x >> 6);
   const int64_t r_begin = wave * rows_per_wave;
-  if (r_begin >= rows) return;  // the whole wave (no block barriers here)
+  if (!ARG && r_begin >= rows) return;  // the whole wave (no block barriers without ARG)
   const int64_t r_end = min(rows, r_begin + rows_per_wave);
   const int nch = cols >> 4;
+  __shared__ uint64_t best[2][kLinWaves][MB];
   for (int64_t m0 = 0; m0 < m_total; m0 += MB) {
+    uint64_t kb = 0;  // ARG: this lane's best key, token m0 + lane % MB (lanes < 4 * MB)
     const int mb_here = static_cast<int>(min(static_cast<int64_t>(MB), m_total - m0));
     // Every load below comes from a clamped address with no branch around it
     // (a load under a divergent branch is waited for at once when the other
@@ -234,9 +258,79 @@ __global__ __launch_bounds__(64 * kLinWaves) void int8_linear_kernel(
       for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb)
-          if (lane == i * MB + mb && r0 + i < r_end && mb < mb_here) y[(m0 + mb) * rows + r0 + i] = flat[i * MB + mb];
+          if (lane == i * MB + mb && r0 + i < r_end && mb < mb_here) {
+            y[(m0 + mb) * rows + r0 + i] = flat[i * MB + mb];
+            if constexpr (ARG) {
+              const uint64_t k = arg_key(flat[i * MB + mb], static_cast<uint32_t>(r0 + i));
+              kb = k > kb ? k : kb;
+            }
+          }
+    }
+    if constexpr (ARG) {
+      // lanes mb, MB + mb, 2 MB + mb, 3 MB + mb hold token mb's keys
+      uint64_t o = shfl_xor_u64(kb, MB);
+      kb = o > kb ? o : kb;
+      o = shfl_xor_u64(kb, 2 * MB);
+      kb = o > kb ? o : kb;
+      const int par = static_cast<int>((m0 / MB) & 1);  // a buffer per parity: one barrier per token group
+      if (lane < MB) best[par][threadIdx.x >> 6][lane] = kb;
+      __syncthreads();
+      if (threadIdx.x < MB && static_cast<int>(threadIdx.x) < mb_here) {
+        uint64_t b = best[par][0][threadIdx.x];
+#pragma unroll
+        for (int w = 1; w < kLinWaves; ++w) b = best[par][w][threadIdx.x] > b ? best[par][w][threadIdx.x] : b;
+        keys[(m0 + threadIdx.x) * gridDim.x + blockIdx.x] = b;
+      }
     }
   }
+}
+
+constexpr int kPickThreads = 1024;
+constexpr int kPickRegs = 8;  // keys in flight per lane and round
+
+// The argmax of each token from the int8_linear_kernel blocks' keys
+// [m, parts], in one block: R = min(16, pow2 >= m) tokens at a time, 16 / R
+// waves per token.  ids[t] = the winning index; with pos, history[t, *pos + 1]
+// = ids[t] (when inside [0, hist_len)) and then *pos += 1.
+__global__ __launch_bounds__(kPickThreads) void argmax_pick_kernel(const uint64_t *__restrict__ keys, int parts,
+                                                                   int64_t m, int rsh, int64_t *__restrict__ ids,
+                                                                   int64_t *__restrict__ history, int64_t hist_len,
+                                                                   int64_t *__restrict__ pos) {
+  __shared__ uint64_t wbest[kPickThreads / 64];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int R = 1 << rsh, G = (kPickThreads / 64) >> rsh;  // tokens at a time, waves per token
+  const int slot = wave / G, gw = wave % G;
+  const int64_t p0 = pos ? pos[0] : 0;
+  for (int64_t base = 0; base < m; base += R) {
+    const int64_t t = base + slot;
+    const uint64_t *kt = keys + (t < m ? t : 0) * parts;
+    uint64_t kb = 0;
+    for (int p = gw * 64 + lane; p < parts; p += G * 64 * kPickRegs) {
+      uint64_t v[kPickRegs];
+#pragma unroll
+      for (int k = 0; k < kPickRegs; ++k) {
+        const int pk = p + k * G * 64;
+        v[k] = kt[pk < parts ? pk : 0];  // clamped: every load unconditional
+      }
+#pragma unroll
+      for (int k = 0; k < kPickRegs; ++k) kb = v[k] > kb ? v[k] : kb;
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+      const uint64_t o = shfl_xor_u64(kb, off);
+      kb = o > kb ? o : kb;
+    }
+    if (lane == 0) wbest[wave] = kb;
+    __syncthreads();
+    if (gw == 0 && lane == 0 && t < m) {
+      for (int w = 1; w < G; ++w) kb = wbest[wave + w] > kb ? wbest[wave + w] : kb;
+      const int64_t id = static_cast<int64_t>(~static_cast<uint32_t>(kb));
+      ids[t] = id;
+      if (pos && history && p0 + 1 >= 0 && p0 + 1 < hist_len) history[t * hist_len + p0 + 1] = id;
+    }
+    __syncthreads();
+  }
+  if (pos && tid == 0) pos[0] = p0 + 1;
 }
 
 // one wave per token; cols % 4 == 0, q rows 4-byte aligned, pos_w / out 16-byte aligned
@@ -307,31 +401,46 @@ int launch_int8_dequant(const int8_t *q, const uint16_t *mu16, int64_t rows, int
   return check_launch("int8_dequant_kernel");
 }
 
+int int8_linear_blocks(int64_t rows, int64_t *rows_per_wave) {
+  // about 8 waves of 4-row groups per SIMD over the chip (1,024 SIMDs)
+  int64_t rpw = (rows + 8 * 1024 - 1) / (8 * 1024);
+  rpw = rpw < 4 ? 4 : (rpw + 3) / 4 * 4;
+  if (rows_per_wave) *rows_per_wave = rpw;
+  const int64_t waves = (rows + rpw - 1) / rpw;
+  return static_cast<int>(std::min<int64_t>((waves + kLinWaves - 1) / kLinWaves, 0x7FFFFFFFll));
+}
+
 int launch_int8_linear(const int8_t *q, const uint16_t *mu16, int64_t rows, int64_t cols, const float *x, int64_t m,
-                       const float *norm_w, float eps, float *y, hipStream_t s) {
+                       const float *norm_w, float eps, float *y, uint64_t *keys, hipStream_t s) {
   if (rows == 0 || m == 0) return PLX_OK;
   if (cols <= 0 || cols % 16 != 0 || cols > 64 * 16 * 4)
     return fail(PLX_EINVAL, "int8_linear: %lld columns (a multiple of 16 up to 4,096)", static_cast<long long>(cols));
   const uintptr_t al = reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(x) |
                        reinterpret_cast<uintptr_t>(norm_w);
   if ((al & 15u) != 0) return fail(PLX_EINVAL, "int8_linear: q, x and the norm weight must be 16-byte aligned");
-  // about 8 waves of 4-row groups per SIMD over the chip (1,024 SIMDs)
-  int64_t rpw = (rows + 8 * 1024 - 1) / (8 * 1024);
-  rpw = rpw < 4 ? 4 : (rpw + 3) / 4 * 4;
-  const int64_t waves = (rows + rpw - 1) / rpw;
-  const int64_t blocks = (waves + kLinWaves - 1) / kLinWaves;
-  if (blocks > 0x7FFFFFFFll) return fail(PLX_EINVAL, "int8_linear: too many rows");
+  if (rows > 0x7FFFFFFFll) return fail(PLX_EINVAL, "int8_linear: too many rows");
+  int64_t rpw = 0;
+  const int blocks = int8_linear_blocks(rows, &rpw);
   const int cpl = static_cast<int>((cols / 16 + 63) / 64);
   const int mb = m >= 4 ? 4 : m >= 2 ? 2 : 1;
   const dim3 g(static_cast<unsigned>(blocks)), b(64 * kLinWaves);
   const int ci = static_cast<int>(cols);
   const int ri = static_cast<int>(rpw);
-#define PLX_I8L(CPL, MB)                                                                                         \
-  do {                                                                                                           \
-    if (norm_w)                                                                                                  \
-      hipLaunchKernelGGL((int8_linear_kernel<CPL, MB, true>), g, b, 0, s, q, mu16, rows, ci, x, m, norm_w, eps, ri, y); \
-    else                                                                                                         \
-      hipLaunchKernelGGL((int8_linear_kernel<CPL, MB, false>), g, b, 0, s, q, mu16, rows, ci, x, m, norm_w, eps, ri, y); \
+#define PLX_I8L_K(CPL, MB, NORM)                                                                                \
+  do {                                                                                                          \
+    if (keys)                                                                                                   \
+      hipLaunchKernelGGL((int8_linear_kernel<CPL, MB, NORM, true>), g, b, 0, s, q, mu16, rows, ci, x, m, norm_w, \
+                         eps, ri, y, keys);                                                                     \
+    else                                                                                                        \
+      hipLaunchKernelGGL((int8_linear_kernel<CPL, MB, NORM, false>), g, b, 0, s, q, mu16, rows, ci, x, m, norm_w, \
+                         eps, ri, y, keys);                                                                     \
+  } while (0)
+#define PLX_I8L(CPL, MB)        \
+  do {                          \
+    if (norm_w)                 \
+      PLX_I8L_K(CPL, MB, true); \
+    else                        \
+      PLX_I8L_K(CPL, MB, false); \
   } while (0)
 #define PLX_I8L_MB(CPL)  \
   do {                   \
@@ -350,7 +459,32 @@ int launch_int8_linear(const int8_t *q, const uint16_t *mu16, int64_t rows, int6
     PLX_I8L_MB(4);
 #undef PLX_I8L_MB
 #undef PLX_I8L
+#undef PLX_I8L_K
   return check_launch("int8_linear_kernel");
+}
+
+int launch_int8_linear_argmax(const int8_t *q, const uint16_t *mu16, int64_t rows, int64_t cols, const float *x,
+                              int64_t m, const float *norm_w, float eps, float *y, int64_t *ids, int64_t *history,
+                              int64_t hist_len, int64_t *pos, void *workspace, size_t workspace_bytes, hipStream_t s) {
+  if (m == 0) return PLX_OK;
+  if (rows <= 0 || rows > 0x7FFFFFFFll) return fail(PLX_EINVAL, "int8_linear_argmax: %lld rows", static_cast<long long>(rows));
+  const int parts = int8_linear_blocks(rows, nullptr);
+  const size_t need = static_cast<size_t>(m) * static_cast<size_t>(parts) * sizeof(uint64_t);
+  if (workspace == nullptr || workspace_bytes < need || (reinterpret_cast<uintptr_t>(workspace) & 7u) != 0)
+    return fail(PLX_EINVAL, "int8_linear_argmax: workspace of %zu bytes (8-byte aligned) needed", need);
+  uint64_t *keys = static_cast<uint64_t *>(workspace);
+  const int st = launch_int8_linear(q, mu16, rows, cols, x, m, norm_w, eps, y, keys, s);
+  if (st != PLX_OK) return st;
+  int rsh = 0;
+  while ((int64_t{1} << rsh) < m && rsh < 4) ++rsh;
+  hipLaunchKernelGGL(argmax_pick_kernel, dim3(1), dim3(kPickThreads), 0, s, keys, parts, m, rsh, ids, history,
+                     hist_len, pos);
+  return check_launch("argmax_pick_kernel");
+}
+
+size_t int8_linear_argmax_workspace_bytes(int64_t rows, int64_t m) {
+  if (rows <= 0 || m <= 0 || rows > 0x7FFFFFFFll) return 0;
+  return static_cast<size_t>(m) * static_cast<size_t>(int8_linear_blocks(rows, nullptr)) * sizeof(uint64_t);
 }
 
 int launch_int8_embed(const int8_t *q, const uint16_t *mu16, int64_t vocab, int64_t cols, const int64_t *idx,

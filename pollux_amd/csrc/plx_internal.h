@@ -82,7 +82,11 @@ int launch_gather(const int32_t *idx, int64_t n, int out_dtype, void *out, hipSt
 int launch_dequant_f16(const uint8_t *packed, const uint16_t *sigma16, int64_t rows, int64_t cols,
                        uint16_t *w16, hipStream_t s);
 int launch_int8_linear(const int8_t *q, const uint16_t *mu16, int64_t rows, int64_t cols, const float *x, int64_t m,
-                       const float *norm_w, float eps, float *y, hipStream_t s);
+                       const float *norm_w, float eps, float *y, uint64_t *keys, hipStream_t s);
+int launch_int8_linear_argmax(const int8_t *q, const uint16_t *mu16, int64_t rows, int64_t cols, const float *x,
+                              int64_t m, const float *norm_w, float eps, float *y, int64_t *ids, int64_t *history,
+                              int64_t hist_len, int64_t *pos, void *workspace, size_t workspace_bytes, hipStream_t s);
+size_t int8_linear_argmax_workspace_bytes(int64_t rows, int64_t m);
 int launch_int8_embed(const int8_t *q, const uint16_t *mu16, int64_t vocab, int64_t cols, const int64_t *idx,
                       int64_t n, int64_t t, const float *pos_w, int64_t pos_rows, const int64_t *pos0, float *out,
                       hipStream_t s);

@@ -31,7 +31,15 @@ import torch.nn.functional as F
 
 from . import _lib
 from .castor import H24_DIM, assert_row_aligned_width
-from .packed import PackedH24Linear, PackedInt8Embedding, PackedInt8Linear, int8_embed, packed_linear_group
+from .packed import (
+    PackedH24Linear,
+    PackedInt8Embedding,
+    PackedInt8Linear,
+    int8_embed,
+    int8_linear_argmax,
+    int8_linear_argmax_workspace,
+    packed_linear_group,
+)
 from .plx import check_fingerprint, load_plx
 
 # pollux.py:258-278: the config fields and their aliases
@@ -391,6 +399,13 @@ class GraphDecoder:
         self.greedy = bool(greedy)
         # token chosen at each position (greedy); one slot past the cache for the last step's choice
         self.history = torch.zeros(batch, self.max_len + 1, dtype=torch.long, device=device) if greedy else None
+        # greedy with the INT8 head's GEMV: the argmax, the history entry and the position advance run as the
+        # head kernel's epilogue plus one small kernel
+        head = model.head
+        self._head_ws = None
+        if greedy and isinstance(head, PackedInt8Linear) and head.gemv_runs(
+                torch.empty(batch, head.in_features, device="meta")):
+            self._head_ws = int8_linear_argmax_workspace(head.out_features, batch, device)
         self.length = 0
         self.graph = None
         self.logits = None
@@ -402,6 +417,10 @@ class GraphDecoder:
         x = m.embed(self.ids.view(b, 1), self.pos)
         for i, blk in enumerate(m.blocks):
             x = blk(x, self.cache, i, self.pos)
+        if self._head_ws is not None and x.dtype == torch.float32:
+            return int8_linear_argmax(m.head.weight_int8, m.head.mu_rows, x[:, -1], self.ids,
+                                      norm=(m.ln_f.weight, m.ln_f.eps), history=self.history, pos=self.pos,
+                                      workspace=self._head_ws)
         self.pos += 1
         logits = m.logits(x)[:, -1]
         if self.greedy:

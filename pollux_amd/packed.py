@@ -325,6 +325,60 @@ def int8_linear(q: torch.Tensor, mu16: torch.Tensor, x: torch.Tensor, *,
     return y.reshape(*x.shape[:-1], rows)
 
 
+def int8_linear_argmax_workspace(rows: int, tokens: int, device) -> torch.Tensor:
+    """The workspace int8_linear_argmax needs for ``rows`` output rows and ``tokens`` tokens (uint8)."""
+    n = int(_lib.lib().plx_int8_linear_argmax_workspace_bytes(int(rows), int(tokens)))
+    return torch.empty(max(n, 8), dtype=torch.uint8, device=device)
+
+
+def int8_linear_argmax(q: torch.Tensor, mu16: torch.Tensor, x: torch.Tensor, ids: torch.Tensor, *,
+                       norm: tuple[torch.Tensor, float] | None = None, history: torch.Tensor | None = None,
+                       pos: torch.Tensor | None = None, workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """int8_linear with the argmax of each token's outputs into ``ids`` (plx_int8_linear_argmax).
+
+    ids int64 [tokens]: torch.argmax(y, -1) of the returned y (greedy decoding,
+    generate.py:313-320 with top_k = 1).  ``pos`` (0-dim int64 device
+    tensor): the kernel then writes ids into ``history`` [tokens, L] (or None)
+    at column pos + 1 and advances pos by one.  ``workspace``: from
+    int8_linear_argmax_workspace (allocated per call when None).
+    """
+    _lib.require_device(x, "int8_linear_argmax input")
+    if q.dtype != torch.int8 or mu16.dtype != torch.float16 or x.dtype != torch.float32:
+        raise ValueError("int8_linear_argmax: int8 q, float16 mu and float32 x")
+    rows, cols = q.shape
+    if x.shape[-1] != cols or mu16.numel() != rows:
+        raise ValueError(f"int8_linear_argmax: x has {x.shape[-1]} features, weight [{rows}, {cols}]")
+    xx = x.reshape(-1, cols).contiguous()
+    if xx.data_ptr() % 16:
+        xx = xx.clone()
+    m = xx.shape[0]
+    if ids.dtype != torch.long or ids.numel() != m or not ids.is_contiguous():
+        raise ValueError(f"int8_linear_argmax: ids must be contiguous int64 with {m} values")
+    if history is not None:
+        if pos is None or history.dtype != torch.long or history.dim() != 2 or history.shape[0] != m \
+                or not history.is_contiguous():
+            raise ValueError("int8_linear_argmax: history must be contiguous int64 [tokens, L], with pos")
+    if pos is not None and (pos.dtype != torch.long or pos.numel() != 1):
+        raise ValueError("int8_linear_argmax: pos must be one int64 value")
+    nw, eps = None, 0.0
+    if norm is not None:
+        nw, eps = norm[0].detach().reshape(-1).contiguous(), float(norm[1])
+        if nw.dtype != torch.float32 or nw.numel() != cols:
+            raise ValueError(f"int8_linear_argmax: the norm weight must be fp32 with {cols} values")
+        if nw.data_ptr() % 16:
+            nw = nw.clone()
+    if workspace is None:
+        workspace = int8_linear_argmax_workspace(rows, m, x.device)
+    y = torch.empty((m, rows), dtype=torch.float32, device=x.device)
+    with torch.cuda.device(x.device):
+        st = _lib.lib().plx_int8_linear_argmax(
+            _lib.ptr(q.contiguous()), _lib.ptr(mu16.contiguous()), rows, cols, _lib.ptr(xx), m, _lib.ptr(nw), eps,
+            _lib.ptr(y), _lib.ptr(ids), _lib.ptr(history), 0 if history is None else history.shape[1], _lib.ptr(pos),
+            _lib.ptr(workspace), workspace.numel(), _lib.stream_of(x.device))
+    _lib.check(st, "int8_linear_argmax")
+    return y.reshape(*x.shape[:-1], rows)
+
+
 def int8_embed(q: torch.Tensor, mu16: torch.Tensor, ids: torch.Tensor, *, pos_weight: torch.Tensor | None = None,
                pos0: torch.Tensor | None = None) -> torch.Tensor:
     """fp32 [b, t, cols] = W[ids] (+ pos_weight[p0 + i] at step i), one HIP kernel (plx_int8_embed).
@@ -414,13 +468,17 @@ class PackedInt8Linear(_PackedInt8Rows):
         run the INT8 GEMV (norm fused in); others take the reference's
         F.linear on the fp16 weight cast to x's dtype (kept for reuse).
         """
-        if (not self._materialized and self.bias is None and x.dtype == torch.float32
-                and x.numel() // max(self.in_features, 1) <= self.gemv_max_tokens
-                and self.in_features % 16 == 0 and self.in_features <= 4096):
+        if self.gemv_runs(x):
             return int8_linear(self.weight_int8, self.mu_rows, x, norm=norm)
         if norm is not None:
             x = x * torch.rsqrt(x.pow(2).mean(dim=-1, keepdim=True) + norm[1]) * norm[0]
         return F.linear(x, self._weight_as(x.dtype), self.bias)
+
+    def gemv_runs(self, x: torch.Tensor) -> bool:
+        """Whether forward(x) runs the INT8 GEMV (packed, no bias, fp32 x of at most gemv_max_tokens tokens)."""
+        return (not self._materialized and self.bias is None and x.dtype == torch.float32
+                and x.numel() // max(self.in_features, 1) <= self.gemv_max_tokens
+                and self.in_features % 16 == 0 and self.in_features <= 4096)
 
     def _weight_as(self, dtype: torch.dtype) -> torch.Tensor:
         """weight.to(dtype) (pollux.py:562-563), cast once per dtype and kept (the weights are frozen)."""

@@ -117,6 +117,54 @@ def test_int8_linear_matches_fp64(dev, rows, cols, m):
     _check_int8_linear(yn, xn, wq, bound=2e-5)  # + the norm's rounding (a few ulp of x)
 
 
+# the head's shape at 1, 3 and 16 tokens (a pick block of 16, 4 and 1 waves per token), 20 tokens (two
+# rounds of 16), few rows (one GEMV block), rows % 4 != 0
+@pytest.mark.parametrize("rows,cols,m", [(50688, 1920, 1), (50688, 1920, 3), (50688, 1920, 16), (4103, 1920, 20),
+                                         (5, 48, 2), (999, 1040, 5)])
+def test_int8_linear_argmax_matches_torch(dev, rows, cols, m):
+    """ids == torch.argmax(y, -1) of the same y (equal to int8_linear's), with ties, NaN rows, history and pos."""
+    from pollux_amd.packed import int8_linear, int8_linear_argmax, int8_linear_argmax_workspace
+
+    g = torch.Generator().manual_seed(rows + 7 * m)
+    q = torch.randint(-128, 128, (rows, cols), dtype=torch.int8, generator=g)
+    mu = (torch.rand(rows, generator=g) * 0.2 + 1e-3).to(torch.float16)
+    xc = torch.randn(m, cols, generator=g)
+    x = xc.to(dev)
+    nw = (1.0 + 0.1 * torch.randn(cols, generator=g)).abs().to(dev)
+    if rows > 8:
+        # token 0's maximum three times (rows matched to its signs), at a lower row and two higher ones
+        q[rows // 2] = q[rows - 2] = q[3] = (torch.sign(xc[0]) * 127).to(torch.int8)
+        mu[rows // 2] = mu[rows - 2] = mu[3] = 0.5
+    qd, mud = q.to(dev), mu.to(dev)
+    hist = torch.full((m, 9), -1, dtype=torch.long, device=dev)
+    pos = torch.tensor(4, dtype=torch.long, device=dev)
+    ids = torch.empty(m, dtype=torch.long, device=dev)
+    ws = int8_linear_argmax_workspace(rows, m, dev)
+    y = int8_linear_argmax(qd, mud, x, ids, norm=(nw, 1e-5), history=hist, pos=pos, workspace=ws)
+    assert torch.equal(y, int8_linear(qd, mud, x, norm=(nw, 1e-5)))
+    want = torch.argmax(y, dim=-1)
+    print(f"[int8] linear_argmax {rows}x{cols} m={m}: ids {ids[:4].tolist()}", flush=True)
+    assert torch.equal(ids, want)
+    if rows > 8:
+        assert y[0, 3] == y[0, rows // 2] == y[0, rows - 2] == y[0].max() and int(ids[0]) == 3
+    assert int(pos) == 5 and torch.equal(hist[:, 5], ids)
+    assert (hist[:, :5] == -1).all() and (hist[:, 6:] == -1).all()
+    # a NaN row beats every number (the lower of two NaN rows wins); a position past the history writes nothing
+    if rows > 8:
+        mu[rows - 1] = mu[rows // 3] = float("nan")
+        mud = mu.to(dev)
+        pos.fill_(8)
+        y = int8_linear_argmax(qd, mud, x, ids, history=hist, pos=pos)  # workspace allocated per call
+        assert torch.isnan(y[:, rows // 3]).all()
+        assert torch.equal(ids, torch.full_like(ids, rows // 3)) and torch.equal(ids, torch.argmax(y, dim=-1))
+        assert int(pos) == 9 and (hist[:, 6:] == -1).all()
+    # no position: ids only; a workspace too small is refused
+    y = int8_linear_argmax(qd, mud, x[:1], ids[:1], workspace=ws)
+    assert torch.equal(ids[:1], torch.argmax(y, dim=-1))
+    with pytest.raises(Exception, match="workspace"):
+        int8_linear_argmax(qd, mud, x, ids, workspace=ws[:8])
+
+
 def test_int8_embed_with_positions(dev):
     from pollux_amd.packed import int8_embed
 
