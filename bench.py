@@ -470,6 +470,7 @@ def decode_extras(device, prompt_len=64, new_tokens=128):
                 c = model.new_cache(1)
                 model.prefill(prompt, c, last_only=True)
 
+        run_prefill(1)  # untimed: the first new cache (283 MB) may need a fresh device allocation
         t_prefill = timed(run_prefill, 8)
         pdec = GraphDecoder(model, batch=1)
         pdec.prefill(prompt)  # captures the 64-position prefill graph (and the step graph)
