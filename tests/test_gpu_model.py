@@ -164,12 +164,17 @@ def test_graph_decoder_matches_eager_decode(dev, packed):
     assert worst <= 1e-5
 
 
-def test_graph_greedy_decode_matches_eager_argmax(dev, packed):
-    # the captured step's own argmax and token feedback against an eager KV-cached greedy loop
+@pytest.mark.parametrize("fused_head", [True, False])
+def test_graph_greedy_decode_matches_eager_argmax(dev, packed, fused_head):
+    # the captured step's own argmax and token feedback against an eager KV-cached greedy loop; with the
+    # choice in the INT8 head GEMV's epilogue, and (head GEMV limited to 1 token) after the F.linear head
     from pollux_amd.model import GraphDecoder
 
     model = PackedPolluxModel.from_packed_checkpoint(str(packed[0]), dev)
+    if not fused_head:
+        model.head.gemv_max_tokens = 1
     dec = GraphDecoder(model, batch=2, greedy=True)
+    assert (dec._head_ws is not None) == fused_head
     idx = torch.randint(0, 90, (2, 4), generator=torch.Generator().manual_seed(9)).to(dev)
     with torch.inference_mode():
         first = dec.prefill(idx).argmax(-1)
