@@ -541,7 +541,8 @@ def main() -> int:
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(
             "bench.py measures one GPU only: this build's hot path (Leech quantize / pack / dequant) is "
-            "benchmarked per device; multi-GPU sharding is described in DESIGN.md, not run.",
+            "benchmarked per device (atoms and rows shard with no exchange; the packed indices are what "
+            "ranks would all-gather), and no multi-GPU run is made.",
             file=sys.stderr,
         )
         return 2
