@@ -16,12 +16,14 @@ packing     18-bit pack / unpack (castor.py:226-260)
 nn          exact (float64) nearest-neighbour scoring for the three reference
             semantics NN-B / NN-T / NN-P, with near-tie classification
             (castor.py:407-460, 544-557; pack.py:167-177)
-rowscale    row RMS, normalisation, rescale and the pack-time sigma16
-            (castor.py:309-339; pack.py:164; pollux.py:874-884)
-dequant     fp16 materialisation and the dense reference matmul
-            (pollux.py:485-507)
-torch_ref   the reference's non-Triton CPU path restated with the same torch
-            ops (castor.py:544-557) -- the CPU baseline of bench.py
+optim       the H24 branch of the optimiser step with every rounding explicit
+            (pollux.py:815-878)
+torch_ref   the reference's CPU path restated with the same torch ops:
+            NN-B / NN-P search (castor.py:544-557, pack.py:167-177), row RMS,
+            normalisation, rescale, the pack-time sigma16 (castor.py:309-339,
+            pack.py:164, pollux.py:874-884), fp16 materialisation and the
+            dense linear (pollux.py:485-507) -- also the CPU baseline of
+            bench.py
 
 How each function is pinned (golden vectors, closed forms, invariants,
 independent restatements) is listed in each module's header.

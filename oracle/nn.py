@@ -16,22 +16,27 @@ NN-P  pack.py:167-177 (pack time).  fp32 atoms against the fp32 codebook, fp32
 Scores here are computed exactly (float64; every product of two bf16 or two
 fp32 values is exact in float64) and then rounded the way each mode rounds.
 An fp32 contraction of 24 terms -- whatever its summation order, on a CPU BLAS
-or on MFMA -- lands within ``DELTA_REL * sum_i |x_i c_i|`` of the exact value
-(measured on MI355X MFMA: worst 2^-22.6; sequential fp32 bound ~2^-19.5 with
-typical error far smaller).  An atom is a *near-tie* when perturbing its
-candidate scores anywhere inside that envelope could change the selected index;
-every other atom has one answer that any correct fp32 implementation must
-reproduce bit-exactly.  Near-ties are counted and reported, never silently
-excluded.
+or on MFMA, with exact (bf16 x bf16) or once-rounded (fp32 x fp32) products --
+lands within ``DELTA_REL * sum_i |x_i c_i|`` of the exact value, with
+DELTA_REL = 24 * 2^-24 = 2^-19.4: the worst-case bound of n * u for n = 24
+terms and u = 2^-24 (each of at most 23 additions and the product rounds at
+most once per term).  It is a bound, not a measurement: MFMA on MI355X was
+measured at worst 2^-22.6.  An atom is a *near-tie* when perturbing its
+candidate scores anywhere inside that envelope could change the selected
+index; every other atom has one answer that any correct fp32 implementation
+must reproduce bit-exactly.  Near-ties are counted and reported, never
+silently excluded.
 
 Pinned by (tests/test_oracle_nn.py): every codebook vector maps to its own
 index in all three modes; x = 0 maps to 0; NN-P is invariant under positive
 scaling; the snap boundary 2*M < 0x407FFFFF is exercised from both sides;
 agreement with the torch-op restatement of NN-B (oracle/torch_ref.py, the
-reference's own ops) on every non-near-tie atom; and agreement with an
-independent structured decoder (Walsh-Hadamard transform over the Golay code
-for type-3 rows, octad sums for type-2, top pairs for type-1) in
-tests/test_oracle_nn.py.
+reference's own ops) on every non-near-tie atom; and, in all three modes on
+2,000 atoms (row-scaled weights, sphere atoms, contact-pair midpoints),
+agreement with an independent structured decoder that never reads the
+sorted table: a +-1 transform over the 4,096 Golay words with the -3
+correction for type 3, per-octad |x| sums with the sign-parity fix for type
+2, the two largest |x_i| for type 1 (tests/test_oracle_nn.py).
 """
 
 from __future__ import annotations
@@ -40,7 +45,7 @@ import numpy as np
 
 from . import codebook as cbm
 
-DELTA_REL = 2.0 ** -20
+DELTA_REL = 24 * 2.0 ** -24  # n * u for n = 24 fp32 terms (any summation order)
 C_SQ_NORM_F32 = np.uint32(0x407FFFFF).view(np.float32)  # fp32 |codebook[1]|^2 (castor.py:522)
 NUMERICAL_EPSILON_F32 = np.float32(1e-8)
 BF16_TWO = 0x4000  # bf16 bits of 2.0: NN-B snaps iff the bf16 max is below 2.0

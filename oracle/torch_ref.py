@@ -8,9 +8,33 @@ the reference calls (autocast-bf16 matmul, ``.float().max(-1)``, ``pow``,
 the reference's results by construction.  bench.py times ``nn_b_indices`` on
 the host cores as the CPU baseline ("kind": "port").
 
-Pinned by (tests/test_oracle_nn.py, tests/test_oracle_rowscale.py): agreement
-with the exact float64 oracle (oracle/nn.py) on every non-near-tie atom, and
-float64 closed forms for the row scale (within 2 fp32 ulp).
+Pinned by:
+  nn_b_indices, nn_p_indices   agreement with the exact float64 oracle
+                               (oracle/nn.py) on every non-near-tie atom
+                               (tests/test_oracle_nn.py);
+  row_rms                      float64 closed form over the fp32 squares,
+                               within 1 fp32 ulp, on seeded rows, a zero row,
+                               one huge element, subnormals, an overflowing
+                               square (tests/test_oracle_rowscale.py);
+  normalize, lattice_input     correctly rounded fp32 quotients computed in
+                               float64, bit-exact, including the sigma clamp;
+  sigma16_from_sigma           float64 product rounded to fp32, the clamp,
+                               numpy's RNE cast to fp16, bit-exact over the
+                               fp16 rounding boundaries, subnormals, overflow;
+  reconstruct                  fp32(fp32(c * sigma) * 0x3F3504F3) from float64
+                               products, bit-exact;
+  materialize                  numpy float16 emulation of
+                               fp16(fp32(fp16(c16 * sigma16)) * fp32(1/sqrt 2)),
+                               exhaustive over every finite fp16 sigma and all
+                               8 alphabet values;
+  linear_fp32                  float64 matmul within K * 2^-24 * sum|x||w|;
+  pollux_h24_update            rule by rule against oracle/optim.py
+                               (tests/test_oracle_optim.py).
+Each of these tests also shows that a plausible slip (eps outside the sqrt,
+the clamp before the multiply, one rounding instead of two, a multiply by
+fp32(sqrt 2) instead of the division, bf16 weights) fails the same check.
+``linear_as_reference``, ``int8_materialize`` and ``pollux_packed_forward``
+compose the pinned pieces with torch's own ops (F.linear, F.gelu, SDPA).
 """
 
 from __future__ import annotations
@@ -91,9 +115,14 @@ def requantize(latent: torch.Tensor, sigma: torch.Tensor | None = None):
     return idx, sigma, reconstruct(center, sigma)
 
 
+def sigma16_from_sigma(sigma: torch.Tensor) -> torch.Tensor:
+    """The scale step of pack.py:164 on a given fp32 row RMS: fp16(clamp(sigma * fp32(sqrt(12)), 1e-8))."""
+    return (sigma.float() * math.sqrt(12.0)).clamp_min(NUMERICAL_EPSILON).to(torch.float16)
+
+
 def sigma16_pack(w: torch.Tensor) -> torch.Tensor:
     """pack.py:164: fp16(clamp(row_rms(w) * fp32(sqrt(12)), 1e-8))."""
-    return (row_rms(w.detach().float()) * math.sqrt(12.0)).clamp_min(NUMERICAL_EPSILON).to(torch.float16)
+    return sigma16_from_sigma(row_rms(w.detach().float()))
 
 
 def materialize(indices: torch.Tensor, sigma16: torch.Tensor, out_features: int, in_features: int) -> torch.Tensor:

@@ -105,3 +105,148 @@ def test_nn_b_differs_from_nn_t_on_bf16_ties():
     t = nn.quantize(x, "T")
     frac = np.mean(b["idx"] != t["idx"])
     assert 0.01 < frac < 0.10
+
+
+# ---------------------------------------------------------------------------
+# Independent cross-check: a structured decoder built from the Golay code.
+#
+# Every kissing point is one of three shapes (castor.py:98-143), so the best
+# score of each shape follows from textbook routines instead of the sorted
+# 196,560-row table that nn.quantize scans:
+#   type 1 (+-4, +-4, 0^22): v4 * (sum of the two largest |x_i|);
+#   type 2 (+-2 on an octad, even number of minus signs): per octad
+#          v2 * sum|x_i|, less 2 * v2 * min|x_i| when the signs of x on the
+#          octad have odd parity;
+#   type 3 (-1 where the Golay word has a bit, +1 elsewhere, then -3 at pos):
+#          T(w) = sum_i (-1)^{w_i} x_i for all 4,096 words (a +-1 transform
+#          over the code), then v1 * (T(w) - e_pos(w) x_pos) - v3 * x_pos.
+# v1..v4 are the table's values of 1, 2, 3, 4 raw units: bf16(k * fp32(1/sqrt 8))
+# for NN-B / NN-T (autocast rounds the fp32 table to bf16), the fp32 table
+# values for NN-P.  The decoder also returns the winning vector in raw units,
+# so the brute-force index's table row is checked against it.
+# ---------------------------------------------------------------------------
+
+
+def _unit_values(mode):
+    vals = cb.codebook_f32()
+    raw = cb.codebook_int8()
+    out = {}
+    for k in (1, 2, 3, 4):
+        r, c = np.argwhere(np.abs(raw) == k)[0]
+        v = abs(vals[r, c])
+        out[k] = float(cb.bf16_to_f32(cb.bf16_round_bits(np.array([v], np.float32)))[0]) if mode != "P" else float(v)
+    return out
+
+
+def structured_decode(x: np.ndarray, mode: str):
+    """Best exact score and its raw vector per atom. x: [N, 24] fp32. Returns (score f64 [N], raw int [N, 24])."""
+    v = _unit_values(mode)
+    xq = x.astype(np.float64) if mode == "P" else cb.bf16_to_f32(cb.bf16_round_bits(x)).astype(np.float64)
+    n = xq.shape[0]
+    ax = np.abs(xq)
+    sgn = np.where(xq < 0, -1, 1)
+    # type 1
+    top2 = np.argsort(-ax, axis=1, kind="stable")[:, :2]
+    s1 = v[4] * np.take_along_axis(ax, top2, 1).sum(1)
+    vec1 = np.zeros((n, 24), np.int64)
+    np.put_along_axis(vec1, top2, 4 * np.take_along_axis(sgn, top2, 1), 1)
+    # type 2
+    words = cb.extended_golay_words()
+    bits = ((words[:, None] >> np.arange(24)[None, :]) & 1).astype(bool)
+    octads = np.array([np.nonzero(b)[0] for b in bits if b.sum() == 8])
+    assert octads.shape == (759, 8)
+    A = ax[:, octads]  # [N, 759, 8]
+    odd = (xq[:, octads] < 0).sum(2) % 2 == 1
+    s2_all = v[2] * (A.sum(2) - 2.0 * A.min(2) * odd)
+    best_o = s2_all.argmax(1)
+    s2 = s2_all[np.arange(n), best_o]
+    vec2 = np.zeros((n, 24), np.int64)
+    for r in range(n):
+        pos = octads[best_o[r]]
+        e = sgn[r, pos].copy()
+        if odd[r, best_o[r]]:
+            e[np.argmin(ax[r, pos])] *= -1
+        vec2[r, pos] = 2 * e
+    # type 3
+    E = np.where(bits, -1.0, 1.0)  # [4096, 24]
+    T = xq @ E.T  # [N, 4096]
+    s3 = np.full(n, -np.inf)
+    arg3 = np.zeros((n, 2), np.int64)
+    for p in range(24):
+        sc = v[1] * (T - E[None, :, p] * xq[:, p : p + 1]) - v[3] * xq[:, p : p + 1]
+        w = sc.argmax(1)
+        m = sc[np.arange(n), w]
+        better = m > s3
+        s3[better] = m[better]
+        arg3[better] = np.stack([w[better], np.full(better.sum(), p)], 1)
+    vec3 = E[arg3[:, 0]].astype(np.int64)
+    vec3[np.arange(n), arg3[:, 1]] = -3
+    scores = np.stack([s1, s2, s3], 1)
+    which = scores.argmax(1)
+    best = scores[np.arange(n), which]
+    vec = np.where((which == 0)[:, None], vec1, np.where((which == 1)[:, None], vec2, vec3))
+    return best, vec
+
+
+def _cross_check_atoms():
+    g = torch.Generator().manual_seed(21)
+    parts = [_lattice_atoms(32, 1152, 22)[:1200].numpy()]
+    d = torch.randn(600, 24, generator=g)
+    r = torch.rand(600, 1, generator=g) * 2.0 * np.sqrt(32.0) * float(cb.LEECH_SCALE_F32)
+    parts.append((d / d.norm(dim=1, keepdim=True) * r).numpy())  # config-4 style sphere atoms (lattice units)
+    rng = np.random.default_rng(23)
+    c32 = cb.codebook_f32()
+    raw = cb.codebook_int8().astype(np.int32)
+    a = rng.integers(1, 196561, 200)
+    partner = []
+    for k in a:  # a partner at raw inner product 16: the midpoint sits on a Voronoi face
+        while True:
+            cand = rng.integers(1, 196561, 512)
+            hit = np.nonzero(raw[cand] @ raw[k] == 16)[0]
+            if len(hit):
+                partner.append(cand[hit[0]])
+                break
+    mids = 0.5 * (c32[a] + c32[np.array(partner)]) + rng.normal(0, 1e-3, (200, 24))
+    parts.append(mids.astype(np.float32))
+    return np.concatenate(parts).astype(np.float32)
+
+
+@pytest.mark.parametrize("mode", ["B", "T", "P"])
+def test_structured_decoder_agrees_with_brute_force(mode):
+    x = _cross_check_atoms()
+    assert x.shape[0] >= 2000
+    if mode == "P":
+        x = x * np.float32(0.0137)  # raw-weight scale; NN-P is scale invariant
+    r = nn.quantize(x, mode)
+    best, vec = structured_decode(x, mode)
+    near = r["near_tie"]
+    assert near.mean() < 0.05
+    raw = cb.codebook_int8()
+    ok = ~near
+    idx = r["idx"]
+    if mode == "P":
+        kept = ok & (idx > 0)
+        # the oracle's winning row is the decoder's vector, and its fp32 score is the decoder's max
+        assert np.array_equal(raw[idx[kept]], vec[kept])
+        assert np.allclose(r["top"][kept], best[kept].astype(np.float32), rtol=2 ** -22, atol=0)
+        return
+    v = _unit_values(mode)
+    snap = 2.0 * best.astype(np.float32) < np.float32(np.uint32(0x407FFFFF).view(np.float32))
+    if mode == "B":
+        # the bucket is bf16(max score); the origin wins iff that bucket is below 2.0
+        bucket = cb.bf16_to_f32(cb.bf16_round_bits(best.astype(np.float32))).astype(np.float64)
+        assert np.array_equal(r["top"][ok], bucket[ok])
+        assert np.array_equal(idx[ok] == 0, (bucket < 2.0)[ok])
+        # the chosen code's own score rounds into the same bucket (it may be another code of that bucket)
+        kept = ok & (idx > 0)
+        xq = cb.bf16_to_f32(cb.bf16_round_bits(x)).astype(np.float64)
+        cv = np.select([np.abs(raw[idx[kept]]) == k for k in (1, 2, 3, 4)],
+                       [np.sign(raw[idx[kept]]) * v[k] for k in (1, 2, 3, 4)], 0.0)
+        own = (cv * xq[kept]).sum(1).astype(np.float32)
+        assert np.array_equal(cb.bf16_round_bits(own), cb.bf16_round_bits(best[kept].astype(np.float32)))
+    else:
+        assert np.array_equal(idx[ok] == 0, snap[ok])
+        kept = ok & (idx > 0)
+        assert np.array_equal(raw[idx[kept]], vec[kept])
+        assert np.array_equal(r["top"][kept], best[kept].astype(np.float32).astype(np.float64))
+    assert kept.sum() > 1000
