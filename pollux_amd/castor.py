@@ -15,8 +15,14 @@ Differences from the reference, by design:
     Triton kernel's fp32-score semantics (NN-T, castor.py:407-460) are
     available through ``set_nn_mode("fp32")`` or POLLUX_AMD_NN_MODE=fp32.
   * The quantizer always searches the canonical codebook; a ``codebook``
-    argument must equal it (checked once per tensor version) -- the reference
-    only ever passes ``get_h24_codebook(...)``.
+    argument must equal ``get_h24_codebook`` in its own dtype (checked once
+    per tensor and version) -- the reference only ever passes that table.
+    Its dtype keeps the reference's meaning (castor.py:521-522, 533, 559):
+    the returned vectors are the passed table's values cast to the latent's
+    dtype; under NN-B an fp16 or bf16 table gives the fp32 table's indices
+    (their bf16 operands are identical and 2*M < c_sq of either table is the
+    same test on bf16 scores M); NN-T, whose fp32 scores would meet the
+    rounded table's c_sq = 3.99915, accepts fp32 / fp64 tables only.
   * ``chunk_size`` is accepted for signature compatibility; the kernel never
     materialises scores, so it has no memory-bounding role.
 """
@@ -26,6 +32,7 @@ from __future__ import annotations
 import math
 import os
 import threading
+import weakref
 from functools import lru_cache
 
 import numpy as np
@@ -225,26 +232,53 @@ def scale_matrix_by_row_rms(weight: torch.Tensor, sigma_rows: torch.Tensor) -> t
 # Quantizer (castor.py:487-580)
 # =============================================================================
 
-_checked_codebooks: dict[tuple[int, int, int], bool] = {}
+_CODEBOOK_DTYPES = (torch.float32, torch.float64, torch.float16, torch.bfloat16)
+# id(table) -> (weak reference, _version, equals the canonical table); entries
+# leave with their tensor, so a new tensor at a reused address is checked anew
+_checked_codebooks: dict[int, tuple] = {}
 
 
-def _check_codebook(codebook: torch.Tensor, device: torch.device) -> None:
+def _codebook_is_canonical(codebook: torch.Tensor) -> bool:
     if tuple(codebook.shape) != (H24_CODEBOOK_COUNT, H24_DIM):
         raise ValueError(
             f"codebook must have shape ({H24_CODEBOOK_COUNT}, {H24_DIM}); got {tuple(codebook.shape)}"
         )
-    key = (codebook.data_ptr(), codebook._version, hash(codebook.dtype))
-    ok = _checked_codebooks.get(key)
-    if ok is None:
-        ref = get_h24_codebook(codebook.device, codebook.dtype)
-        ok = bool(torch.equal(codebook, ref))
-        if len(_checked_codebooks) > 64:
-            _checked_codebooks.clear()
-        _checked_codebooks[key] = ok
-    if not ok:
+    if codebook.dtype not in _CODEBOOK_DTYPES:
+        raise ValueError(f"codebook dtype must be one of {_CODEBOOK_DTYPES}; got {codebook.dtype}")
+    # inference tensors have no version counter: compare them on every call
+    version = None if codebook.is_inference() else codebook._version
+    key = id(codebook)
+    ent = _checked_codebooks.get(key)
+    if version is not None and ent is not None and ent[0]() is codebook and ent[1] == version:
+        return ent[2]
+    ok = bool(torch.equal(codebook, get_h24_codebook(codebook.device, codebook.dtype)))
+    if version is not None:
+        ref = weakref.ref(codebook, lambda _r, k=key: _checked_codebooks.pop(k, None))
+        _checked_codebooks[key] = (ref, version, ok)
+    return ok
+
+
+def _check_codebook(codebook: torch.Tensor, semantics: str) -> None:
+    """Refuse a codebook argument whose search semantics this library does not reproduce.
+
+    semantics: "bf16" (NN-B), "fp32" (NN-T) or "pack" (NN-P, pack.py:167-177).
+    """
+    if not _codebook_is_canonical(codebook):
         raise ValueError(
             "pollux_amd quantizes against the canonical Leech codebook only; the codebook argument "
             "differs from get_h24_codebook()"
+        )
+    dt = codebook.dtype
+    if semantics == "fp32" and dt in (torch.float16, torch.bfloat16):
+        raise ValueError(
+            f"NN-T (fp32 scores) against a {dt} codebook compares 2*max with |kp[0]|^2 of the rounded "
+            "table (3.99915, castor.py:521-522), which this library does not reproduce; pass the "
+            "fp32 table (get_h24_codebook(device, torch.float32)) or use NN-B"
+        )
+    if semantics == "pack" and dt == torch.bfloat16:
+        raise ValueError(
+            "the pack-time search (pack.py:167-177) against a bfloat16 codebook scores 3s rounded to "
+            "1.0625, which this library does not reproduce; pass the fp32 table as pack.py:259 does"
         )
 
 
@@ -312,9 +346,14 @@ def castor_quantize_leech(
     if x.shape[0] == 0:
         return latent.clone()
     _lib.require_device(latent, "castor_quantize_leech input")
-    _check_codebook(codebook, latent.device)
-    idx = quantize_indices(x)
-    return gather_codebook(idx, latent.dtype).view(orig_shape)
+    mode = _nn_mode
+    _check_codebook(codebook, mode)
+    idx = quantize_indices(x, mode=mode)
+    # codebook.to(dtype=latent.dtype).index_select(...) of the passed table (castor.py:533, 559)
+    out = gather_codebook(idx, codebook.dtype)
+    if out.dtype != latent.dtype:
+        out = out.to(latent.dtype)
+    return out.view(orig_shape)
 
 
 class CastorQuantizeLeech(torch.autograd.Function):

@@ -382,9 +382,14 @@ class GraphDecoder:
     Usage: ``dec.prefill(prompt_ids)`` then ``logits = dec.decode(next_ids)``
     per token; the returned logits tensor is reused by the next replay.
     With ``greedy=True`` the captured step also takes the argmax of its
-    logits (generate.py:313-320 with top_k = 1), records it at its position
-    and feeds it to the next replay: ``dec.decode_greedy(first_ids, n)`` then
-    decodes n tokens without the host in the loop.
+    logits, records it at its position and feeds it to the next replay:
+    ``dec.decode_greedy(first_ids, n)`` then decodes n tokens without the
+    host in the loop.  This is a raw-argmax path for measuring decode
+    throughput, not the reference's sampler: the argmax runs over all
+    ``vocab_size`` rows of the head, including any padded rows past the
+    tokenizer's vocabulary, and applies no repetition penalty
+    (generate.py:286-336 defaults to 1.1), so its tokens can differ from
+    generate.py's.  ``generate`` below applies the reference's sampling rules.
     """
 
     def __init__(self, model: PackedPolluxModel, batch: int = 1, max_len: int | None = None,

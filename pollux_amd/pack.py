@@ -76,11 +76,17 @@ def quantize_h24_layer(weight: torch.Tensor, *, return_indices: bool = False):
 def _quantize_h24_layer(weight: torch.Tensor, codebook: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     """pack._quantize_h24_layer (pack.py:139-180): (packed uint8, sigma_rows fp16), both on the CPU.
 
-    ``codebook`` must be the canonical table (get_h24_codebook, any dtype);
-    the search always uses its fp32 values, as the reference does.
+    ``codebook`` must be the canonical table (get_h24_codebook) in fp32 or
+    fp64, whose values the reference scores (``codebook[1:].to(fp32)``), or
+    in fp16: the fp16 table is the raw integer codes times 0.353515625
+    exactly, so its scores order the codes like the fp32 table's up to
+    4.8e-8 * |x_pos| (fp32(3s) - 3s), inside the near-tie envelope, and the
+    indices agree on every atom that is not a near-tie.  A bfloat16 table
+    (3s rounded to 1.0625) scores type-3 codes differently and raises
+    ValueError.
     """
     _lib.require_device(weight, "_quantize_h24_layer input")
-    _check_codebook(codebook, weight.device)
+    _check_codebook(codebook, "pack")
     packed, sigma = quantize_h24_layer(weight)
     return packed.cpu(), sigma.cpu()
 

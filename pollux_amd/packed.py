@@ -481,13 +481,26 @@ class PackedInt8Linear(_PackedInt8Rows):
                 and self.in_features % 16 == 0 and self.in_features <= 4096)
 
     def _weight_as(self, dtype: torch.dtype) -> torch.Tensor:
-        """weight.to(dtype) (pollux.py:562-563), cast once per dtype and kept (the weights are frozen)."""
+        """weight.to(dtype) (pollux.py:562-563), cast once per dtype and source state, then reused.
+
+        The entry holds the source tensors themselves (compared by identity) and
+        their version counters, so replacing the buffers (``load_state_dict``
+        on a materialised layer, ``materialize``) or writing them in place
+        (``load_state_dict`` on a packed layer copies into the buffers) makes
+        the next call cast again.  Tensors made under ``torch.inference_mode``
+        keep no version counter: for those an in-place write is not seen, so
+        replace such buffers instead.
+        """
         if self._materialized and self.weight.dtype == dtype:
             return self.weight
+        src = (self.weight,) if self._materialized else (self.weight_int8, self.mu_rows)
+        versions = tuple(None if t.is_inference() else t._version for t in src)
         cache = self.__dict__.setdefault("_cast", {})
-        w = cache.get(dtype)
-        dev = (self.weight if self._materialized else self.weight_int8).device
-        if w is None or w.device != dev:
-            w16 = self.weight if self._materialized else dequantize_int8_rows(self.weight_int8, self.mu_rows)
-            w = cache[dtype] = w16.detach().to(dtype=dtype)
+        hit = cache.get(dtype)
+        if hit is not None and len(hit[0]) == len(src) and all(a is b for a, b in zip(hit[0], src)) \
+                and hit[1] == versions:
+            return hit[2]
+        w16 = self.weight if self._materialized else dequantize_int8_rows(self.weight_int8, self.mu_rows)
+        w = w16.detach().to(dtype=dtype)
+        cache[dtype] = (src, versions, w)
         return w

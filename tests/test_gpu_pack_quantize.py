@@ -122,3 +122,21 @@ def test_quantize_h24_layer_matches_reference_composition(dev):
     p2, s2, i2 = plx_pack.quantize_h24_layer(w.to(dev), return_indices=True)
     assert torch.equal(p2.cpu(), packed) and torch.equal(s2.cpu(), sigma)
     assert np.array_equal(i2.cpu().numpy().astype(np.int64), idx)
+
+
+def test_quantize_h24_layer_codebook_dtypes(dev):
+    # pack.py:167: the fp16 table is the raw codes times 0.353515625 exactly, so
+    # its indices equal the fp32 table's off near-ties; a bf16 table is refused
+    g = torch.Generator().manual_seed(16)
+    w = (torch.randn(64, 480, generator=g) * 0.02).to(dev)
+    p32, s32 = plx_pack._quantize_h24_layer(w, castor.get_h24_codebook(dev, torch.float32))
+    p16, s16 = plx_pack._quantize_h24_layer(w, castor.get_h24_codebook(dev, torch.float16))
+    assert torch.equal(s32, s16)
+    n = w.numel() // 24
+    i32, i16 = packing.unpack(p32.numpy(), n), packing.unpack(p16.numpy(), n)
+    diff = np.nonzero(i32 != i16)[0]
+    if len(diff):
+        r = nn.quantize(w.reshape(-1, 24).cpu().numpy()[diff], "P")
+        assert r["near_tie"].all()
+    with pytest.raises(ValueError, match="bfloat16"):
+        plx_pack._quantize_h24_layer(w, castor.get_h24_codebook(dev, torch.bfloat16))

@@ -80,6 +80,32 @@ def test_packed_int8_layers(dev):
     assert torch.equal(lin(x), want)
 
 
+def test_packed_int8_linear_sees_new_weights(dev):
+    # the cached cast of the head weight (token batches above the GEMV limit) is
+    # rebuilt after load_state_dict copies new values into the buffers in place
+    g = torch.Generator().manual_seed(81)
+    lin = PackedInt8Linear(48, 100).to(dev)
+    states = []
+    for _ in range(2):
+        q, mu = plx_pack.quantize_int8_rows(torch.randn(100, 48, generator=g).to(dev))
+        states.append({"weight_int8": q, "mu_rows": mu})
+    big = torch.randn(20, 48, generator=g).to(dev)
+    for st in states + states[:1]:
+        lin.load_state_dict(st)
+        want = torch.nn.functional.linear(big, _ref_int8_materialize(st["weight_int8"], st["mu_rows"]).float())
+        assert torch.equal(lin(big), want)
+        assert torch.equal(lin(big.to(torch.bfloat16)),
+                           torch.nn.functional.linear(big.to(torch.bfloat16),
+                                                      _ref_int8_materialize(st["weight_int8"], st["mu_rows"])
+                                                      .to(torch.bfloat16)))
+    # replacing a buffer object is seen too
+    lin.weight_int8 = states[1]["weight_int8"].clone()
+    lin.mu_rows = states[1]["mu_rows"].clone()
+    want = torch.nn.functional.linear(big, _ref_int8_materialize(states[1]["weight_int8"],
+                                                                 states[1]["mu_rows"]).float())
+    assert torch.equal(lin(big), want)
+
+
 def _check_int8_linear(y, x, w16, bound=1e-5):
     """y against fp64 x @ w16.T: |err| <= bound * sum |x||w| per element (fp32 accumulation)."""
     xd, wd = x.double().cpu(), w16.double().cpu()

@@ -119,3 +119,63 @@ def test_non_canonical_codebook_is_rejected(dev):
     cbk[5, 0] += 1.0
     with pytest.raises(ValueError):
         castor.castor_quantize_leech(torch.zeros(4, 24, device=dev), cbk)
+
+
+def test_codebook_checked_again_after_in_place_change_and_address_reuse(dev):
+    x = torch.zeros(4, 24, device=dev)
+    cbk = castor.get_h24_codebook(dev, torch.float32)
+    castor.castor_quantize_leech(x, cbk)  # accepted and cached
+    cbk[7, 3] = 0.5  # in place: a new version of the same tensor
+    with pytest.raises(ValueError):
+        castor.castor_quantize_leech(x, cbk)
+    ok = castor.get_h24_codebook(dev, torch.float32)
+    castor.castor_quantize_leech(x, ok)
+    addr = ok.data_ptr()
+    del ok
+    bad = torch.empty(196561, 24, device=dev)  # the caching allocator usually hands back the same block
+    bad.copy_(castor.get_h24_codebook(dev, torch.float32))
+    bad[11, 0] = 9.0
+    print(f"[codebook] reused address: {bad.data_ptr() == addr}", flush=True)
+    with pytest.raises(ValueError):
+        castor.castor_quantize_leech(x, bad)
+
+
+def test_inference_mode_codebook(dev):
+    # an inference tensor has no version counter; it is compared on every call
+    x = _lattice_atoms(4, 1152, 52).to(dev)
+    with torch.inference_mode():
+        cbk = castor.get_h24_codebook(dev, torch.float32)
+        a = castor.castor_quantize_leech(x, cbk)
+    b = castor.castor_quantize_leech(x, cbk)
+    assert torch.equal(a, b)
+    with torch.inference_mode():
+        bad = cbk.clone()
+        bad[3, 3] = 1.0
+        with pytest.raises(ValueError):
+            castor.castor_quantize_leech(x, bad)
+
+
+@pytest.mark.parametrize("table", [torch.float16, torch.bfloat16, torch.float64])
+@pytest.mark.parametrize("out", [torch.float32, torch.float16, torch.bfloat16])
+def test_codebook_dtype_semantics_nn_b(dev, table, out):
+    # castor.py:521-559 with a rounded table: NN-B indices equal the fp32 table's
+    # (identical bf16 operands; 2*M < c_sq is the same test on bf16 scores), and
+    # the vectors are the passed table's values cast to the latent's dtype
+    x = _lattice_atoms(8, 1152, 53).to(dev).to(out)
+    cbk = castor.get_h24_codebook(dev, table)
+    got = castor.castor_quantize_leech(x, cbk)
+    idx = castor.quantize_indices(x, mode="bf16").long()
+    want = cbk.to(out).index_select(0, idx).view(x.shape)
+    assert got.dtype == out and torch.equal(got, want)
+
+
+def test_codebook_dtype_nn_t_refuses_rounded_tables(dev):
+    x = torch.zeros(4, 24, device=dev)
+    castor.set_nn_mode("fp32")
+    try:
+        castor.castor_quantize_leech(x, castor.get_h24_codebook(dev, torch.float32))
+        for dt in (torch.float16, torch.bfloat16):
+            with pytest.raises(ValueError, match="NN-T"):
+                castor.castor_quantize_leech(x, castor.get_h24_codebook(dev, dt))
+    finally:
+        castor.set_nn_mode("bf16")
