@@ -1,22 +1,30 @@
 #!/usr/bin/env python3
 """Benchmark of the Leech-lattice quantization hot path on one MI355X.
 
-Headline (BASELINE.json metric): atoms/s of the fused per-step requantize of a
-Pollux-1152 layer (QKV 3456x1152, O 1152x1152, up 4608x1152,
-down 1152x4608 in torch (out, in) layout; fp32 N(0, 0.02) draws rounded to
-bf16 "master weights" and held as fp32 latents).  One step = for each of the
-four latents: row scale -> NN-B quantize -> 18-bit pack -> reconstructed fp32
-weight (pollux.py:874-884 + castor.pack_indices), inputs resident in HBM.
+Headline (BASELINE.json metric, config 4): atoms/s of the bulk NN-B quantizer
+(castor.py:544-557 semantics: bf16 operands, bf16 scores, lowest index) on
+16,777,200 24-d fp32 atoms (209,715 rows of 1920 = 80 atoms per row, the
+config's 16,777,216 rounded down to whole rows) whose directions are uniform
+on S^23 and whose radius is U(0, 2) * sqrt(32), fed directly as quantizer
+input.  One step = ``castor.quantize_indices`` over all of them (fp32 atoms
+resident in HBM -> int32 codebook indices).
 
 The JSON line also carries
-  roofline      the scoring kernel (nn_kernel) against dense bf16 MFMA peak:
-                algorithmic flops 2*24*196,560 per atom over its HIP-event
-                kernel time inside the timed region;
-  cpu_baseline  the reference's own CPU path (autocast-bf16 matmul + max,
-                castor.py:544-557, plus its row scale and pack) restated with
-                the same torch ops (oracle/torch_ref.py) on a bounded sample
-                of the same workload, on this host's cores;
-  extras        pack / unpack / dequant HBM GB/s at BASELINE config-4 scale.
+  roofline      the scoring kernel (nn_kernel) of that launch against the dense
+                bf16 MFMA peak: algorithmic flops 2*24*196,560 per atom over its
+                HIP-event kernel time inside the timed region (events recorded
+                on the launch stream); traffic from profiles/ (rocprofv3 --pmc);
+  dequant_gemv  the metric's second half: the fused dequant-GEMV at d=1920
+                (config 5, batch 1) in compressed-stream GB/s and as a fraction
+                of HBM peak;
+  cpu_baseline  the reference's own CPU path (autocast-bf16 matmul + max in
+                chunks of 4096, castor.py:549-557) restated with the same torch
+                ops (oracle/torch_ref.py) on a bounded prefix of the same atoms,
+                on this host's physical cores;
+  parity        that prefix's CPU indices against the GPU's, each disagreement
+                classified by the exact oracle (near-tie or not);
+  extras        config 2 / 3 requantize steps, pack / unpack / dequant HBM GB/s,
+                dequant-GEMM, the fused optimiser step, pack-time NN-P, decode.
 
     python bench.py [--steps K] [--warmup W] [--gpus 1]
 """
@@ -38,6 +46,7 @@ FLOP_PER_ATOM = 2 * 24 * 196_560  # 9,434,880 algorithmic flops (origin free, K 
 PEAK_BF16_FLOPS = 2.5e15  # MI355X dense bf16 MFMA
 PEAK_HBM_BPS = 8.0e12  # MI355X HBM3E
 C2_SHAPES = [(3456, 1152), (1152, 1152), (4608, 1152), (1152, 4608)]
+C4_ROWS, C4_ATOMS_PER_ROW = 209_715, 80  # 16,777,200 atoms as rows of 1920
 
 
 def log(*a):
@@ -81,33 +90,74 @@ def time_gpu(fn, iters, warmup, rounds=1, warm_s=0.0):
     return sorted(per)[len(per) // 2]
 
 
-def cpu_baseline(mats, target_atoms):
-    """The reference's CPU path on the first rows of the QKV latent (a bounded sample)."""
+def host_cpu():
+    """(physical cores this process may run on, CPU model name) from /sys and /proc (lscpu's sources)."""
+    cpus = sorted(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else list(range(os.cpu_count() or 1))
+    cores = set()
+    for c in cpus:
+        base = Path(f"/sys/devices/system/cpu/cpu{c}/topology")
+        try:
+            cores.add(((base / "physical_package_id").read_text().strip(), (base / "core_id").read_text().strip()))
+        except OSError:
+            cores.add(("?", str(c)))
+    model = "unknown"
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.lower().startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return max(1, len(cores)), len(cpus), model
+
+
+def cpu_baseline(x_gpu, idx_gpu, target_atoms):
+    """The reference's CPU path (castor.py:549-557) on the first atoms of the headline input, plus parity.
+
+    Returns (cpu_baseline record, parity record): the same torch ops on the
+    host's physical cores, timed; their indices against the GPU's for the same
+    atoms, each disagreement classified by the exact oracle (oracle/nn.py).
+    """
+    import numpy as np
     import torch
 
-    from oracle import packing, torch_ref
+    from oracle import nn, torch_ref
 
-    cores = os.cpu_count() or 1
-    torch.set_num_threads(cores)
-    w = mats[0].cpu()
-    rows = max(1, target_atoms // (w.shape[1] // 24))
-    sample = w[:rows]
+    phys, logical, model = host_cpu()
+    torch.set_num_threads(phys)
+    n = min(int(target_atoms), x_gpu.shape[0])
+    x = x_gpu[:n].cpu()
+    kp = torch_ref.codebook_tensor()[1:]
+    torch_ref.nn_b_indices(x[:4096], kp=kp)  # untimed: first-call setup of the bf16 matmul
     t0 = time.perf_counter()
-    x, sigma = torch_ref.lattice_input(sample)
-    idx = torch_ref.nn_b_indices(x)
-    packing.pack(idx.numpy())
-    center = torch_ref.codebook_tensor()[idx].reshape(sample.shape)
-    torch_ref.reconstruct(center, sigma)
+    idx_cpu = torch_ref.nn_b_indices(x, kp=kp)
     dt = time.perf_counter() - t0
-    n = sample.numel() // 24
-    return {
+    got = idx_gpu[:n].long().cpu()
+    diff = (got != idx_cpu).nonzero().flatten().numpy()
+    near = 0
+    if len(diff):
+        r = nn.quantize(x[torch.from_numpy(diff)].numpy(), "B")
+        near = int(r["near_tie"].sum())
+    base = {
         "value": n / dt,
         "unit": "atoms/s",
-        "cores": torch.get_num_threads(),
+        "cores": phys,
         "kind": "port",
-        "sample": f"first {rows} rows ({n} atoms) of the config-2 QKV latent: row scale, "
-        f"autocast-bf16 matmul + max (castor.py:549-557, chunk 4096), pack; {dt:.1f} s",
+        "sample": f"first {n} atoms of the headline input (config 4): the reference's NN-B CPU path "
+        f"(autocast-bf16 matmul + max, chunk 4096, castor.py:549-557) restated with the same torch ops, "
+        f"{dt:.1f} s on {phys} threads",
+        "cpu_model": model,
+        "logical_cpus_available": logical,
     }
+    parity = {
+        "atoms_compared": n,
+        "against": "the reference's NN-B torch ops on the host (oracle/torch_ref.nn_b_indices)",
+        "disagree": int(len(diff)),
+        "near_tie": near,
+        "not_near_tie": int(len(diff)) - near,
+        "near_tie_envelope": "24 * 2^-24 * sum|x_i c_i| (any fp32 summation order)",
+    }
+    return base, parity
 
 
 def extras(device, iters=20):
@@ -245,14 +295,28 @@ def pack_time_extras(mats, iters=5):
             "note": "quantize_h24_layer (NN-P + sigma16 + 18-bit pack) on the four config-2 weights"}
 
 
-def traffic_from_profiles():
-    p = ROOT / "profiles" / "nn_kernel_c2_traffic.json"
+def traffic_from_profiles(name="nn_kernel_c4_traffic.json"):
+    """HBM bytes per nn_kernel launch measured by two rocprofv3 --pmc runs (committed under profiles/)."""
+    p = ROOT / "profiles" / name
     if p.exists():
         try:
             return json.loads(p.read_text()).get("hbm_bytes_per_launch")
         except (ValueError, OSError):
             return None
     return None
+
+
+def make_c4(device, seed=404):
+    """16,777,200 atoms, directions uniform on S^23, radius U(0, 2) * sqrt(32)."""
+    import numpy as np
+    import torch
+
+    n = C4_ROWS * C4_ATOMS_PER_ROW
+    g = torch.Generator(device=device).manual_seed(seed)
+    d = torch.randn(n, 24, generator=g, device=device)
+    x = d / d.norm(dim=1, keepdim=True) * (torch.rand(n, 1, generator=g, device=device) * 2.0 * np.sqrt(32.0))
+    del d
+    return x
 
 
 def _nn_profiled(fn, iters):
@@ -272,15 +336,16 @@ def _nn_profiled(fn, iters):
     return t, tot_ms.value / max(1, launches.value)
 
 
-def sweep_extras(device):
-    """The bulk quantizer at BASELINE config 4 and the Pollux-1920 layer of config 3.
+def sweep_extras(device, mode="bf16", steps=10):
+    """The other BASELINE quantizer configs: the config-2 and config-3 requantize steps.
 
-    config 4: 16,777,200 atoms (209,715 rows of 1920) with directions on S^23
-    and radius U(0, 2) * sqrt(32), fed to quantize_indices (NN-B).  config 3:
-    the fused requantize (as the headline step) of the four Pollux-1920
-    latents, then quantize_indices on their lattice-unit atoms with 5% replaced
-    by midpoints of code pairs at raw inner product 16 (+ N(0, 1e-3) noise)
-    and 5% by random directions at norm sqrt 2 (the origin boundary).
+    config 2: the fused requantize (row scale, NN-B, pack, reconstructed
+    weight) of the four Pollux-1152 latents, per latent (the reference's
+    per-parameter loop) and as one batched sweep.  config 3: the same step on
+    the four Pollux-1920 latents, then quantize_indices on their lattice-unit
+    atoms with 5% replaced by midpoints of code pairs at raw inner product 16
+    (+ N(0, 1e-3) noise) and 5% by random directions at norm sqrt 2 (the
+    origin boundary).
     """
     import numpy as np
     import torch
@@ -288,19 +353,26 @@ def sweep_extras(device):
     from pollux_amd import castor
 
     out = {}
-    n = 209_715 * 80
-    g = torch.Generator(device=device).manual_seed(404)
-    d = torch.randn(n, 24, generator=g, device=device)
-    x = d / d.norm(dim=1, keepdim=True) * (torch.rand(n, 1, generator=g, device=device) * 2.0 * np.sqrt(32.0))
-    del d
-    castor.quantize_indices(x, mode="bf16")
-    t, k_ms = _nn_profiled(lambda: castor.quantize_indices(x, mode="bf16"), 3)
-    out["config4_quantize"] = {
-        "atoms": n, "ms": t * 1e3, "atoms_per_s": n / t, "nn_kernel_ms": k_ms,
-        "nn_kernel_mfma_frac": FLOP_PER_ATOM * n / (k_ms / 1e3) / PEAK_BF16_FLOPS,
-        "note": "quantize_indices (NN-B: bf16 scores, lowest index) on uniform-sphere atoms"}
-    del x
-    torch.cuda.empty_cache()
+    mats2 = make_c2(device)
+    atoms2 = sum(r * c // 24 for r, c in C2_SHAPES)
+
+    def step2():
+        for w in mats2:
+            castor.requantize_h24(w, mode=mode)
+
+    step2()
+    t, k_ms = _nn_profiled(step2, steps)
+    out["config2_requantize"] = {
+        "atoms": atoms2, "ms_per_step": t * 1e3, "atoms_per_s": atoms2 / t, "nn_kernel_ms_avg": k_ms,
+        "nn_kernel_mfma_frac": FLOP_PER_ATOM * atoms2 / 4 / (k_ms / 1e3) / PEAK_BF16_FLOPS,
+        "note": "fused row scale + NN-B + pack + reconstructed weight of QKV 3456x1152, O 1152x1152, up 4608x1152, "
+                "down 1152x4608 (bf16-rounded N(0, 0.02) master weights), one requantize_h24 call per latent "
+                "(pollux.py:828-884); nn_kernel_mfma_frac over the average of the four launches"}
+    t_b = time_gpu(lambda: castor.requantize_h24_many(mats2, mode=mode), steps, 2)
+    out["config2_requantize_batched"] = {
+        "ms_per_step": t_b * 1e3, "atoms_per_s": atoms2 / t_b,
+        "note": "the same step as one requantize_h24_many call (plx_requantize_batch, one sweep for all four)"}
+    del mats2
 
     shapes = [(5760, 1920), (1920, 1920), (7680, 1920), (1920, 7680)]
     g = torch.Generator(device=device).manual_seed(303)
@@ -513,20 +585,45 @@ def decode_extras(device, prompt_len=64, new_tokens=128):
     return out
 
 
+def gemv_headline(gemv):
+    """The metric's "dequant-GEMV GB/s at d=1920" from the config-5 batch-1 rows of gemv_extras."""
+    rows = {}
+    tot_bytes = tot_s = 0.0
+    for name, (of, inf) in (("up_7680x1920", (7680, 1920)), ("down_1920x7680", (1920, 7680))):
+        us = gemv[f"{name}_M1_us"]
+        nbytes = (of * inf // 24 + 3) // 4 * 9 + 2 * of + 2 * inf + 4 * of
+        rows[name] = {"us_per_call": us, "compressed_bytes": nbytes, "GBps": nbytes / (us * 1e-6) / 1e9,
+                      "hbm_frac": nbytes / (us * 1e-6) / PEAK_HBM_BPS}
+        tot_bytes += nbytes
+        tot_s += us * 1e-6
+    return {
+        "GBps": tot_bytes / tot_s / 1e9,
+        "unit": "GB/s",
+        "hbm_frac": tot_bytes / tot_s / PEAK_HBM_BPS,
+        "peak": PEAK_HBM_BPS / 1e9,
+        "per_matrix": rows,
+        "workload": "BASELINE config 5 at batch 1: y = x W^T with W the packed 18-bit indices + fp16 row scales "
+        "of a 7680x1920 and a 1920x7680 weight (never materialised), bf16 x, fp32 accumulation and output",
+        "bytes": "compressed stream: packed indices + sigma16 + x (bf16) + y (fp32) per call",
+        "timing": "HIP graph of 200 calls on distinct packed copies (276 MB, above the 256 MB MALL), replayed 5x",
+    }
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--cpu-atoms", type=int, default=165_888, help="CPU baseline sample size (atoms)")
+    ap.add_argument("--cpu-atoms", type=int, default=262_144, help="CPU baseline sample size (atoms)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true")
     ap.add_argument("--mode", default="bf16", choices=["bf16", "fp32"])
     ap.add_argument(
         "--pmc-workload",
-        action="store_true",
+        choices=["c4", "c2"],
+        default=None,
         help="for rocprofv3 --pmc runs: 5 copies of a 256 MiB fp32 tensor (HBM-counter calibration), then "
-        "--steps config-2 steps; prints nothing",
+        "--steps headline (c4) steps or config-2 requantize steps (c2); prints nothing",
     )
     ap.add_argument(
         "--decode-workload",
@@ -563,36 +660,39 @@ def main() -> int:
         print(decode_workload(dev, args.decode_workload), flush=True)
         return 0
 
-    mats = make_c2(dev)
-    atoms = sum(r * c // 24 for r, c in C2_SHAPES)
-
-    def step():
-        for w in mats:
-            castor.requantize_h24(w, mode=args.mode)
-
-    def step_batched():
-        # one scoring sweep over the layer's four latents (plx_requantize_batch)
-        castor.requantize_h24_many(mats, mode=args.mode)
-
     if args.pmc_workload:
         src = torch.ones(64 * 1024 * 1024, dtype=torch.float32, device=dev)  # 256 MiB
         dst = torch.empty_like(src)
         for _ in range(5):
             dst.copy_(src)
-        for _ in range(args.steps):
-            step()
+        del src, dst
+        if args.pmc_workload == "c2":
+            mats = make_c2(dev)
+            for _ in range(args.steps):
+                for w in mats:
+                    castor.requantize_h24(w, mode=args.mode)
+        else:
+            x = make_c4(dev)
+            for _ in range(args.steps):
+                castor.quantize_indices(x, mode=args.mode)
         torch.cuda.synchronize()
         return 0
 
-    log(f"[bench] warmup {args.warmup} steps, workload config 2 ({atoms} atoms/step)")
+    x = make_c4(dev)
+    atoms = x.shape[0]
+
+    def step():
+        return castor.quantize_indices(x, mode=args.mode)
+
+    log(f"[bench] warmup {args.warmup} steps, workload config 4 ({atoms} atoms/step)")
     for _ in range(args.warmup):
-        step()
+        idx = step()
     torch.cuda.synchronize()
     _lib.check(lib.plx_profile_begin(), "plx_profile_begin")
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
-        step()
+        idx = step()
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     import ctypes
@@ -617,6 +717,7 @@ def main() -> int:
         "kernel_launches": int(launches.value),
         "kernel_avg_ms": tot_ms.value / max(1, launches.value),
         "flop_per_atom": FLOP_PER_ATOM,
+        "flop_per_launch": FLOP_PER_ATOM * atoms,
         "mfma_issue_frac": achieved * 32 / 24 / PEAK_BF16_FLOPS,
     }
 
@@ -634,30 +735,34 @@ def main() -> int:
         "dtype": "bf16",
         "data": "synthetic",
         "config": {
-            "workload": "BASELINE config 2: Pollux-1152 single-layer requantize (row scale + NN-B quantize + "
-            "18-bit pack + reconstructed weight) of QKV 3456x1152, O 1152x1152, up 4608x1152, down 1152x4608",
+            "workload": "BASELINE config 4: bulk NN-B quantize of 16,777,200 24-d fp32 atoms (209,715 rows of "
+            "1920, the config's 16,777,216 rounded down to whole rows), directions uniform on S^23, radius "
+            "U(0, 2) * sqrt(32), fed directly as quantizer input; fp32 atoms in HBM -> int32 indices",
             "atoms_per_step": atoms,
-            "call": "castor.requantize_h24 per latent, as the reference's per-parameter loop (pollux.py:828-884)",
+            "call": "castor.quantize_indices (plx_quantize: operand prep, nn_kernel scoring sweep, resolve)",
             "nn_mode": "NN-B (bf16 scores)" if args.mode == "bf16" else "NN-T (fp32 scores)",
-            "seed": 2024,
+            "seed": 404,
         },
         "roofline": roofline,
     }
+    log("[bench] dequant-GEMV / GEMM at config 5")
+    gemv = gemv_extras(dev)
+    result["dequant_gemv"] = gemv_headline(gemv)
+    if not args.no_cpu_baseline:
+        log(f"[bench] CPU baseline + parity on {args.cpu_atoms} atoms")
+        result["cpu_baseline"], result["parity"] = cpu_baseline(x, idx, args.cpu_atoms)
+    del x, idx
+    torch.cuda.empty_cache()
     if not args.no_extras:
-        log("[bench] extras: pack / unpack / dequant at config-4 scale; dequant-GEMV/GEMM at config 5")
+        log("[bench] extras: config 2 / 3 steps, pack / unpack / dequant at config-4 scale, optimiser, decode")
         result["extras"] = extras(dev)
-        t_b = time_gpu(step_batched, args.steps, 2)
-        result["extras"]["requantize_batched"] = {
-            "ms_per_step": t_b * 1e3, "atoms_per_s": atoms / t_b,
-            "note": "the same step as one requantize_h24_many call (plx_requantize_batch, one sweep for all four)"}
-        result["extras"]["dequant_linear"] = gemv_extras(dev)
+        result["extras"]["dequant_linear"] = gemv
+        result["extras"]["quantizer_sweeps"] = sweep_extras(dev, args.mode)
+        mats = make_c2(dev)
         result["extras"]["optimizer_step"] = optim_extras(dev, mats)
         result["extras"]["pack_time_nn_p"] = pack_time_extras(mats)
+        del mats
         result["extras"]["packed_decode"] = decode_extras(dev)
-        result["extras"]["quantizer_sweeps"] = sweep_extras(dev)
-    if not args.no_cpu_baseline:
-        log(f"[bench] CPU baseline on {args.cpu_atoms} atoms")
-        result["cpu_baseline"] = cpu_baseline(mats, args.cpu_atoms)
     print(json.dumps(result), flush=True)
     return 0
 

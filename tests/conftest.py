@@ -28,3 +28,26 @@ def seeded(seed: int):
     g = torch.Generator()
     g.manual_seed(seed)
     return g
+
+
+# Near-tie / mismatch counts recorded by the parity tests; printed in the
+# terminal summary (visible under -q) and written to gpurun_out/ when present.
+PARITY_RECORDS: list = []
+
+
+@pytest.fixture(scope="session")
+def parity_report():
+    return PARITY_RECORDS
+
+
+def pytest_terminal_summary(terminalreporter, exitstatus, config):
+    if not PARITY_RECORDS:
+        return
+    import json
+
+    terminalreporter.section("index parity vs the reference (disagreements by class)")
+    for r in PARITY_RECORDS:
+        terminalreporter.write_line(json.dumps(r))
+    out = ROOT / "gpurun_out"
+    if out.is_dir():
+        (out / "parity_report.json").write_text(json.dumps(PARITY_RECORDS, indent=1))
