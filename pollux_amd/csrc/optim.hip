@@ -2,10 +2,16 @@
 // pollux_step, pollux.py:836-878); the requantize that follows it
 // (pollux.py:880-884) reuses the quantizer's launch path.
 //
-// One thread per 24-element atom reads grad, m, v and the latent once and
-// writes m, v and the latent once.  Every operation reproduces one torch op of
-// the reference and its rounding (fp32 tensors, Python floats entering as
-// fp32, as torch evaluates them on the CPU):
+// A block of 256 threads owns 256 atoms (6,144 elements = 1,536 float4) and
+// reads grad, m, v and the latent once and writes m, v and the latent once,
+// all as float4 streams in which consecutive lanes touch consecutive 16-byte
+// pieces (thread t moves pieces t, t+256, ..., t+1280), so every wave access
+// is 1 KiB contiguous.  The elementwise part runs on those pieces; the capped
+// step s goes through LDS, where thread t computes atom t's norm in the
+// reference's order and its cap factor, which the latent update reads back
+// per piece.  Every operation reproduces one torch op of the reference and
+// its rounding (fp32 tensors, Python floats entering as fp32, as torch
+// evaluates them on the CPU):
 //   m   = fma(g, 1-b1, m*b1)                 m.mul_(b1).add_(g, alpha=1-b1)
 //   v   = fma((1-b2)*g, g, v*b2)             v.mul_(b2).addcmul_(g, g, value=1-b2)
 //   q   = (m/bc1) / (sqrt(v/bc2) + eps)      m_unbiased / denom
@@ -34,25 +40,9 @@
 namespace plx {
 namespace {
 
-constexpr int kOptThreads = 256;
-
-__device__ __forceinline__ void load24(const float *__restrict__ p, float *v) {
-  const float4 *q = reinterpret_cast<const float4 *>(p);
-#pragma unroll
-  for (int i = 0; i < 6; ++i) {
-    const float4 t = q[i];
-    v[4 * i] = t.x;
-    v[4 * i + 1] = t.y;
-    v[4 * i + 2] = t.z;
-    v[4 * i + 3] = t.w;
-  }
-}
-
-__device__ __forceinline__ void store24(float *__restrict__ p, const float *v) {
-  float4 *q = reinterpret_cast<float4 *>(p);
-#pragma unroll
-  for (int i = 0; i < 6; ++i) q[i] = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
-}
+constexpr int kOptThreads = 256;                     // = atoms per block
+constexpr int kOptPieces = kOptThreads * kDim / 4;   // float4 pieces per block (1,536)
+constexpr int kOptPerThread = kOptPieces / kOptThreads;  // 6
 
 __global__ __launch_bounds__(kOptThreads) void adam_h24_kernel(const float *__restrict__ grad, float *__restrict__ m,
                                                                float *__restrict__ v, float *__restrict__ latent,
@@ -61,53 +51,77 @@ __global__ __launch_bounds__(kOptThreads) void adam_h24_kernel(const float *__re
   // no contraction: a multiply feeding an add (latent * wdf + s) stays two
   // roundings, as in the reference; every FMA below is an explicit __fmaf_rn
 #pragma clang fp contract(off)
+  __shared__ __align__(16) float sl[kOptThreads * kDim];  // the block's capped-step inputs s, atom-major
+  __shared__ float fac_s[kOptThreads];                    // per atom: min(cap / (|s| + eps), 1)
   __shared__ float red[kOptThreads];
-  const int64_t a = static_cast<int64_t>(blockIdx.x) * kOptThreads + threadIdx.x;
-  float e2 = 0.f;  // this atom's sum of squared capped steps
-  if (a < n_atoms) {
-    const float b1 = scal[0], omb1 = scal[1], b2 = scal[2], omb2 = scal[3];
-    const float bc1 = scal[4], bc2 = scal[5], neg_scale = scal[6], wdf = scal[7], cap = scal[8];
-    const float eps = __uint_as_float(kEpsBits);
-    float g[kDim], mm[kDim], vv[kDim], s[kDim];
-    load24(grad + a * kDim, g);
-    load24(m + a * kDim, mm);
-    load24(v + a * kDim, vv);
+  const int tid = threadIdx.x;
+  const int64_t a0 = static_cast<int64_t>(blockIdx.x) * kOptThreads;
+  const int64_t pieces = min(static_cast<int64_t>(kOptPieces), (n_atoms - a0) * (kDim / 4));  // whole atoms
+  const float4 *g4 = reinterpret_cast<const float4 *>(grad + a0 * kDim);
+  float4 *m4 = reinterpret_cast<float4 *>(m + a0 * kDim);
+  float4 *v4 = reinterpret_cast<float4 *>(v + a0 * kDim);
+  float4 *l4 = reinterpret_cast<float4 *>(latent + a0 * kDim);
+  const float b1 = scal[0], omb1 = scal[1], b2 = scal[2], omb2 = scal[3];
+  const float bc1 = scal[4], bc2 = scal[5], neg_scale = scal[6], wdf = scal[7], cap = scal[8];
+  const float eps = __uint_as_float(kEpsBits);
+
+  float4 lat[kOptPerThread];
 #pragma unroll
-    for (int c = 0; c < kDim; ++c) {
-      mm[c] = __fmaf_rn(g[c], omb1, mm[c] * b1);
-      vv[c] = __fmaf_rn(omb2 * g[c], g[c], vv[c] * b2);
-      const float mu = mm[c] / bc1;
-      const float den = sqrtf(vv[c] / bc2) + eps;
-      s[c] = neg_scale * (mu / den);
+  for (int j = 0; j < kOptPerThread; ++j) {
+    const int i = tid + j * kOptThreads;
+    if (i >= pieces) continue;
+    const float4 g = g4[i];
+    float4 mm = m4[i], vv = v4[i];
+    lat[j] = l4[i];
+    float gv[4] = {g.x, g.y, g.z, g.w}, mv[4] = {mm.x, mm.y, mm.z, mm.w}, vw[4] = {vv.x, vv.y, vv.z, vv.w};
+    float sv[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      mv[c] = __fmaf_rn(gv[c], omb1, mv[c] * b1);
+      vw[c] = __fmaf_rn(omb2 * gv[c], gv[c], vw[c] * b2);
+      const float mu = mv[c] / bc1;
+      const float den = sqrtf(vw[c] / bc2) + eps;
+      sv[c] = neg_scale * (mu / den);
     }
-    store24(m + a * kDim, mm);
-    store24(v + a * kDim, vv);
+    m4[i] = make_float4(mv[0], mv[1], mv[2], mv[3]);
+    v4[i] = make_float4(vw[0], vw[1], vw[2], vw[3]);
+    reinterpret_cast<float4 *>(sl)[i] = make_float4(sv[0], sv[1], sv[2], sv[3]);
+  }
+  __syncthreads();
+  // atom tid: torch.linalg.vector_norm over its 24 values (8 FMA accumulators,
+  // lane i taking coordinates i, i+8, i+16, then summed in lane order)
+  if (a0 + tid < n_atoms) {
+    const float *sa = sl + tid * kDim;
     float acc[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) acc[i] = __fmaf_rn(s[i + 16], s[i + 16], __fmaf_rn(s[i + 8], s[i + 8], s[i] * s[i]));
+    for (int i = 0; i < 8; ++i) acc[i] = __fmaf_rn(sa[i + 16], sa[i + 16], __fmaf_rn(sa[i + 8], sa[i + 8], sa[i] * sa[i]));
     float n2 = acc[0];
 #pragma unroll
     for (int i = 1; i < 8; ++i) n2 = n2 + acc[i];
     // torch evaluates `cap / t` (a Python float over a tensor) as reciprocal(t) * cap
-    const float fac = fminf((1.0f / (sqrtf(n2) + eps)) * cap, 1.0f);
-    float lat[kDim];
-    load24(latent + a * kDim, lat);
-#pragma unroll
-    for (int c = 0; c < kDim; ++c) {
-      const float sc = s[c] * fac;
-      lat[c] = lat[c] * wdf + sc;
-      e2 = __fmaf_rn(sc, sc, e2);
-    }
-    store24(latent + a * kDim, lat);
+    fac_s[tid] = fminf((1.0f / (sqrtf(n2) + eps)) * cap, 1.0f);
   }
-  red[threadIdx.x] = e2;
+  __syncthreads();
+  float e2 = 0.f;  // this thread's sum of squared capped steps
+#pragma unroll
+  for (int j = 0; j < kOptPerThread; ++j) {
+    const int i = tid + j * kOptThreads;
+    if (i >= pieces) continue;
+    const float fac = fac_s[i / (kDim / 4)];
+    const float4 sv = reinterpret_cast<const float4 *>(sl)[i];
+    const float sc[4] = {sv.x * fac, sv.y * fac, sv.z * fac, sv.w * fac};
+    l4[i] = make_float4(lat[j].x * wdf + sc[0], lat[j].y * wdf + sc[1], lat[j].z * wdf + sc[2], lat[j].w * wdf + sc[3]);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) e2 = __fmaf_rn(sc[c], sc[c], e2);
+  }
+  red[tid] = e2;
   __syncthreads();
 #pragma unroll
   for (int w = kOptThreads / 2; w > 0; w >>= 1) {
-    if (threadIdx.x < w) red[threadIdx.x] = red[threadIdx.x] + red[threadIdx.x + w];
+    if (tid < w) red[tid] = red[tid] + red[tid + w];
     __syncthreads();
   }
-  if (threadIdx.x == 0) partial[blockIdx.x] = red[0];
+  if (tid == 0) partial[blockIdx.x] = red[0];
 }
 
 // norm_out[0] = sqrt(sum of the block partials), summed in a fixed order.

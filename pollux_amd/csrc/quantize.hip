@@ -36,15 +36,23 @@
 //   only lose to the origin threshold R starts at).  NN-B raises R to the
 //   largest fp32 that still rounds to the new bucket, so later codes in the
 //   same bucket never displace the earlier group; NN-T raises R to the score.
-//   Each (atom, slice) ends as a 16-byte record: the best key and, per lane,
-//   the best group of the lanes that hold it.
+//   Each (atom, slice) ends as one atomic max into the atom's key word:
+//   (best bucket or score, 1023 - earliest group reaching it, mask of the
+//   atom's four lanes whose earliest group that is), 32 bits for NN-B
+//   (bucket << 16 | (1023 - g) << 6 | mask << 2), 64 bits for NN-T / NN-P
+//   (score << 32 | (1023 - g) << 4 | mask).  Slices own disjoint groups, so
+//   the maximum over slices is the highest bucket / score, then the earliest
+//   group holding it -- the group of the lowest code the selection rule
+//   wants -- and no two slices write the same (score, group).  prep_kernel
+//   (NN-P: clear_keys_kernel) zeroes the keys; 0 means the origin threshold
+//   was never beaten.
 //
-// resolve_kernel -- per atom the maximum key over the slices, then an
-//   exact-product rescan (v_dot2_f32_bf16; NN-P: fp64 dot products of the
-//   fp32 atom and the fp32 codebook rows, exact up to 2^-48) of the few
-//   groups that hold it to find the lowest code, kG lanes per group with
-//   coalesced table reads, then the index and the packed 9-byte groups.  Both
-//   fp32 sums (MFMA, dot2) lie within 2^-20 * sum|x_i c_i| of the exact score
+// resolve_kernel -- per atom its key, then an exact-product rescan
+//   (v_dot2_f32_bf16; NN-P: fp64 dot products of the fp32 atom and the fp32
+//   codebook rows, exact up to 2^-48) of the key's group in the lanes of its
+//   mask to find the lowest code, kG lanes per (group, lane) with coalesced
+//   table reads, then the index and the packed 9-byte groups.  Both fp32 sums
+//   (MFMA, dot2) lie within 24 * 2^-24 * sum|x_i c_i| of the exact score
 //   (MFMA measured at < 2^-22), so the result equals the exact-score answer
 //   on every atom that is not a near-tie within that envelope.
 
@@ -130,12 +138,16 @@ __device__ __forceinline__ void load_coords8(const float *__restrict__ src, cons
 // 16-byte plane of 8 per thread), written once per launch so the scoring
 // blocks of all slices load ready-made MFMA B operands instead of each
 // repeating the row-scale divisions.  NN-B / NN-T only.
+// Also clears the atoms' 8-byte key slots (keys8 may hold 32-bit keys in its
+// first half: NN-B), before nn_kernel merges its slices into them.
 template <bool FUSED>
 __global__ __launch_bounds__(256) void prep_kernel(const float *__restrict__ src, const float *__restrict__ sigma,
-                                                   int64_t atoms_per_row, int64_t n_atoms, uint4 *__restrict__ xb) {
+                                                   int64_t atoms_per_row, int64_t n_atoms, uint4 *__restrict__ xb,
+                                                   uint2 *__restrict__ keys8) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;  // plane i % 3 of atom i / 3
   if (i >= n_atoms * 3) return;
   const int64_t a = i / 3;
+  if (i == 3 * a) keys8[a] = make_uint2(0u, 0u);
   float v[8];
   load_coords8<FUSED>(src, sigma, atoms_per_row, n_atoms, a, static_cast<int>(i - 3 * a), v);
   uint4 w;
@@ -144,6 +156,12 @@ __global__ __launch_bounds__(256) void prep_kernel(const float *__restrict__ src
   w.z = bf16_rne_bits(v[4]) | (bf16_rne_bits(v[5]) << 16);
   w.w = bf16_rne_bits(v[6]) | (bf16_rne_bits(v[7]) << 16);
   xb[i] = w;
+}
+
+// NN-P has no prep pass: its key slots are cleared here.
+__global__ __launch_bounds__(256) void clear_keys_kernel(uint2 *__restrict__ keys8, int64_t n) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i < n) keys8[i] = make_uint2(0u, 0u);
 }
 
 // NN-B tracking key of a group: bucket (round-half-up, see raised_threshold)
@@ -160,8 +178,7 @@ __device__ __forceinline__ int group_key(int gm, int group) {
 template <int MODE>
 __global__ __launch_bounds__(kThreads, 2) void nn_kernel(const void *__restrict__ src, int64_t n_atoms,
                                                           const uint8_t *__restrict__ tiles, int n_slices,
-                                                          int tiles_per_slice, uint32_t *__restrict__ keys,
-                                                          uint2 *__restrict__ groups) {
+                                                          int tiles_per_slice, void *__restrict__ keys) {
   __shared__ __align__(16) uint8_t lds[2][kStageBytes];
 
   const int slice = static_cast<int>(blockIdx.x % static_cast<unsigned>(n_slices));
@@ -330,60 +347,68 @@ __global__ __launch_bounds__(kThreads, 2) void nn_kernel(const void *__restrict_
     }
   }
 
-  // ---- per (atom, slice) record for the resolve kernel ----
-  // key: the slice's best bucket (NN-B, bf16 bits) or fp32 score bits (NN-T),
-  // 0 when nothing beat the origin threshold; then, for each of the four lanes
-  // of the atom, its best group if it holds the slice maximum (else 0xFFFF).
-  // NN-B: only the lanes whose earliest group at that bucket is the slice's
-  // earliest -- the lowest code of the bucket lies in that group.
+  // ---- merge this slice into the atom's key ----
+  // The four lanes of atom j (j, j+16, j+32, j+48) hold the slice's best
+  // per lane; their maximum is the slice's best (score, earliest group) and
+  // the mask names the lanes that reached it in that group.
 #pragma unroll
   for (int at = 0; at < kAT; ++at) {
-    int Rm = R[at];
-    Rm = max(Rm, __shfl_xor(Rm, 16, 64));
-    Rm = max(Rm, __shfl_xor(Rm, 32, 64));
-    uint32_t g16;
-    if constexpr (MODE == kModeB)
-      g16 = (R[at] == Rm && Rm != initial_threshold<MODE>()) ? 0xFFFFu - (static_cast<uint32_t>(R[at]) & 0xFFFFu)
-                                                              : 0xFFFFu;
-    else
-      g16 = (best[at] >= 0 && R[at] == Rm) ? static_cast<uint32_t>(best[at]) : 0xFFFFu;
-    const uint32_t g0 = static_cast<uint32_t>(__shfl(static_cast<int>(g16), j, 64));
-    const uint32_t g1 = static_cast<uint32_t>(__shfl(static_cast<int>(g16), j + 16, 64));
-    const uint32_t g2 = static_cast<uint32_t>(__shfl(static_cast<int>(g16), j + 32, 64));
-    const uint32_t g3 = static_cast<uint32_t>(__shfl(static_cast<int>(g16), j + 48, 64));
     const int64_t a = wave_atom0 + at * 16 + j;
-    if (q == 0 && a < n_atoms) {
-      const bool hit = Rm != initial_threshold<MODE>();
-      const uint32_t key = hit ? (MODE == kModeB ? static_cast<uint32_t>(Rm) >> 16 : static_cast<uint32_t>(Rm)) : 0u;
-      keys[static_cast<int64_t>(slice) * n_atoms + a] = key;
-      groups[static_cast<int64_t>(slice) * n_atoms + a] = make_uint2(g0 | (g1 << 16), g2 | (g3 << 16));
+    if constexpr (MODE == kModeB) {
+      int Rm = R[at];
+      Rm = max(Rm, __shfl_xor(Rm, 16, 64));
+      Rm = max(Rm, __shfl_xor(Rm, 32, 64));
+      const uint64_t bal = __ballot(R[at] == Rm);  // bit l: lane l holds the maximum
+      const uint32_t mask = static_cast<uint32_t>(((bal >> j) & 1u) | ((bal >> (j + 15)) & 2u) |
+                                                  ((bal >> (j + 30)) & 4u) | ((bal >> (j + 45)) & 8u));
+      const uint32_t g = 0xFFFFu - (static_cast<uint32_t>(Rm) & 0xFFFFu);
+      // no hit: key 0, which leaves the atom's key as it is (a select, not a
+      // branch: a conditional atomic here costs the main loop ~20 VGPRs)
+      const uint32_t key = Rm != initial_threshold<MODE>()
+                               ? (static_cast<uint32_t>(Rm) & 0xFFFF0000u) | ((0x3FFu - g) << 6) | (mask << 2)
+                               : 0u;
+      if (q == 0 && a < n_atoms) atomicMax(static_cast<unsigned int *>(keys) + a, key);
+    } else {
+      // (score, 1023 - group) as one 64-bit value, lanes that never beat the threshold 0
+      const bool hit = best[at] >= 0;
+      uint64_t v = hit ? (static_cast<uint64_t>(static_cast<uint32_t>(R[at])) << 32) |
+                             (static_cast<uint64_t>(0x3FFu - static_cast<uint32_t>(best[at])) << 4)
+                       : 0ull;
+      uint64_t vm = v;
+      uint64_t o = static_cast<uint64_t>(__shfl_xor(static_cast<long long>(vm), 16, 64));
+      vm = o > vm ? o : vm;
+      o = static_cast<uint64_t>(__shfl_xor(static_cast<long long>(vm), 32, 64));
+      vm = o > vm ? o : vm;
+      const uint64_t bal = __ballot(v == vm);
+      const uint64_t mask = ((bal >> j) & 1u) | ((bal >> (j + 15)) & 2u) | ((bal >> (j + 30)) & 4u) |
+                            ((bal >> (j + 45)) & 8u);
+      const uint64_t key = vm != 0ull ? vm | mask : 0ull;
+      if (q == 0 && a < n_atoms) atomicMax(static_cast<unsigned long long *>(keys) + a, static_cast<unsigned long long>(key));
     }
   }
 }
 
-// Resolve: per block 256 atoms, in rounds.
-//   scan     thread per atom: the maximum key M over the slices, the atom's
-//            coordinates into LDS (bf16 pairs; NN-P: fp32), then up to
-//            kRsPerRound candidate slots (slice, lane) whose record holds M,
-//            each naming a group of kG tiles x 4 codes of that lane;
+// Resolve: per block 256 atoms.
+//   scan     thread per atom: its key (the bucket or score M, the earliest
+//            group G holding it, the lanes of G that reach it), the atom's
+//            coordinates into LDS (bf16 pairs; NN-P: fp32), one candidate
+//            per lane of the mask, each naming G's kG tiles x 4 codes of that lane;
 //   compact  a block-wide prefix sum packs the candidates into one list;
 //   rescan   kG lanes per candidate, lane t scoring the 4 codes of tile t of
-//            the group (NN-B/T: 192 B contiguous in the lane-major bf16
-//            table, v_dot2_f32_bf16 = exact bf16 products, fp32 sums; NN-P:
-//            4 consecutive rows of the raw int8 codebook, fp64 dot products of
+//            the group (NN-B/T: 3-bit value ids from kp_dq expanded to bf16,
+//            v_dot2_f32_bf16 = exact bf16 products, fp32 sums; NN-P: 4
+//            consecutive rows of the raw int8 codebook, fp64 dot products of
 //            the fp32 atom with the fp32 codebook values, exact to 2^-48),
-//            then a 3-step shuffle reduction per candidate;
+//            then a 4-step shuffle reduction per candidate;
 //   merge    thread per atom folds its candidates' results in list order.
-// An atom with more than kRsPerRound candidates continues in the next round.
-// keys / groups / xb point at this call's first atom; the records of slice s
-// start rec_stride atoms apart (the atom count of the sweep, which may cover
-// several matrices).
+// keys / xb point at this call's first atom (a batched sweep covers several
+// matrices; each resolves its own range).
 // NN-B picks the lowest code whose bf16 score bucket equals M (falling back to
 // the best rounded score, lowest code on ties, if the fp32 sums disagree with
 // the sweep's); NN-T the highest fp32 score, lowest code on ties; NN-P the
 // highest fp64 score, lowest code on ties.  Then the int32 index and,
 // optionally, the packed 9-byte groups.
-constexpr int kRsPerRound = 4;
+constexpr int kRsPerRound = 4;  // lanes of one atom: every candidate in one round
 constexpr int kRsCap = 256 * kRsPerRound;
 
 template <int MODE>
@@ -392,9 +417,7 @@ struct RsScore {  // per-candidate / per-atom running result
 };
 
 template <int MODE, bool FUSED>
-__global__ __launch_bounds__(256) void resolve_kernel(const uint32_t *__restrict__ keys,
-                                                      const uint2 *__restrict__ groups, int n_slices,
-                                                      int64_t rec_stride, int64_t n_atoms,
+__global__ __launch_bounds__(256) void resolve_kernel(const void *__restrict__ keys, int64_t n_atoms,
                                                       const float *__restrict__ src,
                                                       const float *__restrict__ sigma, int64_t atoms_per_row,
                                                       const uint4 *__restrict__ xb, const uint8_t *__restrict__ rescan,
@@ -407,7 +430,7 @@ __global__ __launch_bounds__(256) void resolve_kernel(const uint32_t *__restrict
   __shared__ score_t res_v[kRsCap];
   __shared__ uint32_t res_code[kRsCap];
   __shared__ uint32_t res_found[MODE == kModeB ? kRsCap : 1];
-  __shared__ uint32_t Ms[256];                    // per atom: the maximum key
+  __shared__ uint32_t Ms[256];                    // per atom: the sweep's best bucket (NN-B)
   __shared__ int wave_sum[4];
   __shared__ int32_t ids[256];
   __shared__ __align__(16) uint8_t bytes[64 * 9];
@@ -416,24 +439,20 @@ __global__ __launch_bounds__(256) void resolve_kernel(const uint32_t *__restrict
   const int64_t a0 = static_cast<int64_t>(blockIdx.x) * 256;
   const int64_t a = a0 + tid;
 
-  // ---- scan: M and the slices holding it, coordinates, origin rules ----
-  // Only the 4-byte keys are read here, 8 slices' loads in flight at a time.
-  uint32_t M = 0;
-  uint64_t mask = 0;  // slices whose key equals M (n_slices <= 64)
+  // ---- scan: the key, coordinates, origin rules ----
+  uint32_t M = 0, G = 0, lanes = 0;
   bool active = false;
   if (a < n_atoms) {
-    for (int s0 = 0; s0 < n_slices; s0 += 8) {
-      uint32_t k[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) k[i] = s0 + i < n_slices ? keys[static_cast<int64_t>(s0 + i) * rec_stride + a] : 0u;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        if (k[i] > M) {
-          M = k[i];
-          mask = 0;
-        }
-        if (k[i] == M) mask |= uint64_t{1} << (s0 + i);
-      }
+    if constexpr (MODE == kModeB) {
+      const uint32_t k = static_cast<const uint32_t *>(keys)[a];
+      M = k >> 16;
+      G = 0x3FFu - ((k >> 6) & 0x3FFu);
+      lanes = (k >> 2) & 0xFu;
+    } else {
+      const uint64_t k = static_cast<const unsigned long long *>(keys)[a];
+      M = static_cast<uint32_t>(k >> 32);
+      G = 0x3FFu - static_cast<uint32_t>((k >> 4) & 0x3FFu);
+      lanes = static_cast<uint32_t>(k & 0xFu);
     }
     double nrm2 = 0.0;
 #pragma unroll
@@ -452,36 +471,21 @@ __global__ __launch_bounds__(256) void resolve_kernel(const uint32_t *__restrict
     }
     // NN-P's origin rule (pack.py:174): |x|_2 < fp32(1e-8); no scan needed
     const bool p_snap = MODE == kModeP && sqrt(nrm2) < static_cast<double>(__uint_as_float(kEpsBits));
-    active = M != 0 && !p_snap;
+    active = M != 0 && lanes != 0 && !p_snap;
   }
   Ms[tid] = M;
 
   uint32_t found = 0xFFFFFFFFu;  // NN-B: lowest code whose bucket equals M
   score_t best_v = -__builtin_inf();
   uint32_t best_code = 0xFFFFFFFFu;
-  int qpos = 0;  // next lane of the lowest slice left in mask
-  for (;;) {
-    // ---- this thread's next candidates: lanes (in order) of the slices in mask ----
+  {
+    // ---- this thread's candidates: the lanes of its mask, all in group G ----
     int nm = 0;
     if (active) {
-      int loaded = -1;
-      uint2 rec = make_uint2(0u, 0u);
-      while (mask != 0 && nm < kRsPerRound) {
-        const int s = __builtin_ctzll(mask);
-        if (s != loaded) {
-          rec = groups[static_cast<int64_t>(s) * rec_stride + a];
-          loaded = s;
-        }
-        const int qq = qpos;
-        const uint32_t g = (((qq & 2) ? rec.y : rec.x) >> (16 * (qq & 1))) & 0xFFFFu;
-        if (++qpos == 4) {
-          qpos = 0;
-          mask &= mask - 1;
-        }
-        if (g != 0xFFFFu) tmp[nm++ * 256 + tid] = static_cast<uint32_t>(tid) | static_cast<uint32_t>(qq) << 8 | g << 10;
-      }
+#pragma unroll
+      for (int qq = 0; qq < 4; ++qq)
+        if ((lanes >> qq) & 1u) tmp[nm++ * 256 + tid] = static_cast<uint32_t>(tid) | static_cast<uint32_t>(qq) << 8 | G << 10;
     }
-    const bool more = nm == kRsPerRound && mask != 0;
 
     // ---- compact: exclusive prefix sum of nm over the block ----
     int incl = nm;
@@ -612,7 +616,6 @@ __global__ __launch_bounds__(256) void resolve_kernel(const uint32_t *__restrict
       }
       if constexpr (MODE == kModeB) found = min(found, res_found[off + i]);
     }
-    if (!__syncthreads_or(more)) break;
   }
 
   int32_t id = 0;
@@ -686,23 +689,23 @@ __global__ __launch_bounds__(256) void gather_kernel(const int32_t *__restrict__
   }
 }
 
-// Codebook slices per launch: 8 keeps each XCD on its own 1.18 MB of the bf16
-// codebook (L2-resident); small launches use more slices so the grid still
-// has several waves of work-groups per CU slot.
+// Codebook slices per launch.  Blocks are dispatched round-robin over the 8
+// XCDs, so with 4 slices each XCD streams one 2.36 MB quarter of the bf16
+// codebook (L2-resident in its 4 MB L2) and each atom block's operand planes
+// are fetched by 4 XCDs (with 8 slices: 1.18 MB per XCD, planes fetched 8
+// times; measured on 16.8M atoms: 4 slices 0.5% faster, half the plane
+// traffic).  Small launches use more slices so the grid still has several
+// waves of work-groups per CU slot.
 int choose_slices(int64_t ablocks) {
-  int s = 8;
+  int s = 4;
   while (s < 64 && ablocks * s < 6144) s *= 2;
   return s;
 }
 
-// per-(atom, slice) records as two arrays: 4-byte keys, then the 8-byte lane groups
-size_t records_bytes(int64_t n_atoms) {
-  const int64_t ablocks = (n_atoms + kAtomsPerBlock - 1) / kAtomsPerBlock;
-  const size_t n_rec = static_cast<size_t>(n_atoms) * static_cast<size_t>(choose_slices(ablocks));
-  return ((n_rec * 4 + 255) & ~static_cast<size_t>(255)) + n_rec * 8;
-}
+// per-atom key slots (8 bytes; NN-B uses the first 4 n bytes as 32-bit keys)
+size_t keys_bytes(int64_t n_atoms) { return (static_cast<size_t>(n_atoms) * 8 + 255) & ~static_cast<size_t>(255); }
 
-// workspace = per-(atom, slice) records, then (NN-B / NN-T) the bf16 planes
+// workspace = per-atom keys, then (NN-B / NN-T) the bf16 planes
 template <int MODE, bool FUSED>
 int launch_mode(const float *x, const float *sigma, int64_t apr, int64_t n_atoms, const DeviceTables *tab,
                 int32_t *idx_out, uint8_t *packed_out, uint8_t *workspace, hipStream_t s) {
@@ -711,15 +714,17 @@ int launch_mode(const float *x, const float *sigma, int64_t apr, int64_t n_atoms
   const int tiles_per_slice = kPaddedTiles / n_slices;
   const int64_t grid = ablocks * n_slices;
   if (grid > 0x7FFFFFFFll) return fail(PLX_EINVAL, "quantize: %lld atoms exceed one launch", static_cast<long long>(n_atoms));
-  const size_t n_rec = static_cast<size_t>(n_atoms) * static_cast<size_t>(n_slices);
-  uint32_t *keys = reinterpret_cast<uint32_t *>(workspace);
-  uint2 *groups = reinterpret_cast<uint2 *>(workspace + ((n_rec * 4 + 255) & ~static_cast<size_t>(255)));
-  uint4 *xb = reinterpret_cast<uint4 *>(workspace + ((records_bytes(n_atoms) + 255) & ~static_cast<size_t>(255)));
+  uint2 *keys8 = reinterpret_cast<uint2 *>(workspace);
+  uint4 *xb = reinterpret_cast<uint4 *>(workspace + keys_bytes(n_atoms));
   int st;
   if (MODE != kModeP) {
     hipLaunchKernelGGL((prep_kernel<FUSED>), dim3(static_cast<unsigned>((n_atoms * 3 + 255) / 256)), dim3(256), 0, s, x,
-                       sigma, apr, n_atoms, xb);
+                       sigma, apr, n_atoms, xb, keys8);
     if ((st = check_launch("prep_kernel")) != PLX_OK) return st;
+  } else {
+    hipLaunchKernelGGL(clear_keys_kernel, dim3(static_cast<unsigned>((n_atoms + 255) / 256)), dim3(256), 0, s, keys8,
+                       n_atoms);
+    if ((st = check_launch("clear_keys_kernel")) != PLX_OK) return st;
   }
   profile_before(s);
   const uint8_t *tiles = MODE == kModeP ? tab->kp_raw_tiles : tab->kp_bf16_tiles;
@@ -727,11 +732,11 @@ int launch_mode(const float *x, const float *sigma, int64_t apr, int64_t n_atoms
       MODE == kModeP ? reinterpret_cast<const uint8_t *>(tab->cb_raw) : reinterpret_cast<const uint8_t *>(tab->kp_dq);
   const void *operand = MODE == kModeP ? static_cast<const void *>(x) : static_cast<const void *>(xb);
   hipLaunchKernelGGL((nn_kernel<MODE>), dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0, s, operand, n_atoms, tiles,
-                     n_slices, tiles_per_slice, keys, groups);
+                     n_slices, tiles_per_slice, static_cast<void *>(keys8));
   if ((st = check_launch("nn_kernel")) != PLX_OK) return st;
   profile_after(s);
   hipLaunchKernelGGL((resolve_kernel<MODE, FUSED>), dim3(static_cast<unsigned>((n_atoms + 255) / 256)), dim3(256), 0, s,
-                     keys, groups, n_slices, n_atoms, n_atoms, x, sigma, apr, xb, rescan, idx_out, packed_out);
+                     static_cast<const void *>(keys8), n_atoms, x, sigma, apr, xb, rescan, idx_out, packed_out);
   return check_launch("resolve_kernel");
 }
 
@@ -739,7 +744,7 @@ int launch_mode(const float *x, const float *sigma, int64_t apr, int64_t n_atoms
 
 size_t quantize_workspace_bytes(int64_t n_atoms) {
   if (n_atoms <= 0) return 0;
-  return ((records_bytes(n_atoms) + 255) & ~static_cast<size_t>(255)) + static_cast<size_t>(n_atoms) * 48;
+  return keys_bytes(n_atoms) + static_cast<size_t>(n_atoms) * 48;
 }
 
 int launch_quantize(const float *x, const float *sigma, int64_t rows, int64_t cols, int64_t n_atoms, int mode,
@@ -793,10 +798,8 @@ int launch_batch_mode(const RequantItem *items, int n_items, const DeviceTables 
   const int tiles_per_slice = kPaddedTiles / n_slices;
   const int64_t grid = ablocks * n_slices;
   if (grid > 0x7FFFFFFFll) return fail(PLX_EINVAL, "requantize_batch: %lld atoms exceed one launch", static_cast<long long>(total));
-  const size_t n_rec = static_cast<size_t>(total) * static_cast<size_t>(n_slices);
-  uint32_t *keys = reinterpret_cast<uint32_t *>(workspace);
-  uint2 *groups = reinterpret_cast<uint2 *>(workspace + ((n_rec * 4 + 255) & ~static_cast<size_t>(255)));
-  uint4 *xb = reinterpret_cast<uint4 *>(workspace + ((records_bytes(total) + 255) & ~static_cast<size_t>(255)));
+  uint2 *keys8 = reinterpret_cast<uint2 *>(workspace);
+  uint4 *xb = reinterpret_cast<uint4 *>(workspace + keys_bytes(total));
   int st;
   int64_t off = 0;
   for (int i = 0; i < n_items; ++i) {
@@ -805,13 +808,14 @@ int launch_batch_mode(const RequantItem *items, int n_items, const DeviceTables 
     if (n == 0) continue;
     if ((st = launch_row_rms(it.latent, it.rows, it.cols, it.sigma, nullptr, s)) != PLX_OK) return st;
     hipLaunchKernelGGL((prep_kernel<true>), dim3(static_cast<unsigned>((n * 3 + 255) / 256)), dim3(256), 0, s, it.latent,
-                       it.sigma, apr, n, xb + off * 3);
+                       it.sigma, apr, n, xb + off * 3, keys8 + off);
     if ((st = check_launch("prep_kernel")) != PLX_OK) return st;
     off += n;
   }
   profile_before(s);
   hipLaunchKernelGGL((nn_kernel<MODE>), dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0, s,
-                     static_cast<const void *>(xb), total, tab->kp_bf16_tiles, n_slices, tiles_per_slice, keys, groups);
+                     static_cast<const void *>(xb), total, tab->kp_bf16_tiles, n_slices, tiles_per_slice,
+                     static_cast<void *>(keys8));
   if ((st = check_launch("nn_kernel")) != PLX_OK) return st;
   profile_after(s);
   off = 0;
@@ -820,7 +824,9 @@ int launch_batch_mode(const RequantItem *items, int n_items, const DeviceTables 
     const int64_t apr = it.cols / kDim, n = it.rows * apr;
     if (n == 0) continue;
     hipLaunchKernelGGL((resolve_kernel<MODE, true>), dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s,
-                       keys + off, groups + off, n_slices, total, n, it.latent, it.sigma, apr, xb + off * 3,
+                       MODE == kModeB ? static_cast<const void *>(reinterpret_cast<const uint32_t *>(keys8) + off)
+                                      : static_cast<const void *>(keys8 + off),
+                       n, it.latent, it.sigma, apr, xb + off * 3,
                        reinterpret_cast<const uint8_t *>(tab->kp_dq), it.idx, it.packed);
     if ((st = check_launch("resolve_kernel")) != PLX_OK) return st;
     if (it.weight) {
