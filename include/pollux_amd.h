@@ -76,8 +76,10 @@ int plx_codebook_f32(float *out, int64_t n_floats);
 int plx_codebook_fingerprint(float *out16);
 
 /* Build (once per device) the device-resident codebook tables on the current
- * device.  Every compute entry point calls it lazily; calling it up front
- * moves the one-time upload out of the first timed call. */
+ * device and resolve the device address of plx_requantize_noalloc's scratch
+ * array.  Every compute entry point except plx_requantize_noalloc builds the
+ * tables lazily; calling it up front moves the one-time upload out of the
+ * first timed call. */
 int plx_device_init(void);
 
 /* ---- 18-bit packing (castor.py:226-260) --------------------------------- */
@@ -128,6 +130,23 @@ int plx_gather_codebook(const int32_t *idx, int64_t n, int out_dtype, void *out,
 int plx_requantize(const float *latent, int64_t rows, int64_t cols, int mode,
                    float *sigma_out, int32_t *idx_out, uint8_t *packed_out, float *weight_out,
                    void *workspace, size_t workspace_bytes, void *stream);
+
+/* plx_requantize without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving or
+ * training loops, harnesses that forbid hipMalloc).  No counterpart in the
+ * reference: it serves those callers only.  Same arguments, results and
+ * errors as plx_requantize minus the workspace, which is a library-owned
+ * device array of PLX_NOALLOC_MAX_ATOMS * 56 bytes (56 MiB) held by each
+ * device the library runs on until the process ends.  It allocates nothing:
+ * call plx_device_init() on the device first (outside any capture), which
+ * builds the codebook tables and resolves the array's address; without it
+ * the call fails with PLX_EINVAL.  More than PLX_NOALLOC_MAX_ATOMS atoms
+ * (rows * cols / 24) fail with PLX_EINVAL.  All calls on one device share
+ * the array: calls that overlap in time on one device (different streams)
+ * race and must be serialised by the caller. */
+#define PLX_NOALLOC_MAX_ATOMS 1048576
+int plx_requantize_noalloc(const float *latent, int64_t rows, int64_t cols, int mode, float *sigma_out,
+                           int32_t *idx_out, uint8_t *packed_out, float *weight_out, void *stream);
 
 /* One matrix of plx_requantize_batch: the arguments of plx_requantize. */
 typedef struct plx_requantize_item {

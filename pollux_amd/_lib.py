@@ -39,6 +39,7 @@ SIGNATURES = {
     "plx_requantize": (_int, [_vp, _i64, _i64, _int, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
     "plx_quantize_layer_pack": (_int, [_vp, _i64, _i64, _vp, _vp, _vp, _vp, _sz, _vp]),
     "plx_requantize_batch": (_int, [_vp, _int, _int, _vp, _sz, _vp]),
+    "plx_requantize_noalloc": (_int, [_vp, _i64, _i64, _int, _vp, _vp, _vp, _vp, _vp]),
     "plx_pollux_step_workspace_bytes": (_sz, [_i64, _i64]),
     "plx_pollux_step_h24": (_int, [_vp, _vp, _vp, _vp, _i64, _i64, _vp, _int, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
     "plx_quantize_int8_rows": (_int, [_vp, _i64, _i64, _vp, _vp, _vp]),

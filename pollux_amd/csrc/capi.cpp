@@ -83,7 +83,9 @@ int plx_codebook_fingerprint(float *out16) {
 
 int plx_device_init(void) {
   const DeviceTables *t = nullptr;
-  return get_tables(&t);
+  const int st = get_tables(&t);
+  if (st != PLX_OK) return st;
+  return noalloc_setup();
 }
 
 int plx_pack_indices(const void *indices, int idx_is_i64, int64_t n, uint8_t *out, void *stream) {
@@ -160,6 +162,23 @@ int plx_requantize(const float *latent, int64_t rows, int64_t cols, int mode, fl
   if (st != PLX_OK) return st;
   return launch_quantize(latent, sigma_out, rows, cols, n_atoms, mode, idx_out, packed_out, weight_out, workspace,
                          workspace_bytes, as_stream(stream));
+}
+
+int plx_requantize_noalloc(const float *latent, int64_t rows, int64_t cols, int mode, float *sigma_out,
+                           int32_t *idx_out, uint8_t *packed_out, float *weight_out, void *stream) {
+  PLX_REQUIRE(rows >= 0 && cols > 0, "plx_requantize_noalloc: bad shape (%lld, %lld)", static_cast<long long>(rows),
+              static_cast<long long>(cols));
+  PLX_REQUIRE(cols % kDim == 0, "Pollux requires in_features divisible by H24_DIM=24; got %lld.",
+              static_cast<long long>(cols));
+  PLX_REQUIRE(mode == PLX_NN_BF16_SCORES || mode == PLX_NN_FP32_SCORES, "plx_requantize_noalloc: unknown mode %d",
+              mode);
+  PLX_REQUIRE(rows <= static_cast<int64_t>(PLX_NOALLOC_MAX_ATOMS) * kDim / cols,
+              "plx_requantize_noalloc: %lld x %lld is more than its maximum of %d atoms (use plx_requantize)",
+              static_cast<long long>(rows), static_cast<long long>(cols), PLX_NOALLOC_MAX_ATOMS);
+  if (rows == 0) return PLX_OK;
+  PLX_REQUIRE(latent != nullptr && sigma_out != nullptr && idx_out != nullptr, "plx_requantize_noalloc: null pointer");
+  return launch_requantize_noalloc(latent, rows, cols, mode, sigma_out, idx_out, packed_out, weight_out,
+                                   as_stream(stream));
 }
 
 int plx_requantize_batch(const plx_requantize_item *items, int n_items, int mode, void *workspace,

@@ -47,6 +47,9 @@ float raw_to_f32(int k);
 
 // Lazily built per-device tables for the current device (tables.cpp).
 int get_tables(const DeviceTables **out);
+// The current device's tables if plx_device_init (or any earlier call) built
+// them; PLX_EINVAL without allocating anything otherwise (tables.cpp).
+int get_tables_built(const DeviceTables **out);
 
 // Error reporting (capi.cpp).
 int fail(int code, const char *fmt, ...);
@@ -66,6 +69,12 @@ int launch_quantize(const float *x, const float *sigma, int64_t rows, int64_t co
                     int mode, int32_t *idx_out, uint8_t *packed_out, float *weight_out,
                     void *workspace, size_t workspace_bytes, hipStream_t s);
 size_t quantize_workspace_bytes(int64_t n_atoms);
+// The allocation-free requantize (quantize.hip): its workspace is the file-scope
+// device array `scratch`, whose per-device address noalloc_setup() resolves
+// once per device (current device) and caches.
+int noalloc_setup();
+int launch_requantize_noalloc(const float *latent, int64_t rows, int64_t cols, int mode, float *sigma_out,
+                              int32_t *idx_out, uint8_t *packed_out, float *weight_out, hipStream_t s);
 // One matrix of a batched requantize (the latent's row scale, indices, packed
 // bytes and reconstructed weight; packed and weight may be null).
 struct RequantItem {

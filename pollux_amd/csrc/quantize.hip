@@ -56,6 +56,7 @@
 //   (MFMA measured at < 2^-22), so the result equals the exact-score answer
 //   on every atom that is not a near-tie within that envelope.
 
+#include <mutex>
 #include <type_traits>
 
 #include "plx_device.h"
@@ -859,6 +860,63 @@ int launch_requantize_batch(const RequantItem *items, int n_items, int mode, voi
   uint8_t *ws = static_cast<uint8_t *>(workspace);
   return mode == PLX_NN_BF16_SCORES ? launch_batch_mode<PLX_NN_BF16_SCORES>(items, n_items, tab, ws, s)
                                     : launch_batch_mode<PLX_NN_FP32_SCORES>(items, n_items, tab, ws, s);
+}
+
+// ---- allocation-free requantize (plx_requantize_noalloc) ----
+// The workspace of up to PLX_NOALLOC_MAX_ATOMS atoms (per-atom keys, then the
+// bf16 operand planes) as one file-scope device array, held by every device
+// the library runs on until the process ends.  In host code `scratch` names a
+// host-side stand-in: its device address comes from hipGetSymbolAddress, once
+// per device, and only that address is passed to kernels.  Every call on a
+// device shares its array; prep_kernel clears the keys each call, so a call
+// needs nothing from the previous one, but calls that overlap on one device
+// (different streams at once) race on it.
+static_assert(PLX_NOALLOC_MAX_ATOMS > 0, "maximum atoms of the allocation-free entry point");
+constexpr size_t kScratchBytes = static_cast<size_t>(PLX_NOALLOC_MAX_ATOMS) * (8 + 48);
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+namespace {
+std::mutex g_scratch_mu;
+void *g_scratch[64] = {};  // per device: the address of `scratch`
+}  // namespace
+
+int noalloc_setup() {
+  int dev = 0;
+  int st = check_hip(hipGetDevice(&dev), "hipGetDevice");
+  if (st != PLX_OK) return st;
+  if (dev < 0 || dev >= 64) return fail(PLX_EINVAL, "device ordinal %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch[dev] != nullptr) return PLX_OK;
+  void *p = nullptr;
+  st = check_hip(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+  if (st != PLX_OK) return st;
+  if (p == nullptr || (reinterpret_cast<uintptr_t>(p) & 255u) != 0)
+    return fail(PLX_EHIP, "the scratch array of device %d has no usable device address", dev);
+  g_scratch[dev] = p;
+  return PLX_OK;
+}
+
+int launch_requantize_noalloc(const float *latent, int64_t rows, int64_t cols, int mode, float *sigma_out,
+                              int32_t *idx_out, uint8_t *packed_out, float *weight_out, hipStream_t s) {
+  const int64_t n_atoms = rows * (cols / kDim);
+  if (n_atoms > PLX_NOALLOC_MAX_ATOMS)
+    return fail(PLX_EINVAL, "plx_requantize_noalloc: %lld atoms exceed its maximum of %d (use plx_requantize)",
+                static_cast<long long>(n_atoms), PLX_NOALLOC_MAX_ATOMS);
+  const DeviceTables *tab = nullptr;
+  int st = get_tables_built(&tab);  // never builds (allocates) them here
+  if (st != PLX_OK) return st;
+  int dev = 0;
+  if ((st = check_hip(hipGetDevice(&dev), "hipGetDevice")) != PLX_OK) return st;
+  void *ws = nullptr;
+  {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    ws = g_scratch[dev];
+  }
+  if (ws == nullptr)
+    return fail(PLX_EINVAL, "plx_requantize_noalloc: call plx_device_init() on device %d first", dev);
+  if ((st = launch_row_rms(latent, rows, cols, sigma_out, nullptr, s)) != PLX_OK) return st;
+  return launch_quantize(latent, sigma_out, rows, cols, n_atoms, mode, idx_out, packed_out, weight_out, ws,
+                         kScratchBytes, s);
 }
 
 int launch_gather(const int32_t *idx, int64_t n, int out_dtype, void *out, hipStream_t s) {

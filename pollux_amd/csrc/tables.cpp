@@ -143,4 +143,17 @@ int get_tables(const DeviceTables **out) {
   return PLX_OK;
 }
 
+int get_tables_built(const DeviceTables **out) {
+  int dev = 0;
+  int st = check_hip(hipGetDevice(&dev), "hipGetDevice");
+  if (st != PLX_OK) return st;
+  if (dev < 0 || dev >= 64) return fail(PLX_EINVAL, "device ordinal %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_mu);
+  const DeviceTables *t = &g_tables[dev];
+  if (t->device != dev)
+    return fail(PLX_EINVAL, "the codebook tables of device %d are not built: call plx_device_init() on it first", dev);
+  *out = t;
+  return PLX_OK;
+}
+
 }  // namespace plx
