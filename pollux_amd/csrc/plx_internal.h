@@ -14,15 +14,27 @@ constexpr int kDim = 24;
 constexpr int kKissing = 196560;
 constexpr int kCodebook = 196561;
 
-// MFMA codebook tiles: 16 kissing points per tile, stored as three K-planes
-// (coordinates 8p..8p+7) of 16 rows x 8 bf16, i.e. 768 bytes per tile.  The
-// tile array is padded with all-zero tiles to kPaddedTiles so that every
-// slice / stage / group split divides it evenly; a zero code scores exactly 0
-// and can never beat the origin threshold.
+// MFMA codebook tiles: 16 codes per tile, stored as three K-planes
+// (coordinates 8p..8p+7) of 16 rows x 8 bf16, i.e. 768 bytes per tile.
 constexpr int kTileCodes = 16;
 constexpr int kTileBytes = 768;
-constexpr int kRealTiles = kKissing / kTileCodes;  // 12285
-constexpr int kPaddedTiles = 12288;                // 2^12 * 3
+
+// Sweep order of the scoring kernels.  The 98,256 codes of types 1 and 2
+// (+-4 pairs, +-2 octads) are closed under negation and negation reverses the
+// lexicographic order, so sorted they pair up as s_k and s_{2P-1-k} = -s_k.
+// The sweep scores the 98,304 type-3 codes (one -3; no antipodes in this
+// codebook) in index order, then one representative per antipodal pair (the
+// lower index s_k, k < P = 49,128) in index order: the score of -s_k is
+// exactly -score(s_k) (bf16 operands negate exactly, fp32 sums round
+// symmetrically), so a max of |score| over the representatives covers both
+// members -- 147,432 codes scored instead of 196,560.  Padded with all-zero
+// codes (score 0, never above the origin threshold) to whole tiles.
+constexpr int kType3Codes = 98304;
+constexpr int kPairCodes = 49128;
+constexpr int kType3Tiles = kType3Codes / kTileCodes;                        // 6144
+constexpr int kPairTiles = (kPairCodes + kTileCodes - 1) / kTileCodes;      // 3071
+constexpr int kSweepTiles = 9216;  // 6144 + 3071 + 1 zero tile = 2^10 * 9
+static_assert(kType3Tiles + kPairTiles <= kSweepTiles, "sweep tiles");
 
 // fp32 constants of the reference (castor.py:47,50,68; castor.py:522; pack.py:164)
 constexpr uint32_t kLeechScaleBits = 0x3EB504F3u;  // fp32(1/sqrt 8)
@@ -33,11 +45,14 @@ constexpr uint32_t kSqrt12Bits = 0x405DB3D7u;      // fp32(sqrt 12)
 
 struct DeviceTables {
   int device = -1;
-  uint8_t *kp_bf16_tiles = nullptr;  // [kPaddedTiles][3][16][8] bf16 bits (MFMA A-operand layout)
+  uint8_t *sw_bf16_tiles = nullptr;  // [kSweepTiles][3][16][8] bf16 bits of the sweep codes (MFMA A operands)
+  uint8_t *sw_raw_tiles = nullptr;   // the same layout, bf16 bits of the raw integers (NN-P)
+  uint32_t *sw_dq = nullptr;         // [kSweepTiles*16][3] value-id words of the sweep codes (rescans)
+  uint32_t *sw_idx = nullptr;        // [kSweepTiles*16] codebook row of each sweep code, 0 for padding
+  uint32_t *sw_anti = nullptr;       // [(kSweepTiles-kType3Tiles)*16] antipode rows, from the pair region's start
   int8_t *cb_raw = nullptr;          // [kCodebook][24] raw integer coordinates
   uint8_t *kp_gemv = nullptr;        // [kCodebook] x 16 B: 24 signed nibbles + (type | pos << 8)
   uint32_t *kp_dq = nullptr;         // [kCodebook][3] words: 3-bit value ids of 8 coordinates per word
-  uint8_t *kp_raw_tiles = nullptr;   // [kPaddedTiles][3][16][8] bf16 bits of the raw integers (NN-P)
 };
 
 // Host generator (codebook.cpp): raw coordinates, origin first, sorted.

@@ -139,16 +139,16 @@ __device__ __forceinline__ void load_coords8(const float *__restrict__ src, cons
 // 16-byte plane of 8 per thread), written once per launch so the scoring
 // blocks of all slices load ready-made MFMA B operands instead of each
 // repeating the row-scale divisions.  NN-B / NN-T only.
-// Also clears the atoms' 8-byte key slots (keys8 may hold 32-bit keys in its
-// first half: NN-B), before nn_kernel merges its slices into them.
+// Also clears the atoms' 16-byte key slots before nn_kernel merges its
+// slices into them.
 template <bool FUSED>
 __global__ __launch_bounds__(256) void prep_kernel(const float *__restrict__ src, const float *__restrict__ sigma,
                                                    int64_t atoms_per_row, int64_t n_atoms, uint4 *__restrict__ xb,
-                                                   uint2 *__restrict__ keys8) {
+                                                   uint4 *__restrict__ keys) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;  // plane i % 3 of atom i / 3
   if (i >= n_atoms * 3) return;
   const int64_t a = i / 3;
-  if (i == 3 * a) keys8[a] = make_uint2(0u, 0u);
+  if (i == 3 * a) keys[a] = make_uint4(0u, 0u, 0u, 0u);
   float v[8];
   load_coords8<FUSED>(src, sigma, atoms_per_row, n_atoms, a, static_cast<int>(i - 3 * a), v);
   uint4 w;
@@ -160,14 +160,14 @@ __global__ __launch_bounds__(256) void prep_kernel(const float *__restrict__ src
 }
 
 // NN-P has no prep pass: its key slots are cleared here.
-__global__ __launch_bounds__(256) void clear_keys_kernel(uint2 *__restrict__ keys8, int64_t n) {
+__global__ __launch_bounds__(256) void clear_keys_kernel(uint4 *__restrict__ keys, int64_t n) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  if (i < n) keys8[i] = make_uint2(0u, 0u);
+  if (i < n) keys[i] = make_uint4(0u, 0u, 0u, 0u);
 }
 
-// NN-B tracking key of a group: bucket (round-half-up, see raised_threshold)
-// in the high half, 0xFFFF - group in the low half, so one signed max keeps
-// the highest bucket and, within it, the earliest group.
+// NN-B tracking key of a type-3 group: bucket (round-half-up, see
+// raised_threshold) in the high half, 0xFFFF - group in the low half, so one
+// signed max keeps the highest bucket and, within it, the earliest group.
 // v_perm_b32 takes bytes 2-3 of the rounded score and bytes 0-1 of the
 // (uniform) group field in one instruction.
 __device__ __forceinline__ int group_key(int gm, int group) {
@@ -175,11 +175,46 @@ __device__ __forceinline__ int group_key(int gm, int group) {
                                                 static_cast<uint32_t>(0xFFFF - group) & 0xFFFFu, 0x07060100u));
 }
 
+// NN-B tracking of a pair group g (index within the slice's pair range,
+// < 256) whose max |score| is gm, in one unsigned word: bucket << 17 | many <<
+// 16 | (255 - first) << 8 | last -- the earliest and the latest group at the
+// highest bucket, and whether a third group reached it.  A higher bucket
+// replaces the word (first = last = g); the same bucket keeps first, moves
+// last to g and sets `many` if first != last already.  The resolve then
+// knows every group at the best bucket (first and last of each lane) unless
+// `many` is set.  The bucket of a positive score (< 0x8000) fits 15 bits;
+// kPairInit (bucket 0x3FFF) is below every hit (bucket >= 0x4000).
+constexpr uint32_t kPairInit = 0x7FFFFFFFu;
+__device__ __forceinline__ uint32_t pair_key(uint32_t R, int gm, int g) {
+  const uint32_t gf = static_cast<uint32_t>(g) & 0xFFu;
+  const uint32_t bk = (static_cast<uint32_t>(gm) + 0x8000u) >> 16;  // bucket, round half up
+  const uint32_t nk = (bk << 17) | ((255u - gf) << 8) | gf;
+  const uint32_t t = max(R, nk);
+  // (255 - first) + last + 1 is 0 mod 256 exactly when first == last
+  const uint32_t many = (((t >> 8) + t + 1u) & 0xFFu) != 0u ? 0x10000u : 0u;
+  return ((t ^ nk) >> 17) == 0u ? (t & 0xFFFFFF00u) | many | gf : t;
+}
+
+// Lane mask (bit k = lane j + 16k, the four lanes of atom j) from a wave ballot.
+__device__ __forceinline__ uint32_t atom_lanes(uint64_t bal, int j) {
+  return static_cast<uint32_t>(((bal >> j) & 1u) | ((bal >> (j + 15)) & 2u) | ((bal >> (j + 30)) & 4u) |
+                               ((bal >> (j + 45)) & 8u));
+}
+
 // src: NN-P: the fp32 atoms; NN-B / NN-T: xb, the bf16 planes of prep_kernel.
+// tiles: the sweep-order tiles (type-3 codes, then pair representatives).
+// recs (NN-B): one record per (atom, slice >= s0, the slices holding pair
+// tiles), [slice - s0][n_atoms].
+// NN-B: at most 168 VGPRs (3 waves per SIMD; the MFMA issue rate needs the
+// third wave), which costs two 8-byte spills outside the scoring loops;
+// NN-T / NN-P keep 2 waves per SIMD (their wider keys and split operands
+// would spill inside the loops at 168).
 template <int MODE>
-__global__ __launch_bounds__(kThreads, 2) void nn_kernel(const void *__restrict__ src, int64_t n_atoms,
+__global__ __launch_bounds__(kThreads, MODE == kModeB ? 3 : 2) void nn_kernel(const void *__restrict__ src,
+                                                                             int64_t n_atoms,
                                                           const uint8_t *__restrict__ tiles, int n_slices,
-                                                          int tiles_per_slice, void *__restrict__ keys) {
+                                                          int tiles_per_slice, uint4 *__restrict__ keys,
+                                                          uint64_t *__restrict__ recs, int s0) {
   __shared__ __align__(16) uint8_t lds[2][kStageBytes];
 
   const int slice = static_cast<int>(blockIdx.x % static_cast<unsigned>(n_slices));
@@ -217,15 +252,11 @@ __global__ __launch_bounds__(kThreads, 2) void nn_kernel(const void *__restrict_
     }
   }
 
-  int R[kAT], best[kAT];
-#pragma unroll
-  for (int at = 0; at < kAT; ++at) {
-    R[at] = initial_threshold<MODE>();
-    best[at] = -1;
-  }
-
   const int t0 = slice * tiles_per_slice;
   const int n_stages = tiles_per_slice / kST;
+  // stages [0, n_t) hold type-3 tiles, [n_t, n_stages) pair representatives
+  // (the region boundary falls on a stage boundary)
+  const int n_t = min(max(kType3Tiles - t0, 0) / kST, n_stages);
   const uint4 *gsrc = reinterpret_cast<const uint4 *>(tiles + static_cast<size_t>(t0) * kTileBytes);
   // Stage s is copied L2 -> LDS by global_load_lds_dwordx4 (no VGPR staging):
   // wave w, lane l moves vector i*256 + 64w + l, so each wave fills a
@@ -243,217 +274,382 @@ __global__ __launch_bounds__(kThreads, 2) void nn_kernel(const void *__restrict_
   __syncthreads();
 
   const int a_off = (q < 3 ? q : 0) * 256 + j * 16;
+  int R[kAT], best[kAT];
+
+  // Stages [st0, st1) of one region.  PAIR: the fold takes max |score| (the
+  // antipode of each representative scores exactly its negation), and NN-B
+  // tracks the first and last group at the best bucket (pair_key).
   // Software pipeline: the MFMA result of tile k for atom tile `at` is folded
   // into the group maximum while tile k+1's MFMAs issue, and tile k+1's A
   // operand is read from LDS right after tile k's first MFMA.  A group of kG
   // tiles is compared against the threshold once its last tile has been
   // folded, i.e. during the next group's first tile (NN-B: the next group's
-  // tile at % 8); the slice's last tile is folded after the loop.
-  int gm[kAT];
-  f32x4 acc[kAT], part[kAT];
+  // tile at % 8); the region's last tile is folded after its loop.
+  auto run = [&](auto pair_tag, int st0, int st1) {
+    constexpr bool PAIR = decltype(pair_tag)::value;
+    const int g_base = (t0 + st0 * kST) / kG;  // global group of the region's first group in this slice
 #pragma unroll
-  for (int at = 0; at < kAT; ++at) {
-    gm[at] = INT_MIN;
-    acc[at] = f32x4{-0.f, -0.f, -0.f, -0.f};  // INT_MIN bit patterns: neutral for the fold
-  }
-  int group_prev = -1;  // global id of the group whose compare is pending
-  for (int st = 0; st < n_stages; ++st) {
-    const int buf = st & 1;
-    if (st + 1 < n_stages) stage_copy(st + 1, buf ^ 1);
-    const uint8_t *L = lds[buf] + a_off;
-    bf16x8 a = *reinterpret_cast<const bf16x8 *>(L);
-    bool up[kAT];
-    int gdone[kAT];
-    // One group of kG tiles: tile 0 closes the previous group, tile 1 starts
-    // this group's maximum.
-    auto group_tiles = [&](int k0) {
-      constexpr bool FIRST = true;
+    for (int at = 0; at < kAT; ++at) {
+      R[at] = PAIR && MODE == kModeB ? static_cast<int>(kPairInit) : initial_threshold<MODE>();
+      best[at] = -1;
+    }
+    int gm[kAT];
+    f32x4 acc[kAT], part[kAT];
 #pragma unroll
-      for (int t = 0; t < kG; ++t) {
-        const int k = k0 + t;
-        bf16x8 an;
+    for (int at = 0; at < kAT; ++at) {
+      gm[at] = INT_MIN;
+      acc[at] = f32x4{-0.f, -0.f, -0.f, -0.f};  // INT_MIN bit patterns: neutral for the fold
+    }
+    int group_prev = -1;  // global id of the group whose compare is pending
+    for (int st = st0; st < st1; ++st) {
+      const int buf = st & 1;
+      if (st + 1 < n_stages) stage_copy(st + 1, buf ^ 1);
+      const uint8_t *L = lds[buf] + a_off;
+      bf16x8 a = *reinterpret_cast<const bf16x8 *>(L);
+      bool up[kAT];
+      int gdone[kAT];
+      // One group of kG tiles: tile 0 closes the previous group, tile 1 starts
+      // this group's maximum.
+      auto group_tiles = [&](int k0) {
 #pragma unroll
-        for (int at = 0; at < kAT; ++at) {
-          const f32x4 c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b[0][at], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-          if (at == 0) {
-            // the LDS wait that guards `a` must not also wait for this read
+        for (int t = 0; t < kG; ++t) {
+          const int k = k0 + t;
+          bf16x8 an;
+#pragma unroll
+          for (int at = 0; at < kAT; ++at) {
+            const f32x4 c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b[0][at], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+            if (at == 0) {
+              // the LDS wait that guards `a` must not also wait for this read
+              __builtin_amdgcn_sched_barrier(0);
+              an = *reinterpret_cast<const bf16x8 *>(L + (k + 1 < kST ? k + 1 : k) * kTileBytes);
+            }
+            int m;
+            if constexpr (PAIR) {
+              // v_max3_f32 with |.| source modifiers: the same two VALU ops
+              float mf;
+              if (t == 1) {
+                mf = __builtin_fmaxf(__builtin_fmaxf(__builtin_fabsf(acc[at][0]), __builtin_fabsf(acc[at][1])),
+                                     __builtin_fabsf(acc[at][2]));
+                mf = __builtin_fmaxf(mf, __builtin_fabsf(acc[at][3]));
+              } else {
+                mf = __builtin_fmaxf(__builtin_fmaxf(__int_as_float(gm[at]), __builtin_fabsf(acc[at][0])),
+                                     __builtin_fabsf(acc[at][1]));
+                mf = __builtin_fmaxf(__builtin_fmaxf(mf, __builtin_fabsf(acc[at][2])), __builtin_fabsf(acc[at][3]));
+              }
+              m = __float_as_int(mf);
+            } else {
+              if (t == 1) {
+                m = max(max(__float_as_int(acc[at][0]), __float_as_int(acc[at][1])), __float_as_int(acc[at][2]));
+                m = max(m, __float_as_int(acc[at][3]));
+              } else {
+                m = max(max(gm[at], __float_as_int(acc[at][0])), __float_as_int(acc[at][1]));
+                m = max(max(m, __float_as_int(acc[at][2])), __float_as_int(acc[at][3]));
+              }
+            }
+            // The empty asm pins the fold next to this MFMA (IR passes would
+            // otherwise sink the chain to the group end) and the sched_barrier
+            // stops the machine scheduler from hoisting every MFMA, so the
+            // matrix pipe and the VALU work in parallel.
+            asm volatile("" : "+v"(m));
+            if (t == 0) {
+              gdone[at] = m;
+              if constexpr (MODE != kModeB) up[at] = m > R[at];
+            }
+            // NN-B: the closed group's key enters R in tile at % 8 of the next
+            // group, one atom tile per code tile, so the key's VALU work is
+            // spread evenly under the MFMAs instead of piling up in tile 0.
+            if (MODE == kModeB && at % 8 == t) {
+              if constexpr (PAIR)
+                R[at] = static_cast<int>(pair_key(static_cast<uint32_t>(R[at]), gdone[at], group_prev - g_base));
+              else
+                R[at] = max(R[at], group_key(gdone[at], group_prev));
+            }
+            gm[at] = m;
+            if constexpr (NS == 1)
+              acc[at] = c;
+            else
+              part[at] = c;
             __builtin_amdgcn_sched_barrier(0);
-            an = *reinterpret_cast<const bf16x8 *>(L + (k + 1 < kST ? k + 1 : k) * kTileBytes);
           }
-          int m;
-          if (FIRST && t == 1) {
-            m = max(max(__float_as_int(acc[at][0]), __float_as_int(acc[at][1])), __float_as_int(acc[at][2]));
-            m = max(m, __float_as_int(acc[at][3]));
-          } else {
-            m = max(max(gm[at], __float_as_int(acc[at][0])), __float_as_int(acc[at][1]));
-            m = max(max(m, __float_as_int(acc[at][2])), __float_as_int(acc[at][3]));
-          }
-          // The empty asm pins the fold next to this MFMA (IR passes would
-          // otherwise sink the chain to the group end) and the sched_barrier
-          // stops the machine scheduler from hoisting every MFMA, so the
-          // matrix pipe and the VALU work in parallel.
-          asm volatile("" : "+v"(m));
-          if (FIRST && t == 0) {
-            gdone[at] = m;
-            if constexpr (MODE != kModeB) up[at] = m > R[at];
-          }
-          // NN-B: the closed group's key enters R in tile at % 8 of the next
-          // group, one atom tile per code tile, so the key's VALU work is
-          // spread evenly under the MFMAs instead of piling up in tile 0.
-          if (MODE == kModeB && at % 8 == t) R[at] = max(R[at], group_key(gdone[at], group_prev));
-          gm[at] = m;
-          if constexpr (NS == 1)
-            acc[at] = c;
-          else
-            part[at] = c;
-          __builtin_amdgcn_sched_barrier(0);
-        }
-        if constexpr (NS == 3) {
+          if constexpr (NS == 3) {
 #pragma unroll
-          for (int at = 0; at < kAT; ++at)
-            part[at] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b[1][at], part[at], 0, 0, 0);
+            for (int at = 0; at < kAT; ++at)
+              part[at] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b[1][at], part[at], 0, 0, 0);
 #pragma unroll
-          for (int at = 0; at < kAT; ++at)
-            acc[at] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b[2][at], part[at], 0, 0, 0);
+            for (int at = 0; at < kAT; ++at)
+              acc[at] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b[2][at], part[at], 0, 0, 0);
+          }
+          a = an;
         }
-        a = an;
-      }
-    };
+      };
 #pragma unroll 1
-    for (int k0 = 0; k0 < kST; k0 += kG) {
-      group_tiles(k0);
-      if constexpr (MODE != kModeB) {
+      for (int k0 = 0; k0 < kST; k0 += kG) {
+        group_tiles(k0);
+        if constexpr (MODE != kModeB) {
 #pragma unroll
-        for (int at = 0; at < kAT; ++at) {
-          if (up[at]) {
-            R[at] = raised_threshold<MODE>(gdone[at]);
-            best[at] = group_prev;
+          for (int at = 0; at < kAT; ++at) {
+            if (up[at]) {
+              R[at] = raised_threshold<MODE>(gdone[at]);
+              best[at] = group_prev;
+            }
           }
         }
+        group_prev = (t0 + st * kST + k0) / kG;
       }
-      group_prev = (t0 + st * kST + k0) / kG;
+      __syncthreads();
     }
-    __syncthreads();
-  }
-  // fold the slice's last tile and close its last group
+    // fold the region's last tile and close its last group
 #pragma unroll
-  for (int at = 0; at < kAT; ++at) {
-    int m = max(max(gm[at], __float_as_int(acc[at][0])), __float_as_int(acc[at][1]));
-    m = max(max(m, __float_as_int(acc[at][2])), __float_as_int(acc[at][3]));
-    if constexpr (MODE == kModeB) {
-      R[at] = max(R[at], group_key(m, group_prev));
-    } else if (m > R[at]) {
-      R[at] = raised_threshold<MODE>(m);
-      best[at] = group_prev;
+    for (int at = 0; at < kAT; ++at) {
+      int m;
+      if constexpr (PAIR) {
+        float mf = __builtin_fmaxf(__builtin_fmaxf(__int_as_float(gm[at]), __builtin_fabsf(acc[at][0])),
+                                   __builtin_fabsf(acc[at][1]));
+        mf = __builtin_fmaxf(__builtin_fmaxf(mf, __builtin_fabsf(acc[at][2])), __builtin_fabsf(acc[at][3]));
+        m = __float_as_int(mf);
+      } else {
+        m = max(max(gm[at], __float_as_int(acc[at][0])), __float_as_int(acc[at][1]));
+        m = max(max(m, __float_as_int(acc[at][2])), __float_as_int(acc[at][3]));
+      }
+      if constexpr (MODE == kModeB) {
+        if constexpr (PAIR)
+          R[at] = static_cast<int>(pair_key(static_cast<uint32_t>(R[at]), m, group_prev - g_base));
+        else
+          R[at] = max(R[at], group_key(m, group_prev));
+      } else if (m > R[at]) {
+        R[at] = raised_threshold<MODE>(m);
+        best[at] = group_prev;
+      }
     }
-  }
 
-  // ---- merge this slice into the atom's key ----
-  // The four lanes of atom j (j, j+16, j+32, j+48) hold the slice's best
-  // per lane; their maximum is the slice's best (score, earliest group) and
-  // the mask names the lanes that reached it in that group.
+    // ---- merge this region of the slice into the atom's keys ----
+    // The four lanes of atom j (j, j+16, j+32, j+48) hold the slice's best per
+    // lane; their maximum is the slice's best (score, group) and the mask
+    // names the lanes that reached it there.  A lane without a hit merges 0 (a
+    // select, not a branch: a conditional atomic here costs the main loop
+    // ~20 VGPRs).
 #pragma unroll
-  for (int at = 0; at < kAT; ++at) {
-    const int64_t a = wave_atom0 + at * 16 + j;
-    if constexpr (MODE == kModeB) {
-      int Rm = R[at];
-      Rm = max(Rm, __shfl_xor(Rm, 16, 64));
-      Rm = max(Rm, __shfl_xor(Rm, 32, 64));
-      const uint64_t bal = __ballot(R[at] == Rm);  // bit l: lane l holds the maximum
-      const uint32_t mask = static_cast<uint32_t>(((bal >> j) & 1u) | ((bal >> (j + 15)) & 2u) |
-                                                  ((bal >> (j + 30)) & 4u) | ((bal >> (j + 45)) & 8u));
-      const uint32_t g = 0xFFFFu - (static_cast<uint32_t>(Rm) & 0xFFFFu);
-      // no hit: key 0, which leaves the atom's key as it is (a select, not a
-      // branch: a conditional atomic here costs the main loop ~20 VGPRs)
-      const uint32_t key = Rm != initial_threshold<MODE>()
-                               ? (static_cast<uint32_t>(Rm) & 0xFFFF0000u) | ((0x3FFu - g) << 6) | (mask << 2)
-                               : 0u;
-      if (q == 0 && a < n_atoms) atomicMax(static_cast<unsigned int *>(keys) + a, key);
-    } else {
-      // (score, 1023 - group) as one 64-bit value, lanes that never beat the threshold 0
-      const bool hit = best[at] >= 0;
-      uint64_t v = hit ? (static_cast<uint64_t>(static_cast<uint32_t>(R[at])) << 32) |
-                             (static_cast<uint64_t>(0x3FFu - static_cast<uint32_t>(best[at])) << 4)
-                       : 0ull;
-      uint64_t vm = v;
-      uint64_t o = static_cast<uint64_t>(__shfl_xor(static_cast<long long>(vm), 16, 64));
-      vm = o > vm ? o : vm;
-      o = static_cast<uint64_t>(__shfl_xor(static_cast<long long>(vm), 32, 64));
-      vm = o > vm ? o : vm;
-      const uint64_t bal = __ballot(v == vm);
-      const uint64_t mask = ((bal >> j) & 1u) | ((bal >> (j + 15)) & 2u) | ((bal >> (j + 30)) & 4u) |
-                            ((bal >> (j + 45)) & 8u);
-      const uint64_t key = vm != 0ull ? vm | mask : 0ull;
-      if (q == 0 && a < n_atoms) atomicMax(static_cast<unsigned long long *>(keys) + a, static_cast<unsigned long long>(key));
+    for (int at = 0; at < kAT; ++at) {
+      const int64_t a = wave_atom0 + at * 16 + j;
+      const bool mine = q == 0 && a < n_atoms;
+      if constexpr (MODE == kModeB && !PAIR) {
+        int Rm = R[at];
+        Rm = max(Rm, __shfl_xor(Rm, 16, 64));
+        Rm = max(Rm, __shfl_xor(Rm, 32, 64));
+        const uint32_t mask = atom_lanes(__ballot(R[at] == Rm), j);
+        const uint32_t g = 0xFFFFu - (static_cast<uint32_t>(Rm) & 0xFFFFu);
+        const uint32_t key = Rm != initial_threshold<MODE>()
+                                 ? (static_cast<uint32_t>(Rm) & 0xFFFF0000u) | ((0x3FFu - g) << 6) | (mask << 2)
+                                 : 0u;
+        if (mine) atomicMax(&keys[a].x, key);
+      } else if constexpr (MODE == kModeB) {
+        // This slice's record: the best bucket Bm over the atom's lanes; among
+        // the lanes at Bm, the earliest first group F and the latest last
+        // group L (pair-region indices), the lanes with a hit in F and in L,
+        // and `many` when some group at Bm is neither F nor L.
+        const uint32_t r = static_cast<uint32_t>(R[at]);
+        const bool hit = r >= 0x80000000u;  // bucket >= 0x4000
+        const uint32_t bkt = hit ? r >> 17 : 0u;
+        uint32_t bm = max(bkt, static_cast<uint32_t>(__shfl_xor(static_cast<int>(bkt), 16, 64)));
+        bm = max(bm, static_cast<uint32_t>(__shfl_xor(static_cast<int>(bm), 32, 64)));
+        const bool at_m = hit && bkt == bm;
+        const uint32_t fl = 255u - ((r >> 8) & 0xFFu), ll = r & 0xFFu;
+        uint32_t F = at_m ? fl : 255u, Lg = at_m ? ll : 0u;
+        F = min(F, static_cast<uint32_t>(__shfl_xor(static_cast<int>(F), 16, 64)));
+        F = min(F, static_cast<uint32_t>(__shfl_xor(static_cast<int>(F), 32, 64)));
+        Lg = max(Lg, static_cast<uint32_t>(__shfl_xor(static_cast<int>(Lg), 16, 64)));
+        Lg = max(Lg, static_cast<uint32_t>(__shfl_xor(static_cast<int>(Lg), 32, 64)));
+        const uint32_t mf = atom_lanes(__ballot(at_m && (fl == F || ll == F)), j);
+        const uint32_t ml = atom_lanes(__ballot(at_m && (fl == Lg || ll == Lg)), j);
+        const bool odd = at_m && (((r >> 16) & 1u) != 0u || (fl != F && fl != Lg) || (ll != F && ll != Lg));
+        const uint32_t many = atom_lanes(__ballot(odd), j) != 0u ? 1u : 0u;
+        const uint64_t pb = static_cast<uint64_t>(g_base - kType3Tiles / kG);
+        const uint64_t rec = bm != 0u ? (static_cast<uint64_t>(bm) << 48) | (static_cast<uint64_t>(many) << 40) |
+                                            ((pb + F) << 32) | ((pb + Lg) << 24) | (mf << 4) | ml
+                                      : 0ull;
+        if (mine) recs[static_cast<int64_t>(slice - s0) * n_atoms + a] = rec;
+      } else {
+        // (score, 1023 - group) as one 64-bit value (pair groups counted from
+        // the pair region's start), lanes that never beat the threshold 0
+        const bool hit = best[at] >= 0;
+        const uint32_t g = static_cast<uint32_t>(best[at] - (PAIR ? kType3Tiles / kG : 0));
+        const uint64_t v = hit ? (static_cast<uint64_t>(static_cast<uint32_t>(R[at])) << 32) |
+                                     (static_cast<uint64_t>(0x3FFu - g) << 4)
+                               : 0ull;
+        uint64_t vm = v;
+        uint64_t o = static_cast<uint64_t>(__shfl_xor(static_cast<long long>(vm), 16, 64));
+        vm = o > vm ? o : vm;
+        o = static_cast<uint64_t>(__shfl_xor(static_cast<long long>(vm), 32, 64));
+        vm = o > vm ? o : vm;
+        const uint64_t mask = atom_lanes(__ballot(v == vm), j);
+        const uint64_t key = vm != 0ull ? vm | mask : 0ull;
+        if (mine)
+          atomicMax(reinterpret_cast<unsigned long long *>(&keys[a]) + (PAIR ? 1 : 0),
+                    static_cast<unsigned long long>(key));
+      }
     }
-  }
+  };
+  if (n_t > 0) run(std::integral_constant<bool, false>{}, 0, n_t);
+  if (n_t < n_stages) run(std::integral_constant<bool, true>{}, n_t, n_stages);
 }
 
 // Resolve: per block 256 atoms.
-//   scan     thread per atom: its key (the bucket or score M, the earliest
-//            group G holding it, the lanes of G that reach it), the atom's
-//            coordinates into LDS (bf16 pairs; NN-P: fp32), one candidate
-//            per lane of the mask, each naming G's kG tiles x 4 codes of that lane;
-//   compact  a block-wide prefix sum packs the candidates into one list;
-//   rescan   kG lanes per candidate, lane t scoring the 4 codes of tile t of
-//            the group (NN-B/T: 3-bit value ids from kp_dq expanded to bf16,
-//            v_dot2_f32_bf16 = exact bf16 products, fp32 sums; NN-P: 4
-//            consecutive rows of the raw int8 codebook, fp64 dot products of
-//            the fp32 atom with the fp32 codebook values, exact to 2^-48),
-//            then a 4-step shuffle reduction per candidate;
-//   merge    thread per atom folds its candidates' results in list order.
-// keys / xb point at this call's first atom (a batched sweep covers several
-// matrices; each resolves its own range).
-// NN-B picks the lowest code whose bf16 score bucket equals M (falling back to
-// the best rounded score, lowest code on ties, if the fp32 sums disagree with
-// the sweep's); NN-T the highest fp32 score, lowest code on ties; NN-P the
-// highest fp64 score, lowest code on ties.  Then the int32 index and,
+//   scan     thread per atom: its keys (type-3 region; pair region: NN-B the
+//            first and the last group at the best bucket, NN-T / NN-P the
+//            first group at the best |score|), the atom's coordinates into LDS
+//            (bf16 pairs; NN-P: fp32), and its candidates: (group, lane) of
+//            the keys' masks in the regions holding the overall best;
+//   rounds   up to kRsPerRound candidates per atom per round, compacted into
+//            one LDS list by a block prefix sum and rescanned kG lanes per
+//            candidate, lane t scoring the 4 codes of tile t of the group
+//            (NN-B/T: value ids from sw_dq expanded to bf16 pairs,
+//            v_dot2_f32_bf16 = exact bf16 products, fp32 sums; NN-P: the
+//            rows' raw int8 coordinates, fp64 dot products of the fp32 atom
+//            with the fp32 codebook values, exact to 2^-48), reduced by
+//            shuffles and merged per atom;
+//   span     NN-B atoms whose best pair bucket is reached in a group that is
+//            neither a first nor a last group of any lane (a lane with three or
+//            more such groups, or three or more pair slices at that bucket) and
+//            whose earliest such group holds no positive hit: the pair groups
+//            after the earliest up to the latest are rescanned by the whole
+//            block, in ascending chunks, until one holds a positive hit
+//            (~0.04% of atoms).
+// Selection (the reference's rule: lowest codebook row among the best):
+//   a type-3 code wins with its own row; a representative r with score s wins
+//   as r when s is the best (s > 0) and as its antipode when -s is.  Rows of
+//   representatives rise with sweep order and their antipodes' rows fall
+//   (negation reverses the lexicographic order) and every representative row
+//   is below every antipode row, so among pair codes the lowest winning row is
+//   the lowest positive hit if one exists -- in the first group that reaches
+//   the best bucket when that group has one, else somewhere up to the last --
+//   and otherwise the antipode of the highest negative hit, which lies in the
+//   last group.  The answer is the lower of that and the type-3 winner.
+// NN-T / NN-P compare exact scores, where two codes reach the same maximum
+// only on an exact fp32 tie (a near-tie); the first group's winner is taken.
+// NN-B falls back to the best rounded score, lowest row on ties, if the fp32
+// sums disagree with the sweep's bucket.  Then the int32 index and,
 // optionally, the packed 9-byte groups.
-constexpr int kRsPerRound = 4;  // lanes of one atom: every candidate in one round
+constexpr int kRsPerRound = 4;
 constexpr int kRsCap = 256 * kRsPerRound;
+constexpr uint32_t kNone = 0xFFFFFFFFu;
 
 template <int MODE>
 struct RsScore {  // per-candidate / per-atom running result
   typedef typename std::conditional<MODE == kModeP, double, float>::type T;
 };
 
+// Sweep position (global, code granularity) of lane qq's code e in tile t of group g.
+__device__ __forceinline__ int sweep_pos(int g, int t, int qq, int e) { return (g * kG + t) * kTileCodes + 4 * qq + e; }
+
 template <int MODE, bool FUSED>
-__global__ __launch_bounds__(256) void resolve_kernel(const void *__restrict__ keys, int64_t n_atoms,
+__global__ __launch_bounds__(256) void resolve_kernel(const uint4 *__restrict__ keys, int64_t n_atoms,
                                                       const float *__restrict__ src,
                                                       const float *__restrict__ sigma, int64_t atoms_per_row,
-                                                      const uint4 *__restrict__ xb, const uint8_t *__restrict__ rescan,
+                                                      const uint4 *__restrict__ xb,
+                                                      const uint32_t *__restrict__ sw_dq,
+                                                      const uint32_t *__restrict__ sw_idx,
+                                                      const uint32_t *__restrict__ sw_anti,
+                                                      const int8_t *__restrict__ cb_raw,
+                                                      const uint8_t *__restrict__ sw_tiles,
+                                                      const uint64_t *__restrict__ recs, int n_recs,
+                                                      int64_t rec_stride,
                                                       int32_t *__restrict__ idx_out, uint8_t *__restrict__ packed_out) {
   typedef typename RsScore<MODE>::T score_t;
+  constexpr bool B = MODE == kModeB;
   constexpr int XW = MODE == kModeP ? kDim : 12;  // words of one atom's coordinates in LDS
+  constexpr int kP0 = kType3Tiles / kG;           // first global group of the pair region
   __shared__ __align__(16) uint32_t xs[256 * XW];
   __shared__ uint32_t tmp[kRsPerRound * 256];     // per-thread candidates before compaction
-  __shared__ uint32_t cand[kRsCap];               // atom | lane << 8 | group << 10
+  __shared__ uint32_t cand[kRsCap];               // atom | lane << 8 | pair << 10 | global group << 11
   __shared__ score_t res_v[kRsCap];
-  __shared__ uint32_t res_code[kRsCap];
-  __shared__ uint32_t res_found[MODE == kModeB ? kRsCap : 1];
-  __shared__ uint32_t Ms[256];                    // per atom: the sweep's best bucket (NN-B)
+  __shared__ uint32_t res_c[kRsCap];              // row of the best (rounded) score
+  __shared__ uint32_t res_f0[B ? kRsCap : 1];     // NN-B: lowest row at bucket M (pair: positive hits)
+  __shared__ uint32_t res_f1[B ? kRsCap : 1];     // NN-B pair: lowest antipode row of negative hits
+  __shared__ uint32_t Ms[256];                    // per atom: the best bucket (NN-B)
   __shared__ int wave_sum[4];
   __shared__ int32_t ids[256];
   __shared__ __align__(16) uint8_t bytes[64 * 9];
+  __shared__ uint32_t span_list[B ? 256 : 1];      // NN-B: atoms needing the span rescan, their first code,
+  __shared__ uint32_t span_lo[B ? 256 : 1];        // code count, running offset and lowest positive-hit row
+  __shared__ uint32_t span_cnt[B ? 256 : 1];
+  __shared__ uint32_t span_min[B ? 256 : 1];
+  __shared__ uint32_t span_n;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t a0 = static_cast<int64_t>(blockIdx.x) * 256;
   const int64_t a = a0 + tid;
+  if (tid == 0) span_n = 0;
 
-  // ---- scan: the key, coordinates, origin rules ----
-  uint32_t M = 0, G = 0, lanes = 0;
+  // ---- scan: keys, coordinates, origin rules ----
+  // candidate groups (global) and lane masks: [0] type-3; [1..4] pair groups:
+  // NN-B the first and last group of the pair record with the earliest first
+  // group and of the one with the latest last group (the records of the pair
+  // slices at the best pair bucket, in slice = group order); NN-T / NN-P the
+  // first group at the best |score| in [1]
+  uint32_t M = 0, grp[5] = {0u, 0u, 0u, 0u, 0u}, lanes[5] = {0u, 0u, 0u, 0u, 0u};
+  uint32_t span_g0 = 0, span_g1 = 0;  // NN-B: pair groups (span_g0, span_g1] to rescan for positive hits
+  bool many = false;
   bool active = false;
   if (a < n_atoms) {
-    if constexpr (MODE == kModeB) {
-      const uint32_t k = static_cast<const uint32_t *>(keys)[a];
-      M = k >> 16;
-      G = 0x3FFu - ((k >> 6) & 0x3FFu);
-      lanes = (k >> 2) & 0xFu;
+    const uint4 k = keys[a];
+    if constexpr (B) {
+      const uint32_t MT = k.x >> 16;
+      uint32_t MP = 0u;
+      uint64_t rF = 0ull, rL = 0ull;
+      int n_at = 0;
+      for (int i = 0; i < n_recs; ++i) {
+        const uint64_t r = recs[static_cast<int64_t>(i) * rec_stride + a];
+        const uint32_t bb = static_cast<uint32_t>(r >> 48);
+        if (bb > MP) {
+          MP = bb;
+          rF = rL = r;
+          n_at = 1;
+          many = ((r >> 40) & 1ull) != 0ull;
+        } else if (bb == MP && bb != 0u) {
+          rL = r;
+          ++n_at;
+          many |= ((r >> 40) & 1ull) != 0ull;
+        }
+      }
+      many |= n_at > 2;  // a record between the two: its groups are not candidates
+      M = max(MT, MP);
+      if (M != 0u && MT == M) {
+        grp[0] = 0x3FFu - ((k.x >> 6) & 0x3FFu);
+        lanes[0] = (k.x >> 2) & 0xFu;
+      }
+      if (M != 0u && MP == M) {
+        const uint64_t rr[2] = {rF, rL};
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          if (h == 1 && n_at < 2) break;
+          const uint32_t F = kP0 + static_cast<uint32_t>((rr[h] >> 32) & 0xFFu);
+          const uint32_t Lg = kP0 + static_cast<uint32_t>((rr[h] >> 24) & 0xFFu);
+          grp[1 + 2 * h] = F;
+          lanes[1 + 2 * h] = static_cast<uint32_t>((rr[h] >> 4) & 0xFu);
+          if (Lg == F) {
+            lanes[1 + 2 * h] |= static_cast<uint32_t>(rr[h] & 0xFu);
+          } else {
+            grp[2 + 2 * h] = Lg;
+            lanes[2 + 2 * h] = static_cast<uint32_t>(rr[h] & 0xFu);
+          }
+        }
+        span_g0 = kP0 + static_cast<uint32_t>((rF >> 32) & 0xFFu);
+        span_g1 = kP0 + static_cast<uint32_t>((rL >> 24) & 0xFFu);
+      } else {
+        many = false;
+      }
     } else {
-      const uint64_t k = static_cast<const unsigned long long *>(keys)[a];
-      M = static_cast<uint32_t>(k >> 32);
-      G = 0x3FFu - static_cast<uint32_t>((k >> 4) & 0x3FFu);
-      lanes = static_cast<uint32_t>(k & 0xFu);
+      const uint64_t kt = (static_cast<uint64_t>(k.y) << 32) | k.x, kp = (static_cast<uint64_t>(k.w) << 32) | k.z;
+      const uint32_t MT = static_cast<uint32_t>(kt >> 32), MP = static_cast<uint32_t>(kp >> 32);
+      M = max(MT, MP);
+      if (kt != 0ull && MT == M) {
+        grp[0] = 0x3FFu - static_cast<uint32_t>((kt >> 4) & 0x3FFu);
+        lanes[0] = static_cast<uint32_t>(kt & 0xFu);
+      }
+      if (kp != 0ull && MP == M) {
+        grp[1] = kP0 + 0x3FFu - static_cast<uint32_t>((kp >> 4) & 0x3FFu);
+        lanes[1] = static_cast<uint32_t>(kp & 0xFu);
+      }
     }
     double nrm2 = 0.0;
 #pragma unroll
@@ -472,20 +668,32 @@ __global__ __launch_bounds__(256) void resolve_kernel(const void *__restrict__ k
     }
     // NN-P's origin rule (pack.py:174): |x|_2 < fp32(1e-8); no scan needed
     const bool p_snap = MODE == kModeP && sqrt(nrm2) < static_cast<double>(__uint_as_float(kEpsBits));
-    active = M != 0 && lanes != 0 && !p_snap;
+    active = M != 0u && (lanes[0] | lanes[1] | lanes[2] | lanes[3] | lanes[4]) != 0u && !p_snap;
   }
   Ms[tid] = M;
 
-  uint32_t found = 0xFFFFFFFFu;  // NN-B: lowest code whose bucket equals M
+  // per-atom merge state
+  uint32_t fT = kNone, fPpos = kNone, fPneg = kNone;  // NN-B
+  bool pos_first = false;  // NN-B: a positive hit in the earliest pair group (then the lowest pair row is known)
   score_t best_v = -__builtin_inf();
-  uint32_t best_code = 0xFFFFFFFFu;
-  {
-    // ---- this thread's candidates: the lanes of its mask, all in group G ----
+  uint32_t best_code = kNone;
+  int next = 0;  // next candidate slot: 4 * kind + lane
+  const uint4 bt = bf16_value_table();
+  for (;;) {
+    // ---- this thread's next candidates ----
     int nm = 0;
     if (active) {
-#pragma unroll
-      for (int qq = 0; qq < 4; ++qq)
-        if ((lanes >> qq) & 1u) tmp[nm++ * 256 + tid] = static_cast<uint32_t>(tid) | static_cast<uint32_t>(qq) << 8 | G << 10;
+      while (next < 20 && nm < kRsPerRound) {
+        const int kind = next >> 2, qq = next & 3;
+        ++next;
+        if ((lanes[kind] >> qq) & 1u)
+          tmp[nm++ * 256 + tid] = static_cast<uint32_t>(tid) | static_cast<uint32_t>(qq) << 8 |
+                                  static_cast<uint32_t>(kind != 0) << 10 | grp[kind] << 11;
+      }
+    }
+    bool more = false;
+    if (active) {
+      for (int s2 = next; s2 < 20; ++s2) more |= ((lanes[s2 >> 2] >> (s2 & 3)) & 1u) != 0u;
     }
 
     // ---- compact: exclusive prefix sum of nm over the block ----
@@ -508,101 +716,111 @@ __global__ __launch_bounds__(256) void resolve_kernel(const void *__restrict__ k
     __syncthreads();
 
     // ---- rescan: kG lanes per candidate ----
-    const uint4 bt = bf16_value_table();
     for (int task = tid; task < total * kG; task += 256) {
       const int c = task / kG, t = task % kG;
       const uint32_t cd = cand[c];
       const int al = static_cast<int>(cd & 0xFFu), qq = static_cast<int>((cd >> 8) & 3u);
-      const int tile = static_cast<int>(cd >> 10) * kG + t;
-      uint32_t f = 0xFFFFFFFFu, bc = 0xFFFFFFFFu;
+      const bool pair = ((cd >> 10) & 1u) != 0u;
+      const int g = static_cast<int>(cd >> 11);
+      uint32_t f0 = kNone, f1 = kNone, bc = kNone;
       score_t bv = -__builtin_inf();
-      if (tile < kRealTiles) {
-        if constexpr (MODE == kModeP) {
-          double xd[kDim];
+      const uint32_t Mk = Ms[al];
+      const int pos0 = sweep_pos(g, t, qq, 0);
+      uint32_t rows[4], arows[4];
 #pragma unroll
-          for (int k = 0; k < kDim; ++k) xd[k] = static_cast<double>(__uint_as_float(xs[al * XW + k]));
-          const uint32_t code0 = static_cast<uint32_t>(tile * kTileCodes + 4 * qq);
-          const uint2 *cr = reinterpret_cast<const uint2 *>(rescan + (static_cast<size_t>(code0) + 1) * kDim);
-          uint2 rw[12];
+      for (int e = 0; e < 4; ++e) {
+        rows[e] = sw_idx[pos0 + e];
+        arows[e] = pair ? sw_anti[pos0 + e - kType3Codes] : 0u;
+      }
+      score_t sc[4];
+      if constexpr (MODE == kModeP) {
+        double xd[kDim];
 #pragma unroll
-          for (int k = 0; k < 12; ++k) rw[k] = cr[k];
+        for (int k = 0; k < kDim; ++k) xd[k] = static_cast<double>(__uint_as_float(xs[al * XW + k]));
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const uint32_t w6[6] = {rw[3 * e].x, rw[3 * e].y, rw[3 * e + 1].x, rw[3 * e + 1].y, rw[3 * e + 2].x,
-                                    rw[3 * e + 2].y};
-            double sc = 0.0;
+        for (int e = 0; e < 4; ++e) {
+          const uint2 *cr = reinterpret_cast<const uint2 *>(cb_raw + static_cast<size_t>(rows[e]) * kDim);
+          const uint2 r0 = cr[0], r1 = cr[1], r2 = cr[2];
+          const uint32_t w6[6] = {r0.x, r0.y, r1.x, r1.y, r2.x, r2.y};
+          double s = 0.0;
 #pragma unroll
-            for (int k = 0; k < kDim; ++k) {
-              const int r = static_cast<int32_t>(w6[k / 4] << (24 - 8 * (k % 4))) >> 24;
-              sc = fma(xd[k], static_cast<double>(raw_value_f32(r)), sc);
-            }
-            if (sc > bv) {  // codes ascend with e: the first maximum is kept
-              bv = sc;
-              bc = code0 + e;
-            }
+          for (int k = 0; k < kDim; ++k) {
+            const int r = static_cast<int32_t>(w6[k / 4] << (24 - 8 * (k % 4))) >> 24;
+            s = fma(xd[k], static_cast<double>(raw_value_f32(r)), s);
           }
-        } else {
-          const uint4 *xq = reinterpret_cast<const uint4 *>(xs + al * XW);
-          const uint4 x0 = xq[0], x1 = xq[1], x2 = xq[2];
-          const uint32_t xw[12] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w, x2.x, x2.y, x2.z, x2.w};
-          // 4 consecutive codebook rows (code + 1): 12 words of 3-bit value
-          // ids, expanded to bf16 pairs by byte lookups
-          const uint32_t code0 = static_cast<uint32_t>(tile * kTileCodes + 4 * qq);
-          const uint32_t *cp = reinterpret_cast<const uint32_t *>(rescan) + (static_cast<size_t>(code0) + 1) * 3;
-          uint32_t idw[12];
+          sc[e] = s;
+        }
+      } else {
+        const uint4 *xq = reinterpret_cast<const uint4 *>(xs + al * XW);
+        const uint4 x0 = xq[0], x1 = xq[1], x2 = xq[2];
+        const uint32_t xw[12] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w, x2.x, x2.y, x2.z, x2.w};
+        uint32_t idw[12];
 #pragma unroll
-          for (int k = 0; k < 12; ++k) idw[k] = cp[k];
-          const uint32_t Mk = Ms[al];
+        for (int k = 0; k < 12; ++k) idw[k] = sw_dq[static_cast<size_t>(pos0) * 3 + k];
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            uint32_t cw[12];
+        for (int e = 0; e < 4; ++e) {
+          uint32_t cw[12];
 #pragma unroll
-            for (int p = 0; p < 3; ++p) {
-              const uint4 o = ids_to_pairs(idw[3 * e + p], bt);
-              cw[4 * p] = o.x;
-              cw[4 * p + 1] = o.y;
-              cw[4 * p + 2] = o.z;
-              cw[4 * p + 3] = o.w;
-            }
-            float sc = 0.f;
-#pragma unroll
-            for (int d = 0; d < 12; ++d)
-              sc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, xw[d]), __builtin_bit_cast(bf16x2, cw[d]),
-                                                   sc, false);
-            const uint32_t code = static_cast<uint32_t>(tile * kTileCodes + 4 * qq + e);
-            float v = sc;
-            if (MODE == kModeB) {
-              const uint32_t bk = bf16_rne_bits(sc);
-              v = bf16_bits_to_float(bk);
-              if (bk == Mk && code < f) f = code;
-            }
-            if (v > bv) {
-              bv = v;
-              bc = code;
-            }
+          for (int p = 0; p < 3; ++p) {
+            const uint4 o = ids_to_pairs(idw[3 * e + p], bt);
+            cw[4 * p] = o.x;
+            cw[4 * p + 1] = o.y;
+            cw[4 * p + 2] = o.z;
+            cw[4 * p + 3] = o.w;
           }
+          float s = 0.f;
+#pragma unroll
+          for (int d = 0; d < 12; ++d)
+            s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, xw[d]), __builtin_bit_cast(bf16x2, cw[d]), s,
+                                                false);
+          sc[e] = s;
         }
       }
-      // reduce over the candidate's kG lanes: lowest found code; best score, lowest code on ties
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        if (rows[e] == 0u) continue;  // padding
+        // the code's candidate value and row: a pair code counts with |s|,
+        // as its representative's row when s >= 0 and its antipode's when s < 0
+        const bool neg = pair && sc[e] < static_cast<score_t>(0);
+        const uint32_t row = neg ? arows[e] : rows[e];
+        score_t v = pair && neg ? -sc[e] : sc[e];
+        if constexpr (B) {
+          const uint32_t bk = bf16_rne_bits(static_cast<float>(sc[e]));
+          if (!pair && bk == Mk) f0 = min(f0, row);
+          if (pair && bk == Mk) f0 = min(f0, rows[e]);
+          if (pair && bk == (Mk | 0x8000u)) f1 = min(f1, arows[e]);
+          v = bf16_bits_to_float(bf16_rne_bits(static_cast<float>(v)));
+        }
+        if (v > bv || (v == bv && row < bc)) {
+          bv = v;
+          bc = row;
+        }
+      }
+      // reduce over the candidate's kG lanes
 #pragma unroll
       for (int d = 1; d < kG; d <<= 1) {
-        const uint32_t of = static_cast<uint32_t>(__shfl_xor(static_cast<int>(f), d, 64));
         const uint32_t oc = static_cast<uint32_t>(__shfl_xor(static_cast<int>(bc), d, 64));
         score_t ov;
         if constexpr (MODE == kModeP)
           ov = __longlong_as_double(__shfl_xor(__double_as_longlong(bv), d, 64));
         else
           ov = __shfl_xor(bv, d, 64);
-        f = min(f, of);
         if (ov > bv || (ov == bv && oc < bc)) {
           bv = ov;
           bc = oc;
         }
+        if constexpr (B) {
+          f0 = min(f0, static_cast<uint32_t>(__shfl_xor(static_cast<int>(f0), d, 64)));
+          f1 = min(f1, static_cast<uint32_t>(__shfl_xor(static_cast<int>(f1), d, 64)));
+        }
       }
       if (t == 0) {
         res_v[c] = bv;
-        res_code[c] = bc;
-        if constexpr (MODE == kModeB) res_found[c] = f;
+        res_c[c] = bc;
+        if constexpr (B) {
+          res_f0[c] = f0;
+          res_f1[c] = f1;
+        }
       }
     }
     __syncthreads();
@@ -610,31 +828,103 @@ __global__ __launch_bounds__(256) void resolve_kernel(const void *__restrict__ k
     // ---- merge this thread's candidates ----
     for (int i = 0; i < nm; ++i) {
       const score_t v = res_v[off + i];
-      const uint32_t code = res_code[off + i];
+      const uint32_t code = res_c[off + i];
       if (v > best_v || (v == best_v && code < best_code)) {
         best_v = v;
         best_code = code;
       }
-      if constexpr (MODE == kModeB) found = min(found, res_found[off + i]);
+      if constexpr (B) {
+        if (((cand[off + i] >> 10) & 1u) == 0u) {
+          fT = min(fT, res_f0[off + i]);
+        } else {
+          fPpos = min(fPpos, res_f0[off + i]);
+          fPneg = min(fPneg, res_f1[off + i]);
+          pos_first |= (cand[off + i] >> 11) == span_g0 && res_f0[off + i] != kNone;
+        }
+      }
     }
+    if (!__syncthreads_or(more)) break;
+  }
+
+  uint32_t fS = kNone;  // NN-B: the lowest winning pair-code row
+  if constexpr (B) {
+    // ---- span rescan for atoms whose first pair group has only negative hits ----
+    // (rare: some group at the best pair bucket is not among the candidates)
+    // The block steps through the span in ascending chunks of kSpanChunk
+    // codes, kSpanChunk / 256 per thread with all their loads (the codes' bf16
+    // planes from the sweep tiles) issued first, and stops at the first chunk
+    // holding a positive hit: the lowest of that chunk's hits (an LDS atomic
+    // min) is the lowest positive row, since every earlier chunk had none.
+    const bool span = active && many && !pos_first && span_g1 > span_g0;
+    if (span) {
+      const uint32_t slot = atomicAdd(&span_n, 1u);
+      span_list[slot] = static_cast<uint32_t>(tid);
+      span_lo[slot] = (span_g0 + 1u) * kG * kTileCodes;
+      span_cnt[slot] = (span_g1 - span_g0) * kG * kTileCodes;
+      span_min[slot] = kNone;
+    }
+    __syncthreads();
+    const int n_span = static_cast<int>(span_n);
+    constexpr int kSpanPer = 8;  // codes per thread per chunk
+    for (int si = 0; si < n_span; ++si) {
+      const int al = static_cast<int>(span_list[si]);
+      const uint32_t lo = span_lo[si], cnt = span_cnt[si];
+      const uint32_t Mk = Ms[al];
+      const uint4 *xq = reinterpret_cast<const uint4 *>(xs + al * XW);
+      const uint4 x0 = xq[0], x1 = xq[1], x2 = xq[2];
+      const uint32_t xw[12] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w, x2.x, x2.y, x2.z, x2.w};
+      for (uint32_t base = 0; base < cnt; base += 256u * kSpanPer) {
+        uint4 pl[kSpanPer][3];
+#pragma unroll
+        for (int u = 0; u < kSpanPer; ++u) {
+          const uint32_t w = base + static_cast<uint32_t>(u) * 256u + static_cast<uint32_t>(tid);
+          const uint32_t pos = lo + (w < cnt ? w : 0u);
+          const uint8_t *tb = sw_tiles + static_cast<size_t>(pos / kTileCodes) * kTileBytes + (pos % kTileCodes) * 16;
+#pragma unroll
+          for (int p3 = 0; p3 < 3; ++p3) pl[u][p3] = *reinterpret_cast<const uint4 *>(tb + p3 * 256);
+        }
+        uint32_t mine = kNone;
+#pragma unroll
+        for (int u = 0; u < kSpanPer; ++u) {
+          const uint32_t w = base + static_cast<uint32_t>(u) * 256u + static_cast<uint32_t>(tid);
+          const uint32_t cw[12] = {pl[u][0].x, pl[u][0].y, pl[u][0].z, pl[u][0].w, pl[u][1].x, pl[u][1].y,
+                                   pl[u][1].z, pl[u][1].w, pl[u][2].x, pl[u][2].y, pl[u][2].z, pl[u][2].w};
+          float sc2 = 0.f;
+#pragma unroll
+          for (int d = 0; d < 12; ++d)
+            sc2 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, xw[d]), __builtin_bit_cast(bf16x2, cw[d]),
+                                                  sc2, false);
+          if (w < cnt && bf16_rne_bits(sc2) == Mk) {
+            const uint32_t row = sw_idx[lo + w];
+            if (row != 0u) mine = min(mine, row);
+          }
+        }
+        if (mine != kNone) atomicMin(&span_min[si], mine);
+        if (__syncthreads_or(mine != kNone)) break;
+      }
+      __syncthreads();
+      if (tid == al) fPpos = min(fPpos, span_min[si]);
+    }
+    fS = fPpos != kNone ? fPpos : fPneg;
   }
 
   int32_t id = 0;
   if (active) {
     bool snap;
-    uint32_t code;
+    uint32_t row;
     if (MODE == kModeP) {
-      code = best_code;
-      snap = best_code == 0xFFFFFFFFu;  // non-finite atom: no score compared
-    } else if (MODE == kModeB) {
-      const uint32_t bucket = found != 0xFFFFFFFFu ? M : (__float_as_uint(static_cast<float>(best_v)) >> 16);
-      code = found != 0xFFFFFFFFu ? found : best_code;
+      row = best_code;
+      snap = best_code == kNone;  // non-finite atom: no score compared
+    } else if (B) {
+      const uint32_t found = min(fT, fS);
+      const uint32_t bucket = found != kNone ? M : (__float_as_uint(static_cast<float>(best_v)) >> 16);
+      row = found != kNone ? found : best_code;
       snap = !(best_v > 0.f) || bucket < 0x4000u;  // bf16 max below 2.0
     } else {
-      code = best_code;
+      row = best_code;
       snap = !(2.0f * static_cast<float>(best_v) >= __uint_as_float(kCSqNormBits));
     }
-    id = snap ? 0 : static_cast<int32_t>(code) + 1;
+    id = snap || row == kNone ? 0 : static_cast<int32_t>(row);
   }
   if (idx_out && a < n_atoms) idx_out[a] = id;
   if (!packed_out) return;
@@ -691,53 +981,69 @@ __global__ __launch_bounds__(256) void gather_kernel(const int32_t *__restrict__
 }
 
 // Codebook slices per launch.  Blocks are dispatched round-robin over the 8
-// XCDs, so with 4 slices each XCD streams one 2.36 MB quarter of the bf16
-// codebook (L2-resident in its 4 MB L2) and each atom block's operand planes
-// are fetched by 4 XCDs (with 8 slices: 1.18 MB per XCD, planes fetched 8
-// times; measured on 16.8M atoms: 4 slices 0.5% faster, half the plane
-// traffic).  Small launches use more slices so the grid still has several
-// waves of work-groups per CU slot.
+// XCDs, so with 4 slices each XCD streams one quarter of the 7.1 MB sweep
+// table (L2-resident in its 4 MB L2) and each atom block's operand planes are
+// fetched by 4 XCDs (with 8 slices, 8 times; measured on 16.8M atoms: 4
+// slices 0.5% faster, half the plane traffic).  Small launches use more
+// slices so the grid still has several waves of work-groups per CU slot, up
+// to 32 (9216 tiles / 32 = 9 whole stages per slice).
 int choose_slices(int64_t ablocks) {
   int s = 4;
-  while (s < 64 && ablocks * s < 6144) s *= 2;
+  while (s < 32 && ablocks * s < 6144) s *= 2;
   return s;
 }
+static_assert(kSweepTiles % (32 * kST) == 0, "every slice count holds whole stages");
+static_assert(kType3Tiles % kST == 0, "the pair region starts on a stage boundary");
 
-// per-atom key slots (8 bytes; NN-B uses the first 4 n bytes as 32-bit keys)
-size_t keys_bytes(int64_t n_atoms) { return (static_cast<size_t>(n_atoms) * 8 + 255) & ~static_cast<size_t>(255); }
+// per-atom key slots: 16 bytes (NN-B: the type-3 key; NN-T / NN-P: type-3
+// and pair keys of 64 bits)
+size_t keys_bytes(int64_t n_atoms) { return (static_cast<size_t>(n_atoms) * 16 + 255) & ~static_cast<size_t>(255); }
 
-// workspace = per-atom keys, then (NN-B / NN-T) the bf16 planes
+// First slice holding pair tiles, for a launch of n_slices slices.
+int first_pair_slice(int n_slices) { return kType3Tiles / (kSweepTiles / n_slices); }
+
+// NN-B pair records: 8 bytes per (atom, slice holding pair tiles)
+size_t recs_bytes(int64_t n_atoms) {
+  const int64_t ablocks = (n_atoms + kAtomsPerBlock - 1) / kAtomsPerBlock;
+  const int n_slices = choose_slices(ablocks);
+  const size_t n_p = static_cast<size_t>(n_slices - first_pair_slice(n_slices));
+  return (static_cast<size_t>(n_atoms) * n_p * 8 + 255) & ~static_cast<size_t>(255);
+}
+
+// workspace = per-atom keys, the NN-B pair records, then (NN-B / NN-T) the bf16 planes
 template <int MODE, bool FUSED>
 int launch_mode(const float *x, const float *sigma, int64_t apr, int64_t n_atoms, const DeviceTables *tab,
                 int32_t *idx_out, uint8_t *packed_out, uint8_t *workspace, hipStream_t s) {
   const int64_t ablocks = (n_atoms + kAtomsPerBlock - 1) / kAtomsPerBlock;
   const int n_slices = choose_slices(ablocks);
-  const int tiles_per_slice = kPaddedTiles / n_slices;
+  const int tiles_per_slice = kSweepTiles / n_slices;
   const int64_t grid = ablocks * n_slices;
   if (grid > 0x7FFFFFFFll) return fail(PLX_EINVAL, "quantize: %lld atoms exceed one launch", static_cast<long long>(n_atoms));
-  uint2 *keys8 = reinterpret_cast<uint2 *>(workspace);
-  uint4 *xb = reinterpret_cast<uint4 *>(workspace + keys_bytes(n_atoms));
+  uint4 *keys = reinterpret_cast<uint4 *>(workspace);
+  uint64_t *recs = reinterpret_cast<uint64_t *>(workspace + keys_bytes(n_atoms));
+  uint4 *xb = reinterpret_cast<uint4 *>(workspace + keys_bytes(n_atoms) + recs_bytes(n_atoms));
+  const int s0 = first_pair_slice(n_slices);
   int st;
   if (MODE != kModeP) {
     hipLaunchKernelGGL((prep_kernel<FUSED>), dim3(static_cast<unsigned>((n_atoms * 3 + 255) / 256)), dim3(256), 0, s, x,
-                       sigma, apr, n_atoms, xb, keys8);
+                       sigma, apr, n_atoms, xb, keys);
     if ((st = check_launch("prep_kernel")) != PLX_OK) return st;
   } else {
-    hipLaunchKernelGGL(clear_keys_kernel, dim3(static_cast<unsigned>((n_atoms + 255) / 256)), dim3(256), 0, s, keys8,
+    hipLaunchKernelGGL(clear_keys_kernel, dim3(static_cast<unsigned>((n_atoms + 255) / 256)), dim3(256), 0, s, keys,
                        n_atoms);
     if ((st = check_launch("clear_keys_kernel")) != PLX_OK) return st;
   }
   profile_before(s);
-  const uint8_t *tiles = MODE == kModeP ? tab->kp_raw_tiles : tab->kp_bf16_tiles;
-  const uint8_t *rescan =
-      MODE == kModeP ? reinterpret_cast<const uint8_t *>(tab->cb_raw) : reinterpret_cast<const uint8_t *>(tab->kp_dq);
+  const uint8_t *tiles = MODE == kModeP ? tab->sw_raw_tiles : tab->sw_bf16_tiles;
   const void *operand = MODE == kModeP ? static_cast<const void *>(x) : static_cast<const void *>(xb);
   hipLaunchKernelGGL((nn_kernel<MODE>), dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0, s, operand, n_atoms, tiles,
-                     n_slices, tiles_per_slice, static_cast<void *>(keys8));
+                     n_slices, tiles_per_slice, keys, recs, s0);
   if ((st = check_launch("nn_kernel")) != PLX_OK) return st;
   profile_after(s);
   hipLaunchKernelGGL((resolve_kernel<MODE, FUSED>), dim3(static_cast<unsigned>((n_atoms + 255) / 256)), dim3(256), 0, s,
-                     static_cast<const void *>(keys8), n_atoms, x, sigma, apr, xb, rescan, idx_out, packed_out);
+                     keys, n_atoms, x, sigma, apr, xb, tab->sw_dq, tab->sw_idx, tab->sw_anti, tab->cb_raw,
+                     tab->sw_bf16_tiles, static_cast<const uint64_t *>(recs), n_slices - s0, n_atoms, idx_out,
+                     packed_out);
   return check_launch("resolve_kernel");
 }
 
@@ -745,7 +1051,7 @@ int launch_mode(const float *x, const float *sigma, int64_t apr, int64_t n_atoms
 
 size_t quantize_workspace_bytes(int64_t n_atoms) {
   if (n_atoms <= 0) return 0;
-  return keys_bytes(n_atoms) + static_cast<size_t>(n_atoms) * 48;
+  return keys_bytes(n_atoms) + recs_bytes(n_atoms) + static_cast<size_t>(n_atoms) * 48;
 }
 
 int launch_quantize(const float *x, const float *sigma, int64_t rows, int64_t cols, int64_t n_atoms, int mode,
@@ -796,11 +1102,13 @@ int launch_batch_mode(const RequantItem *items, int n_items, const DeviceTables 
   if (total == 0) return PLX_OK;
   const int64_t ablocks = (total + kAtomsPerBlock - 1) / kAtomsPerBlock;
   const int n_slices = choose_slices(ablocks);
-  const int tiles_per_slice = kPaddedTiles / n_slices;
+  const int tiles_per_slice = kSweepTiles / n_slices;
   const int64_t grid = ablocks * n_slices;
   if (grid > 0x7FFFFFFFll) return fail(PLX_EINVAL, "requantize_batch: %lld atoms exceed one launch", static_cast<long long>(total));
-  uint2 *keys8 = reinterpret_cast<uint2 *>(workspace);
-  uint4 *xb = reinterpret_cast<uint4 *>(workspace + keys_bytes(total));
+  uint4 *keys = reinterpret_cast<uint4 *>(workspace);
+  uint64_t *recs = reinterpret_cast<uint64_t *>(workspace + keys_bytes(total));
+  uint4 *xb = reinterpret_cast<uint4 *>(workspace + keys_bytes(total) + recs_bytes(total));
+  const int s0 = first_pair_slice(n_slices);
   int st;
   int64_t off = 0;
   for (int i = 0; i < n_items; ++i) {
@@ -809,14 +1117,13 @@ int launch_batch_mode(const RequantItem *items, int n_items, const DeviceTables 
     if (n == 0) continue;
     if ((st = launch_row_rms(it.latent, it.rows, it.cols, it.sigma, nullptr, s)) != PLX_OK) return st;
     hipLaunchKernelGGL((prep_kernel<true>), dim3(static_cast<unsigned>((n * 3 + 255) / 256)), dim3(256), 0, s, it.latent,
-                       it.sigma, apr, n, xb + off * 3, keys8 + off);
+                       it.sigma, apr, n, xb + off * 3, keys + off);
     if ((st = check_launch("prep_kernel")) != PLX_OK) return st;
     off += n;
   }
   profile_before(s);
   hipLaunchKernelGGL((nn_kernel<MODE>), dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0, s,
-                     static_cast<const void *>(xb), total, tab->kp_bf16_tiles, n_slices, tiles_per_slice,
-                     static_cast<void *>(keys8));
+                     static_cast<const void *>(xb), total, tab->sw_bf16_tiles, n_slices, tiles_per_slice, keys, recs, s0);
   if ((st = check_launch("nn_kernel")) != PLX_OK) return st;
   profile_after(s);
   off = 0;
@@ -825,10 +1132,9 @@ int launch_batch_mode(const RequantItem *items, int n_items, const DeviceTables 
     const int64_t apr = it.cols / kDim, n = it.rows * apr;
     if (n == 0) continue;
     hipLaunchKernelGGL((resolve_kernel<MODE, true>), dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s,
-                       MODE == kModeB ? static_cast<const void *>(reinterpret_cast<const uint32_t *>(keys8) + off)
-                                      : static_cast<const void *>(keys8 + off),
-                       n, it.latent, it.sigma, apr, xb + off * 3,
-                       reinterpret_cast<const uint8_t *>(tab->kp_dq), it.idx, it.packed);
+                       keys + off, n, it.latent, it.sigma, apr, xb + off * 3, tab->sw_dq, tab->sw_idx, tab->sw_anti,
+                       tab->cb_raw, tab->sw_bf16_tiles, static_cast<const uint64_t *>(recs + off), n_slices - s0, total,
+                       it.idx, it.packed);
     if ((st = check_launch("resolve_kernel")) != PLX_OK) return st;
     if (it.weight) {
       hipLaunchKernelGGL((gather_kernel<0, true>), dim3(static_cast<unsigned>((n * 6 + 255) / 256)), dim3(256), 0, s,
@@ -872,7 +1178,10 @@ int launch_requantize_batch(const RequantItem *items, int n_items, int mode, voi
 // needs nothing from the previous one, but calls that overlap on one device
 // (different streams at once) race on it.
 static_assert(PLX_NOALLOC_MAX_ATOMS > 0, "maximum atoms of the allocation-free entry point");
-constexpr size_t kScratchBytes = static_cast<size_t>(PLX_NOALLOC_MAX_ATOMS) * (8 + 48);
+// (at 2^20 atoms a launch uses 8 slices, 3 of them holding pair tiles: 16 B
+// of keys + 3 x 8 B of pair records + 48 B of operand planes per atom, the
+// largest workspace of any size up to the maximum; checked on every call)
+constexpr size_t kScratchBytes = static_cast<size_t>(PLX_NOALLOC_MAX_ATOMS) * (16 + 3 * 8 + 48);
 static __device__ __align__(256) uint8_t scratch[kScratchBytes];
 
 namespace {

@@ -1,23 +1,28 @@
 // Per-device codebook tables, built once per device and kept until exit.
 //
-// kp_bf16_tiles  the 196,560 kissing points (codebook rows 1..196560) rounded
-//                to bf16 exactly as the reference's bf16 casts round them
-//                (castor.py:437, autocast at castor.py:552), in the MFMA tile
-//                layout of quantize.hip; 12288 tiles x 768 B = 9,437,184 B.
+// sw_bf16_tiles  the scoring sweep's codes (plx_internal.h: the 98,304 type-3
+//                codes, then one representative per antipodal pair of types
+//                1-2, zero-padded) rounded to bf16 exactly as the reference's
+//                bf16 casts round them (castor.py:437, autocast at
+//                castor.py:552), in the MFMA tile layout of quantize.hip;
+//                9216 tiles x 768 B = 7,077,888 B.
+// sw_raw_tiles   the same codes' raw integers (exact in bf16), same layout,
+//                for the fp32-exact NN-P scoring (7,077,888 B).
+// sw_dq          the sweep codes' value-id words (kp_dq's format, below) in
+//                sweep order, for the quantizer's rescans (1,769,472 B).
+// sw_idx         the codebook row of every sweep code (0 for padding) and
+// sw_anti        the codebook row of each representative's antipode, indexed
+//                from the pair region's start (589,824 + 196,608 B).
 // cb_raw         the raw int8 coordinates of all 196,561 rows (4,717,464 B);
 //                decoded per value into fp32 / bf16 / fp16 by the kernels.
 // kp_gemv        per code 16 B for the fused dequant-linear: the 24 raw
 //                coordinates as signed 4-bit fields, then type (0 origin,
 //                1 = +-4 pair, 2 = +-2 octad, 3 = one -3) | position of -3 << 8
 //                (3,144,976 B).
-// kp_dq          per code 3 words for the dequant kernel and the quantizer's
-//                NN-B / NN-T rescans: the raw alphabet
+// kp_dq          per code 3 words for the dequant kernel: the raw alphabet
 //                {0,1,2,4,-4,-3,-2,-1} (there is no +3) as value ids 0..7,
 //                word p byte i = id(coord 8p+i) | id(coord 8p+4+i) << 4, the
 //                order v_perm_b32 lookups want (2,358,732 B).
-// kp_raw_tiles   the raw integer coordinates (exact in bf16) in the MFMA tile
-//                layout of kp_bf16_tiles, for the fp32-exact NN-P scoring
-//                (9,437,184 B).
 
 #include <cstring>
 #include <mutex>
@@ -45,26 +50,48 @@ int build(int dev, DeviceTables *t) {
   uint16_t bf_of[9];
   for (int k = -4; k <= 4; ++k) bf_of[k + 4] = f32_to_bf16_rne(raw_to_f32(k));
 
-  std::vector<uint16_t> tiles(static_cast<size_t>(kPaddedTiles) * (kTileBytes / 2), 0);
-  for (int tile = 0; tile < kRealTiles; ++tile)
-    for (int p = 0; p < 3; ++p)
-      for (int i = 0; i < kTileCodes; ++i)
-        for (int e = 0; e < 8; ++e) {
-          const int code = tile * kTileCodes + i + 1;  // codebook row (origin excluded)
-          const int k = raw[static_cast<size_t>(code) * kDim + 8 * p + e];
-          tiles[static_cast<size_t>(tile) * 384 + p * 128 + i * 8 + e] = bf_of[k + 4];
-        }
+  // sweep order: type-3 rows (a -3 coordinate) in index order, then the lower
+  // half of the sorted type-1/2 rows (their antipodes are the upper half,
+  // reversed); every antipode relation is checked here
+  std::vector<int32_t> sym, sweep, anti;
+  sym.reserve(2 * kPairCodes);
+  sweep.reserve(static_cast<size_t>(kSweepTiles) * kTileCodes);
+  for (int code = 1; code < kCodebook; ++code) {
+    const int8_t *r = raw + static_cast<size_t>(code) * kDim;
+    bool three = false;
+    for (int c = 0; c < kDim; ++c) three |= r[c] == -3;
+    if (three)
+      sweep.push_back(code);
+    else
+      sym.push_back(code);
+  }
+  if (static_cast<int>(sweep.size()) != kType3Codes || static_cast<int>(sym.size()) != 2 * kPairCodes)
+    return fail(PLX_EINVAL, "codebook has %zu type-3 and %zu type-1/2 rows", sweep.size(), sym.size());
+  for (int k = 0; k < kPairCodes; ++k) {
+    const int8_t *a = raw + static_cast<size_t>(sym[k]) * kDim;
+    const int8_t *b = raw + static_cast<size_t>(sym[2 * kPairCodes - 1 - k]) * kDim;
+    for (int c = 0; c < kDim; ++c)
+      if (a[c] != -b[c]) return fail(PLX_EINVAL, "codebook row %d has no antipode at the mirrored rank", sym[k]);
+    sweep.push_back(sym[k]);
+    anti.push_back(sym[2 * kPairCodes - 1 - k]);
+  }
+  sweep.resize(static_cast<size_t>(kSweepTiles) * kTileCodes, 0);
+  anti.resize(static_cast<size_t>(kSweepTiles - kType3Tiles) * kTileCodes, 0);  // every pair-region position
 
-  // raw-integer tiles (NN-P): same layout, value k as bf16
+  std::vector<uint16_t> tiles(static_cast<size_t>(kSweepTiles) * (kTileBytes / 2), 0);
   std::vector<uint16_t> raw_tiles(tiles.size(), 0);
-  for (int tile = 0; tile < kRealTiles; ++tile)
-    for (int p = 0; p < 3; ++p)
-      for (int i = 0; i < kTileCodes; ++i)
+  for (int tile = 0; tile < kSweepTiles; ++tile)
+    for (int i = 0; i < kTileCodes; ++i) {
+      const int code = sweep[static_cast<size_t>(tile) * kTileCodes + i];
+      if (code == 0) continue;  // padding stays zero
+      for (int p = 0; p < 3; ++p)
         for (int e = 0; e < 8; ++e) {
-          const int code = tile * kTileCodes + i + 1;
-          const float k = static_cast<float>(raw[static_cast<size_t>(code) * kDim + 8 * p + e]);
-          raw_tiles[static_cast<size_t>(tile) * 384 + p * 128 + i * 8 + e] = f32_to_bf16_rne(k);
+          const int k = raw[static_cast<size_t>(code) * kDim + 8 * p + e];
+          const size_t at = static_cast<size_t>(tile) * 384 + p * 128 + i * 8 + e;
+          tiles[at] = bf_of[k + 4];
+          raw_tiles[at] = f32_to_bf16_rne(static_cast<float>(k));
         }
+    }
 
   // dequant-linear entries: 24 signed 4-bit coordinates, then type | pos << 8
   std::vector<uint32_t> gemv(static_cast<size_t>(kCodebook) * 4, 0);
@@ -94,13 +121,21 @@ int build(int dev, DeviceTables *t) {
     size_t bytes;
     void **dev;
   };
-  void *dt = nullptr, *dr = nullptr, *dg = nullptr, *dd = nullptr, *drt = nullptr;
+  std::vector<uint32_t> sw_dq(sweep.size() * 3, 0);
+  for (size_t i = 0; i < sweep.size(); ++i)
+    for (int p = 0; p < 3; ++p) sw_dq[i * 3 + p] = dq[static_cast<size_t>(sweep[i]) * 3 + p];
+
+  void *dt = nullptr, *drt = nullptr, *dsq = nullptr, *dsi = nullptr, *dsa = nullptr, *dr = nullptr, *dg = nullptr,
+       *dd = nullptr;
   const Upload ups[] = {
       {tiles.data(), tiles.size() * 2, &dt},
+      {raw_tiles.data(), raw_tiles.size() * 2, &drt},
+      {sw_dq.data(), sw_dq.size() * 4, &dsq},
+      {sweep.data(), sweep.size() * 4, &dsi},
+      {anti.data(), anti.size() * 4, &dsa},
       {raw, static_cast<size_t>(kCodebook) * kDim, &dr},
       {gemv.data(), gemv.size() * 4, &dg},
       {dq.data(), dq.size() * 4, &dd},
-      {raw_tiles.data(), raw_tiles.size() * 2, &drt},
   };
   int st = PLX_OK;
   for (const Upload &u : ups) {
@@ -117,11 +152,14 @@ int build(int dev, DeviceTables *t) {
       if (*u.dev) (void)hipFree(*u.dev);
     return st;
   }
-  t->kp_bf16_tiles = static_cast<uint8_t *>(dt);
+  t->sw_bf16_tiles = static_cast<uint8_t *>(dt);
+  t->sw_raw_tiles = static_cast<uint8_t *>(drt);
+  t->sw_dq = static_cast<uint32_t *>(dsq);
+  t->sw_idx = static_cast<uint32_t *>(dsi);
+  t->sw_anti = static_cast<uint32_t *>(dsa);
   t->cb_raw = static_cast<int8_t *>(dr);
   t->kp_gemv = static_cast<uint8_t *>(dg);
   t->kp_dq = static_cast<uint32_t *>(dd);
-  t->kp_raw_tiles = static_cast<uint8_t *>(drt);
   t->device = dev;
   return PLX_OK;
 }
