@@ -716,39 +716,46 @@ __global__ __launch_bounds__(256) void resolve_kernel(const uint4 *__restrict__ 
     __syncthreads();
 
     // ---- rescan: kG lanes per candidate ----
+    // Rows are monotone in sweep position within a region (rising for type-3
+    // codes and representatives, falling for antipodes, and every
+    // representative row is below every antipode row), so a lane tracks
+    // positions and the candidate looks its rows up once, after the lane
+    // reduction: NN-B the lowest position at bucket M (type-3: any score;
+    // pair: positive) and the highest pair position at bucket M with a
+    // negative score; all modes the best (value, preference, position), the
+    // preference ordering equal values the way their rows order.
+    constexpr uint32_t kPrefBase = 1u << 20;  // above every sweep position
     for (int task = tid; task < total * kG; task += 256) {
       const int c = task / kG, t = task % kG;
       const uint32_t cd = cand[c];
       const int al = static_cast<int>(cd & 0xFFu), qq = static_cast<int>((cd >> 8) & 3u);
       const bool pair = ((cd >> 10) & 1u) != 0u;
       const int g = static_cast<int>(cd >> 11);
-      uint32_t f0 = kNone, f1 = kNone, bc = kNone;
+      uint32_t p_lo = kNone, bpref = 0u;
+      int p_hi = -1, bpos = -1;
       score_t bv = -__builtin_inf();
       const uint32_t Mk = Ms[al];
       const int pos0 = sweep_pos(g, t, qq, 0);
-      uint32_t rows[4], arows[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        rows[e] = sw_idx[pos0 + e];
-        arows[e] = pair ? sw_anti[pos0 + e - kType3Codes] : 0u;
-      }
       score_t sc[4];
       if constexpr (MODE == kModeP) {
         double xd[kDim];
 #pragma unroll
         for (int k = 0; k < kDim; ++k) xd[k] = static_cast<double>(__uint_as_float(xs[al * XW + k]));
+        uint32_t rows[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) rows[e] = sw_idx[pos0 + e];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const uint2 *cr = reinterpret_cast<const uint2 *>(cb_raw + static_cast<size_t>(rows[e]) * kDim);
           const uint2 r0 = cr[0], r1 = cr[1], r2 = cr[2];
           const uint32_t w6[6] = {r0.x, r0.y, r1.x, r1.y, r2.x, r2.y};
-          double s = 0.0;
+          double sv = 0.0;
 #pragma unroll
           for (int k = 0; k < kDim; ++k) {
             const int r = static_cast<int32_t>(w6[k / 4] << (24 - 8 * (k % 4))) >> 24;
-            s = fma(xd[k], static_cast<double>(raw_value_f32(r)), s);
+            sv = fma(xd[k], static_cast<double>(raw_value_f32(r)), sv);
           }
-          sc[e] = s;
+          sc[e] = sv;
         }
       } else {
         const uint4 *xq = reinterpret_cast<const uint4 *>(xs + al * XW);
@@ -761,65 +768,68 @@ __global__ __launch_bounds__(256) void resolve_kernel(const uint4 *__restrict__ 
         for (int e = 0; e < 4; ++e) {
           uint32_t cw[12];
 #pragma unroll
-          for (int p = 0; p < 3; ++p) {
-            const uint4 o = ids_to_pairs(idw[3 * e + p], bt);
-            cw[4 * p] = o.x;
-            cw[4 * p + 1] = o.y;
-            cw[4 * p + 2] = o.z;
-            cw[4 * p + 3] = o.w;
+          for (int p3 = 0; p3 < 3; ++p3) {
+            const uint4 o = ids_to_pairs(idw[3 * e + p3], bt);
+            cw[4 * p3] = o.x;
+            cw[4 * p3 + 1] = o.y;
+            cw[4 * p3 + 2] = o.z;
+            cw[4 * p3 + 3] = o.w;
           }
-          float s = 0.f;
+          float sv = 0.f;
 #pragma unroll
           for (int d = 0; d < 12; ++d)
-            s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, xw[d]), __builtin_bit_cast(bf16x2, cw[d]), s,
-                                                false);
-          sc[e] = s;
+            sv = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, xw[d]), __builtin_bit_cast(bf16x2, cw[d]), sv,
+                                                 false);
+          sc[e] = sv;
         }
       }
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        if (rows[e] == 0u) continue;  // padding
-        // the code's candidate value and row: a pair code counts with |s|,
-        // as its representative's row when s >= 0 and its antipode's when s < 0
+        const int pos = pos0 + e;
         const bool neg = pair && sc[e] < static_cast<score_t>(0);
-        const uint32_t row = neg ? arows[e] : rows[e];
-        score_t v = pair && neg ? -sc[e] : sc[e];
+        score_t v = neg ? -sc[e] : sc[e];
+        const uint32_t pref = !pair ? kPrefBase - static_cast<uint32_t>(pos)
+                              : neg ? static_cast<uint32_t>(pos)
+                                    : 0x80000000u + kPrefBase - static_cast<uint32_t>(pos);
         if constexpr (B) {
           const uint32_t bk = bf16_rne_bits(static_cast<float>(sc[e]));
-          if (!pair && bk == Mk) f0 = min(f0, row);
-          if (pair && bk == Mk) f0 = min(f0, rows[e]);
-          if (pair && bk == (Mk | 0x8000u)) f1 = min(f1, arows[e]);
+          if (bk == Mk) p_lo = min(p_lo, static_cast<uint32_t>(pos));
+          if (pair && bk == (Mk | 0x8000u)) p_hi = max(p_hi, pos);
           v = bf16_bits_to_float(bf16_rne_bits(static_cast<float>(v)));
         }
-        if (v > bv || (v == bv && row < bc)) {
+        if (v > bv || (v == bv && pref > bpref)) {
           bv = v;
-          bc = row;
+          bpref = pref;
+          bpos = pos;
         }
       }
       // reduce over the candidate's kG lanes
 #pragma unroll
       for (int d = 1; d < kG; d <<= 1) {
-        const uint32_t oc = static_cast<uint32_t>(__shfl_xor(static_cast<int>(bc), d, 64));
+        const uint32_t opref = static_cast<uint32_t>(__shfl_xor(static_cast<int>(bpref), d, 64));
+        const int opos = __shfl_xor(bpos, d, 64);
         score_t ov;
         if constexpr (MODE == kModeP)
           ov = __longlong_as_double(__shfl_xor(__double_as_longlong(bv), d, 64));
         else
           ov = __shfl_xor(bv, d, 64);
-        if (ov > bv || (ov == bv && oc < bc)) {
+        if (ov > bv || (ov == bv && opref > bpref)) {
           bv = ov;
-          bc = oc;
+          bpref = opref;
+          bpos = opos;
         }
         if constexpr (B) {
-          f0 = min(f0, static_cast<uint32_t>(__shfl_xor(static_cast<int>(f0), d, 64)));
-          f1 = min(f1, static_cast<uint32_t>(__shfl_xor(static_cast<int>(f1), d, 64)));
+          p_lo = min(p_lo, static_cast<uint32_t>(__shfl_xor(static_cast<int>(p_lo), d, 64)));
+          p_hi = max(p_hi, __shfl_xor(p_hi, d, 64));
         }
       }
       if (t == 0) {
+        const bool bneg = pair && bpref < 0x80000000u;
         res_v[c] = bv;
-        res_c[c] = bc;
+        res_c[c] = bpos < 0 ? kNone : bneg ? sw_anti[bpos - kType3Codes] : sw_idx[bpos];
         if constexpr (B) {
-          res_f0[c] = f0;
-          res_f1[c] = f1;
+          res_f0[c] = p_lo == kNone ? kNone : sw_idx[p_lo];
+          res_f1[c] = p_hi < 0 ? kNone : sw_anti[p_hi - kType3Codes];
         }
       }
     }
