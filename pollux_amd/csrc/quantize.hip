@@ -1,15 +1,20 @@
 // Leech nearest-neighbour quantizer on CDNA4 MFMA (replaces castor.py:374-560).
 //
-// Scores x.c of every atom against all 196,560 kissing points as a dense bf16
+// Scores x.c of every atom against the 196,560 kissing points as a dense bf16
 // contraction on v_mfma_f32_16x16x32_bf16 (K = 24 coordinates + 8 zero pad),
 // keeping only a running maximum per (atom, lane) and the index of the code
-// group where it was reached; no score is ever written to memory.
+// group where it was reached; no score is ever written to memory.  The sweep
+// covers 147,432 codes: the 98,304 type-3 codes and one representative per
+// antipodal pair of the type-1/2 codes, whose |score| stands for both members
+// (plx_internal.h).
 //
 // nn_kernel -- the scoring sweep.
 //   grid.x = atom_blocks * n_slices; block b works on atom block b / n_slices
-//   and codebook slice b % n_slices.  Work-groups are dispatched round-robin
-//   over the 8 XCDs, so with 8 slices each XCD only ever streams its own
-//   1.18 MB of the 9.4 MB bf16 codebook and serves it from its 4 MB L2.
+//   and codebook slice b % n_slices.  Large launches use one slice: every
+//   block sweeps the whole 7.1 MB bf16 sweep table and reads its atoms' bf16
+//   planes once; the blocks resident on an XCD sweep the table at nearby
+//   positions and share its 4 MB L2 (~97% hits), the rest comes from MALL.
+//   Small launches split the table into slices so the grid fills the chip.
 //   A block is 4 waves; a wave holds 12 atom tiles of 16 atoms as MFMA B
 //   operands in registers (768 atoms per block) and sweeps its slice, staged
 //   through LDS 32 code tiles (24 KB) at a time, double buffered, with the
@@ -50,7 +55,7 @@
 // resolve_kernel -- per atom its key, then an exact-product rescan
 //   (v_dot2_f32_bf16; NN-P: fp64 dot products of the fp32 atom and the fp32
 //   codebook rows, exact up to 2^-48) of the key's group in the lanes of its
-//   mask to find the lowest code, kG lanes per (group, lane) with coalesced
+//   mask to find the lowest code, 4 lanes per (group, lane) with coalesced
 //   table reads, then the index and the packed 9-byte groups.  Both fp32 sums
 //   (MFMA, dot2) lie within 24 * 2^-24 * sum|x_i c_i| of the exact score
 //   (MFMA measured at < 2^-22), so the result equals the exact-score answer
@@ -500,13 +505,13 @@ __global__ __launch_bounds__(kThreads, MODE == kModeB ? 3 : 2) void nn_kernel(co
 //            (bf16 pairs; NN-P: fp32), and its candidates: (group, lane) of
 //            the keys' masks in the regions holding the overall best;
 //   rounds   up to kRsPerRound candidates per atom per round, compacted into
-//            one LDS list by a block prefix sum and rescanned kG lanes per
-//            candidate, lane t scoring the 4 codes of tile t of the group
-//            (NN-B/T: value ids from sw_dq expanded to bf16 pairs,
-//            v_dot2_f32_bf16 = exact bf16 products, fp32 sums; NN-P: the
-//            rows' raw int8 coordinates, fp64 dot products of the fp32 atom
-//            with the fp32 codebook values, exact to 2^-48), reduced by
-//            shuffles and merged per atom;
+//            one LDS list by a block prefix sum and rescanned kRL = 4 lanes
+//            per candidate, lane t scoring the 4 codes of its quarter in
+//            tiles t, t+4, t+8, t+12 of the group (NN-B/T: value ids from
+//            sw_dq expanded to bf16 pairs, v_dot2_f32_bf16 = exact bf16
+//            products, fp32 sums; NN-P: the rows' raw int8 coordinates, fp64
+//            dot products of the fp32 atom with the fp32 codebook values,
+//            exact to 2^-48), combined by DPP quad moves and merged per atom;
 //   span     NN-B atoms whose best pair bucket is reached in a group that is
 //            neither a first nor a last group of any lane (a lane with three or
 //            more such groups, or three or more pair slices at that bucket) and
@@ -531,6 +536,8 @@ __global__ __launch_bounds__(kThreads, MODE == kModeB ? 3 : 2) void nn_kernel(co
 // optionally, the packed 9-byte groups.
 constexpr int kRsPerRound = 4;
 constexpr int kRsCap = 256 * kRsPerRound;
+constexpr int kRL = 4;         // rescan lanes per candidate (one quad)
+constexpr int kRT = kG / kRL;  // tiles per rescan lane
 constexpr uint32_t kNone = 0xFFFFFFFFu;
 
 template <int MODE>
@@ -715,121 +722,142 @@ __global__ __launch_bounds__(256) void resolve_kernel(const uint4 *__restrict__ 
     for (int i = 0; i < nm; ++i) cand[off + i] = tmp[i * 256 + tid];
     __syncthreads();
 
-    // ---- rescan: kG lanes per candidate ----
-    // Rows are monotone in sweep position within a region (rising for type-3
-    // codes and representatives, falling for antipodes, and every
-    // representative row is below every antipode row), so a lane tracks
-    // positions and the candidate looks its rows up once, after the lane
+    // ---- rescan: kRL lanes per candidate ----
+    // Lane t of a candidate scores the 4 codes of its quarter in tiles t,
+    // t + kRL, ... of the group (16 codes), then the candidate's lanes combine
+    // by DPP quad moves.  Rows are monotone in sweep position within a region
+    // (rising for type-3 codes and representatives, falling for antipodes,
+    // and every representative row is below every antipode row), so a lane
+    // tracks positions and the candidate looks its rows up once, after the
     // reduction: NN-B the lowest position at bucket M (type-3: any score;
     // pair: positive) and the highest pair position at bucket M with a
-    // negative score; all modes the best (value, preference, position), the
-    // preference ordering equal values the way their rows order.
+    // negative score; all modes the best value and a preference that orders
+    // equal values the way their rows order and encodes the position
+    // (type-3: kPrefBase - pos; pair, positive: 2^31 + kPrefBase - pos; pair,
+    // negative: pos; 0: nothing compared).
     constexpr uint32_t kPrefBase = 1u << 20;  // above every sweep position
-    for (int task = tid; task < total * kG; task += 256) {
-      const int c = task / kG, t = task % kG;
+    const int n_tasks = total * kRL;           // a multiple of kRL: quads stay whole
+    for (int task = tid; task < n_tasks; task += 256) {
+      const int c = task / kRL, t = task % kRL;
       const uint32_t cd = cand[c];
       const int al = static_cast<int>(cd & 0xFFu), qq = static_cast<int>((cd >> 8) & 3u);
       const bool pair = ((cd >> 10) & 1u) != 0u;
       const int g = static_cast<int>(cd >> 11);
-      uint32_t p_lo = kNone, bpref = 0u;
-      int p_hi = -1, bpos = -1;
-      score_t bv = -__builtin_inf();
-      const uint32_t Mk = Ms[al];
-      const int pos0 = sweep_pos(g, t, qq, 0);
-      score_t sc[4];
+      int pos0[kRT];
+#pragma unroll
+      for (int j = 0; j < kRT; ++j) pos0[j] = sweep_pos(g, t + kRL * j, qq, 0);
+      score_t sc[kRT][4];
       if constexpr (MODE == kModeP) {
+        uint32_t rows[kRT][4];
+#pragma unroll
+        for (int j = 0; j < kRT; ++j)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) rows[j][e] = sw_idx[pos0[j] + e];
         double xd[kDim];
 #pragma unroll
         for (int k = 0; k < kDim; ++k) xd[k] = static_cast<double>(__uint_as_float(xs[al * XW + k]));
-        uint32_t rows[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) rows[e] = sw_idx[pos0 + e];
+        for (int j = 0; j < kRT; ++j)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const uint2 *cr = reinterpret_cast<const uint2 *>(cb_raw + static_cast<size_t>(rows[e]) * kDim);
-          const uint2 r0 = cr[0], r1 = cr[1], r2 = cr[2];
-          const uint32_t w6[6] = {r0.x, r0.y, r1.x, r1.y, r2.x, r2.y};
-          double sv = 0.0;
+          for (int e = 0; e < 4; ++e) {
+            const uint2 *cr = reinterpret_cast<const uint2 *>(cb_raw + static_cast<size_t>(rows[j][e]) * kDim);
+            const uint2 r0 = cr[0], r1 = cr[1], r2 = cr[2];
+            const uint32_t w6[6] = {r0.x, r0.y, r1.x, r1.y, r2.x, r2.y};
+            double sv = 0.0;
 #pragma unroll
-          for (int k = 0; k < kDim; ++k) {
-            const int r = static_cast<int32_t>(w6[k / 4] << (24 - 8 * (k % 4))) >> 24;
-            sv = fma(xd[k], static_cast<double>(raw_value_f32(r)), sv);
+            for (int k = 0; k < kDim; ++k) {
+              const int r = static_cast<int32_t>(w6[k / 4] << (24 - 8 * (k % 4))) >> 24;
+              sv = fma(xd[k], static_cast<double>(raw_value_f32(r)), sv);
+            }
+            sc[j][e] = sv;
           }
-          sc[e] = sv;
-        }
       } else {
+        uint32_t idw[kRT][12];
+#pragma unroll
+        for (int j = 0; j < kRT; ++j) {
+          const uint4 *q = reinterpret_cast<const uint4 *>(sw_dq + static_cast<size_t>(pos0[j]) * 3);
+          const uint4 q0 = q[0], q1 = q[1], q2 = q[2];
+          const uint32_t w[12] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w, q2.x, q2.y, q2.z, q2.w};
+#pragma unroll
+          for (int k = 0; k < 12; ++k) idw[j][k] = w[k];
+        }
         const uint4 *xq = reinterpret_cast<const uint4 *>(xs + al * XW);
         const uint4 x0 = xq[0], x1 = xq[1], x2 = xq[2];
         const uint32_t xw[12] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w, x2.x, x2.y, x2.z, x2.w};
-        uint32_t idw[12];
 #pragma unroll
-        for (int k = 0; k < 12; ++k) idw[k] = sw_dq[static_cast<size_t>(pos0) * 3 + k];
+        for (int j = 0; j < kRT; ++j)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            uint32_t cw[12];
+#pragma unroll
+            for (int p3 = 0; p3 < 3; ++p3) {
+              const uint4 o = ids_to_pairs(idw[j][3 * e + p3], bt);
+              cw[4 * p3] = o.x;
+              cw[4 * p3 + 1] = o.y;
+              cw[4 * p3 + 2] = o.z;
+              cw[4 * p3 + 3] = o.w;
+            }
+            float sv = 0.f;
+#pragma unroll
+            for (int d = 0; d < 12; ++d)
+              sv = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, xw[d]), __builtin_bit_cast(bf16x2, cw[d]),
+                                                   sv, false);
+            sc[j][e] = sv;
+          }
+      }
+      const uint32_t Mk = Ms[al];
+      uint32_t p_lo = kNone, bpref = 0u, p_hi = 0u;  // p_hi: highest negative-hit position + 1
+      score_t bv = -__builtin_inf();
+#pragma unroll
+      for (int j = 0; j < kRT; ++j)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          uint32_t cw[12];
-#pragma unroll
-          for (int p3 = 0; p3 < 3; ++p3) {
-            const uint4 o = ids_to_pairs(idw[3 * e + p3], bt);
-            cw[4 * p3] = o.x;
-            cw[4 * p3 + 1] = o.y;
-            cw[4 * p3 + 2] = o.z;
-            cw[4 * p3 + 3] = o.w;
+          const uint32_t pos = static_cast<uint32_t>(pos0[j] + e);
+          const bool neg = pair && sc[j][e] < static_cast<score_t>(0);
+          score_t v = neg ? -sc[j][e] : sc[j][e];
+          const uint32_t pref = !pair ? kPrefBase - pos : neg ? pos : 0x80000000u + kPrefBase - pos;
+          if constexpr (B) {
+            const uint32_t bk = bf16_rne_bits(static_cast<float>(sc[j][e]));
+            if (bk == Mk) p_lo = min(p_lo, pos);
+            if (pair && bk == (Mk | 0x8000u)) p_hi = max(p_hi, pos + 1u);
+            v = bf16_bits_to_float(bf16_rne_bits(static_cast<float>(v)));
           }
-          float sv = 0.f;
-#pragma unroll
-          for (int d = 0; d < 12; ++d)
-            sv = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, xw[d]), __builtin_bit_cast(bf16x2, cw[d]), sv,
-                                                 false);
-          sc[e] = sv;
+          if (v > bv || (v == bv && pref > bpref)) {
+            bv = v;
+            bpref = pref;
+          }
         }
-      }
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int pos = pos0 + e;
-        const bool neg = pair && sc[e] < static_cast<score_t>(0);
-        score_t v = neg ? -sc[e] : sc[e];
-        const uint32_t pref = !pair ? kPrefBase - static_cast<uint32_t>(pos)
-                              : neg ? static_cast<uint32_t>(pos)
-                                    : 0x80000000u + kPrefBase - static_cast<uint32_t>(pos);
-        if constexpr (B) {
-          const uint32_t bk = bf16_rne_bits(static_cast<float>(sc[e]));
-          if (bk == Mk) p_lo = min(p_lo, static_cast<uint32_t>(pos));
-          if (pair && bk == (Mk | 0x8000u)) p_hi = max(p_hi, pos);
-          v = bf16_bits_to_float(bf16_rne_bits(static_cast<float>(v)));
-        }
-        if (v > bv || (v == bv && pref > bpref)) {
-          bv = v;
-          bpref = pref;
-          bpos = pos;
-        }
-      }
-      // reduce over the candidate's kG lanes
-#pragma unroll
-      for (int d = 1; d < kG; d <<= 1) {
-        const uint32_t opref = static_cast<uint32_t>(__shfl_xor(static_cast<int>(bpref), d, 64));
-        const int opos = __shfl_xor(bpos, d, 64);
+      // combine the candidate's kRL = 4 lanes (one quad): xor 1, then xor 2
+      auto step = [&](auto ctrl) {
+        constexpr int C = decltype(ctrl)::value;
+        const uint32_t opref = dpp_u32<C>(bpref);
         score_t ov;
-        if constexpr (MODE == kModeP)
-          ov = __longlong_as_double(__shfl_xor(__double_as_longlong(bv), d, 64));
-        else
-          ov = __shfl_xor(bv, d, 64);
+        if constexpr (MODE == kModeP) {
+          const uint64_t b = static_cast<uint64_t>(__double_as_longlong(bv));
+          const uint64_t o = static_cast<uint64_t>(dpp_u32<C>(static_cast<uint32_t>(b))) |
+                             static_cast<uint64_t>(dpp_u32<C>(static_cast<uint32_t>(b >> 32))) << 32;
+          ov = __longlong_as_double(static_cast<long long>(o));
+        } else {
+          ov = dpp_f32<C>(bv);
+        }
         if (ov > bv || (ov == bv && opref > bpref)) {
           bv = ov;
           bpref = opref;
-          bpos = opos;
         }
         if constexpr (B) {
-          p_lo = min(p_lo, static_cast<uint32_t>(__shfl_xor(static_cast<int>(p_lo), d, 64)));
-          p_hi = max(p_hi, __shfl_xor(p_hi, d, 64));
+          p_lo = min(p_lo, dpp_u32<C>(p_lo));
+          p_hi = max(p_hi, dpp_u32<C>(p_hi));
         }
-      }
+      };
+      step(std::integral_constant<int, 0xB1>{});
+      step(std::integral_constant<int, 0x4E>{});
       if (t == 0) {
-        const bool bneg = pair && bpref < 0x80000000u;
+        const uint32_t bpos = !pair ? kPrefBase - bpref : bpref < 0x80000000u ? bpref : 0x80000000u + kPrefBase - bpref;
         res_v[c] = bv;
-        res_c[c] = bpos < 0 ? kNone : bneg ? sw_anti[bpos - kType3Codes] : sw_idx[bpos];
+        res_c[c] = bpref == 0u ? kNone : pair && bpref < 0x80000000u ? sw_anti[bpos - kType3Codes] : sw_idx[bpos];
         if constexpr (B) {
           res_f0[c] = p_lo == kNone ? kNone : sw_idx[p_lo];
-          res_f1[c] = p_hi < 0 ? kNone : sw_anti[p_hi - kType3Codes];
+          res_f1[c] = p_hi == 0u ? kNone : sw_anti[p_hi - 1u - kType3Codes];
         }
       }
     }
@@ -990,15 +1018,15 @@ __global__ __launch_bounds__(256) void gather_kernel(const int32_t *__restrict__
   }
 }
 
-// Codebook slices per launch.  Blocks are dispatched round-robin over the 8
-// XCDs, so with 4 slices each XCD streams one quarter of the 7.1 MB sweep
-// table (L2-resident in its 4 MB L2) and each atom block's operand planes are
-// fetched by 4 XCDs (with 8 slices, 8 times; measured on 16.8M atoms: 4
-// slices 0.5% faster, half the plane traffic).  Small launches use more
-// slices so the grid still has several waves of work-groups per CU slot, up
-// to 32 (9216 tiles / 32 = 9 whole stages per slice).
+// Codebook slices per launch.  One slice when the atom blocks alone give
+// every CU slot several waves of work-groups (>= 6144 blocks): each atom's
+// planes are read once and the longer sweep per block amortises its set-up
+// and flushes (measured on 16.8M atoms: 84.3 ms with 1 slice, 87.2 with 2,
+// 89.4 with 4, identical indices).  Smaller launches double the slice count
+// until the grid reaches that size, up to 32 (9216 tiles / 32 = 9 whole
+// stages per slice).
 int choose_slices(int64_t ablocks) {
-  int s = 4;
+  int s = 1;
   while (s < 32 && ablocks * s < 6144) s *= 2;
   return s;
 }
