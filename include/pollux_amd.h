@@ -136,7 +136,7 @@ int plx_requantize(const float *latent, int64_t rows, int64_t cols, int mode,
  * training loops, harnesses that forbid hipMalloc).  No counterpart in the
  * reference: it serves those callers only.  Same arguments, results and
  * errors as plx_requantize minus the workspace, which is a library-owned
- * device array of PLX_NOALLOC_MAX_ATOMS * 64 bytes (64 MiB) held by each
+ * device array of PLX_NOALLOC_MAX_ATOMS * 88 bytes (88 MiB) held by each
  * device the library runs on until the process ends.  It allocates nothing:
  * call plx_device_init() on the device first (outside any capture), which
  * builds the codebook tables and resolves the array's address; without it
