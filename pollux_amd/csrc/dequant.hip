@@ -37,7 +37,7 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kDqAtoms = 256;                      // atoms per block
-constexpr int kDqChunks = kDqAtoms * 3;            // 16-byte output chunks per block
+
 constexpr int kDqPackedBytes = kDqAtoms / 4 * 9;   // 576
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
@@ -638,15 +638,16 @@ int launch_dql(DqlTargets t, int64_t apr, const void *x, int64_t m, const uint4 
 //             block's rows;
 //   k loop:   each wave takes a contiguous share of the block's atoms in
 //             quads of 4 (= 3 K steps of 32) and reads its activation
-//             fragments from a fragment-order copy of x that a small kernel
-//             writes first (L2-resident: every block reads all of it), PD
-//             quads ahead in registers; per K step a
+//             fragments (up to 32 bf16 tokens: from x in place; otherwise
+//             from a fragment-order copy that a small kernel writes first,
+//             fp32 x as three bf16 parts; L2-resident either way: every block
+//             reads all of it), PD quads ahead in registers; per K step a
 //             lane decodes its B fragments (8 weights of one row = one plane
 //             of one atom) from one LDS word with v_perm_b32 byte lookups and
 //             issues 2*MT MFMAs (4*MT when EXACT).  No block barrier inside
 //             the loop.
 //   epilogue: the waves' fp32 tiles are summed through LDS in wave order.
-// xfrag_kernel runs first and writes the fragment-order copy of x into the
+// When the copy is used, xfrag_kernel runs first and writes it into the
 // caller's workspace.
 // Summing the splits inside this kernel instead (the last split block of a row
 // block adds the others' tiles) measured slower both ways it can be made
@@ -720,14 +721,15 @@ __device__ __forceinline__ void group_codes(uint32_t d0, uint32_t d1, uint32_t d
   c[3] = static_cast<int32_t>(((lo & 0x3FFu) << 8) | b8);
 }
 
-// Fragment-order copy of the activations for dqmm_kernel.  One thread per
-// 16-byte fragment position (slab, quad Q, K step s, token tile t, lane):
-// x[64 slab + 16t + (lane & 15)][96Q + 32s + 8(lane >> 4) .. +8), zero for
-// tokens >= m and columns >= cols, stored at xf[slab][Q][part][s][t][lane].
-// bf16 x is one part.  fp32 x is split exactly into three bf16 parts, x = h +
-// m + l (h = bf16(x), m = bf16(x - h), l = x - h - m, exact while the parts
-// stay normal, |x| >= ~2^-110; inf / nan go to h alone), so that bf16 MFMAs
-// form the products of the fp32 activations.
+// Fragment-order copy of the activations for dqmm_kernel (fp32 x, and bf16 x
+// above 32 tokens).  One thread per 16-byte fragment position (slab, quad Q,
+// K step s, token tile t, lane): x[64 slab + 16t + (lane & 15)][96Q + 32s +
+// 8(lane >> 4) .. +8), zero for tokens >= m and columns >= cols, stored at
+// xf[slab][Q][part][s][t][lane].  bf16 x is one part.  fp32 x is split
+// exactly into three bf16 parts, x = h + m + l (h = bf16(x), m = bf16(x - h),
+// l = x - h - m, exact while the parts stay normal, |x| >= ~2^-110; inf / nan
+// go to h alone), so that bf16 MFMAs form the products of the fp32
+// activations.
 template <bool XF32>
 __global__ __launch_bounds__(256) void xfrag_kernel(const void *__restrict__ x, int64_t m_total, int64_t cols,
                                                     int64_t n_quads_row, uint4 *__restrict__ xf) {
@@ -789,7 +791,7 @@ __device__ __forceinline__ uint32_t hi_lo_pack(float v) {
 
 // token tiles of 16; waves per block; quads of x in flight per wave; exact fp16 weights (hi + lo);
 // bf16 parts per activation (1: bf16 x; 3: fp32 x, see xfrag_kernel)
-template <int MT, int WV, int PD, bool EXACT, int XP>
+template <int MT, int WV, int PD, bool EXACT, int XP, bool XD>
 __global__ __launch_bounds__(64 * WV, WV <= 4 ? 2 : 1) void dqmm_kernel(
     const uint8_t *__restrict__ packed, int64_t packed_bytes, const uint16_t *__restrict__ sigma16, int64_t rows,
     int64_t atoms_per_row, const uint4 *__restrict__ xf, int64_t n_quads_row, int64_t m_total, int splits, int apb,
@@ -816,19 +818,29 @@ __global__ __launch_bounds__(64 * WV, WV <= 4 ? 2 : 1) void dqmm_kernel(
   const int wq0 = wave * qbase + min(wave, qextra);
   const int wqn = qbase + (wave < qextra ? 1 : 0);
 
-  // ---- activation fragments, from the fragment-order copy of x (xfrag_kernel) ----
-  // Quad Q of the row, K step s, token tile t: 64 lanes x 16 B contiguous, so
-  // one wave load reads 1 KB (8 whole cache lines; read straight from x, the
-  // same fragments touch 16 half lines per load, measured ~30% slower).  Raw
-  // buffer loads over the slab's part: a quad past this wave's share takes an
-  // out-of-range offset, which returns zeros without touching memory, so the
-  // loads need no branches (the compiler can then wait for one quad's loads
-  // while the next quads' stay in flight).
-  const int slab_bytes = static_cast<int>(n_quads_row * XP * kXfQuadBytes);
+  // ---- activation fragments ----
+  // Quad Q of the row, K step s, token tile t: lane (j, q) holds token 16t + j,
+  // columns 96Q + 32s + 8q .. +8.  XD (bf16 x, up to 32 tokens): read
+  // straight from x, 16 token rows x 64 B per wave load (half lines).
+  // Otherwise from the fragment-order copy xfrag_kernel writes (1 KB
+  // contiguous per wave load).  Measured per 7680x1920 call: at 17 tokens in
+  // place 8.6 us against 10.4 with the copy kernel; at 64 tokens 13.9 against
+  // 12.1 (16 half lines per load twice as many tokens outweigh the launch).
+  // Raw buffer loads: a quad past this wave's share, a column past the row and
+  // (XD) a token past m take an out-of-range offset, which returns zeros
+  // without touching memory, so the loads need no branches (the compiler can
+  // then wait for one quad's loads while the next quads' stay in flight).
+  const int64_t cols = atoms_per_row * kDim;
+  const int slab_bytes =
+      XD ? static_cast<int>(min(static_cast<int64_t>(64), m_total - tok0) * cols * 2)
+         : static_cast<int>(n_quads_row * XP * kXfQuadBytes);
   const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint4 *>(xf + static_cast<int64_t>(blockIdx.y) * (slab_bytes / 16)), static_cast<short>(0), slab_bytes,
-      kBufferFlags);
-  const int xbase = static_cast<int>(a_begin / 4 + wq0) * XP * kXfQuadBytes + 16 * lane;
+      XD ? const_cast<uint8_t *>(reinterpret_cast<const uint8_t *>(xf) + tok0 * cols * 2)
+         : reinterpret_cast<uint8_t *>(const_cast<uint4 *>(xf + static_cast<int64_t>(blockIdx.y) * (slab_bytes / 16))),
+      static_cast<short>(0), slab_bytes, kBufferFlags);
+  const int xbase = XD ? static_cast<int>(j * cols * 2 + 16 * q)
+                       : static_cast<int>(a_begin / 4 + wq0) * XP * kXfQuadBytes + 16 * lane;
+  const int xcol0 = static_cast<int>(96 * (a_begin / 4 + wq0)) + 8 * q;  // XD: this lane's first column
   auto load_quad = [&](uint4 (&xa)[3][XP][MT], int qd) {
 #pragma unroll
     for (int s = 0; s < 3; ++s) {
@@ -836,7 +848,14 @@ __global__ __launch_bounds__(64 * WV, WV <= 4 ? 2 : 1) void dqmm_kernel(
       for (int pp = 0; pp < XP; ++pp) {
 #pragma unroll
         for (int t = 0; t < MT; ++t) {
-          int off = qd < wqn ? xbase + (qd * XP + pp) * kXfQuadBytes + (4 * s + t) * 1024 : kBufferOutOfRange;
+          int off;
+          if constexpr (XD) {
+            const int col = xcol0 + 96 * qd + 32 * s;
+            off = qd < wqn && col < cols ? xbase + t * static_cast<int>(16 * cols * 2) + 2 * (col - 8 * q)
+                                         : kBufferOutOfRange;
+          } else {
+            off = qd < wqn ? xbase + (qd * XP + pp) * kXfQuadBytes + (4 * s + t) * 1024 : kBufferOutOfRange;
+          }
           asm("" : "+v"(off));  // one unconditional load (not one per select outcome under branches)
           xa[s][pp][t] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(xrs, off, 0, 0));
         }
@@ -1105,7 +1124,7 @@ MmPlan mm_plan(int64_t rows, int64_t apr) {
   return p;
 }
 
-template <int MT, int WV, int PD, bool EXACT, int XP>
+template <int MT, int WV, int PD, bool EXACT, int XP, bool XD>
 int launch_dqmm_t(const uint8_t *packed, int64_t pb, const uint16_t *sigma16, int64_t rows, int64_t apr,
                   const uint4 *xf, int64_t m, float *y, float *partial, const MmPlan &pl, const uint32_t *kp_dq,
                   const float *residual, int gelu, hipStream_t s) {
@@ -1115,7 +1134,7 @@ int launch_dqmm_t(const uint8_t *packed, int64_t pb, const uint16_t *sigma16, in
   const size_t region = static_cast<size_t>(max(kMmRows * mm_row_words(pl.apb), WV * 16 * MT * kMmRedStride)) * 4;
   const size_t shm = region + static_cast<size_t>(kMmRows) * 16 * (EXACT ? 2 : 1);
   const dim3 g(static_cast<unsigned>(row_blocks * pl.splits), static_cast<unsigned>(slabs));
-  hipLaunchKernelGGL((dqmm_kernel<MT, WV, PD, EXACT, XP>), g, dim3(64 * WV), shm, s, packed, pb, sigma16, rows, apr, xf, nq, m,
+  hipLaunchKernelGGL((dqmm_kernel<MT, WV, PD, EXACT, XP, XD>), g, dim3(64 * WV), shm, s, packed, pb, sigma16, rows, apr, xf, nq, m,
                      pl.splits, pl.apb, kp_dq, y, partial, residual, gelu);
   return check_launch("dqmm_kernel");
 }
@@ -1123,17 +1142,23 @@ int launch_dqmm_t(const uint8_t *packed, int64_t pb, const uint16_t *sigma16, in
 template <int MT>
 int launch_dqmm(const uint8_t *packed, int64_t pb, const uint16_t *sigma16, int64_t rows, int64_t apr,
                 const uint4 *xf, int64_t m, float *y, float *partial, const MmPlan &pl, const uint32_t *kp_dq,
-                bool exact, bool x_f32, const float *residual, int gelu, hipStream_t s) {
+                bool exact, bool x_f32, bool direct, const float *residual, int gelu, hipStream_t s) {
   // 8 waves (two per SIMD cover each other's load latency), one quad of x in
-  // flight per wave; 4 waves with 2 quads in flight measured within 3%
+  // flight per wave; 4 waves with 2 quads in flight measured within 3%.
+  // `direct`: bf16 x read in place (xf = x), else the fragment-order copy.
   if (x_f32)
-    return launch_dqmm_t<MT, 8, 1, true, 3>(packed, pb, sigma16, rows, apr, xf, m, y, partial, pl, kp_dq, residual,
-                                            gelu, s);
-  if (exact)
-    return launch_dqmm_t<MT, 8, 1, true, 1>(packed, pb, sigma16, rows, apr, xf, m, y, partial, pl, kp_dq, residual,
-                                            gelu, s);
-  return launch_dqmm_t<MT, 8, 1, false, 1>(packed, pb, sigma16, rows, apr, xf, m, y, partial, pl, kp_dq, residual,
-                                           gelu, s);
+    return launch_dqmm_t<MT, 8, 1, true, 3, false>(packed, pb, sigma16, rows, apr, xf, m, y, partial, pl, kp_dq,
+                                                   residual, gelu, s);
+  if constexpr (MT <= 2)  // direct is only chosen up to 32 tokens
+    if (direct)
+      return exact ? launch_dqmm_t<MT, 8, 1, true, 1, true>(packed, pb, sigma16, rows, apr, xf, m, y, partial, pl, kp_dq,
+                                                            residual, gelu, s)
+                   : launch_dqmm_t<MT, 8, 1, false, 1, true>(packed, pb, sigma16, rows, apr, xf, m, y, partial, pl,
+                                                             kp_dq, residual, gelu, s);
+  return exact ? launch_dqmm_t<MT, 8, 1, true, 1, false>(packed, pb, sigma16, rows, apr, xf, m, y, partial, pl, kp_dq,
+                                                         residual, gelu, s)
+               : launch_dqmm_t<MT, 8, 1, false, 1, false>(packed, pb, sigma16, rows, apr, xf, m, y, partial, pl,
+                                                          kp_dq, residual, gelu, s);
 }
 
 // Workspace of the batched path: the fragment-order x copy (a multiple of 256
@@ -1143,10 +1168,14 @@ struct MmWorkspace {
   size_t total() const { return xf + partial; }
 };
 
+// bf16 x of up to 32 tokens is read in place by dqmm_kernel; larger batches
+// and fp32 x go through the fragment-order copy.
+bool mm_x_copy(bool x_f32, int64_t m) { return x_f32 || m > 32; }
+
 MmWorkspace mm_workspace(int64_t rows, int64_t cols, int64_t m, const MmPlan &pl, bool x_f32) {
   MmWorkspace w;
   const size_t slabs = static_cast<size_t>((m + 63) / 64);
-  w.xf = slabs * static_cast<size_t>((cols / kDim + 3) / 4) * kXfQuadBytes * (x_f32 ? 3 : 1);
+  if (mm_x_copy(x_f32, m)) w.xf = slabs * static_cast<size_t>((cols / kDim + 3) / 4) * kXfQuadBytes * (x_f32 ? 3 : 1);
   if (pl.splits > 1) w.partial = slabs * pl.splits * 64 * static_cast<size_t>(rows) * sizeof(float);
   return w;
 }
@@ -1222,7 +1251,7 @@ int launch_dequant_linear_multi(const DqlTarget *targets, int n, int64_t cols, c
       return fail(PLX_EINVAL, "dequant_linear: %lld columns exceed the batched path's %lld", static_cast<long long>(cols),
                   static_cast<long long>(kMmMaxCols));
     uint8_t *wsb = static_cast<uint8_t *>(workspace);
-    uint4 *xf = reinterpret_cast<uint4 *>(wsb);
+    const uint4 *xf = reinterpret_cast<const uint4 *>(wsb);
     const int64_t slabs = (m + 63) / 64, nq = (apr + 3) / 4;
     const dim3 gx(static_cast<unsigned>(nq * 3), static_cast<unsigned>(slabs));
     if (norm) {
@@ -1230,11 +1259,16 @@ int launch_dequant_linear_multi(const DqlTarget *targets, int n, int64_t cols, c
       if (st != PLX_OK) return st;
       x = xnorm;
     }
-    if (x_is_f32)
-      hipLaunchKernelGGL((xfrag_kernel<true>), gx, dim3(256), 0, s, x, m, cols, nq, xf);
-    else
-      hipLaunchKernelGGL((xfrag_kernel<false>), gx, dim3(256), 0, s, x, m, cols, nq, xf);
-    st = check_launch("xfrag_kernel");
+    const bool copy = mm_x_copy(x_is_f32 != 0, m);
+    if (copy) {
+      if (x_is_f32)
+        hipLaunchKernelGGL((xfrag_kernel<true>), gx, dim3(256), 0, s, x, m, cols, nq, reinterpret_cast<uint4 *>(wsb));
+      else
+        hipLaunchKernelGGL((xfrag_kernel<false>), gx, dim3(256), 0, s, x, m, cols, nq, reinterpret_cast<uint4 *>(wsb));
+      st = check_launch("xfrag_kernel");
+    } else {
+      xf = static_cast<const uint4 *>(x);  // read in place by dqmm_kernel
+    }
     for (int i = 0; i < n && st == PLX_OK; ++i) {
       const DqlTarget &t = targets[i];
       if (t.rows <= 0) continue;
@@ -1242,9 +1276,9 @@ int launch_dequant_linear_multi(const DqlTarget *targets, int n, int64_t cols, c
       float *part = reinterpret_cast<float *>(wsb + mm_workspace(t.rows, cols, m, pl, x_is_f32 != 0).xf);
       const int64_t pb = ((t.rows * apr + 3) / 4) * 9;  // packed stream length
       st = m > 32 ? launch_dqmm<4>(t.packed, pb, t.sigma16, t.rows, apr, xf, m, t.y, part, pl, tab->kp_dq, !round_w,
-                                   x_is_f32, t.residual, gelu, s)
+                                   x_is_f32, !copy, t.residual, gelu, s)
                   : launch_dqmm<2>(t.packed, pb, t.sigma16, t.rows, apr, xf, m, t.y, part, pl, tab->kp_dq, !round_w,
-                                   x_is_f32, t.residual, gelu, s);
+                                   x_is_f32, !copy, t.residual, gelu, s);
       if (st != PLX_OK || pl.splits == 1) continue;
       const int64_t cnt = m * t.rows;
       if (t.rows % 4 == 0 && (reinterpret_cast<uintptr_t>(t.y) & 15u) == 0)

@@ -2,14 +2,19 @@
 // pollux_step, pollux.py:836-878); the requantize that follows it
 // (pollux.py:880-884) reuses the quantizer's launch path.
 //
-// A block of 256 threads owns 256 atoms (6,144 elements = 1,536 float4) and
+// A block of NT threads owns NT atoms (NT * 24 elements = NT * 6 float4) and
 // reads grad, m, v and the latent once and writes m, v and the latent once,
 // all as float4 streams in which consecutive lanes touch consecutive 16-byte
-// pieces (thread t moves pieces t, t+256, ..., t+1280), so every wave access
-// is 1 KiB contiguous.  The elementwise part runs on those pieces; the capped
-// step s goes through LDS, where thread t computes atom t's norm in the
-// reference's order and its cap factor, which the latent update reads back
-// per piece.  Every operation reproduces one torch op of the reference and
+// pieces (thread t moves pieces t, t+NT, ..., t+5NT), so every wave access is
+// 1 KiB contiguous.  The streams are nontemporal (each byte is touched once:
+// loads and stores that do not claim cache lines for reuse), which took the
+// 4608x1152 update from 33.5 to 26.3 us.  NT = 64 for large launches (4x the
+// blocks of NT = 256 balance better: 26.3 against 28.5 us), 256 below ~100K
+// atoms (fewer, fuller blocks: 10.7 against 11.6 us at 55,296 atoms).  The
+// elementwise part runs on those pieces; the capped step s goes through LDS,
+// where thread t computes atom t's norm in the reference's order and its cap
+// factor, which the latent update reads back per piece.
+// Every operation reproduces one torch op of the reference and
 // its rounding (fp32 tensors, Python floats entering as fp32, as torch
 // evaluates them on the CPU):
 //   m   = fma(g, 1-b1, m*b1)                 m.mul_(b1).add_(g, alpha=1-b1)
@@ -40,23 +45,37 @@
 namespace plx {
 namespace {
 
-constexpr int kOptThreads = 256;                     // = atoms per block
-constexpr int kOptPieces = kOptThreads * kDim / 4;   // float4 pieces per block (1,536)
-constexpr int kOptPerThread = kOptPieces / kOptThreads;  // 6
+constexpr int kOptSmall = 256;        // atoms (= threads) per block below kOptLargeAtoms
+constexpr int kOptLarge = 64;         // ... and from there on
+constexpr int64_t kOptLargeAtoms = 98304;
+constexpr int kEnergyThreads = 256;
 
-__global__ __launch_bounds__(kOptThreads) void adam_h24_kernel(const float *__restrict__ grad, float *__restrict__ m,
-                                                               float *__restrict__ v, float *__restrict__ latent,
-                                                               int64_t n_atoms, const float *__restrict__ scal,
-                                                               float *__restrict__ partial) {
+typedef float f32x4_nt __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float4 load_nt(const float4 *p) {
+  const f32x4_nt v = __builtin_nontemporal_load(reinterpret_cast<const f32x4_nt *>(p));
+  return make_float4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ void store_nt(float4 *p, float a, float b, float c, float d) {
+  __builtin_nontemporal_store(f32x4_nt{a, b, c, d}, reinterpret_cast<f32x4_nt *>(p));
+}
+
+template <int NT>
+__global__ __launch_bounds__(NT) void adam_h24_kernel(const float *__restrict__ grad, float *__restrict__ m,
+                                                      float *__restrict__ v, float *__restrict__ latent,
+                                                      int64_t n_atoms, const float *__restrict__ scal,
+                                                      float *__restrict__ partial) {
   // no contraction: a multiply feeding an add (latent * wdf + s) stays two
   // roundings, as in the reference; every FMA below is an explicit __fmaf_rn
 #pragma clang fp contract(off)
-  __shared__ __align__(16) float sl[kOptThreads * kDim];  // the block's capped-step inputs s, atom-major
-  __shared__ float fac_s[kOptThreads];                    // per atom: min(cap / (|s| + eps), 1)
-  __shared__ float red[kOptThreads];
+  constexpr int kPieces = NT * kDim / 4;        // float4 pieces per block
+  constexpr int kPerThread = kPieces / NT;      // 6
+  __shared__ __align__(16) float sl[NT * kDim];  // the block's capped-step inputs s, atom-major
+  __shared__ float fac_s[NT];                    // per atom: min(cap / (|s| + eps), 1)
+  __shared__ float red[NT];
   const int tid = threadIdx.x;
-  const int64_t a0 = static_cast<int64_t>(blockIdx.x) * kOptThreads;
-  const int64_t pieces = min(static_cast<int64_t>(kOptPieces), (n_atoms - a0) * (kDim / 4));  // whole atoms
+  const int64_t a0 = static_cast<int64_t>(blockIdx.x) * NT;
+  const int64_t pieces = min(static_cast<int64_t>(kPieces), (n_atoms - a0) * (kDim / 4));  // whole atoms
   const float4 *g4 = reinterpret_cast<const float4 *>(grad + a0 * kDim);
   float4 *m4 = reinterpret_cast<float4 *>(m + a0 * kDim);
   float4 *v4 = reinterpret_cast<float4 *>(v + a0 * kDim);
@@ -65,14 +84,13 @@ __global__ __launch_bounds__(kOptThreads) void adam_h24_kernel(const float *__re
   const float bc1 = scal[4], bc2 = scal[5], neg_scale = scal[6], wdf = scal[7], cap = scal[8];
   const float eps = __uint_as_float(kEpsBits);
 
-  float4 lat[kOptPerThread];
+  float4 lat[kPerThread];
 #pragma unroll
-  for (int j = 0; j < kOptPerThread; ++j) {
-    const int i = tid + j * kOptThreads;
+  for (int j = 0; j < kPerThread; ++j) {
+    const int i = tid + j * NT;
     if (i >= pieces) continue;
-    const float4 g = g4[i];
-    float4 mm = m4[i], vv = v4[i];
-    lat[j] = l4[i];
+    const float4 g = load_nt(g4 + i), mm = load_nt(m4 + i), vv = load_nt(v4 + i);
+    lat[j] = load_nt(l4 + i);
     float gv[4] = {g.x, g.y, g.z, g.w}, mv[4] = {mm.x, mm.y, mm.z, mm.w}, vw[4] = {vv.x, vv.y, vv.z, vv.w};
     float sv[4];
 #pragma unroll
@@ -83,8 +101,8 @@ __global__ __launch_bounds__(kOptThreads) void adam_h24_kernel(const float *__re
       const float den = sqrtf(vw[c] / bc2) + eps;
       sv[c] = neg_scale * (mu / den);
     }
-    m4[i] = make_float4(mv[0], mv[1], mv[2], mv[3]);
-    v4[i] = make_float4(vw[0], vw[1], vw[2], vw[3]);
+    store_nt(m4 + i, mv[0], mv[1], mv[2], mv[3]);
+    store_nt(v4 + i, vw[0], vw[1], vw[2], vw[3]);
     reinterpret_cast<float4 *>(sl)[i] = make_float4(sv[0], sv[1], sv[2], sv[3]);
   }
   __syncthreads();
@@ -104,20 +122,20 @@ __global__ __launch_bounds__(kOptThreads) void adam_h24_kernel(const float *__re
   __syncthreads();
   float e2 = 0.f;  // this thread's sum of squared capped steps
 #pragma unroll
-  for (int j = 0; j < kOptPerThread; ++j) {
-    const int i = tid + j * kOptThreads;
+  for (int j = 0; j < kPerThread; ++j) {
+    const int i = tid + j * NT;
     if (i >= pieces) continue;
     const float fac = fac_s[i / (kDim / 4)];
     const float4 sv = reinterpret_cast<const float4 *>(sl)[i];
     const float sc[4] = {sv.x * fac, sv.y * fac, sv.z * fac, sv.w * fac};
-    l4[i] = make_float4(lat[j].x * wdf + sc[0], lat[j].y * wdf + sc[1], lat[j].z * wdf + sc[2], lat[j].w * wdf + sc[3]);
+    store_nt(l4 + i, lat[j].x * wdf + sc[0], lat[j].y * wdf + sc[1], lat[j].z * wdf + sc[2], lat[j].w * wdf + sc[3]);
 #pragma unroll
     for (int c = 0; c < 4; ++c) e2 = __fmaf_rn(sc[c], sc[c], e2);
   }
   red[tid] = e2;
   __syncthreads();
 #pragma unroll
-  for (int w = kOptThreads / 2; w > 0; w >>= 1) {
+  for (int w = NT / 2; w > 0; w >>= 1) {
     if (tid < w) red[tid] = red[tid] + red[tid + w];
     __syncthreads();
   }
@@ -125,22 +143,23 @@ __global__ __launch_bounds__(kOptThreads) void adam_h24_kernel(const float *__re
 }
 
 // norm_out[0] = sqrt(sum of the block partials), summed in a fixed order.
-__global__ __launch_bounds__(kOptThreads) void energy_kernel(const float *__restrict__ partial, int64_t n,
+__global__ __launch_bounds__(kEnergyThreads) void energy_kernel(const float *__restrict__ partial, int64_t n,
                                                              float *__restrict__ norm_out) {
-  __shared__ float red[kOptThreads];
+  __shared__ float red[kEnergyThreads];
   float s = 0.f;
-  for (int64_t i = threadIdx.x; i < n; i += kOptThreads) s = __fadd_rn(s, partial[i]);
+  for (int64_t i = threadIdx.x; i < n; i += kEnergyThreads) s = __fadd_rn(s, partial[i]);
   red[threadIdx.x] = s;
   __syncthreads();
 #pragma unroll
-  for (int w = kOptThreads / 2; w > 0; w >>= 1) {
+  for (int w = kEnergyThreads / 2; w > 0; w >>= 1) {
     if (threadIdx.x < w) red[threadIdx.x] = __fadd_rn(red[threadIdx.x], red[threadIdx.x + w]);
     __syncthreads();
   }
   if (threadIdx.x == 0) norm_out[0] = sqrtf(red[0]);
 }
 
-int64_t opt_blocks(int64_t n_atoms) { return (n_atoms + kOptThreads - 1) / kOptThreads; }
+int opt_threads(int64_t n_atoms) { return n_atoms >= kOptLargeAtoms ? kOptLarge : kOptSmall; }
+int64_t opt_blocks(int64_t n_atoms) { return (n_atoms + opt_threads(n_atoms) - 1) / opt_threads(n_atoms); }
 
 }  // namespace
 
@@ -157,12 +176,16 @@ int launch_adam_h24(const float *grad, float *m, float *v, float *latent, int64_
   const int64_t blocks = opt_blocks(n_atoms);
   if (blocks > 0x7FFFFFFFll) return fail(PLX_EINVAL, "pollux_step_h24: %lld atoms exceed one launch", static_cast<long long>(n_atoms));
   float *partial = static_cast<float *>(workspace);
-  hipLaunchKernelGGL(adam_h24_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kOptThreads), 0, s, grad, m, v, latent,
-                     n_atoms, scalars, partial);
+  if (opt_threads(n_atoms) == kOptLarge)
+    hipLaunchKernelGGL((adam_h24_kernel<kOptLarge>), dim3(static_cast<unsigned>(blocks)), dim3(kOptLarge), 0, s, grad, m,
+                       v, latent, n_atoms, scalars, partial);
+  else
+    hipLaunchKernelGGL((adam_h24_kernel<kOptSmall>), dim3(static_cast<unsigned>(blocks)), dim3(kOptSmall), 0, s, grad, m,
+                       v, latent, n_atoms, scalars, partial);
   int st = check_launch("adam_h24_kernel");
   if (st != PLX_OK) return st;
   if (adam_norm_out) {
-    hipLaunchKernelGGL(energy_kernel, dim3(1), dim3(kOptThreads), 0, s, partial, blocks, adam_norm_out);
+    hipLaunchKernelGGL(energy_kernel, dim3(1), dim3(kEnergyThreads), 0, s, partial, blocks, adam_norm_out);
     st = check_launch("energy_kernel");
   }
   return st;
