@@ -284,6 +284,20 @@ int plx_decode_attention(const float *q, const float *k, const float *v, const f
                          const float *k_norm_w, float eps, float *k_cache, float *v_cache,
                          const int64_t *pos, int64_t n, int64_t max_len, float *out, void *stream);
 
+/* The attention of t new positions p0 .. p0+t-1 of each of b sequences (a
+ * prompt's prefill over a cached prefix: pollux.py:615-626 with is_causal,
+ * positions < p0 taken from the caches).  q, k, v, out: fp32 [b, t, heads,
+ * 24] (the projections' [b, t, heads*24] rows); q_norm_w, k_norm_w: fp32 [24];
+ * caches fp32 [b, heads, max_len, 24].  Writes RMSNorm(k) and v at positions
+ * p0 .. p0+t-1, then out[s, i, h] = softmax_{j <= p0+i}(RMSNorm(q_i) . K_j /
+ * sqrt 24) V_j.  All arrays 16-byte aligned; p0 + t <= max_len.  Replaces the
+ * q_ln / k_ln calls, the cache writes and F.scaled_dot_product_attention of the
+ * attention's multi-token path (no counterpart in the reference, which has no
+ * cache: with p0 = 0 it is pollux.py:615-626 itself). */
+int plx_prefill_attention(const float *q, const float *k, const float *v, const float *q_norm_w,
+                          const float *k_norm_w, float eps, float *k_cache, float *v_cache, int64_t b,
+                          int64_t heads, int64_t t, int64_t p0, int64_t max_len, float *out, void *stream);
+
 /* out[r] = the index of the maximum of x[r, :] (fp32 [rows, cols], int64 out):
  * torch.argmax's rule (the first index among equal maxima; a NaN counts as the
  * maximum).  Greedy decoding's token choice (generate.py:313-320, top_k = 1)

@@ -327,6 +327,17 @@ int plx_decode_attention(const float *q, const float *k, const float *v, const f
                                  as_stream(stream));
 }
 
+int plx_prefill_attention(const float *q, const float *k, const float *v, const float *q_norm_w,
+                          const float *k_norm_w, float eps, float *k_cache, float *v_cache, int64_t b, int64_t heads,
+                          int64_t t, int64_t p0, int64_t max_len, float *out, void *stream) {
+  PLX_REQUIRE(b >= 0 && heads >= 0 && t >= 0, "plx_prefill_attention: negative shape (%lld, %lld, %lld)",
+              static_cast<long long>(b), static_cast<long long>(t), static_cast<long long>(heads));
+  if (b == 0 || heads == 0 || t == 0) return PLX_OK;
+  PLX_REQUIRE(q && k && v && q_norm_w && k_norm_w && k_cache && v_cache && out, "plx_prefill_attention: null pointer");
+  return launch_prefill_attention(q, k, v, q_norm_w, k_norm_w, eps, k_cache, v_cache, b, heads, t, p0, max_len, out,
+                                  as_stream(stream));
+}
+
 size_t plx_dequant_linear_workspace_bytes(int64_t rows, int64_t cols, int64_t m_rows, int flags) {
   if (rows <= 0 || cols <= 0 || cols % kDim != 0 || m_rows <= 0) return 0;
   return dequant_linear_workspace_bytes(rows, cols, m_rows, flags);

@@ -16,6 +16,16 @@
 //   Reading the position from device memory lets a captured graph replay the
 //   step while the position advances on the device; a position outside the
 //   cache writes nothing and yields NaN outputs.
+//
+// prefill_attention_kernel: the same for a chunk of up to 256 new positions
+//   p .. p+tc-1 of every sequence (the prompt of a prefill, pollux.py:615-626
+//   with is_causal over the cached prefix): one block per (head, sequence)
+//   normalises the chunk's q and k rows (a thread per row), writes k and v
+//   into the caches and keeps all three in LDS; then 16 lanes per query i
+//   (keys j = lane, lane + 16, ... <= p + i; cached ones from the caches, the
+//   chunk's from LDS) run an online softmax each and combine by DPP within
+//   their row of 16 lanes.  Chunks of a longer prompt are consecutive launches,
+//   so each one reads the previous chunks' rows from the caches.
 
 #include "plx_device.h"
 
@@ -215,6 +225,123 @@ __global__ __launch_bounds__(kAttnThreads) void decode_attention_kernel(
   }
 }
 
+constexpr int kPrefillChunk = 256;  // new positions per launch (q, k, v rows of the chunk in LDS: 72 KB)
+
+// q, k, v, out: [b, t, H, 24] (rows of the whole prompt; this launch takes rows
+// c0 .. c0+tc-1 of each sequence at cache positions p .. p+tc-1); caches
+// [b, H, max_len, 24].
+__global__ __launch_bounds__(kAttnThreads) void prefill_attention_kernel(
+    const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v,
+    const float *__restrict__ q_w, const float *__restrict__ k_w, float eps, float *__restrict__ k_cache,
+    float *__restrict__ v_cache, int64_t heads, int64_t t_total, int64_t c0, int tc, int64_t p, int64_t max_len,
+    float scale, float *__restrict__ out) {
+  __shared__ __align__(16) float qs[kPrefillChunk][kDim];
+  __shared__ __align__(16) float ks[kPrefillChunk][kDim];
+  __shared__ __align__(16) float vs[kPrefillChunk][kDim];
+  const int tid = threadIdx.x;
+  const int64_t h = blockIdx.x, bb = blockIdx.y;
+  const int64_t row_stride = heads * kDim;                           // between positions of one sequence
+  const int64_t in0 = (bb * t_total + c0) * row_stride + h * kDim;   // row c0 of this (sequence, head)
+  float *kc = k_cache + (bb * heads + h) * max_len * kDim;
+  float *vc = v_cache + (bb * heads + h) * max_len * kDim;
+
+  // the chunk's rows: RMS norms of q and k (q_ln / k_ln), k and v into the caches
+  for (int r = tid; r < tc; r += kAttnThreads) {
+    const float4 *q4 = reinterpret_cast<const float4 *>(q + in0 + r * row_stride);
+    const float4 *k4 = reinterpret_cast<const float4 *>(k + in0 + r * row_stride);
+    const float4 *v4 = reinterpret_cast<const float4 *>(v + in0 + r * row_stride);
+    float qv[kDim], kv[kDim], vv[kDim];
+#pragma unroll
+    for (int i = 0; i < kDim / 4; ++i) {
+      const float4 a = q4[i], b = k4[i], c = v4[i];
+      qv[4 * i] = a.x; qv[4 * i + 1] = a.y; qv[4 * i + 2] = a.z; qv[4 * i + 3] = a.w;
+      kv[4 * i] = b.x; kv[4 * i + 1] = b.y; kv[4 * i + 2] = b.z; kv[4 * i + 3] = b.w;
+      vv[4 * i] = c.x; vv[4 * i + 1] = c.y; vv[4 * i + 2] = c.z; vv[4 * i + 3] = c.w;
+    }
+    float sq = 0.f, sk = 0.f;
+#pragma unroll
+    for (int i = 0; i < kDim; ++i) {
+      sq = fmaf(qv[i], qv[i], sq);
+      sk = fmaf(kv[i], kv[i], sk);
+    }
+    const float rq = 1.0f / sqrtf(sq / static_cast<float>(kDim) + eps);
+    const float rk = 1.0f / sqrtf(sk / static_cast<float>(kDim) + eps);
+    float4 *kd = reinterpret_cast<float4 *>(kc + (p + r) * kDim);
+    float4 *vd = reinterpret_cast<float4 *>(vc + (p + r) * kDim);
+#pragma unroll
+    for (int i = 0; i < kDim / 4; ++i) {
+      const float4 qn = make_float4(qv[4 * i] * rq * q_w[4 * i], qv[4 * i + 1] * rq * q_w[4 * i + 1],
+                                    qv[4 * i + 2] * rq * q_w[4 * i + 2], qv[4 * i + 3] * rq * q_w[4 * i + 3]);
+      const float4 kn = make_float4(kv[4 * i] * rk * k_w[4 * i], kv[4 * i + 1] * rk * k_w[4 * i + 1],
+                                    kv[4 * i + 2] * rk * k_w[4 * i + 2], kv[4 * i + 3] * rk * k_w[4 * i + 3]);
+      const float4 vn = make_float4(vv[4 * i], vv[4 * i + 1], vv[4 * i + 2], vv[4 * i + 3]);
+      reinterpret_cast<float4 *>(qs[r])[i] = qn;
+      reinterpret_cast<float4 *>(ks[r])[i] = kn;
+      reinterpret_cast<float4 *>(vs[r])[i] = vn;
+      kd[i] = kn;
+      vd[i] = vn;
+    }
+  }
+  __syncthreads();
+
+  // 16 lanes (one DPP row) per query; a row whose query is past the chunk
+  // skips the round as a whole, so every DPP exchange sees its full row
+  const int grp = tid >> 4, l16 = tid & 15;
+  for (int i = grp; i < tc; i += kAttnThreads / 16) {
+    const int64_t last = p + i;  // the query's own position: keys 0 .. last
+    float qr[kDim];
+#pragma unroll
+    for (int c = 0; c < kDim; ++c) qr[c] = qs[i][c];
+    float m = -INFINITY, l = 0.f, acc[kDim];
+#pragma unroll
+    for (int c = 0; c < kDim; ++c) acc[c] = 0.f;
+    auto step = [&](const float4 *k4, const float4 *v4) {
+      float kr[kDim], vr[kDim];
+#pragma unroll
+      for (int c = 0; c < kDim / 4; ++c) {
+        const float4 a = k4[c], b = v4[c];
+        kr[4 * c] = a.x; kr[4 * c + 1] = a.y; kr[4 * c + 2] = a.z; kr[4 * c + 3] = a.w;
+        vr[4 * c] = b.x; vr[4 * c + 1] = b.y; vr[4 * c + 2] = b.z; vr[4 * c + 3] = b.w;
+      }
+      float sc = 0.f;
+#pragma unroll
+      for (int c = 0; c < kDim; ++c) sc = fmaf(qr[c], kr[c], sc);
+      sc *= scale;
+      const float mn = fmaxf(m, sc);
+      const float a = expf(m - mn), pr = expf(sc - mn);  // m = -inf at a lane's first key: a = 0
+      l = fmaf(l, a, pr);
+#pragma unroll
+      for (int c = 0; c < kDim; ++c) acc[c] = fmaf(acc[c], a, pr * vr[c]);
+      m = mn;
+    };
+    // keys j = l16 + 16n in increasing order: the cached ones, then the chunk's
+    int64_t j = l16;
+    for (; j < p; j += 16)
+      step(reinterpret_cast<const float4 *>(kc + j * kDim), reinterpret_cast<const float4 *>(vc + j * kDim));
+    for (; j <= last; j += 16)
+      step(reinterpret_cast<const float4 *>(ks[j - p]), reinterpret_cast<const float4 *>(vs[j - p]));
+    // the row's maximum, every lane's state rescaled to it, then the sums
+    float bmv[1] = {m};
+    group_reduce<16, true>(bmv);
+    const float f = m == -INFINITY ? 0.f : expf(m - bmv[0]);
+    float part[kDim + 1];
+#pragma unroll
+    for (int c = 0; c < kDim; ++c) part[c] = acc[c] * f;
+    part[kDim] = l * f;
+    group_reduce<16>(part);
+    float *o = out + in0 + static_cast<int64_t>(i) * row_stride;
+    const float inv = part[kDim];
+    // lane c writes coordinate c, lanes 0..7 also c + 16 (static indices: no scratch)
+    float v0 = part[0], v1 = part[16];
+#pragma unroll
+    for (int c = 1; c < 16; ++c) v0 = l16 == c ? part[c] : v0;
+#pragma unroll
+    for (int c = 17; c < kDim; ++c) v1 = l16 == c - 16 ? part[c] : v1;
+    o[l16] = v0 / inv;
+    if (l16 < kDim - 16) o[16 + l16] = v1 / inv;
+  }
+}
+
 // torch.argmax's order: a NaN beats every number; among equal values (or
 // NaNs) the lowest index wins.
 __device__ __forceinline__ bool arg_better(float v, int i, float bv, int bi) {
@@ -328,6 +455,32 @@ int launch_decode_attention(const float *q, const float *k, const float *v, cons
   hipLaunchKernelGGL(decode_attention_kernel, dim3(static_cast<unsigned>(seqs_heads)), dim3(kAttnThreads), 0, s, q, k,
                      v, q_w, k_w, eps, k_cache, v_cache, pos, max_len, 1.0f / sqrtf(static_cast<float>(kDim)), out);
   return check_launch("decode_attention_kernel");
+}
+
+int launch_prefill_attention(const float *q, const float *k, const float *v, const float *q_w, const float *k_w,
+                             float eps, float *k_cache, float *v_cache, int64_t b, int64_t heads, int64_t t, int64_t p0,
+                             int64_t max_len, float *out, hipStream_t s) {
+  if (b <= 0 || heads <= 0 || t <= 0) return PLX_OK;
+  if (max_len <= 0 || max_len > (1 << 24))
+    return fail(PLX_EINVAL, "prefill_attention: cache length %lld outside 1..2^24", static_cast<long long>(max_len));
+  if (p0 < 0 || p0 + t > max_len)
+    return fail(PLX_EINVAL, "prefill_attention: positions %lld..%lld outside the cache of %lld", static_cast<long long>(p0),
+                static_cast<long long>(p0 + t - 1), static_cast<long long>(max_len));
+  if (heads > 0xFFFFll || b > 0xFFFFll) return fail(PLX_EINVAL, "prefill_attention: too many heads or sequences");
+  const uintptr_t al = reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) | reinterpret_cast<uintptr_t>(v) |
+                       reinterpret_cast<uintptr_t>(k_cache) | reinterpret_cast<uintptr_t>(v_cache) |
+                       reinterpret_cast<uintptr_t>(out);
+  if ((al & 15u) != 0) return fail(PLX_EINVAL, "prefill_attention: q, k, v, caches and out must be 16-byte aligned");
+  const float scale = 1.0f / sqrtf(static_cast<float>(kDim));
+  for (int64_t c0 = 0; c0 < t; c0 += kPrefillChunk) {
+    const int tc = static_cast<int>(t - c0 < kPrefillChunk ? t - c0 : kPrefillChunk);
+    hipLaunchKernelGGL(prefill_attention_kernel, dim3(static_cast<unsigned>(heads), static_cast<unsigned>(b)),
+                       dim3(kAttnThreads), 0, s, q, k, v, q_w, k_w, eps, k_cache, v_cache, heads, t, c0, tc, p0 + c0,
+                       max_len, scale, out);
+    const int st = check_launch("prefill_attention_kernel");
+    if (st != PLX_OK) return st;
+  }
+  return PLX_OK;
 }
 
 }  // namespace plx

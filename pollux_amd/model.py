@@ -27,7 +27,6 @@ from typing import Any
 
 import torch
 import torch.nn as nn
-import torch.nn.functional as F
 
 from . import _lib
 from .castor import H24_DIM, assert_row_aligned_width
@@ -153,6 +152,27 @@ def decode_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q_ln: RM
     return out
 
 
+def prefill_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q_ln: RMSNorm, k_ln: RMSNorm,
+                      k_cache: torch.Tensor, v_cache: torch.Tensor, p0: int) -> torch.Tensor:
+    """Causal attention of t new positions p0 .. p0+t-1 per sequence (plx_prefill_attention).
+
+    q, k, v: [b, t, H*24] projections; caches [b, H, max_len, 24]. Writes
+    k_ln(k) and v at positions p0 .. p0+t-1 and returns [b, t, H*24]: each query
+    attends to every position up to its own (the cached prefix included).
+    """
+    b, t, c = q.shape
+    heads = c // H24_DIM
+    out = torch.empty(b, t, c, dtype=torch.float32, device=q.device)
+    qq, kk, vv = q.contiguous(), k.contiguous(), v.contiguous()
+    with torch.cuda.device(q.device):
+        st = _lib.lib().plx_prefill_attention(
+            _lib.ptr(qq), _lib.ptr(kk), _lib.ptr(vv), _lib.ptr(q_ln.weight.detach()), _lib.ptr(k_ln.weight.detach()),
+            float(q_ln.eps), _lib.ptr(k_cache), _lib.ptr(v_cache), b, heads, t, int(p0), k_cache.shape[2],
+            _lib.ptr(out), _lib.stream_of(q.device))
+    _lib.check(st, "prefill_attention")
+    return out
+
+
 class RMSNorm(nn.Module):
     """x * rsqrt(mean(x^2) + eps) * weight over the last dimension (pollux.py:566-582), fused on the device."""
 
@@ -212,24 +232,16 @@ class PackedCausalAttention(nn.Module):
                 pos = torch.full((), cache.length, dtype=torch.long, device=x.device)
             o = decode_attention(q, k, v, self.q_ln, self.k_ln, cache.k[layer], cache.v[layer], pos)
             return packed_linear_group([self.o_proj], o, residuals=[residual])[0]
-        q = self.q_ln(q.view(b, t, self.n_heads, self.d_head)).transpose(1, 2)
-        k = self.k_ln(k.view(b, t, self.n_heads, self.d_head)).transpose(1, 2)
-        v = v.view(b, t, self.n_heads, self.d_head).transpose(1, 2)
+        # q / k norms, cache writes and the causal attention in one kernel; without
+        # a cache the keys and values go to a scratch cache of the prompt's length
         if cache is None:
-            attn = F.scaled_dot_product_attention(q, k, v, is_causal=True)
+            kc = torch.empty(b, self.n_heads, t, self.d_head, dtype=torch.float32, device=x.device)
+            vc = torch.empty_like(kc)
+            p0 = 0
         else:
-            p0 = cache.length
-            cache.k[layer][:, :, p0:p0 + t] = k
-            cache.v[layer][:, :, p0:p0 + t] = v
-            keys, vals = cache.k[layer][:, :, :p0 + t], cache.v[layer][:, :, :p0 + t]
-            if p0 == 0:
-                attn = F.scaled_dot_product_attention(q, keys, vals, is_causal=True)
-            else:
-                # query i sits at position p0 + i and sees positions <= p0 + i
-                allowed = torch.ones(t, p0 + t, dtype=torch.bool, device=x.device).tril(diagonal=p0)
-                attn = F.scaled_dot_product_attention(q, keys, vals, attn_mask=allowed)
-        return packed_linear_group([self.o_proj], attn.transpose(1, 2).contiguous().view(b, t, c),
-                                   residuals=[residual])[0]
+            kc, vc, p0 = cache.k[layer], cache.v[layer], cache.length
+        attn = prefill_attention(q, k, v, self.q_ln, self.k_ln, kc, vc, p0)
+        return packed_linear_group([self.o_proj], attn, residuals=[residual])[0]
 
 
 class PackedMLP(nn.Module):

@@ -1,11 +1,15 @@
-"""plx_rms_norm and plx_decode_attention (the packed decoder's fused steps) against torch fp32 references.
+"""plx_rms_norm, plx_decode_attention and plx_prefill_attention (the packed decoder's fused steps)
+against torch references.
 
 Bars (stated): RMS norm within 2e-6 relative per element of the torch
 expression x * rsqrt(mean(x^2) + eps) * w (pollux.py:580-582); decode
 attention within 1e-5 relative (L2) of scaled_dot_product_attention over the
 cache with the new row appended, the written cache row within 2e-6 of the
 normalised k and v bit-exact, every other cache row untouched; a position
-outside the cache writes nothing and returns NaN.
+outside the cache writes nothing and returns NaN.  Prefill attention: within
+1e-5 relative (L2) of the causal attention computed in fp64 on the CPU over
+the cached prefix and the new rows, written rows as for decode, every other
+cache row untouched, positions past the cache refused.
 """
 
 import math
@@ -13,7 +17,7 @@ import math
 import pytest
 import torch
 
-from pollux_amd.model import RMSNorm, decode_attention, rms_norm
+from pollux_amd.model import RMSNorm, decode_attention, prefill_attention, rms_norm
 
 pytestmark = pytest.mark.gpu
 
@@ -129,3 +133,56 @@ def test_argmax_rows_long_rows_and_out(dev):
     assert torch.equal(out, torch.argmax(x, dim=-1))
     with pytest.raises(ValueError):
         argmax_rows(x, out=torch.empty(3, dtype=torch.long, device=dev))
+
+
+# (b, heads, t, p0, max_len): a Pollux-1920 prompt, two chunks of 256, a cached
+# prefix, one token, a prefix plus more than a chunk
+@pytest.mark.parametrize("b,heads,t,p0,max_len", [(1, 80, 64, 0, 128), (2, 3, 300, 0, 300), (2, 5, 17, 40, 64),
+                                                  (1, 2, 1, 0, 4), (1, 4, 257, 7, 300)])
+def test_prefill_attention(dev, b, heads, t, p0, max_len):
+    g = torch.Generator().manual_seed(b * 7919 + heads * 31 + t + p0)
+    c = heads * 24
+    q = torch.randn(b, t, c, generator=g)
+    k = torch.randn(b, t, c, generator=g)
+    v = torch.randn(b, t, c, generator=g)
+    qw = 1.0 + 0.1 * torch.randn(24, generator=g)
+    kw = 1.0 + 0.1 * torch.randn(24, generator=g)
+    kc0 = torch.randn(b, heads, max_len, 24, generator=g)
+    vc0 = torch.randn(b, heads, max_len, 24, generator=g)
+    q_ln, k_ln = RMSNorm(24).to(dev), RMSNorm(24).to(dev)
+    with torch.no_grad():
+        q_ln.weight.copy_(qw)
+        k_ln.weight.copy_(kw)
+    kc, vc = kc0.to(dev), vc0.to(dev)
+    with torch.no_grad():
+        out = prefill_attention(q.to(dev), k.to(dev), v.to(dev), q_ln, k_ln, kc, vc, p0)
+    # reference (fp64, CPU): new rows at p0 .. p0+t-1, query i sees positions <= p0 + i
+    qn = _ref_norm(q.view(b, t, heads, 24).double(), qw.double()).transpose(1, 2).contiguous()
+    kn = _ref_norm(k.view(b, t, heads, 24).double(), kw.double()).transpose(1, 2).contiguous()
+    vn = v.view(b, t, heads, 24).double().transpose(1, 2).contiguous()
+    keys, vals = kc0.double().clone(), vc0.double().clone()
+    keys[:, :, p0:p0 + t] = kn
+    vals[:, :, p0:p0 + t] = vn
+    keys, vals = keys[:, :, :p0 + t].contiguous(), vals[:, :, :p0 + t].contiguous()
+    s = torch.matmul(qn, keys.transpose(-1, -2).contiguous()) / math.sqrt(24)
+    allowed = torch.ones(t, p0 + t, dtype=torch.bool).tril(diagonal=p0)
+    s = s.masked_fill(~allowed, float("-inf"))
+    ref = torch.matmul(torch.softmax(s, dim=-1), vals).transpose(1, 2).reshape(b, t, c)
+    rel = ((out.cpu().double() - ref).norm() / ref.norm()).item()
+    print(f"[dec] prefill_attention b={b} H={heads} t={t} p0={p0}: rel {rel:.2e}", flush=True)
+    assert rel <= 1e-5
+    kcc, vcc = kc.cpu(), vc.cpu()
+    assert ((kcc[:, :, p0:p0 + t].double() - kn).abs() / kn.abs().clamp_min(1e-30)).max().item() <= 2e-6
+    assert torch.equal(vcc[:, :, p0:p0 + t], v.view(b, t, heads, 24).transpose(1, 2))
+    rest = [j for j in range(max_len) if not p0 <= j < p0 + t]
+    assert torch.equal(kcc[:, :, rest], kc0[:, :, rest]) and torch.equal(vcc[:, :, rest], vc0[:, :, rest])
+
+
+def test_prefill_attention_refuses_positions_past_the_cache(dev):
+    b, heads, max_len = 1, 2, 8
+    x = torch.randn(b, 5, 48, device=dev)
+    kc = torch.zeros(b, heads, max_len, 24, device=dev)
+    ln = RMSNorm(24).to(dev)
+    with pytest.raises(ValueError):
+        prefill_attention(x, x, x, ln, ln, kc, kc.clone(), 4)
+    assert torch.equal(kc, torch.zeros_like(kc))
