@@ -323,8 +323,10 @@ int plx_dequant_int8_rows(const int8_t *q, const uint16_t *mu16, int64_t rows, i
  * (pollux.py:562-563, F.linear(x, W.to(x.dtype))).  n(x) = x, or with a
  * norm_weight (fp32 [cols]) x * rsqrt(mean(x^2) + norm_eps) * norm_weight per
  * token (the final norm ln_f before the head, pollux.py:699-700).
- * cols % 16 == 0 and <= 4,096; q, x, norm_weight 16-byte aligned.  Streams the
- * INT8 rows once per 4 tokens (meant for decode batches of a few tokens). */
+ * cols % 16 == 0 and <= 4,096; q, x, norm_weight 16-byte aligned.  Up to 4
+ * tokens a GEMV streams the INT8 rows once per 4 tokens; from 5 tokens an MFMA
+ * kernel reads them once per 64 tokens (both exact products, fp32 sums; with a
+ * norm the MFMA kernel scales each token's sums by the rsqrt at the end). */
 int plx_int8_linear(const int8_t *q, const uint16_t *mu16, int64_t rows, int64_t cols, const float *x,
                     int64_t m_rows, const float *norm_weight, float norm_eps, float *y, void *stream);
 

@@ -25,6 +25,20 @@
 //   1152 gives q exactly, and one fp16 multiply by s16 rounds q * s16 once -
 //   the same value as fp16(fp32(q) * fp32(s16)), whose fp32 product is exact.
 //
+// int8mm_kernel: the same product for two or more tokens on MFMA.  A block
+//   owns 64 rows x 16*MT tokens and its 4 waves split K (each wave a
+//   contiguous run of 32-column steps).  Per step a lane decodes 8 weights of
+//   one row per row tile (the fp16 values above, split exactly into bf16
+//   hi + lo: lo = W - bf16(W) has at most 3 significant bits) and splits 8
+//   activations of one token per token tile exactly into three bf16 parts
+//   (x = h + m + l), so five v_mfma_f32_16x16x32_bf16 per tile pair (h, m, l
+//   times hi; h, m times lo; l * lo is below 2^-25 of the product) form the
+//   products of fp32 x with the fp16 weights in fp32 accumulation.  The
+//   waves' tiles are summed through LDS in wave order.  With ln_f the
+//   activations enter as x * w (the norm weight) and each token's sum is
+//   scaled by rsqrt(mean(x^2) + eps) at the end, the sums of squares taken
+//   from the same loads.  With keys, each block's best argmax key per token.
+//
 // int8_embed_kernel: out[b, i, :] = fp32(w[idx[b, i], :]) + pos_w[p0 + i, :]
 //   (PackedInt8Embedding.forward + the position embedding, pollux.py:532-533,
 //   691-693), p0 read from device memory (a captured graph replays it while
@@ -285,6 +299,230 @@ __global__ __launch_bounds__(64 * kLinWaves) void int8_linear_kernel(
   }
 }
 
+typedef __bf16 bf16x8_i8 __attribute__((ext_vector_type(8)));
+typedef float f32x4_i8 __attribute__((ext_vector_type(4)));
+
+constexpr int kI8mmRows = 64;     // output rows per block (four MFMA row tiles)
+constexpr int kI8mmWaves = 4;     // waves per block, splitting K
+constexpr int kI8mmRedStride = 68; // floats per token row of the cross-wave sum (64 rows + pad)
+
+// Two fp32 values rounded to bf16 (RNE) by one v_cvt_pk_bf16_f32, low half first.
+__device__ __forceinline__ uint32_t pk_bf16(float a, float b) {
+  typedef __bf16 bf16x2_i8 __attribute__((ext_vector_type(2)));
+  const bf16x2_i8 v = {static_cast<__bf16>(a), static_cast<__bf16>(b)};
+  return __builtin_bit_cast(uint32_t, v);
+}
+__device__ __forceinline__ float bf16_lo_f32(uint32_t p) { return __uint_as_float(p << 16); }
+__device__ __forceinline__ float bf16_hi_f32(uint32_t p) { return __uint_as_float(p & 0xFFFF0000u); }
+
+// 8 fp32 values split exactly into three bf16 parts (v = h + m + l while the
+// parts stay normal; inf / nan go to h alone), packed as bf16x8 each
+__device__ __forceinline__ void split3_bf16x8(const float (&v)[8], bf16x8_i8 &h, bf16x8_i8 &m, bf16x8_i8 &l) {
+  uint32_t ph[4], pm[4], pl[4];
+#pragma unroll
+  for (int e = 0; e < 8; e += 2) {
+    const bool fa = fabsf(v[e]) <= 3.0e38f, fb = fabsf(v[e + 1]) <= 3.0e38f;
+    ph[e / 2] = pk_bf16(v[e], v[e + 1]);
+    const float ra = fa ? v[e] - bf16_lo_f32(ph[e / 2]) : 0.f, rb = fb ? v[e + 1] - bf16_hi_f32(ph[e / 2]) : 0.f;
+    pm[e / 2] = pk_bf16(ra, rb);
+    pl[e / 2] = pk_bf16(ra - bf16_lo_f32(pm[e / 2]), rb - bf16_hi_f32(pm[e / 2]));
+  }
+  typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+  h = __builtin_bit_cast(bf16x8_i8, u4{ph[0], ph[1], ph[2], ph[3]});
+  m = __builtin_bit_cast(bf16x8_i8, u4{pm[0], pm[1], pm[2], pm[3]});
+  l = __builtin_bit_cast(bf16x8_i8, u4{pl[0], pl[1], pl[2], pl[3]});
+}
+
+// the 8 fp16 weights of 8 int8 values (bytes of d0, d1) times s2, split
+// exactly into bf16 hi + lo (inf / nan weights, from an fp16 overflow of
+// q * s16 or a nan scale, go to hi alone)
+__device__ __forceinline__ void int8x8_hilo(uint32_t d0, uint32_t d1, __half2 s2, bf16x8_i8 &hi, bf16x8_i8 &lo) {
+  __half2 w[4];
+  int8x4_weights(d0, s2, w[0], w[1]);
+  int8x4_weights(d1, s2, w[2], w[3]);
+  uint32_t ph[4], pl[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float a = __low2float(w[i]), b = __high2float(w[i]);
+    ph[i] = pk_bf16(a, b);
+    const float ra = fabsf(a) <= 65504.0f ? a - bf16_lo_f32(ph[i]) : 0.f;
+    const float rb = fabsf(b) <= 65504.0f ? b - bf16_hi_f32(ph[i]) : 0.f;
+    pl[i] = pk_bf16(ra, rb);
+  }
+  typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+  hi = __builtin_bit_cast(bf16x8_i8, u4{ph[0], ph[1], ph[2], ph[3]});
+  lo = __builtin_bit_cast(bf16x8_i8, u4{pl[0], pl[1], pl[2], pl[3]});
+}
+
+template <int MT, bool NORM, bool ARG>
+__global__ __launch_bounds__(64 * kI8mmWaves, 2) void int8mm_kernel(
+    const int8_t *__restrict__ q, const uint16_t *__restrict__ mu16, int64_t rows, int cols,
+    const float *__restrict__ x, int64_t m_total, const float *__restrict__ norm_w, float eps, float *__restrict__ y,
+    uint64_t *__restrict__ keys) {
+  constexpr int TOK = 16 * MT;
+  __shared__ __align__(16) float red[kI8mmWaves][TOK][kI8mmRedStride];
+  __shared__ float sq[kI8mmWaves][TOK];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, j = lane & 15, qd = lane >> 4;
+  const int64_t row0 = static_cast<int64_t>(blockIdx.x) * kI8mmRows;
+  const int64_t tok0 = static_cast<int64_t>(blockIdx.y) * TOK;
+  const int nsteps = (cols + 31) / 32;
+  const int sb = nsteps / kI8mmWaves, sx = nsteps % kI8mmWaves;
+  const int s0 = wave * sb + min(wave, sx), sn = sb + (wave < sx ? 1 : 0);
+
+  // per row tile: this lane's row (clamped; rows past the end decode, never stored) and its scale
+  __half2 s2[4];
+  const int8_t *qrow[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int64_t row = row0 + 16 * r + j < rows ? row0 + 16 * r + j : rows - 1;
+    s2[r] = __float2half2_rn(int8_row_scale(mu16[row]));  // exact: an fp16 value
+    qrow[r] = q + row * cols;
+  }
+  const float *xrow[MT];
+  bool tok_ok[MT];
+#pragma unroll
+  for (int t = 0; t < MT; ++t) {
+    const int64_t tok = tok0 + 16 * t + j;
+    tok_ok[t] = tok < m_total;
+    xrow[t] = x + (tok_ok[t] ? tok : 0) * static_cast<int64_t>(cols);
+  }
+
+  f32x4_i8 acc[MT][4];
+#pragma unroll
+  for (int t = 0; t < MT; ++t)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) acc[t][r] = f32x4_i8{0.f, 0.f, 0.f, 0.f};
+  float ssq[MT];
+#pragma unroll
+  for (int t = 0; t < MT; ++t) ssq[t] = 0.f;
+
+  // Raw operands of one step (activations: 8 per token tile; weights: 8 bytes
+  // per row tile) in a ring of D steps: the loads of step i + D
+  // go out as step i is computed, so a wave keeps several HBM round trips in
+  // flight (one step's work is far shorter than one trip).
+  constexpr int D = MT == 4 ? 2 : 4;
+  float xv[D][MT][8];
+  uint2 wv[D][4];
+  auto load_step = [&](int step, float (&xs)[MT][8], uint2 (&ws)[4]) {
+    const int k = 32 * step + 8 * qd;
+    const bool kok = k < cols && step < s0 + sn;
+    const int kk = kok ? k : 0;
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+      const float4 *p = reinterpret_cast<const float4 *>(xrow[t] + kk);
+      const float4 a = p[0], b = p[1];
+      const bool ok = kok && tok_ok[t];
+      xs[t][0] = ok ? a.x : 0.f; xs[t][1] = ok ? a.y : 0.f; xs[t][2] = ok ? a.z : 0.f; xs[t][3] = ok ? a.w : 0.f;
+      xs[t][4] = ok ? b.x : 0.f; xs[t][5] = ok ? b.y : 0.f; xs[t][6] = ok ? b.z : 0.f; xs[t][7] = ok ? b.w : 0.f;
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const uint2 d = *reinterpret_cast<const uint2 *>(qrow[r] + kk);
+      ws[r] = kok ? d : make_uint2(0u, 0u);  // zero bytes: weight 0
+    }
+  };
+  auto compute_step = [&](int step, const float (&xs)[MT][8], const uint2 (&ws)[4]) {
+    float g[8];
+    if constexpr (NORM) {
+      const int k = 32 * step + 8 * qd;
+      const float4 *gp = reinterpret_cast<const float4 *>(norm_w + (k < cols ? k : 0));
+      const float4 a = gp[0], b = gp[1];
+      g[0] = a.x; g[1] = a.y; g[2] = a.z; g[3] = a.w; g[4] = b.x; g[5] = b.y; g[6] = b.z; g[7] = b.w;
+    }
+    bf16x8_i8 wh[4], wl[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) int8x8_hilo(ws[r].x, ws[r].y, s2[r], wh[r], wl[r]);
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+      float v[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        v[e] = xs[t][e];
+        if constexpr (NORM) {
+          ssq[t] = fmaf(v[e], v[e], ssq[t]);
+          v[e] = v[e] * g[e];
+        }
+      }
+      bf16x8_i8 xh, xm, xl;
+      split3_bf16x8(v, xh, xm, xl);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        acc[t][r] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xh, wh[r], acc[t][r], 0, 0, 0);
+        acc[t][r] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xm, wh[r], acc[t][r], 0, 0, 0);
+        acc[t][r] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xl, wh[r], acc[t][r], 0, 0, 0);
+        acc[t][r] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xh, wl[r], acc[t][r], 0, 0, 0);
+        acc[t][r] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xm, wl[r], acc[t][r], 0, 0, 0);
+      }
+    }
+  };
+#pragma unroll
+  for (int u = 0; u < D; ++u) load_step(s0 + u, xv[u], wv[u]);
+  for (int i = 0; i < sn; i += D) {
+#pragma unroll
+    for (int u = 0; u < D; ++u) {
+      if (i + u < sn) {  // wave-uniform
+        compute_step(s0 + i + u, xv[u], wv[u]);
+        load_step(s0 + i + u + D, xv[u], wv[u]);  // past the wave's steps: zeros, no memory read past the row
+      }
+    }
+  }
+
+  // ---- epilogue: C[token 16t + 4qd + e][row 16r + j] of every wave into LDS, summed in wave order ----
+#pragma unroll
+  for (int t = 0; t < MT; ++t)
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) red[wave][16 * t + 4 * qd + e][16 * r + j] = acc[t][r][e];
+  if constexpr (NORM) {
+    // token 16t + j: the four lane groups' sums, then the waves' (below)
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+      float v = ssq[t];
+      v += __shfl_xor(v, 16, 64);
+      v += __shfl_xor(v, 32, 64);
+      if (qd == 0) sq[wave][16 * t + j] = v;
+    }
+  }
+  __syncthreads();
+  constexpr int kTpt = 64 * kI8mmWaves / TOK;  // threads per token
+  constexpr int kRpt = kI8mmRows / kTpt;        // rows per thread
+  const int tl = tid / kTpt, part = tid % kTpt;
+  const int64_t tok = tok0 + tl;
+  float rs = 1.0f;
+  if constexpr (NORM) {
+    float t2 = sq[0][tl];
+#pragma unroll
+    for (int w = 1; w < kI8mmWaves; ++w) t2 += sq[w][tl];
+    rs = 1.0f / sqrtf(t2 / static_cast<float>(cols) + eps);
+  }
+  uint64_t kb = 0;
+#pragma unroll
+  for (int i = 0; i < kRpt; ++i) {
+    const int rr = part + kTpt * i;
+    float sum = red[0][tl][rr];
+#pragma unroll
+    for (int w = 1; w < kI8mmWaves; ++w) sum += red[w][tl][rr];
+    if constexpr (NORM) sum *= rs;
+    const int64_t row = row0 + rr;
+    if (tok < m_total && row < rows) {
+      y[tok * rows + row] = sum;
+      if constexpr (ARG) {
+        const uint64_t k = arg_key(sum, static_cast<uint32_t>(row));
+        kb = k > kb ? k : kb;
+      }
+    }
+  }
+  if constexpr (ARG) {
+#pragma unroll
+    for (int d = 1; d < kTpt; d <<= 1) {
+      const uint64_t o = shfl_xor_u64(kb, d);
+      kb = o > kb ? o : kb;
+    }
+    if (part == 0 && tok < m_total) keys[tok * gridDim.x + blockIdx.x] = kb;
+  }
+}
+
 constexpr int kPickThreads = 1024;
 constexpr int kPickRegs = 8;  // keys in flight per lane and round
 
@@ -410,6 +648,53 @@ int int8_linear_blocks(int64_t rows, int64_t *rows_per_wave) {
   return static_cast<int>(std::min<int64_t>((waves + kLinWaves - 1) / kLinWaves, 0x7FFFFFFFll));
 }
 
+// From this many tokens the MFMA kernel runs: it reads the weights once for up
+// to 64 tokens, the GEMV once per 4 tokens.  Measured on the Pollux head
+// (50,688 x 1,920): GEMV 20.8 / 25.8 / 47.4 / 79.2 us at 1 / 2 / 4 / 5 tokens;
+// MFMA 61-62 us at 5..16 tokens (VALU-bound by the weight decode), 75 at 17,
+// 102 at 33, 165 at 65, 338 at 256 (torch F.linear on the cached fp32 cast:
+// 70-73, 76, 95, 162, 392).
+constexpr int64_t kI8mmMinTokens = 5;
+
+int64_t int8mm_row_blocks(int64_t rows) { return (rows + kI8mmRows - 1) / kI8mmRows; }
+
+int launch_int8mm(const int8_t *q, const uint16_t *mu16, int64_t rows, int cols, const float *x, int64_t m,
+                  const float *norm_w, float eps, float *y, uint64_t *keys, hipStream_t s) {
+  const int mt = m <= 16 ? 1 : m <= 32 ? 2 : 4;
+  const int64_t slabs = (m + 16 * mt - 1) / (16 * mt);
+  if (slabs > 0xFFFFll) return fail(PLX_EINVAL, "int8_linear: %lld tokens", static_cast<long long>(m));
+  const dim3 g(static_cast<unsigned>(int8mm_row_blocks(rows)), static_cast<unsigned>(slabs)), b(64 * kI8mmWaves);
+#define PLX_I8MM_K(MT, NORM)                                                                                        \
+  do {                                                                                                              \
+    if (keys)                                                                                                       \
+      hipLaunchKernelGGL((int8mm_kernel<MT, NORM, true>), g, b, 0, s, q, mu16, rows, cols, x, m, norm_w, eps, y, keys); \
+    else                                                                                                            \
+      hipLaunchKernelGGL((int8mm_kernel<MT, NORM, false>), g, b, 0, s, q, mu16, rows, cols, x, m, norm_w, eps, y,    \
+                         keys);                                                                                     \
+  } while (0)
+#define PLX_I8MM(MT)              \
+  do {                            \
+    if (norm_w)                   \
+      PLX_I8MM_K(MT, true);       \
+    else                          \
+      PLX_I8MM_K(MT, false);      \
+  } while (0)
+  if (mt == 1)
+    PLX_I8MM(1);
+  else if (mt == 2)
+    PLX_I8MM(2);
+  else
+    PLX_I8MM(4);
+#undef PLX_I8MM
+#undef PLX_I8MM_K
+  return check_launch("int8mm_kernel");
+}
+
+// blocks of the kernel a call at m tokens launches (the argmax keys' parts)
+int64_t int8_linear_parts(int64_t rows, int64_t m) {
+  return m >= kI8mmMinTokens ? int8mm_row_blocks(rows) : int8_linear_blocks(rows, nullptr);
+}
+
 int launch_int8_linear(const int8_t *q, const uint16_t *mu16, int64_t rows, int64_t cols, const float *x, int64_t m,
                        const float *norm_w, float eps, float *y, uint64_t *keys, hipStream_t s) {
   if (rows == 0 || m == 0) return PLX_OK;
@@ -419,6 +704,7 @@ int launch_int8_linear(const int8_t *q, const uint16_t *mu16, int64_t rows, int6
                        reinterpret_cast<uintptr_t>(norm_w);
   if ((al & 15u) != 0) return fail(PLX_EINVAL, "int8_linear: q, x and the norm weight must be 16-byte aligned");
   if (rows > 0x7FFFFFFFll) return fail(PLX_EINVAL, "int8_linear: too many rows");
+  if (m >= kI8mmMinTokens) return launch_int8mm(q, mu16, rows, static_cast<int>(cols), x, m, norm_w, eps, y, keys, s);
   int64_t rpw = 0;
   const int blocks = int8_linear_blocks(rows, &rpw);
   const int cpl = static_cast<int>((cols / 16 + 63) / 64);
@@ -468,7 +754,7 @@ int launch_int8_linear_argmax(const int8_t *q, const uint16_t *mu16, int64_t row
                               int64_t hist_len, int64_t *pos, void *workspace, size_t workspace_bytes, hipStream_t s) {
   if (m == 0) return PLX_OK;
   if (rows <= 0 || rows > 0x7FFFFFFFll) return fail(PLX_EINVAL, "int8_linear_argmax: %lld rows", static_cast<long long>(rows));
-  const int parts = int8_linear_blocks(rows, nullptr);
+  const int64_t parts = int8_linear_parts(rows, m);
   const size_t need = static_cast<size_t>(m) * static_cast<size_t>(parts) * sizeof(uint64_t);
   if (workspace == nullptr || workspace_bytes < need || (reinterpret_cast<uintptr_t>(workspace) & 7u) != 0)
     return fail(PLX_EINVAL, "int8_linear_argmax: workspace of %zu bytes (8-byte aligned) needed", need);
@@ -477,14 +763,14 @@ int launch_int8_linear_argmax(const int8_t *q, const uint16_t *mu16, int64_t row
   if (st != PLX_OK) return st;
   int rsh = 0;
   while ((int64_t{1} << rsh) < m && rsh < 4) ++rsh;
-  hipLaunchKernelGGL(argmax_pick_kernel, dim3(1), dim3(kPickThreads), 0, s, keys, parts, m, rsh, ids, history,
-                     hist_len, pos);
+  hipLaunchKernelGGL(argmax_pick_kernel, dim3(1), dim3(kPickThreads), 0, s, keys, static_cast<int>(parts), m, rsh, ids,
+                     history, hist_len, pos);
   return check_launch("argmax_pick_kernel");
 }
 
 size_t int8_linear_argmax_workspace_bytes(int64_t rows, int64_t m) {
   if (rows <= 0 || m <= 0 || rows > 0x7FFFFFFFll) return 0;
-  return static_cast<size_t>(m) * static_cast<size_t>(int8_linear_blocks(rows, nullptr)) * sizeof(uint64_t);
+  return static_cast<size_t>(m) * static_cast<size_t>(int8_linear_parts(rows, m)) * sizeof(uint64_t);
 }
 
 int launch_int8_embed(const int8_t *q, const uint16_t *mu16, int64_t vocab, int64_t cols, const int64_t *idx,

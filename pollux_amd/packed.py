@@ -458,14 +458,15 @@ class PackedInt8Linear(_PackedInt8Rows):
         else:
             self.register_parameter("bias", None)
 
-    # token counts up to which the INT8 GEMV runs (it streams the rows once per 4 tokens)
-    gemv_max_tokens = 16
+    # token counts up to which the INT8 kernels run (plx_int8_linear: the GEMV at one
+    # token, the MFMA kernel above); larger batches take the reference's F.linear
+    gemv_max_tokens = 1 << 20
 
     def forward(self, x: torch.Tensor, norm: tuple[torch.Tensor, float] | None = None) -> torch.Tensor:
         """F.linear(n(x), W.to(x.dtype), bias) (pollux.py:562-563); ``norm``: (weight, eps) of an RMSNorm on x, or None.
 
         Until materialize(), fp32 batches of up to ``gemv_max_tokens`` tokens
-        run the INT8 GEMV (norm fused in); others take the reference's
+        run the INT8 kernels (norm fused in); others take the reference's
         F.linear on the fp16 weight cast to x's dtype (kept for reuse).
         """
         if self.gemv_runs(x):
@@ -475,7 +476,7 @@ class PackedInt8Linear(_PackedInt8Rows):
         return F.linear(x, self._weight_as(x.dtype), self.bias)
 
     def gemv_runs(self, x: torch.Tensor) -> bool:
-        """Whether forward(x) runs the INT8 GEMV (packed, no bias, fp32 x of at most gemv_max_tokens tokens)."""
+        """Whether forward(x) runs the INT8 kernels (packed, no bias, fp32 x of at most gemv_max_tokens tokens)."""
         return (not self._materialized and self.bias is None and x.dtype == torch.float32
                 and x.numel() // max(self.in_features, 1) <= self.gemv_max_tokens
                 and self.in_features % 16 == 0 and self.in_features <= 4096)

@@ -69,10 +69,12 @@ def test_packed_int8_layers(dev):
     x = torch.randn(4, 48, generator=g).to(dev)
     wq = _ref_int8_materialize(q, mu)
     assert torch.equal(emb(ids), torch.nn.functional.embedding(ids, wq.float()))
-    # fused INT8 GEMV: exact products, another summation order than F.linear
+    # fused INT8 kernels (4 tokens, 20 tokens: MFMA): exact products, another summation order than F.linear
     want = torch.nn.functional.linear(x, wq.float())
     _check_int8_linear(lin(x), x, wq)
-    big = torch.randn(20, 48, generator=g).to(dev)  # beyond the GEMV's token limit: the reference's F.linear
+    big = torch.randn(20, 48, generator=g).to(dev)
+    _check_int8_linear(lin(big), big, wq)
+    lin.gemv_max_tokens = 16  # beyond the kernels' token limit: the reference's F.linear
     assert torch.equal(lin(big), torch.nn.functional.linear(big, wq.float()))
     for m in (emb, lin):
         m.materialize()
@@ -85,6 +87,7 @@ def test_packed_int8_linear_sees_new_weights(dev):
     # rebuilt after load_state_dict copies new values into the buffers in place
     g = torch.Generator().manual_seed(81)
     lin = PackedInt8Linear(48, 100).to(dev)
+    lin.gemv_max_tokens = 16  # 20 tokens take the F.linear path and its cached cast
     states = []
     for _ in range(2):
         q, mu = plx_pack.quantize_int8_rows(torch.randn(100, 48, generator=g).to(dev))
@@ -117,10 +120,12 @@ def _check_int8_linear(y, x, w16, bound=1e-5):
     assert worst <= bound
 
 
-# rows % 4 != 0, 16 columns (one chunk), 1,040 columns (a second chunk on one lane only),
-# 1,920 (the Pollux head), 4,096 (four chunks per lane); 1..16 tokens (chunks of 4, 2, 1)
+# rows % 4 != 0, 16 columns (one chunk), 1,040 columns (a second chunk on one lane only; K steps past the
+# row), 1,920 (the Pollux head), 4,096 (four chunks per lane); one token (the GEMV), 2..16 tokens (MFMA, one
+# token tile), 17..32 (two), 33 and more (four per 64-token slab; 65 and 100: a second, partial slab)
 @pytest.mark.parametrize("rows,cols,m", [(4103, 1920, 1), (4103, 1920, 2), (4103, 1920, 7), (513, 16, 3),
-                                         (999, 1040, 5), (257, 4096, 4), (130, 4096, 16), (61, 48, 1)])
+                                         (999, 1040, 5), (257, 4096, 4), (130, 4096, 16), (61, 48, 1),
+                                         (4103, 1920, 17), (1000, 1920, 33), (2049, 1920, 65), (77, 1040, 100)])
 def test_int8_linear_matches_fp64(dev, rows, cols, m):
     from pollux_amd.packed import int8_linear
 
