@@ -567,11 +567,140 @@ __global__ __launch_bounds__(NT) void dqlinear_kernel(const DqlArgs<GEN> targets
   }
 }
 
+// One token of bf16 activations, one target, no epilogue (the plain GEMV
+// call): the arithmetic of dqlinear_kernel<L, 1> with two changes.
+// - Each plane of 8 raw integers becomes 4 bf16 pairs by v_perm_b32 byte
+//   lookups of its kp_dq value ids (exact: the integers are small), and
+//   v_dot2_f32_bf16 multiplies them by the bf16 x pairs (exact products,
+//   fp32 sums): 12 dot products and 24 lookups per atom where the fp32 path
+//   spends 24 extract / convert / fma triples.  kp_dot holds each code's
+//   3 kp_dq words and its type | position of -3 << 8 (16 B, one gather).
+// - It is written so that the compiler issues one round of loads (packed
+//   bytes as raw buffer loads, sigma16, x), one barrier, one round of LDS
+//   reads of the lane's atom bytes and one round of gathers: every thread
+//   stores to LDS (no load sits under a branch) and atoms past the row
+//   decode as the origin (no branch per atom).
+// Measured in a graph of 200 calls on distinct copies (bench.py): 7680 x 1920
+// 5.65 -> 5.40 us, 1920 x 7680 5.95 -> 5.43 us.  fp32 activations keep
+// dqlinear_kernel (this layout measured the same there).
+constexpr int kG1Atoms = 5;  // atoms per lane
+template <int L>
+__global__ __launch_bounds__(512) void dqgemv1_kernel(const uint8_t *__restrict__ packed, int packed_bytes,
+                                                      const uint16_t *__restrict__ sigma16, int rows, int apr,
+                                                      const uint16_t *__restrict__ x, const uint4 *__restrict__ kp_dot,
+                                                      int round_w, float *__restrict__ y) {
+  constexpr int NT = 512, R = NT / L, G = kG1Atoms;
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  extern __shared__ __align__(16) uint8_t smem[];
+  const int tid = threadIdx.x;
+  const int sub = tid % L;
+  const int row0 = static_cast<int>(blockIdx.x) * R;
+  const int row = row0 + tid / L;
+  const int rows_here = min(R, rows - row0);
+  const int cols = apr * kDim;
+  // the block's whole 9-byte groups [g_lo, g_hi) as aligned 16-byte vectors (the host checks nvec <= NT)
+  const int atom0 = row0 * apr;
+  const int g_lo = atom0 >> 2, g_hi = (atom0 + rows_here * apr + 3) >> 2;
+  const int start = g_lo * 9, base16 = start & ~15;
+  const int nvec = (g_hi * 9 - base16 + 15) >> 4;
+  const int pb_off = start - base16;
+  // LDS: NT packed vectors, then 2 NT pieces of 8 bf16 x values
+  uint16_t *xh = reinterpret_cast<uint16_t *>(smem + NT * 16);
+  // round of loads: packed vector, sigma16, x pieces.  The buffer range covers the stream
+  // rounded up to whole dwords (a dword reaching past the range reads as zero; the last
+  // dword lies in the same page as the stream's last byte, the base being 16-byte aligned);
+  // dwords wholly past it read as zero.
+  const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t *>(packed), static_cast<short>(0), (packed_bytes + 3) & ~3, 0x00020000);
+  int poff = tid < nvec ? base16 + 16 * tid : 0x7FFFFFF0;
+  asm("" : "+v"(poff));
+  const uint32_t d0 = __builtin_amdgcn_raw_buffer_load_b32(prs, poff, 0, 0);
+  const uint32_t d1 = __builtin_amdgcn_raw_buffer_load_b32(prs, poff + 4, 0, 0);
+  const uint32_t d2 = __builtin_amdgcn_raw_buffer_load_b32(prs, poff + 8, 0, 0);
+  const uint32_t d3 = __builtin_amdgcn_raw_buffer_load_b32(prs, poff + 12, 0, 0);
+  const uint16_t sig_bits = sigma16[row < rows ? row : rows - 1];
+  const int items = cols / 8;  // pieces of x (the host checks items <= 2 * NT)
+  uint4 xq[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int it = tid + h * NT;
+    xq[h] = reinterpret_cast<const uint4 *>(x)[it < items ? it : 0];
+  }
+  reinterpret_cast<uint4 *>(smem)[tid] = make_uint4(d0, d1, d2, d3);
+#pragma unroll
+  for (int h = 0; h < 2; ++h) reinterpret_cast<uint4 *>(xh)[tid + h * NT] = xq[h];  // pieces past x: unused slots
+  __syncthreads();
+  float sig = __half2float(__ushort_as_half(sig_bits));
+  asm volatile("" : "+v"(sig));  // keeps the sigma16 load in the first round (else it sinks into the epilogue)
+  // round of LDS reads: the lane's atoms sub, sub + L, ... (clamped to the block's atoms), 3 bytes
+  // each from two aligned words
+  const int lrow = min(tid / L, rows_here - 1);
+  const int nbase = lrow * apr + (atom0 - g_lo * 4);
+  uint32_t w0[G], w1[G];
+  int nn[G];
+#pragma unroll
+  for (int i = 0; i < G; ++i) {
+    nn[i] = nbase + min(sub + i * L, apr - 1);
+    const int off = pb_off + (nn[i] >> 2) * 9 + 2 * (nn[i] & 3);
+    const uint32_t *wp = reinterpret_cast<const uint32_t *>(smem + (off & ~3));
+    w0[i] = wp[0];
+    w1[i] = wp[1];
+  }
+  // round of gathers
+  uint4 e[G];
+#pragma unroll
+  for (int i = 0; i < G; ++i) {
+    const int n = nn[i];
+    const uint32_t o = static_cast<uint32_t>((pb_off + (n >> 2) * 9 + 2 * (n & 3)) & 3);
+    const uint32_t v = __builtin_amdgcn_perm(w1[i], w0[i], (o + 2) | ((o + 1) << 8) | (o << 16) | 0x0C000000u);
+    int32_t code = static_cast<int32_t>((v >> (6 - 2 * (n & 3))) & 0x3FFFFu);
+    if (code > kKissing || sub + i * L >= apr) code = 0;
+    e[i] = kp_dot[code];
+  }
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  const uint4 itab = int_value_table();
+#pragma unroll
+  for (int i = 0; i < G; ++i) {
+    const int a = min(sub + i * L, apr - 1);
+    const uint32_t type = e[i].w & 3u;
+    const int pos = static_cast<int>((e[i].w >> 8) & 31u);
+    const uint32_t cw[3] = {e[i].x, e[i].y, e[i].z};
+    float D = 0.f;
+#pragma unroll
+    for (int p = 0; p < 3; ++p) {
+      const uint4 kp = ids_to_pairs(cw[p], itab);
+      const uint4 xv = *reinterpret_cast<const uint4 *>(xh + a * kDim + 8 * p);
+      D = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, kp.x), __builtin_bit_cast(bf16x2_t, xv.x), D, false);
+      D = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, kp.y), __builtin_bit_cast(bf16x2_t, xv.y), D, false);
+      D = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, kp.z), __builtin_bit_cast(bf16x2_t, xv.z), D, false);
+      D = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, kp.w), __builtin_bit_cast(bf16x2_t, xv.w), D, false);
+    }
+    const float xp = __uint_as_float(static_cast<uint32_t>(xh[a * kDim + pos]) << 16);
+    acc[0] += type == 1u ? D : 0.f;
+    acc[1] += type == 2u ? D : 0.f;
+    acc[2] += type == 3u ? fmaf(3.f, xp, D) : 0.f;
+    acc[3] += type == 3u ? xp : 0.f;
+  }
+  group_reduce<L>(acc);
+  if (sub == 0 && row < rows) {
+    const float sl = __uint_as_float(kSLatticeBits);
+    const float v1 = __half2float(__ushort_as_half(static_cast<uint16_t>(dq_value(1, sig, sl))));
+    const float v2 = __half2float(__ushort_as_half(static_cast<uint16_t>(dq_value(2, sig, sl))));
+    const float v3 = __half2float(__ushort_as_half(static_cast<uint16_t>(dq_value(3, sig, sl))));
+    const float v4 = __half2float(__ushort_as_half(static_cast<uint16_t>(dq_value(4, sig, sl))));
+    const float m1 = round_w ? bf16_bits_to_float(bf16_rne_bits(v1)) : v1;
+    const float m2 = round_w ? bf16_bits_to_float(bf16_rne_bits(v2)) : v2;
+    const float m3 = round_w ? bf16_bits_to_float(bf16_rne_bits(v3)) : v3;
+    const float m4 = round_w ? bf16_bits_to_float(bf16_rne_bits(v4)) : v4;
+    y[row] = m4 * (acc[0] * 0.25f) + m2 * (acc[1] * 0.5f) + m1 * acc[2] - m3 * acc[3];
+  }
+}
+
 // t.norm_w (fp32 x only): x is normalised in the kernel when its rows fit in
 // LDS, else by rmsnorm into xnorm ([m, cols] fp32) first.
 template <int L, bool XF32, int NT>
-int launch_dql(DqlTargets t, int64_t apr, const void *x, int64_t m, const uint4 *tab, int round_w, int gelu,
-               float *xnorm, hipStream_t s) {
+int launch_dql(DqlTargets t, int64_t apr, const void *x, int64_t m, const uint4 *tab, const uint4 *kp_dot, int round_w,
+               int gelu, float *xnorm, hipStream_t s) {
   constexpr int R = NT / L;
   int64_t blocks = 0;
   for (int i = 0; i < t.n; ++i) blocks = max(blocks, (t.rows[i] + R - 1) / R);
@@ -596,6 +725,18 @@ int launch_dql(DqlTargets t, int64_t apr, const void *x, int64_t m, const uint4 
     t.norm_w = nullptr;
   }
   const bool gen = t.n > 1 || t.residual[0] != nullptr || gelu || t.norm_w != nullptr;
+  if constexpr (NT == 512 && !XF32) {
+    // one token of bf16 x, one target: dqgemv1_kernel (at most kG1Atoms atoms per lane, int offsets)
+    const int64_t nvec_max = (R * apr / 4 + 2) * 9 / 16 + 2;
+    if (!gen && m == 1 && apr >= 1 && apr <= static_cast<int64_t>(kG1Atoms) * L && nvec_max <= NT &&
+        cols / 8 <= 2 * NT && t.packed_bytes[0] < (static_cast<int64_t>(1) << 30) &&
+        t.rows[0] < (static_cast<int64_t>(1) << 30)) {
+      hipLaunchKernelGGL((dqgemv1_kernel<L>), g, dim3(NT), static_cast<size_t>(NT) * (16 + 32), s, t.packed[0],
+                         static_cast<int>(t.packed_bytes[0]), t.sigma16[0], static_cast<int>(t.rows[0]),
+                         static_cast<int>(apr), static_cast<const uint16_t *>(x), kp_dot, round_w, t.y[0]);
+      return check_launch("dqgemv1_kernel");
+    }
+  }
 #define PLX_DQL(MB, XL, XR) \
   do {                                                                                                          \
     if (gen)                                                                                                    \
@@ -1292,6 +1433,7 @@ int launch_dequant_linear_multi(const DqlTarget *targets, int n, int64_t cols, c
     return st;
   }
   const uint4 *kp = reinterpret_cast<const uint4 *>(tab->kp_gemv);
+  const uint4 *kd = reinterpret_cast<const uint4 *>(tab->kp_dot);
   // up to kDqlMaxTargets targets per GEMV launch
   for (int i0 = 0; i0 < n && st == PLX_OK; i0 += kDqlMaxTargets) {
     DqlTargets t{};
@@ -1311,25 +1453,25 @@ int launch_dequant_linear_multi(const DqlTarget *targets, int n, int64_t cols, c
     // 1920-row q/k/v and o_proj launches of the decode step 3% faster with 32, from the doubled grid);
     // 512-thread blocks (4% faster than 256 at M = 1, 1,024 slower), 256 for rows too long to stage 8 in LDS
     if (apr >= 3072)
-      st = x_is_f32 ? launch_dql<64, true, 256>(t, apr, x, m, kp, round_w, gelu, xnorm, s)
-                    : launch_dql<64, false, 256>(t, apr, x, m, kp, round_w, gelu, xnorm, s);
+      st = x_is_f32 ? launch_dql<64, true, 256>(t, apr, x, m, kp, kd, round_w, gelu, xnorm, s)
+                    : launch_dql<64, false, 256>(t, apr, x, m, kp, kd, round_w, gelu, xnorm, s);
     else if (apr >= 160)
-      st = x_is_f32 ? launch_dql<64, true, 512>(t, apr, x, m, kp, round_w, gelu, xnorm, s)
-                    : launch_dql<64, false, 512>(t, apr, x, m, kp, round_w, gelu, xnorm, s);
+      st = x_is_f32 ? launch_dql<64, true, 512>(t, apr, x, m, kp, kd, round_w, gelu, xnorm, s)
+                    : launch_dql<64, false, 512>(t, apr, x, m, kp, kd, round_w, gelu, xnorm, s);
     else if (apr >= 16) {
       // 32 lanes per row (16 rows per block) when 16 would leave the grid under 192 blocks
       int64_t mrows = 0;
       for (int i = 0; i < t.n; ++i) mrows = t.rows[i] > mrows ? t.rows[i] : mrows;
       if ((mrows + 31) / 32 * t.n < 192)
-        st = x_is_f32 ? launch_dql<32, true, 512>(t, apr, x, m, kp, round_w, gelu, xnorm, s)
-                      : launch_dql<32, false, 512>(t, apr, x, m, kp, round_w, gelu, xnorm, s);
+        st = x_is_f32 ? launch_dql<32, true, 512>(t, apr, x, m, kp, kd, round_w, gelu, xnorm, s)
+                      : launch_dql<32, false, 512>(t, apr, x, m, kp, kd, round_w, gelu, xnorm, s);
       else
-        st = x_is_f32 ? launch_dql<16, true, 512>(t, apr, x, m, kp, round_w, gelu, xnorm, s)
-                      : launch_dql<16, false, 512>(t, apr, x, m, kp, round_w, gelu, xnorm, s);
+        st = x_is_f32 ? launch_dql<16, true, 512>(t, apr, x, m, kp, kd, round_w, gelu, xnorm, s)
+                      : launch_dql<16, false, 512>(t, apr, x, m, kp, kd, round_w, gelu, xnorm, s);
     }
     else
-      st = x_is_f32 ? launch_dql<8, true, 512>(t, apr, x, m, kp, round_w, gelu, xnorm, s)
-                    : launch_dql<8, false, 512>(t, apr, x, m, kp, round_w, gelu, xnorm, s);
+      st = x_is_f32 ? launch_dql<8, true, 512>(t, apr, x, m, kp, kd, round_w, gelu, xnorm, s)
+                    : launch_dql<8, false, 512>(t, apr, x, m, kp, kd, round_w, gelu, xnorm, s);
   }
   return st;
 }

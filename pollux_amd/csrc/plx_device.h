@@ -126,6 +126,21 @@ __device__ __forceinline__ uint4 bf16_value_table() {
   return t;
 }
 
+// The same byte tables for the raw integers themselves (bf16 of {0, 1, 2, 4,
+// -4, -3, -2, -1}, all exact).
+__device__ __forceinline__ uint4 int_value_table() {
+  const int kv[8] = {0, 1, 2, 4, -4, -3, -2, -1};
+  uint32_t e[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) e[i] = bf16_rne_bits(static_cast<float>(kv[i]));
+  uint4 t;
+  t.x = (e[0] & 0xFFu) | (e[1] & 0xFFu) << 8 | (e[2] & 0xFFu) << 16 | (e[3] & 0xFFu) << 24;
+  t.y = (e[4] & 0xFFu) | (e[5] & 0xFFu) << 8 | (e[6] & 0xFFu) << 16 | (e[7] & 0xFFu) << 24;
+  t.z = (e[0] >> 8) | (e[1] >> 8) << 8 | (e[2] >> 8) << 16 | (e[3] >> 8) << 24;
+  t.w = (e[4] >> 8) | (e[5] >> 8) << 8 | (e[6] >> 8) << 16 | (e[7] >> 8) << 24;
+  return t;
+}
+
 // One kp_dq word (byte i = id of coordinate i | id of coordinate 4+i << 4)
 // -> the 8 16-bit values as pairs (coordinates 0,1 | 2,3 | 4,5 | 6,7), low
 // half first, through 6 v_perm_b32 byte lookups in a 4-word table t.

@@ -53,6 +53,7 @@ struct DeviceTables {
   int8_t *cb_raw = nullptr;          // [kCodebook][24] raw integer coordinates
   uint8_t *kp_gemv = nullptr;        // [kCodebook] x 16 B: 24 signed nibbles + (type | pos << 8)
   uint32_t *kp_dq = nullptr;         // [kCodebook][3] words: 3-bit value ids of 8 coordinates per word
+  uint32_t *kp_dot = nullptr;        // [kCodebook][4] words: kp_dq's 3 words, then kp_gemv's (type | pos << 8)
 };
 
 // Host generator (codebook.cpp): raw coordinates, origin first, sorted.

@@ -23,6 +23,9 @@
 //                {0,1,2,4,-4,-3,-2,-1} (there is no +3) as value ids 0..7,
 //                word p byte i = id(coord 8p+i) | id(coord 8p+4+i) << 4, the
 //                order v_perm_b32 lookups want (2,358,732 B).
+// kp_dot         per code 16 B for the one-token dequant-GEMV with bf16
+//                activations: kp_dq's 3 words, then type | position of -3 << 8
+//                as in kp_gemv (3,144,976 B).
 
 #include <cstring>
 #include <mutex>
@@ -98,6 +101,7 @@ int build(int dev, DeviceTables *t) {
   // dequant value ids (raw k -> id): 0->0 1->1 2->2 4->3 -4->4 -3->5 -2->6 -1->7
   static const uint32_t kId[9] = {4, 5, 6, 7, 0, 1, 2, 0xFF, 3};
   std::vector<uint32_t> dq(static_cast<size_t>(kCodebook) * 3, 0);
+  std::vector<uint32_t> dot(static_cast<size_t>(kCodebook) * 4, 0);
   for (int code = 0; code < kCodebook; ++code) {
     const int8_t *r = raw + static_cast<size_t>(code) * kDim;
     uint32_t *e = gemv.data() + static_cast<size_t>(code) * 4;
@@ -114,6 +118,11 @@ int build(int dev, DeviceTables *t) {
     }
     const uint32_t type = nz == 0 ? 0u : nz == 2 ? 1u : nz == 8 ? 2u : 3u;
     e[3] = type | (static_cast<uint32_t>(pos) << 8);
+    uint32_t *o = dot.data() + static_cast<size_t>(code) * 4;
+    o[0] = d[0];
+    o[1] = d[1];
+    o[2] = d[2];
+    o[3] = e[3];
   }
 
   struct Upload {
@@ -126,7 +135,7 @@ int build(int dev, DeviceTables *t) {
     for (int p = 0; p < 3; ++p) sw_dq[i * 3 + p] = dq[static_cast<size_t>(sweep[i]) * 3 + p];
 
   void *dt = nullptr, *drt = nullptr, *dsq = nullptr, *dsi = nullptr, *dsa = nullptr, *dr = nullptr, *dg = nullptr,
-       *dd = nullptr;
+       *dd = nullptr, *dk = nullptr;
   const Upload ups[] = {
       {tiles.data(), tiles.size() * 2, &dt},
       {raw_tiles.data(), raw_tiles.size() * 2, &drt},
@@ -136,6 +145,7 @@ int build(int dev, DeviceTables *t) {
       {raw, static_cast<size_t>(kCodebook) * kDim, &dr},
       {gemv.data(), gemv.size() * 4, &dg},
       {dq.data(), dq.size() * 4, &dd},
+      {dot.data(), dot.size() * 4, &dk},
   };
   int st = PLX_OK;
   for (const Upload &u : ups) {
@@ -160,6 +170,7 @@ int build(int dev, DeviceTables *t) {
   t->cb_raw = static_cast<int8_t *>(dr);
   t->kp_gemv = static_cast<uint8_t *>(dg);
   t->kp_dq = static_cast<uint32_t *>(dd);
+  t->kp_dot = static_cast<uint32_t *>(dk);
   t->device = dev;
   return PLX_OK;
 }
