@@ -213,14 +213,17 @@ def gemv_extras(device, copies=200, m_gemm=64, replays=5):
     """
     import torch
 
-    from pollux_amd import dequant_linear
+    from pollux_amd import castor, dequant_linear
 
     out = {}
     for name, (of, inf) in (("up_7680x1920", (7680, 1920)), ("down_1920x7680", (1920, 7680))):
         g = torch.Generator(device=device).manual_seed(of)
         n_atoms = of * inf // 24
         nbytes = (n_atoms + 3) // 4 * 9
-        pk = torch.randint(0, 256, (copies, nbytes), generator=g, device=device, dtype=torch.uint8)
+        # indices uniform over 0..196,560 (config 5), packed per copy
+        pk = torch.empty(copies, nbytes, dtype=torch.uint8, device=device)
+        for i in range(copies):
+            pk[i] = castor.pack_indices(torch.randint(0, 196561, (n_atoms,), generator=g, device=device))
         sg = (torch.rand(copies, of, generator=g, device=device) * 0.045 + 0.005).half()
         for m, mode in ((1, "exact"), (m_gemm, "exact"), (m_gemm, "as_x")):
             x = torch.randn(m, inf, generator=g, device=device).to(torch.bfloat16)
