@@ -136,6 +136,21 @@ def test_reference_literal_rounding(dev, shape, m):
     _check(y, x, w16, mode="as_x")
 
 
+# one token of bf16 x: rows of 1, 2, 10, 48 (16 lanes), 49 (groups straddle rows), 192 (64 lanes) atoms,
+# row counts that leave the last block partly empty, and a row longer than the one-token kernel takes
+@pytest.mark.parametrize("shape", [(24, 24), (37, 48), (33, 240), (1152, 1152), (7, 1176), (100, 4608), (130, 24),
+                                   (5, 73728)])
+@pytest.mark.parametrize("mode", ["exact", "as_x"])
+def test_one_token_bf16_ragged(dev, shape, mode):
+    out_f, in_f = shape
+    idx, sig, packed, g = _layer(out_f, in_f, 17 * out_f + in_f)
+    mag = torch.pow(2.0, torch.randint(-40, 41, (1, in_f), generator=g).float())
+    x = (torch.randn(1, in_f, generator=g) * mag).to(torch.bfloat16)
+    w16 = torch_ref.materialize(idx, sig, out_f, in_f)
+    y = dequant_linear(packed.to(dev), sig.to(dev), out_f, in_f, x.to(dev), weight_rounding=mode).cpu()
+    _check(y, x, w16, mode=mode)
+
+
 def test_literal_rounding_is_exact_for_fp32_activations(dev):
     # W.to(fp32) is exact, so both modes agree bit for bit with fp32 x
     out_f, in_f = 64, 1152
