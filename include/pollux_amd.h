@@ -215,6 +215,28 @@ int plx_dequant_f16(const uint8_t *packed, int64_t n_packed_bytes, const uint16_
 #define PLX_DQL_GELU 4   /* y = gelu(x W^T), torch's erf form (pollux.py:645) */
 #define PLX_DQL_RMS_NORM 8 /* plx_dequant_linear_multi only: RMS-normalise each fp32 x
                               row first (pre-norm of pollux.py:660-661) */
+#define PLX_DQL_PLANES 16  /* `packed` is the plane layout of the weight
+                              (plx_h24_plane_layout, 6 bytes per atom) instead of
+                              the 18-bit stream; taken by plx_dequant_linear for
+                              one token of bf16 x and for batches above 4 tokens */
+
+/* The plane layout of a packed weight: per atom 3 little-endian uint16
+ * records (6 bytes, atom order), one per 8-coordinate plane: a 13-bit index
+ * into the table of the 4,961 distinct planes of the codebook rows
+ * (plx_plane_table) | 3 extra bits (record 0: the code's type, 0 origin,
+ * 1 = +-4 pair, 2 = +-2 octad, 3 = one -3; records 1 and 2: bits 0-2 and 3-4 of
+ * the -3 position).  Kernels decode a code from a table they keep in LDS
+ * instead of gathering from the 3 MB per-code tables, so a packed layer built
+ * once into this layout (6 B per atom next to its 2.25 B packed stream) runs
+ * its dequant-linear without per-atom gathers.  packed: ((n_atoms+3)/4)*9
+ * bytes (indices above 196,560 map to the origin); planes: [3*n_atoms].
+ * No counterpart in the reference (a derived layout of its packed buffers). */
+int plx_h24_plane_layout(const uint8_t *packed, int64_t n_atoms, uint16_t *planes, void *stream);
+/* Host copy of the plane table: value-id words (kp_dq order: byte i = id of
+ * coordinate i | id of coordinate 4+i << 4, ids 0..7 = raw values
+ * {0,1,2,4,-4,-3,-2,-1}), ascending.  Returns the number of planes; copies at
+ * most `capacity` of them into ids (which may be NULL).  Needs no device. */
+int64_t plx_plane_table(uint32_t *ids, int64_t capacity);
 
 /* Workspace (device bytes, 16-byte aligned) plx_dequant_linear needs for
  * this shape, batch and flags (0 when none). */

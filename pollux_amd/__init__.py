@@ -22,9 +22,10 @@ from .packed import (  # noqa: F401
     dequant_linear,
     dequantize_h24,
     dequantize_int8_rows,
+    h24_plane_layout,
 )
 
 __all__ = [
     "castor", "model", "optim", "pack", "plx", "PackedH24Linear", "PackedInt8Embedding", "PackedInt8Linear",
-    "dequant_linear", "dequantize_h24", "dequantize_int8_rows",
+    "dequant_linear", "dequantize_h24", "dequantize_int8_rows", "h24_plane_layout",
 ]

@@ -5,6 +5,7 @@
 
 #include <cstdarg>
 #include <cstdio>
+#include <algorithm>
 #include <cstring>
 #include <string>
 #include <vector>
@@ -349,16 +350,39 @@ int plx_dequant_linear(const uint8_t *packed, int64_t n_packed_bytes, const uint
   PLX_REQUIRE(rows >= 0 && cols > 0 && cols % kDim == 0, "plx_dequant_linear: bad shape (%lld, %lld)",
               static_cast<long long>(rows), static_cast<long long>(cols));
   PLX_REQUIRE(m_rows >= 0, "plx_dequant_linear: negative batch");
-  PLX_REQUIRE((flags & ~(PLX_DQL_X_F32 | PLX_DQL_W_AS_X | PLX_DQL_GELU)) == 0, "plx_dequant_linear: unknown flags 0x%x",
-              flags);
+  PLX_REQUIRE((flags & ~(PLX_DQL_X_F32 | PLX_DQL_W_AS_X | PLX_DQL_GELU | PLX_DQL_PLANES)) == 0,
+              "plx_dequant_linear: unknown flags 0x%x", flags);
   const int64_t n_atoms = rows * (cols / kDim);
-  PLX_REQUIRE(n_packed_bytes == ((n_atoms + 3) / 4) * 9,
-              "plx_dequant_linear: packed length %lld does not match %lld atoms", static_cast<long long>(n_packed_bytes),
-              static_cast<long long>(n_atoms));
+  if (flags & PLX_DQL_PLANES) {
+    PLX_REQUIRE(n_packed_bytes == 6 * n_atoms, "plx_dequant_linear: plane layout of %lld bytes does not match %lld atoms",
+                static_cast<long long>(n_packed_bytes), static_cast<long long>(n_atoms));
+    PLX_REQUIRE(m_rows > 4 || (m_rows == 1 && !(flags & PLX_DQL_X_F32)),
+                "plx_dequant_linear: the plane layout takes one token of bf16 x or more than 4 tokens (got %lld)",
+                static_cast<long long>(m_rows));
+  } else {
+    PLX_REQUIRE(n_packed_bytes == ((n_atoms + 3) / 4) * 9,
+                "plx_dequant_linear: packed length %lld does not match %lld atoms",
+                static_cast<long long>(n_packed_bytes), static_cast<long long>(n_atoms));
+  }
   if (rows == 0 || m_rows == 0) return PLX_OK;
   PLX_REQUIRE(packed != nullptr && sigma16 != nullptr && x != nullptr && y != nullptr, "plx_dequant_linear: null pointer");
   return launch_dequant_linear(packed, sigma16, rows, cols, x, flags, m_rows, y, workspace, workspace_bytes,
                                as_stream(stream));
+}
+
+int plx_h24_plane_layout(const uint8_t *packed, int64_t n_atoms, uint16_t *planes, void *stream) {
+  PLX_REQUIRE(n_atoms >= 0, "plx_h24_plane_layout: negative atom count");
+  if (n_atoms == 0) return PLX_OK;
+  PLX_REQUIRE(packed != nullptr && planes != nullptr, "plx_h24_plane_layout: null pointer");
+  return launch_plane_layout(packed, n_atoms, planes, as_stream(stream));
+}
+
+int64_t plx_plane_table(uint32_t *ids, int64_t capacity) {
+  const PlaneTables *pt = plane_tables_host();
+  if (!pt) return fail(PLX_EINVAL, "plane table construction failed");
+  const int64_t n = static_cast<int64_t>(pt->ids.size());
+  if (ids && capacity > 0) std::memcpy(ids, pt->ids.data(), static_cast<size_t>(std::min(n, capacity)) * 4);
+  return n;
 }
 
 int plx_int8_linear(const int8_t *q, const uint16_t *mu16, int64_t rows, int64_t cols, const float *x, int64_t m_rows,

@@ -584,12 +584,18 @@ __global__ __launch_bounds__(NT) void dqlinear_kernel(const DqlArgs<GEN> targets
 // 5.65 -> 5.40 us, 1920 x 7680 5.95 -> 5.43 us.  fp32 activations keep
 // dqlinear_kernel (this layout measured the same there).
 constexpr int kG1Atoms = 5;  // atoms per lane
-template <int L>
+// PL: `packed` is the plane layout (3 uint16 records per atom): the value-id
+// words come from the plane table staged in LDS instead of a kp_dot gather
+// (same graph, A/B: 7680 x 1920 5.34 -> 4.94 us, 1920 x 7680 5.49 -> 5.34 us).
+template <int L, bool PL>
 __global__ __launch_bounds__(512) void dqgemv1_kernel(const uint8_t *__restrict__ packed, int packed_bytes,
                                                       const uint16_t *__restrict__ sigma16, int rows, int apr,
                                                       const uint16_t *__restrict__ x, const uint4 *__restrict__ kp_dot,
-                                                      int round_w, float *__restrict__ y) {
+                                                      const uint32_t *__restrict__ pl_ids, int pl_vecs, int round_w,
+                                                      float *__restrict__ y) {
   constexpr int NT = 512, R = NT / L, G = kG1Atoms;
+  constexpr int VPT = PL ? 2 : 1;   // staged 16-byte vectors of the block's atom bytes per thread
+  constexpr int TPT = 3;            // PL: plane-table vectors per thread (the host checks pl_vecs <= TPT * NT)
   typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
   extern __shared__ __align__(16) uint8_t smem[];
   const int tid = threadIdx.x;
@@ -598,26 +604,41 @@ __global__ __launch_bounds__(512) void dqgemv1_kernel(const uint8_t *__restrict_
   const int row = row0 + tid / L;
   const int rows_here = min(R, rows - row0);
   const int cols = apr * kDim;
-  // the block's whole 9-byte groups [g_lo, g_hi) as aligned 16-byte vectors (the host checks nvec <= NT)
+  // the block's atom bytes as aligned 16-byte vectors (the host checks nvec <= VPT * NT):
+  // whole 9-byte groups [g_lo, g_hi) of the packed stream, or 6 bytes per atom of the plane layout
   const int atom0 = row0 * apr;
   const int g_lo = atom0 >> 2, g_hi = (atom0 + rows_here * apr + 3) >> 2;
-  const int start = g_lo * 9, base16 = start & ~15;
-  const int nvec = (g_hi * 9 - base16 + 15) >> 4;
+  const int start = PL ? 6 * atom0 : g_lo * 9, end = PL ? 6 * (atom0 + rows_here * apr) : g_hi * 9;
+  const int base16 = start & ~15;
+  const int nvec = (end - base16 + 15) >> 4;
   const int pb_off = start - base16;
-  // LDS: NT packed vectors, then 2 NT pieces of 8 bf16 x values
-  uint16_t *xh = reinterpret_cast<uint16_t *>(smem + NT * 16);
-  // round of loads: packed vector, sigma16, x pieces.  The buffer range covers the stream
-  // rounded up to whole dwords (a dword reaching past the range reads as zero; the last
+  // LDS: VPT NT atom-byte vectors, 2 NT pieces of 8 bf16 x values, (PL) TPT NT plane-table vectors;
+  // every thread stores all its slots, so no load sits under a branch
+  uint16_t *xh = reinterpret_cast<uint16_t *>(smem + VPT * NT * 16);
+  uint32_t *ptab = reinterpret_cast<uint32_t *>(smem + VPT * NT * 16 + 2 * NT * 16);
+  // round of loads: atom bytes, plane table, sigma16, x pieces.  The buffer range covers the
+  // stream rounded up to whole dwords (a dword reaching past the range reads as zero; the last
   // dword lies in the same page as the stream's last byte, the base being 16-byte aligned);
   // dwords wholly past it read as zero.
   const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint8_t *>(packed), static_cast<short>(0), (packed_bytes + 3) & ~3, 0x00020000);
-  int poff = tid < nvec ? base16 + 16 * tid : 0x7FFFFFF0;
-  asm("" : "+v"(poff));
-  const uint32_t d0 = __builtin_amdgcn_raw_buffer_load_b32(prs, poff, 0, 0);
-  const uint32_t d1 = __builtin_amdgcn_raw_buffer_load_b32(prs, poff + 4, 0, 0);
-  const uint32_t d2 = __builtin_amdgcn_raw_buffer_load_b32(prs, poff + 8, 0, 0);
-  const uint32_t d3 = __builtin_amdgcn_raw_buffer_load_b32(prs, poff + 12, 0, 0);
+  uint32_t d[VPT][4];
+#pragma unroll
+  for (int v = 0; v < VPT; ++v) {
+    const int vi = tid + v * NT;
+    int poff = vi < nvec ? base16 + 16 * vi : 0x7FFFFFF0;
+    asm("" : "+v"(poff));
+#pragma unroll
+    for (int k = 0; k < 4; ++k) d[v][k] = __builtin_amdgcn_raw_buffer_load_b32(prs, poff + 4 * k, 0, 0);
+  }
+  uint4 tq[PL ? TPT : 1];
+  if constexpr (PL) {
+#pragma unroll
+    for (int v = 0; v < TPT; ++v) {
+      const int vi = tid + v * NT;
+      tq[v] = reinterpret_cast<const uint4 *>(pl_ids)[vi < pl_vecs ? vi : 0];
+    }
+  }
   const uint16_t sig_bits = sigma16[row < rows ? row : rows - 1];
   const int items = cols / 8;  // pieces of x (the host checks items <= 2 * NT)
   uint4 xq[2];
@@ -626,36 +647,60 @@ __global__ __launch_bounds__(512) void dqgemv1_kernel(const uint8_t *__restrict_
     const int it = tid + h * NT;
     xq[h] = reinterpret_cast<const uint4 *>(x)[it < items ? it : 0];
   }
-  reinterpret_cast<uint4 *>(smem)[tid] = make_uint4(d0, d1, d2, d3);
+#pragma unroll
+  for (int v = 0; v < VPT; ++v) reinterpret_cast<uint4 *>(smem)[tid + v * NT] = make_uint4(d[v][0], d[v][1], d[v][2], d[v][3]);
 #pragma unroll
   for (int h = 0; h < 2; ++h) reinterpret_cast<uint4 *>(xh)[tid + h * NT] = xq[h];  // pieces past x: unused slots
+  if constexpr (PL) {
+#pragma unroll
+    for (int v = 0; v < TPT; ++v) reinterpret_cast<uint4 *>(ptab)[tid + v * NT] = tq[v];
+  }
   __syncthreads();
   float sig = __half2float(__ushort_as_half(sig_bits));
   asm volatile("" : "+v"(sig));  // keeps the sigma16 load in the first round (else it sinks into the epilogue)
-  // round of LDS reads: the lane's atoms sub, sub + L, ... (clamped to the block's atoms), 3 bytes
-  // each from two aligned words
   const int lrow = min(tid / L, rows_here - 1);
-  const int nbase = lrow * apr + (atom0 - g_lo * 4);
-  uint32_t w0[G], w1[G];
-  int nn[G];
+  uint4 e[G];  // per atom: the 3 value-id words, then type | position of -3 << 8
+  if constexpr (PL) {
+    // round of LDS reads: the lane's atoms' 3 records, then their planes' value-id words
+    uint32_t r[G][3];
 #pragma unroll
-  for (int i = 0; i < G; ++i) {
-    nn[i] = nbase + min(sub + i * L, apr - 1);
-    const int off = pb_off + (nn[i] >> 2) * 9 + 2 * (nn[i] & 3);
-    const uint32_t *wp = reinterpret_cast<const uint32_t *>(smem + (off & ~3));
-    w0[i] = wp[0];
-    w1[i] = wp[1];
-  }
-  // round of gathers
-  uint4 e[G];
+    for (int i = 0; i < G; ++i) {
+      const int off = pb_off + 6 * (lrow * apr + min(sub + i * L, apr - 1));
+      const uint16_t *rp = reinterpret_cast<const uint16_t *>(smem + off);
+      r[i][0] = rp[0];
+      r[i][1] = rp[1];
+      r[i][2] = rp[2];
+    }
 #pragma unroll
-  for (int i = 0; i < G; ++i) {
-    const int n = nn[i];
-    const uint32_t o = static_cast<uint32_t>((pb_off + (n >> 2) * 9 + 2 * (n & 3)) & 3);
-    const uint32_t v = __builtin_amdgcn_perm(w1[i], w0[i], (o + 2) | ((o + 1) << 8) | (o << 16) | 0x0C000000u);
-    int32_t code = static_cast<int32_t>((v >> (6 - 2 * (n & 3))) & 0x3FFFFu);
-    if (code > kKissing || sub + i * L >= apr) code = 0;
-    e[i] = kp_dot[code];
+    for (int i = 0; i < G; ++i) {
+      const bool in = sub + i * L < apr;
+      const uint32_t type = in ? (r[i][0] >> 13) & 3u : 0u;
+      const uint32_t pos = ((r[i][1] >> 13) & 7u) | ((r[i][2] >> 13) & 3u) << 3;
+      e[i] = make_uint4(ptab[r[i][0] & 0x1FFFu], ptab[r[i][1] & 0x1FFFu], ptab[r[i][2] & 0x1FFFu], type | pos << 8);
+    }
+  } else {
+    // round of LDS reads: the lane's atoms sub, sub + L, ... (clamped to the block's atoms), 3 bytes
+    // each from two aligned words; then the round of gathers
+    const int nbase = lrow * apr + (atom0 - g_lo * 4);
+    uint32_t w0[G], w1[G];
+    int nn[G];
+#pragma unroll
+    for (int i = 0; i < G; ++i) {
+      nn[i] = nbase + min(sub + i * L, apr - 1);
+      const int off = pb_off + (nn[i] >> 2) * 9 + 2 * (nn[i] & 3);
+      const uint32_t *wp = reinterpret_cast<const uint32_t *>(smem + (off & ~3));
+      w0[i] = wp[0];
+      w1[i] = wp[1];
+    }
+#pragma unroll
+    for (int i = 0; i < G; ++i) {
+      const int n = nn[i];
+      const uint32_t o = static_cast<uint32_t>((pb_off + (n >> 2) * 9 + 2 * (n & 3)) & 3);
+      const uint32_t v = __builtin_amdgcn_perm(w1[i], w0[i], (o + 2) | ((o + 1) << 8) | (o << 16) | 0x0C000000u);
+      int32_t code = static_cast<int32_t>((v >> (6 - 2 * (n & 3))) & 0x3FFFFu);
+      if (code > kKissing || sub + i * L >= apr) code = 0;
+      e[i] = kp_dot[code];
+    }
   }
   float acc[4] = {0.f, 0.f, 0.f, 0.f};
   const uint4 itab = int_value_table();
@@ -696,6 +741,49 @@ __global__ __launch_bounds__(512) void dqgemv1_kernel(const uint8_t *__restrict_
   }
 }
 
+// packed 18-bit indices -> the plane layout: per atom the 3 records of its code
+__global__ __launch_bounds__(256) void plane_layout_kernel(const uint8_t *__restrict__ packed, int64_t n_atoms,
+                                                           const uint16_t *__restrict__ code_planes,
+                                                           uint16_t *__restrict__ planes) {
+  const int64_t n = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (n >= n_atoms) return;
+  int32_t code = packed_index(packed, n);
+  if (code > kKissing) code = 0;
+  const uint2 r = *reinterpret_cast<const uint2 *>(code_planes + static_cast<int64_t>(code) * 4);
+  planes[3 * n] = static_cast<uint16_t>(r.x & 0xFFFFu);
+  planes[3 * n + 1] = static_cast<uint16_t>(r.x >> 16);
+  planes[3 * n + 2] = static_cast<uint16_t>(r.y & 0xFFFFu);
+}
+
+// One token of bf16 x from the plane layout (dqgemv1_kernel<L, true>): L lanes per row by row
+// length as in launch_dql; rows of more than 320 atoms are refused (the packed stream takes them).
+template <int L>
+int launch_gemv1_planes_l(const uint8_t *planes, const uint16_t *sigma16, int64_t rows, int64_t apr, const void *x,
+                          const DeviceTables *tab, int round_w, float *y, hipStream_t s) {
+  constexpr int NT = 512, R = NT / L;
+  const int64_t blocks = (rows + R - 1) / R;
+  const int64_t nvec_max = (6 * R * apr + 31) / 16;
+  const int64_t pl_vecs = (static_cast<int64_t>(plane_tables_host()->ids.size()) + 3) / 4;
+  if (apr > static_cast<int64_t>(kG1Atoms) * L || nvec_max > 2 * NT || apr * kDim / 8 > 2 * NT || pl_vecs > 3 * NT ||
+      6 * rows * apr >= (static_cast<int64_t>(1) << 30))
+    return fail(PLX_EINVAL, "dequant_linear: the plane layout takes rows of at most %d atoms at one token (got %lld)",
+                kG1Atoms * 64, static_cast<long long>(apr));
+  hipLaunchKernelGGL((dqgemv1_kernel<L, true>), dim3(static_cast<unsigned>(blocks)), dim3(NT),
+                     static_cast<size_t>(NT) * (32 + 32 + 48), s, planes, static_cast<int>(6 * rows * apr), sigma16,
+                     static_cast<int>(rows), static_cast<int>(apr), static_cast<const uint16_t *>(x),
+                     static_cast<const uint4 *>(nullptr), tab->pl_ids, static_cast<int>(pl_vecs), round_w, y);
+  return check_launch("dqgemv1_kernel");
+}
+
+int launch_gemv1_planes(const uint8_t *planes, const uint16_t *sigma16, int64_t rows, int64_t apr, const void *x,
+                        const DeviceTables *tab, int round_w, float *y, hipStream_t s) {
+  if (apr >= 160) return launch_gemv1_planes_l<64>(planes, sigma16, rows, apr, x, tab, round_w, y, s);
+  if (apr >= 16)
+    return (rows + 31) / 32 < 192 ? launch_gemv1_planes_l<32>(planes, sigma16, rows, apr, x, tab, round_w, y, s)
+                                  : launch_gemv1_planes_l<16>(planes, sigma16, rows, apr, x, tab, round_w, y, s);
+  return launch_gemv1_planes_l<8>(planes, sigma16, rows, apr, x, tab, round_w, y, s);
+}
+
 // t.norm_w (fp32 x only): x is normalised in the kernel when its rows fit in
 // LDS, else by rmsnorm into xnorm ([m, cols] fp32) first.
 template <int L, bool XF32, int NT>
@@ -731,9 +819,9 @@ int launch_dql(DqlTargets t, int64_t apr, const void *x, int64_t m, const uint4 
     if (!gen && m == 1 && apr >= 1 && apr <= static_cast<int64_t>(kG1Atoms) * L && nvec_max <= NT &&
         cols / 8 <= 2 * NT && t.packed_bytes[0] < (static_cast<int64_t>(1) << 30) &&
         t.rows[0] < (static_cast<int64_t>(1) << 30)) {
-      hipLaunchKernelGGL((dqgemv1_kernel<L>), g, dim3(NT), static_cast<size_t>(NT) * (16 + 32), s, t.packed[0],
+      hipLaunchKernelGGL((dqgemv1_kernel<L, false>), g, dim3(NT), static_cast<size_t>(NT) * (16 + 32), s, t.packed[0],
                          static_cast<int>(t.packed_bytes[0]), t.sigma16[0], static_cast<int>(t.rows[0]),
-                         static_cast<int>(apr), static_cast<const uint16_t *>(x), kp_dot, round_w, t.y[0]);
+                         static_cast<int>(apr), static_cast<const uint16_t *>(x), kp_dot, nullptr, 0, round_w, t.y[0]);
       return check_launch("dqgemv1_kernel");
     }
   }
@@ -932,20 +1020,25 @@ __device__ __forceinline__ uint32_t hi_lo_pack(float v) {
 
 // token tiles of 16; waves per block; quads of x in flight per wave; exact fp16 weights (hi + lo);
 // bf16 parts per activation (1: bf16 x; 3: fp32 x, see xfrag_kernel)
-template <int MT, int WV, int PD, bool EXACT, int XP, bool XD>
+// PLN: `packed` is the plane layout (3 uint16 records per atom); the value-id
+// words come from the plane table, staged in LDS, instead of kp_dq gathers.
+template <int MT, int WV, int PD, bool EXACT, int XP, bool XD, bool PLN>
 __global__ __launch_bounds__(64 * WV, WV <= 4 ? 2 : 1) void dqmm_kernel(
     const uint8_t *__restrict__ packed, int64_t packed_bytes, const uint16_t *__restrict__ sigma16, int64_t rows,
     int64_t atoms_per_row, const uint4 *__restrict__ xf, int64_t n_quads_row, int64_t m_total, int splits, int apb,
-    const uint32_t *__restrict__ kp_dq, float *__restrict__ y, float *__restrict__ partial,
-    const float *__restrict__ residual, int gelu) {
+    const uint32_t *__restrict__ kp_dq, const uint32_t *__restrict__ pl_ids, int pl_vecs, float *__restrict__ y,
+    float *__restrict__ partial, const float *__restrict__ residual, int gelu) {
   extern __shared__ __align__(16) uint8_t smem[];
   constexpr int NT = 64 * WV;
   constexpr int TOK = 16 * MT;
   const int ws = mm_row_words(apb);
-  const int region = max(kMmRows * ws, WV * TOK * kMmRedStride) * 4;
+  constexpr int TPT = 3;  // PLN: plane-table vectors per thread (the host checks pl_vecs <= TPT * NT)
+  const int region = max(kMmRows * ws + (PLN ? TPT * NT * 4 : 0), WV * TOK * kMmRedStride) * 4;
   uint32_t *wt = reinterpret_cast<uint32_t *>(smem);          // [32][ws] kp_dq words
   float *red = reinterpret_cast<float *>(smem);               // after the k loop: [WV][TOK][kMmRedStride]
   uint4 *rtab = reinterpret_cast<uint4 *>(smem + region);     // [EXACT ? 2 : 1][32] row byte tables
+  // PLN: the plane table, after the kp_dq words (read in the prologue only; the cross-wave sum may reuse it)
+  uint32_t *ptab = wt + kMmRows * ws;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, j = lane & 15, q = lane >> 4;
   const int64_t row_block = blockIdx.x / static_cast<unsigned>(splits);
   const int split = static_cast<int>(blockIdx.x % static_cast<unsigned>(splits));
@@ -1038,7 +1131,48 @@ __global__ __launch_bounds__(64 * WV, WV <= 4 ? 2 : 1) void dqmm_kernel(
   // Rows holding a multiple of 4 atoms: a thread decodes whole 9-byte groups
   // (4 codes from 3 dwords); the row tables are built while those loads are
   // in flight, then all table loads are issued before any LDS store.
-  if ((atoms_per_row & 3) == 0) {
+  if constexpr (PLN) {
+    // the block's (row, atom) records (atoms up to the end of the last quad), requested before the
+    // plane table is staged; then one barrier and the table lookups
+    constexpr int NA = (kMmRows * kMmMaxApb + NT - 1) / NT;  // (row, atom) pairs per thread at most
+    const int na = 4 * n_quads;
+    uint32_t rec[NA][3];
+#pragma unroll
+    for (int u = 0; u < NA; ++u) {
+      const int c = u * NT + tid;
+      const int r = c / na, a = c - r * na;
+      const int64_t row = row0 + r, atom = a_begin + a;
+      const bool live = c < kMmRows * na && row < rows && atom < atoms_per_row;
+      const uint16_t *rp = reinterpret_cast<const uint16_t *>(packed) + 3 * (live ? row * atoms_per_row + atom : 0);
+      const uint32_t lm = live ? 0xFFFFu : 0u;  // records past the weight read as plane 0 (the origin's)
+      rec[u][0] = rp[0] & lm;
+      rec[u][1] = rp[1] & lm;
+      rec[u][2] = rp[2] & lm;
+    }
+    // the plane table: TPT vectors per thread, stored unconditionally
+    uint4 tq[TPT];
+#pragma unroll
+    for (int v = 0; v < TPT; ++v) {
+      const int vi = tid + v * NT;
+      tq[v] = reinterpret_cast<const uint4 *>(pl_ids)[vi < pl_vecs ? vi : 0];
+    }
+#pragma unroll
+    for (int v = 0; v < TPT; ++v) reinterpret_cast<uint4 *>(ptab)[tid + v * NT] = tq[v];
+    build_row_tables();
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < NA; ++u) {
+      const int c = u * NT + tid;
+      if (c < kMmRows * na) {
+        const int r = c / na, a = c - r * na;
+        uint32_t *d = wt + r * ws + 3 * a;
+        // the origin's plane (all ids 0) for rows and atoms past the weight: index 0 of the table
+        d[0] = ptab[rec[u][0] & 0x1FFFu];
+        d[1] = ptab[rec[u][1] & 0x1FFFu];
+        d[2] = ptab[rec[u][2] & 0x1FFFu];
+      }
+    }
+  } else if ((atoms_per_row & 3) == 0) {
     constexpr int NG = (kMmRows * kMmMaxApb / 4 + NT - 1) / NT;  // groups per thread at most
     const int gpr = n_quads;                                     // groups per row in this block
     uint32_t dw[NG][3], off[NG];
@@ -1268,38 +1402,47 @@ MmPlan mm_plan(int64_t rows, int64_t apr) {
 template <int MT, int WV, int PD, bool EXACT, int XP, bool XD>
 int launch_dqmm_t(const uint8_t *packed, int64_t pb, const uint16_t *sigma16, int64_t rows, int64_t apr,
                   const uint4 *xf, int64_t m, float *y, float *partial, const MmPlan &pl, const uint32_t *kp_dq,
-                  const float *residual, int gelu, hipStream_t s) {
+                  const uint32_t *pl_ids, int pl_vecs, const float *residual, int gelu, hipStream_t s) {
   const int64_t row_blocks = (rows + kMmRows - 1) / kMmRows;
   const int64_t slabs = (m + 63) / 64;
   const int64_t nq = (apr + 3) / 4;
-  const size_t region = static_cast<size_t>(max(kMmRows * mm_row_words(pl.apb), WV * 16 * MT * kMmRedStride)) * 4;
+  // PLN: 3 plane-table vectors per thread after the kp_dq words (the region the cross-wave sum reuses)
+  const size_t region = static_cast<size_t>(max(kMmRows * mm_row_words(pl.apb) + (pl_ids ? 3 * 64 * WV * 4 : 0),
+                                                WV * 16 * MT * kMmRedStride)) * 4;
   const size_t shm = region + static_cast<size_t>(kMmRows) * 16 * (EXACT ? 2 : 1);
+  if (pl_ids && (pl_vecs > 3 * 64 * WV || shm > 80 * 1024))  // two blocks per CU
+    return fail(PLX_EINVAL, "dequant_linear: the plane table does not fit this GEMM block");
   const dim3 g(static_cast<unsigned>(row_blocks * pl.splits), static_cast<unsigned>(slabs));
-  hipLaunchKernelGGL((dqmm_kernel<MT, WV, PD, EXACT, XP, XD>), g, dim3(64 * WV), shm, s, packed, pb, sigma16, rows, apr, xf, nq, m,
-                     pl.splits, pl.apb, kp_dq, y, partial, residual, gelu);
+  if (pl_ids)
+    hipLaunchKernelGGL((dqmm_kernel<MT, WV, PD, EXACT, XP, XD, true>), g, dim3(64 * WV), shm, s, packed, pb, sigma16,
+                       rows, apr, xf, nq, m, pl.splits, pl.apb, kp_dq, pl_ids, pl_vecs, y, partial, residual, gelu);
+  else
+    hipLaunchKernelGGL((dqmm_kernel<MT, WV, PD, EXACT, XP, XD, false>), g, dim3(64 * WV), shm, s, packed, pb, sigma16,
+                       rows, apr, xf, nq, m, pl.splits, pl.apb, kp_dq, pl_ids, pl_vecs, y, partial, residual, gelu);
   return check_launch("dqmm_kernel");
 }
 
 template <int MT>
 int launch_dqmm(const uint8_t *packed, int64_t pb, const uint16_t *sigma16, int64_t rows, int64_t apr,
                 const uint4 *xf, int64_t m, float *y, float *partial, const MmPlan &pl, const uint32_t *kp_dq,
-                bool exact, bool x_f32, bool direct, const float *residual, int gelu, hipStream_t s) {
+                const uint32_t *pl_ids, int pl_vecs, bool exact, bool x_f32, bool direct, const float *residual,
+                int gelu, hipStream_t s) {
   // 8 waves (two per SIMD cover each other's load latency), one quad of x in
   // flight per wave; 4 waves with 2 quads in flight measured within 3%.
   // `direct`: bf16 x read in place (xf = x), else the fragment-order copy.
   if (x_f32)
-    return launch_dqmm_t<MT, 8, 1, true, 3, false>(packed, pb, sigma16, rows, apr, xf, m, y, partial, pl, kp_dq,
+    return launch_dqmm_t<MT, 8, 1, true, 3, false>(packed, pb, sigma16, rows, apr, xf, m, y, partial, pl, kp_dq, pl_ids, pl_vecs,
                                                    residual, gelu, s);
   if constexpr (MT <= 2)  // direct is only chosen up to 32 tokens
     if (direct)
-      return exact ? launch_dqmm_t<MT, 8, 1, true, 1, true>(packed, pb, sigma16, rows, apr, xf, m, y, partial, pl, kp_dq,
+      return exact ? launch_dqmm_t<MT, 8, 1, true, 1, true>(packed, pb, sigma16, rows, apr, xf, m, y, partial, pl, kp_dq, pl_ids, pl_vecs,
                                                             residual, gelu, s)
                    : launch_dqmm_t<MT, 8, 1, false, 1, true>(packed, pb, sigma16, rows, apr, xf, m, y, partial, pl,
-                                                             kp_dq, residual, gelu, s);
-  return exact ? launch_dqmm_t<MT, 8, 1, true, 1, false>(packed, pb, sigma16, rows, apr, xf, m, y, partial, pl, kp_dq,
+                                                             kp_dq, pl_ids, pl_vecs, residual, gelu, s);
+  return exact ? launch_dqmm_t<MT, 8, 1, true, 1, false>(packed, pb, sigma16, rows, apr, xf, m, y, partial, pl, kp_dq, pl_ids, pl_vecs,
                                                          residual, gelu, s)
                : launch_dqmm_t<MT, 8, 1, false, 1, false>(packed, pb, sigma16, rows, apr, xf, m, y, partial, pl,
-                                                          kp_dq, residual, gelu, s);
+                                                          kp_dq, pl_ids, pl_vecs, residual, gelu, s);
 }
 
 // Workspace of the batched path: the fragment-order x copy (a multiple of 256
@@ -1382,6 +1525,8 @@ int launch_dequant_linear_multi(const DqlTarget *targets, int n, int64_t cols, c
   int st = get_tables(&tab);
   if (st != PLX_OK) return st;
   const int64_t apr = cols / kDim;
+  const bool planes = (flags & PLX_DQL_PLANES) != 0;  // `packed` holds plane-layout records
+  const int pl_vecs = static_cast<int>((plane_tables_host()->ids.size() + 3) / 4);
   float *xnorm = norm ? reinterpret_cast<float *>(static_cast<uint8_t *>(workspace) +
                                                   ((mm_workspace_bytes_multi(rows_list, n, cols, m, flags) + 255) &
                                                    ~static_cast<size_t>(255)))
@@ -1416,10 +1561,12 @@ int launch_dequant_linear_multi(const DqlTarget *targets, int n, int64_t cols, c
       const MmPlan pl = mm_plan(t.rows, apr);
       float *part = reinterpret_cast<float *>(wsb + mm_workspace(t.rows, cols, m, pl, x_is_f32 != 0).xf);
       const int64_t pb = ((t.rows * apr + 3) / 4) * 9;  // packed stream length
-      st = m > 32 ? launch_dqmm<4>(t.packed, pb, t.sigma16, t.rows, apr, xf, m, t.y, part, pl, tab->kp_dq, !round_w,
-                                   x_is_f32, !copy, t.residual, gelu, s)
-                  : launch_dqmm<2>(t.packed, pb, t.sigma16, t.rows, apr, xf, m, t.y, part, pl, tab->kp_dq, !round_w,
-                                   x_is_f32, !copy, t.residual, gelu, s);
+      st = m > 32 ? launch_dqmm<4>(t.packed, planes ? 6 * t.rows * apr : pb, t.sigma16, t.rows, apr, xf, m, t.y,
+                                   part, pl, tab->kp_dq, planes ? tab->pl_ids : nullptr, pl_vecs, !round_w, x_is_f32,
+                                   !copy, t.residual, gelu, s)
+                  : launch_dqmm<2>(t.packed, planes ? 6 * t.rows * apr : pb, t.sigma16, t.rows, apr, xf, m, t.y,
+                                   part, pl, tab->kp_dq, planes ? tab->pl_ids : nullptr, pl_vecs, !round_w, x_is_f32,
+                                   !copy, t.residual, gelu, s);
       if (st != PLX_OK || pl.splits == 1) continue;
       const int64_t cnt = m * t.rows;
       if (t.rows % 4 == 0 && (reinterpret_cast<uintptr_t>(t.y) & 15u) == 0)
@@ -1431,6 +1578,14 @@ int launch_dequant_linear_multi(const DqlTarget *targets, int n, int64_t cols, c
       st = check_launch("dqmm_reduce_kernel");
     }
     return st;
+  }
+  if (planes) {
+    // the plane layout at one token: one target of bf16 x, no norm or epilogue
+    if (n != 1 || m != 1 || x_is_f32 || norm || gelu || targets[0].residual)
+      return fail(PLX_EINVAL, "dequant_linear: the plane layout takes one token of bf16 x and one plain target");
+    if (targets[0].rows <= 0) return PLX_OK;
+    return launch_gemv1_planes(targets[0].packed, targets[0].sigma16, targets[0].rows, apr, x, tab, round_w,
+                               targets[0].y, s);
   }
   const uint4 *kp = reinterpret_cast<const uint4 *>(tab->kp_gemv);
   const uint4 *kd = reinterpret_cast<const uint4 *>(tab->kp_dot);
@@ -1474,6 +1629,17 @@ int launch_dequant_linear_multi(const DqlTarget *targets, int n, int64_t cols, c
                     : launch_dql<8, false, 512>(t, apr, x, m, kp, kd, round_w, gelu, xnorm, s);
   }
   return st;
+}
+
+int launch_plane_layout(const uint8_t *packed, int64_t n_atoms, uint16_t *planes, hipStream_t s) {
+  const DeviceTables *tab = nullptr;
+  int st = get_tables(&tab);
+  if (st != PLX_OK) return st;
+  const int64_t blocks = (n_atoms + 255) / 256;
+  if (blocks > 0x7FFFFFFFll) return fail(PLX_EINVAL, "plane_layout: %lld atoms exceed one launch", static_cast<long long>(n_atoms));
+  hipLaunchKernelGGL(plane_layout_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, packed, n_atoms,
+                     tab->code_planes, planes);
+  return check_launch("plane_layout_kernel");
 }
 
 int launch_dequant_linear(const uint8_t *packed, const uint16_t *sigma16, int64_t rows, int64_t cols, const void *x,

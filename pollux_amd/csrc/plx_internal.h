@@ -5,6 +5,7 @@
 
 #include <cstddef>
 #include <cstdint>
+#include <vector>
 
 #include "../../include/pollux_amd.h"
 
@@ -54,7 +55,22 @@ struct DeviceTables {
   uint8_t *kp_gemv = nullptr;        // [kCodebook] x 16 B: 24 signed nibbles + (type | pos << 8)
   uint32_t *kp_dq = nullptr;         // [kCodebook][3] words: 3-bit value ids of 8 coordinates per word
   uint32_t *kp_dot = nullptr;        // [kCodebook][4] words: kp_dq's 3 words, then kp_gemv's (type | pos << 8)
+  uint32_t *pl_ids = nullptr;        // [n_planes] value-id word (kp_dq's format) of each distinct plane
+  uint16_t *code_planes = nullptr;   // [kCodebook][4] the plane-layout record of each code (3 used)
 };
+
+// Plane tables (tables.cpp; host, built once): the codebook rows take only a
+// few thousand distinct 8-coordinate planes.  ids = their value-id words
+// (kp_dq's format), ascending; code_planes[4 code + p] = the record of code's
+// plane p in the plane layout: plane index (13 bits) | extra << 13, the extra
+// bits being the code's type (record 0), bits 0-2 of its -3 position (record
+// 1) and bits 3-4 (record 2).
+constexpr int kMaxPlanes = 8192;
+struct PlaneTables {
+  std::vector<uint32_t> ids;
+  std::vector<uint16_t> code_planes;
+};
+const PlaneTables *plane_tables_host();
 
 // Host generator (codebook.cpp): raw coordinates, origin first, sorted.
 const int8_t *codebook_raw_host();
@@ -136,6 +152,8 @@ int launch_dequant_linear_multi(const DqlTarget *targets, int n, int64_t cols, c
                                 const float *norm_w, float norm_eps, void *workspace, size_t workspace_bytes,
                                 hipStream_t s);
 size_t dequant_linear_workspace_bytes(int64_t rows, int64_t cols, int64_t m, int flags);
+// packed 18-bit indices -> plane layout (3 uint16 records per atom)
+int launch_plane_layout(const uint8_t *packed, int64_t n_atoms, uint16_t *planes, hipStream_t s);
 int launch_dequant_linear(const uint8_t *packed, const uint16_t *sigma16, int64_t rows, int64_t cols, const void *x,
                           int flags, int64_t m, float *y, void *workspace, size_t workspace_bytes, hipStream_t s);
 size_t adam_h24_workspace_bytes(int64_t n_atoms);

@@ -26,7 +26,13 @@
 // kp_dot         per code 16 B for the one-token dequant-GEMV with bf16
 //                activations: kp_dq's 3 words, then type | position of -3 << 8
 //                as in kp_gemv (3,144,976 B).
+// pl_ids         the value-id words of the 4,961 distinct 8-coordinate planes
+//                of the codebook rows (19,844 B: staged in LDS by the kernels
+//                that read the plane layout), and
+// code_planes    per code its 3 plane-layout records (plx_internal.h), for
+//                plx_h24_plane_layout (1,572,488 B).
 
+#include <algorithm>
 #include <cstring>
 #include <mutex>
 #include <vector>
@@ -45,6 +51,48 @@ uint16_t f32_to_bf16_rne(float f) {
 
 std::mutex g_mu;
 DeviceTables g_tables[64];
+
+// dequant value ids (raw k -> id): 0->0 1->1 2->2 4->3 -4->4 -3->5 -2->6 -1->7
+const uint32_t kId[9] = {4, 5, 6, 7, 0, 1, 2, 0xFF, 3};
+
+// Value-id word of plane p of a raw row: byte i = id(coord 8p+i) | id(coord 8p+4+i) << 4.
+uint32_t plane_ids(const int8_t *r, int p) {
+  uint32_t d = 0;
+  for (int w = 0; w < 8; ++w) d |= kId[r[8 * p + w] + 4] << (8 * (w % 4) + 4 * (w / 4));
+  return d;
+}
+
+PlaneTables build_planes() {
+  PlaneTables pt;
+  const int8_t *raw = codebook_raw_host();
+  if (!raw) return pt;
+  std::vector<uint32_t> all;
+  all.reserve(static_cast<size_t>(kCodebook) * 3);
+  for (int code = 0; code < kCodebook; ++code)
+    for (int p = 0; p < 3; ++p) all.push_back(plane_ids(raw + static_cast<size_t>(code) * kDim, p));
+  std::vector<uint32_t> uniq(all);
+  std::sort(uniq.begin(), uniq.end());
+  uniq.erase(std::unique(uniq.begin(), uniq.end()), uniq.end());
+  if (uniq.size() > static_cast<size_t>(kMaxPlanes)) return pt;  // signals a failure (13-bit plane indices)
+  pt.code_planes.assign(static_cast<size_t>(kCodebook) * 4, 0);
+  for (int code = 0; code < kCodebook; ++code) {
+    const int8_t *r = raw + static_cast<size_t>(code) * kDim;
+    int nz = 0, pos = 0;
+    for (int c = 0; c < kDim; ++c) {
+      nz += r[c] != 0;
+      if (r[c] == -3) pos = c;
+    }
+    const uint32_t type = nz == 0 ? 0u : nz == 2 ? 1u : nz == 8 ? 2u : 3u;
+    const uint32_t extra[3] = {type, static_cast<uint32_t>(pos) & 7u, static_cast<uint32_t>(pos) >> 3};
+    for (int p = 0; p < 3; ++p) {
+      const uint32_t w = all[static_cast<size_t>(code) * 3 + p];
+      const uint32_t k = static_cast<uint32_t>(std::lower_bound(uniq.begin(), uniq.end(), w) - uniq.begin());
+      pt.code_planes[static_cast<size_t>(code) * 4 + p] = static_cast<uint16_t>(k | extra[p] << 13);
+    }
+  }
+  pt.ids = std::move(uniq);
+  return pt;
+}
 
 int build(int dev, DeviceTables *t) {
   const int8_t *raw = codebook_raw_host();
@@ -98,8 +146,6 @@ int build(int dev, DeviceTables *t) {
 
   // dequant-linear entries: 24 signed 4-bit coordinates, then type | pos << 8
   std::vector<uint32_t> gemv(static_cast<size_t>(kCodebook) * 4, 0);
-  // dequant value ids (raw k -> id): 0->0 1->1 2->2 4->3 -4->4 -3->5 -2->6 -1->7
-  static const uint32_t kId[9] = {4, 5, 6, 7, 0, 1, 2, 0xFF, 3};
   std::vector<uint32_t> dq(static_cast<size_t>(kCodebook) * 3, 0);
   std::vector<uint32_t> dot(static_cast<size_t>(kCodebook) * 4, 0);
   for (int code = 0; code < kCodebook; ++code) {
@@ -135,7 +181,11 @@ int build(int dev, DeviceTables *t) {
     for (int p = 0; p < 3; ++p) sw_dq[i * 3 + p] = dq[static_cast<size_t>(sweep[i]) * 3 + p];
 
   void *dt = nullptr, *drt = nullptr, *dsq = nullptr, *dsi = nullptr, *dsa = nullptr, *dr = nullptr, *dg = nullptr,
-       *dd = nullptr, *dk = nullptr;
+       *dd = nullptr, *dk = nullptr, *dpi = nullptr, *dcp = nullptr;
+  const PlaneTables *pt = plane_tables_host();
+  if (!pt) return fail(PLX_EINVAL, "the codebook rows take more than %d distinct planes", kMaxPlanes);
+  std::vector<uint32_t> pl_pad(pt->ids);  // whole 16-byte vectors (the kernels stage it by uint4)
+  pl_pad.resize((pl_pad.size() + 3) & ~static_cast<size_t>(3), 0u);
   const Upload ups[] = {
       {tiles.data(), tiles.size() * 2, &dt},
       {raw_tiles.data(), raw_tiles.size() * 2, &drt},
@@ -146,6 +196,8 @@ int build(int dev, DeviceTables *t) {
       {gemv.data(), gemv.size() * 4, &dg},
       {dq.data(), dq.size() * 4, &dd},
       {dot.data(), dot.size() * 4, &dk},
+      {pl_pad.data(), pl_pad.size() * 4, &dpi},
+      {pt->code_planes.data(), pt->code_planes.size() * 2, &dcp},
   };
   int st = PLX_OK;
   for (const Upload &u : ups) {
@@ -171,11 +223,20 @@ int build(int dev, DeviceTables *t) {
   t->kp_gemv = static_cast<uint8_t *>(dg);
   t->kp_dq = static_cast<uint32_t *>(dd);
   t->kp_dot = static_cast<uint32_t *>(dk);
+  t->pl_ids = static_cast<uint32_t *>(dpi);
+  t->code_planes = static_cast<uint16_t *>(dcp);
   t->device = dev;
   return PLX_OK;
 }
 
 }  // namespace
+
+const PlaneTables *plane_tables_host() {
+  static std::once_flag once;
+  static PlaneTables pt;
+  std::call_once(once, [] { pt = build_planes(); });
+  return pt.ids.empty() ? nullptr : &pt;
+}
 
 int get_tables(const DeviceTables **out) {
   int dev = 0;

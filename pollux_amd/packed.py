@@ -40,12 +40,40 @@ def dequantize_h24(packed: torch.Tensor, sigma16: torch.Tensor, out_features: in
     return out
 
 
-DQL_X_F32, DQL_W_AS_X, DQL_GELU, DQL_RMS_NORM = 1, 2, 4, 8  # plx_dequant_linear flags (include/pollux_amd.h)
+DQL_X_F32, DQL_W_AS_X, DQL_GELU, DQL_RMS_NORM, DQL_PLANES = 1, 2, 4, 8, 16  # plx_dequant_linear flags (include/pollux_amd.h)
+
+
+def h24_plane_layout(packed: torch.Tensor, n_atoms: int) -> torch.Tensor:
+    """The plane layout of a packed weight (plx_h24_plane_layout): int16 [3 * n_atoms], 6 bytes per atom.
+
+    Per atom 3 records naming its three 8-coordinate planes in the table of the
+    codebook's 4,961 distinct planes, so the dequant-linear kernels decode codes
+    from a table in LDS instead of gathering from the 3 MB per-code tables.  A
+    derived buffer: the packed stream stays the weight's state.
+    """
+    _lib.require_device(packed, "h24_plane_layout input")
+    if packed.dtype != torch.uint8:
+        raise ValueError("packed weights must be uint8")
+    if packed.numel() != ((n_atoms + 3) // 4) * 9:
+        raise ValueError(f"packed length {packed.numel()} does not match {n_atoms} atoms")
+    pk = packed.reshape(-1).contiguous()
+    out = torch.empty(3 * n_atoms, dtype=torch.int16, device=pk.device)
+    if n_atoms:
+        with torch.cuda.device(pk.device):
+            st = _lib.lib().plx_h24_plane_layout(_lib.ptr(pk), n_atoms, _lib.ptr(out), _lib.stream_of(pk.device))
+        _lib.check(st, "h24_plane_layout")
+    return out
+
+
+def plane_layout_takes(m: int, x_dtype: torch.dtype, in_features: int) -> bool:
+    """Whether dequant_linear runs a batch of m tokens from the plane layout: one token of bf16 x
+    with rows of at most 320 atoms, or more than 4 tokens (the GEMM)."""
+    return m > 4 or (m == 1 and x_dtype == torch.bfloat16 and in_features // 24 <= 320)
 
 
 def dequant_linear(
     packed: torch.Tensor, sigma16: torch.Tensor, out_features: int, in_features: int, x: torch.Tensor,
-    weight_rounding: str = "exact",
+    weight_rounding: str = "exact", planes: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """y = x @ W.T in fp32 without materialising W (pollux.py:491-507).
 
@@ -55,6 +83,8 @@ def dequant_linear(
     i.e. with bf16 activations the fp16 weight is rounded to bf16 first (for
     fp32 activations the two are the same).
     x: [..., in] bf16 or fp32 (other float dtypes are cast to fp32); returns fp32 [..., out].
+    planes: the weight's h24_plane_layout, used for the batches plane_layout_takes
+    names (same results, no per-atom table gathers); else the packed stream.
     """
     _lib.require_device(packed, "dequant_linear packed input")
     if packed.dtype != torch.uint8 or sigma16.dtype != torch.float16:
@@ -77,12 +107,22 @@ def dequant_linear(
     sg = sigma16.reshape(-1).contiguous()
     y = torch.empty((xx.shape[0], out_features), dtype=torch.float32, device=pk.device)
     flags = (DQL_X_F32 if xx.dtype == torch.float32 else 0) | (DQL_W_AS_X if weight_rounding == "as_x" else 0)
+    src, nsrc = pk, pk.numel()
+    if planes is not None and plane_layout_takes(xx.shape[0], xx.dtype, in_features):
+        n_atoms = out_features * (in_features // 24)
+        if planes.dtype != torch.int16 or planes.numel() != 3 * n_atoms or planes.device != pk.device:
+            raise ValueError("planes must be the weight's int16 plane layout (h24_plane_layout) on its device")
+        src = planes.contiguous()
+        if src.data_ptr() % 16:
+            src = src.clone()
+        nsrc = 6 * n_atoms
+        flags |= DQL_PLANES
     lib = _lib.lib()
     nws = int(lib.plx_dequant_linear_workspace_bytes(out_features, in_features, xx.shape[0], flags))
     ws = torch.empty(max(nws, 16), dtype=torch.uint8, device=pk.device) if nws else None
     with torch.cuda.device(pk.device):
         st = lib.plx_dequant_linear(
-            _lib.ptr(pk), pk.numel(), _lib.ptr(sg), out_features, in_features, _lib.ptr(xx),
+            _lib.ptr(src), nsrc, _lib.ptr(sg), out_features, in_features, _lib.ptr(xx),
             flags, xx.shape[0], _lib.ptr(y), _lib.ptr(ws), nws, _lib.stream_of(pk.device),
         )
     _lib.check(st, "dequant_linear")
@@ -229,10 +269,14 @@ class PackedH24Linear(nn.Module):
 
     Before materialize, forward runs dequant_linear with ``weight_rounding``
     (class default "exact"; "as_x" reproduces the reference's rounding of W to
-    x's dtype).
+    x's dtype).  With ``use_plane_layout`` (class default True) the batches
+    plane_layout_takes names read a plane layout of the weight kept beside the
+    packed buffer (6 B per atom, built on first use; same results, no per-atom
+    table gathers); False keeps only the packed stream resident.
     """
 
     weight_rounding = "exact"
+    use_plane_layout = True
 
     def __init__(self, in_features: int, out_features: int, bias: bool = False) -> None:
         super().__init__()
@@ -259,11 +303,30 @@ class PackedH24Linear(nn.Module):
         del self.sigma_rows
         self._materialized = True
 
+    def plane_layout(self) -> torch.Tensor:
+        """The packed weight's h24_plane_layout, built on first use and kept beside it (not part of the state).
+
+        Rebuilt when packed_weights is replaced (compared by identity) or modified in place (its version
+        counter; a tensor created under ``torch.inference_mode`` keeps none, so replace such a buffer instead).
+        """
+        pk = self.packed_weights
+        ver = None if pk.is_inference() else pk._version
+        hit = self.__dict__.get("_planes")
+        if hit is not None and hit[0] is pk and hit[1] == ver:
+            return hit[2]
+        planes = h24_plane_layout(pk, self.num_atoms)
+        self.__dict__["_planes"] = (pk, ver, planes)
+        return planes
+
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         if not self._materialized:
-            # fused path: weights stay packed (0.76 bits/param); fp32 result cast to x's dtype
+            # fused path: weights stay packed (0.76 bits/param); fp32 result cast to x's dtype.  The batches
+            # plane_layout_takes names run from the plane layout (6 B per atom, built once).
+            m = x.numel() // self.in_features if self.in_features else 0
+            takes = self.use_plane_layout and plane_layout_takes(m, x.dtype, self.in_features)
+            planes = self.plane_layout() if takes else None
             y = dequant_linear(self.packed_weights, self.sigma_rows, self.out_features, self.in_features, x,
-                               weight_rounding=self.weight_rounding).to(x.dtype)
+                               weight_rounding=self.weight_rounding, planes=planes).to(x.dtype)
             return y if self.bias is None else y + self.bias.to(x.dtype)
         return F.linear(x, self.weight.to(dtype=x.dtype), self.bias)
 

@@ -92,3 +92,23 @@ def test_cpu_tensors_are_rejected():
     # N == 0 keeps the reference's early return (castor.py:519-520)
     e = torch.zeros(0, 24)
     assert castor.castor_quantize_leech(e, None).shape == (0, 24)
+
+
+def test_plane_table_is_the_set_of_codebook_planes():
+    # the 8-coordinate planes of every codebook row, as value-id words (byte i = id(c_i) | id(c_{4+i}) << 4)
+    lib = _lib.lib()
+    n = int(lib.plx_plane_table(None, 0))
+    ids = np.zeros(n, np.uint32)
+    assert int(lib.plx_plane_table(ids.ctypes.data, n)) == n
+    assert np.all(np.diff(ids.astype(np.int64)) > 0)  # ascending, distinct
+    values = np.array([0, 1, 2, 4, -4, -3, -2, -1], np.int8)
+    nib = (ids[:, None] >> (4 * np.arange(8, dtype=np.uint32))[None, :]) & 0xF
+    assert nib.max() < 8
+    # nibble 2i is coordinate i, nibble 2i+1 coordinate 4+i
+    order = np.array([0, 2, 4, 6, 1, 3, 5, 7])
+    planes = values[nib[:, order]]
+    raw = cb.codebook_int8().reshape(-1, 3, 8).reshape(-1, 8)
+    want = np.unique(raw, axis=0)
+    got = np.unique(planes, axis=0)
+    assert len(got) == n == len(want) == 4961
+    assert np.array_equal(got, want)
