@@ -224,7 +224,10 @@ def _fused_group(layers: list) -> tuple[torch.Tensor, torch.Tensor, int, list[in
         r += l.out_features
     fused = (torch.cat([l.packed_weights.reshape(-1) for l in layers]),
              torch.cat([l.sigma_rows.reshape(-1) for l in layers]), r, offs)
-    layers[0].__dict__["_stacked"] = (bufs, versions, fused)
+    if not torch.cuda.is_current_stream_capturing():
+        # under graph capture the copies run only on replay: the captured graph makes its own, and
+        # nothing is kept for eager calls that may come before a replay
+        layers[0].__dict__["_stacked"] = (bufs, versions, fused)
     return fused
 
 
@@ -303,7 +306,7 @@ class PackedH24Linear(nn.Module):
         del self.sigma_rows
         self._materialized = True
 
-    def plane_layout(self) -> torch.Tensor:
+    def plane_layout(self) -> torch.Tensor | None:
         """The packed weight's h24_plane_layout, built on first use and kept beside it (not part of the state).
 
         Rebuilt when packed_weights is replaced (compared by identity) or modified in place (its version
@@ -314,6 +317,10 @@ class PackedH24Linear(nn.Module):
         hit = self.__dict__.get("_planes")
         if hit is not None and hit[0] is pk and hit[1] == ver:
             return hit[2]
+        if torch.cuda.is_current_stream_capturing():
+            # a layout built under graph capture holds nothing until the graph is replayed: callers
+            # then read the packed stream (build the layout with an eager call before capturing)
+            return None
         planes = h24_plane_layout(pk, self.num_atoms)
         self.__dict__["_planes"] = (pk, ver, planes)
         return planes

@@ -155,3 +155,41 @@ def test_packed_layer_keeps_its_layout_current(dev):
     assert ((y2 - ref2).norm() / ref2.norm()).item() <= 1e-2
     layer.use_plane_layout = False  # packed stream only: the same results
     assert torch.equal(layer(xb.to(dev)).float().cpu(), y2)
+
+
+def test_graph_captured_before_any_eager_call(dev):
+    # Derived buffers (plane layout, stacked q/k/v copy) built under capture hold nothing until a replay:
+    # none is kept for eager calls, and the captured graph still computes the right result.
+    from pollux_amd.packed import packed_linear_group
+
+    with torch.cuda.device(dev):
+        _lib.check(_lib.lib().plx_device_init(), "init")
+    out_f, in_f = 96, 1152
+    layers, w16s = [], []
+    for i in range(3):
+        idx, sig, packed, g = _layer(out_f, in_f, 40 + i)
+        lyr = PackedH24Linear(in_f, out_f)
+        lyr.load_state_dict({"packed_weights": packed, "sigma_rows": sig})
+        layers.append(lyr.to(dev))
+        w16s.append(torch_ref.materialize(idx, sig, out_f, in_f))
+    xb = torch.randn(9, in_f, generator=torch.Generator().manual_seed(3)).to(torch.bfloat16)
+    refs = [torch_ref.linear_fp32(xb, w).to(torch.bfloat16).float() for w in w16s]
+    xd = xb.to(dev)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        y_single = layers[0](xd)
+        y_group = packed_linear_group(layers, xd.float())
+    assert "_planes" not in layers[0].__dict__ and "_stacked" not in layers[0].__dict__
+
+    def close(a, b):
+        return ((a.float().cpu() - b).norm() / b.norm()).item() <= 1e-2  # bf16 rounding of the outputs
+
+    assert close(layers[0](xd), refs[0])  # eager: builds the layout now
+    eager_group = packed_linear_group(layers, xd.float())
+    assert all(close(a, r) for a, r in zip(eager_group, refs))
+    for _ in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert close(y_single, refs[0])
+        assert all(close(a, r) for a, r in zip(y_group, refs))
+        assert close(layers[1](xd), refs[1])  # eager work between the replays
