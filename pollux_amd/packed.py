@@ -203,6 +203,11 @@ def dequant_linear_multi(
     return [y.reshape(*lead, y.shape[1]) for y in ys]
 
 
+def _capturing() -> bool:
+    """Whether the current stream is capturing a HIP graph (False on a host without a device)."""
+    return torch.cuda.is_available() and torch.cuda.is_current_stream_capturing()
+
+
 def _fused_group(layers: list) -> tuple[torch.Tensor, torch.Tensor, int, list[int]]:
     """(packed, sigma16, rows, row offsets) of ``layers`` stacked along their output rows.
 
@@ -224,7 +229,7 @@ def _fused_group(layers: list) -> tuple[torch.Tensor, torch.Tensor, int, list[in
         r += l.out_features
     fused = (torch.cat([l.packed_weights.reshape(-1) for l in layers]),
              torch.cat([l.sigma_rows.reshape(-1) for l in layers]), r, offs)
-    if not torch.cuda.is_current_stream_capturing():
+    if not _capturing():
         # under graph capture the copies run only on replay: the captured graph makes its own, and
         # nothing is kept for eager calls that may come before a replay
         layers[0].__dict__["_stacked"] = (bufs, versions, fused)
@@ -317,7 +322,7 @@ class PackedH24Linear(nn.Module):
         hit = self.__dict__.get("_planes")
         if hit is not None and hit[0] is pk and hit[1] == ver:
             return hit[2]
-        if torch.cuda.is_current_stream_capturing():
+        if _capturing():
             # a layout built under graph capture holds nothing until the graph is replayed: callers
             # then read the packed stream (build the layout with an eager call before capturing)
             return None
@@ -573,5 +578,6 @@ class PackedInt8Linear(_PackedInt8Rows):
             return hit[2]
         w16 = self.weight if self._materialized else dequantize_int8_rows(self.weight_int8, self.mu_rows)
         w = w16.detach().to(dtype=dtype)
-        cache[dtype] = (src, versions, w)
+        if not _capturing():  # a cast made under capture is filled only on replay
+            cache[dtype] = (src, versions, w)
         return w

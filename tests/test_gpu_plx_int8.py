@@ -109,6 +109,27 @@ def test_packed_int8_linear_sees_new_weights(dev):
     assert torch.equal(lin(big), want)
 
 
+def test_packed_int8_linear_cast_not_kept_from_graph_capture(dev):
+    # a cast made under graph capture is filled only on replay: it is not kept for eager calls
+    g = torch.Generator().manual_seed(82)
+    lin = PackedInt8Linear(48, 100).to(dev)
+    lin.gemv_max_tokens = 16
+    q, mu = plx_pack.quantize_int8_rows(torch.randn(100, 48, generator=g).to(dev))
+    lin.load_state_dict({"weight_int8": q, "mu_rows": mu})
+    big = torch.randn(20, 48, generator=g).to(dev)
+    want = torch.nn.functional.linear(big, _ref_int8_materialize(q, mu).float())
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        y = lin(big)
+    assert torch.float32 not in lin.__dict__.get("_cast", {})
+    assert torch.equal(lin(big), want)
+    for _ in range(2):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y, want)
+
+
 def _check_int8_linear(y, x, w16, bound=1e-5):
     """y against fp64 x @ w16.T: |err| <= bound * sum |x||w| per element (fp32 accumulation)."""
     xd, wd = x.double().cpu(), w16.double().cpu()
