@@ -217,8 +217,10 @@ int plx_dequant_f16(const uint8_t *packed, int64_t n_packed_bytes, const uint16_
                               row first (pre-norm of pollux.py:660-661) */
 #define PLX_DQL_PLANES 16  /* `packed` is the plane layout of the weight
                               (plx_h24_plane_layout, 6 bytes per atom) instead of
-                              the 18-bit stream; taken by plx_dequant_linear for
-                              one token of bf16 x and for batches above 4 tokens */
+                              the 18-bit stream (each target's, for
+                              plx_dequant_linear_multi); taken for one token
+                              (rows of at most 320 atoms) and for batches above
+                              4 tokens, with the same results */
 
 /* The plane layout of a packed weight: per atom 3 little-endian uint16
  * records (6 bytes, atom order), one per 8-coordinate plane: a 13-bit index

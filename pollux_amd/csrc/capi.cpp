@@ -280,8 +280,11 @@ int plx_dequant_linear_multi(const plx_dql_target *targets, int n, int64_t cols,
   PLX_REQUIRE(cols > 0 && cols % kDim == 0, "plx_dequant_linear_multi: bad column count %lld",
               static_cast<long long>(cols));
   PLX_REQUIRE(m_rows >= 0, "plx_dequant_linear_multi: negative batch");
-  PLX_REQUIRE((flags & ~(PLX_DQL_X_F32 | PLX_DQL_W_AS_X | PLX_DQL_GELU | PLX_DQL_RMS_NORM)) == 0,
+  PLX_REQUIRE((flags & ~(PLX_DQL_X_F32 | PLX_DQL_W_AS_X | PLX_DQL_GELU | PLX_DQL_RMS_NORM | PLX_DQL_PLANES)) == 0,
               "plx_dequant_linear_multi: unknown flags 0x%x", flags);
+  PLX_REQUIRE(!(flags & PLX_DQL_PLANES) || m_rows <= 1 || m_rows > 4,
+              "plx_dequant_linear_multi: the plane layout takes one token or more than 4 (got %lld)",
+              static_cast<long long>(m_rows));
   PLX_REQUIRE(((flags & PLX_DQL_RMS_NORM) != 0) == (norm_weight != nullptr),
               "plx_dequant_linear_multi: PLX_DQL_RMS_NORM needs a norm weight, and a norm weight the flag");
   PLX_REQUIRE(!(flags & PLX_DQL_RMS_NORM) || (flags & PLX_DQL_X_F32),
@@ -356,8 +359,8 @@ int plx_dequant_linear(const uint8_t *packed, int64_t n_packed_bytes, const uint
   if (flags & PLX_DQL_PLANES) {
     PLX_REQUIRE(n_packed_bytes == 6 * n_atoms, "plx_dequant_linear: plane layout of %lld bytes does not match %lld atoms",
                 static_cast<long long>(n_packed_bytes), static_cast<long long>(n_atoms));
-    PLX_REQUIRE(m_rows > 4 || (m_rows == 1 && !(flags & PLX_DQL_X_F32)),
-                "plx_dequant_linear: the plane layout takes one token of bf16 x or more than 4 tokens (got %lld)",
+    PLX_REQUIRE(m_rows > 4 || m_rows <= 1,
+                "plx_dequant_linear: the plane layout takes one token or more than 4 (got %lld)",
                 static_cast<long long>(m_rows));
   } else {
     PLX_REQUIRE(n_packed_bytes == ((n_atoms + 3) / 4) * 9,

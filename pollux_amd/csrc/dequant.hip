@@ -263,16 +263,23 @@ using DqlArgs = typename std::conditional<GEN, DqlTargets, DqlOne>::type;
 // 320 at 64) give every lane exactly 5 atoms, one round (4 per round: two
 // rounds, 2% slower at one token; 8: wasted slots, 11% slower)
 constexpr int kDqlGather = 5;
+constexpr int kDqlPlVecs = 2;          // PL: record vectors per thread at 512 threads (16 KB per block)
+constexpr int kDqlPlTableVecs = 1536;  // PL: plane-table capacity in 16-byte vectors (24 KB)
 
 // GEN: several targets and the epilogue (DqlTargets); else one target, no epilogue (DqlOne).
 // XREG (with XL, m_total <= MB and MB token rows of at most 8 * NT values): x
 // goes through registers into LDS and the general staging loop is compiled
 // out - at one token these kernels are short enough that their code size
 // shows in the time (cold instruction fetch).
-template <int L, int MB, bool XF32, bool XL, int NT, bool GEN, bool XREG>
+// PL: `packed` is the plane layout (3 uint16 records per atom); the coordinate
+// words come from the plane table (kp_gemv's format) staged in LDS instead of a
+// kp_gemv gather; the block's records are staged with kDqlPlVecs raw buffer
+// loads per thread, x after them, the table after x.
+template <int L, int MB, bool XF32, bool XL, int NT, bool GEN, bool XREG, bool PL = false>
 __global__ __launch_bounds__(NT) void dqlinear_kernel(const DqlArgs<GEN> targets, int64_t atoms_per_row,
                                                        const void *__restrict__ x, int64_t m_total,
-                                                       const uint4 *__restrict__ kp_gemv, int round_w, int gelu) {
+                                                       const uint4 *__restrict__ kp_gemv, int round_w, int gelu,
+                                                       const uint32_t *__restrict__ pl_nib, int pl_vecs) {
   extern __shared__ __align__(16) uint8_t smem[];
   __shared__ float norm_red[NT / 64][MB];  // per-wave sums of squares (GEN with norm_w)
   constexpr int R = NT / L;
@@ -314,16 +321,45 @@ __global__ __launch_bounds__(NT) void dqlinear_kernel(const DqlArgs<GEN> targets
   // Copy the bytes [g_lo*9, g_hi*9) as aligned 16-byte vectors: byte b of the
   // stream lands at LDS offset b - base16, so vectors stay aligned on both
   // sides; a last vector that would cross the end of the stream goes bytewise.
-  const int64_t start = g_lo * 9, end = g_hi * 9, base16 = start & ~static_cast<int64_t>(15);
+  const int64_t start = PL ? 6 * atom0 : g_lo * 9;
+  const int64_t end = PL ? 6 * (atom0 + rows_here * atoms_per_row) : g_hi * 9;
+  const int64_t base16 = start & ~static_cast<int64_t>(15);
   const int nvec = static_cast<int>((end - base16 + 15) >> 4);
   const uint8_t *pb = smem + (start - base16);
-  float *xs = reinterpret_cast<float *>(smem + static_cast<int64_t>(nvec) * 16);
+  constexpr int PVT = kDqlPlVecs * 512 / NT;  // PL: staged record vectors per thread
+  float *xs = reinterpret_cast<float *>(smem + (PL ? PVT * NT * 16 : static_cast<int64_t>(nvec) * 16));
+  constexpr int TPT = (kDqlPlTableVecs + NT - 1) / NT;  // PL: plane-table vectors per thread
+  uint32_t *ptab = reinterpret_cast<uint32_t *>(reinterpret_cast<uint8_t *>(xs) +
+                                                (XL ? static_cast<int64_t>(MB) * atoms_per_row * kDim * 4 : 0));
   // the thread's first vector is requested before anything else (from a
   // clamped address, so no branch holds the load)
   const int64_t gb0 = base16 + 16 * static_cast<int64_t>(threadIdx.x);
   const bool v0ok = static_cast<int>(threadIdx.x) < nvec && gb0 + 16 <= packed_bytes;
   uint4 pk0 = make_uint4(0u, 0u, 0u, 0u);
-  if (packed_bytes >= 16) pk0 = gload16(packed + (v0ok ? gb0 : 0));
+  if (!PL && packed_bytes >= 16) pk0 = gload16(packed + (v0ok ? gb0 : 0));
+  // PL: the block's records by raw buffer loads (a dword wholly or partly past the layout reads as
+  // zero; the range is the layout rounded up to whole dwords, inside the allocation's last page)
+  uint32_t pd[PL ? PVT : 1][4];
+  if constexpr (PL) {
+    const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t *>(packed), static_cast<short>(0), static_cast<int>((packed_bytes + 3) & ~3ll), 0x00020000);
+#pragma unroll
+    for (int v = 0; v < PVT; ++v) {
+      const int vi = static_cast<int>(threadIdx.x) + v * NT;
+      int poff = vi < nvec ? static_cast<int>(base16) + 16 * vi : 0x7FFFFFF0;
+      asm("" : "+v"(poff));
+#pragma unroll
+      for (int k = 0; k < 4; ++k) pd[v][k] = __builtin_amdgcn_raw_buffer_load_b32(prs, poff + 4 * k, 0, 0);
+    }
+  }
+  uint4 tq[PL ? TPT : 1];
+  if constexpr (PL) {
+#pragma unroll
+    for (int v = 0; v < TPT; ++v) {
+      const int vi = static_cast<int>(threadIdx.x) + v * NT;
+      tq[v] = reinterpret_cast<const uint4 *>(pl_nib)[vi < pl_vecs ? vi : 0];
+    }
+  }
 
   // requests that need nothing staged: sigma16, residuals and (first MB tokens) x and norm weights;
   // every lane loads its (clamped) row: a load under a divergent branch would be
@@ -357,7 +393,14 @@ __global__ __launch_bounds__(NT) void dqlinear_kernel(const DqlArgs<GEN> targets
     }
   }
 
-  for (int i = threadIdx.x; i < nvec; i += NT) {
+  if constexpr (PL) {
+#pragma unroll
+    for (int v = 0; v < PVT; ++v)
+      reinterpret_cast<uint4 *>(smem)[threadIdx.x + v * NT] = make_uint4(pd[v][0], pd[v][1], pd[v][2], pd[v][3]);
+#pragma unroll
+    for (int v = 0; v < TPT; ++v) reinterpret_cast<uint4 *>(ptab)[threadIdx.x + v * NT] = tq[v];
+  }
+  for (int i = threadIdx.x; !PL && i < nvec; i += NT) {
     const int64_t gb = base16 + 16 * static_cast<int64_t>(i);
     if (i == static_cast<int>(threadIdx.x) && v0ok) {
       reinterpret_cast<uint4 *>(smem)[i] = pk0;
@@ -474,12 +517,19 @@ __global__ __launch_bounds__(NT) void dqlinear_kernel(const DqlArgs<GEN> targets
     if (live) {
       // block-local 32-bit atom indices (the staged groups hold < 2^31 atoms)
       const int apr32 = static_cast<int>(atoms_per_row);
-      const int nbase = static_cast<int>(row * atoms_per_row - g_lo * 4);  // atom index relative to the staged groups
+      const int nbase = static_cast<int>(row * atoms_per_row - (PL ? atom0 : g_lo * 4));  // atom index in the stage
       for (int a0 = sub; a0 < apr32; a0 += kDqlGather * L) {
         uint4 e[kDqlGather];
 #pragma unroll
         for (int i = 0; i < kDqlGather; ++i) {
           const int a = a0 + i * L;
+          if constexpr (PL) {
+            const uint16_t *rp = reinterpret_cast<const uint16_t *>(pb + 6 * (nbase + min(a, apr32 - 1)));
+            const uint32_t r0 = rp[0], r1 = rp[1], r2 = rp[2];
+            const uint32_t pos = ((r1 >> 13) & 7u) | ((r2 >> 13) & 3u) << 3;
+            e[i] = make_uint4(ptab[r0 & 0x1FFFu], ptab[r1 & 0x1FFFu], ptab[r2 & 0x1FFFu], ((r0 >> 13) & 3u) | pos << 8);
+            continue;
+          }
           int32_t code = 0;
           if (a < apr32) {
             const int n = nbase + a;
@@ -786,9 +836,10 @@ int launch_gemv1_planes(const uint8_t *planes, const uint16_t *sigma16, int64_t 
 
 // t.norm_w (fp32 x only): x is normalised in the kernel when its rows fit in
 // LDS, else by rmsnorm into xnorm ([m, cols] fp32) first.
-template <int L, bool XF32, int NT>
+// PL: the targets' `packed` are plane layouts (one token; always the general kernel).
+template <int L, bool XF32, int NT, bool PL = false>
 int launch_dql(DqlTargets t, int64_t apr, const void *x, int64_t m, const uint4 *tab, const uint4 *kp_dot, int round_w,
-               int gelu, float *xnorm, hipStream_t s) {
+               int gelu, float *xnorm, hipStream_t s, const uint32_t *pl_nib = nullptr, int pl_vecs = 0) {
   constexpr int R = NT / L;
   int64_t blocks = 0;
   for (int i = 0; i < t.n; ++i) blocks = max(blocks, (t.rows[i] + R - 1) / R);
@@ -801,9 +852,15 @@ int launch_dql(DqlTargets t, int64_t apr, const void *x, int64_t m, const uint4 
   const int64_t cols = apr * kDim;
   const int mb = m >= 4 ? 4 : m >= 2 ? 2 : 1;
   const size_t xbytes = static_cast<size_t>(mb) * cols * 4;
-  const bool xl = p16 + xbytes <= 48 * 1024;
-  const size_t shm = xl ? p16 + xbytes : p16;
-  if (shm > 64 * 1024) return fail(PLX_EINVAL, "dequant_linear: rows of %lld atoms are too long", static_cast<long long>(apr));
+  // PL: records (kDqlPlVecs * 512 vectors, all stored), x when it fits, the plane table
+  const size_t prec = static_cast<size_t>(kDqlPlVecs) * 512 * 16;
+  const bool xl = PL ? xbytes <= 48 * 1024 : p16 + xbytes <= 48 * 1024;
+  const size_t shm = PL ? prec + (xl ? xbytes : 0) + static_cast<size_t>(kDqlPlTableVecs) * 16 : xl ? p16 + xbytes : p16;
+  if (PL && (m != 1 || (6 * R * apr + 31) / 16 > kDqlPlVecs * 512 || pl_vecs > kDqlPlTableVecs))
+    return fail(PLX_EINVAL, "dequant_linear: the plane layout takes one token and rows of at most %d atoms here",
+                kDqlPlVecs * 512 * 16 / (6 * R) - 1);
+  if (shm > (PL ? 96 : 64) * 1024)
+    return fail(PLX_EINVAL, "dequant_linear: rows of %lld atoms are too long", static_cast<long long>(apr));
   // x through registers: one pass over all tokens, at most one 8-value piece per thread
   const bool xreg = xl && m <= mb && m * cols <= 8 * NT;
   if (t.norm_w && !xl) {
@@ -812,8 +869,8 @@ int launch_dql(DqlTargets t, int64_t apr, const void *x, int64_t m, const uint4 
     x = xnorm;
     t.norm_w = nullptr;
   }
-  const bool gen = t.n > 1 || t.residual[0] != nullptr || gelu || t.norm_w != nullptr;
-  if constexpr (NT == 512 && !XF32) {
+  const bool gen = PL || t.n > 1 || t.residual[0] != nullptr || gelu || t.norm_w != nullptr;
+  if constexpr (NT == 512 && !XF32 && !PL) {
     // one token of bf16 x, one target: dqgemv1_kernel (at most kG1Atoms atoms per lane, int offsets)
     const int64_t nvec_max = (R * apr / 4 + 2) * 9 / 16 + 2;
     if (!gen && m == 1 && apr >= 1 && apr <= static_cast<int64_t>(kG1Atoms) * L && nvec_max <= NT &&
@@ -829,11 +886,23 @@ int launch_dql(DqlTargets t, int64_t apr, const void *x, int64_t m, const uint4 
   do {                                                                                                          \
     if (gen)                                                                                                    \
       hipLaunchKernelGGL((dqlinear_kernel<L, MB, XF32, XL, NT, true, XR>), g, dim3(NT), shm, s, t, apr, x, m, tab, \
-                         round_w, gelu);                                                                         \
+                         round_w, gelu, nullptr, 0);                                                             \
     else                                                                                                        \
       hipLaunchKernelGGL((dqlinear_kernel<L, MB, XF32, XL, NT, false, XR>), g, dim3(NT), shm, s, one, apr, x, m,  \
-                         tab, round_w, 0);                                                                       \
+                         tab, round_w, 0, nullptr, 0);                                                           \
   } while (0)
+  if constexpr (PL) {
+    if (xreg)
+      hipLaunchKernelGGL((dqlinear_kernel<L, 1, XF32, true, NT, true, true, true>), g, dim3(NT), shm, s, t, apr, x, m,
+                         tab, round_w, gelu, pl_nib, pl_vecs);
+    else if (xl)
+      hipLaunchKernelGGL((dqlinear_kernel<L, 1, XF32, true, NT, true, false, true>), g, dim3(NT), shm, s, t, apr, x,
+                         m, tab, round_w, gelu, pl_nib, pl_vecs);
+    else
+      hipLaunchKernelGGL((dqlinear_kernel<L, 1, XF32, false, NT, true, false, true>), g, dim3(NT), shm, s, t, apr, x,
+                         m, tab, round_w, gelu, pl_nib, pl_vecs);
+    return check_launch("dqlinear_kernel");
+  }
   if (mb == 4) {
     if (xreg) PLX_DQL(4, true, true); else if (xl) PLX_DQL(4, true, false); else PLX_DQL(4, false, false);
   } else if (mb == 2) {
@@ -1580,12 +1649,17 @@ int launch_dequant_linear_multi(const DqlTarget *targets, int n, int64_t cols, c
     return st;
   }
   if (planes) {
-    // the plane layout at one token: one target of bf16 x, no norm or epilogue
-    if (n != 1 || m != 1 || x_is_f32 || norm || gelu || targets[0].residual)
-      return fail(PLX_EINVAL, "dequant_linear: the plane layout takes one token of bf16 x and one plain target");
-    if (targets[0].rows <= 0) return PLX_OK;
-    return launch_gemv1_planes(targets[0].packed, targets[0].sigma16, targets[0].rows, apr, x, tab, round_w,
-                               targets[0].y, s);
+    // the plane layout below the MFMA path: one token only
+    if (m != 1) return fail(PLX_EINVAL, "dequant_linear: the plane layout takes one token or more than 4 (got %lld)",
+                            static_cast<long long>(m));
+    if (n == 1 && !x_is_f32 && !norm && !gelu && !targets[0].residual) {  // the plain bf16 call
+      if (targets[0].rows <= 0) return PLX_OK;
+      return launch_gemv1_planes(targets[0].packed, targets[0].sigma16, targets[0].rows, apr, x, tab, round_w,
+                                 targets[0].y, s);
+    }
+    if (apr > 320)
+      return fail(PLX_EINVAL, "dequant_linear: the plane layout takes rows of at most 320 atoms at one token (got %lld)",
+                  static_cast<long long>(apr));
   }
   const uint4 *kp = reinterpret_cast<const uint4 *>(tab->kp_gemv);
   const uint4 *kd = reinterpret_cast<const uint4 *>(tab->kp_dot);
@@ -1596,7 +1670,7 @@ int launch_dequant_linear_multi(const DqlTarget *targets, int n, int64_t cols, c
     for (int i = 0; i < kDqlMaxTargets; ++i) {
       const DqlTarget &src = targets[i0 + (i < t.n ? i : 0)];
       t.packed[i] = src.packed;
-      t.packed_bytes[i] = ((src.rows * apr + 3) / 4) * 9;
+      t.packed_bytes[i] = planes ? 6 * src.rows * apr : ((src.rows * apr + 3) / 4) * 9;
       t.sigma16[i] = src.sigma16;
       t.rows[i] = i < t.n ? src.rows : 0;
       t.y[i] = src.y;
@@ -1607,26 +1681,30 @@ int launch_dequant_linear_multi(const DqlTarget *targets, int n, int64_t cols, c
     // lanes per row: about 3-5 atoms per lane (7680 x 1920 at M = 1: 16 lanes as fast as 32, 8 slower; the
     // 1920-row q/k/v and o_proj launches of the decode step 3% faster with 32, from the doubled grid);
     // 512-thread blocks (4% faster than 256 at M = 1, 1,024 slower), 256 for rows too long to stage 8 in LDS
-    if (apr >= 3072)
+#define PLX_DQL_SEL(L_)                                                                                   \
+  (planes ? (x_is_f32 ? launch_dql<L_, true, 512, true>(t, apr, x, m, kp, kd, round_w, gelu, xnorm, s, tab->pl_nib, \
+                                                        pl_vecs)                                                    \
+                      : launch_dql<L_, false, 512, true>(t, apr, x, m, kp, kd, round_w, gelu, xnorm, s,             \
+                                                         tab->pl_nib, pl_vecs))                                     \
+          : (x_is_f32 ? launch_dql<L_, true, 512>(t, apr, x, m, kp, kd, round_w, gelu, xnorm, s)                    \
+                      : launch_dql<L_, false, 512>(t, apr, x, m, kp, kd, round_w, gelu, xnorm, s)))
+    if (apr >= 3072)  // (the plane layout stops at 320 atoms per row)
       st = x_is_f32 ? launch_dql<64, true, 256>(t, apr, x, m, kp, kd, round_w, gelu, xnorm, s)
                     : launch_dql<64, false, 256>(t, apr, x, m, kp, kd, round_w, gelu, xnorm, s);
     else if (apr >= 160)
-      st = x_is_f32 ? launch_dql<64, true, 512>(t, apr, x, m, kp, kd, round_w, gelu, xnorm, s)
-                    : launch_dql<64, false, 512>(t, apr, x, m, kp, kd, round_w, gelu, xnorm, s);
+      st = PLX_DQL_SEL(64);
     else if (apr >= 16) {
       // 32 lanes per row (16 rows per block) when 16 would leave the grid under 192 blocks
       int64_t mrows = 0;
       for (int i = 0; i < t.n; ++i) mrows = t.rows[i] > mrows ? t.rows[i] : mrows;
       if ((mrows + 31) / 32 * t.n < 192)
-        st = x_is_f32 ? launch_dql<32, true, 512>(t, apr, x, m, kp, kd, round_w, gelu, xnorm, s)
-                      : launch_dql<32, false, 512>(t, apr, x, m, kp, kd, round_w, gelu, xnorm, s);
+        st = PLX_DQL_SEL(32);
       else
-        st = x_is_f32 ? launch_dql<16, true, 512>(t, apr, x, m, kp, kd, round_w, gelu, xnorm, s)
-                      : launch_dql<16, false, 512>(t, apr, x, m, kp, kd, round_w, gelu, xnorm, s);
+        st = PLX_DQL_SEL(16);
     }
     else
-      st = x_is_f32 ? launch_dql<8, true, 512>(t, apr, x, m, kp, kd, round_w, gelu, xnorm, s)
-                    : launch_dql<8, false, 512>(t, apr, x, m, kp, kd, round_w, gelu, xnorm, s);
+      st = PLX_DQL_SEL(8);
+#undef PLX_DQL_SEL
   }
   return st;
 }

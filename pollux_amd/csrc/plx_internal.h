@@ -57,6 +57,7 @@ struct DeviceTables {
   uint32_t *kp_dot = nullptr;        // [kCodebook][4] words: kp_dq's 3 words, then kp_gemv's (type | pos << 8)
   uint32_t *pl_ids = nullptr;        // [n_planes] value-id word (kp_dq's format) of each distinct plane
   uint16_t *code_planes = nullptr;   // [kCodebook][4] the plane-layout record of each code (3 used)
+  uint32_t *pl_nib = nullptr;        // [n_planes] the same planes as kp_gemv words: 8 signed 4-bit coordinates
 };
 
 // Plane tables (tables.cpp; host, built once): the codebook rows take only a

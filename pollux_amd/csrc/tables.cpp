@@ -28,7 +28,9 @@
 //                as in kp_gemv (3,144,976 B).
 // pl_ids         the value-id words of the 4,961 distinct 8-coordinate planes
 //                of the codebook rows (19,844 B: staged in LDS by the kernels
-//                that read the plane layout), and
+//                that read the plane layout),
+// pl_nib         the same planes as kp_gemv coordinate words (8 signed 4-bit
+//                fields, 19,844 B), for the fp32 dequant-linear kernel, and
 // code_planes    per code its 3 plane-layout records (plx_internal.h), for
 //                plx_h24_plane_layout (1,572,488 B).
 
@@ -181,11 +183,19 @@ int build(int dev, DeviceTables *t) {
     for (int p = 0; p < 3; ++p) sw_dq[i * 3 + p] = dq[static_cast<size_t>(sweep[i]) * 3 + p];
 
   void *dt = nullptr, *drt = nullptr, *dsq = nullptr, *dsi = nullptr, *dsa = nullptr, *dr = nullptr, *dg = nullptr,
-       *dd = nullptr, *dk = nullptr, *dpi = nullptr, *dcp = nullptr;
+       *dd = nullptr, *dk = nullptr, *dpi = nullptr, *dcp = nullptr, *dpn = nullptr;
   const PlaneTables *pt = plane_tables_host();
   if (!pt) return fail(PLX_EINVAL, "the codebook rows take more than %d distinct planes", kMaxPlanes);
   std::vector<uint32_t> pl_pad(pt->ids);  // whole 16-byte vectors (the kernels stage it by uint4)
   pl_pad.resize((pl_pad.size() + 3) & ~static_cast<size_t>(3), 0u);
+  // value id -> raw value (kId's inverse), then the plane's coordinates as signed nibbles
+  static const int kIdValue[8] = {0, 1, 2, 4, -4, -3, -2, -1};
+  std::vector<uint32_t> pl_nib(pl_pad.size(), 0u);
+  for (size_t k = 0; k < pt->ids.size(); ++k)
+    for (int w = 0; w < 8; ++w) {
+      const uint32_t id = (pt->ids[k] >> (8 * (w % 4) + 4 * (w / 4))) & 0xFu;
+      pl_nib[k] |= (static_cast<uint32_t>(kIdValue[id & 7u]) & 0xFu) << (4 * w);
+    }
   const Upload ups[] = {
       {tiles.data(), tiles.size() * 2, &dt},
       {raw_tiles.data(), raw_tiles.size() * 2, &drt},
@@ -198,6 +208,7 @@ int build(int dev, DeviceTables *t) {
       {dot.data(), dot.size() * 4, &dk},
       {pl_pad.data(), pl_pad.size() * 4, &dpi},
       {pt->code_planes.data(), pt->code_planes.size() * 2, &dcp},
+      {pl_nib.data(), pl_nib.size() * 4, &dpn},
   };
   int st = PLX_OK;
   for (const Upload &u : ups) {
@@ -225,6 +236,7 @@ int build(int dev, DeviceTables *t) {
   t->kp_dot = static_cast<uint32_t *>(dk);
   t->pl_ids = static_cast<uint32_t *>(dpi);
   t->code_planes = static_cast<uint16_t *>(dcp);
+  t->pl_nib = static_cast<uint32_t *>(dpn);
   t->device = dev;
   return PLX_OK;
 }

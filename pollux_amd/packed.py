@@ -65,10 +65,10 @@ def h24_plane_layout(packed: torch.Tensor, n_atoms: int) -> torch.Tensor:
     return out
 
 
-def plane_layout_takes(m: int, x_dtype: torch.dtype, in_features: int) -> bool:
-    """Whether dequant_linear runs a batch of m tokens from the plane layout: one token of bf16 x
-    with rows of at most 320 atoms, or more than 4 tokens (the GEMM)."""
-    return m > 4 or (m == 1 and x_dtype == torch.bfloat16 and in_features // 24 <= 320)
+def plane_layout_takes(m: int, in_features: int) -> bool:
+    """Whether the dequant-linear kernels run a batch of m tokens from the plane layout: one token
+    with rows of at most 320 atoms (the GEMVs), or more than 4 tokens (the GEMM)."""
+    return m > 4 or (m == 1 and in_features // 24 <= 320)
 
 
 def dequant_linear(
@@ -108,7 +108,7 @@ def dequant_linear(
     y = torch.empty((xx.shape[0], out_features), dtype=torch.float32, device=pk.device)
     flags = (DQL_X_F32 if xx.dtype == torch.float32 else 0) | (DQL_W_AS_X if weight_rounding == "as_x" else 0)
     src, nsrc = pk, pk.numel()
-    if planes is not None and plane_layout_takes(xx.shape[0], xx.dtype, in_features):
+    if planes is not None and plane_layout_takes(xx.shape[0], in_features):
         n_atoms = out_features * (in_features // 24)
         if planes.dtype != torch.int16 or planes.numel() != 3 * n_atoms or planes.device != pk.device:
             raise ValueError("planes must be the weight's int16 plane layout (h24_plane_layout) on its device")
@@ -132,7 +132,7 @@ def dequant_linear(
 def dequant_linear_multi(
     weights: list[tuple[torch.Tensor, torch.Tensor, int]], in_features: int, x: torch.Tensor, *,
     residuals: list[torch.Tensor | None] | None = None, gelu: bool = False, weight_rounding: str = "exact",
-    norm: tuple[torch.Tensor, float] | None = None,
+    norm: tuple[torch.Tensor, float] | None = None, planes: list[torch.Tensor] | None = None,
 ) -> list[torch.Tensor]:
     """Several packed weights sharing x in one call: [residual_i +] act(n(x) @ W_i.T), fp32 [..., out_i] each.
 
@@ -142,11 +142,15 @@ def dequant_linear_multi(
     RMSNorm applied to x first (fp32 x; n = identity when None).  At up to 4
     tokens, four targets share one GEMV launch, which also normalises x.
     Results equal separate dequant_linear calls followed by the same epilogue.
+    ``planes``: each weight's h24_plane_layout, read for the batches
+    plane_layout_takes names (same results), else the packed streams.
     """
     if weight_rounding not in ("exact", "as_x"):
         raise ValueError(f"weight_rounding must be 'exact' or 'as_x', got {weight_rounding!r}")
     if not 1 <= len(weights) <= 16:
         raise ValueError("dequant_linear_multi takes 1..16 weights")
+    if planes is not None and len(planes) != len(weights):
+        raise ValueError("planes: one plane layout per weight")
     assert_row_aligned_in_features(in_features)
     if x.shape[-1] != in_features:
         raise ValueError(f"x has {x.shape[-1]} features, layer expects {in_features}")
@@ -159,6 +163,7 @@ def dequant_linear_multi(
         xx = xx.clone()
     _lib.require_device(xx, "dequant_linear_multi x")
     m = xx.shape[0]
+    use_planes = planes is not None and plane_layout_takes(m, in_features)
     residuals = residuals or [None] * len(weights)
     arr = (_lib.DqlTarget * len(weights))()
     ys, keep = [], []
@@ -172,6 +177,13 @@ def dequant_linear_multi(
         sg = sg.reshape(-1).contiguous()
         if sg.numel() != out_f or pk.numel() != ((out_f * in_features // 24 + 3) // 4) * 9:
             raise ValueError(f"target {i}: packed / sigma sizes do not match [{out_f}, {in_features}]")
+        if use_planes:
+            pl = planes[i]
+            if pl.dtype != torch.int16 or pl.numel() != 3 * out_f * (in_features // 24) or pl.device != pk.device:
+                raise ValueError(f"target {i}: planes must be the weight's int16 plane layout on its device")
+            pk = pl.reshape(-1).contiguous()
+            if pk.data_ptr() % 16:
+                pk = pk.clone()
         y = torch.empty((m, out_f), dtype=torch.float32, device=xx.device)
         r = residuals[i]
         if r is not None:
@@ -182,7 +194,7 @@ def dequant_linear_multi(
         keep += [pk, sg, r]
         ys.append(y)
     flags = (DQL_X_F32 if xx.dtype == torch.float32 else 0) | (DQL_W_AS_X if weight_rounding == "as_x" else 0) | (
-        DQL_GELU if gelu else 0)
+        DQL_GELU if gelu else 0) | (DQL_PLANES if use_planes else 0)
     nw, eps = None, 0.0
     if norm is not None:
         nw, eps = norm[0].detach(), float(norm[1])
@@ -236,6 +248,19 @@ def _fused_group(layers: list) -> tuple[torch.Tensor, torch.Tensor, int, list[in
     return fused
 
 
+def _stacked_planes(layers: list, planes: list[torch.Tensor]) -> torch.Tensor:
+    """The layers' plane layouts stacked along their output rows (records concatenate atom for atom),
+    kept on the first layer while the same layout tensors are passed (each layer rebuilds its own
+    layout when its packed buffer changes, which gives a new tensor here)."""
+    hit = layers[0].__dict__.get("_stacked_planes")
+    if hit is not None and len(hit[0]) == len(planes) and all(a is b for a, b in zip(hit[0], planes)):
+        return hit[1]
+    stacked = torch.cat([p.reshape(-1) for p in planes])
+    if not _capturing():
+        layers[0].__dict__["_stacked_planes"] = (tuple(planes), stacked)
+    return stacked
+
+
 def packed_linear_group(layers: list, x: torch.Tensor, *, residuals: list | None = None,
                         gelu: bool = False, norm: tuple[torch.Tensor, float] | None = None) -> list[torch.Tensor]:
     """[residual +] act(layer(n(x))) for PackedH24Linear layers sharing x, fused when they are all packed.
@@ -248,18 +273,25 @@ def packed_linear_group(layers: list, x: torch.Tensor, *, residuals: list | None
     residuals = residuals or [None] * len(layers)
     if all(isinstance(l, PackedH24Linear) and not l._materialized and l.bias is None for l in layers):
         in_f = layers[0].in_features
-        if (len(layers) > 1 and x.numel() // max(in_f, 1) > 4 and all(r is None for r in residuals)
+        m = x.numel() // max(in_f, 1)
+        planes = None
+        if all(l.use_plane_layout and l.in_features == in_f for l in layers) and plane_layout_takes(m, in_f):
+            planes = [l.plane_layout() for l in layers]
+            if any(p is None for p in planes):  # under graph capture without built layouts
+                planes = None
+        if (len(layers) > 1 and m > 4 and all(r is None for r in residuals)
                 and all(l.in_features == in_f and (l.out_features * in_f // 24) % 4 == 0 for l in layers)
                 and len({l.weight_rounding for l in layers}) == 1):
             # above 4 tokens the weights run as separate GEMM launches: one stacked weight takes one
             packed, sigma, rows, offs = _fused_group(layers)
+            stacked_planes = None if planes is None else [_stacked_planes(layers, planes)]
             (y,) = dequant_linear_multi([(packed, sigma, rows)], in_f, x, gelu=gelu,
-                                        weight_rounding=layers[0].weight_rounding, norm=norm)
+                                        weight_rounding=layers[0].weight_rounding, norm=norm, planes=stacked_planes)
             y = y.to(x.dtype)
             return [y[..., o:o + l.out_features] for l, o in zip(layers, offs)]
         ys = dequant_linear_multi([(l.packed_weights, l.sigma_rows, l.out_features) for l in layers],
                                   layers[0].in_features, x, residuals=residuals, gelu=gelu,
-                                  weight_rounding=layers[0].weight_rounding, norm=norm)
+                                  weight_rounding=layers[0].weight_rounding, norm=norm, planes=planes)
         return [y.to(x.dtype) for y in ys]
     if norm is not None:
         x = x * torch.rsqrt(x.pow(2).mean(dim=-1, keepdim=True) + norm[1]) * norm[0]
@@ -335,7 +367,7 @@ class PackedH24Linear(nn.Module):
             # fused path: weights stay packed (0.76 bits/param); fp32 result cast to x's dtype.  The batches
             # plane_layout_takes names run from the plane layout (6 B per atom, built once).
             m = x.numel() // self.in_features if self.in_features else 0
-            takes = self.use_plane_layout and plane_layout_takes(m, x.dtype, self.in_features)
+            takes = self.use_plane_layout and plane_layout_takes(m, self.in_features)
             planes = self.plane_layout() if takes else None
             y = dequant_linear(self.packed_weights, self.sigma_rows, self.out_features, self.in_features, x,
                                weight_rounding=self.weight_rounding, planes=planes).to(x.dtype)

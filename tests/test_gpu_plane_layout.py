@@ -193,3 +193,60 @@ def test_graph_captured_before_any_eager_call(dev):
         assert close(y_single, refs[0])
         assert all(close(a, r) for a, r in zip(y_group, refs))
         assert close(layers[1](xd), refs[1])  # eager work between the replays
+
+
+# one token through the multi-target kernel (q/k/v-style groups, the norm prologue, GELU and residual
+# epilogues, fp32 and bf16 x) from the plane layouts: the same results as from the packed streams, bit
+# for bit; rows of 2, 7, 48, 80 and 320 atoms (8, 16, 32 and 64 lanes per row), ragged row counts
+@pytest.mark.parametrize("shapes,in_f", [([(96, 1152)] * 3, 1152), ([(37, 48), (5, 48)], 48), ([(130, 168)], 168),
+                                         ([(1920, 1920)] * 3, 1920), ([(7680, 1920)], 1920), ([(1920, 7680)], 7680)])
+@pytest.mark.parametrize("variant", ["fp32_norm", "fp32_gelu", "fp32_residual", "bf16_plain", "bf16_as_x"])
+def test_multi_target_one_token_from_layout(dev, shapes, in_f, variant):
+    from pollux_amd.packed import dequant_linear_multi
+
+    g = torch.Generator().manual_seed(len(shapes) * 1000 + in_f)
+    weights, planes, w16s = [], [], []
+    for k, (out_f, _) in enumerate(shapes):
+        idx, sig, packed, _ = _layer(out_f, in_f, 7 * k + in_f)
+        pk, sg = packed.to(dev), sig.to(dev)
+        weights.append((pk, sg, out_f))
+        planes.append(h24_plane_layout(pk, out_f * in_f // 24))
+        w16s.append(torch_ref.materialize(idx, sig, out_f, in_f))
+    dtype = torch.bfloat16 if variant.startswith("bf16") else torch.float32
+    x = (torch.randn(1, in_f, generator=g) * 2.0).to(dtype).to(dev)
+    kw = {}
+    if variant == "fp32_norm":
+        kw["norm"] = ((1.0 + 0.1 * torch.randn(in_f, generator=g)).to(dev), 1e-5)
+    elif variant == "fp32_gelu":
+        kw["gelu"] = True
+    elif variant == "fp32_residual":
+        kw["residuals"] = [torch.randn(1, o, generator=g).to(dev) for o, _ in shapes]
+    elif variant == "bf16_as_x":
+        kw["weight_rounding"] = "as_x"
+    y_pl = dequant_linear_multi(weights, in_f, x, planes=planes, **kw)
+    y_pk = dequant_linear_multi(weights, in_f, x, **kw)
+    print(f"[planes multi] {shapes[0]} x{len(shapes)} {variant}", flush=True)
+    for a, b in zip(y_pl, y_pk):
+        assert torch.equal(a, b)
+    if variant in ("bf16_plain", "bf16_as_x"):
+        for y, w16 in zip(y_pl, w16s):
+            _check(y.cpu(), x.cpu(), w16, "exact" if variant == "bf16_plain" else "as_x")
+
+
+def test_multi_target_layout_refused_for_long_rows(dev):
+    # rows of more than 320 atoms at one token read the packed stream: the C-ABI refuses the flag
+    out_f, in_f = 8, 7704
+    idx, sig, packed, g = _layer(out_f, in_f, 9)
+    pk, sg = packed.to(dev), sig.to(dev)
+    planes = h24_plane_layout(pk, out_f * in_f // 24)
+    x = torch.randn(1, in_f, generator=g).to(dev)
+    y = torch.empty(1, out_f, device=dev)
+    arr = (_lib.DqlTarget * 1)()
+    arr[0] = _lib.DqlTarget(planes.data_ptr(), sg.data_ptr(), out_f, y.data_ptr(), None)
+    st = _lib.lib().plx_dequant_linear_multi(arr, 1, in_f, x.data_ptr(), 1 | DQL_PLANES, 1, None, 0.0, None, 0,
+                                             _lib.stream_of(dev))
+    assert st == _lib.PLX_EINVAL
+    from pollux_amd.packed import dequant_linear_multi
+    (y2,) = dequant_linear_multi([(pk, sg, out_f)], in_f, x, planes=[planes])  # falls back to the packed stream
+    assert ((y2.cpu().double() - torch_ref.linear_fp32(x.cpu(), torch_ref.materialize(idx, sig, out_f, in_f)).double())
+            .norm() / y2.cpu().double().norm()).item() <= REL_L2
