@@ -828,9 +828,11 @@ int launch_gemv1_planes_l(const uint8_t *planes, const uint16_t *sigma16, int64_
 int launch_gemv1_planes(const uint8_t *planes, const uint16_t *sigma16, int64_t rows, int64_t apr, const void *x,
                         const DeviceTables *tab, int round_w, float *y, hipStream_t s) {
   if (apr >= 160) return launch_gemv1_planes_l<64>(planes, sigma16, rows, apr, x, tab, round_w, y, s);
+  // 16 lanes (32 rows per block) only while the block's records fit its 2 vectors per thread
   if (apr >= 16)
-    return (rows + 31) / 32 < 192 ? launch_gemv1_planes_l<32>(planes, sigma16, rows, apr, x, tab, round_w, y, s)
-                                  : launch_gemv1_planes_l<16>(planes, sigma16, rows, apr, x, tab, round_w, y, s);
+    return (rows + 31) / 32 < 192 || 6 * 32 * apr + 31 > 16 * 2 * 512
+               ? launch_gemv1_planes_l<32>(planes, sigma16, rows, apr, x, tab, round_w, y, s)
+               : launch_gemv1_planes_l<16>(planes, sigma16, rows, apr, x, tab, round_w, y, s);
   return launch_gemv1_planes_l<8>(planes, sigma16, rows, apr, x, tab, round_w, y, s);
 }
 
@@ -1697,7 +1699,8 @@ int launch_dequant_linear_multi(const DqlTarget *targets, int n, int64_t cols, c
       // 32 lanes per row (16 rows per block) when 16 would leave the grid under 192 blocks
       int64_t mrows = 0;
       for (int i = 0; i < t.n; ++i) mrows = t.rows[i] > mrows ? t.rows[i] : mrows;
-      if ((mrows + 31) / 32 * t.n < 192)
+      // (the plane layout: 16 lanes only while a block's records fit its stage)
+      if ((mrows + 31) / 32 * t.n < 192 || (planes && 6 * 32 * apr + 31 > 16 * kDqlPlVecs * 512))
         st = PLX_DQL_SEL(32);
       else
         st = PLX_DQL_SEL(16);

@@ -6,9 +6,11 @@ read as the origin) is laid out and decoded back through the host plane table
 and the extra bits the code's type (from its count of non-zero coordinates)
 and the position of its -3, both taken from the oracle rows.
 Dequant-linear from the layout: the same kernels as from the packed stream
-after the decode, so the results must equal the packed path's bit for bit, and
-both must meet the tolerance of the fused dequant-linear against the oracle
-(relative L2 <= 1e-5, per element <= 1e-5 * sum_i |x_i W_i|).
+after the decode, so the results must equal the packed path's bit for bit
+where both run the same lane layout (rows of more than 80 atoms at one token
+may take another, summing in another order), and both must meet the
+tolerance of the fused dequant-linear against the oracle (relative L2 <=
+1e-5, per element <= 1e-5 * sum_i |x_i W_i|).
 """
 
 import numpy as np
@@ -88,7 +90,8 @@ def _check(y, x, w16, mode):
 @pytest.mark.parametrize("shape,m,dtype", [
     ((24, 24), 1, torch.bfloat16), ((37, 48), 1, torch.bfloat16), ((33, 240), 1, torch.bfloat16),
     ((1152, 1152), 1, torch.bfloat16), ((7, 1176), 1, torch.bfloat16), ((100, 4608), 1, torch.bfloat16),
-    ((130, 7680), 1, torch.bfloat16), ((7680, 1920), 1, torch.bfloat16),
+    ((130, 7680), 1, torch.bfloat16), ((7680, 1920), 1, torch.bfloat16), ((6200, 2304), 1, torch.bfloat16),
+    ((6200, 3816), 1, torch.bfloat16), ((6200, 2304), 1, torch.float32),
     ((1152, 1152), 17, torch.bfloat16), ((37, 1920), 33, torch.bfloat16), ((20, 240), 64, torch.bfloat16),
     ((7680, 1920), 64, torch.bfloat16), ((1920, 7680), 64, torch.bfloat16), ((100, 4608), 5, torch.float32),
     ((37, 48), 40, torch.float32), ((1152, 1152), 100, torch.float32),
@@ -105,9 +108,15 @@ def test_dequant_linear_from_layout(dev, shape, m, dtype, mode):
     planes = h24_plane_layout(pk, out_f * in_f // 24)
     y_pl = dequant_linear(pk, sg, out_f, in_f, xd, weight_rounding=mode, planes=planes).cpu()
     y_pk = dequant_linear(pk, sg, out_f, in_f, xd, weight_rounding=mode).cpu()
-    print(f"[planes] {shape} m={m} {dtype} {mode}", flush=True)
-    assert torch.equal(y_pl, y_pk)
-    _check(y_pl, x, torch_ref.materialize(idx, sig, out_f, in_f), mode)
+    same = torch.equal(y_pl, y_pk)
+    print(f"[planes] {shape} m={m} {dtype} {mode}: equal to the packed path: {same}", flush=True)
+    w16 = torch_ref.materialize(idx, sig, out_f, in_f)
+    _check(y_pl, x, w16, mode)
+    if not same:
+        # rows that the packed stream runs with another lane layout (e.g. more than 80 atoms at 16 lanes)
+        # sum in another order: both must then meet the tolerance
+        assert in_f // 24 > 80
+        _check(y_pk, x, w16, mode)
 
 
 def test_layout_refused_where_no_kernel_reads_it(dev):
@@ -199,7 +208,8 @@ def test_graph_captured_before_any_eager_call(dev):
 # epilogues, fp32 and bf16 x) from the plane layouts: the same results as from the packed streams, bit
 # for bit; rows of 2, 7, 48, 80 and 320 atoms (8, 16, 32 and 64 lanes per row), ragged row counts
 @pytest.mark.parametrize("shapes,in_f", [([(96, 1152)] * 3, 1152), ([(37, 48), (5, 48)], 48), ([(130, 168)], 168),
-                                         ([(1920, 1920)] * 3, 1920), ([(7680, 1920)], 1920), ([(1920, 7680)], 7680)])
+                                         ([(1920, 1920)] * 3, 1920), ([(7680, 1920)], 1920), ([(1920, 7680)], 7680),
+                                         ([(6200, 2304)], 2304), ([(3200, 3816)] * 2, 3816)])
 @pytest.mark.parametrize("variant", ["fp32_norm", "fp32_gelu", "fp32_residual", "bf16_plain", "bf16_as_x"])
 def test_multi_target_one_token_from_layout(dev, shapes, in_f, variant):
     from pollux_amd.packed import dequant_linear_multi
@@ -225,9 +235,19 @@ def test_multi_target_one_token_from_layout(dev, shapes, in_f, variant):
         kw["weight_rounding"] = "as_x"
     y_pl = dequant_linear_multi(weights, in_f, x, planes=planes, **kw)
     y_pk = dequant_linear_multi(weights, in_f, x, **kw)
-    print(f"[planes multi] {shapes[0]} x{len(shapes)} {variant}", flush=True)
-    for a, b in zip(y_pl, y_pk):
-        assert torch.equal(a, b)
+    same = all(torch.equal(a, b) for a, b in zip(y_pl, y_pk))
+    print(f"[planes multi] {shapes[0]} x{len(shapes)} {variant}: equal to the packed path: {same}", flush=True)
+    if not same:
+        # another lane layout for these rows (more than 80 atoms at 16 lanes): another summation order, so
+        # the two results differ by at most twice the per-element bound (GELU's slope is below 1.13)
+        assert in_f // 24 > 80
+        xn = x.float().cpu()
+        if "norm" in kw:
+            nw = kw["norm"][0].cpu()
+            xn = xn * torch.rsqrt(xn.pow(2).mean(-1, keepdim=True) + kw["norm"][1]) * nw
+        for a, b, w16 in zip(y_pl, y_pk, w16s):
+            bound = 2.3 * ELEM * (xn.double().abs() @ w16.double().abs().t())
+            assert ((a.cpu().double() - b.cpu().double()).abs() <= bound).all()
     if variant in ("bf16_plain", "bf16_as_x"):
         for y, w16 in zip(y_pl, w16s):
             _check(y.cpu(), x.cpu(), w16, "exact" if variant == "bf16_plain" else "as_x")
