@@ -861,6 +861,9 @@ int launch_dql(DqlTargets t, int64_t apr, const void *x, int64_t m, const uint4 
   if (PL && (m != 1 || (6 * R * apr + 31) / 16 > kDqlPlVecs * 512 || pl_vecs > kDqlPlTableVecs))
     return fail(PLX_EINVAL, "dequant_linear: the plane layout takes one token and rows of at most %d atoms here",
                 kDqlPlVecs * 512 * 16 / (6 * R) - 1);
+  for (int i = 0; PL && i < t.n; ++i)  // 32-bit buffer offsets
+    if (t.packed_bytes[i] >= (static_cast<int64_t>(1) << 30))
+      return fail(PLX_EINVAL, "dequant_linear: plane layouts of 2^30 bytes or more are not read at one token");
   if (shm > (PL ? 96 : 64) * 1024)
     return fail(PLX_EINVAL, "dequant_linear: rows of %lld atoms are too long", static_cast<long long>(apr));
   // x through registers: one pass over all tokens, at most one 8-value piece per thread

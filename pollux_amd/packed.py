@@ -67,7 +67,8 @@ def h24_plane_layout(packed: torch.Tensor, n_atoms: int) -> torch.Tensor:
 
 def plane_layout_takes(m: int, in_features: int) -> bool:
     """Whether the dequant-linear kernels run a batch of m tokens from the plane layout: one token
-    with rows of at most 320 atoms (the GEMVs), or more than 4 tokens (the GEMM)."""
+    with rows of at most 320 atoms (the GEMVs), or more than 4 tokens (the GEMM); layouts of 2^30
+    bytes or more are not read (their kernels index them with 32-bit offsets)."""
     return m > 4 or (m == 1 and in_features // 24 <= 320)
 
 
@@ -108,8 +109,8 @@ def dequant_linear(
     y = torch.empty((xx.shape[0], out_features), dtype=torch.float32, device=pk.device)
     flags = (DQL_X_F32 if xx.dtype == torch.float32 else 0) | (DQL_W_AS_X if weight_rounding == "as_x" else 0)
     src, nsrc = pk, pk.numel()
-    if planes is not None and plane_layout_takes(xx.shape[0], in_features):
-        n_atoms = out_features * (in_features // 24)
+    n_atoms = out_features * (in_features // 24)
+    if planes is not None and plane_layout_takes(xx.shape[0], in_features) and 6 * n_atoms < 1 << 30:
         if planes.dtype != torch.int16 or planes.numel() != 3 * n_atoms or planes.device != pk.device:
             raise ValueError("planes must be the weight's int16 plane layout (h24_plane_layout) on its device")
         src = planes.contiguous()
@@ -163,7 +164,8 @@ def dequant_linear_multi(
         xx = xx.clone()
     _lib.require_device(xx, "dequant_linear_multi x")
     m = xx.shape[0]
-    use_planes = planes is not None and plane_layout_takes(m, in_features)
+    use_planes = (planes is not None and plane_layout_takes(m, in_features)
+                  and all(6 * out_f * (in_features // 24) < 1 << 30 for _, _, out_f in weights))
     residuals = residuals or [None] * len(weights)
     arr = (_lib.DqlTarget * len(weights))()
     ys, keep = [], []
