@@ -230,10 +230,12 @@ int plx_dequant_f16(const uint8_t *packed, int64_t n_packed_bytes, const uint16_
  * the -3 position).  Kernels decode a code from a table they keep in LDS
  * instead of gathering from the 3 MB per-code tables, so a packed layer built
  * once into this layout (6 B per atom next to its 2.25 B packed stream) runs
- * its dequant-linear without per-atom gathers.  packed: ((n_atoms+3)/4)*9
- * bytes (indices above 196,560 map to the origin); planes: [3*n_atoms].
+ * its dequant-linear without per-atom gathers.  packed: n_packed_bytes =
+ * ((n_atoms+3)/4)*9 bytes (indices above 196,560 map to the origin); planes:
+ * [3*n_atoms].
  * No counterpart in the reference (a derived layout of its packed buffers). */
-int plx_h24_plane_layout(const uint8_t *packed, int64_t n_atoms, uint16_t *planes, void *stream);
+int plx_h24_plane_layout(const uint8_t *packed, int64_t n_packed_bytes, int64_t n_atoms, uint16_t *planes,
+                         void *stream);
 /* Host copy of the plane table: value-id words (kp_dq order: byte i = id of
  * coordinate i | id of coordinate 4+i << 4, ids 0..7 = raw values
  * {0,1,2,4,-4,-3,-2,-1}), ascending.  Returns the number of planes; copies at

@@ -47,7 +47,7 @@ SIGNATURES = {
     "plx_dequant_f16": (_int, [_vp, _i64, _vp, _i64, _i64, _vp, _vp]),
     "plx_dequant_linear_workspace_bytes": (_sz, [_i64, _i64, _i64, _int]),
     "plx_dequant_linear": (_int, [_vp, _i64, _vp, _i64, _i64, _vp, _int, _i64, _vp, _vp, _sz, _vp]),
-    "plx_h24_plane_layout": (_int, [_vp, _i64, _vp, _vp]),
+    "plx_h24_plane_layout": (_int, [_vp, _i64, _i64, _vp, _vp]),
     "plx_plane_table": (_i64, [_vp, _i64]),
     "plx_dequant_linear_multi_workspace_bytes": (_sz, [_vp, _int, _i64, _i64, _int]),
     "plx_dequant_linear_multi": (_int, [_vp, _int, _i64, _vp, _int, _i64, _vp, ctypes.c_float, _vp, _sz, _vp]),

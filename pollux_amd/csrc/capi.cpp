@@ -373,8 +373,11 @@ int plx_dequant_linear(const uint8_t *packed, int64_t n_packed_bytes, const uint
                                as_stream(stream));
 }
 
-int plx_h24_plane_layout(const uint8_t *packed, int64_t n_atoms, uint16_t *planes, void *stream) {
+int plx_h24_plane_layout(const uint8_t *packed, int64_t n_packed_bytes, int64_t n_atoms, uint16_t *planes,
+                         void *stream) {
   PLX_REQUIRE(n_atoms >= 0, "plx_h24_plane_layout: negative atom count");
+  PLX_REQUIRE(n_packed_bytes == ((n_atoms + 3) / 4) * 9, "plx_h24_plane_layout: packed length %lld does not match %lld atoms",
+              static_cast<long long>(n_packed_bytes), static_cast<long long>(n_atoms));
   if (n_atoms == 0) return PLX_OK;
   PLX_REQUIRE(packed != nullptr && planes != nullptr, "plx_h24_plane_layout: null pointer");
   return launch_plane_layout(packed, n_atoms, planes, as_stream(stream));

@@ -60,7 +60,8 @@ def h24_plane_layout(packed: torch.Tensor, n_atoms: int) -> torch.Tensor:
     out = torch.empty(3 * n_atoms, dtype=torch.int16, device=pk.device)
     if n_atoms:
         with torch.cuda.device(pk.device):
-            st = _lib.lib().plx_h24_plane_layout(_lib.ptr(pk), n_atoms, _lib.ptr(out), _lib.stream_of(pk.device))
+            st = _lib.lib().plx_h24_plane_layout(_lib.ptr(pk), pk.numel(), n_atoms, _lib.ptr(out),
+                                                 _lib.stream_of(pk.device))
         _lib.check(st, "h24_plane_layout")
     return out
 

@@ -69,6 +69,11 @@ def test_validation_happens_before_device_work():
     # zero-sized work is a no-op success
     assert lib.plx_pack_indices(None, 1, 0, None, None) == _lib.PLX_OK
     assert lib.plx_quantize_workspace_bytes(1000) >= 8000
+    # plane layout: the packed length must match the atom count; the flag's batch sizes
+    assert lib.plx_h24_plane_layout(None, 18, 9, None, None) == _lib.PLX_EINVAL
+    assert lib.plx_h24_plane_layout(None, 0, 0, None, None) == _lib.PLX_OK
+    assert lib.plx_dequant_linear(None, 6 * 80, None, 40, 48, None, 16, 3, None, None, 0, None) == _lib.PLX_EINVAL
+    assert b"plane layout" in lib.plx_last_error()
 
 
 def test_host_helpers_mirror_reference():

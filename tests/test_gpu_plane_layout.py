@@ -64,7 +64,9 @@ def test_layout_argument_checks(dev):
     with pytest.raises(ValueError):
         h24_plane_layout(packed, 9)  # 18 bytes hold 5..8 atoms
     lib = _lib.lib()
-    assert lib.plx_h24_plane_layout(None, -1, None, None) == _lib.PLX_EINVAL
+    assert lib.plx_h24_plane_layout(None, 0, -1, None, None) == _lib.PLX_EINVAL
+    assert lib.plx_h24_plane_layout(None, 18, 9, None, None) == _lib.PLX_EINVAL  # 9 atoms take 27 bytes
+    assert b"does not match" in lib.plx_last_error()
     assert h24_plane_layout(torch.zeros(0, dtype=torch.uint8, device=dev), 0).numel() == 0
 
 
