@@ -264,7 +264,7 @@ using DqlArgs = typename std::conditional<GEN, DqlTargets, DqlOne>::type;
 // rounds, 2% slower at one token; 8: wasted slots, 11% slower)
 constexpr int kDqlGather = 5;
 constexpr int kDqlPlVecs = 2;          // PL: record vectors per thread at 512 threads (16 KB per block)
-constexpr int kDqlPlTableVecs = 1536;  // PL: plane-table capacity in 16-byte vectors (24 KB)
+constexpr int kDqlPlTableVecs = 1536;  // PL: plane-table capacity in 16-byte vectors (24 KB; lookups clamped to it)
 
 // GEN: several targets and the epilogue (DqlTargets); else one target, no epilogue (DqlOne).
 // XREG (with XL, m_total <= MB and MB token rows of at most 8 * NT values): x
@@ -527,7 +527,9 @@ __global__ __launch_bounds__(NT) void dqlinear_kernel(const DqlArgs<GEN> targets
             const uint16_t *rp = reinterpret_cast<const uint16_t *>(pb + 6 * (nbase + min(a, apr32 - 1)));
             const uint32_t r0 = rp[0], r1 = rp[1], r2 = rp[2];
             const uint32_t pos = ((r1 >> 13) & 7u) | ((r2 >> 13) & 3u) << 3;
-            e[i] = make_uint4(ptab[r0 & 0x1FFFu], ptab[r1 & 0x1FFFu], ptab[r2 & 0x1FFFu], ((r0 >> 13) & 3u) | pos << 8);
+            constexpr uint32_t kLast = TPT * NT * 4 - 1;  // clamped to the staged table (any layout stays inside)
+            e[i] = make_uint4(ptab[min(r0 & 0x1FFFu, kLast)], ptab[min(r1 & 0x1FFFu, kLast)],
+                              ptab[min(r2 & 0x1FFFu, kLast)], ((r0 >> 13) & 3u) | pos << 8);
             continue;
           }
           int32_t code = 0;
@@ -645,7 +647,7 @@ __global__ __launch_bounds__(512) void dqgemv1_kernel(const uint8_t *__restrict_
                                                       float *__restrict__ y) {
   constexpr int NT = 512, R = NT / L, G = kG1Atoms;
   constexpr int VPT = PL ? 2 : 1;   // staged 16-byte vectors of the block's atom bytes per thread
-  constexpr int TPT = 3;            // PL: plane-table vectors per thread (the host checks pl_vecs <= TPT * NT)
+  constexpr int TPT = 3;  // PL: plane-table vectors per thread (the host checks pl_vecs <= TPT * NT; lookups clamped to them)
   typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
   extern __shared__ __align__(16) uint8_t smem[];
   const int tid = threadIdx.x;
@@ -726,7 +728,10 @@ __global__ __launch_bounds__(512) void dqgemv1_kernel(const uint8_t *__restrict_
       const bool in = sub + i * L < apr;
       const uint32_t type = in ? (r[i][0] >> 13) & 3u : 0u;
       const uint32_t pos = ((r[i][1] >> 13) & 7u) | ((r[i][2] >> 13) & 3u) << 3;
-      e[i] = make_uint4(ptab[r[i][0] & 0x1FFFu], ptab[r[i][1] & 0x1FFFu], ptab[r[i][2] & 0x1FFFu], type | pos << 8);
+      // (clamped to the staged table: a layout not made by plane_layout_kernel cannot index past it)
+      constexpr uint32_t kLast = TPT * NT * 4 - 1;
+      e[i] = make_uint4(ptab[min(r[i][0] & 0x1FFFu, kLast)], ptab[min(r[i][1] & 0x1FFFu, kLast)],
+                        ptab[min(r[i][2] & 0x1FFFu, kLast)], type | pos << 8);
     }
   } else {
     // round of LDS reads: the lane's atoms sub, sub + L, ... (clamped to the block's atoms), 3 bytes
@@ -1241,9 +1246,10 @@ __global__ __launch_bounds__(64 * WV, WV <= 4 ? 2 : 1) void dqmm_kernel(
         const int r = c / na, a = c - r * na;
         uint32_t *d = wt + r * ws + 3 * a;
         // the origin's plane (all ids 0) for rows and atoms past the weight: index 0 of the table
-        d[0] = ptab[rec[u][0] & 0x1FFFu];
-        d[1] = ptab[rec[u][1] & 0x1FFFu];
-        d[2] = ptab[rec[u][2] & 0x1FFFu];
+        // (clamped to the staged table: a layout not made by plane_layout_kernel cannot index past it)
+        d[0] = ptab[min(rec[u][0] & 0x1FFFu, static_cast<uint32_t>(TPT * NT * 4 - 1))];
+        d[1] = ptab[min(rec[u][1] & 0x1FFFu, static_cast<uint32_t>(TPT * NT * 4 - 1))];
+        d[2] = ptab[min(rec[u][2] & 0x1FFFu, static_cast<uint32_t>(TPT * NT * 4 - 1))];
       }
     }
   } else if ((atoms_per_row & 3) == 0) {

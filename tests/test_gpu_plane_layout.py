@@ -272,3 +272,23 @@ def test_multi_target_layout_refused_for_long_rows(dev):
     (y2,) = dequant_linear_multi([(pk, sg, out_f)], in_f, x, planes=[planes])  # falls back to the packed stream
     assert ((y2.cpu().double() - torch_ref.linear_fp32(x.cpu(), torch_ref.materialize(idx, sig, out_f, in_f)).double())
             .norm() / y2.cpu().double().norm()).item() <= REL_L2
+
+
+def test_any_layout_content_stays_inside_the_tables(dev):
+    # the kernels clamp plane indices to their staged table and the position bits stay inside the staged
+    # x, so a buffer of arbitrary records (not made by h24_plane_layout) gives finite output, no error
+    out_f, in_f = 96, 1920
+    idx, sig, packed, g = _layer(out_f, in_f, 50)
+    pk, sg = packed.to(dev), sig.to(dev)
+    junk = torch.randint(-32768, 32768, (3 * out_f * in_f // 24,), generator=g, dtype=torch.int32)
+    junk = junk.to(torch.int16).to(dev)
+    for m, dtype in ((1, torch.bfloat16), (1, torch.float32), (8, torch.bfloat16), (8, torch.float32)):
+        x = torch.randn(m, in_f, generator=g).to(dtype).to(dev)
+        y = dequant_linear(pk, sg, out_f, in_f, x, planes=junk)
+        torch.cuda.synchronize()
+        assert torch.isfinite(y).all()
+    from pollux_amd.packed import dequant_linear_multi
+    x = torch.randn(1, in_f, generator=g).to(dev)
+    ys = dequant_linear_multi([(pk, sg, out_f)] * 2, in_f, x, planes=[junk, junk], gelu=True)
+    torch.cuda.synchronize()
+    assert all(torch.isfinite(y).all() for y in ys)
