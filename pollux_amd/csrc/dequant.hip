@@ -1644,9 +1644,12 @@ int launch_dequant_linear_multi(const DqlTarget *targets, int n, int64_t cols, c
       st = m > 32 ? launch_dqmm<4>(t.packed, planes ? 6 * t.rows * apr : pb, t.sigma16, t.rows, apr, xf, m, t.y,
                                    part, pl, tab->kp_dq, planes ? tab->pl_ids : nullptr, pl_vecs, !round_w, x_is_f32,
                                    !copy, t.residual, gelu, s)
-                  : launch_dqmm<2>(t.packed, planes ? 6 * t.rows * apr : pb, t.sigma16, t.rows, apr, xf, m, t.y,
-                                   part, pl, tab->kp_dq, planes ? tab->pl_ids : nullptr, pl_vecs, !round_w, x_is_f32,
-                                   !copy, t.residual, gelu, s);
+                  : m > 16 ? launch_dqmm<2>(t.packed, planes ? 6 * t.rows * apr : pb, t.sigma16, t.rows, apr, xf, m,
+                                            t.y, part, pl, tab->kp_dq, planes ? tab->pl_ids : nullptr, pl_vecs,
+                                            !round_w, x_is_f32, !copy, t.residual, gelu, s)
+                           : launch_dqmm<1>(t.packed, planes ? 6 * t.rows * apr : pb, t.sigma16, t.rows, apr, xf, m,
+                                            t.y, part, pl, tab->kp_dq, planes ? tab->pl_ids : nullptr, pl_vecs,
+                                            !round_w, x_is_f32, !copy, t.residual, gelu, s);
       if (st != PLX_OK || pl.splits == 1) continue;
       const int64_t cnt = m * t.rows;
       if (t.rows % 4 == 0 && (reinterpret_cast<uintptr_t>(t.y) & 15u) == 0)
