@@ -252,8 +252,9 @@ size_t plx_dequant_linear_workspace_bytes(int64_t rows, int64_t cols, int64_t m_
  * the fp16 weights are exact and accumulated in fp32: the numerics of
  * F.linear(x.float(), W.float()).  With PLX_DQL_W_AS_X and bf16 x the weights
  * are rounded to bf16 (RNE) first; with PLX_DQL_GELU, y = gelu(x W^T) (torch's
- * erf form).  Results are deterministic (fixed summation order).  Batches above 4 tokens run on MFMA (fp32 x split exactly into
- * three bf16 parts) and need the workspace sized by
+ * erf form).  Results are deterministic (fixed summation order).  Batches
+ * above 4 tokens of fp32 x (split exactly into three bf16 parts) or above 2 of
+ * bf16 x run on MFMA and need the workspace sized by
  * plx_dequant_linear_workspace_bytes (a fragment-order copy of x, plus split
  * partial tiles for narrow layers); cols <= 2^22.
  * Replaces PackedH24Linear.forward after materialize (pollux.py:506-507:

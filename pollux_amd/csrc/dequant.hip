@@ -1544,11 +1544,13 @@ MmWorkspace mm_workspace(int64_t rows, int64_t cols, int64_t m, const MmPlan &pl
   return w;
 }
 
-// GEMV up to 4 tokens, MFMA GEMM above: the GEMV streams the packed rows and
-// repeats its codebook gathers once per 4 tokens, the GEMM's cost barely
-// changes between 5 and 64 tokens (measured per call: 7680x1920 GEMV 9.6 us at
-// 4 tokens, 13.9 at 6; GEMM 13.0 at 17; 1920x7680 16.6 / 23.7 against 16.0)
-bool uses_mfma(int /*flags*/, int64_t m) { return m > 4; }
+// GEMV up to 4 tokens of fp32 x and 2 of bf16 x, MFMA GEMM above: the GEMV
+// streams the packed rows and repeats its codebook gathers once per 4 tokens,
+// the GEMM's cost barely changes with the batch (measured per call, fp32 x:
+// 7680x1920 GEMV 9.6 us at 4 tokens, 13.9 at 6; GEMM 11.1 at 5 with one token
+// tile; bf16 x, 7680x1920 / 1920x7680: GEMV 6.3 / 8.3 at 2 tokens, 10.1 / 13.2
+// at 3, 9.0 / 11.5 at 4; GEMM 6.9 / 8.9 at each of 2-4)
+bool uses_mfma(int flags, int64_t m) { return m > ((flags & PLX_DQL_X_F32) ? 4 : 2); }
 
 }  // namespace
 
