@@ -302,28 +302,32 @@ int plx_rms_norm(const float *x, const float *w, float *y, int64_t rows, int64_t
 
 /* The attention of one new token per sequence (pollux.py:615-626 at the last
  * position).  q, k, v: fp32 [n, 24] projections of the new token, n = sequences
- * x heads; q_norm_w, k_norm_w: fp32 [24] (q_ln, k_ln weights); caches fp32
+ * x heads, or with qkv_stride > 0 each sequence's row of `heads` heads
+ * qkv_stride floats apart (q, k and v as column slices of one stacked
+ * projection); q_norm_w, k_norm_w: fp32 [24] (q_ln, k_ln weights); caches fp32
  * [n, max_len, 24] (16-byte aligned); *pos: the new token's position (device
  * int64).  Writes RMSNorm(k) and v at position *pos, then out fp32 [n, 24] =
  * softmax_{j <= pos}(RMSNorm(q) . K_j / sqrt 24) V_j.  A position outside
  * 0..max_len-1 writes nothing to the caches and sets out to NaN. */
-int plx_decode_attention(const float *q, const float *k, const float *v, const float *q_norm_w,
-                         const float *k_norm_w, float eps, float *k_cache, float *v_cache,
-                         const int64_t *pos, int64_t n, int64_t max_len, float *out, void *stream);
+int plx_decode_attention(const float *q, const float *k, const float *v, int64_t qkv_stride, const float *q_norm_w,
+                         const float *k_norm_w, float eps, float *k_cache, float *v_cache, const int64_t *pos,
+                         int64_t n, int64_t heads, int64_t max_len, float *out, void *stream);
 
 /* The attention of t new positions p0 .. p0+t-1 of each of b sequences (a
  * prompt's prefill over a cached prefix: pollux.py:615-626 with is_causal,
  * positions < p0 taken from the caches).  q, k, v, out: fp32 [b, t, heads,
- * 24] (the projections' [b, t, heads*24] rows); q_norm_w, k_norm_w: fp32 [24];
+ * 24] (the projections' [b, t, heads*24] rows; with qkv_stride > 0 the rows of
+ * q, k and v are qkv_stride floats apart, a multiple of 4: column slices of one
+ * stacked projection); q_norm_w, k_norm_w: fp32 [24];
  * caches fp32 [b, heads, max_len, 24].  Writes RMSNorm(k) and v at positions
  * p0 .. p0+t-1, then out[s, i, h] = softmax_{j <= p0+i}(RMSNorm(q_i) . K_j /
  * sqrt 24) V_j.  All arrays 16-byte aligned; p0 + t <= max_len.  Replaces the
  * q_ln / k_ln calls, the cache writes and F.scaled_dot_product_attention of the
  * attention's multi-token path (no counterpart in the reference, which has no
  * cache: with p0 = 0 it is pollux.py:615-626 itself). */
-int plx_prefill_attention(const float *q, const float *k, const float *v, const float *q_norm_w,
-                          const float *k_norm_w, float eps, float *k_cache, float *v_cache, int64_t b,
-                          int64_t heads, int64_t t, int64_t p0, int64_t max_len, float *out, void *stream);
+int plx_prefill_attention(const float *q, const float *k, const float *v, int64_t qkv_stride, const float *q_norm_w,
+                          const float *k_norm_w, float eps, float *k_cache, float *v_cache, int64_t b, int64_t heads,
+                          int64_t t, int64_t p0, int64_t max_len, float *out, void *stream);
 
 /* out[r] = the index of the maximum of x[r, :] (fp32 [rows, cols], int64 out):
  * torch.argmax's rule (the first index among equal maxima; a NaN counts as the

@@ -58,9 +58,10 @@ SIGNATURES = {
     "plx_int8_embed": (_int, [_vp, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _vp, _vp, _vp]),
     "plx_argmax_rows": (_int, [_vp, _i64, _i64, _vp, _vp]),
     "plx_rms_norm": (_int, [_vp, _vp, _vp, _i64, _i64, ctypes.c_float, _vp]),
-    "plx_decode_attention": (_int, [_vp, _vp, _vp, _vp, _vp, ctypes.c_float, _vp, _vp, _vp, _i64, _i64, _vp, _vp]),
-    "plx_prefill_attention": (_int, [_vp, _vp, _vp, _vp, _vp, ctypes.c_float, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
-                                     _vp, _vp]),
+    "plx_decode_attention": (_int, [_vp, _vp, _vp, _i64, _vp, _vp, ctypes.c_float, _vp, _vp, _vp, _i64, _i64, _i64, _vp,
+                                    _vp]),
+    "plx_prefill_attention": (_int, [_vp, _vp, _vp, _i64, _vp, _vp, ctypes.c_float, _vp, _vp, _i64, _i64, _i64, _i64,
+                                     _i64, _vp, _vp]),
     "plx_profile_begin": (_int, []),
     "plx_profile_end": (_int, [_vp, _vp]),
 }

@@ -320,26 +320,27 @@ int plx_argmax_rows(const float *x, int64_t rows, int64_t cols, int64_t *out, vo
   return launch_argmax_rows(x, rows, cols, out, as_stream(stream));
 }
 
-int plx_decode_attention(const float *q, const float *k, const float *v, const float *q_norm_w,
+int plx_decode_attention(const float *q, const float *k, const float *v, int64_t qkv_stride, const float *q_norm_w,
                          const float *k_norm_w, float eps, float *k_cache, float *v_cache, const int64_t *pos,
-                         int64_t n, int64_t max_len, float *out, void *stream) {
-  PLX_REQUIRE(n >= 0, "plx_decode_attention: negative head count");
+                         int64_t n, int64_t heads, int64_t max_len, float *out, void *stream) {
+  PLX_REQUIRE(n >= 0 && qkv_stride >= 0, "plx_decode_attention: negative head count or stride");
   if (n == 0) return PLX_OK;
   PLX_REQUIRE(q && k && v && q_norm_w && k_norm_w && k_cache && v_cache && pos && out,
               "plx_decode_attention: null pointer");
-  return launch_decode_attention(q, k, v, q_norm_w, k_norm_w, eps, k_cache, v_cache, pos, n, max_len, out,
-                                 as_stream(stream));
+  return launch_decode_attention(q, k, v, qkv_stride, heads, q_norm_w, k_norm_w, eps, k_cache, v_cache, pos, n,
+                                 max_len, out, as_stream(stream));
 }
 
-int plx_prefill_attention(const float *q, const float *k, const float *v, const float *q_norm_w,
+int plx_prefill_attention(const float *q, const float *k, const float *v, int64_t qkv_stride, const float *q_norm_w,
                           const float *k_norm_w, float eps, float *k_cache, float *v_cache, int64_t b, int64_t heads,
                           int64_t t, int64_t p0, int64_t max_len, float *out, void *stream) {
+  PLX_REQUIRE(qkv_stride >= 0, "plx_prefill_attention: negative stride");
   PLX_REQUIRE(b >= 0 && heads >= 0 && t >= 0, "plx_prefill_attention: negative shape (%lld, %lld, %lld)",
               static_cast<long long>(b), static_cast<long long>(t), static_cast<long long>(heads));
   if (b == 0 || heads == 0 || t == 0) return PLX_OK;
   PLX_REQUIRE(q && k && v && q_norm_w && k_norm_w && k_cache && v_cache && out, "plx_prefill_attention: null pointer");
-  return launch_prefill_attention(q, k, v, q_norm_w, k_norm_w, eps, k_cache, v_cache, b, heads, t, p0, max_len, out,
-                                  as_stream(stream));
+  return launch_prefill_attention(q, k, v, qkv_stride, q_norm_w, k_norm_w, eps, k_cache, v_cache, b, heads, t, p0,
+                                  max_len, out, as_stream(stream));
 }
 
 size_t plx_dequant_linear_workspace_bytes(int64_t rows, int64_t cols, int64_t m_rows, int flags) {

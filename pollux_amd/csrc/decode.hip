@@ -105,17 +105,19 @@ __global__ __launch_bounds__(64 * kNormRowsPerBlock) void rmsnorm_kernel(const f
 // first 256 positions right after it, from clamped addresses (no branch holds a
 // load).
 __global__ __launch_bounds__(kAttnThreads) void decode_attention_kernel(
-    const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v,
-    const float *__restrict__ q_w, const float *__restrict__ k_w, float eps, float *__restrict__ k_cache,
-    float *__restrict__ v_cache, const int64_t *__restrict__ pos_ptr, int64_t max_len, float scale,
-    float *__restrict__ out) {
+    const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v, int64_t heads,
+    int64_t in_stride, const float *__restrict__ q_w, const float *__restrict__ k_w, float eps,
+    float *__restrict__ k_cache, float *__restrict__ v_cache, const int64_t *__restrict__ pos_ptr, int64_t max_len,
+    float scale, float *__restrict__ out) {
   __shared__ float qn[kDim], kn[kDim], vn[kDim];
   __shared__ float red[kAttnThreads / 64][kDim + 1];
   __shared__ float stat[kAttnThreads / 64];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t bh = blockIdx.x;  // sequence * H + head
   const int c = lane < kDim ? lane : 0;  // every wave loads the head's 24 values (lanes 0..23)
-  const float qv = q[bh * kDim + c], kv = k[bh * kDim + c], vv = v[bh * kDim + c];
+  // q, k, v rows of `heads` heads, in_stride floats apart per sequence
+  const int64_t in = (bh / heads) * in_stride + (bh % heads) * kDim + c;
+  const float qv = q[in], kv = k[in], vv = v[in];
   const float qw = q_w[c], kw = k_w[c];
   const int64_t pos = *pos_ptr;
   if (pos < 0 || pos >= max_len) {  // the caller's position is outside the cache: write nothing
@@ -233,23 +235,24 @@ constexpr int kPrefillChunk = 256;  // new positions per launch (q, k, v rows of
 __global__ __launch_bounds__(kAttnThreads) void prefill_attention_kernel(
     const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v,
     const float *__restrict__ q_w, const float *__restrict__ k_w, float eps, float *__restrict__ k_cache,
-    float *__restrict__ v_cache, int64_t heads, int64_t t_total, int64_t c0, int tc, int64_t p, int64_t max_len,
-    float scale, float *__restrict__ out) {
+    float *__restrict__ v_cache, int64_t heads, int64_t in_stride, int64_t t_total, int64_t c0, int tc, int64_t p,
+    int64_t max_len, float scale, float *__restrict__ out) {
   __shared__ __align__(16) float qs[kPrefillChunk][kDim];
   __shared__ __align__(16) float ks[kPrefillChunk][kDim];
   __shared__ __align__(16) float vs[kPrefillChunk][kDim];
   const int tid = threadIdx.x;
   const int64_t h = blockIdx.x, bb = blockIdx.y;
-  const int64_t row_stride = heads * kDim;                           // between positions of one sequence
-  const int64_t in0 = (bb * t_total + c0) * row_stride + h * kDim;   // row c0 of this (sequence, head)
+  const int64_t row_stride = heads * kDim;                           // out: between positions of one sequence
+  const int64_t in0 = (bb * t_total + c0) * in_stride + h * kDim;    // q, k, v: row c0 of this (sequence, head)
+  const int64_t out0 = (bb * t_total + c0) * row_stride + h * kDim;
   float *kc = k_cache + (bb * heads + h) * max_len * kDim;
   float *vc = v_cache + (bb * heads + h) * max_len * kDim;
 
   // the chunk's rows: RMS norms of q and k (q_ln / k_ln), k and v into the caches
   for (int r = tid; r < tc; r += kAttnThreads) {
-    const float4 *q4 = reinterpret_cast<const float4 *>(q + in0 + r * row_stride);
-    const float4 *k4 = reinterpret_cast<const float4 *>(k + in0 + r * row_stride);
-    const float4 *v4 = reinterpret_cast<const float4 *>(v + in0 + r * row_stride);
+    const float4 *q4 = reinterpret_cast<const float4 *>(q + in0 + r * in_stride);
+    const float4 *k4 = reinterpret_cast<const float4 *>(k + in0 + r * in_stride);
+    const float4 *v4 = reinterpret_cast<const float4 *>(v + in0 + r * in_stride);
     float qv[kDim], kv[kDim], vv[kDim];
 #pragma unroll
     for (int i = 0; i < kDim / 4; ++i) {
@@ -329,7 +332,7 @@ __global__ __launch_bounds__(kAttnThreads) void prefill_attention_kernel(
     for (int c = 0; c < kDim; ++c) part[c] = acc[c] * f;
     part[kDim] = l * f;
     group_reduce<16>(part);
-    float *o = out + in0 + static_cast<int64_t>(i) * row_stride;
+    float *o = out + out0 + static_cast<int64_t>(i) * row_stride;
     const float inv = part[kDim];
     // lane c writes coordinate c, lanes 0..7 also c + 16 (static indices: no scratch)
     float v0 = part[0], v1 = part[16];
@@ -443,23 +446,31 @@ int launch_rms_norm(const float *x, const float *w, float *y, int64_t rows, int6
   return check_launch("rmsnorm_kernel");
 }
 
-int launch_decode_attention(const float *q, const float *k, const float *v, const float *q_w, const float *k_w,
-                            float eps, float *k_cache, float *v_cache, const int64_t *pos, int64_t seqs_heads,
-                            int64_t max_len, float *out, hipStream_t s) {
+int launch_decode_attention(const float *q, const float *k, const float *v, int64_t qkv_stride, int64_t heads,
+                            const float *q_w, const float *k_w, float eps, float *k_cache, float *v_cache,
+                            const int64_t *pos, int64_t seqs_heads, int64_t max_len, float *out, hipStream_t s) {
   if (seqs_heads <= 0) return PLX_OK;
   if (max_len <= 0 || max_len > (1 << 24))
     return fail(PLX_EINVAL, "decode_attention: cache length %lld outside 1..2^24", static_cast<long long>(max_len));
   if (seqs_heads > 0x7FFFFFFFll) return fail(PLX_EINVAL, "decode_attention: too many heads");
   const uintptr_t al = reinterpret_cast<uintptr_t>(k_cache) | reinterpret_cast<uintptr_t>(v_cache);
   if ((al & 15u) != 0) return fail(PLX_EINVAL, "decode_attention: caches must be 16-byte aligned");
+  if (qkv_stride == 0) {  // contiguous [seqs_heads, 24]
+    heads = 1;
+    qkv_stride = kDim;
+  }
+  if (heads <= 0 || seqs_heads % heads != 0 || qkv_stride < heads * kDim)
+    return fail(PLX_EINVAL, "decode_attention: rows of %lld heads %lld floats apart do not tile %lld head rows",
+                static_cast<long long>(heads), static_cast<long long>(qkv_stride), static_cast<long long>(seqs_heads));
   hipLaunchKernelGGL(decode_attention_kernel, dim3(static_cast<unsigned>(seqs_heads)), dim3(kAttnThreads), 0, s, q, k,
-                     v, q_w, k_w, eps, k_cache, v_cache, pos, max_len, 1.0f / sqrtf(static_cast<float>(kDim)), out);
+                     v, heads, qkv_stride, q_w, k_w, eps, k_cache, v_cache, pos, max_len,
+                     1.0f / sqrtf(static_cast<float>(kDim)), out);
   return check_launch("decode_attention_kernel");
 }
 
-int launch_prefill_attention(const float *q, const float *k, const float *v, const float *q_w, const float *k_w,
-                             float eps, float *k_cache, float *v_cache, int64_t b, int64_t heads, int64_t t, int64_t p0,
-                             int64_t max_len, float *out, hipStream_t s) {
+int launch_prefill_attention(const float *q, const float *k, const float *v, int64_t qkv_stride, const float *q_w,
+                             const float *k_w, float eps, float *k_cache, float *v_cache, int64_t b, int64_t heads,
+                             int64_t t, int64_t p0, int64_t max_len, float *out, hipStream_t s) {
   if (b <= 0 || heads <= 0 || t <= 0) return PLX_OK;
   if (max_len <= 0 || max_len > (1 << 24))
     return fail(PLX_EINVAL, "prefill_attention: cache length %lld outside 1..2^24", static_cast<long long>(max_len));
@@ -471,12 +482,16 @@ int launch_prefill_attention(const float *q, const float *k, const float *v, con
                        reinterpret_cast<uintptr_t>(k_cache) | reinterpret_cast<uintptr_t>(v_cache) |
                        reinterpret_cast<uintptr_t>(out);
   if ((al & 15u) != 0) return fail(PLX_EINVAL, "prefill_attention: q, k, v, caches and out must be 16-byte aligned");
+  if (qkv_stride == 0) qkv_stride = heads * kDim;  // contiguous rows
+  if (qkv_stride < heads * kDim || qkv_stride % 4 != 0)
+    return fail(PLX_EINVAL, "prefill_attention: q, k, v rows %lld floats apart (at least %lld, a multiple of 4)",
+                static_cast<long long>(qkv_stride), static_cast<long long>(heads * kDim));
   const float scale = 1.0f / sqrtf(static_cast<float>(kDim));
   for (int64_t c0 = 0; c0 < t; c0 += kPrefillChunk) {
     const int tc = static_cast<int>(t - c0 < kPrefillChunk ? t - c0 : kPrefillChunk);
     hipLaunchKernelGGL(prefill_attention_kernel, dim3(static_cast<unsigned>(heads), static_cast<unsigned>(b)),
-                       dim3(kAttnThreads), 0, s, q, k, v, q_w, k_w, eps, k_cache, v_cache, heads, t, c0, tc, p0 + c0,
-                       max_len, scale, out);
+                       dim3(kAttnThreads), 0, s, q, k, v, q_w, k_w, eps, k_cache, v_cache, heads, qkv_stride, t, c0, tc,
+                       p0 + c0, max_len, scale, out);
     const int st = check_launch("prefill_attention_kernel");
     if (st != PLX_OK) return st;
   }

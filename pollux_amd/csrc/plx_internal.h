@@ -134,12 +134,12 @@ int launch_int8_embed(const int8_t *q, const uint16_t *mu16, int64_t vocab, int6
                       hipStream_t s);
 int launch_argmax_rows(const float *x, int64_t rows, int64_t cols, int64_t *out, hipStream_t s);
 int launch_rms_norm(const float *x, const float *w, float *y, int64_t rows, int64_t d, float eps, hipStream_t s);
-int launch_decode_attention(const float *q, const float *k, const float *v, const float *q_w, const float *k_w,
-                            float eps, float *k_cache, float *v_cache, const int64_t *pos, int64_t seqs_heads,
-                            int64_t max_len, float *out, hipStream_t s);
-int launch_prefill_attention(const float *q, const float *k, const float *v, const float *q_w, const float *k_w,
-                             float eps, float *k_cache, float *v_cache, int64_t b, int64_t heads, int64_t t, int64_t p0,
-                             int64_t max_len, float *out, hipStream_t s);
+int launch_decode_attention(const float *q, const float *k, const float *v, int64_t qkv_stride, int64_t heads,
+                            const float *q_w, const float *k_w, float eps, float *k_cache, float *v_cache,
+                            const int64_t *pos, int64_t seqs_heads, int64_t max_len, float *out, hipStream_t s);
+int launch_prefill_attention(const float *q, const float *k, const float *v, int64_t qkv_stride, const float *q_w,
+                             const float *k_w, float eps, float *k_cache, float *v_cache, int64_t b, int64_t heads,
+                             int64_t t, int64_t p0, int64_t max_len, float *out, hipStream_t s);
 // One weight of a multi-target dequant-linear call (all share x and cols).
 struct DqlTarget {
   const uint8_t *packed;

@@ -132,22 +132,43 @@ def argmax_rows(x: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tenso
     return out
 
 
+def _qkv_rows(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor):
+    """(q, k, v, row stride) for the attention kernels: [b, t, c] views whose token rows lie a common
+    stride apart (column slices of one stacked projection) are passed as they are, anything else
+    as contiguous copies (stride 0)."""
+    b, t, c = q.shape
+
+    def stride_of(x):
+        if x.shape != q.shape or x.stride(2) != 1 or x.data_ptr() % 16:
+            return None
+        s = x.stride(1) if t > 1 else x.stride(0)
+        if b > 1 and x.stride(0) != t * s:
+            return None
+        return s if s >= c and s % 4 == 0 else None
+
+    strides = {stride_of(x) for x in (q, k, v)}
+    if len(strides) == 1 and None not in strides:
+        return q, k, v, strides.pop()
+    return q.contiguous(), k.contiguous(), v.contiguous(), 0
+
+
 def decode_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q_ln: RMSNorm, k_ln: RMSNorm,
                      k_cache: torch.Tensor, v_cache: torch.Tensor, pos: torch.Tensor) -> torch.Tensor:
     """Attention of one new token per sequence over the cache (plx_decode_attention).
 
-    q, k, v: [b, 1, H*24] projections; caches [b, H, max_len, 24]; pos: 0-dim
-    int64 device tensor.  Writes k_ln(k) and v at ``pos``; returns [b, 1, H*24].
+    q, k, v: [b, 1, H*24] projections (contiguous, or column slices of one stacked projection);
+    caches [b, H, max_len, 24]; pos: 0-dim int64 device tensor.  Writes k_ln(k) and v at ``pos``;
+    returns [b, 1, H*24].
     """
     b, t, c = q.shape
-    n = b * (c // H24_DIM)
-    out = torch.empty_like(q)
-    qq, kk, vv = q.contiguous(), k.contiguous(), v.contiguous()
+    heads = c // H24_DIM
+    out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    qq, kk, vv, stride = _qkv_rows(q, k, v)
     with torch.cuda.device(q.device):
         st = _lib.lib().plx_decode_attention(
-            _lib.ptr(qq), _lib.ptr(kk), _lib.ptr(vv), _lib.ptr(q_ln.weight.detach()), _lib.ptr(k_ln.weight.detach()),
-            float(q_ln.eps), _lib.ptr(k_cache), _lib.ptr(v_cache), _lib.ptr(pos), n, k_cache.shape[2], _lib.ptr(out),
-            _lib.stream_of(q.device))
+            _lib.ptr(qq), _lib.ptr(kk), _lib.ptr(vv), stride, _lib.ptr(q_ln.weight.detach()),
+            _lib.ptr(k_ln.weight.detach()), float(q_ln.eps), _lib.ptr(k_cache), _lib.ptr(v_cache), _lib.ptr(pos),
+            b * heads, heads, k_cache.shape[2], _lib.ptr(out), _lib.stream_of(q.device))
     _lib.check(st, "decode_attention")
     return out
 
@@ -163,12 +184,12 @@ def prefill_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q_ln: R
     b, t, c = q.shape
     heads = c // H24_DIM
     out = torch.empty(b, t, c, dtype=torch.float32, device=q.device)
-    qq, kk, vv = q.contiguous(), k.contiguous(), v.contiguous()
+    qq, kk, vv, stride = _qkv_rows(q, k, v)
     with torch.cuda.device(q.device):
         st = _lib.lib().plx_prefill_attention(
-            _lib.ptr(qq), _lib.ptr(kk), _lib.ptr(vv), _lib.ptr(q_ln.weight.detach()), _lib.ptr(k_ln.weight.detach()),
-            float(q_ln.eps), _lib.ptr(k_cache), _lib.ptr(v_cache), b, heads, t, int(p0), k_cache.shape[2],
-            _lib.ptr(out), _lib.stream_of(q.device))
+            _lib.ptr(qq), _lib.ptr(kk), _lib.ptr(vv), stride, _lib.ptr(q_ln.weight.detach()),
+            _lib.ptr(k_ln.weight.detach()), float(q_ln.eps), _lib.ptr(k_cache), _lib.ptr(v_cache), b, heads, t,
+            int(p0), k_cache.shape[2], _lib.ptr(out), _lib.stream_of(q.device))
     _lib.check(st, "prefill_attention")
     return out
 

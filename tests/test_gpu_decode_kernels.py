@@ -186,3 +186,32 @@ def test_prefill_attention_refuses_positions_past_the_cache(dev):
     with pytest.raises(ValueError):
         prefill_attention(x, x, x, ln, ln, kc, kc.clone(), 4)
     assert torch.equal(kc, torch.zeros_like(kc))
+
+
+@pytest.mark.parametrize("b,t", [(3, 1), (16, 1), (2, 5), (1, 9)])
+def test_attention_reads_column_slices_of_a_stacked_projection(dev, b, t):
+    # q, k, v as column slices of one [b, t, 3c] projection (the stacked q/k/v GEMM's output) are read
+    # in place, rows 3c floats apart: the same results and cache writes as from contiguous copies
+    heads, max_len = 4, 32
+    c = heads * 24
+    g = torch.Generator().manual_seed(b * 10 + t)
+    qkv = torch.randn(b, t, 3 * c, generator=g).to(dev)
+    q, k, v = qkv[..., :c], qkv[..., c:2 * c], qkv[..., 2 * c:]
+    assert not q.is_contiguous()
+    q_ln, k_ln = RMSNorm(24).to(dev), RMSNorm(24).to(dev)
+    with torch.no_grad():
+        q_ln.weight.copy_(1.0 + 0.1 * torch.randn(24, generator=g))
+        k_ln.weight.copy_(1.0 + 0.1 * torch.randn(24, generator=g))
+    kc = torch.randn(b, heads, max_len, 24, generator=g).to(dev)
+    vc = torch.randn(b, heads, max_len, 24, generator=g).to(dev)
+    kc2, vc2 = kc.clone(), vc.clone()
+    with torch.no_grad():
+        if t == 1:
+            p = torch.tensor(7, dtype=torch.long, device=dev)
+            a = decode_attention(q, k, v, q_ln, k_ln, kc, vc, p)
+            r = decode_attention(q.contiguous(), k.contiguous(), v.contiguous(), q_ln, k_ln, kc2, vc2, p)
+        else:
+            a = prefill_attention(q, k, v, q_ln, k_ln, kc, vc, 3)
+            r = prefill_attention(q.contiguous(), k.contiguous(), v.contiguous(), q_ln, k_ln, kc2, vc2, 3)
+    assert torch.equal(a, r)
+    assert torch.equal(kc, kc2) and torch.equal(vc, vc2)
