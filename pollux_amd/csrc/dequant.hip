@@ -1090,6 +1090,74 @@ __global__ __launch_bounds__(256) void xfrag_kernel(const void *__restrict__ x, 
   }
 }
 
+// RMS norm of fp32 token rows written straight into the fragment-order copy:
+// rmsnorm_kernel (decode.hip) and xfrag_kernel<true> in one launch, with the
+// same values (the sum of squares in rmsnorm_kernel's order: lane l holds
+// float4 l + 64k of the row, fmaf over k and the four components, then the
+// wave sum).  One wave per token row of each 64-token slab; rows >= m write
+// zeros.  Fragment 32k + j holds the row's columns 8(32k + j) .. +8, i.e.
+// float4s 64k + 2j and 64k + 2j + 1: lanes 2j and 2j + 1 each write their
+// 8-byte half of the fragment in every part.  Rows of up to 32 * kNfVec
+// fragments (kNfVec * 256 columns, padding of the last quad included).
+constexpr int kNfVec = 8;
+__global__ __launch_bounds__(256) void normfrag_kernel(const float *__restrict__ x, const float *__restrict__ w,
+                                                       int64_t m_total, int cols, int64_t n_quads_row, float eps,
+                                                       uint2 *__restrict__ xf) {
+  constexpr int kQuadFrags = kXfQuadBytes / 16;
+  const int lane = threadIdx.x & 63;
+  const int64_t tok = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  const int64_t slab = tok >> 6;
+  const int t = static_cast<int>((tok >> 4) & 3), tl = static_cast<int>(tok & 15);
+  const int n4 = cols >> 2;
+  const bool live = tok < m_total;
+  const float4 *xr = reinterpret_cast<const float4 *>(x + (live ? tok : 0) * static_cast<int64_t>(cols));
+  const float4 *wr = reinterpret_cast<const float4 *>(w);
+  float4 v[kNfVec], g[kNfVec];
+#pragma unroll
+  for (int k = 0; k < kNfVec; ++k) {
+    const int i = lane + 64 * k;
+    v[k] = live && i < n4 ? xr[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+    g[k] = i < n4 ? wr[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int k = 0; k < kNfVec; ++k) {
+    ss = fmaf(v[k].x, v[k].x, ss);
+    ss = fmaf(v[k].y, v[k].y, ss);
+    ss = fmaf(v[k].z, v[k].z, ss);
+    ss = fmaf(v[k].w, v[k].w, ss);
+  }
+  ss = wave_reduce_sum(ss);
+  const float r = 1.0f / sqrtf(ss / static_cast<float>(cols) + eps);
+  const int64_t n_frag = n_quads_row * 12;
+  const int64_t per_slab = n_quads_row * kQuadFrags;
+  uint2 *dst = xf + 2 * slab * per_slab * 3 + (lane & 1);
+#pragma unroll
+  for (int k = 0; k < kNfVec; ++k) {
+    const int fg = 32 * k + (lane >> 1);
+    if (fg >= n_frag) continue;
+    const int qs = fg >> 2, c8 = fg & 3, quad = qs / 3;
+    const int64_t within = static_cast<int64_t>(qs * 4 + t) * 64 + tl + 16 * c8 - static_cast<int64_t>(quad) * kQuadFrags;
+    const float y[4] = {v[k].x * r * g[k].x, v[k].y * r * g[k].y, v[k].z * r * g[k].z, v[k].w * r * g[k].w};
+    uint32_t hb[4], mb[4], lb[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float xv = live ? y[e] : 0.f;
+      hb[e] = bf16_rne_bits(xv);
+      mb[e] = lb[e] = 0u;
+      if (fabsf(xv) <= 3.0e38f) {
+        const float r1 = xv - __uint_as_float(hb[e] << 16);
+        mb[e] = bf16_rne_bits(r1);
+        lb[e] = bf16_rne_bits(r1 - __uint_as_float(mb[e] << 16));
+      }
+    }
+    uint2 *d = dst + 2 * (static_cast<int64_t>(quad) * 3 * kQuadFrags + within);
+    d[0] = make_uint2(hb[0] | (hb[1] << 16), hb[2] | (hb[3] << 16));
+    d[2 * kQuadFrags] = make_uint2(mb[0] | (mb[1] << 16), mb[2] | (mb[3] << 16));
+    d[4 * kQuadFrags] = make_uint2(lb[0] | (lb[1] << 16), lb[2] | (lb[3] << 16));
+  }
+}
+
 // (hi | lo << 16) with hi + lo == v exactly for an fp16 value v (lo = 0 for inf / nan)
 __device__ __forceinline__ uint32_t hi_lo_pack(float v) {
   const uint32_t hb = bf16_rne_bits(v);
@@ -1622,20 +1690,29 @@ int launch_dequant_linear_multi(const DqlTarget *targets, int n, int64_t cols, c
     const uint4 *xf = reinterpret_cast<const uint4 *>(wsb);
     const int64_t slabs = (m + 63) / 64, nq = (apr + 3) / 4;
     const dim3 gx(static_cast<unsigned>(nq * 3), static_cast<unsigned>(slabs));
-    if (norm) {
-      st = launch_rms_norm(static_cast<const float *>(x), norm_w, xnorm, m, cols, norm_eps, s);
-      if (st != PLX_OK) return st;
-      x = xnorm;
-    }
     const bool copy = mm_x_copy(x_is_f32 != 0, m);
-    if (copy) {
-      if (x_is_f32)
-        hipLaunchKernelGGL((xfrag_kernel<true>), gx, dim3(256), 0, s, x, m, cols, nq, reinterpret_cast<uint4 *>(wsb));
-      else
-        hipLaunchKernelGGL((xfrag_kernel<false>), gx, dim3(256), 0, s, x, m, cols, nq, reinterpret_cast<uint4 *>(wsb));
-      st = check_launch("xfrag_kernel");
+    if (norm && copy && nq * 12 <= 32 * kNfVec) {
+      // the norm writes the fragment-order copy itself (rows that fit normfrag_kernel's registers)
+      hipLaunchKernelGGL(normfrag_kernel, dim3(static_cast<unsigned>(slabs * 16)), dim3(256), 0, s,
+                         static_cast<const float *>(x), norm_w, m, static_cast<int>(cols), nq, norm_eps,
+                         reinterpret_cast<uint2 *>(wsb));
+      st = check_launch("normfrag_kernel");
     } else {
-      xf = static_cast<const uint4 *>(x);  // read in place by dqmm_kernel
+      if (norm) {
+        st = launch_rms_norm(static_cast<const float *>(x), norm_w, xnorm, m, cols, norm_eps, s);
+        if (st != PLX_OK) return st;
+        x = xnorm;
+      }
+      if (copy) {
+        if (x_is_f32)
+          hipLaunchKernelGGL((xfrag_kernel<true>), gx, dim3(256), 0, s, x, m, cols, nq, reinterpret_cast<uint4 *>(wsb));
+        else
+          hipLaunchKernelGGL((xfrag_kernel<false>), gx, dim3(256), 0, s, x, m, cols, nq,
+                             reinterpret_cast<uint4 *>(wsb));
+        st = check_launch("xfrag_kernel");
+      } else {
+        xf = static_cast<const uint4 *>(x);  // read in place by dqmm_kernel
+      }
     }
     for (int i = 0; i < n && st == PLX_OK; ++i) {
       const DqlTarget &t = targets[i];

@@ -227,10 +227,14 @@ def test_multi_target_bad_arguments(dev):
         dequant_linear_multi([(packed.to(dev), sig.to(dev), 48)], 48, x, residuals=[torch.zeros(3, device=dev)])
 
 
-# in-kernel norm: m = 1, 3 (two token chunks of 2), 7 (chunks of 4 and 3) at 1920 columns;
-# x too wide to stage in LDS (5 x 3072: the norm runs as plx_rms_norm into the workspace first);
-# the MFMA batch path (40 tokens)
-@pytest.mark.parametrize("m,in_f", [(1, 1920), (3, 1920), (7, 1920), (5, 3072), (40, 1920)])
+# in-kernel norm of the GEMV path: m = 1, 3 (two token chunks of 2) at 1920 columns; the MFMA
+# batch path, where the norm writes the fragment-order copy in one launch (normfrag_kernel): 7,
+# 40 and 65 tokens (two slabs) at 1920 columns, 16 tokens at 1944 (81 atoms: the last quad of 4
+# atoms is padded with zeros); rows too wide for it (5 x 3072, 20 x 2064: plx_rms_norm into the
+# workspace, then the fragment-order copy)
+@pytest.mark.parametrize(
+    "m,in_f", [(1, 1920), (3, 1920), (7, 1920), (5, 3072), (40, 1920), (65, 1920), (16, 1944), (20, 2064)]
+)
 def test_multi_target_rms_norm_prologue(dev, m, in_f):
     from pollux_amd.model import rms_norm
     from pollux_amd.packed import dequant_linear_multi
@@ -244,7 +248,7 @@ def test_multi_target_rms_norm_prologue(dev, m, in_f):
     weights = [(pk.to(dev), sig.to(dev), o) for (idx, sig, pk, _), o in zip(layers, shapes)]
     ys = dequant_linear_multi(weights, in_f, x, residuals=[r, None], norm=(nw, 1e-8))
     xn = rms_norm(x, nw, 1e-8)
-    in_lds = m <= 16 and in_f == 1920
+    in_lds = m <= 4 and in_f == 1920  # the GEMV path's norm; the MFMA path's equals plx_rms_norm's bit for bit
     for i, ((pk, sg, o), y) in enumerate(zip(weights, ys)):
         sep = dequant_linear(pk, sg, o, in_f, xn) + (r if i == 0 else 0.0)
         if in_lds:  # the sum of squares is taken in another order than plx_rms_norm's
