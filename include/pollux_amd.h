@@ -303,8 +303,9 @@ int plx_rms_norm(const float *x, const float *w, float *y, int64_t rows, int64_t
 /* The attention of one new token per sequence (pollux.py:615-626 at the last
  * position).  q, k, v: fp32 [n, 24] projections of the new token, n = sequences
  * x heads, or with qkv_stride > 0 each sequence's row of `heads` heads
- * qkv_stride floats apart (q, k and v as column slices of one stacked
- * projection); q_norm_w, k_norm_w: fp32 [24] (q_ln, k_ln weights); caches fp32
+ * qkv_stride floats apart, an even number (q, k and v as column slices of one
+ * stacked projection); q_norm_w, k_norm_w: fp32 [24] (q_ln, k_ln weights); q,
+ * k, v and the weights 8-byte aligned; caches fp32
  * [n, max_len, 24] (16-byte aligned); *pos: the new token's position (device
  * int64).  Writes RMSNorm(k) and v at position *pos, then out fp32 [n, 24] =
  * softmax_{j <= pos}(RMSNorm(q) . K_j / sqrt 24) V_j.  A position outside

@@ -11,8 +11,8 @@
 //   pollux.py:615-620), writes k and v into the caches at the position read
 //   from device memory, then computes softmax_j<=pos(q . K_j / sqrt 24) V_j
 //   over the cached positions (the causal scaled_dot_product_attention of
-//   pollux.py:624 for the last query): an online softmax per thread over its
-//   positions, combined across the block at the end.
+//   pollux.py:624 for the last query): an online softmax per group of four
+//   lanes over its positions, combined across the block at the end.
 //   Reading the position from device memory lets a captured graph replay the
 //   step while the position advances on the device; a position outside the
 //   cache writes nothing and yields NaN outputs.
@@ -97,131 +97,172 @@ __global__ __launch_bounds__(64 * kNormRowsPerBlock) void rmsnorm_kernel(const f
 }
 
 // q, k, v: [b, H, 24] projections of the new token; caches [b, H, max_len, 24];
-// out [b, H, 24].  Thread t takes the cached positions t, t + 256, ... below
-// pos with an online softmax (running max, sum and the 24 weighted-V sums);
-// the new position's normalised k and its v go through LDS (they are written
-// to the caches, not read back).  Every load that does not depend on the
-// position (q, k, v, norm weights) is issued before it, every row load for the
-// first 256 positions right after it, from clamped addresses (no branch holds a
-// load).
-__global__ __launch_bounds__(kAttnThreads) void decode_attention_kernel(
+// out [b, H, 24].  Four lanes share a position: lane l of wave w holds dims
+// 6(l & 3) .. +6 of the K and V rows of positions 64r + 16w + (l >> 2),
+// r = 0, 1, ..., so one wave load covers 16 consecutive rows (1.5 KB) where a
+// row per lane touched 64 cache lines per instruction.  Each group of four
+// runs an online softmax over its positions (the score: its partial dot
+// products summed over the four lanes, the same bits in each); the groups
+// combine within the wave by DPP / shuffles over lanes of equal dims, the
+// waves through LDS.  The positions' K / V rows are loaded kAttnRounds rounds
+// of 64 at a time, from clamped addresses (no branch holds a load); round 0
+// before the position is read (rows clamped to the cache), so those loads
+// and the position's are in flight together.  The new position's normalised
+// k and its v stand in for its (not yet written) cache rows.  96 VGPRs
+// (5 waves per SIMD: 16 sequences x 80 heads are resident at once).
+constexpr int kAttnRounds = 4;
+__global__ __launch_bounds__(kAttnThreads, 5) void decode_attention_kernel(
     const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v, int64_t heads,
     int64_t in_stride, const float *__restrict__ q_w, const float *__restrict__ k_w, float eps,
     float *__restrict__ k_cache, float *__restrict__ v_cache, const int64_t *__restrict__ pos_ptr, int64_t max_len,
     float scale, float *__restrict__ out) {
-  __shared__ float qn[kDim], kn[kDim], vn[kDim];
-  __shared__ float red[kAttnThreads / 64][kDim + 1];
-  __shared__ float stat[kAttnThreads / 64];
+  constexpr int kSub = kDim / 4;  // dims per lane
+  __shared__ float red[kAttnThreads / 64][kDim + 2];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int64_t bh = blockIdx.x;  // sequence * H + head
-  const int c = lane < kDim ? lane : 0;  // every wave loads the head's 24 values (lanes 0..23)
+  const int d0 = (lane & 3) * kSub;
+  const int grp = wave * 16 + (lane >> 2);  // position within a round of 64
+  const int64_t bh = blockIdx.x;            // sequence * H + head
+  float *kc = k_cache + bh * max_len * kDim + d0;
+  float *vc = v_cache + bh * max_len * kDim + d0;
+  float kr[kAttnRounds][kSub], vr[kAttnRounds][kSub];
+  auto load_row = [&](int r, int64_t j) {
+    const float2 *a = reinterpret_cast<const float2 *>(kc + j * kDim);
+    const float2 *b = reinterpret_cast<const float2 *>(vc + j * kDim);
+#pragma unroll
+    for (int i = 0; i < kSub / 2; ++i) {
+      const float2 x = a[i], y = b[i];
+      kr[r][2 * i] = x.x; kr[r][2 * i + 1] = x.y;
+      vr[r][2 * i] = y.x; vr[r][2 * i + 1] = y.y;
+    }
+  };
+  load_row(0, grp < max_len ? grp : max_len - 1);
   // q, k, v rows of `heads` heads, in_stride floats apart per sequence
-  const int64_t in = (bh / heads) * in_stride + (bh % heads) * kDim + c;
-  const float qv = q[in], kv = k[in], vv = v[in];
-  const float qw = q_w[c], kw = k_w[c];
+  const int64_t in = (bh / heads) * in_stride + (bh % heads) * kDim + d0;
+  float qv[kSub], kv[kSub], vn[kSub], qw[kSub], kw[kSub];
+#pragma unroll
+  for (int i = 0; i < kSub / 2; ++i) {
+    const float2 a = reinterpret_cast<const float2 *>(q + in)[i], b = reinterpret_cast<const float2 *>(k + in)[i];
+    const float2 c = reinterpret_cast<const float2 *>(v + in)[i];
+    const float2 e = reinterpret_cast<const float2 *>(q_w + d0)[i], f = reinterpret_cast<const float2 *>(k_w + d0)[i];
+    qv[2 * i] = a.x; qv[2 * i + 1] = a.y; kv[2 * i] = b.x; kv[2 * i + 1] = b.y;
+    vn[2 * i] = c.x; vn[2 * i + 1] = c.y; qw[2 * i] = e.x; qw[2 * i + 1] = e.y;
+    kw[2 * i] = f.x; kw[2 * i + 1] = f.y;
+  }
   const int64_t pos = *pos_ptr;
   if (pos < 0 || pos >= max_len) {  // the caller's position is outside the cache: write nothing
     if (tid < kDim) out[bh * kDim + tid] = __builtin_nanf("");
     return;
   }
-  float *kc = k_cache + bh * max_len * kDim;
-  float *vc = v_cache + bh * max_len * kDim;
-  // this thread's first cached position (row 0 stands in when there is none: loaded, never used)
-  const int64_t j0 = tid < pos ? tid : 0;
-  float kr[kDim], vr[kDim];
 #pragma unroll
-  for (int i = 0; i < kDim / 4; ++i) {
-    const float4 a = reinterpret_cast<const float4 *>(kc + j0 * kDim)[i];
-    const float4 b = reinterpret_cast<const float4 *>(vc + j0 * kDim)[i];
-    kr[4 * i] = a.x; kr[4 * i + 1] = a.y; kr[4 * i + 2] = a.z; kr[4 * i + 3] = a.w;
-    vr[4 * i] = b.x; vr[4 * i + 1] = b.y; vr[4 * i + 2] = b.z; vr[4 * i + 3] = b.w;
+  for (int r = 1; r < kAttnRounds; ++r) {
+    const int64_t j = 64 * r + grp;
+    load_row(r, j < pos ? j : pos);
   }
 
-  // per-head RMS norms of q and k (24 values each), computed by every wave (no
-  // branch around the loads above, which the compiler would otherwise sink into
-  // it and wait for one by one); wave 0 stores the new row in LDS and the caches
-  {
-    const bool on = lane < kDim;
-    float sq[2] = {on ? qv * qv : 0.f, on ? kv * kv : 0.f};
-    group_reduce<64>(sq);
-    const float rq = 1.0f / sqrtf(sq[0] / static_cast<float>(kDim) + eps);
-    const float rk = 1.0f / sqrtf(sq[1] / static_cast<float>(kDim) + eps);
-    const float kk = kv * rk * kw;
-    if (tid < kDim) {
-      qn[lane] = qv * rq * qw;
-      kn[lane] = kk;
-      vn[lane] = vv;
-      kc[pos * kDim + lane] = kk;
-      vc[pos * kDim + lane] = vv;
+  // per-head RMS norms of q and k: 6 squares per lane, summed over the four lanes
+  float sq[2] = {0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < kSub; ++i) {
+    sq[0] = fmaf(qv[i], qv[i], sq[0]);
+    sq[1] = fmaf(kv[i], kv[i], sq[1]);
+  }
+#pragma unroll
+  for (int u = 0; u < 2; ++u) sq[u] += dpp_f32<0xB1>(sq[u]);
+#pragma unroll
+  for (int u = 0; u < 2; ++u) sq[u] += dpp_f32<0x4E>(sq[u]);
+  const float rq = 1.0f / sqrtf(sq[0] / static_cast<float>(kDim) + eps);
+  const float rk = 1.0f / sqrtf(sq[1] / static_cast<float>(kDim) + eps);
+  float qn[kSub], kn[kSub];
+#pragma unroll
+  for (int i = 0; i < kSub; ++i) {
+    qn[i] = qv[i] * rq * qw[i];
+    kn[i] = kv[i] * rk * kw[i];
+  }
+  if (tid < 4) {  // the new row into the caches
+#pragma unroll
+    for (int i = 0; i < kSub / 2; ++i) {
+      reinterpret_cast<float2 *>(kc + pos * kDim)[i] = make_float2(kn[2 * i], kn[2 * i + 1]);
+      reinterpret_cast<float2 *>(vc + pos * kDim)[i] = make_float2(vn[2 * i], vn[2 * i + 1]);
     }
   }
-  __syncthreads();
 
-  float qr[kDim];
+  float m = -INFINITY, l = 0.f, acc[kSub];
 #pragma unroll
-  for (int i = 0; i < kDim; ++i) qr[i] = qn[i];
-  float m = -INFINITY, l = 0.f, acc[kDim];
-#pragma unroll
-  for (int i = 0; i < kDim; ++i) acc[i] = 0.f;
-  // online softmax step with key row kk and value row vv
-  auto step = [&](const float *kk, const float *vrow) {
+  for (int i = 0; i < kSub; ++i) acc[i] = 0.f;
+  // online softmax step of this group with key row kk and value row vv (all four lanes take it)
+  auto step = [&](const float *kk, const float *vv) {
     float s = 0.f;
 #pragma unroll
-    for (int i = 0; i < kDim; ++i) s = fmaf(qr[i], kk[i], s);
+    for (int i = 0; i < kSub; ++i) s = fmaf(qn[i], kk[i], s);
+    s += dpp_f32<0xB1>(s);
+    s += dpp_f32<0x4E>(s);
     s *= scale;
     const float mn = fmaxf(m, s);
     const float a = expf(m - mn), p = expf(s - mn);  // m = -inf at the first step: a = 0
     l = fmaf(l, a, p);
 #pragma unroll
-    for (int i = 0; i < kDim; ++i) acc[i] = fmaf(acc[i], a, p * vrow[i]);
+    for (int i = 0; i < kSub; ++i) acc[i] = fmaf(acc[i], a, p * vv[i]);
     m = mn;
   };
-  if (tid < pos) step(kr, vr);
-  for (int64_t j = tid + kAttnThreads; j < pos; j += kAttnThreads) {
+  const int64_t n_rounds = pos / 64 + 1;  // positions 0 .. pos
+  for (int64_t r0 = 0; r0 < n_rounds; r0 += kAttnRounds) {
+    if (r0 > 0) {
 #pragma unroll
-    for (int i = 0; i < kDim / 4; ++i) {
-      const float4 a = reinterpret_cast<const float4 *>(kc + j * kDim)[i];
-      const float4 b = reinterpret_cast<const float4 *>(vc + j * kDim)[i];
-      kr[4 * i] = a.x; kr[4 * i + 1] = a.y; kr[4 * i + 2] = a.z; kr[4 * i + 3] = a.w;
-      vr[4 * i] = b.x; vr[4 * i + 1] = b.y; vr[4 * i + 2] = b.z; vr[4 * i + 3] = b.w;
+      for (int r = 0; r < kAttnRounds; ++r) {
+        const int64_t j = 64 * (r0 + r) + grp;
+        load_row(r, j < pos ? j : pos);
+      }
     }
-    step(kr, vr);
-  }
-  if (tid == pos % kAttnThreads) {  // the new position
 #pragma unroll
-    for (int i = 0; i < kDim; ++i) {
-      kr[i] = kn[i];
-      vr[i] = vn[i];
+    for (int r = 0; r < kAttnRounds; ++r) {
+      if (r0 + r >= n_rounds) break;
+      const int64_t j = 64 * (r0 + r) + grp;
+      if (j < pos) {
+        step(kr[r], vr[r]);
+      } else if (j == pos) {
+        step(kn, vn);
+      }
     }
-    step(kr, vr);
   }
 
-  // block max of the running maxima, then every thread's state rescaled to it
+  // the wave's maximum, every group's state rescaled to it and summed over the
+  // groups (lanes of equal dims: DPP row rotations by 4 and 8, then shuffles)
   float bmv[1] = {m};
   group_reduce<64, true>(bmv);
-  float bm = bmv[0];
-  if (lane == 0) stat[wave] = bm;
-  __syncthreads();
-  bm = stat[0];
-#pragma unroll
-  for (int w = 1; w < kAttnThreads / 64; ++w) bm = fmaxf(bm, stat[w]);
+  const float bm = bmv[0];
   const float f = m == -INFINITY ? 0.f : expf(m - bm);
-  float part[kDim + 1];
+  float part[kSub + 1];
 #pragma unroll
-  for (int i = 0; i < kDim; ++i) part[i] = acc[i] * f;
-  part[kDim] = l * f;
-  group_reduce<64>(part);
-  if (lane == 0) {
+  for (int i = 0; i < kSub; ++i) part[i] = acc[i] * f;
+  part[kSub] = l * f;
 #pragma unroll
-    for (int i = 0; i <= kDim; ++i) red[wave][i] = part[i];
+  for (int i = 0; i <= kSub; ++i) part[i] += dpp_f32<0x124>(part[i]);
+#pragma unroll
+  for (int i = 0; i <= kSub; ++i) part[i] += dpp_f32<0x128>(part[i]);
+#pragma unroll
+  for (int i = 0; i <= kSub; ++i) part[i] += __shfl_xor(part[i], 16, 64);
+#pragma unroll
+  for (int i = 0; i <= kSub; ++i) part[i] += __shfl_xor(part[i], 32, 64);
+  if (lane < 4) {
+#pragma unroll
+    for (int i = 0; i < kSub; ++i) red[wave][d0 + i] = part[i];
+    if (lane == 0) {
+      red[wave][kDim] = part[kSub];
+      red[wave][kDim + 1] = bm;
+    }
   }
   __syncthreads();
   if (tid < kDim) {
+    float gm = red[0][kDim + 1];
+#pragma unroll
+    for (int w = 1; w < kAttnThreads / 64; ++w) gm = fmaxf(gm, red[w][kDim + 1]);
     float sacc = 0.f, sl = 0.f;
 #pragma unroll
     for (int w = 0; w < kAttnThreads / 64; ++w) {
-      sacc += red[w][tid];
-      sl += red[w][kDim];
+      const float mw = red[w][kDim + 1];
+      const float g = mw == -INFINITY ? 0.f : expf(mw - gm);
+      sacc = fmaf(red[w][tid], g, sacc);
+      sl = fmaf(red[w][kDim], g, sl);
     }
     out[bh * kDim + tid] = sacc / sl;
   }
@@ -462,6 +503,12 @@ int launch_decode_attention(const float *q, const float *k, const float *v, int6
   if (heads <= 0 || seqs_heads % heads != 0 || qkv_stride < heads * kDim)
     return fail(PLX_EINVAL, "decode_attention: rows of %lld heads %lld floats apart do not tile %lld head rows",
                 static_cast<long long>(heads), static_cast<long long>(qkv_stride), static_cast<long long>(seqs_heads));
+  // the kernel reads q, k, v and the norm weights as float2
+  const uintptr_t al8 = reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) |
+                        reinterpret_cast<uintptr_t>(v) | reinterpret_cast<uintptr_t>(q_w) |
+                        reinterpret_cast<uintptr_t>(k_w);
+  if ((al8 & 7u) != 0 || (qkv_stride & 1) != 0)
+    return fail(PLX_EINVAL, "decode_attention: q, k, v and the norm weights must be 8-byte aligned, the row stride even");
   hipLaunchKernelGGL(decode_attention_kernel, dim3(static_cast<unsigned>(seqs_heads)), dim3(kAttnThreads), 0, s, q, k,
                      v, heads, qkv_stride, q_w, k_w, eps, k_cache, v_cache, pos, max_len,
                      1.0f / sqrtf(static_cast<float>(kDim)), out);

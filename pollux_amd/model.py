@@ -149,7 +149,12 @@ def _qkv_rows(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor):
     strides = {stride_of(x) for x in (q, k, v)}
     if len(strides) == 1 and None not in strides:
         return q, k, v, strides.pop()
-    return q.contiguous(), k.contiguous(), v.contiguous(), 0
+
+    def aligned(x):  # the kernels read rows in 8- and 16-byte pieces
+        x = x.contiguous()
+        return x if x.data_ptr() % 16 == 0 else x.clone()
+
+    return aligned(q), aligned(k), aligned(v), 0
 
 
 def decode_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q_ln: RMSNorm, k_ln: RMSNorm,

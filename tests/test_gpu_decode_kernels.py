@@ -49,9 +49,12 @@ def test_rms_norm_zero_row_and_module(dev):
     assert torch.allclose(y[1], torch.ones(48, device=dev), rtol=1e-6)
 
 
-# positions below one block's width, several passes of it (299, 1500), the first position (0)
+# positions below one round of 64 (5 in a cache of 8 rows), at and across the round edges (63, 64,
+# 255, 256: a block loads 4 rounds per trip), several trips (299, 1500), the first position (0), a
+# batch of 16 sequences x 80 heads (the batched decode step)
 @pytest.mark.parametrize("b,heads,max_len,pos", [(1, 80, 1024, 64), (2, 3, 16, 0), (1, 5, 300, 299), (3, 2, 8, 5),
-                                                 (1, 4, 2048, 1500)])
+                                                 (1, 4, 2048, 1500), (2, 3, 64, 63), (1, 2, 600, 255),
+                                                 (1, 2, 600, 256), (16, 80, 256, 100)])
 def test_decode_attention(dev, b, heads, max_len, pos):
     g = torch.Generator().manual_seed(b * 1000 + heads + pos)
     c = heads * 24
@@ -84,6 +87,39 @@ def test_decode_attention(dev, b, heads, max_len, pos):
     assert torch.equal(vc[:, :, pos], v.view(b, heads, 24))
     rest = [j for j in range(max_len) if j != pos]
     assert torch.equal(kc[:, :, rest], kc0[:, :, rest]) and torch.equal(vc[:, :, rest], vc0[:, :, rest])
+
+
+def test_decode_attention_alignment(dev):
+    # a contiguous q that starts 4 bytes past a 16-byte boundary is copied to an aligned buffer by the
+    # wrapper (same result); the C ABI refuses a q that is not 8-byte aligned and an odd row stride
+    from pollux_amd import _lib
+
+    b, heads, max_len, pos = 2, 3, 32, 9
+    g = torch.Generator().manual_seed(77)
+    base = torch.randn(b * heads * 24 + 1, generator=g).to(dev)
+    q_off = base[1:].view(b, 1, heads * 24)
+    assert q_off.data_ptr() % 16 == 4
+    k = torch.randn(b, 1, heads * 24, generator=g).to(dev)
+    v = torch.randn(b, 1, heads * 24, generator=g).to(dev)
+    ln = RMSNorm(24).to(dev)
+    kc = torch.randn(b, heads, max_len, 24, generator=g).to(dev)
+    vc = torch.randn(b, heads, max_len, 24, generator=g).to(dev)
+    kc2, vc2 = kc.clone(), vc.clone()
+    p = torch.tensor(pos, dtype=torch.long, device=dev)
+    with torch.no_grad():
+        out = decode_attention(q_off, k, v, ln, ln, kc, vc, p)
+        ref = decode_attention(q_off.clone(), k, v, ln, ln, kc2, vc2, p)
+    assert torch.equal(out, ref) and torch.equal(kc, kc2)
+    lib = _lib.lib()
+    w = ln.weight.detach()
+    o = torch.empty(b * heads, 24, device=dev)
+    s = _lib.stream_of(dev)
+    for qp, stride in ((q_off.data_ptr(), 0), (ref.data_ptr(), 0), (ref.data_ptr(), 73)):
+        st = lib.plx_decode_attention(qp, k.data_ptr(), v.data_ptr(), stride, w.data_ptr(), w.data_ptr(), 1e-8,
+                                      kc.data_ptr(), vc.data_ptr(), p.data_ptr(), b * heads, heads, max_len,
+                                      o.data_ptr(), s)
+        assert (st != 0) == (qp % 8 != 0 or stride % 2 != 0)
+    torch.cuda.synchronize()
 
 
 def test_decode_attention_position_outside_cache(dev):
