@@ -979,8 +979,6 @@ constexpr int kMmTargetBlocks = 192;    // K is split until the grid holds about
 constexpr int kMmRedStride = 36;        // floats per token in the cross-wave sum (conflict-free writes)
 constexpr int kXfQuadBytes = 3 * 4 * 1024;       // fragment-order x: 3 K steps x 4 token tiles x 64 lanes x 16 B
 constexpr int64_t kMmMaxCols = 1 << 22;           // a slab of fragment-order x (3 parts) stays below 2^31 bytes
-constexpr int kBufferFlags = 0x00020000;          // raw buffer descriptor word 3 on gfx9 (gfx950)
-constexpr int kBufferOutOfRange = 0x7FFFFFF0;     // a byte offset past every buffer range used here
 
 // Words per row of the block's kp_dq tile: 3 per atom, padded to 4 mod 8 so the
 // 16 rows of a B tile read by one instruction fall into distinct banks.

@@ -369,23 +369,28 @@ __global__ __launch_bounds__(64 * kI8mmWaves, 2) void int8mm_kernel(
   const int sb = nsteps / kI8mmWaves, sx = nsteps % kI8mmWaves;
   const int s0 = wave * sb + min(wave, sx), sn = sb + (wave < sx ? 1 : 0);
 
-  // per row tile: this lane's row (clamped; rows past the end decode, never stored) and its scale
+  // per row tile: this lane's row scale (a row past the end takes the last row's: decoded, never stored)
   __half2 s2[4];
-  const int8_t *qrow[4];
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const int64_t row = row0 + 16 * r + j < rows ? row0 + 16 * r + j : rows - 1;
     s2[r] = __float2half2_rn(int8_row_scale(mu16[row]));  // exact: an fp16 value
-    qrow[r] = q + row * cols;
   }
-  const float *xrow[MT];
-  bool tok_ok[MT];
-#pragma unroll
-  for (int t = 0; t < MT; ++t) {
-    const int64_t tok = tok0 + 16 * t + j;
-    tok_ok[t] = tok < m_total;
-    xrow[t] = x + (tok_ok[t] ? tok : 0) * static_cast<int64_t>(cols);
-  }
+  // Raw buffer loads over the block's rows of q and tokens of x: a row or
+  // token past the end, a column past the row and a step past the wave's
+  // share fall outside the ranges and read as zeros (weight 0, activation 0),
+  // so no load sits under a branch or feeds a select, and the ring below keeps
+  // D steps of loads in flight (with the selects at load time every step
+  // waited for its own loads).
+  const int64_t rows_b = rows - row0 < kI8mmRows ? rows - row0 : kI8mmRows;
+  const int64_t toks_b = m_total - tok0 < TOK ? m_total - tok0 : TOK;
+  const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<int8_t *>(q + row0 * cols), static_cast<short>(0), static_cast<int>(rows_b * cols), kBufferFlags);
+  const __amdgpu_buffer_rsrc_t xrs =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(x + tok0 * cols), static_cast<short>(0),
+                                        static_cast<int>(toks_b * cols * 4), kBufferFlags);
+  const __amdgpu_buffer_rsrc_t grs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float *>(NORM ? norm_w : x), static_cast<short>(0), NORM ? cols * 4 : 0, kBufferFlags);
 
   f32x4_i8 acc[MT][4];
 #pragma unroll
@@ -397,37 +402,46 @@ __global__ __launch_bounds__(64 * kI8mmWaves, 2) void int8mm_kernel(
   for (int t = 0; t < MT; ++t) ssq[t] = 0.f;
 
   // Raw operands of one step (activations: 8 per token tile; weights: 8 bytes
-  // per row tile) in a ring of D steps: the loads of step i + D
-  // go out as step i is computed, so a wave keeps several HBM round trips in
-  // flight (one step's work is far shorter than one trip).
-  constexpr int D = MT == 4 ? 2 : 4;
-  float xv[D][MT][8];
+  // per row tile; NORM: 8 norm weights) in a ring of D steps: the loads of
+  // step i + D go out as step i is computed, so a wave keeps several HBM round
+  // trips in flight (one step's work is far shorter than one trip).
+  constexpr int D = 2;  // 2 measured faster than 3 or 4 at 5..256 tokens (fewer VGPRs: 3 waves per SIMD)
+  uint4 xv[D][MT][2];
   uint2 wv[D][4];
-  auto load_step = [&](int step, float (&xs)[MT][8], uint2 (&ws)[4]) {
+  uint4 gv[D][NORM ? 2 : 1];
+  auto load_step = [&](int step, uint4 (&xs)[MT][2], uint2 (&ws)[4], uint4 (&gs)[NORM ? 2 : 1]) {
     const int k = 32 * step + 8 * qd;
     const bool kok = k < cols && step < s0 + sn;
-    const int kk = kok ? k : 0;
-#pragma unroll
-    for (int t = 0; t < MT; ++t) {
-      const float4 *p = reinterpret_cast<const float4 *>(xrow[t] + kk);
-      const float4 a = p[0], b = p[1];
-      const bool ok = kok && tok_ok[t];
-      xs[t][0] = ok ? a.x : 0.f; xs[t][1] = ok ? a.y : 0.f; xs[t][2] = ok ? a.z : 0.f; xs[t][3] = ok ? a.w : 0.f;
-      xs[t][4] = ok ? b.x : 0.f; xs[t][5] = ok ? b.y : 0.f; xs[t][6] = ok ? b.z : 0.f; xs[t][7] = ok ? b.w : 0.f;
-    }
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const uint2 d = *reinterpret_cast<const uint2 *>(qrow[r] + kk);
-      ws[r] = kok ? d : make_uint2(0u, 0u);  // zero bytes: weight 0
+      int off = kok ? (16 * r + j) * cols + k : kBufferOutOfRange;
+      asm("" : "+v"(off));
+      ws[r] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(wrs, off, 0, 0));
+    }
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+      int off = kok ? ((16 * t + j) * cols + k) * 4 : kBufferOutOfRange;
+      asm("" : "+v"(off));
+      xs[t][0] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(xrs, off, 0, 0));
+      xs[t][1] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(xrs, off, 16, 0));
+    }
+    if constexpr (NORM) {
+      int off = kok ? 4 * k : kBufferOutOfRange;
+      asm("" : "+v"(off));
+      gs[0] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(grs, off, 0, 0));
+      gs[1] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(grs, off, 16, 0));
     }
   };
-  auto compute_step = [&](int step, const float (&xs)[MT][8], const uint2 (&ws)[4]) {
+  auto compute_step = [&](const uint4 (&xs)[MT][2], const uint2 (&ws)[4], const uint4 (&gs)[NORM ? 2 : 1]) {
     float g[8];
     if constexpr (NORM) {
-      const int k = 32 * step + 8 * qd;
-      const float4 *gp = reinterpret_cast<const float4 *>(norm_w + (k < cols ? k : 0));
-      const float4 a = gp[0], b = gp[1];
-      g[0] = a.x; g[1] = a.y; g[2] = a.z; g[3] = a.w; g[4] = b.x; g[5] = b.y; g[6] = b.z; g[7] = b.w;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        g[4 * h] = __uint_as_float(gs[h].x);
+        g[4 * h + 1] = __uint_as_float(gs[h].y);
+        g[4 * h + 2] = __uint_as_float(gs[h].z);
+        g[4 * h + 3] = __uint_as_float(gs[h].w);
+      }
     }
     bf16x8_i8 wh[4], wl[4];
 #pragma unroll
@@ -436,8 +450,14 @@ __global__ __launch_bounds__(64 * kI8mmWaves, 2) void int8mm_kernel(
     for (int t = 0; t < MT; ++t) {
       float v[8];
 #pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        v[4 * h] = __uint_as_float(xs[t][h].x);
+        v[4 * h + 1] = __uint_as_float(xs[t][h].y);
+        v[4 * h + 2] = __uint_as_float(xs[t][h].z);
+        v[4 * h + 3] = __uint_as_float(xs[t][h].w);
+      }
+#pragma unroll
       for (int e = 0; e < 8; ++e) {
-        v[e] = xs[t][e];
         if constexpr (NORM) {
           ssq[t] = fmaf(v[e], v[e], ssq[t]);
           v[e] = v[e] * g[e];
@@ -456,13 +476,13 @@ __global__ __launch_bounds__(64 * kI8mmWaves, 2) void int8mm_kernel(
     }
   };
 #pragma unroll
-  for (int u = 0; u < D; ++u) load_step(s0 + u, xv[u], wv[u]);
+  for (int u = 0; u < D; ++u) load_step(s0 + u, xv[u], wv[u], gv[u]);
   for (int i = 0; i < sn; i += D) {
 #pragma unroll
     for (int u = 0; u < D; ++u) {
       if (i + u < sn) {  // wave-uniform
-        compute_step(s0 + i + u, xv[u], wv[u]);
-        load_step(s0 + i + u + D, xv[u], wv[u]);  // past the wave's steps: zeros, no memory read past the row
+        compute_step(xv[u], wv[u], gv[u]);
+        load_step(s0 + i + u + D, xv[u], wv[u], gv[u]);  // past the wave's steps: out of range, zeros
       }
     }
   }
@@ -651,9 +671,10 @@ int int8_linear_blocks(int64_t rows, int64_t *rows_per_wave) {
 // From this many tokens the MFMA kernel runs: it reads the weights once for up
 // to 64 tokens, the GEMV once per 4 tokens.  Measured on the Pollux head
 // (50,688 x 1,920): GEMV 20.8 / 25.8 / 47.4 / 79.2 us at 1 / 2 / 4 / 5 tokens;
-// MFMA 61-62 us at 5..16 tokens (VALU-bound by the weight decode), 75 at 17,
-// 102 at 33, 165 at 65, 338 at 256 (torch F.linear on the cached fp32 cast:
-// 70-73, 76, 95, 162, 392).
+// MFMA 52-54 us at 5..16 tokens (VALU-bound by the weight decode and the exact
+// bf16 splits: ~10 VALU instructions per weight), 67 at 17, 99 at 33, 170 at
+// 65, 373 at 256 (torch F.linear on the cached fp32 cast: 70-73, 76, 95, 162,
+// 392).
 constexpr int64_t kI8mmMinTokens = 5;
 
 int64_t int8mm_row_blocks(int64_t rows) { return (rows + kI8mmRows - 1) / kI8mmRows; }

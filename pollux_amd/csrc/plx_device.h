@@ -16,6 +16,12 @@ __device__ __forceinline__ uint32_t bf16_rne_bits(float f) {
 
 __device__ __forceinline__ float bf16_bits_to_float(uint32_t b) { return __uint_as_float(b << 16); }
 
+// Raw buffer loads: descriptor word 3 on gfx9 (gfx950), and a byte offset past
+// every buffer range the kernels use (such a load reads zeros and touches no
+// memory, so a load that may fall outside its data needs no branch).
+constexpr int kBufferFlags = 0x00020000;
+constexpr int kBufferOutOfRange = 0x7FFFFFF0;
+
 // fp32 value of raw codebook coordinate k in -4..4: k * fp32(1/sqrt 8) rounded to fp32.
 __device__ __forceinline__ float raw_value_f32(int k) {
   return static_cast<float>(k) * __uint_as_float(kLeechScaleBits);
