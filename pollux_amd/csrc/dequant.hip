@@ -975,7 +975,9 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kMmRows = 32;             // output rows per block
 constexpr int kMmMaxApb = 128;          // atoms of a row per block (kp_dq tile: 32 x 388 words = 49.7 KB)
-constexpr int kMmTargetBlocks = 192;    // K is split until the grid holds about this many blocks
+constexpr int kMmTargetBlocks = 192;    // K is split until the grid holds about this many blocks,
+constexpr int kMmNoSplitBlocks = 176;   // unless the rows alone give this many (the 5,760-row stacked q/k/v:
+                                        // 180 blocks unsplit beat 360 + the split sum at 16 and 64 tokens)
 constexpr int kMmRedStride = 36;        // floats per token in the cross-wave sum (conflict-free writes)
 constexpr int kXfQuadBytes = 3 * 4 * 1024;       // fragment-order x: 3 K steps x 4 token tiles x 64 lanes x 16 B
 constexpr int64_t kMmMaxCols = 1 << 22;           // a slab of fragment-order x (3 parts) stays below 2^31 bytes
@@ -1537,7 +1539,8 @@ struct MmPlan {
 MmPlan mm_plan(int64_t rows, int64_t apr) {
   MmPlan p;
   const int64_t row_blocks = (rows + kMmRows - 1) / kMmRows;
-  int64_t s = max((apr + kMmMaxApb - 1) / kMmMaxApb, (kMmTargetBlocks + row_blocks - 1) / row_blocks);
+  const int64_t fill = row_blocks >= kMmNoSplitBlocks ? 1 : (kMmTargetBlocks + row_blocks - 1) / row_blocks;
+  int64_t s = max((apr + kMmMaxApb - 1) / kMmMaxApb, fill);
   s = max(static_cast<int64_t>(1), min(s, (apr + 3) / 4));
   const int64_t apb = (((apr + s - 1) / s) + 3) & ~static_cast<int64_t>(3);
   p.apb = static_cast<int>(apb);
