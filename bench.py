@@ -488,16 +488,17 @@ def random_packed_pollux(device):
     return PackedPolluxModel.from_packed_checkpoint(payload, device), g, payload
 
 
-def decode_workload(device, n_tokens, prompt_len=64):
-    """Greedy graph decode of n_tokens after a prompt (random packed Pollux-1920); returns a summary line."""
+def decode_workload(device, n_tokens, prompt_len=64, batch=1):
+    """Greedy graph decode of n_tokens after a prompt per sequence (random packed Pollux-1920, `batch`
+    sequences per step); returns a summary line."""
     import torch
 
     from pollux_amd.model import GraphDecoder
 
     model, g, _ = random_packed_pollux(device)
-    prompt = torch.randint(0, 50257, (1, prompt_len), generator=g, device=device)
+    prompt = torch.randint(0, 50257, (batch, prompt_len), generator=g, device=device)
     with torch.inference_mode():
-        dec = GraphDecoder(model, batch=1, greedy=True)
+        dec = GraphDecoder(model, batch=batch, greedy=True)
         first = dec.prefill(prompt).argmax(-1)
         t = dec.decode_greedy(first, 8)[:, -1]
         torch.cuda.synchronize()
@@ -507,8 +508,8 @@ def decode_workload(device, n_tokens, prompt_len=64):
         e1.record()
         e1.synchronize()
     ms = e0.elapsed_time(e1) / n_tokens
-    return (f"packed decode (graph with the argmax inside, batch 1, prompt {prompt_len}): {ms:.4f} ms/token over "
-            f"{n_tokens} tokens")
+    return (f"packed decode (graph with the argmax inside, batch {batch}, prompt {prompt_len}): {ms:.4f} ms per step "
+            f"over {n_tokens} steps ({batch * 1e3 / ms:.0f} tokens/s)")
 
 
 def decode_extras(device, prompt_len=64, new_tokens=128):
@@ -675,6 +676,8 @@ def main() -> int:
         help="for rocprofv3 runs: the packed Pollux-1920 decoder only (prefill 64 tokens, then N greedy tokens "
         "replayed from its HIP graph); prints one line with ms/token",
     )
+    ap.add_argument("--decode-batch", type=int, default=1, metavar="B",
+                    help="with --decode-workload: B sequences per decode step")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -699,7 +702,7 @@ def main() -> int:
         _lib.check(lib.plx_device_init(), "plx_device_init")
 
     if args.decode_workload:
-        print(decode_workload(dev, args.decode_workload), flush=True)
+        print(decode_workload(dev, args.decode_workload, batch=args.decode_batch), flush=True)
         return 0
 
     if args.pmc_workload:
