@@ -49,12 +49,13 @@ def test_rms_norm_zero_row_and_module(dev):
     assert torch.allclose(y[1], torch.ones(48, device=dev), rtol=1e-6)
 
 
-# positions below one round of 64 (5 in a cache of 8 rows), at and across the round edges (63, 64,
-# 255, 256: a block loads 4 rounds per trip), several trips (299, 1500), the first position (0), a
-# batch of 16 sequences x 80 heads (the batched decode step)
+# positions below one round of 64 (5 in a cache of 8 rows), at and across the round edges (63, 64)
+# and the trip edges (191, 192: a block loads 3 rounds per trip; 255, 256), several trips (299,
+# 1500), the first position (0), a batch of 16 sequences x 80 heads (the batched decode step)
 @pytest.mark.parametrize("b,heads,max_len,pos", [(1, 80, 1024, 64), (2, 3, 16, 0), (1, 5, 300, 299), (3, 2, 8, 5),
-                                                 (1, 4, 2048, 1500), (2, 3, 64, 63), (1, 2, 600, 255),
-                                                 (1, 2, 600, 256), (16, 80, 256, 100)])
+                                                 (1, 4, 2048, 1500), (2, 3, 64, 63), (1, 2, 600, 191),
+                                                 (1, 2, 600, 192), (1, 2, 600, 255), (1, 2, 600, 256),
+                                                 (16, 80, 256, 100)])
 def test_decode_attention(dev, b, heads, max_len, pos):
     g = torch.Generator().manual_seed(b * 1000 + heads + pos)
     c = heads * 24
