@@ -1032,7 +1032,8 @@ __device__ __forceinline__ void group_codes(uint32_t d0, uint32_t d1, uint32_t d
 // Fragment-order copy of the activations for dqmm_kernel (fp32 x, and bf16 x
 // above 32 tokens).  One thread per 16-byte fragment position (slab, quad Q,
 // K step s, token tile t, lane): x[64 slab + 16t + (lane & 15)][96Q + 32s +
-// 8(lane >> 4) .. +8), zero for tokens >= m and columns >= cols, stored at
+// 8(lane >> 4) .. +8), zero for tokens >= m and columns >= cols (token tiles
+// t >= `tiles`, which the GEMM does not read, are not written), stored at
 // xf[slab][Q][part][s][t][lane].  bf16 x is one part.  fp32 x is split
 // exactly into three bf16 parts, x = h + m + l (h = bf16(x), m = bf16(x - h),
 // l = x - h - m, exact while the parts stay normal, |x| >= ~2^-110; inf / nan
@@ -1040,7 +1041,7 @@ __device__ __forceinline__ void group_codes(uint32_t d0, uint32_t d1, uint32_t d
 // activations.
 template <bool XF32>
 __global__ __launch_bounds__(256) void xfrag_kernel(const void *__restrict__ x, int64_t m_total, int64_t cols,
-                                                    int64_t n_quads_row, uint4 *__restrict__ xf) {
+                                                    int64_t n_quads_row, int tiles, uint4 *__restrict__ xf) {
   constexpr int XP = XF32 ? 3 : 1;
   constexpr int kQuadFrags = kXfQuadBytes / 16;  // 768 per part
   const int64_t per_slab = n_quads_row * kQuadFrags;
@@ -1049,6 +1050,7 @@ __global__ __launch_bounds__(256) void xfrag_kernel(const void *__restrict__ x, 
   const int lane = static_cast<int>(f & 63);
   const int64_t rest = f >> 6;  // (3Q + s) * 4 + t
   const int t = static_cast<int>(rest & 3);
+  if (t >= tiles) return;  // a token tile the GEMM does not read (it reads `tiles` per slab)
   const int64_t qs = rest >> 2;  // 3Q + s
   const int64_t quad = qs / 3, within = f - quad * kQuadFrags;
   const int64_t tok = static_cast<int64_t>(blockIdx.y) * 64 + 16 * t + (lane & 15);
@@ -1101,13 +1103,14 @@ __global__ __launch_bounds__(256) void xfrag_kernel(const void *__restrict__ x, 
 // fragments (kNfVec * 256 columns, padding of the last quad included).
 constexpr int kNfVec = 8;
 __global__ __launch_bounds__(256) void normfrag_kernel(const float *__restrict__ x, const float *__restrict__ w,
-                                                       int64_t m_total, int cols, int64_t n_quads_row, float eps,
-                                                       uint2 *__restrict__ xf) {
+                                                       int64_t m_total, int cols, int64_t n_quads_row, int tiles,
+                                                       float eps, uint2 *__restrict__ xf) {
   constexpr int kQuadFrags = kXfQuadBytes / 16;
   const int lane = threadIdx.x & 63;
   const int64_t tok = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
   const int64_t slab = tok >> 6;
   const int t = static_cast<int>((tok >> 4) & 3), tl = static_cast<int>(tok & 15);
+  if (t >= tiles) return;  // a token tile the GEMM does not read (the whole wave: one row)
   const int n4 = cols >> 2;
   const bool live = tok < m_total;
   const float4 *xr = reinterpret_cast<const float4 *>(x + (live ? tok : 0) * static_cast<int64_t>(cols));
@@ -1692,10 +1695,12 @@ int launch_dequant_linear_multi(const DqlTarget *targets, int n, int64_t cols, c
     const int64_t slabs = (m + 63) / 64, nq = (apr + 3) / 4;
     const dim3 gx(static_cast<unsigned>(nq * 3), static_cast<unsigned>(slabs));
     const bool copy = mm_x_copy(x_is_f32 != 0, m);
+    // token tiles per slab the GEMM reads (its MT below): the copies write only these
+    const int tiles = m > 32 ? 4 : m > 16 ? 2 : 1;
     if (norm && copy && nq * 12 <= 32 * kNfVec) {
       // the norm writes the fragment-order copy itself (rows that fit normfrag_kernel's registers)
       hipLaunchKernelGGL(normfrag_kernel, dim3(static_cast<unsigned>(slabs * 16)), dim3(256), 0, s,
-                         static_cast<const float *>(x), norm_w, m, static_cast<int>(cols), nq, norm_eps,
+                         static_cast<const float *>(x), norm_w, m, static_cast<int>(cols), nq, tiles, norm_eps,
                          reinterpret_cast<uint2 *>(wsb));
       st = check_launch("normfrag_kernel");
     } else {
@@ -1706,9 +1711,10 @@ int launch_dequant_linear_multi(const DqlTarget *targets, int n, int64_t cols, c
       }
       if (copy) {
         if (x_is_f32)
-          hipLaunchKernelGGL((xfrag_kernel<true>), gx, dim3(256), 0, s, x, m, cols, nq, reinterpret_cast<uint4 *>(wsb));
+          hipLaunchKernelGGL((xfrag_kernel<true>), gx, dim3(256), 0, s, x, m, cols, nq, tiles,
+                             reinterpret_cast<uint4 *>(wsb));
         else
-          hipLaunchKernelGGL((xfrag_kernel<false>), gx, dim3(256), 0, s, x, m, cols, nq,
+          hipLaunchKernelGGL((xfrag_kernel<false>), gx, dim3(256), 0, s, x, m, cols, nq, tiles,
                              reinterpret_cast<uint4 *>(wsb));
         st = check_launch("xfrag_kernel");
       } else {
