@@ -1097,7 +1097,7 @@ __global__ __launch_bounds__(256) void xfrag_kernel(const void *__restrict__ x, 
 // same values (the sum of squares in rmsnorm_kernel's order: lane l holds
 // float4 l + 64k of the row, fmaf over k and the four components, then the
 // wave sum).  One wave per token row of each 64-token slab; rows >= m write
-// zeros.  Fragment 32k + j holds the row's columns 8(32k + j) .. +8, i.e.
+// zeros, rows of token tiles the GEMM does not read (t >= tiles) nothing.  Fragment 32k + j holds the row's columns 8(32k + j) .. +8, i.e.
 // float4s 64k + 2j and 64k + 2j + 1: lanes 2j and 2j + 1 each write their
 // 8-byte half of the fragment in every part.  Rows of up to 32 * kNfVec
 // fragments (kNfVec * 256 columns, padding of the last quad included).
