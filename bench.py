@@ -171,41 +171,121 @@ def cpu_baseline(x_gpu, idx_gpu, target_atoms):
         "near_tie": near,
         "not_near_tie": int(len(diff)) - near,
         "near_tie_envelope": "24 * 2^-24 * sum|x_i c_i| (any fp32 summation order)",
+        "requantize_config1": requantize_parity(x_gpu.device),
     }
     return base, parity
 
 
-def extras(device, iters=20):
+def requantize_parity(device):
+    """Config 1 through the fused requantize (row scale + NN-B) against the reference's CPU composition.
+
+    Every atom of the seeded 1152x1152 fp32 N(0, 0.02) weight; disagreements
+    classified as near_tie / sigma_ulp / real (oracle/parity.py), with the
+    sigma statistics against the stated bar (within 2 fp32 ulp).
+    """
     import torch
 
-    from pollux_amd import castor, dequantize_h24
+    from oracle import parity, torch_ref
+    from pollux_amd import castor
+
+    g = torch.Generator().manual_seed(1152)
+    w = torch.randn(1152, 1152, generator=g) * 0.02
+    got = castor.requantize_h24(w.to(device))
+    idx_ref, sig_ref, _ = torch_ref.requantize(w)
+    c = parity.classify_requantize(w, got["indices"].cpu(), got["sigma"].cpu(), idx_ref, sig_ref)
+    c.pop("real_at")
+    c["sigma_bar"] = f"row RMS within {parity.SIGMA_BAR_ULP} fp32 ulp of torch's CPU reduction"
+    c["case"] = "config 1 (1152x1152 fp32 N(0, 0.02)), every atom, fused requantize vs oracle/torch_ref.requantize"
+    return c
+
+
+def extras(device, iters=24, sets=4):
+    """Pack / unpack / dequant at config-4 size, each call on the next of `sets` distinct buffer sets.
+
+    One set is 16,777,200 int64 indices (134 MB) + their packed bytes (37.7 MB);
+    4 sets (688 MB) cycle so that a set's buffers were last touched 516 MB of
+    traffic earlier, twice the 256 MB Infinity Cache: each call streams from
+    HBM.  Dequant writes 805 MB of fp16 per call.  Rates: per Python call
+    (median of 5 rounds of `iters` calls, after >= 0.3 s of warmup calls) and
+    per kernel (HIP events on the launch stream around every launch).
+    """
+    import torch
+
+    from pollux_amd import _lib, castor, dequantize_h24
 
     out = {}
     n = 16_777_200  # config 4: 209,715 rows of 1920 = 80 atoms/row
-    g = torch.Generator(device=device).manual_seed(7)
-    idx = torch.randint(0, 196561, (n,), generator=g, device=device, dtype=torch.int64)
-    packed = castor.pack_indices(idx)
-    t = time_gpu(lambda: castor.pack_indices(idx), iters, 10, 5, 0.3)
-    out["pack_GBps"] = (8 + 2.25) * n / t / 1e9
-    t = time_gpu(lambda: castor.unpack_indices(packed, n), iters, 10, 5, 0.3)
-    out["unpack_GBps"] = (2.25 + 8) * n / t / 1e9
     rows, cols = 209_715, 1920
+    g = torch.Generator(device=device).manual_seed(7)
+    idx = [torch.randint(0, 196561, (n,), generator=g, device=device, dtype=torch.int64) for _ in range(sets)]
+    packed = [castor.pack_indices(i) for i in idx]
     sig = (torch.rand(rows, generator=g, device=device) * 0.045 + 0.005).half()
-    t = time_gpu(lambda: dequantize_h24(packed, sig, rows, cols), iters, 10, 5, 0.3)
-    out["dequant_GBps"] = (2.25 * n + 48 * n + 2 * rows) / t / 1e9
+    cyc = {"k": 0}
+
+    def rot(fn):
+        def call():
+            k = cyc["k"] = (cyc["k"] + 1) % sets
+            return fn(k)
+        return call
+
+    unit = {"pack": (8 + 2.25) * n, "unpack": (2.25 + 8) * n, "dequant": 2.25 * n + 48 * n + 2 * rows}
+    calls = {
+        "pack": (rot(lambda k: castor.pack_indices(idx[k])), _lib.PROF_PACK),
+        "unpack": (rot(lambda k: castor.unpack_indices(packed[k], n)), _lib.PROF_UNPACK),
+        "dequant": (rot(lambda k: dequantize_h24(packed[k], sig, rows, cols)), _lib.PROF_DEQUANT),
+    }
+    for name, (fn, kid) in calls.items():
+        t, k_ms = _profiled(fn, iters, kid, warmup=10, rounds=5, warm_s=0.3)
+        out[f"{name}_GBps"] = unit[name] / t / 1e9
+        out[f"{name}_hbm_frac"] = unit[name] / t / PEAK_HBM_BPS
+        out[f"{name}_kernel_us"] = k_ms * 1e3
+        out[f"{name}_kernel_GBps"] = unit[name] / (k_ms / 1e3) / 1e9
+        out[f"{name}_kernel_hbm_frac"] = unit[name] / (k_ms / 1e3) / PEAK_HBM_BPS
     out["hbm_peak_GBps"] = PEAK_HBM_BPS / 1e9
-    for k in ("pack", "unpack", "dequant"):
-        out[f"{k}_hbm_frac"] = out[f"{k}_GBps"] * 1e9 / PEAK_HBM_BPS
-    out["scale"] = ("16,777,200 indices / atoms (BASELINE config 4 size), rows of 1920; median of 5 rounds of "
-                    f"{iters} back-to-back calls after >= 0.3 s of warmup calls")
+    out["bytes_per_call"] = {k: int(v) for k, v in unit.items()}
+    out["scale"] = (f"16,777,200 indices / atoms (BASELINE config 4 size), rows of 1920; each call on the next of "
+                    f"{sets} distinct buffer sets ({sets} x 172 MB, twice the 256 MB Infinity Cache between two "
+                    f"touches of a set); per call: median of 5 rounds of {iters} back-to-back calls after >= 0.3 s "
+                    "of warmup calls; per kernel: HIP events around every launch on its stream")
+    del idx, packed
     return out
 
 
-def gemv_extras(device, copies=200, m_gemm=64, replays=5):
+def hbm_workload(device, calls):
+    """The HBM-bound kernels on rotating buffers, for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs."""
+    import torch
+
+    from pollux_amd import castor, dequantize_h24, optim
+
+    n, rows, cols, sets = 16_777_200, 209_715, 1920, 4
+    g = torch.Generator(device=device).manual_seed(7)
+    idx = [torch.randint(0, 196561, (n,), generator=g, device=device, dtype=torch.int64) for _ in range(sets)]
+    packed = [castor.pack_indices(i) for i in idx]
+    sig = (torch.rand(rows, generator=g, device=device) * 0.045 + 0.005).half()
+    for k in range(calls):
+        castor.pack_indices(idx[k % sets])
+    for k in range(calls):
+        castor.unpack_indices(packed[k % sets], n)
+    for k in range(calls):
+        dequantize_h24(packed[k % sets], sig, rows, cols)
+    torch.cuda.synchronize()
+    del idx, packed
+    shapes = [(r, c) for r, c in C2_SHAPES]
+    states = [_optim_state(device, shapes, g) for _ in range(3)]
+    heat = torch.tensor(0.5, device=device)
+    for k in range(calls):
+        sc = optim.step_scalars(heat, k, optim.width_inertia(1152), device)
+        for st in states[k % 3]:
+            optim.pollux_h24_step_(*st, heat=heat, step=k, width_inertia=1.0, scalars=sc)
+    torch.cuda.synchronize()
+
+
+def gemv_extras(device, copies=400, m_gemm=64, replays=5):
     """Config 5: fused dequant-GEMV (M=1) and dequant-GEMM (M=64) on [7680,1920] and [1920,7680].
 
-    `copies` calls, each on a distinct packed weight (>= 256 MB in total, above
-    the 256 MB Infinity Cache, so the compressed stream is read from HBM), are
+    `copies` calls, each on a distinct packed weight (400 x 1.38 MB = 553 MB,
+    more than twice the 256 MB Infinity Cache, so the compressed stream is read
+    from HBM), are
     captured in one HIP graph; the graph is replayed and HIP events on the
     replay stream give the device time per call (kernel plus graph dispatch,
     without the Python call overhead).  Replay outputs are checked against an
@@ -274,40 +354,104 @@ def gemv_extras(device, copies=200, m_gemm=64, replays=5):
     return out
 
 
-def optim_extras(device, mats, iters=10):
-    """Fused optimiser step + requantize (pollux.py:836-884) of the config-2 latents.
+POLLUX1920_H24 = (
+    [("tok_emb", 50688, 1920), ("pos_emb", 1024, 1920), ("head", 50688, 1920)]
+    + [(f"blocks.{i}.{n}", r, c) for i in range(18) for n, r, c in (
+        ("attn.q_proj", 1920, 1920), ("attn.k_proj", 1920, 1920), ("attn.v_proj", 1920, 1920),
+        ("attn.o_proj", 1920, 1920), ("mlp.fc1", 7680, 1920), ("mlp.fc2", 1920, 7680))]
+)  # every >= 2-D H24 tensor pollux_step updates (pollux.py:828-888): 41,369,600 atoms
 
-    One step = plx_pollux_step_h24 on each of the four matrices: the Adam /
-    speed-cap / decay update (one HBM pass: grad, m, v, latent read, m, v,
-    latent written = 28 B per element) followed by the requantize.
+
+def _optim_state(device, shapes, g):
+    """(p, grad, m, v, latent) per shape: grad N(0, 1e-3), m N(0, 3e-4), v U(0, 1e-6), latent N(0, 0.02)."""
+    import torch
+
+    out = []
+    for r, c in shapes:
+        out.append((torch.empty(r, c, device=device), torch.randn(r, c, generator=g, device=device) * 1e-3,
+                    torch.randn(r, c, generator=g, device=device) * 3e-4,
+                    torch.rand(r, c, generator=g, device=device) * 1e-6,
+                    torch.randn(r, c, generator=g, device=device) * 0.02))
+    return out
+
+
+def optim_extras(device, mats, iters=9, sets=3):
+    """Fused optimiser step + requantize (pollux.py:828-888).
+
+    config 2: one step = the four Pollux-1152 latents, per parameter
+    (plx_pollux_step_h24, four calls) and batched (plx_pollux_step_h24_batch:
+    four update passes, one scoring sweep); each step on the next of `sets`
+    distinct optimiser states (3 x 318 MB), so the update streams from HBM.
+    The update kernel alone (28 B per element: grad, m, v, latent read; m, v,
+    latent written) is timed by HIP events around every launch.
+    Pollux-1920: one batched step over every H24 tensor of the model (18
+    layers' q/k/v/o/fc1/fc2, tok_emb, pos_emb, head: 41.4 M atoms).
     """
     import torch
 
-    from pollux_amd import optim
+    from pollux_amd import _lib, optim
 
     g = torch.Generator(device=device).manual_seed(11)
-    state = []
-    for w in mats:
-        state.append((torch.randn(w.shape, generator=g, device=device) * 1e-3,
-                      torch.zeros_like(w), torch.zeros_like(w), w.clone(), torch.empty_like(w)))
+    shapes = [tuple(w.shape) for w in mats]
+    states = [_optim_state(device, shapes, g) for _ in range(sets)]
     heat = torch.tensor(0.5, device=device)
     inertia = optim.width_inertia(1152)
     counter = torch.zeros((), dtype=torch.int64, device=device)  # the optimiser's device-resident step counter
+    cyc = {"k": 0}
 
     def step():
+        cyc["k"] = (cyc["k"] + 1) % sets
         sc = optim.step_scalars(heat, counter, inertia, device)  # once per step, as pollux.py:815-820
-        for grad, m, v, lat, p in state:
-            optim.pollux_h24_step_(p, grad, m, v, lat, heat=heat, step=counter, width_inertia=inertia, scalars=sc)
+        for st in states[cyc["k"]]:
+            optim.pollux_h24_step_(*st, heat=heat, step=counter, width_inertia=inertia, scalars=sc)
         counter.add_(1)
 
-    t = time_gpu(step, iters, 3)
-    n_el = sum(w.numel() for w in mats)
-    return {
+    def step_batched():
+        cyc["k"] = (cyc["k"] + 1) % sets
+        sc = optim.step_scalars(heat, counter, inertia, device)
+        optim.pollux_h24_step_many_(states[cyc["k"]], heat=heat, step=counter, width_inertia=inertia, scalars=sc)
+        counter.add_(1)
+
+    n_el = sum(r * c for r, c in shapes)
+    t, adam_ms = _profiled(step, iters, _lib.PROF_ADAM, warmup=3)
+    t_b, _ = _profiled(step_batched, iters, _lib.PROF_ADAM, warmup=3)
+    adam_bytes = 28 * n_el / len(shapes)  # per launch, averaged over the four matrices
+    out = {
         "step_ms": t * 1e3,
         "atoms_per_s": n_el / 24 / t,
-        "note": "4 x plx_pollux_step_h24 (fused Adam/speed-cap/decay update + requantize) on the config-2 latents",
+        "batched_step_ms": t_b * 1e3,
+        "batched_atoms_per_s": n_el / 24 / t_b,
+        "update_kernel_us_avg": adam_ms * 1e3,
+        "update_kernel_GBps": adam_bytes / (adam_ms / 1e3) / 1e9,
+        "update_kernel_hbm_frac": adam_bytes / (adam_ms / 1e3) / PEAK_HBM_BPS,
         "update_bytes_per_element": 28,
+        "note": f"config-2 latents; step_ms: 4 x plx_pollux_step_h24 (fused Adam/speed-cap/decay update + "
+                f"requantize); batched: plx_pollux_step_h24_batch; each step on the next of {sets} distinct "
+                "optimiser states (318 MB each); update kernel timed by HIP events on its stream",
     }
+    del states
+    torch.cuda.empty_cache()
+    # a whole Pollux-1920 step's H24 tensors
+    shapes = [(r, c) for _, r, c in POLLUX1920_H24]
+    state = _optim_state(device, shapes, g)
+    inertia = optim.width_inertia(1920)
+    atoms = sum(r * c for r, c in shapes) // 24
+
+    def full_step():
+        sc = optim.step_scalars(heat, counter, inertia, device)
+        optim.pollux_h24_step_many_(state, heat=heat, step=counter, width_inertia=inertia, scalars=sc)
+        counter.add_(1)
+
+    t_f, nn_ms = _profiled(full_step, 3, 0, warmup=1)
+    out["pollux1920_step"] = {
+        "atoms": atoms, "step_ms": t_f * 1e3, "atoms_per_s": atoms / t_f, "nn_kernel_ms": nn_ms,
+        "nn_kernel_mfma_frac": FLOP_PER_ATOM * atoms / (nn_ms / 1e3) / PEAK_BF16_FLOPS,
+        "note": "plx_pollux_step_h24_batch over all 111 H24 tensors of Pollux-1920 (18 x q/k/v/o 1920x1920, "
+                "fc1 7680x1920, fc2 1920x7680; tok_emb and head 50688x1920; pos_emb 1024x1920): 111 update "
+                "passes and one scoring sweep; synthetic state (latent N(0, 0.02))"}
+    del state
+    torch.cuda.empty_cache()
+    return out
 
 
 def pack_time_extras(mats, iters=5):
@@ -349,8 +493,12 @@ def make_c4(device, seed=404):
     return x
 
 
-def _nn_profiled(fn, iters):
-    """(seconds per call, nn_kernel ms per launch) of fn over iters calls, nn_kernel timed by HIP events."""
+def _profiled(fn, iters, kernel=0, warmup=0, rounds=1, warm_s=0.0):
+    """(seconds per call, selected kernel's ms per launch) of fn, the kernel timed by HIP events.
+
+    kernel: a PLX_PROF_* id (0 = nn_kernel, 1 pack, 2 unpack, 3 dequant, 4 the optimiser update); the
+    events are recorded on the kernel's launch stream around every launch of the timed calls.
+    """
     import ctypes
 
     import torch
@@ -358,12 +506,21 @@ def _nn_profiled(fn, iters):
     from pollux_amd import _lib
 
     lib = _lib.lib()
+    if warmup or warm_s:
+        time_gpu(fn, 0, warmup, 1, warm_s)
     torch.cuda.synchronize()
+    _lib.check(lib.plx_profile_select(kernel), "plx_profile_select")
     _lib.check(lib.plx_profile_begin(), "plx_profile_begin")
-    t = time_gpu(fn, iters, 0)
+    t = time_gpu(fn, iters, 0, rounds)
     tot_ms, launches = ctypes.c_double(), ctypes.c_int64()
     _lib.check(lib.plx_profile_end(ctypes.byref(tot_ms), ctypes.byref(launches)), "plx_profile_end")
+    _lib.check(lib.plx_profile_select(0), "plx_profile_select")
     return t, tot_ms.value / max(1, launches.value)
+
+
+def _nn_profiled(fn, iters):
+    """(seconds per call, nn_kernel ms per launch) of fn over iters calls, nn_kernel timed by HIP events."""
+    return _profiled(fn, iters, 0)
 
 
 def sweep_extras(device, mode="bf16", steps=10):
@@ -648,7 +805,7 @@ def gemv_headline(gemv):
         "workload": "BASELINE config 5 at batch 1: y = x W^T with W the packed 18-bit indices + fp16 row scales "
         "of a 7680x1920 and a 1920x7680 weight (never materialised), bf16 x, fp32 accumulation and output",
         "bytes": "compressed stream: packed indices + sigma16 + x (bf16) + y (fp32) per call",
-        "timing": "HIP graph of 200 calls on distinct packed copies (276 MB, above the 256 MB MALL), replayed 5x",
+        "timing": "HIP graph of 400 calls on distinct packed copies (553 MB, twice the 256 MB MALL), replayed 5x",
     }
 
 
@@ -663,10 +820,12 @@ def main() -> int:
     ap.add_argument("--mode", default="bf16", choices=["bf16", "fp32"])
     ap.add_argument(
         "--pmc-workload",
-        choices=["c4", "c2"],
+        choices=["c4", "c2", "hbm"],
         default=None,
         help="for rocprofv3 --pmc runs: 5 copies of a 256 MiB fp32 tensor (HBM-counter calibration), then "
-        "--steps headline (c4) steps or config-2 requantize steps (c2); prints nothing",
+        "--steps headline (c4) steps, config-2 requantize steps (c2), or (hbm) --steps calls each of pack, "
+        "unpack and dequant at config-4 size on 4 rotating buffer sets and of the config-2 optimiser step on "
+        "3 rotating states; prints nothing",
     )
     ap.add_argument(
         "--decode-workload",
@@ -711,7 +870,9 @@ def main() -> int:
         for _ in range(5):
             dst.copy_(src)
         del src, dst
-        if args.pmc_workload == "c2":
+        if args.pmc_workload == "hbm":
+            hbm_workload(dev, args.steps)
+        elif args.pmc_workload == "c2":
             mats = make_c2(dev)
             for _ in range(args.steps):
                 for w in mats:

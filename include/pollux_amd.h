@@ -201,6 +201,36 @@ int plx_pollux_step_h24(const float *grad, float *m, float *v, float *latent, in
                         uint8_t *packed_out, float *weight_out, float *adam_norm_out,
                         void *workspace, size_t workspace_bytes, void *stream);
 
+/* One H24 parameter of plx_pollux_step_h24_batch: the per-parameter
+ * arguments of plx_pollux_step_h24. */
+typedef struct plx_pollux_step_item {
+  const float *grad;     /* float[rows*cols], 16-byte aligned */
+  float *m, *v, *latent; /* float[rows*cols], 16-byte aligned, updated in place */
+  int64_t rows, cols;    /* cols % 24 == 0 */
+  float *sigma_out;      /* float[rows] */
+  int32_t *idx_out;      /* int32[rows*cols/24] */
+  uint8_t *packed_out;   /* uint8[((N+3)/4)*9] or NULL */
+  float *weight_out;     /* float[rows*cols] or NULL: the parameter's new data */
+  float *adam_norm_out;  /* float[1] or NULL: |s|_2 over the parameter */
+} plx_pollux_step_item;
+
+/* Workspace (device bytes) plx_pollux_step_h24_batch needs for these items
+ * (items is a HOST array). */
+size_t plx_pollux_step_batch_workspace_bytes(const plx_pollux_step_item *items, int n_items);
+
+/* One optimiser step of every H24 parameter of a pollux_step call: per
+ * parameter the update of plx_pollux_step_h24 (one pass over grad, m, v and
+ * the latent), then the requantize of all new latents with one scoring sweep
+ * over all their atoms (plx_requantize_batch).  m, v and the latents are
+ * bit-identical to n_items plx_pollux_step_h24 calls; indices equal them up
+ * to near-ties.  scalars: the DEVICE float[9] of plx_pollux_step_h24, shared
+ * by every item (the reference computes them once per step: one heat, one
+ * step counter, one width_inertia for all matrices, pollux.py:785, 815-820,
+ * 849-852).  items is a HOST array.  Replaces the loop over the H24 tensors
+ * of pollux_step (pollux.py:828-888), tok_emb, pos_emb and head included. */
+int plx_pollux_step_h24_batch(const plx_pollux_step_item *items, int n_items, const float *scalars, int mode,
+                              void *workspace, size_t workspace_bytes, void *stream);
+
 /* ---- dequantization (pollux.py:485-507) -------------------------------- */
 /* w16 = fp16(fp16(codebook16[unpack(packed)] * sigma16[row]) * fp32(1/sqrt 2)),
  * shape [rows, cols] as raw fp16 bits.  Replaces PackedH24Linear.materialize
@@ -392,12 +422,20 @@ int plx_int8_embed(const int8_t *q, const uint16_t *mu16, int64_t vocab, int64_t
                    float *out, void *stream);
 
 /* ---- kernel timing (diagnostics; no counterpart in the reference) ------ */
-/* While enabled, every launch of the quantizer's scoring kernel (nn_kernel)
- * is bracketed by HIP events recorded on its launch stream (up to 4096
- * launches).  plx_profile_begin() clears and enables recording;
- * plx_profile_end() disables it, waits for the recorded events and returns
- * the summed kernel time (ms) and the number of launches.  Used by bench.py
- * for the roofline's per-launch kernel duration. */
+/* While enabled, every launch of the selected kernel (default: the
+ * quantizer's scoring kernel nn_kernel) is bracketed by HIP events recorded
+ * on its launch stream (up to 4096 launches).  plx_profile_select() picks
+ * the kernel (while recording is off); plx_profile_begin() clears and
+ * enables recording; plx_profile_end() disables it, waits for the recorded
+ * events and returns the summed kernel time (ms) and the number of
+ * launches.  Used by bench.py for the roofline's per-launch kernel duration
+ * and the HBM kernels' bandwidth. */
+#define PLX_PROF_NN 0      /* nn_kernel (plx_quantize / plx_requantize*) */
+#define PLX_PROF_PACK 1    /* pack_kernel (plx_pack_indices) */
+#define PLX_PROF_UNPACK 2  /* unpack_kernel (plx_unpack_indices) */
+#define PLX_PROF_DEQUANT 3 /* dequant_kernel (plx_dequant_f16) */
+#define PLX_PROF_ADAM 4    /* adam_h24_kernel (plx_pollux_step_h24*) */
+int plx_profile_select(int kernel);
 int plx_profile_begin(void);
 int plx_profile_end(double *total_ms, int64_t *launches);
 

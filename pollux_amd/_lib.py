@@ -18,6 +18,7 @@ LIB_PATH = Path(__file__).resolve().parent / "lib" / "libpollux_amd.so"
 PLX_OK, PLX_EINVAL, PLX_EHIP, PLX_ENOMEM = 0, 1, 2, 3
 NN_BF16_SCORES, NN_FP32_SCORES, NN_PACK_FP32 = 0, 1, 2
 DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
+PROF_NN, PROF_PACK, PROF_UNPACK, PROF_DEQUANT, PROF_ADAM = 0, 1, 2, 3, 4  # plx_profile_select
 
 _vp, _i64, _int, _sz = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_size_t
 
@@ -42,6 +43,8 @@ SIGNATURES = {
     "plx_requantize_noalloc": (_int, [_vp, _i64, _i64, _int, _vp, _vp, _vp, _vp, _vp]),
     "plx_pollux_step_workspace_bytes": (_sz, [_i64, _i64]),
     "plx_pollux_step_h24": (_int, [_vp, _vp, _vp, _vp, _i64, _i64, _vp, _int, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "plx_pollux_step_batch_workspace_bytes": (_sz, [_vp, _int]),
+    "plx_pollux_step_h24_batch": (_int, [_vp, _int, _vp, _int, _vp, _sz, _vp]),
     "plx_quantize_int8_rows": (_int, [_vp, _i64, _i64, _vp, _vp, _vp]),
     "plx_dequant_int8_rows": (_int, [_vp, _vp, _i64, _i64, _vp, _vp]),
     "plx_dequant_f16": (_int, [_vp, _i64, _vp, _i64, _i64, _vp, _vp]),
@@ -62,9 +65,19 @@ SIGNATURES = {
                                     _vp]),
     "plx_prefill_attention": (_int, [_vp, _vp, _vp, _i64, _vp, _vp, ctypes.c_float, _vp, _vp, _i64, _i64, _i64, _i64,
                                      _i64, _vp, _vp]),
+    "plx_profile_select": (_int, [_int]),
     "plx_profile_begin": (_int, []),
     "plx_profile_end": (_int, [_vp, _vp]),
 }
+
+class PolluxStepItem(ctypes.Structure):
+    """plx_pollux_step_item (include/pollux_amd.h)."""
+
+    _fields_ = [
+        ("grad", _vp), ("m", _vp), ("v", _vp), ("latent", _vp), ("rows", _i64), ("cols", _i64),
+        ("sigma_out", _vp), ("idx_out", _vp), ("packed_out", _vp), ("weight_out", _vp), ("adam_norm_out", _vp),
+    ]
+
 
 class RequantizeItem(ctypes.Structure):
     """plx_requantize_item (include/pollux_amd.h)."""

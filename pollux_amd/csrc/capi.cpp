@@ -159,7 +159,11 @@ int plx_requantize(const float *latent, int64_t rows, int64_t cols, int mode, fl
   if (rows == 0) return PLX_OK;
   PLX_REQUIRE(latent != nullptr && sigma_out != nullptr && idx_out != nullptr, "plx_requantize: null pointer");
   const int64_t n_atoms = rows * (cols / kDim);
-  int st = launch_row_rms(latent, rows, cols, sigma_out, nullptr, as_stream(stream));
+  int st = check_quantize_args(latent, n_atoms, workspace, workspace_bytes);  // before anything is written
+  if (st != PLX_OK) return st;
+  const DeviceTables *tab = nullptr;
+  if ((st = get_tables(&tab)) != PLX_OK) return st;
+  st = launch_row_rms(latent, rows, cols, sigma_out, nullptr, as_stream(stream));
   if (st != PLX_OK) return st;
   return launch_quantize(latent, sigma_out, rows, cols, n_atoms, mode, idx_out, packed_out, weight_out, workspace,
                          workspace_bytes, as_stream(stream));
@@ -225,13 +229,81 @@ int plx_pollux_step_h24(const float *grad, float *m, float *v, float *latent, in
               "plx_pollux_step_h24: workspace of %zu bytes is smaller than the %zu needed", workspace_bytes, need);
   const int64_t n_atoms = rows * (cols / kDim);
   const size_t qws = (quantize_workspace_bytes(n_atoms) + 255) & ~static_cast<size_t>(255);
-  int st = launch_adam_h24(grad, m, v, latent, n_atoms, scalars, adam_norm_out, static_cast<uint8_t *>(workspace) + qws,
+  int st = check_quantize_args(latent, n_atoms, workspace, qws);  // before anything is written
+  if (st != PLX_OK) return st;
+  const DeviceTables *tab = nullptr;
+  if ((st = get_tables(&tab)) != PLX_OK) return st;
+  st = launch_adam_h24(grad, m, v, latent, n_atoms, scalars, adam_norm_out, static_cast<uint8_t *>(workspace) + qws,
                            as_stream(stream));
   if (st != PLX_OK) return st;
   st = launch_row_rms(latent, rows, cols, sigma_out, nullptr, as_stream(stream));
   if (st != PLX_OK) return st;
   return launch_quantize(latent, sigma_out, rows, cols, n_atoms, mode, idx_out, packed_out, weight_out, workspace, qws,
                          as_stream(stream));
+}
+
+size_t plx_pollux_step_batch_workspace_bytes(const plx_pollux_step_item *items, int n_items) {
+  if (items == nullptr || n_items <= 0) return 0;
+  int64_t total = 0;
+  size_t adam = 0;
+  for (int i = 0; i < n_items; ++i) {
+    const plx_pollux_step_item &x = items[i];
+    if (x.rows < 0 || x.cols <= 0 || x.cols % kDim != 0) return 0;
+    const int64_t n = x.rows * (x.cols / kDim);
+    total += n;
+    adam += (adam_h24_workspace_bytes(n) + 255) & ~static_cast<size_t>(255);
+  }
+  return ((quantize_workspace_bytes(total) + 255) & ~static_cast<size_t>(255)) + adam;
+}
+
+int plx_pollux_step_h24_batch(const plx_pollux_step_item *items, int n_items, const float *scalars, int mode,
+                              void *workspace, size_t workspace_bytes, void *stream) {
+  PLX_REQUIRE(n_items >= 0 && n_items <= 4096, "plx_pollux_step_h24_batch: bad item count %d", n_items);
+  PLX_REQUIRE(mode == PLX_NN_BF16_SCORES || mode == PLX_NN_FP32_SCORES, "plx_pollux_step_h24_batch: unknown mode %d",
+              mode);
+  if (n_items == 0) return PLX_OK;
+  PLX_REQUIRE(items != nullptr && scalars != nullptr, "plx_pollux_step_h24_batch: null item array or scalars");
+  // every check before the first launch: a refused call writes nothing
+  int64_t total = 0;
+  for (int i = 0; i < n_items; ++i) {
+    const plx_pollux_step_item &x = items[i];
+    PLX_REQUIRE(x.rows >= 0 && x.cols > 0, "plx_pollux_step_h24_batch: item %d has a bad shape (%lld, %lld)", i,
+                static_cast<long long>(x.rows), static_cast<long long>(x.cols));
+    PLX_REQUIRE(x.cols % kDim == 0, "Pollux requires in_features divisible by H24_DIM=24; got %lld (item %d).",
+                static_cast<long long>(x.cols), i);
+    if (x.rows == 0) continue;
+    PLX_REQUIRE(x.grad != nullptr && x.m != nullptr && x.v != nullptr && x.latent != nullptr &&
+                    x.sigma_out != nullptr && x.idx_out != nullptr,
+                "plx_pollux_step_h24_batch: item %d has a null pointer", i);
+    const uintptr_t al = reinterpret_cast<uintptr_t>(x.grad) | reinterpret_cast<uintptr_t>(x.m) |
+                         reinterpret_cast<uintptr_t>(x.v) | reinterpret_cast<uintptr_t>(x.latent);
+    PLX_REQUIRE((al & 15u) == 0, "plx_pollux_step_h24_batch: item %d: grad, m, v and latent must be 16-byte aligned",
+                i);
+    total += x.rows * (x.cols / kDim);
+  }
+  if (total == 0) return PLX_OK;
+  const size_t need = plx_pollux_step_batch_workspace_bytes(items, n_items);
+  PLX_REQUIRE(workspace != nullptr && workspace_bytes >= need,
+              "plx_pollux_step_h24_batch: workspace of %zu bytes is smaller than the %zu needed", workspace_bytes, need);
+  const size_t qws = (quantize_workspace_bytes(total) + 255) & ~static_cast<size_t>(255);
+  int st = check_quantize_args(items[0].latent, total, workspace, qws);
+  if (st != PLX_OK) return st;
+  const DeviceTables *tab = nullptr;
+  if ((st = get_tables(&tab)) != PLX_OK) return st;
+  hipStream_t s = as_stream(stream);
+  uint8_t *adam_ws = static_cast<uint8_t *>(workspace) + qws;
+  std::vector<RequantItem> its;
+  its.reserve(static_cast<size_t>(n_items));
+  for (int i = 0; i < n_items; ++i) {
+    const plx_pollux_step_item &x = items[i];
+    if (x.rows == 0) continue;
+    const int64_t n = x.rows * (x.cols / kDim);
+    st = launch_adam_h24(x.grad, x.m, x.v, x.latent, n, scalars, x.adam_norm_out, adam_ws, s);
+    if (st != PLX_OK) return st;
+    adam_ws += (adam_h24_workspace_bytes(n) + 255) & ~static_cast<size_t>(255);
+    its.push_back(RequantItem{x.latent, x.rows, x.cols, x.sigma_out, x.idx_out, x.packed_out, x.weight_out});
+  }
+  return launch_requantize_batch(its.data(), static_cast<int>(its.size()), mode, workspace, qws, s);
 }
 
 int plx_quantize_layer_pack(const float *w, int64_t rows, int64_t cols, uint8_t *packed_out, uint16_t *sigma16_out,
@@ -243,7 +315,11 @@ int plx_quantize_layer_pack(const float *w, int64_t rows, int64_t cols, uint8_t 
   if (rows == 0) return PLX_OK;
   PLX_REQUIRE(w != nullptr && packed_out != nullptr && sigma16_out != nullptr, "plx_quantize_layer_pack: null pointer");
   const int64_t n_atoms = rows * (cols / kDim);
-  int st = launch_row_rms(w, rows, cols, nullptr, sigma16_out, as_stream(stream));
+  int st = check_quantize_args(w, n_atoms, workspace, workspace_bytes);  // before anything is written
+  if (st != PLX_OK) return st;
+  const DeviceTables *tab = nullptr;
+  if ((st = get_tables(&tab)) != PLX_OK) return st;
+  st = launch_row_rms(w, rows, cols, nullptr, sigma16_out, as_stream(stream));
   if (st != PLX_OK) return st;
   return launch_quantize(w, nullptr, rows, cols, n_atoms, PLX_NN_PACK_FP32, idx_out, packed_out, nullptr, workspace,
                          workspace_bytes, as_stream(stream));

@@ -120,7 +120,9 @@ int launch_dequant_f16(const uint8_t *packed, const uint16_t *sigma16, int64_t r
   if (n_atoms == 0) return PLX_OK;
   const int64_t pb = (n_atoms + 3) / 4 * 9;
   const dim3 g(static_cast<unsigned>((n_atoms + kDqAtoms - 1) / kDqAtoms));
+  profile_before(s, PLX_PROF_DEQUANT);
   hipLaunchKernelGGL(dequant_kernel, g, dim3(kThreads), 0, s, packed, pb, sigma16, n_atoms, apr, tab->kp_dq, w16);
+  profile_after(s, PLX_PROF_DEQUANT);
   return check_launch("dequant_kernel");
 }
 
@@ -833,9 +835,10 @@ int launch_gemv1_planes_l(const uint8_t *planes, const uint16_t *sigma16, int64_
 int launch_gemv1_planes(const uint8_t *planes, const uint16_t *sigma16, int64_t rows, int64_t apr, const void *x,
                         const DeviceTables *tab, int round_w, float *y, hipStream_t s) {
   if (apr >= 160) return launch_gemv1_planes_l<64>(planes, sigma16, rows, apr, x, tab, round_w, y, s);
-  // 16 lanes (32 rows per block) only while the block's records fit its 2 vectors per thread
+  // 16 lanes (32 rows per block) only while a lane's share is at most kG1Atoms atoms and the
+  // block's records fit its 2 vectors per thread
   if (apr >= 16)
-    return (rows + 31) / 32 < 192 || 6 * 32 * apr + 31 > 16 * 2 * 512
+    return (rows + 31) / 32 < 192 || apr > static_cast<int64_t>(kG1Atoms) * 16 || 6 * 32 * apr + 31 > 16 * 2 * 512
                ? launch_gemv1_planes_l<32>(planes, sigma16, rows, apr, x, tab, round_w, y, s)
                : launch_gemv1_planes_l<16>(planes, sigma16, rows, apr, x, tab, round_w, y, s);
   return launch_gemv1_planes_l<8>(planes, sigma16, rows, apr, x, tab, round_w, y, s);

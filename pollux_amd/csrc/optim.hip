@@ -176,12 +176,14 @@ int launch_adam_h24(const float *grad, float *m, float *v, float *latent, int64_
   const int64_t blocks = opt_blocks(n_atoms);
   if (blocks > 0x7FFFFFFFll) return fail(PLX_EINVAL, "pollux_step_h24: %lld atoms exceed one launch", static_cast<long long>(n_atoms));
   float *partial = static_cast<float *>(workspace);
+  profile_before(s, PLX_PROF_ADAM);
   if (opt_threads(n_atoms) == kOptLarge)
     hipLaunchKernelGGL((adam_h24_kernel<kOptLarge>), dim3(static_cast<unsigned>(blocks)), dim3(kOptLarge), 0, s, grad, m,
                        v, latent, n_atoms, scalars, partial);
   else
     hipLaunchKernelGGL((adam_h24_kernel<kOptSmall>), dim3(static_cast<unsigned>(blocks)), dim3(kOptSmall), 0, s, grad, m,
                        v, latent, n_atoms, scalars, partial);
+  profile_after(s, PLX_PROF_ADAM);
   int st = check_launch("adam_h24_kernel");
   if (st != PLX_OK) return st;
   if (adam_norm_out) {

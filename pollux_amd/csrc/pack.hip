@@ -114,12 +114,14 @@ int launch_pack(const void *idx, int idx_is_i64, int64_t n, uint8_t *out, hipStr
   const int64_t n_groups = (n + 3) / 4;
   const int64_t blocks = (n_groups + kThreads - 1) / kThreads;
   const bool vec_ok = host_aligned16(idx) && host_aligned16(out);
+  profile_before(s, PLX_PROF_PACK);
   if (idx_is_i64)
     hipLaunchKernelGGL(pack_kernel<true>, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0, s, idx, n, out,
                        n_groups, vec_ok);
   else
     hipLaunchKernelGGL(pack_kernel<false>, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0, s, idx, n, out,
                        n_groups, vec_ok);
+  profile_after(s, PLX_PROF_PACK);
   return check_launch("pack_kernel");
 }
 
@@ -127,8 +129,10 @@ int launch_unpack(const uint8_t *packed, int64_t num_indices, int64_t *out, hipS
   const int64_t n_groups = (num_indices + 3) / 4;
   const int64_t blocks = (n_groups + kThreads - 1) / kThreads;
   const bool vec_ok = host_aligned16(packed) && host_aligned16(out);
+  profile_before(s, PLX_PROF_UNPACK);
   hipLaunchKernelGGL(unpack_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0, s, packed, num_indices,
                      out, n_groups, vec_ok);
+  profile_after(s, PLX_PROF_UNPACK);
   return check_launch("unpack_kernel");
 }
 

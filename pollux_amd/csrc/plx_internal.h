@@ -90,8 +90,9 @@ int check_hip(hipError_t e, const char *what);
 int check_launch(const char *what);
 
 // Event bracketing of the scoring kernel (profile.cpp); no-ops unless enabled.
-void profile_before(hipStream_t s);
-void profile_after(hipStream_t s);
+// `kernel`: the PLX_PROF_* id of the bracketed kernel; only the selected one is recorded.
+void profile_before(hipStream_t s, int kernel = PLX_PROF_NN);
+void profile_after(hipStream_t s, int kernel = PLX_PROF_NN);
 
 // Kernel launchers (one per .hip file); return PLX_* status.
 int launch_pack(const void *idx, int idx_is_i64, int64_t n, uint8_t *out, hipStream_t s);
@@ -102,6 +103,9 @@ int launch_quantize(const float *x, const float *sigma, int64_t rows, int64_t co
                     int mode, int32_t *idx_out, uint8_t *packed_out, float *weight_out,
                     void *workspace, size_t workspace_bytes, hipStream_t s);
 size_t quantize_workspace_bytes(int64_t n_atoms);
+// The checks launch_quantize makes before its first launch (workspace size, 16-byte alignment of the
+// input and the workspace, grid limits); composite entry points run them before launching anything.
+int check_quantize_args(const float *x, int64_t n_atoms, const void *workspace, size_t workspace_bytes);
 // The allocation-free requantize (quantize.hip): its workspace is the file-scope
 // device array `scratch`, whose per-device address noalloc_setup() resolves
 // once per device (current device) and caches.

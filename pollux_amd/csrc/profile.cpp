@@ -1,4 +1,6 @@
-// HIP-event timing of the quantizer's scoring kernel for bench.py.
+// HIP-event timing of one selected kernel (plx_profile_select: the quantizer's
+// scoring kernel by default, or pack / unpack / dequant / the optimiser
+// update) for bench.py.
 //
 // Events come from a pool created at plx_profile_begin(), so nothing is
 // allocated inside the timed region; recording stops silently when the pool
@@ -20,6 +22,7 @@ struct Profile {
   std::vector<hipEvent_t> start, stop;
   int used = 0;
   bool open = false;  // a start event has been recorded without its stop
+  int kernel = PLX_PROF_NN;
 };
 
 Profile &prof() {
@@ -29,17 +32,17 @@ Profile &prof() {
 
 }  // namespace
 
-void profile_before(hipStream_t s) {
+void profile_before(hipStream_t s, int kernel) {
   Profile &p = prof();
   std::lock_guard<std::mutex> lock(p.mu);
-  if (!p.enabled || p.used >= static_cast<int>(p.start.size())) return;
+  if (!p.enabled || kernel != p.kernel || p.used >= static_cast<int>(p.start.size())) return;
   if (hipEventRecord(p.start[p.used], s) == hipSuccess) p.open = true;
 }
 
-void profile_after(hipStream_t s) {
+void profile_after(hipStream_t s, int kernel) {
   Profile &p = prof();
   std::lock_guard<std::mutex> lock(p.mu);
-  if (!p.enabled || !p.open) return;
+  if (!p.enabled || kernel != p.kernel || !p.open) return;
   if (hipEventRecord(p.stop[p.used], s) == hipSuccess) ++p.used;
   p.open = false;
 }
@@ -49,6 +52,16 @@ void profile_after(hipStream_t s) {
 using namespace plx;
 
 extern "C" {
+
+int plx_profile_select(int kernel) {
+  if (kernel < PLX_PROF_NN || kernel > PLX_PROF_ADAM)
+    return fail(PLX_EINVAL, "plx_profile_select: unknown kernel id %d", kernel);
+  Profile &p = prof();
+  std::lock_guard<std::mutex> lock(p.mu);
+  if (p.enabled) return fail(PLX_EINVAL, "plx_profile_select: recording is on (call it before plx_profile_begin)");
+  p.kernel = kernel;
+  return PLX_OK;
+}
 
 int plx_profile_begin(void) {
   Profile &p = prof();

@@ -1092,18 +1092,28 @@ size_t quantize_workspace_bytes(int64_t n_atoms) {
   return keys_bytes(n_atoms) + recs_bytes(n_atoms) + static_cast<size_t>(n_atoms) * 48;
 }
 
-int launch_quantize(const float *x, const float *sigma, int64_t rows, int64_t cols, int64_t n_atoms, int mode,
-                    int32_t *idx_out, uint8_t *packed_out, float *weight_out, void *workspace,
-                    size_t workspace_bytes, hipStream_t s) {
-  (void)rows;
+int check_quantize_args(const float *x, int64_t n_atoms, const void *workspace, size_t workspace_bytes) {
   if (n_atoms <= 0) return PLX_OK;
   if (workspace == nullptr || workspace_bytes < quantize_workspace_bytes(n_atoms))
     return fail(PLX_EINVAL, "quantize: workspace of %zu bytes is smaller than the %zu needed for %lld atoms",
                 workspace_bytes, quantize_workspace_bytes(n_atoms), static_cast<long long>(n_atoms));
   if ((reinterpret_cast<uintptr_t>(x) & 15u) != 0 || (reinterpret_cast<uintptr_t>(workspace) & 15u) != 0)
     return fail(PLX_EINVAL, "quantize: input and workspace must be 16-byte aligned");
+  const int64_t ablocks = (n_atoms + kAtomsPerBlock - 1) / kAtomsPerBlock;
+  if (ablocks * choose_slices(ablocks) > 0x7FFFFFFFll || (n_atoms * 6 + 255) / 256 > 0x7FFFFFFFll)
+    return fail(PLX_EINVAL, "quantize: %lld atoms exceed one launch", static_cast<long long>(n_atoms));
+  return PLX_OK;
+}
+
+int launch_quantize(const float *x, const float *sigma, int64_t rows, int64_t cols, int64_t n_atoms, int mode,
+                    int32_t *idx_out, uint8_t *packed_out, float *weight_out, void *workspace,
+                    size_t workspace_bytes, hipStream_t s) {
+  (void)rows;
+  if (n_atoms <= 0) return PLX_OK;
+  int st = check_quantize_args(x, n_atoms, workspace, workspace_bytes);
+  if (st != PLX_OK) return st;
   const DeviceTables *tab = nullptr;
-  int st = get_tables(&tab);
+  st = get_tables(&tab);
   if (st != PLX_OK) return st;
   uint8_t *ws = static_cast<uint8_t *>(workspace);
   const bool fused = sigma != nullptr;
@@ -1261,6 +1271,8 @@ int launch_requantize_noalloc(const float *latent, int64_t rows, int64_t cols, i
   }
   if (ws == nullptr)
     return fail(PLX_EINVAL, "plx_requantize_noalloc: call plx_device_init() on device %d first", dev);
+  // every argument check before the first launch: a refused call writes nothing
+  if ((st = check_quantize_args(latent, n_atoms, ws, kScratchBytes)) != PLX_OK) return st;
   if ((st = launch_row_rms(latent, rows, cols, sigma_out, nullptr, s)) != PLX_OK) return st;
   return launch_quantize(latent, sigma_out, rows, cols, n_atoms, mode, idx_out, packed_out, weight_out, ws,
                          kScratchBytes, s);

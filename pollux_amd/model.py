@@ -23,7 +23,7 @@ by its fp16 weight cast to fp32 (pollux.py:562-563).
 from __future__ import annotations
 
 from dataclasses import dataclass
-from typing import Any
+from typing import Any, Callable
 
 import torch
 import torch.nn as nn
@@ -569,79 +569,38 @@ class GraphDecoder:
         return self.history[:, start:start + n].clone()
 
 
-# ---- sampling (generate.py:228-278) ------------------------------------------------
-
-
-def mask_inactive_vocab(logits: torch.Tensor, active_vocab: int) -> torch.Tensor:
-    """Logits beyond the tokenizer vocabulary set to -inf (generate.py:228-233)."""
-    if logits.size(-1) <= active_vocab:
-        return logits
-    mask = torch.arange(logits.size(-1), device=logits.device) >= active_vocab
-    return logits.masked_fill(mask, float("-inf"))
-
-
-def apply_repetition_penalty(logits: torch.Tensor, ids: torch.Tensor, penalty: float) -> None:
-    """In place: seen tokens' positive logits divided by the penalty, negative ones multiplied (generate.py:240-253)."""
-    if penalty <= 1.0:
-        return
-    seen = torch.unique(ids)
-    seen = seen[(seen >= 0) & (seen < logits.numel())]
-    if seen.numel() == 0:
-        return
-    vals = logits[seen]
-    logits[seen] = torch.where(vals > 0, vals / penalty, vals * penalty)
-
-
-def apply_top_k(logits: torch.Tensor, k: int) -> torch.Tensor:
-    """Keep the k largest logits (generate.py:256-262)."""
-    if k <= 0 or k >= logits.numel():
-        return logits
-    _, keep = torch.topk(logits, k)
-    drop = torch.ones_like(logits, dtype=torch.bool)
-    drop.scatter_(0, keep, False)
-    return logits.masked_fill(drop, float("-inf"))
-
-
-def apply_top_p(logits: torch.Tensor, p: float) -> torch.Tensor:
-    """Nucleus filter: keep the smallest prefix of the sorted distribution reaching p (generate.py:265-278)."""
-    if p <= 0.0 or p >= 1.0:
-        return logits
-    sorted_logits, order = torch.sort(logits, descending=True)
-    cumulative = torch.cumsum(torch.softmax(sorted_logits, dim=-1), dim=-1)
-    remove = cumulative > p
-    remove[1:] = remove[:-1].clone()
-    remove[0] = False
-    drop = torch.zeros_like(logits, dtype=torch.bool)
-    drop.scatter_(0, order, remove)
-    return logits.masked_fill(drop, float("-inf"))
-
-
 @torch.inference_mode()
-def generate(model: PackedPolluxModel, ids: list[int], *, max_new_tokens: int = 80, temperature: float = 0.6,
-             top_k: int = 50, top_p: float = 0.9, repetition_penalty: float = 1.1, active_vocab: int | None = None,
-             eos_id: int = 50256, generator: torch.Generator | None = None, use_cache: bool = True,
-             use_graph: bool = False) -> list[int]:
-    """The token loop of generate.generate (generate.py:286-336) on token ids.
+def generate(model: PackedPolluxModel, ids: list[int], *, max_new_tokens: int = 80,
+             sample: Callable[[torch.Tensor, torch.Tensor], int] | None = None, eos_id: int = 50256,
+             use_cache: bool = True, use_graph: bool = False) -> list[int]:
+    """The model side of generate.generate's token loop (generate.py:286-336) on token ids.
 
-    Sampling follows the reference step for step (vocabulary mask, repetition
-    penalty, temperature, top-k, top-p, multinomial).  With ``use_cache`` the
-    prompt is prefilled once and each new token is one ``decode`` position;
-    once the sequence is longer than seq_len the reference's window
-    ``idx[:, -seq_len:]`` restarts the positions at 0, so from then on every
-    step recomputes the window, exactly as the reference does.
-    ``use_graph`` (with ``use_cache``): the prefill and the decode steps are
-    replayed from a ``GraphDecoder``'s graphs (captured once per call, worth it
-    for long generations); the sampling stays on the host's stream.
+    Each step's fp32 logits of the last position ([vocab]) go to
+    ``sample(logits, ids)`` with the sequence so far (``ids`` [1, t] int64 on
+    the device), which returns the next token id; the caller supplies the
+    reference's own sampling there (vocabulary mask, repetition penalty,
+    temperature, top-k / top-p, multinomial).  ``sample=None`` is greedy:
+    the first index of the largest logit, as ``torch.argmax``.  With
+    ``use_cache`` the prompt is prefilled once and each new token is one
+    ``decode`` position; once the sequence is longer than seq_len the
+    reference's window ``idx[:, -seq_len:]`` restarts the positions at 0, so
+    from then on every step recomputes the window, exactly as the reference
+    does.  ``use_graph`` (with ``use_cache``): the prefill and the decode
+    steps are replayed from a ``GraphDecoder``'s graphs (captured once per
+    call, worth it for long generations); ``sample`` runs on the host's stream
+    between replays.  Prompt ids outside [0, vocab_size) are refused.
     """
     device = model.pos_emb.weight.device
     seq_len = int(model.cfg.seq_len)
-    v_active = active_vocab or eos_id + 1
-    ids = [t for t in ids if 0 <= t < v_active] or [eos_id]
+    vocab = int(model.cfg.vocab_size)
+    if not ids:
+        raise ValueError("generate needs at least one prompt token")
+    if any(t < 0 or t >= vocab for t in ids):
+        raise ValueError(f"prompt token ids must lie in [0, {vocab})")
     idx = torch.tensor([ids], device=device, dtype=torch.long)
     dec = GraphDecoder(model, batch=1) if (use_cache and use_graph) else None
     cache = model.new_cache(1, seq_len) if (use_cache and dec is None) else None
     started = False
-    logits = None
     for _ in range(max_new_tokens):
         if dec is not None and idx.shape[1] <= seq_len:
             logits = dec.decode(idx[:, -1]) if started else dec.prefill(idx)
@@ -653,13 +612,10 @@ def generate(model: PackedPolluxModel, ids: list[int], *, max_new_tokens: int = 
                 logits = model.decode(idx[:, -1], cache)
         else:
             logits = model(idx[:, -seq_len:], last_only=True)[:, -1]
-        logits = mask_inactive_vocab(logits.float()[0], v_active)
-        apply_repetition_penalty(logits, idx[0], repetition_penalty)
-        if temperature > 0:
-            logits = logits / max(float(temperature), 1e-8)
-        logits = apply_top_p(apply_top_k(logits, top_k), top_p)
-        probs = torch.softmax(logits, dim=-1)
-        next_id = int(torch.multinomial(probs, num_samples=1, generator=generator).item())
+        row = logits.float()[0]
+        next_id = int(torch.argmax(row).item()) if sample is None else int(sample(row.clone(), idx))
+        if not 0 <= next_id < vocab:
+            raise ValueError(f"sample returned token id {next_id} outside [0, {vocab})")
         idx = torch.cat([idx, torch.tensor([[next_id]], device=device)], dim=1)
         if next_id == eos_id:
             break

@@ -140,3 +140,77 @@ def pollux_h24_step_(
     if return_codes:
         return norm, {"sigma": sigma, "indices": idx, "packed": packed}
     return norm
+
+
+def pollux_h24_step_many_(
+    params: list[tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]],
+    *,
+    heat: torch.Tensor | float,
+    step: torch.Tensor | int,
+    width_inertia: float,
+    mode: str | None = None,
+    return_codes: bool = False,
+    scalars: torch.Tensor | None = None,
+):
+    """pollux.py:828-888 for every H24 parameter of one step: pollux_h24_step_ on each (p, grad, m, v, latent).
+
+    One update pass per parameter, then one scoring sweep over the atoms of all
+    their new latents (plx_pollux_step_h24_batch): m, v, latents and the norms
+    are bit-identical to separate pollux_h24_step_ calls, indices equal them up
+    to near-ties.  All tensors on one device; the step scalars are shared (one
+    heat, step counter and width_inertia per step, pollux.py:785, 815-820).
+    Returns the list of 0-dim step norms (and, with ``return_codes``, the list
+    of dict(sigma, indices, packed)).
+    """
+    if not params:
+        return ([], []) if return_codes else []
+    dev = params[0][0].device
+    scal = scalars if scalars is not None else step_scalars(heat, step, float(width_inertia), dev)
+    if scal.dtype != torch.float32 or scal.numel() != 9 or scal.device != dev:
+        raise ValueError("pollux_h24_step_many_: scalars must be the 9 float32 values of step_scalars on the device")
+    scal = scal.contiguous()
+    items, keep, outs = [], [], []
+    for k, (p, grad, m, v, latent) in enumerate(params):
+        if p.dim() != 2:
+            raise ValueError(f"pollux_h24_step_many_: parameter {k} is {p.dim()}D, expected 2D")
+        rows, cols = p.shape
+        assert_row_aligned_in_features(cols)
+        for name, t in (("grad", grad), ("m", m), ("v", v), ("latent", latent), ("p", p)):
+            _lib.require_device(t, f"pollux_h24_step_many_ {name}")
+            if t.device != dev:
+                raise ValueError("pollux_h24_step_many_: all tensors must be on one device")
+            if t.shape != p.shape or t.dtype != torch.float32:
+                raise ValueError(f"pollux_h24_step_many_: {name} of parameter {k} must be float32 {tuple(p.shape)}")
+        for name, t in (("m", m), ("v", v), ("latent", latent)):
+            if not t.is_contiguous():
+                raise ValueError(f"pollux_h24_step_many_: {name} is updated in place and must be contiguous")
+        n = rows * (cols // H24_DIM)
+        g = grad.detach().contiguous()
+        o = {
+            "sigma": torch.empty(rows, dtype=torch.float32, device=dev),
+            "indices": torch.empty(n, dtype=torch.int32, device=dev),
+            "packed": torch.empty(((n + 3) // 4) * BYTES_PER_CHUNK, dtype=torch.uint8, device=dev)
+            if return_codes else None,
+            "norm": torch.empty((), dtype=torch.float32, device=dev),
+        }
+        w = p.data if p.data.is_contiguous() else torch.empty_like(p.data)
+        keep.append((g, w, p))
+        outs.append(o)
+        items.append(_lib.PolluxStepItem(_lib.ptr(g), _lib.ptr(m), _lib.ptr(v), _lib.ptr(latent), rows, cols,
+                                         _lib.ptr(o["sigma"]), _lib.ptr(o["indices"]), _lib.ptr(o["packed"]),
+                                         _lib.ptr(w), _lib.ptr(o["norm"])))
+    arr = (_lib.PolluxStepItem * len(items))(*items)
+    nws = int(_lib.lib().plx_pollux_step_batch_workspace_bytes(arr, len(items)))
+    ws = torch.empty(max(nws, 16), dtype=torch.uint8, device=dev)
+    with torch.cuda.device(dev):
+        st = _lib.lib().plx_pollux_step_h24_batch(arr, len(items), _lib.ptr(scal),
+                                                  _castor._MODES[mode or _castor._nn_mode], _lib.ptr(ws), nws,
+                                                  _lib.stream_of(dev))
+    _lib.check(st, "pollux_h24_step_many_")
+    for g, w, p in keep:
+        if w is not p.data:
+            p.data.copy_(w)
+    norms = [o["norm"] for o in outs]
+    if return_codes:
+        return norms, [{"sigma": o["sigma"], "indices": o["indices"], "packed": o["packed"]} for o in outs]
+    return norms

@@ -76,6 +76,37 @@ def test_validation_happens_before_device_work():
     assert b"plane layout" in lib.plx_last_error()
 
 
+def test_composite_entry_points_refuse_before_their_first_launch():
+    # non-null dummy addresses (never dereferenced): a too-small workspace or a misaligned latent must be
+    # refused as PLX_EINVAL before row_rms / adam / any table build runs, not as a launch error (PLX_EHIP)
+    lib = _lib.lib()
+    a, b, c = 0x10000, 0x20000, 0x30000
+    need = int(lib.plx_quantize_workspace_bytes(4 * 48))
+    assert lib.plx_requantize(a, 4, 1152, 0, b, c, None, None, c, need - 1, None) == _lib.PLX_EINVAL
+    assert b"workspace" in lib.plx_last_error()
+    assert lib.plx_requantize(a + 4, 4, 1152, 0, b, c, None, None, c, need, None) == _lib.PLX_EINVAL
+    assert b"aligned" in lib.plx_last_error()
+    assert lib.plx_quantize_layer_pack(a, 4, 1152, b, c, None, c, need - 1, None) == _lib.PLX_EINVAL
+    assert b"workspace" in lib.plx_last_error()
+    step_need = int(lib.plx_pollux_step_workspace_bytes(4, 1152))
+    assert step_need > need
+    assert lib.plx_pollux_step_h24(a, a, a, a, 4, 1152, a, 0, b, c, None, None, None, c, step_need - 1,
+                                   None) == _lib.PLX_EINVAL
+    assert lib.plx_pollux_step_h24(a, a, a, a + 4, 4, 1152, a, 0, b, c, None, None, None, c, step_need,
+                                   None) == _lib.PLX_EINVAL
+    assert b"aligned" in lib.plx_last_error()
+    # the batched step: too small a workspace, then a misaligned latent in its second item
+    items = (_lib.PolluxStepItem * 2)(_lib.PolluxStepItem(a, a, a, a, 4, 1152, b, c, None, None, None),
+                                     _lib.PolluxStepItem(a, a, a, a, 2, 48, b, c, None, None, None))
+    bneed = int(lib.plx_pollux_step_batch_workspace_bytes(items, 2))
+    assert bneed > int(lib.plx_quantize_workspace_bytes(4 * 48 + 4))
+    assert lib.plx_pollux_step_h24_batch(items, 2, a, 0, c, bneed - 1, None) == _lib.PLX_EINVAL
+    assert b"workspace" in lib.plx_last_error()
+    items[1].latent = a + 4
+    assert lib.plx_pollux_step_h24_batch(items, 2, a, 0, c, bneed, None) == _lib.PLX_EINVAL
+    assert b"aligned" in lib.plx_last_error()
+
+
 def test_host_helpers_mirror_reference():
     assert castor.h24_linear_atom_count(1152, 1152) == 55296
     with pytest.raises(ValueError):

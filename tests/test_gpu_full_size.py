@@ -13,9 +13,10 @@ import numpy as np
 import pytest
 import torch
 
-from oracle import codebook as cb
 from oracle import nn, packing, torch_ref
 from pollux_amd import castor
+
+import c3_stress  # tests/ is on sys.path (pytest's rootdir-relative import of this directory)
 
 pytestmark = pytest.mark.gpu
 
@@ -68,45 +69,15 @@ def test_config3_boundary_stress_full_size(dev):
     # Pollux-1920 layer, 1,843,200 atoms in lattice units; 5% of atoms replaced by
     # midpoints of code pairs at raw inner product 16 plus N(0, 1e-3) noise, 5%
     # by random directions at norm sqrt 2 (the origin boundary).
-    shapes = [(5760, 1920), (1920, 1920), (7680, 1920), (1920, 7680)]
-    g = torch.Generator().manual_seed(303)
-    xs = []
-    for r, c in shapes:
-        w = torch.randn(r, c, generator=g) * 0.02
-        x, _ = torch_ref.lattice_input(w)
-        xs.append(x.reshape(-1, 24))
-    x = torch.cat(xs)
+    x, mid_at, near_at = c3_stress.build(303)
     n = x.shape[0]
-    assert n == 1_843_200
-    rng = np.random.default_rng(303)
-    perm = rng.permutation(n)
-    mid_at, near_at = perm[: n // 20], perm[n // 20: n // 10]
-    raw = cb.codebook_int8()
-    c32 = cb.codebook_f32()
-    a = rng.integers(1, 196561, len(mid_at))
-    b = np.zeros_like(a)
-    todo = np.arange(len(a))
-    while len(todo):  # a partner at raw inner product 16 (the true-Leech contact)
-        for lo in range(0, len(todo), 4096):
-            t = todo[lo: lo + 4096]
-            cand = rng.integers(1, 196561, (len(t), 256))
-            ip = np.einsum("nkd,nd->nk", raw[cand].astype(np.int32), raw[a[t]].astype(np.int32))
-            hit = ip == 16
-            ok = hit.any(axis=1)
-            b[t[ok]] = cand[ok, hit[ok].argmax(axis=1)]
-        todo = todo[b[todo] == 0]
-    mids = 0.5 * (c32[a] + c32[b]) + rng.normal(0, 1e-3, (len(a), 24)).astype(np.float32)
-    dirs = rng.normal(size=(len(near_at), 24))
-    dirs = dirs / np.linalg.norm(dirs, axis=1, keepdims=True) * np.sqrt(2.0)
-    x[torch.from_numpy(mid_at)] = torch.from_numpy(mids.astype(np.float32))
-    x[torch.from_numpy(near_at)] = torch.from_numpy(dirs.astype(np.float32))
     got = castor.quantize_indices(x.to(dev), mode="bf16").long()
     _stream_checks(dev, got)
     got_cpu = got.cpu().numpy()
     # sample the stressed atoms and the ordinary ones separately
     _sample_check(x[torch.from_numpy(mid_at)], got_cpu[mid_at], "B", 31, "config3 midpoints", max_near=0.05)
     _sample_check(x[torch.from_numpy(near_at)], got_cpu[near_at], "B", 32, "config3 near-origin")
-    rest = np.setdiff1d(np.arange(n), perm[: n // 10])
+    rest = np.setdiff1d(np.arange(n), np.concatenate([mid_at, near_at]))
     _sample_check(x[torch.from_numpy(rest)], got_cpu[rest], "B", 33, "config3 unmodified")
 
 

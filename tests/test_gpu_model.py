@@ -8,9 +8,9 @@ Bars (stated):
   materialised fp16 weights on the GPU;
 * KV-cached decode against the full-prefix forward of the same prefix:
   relative L2 <= 1e-5 per position;
-* token-level generation with and without the cache, greedy (top_k = 1) and
-  sampled with one seed, past seq_len (where the reference's sliding window
-  restarts the positions): identical token ids.
+* token-level generation with and without the cache, greedy and with a
+  caller's seeded sampling step, past seq_len (where the reference's sliding
+  window restarts the positions): identical token ids.
 """
 
 import pytest
@@ -112,19 +112,31 @@ def test_chunked_prefill_and_batch(dev, packed):
             assert _rel(both[b:b + 1], model.decode(nxt[b:b + 1], c1)) <= 1e-5
 
 
-@pytest.mark.parametrize("top_k,temperature", [(1, 0.6), (20, 0.9)])
-def test_generate_with_and_without_cache(dev, packed, top_k, temperature):
+def _seeded_sampler(generator, temperature):
+    """A caller's sampling step: softmax at a temperature and one multinomial draw."""
+    def sample(logits, ids):
+        probs = torch.softmax(logits / temperature, dim=-1)
+        return int(torch.multinomial(probs, 1, generator=generator).item())
+    return sample
+
+
+@pytest.mark.parametrize("sampled", [False, True])
+def test_generate_with_and_without_cache(dev, packed, sampled):
     model = PackedPolluxModel.from_packed_checkpoint(str(packed[0]), dev)
     prompt = [3, 14, 15, 9, 26]
     runs = []
     for use_cache, use_graph in ((True, False), (False, False), (True, True)):
         g = torch.Generator(device=dev).manual_seed(7)
-        runs.append(generate(model, prompt, max_new_tokens=20, top_k=top_k, temperature=temperature, top_p=0.95,
-                             repetition_penalty=1.1, active_vocab=90, eos_id=89, generator=g, use_cache=use_cache,
+        sample = _seeded_sampler(g, 0.9) if sampled else None
+        runs.append(generate(model, prompt, max_new_tokens=20, sample=sample, eos_id=95, use_cache=use_cache,
                              use_graph=use_graph))
     print(f"[model] generated {runs[0]}", flush=True)
     assert runs[0] == runs[1] == runs[2]
     assert runs[0][:5] == prompt and len(runs[0]) > 16  # went past seq_len unless eos came first
+    with pytest.raises(ValueError):
+        generate(model, [96], max_new_tokens=1)
+    with pytest.raises(ValueError):
+        generate(model, prompt, max_new_tokens=1, sample=lambda logits, ids: 96)
 
 
 def test_config_from_plx_payload(dev, packed):

@@ -88,12 +88,14 @@ def _check(y, x, w16, mode):
 
 
 # one token of bf16 x (the one-token GEMV) and batches above 4 tokens (the MFMA GEMM), ragged shapes and
-# both weight roundings; the row of 320 atoms is the longest the one-token kernel takes from the layout
+# both weight roundings; the row of 320 atoms is the longest the one-token kernel takes from the layout;
+# rows of 81-85 atoms in layers of more than 6,112 rows take 32 lanes (16 lanes hold at most 80 atoms)
 @pytest.mark.parametrize("shape,m,dtype", [
     ((24, 24), 1, torch.bfloat16), ((37, 48), 1, torch.bfloat16), ((33, 240), 1, torch.bfloat16),
     ((1152, 1152), 1, torch.bfloat16), ((7, 1176), 1, torch.bfloat16), ((100, 4608), 1, torch.bfloat16),
     ((130, 7680), 1, torch.bfloat16), ((7680, 1920), 1, torch.bfloat16), ((6200, 2304), 1, torch.bfloat16),
     ((6200, 3816), 1, torch.bfloat16), ((6200, 2304), 1, torch.float32),
+    ((6200, 1968), 1, torch.bfloat16), ((6200, 2040), 1, torch.bfloat16),
     ((1152, 1152), 17, torch.bfloat16), ((37, 1920), 33, torch.bfloat16), ((20, 240), 64, torch.bfloat16),
     ((7680, 1920), 64, torch.bfloat16), ((1920, 7680), 64, torch.bfloat16), ((100, 4608), 5, torch.float32),
     ((37, 48), 40, torch.float32), ((1152, 1152), 100, torch.float32),

@@ -75,3 +75,55 @@ def test_noalloc_rejects_more_than_its_maximum(dev):
         # exactly the maximum passes validation (checked without launching: a null latent is refused next)
         st = lib.plx_requantize_noalloc(None, max_atoms, 24, 0, None, None, None, None, _lib.stream_of(dev))
         assert st == _lib.PLX_EINVAL and "null pointer" in lib.plx_last_error().decode()
+
+
+def test_noalloc_call_captured_in_a_graph(dev):
+    # torch.cuda.graph captures in the global mode, where a device allocation by any thread fails the
+    # capture: the call records only kernels.  Each replay (eager work and a synchronisation between
+    # replays, the latent rewritten in place) must equal an eager call on the same latent.
+    lib = _lib.lib()
+    with torch.cuda.device(dev):
+        _lib.check(lib.plx_device_init(), "plx_device_init")
+        g = torch.Generator().manual_seed(77)
+        rows, cols = 384, 1152
+        w = (torch.randn(rows, cols, generator=g) * 0.02).to(dev)
+        o = _outputs(rows, cols, dev)
+        args = (_lib.ptr(w), rows, cols, _lib.NN_BF16_SCORES, _lib.ptr(o["sigma"]), _lib.ptr(o["indices"]),
+                _lib.ptr(o["packed"]), _lib.ptr(o["weight"]))
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):  # warm-up call outside capture (tables already built by init)
+            _lib.check(lib.plx_requantize_noalloc(*args, _lib.stream_of(dev)), "warm-up")
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            st = lib.plx_requantize_noalloc(*args, _lib.stream_of(dev))
+        _lib.check(st, "plx_requantize_noalloc under capture")
+        for rep in range(3):
+            w.copy_((torch.randn(rows, cols, generator=g) * 0.02).to(dev))
+            graph.replay()
+            torch.cuda.synchronize()
+            got = {k: v.clone() for k, v in o.items()}
+            want = _requantize(lib, w, _lib.NN_BF16_SCORES, noalloc=False)
+            torch.cuda.synchronize()
+            print(f"[noalloc] graph replay {rep}: {got['indices'].numel()} atoms", flush=True)
+            for k in ("sigma", "indices", "packed", "weight"):
+                assert torch.equal(got[k], want[k]), (rep, k)
+
+
+def test_noalloc_refusal_writes_nothing(dev):
+    # a latent that is not 16-byte aligned is refused before row_rms runs: sigma_out keeps its contents
+    lib = _lib.lib()
+    with torch.cuda.device(dev):
+        _lib.check(lib.plx_device_init(), "plx_device_init")
+        base = torch.randn(4 * 1152 + 1, device=dev) * 0.02
+        w = base[1:]  # 4 bytes past an aligned allocation
+        assert _lib.ptr(w) % 16 == 4
+        o = _outputs(4, 1152, dev)
+        o["sigma"].fill_(-7.0)
+        st = lib.plx_requantize_noalloc(_lib.ptr(w), 4, 1152, _lib.NN_BF16_SCORES, _lib.ptr(o["sigma"]),
+                                        _lib.ptr(o["indices"]), None, None, _lib.stream_of(dev))
+        torch.cuda.synchronize()
+        assert st == _lib.PLX_EINVAL and "aligned" in lib.plx_last_error().decode()
+        assert torch.all(o["sigma"] == -7.0)
