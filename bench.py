@@ -85,6 +85,8 @@ def time_gpu(fn, iters, warmup, rounds=1, warm_s=0.0):
         if k % 8 == 0:
             torch.cuda.synchronize()
     torch.cuda.synchronize()
+    if iters <= 0:
+        return 0.0
     per = []
     for _ in range(rounds):
         t0 = time.perf_counter()

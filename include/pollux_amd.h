@@ -189,8 +189,9 @@ size_t plx_pollux_step_workspace_bytes(int64_t rows, int64_t cols);
  * then the requantize of plx_requantize on the new latent (sigma_out, idx_out
  * required; packed_out, weight_out nullable; weight_out is the parameter's
  * new data), and, if adam_norm_out is not NULL, adam_norm_out[0] = |s|_2 over
- * the whole parameter.  scalars: DEVICE float[9] = {b1, 1-b1, b2, 1-b2,
- * max(bc1, 1e-8), max(bc2, 1e-8), neg_scale, wdf, cap} as the reference's
+ * the whole parameter (nothing is written when rows == 0).  scalars: DEVICE
+ * float[9] = {b1, 1-b1, b2, 1-b2, max(bc1, 1e-8), max(bc2, 1e-8),
+ * neg_scale, wdf, cap} as the reference's
  * 0-dim fp32 tensors evaluate them (bc = 1 - b^(step+1); neg_scale =
  * -(heat*gamma/C / width_inertia); wdf = 1 - heat*gamma^2; cap =
  * KINEMATIC_LIMIT*s_lattice), so no host synchronisation is needed.
@@ -211,7 +212,7 @@ typedef struct plx_pollux_step_item {
   int32_t *idx_out;      /* int32[rows*cols/24] */
   uint8_t *packed_out;   /* uint8[((N+3)/4)*9] or NULL */
   float *weight_out;     /* float[rows*cols] or NULL: the parameter's new data */
-  float *adam_norm_out;  /* float[1] or NULL: |s|_2 over the parameter */
+  float *adam_norm_out;  /* float[1] or NULL: |s|_2 over the parameter (not written when rows == 0) */
 } plx_pollux_step_item;
 
 /* Workspace (device bytes) plx_pollux_step_h24_batch needs for these items

@@ -29,12 +29,22 @@ Pinned by:
                                8 alphabet values;
   linear_fp32                  float64 matmul within K * 2^-24 * sum|x||w|;
   pollux_h24_update            rule by rule against oracle/optim.py
-                               (tests/test_oracle_optim.py).
+                               (tests/test_oracle_optim.py);
+  int8_materialize             numpy float16 emulation of
+                               fp16(fp32(q) * fp32(fp16(fp32(mu) / 127))),
+                               exhaustive over every finite fp16 mu and all
+                               256 int8 values (tests/test_oracle_forward.py);
+  _rms_norm                    float64 closed form rounded once, within the
+                               first-order bound (d + 5) * 2^-24 relative;
+  pollux_packed_forward        an independent float64 numpy forward of the
+                               same packed state (own dequant emulation,
+                               explicit causal softmax, erf GELU), relative
+                               L2 <= 2e-6.
 Each of these tests also shows that a plausible slip (eps outside the sqrt,
 the clamp before the multiply, one rounding instead of two, a multiply by
-fp32(sqrt 2) instead of the division, bf16 weights) fails the same check.
-``linear_as_reference``, ``int8_materialize`` and ``pollux_packed_forward``
-compose the pinned pieces with torch's own ops (F.linear, F.gelu, SDPA).
+fp32(sqrt 2) instead of the division, bf16 weights, a missing q_ln, the tanh
+GELU, no causal mask) fails the same check.  ``linear_as_reference`` composes
+the pinned pieces with torch's own F.linear.
 """
 
 from __future__ import annotations

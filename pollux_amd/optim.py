@@ -125,7 +125,7 @@ def pollux_h24_step_(
     idx = torch.empty(n, dtype=torch.int32, device=dev)
     packed = torch.empty(((n + 3) // 4) * BYTES_PER_CHUNK, dtype=torch.uint8, device=dev) if return_codes else None
     w = p.data if p.data.is_contiguous() else torch.empty_like(p.data)
-    norm = torch.empty((), dtype=torch.float32, device=dev)
+    norm = torch.zeros((), dtype=torch.float32, device=dev)  # an empty parameter's norm is 0 (not written)
     nws = int(_lib.lib().plx_pollux_step_workspace_bytes(rows, cols))
     ws = torch.empty(max(nws, 16), dtype=torch.uint8, device=dev)
     with torch.cuda.device(dev):
@@ -191,7 +191,7 @@ def pollux_h24_step_many_(
             "indices": torch.empty(n, dtype=torch.int32, device=dev),
             "packed": torch.empty(((n + 3) // 4) * BYTES_PER_CHUNK, dtype=torch.uint8, device=dev)
             if return_codes else None,
-            "norm": torch.empty((), dtype=torch.float32, device=dev),
+            "norm": torch.zeros((), dtype=torch.float32, device=dev),  # stays 0 for an empty parameter
         }
         w = p.data if p.data.is_contiguous() else torch.empty_like(p.data)
         keep.append((g, w, p))

@@ -1,4 +1,4 @@
-"""The packed decoder at the real Pollux-1920 shape: one block and the INT8 head at vocab 50,688.
+"""The packed decoder at the real Pollux-1920 shape: all 18 blocks and the INT8 head at vocab 50,688.
 
 The toy model of test_gpu_model.py exercises every code path; this one runs
 them at the sizes the reference ships (pollux.py:566-702: d 1920, 80 heads of
@@ -21,7 +21,7 @@ from pollux_amd.model import PackedPolluxModel
 
 pytestmark = pytest.mark.gpu
 
-CFG = {"n_layers": 1, "n_heads": 80, "d_head": 24, "n_embd": 1920, "vocab_size": 50688,
+CFG = {"n_layers": 18, "n_heads": 80, "d_head": 24, "n_embd": 1920, "vocab_size": 50688,
        "tokenizer_vocab_size": 50257, "seq_len": 1024}
 
 
@@ -52,7 +52,7 @@ def _dense_state(cfg, seed):
 @pytest.fixture(scope="module")
 def model_and_state(dev):
     state, stats = pack.pack_state_dict(_dense_state(CFG, 1920), dev)
-    assert stats["h24_atom_count"] == (4 * 1920 * 1920 + 2 * 7680 * 1920) // 24
+    assert stats["h24_atom_count"] == 18 * (4 * 1920 * 1920 + 2 * 7680 * 1920) // 24
     payload = {"format": plx.PLX_FORMAT, "config": pack.pack_config(CFG),
                "codebook_fingerprint": castor.codebook_fingerprint(), "state_dict": state}
     return PackedPolluxModel.from_packed_checkpoint(payload, dev), state
@@ -62,6 +62,7 @@ def _rel(a, b):
     return ((a.double() - b.double()).norm() / b.double().norm()).item()
 
 
+@pytest.mark.timeout(600)
 def test_forward_and_cached_decode_at_real_shape(dev, model_and_state):
     model, state = model_and_state
     idx = torch.randint(0, 50257, (2, 12), generator=torch.Generator().manual_seed(11))

@@ -27,11 +27,6 @@ def _ref_int8(w):
     return q, mu.squeeze(-1).to(torch.float16)
 
 
-def _ref_int8_materialize(q, mu16):
-    # pollux.py:526
-    return q.to(torch.float16) * (mu16.unsqueeze(-1).to(torch.float16) / 127.0)
-
-
 @pytest.mark.parametrize("shape", [(50, 1152), (7, 1000), (3, 5, 24), (1, 1), (64,)])
 def test_quantize_int8_matches_reference_ops(dev, shape):
     g = torch.Generator().manual_seed(sum(shape))
@@ -52,7 +47,19 @@ def test_dequant_int8_matches_reference_ops(dev, shape):
     q = torch.randint(-128, 128, shape, dtype=torch.int8, generator=g).to(dev)
     mu = (torch.rand(shape[0], generator=g) * 0.2 + 1e-3).to(torch.float16).to(dev)
     got = dequantize_int8_rows(q, mu)
-    want = _ref_int8_materialize(q, mu)
+    want = torch_ref.int8_materialize(q, mu)  # the reference's expression on the device
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+    assert torch.equal(got.cpu().view(torch.int16), torch_ref.int8_materialize(q.cpu(), mu.cpu()).view(torch.int16))
+
+
+def test_dequant_int8_every_fp16_scale(dev):
+    # all 63,488 finite fp16 mu x all 256 int8 values against the oracle's CPU evaluation (itself pinned
+    # exhaustively against numpy's float16 emulation in tests/test_oracle_forward.py)
+    mu = torch.arange(65536, dtype=torch.int32).to(torch.int16).view(torch.float16)
+    mu = mu[torch.isfinite(mu)]
+    q = torch.arange(-128, 128, dtype=torch.int16).to(torch.int8).repeat(mu.numel(), 1)
+    got = dequantize_int8_rows(q.to(dev), mu.to(dev)).cpu()
+    want = torch_ref.int8_materialize(q, mu)
     assert torch.equal(got.view(torch.int16), want.view(torch.int16))
 
 
@@ -67,7 +74,7 @@ def test_packed_int8_layers(dev):
         m.mu_rows.copy_(mu)
     ids = torch.randint(0, 100, (3, 5), generator=g).to(dev)
     x = torch.randn(4, 48, generator=g).to(dev)
-    wq = _ref_int8_materialize(q, mu)
+    wq = torch_ref.int8_materialize(q, mu)
     assert torch.equal(emb(ids), torch.nn.functional.embedding(ids, wq.float()))
     # fused INT8 kernels (4 tokens, 20 tokens: MFMA): exact products, another summation order than F.linear
     want = torch.nn.functional.linear(x, wq.float())
@@ -95,16 +102,16 @@ def test_packed_int8_linear_sees_new_weights(dev):
     big = torch.randn(20, 48, generator=g).to(dev)
     for st in states + states[:1]:
         lin.load_state_dict(st)
-        want = torch.nn.functional.linear(big, _ref_int8_materialize(st["weight_int8"], st["mu_rows"]).float())
+        want = torch.nn.functional.linear(big, torch_ref.int8_materialize(st["weight_int8"], st["mu_rows"]).float())
         assert torch.equal(lin(big), want)
         assert torch.equal(lin(big.to(torch.bfloat16)),
                            torch.nn.functional.linear(big.to(torch.bfloat16),
-                                                      _ref_int8_materialize(st["weight_int8"], st["mu_rows"])
+                                                      torch_ref.int8_materialize(st["weight_int8"], st["mu_rows"])
                                                       .to(torch.bfloat16)))
     # replacing a buffer object is seen too
     lin.weight_int8 = states[1]["weight_int8"].clone()
     lin.mu_rows = states[1]["mu_rows"].clone()
-    want = torch.nn.functional.linear(big, _ref_int8_materialize(states[1]["weight_int8"],
+    want = torch.nn.functional.linear(big, torch_ref.int8_materialize(states[1]["weight_int8"],
                                                                  states[1]["mu_rows"]).float())
     assert torch.equal(lin(big), want)
 
@@ -117,7 +124,7 @@ def test_packed_int8_linear_cast_not_kept_from_graph_capture(dev):
     q, mu = plx_pack.quantize_int8_rows(torch.randn(100, 48, generator=g).to(dev))
     lin.load_state_dict({"weight_int8": q, "mu_rows": mu})
     big = torch.randn(20, 48, generator=g).to(dev)
-    want = torch.nn.functional.linear(big, _ref_int8_materialize(q, mu).float())
+    want = torch.nn.functional.linear(big, torch_ref.int8_materialize(q, mu).float())
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
@@ -157,7 +164,7 @@ def test_int8_linear_matches_fp64(dev, rows, cols, m):
     mu[1] = 1.3e-4  # s16 ~ 1e-6 is an fp16 subnormal; the row's weights round on both sides of 2^-14
     x = (torch.randn(m, cols, generator=g) * 2.0).to(dev)
     qd, mud = q.to(dev), mu.to(dev)
-    wq = _ref_int8_materialize(qd, mud)
+    wq = torch_ref.int8_materialize(qd, mud)
     y = int8_linear(qd, mud, x)
     assert y.shape == (m, rows)
     _check_int8_linear(y, x, wq)
@@ -225,7 +232,7 @@ def test_int8_embed_with_positions(dev):
     mu = (torch.rand(300, generator=g) * 0.2 + 1e-3).to(torch.float16).to(dev)
     pos_w = torch.randn(40, 72, generator=g).to(dev)
     ids = torch.randint(0, 300, (3, 7), generator=g).to(dev)
-    wq = _ref_int8_materialize(q, mu).float()
+    wq = torch_ref.int8_materialize(q, mu).float()
     p0 = torch.tensor(5, device=dev)
     got = int8_embed(q, mu, ids, pos_weight=pos_w, pos0=p0)
     want = torch.nn.functional.embedding(ids, wq) + pos_w[5:12].unsqueeze(0)
