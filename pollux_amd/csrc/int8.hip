@@ -101,10 +101,10 @@ __global__ __launch_bounds__(256) void int8_dequant_kernel(const int8_t *__restr
   const int lane = threadIdx.x % 64;
   if (row >= rows) return;
   const float inv127 = 1.0f / 127.0f;
-  const float s = __half2float(__float2half_rn(__half2float(__ushort_as_half(mu16[row])) * inv127));
+  const float s = __half2float(__float2half_rn(f32_kept(__half2float(__ushort_as_half(mu16[row])) * inv127)));
   const int8_t *qr = q + row * cols;
   uint16_t *out = w16 + row * cols;
-  auto one = [&](int8_t v) { return __half_as_ushort(__float2half_rn(static_cast<float>(v) * s)); };
+  auto one = [&](int8_t v) { return __half_as_ushort(__float2half_rn(f32_kept(static_cast<float>(v) * s))); };
   if (vec4) {
     for (int64_t i = lane; i < cols / 4; i += 64) {
       const uint32_t b = reinterpret_cast<const uint32_t *>(qr)[i];
@@ -124,7 +124,7 @@ __device__ __forceinline__ float wave_sum64(float v) { return wave_reduce_sum(v)
 
 // s16 of a row as fp32 (fp16(fp32(mu16) * fp32(1/127)))
 __device__ __forceinline__ float int8_row_scale(uint16_t mu) {
-  return __half2float(__float2half_rn(__half2float(__ushort_as_half(mu)) * (1.0f / 127.0f)));
+  return __half2float(__float2half_rn(f32_kept(__half2float(__ushort_as_half(mu)) * (1.0f / 127.0f))));
 }
 
 // the fp16 weights of bytes 0,1 (lo) and 2,3 (hi) of d, each pair times s2
@@ -613,7 +613,7 @@ __global__ __launch_bounds__(256) void int8_embed_kernel(const int8_t *__restric
   const float4 *pr = pos_w ? reinterpret_cast<const float4 *>(pos_w + p * cols) : nullptr;
   const int n4 = cols / 4;
   auto emit = [&](int i, uint32_t b, float4 g, float s) {
-    auto one = [&](int8_t v) { return __half2float(__float2half_rn(static_cast<float>(v) * s)); };
+    auto one = [&](int8_t v) { return __half2float(__float2half_rn(f32_kept(static_cast<float>(v) * s))); };
     float4 v = make_float4(one(static_cast<int8_t>(b)), one(static_cast<int8_t>(b >> 8)),
                            one(static_cast<int8_t>(b >> 16)), one(static_cast<int8_t>(b >> 24)));
     if (pr) v = make_float4(v.x + g.x, v.y + g.y, v.z + g.z, v.w + g.w);

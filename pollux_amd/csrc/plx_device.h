@@ -30,10 +30,19 @@ __device__ __forceinline__ float raw_value_f32(int k) {
 // fp16 bits of the materialised weight for raw coordinate k and row scale sig
 // (pollux.py:492-499): fp16(fp32(fp16(cb16[k] * sig)) * fp32(1/sqrt 2)), both
 // products in fp32 then rounded to fp16, cb16 = fp16(k * fp32(1/sqrt 8)).
+// An fp32 result kept as computed before it is rounded again: the empty asm stops
+// the compiler from folding fp32 product + fp16 conversion into one mixed-precision
+// FMA (v_fma_mixlo_f16 with a +0 addend), which turns a -0 product into +0 and
+// rounds the exact product to fp16 once where torch rounds it to fp32 first.
+__device__ __forceinline__ float f32_kept(float v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
+
 __device__ __forceinline__ uint32_t dq_value(int k, float sig, float sl) {
   const float c16 = __half2float(__float2half_rn(raw_value_f32(k)));
-  const float t = __half2float(__float2half_rn(c16 * sig));
-  return __half_as_ushort(__float2half_rn(t * sl));
+  const float t = __half2float(__float2half_rn(f32_kept(c16 * sig)));
+  return __half_as_ushort(__float2half_rn(f32_kept(t * sl)));
 }
 
 // Lane exchange within rows of 16 lanes by DPP (no trip through the LDS

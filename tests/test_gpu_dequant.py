@@ -29,6 +29,27 @@ def test_dequant_matches_reference_ops(dev, shape):
     assert torch.equal(got.view(torch.int16), want.view(torch.int16))
 
 
+def test_every_fp16_sigma_and_alphabet_value(dev):
+    # all 63,488 finite fp16 sigma (negative, zero, subnormal and huge ones included) x the 8 raw values
+    # {0, +-1, +-2, -3, +-4} at several positions: per row one +-4 pair, one +-2 octad and one type-3 code,
+    # against the oracle's materialize (pinned exhaustively against numpy's float16 emulation)
+    from oracle import codebook as cb
+
+    raw = cb.codebook_int8()
+    pick = [int(np.nonzero((raw == 4).any(1) & (raw == -4).any(1))[0][0]),
+            int(np.nonzero((raw == 2).any(1) & (raw == -2).any(1))[0][0]),
+            int(np.nonzero((raw == -3).any(1) & (raw == 1).any(1) & (raw == -1).any(1))[0][0])]
+    sig = torch.arange(65536, dtype=torch.int32).to(torch.int16).view(torch.float16)
+    sig = sig[torch.isfinite(sig)]
+    rows = sig.numel()
+    idx = torch.tensor(pick, dtype=torch.int64).repeat(rows)
+    packed = torch.from_numpy(packing.pack(idx.numpy()))
+    want = torch_ref.materialize(idx, sig, rows, 72)
+    got = dequantize_h24(packed.to(dev), sig.to(dev), rows, 72).cpu()
+    bad = (got.view(torch.int16) != want.view(torch.int16)).nonzero()
+    assert len(bad) == 0, (len(bad), bad[:5].tolist())
+
+
 def test_sigma_edge_values(dev):
     out_f, in_f = 6, 48
     idx, _, packed = _packed_layer(out_f, in_f, 1)
