@@ -41,6 +41,18 @@ extern "C" {
  *       invariant under positive scaling of the atom).  The reference's
  *       pack-time search, pack._quantize_h24_layer (pack.py:167-177). */
 #define PLX_NN_PACK_FP32 2
+/* Flag OR'ed into PLX_NN_BF16_SCORES (quantize / requantize entry points):
+ * score the 98,304 type-3 codes densely on MFMA (one contraction per code)
+ * instead of the default structured scorer, which scores the 2,048 Golay
+ * sign-pattern pairs and evaluates the few candidate patterns exactly.  Both
+ * have NN-B semantics (equal answers off near-ties); the dense sweep is kept
+ * as the measured baseline of the structured one.  Ignored by the other modes. */
+#define PLX_NN_DENSE_TYPE3 0x100
+/* Flag OR'ed into PLX_NN_BF16_SCORES for plx_quantize (diagnostics): the
+ * structured scorer finds the lowest row at the best bucket by a third sweep
+ * over the patterns -- the path it takes when its per-wave list of surviving
+ * words overflows -- instead of from that list.  Same results. */
+#define PLX_NN_T3_ROWS_BY_SWEEP 0x200
 
 /* ---- element types of plx_gather_codebook's output -------------------- */
 #define PLX_DTYPE_F32 0
@@ -136,7 +148,7 @@ int plx_requantize(const float *latent, int64_t rows, int64_t cols, int mode,
  * training loops, harnesses that forbid hipMalloc).  No counterpart in the
  * reference: it serves those callers only.  Same arguments, results and
  * errors as plx_requantize minus the workspace, which is a library-owned
- * device array of PLX_NOALLOC_MAX_ATOMS * 88 bytes (88 MiB) held by each
+ * device array of PLX_NOALLOC_MAX_ATOMS * 128 bytes (128 MiB) held by each
  * device the library runs on until the process ends.  It allocates nothing:
  * call plx_device_init() on the device first (outside any capture), which
  * builds the codebook tables and resolves the array's address; without it
@@ -436,6 +448,7 @@ int plx_int8_embed(const int8_t *q, const uint16_t *mu16, int64_t vocab, int64_t
 #define PLX_PROF_UNPACK 2  /* unpack_kernel (plx_unpack_indices) */
 #define PLX_PROF_DEQUANT 3 /* dequant_kernel (plx_dequant_f16) */
 #define PLX_PROF_ADAM 4    /* adam_h24_kernel (plx_pollux_step_h24*) */
+#define PLX_PROF_T3 5      /* t3_kernel (the structured type-3 scorer of NN-B) */
 int plx_profile_select(int kernel);
 int plx_profile_begin(void);
 int plx_profile_end(double *total_ms, int64_t *launches);

@@ -45,6 +45,14 @@ using namespace plx;
 
 static inline hipStream_t as_stream(void *s) { return static_cast<hipStream_t>(s); }
 
+// A quantizer mode (NN-B, NN-T, and NN-P where the entry point scores raw atoms), with the dense
+// type-3 flag allowed on NN-B only.
+static inline bool nn_mode_ok(int mode, bool allow_pack) {
+  const int base = mode & ~(PLX_NN_DENSE_TYPE3 | PLX_NN_T3_ROWS_BY_SWEEP);
+  if (mode != base && base != PLX_NN_BF16_SCORES) return false;
+  return base == PLX_NN_BF16_SCORES || base == PLX_NN_FP32_SCORES || (allow_pack && base == PLX_NN_PACK_FP32);
+}
+
 extern "C" {
 
 const char *plx_last_error(void) { return g_last_error.c_str(); }
@@ -130,7 +138,7 @@ size_t plx_quantize_workspace_bytes(int64_t n_atoms) { return quantize_workspace
 int plx_quantize(const float *x, int64_t n_atoms, int mode, int32_t *idx_out, void *workspace,
                  size_t workspace_bytes, void *stream) {
   PLX_REQUIRE(n_atoms >= 0, "plx_quantize: negative atom count");
-  PLX_REQUIRE(mode == PLX_NN_BF16_SCORES || mode == PLX_NN_FP32_SCORES || mode == PLX_NN_PACK_FP32,
+  PLX_REQUIRE(nn_mode_ok(mode, true),
               "plx_quantize: unknown mode %d", mode);
   if (n_atoms == 0) return PLX_OK;
   PLX_REQUIRE(x != nullptr && idx_out != nullptr, "plx_quantize: null pointer");
@@ -155,7 +163,7 @@ int plx_requantize(const float *latent, int64_t rows, int64_t cols, int mode, fl
               static_cast<long long>(cols));
   PLX_REQUIRE(cols % kDim == 0, "Pollux requires in_features divisible by H24_DIM=24; got %lld.",
               static_cast<long long>(cols));
-  PLX_REQUIRE(mode == PLX_NN_BF16_SCORES || mode == PLX_NN_FP32_SCORES, "plx_requantize: unknown mode %d", mode);
+  PLX_REQUIRE(nn_mode_ok(mode, false), "plx_requantize: unknown mode %d", mode);
   if (rows == 0) return PLX_OK;
   PLX_REQUIRE(latent != nullptr && sigma_out != nullptr && idx_out != nullptr, "plx_requantize: null pointer");
   const int64_t n_atoms = rows * (cols / kDim);
@@ -175,7 +183,7 @@ int plx_requantize_noalloc(const float *latent, int64_t rows, int64_t cols, int 
               static_cast<long long>(cols));
   PLX_REQUIRE(cols % kDim == 0, "Pollux requires in_features divisible by H24_DIM=24; got %lld.",
               static_cast<long long>(cols));
-  PLX_REQUIRE(mode == PLX_NN_BF16_SCORES || mode == PLX_NN_FP32_SCORES, "plx_requantize_noalloc: unknown mode %d",
+  PLX_REQUIRE(nn_mode_ok(mode, false), "plx_requantize_noalloc: unknown mode %d",
               mode);
   PLX_REQUIRE(rows <= static_cast<int64_t>(PLX_NOALLOC_MAX_ATOMS) * kDim / cols,
               "plx_requantize_noalloc: %lld x %lld is more than its maximum of %d atoms (use plx_requantize)",
@@ -189,7 +197,7 @@ int plx_requantize_noalloc(const float *latent, int64_t rows, int64_t cols, int 
 int plx_requantize_batch(const plx_requantize_item *items, int n_items, int mode, void *workspace,
                          size_t workspace_bytes, void *stream) {
   PLX_REQUIRE(n_items >= 0 && n_items <= 4096, "plx_requantize_batch: bad item count %d", n_items);
-  PLX_REQUIRE(mode == PLX_NN_BF16_SCORES || mode == PLX_NN_FP32_SCORES, "plx_requantize_batch: unknown mode %d", mode);
+  PLX_REQUIRE(nn_mode_ok(mode, false), "plx_requantize_batch: unknown mode %d", mode);
   if (n_items == 0) return PLX_OK;
   PLX_REQUIRE(items != nullptr, "plx_requantize_batch: null item array");
   std::vector<RequantItem> its(static_cast<size_t>(n_items));
@@ -219,7 +227,7 @@ int plx_pollux_step_h24(const float *grad, float *m, float *v, float *latent, in
               static_cast<long long>(cols));
   PLX_REQUIRE(cols % kDim == 0, "Pollux requires in_features divisible by H24_DIM=24; got %lld.",
               static_cast<long long>(cols));
-  PLX_REQUIRE(mode == PLX_NN_BF16_SCORES || mode == PLX_NN_FP32_SCORES, "plx_pollux_step_h24: unknown mode %d", mode);
+  PLX_REQUIRE(nn_mode_ok(mode, false), "plx_pollux_step_h24: unknown mode %d", mode);
   if (rows == 0) return PLX_OK;
   PLX_REQUIRE(grad != nullptr && m != nullptr && v != nullptr && latent != nullptr && scalars != nullptr &&
                   sigma_out != nullptr && idx_out != nullptr,
@@ -259,7 +267,7 @@ size_t plx_pollux_step_batch_workspace_bytes(const plx_pollux_step_item *items, 
 int plx_pollux_step_h24_batch(const plx_pollux_step_item *items, int n_items, const float *scalars, int mode,
                               void *workspace, size_t workspace_bytes, void *stream) {
   PLX_REQUIRE(n_items >= 0 && n_items <= 4096, "plx_pollux_step_h24_batch: bad item count %d", n_items);
-  PLX_REQUIRE(mode == PLX_NN_BF16_SCORES || mode == PLX_NN_FP32_SCORES, "plx_pollux_step_h24_batch: unknown mode %d",
+  PLX_REQUIRE(nn_mode_ok(mode, false), "plx_pollux_step_h24_batch: unknown mode %d",
               mode);
   if (n_items == 0) return PLX_OK;
   PLX_REQUIRE(items != nullptr && scalars != nullptr, "plx_pollux_step_h24_batch: null item array or scalars");

@@ -93,6 +93,15 @@ const int8_t *codebook_raw_host() {
   return table.empty() ? nullptr : table.data();
 }
 
+const uint32_t *golay_words_host() {
+  static std::once_flag once;
+  static std::array<uint32_t, 4096> words;
+  std::call_once(once, [] {
+    for (uint32_t m = 0; m < 4096; ++m) words[m] = golay_word(m);
+  });
+  return words.data();
+}
+
 float raw_to_f32(int k) {
   float s;
   std::memcpy(&s, &kLeechScaleBits, 4);

@@ -37,6 +37,16 @@ constexpr int kPairTiles = (kPairCodes + kTileCodes - 1) / kTileCodes;      // 3
 constexpr int kSweepTiles = 9216;  // 6144 + 3071 + 1 zero tile = 2^10 * 9
 static_assert(kType3Tiles + kPairTiles <= kSweepTiles, "sweep tiles");
 
+// Structured type-3 scoring (quantize.hip, NN-B): a type-3 code is a Golay
+// sign pattern P(w) (-1 where the codeword w has a 1) times s with one
+// coordinate replaced by -3s, so its score is S(w) - x_p (3s + s P_p(w)) with
+// S(w) = s P(w).x.  The Golay code holds the complement of every word
+// (P(~w) = -P(w)), so the 2,048 words with bit 23 clear represent all 4,096:
+// pattern id r < 2048 is representative r, id r + 2048 its complement.
+constexpr int kT3Reps = 2048;
+constexpr int kT3Tiles = kT3Reps / kTileCodes;  // 128
+constexpr int kT3Words = 2 * kT3Reps;
+
 // fp32 constants of the reference (castor.py:47,50,68; castor.py:522; pack.py:164)
 constexpr uint32_t kLeechScaleBits = 0x3EB504F3u;  // fp32(1/sqrt 8)
 constexpr uint32_t kSLatticeBits = 0x3F3504F3u;    // fp32(1/sqrt 2)
@@ -58,6 +68,9 @@ struct DeviceTables {
   uint32_t *pl_ids = nullptr;        // [n_planes] value-id word (kp_dq's format) of each distinct plane
   uint16_t *code_planes = nullptr;   // [kCodebook][4] the plane-layout record of each code (3 used)
   uint32_t *pl_nib = nullptr;        // [n_planes] the same planes as kp_gemv words: 8 signed 4-bit coordinates
+  uint8_t *t3_tiles = nullptr;       // [kT3Tiles][3][16][8] bf16 sign patterns +-s of the representative words
+  uint32_t *t3_words = nullptr;      // [4096] word of pattern id (representatives, then their complements)
+  uint32_t *t3_rows = nullptr;       // [4096][24] codebook row of the type-3 code (word of id, -3 at position p)
 };
 
 // Plane tables (tables.cpp; host, built once): the codebook rows take only a
@@ -75,6 +88,8 @@ const PlaneTables *plane_tables_host();
 
 // Host generator (codebook.cpp): raw coordinates, origin first, sorted.
 const int8_t *codebook_raw_host();
+// The 4,096 extended Golay codewords (bit b = coordinate b), message order (codebook.cpp).
+const uint32_t *golay_words_host();
 // fp32 value of raw coordinate k (k in -4..4): k * fp32(1/sqrt 8), rounded to fp32.
 float raw_to_f32(int k);
 

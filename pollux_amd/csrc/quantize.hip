@@ -219,7 +219,7 @@ __global__ __launch_bounds__(kThreads, MODE == kModeB ? 3 : 2) void nn_kernel(co
                                                                              int64_t n_atoms,
                                                           const uint8_t *__restrict__ tiles, int n_slices,
                                                           int tiles_per_slice, uint4 *__restrict__ keys,
-                                                          uint64_t *__restrict__ recs, int s0) {
+                                                          uint64_t *__restrict__ recs, int s0, int t0_base) {
   __shared__ __align__(16) uint8_t lds[2][kStageBytes];
 
   const int slice = static_cast<int>(blockIdx.x % static_cast<unsigned>(n_slices));
@@ -257,7 +257,7 @@ __global__ __launch_bounds__(kThreads, MODE == kModeB ? 3 : 2) void nn_kernel(co
     }
   }
 
-  const int t0 = slice * tiles_per_slice;
+  const int t0 = t0_base + slice * tiles_per_slice;  // t0_base: kType3Tiles when only the pair region is swept
   const int n_stages = tiles_per_slice / kST;
   // stages [0, n_t) hold type-3 tiles, [n_t, n_stages) pair representatives
   // (the region boundary falls on a stage boundary)
@@ -498,6 +498,334 @@ __global__ __launch_bounds__(kThreads, MODE == kModeB ? 3 : 2) void nn_kernel(co
   if (n_t < n_stages) run(std::integral_constant<bool, true>{}, n_t, n_stages);
 }
 
+// Structured type-3 scoring (NN-B; replaces the sweep's 6,144 type-3 tiles).
+//
+// A type-3 code (w, p) is the sign pattern P(w) of a Golay word w (-s where
+// w has a 1, +s elsewhere) with coordinate p replaced by -3s, so with the
+// bf16 values s = 0.353515625 and 3s = 1.0625 its score is
+//   score(w, p) = S(w) - x_p (1.0625 + s P_p(w)),   S(w) = s P(w).x,
+// i.e. S(w) - x_p * (alpha = 1.416015625 where w_p = 0, beta = 0.708984375
+// where w_p = 1); both products are exact in fp32 (8 x 8 significant bits).
+// The best code of a word is S(w) + bonus(w) with bonus(w) = max_p of
+// -x_p (alpha or beta), which lies in [e_stop, e1]: e1 = max_p max(-alpha x_p,
+// -beta x_p) and e_stop = the smaller of the two at the p attaining e1 (every
+// word takes one of them there).  The Golay code holds the complement of
+// every word, S(~w) = -S(w), so one MFMA per 16 representative words scores
+// 32 words: 128 tiles instead of 6,144.
+// A block of 4 waves holds AT atom tiles of 16 atoms per wave as MFMA B
+// operands and streams the 128 pattern tiles through LDS three times:
+//   pass 0  the largest |S| per atom: the best type-3 score is at least
+//           S_max + e_stop, and no code below the best pair bucket (the pair
+//           records) or below 2.0 (the origin rule) can win;
+//   pass 1  every lane whose four outputs hold a word that could reach the
+//           lowest bucket still possible (|S| >= lo(bucket) - e1 - margin)
+//           appends one 4-byte entry (atom, tile, lane quarter, 4-bit mask of
+//           its outputs) to the wave's list in LDS; full lists are evaluated
+//           by the wave, one entry per lane: each flagged representative and
+//           its complement get S recomputed from the atom's bf16 coordinates
+//           and their 24 positions scored, and the best bucket M3 per atom is
+//           kept by an LDS atomic max;
+//   pass 2  the same for the words that could reach M3 (a handful): every
+//           (w, p) at bucket M3 gives its codebook row (t3_rows) and the
+//           lowest one is kept by an LDS atomic min.
+// The atom's key gets (M3 << 16, lowest row at M3), or 0 when no type-3 code
+// reaches 2.0; the resolve compares it with the pair region's candidates.
+// Buckets are taken by round-half-up like the dense sweep's, and every score
+// is an fp32 sum of exact products plus one rounding for the bonus, so the
+// answer equals the exact-score answer off near-ties (oracle/nn.py).
+constexpr int kT3ST = 16;                          // pattern tiles per LDS stage
+constexpr int kT3Stages = kT3Tiles / kT3ST;        // 8 per pass
+constexpr int kT3StageBytes = kT3ST * kTileBytes;  // 12,288
+constexpr int kT3StageVecs = kT3StageBytes / 16;   // 768
+constexpr int kT3Cap = 512;                        // candidate entries per wave (4 bytes each)
+constexpr int kT3Surv = 512;                       // survivor words per wave (4 bytes each)
+constexpr float kT3Alpha = 1.416015625f;           // bf16(3s) + bf16(s)
+constexpr float kT3Beta = 0.708984375f;            // bf16(3s) - bf16(s)
+constexpr float kT3S = 0.353515625f;               // bf16(s)
+static_assert(kT3StageVecs % kThreads == 0, "type-3 stage splits evenly over the block");
+static_assert(kT3Tiles % kT3ST == 0, "whole type-3 stages");
+
+__device__ __forceinline__ uint32_t t3_bucket(float v) { return (__float_as_uint(v) + 0x8000u) >> 16; }
+
+// S of representative word wb: sum over the 24 coordinates of (-s where wb has a 1, else +s) * x,
+// in coordinate order (exact products, fp32 sums); xr: the atom's 12 words of bf16 pairs.
+__device__ __forceinline__ float t3_dot(const uint32_t *xr, uint32_t wb) {
+  float S = 0.f;
+#pragma unroll
+  for (int d = 0; d < 12; ++d) {
+    const uint32_t xx = xr[d];
+    const float x0 = __uint_as_float((xx << 16) ^ ((wb >> (2 * d)) & 1u) << 31);
+    const float x1 = __uint_as_float((xx & 0xFFFF0000u) ^ ((wb >> (2 * d + 1)) & 1u) << 31);
+    S = fmaf(x0, kT3S, S);
+    S = fmaf(x1, kT3S, S);
+  }
+  return S;
+}
+
+template <int AT>
+__global__ __launch_bounds__(kThreads, 2) void t3_kernel(const uint4 *__restrict__ xb, int64_t n_atoms,
+                                                         const uint8_t *__restrict__ t3_tiles,
+                                                         const uint32_t *__restrict__ t3_words,
+                                                         const uint32_t *__restrict__ t3_rows,
+                                                         const uint64_t *__restrict__ recs, int n_recs,
+                                                         uint4 *__restrict__ keys, int rows_by_sweep) {
+  constexpr int NA = AT * 16;  // atoms per wave
+  static_assert(NA <= 128, "entry layout: 7 bits of atom");
+  __shared__ __align__(16) uint8_t stg[2][kT3StageBytes];
+  __shared__ uint32_t cand[kWaves][kT3Cap];  // atom | tile << 7 | quarter << 14 | output mask << 16
+  __shared__ uint32_t surv[kWaves][kT3Surv];  // atom | pattern id << 7: words at or above the atom's running best
+  __shared__ __align__(16) uint32_t xw[kWaves][NA][12];  // the atoms' bf16 coordinates (pairs)
+  __shared__ uint32_t st_m[kWaves][NA], st_r[kWaves][NA];
+  __shared__ float st_t[kWaves][NA];  // the atom's threshold on S less its margin (which signs to evaluate)
+  __shared__ uint32_t wtab[kT3Reps];  // representative words
+  __shared__ uint32_t surv_n[kWaves];
+
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, q = lane >> 4, j = lane & 15;
+  const int64_t wave_atom0 = static_cast<int64_t>(blockIdx.x) * (kWaves * NA) + static_cast<int64_t>(wave) * NA;
+
+  for (int i = tid; i < kT3Reps; i += kThreads) wtab[i] = t3_words[i];
+  if (lane == 0) surv_n[wave] = 0u;
+  bf16x8 b[AT];
+  float e1[AT], es[AT];
+#pragma unroll
+  for (int at = 0; at < AT; ++at) {
+    const int64_t a = wave_atom0 + at * 16 + j;
+    uint4 w = make_uint4(0u, 0u, 0u, 0u);
+    if (a < n_atoms && q < 3) w = xb[a * 3 + q];
+    b[at] = __builtin_bit_cast(bf16x8, w);
+    if (q < 3) *reinterpret_cast<uint4 *>(&xw[wave][at * 16 + j][4 * q]) = w;
+    // e1 / e_stop over this lane's 8 coordinates, then over the atom's 3 lanes
+    float hi = -__builtin_inff(), lo = -__builtin_inff();
+    if (q < 3) {
+      const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float x = __uint_as_float(e & 1 ? ww[e / 2] & 0xFFFF0000u : ww[e / 2] << 16);
+        const float v0 = -x * kT3Alpha, v1 = -x * kT3Beta;
+        const float h = fmaxf(v0, v1), l = fminf(v0, v1);
+        if (h > hi || (h == hi && l > lo)) {
+          hi = h;
+          lo = l;
+        }
+      }
+    }
+#pragma unroll
+    for (int sh = 16; sh <= 32; sh <<= 1) {
+      const float oh = __shfl_xor(hi, sh, 64), ol = __shfl_xor(lo, sh, 64);
+      if (oh > hi || (oh == hi && ol > lo)) {
+        hi = oh;
+        lo = ol;
+      }
+    }
+    e1[at] = hi;
+    es[at] = lo;
+  }
+  for (int i = lane; i < NA; i += 64) {
+    st_m[wave][i] = 0u;
+    st_r[wave][i] = 0xFFFFFFFFu;
+  }
+  // the best pair bucket of each atom (records of the pair sweep, which ran first)
+  uint32_t mp[AT];
+#pragma unroll
+  for (int at = 0; at < AT; ++at) {
+    const int64_t a = wave_atom0 + at * 16 + j;
+    uint32_t m = 0u;
+    if (q == 0 && a < n_atoms)
+      for (int i = 0; i < n_recs; ++i) m = max(m, static_cast<uint32_t>(recs[static_cast<int64_t>(i) * n_atoms + a] >> 48));
+    mp[at] = static_cast<uint32_t>(__shfl(static_cast<int>(m), j, 64));
+  }
+
+  const uint4 *gsrc = reinterpret_cast<const uint4 *>(t3_tiles);
+  auto stage_copy = [&](int g, int dst) {
+    const int stage = g % kT3Stages;
+#pragma unroll
+    for (int i = 0; i < kT3StageVecs / kThreads; ++i) {
+      const uint4 *src = gsrc + static_cast<size_t>(stage) * kT3StageVecs + i * kThreads + tid;
+      uint8_t *d = stg[dst] + (i * kThreads + wave * 64) * 16;
+      __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)(src),
+                                       (__attribute__((address_space(3))) void *)(d), 16, 0, 0);
+    }
+  };
+
+  // The scores of word wr (sg: its complement) of atom al at its 24 positions, through f(p, t).
+  auto word_scores = [&](const uint32_t *xr, uint32_t wr, int sg, float D, auto f) {
+    const uint32_t wb = sg ? wr ^ 0xFFFFFFu : wr;
+    const float S = sg ? -D : D;
+#pragma unroll
+    for (int d = 0; d < 12; ++d) {
+      const uint32_t xx = xr[d];
+      f(2 * d, fmaf(-__uint_as_float(xx << 16), ((wb >> (2 * d)) & 1u) ? kT3Beta : kT3Alpha, S));
+      f(2 * d + 1, fmaf(-__uint_as_float(xx & 0xFFFF0000u), ((wb >> (2 * d + 1)) & 1u) ? kT3Beta : kT3Alpha, S));
+    }
+  };
+
+  int cnt = 0;  // entries in this wave's candidate list (wave-uniform)
+  // One entry per lane: each flagged output's representative word and (when it can qualify) its complement.
+  // pass 1: the best bucket of each word -> st_m (atomic max), and the word onto the survivor list when it
+  //         is at or above the atom's running best; pass 2: the lowest row at the atom's st_m -> st_r.
+  auto flush = [&](int pass) {
+    for (int i = lane; i < cnt; i += 64) {
+      const uint32_t ce = cand[wave][i];
+      const int al = static_cast<int>(ce & 0x7Fu);
+      const uint32_t rep0 = ((ce >> 7) & 0x7Fu) * kTileCodes + 4 * ((ce >> 14) & 3u);
+      const uint32_t mask = (ce >> 16) & 0xFu;
+      const uint32_t *xr = xw[wave][al];
+      const uint32_t M = pass == 2 ? st_m[wave][al] : 0u;
+      const float tlo = st_t[wave][al];
+      uint32_t rmin = 0xFFFFFFFFu;
+      // the flagged outputs one at a time (a wave iterates as often as its busiest lane needs)
+      for (uint32_t mk = mask; mk != 0u; mk &= mk - 1u) {
+        const uint32_t rep = rep0 + static_cast<uint32_t>(__builtin_ctz(mk));
+        const uint32_t wr = wtab[rep];
+        const float D = t3_dot(xr, wr);
+        // the word whose S is |D| qualified (|S| passed the threshold); the other sign only when
+        // -|D| can reach the threshold too (an atom whose threshold is about 0 or below)
+        const int sg0 = D < 0.f ? 1 : 0;
+        const int nsg = -fabsf(D) >= tlo ? 2 : 1;
+        for (int u = 0; u < nsg; ++u) {
+          const int sg = sg0 ^ u;
+          const uint32_t wid = rep + (sg ? static_cast<uint32_t>(kT3Reps) : 0u);
+          if (pass == 1) {
+            float best = -__builtin_inff();
+            word_scores(xr, wr, sg, D, [&](int, float t) { best = fmaxf(best, t); });
+            const uint32_t bk = best > 0.f ? t3_bucket(best) : 0u;
+            if (bk >= 0x4000u) {
+              const uint32_t old = atomicMax(&st_m[wave][al], bk);
+              if (bk >= old) {
+                const uint32_t slot = atomicAdd(&surv_n[wave], 1u);
+                if (slot < static_cast<uint32_t>(kT3Surv)) surv[wave][slot] = static_cast<uint32_t>(al) | wid << 7;
+              }
+            }
+          } else {
+            word_scores(xr, wr, sg, D, [&](int p, float t) {
+              if (t > 0.f && t3_bucket(t) == M) rmin = min(rmin, t3_rows[wid * kDim + p]);
+            });
+          }
+        }
+      }
+      if (pass == 2 && rmin != 0xFFFFFFFFu) atomicMin(&st_r[wave][al], rmin);
+    }
+    cnt = 0;
+  };
+
+  float m[AT], thr[AT], mg[AT];
+#pragma unroll
+  for (int at = 0; at < AT; ++at) m[at] = 0.f;
+
+  const int a_off = (q < 3 ? q : 0) * 256 + j * 16;
+  stage_copy(0, 0);
+  __syncthreads();
+  // passes 0 and 1; pass 2 only when some wave's survivor list overflowed
+  int g_end = 2 * kT3Stages;
+  for (int g = 0; g < g_end; ++g) {
+    const int pass = g / kT3Stages, buf = g & 1;
+    if (g + 1 < g_end) stage_copy(g + 1, buf ^ 1);  // (pass 2's first stage: after the decision below)
+    if (g == kT3Stages) {
+      // pass 0 done: the lowest bucket that can still win, and the threshold on |S|
+#pragma unroll
+      for (int at = 0; at < AT; ++at) {
+        float sm = m[at];
+        sm = fmaxf(sm, __shfl_xor(sm, 16, 64));
+        sm = fmaxf(sm, __shfl_xor(sm, 32, 64));
+        mg[at] = (fabsf(sm) + fabsf(e1[at])) * 0x1p-14f;
+        const float lb = sm + es[at] - mg[at];
+        uint32_t mlow = lb > 0.f ? t3_bucket(lb) : 0u;
+        mlow = max(mlow, max(mp[at], 0x4000u));
+        thr[at] = __uint_as_float((mlow << 16) - 0x8000u) - e1[at] - mg[at];
+        if (q == 0) st_t[wave][at * 16 + j] = thr[at] - mg[at];
+      }
+    } else if (g == 2 * kT3Stages) {
+      // pass 2 (the survivors overflowed): thresholds at the atoms' final best buckets
+#pragma unroll
+      for (int at = 0; at < AT; ++at) {
+        const uint32_t M = st_m[wave][at * 16 + j];
+        thr[at] = M >= 0x4000u ? __uint_as_float((M << 16) - 0x8000u) - e1[at] - mg[at] : __builtin_inff();
+        if (q == 0) st_t[wave][at * 16 + j] = thr[at] - mg[at];
+      }
+    }
+    const uint8_t *L = stg[buf] + a_off;
+    const int tile0 = (g % kT3Stages) * kT3ST;
+    for (int k = 0; k < kT3ST; ++k) {
+      const bf16x8 a = *reinterpret_cast<const bf16x8 *>(L + k * kTileBytes);
+      f32x4 c[AT];
+#pragma unroll
+      for (int at = 0; at < AT; ++at)
+        c[at] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b[at], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+      if (pass == 0) {
+#pragma unroll
+        for (int at = 0; at < AT; ++at) {
+          const float v = fmaxf(fmaxf(m[at], fabsf(c[at][0])), fabsf(c[at][1]));
+          m[at] = fmaxf(fmaxf(v, fabsf(c[at][2])), fabsf(c[at][3]));
+        }
+        continue;
+      }
+#pragma unroll
+      for (int at = 0; at < AT; ++at) {
+        // the lane's largest |S| against the atom's threshold (a word and its complement: one test)
+        const float m4 = fmaxf(fmaxf(fabsf(c[at][0]), fabsf(c[at][1])), fmaxf(fabsf(c[at][2]), fabsf(c[at][3])));
+        const bool hit = m4 >= thr[at];
+        const uint64_t msk = __ballot(hit);
+        if (msk == 0ull) continue;
+        if (cnt > kT3Cap - 64) flush(pass);
+        if (hit) {
+          const float T = thr[at];
+          const uint32_t mask = (fabsf(c[at][0]) >= T ? 1u : 0u) | (fabsf(c[at][1]) >= T ? 2u : 0u) |
+                                (fabsf(c[at][2]) >= T ? 4u : 0u) | (fabsf(c[at][3]) >= T ? 8u : 0u);
+          const uint32_t pos = static_cast<uint32_t>(cnt) +
+                               __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(msk >> 32),
+                                                         __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(msk), 0u));
+          cand[wave][pos] = static_cast<uint32_t>(at * 16 + j) | static_cast<uint32_t>(tile0 + k) << 7 |
+                            static_cast<uint32_t>(q) << 14 | mask << 16;
+        }
+        cnt += __popcll(msk);
+      }
+    }
+    // every wave evaluates its list at the stage end, so no wave's evaluation holds the others at the barrier
+    if (pass > 0 && cnt > 0) flush(pass);
+    if (g == 2 * kT3Stages - 1) {
+      // pass 1 done: pass 2 only if a survivor list overflowed (all waves agree)
+      // (rows_by_sweep: pass 2 always -- the path an overflow takes, for its tests)
+      if (__syncthreads_or(rows_by_sweep != 0 || surv_n[wave] > static_cast<uint32_t>(kT3Surv))) {
+        g_end = 3 * kT3Stages;
+        stage_copy(g + 1, buf ^ 1);  // buffer buf ^ 1 was last read in stage g - 1, before the barrier
+        __syncthreads();
+      }
+    } else {
+      __syncthreads();
+    }
+  }
+  if (g_end == 2 * kT3Stages) {
+    // the lowest row at each atom's best bucket, from its survivors (every word that reached the final
+    // best bucket was at or above the running best when it was evaluated)
+    const int ns = static_cast<int>(surv_n[wave]);
+    for (int i = lane; i < ns; i += 64) {
+      const uint32_t se = surv[wave][i];
+      const int al = static_cast<int>(se & 0x7Fu);
+      const uint32_t wid = se >> 7;
+      const uint32_t M = st_m[wave][al];
+      const uint32_t *xr = xw[wave][al];
+      const uint32_t wr = wtab[wid & (kT3Reps - 1)];
+      const int sg = wid >= static_cast<uint32_t>(kT3Reps) ? 1 : 0;
+      const float D = t3_dot(xr, wr);
+      uint32_t rmin = 0xFFFFFFFFu;
+      word_scores(xr, wr, sg, D, [&](int p, float t) {
+        if (t > 0.f && t3_bucket(t) == M) rmin = min(rmin, t3_rows[wid * kDim + p]);
+      });
+      if (rmin != 0xFFFFFFFFu) atomicMin(&st_r[wave][al], rmin);
+    }
+  }
+  __syncthreads();  // (block-uniform: g_end is)
+  if (q == 0) {
+#pragma unroll
+    for (int at = 0; at < AT; ++at) {
+      const int64_t a = wave_atom0 + at * 16 + j;
+      if (a >= n_atoms) continue;
+      const uint32_t M = st_m[wave][at * 16 + j], r = st_r[wave][at * 16 + j];
+      *reinterpret_cast<uint2 *>(&keys[a]) = M >= 0x4000u && r != 0xFFFFFFFFu ? make_uint2(M << 16, r) : make_uint2(0u, 0u);
+    }
+  }
+}
+
 // Resolve: per block 256 atoms.
 //   scan     thread per atom: its keys (type-3 region; pair region: NN-B the
 //            first and the last group at the best bucket, NN-T / NN-P the
@@ -548,7 +876,9 @@ struct RsScore {  // per-candidate / per-atom running result
 // Sweep position (global, code granularity) of lane qq's code e in tile t of group g.
 __device__ __forceinline__ int sweep_pos(int g, int t, int qq, int e) { return (g * kG + t) * kTileCodes + 4 * qq + e; }
 
-template <int MODE, bool FUSED>
+// T3S (NN-B): the type-3 key is t3_kernel's (best bucket << 16, lowest row at
+// it) instead of the dense sweep's group key, so no type-3 group is rescanned.
+template <int MODE, bool FUSED, bool T3S = false>
 __global__ __launch_bounds__(256) void resolve_kernel(const uint4 *__restrict__ keys, int64_t n_atoms,
                                                       const float *__restrict__ src,
                                                       const float *__restrict__ sigma, int64_t atoms_per_row,
@@ -595,6 +925,7 @@ __global__ __launch_bounds__(256) void resolve_kernel(const uint4 *__restrict__ 
   // first group at the best |score| in [1]
   uint32_t M = 0, grp[5] = {0u, 0u, 0u, 0u, 0u}, lanes[5] = {0u, 0u, 0u, 0u, 0u};
   uint32_t span_g0 = 0, span_g1 = 0;  // NN-B: pair groups (span_g0, span_g1] to rescan for positive hits
+  uint32_t t3row = kNone;             // T3S: the lowest type-3 row at the best bucket
   bool many = false;
   bool active = false;
   if (a < n_atoms) {
@@ -621,8 +952,12 @@ __global__ __launch_bounds__(256) void resolve_kernel(const uint4 *__restrict__ 
       many |= n_at > 2;  // a record between the two: its groups are not candidates
       M = max(MT, MP);
       if (M != 0u && MT == M) {
-        grp[0] = 0x3FFu - ((k.x >> 6) & 0x3FFu);
-        lanes[0] = (k.x >> 2) & 0xFu;
+        if constexpr (T3S) {
+          t3row = k.y;
+        } else {
+          grp[0] = 0x3FFu - ((k.x >> 6) & 0x3FFu);
+          lanes[0] = (k.x >> 2) & 0xFu;
+        }
       }
       if (M != 0u && MP == M) {
         const uint64_t rr[2] = {rF, rL};
@@ -675,12 +1010,12 @@ __global__ __launch_bounds__(256) void resolve_kernel(const uint4 *__restrict__ 
     }
     // NN-P's origin rule (pack.py:174): |x|_2 < fp32(1e-8); no scan needed
     const bool p_snap = MODE == kModeP && sqrt(nrm2) < static_cast<double>(__uint_as_float(kEpsBits));
-    active = M != 0u && (lanes[0] | lanes[1] | lanes[2] | lanes[3] | lanes[4]) != 0u && !p_snap;
+    active = M != 0u && ((lanes[0] | lanes[1] | lanes[2] | lanes[3] | lanes[4]) != 0u || t3row != kNone) && !p_snap;
   }
   Ms[tid] = M;
 
   // per-atom merge state
-  uint32_t fT = kNone, fPpos = kNone, fPneg = kNone;  // NN-B
+  uint32_t fT = t3row, fPpos = kNone, fPneg = kNone;  // NN-B
   bool pos_first = false;  // NN-B: a positive hit in the earliest pair group (then the lowest pair row is known)
   score_t best_v = -__builtin_inf();
   uint32_t best_code = kNone;
@@ -957,7 +1292,8 @@ __global__ __launch_bounds__(256) void resolve_kernel(const uint4 *__restrict__ 
       const uint32_t found = min(fT, fS);
       const uint32_t bucket = found != kNone ? M : (__float_as_uint(static_cast<float>(best_v)) >> 16);
       row = found != kNone ? found : best_code;
-      snap = !(best_v > 0.f) || bucket < 0x4000u;  // bf16 max below 2.0
+      // bf16 max below 2.0 (a row found at bucket M needs no rescanned score: T3S type-3 rows have none)
+      snap = (found == kNone && !(best_v > 0.f)) || bucket < 0x4000u;
     } else {
       row = best_code;
       snap = !(2.0f * static_cast<float>(best_v) >= __uint_as_float(kCSqNormBits));
@@ -1040,27 +1376,60 @@ size_t keys_bytes(int64_t n_atoms) { return (static_cast<size_t>(n_atoms) * 16 +
 // First slice holding pair tiles, for a launch of n_slices slices.
 int first_pair_slice(int n_slices) { return kType3Tiles / (kSweepTiles / n_slices); }
 
-// NN-B pair records: 8 bytes per (atom, slice holding pair tiles)
+// NN-B pair records: 8 bytes per (atom, slice holding pair tiles) -- every
+// slice when the structured type-3 scorer runs (the sweep then covers the
+// pair region only), which is the larger of the two layouts
 size_t recs_bytes(int64_t n_atoms) {
   const int64_t ablocks = (n_atoms + kAtomsPerBlock - 1) / kAtomsPerBlock;
   const int n_slices = choose_slices(ablocks);
-  const size_t n_p = static_cast<size_t>(n_slices - first_pair_slice(n_slices));
-  return (static_cast<size_t>(n_atoms) * n_p * 8 + 255) & ~static_cast<size_t>(255);
+  return (static_cast<size_t>(n_atoms) * static_cast<size_t>(n_slices) * 8 + 255) & ~static_cast<size_t>(255);
 }
 
-// workspace = per-atom keys, the NN-B pair records, then (NN-B / NN-T) the bf16 planes
-template <int MODE, bool FUSED>
+// The pair region of the sweep: tiles [kType3Tiles, kSweepTiles), whole stages for every slice count.
+constexpr int kPairSweepTiles = kSweepTiles - kType3Tiles;  // 3,072
+static_assert(kPairSweepTiles % (32 * kST) == 0, "every slice count holds whole pair stages");
+
+// t3_kernel: atom tiles per wave by launch size, so small launches still fill the chip.
+int t3_launch(const uint4 *xb, int64_t n_atoms, const DeviceTables *tab, const uint64_t *recs, int n_recs,
+              uint4 *keys, hipStream_t s, int rows_by_sweep) {
+  const int AT = n_atoms >= 262144 ? 8 : n_atoms >= 131072 ? 4 : n_atoms >= 32768 ? 2 : 1;
+  const int64_t per_block = static_cast<int64_t>(kWaves) * AT * 16;
+  const int64_t blocks = (n_atoms + per_block - 1) / per_block;
+  if (blocks > 0x7FFFFFFFll) return fail(PLX_EINVAL, "quantize: %lld atoms exceed one launch", static_cast<long long>(n_atoms));
+  const dim3 g(static_cast<unsigned>(blocks));
+  profile_before(s, PLX_PROF_T3);
+  if (AT == 8)
+    hipLaunchKernelGGL(t3_kernel<8>, g, dim3(kThreads), 0, s, xb, n_atoms, tab->t3_tiles, tab->t3_words, tab->t3_rows,
+                       recs, n_recs, keys, rows_by_sweep);
+  else if (AT == 4)
+    hipLaunchKernelGGL(t3_kernel<4>, g, dim3(kThreads), 0, s, xb, n_atoms, tab->t3_tiles, tab->t3_words, tab->t3_rows,
+                       recs, n_recs, keys, rows_by_sweep);
+  else if (AT == 2)
+    hipLaunchKernelGGL(t3_kernel<2>, g, dim3(kThreads), 0, s, xb, n_atoms, tab->t3_tiles, tab->t3_words, tab->t3_rows,
+                       recs, n_recs, keys, rows_by_sweep);
+  else
+    hipLaunchKernelGGL(t3_kernel<1>, g, dim3(kThreads), 0, s, xb, n_atoms, tab->t3_tiles, tab->t3_words, tab->t3_rows,
+                       recs, n_recs, keys, rows_by_sweep);
+  profile_after(s, PLX_PROF_T3);
+  return check_launch("t3_kernel");
+}
+
+// workspace = per-atom keys, the NN-B pair records, then (NN-B / NN-T) the bf16 planes.
+// T3S (NN-B): the sweep covers the pair region only and t3_kernel scores the
+// type-3 codes; otherwise every sweep code is scored densely.
+template <int MODE, bool FUSED, bool T3S = false>
 int launch_mode(const float *x, const float *sigma, int64_t apr, int64_t n_atoms, const DeviceTables *tab,
-                int32_t *idx_out, uint8_t *packed_out, uint8_t *workspace, hipStream_t s) {
+                int32_t *idx_out, uint8_t *packed_out, uint8_t *workspace, hipStream_t s, int rows_by_sweep = 0) {
+  static_assert(!T3S || MODE == kModeB, "the structured type-3 scorer has NN-B semantics");
   const int64_t ablocks = (n_atoms + kAtomsPerBlock - 1) / kAtomsPerBlock;
   const int n_slices = choose_slices(ablocks);
-  const int tiles_per_slice = kSweepTiles / n_slices;
+  const int tiles_per_slice = (T3S ? kPairSweepTiles : kSweepTiles) / n_slices;
   const int64_t grid = ablocks * n_slices;
   if (grid > 0x7FFFFFFFll) return fail(PLX_EINVAL, "quantize: %lld atoms exceed one launch", static_cast<long long>(n_atoms));
   uint4 *keys = reinterpret_cast<uint4 *>(workspace);
   uint64_t *recs = reinterpret_cast<uint64_t *>(workspace + keys_bytes(n_atoms));
   uint4 *xb = reinterpret_cast<uint4 *>(workspace + keys_bytes(n_atoms) + recs_bytes(n_atoms));
-  const int s0 = first_pair_slice(n_slices);
+  const int s0 = T3S ? 0 : first_pair_slice(n_slices);
   int st;
   if (MODE != kModeP) {
     hipLaunchKernelGGL((prep_kernel<FUSED>), dim3(static_cast<unsigned>((n_atoms * 3 + 255) / 256)), dim3(256), 0, s, x,
@@ -1075,10 +1444,13 @@ int launch_mode(const float *x, const float *sigma, int64_t apr, int64_t n_atoms
   const uint8_t *tiles = MODE == kModeP ? tab->sw_raw_tiles : tab->sw_bf16_tiles;
   const void *operand = MODE == kModeP ? static_cast<const void *>(x) : static_cast<const void *>(xb);
   hipLaunchKernelGGL((nn_kernel<MODE>), dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0, s, operand, n_atoms, tiles,
-                     n_slices, tiles_per_slice, keys, recs, s0);
+                     n_slices, tiles_per_slice, keys, recs, s0, T3S ? kType3Tiles : 0);
   if ((st = check_launch("nn_kernel")) != PLX_OK) return st;
   profile_after(s);
-  hipLaunchKernelGGL((resolve_kernel<MODE, FUSED>), dim3(static_cast<unsigned>((n_atoms + 255) / 256)), dim3(256), 0, s,
+  if constexpr (T3S) {
+    if ((st = t3_launch(xb, n_atoms, tab, recs, n_slices, keys, s, rows_by_sweep)) != PLX_OK) return st;
+  }
+  hipLaunchKernelGGL((resolve_kernel<MODE, FUSED, T3S>), dim3(static_cast<unsigned>((n_atoms + 255) / 256)), dim3(256), 0, s,
                      keys, n_atoms, x, sigma, apr, xb, tab->sw_dq, tab->sw_idx, tab->sw_anti, tab->cb_raw,
                      tab->sw_bf16_tiles, static_cast<const uint64_t *>(recs), n_slices - s0, n_atoms, idx_out,
                      packed_out);
@@ -1118,8 +1490,16 @@ int launch_quantize(const float *x, const float *sigma, int64_t rows, int64_t co
   uint8_t *ws = static_cast<uint8_t *>(workspace);
   const bool fused = sigma != nullptr;
   const int64_t apr = cols / kDim;
+  const bool dense = (mode & PLX_NN_DENSE_TYPE3) != 0;
+  const int rows_by_sweep = (mode & PLX_NN_T3_ROWS_BY_SWEEP) != 0 ? 1 : 0;
+  mode &= ~(PLX_NN_DENSE_TYPE3 | PLX_NN_T3_ROWS_BY_SWEEP);
   if (mode == PLX_NN_PACK_FP32)
     st = launch_mode<PLX_NN_PACK_FP32, false>(x, nullptr, apr, n_atoms, tab, idx_out, packed_out, ws, s);
+  else if (mode == PLX_NN_BF16_SCORES && !dense)
+    st = fused ? launch_mode<PLX_NN_BF16_SCORES, true, true>(x, sigma, apr, n_atoms, tab, idx_out, packed_out, ws, s,
+                                                             rows_by_sweep)
+               : launch_mode<PLX_NN_BF16_SCORES, false, true>(x, sigma, apr, n_atoms, tab, idx_out, packed_out, ws, s,
+                                                              rows_by_sweep);
   else if (mode == PLX_NN_BF16_SCORES)
     st = fused ? launch_mode<PLX_NN_BF16_SCORES, true>(x, sigma, apr, n_atoms, tab, idx_out, packed_out, ws, s)
                : launch_mode<PLX_NN_BF16_SCORES, false>(x, sigma, apr, n_atoms, tab, idx_out, packed_out, ws, s);
@@ -1142,21 +1522,22 @@ namespace {
 // matrix, one nn_kernel launch over all their atoms (fewer codebook slices per
 // atom block and no per-matrix tail of the grid), then per matrix the resolve
 // (index + pack) and the scaled gather of the reconstructed weight.
-template <int MODE>
+template <int MODE, bool T3S = false>
 int launch_batch_mode(const RequantItem *items, int n_items, const DeviceTables *tab, uint8_t *workspace,
                       hipStream_t s) {
+  static_assert(!T3S || MODE == kModeB, "the structured type-3 scorer has NN-B semantics");
   int64_t total = 0;
   for (int i = 0; i < n_items; ++i) total += items[i].rows * (items[i].cols / kDim);
   if (total == 0) return PLX_OK;
   const int64_t ablocks = (total + kAtomsPerBlock - 1) / kAtomsPerBlock;
   const int n_slices = choose_slices(ablocks);
-  const int tiles_per_slice = kSweepTiles / n_slices;
+  const int tiles_per_slice = (T3S ? kPairSweepTiles : kSweepTiles) / n_slices;
   const int64_t grid = ablocks * n_slices;
   if (grid > 0x7FFFFFFFll) return fail(PLX_EINVAL, "requantize_batch: %lld atoms exceed one launch", static_cast<long long>(total));
   uint4 *keys = reinterpret_cast<uint4 *>(workspace);
   uint64_t *recs = reinterpret_cast<uint64_t *>(workspace + keys_bytes(total));
   uint4 *xb = reinterpret_cast<uint4 *>(workspace + keys_bytes(total) + recs_bytes(total));
-  const int s0 = first_pair_slice(n_slices);
+  const int s0 = T3S ? 0 : first_pair_slice(n_slices);
   int st;
   int64_t off = 0;
   for (int i = 0; i < n_items; ++i) {
@@ -1171,15 +1552,19 @@ int launch_batch_mode(const RequantItem *items, int n_items, const DeviceTables 
   }
   profile_before(s);
   hipLaunchKernelGGL((nn_kernel<MODE>), dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0, s,
-                     static_cast<const void *>(xb), total, tab->sw_bf16_tiles, n_slices, tiles_per_slice, keys, recs, s0);
+                     static_cast<const void *>(xb), total, tab->sw_bf16_tiles, n_slices, tiles_per_slice, keys, recs, s0,
+                     T3S ? kType3Tiles : 0);
   if ((st = check_launch("nn_kernel")) != PLX_OK) return st;
   profile_after(s);
+  if constexpr (T3S) {
+    if ((st = t3_launch(xb, total, tab, recs, n_slices, keys, s, 0)) != PLX_OK) return st;
+  }
   off = 0;
   for (int i = 0; i < n_items; ++i) {
     const RequantItem &it = items[i];
     const int64_t apr = it.cols / kDim, n = it.rows * apr;
     if (n == 0) continue;
-    hipLaunchKernelGGL((resolve_kernel<MODE, true>), dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s,
+    hipLaunchKernelGGL((resolve_kernel<MODE, true, T3S>), dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s,
                        keys + off, n, it.latent, it.sigma, apr, xb + off * 3, tab->sw_dq, tab->sw_idx, tab->sw_anti,
                        tab->cb_raw, tab->sw_bf16_tiles, static_cast<const uint64_t *>(recs + off), n_slices - s0, total,
                        it.idx, it.packed);
@@ -1212,8 +1597,12 @@ int launch_requantize_batch(const RequantItem *items, int n_items, int mode, voi
   int st = get_tables(&tab);
   if (st != PLX_OK) return st;
   uint8_t *ws = static_cast<uint8_t *>(workspace);
-  return mode == PLX_NN_BF16_SCORES ? launch_batch_mode<PLX_NN_BF16_SCORES>(items, n_items, tab, ws, s)
-                                    : launch_batch_mode<PLX_NN_FP32_SCORES>(items, n_items, tab, ws, s);
+  const bool dense = (mode & PLX_NN_DENSE_TYPE3) != 0;
+  mode &= ~(PLX_NN_DENSE_TYPE3 | PLX_NN_T3_ROWS_BY_SWEEP);
+  if (mode == PLX_NN_BF16_SCORES)
+    return dense ? launch_batch_mode<PLX_NN_BF16_SCORES>(items, n_items, tab, ws, s)
+                 : launch_batch_mode<PLX_NN_BF16_SCORES, true>(items, n_items, tab, ws, s);
+  return launch_batch_mode<PLX_NN_FP32_SCORES>(items, n_items, tab, ws, s);
 }
 
 // ---- allocation-free requantize (plx_requantize_noalloc) ----
@@ -1226,10 +1615,11 @@ int launch_requantize_batch(const RequantItem *items, int n_items, int mode, voi
 // needs nothing from the previous one, but calls that overlap on one device
 // (different streams at once) race on it.
 static_assert(PLX_NOALLOC_MAX_ATOMS > 0, "maximum atoms of the allocation-free entry point");
-// (at 2^20 atoms a launch uses 8 slices, 3 of them holding pair tiles: 16 B
-// of keys + 3 x 8 B of pair records + 48 B of operand planes per atom, the
-// largest workspace of any size up to the maximum; checked on every call)
-constexpr size_t kScratchBytes = static_cast<size_t>(PLX_NOALLOC_MAX_ATOMS) * (16 + 3 * 8 + 48);
+// (at 2^20 atoms a launch uses 8 slices, each holding pair tiles: 16 B of
+// keys + 8 x 8 B of pair records + 48 B of operand planes per atom, the
+// largest workspace of any size up to the maximum, plus the 256-byte rounding
+// of its three parts; checked on every call)
+constexpr size_t kScratchBytes = static_cast<size_t>(PLX_NOALLOC_MAX_ATOMS) * (16 + 8 * 8 + 48) + 1024;
 static __device__ __align__(256) uint8_t scratch[kScratchBytes];
 
 namespace {

@@ -33,6 +33,14 @@
 //                fields, 19,844 B), for the fp32 dequant-linear kernel, and
 // code_planes    per code its 3 plane-layout records (plx_internal.h), for
 //                plx_h24_plane_layout (1,572,488 B).
+// t3_tiles       the structured type-3 scorer's MFMA A operands: the sign
+//                patterns +-s (bf16 0x3EB5 / 0xBEB5) of the 2,048
+//                representative Golay words (bit 23 clear, ascending), in the
+//                sweep tiles' layout (128 tiles, 98,304 B);
+// t3_words       the word of each pattern id: representatives, then their
+//                complements (16,384 B);
+// t3_rows        the codebook row of the type-3 code with pattern id r and its
+//                -3 at position p, [4096][24] (393,216 B).
 
 #include <algorithm>
 #include <cstring>
@@ -146,6 +154,48 @@ int build(int dev, DeviceTables *t) {
         }
     }
 
+  // structured type-3 tables: representative words, their sign-pattern tiles,
+  // and the row of every (pattern, -3 position) code, matched against the
+  // codebook's type-3 rows (which must be exactly these 98,304 codes)
+  std::vector<uint32_t> reps;
+  const uint32_t *golay = golay_words_host();
+  for (int m = 0; m < 4096; ++m)
+    if (((golay[m] >> 23) & 1u) == 0u) reps.push_back(golay[m]);
+  std::sort(reps.begin(), reps.end());
+  if (static_cast<int>(reps.size()) != kT3Reps) return fail(PLX_EINVAL, "%zu Golay words with bit 23 clear", reps.size());
+  std::vector<uint32_t> t3w(kT3Words);
+  for (int r = 0; r < kT3Reps; ++r) {
+    t3w[r] = reps[r];
+    t3w[r + kT3Reps] = reps[r] ^ 0xFFFFFFu;
+  }
+  std::vector<uint16_t> t3_tiles(static_cast<size_t>(kT3Tiles) * (kTileBytes / 2), 0);
+  for (int r = 0; r < kT3Reps; ++r)
+    for (int c = 0; c < kDim; ++c)
+      t3_tiles[static_cast<size_t>(r / kTileCodes) * 384 + (c / 8) * 128 + (r % kTileCodes) * 8 + c % 8] =
+          bf_of[((reps[r] >> c) & 1u) ? 3 : 5];  // -s where the word has a 1, +s elsewhere
+  std::vector<std::pair<uint32_t, uint32_t>> t3key;  // (p << 24 | sign bits off p, row)
+  t3key.reserve(kType3Codes);
+  for (int i = 0; i < kType3Codes; ++i) {
+    const int code = sweep[static_cast<size_t>(i)];
+    const int8_t *r = raw + static_cast<size_t>(code) * kDim;
+    uint32_t bits = 0, pos = kDim;
+    for (int c = 0; c < kDim; ++c) {
+      if (r[c] == -3) pos = static_cast<uint32_t>(c);
+      else if (r[c] == -1) bits |= 1u << c;
+    }
+    t3key.emplace_back(pos << 24 | bits, static_cast<uint32_t>(code));
+  }
+  std::sort(t3key.begin(), t3key.end());
+  std::vector<uint32_t> t3rows(static_cast<size_t>(kT3Words) * kDim, 0);
+  for (int id = 0; id < kT3Words; ++id)
+    for (int pp = 0; pp < kDim; ++pp) {
+      const uint32_t key = static_cast<uint32_t>(pp) << 24 | (t3w[id] & ~(1u << pp));
+      const auto it = std::lower_bound(t3key.begin(), t3key.end(), std::make_pair(key, 0u));
+      if (it == t3key.end() || it->first != key)
+        return fail(PLX_EINVAL, "no type-3 codebook row for pattern %d with -3 at %d", id, pp);
+      t3rows[static_cast<size_t>(id) * kDim + pp] = it->second;
+    }
+
   // dequant-linear entries: 24 signed 4-bit coordinates, then type | pos << 8
   std::vector<uint32_t> gemv(static_cast<size_t>(kCodebook) * 4, 0);
   std::vector<uint32_t> dq(static_cast<size_t>(kCodebook) * 3, 0);
@@ -183,7 +233,8 @@ int build(int dev, DeviceTables *t) {
     for (int p = 0; p < 3; ++p) sw_dq[i * 3 + p] = dq[static_cast<size_t>(sweep[i]) * 3 + p];
 
   void *dt = nullptr, *drt = nullptr, *dsq = nullptr, *dsi = nullptr, *dsa = nullptr, *dr = nullptr, *dg = nullptr,
-       *dd = nullptr, *dk = nullptr, *dpi = nullptr, *dcp = nullptr, *dpn = nullptr;
+       *dd = nullptr, *dk = nullptr, *dpi = nullptr, *dcp = nullptr, *dpn = nullptr, *d3t = nullptr, *d3w = nullptr,
+       *d3r = nullptr;
   const PlaneTables *pt = plane_tables_host();
   if (!pt) return fail(PLX_EINVAL, "the codebook rows take more than %d distinct planes", kMaxPlanes);
   std::vector<uint32_t> pl_pad(pt->ids);  // whole 16-byte vectors (the kernels stage it by uint4)
@@ -209,6 +260,9 @@ int build(int dev, DeviceTables *t) {
       {pl_pad.data(), pl_pad.size() * 4, &dpi},
       {pt->code_planes.data(), pt->code_planes.size() * 2, &dcp},
       {pl_nib.data(), pl_nib.size() * 4, &dpn},
+      {t3_tiles.data(), t3_tiles.size() * 2, &d3t},
+      {t3w.data(), t3w.size() * 4, &d3w},
+      {t3rows.data(), t3rows.size() * 4, &d3r},
   };
   int st = PLX_OK;
   for (const Upload &u : ups) {
@@ -237,6 +291,9 @@ int build(int dev, DeviceTables *t) {
   t->pl_ids = static_cast<uint32_t *>(dpi);
   t->code_planes = static_cast<uint16_t *>(dcp);
   t->pl_nib = static_cast<uint32_t *>(dpn);
+  t->t3_tiles = static_cast<uint8_t *>(d3t);
+  t->t3_words = static_cast<uint32_t *>(d3w);
+  t->t3_rows = static_cast<uint32_t *>(d3r);
   t->device = dev;
   return PLX_OK;
 }

@@ -1,0 +1,115 @@
+"""The structured type-3 scorer (t3_kernel, the NN-B default) against the dense type-3 sweep and the oracle.
+
+Both compute NN-B (castor.py:544-557): indices must be equal on every atom that
+is not a near-tie (oracle/nn.py classifies each disagreement).  Cases: the
+config-4 distribution at every launch size the scorer distinguishes (1, 2, 4
+and 8 atom tiles per wave), atoms dominated by one coordinate (whose
+candidate threshold falls to zero or below, so both signs of a word are
+listed), near-origin and zero atoms, ragged small launches, and atoms whose
+best code sits in the type-3 family by construction (scaled type-3 codes plus
+noise).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import codebook as cb
+from oracle import nn
+from pollux_amd import castor
+
+pytestmark = pytest.mark.gpu
+
+
+def _c4_atoms(n, seed):
+    g = torch.Generator().manual_seed(seed)
+    d = torch.randn(n, 24, generator=g)
+    return d / d.norm(dim=1, keepdim=True) * (torch.rand(n, 1, generator=g) * 2.0 * np.sqrt(32.0))
+
+
+def _compare(dev, x, label, max_near=0.002):
+    xs = x.to(dev)
+    got = castor.quantize_indices(xs, mode="bf16").long().cpu()
+    ref = castor.quantize_indices(xs, mode="bf16-dense").long().cpu()
+    diff = (got != ref).nonzero().flatten()
+    near = 0
+    if len(diff):
+        o = nn.quantize(x[diff].numpy(), "B")
+        near = int(o["near_tie"].sum())
+        bad = diff[torch.from_numpy(~o["near_tie"])]
+        assert len(bad) == 0, (label, bad[:10].tolist(), got[bad[:10]].tolist(), ref[bad[:10]].tolist())
+    print(f"[t3 {label}] atoms={len(x)} disagree={len(diff)} near_ties={near}", flush=True)
+    assert len(diff) <= max(2, max_near * len(x))
+    return got
+
+
+@pytest.mark.parametrize("n", [1000, 40_000, 140_000, 300_000])
+def test_structured_equals_dense_c4(dev, n):
+    _compare(dev, _c4_atoms(n, n), f"c4 n={n}")
+
+
+@pytest.mark.parametrize("n", [1, 5, 63, 65, 513, 4097])
+def test_ragged_small_launches(dev, n):
+    x = _c4_atoms(n, 7 + n)
+    got = _compare(dev, x, f"ragged n={n}")
+    o = nn.quantize(x.numpy(), "B")
+    ok = ~o["near_tie"]
+    assert np.array_equal(got.numpy()[ok], o["idx"][ok])
+
+
+def test_spiky_atoms(dev):
+    # one coordinate far larger than the rest: the bound on the bonus spans the whole S range, so the
+    # candidate threshold is <= 0 and both signs of words are listed (the slow but exact path)
+    g = torch.Generator().manual_seed(11)
+    n = 20_000
+    x = torch.randn(n, 24, generator=g) * 0.05
+    k = torch.randint(0, 24, (n,), generator=g)
+    mag = torch.rand(n, generator=g) * 8.0 + 1.0
+    sign = torch.where(torch.rand(n, generator=g) < 0.5, -1.0, 1.0)
+    x[torch.arange(n), k] = mag * sign
+    _compare(dev, x, "spiky")
+
+
+def test_near_origin_and_zero_atoms(dev):
+    g = torch.Generator().manual_seed(12)
+    d = torch.randn(30_000, 24, generator=g)
+    d = d / d.norm(dim=1, keepdim=True)
+    r = torch.rand(30_000, 1, generator=g) * 2.5  # around the origin boundary (norm sqrt 2 in these units)
+    x = torch.cat([torch.zeros(100, 24), d * r])
+    got = _compare(dev, x, "near-origin")
+    assert torch.all(got[:100] == 0)
+
+
+def test_type3_winners(dev):
+    # scaled type-3 codes plus noise: the type-3 family holds the answer, often with close runners-up
+    rng = np.random.default_rng(13)
+    c32 = cb.codebook_f32()
+    raw = cb.codebook_int8()
+    t3 = np.nonzero((raw == -3).any(1))[0]
+    pick = rng.choice(t3, 20_000)
+    x = c32[pick] * rng.uniform(0.6, 1.6, (20_000, 1)) + rng.normal(0, 0.08, (20_000, 24))
+    got = _compare(dev, torch.from_numpy(x.astype(np.float32)), "type-3 winners")
+    assert (got.numpy() == pick).mean() > 0.5
+
+
+def test_fixed_points_of_every_type3_code(dev):
+    c = torch.from_numpy(cb.codebook_f32()[1:].copy())
+    got = castor.quantize_indices(c.to(dev), mode="bf16").long().cpu()
+    assert torch.equal(got, torch.arange(1, 196561))
+
+
+def test_row_sweep_path_equals_survivor_path(dev):
+    # the lowest row at the best bucket comes from the per-wave survivor lists unless one overflows; the
+    # overflow path (a third sweep over the patterns) must give the same indices on every atom
+    g = torch.Generator().manual_seed(14)
+    n = 60_000
+    spiky = torch.randn(n // 4, 24, generator=g) * 0.05
+    spiky[torch.arange(n // 4), torch.randint(0, 24, (n // 4,), generator=g)] = 4.0
+    raw = torch.from_numpy(cb.codebook_f32())
+    t3 = torch.nonzero(torch.from_numpy((cb.codebook_int8() == -3).any(1))).flatten()
+    pick = t3[torch.randint(0, len(t3), (n // 4,), generator=g)]
+    near_t3 = raw[pick] * 1.1 + torch.randn(n // 4, 24, generator=g) * 0.08
+    x = torch.cat([_c4_atoms(n // 2, 15), spiky, near_t3]).to(dev)
+    a = castor.quantize_indices(x, mode="bf16").cpu()
+    b = castor.quantize_indices(x, mode="bf16-rows-sweep").cpu()
+    assert torch.equal(a, b), int((a != b).sum())
