@@ -10,10 +10,14 @@ input.  One step = ``castor.quantize_indices`` over all of them (fp32 atoms
 resident in HBM -> int32 codebook indices).
 
 The JSON line also carries
-  roofline      the scoring kernel (nn_kernel) of that launch against the dense
-                bf16 MFMA peak: algorithmic flops 2*24*196,560 per atom over its
-                HIP-event kernel time inside the timed region (events recorded
-                on the launch stream); traffic from profiles/ (rocprofv3 --pmc);
+  roofline      the dominant kernel of that launch, nn_kernel's sweep of the pair
+                region, against the dense bf16 MFMA peak: algorithmic flops
+                2*24*49,128 per atom (one dot product per type-1 / type-2
+                representative) over its HIP-event kernel time inside the timed
+                region (events recorded on the launch stream); traffic from
+                profiles/ (rocprofv3 --pmc); beside it t3_kernel's time (the
+                structured type-3 scorer);
+  dense_sweep_baseline  the same quantize with every code swept densely;
   dequant_gemv  the metric's second half: the fused dequant-GEMV at d=1920
                 (config 5, batch 1) in compressed-stream GB/s and as a fraction
                 of HBM peak;
@@ -42,12 +46,21 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 METRIC = "atoms/sec Leech NN quantize (+MFMA util %); dequant-GEMV GB/s at d=1920"
-FLOP_PER_ATOM = 2 * 24 * 196_560  # 9,434,880 algorithmic flops (origin free, K padding not counted)
-# MFMA flops the sweep issues per atom: 9,216 tiles of 16 codes (the 98,304
+# The dense sweep (NN-T, NN-P, and NN-B with the dense type-3 sweep): every code scored,
+# 2 * 24 * 196,560 = 9,434,880 flops per atom (origin free, K padding not counted).
+FLOP_PER_ATOM = 2 * 24 * 196_560
+# MFMA flops the dense sweep issues per atom: 9,216 tiles of 16 codes (the 98,304
 # type-3 codes, one representative per antipodal pair of the others, padding)
-# at K = 32 (24 coordinates + 8 zeros) -- 9,437,184, within 0.03% of the
-# algorithmic count: the pair symmetry saves what the K padding costs.
+# at K = 32 (24 coordinates + 8 zeros) -- 9,437,184.
 MFMA_FLOP_ISSUED_PER_ATOM = 2 * 32 * 9216 * 16
+# NN-B's default path: nn_kernel sweeps the pair region only -- 49,128 representatives
+# of the 98,256 type-1 / type-2 codes, whose antipodes' scores are the negations
+# (no products) -- 2 * 24 * 49,128 = 2,358,144 algorithmic flops per atom, issued as
+# 3,072 tiles at K = 32 (3,145,728); t3_kernel scores the 98,304 type-3 codes from
+# 128 tiles of Golay sign patterns plus per-candidate VALU work.
+PAIR_REPS = 49_128
+FLOP_PER_ATOM_PAIRS = 2 * 24 * PAIR_REPS
+MFMA_FLOP_ISSUED_PER_ATOM_PAIRS = 2 * 32 * 3072 * 16
 PEAK_BF16_FLOPS = 2.5e15  # MI355X dense bf16 MFMA
 PEAK_HBM_BPS = 8.0e12  # MI355X HBM3E
 C2_SHAPES = [(3456, 1152), (1152, 1152), (4608, 1152), (1152, 4608)]
@@ -447,7 +460,7 @@ def optim_extras(device, mats, iters=9, sets=3):
     t_f, nn_ms = _profiled(full_step, 3, 0, warmup=1)
     out["pollux1920_step"] = {
         "atoms": atoms, "step_ms": t_f * 1e3, "atoms_per_s": atoms / t_f, "nn_kernel_ms": nn_ms,
-        "nn_kernel_mfma_frac": FLOP_PER_ATOM * atoms / (nn_ms / 1e3) / PEAK_BF16_FLOPS,
+        "nn_kernel_mfma_frac": FLOP_PER_ATOM_PAIRS * atoms / (nn_ms / 1e3) / PEAK_BF16_FLOPS,
         "note": "plx_pollux_step_h24_batch over all 111 H24 tensors of Pollux-1920 (18 x q/k/v/o 1920x1920, "
                 "fc1 7680x1920, fc2 1920x7680; tok_emb and head 50688x1920; pos_emb 1024x1920): 111 update "
                 "passes and one scoring sweep; synthetic state (latent N(0, 0.02))"}
@@ -553,10 +566,11 @@ def sweep_extras(device, mode="bf16", steps=10):
     t, k_ms = _nn_profiled(step2, steps)
     out["config2_requantize"] = {
         "atoms": atoms2, "ms_per_step": t * 1e3, "atoms_per_s": atoms2 / t, "nn_kernel_ms_avg": k_ms,
-        "nn_kernel_mfma_frac": FLOP_PER_ATOM * atoms2 / 4 / (k_ms / 1e3) / PEAK_BF16_FLOPS,
+        "nn_kernel_mfma_frac": FLOP_PER_ATOM_PAIRS * atoms2 / 4 / (k_ms / 1e3) / PEAK_BF16_FLOPS,
         "note": "fused row scale + NN-B + pack + reconstructed weight of QKV 3456x1152, O 1152x1152, up 4608x1152, "
                 "down 1152x4608 (bf16-rounded N(0, 0.02) master weights), one requantize_h24 call per latent "
-                "(pollux.py:828-884); nn_kernel_mfma_frac over the average of the four launches"}
+                "(pollux.py:828-884); nn_kernel_mfma_frac: the pair sweep's algorithmic flops over the average of the "
+                "four launches"}
     t_b = time_gpu(lambda: castor.requantize_h24_many(mats2, mode=mode), steps, 2)
     out["config2_requantize_batched"] = {
         "ms_per_step": t_b * 1e3, "atoms_per_s": atoms2 / t_b,
@@ -819,7 +833,7 @@ def main() -> int:
     ap.add_argument("--cpu-atoms", type=int, default=262_144, help="CPU baseline sample size (atoms)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true")
-    ap.add_argument("--mode", default="bf16", choices=["bf16", "fp32"])
+    ap.add_argument("--mode", default="bf16", choices=["bf16", "bf16-dense", "fp32"])
     ap.add_argument(
         "--pmc-workload",
         choices=["c4", "c2", "hbm"],
@@ -912,23 +926,41 @@ def main() -> int:
     log(f"[bench] timed {args.steps} steps: {ms_per_step:.3f} ms/step, {value:.4g} atoms/s")
 
     kernel_s = tot_ms.value / 1e3
-    flops = FLOP_PER_ATOM * atoms * args.steps
-    achieved = flops / kernel_s if kernel_s > 0 else 0.0
+    structured = args.mode == "bf16"
+    fpa = FLOP_PER_ATOM_PAIRS if structured else FLOP_PER_ATOM
+    issued = MFMA_FLOP_ISSUED_PER_ATOM_PAIRS if structured else MFMA_FLOP_ISSUED_PER_ATOM
+    achieved = fpa * atoms * args.steps / kernel_s if kernel_s > 0 else 0.0
     roofline = {
         "bound": "mfma",
         "achieved": achieved / 1e12,
         "peak": PEAK_BF16_FLOPS / 1e12,
         "unit": "TFLOP/s",
         "frac": achieved / PEAK_BF16_FLOPS,
-        "traffic": traffic_from_profiles(),
-        "kernel": "nn_kernel (bf16 16x16x32 MFMA scoring + running max)",
+        "traffic": traffic_from_profiles("nn_kernel_c4_traffic.json" if structured else "nn_kernel_c4_dense_traffic.json"),
+        "kernel": "nn_kernel (bf16 16x16x32 MFMA scoring + running max)"
+        + (": the pair sweep (type-1 / type-2 representatives, 3,072 tiles)" if structured else ""),
         "kernel_launches": int(launches.value),
         "kernel_avg_ms": tot_ms.value / max(1, launches.value),
-        "flop_per_atom": FLOP_PER_ATOM,
-        "flop_per_launch": FLOP_PER_ATOM * atoms,
-        "mfma_issue_frac": MFMA_FLOP_ISSUED_PER_ATOM * atoms * args.steps / kernel_s / PEAK_BF16_FLOPS
-        if kernel_s > 0 else 0.0,
+        "flop_per_atom": fpa,
+        "flop_per_launch": fpa * atoms,
+        "mfma_issue_frac": issued * atoms * args.steps / kernel_s / PEAK_BF16_FLOPS if kernel_s > 0 else 0.0,
     }
+    if structured:
+        # the rest of the scoring: the structured type-3 scorer, and the dense type-3 sweep it replaces
+        _, t3_ms = _profiled(step, 3, _lib.PROF_T3)
+        t_d, nn_d = _profiled(lambda: castor.quantize_indices(x, mode="bf16-dense"), 3, 0, warmup=1)
+        roofline["flop_per_atom_note"] = (
+            "2 * 24 flops per pair representative (49,128 per atom; an antipode's score is the negation, no "
+            "products); the type-3 codes are scored by t3_kernel, not counted here")
+        roofline["t3_kernel_avg_ms"] = t3_ms
+        roofline["t3_kernel_step_share"] = t3_ms / ms_per_step
+        result_dense = {
+            "ms_per_step": t_d * 1e3, "atoms_per_s": atoms / t_d, "nn_kernel_avg_ms": nn_d,
+            "nn_kernel_frac": FLOP_PER_ATOM * atoms / (nn_d / 1e3) / PEAK_BF16_FLOPS,
+            "nn_kernel_mfma_issue_frac": MFMA_FLOP_ISSUED_PER_ATOM * atoms / (nn_d / 1e3) / PEAK_BF16_FLOPS,
+            "note": "the same workload with every code swept densely (9,216 tiles, 2 * 24 * 196,560 flops per "
+                    "atom; castor mode 'bf16-dense', PLX_NN_DENSE_TYPE3): the baseline the structured type-3 "
+                    "scorer is measured against; identical indices off near-ties"}
 
     result = {
         "metric": METRIC,
@@ -948,12 +980,16 @@ def main() -> int:
             "1920, the config's 16,777,216 rounded down to whole rows), directions uniform on S^23, radius "
             "U(0, 2) * sqrt(32), fed directly as quantizer input; fp32 atoms in HBM -> int32 indices",
             "atoms_per_step": atoms,
-            "call": "castor.quantize_indices (plx_quantize: operand prep, nn_kernel scoring sweep, resolve)",
-            "nn_mode": "NN-B (bf16 scores)" if args.mode == "bf16" else "NN-T (fp32 scores)",
+            "call": "castor.quantize_indices (plx_quantize: operand prep, nn_kernel pair sweep, t3_kernel "
+            "structured type-3 scorer, resolve)" if structured else
+            "castor.quantize_indices (plx_quantize: operand prep, nn_kernel scoring sweep, resolve)",
+            "nn_mode": "NN-T (fp32 scores)" if args.mode == "fp32" else "NN-B (bf16 scores)",
             "seed": 404,
         },
         "roofline": roofline,
     }
+    if structured:
+        result["dense_sweep_baseline"] = result_dense
     log("[bench] dequant-GEMV / GEMM at config 5")
     gemv = gemv_extras(dev)
     result["dequant_gemv"] = gemv_headline(gemv)
