@@ -622,34 +622,43 @@ __global__ __launch_bounds__(NT) void dqlinear_kernel(const DqlArgs<GEN> targets
 }
 
 // One token of bf16 activations, one target, no epilogue (the plain GEMV
-// call): the arithmetic of dqlinear_kernel<L, 1> with two changes.
-// - Each plane of 8 raw integers becomes 4 bf16 pairs by v_perm_b32 byte
-//   lookups of its kp_dq value ids (exact: the integers are small), and
-//   v_dot2_f32_bf16 multiplies them by the bf16 x pairs (exact products,
-//   fp32 sums): 12 dot products and 24 lookups per atom where the fp32 path
-//   spends 24 extract / convert / fma triples.  kp_dot holds each code's
-//   3 kp_dq words and its type | position of -3 << 8 (16 B, one gather).
+// call): the arithmetic of dqlinear_kernel<L, 1> with three changes.
+// - Codes as bf16 pairs from a table of halves: the codebook rows' 8-coordinate
+//   planes take only 161 distinct 4-coordinate halves, so gv_tab holds each
+//   half as two bf16 pairs (raw integers, exact) and each plane as two half
+//   symbols; the block stages it in LDS (11.3 KB with the plane entries, 1.3
+//   KB without) and v_dot2_f32_bf16 multiplies the looked-up pairs by the bf16
+//   x pairs (exact products, fp32 sums in the fixed order pairs 0,1 | 2,3 |
+//   4,5 | 6,7 per plane).  Nothing is decoded per atom: a code (packed stream)
+//   gathers its 8-byte kp_half entry (6 half symbols, type, position of -3), a
+//   plane-layout record its plane's two symbols from LDS.  (The half table
+//   replaced v_perm_b32 expansion of 3-bit value ids, 11 VALU instructions per
+//   plane, and the 19.8 KB table of plane value ids.)
 // - It is written so that the compiler issues one round of loads (packed
-//   bytes as raw buffer loads, sigma16, x), one barrier, one round of LDS
-//   reads of the lane's atom bytes and one round of gathers: every thread
-//   stores to LDS (no load sits under a branch) and atoms past the row
-//   decode as the origin (no branch per atom).
-// Measured in a graph of 200 calls on distinct copies (bench.py): 7680 x 1920
-// 5.65 -> 5.40 us, 1920 x 7680 5.95 -> 5.43 us.  fp32 activations keep
-// dqlinear_kernel (this layout measured the same there).
+//   bytes as raw buffer loads, sigma16, x, the table), one barrier, then the
+//   rounds of LDS reads and gathers: every thread stores to LDS (no load sits
+//   under a branch) and atoms past the row decode as the origin (no branch
+//   per atom).
+// - The epilogue's four dequantized values of the row scale are computed by
+//   four lanes of the row (one each) and broadcast within the quad by DPP.
+// Measured in a graph of 200 calls on distinct copies: value-id expansion
+// 5.40 / 5.43 us (7680 x 1920 / 1920 x 7680), and probe copies attributed
+// 0.44 us to the expansion and 0.23 us to staging the plane value ids.  fp32
+// activations keep dqlinear_kernel (this layout measured the same there).
 constexpr int kG1Atoms = 5;  // atoms per lane
-// PL: `packed` is the plane layout (3 uint16 records per atom): the value-id
-// words come from the plane table staged in LDS instead of a kp_dot gather
-// (same graph, A/B: 7680 x 1920 5.34 -> 4.94 us, 1920 x 7680 5.49 -> 5.34 us).
+// PL: `packed` is the plane layout (3 uint16 records per atom: plane index |
+// extra bits << 13): the plane's two half symbols come from the staged table.
 template <int L, bool PL>
 __global__ __launch_bounds__(512) void dqgemv1_kernel(const uint8_t *__restrict__ packed, int packed_bytes,
                                                       const uint16_t *__restrict__ sigma16, int rows, int apr,
-                                                      const uint16_t *__restrict__ x, const uint4 *__restrict__ kp_dot,
-                                                      const uint32_t *__restrict__ pl_ids, int pl_vecs, int round_w,
+                                                      const uint16_t *__restrict__ x, const uint2 *__restrict__ kp_half,
+                                                      const uint4 *__restrict__ gv_tab, int round_w,
                                                       float *__restrict__ y) {
   constexpr int NT = 512, R = NT / L, G = kG1Atoms;
   constexpr int VPT = PL ? 2 : 1;   // staged 16-byte vectors of the block's atom bytes per thread
-  constexpr int TPT = 3;  // PL: plane-table vectors per thread (the host checks pl_vecs <= TPT * NT; lookups clamped to them)
+  constexpr int TV = PL ? kGvVecs : kGvHalfVecs;  // table vectors staged (PL: halves and plane entries)
+  constexpr int TPT = (TV + NT - 1) / NT;         // per thread
+  static_assert(L >= 8, "the epilogue takes its four values from the row's first quad");
   typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
   extern __shared__ __align__(16) uint8_t smem[];
   const int tid = threadIdx.x;
@@ -666,11 +675,13 @@ __global__ __launch_bounds__(512) void dqgemv1_kernel(const uint8_t *__restrict_
   const int base16 = start & ~15;
   const int nvec = (end - base16 + 15) >> 4;
   const int pb_off = start - base16;
-  // LDS: VPT NT atom-byte vectors, 2 NT pieces of 8 bf16 x values, (PL) TPT NT plane-table vectors;
+  // LDS: VPT NT atom-byte vectors, 2 NT pieces of 8 bf16 x values, TPT NT table vectors;
   // every thread stores all its slots, so no load sits under a branch
   uint16_t *xh = reinterpret_cast<uint16_t *>(smem + VPT * NT * 16);
-  uint32_t *ptab = reinterpret_cast<uint32_t *>(smem + VPT * NT * 16 + 2 * NT * 16);
-  // round of loads: atom bytes, plane table, sigma16, x pieces.  The buffer range covers the
+  uint4 *tabs = reinterpret_cast<uint4 *>(smem + VPT * NT * 16 + 2 * NT * 16);
+  const uint2 *hp = reinterpret_cast<const uint2 *>(tabs);                    // [kGvHalves] half pairs
+  const uint16_t *php = reinterpret_cast<const uint16_t *>(tabs + kGvHalfVecs);  // [kGvPlanes] (PL)
+  // round of loads: atom bytes, table, sigma16, x pieces.  The buffer range covers the
   // stream rounded up to whole dwords (a dword reaching past the range reads as zero; the last
   // dword lies in the same page as the stream's last byte, the base being 16-byte aligned);
   // dwords wholly past it read as zero.
@@ -685,13 +696,11 @@ __global__ __launch_bounds__(512) void dqgemv1_kernel(const uint8_t *__restrict_
 #pragma unroll
     for (int k = 0; k < 4; ++k) d[v][k] = __builtin_amdgcn_raw_buffer_load_b32(prs, poff + 4 * k, 0, 0);
   }
-  uint4 tq[PL ? TPT : 1];
-  if constexpr (PL) {
+  uint4 tq[TPT];
 #pragma unroll
-    for (int v = 0; v < TPT; ++v) {
-      const int vi = tid + v * NT;
-      tq[v] = reinterpret_cast<const uint4 *>(pl_ids)[vi < pl_vecs ? vi : 0];
-    }
+  for (int v = 0; v < TPT; ++v) {
+    const int vi = tid + v * NT;
+    tq[v] = gv_tab[vi < TV ? vi : 0];
   }
   const uint16_t sig_bits = sigma16[row < rows ? row : rows - 1];
   const int items = cols / 8;  // pieces of x (the host checks items <= 2 * NT)
@@ -705,17 +714,16 @@ __global__ __launch_bounds__(512) void dqgemv1_kernel(const uint8_t *__restrict_
   for (int v = 0; v < VPT; ++v) reinterpret_cast<uint4 *>(smem)[tid + v * NT] = make_uint4(d[v][0], d[v][1], d[v][2], d[v][3]);
 #pragma unroll
   for (int h = 0; h < 2; ++h) reinterpret_cast<uint4 *>(xh)[tid + h * NT] = xq[h];  // pieces past x: unused slots
-  if constexpr (PL) {
 #pragma unroll
-    for (int v = 0; v < TPT; ++v) reinterpret_cast<uint4 *>(ptab)[tid + v * NT] = tq[v];
-  }
+  for (int v = 0; v < TPT; ++v) tabs[tid + v * NT] = tq[v];
   __syncthreads();
   float sig = __half2float(__ushort_as_half(sig_bits));
   asm volatile("" : "+v"(sig));  // keeps the sigma16 load in the first round (else it sinks into the epilogue)
   const int lrow = min(tid / L, rows_here - 1);
-  uint4 e[G];  // per atom: the 3 value-id words, then type | position of -3 << 8
+  uint32_t hs[G][3];  // per atom and plane: its two half symbols (lo | hi << 8)
+  uint32_t meta[G];   // per atom: type | position of -3 << 8
   if constexpr (PL) {
-    // round of LDS reads: the lane's atoms' 3 records, then their planes' value-id words
+    // round of LDS reads: the lane's atoms' 3 records, then their planes' half symbols
     uint32_t r[G][3];
 #pragma unroll
     for (int i = 0; i < G; ++i) {
@@ -730,14 +738,14 @@ __global__ __launch_bounds__(512) void dqgemv1_kernel(const uint8_t *__restrict_
       const bool in = sub + i * L < apr;
       const uint32_t type = in ? (r[i][0] >> 13) & 3u : 0u;
       const uint32_t pos = ((r[i][1] >> 13) & 7u) | ((r[i][2] >> 13) & 3u) << 3;
-      // (clamped to the staged table: a layout not made by plane_layout_kernel cannot index past it)
-      constexpr uint32_t kLast = TPT * NT * 4 - 1;
-      e[i] = make_uint4(ptab[min(r[i][0] & 0x1FFFu, kLast)], ptab[min(r[i][1] & 0x1FFFu, kLast)],
-                        ptab[min(r[i][2] & 0x1FFFu, kLast)], type | pos << 8);
+      // (clamped to the staged entries: a layout not made by plane_layout_kernel cannot index past them)
+#pragma unroll
+      for (int k = 0; k < 3; ++k) hs[i][k] = php[min(r[i][k] & 0x1FFFu, static_cast<uint32_t>(kGvPlanes - 1))];
+      meta[i] = type | pos << 8;
     }
   } else {
     // round of LDS reads: the lane's atoms sub, sub + L, ... (clamped to the block's atoms), 3 bytes
-    // each from two aligned words; then the round of gathers
+    // each from two aligned words; then the round of kp_half gathers
     const int nbase = lrow * apr + (atom0 - g_lo * 4);
     uint32_t w0[G], w1[G];
     int nn[G];
@@ -756,26 +764,28 @@ __global__ __launch_bounds__(512) void dqgemv1_kernel(const uint8_t *__restrict_
       const uint32_t v = __builtin_amdgcn_perm(w1[i], w0[i], (o + 2) | ((o + 1) << 8) | (o << 16) | 0x0C000000u);
       int32_t code = static_cast<int32_t>((v >> (6 - 2 * (n & 3))) & 0x3FFFFu);
       if (code > kKissing || sub + i * L >= apr) code = 0;
-      e[i] = kp_dot[code];
+      const uint2 kh = kp_half[code];
+      hs[i][0] = kh.x & 0xFFFFu;
+      hs[i][1] = kh.x >> 16;
+      hs[i][2] = kh.y & 0xFFFFu;
+      meta[i] = kh.y >> 16;
     }
   }
   float acc[4] = {0.f, 0.f, 0.f, 0.f};
-  const uint4 itab = int_value_table();
 #pragma unroll
   for (int i = 0; i < G; ++i) {
     const int a = min(sub + i * L, apr - 1);
-    const uint32_t type = e[i].w & 3u;
-    const int pos = static_cast<int>((e[i].w >> 8) & 31u);
-    const uint32_t cw[3] = {e[i].x, e[i].y, e[i].z};
+    const uint32_t type = meta[i] & 3u;
+    const int pos = static_cast<int>((meta[i] >> 8) & 31u);
     float D = 0.f;
 #pragma unroll
     for (int p = 0; p < 3; ++p) {
-      const uint4 kp = ids_to_pairs(cw[p], itab);
+      const uint2 lo = hp[hs[i][p] & 0xFFu], hi = hp[(hs[i][p] >> 8) & 0xFFu];
       const uint4 xv = *reinterpret_cast<const uint4 *>(xh + a * kDim + 8 * p);
-      D = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, kp.x), __builtin_bit_cast(bf16x2_t, xv.x), D, false);
-      D = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, kp.y), __builtin_bit_cast(bf16x2_t, xv.y), D, false);
-      D = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, kp.z), __builtin_bit_cast(bf16x2_t, xv.z), D, false);
-      D = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, kp.w), __builtin_bit_cast(bf16x2_t, xv.w), D, false);
+      D = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, lo.x), __builtin_bit_cast(bf16x2_t, xv.x), D, false);
+      D = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, lo.y), __builtin_bit_cast(bf16x2_t, xv.y), D, false);
+      D = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, hi.x), __builtin_bit_cast(bf16x2_t, xv.z), D, false);
+      D = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, hi.y), __builtin_bit_cast(bf16x2_t, xv.w), D, false);
     }
     const float xp = __uint_as_float(static_cast<uint32_t>(xh[a * kDim + pos]) << 16);
     acc[0] += type == 1u ? D : 0.f;
@@ -784,18 +794,12 @@ __global__ __launch_bounds__(512) void dqgemv1_kernel(const uint8_t *__restrict_
     acc[3] += type == 3u ? xp : 0.f;
   }
   group_reduce<L>(acc);
-  if (sub == 0 && row < rows) {
-    const float sl = __uint_as_float(kSLatticeBits);
-    const float v1 = __half2float(__ushort_as_half(static_cast<uint16_t>(dq_value(1, sig, sl))));
-    const float v2 = __half2float(__ushort_as_half(static_cast<uint16_t>(dq_value(2, sig, sl))));
-    const float v3 = __half2float(__ushort_as_half(static_cast<uint16_t>(dq_value(3, sig, sl))));
-    const float v4 = __half2float(__ushort_as_half(static_cast<uint16_t>(dq_value(4, sig, sl))));
-    const float m1 = round_w ? bf16_bits_to_float(bf16_rne_bits(v1)) : v1;
-    const float m2 = round_w ? bf16_bits_to_float(bf16_rne_bits(v2)) : v2;
-    const float m3 = round_w ? bf16_bits_to_float(bf16_rne_bits(v3)) : v3;
-    const float m4 = round_w ? bf16_bits_to_float(bf16_rne_bits(v4)) : v4;
-    y[row] = m4 * (acc[0] * 0.25f) + m2 * (acc[1] * 0.5f) + m1 * acc[2] - m3 * acc[3];
-  }
+  // lane sub & 3 of the row's first quad computes the dequantized value of raw coordinate 1 + (sub & 3)
+  const float vk = __half2float(__ushort_as_half(static_cast<uint16_t>(
+      dq_value(1 + (sub & 3), sig, __uint_as_float(kSLatticeBits)))));
+  const float mk = round_w ? bf16_bits_to_float(bf16_rne_bits(vk)) : vk;
+  const float m1 = dpp_f32<0x00>(mk), m2 = dpp_f32<0x55>(mk), m3 = dpp_f32<0xAA>(mk), m4 = dpp_f32<0xFF>(mk);
+  if (sub == 0 && row < rows) y[row] = m4 * (acc[0] * 0.25f) + m2 * (acc[1] * 0.5f) + m1 * acc[2] - m3 * acc[3];
 }
 
 // packed 18-bit indices -> the plane layout: per atom the 3 records of its code
@@ -820,15 +824,15 @@ int launch_gemv1_planes_l(const uint8_t *planes, const uint16_t *sigma16, int64_
   constexpr int NT = 512, R = NT / L;
   const int64_t blocks = (rows + R - 1) / R;
   const int64_t nvec_max = (6 * R * apr + 31) / 16;
-  const int64_t pl_vecs = (static_cast<int64_t>(plane_tables_host()->ids.size()) + 3) / 4;
-  if (apr > static_cast<int64_t>(kG1Atoms) * L || nvec_max > 2 * NT || apr * kDim / 8 > 2 * NT || pl_vecs > 3 * NT ||
+  static_assert(kGvVecs <= 2 * NT, "the GEMV table fits its two LDS slots per thread");
+  if (apr > static_cast<int64_t>(kG1Atoms) * L || nvec_max > 2 * NT || apr * kDim / 8 > 2 * NT ||
       6 * rows * apr >= (static_cast<int64_t>(1) << 30))
     return fail(PLX_EINVAL, "dequant_linear: the plane layout takes rows of at most %d atoms at one token (got %lld)",
                 kG1Atoms * 64, static_cast<long long>(apr));
   hipLaunchKernelGGL((dqgemv1_kernel<L, true>), dim3(static_cast<unsigned>(blocks)), dim3(NT),
-                     static_cast<size_t>(NT) * (32 + 32 + 48), s, planes, static_cast<int>(6 * rows * apr), sigma16,
+                     static_cast<size_t>(NT) * (32 + 32 + 32), s, planes, static_cast<int>(6 * rows * apr), sigma16,
                      static_cast<int>(rows), static_cast<int>(apr), static_cast<const uint16_t *>(x),
-                     static_cast<const uint4 *>(nullptr), tab->pl_ids, static_cast<int>(pl_vecs), round_w, y);
+                     static_cast<const uint2 *>(nullptr), tab->gv_tab, round_w, y);
   return check_launch("dqgemv1_kernel");
 }
 
@@ -848,7 +852,7 @@ int launch_gemv1_planes(const uint8_t *planes, const uint16_t *sigma16, int64_t 
 // LDS, else by rmsnorm into xnorm ([m, cols] fp32) first.
 // PL: the targets' `packed` are plane layouts (one token; always the general kernel).
 template <int L, bool XF32, int NT, bool PL = false>
-int launch_dql(DqlTargets t, int64_t apr, const void *x, int64_t m, const uint4 *tab, const uint4 *kp_dot, int round_w,
+int launch_dql(DqlTargets t, int64_t apr, const void *x, int64_t m, const uint4 *tab, const DeviceTables *dtab, int round_w,
                int gelu, float *xnorm, hipStream_t s, const uint32_t *pl_nib = nullptr, int pl_vecs = 0) {
   constexpr int R = NT / L;
   int64_t blocks = 0;
@@ -889,9 +893,10 @@ int launch_dql(DqlTargets t, int64_t apr, const void *x, int64_t m, const uint4 
     if (!gen && m == 1 && apr >= 1 && apr <= static_cast<int64_t>(kG1Atoms) * L && nvec_max <= NT &&
         cols / 8 <= 2 * NT && t.packed_bytes[0] < (static_cast<int64_t>(1) << 30) &&
         t.rows[0] < (static_cast<int64_t>(1) << 30)) {
-      hipLaunchKernelGGL((dqgemv1_kernel<L, false>), g, dim3(NT), static_cast<size_t>(NT) * (16 + 32), s, t.packed[0],
-                         static_cast<int>(t.packed_bytes[0]), t.sigma16[0], static_cast<int>(t.rows[0]),
-                         static_cast<int>(apr), static_cast<const uint16_t *>(x), kp_dot, nullptr, 0, round_w, t.y[0]);
+      hipLaunchKernelGGL((dqgemv1_kernel<L, false>), g, dim3(NT), static_cast<size_t>(NT) * (16 + 32 + 16), s,
+                         t.packed[0], static_cast<int>(t.packed_bytes[0]), t.sigma16[0], static_cast<int>(t.rows[0]),
+                         static_cast<int>(apr), static_cast<const uint16_t *>(x), dtab->kp_half, dtab->gv_tab, round_w,
+                         t.y[0]);
       return check_launch("dqgemv1_kernel");
     }
   }
@@ -1765,7 +1770,7 @@ int launch_dequant_linear_multi(const DqlTarget *targets, int n, int64_t cols, c
                   static_cast<long long>(apr));
   }
   const uint4 *kp = reinterpret_cast<const uint4 *>(tab->kp_gemv);
-  const uint4 *kd = reinterpret_cast<const uint4 *>(tab->kp_dot);
+  const DeviceTables *kd = tab;
   // up to kDqlMaxTargets targets per GEMV launch
   for (int i0 = 0; i0 < n && st == PLX_OK; i0 += kDqlMaxTargets) {
     DqlTargets t{};

@@ -64,7 +64,8 @@ struct DeviceTables {
   int8_t *cb_raw = nullptr;          // [kCodebook][24] raw integer coordinates
   uint8_t *kp_gemv = nullptr;        // [kCodebook] x 16 B: 24 signed nibbles + (type | pos << 8)
   uint32_t *kp_dq = nullptr;         // [kCodebook][3] words: 3-bit value ids of 8 coordinates per word
-  uint32_t *kp_dot = nullptr;        // [kCodebook][4] words: kp_dq's 3 words, then kp_gemv's (type | pos << 8)
+  uint2 *kp_half = nullptr;          // [kCodebook] 6 half symbols, type, position of -3 (one byte each)
+  uint4 *gv_tab = nullptr;           // [kGvVecs] half bf16 pairs [kGvHalves][2], then plane -> 2 half symbols
   uint32_t *pl_ids = nullptr;        // [n_planes] value-id word (kp_dq's format) of each distinct plane
   uint16_t *code_planes = nullptr;   // [kCodebook][4] the plane-layout record of each code (3 used)
   uint32_t *pl_nib = nullptr;        // [n_planes] the same planes as kp_gemv words: 8 signed 4-bit coordinates
@@ -80,6 +81,12 @@ struct DeviceTables {
 // bits being the code's type (record 0), bits 0-2 of its -3 position (record
 // 1) and bits 3-4 (record 2).
 constexpr int kMaxPlanes = 8192;
+// The one-token dequant-GEMV's table (gv_tab): kGvHalves halves of 2 bf16
+// pairs (8 B), then kGvPlanes uint16 plane entries, as whole 16-byte vectors.
+constexpr int kGvHalves = 168;
+constexpr int kGvPlanes = 4992;
+constexpr int kGvHalfVecs = kGvHalves * 8 / 16;
+constexpr int kGvVecs = kGvHalfVecs + kGvPlanes * 2 / 16;
 struct PlaneTables {
   std::vector<uint32_t> ids;
   std::vector<uint16_t> code_planes;

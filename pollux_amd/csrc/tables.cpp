@@ -23,9 +23,15 @@
 //                {0,1,2,4,-4,-3,-2,-1} (there is no +3) as value ids 0..7,
 //                word p byte i = id(coord 8p+i) | id(coord 8p+4+i) << 4, the
 //                order v_perm_b32 lookups want (2,358,732 B).
-// kp_dot         per code 16 B for the one-token dequant-GEMV with bf16
-//                activations: kp_dq's 3 words, then type | position of -3 << 8
-//                as in kp_gemv (3,144,976 B).
+// gv_halves      the one-token dequant-GEMV's table (bf16 activations): the
+//                161 distinct 4-coordinate halves of the codebook rows' planes
+//                as two bf16 pairs each (coordinates 0,1 | 2,3; raw integers,
+//                exact in bf16), padded to 168 halves, then for each of the
+//                4,961 planes (pl_ids' order) its two half symbols, lo | hi << 8
+//                (padded to 4,992); 11,328 B, staged in LDS by the kernel.
+// kp_half        per code 8 B for the same kernel on the packed stream: the
+//                symbols of its 6 halves (coordinates 4h..4h+3), then its type
+//                and the position of its -3 (as in kp_gemv) (1,572,488 B).
 // pl_ids         the value-id words of the 4,961 distinct 8-coordinate planes
 //                of the codebook rows (19,844 B: staged in LDS by the kernels
 //                that read the plane layout),
@@ -199,7 +205,29 @@ int build(int dev, DeviceTables *t) {
   // dequant-linear entries: 24 signed 4-bit coordinates, then type | pos << 8
   std::vector<uint32_t> gemv(static_cast<size_t>(kCodebook) * 4, 0);
   std::vector<uint32_t> dq(static_cast<size_t>(kCodebook) * 3, 0);
-  std::vector<uint32_t> dot(static_cast<size_t>(kCodebook) * 4, 0);
+  // the distinct 4-coordinate halves (key: the 4 raw values as bytes), ascending
+  auto half_key = [](const int8_t *c) {
+    uint32_t k = 0;
+    for (int i = 0; i < 4; ++i) k |= static_cast<uint32_t>(static_cast<uint8_t>(c[i] + 4)) << (8 * (3 - i));
+    return k;
+  };
+  std::vector<uint32_t> halves;
+  for (int code = 0; code < kCodebook; ++code)
+    for (int h = 0; h < 6; ++h) halves.push_back(half_key(raw + static_cast<size_t>(code) * kDim + 4 * h));
+  std::sort(halves.begin(), halves.end());
+  halves.erase(std::unique(halves.begin(), halves.end()), halves.end());
+  if (static_cast<int>(halves.size()) > kGvHalves) return fail(PLX_EINVAL, "%zu distinct codebook halves", halves.size());
+  auto half_sym = [&](const int8_t *c) {
+    return static_cast<uint32_t>(std::lower_bound(halves.begin(), halves.end(), half_key(c)) - halves.begin());
+  };
+  std::vector<uint32_t> gv(static_cast<size_t>(kGvVecs) * 4, 0);
+  for (size_t k = 0; k < halves.size(); ++k) {
+    uint16_t b[4];
+    for (int i = 0; i < 4; ++i) b[i] = f32_to_bf16_rne(static_cast<float>(static_cast<int>((halves[k] >> (8 * (3 - i))) & 0xFFu) - 4));
+    gv[2 * k] = b[0] | static_cast<uint32_t>(b[1]) << 16;
+    gv[2 * k + 1] = b[2] | static_cast<uint32_t>(b[3]) << 16;
+  }
+  std::vector<uint32_t> kp_half(static_cast<size_t>(kCodebook) * 2, 0);
   for (int code = 0; code < kCodebook; ++code) {
     const int8_t *r = raw + static_cast<size_t>(code) * kDim;
     uint32_t *e = gemv.data() + static_cast<size_t>(code) * 4;
@@ -216,11 +244,9 @@ int build(int dev, DeviceTables *t) {
     }
     const uint32_t type = nz == 0 ? 0u : nz == 2 ? 1u : nz == 8 ? 2u : 3u;
     e[3] = type | (static_cast<uint32_t>(pos) << 8);
-    uint32_t *o = dot.data() + static_cast<size_t>(code) * 4;
-    o[0] = d[0];
-    o[1] = d[1];
-    o[2] = d[2];
-    o[3] = e[3];
+    uint32_t *o = kp_half.data() + static_cast<size_t>(code) * 2;
+    for (int h = 0; h < 6; ++h) o[h / 4] |= half_sym(r + 4 * h) << (8 * (h % 4));
+    o[1] |= type << 16 | static_cast<uint32_t>(pos) << 24;
   }
 
   struct Upload {
@@ -234,7 +260,7 @@ int build(int dev, DeviceTables *t) {
 
   void *dt = nullptr, *drt = nullptr, *dsq = nullptr, *dsi = nullptr, *dsa = nullptr, *dr = nullptr, *dg = nullptr,
        *dd = nullptr, *dk = nullptr, *dpi = nullptr, *dcp = nullptr, *dpn = nullptr, *d3t = nullptr, *d3w = nullptr,
-       *d3r = nullptr;
+       *d3r = nullptr, *dgv = nullptr;
   const PlaneTables *pt = plane_tables_host();
   if (!pt) return fail(PLX_EINVAL, "the codebook rows take more than %d distinct planes", kMaxPlanes);
   std::vector<uint32_t> pl_pad(pt->ids);  // whole 16-byte vectors (the kernels stage it by uint4)
@@ -247,6 +273,16 @@ int build(int dev, DeviceTables *t) {
       const uint32_t id = (pt->ids[k] >> (8 * (w % 4) + 4 * (w / 4))) & 0xFu;
       pl_nib[k] |= (static_cast<uint32_t>(kIdValue[id & 7u]) & 0xFu) << (4 * w);
     }
+  // each plane's two half symbols (the plane's value ids decoded to raw values)
+  {
+    if (pt->ids.size() > static_cast<size_t>(kGvPlanes)) return fail(PLX_EINVAL, "%zu planes", pt->ids.size());
+    uint16_t *ph = reinterpret_cast<uint16_t *>(gv.data() + 2 * kGvHalves);
+    for (size_t k = 0; k < pt->ids.size(); ++k) {
+      int8_t c[8];
+      for (int w = 0; w < 8; ++w) c[w] = static_cast<int8_t>(kIdValue[(pt->ids[k] >> (8 * (w % 4) + 4 * (w / 4))) & 7u]);
+      ph[k] = static_cast<uint16_t>(half_sym(c) | half_sym(c + 4) << 8);
+    }
+  }
   const Upload ups[] = {
       {tiles.data(), tiles.size() * 2, &dt},
       {raw_tiles.data(), raw_tiles.size() * 2, &drt},
@@ -256,7 +292,8 @@ int build(int dev, DeviceTables *t) {
       {raw, static_cast<size_t>(kCodebook) * kDim, &dr},
       {gemv.data(), gemv.size() * 4, &dg},
       {dq.data(), dq.size() * 4, &dd},
-      {dot.data(), dot.size() * 4, &dk},
+      {kp_half.data(), kp_half.size() * 4, &dk},
+      {gv.data(), gv.size() * 4, &dgv},
       {pl_pad.data(), pl_pad.size() * 4, &dpi},
       {pt->code_planes.data(), pt->code_planes.size() * 2, &dcp},
       {pl_nib.data(), pl_nib.size() * 4, &dpn},
@@ -287,7 +324,8 @@ int build(int dev, DeviceTables *t) {
   t->cb_raw = static_cast<int8_t *>(dr);
   t->kp_gemv = static_cast<uint8_t *>(dg);
   t->kp_dq = static_cast<uint32_t *>(dd);
-  t->kp_dot = static_cast<uint32_t *>(dk);
+  t->kp_half = static_cast<uint2 *>(dk);
+  t->gv_tab = static_cast<uint4 *>(dgv);
   t->pl_ids = static_cast<uint32_t *>(dpi);
   t->code_planes = static_cast<uint16_t *>(dcp);
   t->pl_nib = static_cast<uint32_t *>(dpn);
