@@ -359,6 +359,8 @@ def gemv_extras(device, copies=400, m_gemm=64, replays=5):
                 out[f"{key}_layout_GBps"] = (6 * n_atoms + 2 * of + 2 * m * inf + 4 * m * of) / t / 1e9
             out[f"{key}_dense_equiv_GBps"] = (2 * of * inf) / t / 1e9
             out[f"{key}_TFLOPs"] = 2 * m * of * inf / t / 1e12
+        if name == "up_7680x1920":
+            out.update(latency_floor(pk, copies, replays))
         del pk, pl
     out["note"] = (f"HIP graph of {copies} calls on distinct packed copies ({copies} x 1.38 MB), replayed {replays}x; "
                    "compressed bytes = packed + sigma16 + x bf16 + y fp32; dense-equivalent = fp16 weight bytes; "
@@ -791,6 +793,46 @@ def decode_extras(device, prompt_len=64, new_tokens=128):
     return out
 
 
+def latency_floor(pk, copies, replays):
+    """What one graph-replayed call costs at least: a node, and a node plus one HBM round trip.
+
+    The same graph timing as gemv_extras on the smallest kernel of the library
+    (plx_unpack_indices on one 9-byte group: one load, one 32-byte store):
+    node_us with every call reading the same group (an L2 hit), latency_floor_us
+    with call i reading the first group of packed copy i (copies of 1.38 MB
+    apart, so every call's load goes to HBM).
+    """
+    import torch
+
+    from pollux_amd import castor
+
+    res = {}
+    for key, rot in (("node_us", False), ("latency_floor_us", True)):
+        src = [pk[i if rot else 0][:9] for i in range(copies)]
+        side = torch.cuda.Stream(pk.device)
+        side.wait_stream(torch.cuda.current_stream(pk.device))
+        with torch.cuda.stream(side):
+            for i in range(3):
+                castor.unpack_indices(src[i], 4)
+        torch.cuda.current_stream(pk.device).wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            ys = [castor.unpack_indices(src[i], 4) for i in range(copies)]
+        graph.replay()
+        torch.cuda.synchronize()
+        if not torch.equal(ys[-1], castor.unpack_indices(src[-1], 4)):
+            raise RuntimeError("unpack graph replay differs from the eager call")
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(replays):
+            graph.replay()
+        e1.record()
+        e1.synchronize()
+        res[key] = e0.elapsed_time(e1) * 1e3 / (replays * copies)
+        del graph, ys
+    return res
+
+
 def gemv_headline(gemv):
     """The metric's "dequant-GEMV GB/s at d=1920" from the config-5 batch-1 rows of gemv_extras."""
     rows = {}
@@ -805,17 +847,31 @@ def gemv_headline(gemv):
     pl_us = {name: gemv.get(f"{name}_M1_planes_us") for name in rows}
     plane = None
     if all(v is not None for v in pl_us.values()):
+        params = sum(of * inf for of, inf in ((7680, 1920), (1920, 7680)))
+        packed_bits = sum(((of * inf // 24 + 3) // 4 * 9) * 8 + 16 * of for of, inf in ((7680, 1920), (1920, 7680)))
         plane = {
             "us_per_call": pl_us,
             "GBps_on_packed_stream": tot_bytes / (sum(pl_us.values()) * 1e-6) / 1e9,
+            "resident_bits_per_param": {"packed": packed_bits / params,
+                                        "packed_plus_plane_layout": (packed_bits + 48 * params // 24) / params},
             "note": "the same calls reading the plane layout (h24_plane_layout: 6 B per atom built once beside "
                     "the 2.25 B packed stream), which removes the per-atom codebook-table gathers",
         }
+    floor = gemv.get("latency_floor_us")
+    if floor:
+        for r in rows.values():
+            r["latency_floor_frac"] = floor / r["us_per_call"]
     return {
         "GBps": tot_bytes / tot_s / 1e9,
         "unit": "GB/s",
         "hbm_frac": tot_bytes / tot_s / PEAK_HBM_BPS,
         "peak": PEAK_HBM_BPS / 1e9,
+        "latency_floor_us": floor,
+        "node_us": gemv.get("node_us"),
+        "latency_floor_note": "one graph node plus one HBM round trip, measured in the same run (plx_unpack_indices "
+        "on one 9-byte group of a distinct packed copy per call); node_us: the same with an L2-resident group. "
+        "At one token the call is latency-bound: hbm_frac is far from 1 by construction, latency_floor_frac is "
+        "what one call can reach",
         "per_matrix": rows,
         "plane_layout": plane,
         "workload": "BASELINE config 5 at batch 1: y = x W^T with W the packed 18-bit indices + fp16 row scales "

@@ -1433,9 +1433,9 @@ __global__ __launch_bounds__(64 * WV, WV <= 4 ? 2 : 1) void dqmm_kernel(
       if constexpr (EXACT) {
         const bf16x8_t l0 = perm_decode(w0, tb0.x, tb0.y, tb0.z, tb0.w);
         const bf16x8_t l1 = perm_decode(w1, tb1.x, tb1.y, tb1.z, tb1.w);
-        // the third activation part times the weights' low part is below 2^-25 of the product: skipped
+        // every activation part times the weights' low part: the products stay exact
 #pragma unroll
-        for (int pp = 0; pp < (XP == 3 ? 2 : XP); ++pp)
+        for (int pp = 0; pp < XP; ++pp)
 #pragma unroll
           for (int t = 0; t < MT; ++t) {
             const bf16x8_t av = __builtin_bit_cast(bf16x8_t, xa_q[s][pp][t]);

@@ -31,9 +31,9 @@
 //   one row per row tile (the fp16 values above, split exactly into bf16
 //   hi + lo: lo = W - bf16(W) has at most 3 significant bits) and splits 8
 //   activations of one token per token tile exactly into three bf16 parts
-//   (x = h + m + l), so five v_mfma_f32_16x16x32_bf16 per tile pair (h, m, l
-//   times hi; h, m times lo; l * lo is below 2^-25 of the product) form the
-//   products of fp32 x with the fp16 weights in fp32 accumulation.  The
+//   (x = h + m + l), so six v_mfma_f32_16x16x32_bf16 per tile pair (h, m, l
+//   times hi and times lo) form the exact products of fp32 x with the fp16
+//   weights in fp32 accumulation.  The
 //   waves' tiles are summed through LDS in wave order.  With ln_f the
 //   activations enter as x * w (the norm weight) and each token's sum is
 //   scaled by rsqrt(mean(x^2) + eps) at the end, the sums of squares taken
@@ -472,6 +472,7 @@ __global__ __launch_bounds__(64 * kI8mmWaves, 2) void int8mm_kernel(
         acc[t][r] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xl, wh[r], acc[t][r], 0, 0, 0);
         acc[t][r] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xh, wl[r], acc[t][r], 0, 0, 0);
         acc[t][r] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xm, wl[r], acc[t][r], 0, 0, 0);
+        acc[t][r] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xl, wl[r], acc[t][r], 0, 0, 0);
       }
     }
   };

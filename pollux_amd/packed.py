@@ -316,6 +316,10 @@ class PackedH24Linear(nn.Module):
     plane_layout_takes names read a plane layout of the weight kept beside the
     packed buffer (6 B per atom, built on first use; same results, no per-atom
     table gathers); False keeps only the packed stream resident.
+    Resident weight memory before materialize: 0.76 bits/param with the packed
+    stream alone (18-bit indices + fp16 row scales), 2.76 bits/param once the
+    plane layout is built (2 bits/param more) -- set use_plane_layout = False
+    where memory, not the one-token latency, is the limit.
     """
 
     weight_rounding = "exact"
@@ -368,7 +372,8 @@ class PackedH24Linear(nn.Module):
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         if not self._materialized:
             # fused path: weights stay packed (0.76 bits/param); fp32 result cast to x's dtype.  The batches
-            # plane_layout_takes names run from the plane layout (6 B per atom, built once).
+            # plane_layout_takes names run from the plane layout (6 B per atom, built once and kept:
+            # 2.76 bits/param resident with it).
             m = x.numel() // self.in_features if self.in_features else 0
             takes = self.use_plane_layout and plane_layout_takes(m, self.in_features)
             planes = self.plane_layout() if takes else None
