@@ -793,6 +793,43 @@ def decode_extras(device, prompt_len=64, new_tokens=128):
     return out
 
 
+def gemv_workload(device, replays, copies=400):
+    """The config-5 one-token calls of gemv_extras as graphs of `copies` calls, each replayed `replays` times
+    (for rocprofv3 counter runs: up then down, packed stream then plane layout)."""
+    import torch
+
+    from pollux_amd import castor, dequant_linear, h24_plane_layout
+
+    for of, inf in ((7680, 1920), (1920, 7680)):
+        g = torch.Generator(device=device).manual_seed(of)
+        n_atoms = of * inf // 24
+        pk = torch.empty(copies, (n_atoms + 3) // 4 * 9, dtype=torch.uint8, device=device)
+        pl = torch.empty(copies, 3 * n_atoms, dtype=torch.int16, device=device)
+        for i in range(copies):
+            pk[i] = castor.pack_indices(torch.randint(0, 196561, (n_atoms,), generator=g, device=device))
+            pl[i] = h24_plane_layout(pk[i], n_atoms)
+        sg = (torch.rand(copies, of, generator=g, device=device) * 0.045 + 0.005).half()
+        x = torch.randn(1, inf, generator=g, device=device).to(torch.bfloat16)
+        for planes in (False, True):
+            def call(i):
+                return dequant_linear(pk[i], sg[i], of, inf, x, planes=pl[i] if planes else None)
+
+            side = torch.cuda.Stream(device)
+            side.wait_stream(torch.cuda.current_stream(device))
+            with torch.cuda.stream(side):
+                for i in range(3):
+                    call(i)
+            torch.cuda.current_stream(device).wait_stream(side)
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                ys = [call(i) for i in range(copies)]
+            for _ in range(replays):
+                graph.replay()
+            torch.cuda.synchronize()
+            del graph, ys
+        del pk, pl
+
+
 def latency_floor(pk, copies, replays):
     """What one graph-replayed call costs at least: a node, and a node plus one HBM round trip.
 
@@ -892,12 +929,13 @@ def main() -> int:
     ap.add_argument("--mode", default="bf16", choices=["bf16", "bf16-dense", "fp32"])
     ap.add_argument(
         "--pmc-workload",
-        choices=["c4", "c2", "hbm"],
+        choices=["c4", "c2", "hbm", "gemv"],
         default=None,
         help="for rocprofv3 --pmc runs: 5 copies of a 256 MiB fp32 tensor (HBM-counter calibration), then "
         "--steps headline (c4) steps, config-2 requantize steps (c2), or (hbm) --steps calls each of pack, "
         "unpack and dequant at config-4 size on 4 rotating buffer sets and of the config-2 optimiser step on "
-        "3 rotating states; prints nothing",
+        "3 rotating states, or (gemv) --steps replays of the config-5 one-token graphs (400 calls each on "
+        "distinct packed copies: up and down, packed stream then plane layout); prints nothing",
     )
     ap.add_argument(
         "--decode-workload",
@@ -942,7 +980,9 @@ def main() -> int:
         for _ in range(5):
             dst.copy_(src)
         del src, dst
-        if args.pmc_workload == "hbm":
+        if args.pmc_workload == "gemv":
+            gemv_workload(dev, args.steps)
+        elif args.pmc_workload == "hbm":
             hbm_workload(dev, args.steps)
         elif args.pmc_workload == "c2":
             mats = make_c2(dev)
