@@ -793,9 +793,9 @@ def decode_extras(device, prompt_len=64, new_tokens=128):
     return out
 
 
-def gemv_workload(device, replays, copies=400):
-    """The config-5 one-token calls of gemv_extras as graphs of `copies` calls, each replayed `replays` times
-    (for rocprofv3 counter runs: up then down, packed stream then plane layout)."""
+def gemv_workload(device, replays, copies=400, m=1):
+    """The config-5 calls of gemv_extras (one token, or m tokens) as graphs of `copies` calls, each replayed
+    `replays` times (for rocprofv3 counter runs: up then down, packed stream then plane layout)."""
     import torch
 
     from pollux_amd import castor, dequant_linear, h24_plane_layout
@@ -809,7 +809,7 @@ def gemv_workload(device, replays, copies=400):
             pk[i] = castor.pack_indices(torch.randint(0, 196561, (n_atoms,), generator=g, device=device))
             pl[i] = h24_plane_layout(pk[i], n_atoms)
         sg = (torch.rand(copies, of, generator=g, device=device) * 0.045 + 0.005).half()
-        x = torch.randn(1, inf, generator=g, device=device).to(torch.bfloat16)
+        x = torch.randn(m, inf, generator=g, device=device).to(torch.bfloat16)
         for planes in (False, True):
             def call(i):
                 return dequant_linear(pk[i], sg[i], of, inf, x, planes=pl[i] if planes else None)
@@ -929,13 +929,14 @@ def main() -> int:
     ap.add_argument("--mode", default="bf16", choices=["bf16", "bf16-dense", "fp32"])
     ap.add_argument(
         "--pmc-workload",
-        choices=["c4", "c2", "hbm", "gemv"],
+        choices=["c4", "c2", "hbm", "gemv", "gemm"],
         default=None,
         help="for rocprofv3 --pmc runs: 5 copies of a 256 MiB fp32 tensor (HBM-counter calibration), then "
         "--steps headline (c4) steps, config-2 requantize steps (c2), or (hbm) --steps calls each of pack, "
         "unpack and dequant at config-4 size on 4 rotating buffer sets and of the config-2 optimiser step on "
         "3 rotating states, or (gemv) --steps replays of the config-5 one-token graphs (400 calls each on "
-        "distinct packed copies: up and down, packed stream then plane layout); prints nothing",
+        "distinct packed copies: up and down, packed stream then plane layout; gemm: the same at 64 tokens); "
+        "prints nothing",
     )
     ap.add_argument(
         "--decode-workload",
@@ -980,8 +981,8 @@ def main() -> int:
         for _ in range(5):
             dst.copy_(src)
         del src, dst
-        if args.pmc_workload == "gemv":
-            gemv_workload(dev, args.steps)
+        if args.pmc_workload in ("gemv", "gemm"):
+            gemv_workload(dev, args.steps, m=1 if args.pmc_workload == "gemv" else 64)
         elif args.pmc_workload == "hbm":
             hbm_workload(dev, args.steps)
         elif args.pmc_workload == "c2":
