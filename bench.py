@@ -837,13 +837,16 @@ def latency_floor(pk, copies, replays):
     (plx_unpack_indices on one 9-byte group: one load, one 32-byte store):
     node_us with every call reading the same group (an L2 hit), latency_floor_us
     with call i reading the first group of packed copy i (copies of 1.38 MB
-    apart, so every call's load goes to HBM).
+    apart), each replay timed alone right after 640 MB of writes to another
+    buffer have evicted those groups from the L2s and the 256 MB MALL, so every
+    call's load goes to HBM.
     """
     import torch
 
     from pollux_amd import castor
 
     res = {}
+    flush = torch.empty(160 * 1024 * 1024, dtype=torch.float32, device=pk.device)
     for key, rot in (("node_us", False), ("latency_floor_us", True)):
         src = [pk[i if rot else 0][:9] for i in range(copies)]
         side = torch.cuda.Stream(pk.device)
@@ -860,13 +863,18 @@ def latency_floor(pk, copies, replays):
         if not torch.equal(ys[-1], castor.unpack_indices(src[-1], 4)):
             raise RuntimeError("unpack graph replay differs from the eager call")
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
+        tot = 0.0
         for _ in range(replays):
+            if rot:
+                flush.fill_(1.0)
+            e0.record()
             graph.replay()
-        e1.record()
-        e1.synchronize()
-        res[key] = e0.elapsed_time(e1) * 1e3 / (replays * copies)
+            e1.record()
+            e1.synchronize()
+            tot += e0.elapsed_time(e1)
+        res[key] = tot * 1e3 / (replays * copies)
         del graph, ys
+    del flush
     return res
 
 
