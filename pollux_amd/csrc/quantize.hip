@@ -537,8 +537,8 @@ constexpr int kT3ST = 16;                          // pattern tiles per LDS stag
 constexpr int kT3Stages = kT3Tiles / kT3ST;        // 8 per pass
 constexpr int kT3StageBytes = kT3ST * kTileBytes;  // 12,288
 constexpr int kT3StageVecs = kT3StageBytes / 16;   // 768
-constexpr int kT3Cap = 512;                        // candidate entries per wave (4 bytes each)
-constexpr int kT3Surv = 512;                       // survivor words per wave (4 bytes each)
+constexpr int kT3Cap = 384;                        // candidate entries per wave (4 bytes each)
+constexpr int kT3Surv = 384;                       // survivor words per wave (4 bytes each)
 constexpr float kT3Alpha = 1.416015625f;           // bf16(3s) + bf16(s)
 constexpr float kT3Beta = 0.708984375f;            // bf16(3s) - bf16(s)
 constexpr float kT3S = 0.353515625f;               // bf16(s)
@@ -563,7 +563,7 @@ __device__ __forceinline__ float t3_dot(const uint32_t *xr, uint32_t wb) {
 }
 
 template <int AT>
-__global__ __launch_bounds__(kThreads, 2) void t3_kernel(const uint4 *__restrict__ xb, int64_t n_atoms,
+__global__ __launch_bounds__(kThreads, 3) void t3_kernel(const uint4 *__restrict__ xb, int64_t n_atoms,
                                                          const uint8_t *__restrict__ t3_tiles,
                                                          const uint32_t *__restrict__ t3_words,
                                                          const uint32_t *__restrict__ t3_rows,
@@ -577,13 +577,11 @@ __global__ __launch_bounds__(kThreads, 2) void t3_kernel(const uint4 *__restrict
   __shared__ __align__(16) uint32_t xw[kWaves][NA][12];  // the atoms' bf16 coordinates (pairs)
   __shared__ uint32_t st_m[kWaves][NA], st_r[kWaves][NA];
   __shared__ float st_t[kWaves][NA];  // the atom's threshold on S less its margin (which signs to evaluate)
-  __shared__ uint32_t wtab[kT3Reps];  // representative words
   __shared__ uint32_t surv_n[kWaves];
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, q = lane >> 4, j = lane & 15;
   const int64_t wave_atom0 = static_cast<int64_t>(blockIdx.x) * (kWaves * NA) + static_cast<int64_t>(wave) * NA;
 
-  for (int i = tid; i < kT3Reps; i += kThreads) wtab[i] = t3_words[i];
   if (lane == 0) surv_n[wave] = 0u;
   bf16x8 b[AT];
   float e1[AT], es[AT];
@@ -676,7 +674,7 @@ __global__ __launch_bounds__(kThreads, 2) void t3_kernel(const uint4 *__restrict
       // the flagged outputs one at a time (a wave iterates as often as its busiest lane needs)
       for (uint32_t mk = mask; mk != 0u; mk &= mk - 1u) {
         const uint32_t rep = rep0 + static_cast<uint32_t>(__builtin_ctz(mk));
-        const uint32_t wr = wtab[rep];
+        const uint32_t wr = t3_words[rep];
         const float D = t3_dot(xr, wr);
         // the word whose S is |D| qualified (|S| passed the threshold); the other sign only when
         // -|D| can reach the threshold too (an atom whose threshold is about 0 or below)
@@ -804,7 +802,7 @@ __global__ __launch_bounds__(kThreads, 2) void t3_kernel(const uint4 *__restrict
       const uint32_t wid = se >> 7;
       const uint32_t M = st_m[wave][al];
       const uint32_t *xr = xw[wave][al];
-      const uint32_t wr = wtab[wid & (kT3Reps - 1)];
+      const uint32_t wr = t3_words[wid & (kT3Reps - 1)];
       const int sg = wid >= static_cast<uint32_t>(kT3Reps) ? 1 : 0;
       const float D = t3_dot(xr, wr);
       uint32_t rmin = 0xFFFFFFFFu;
@@ -1392,16 +1390,17 @@ static_assert(kPairSweepTiles % (32 * kST) == 0, "every slice count holds whole 
 // t3_kernel: atom tiles per wave by launch size, so small launches still fill the chip.
 int t3_launch(const uint4 *xb, int64_t n_atoms, const DeviceTables *tab, const uint64_t *recs, int n_recs,
               uint4 *keys, hipStream_t s, int rows_by_sweep) {
-  const int AT = n_atoms >= 262144 ? 8 : n_atoms >= 131072 ? 4 : n_atoms >= 32768 ? 2 : 1;
+  // 4 atom tiles per wave from 131,072 atoms: 48 KB of LDS and 159 VGPRs, 3 blocks (12 waves) per CU.
+  // (8 tiles per wave, 2 blocks per CU, measured 14.9 against 12.5 ms on the config-4 launch; 2 tiles at
+  // 4 blocks per CU 13.0 ms; the representative words read from global memory instead of LDS is what
+  // fits the third block.)
+  const int AT = n_atoms >= 131072 ? 4 : n_atoms >= 32768 ? 2 : 1;
   const int64_t per_block = static_cast<int64_t>(kWaves) * AT * 16;
   const int64_t blocks = (n_atoms + per_block - 1) / per_block;
   if (blocks > 0x7FFFFFFFll) return fail(PLX_EINVAL, "quantize: %lld atoms exceed one launch", static_cast<long long>(n_atoms));
   const dim3 g(static_cast<unsigned>(blocks));
   profile_before(s, PLX_PROF_T3);
-  if (AT == 8)
-    hipLaunchKernelGGL(t3_kernel<8>, g, dim3(kThreads), 0, s, xb, n_atoms, tab->t3_tiles, tab->t3_words, tab->t3_rows,
-                       recs, n_recs, keys, rows_by_sweep);
-  else if (AT == 4)
+  if (AT == 4)
     hipLaunchKernelGGL(t3_kernel<4>, g, dim3(kThreads), 0, s, xb, n_atoms, tab->t3_tiles, tab->t3_words, tab->t3_rows,
                        recs, n_recs, keys, rows_by_sweep);
   else if (AT == 2)
