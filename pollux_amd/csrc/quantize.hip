@@ -533,16 +533,16 @@ __global__ __launch_bounds__(kThreads, MODE == kModeB ? 3 : 2) void nn_kernel(co
 // Buckets are taken by round-half-up like the dense sweep's, and every score
 // is an fp32 sum of exact products plus one rounding for the bonus, so the
 // answer equals the exact-score answer off near-ties (oracle/nn.py).
-constexpr int kT3ST = 16;                          // pattern tiles per LDS stage
+constexpr int kT3ST = 8;                           // pattern tiles per LDS stage
 constexpr int kT3Stages = kT3Tiles / kT3ST;        // 8 per pass
-constexpr int kT3StageBytes = kT3ST * kTileBytes;  // 12,288
-constexpr int kT3StageVecs = kT3StageBytes / 16;   // 768
+constexpr int kT3StageBytes = kT3ST * kTileBytes;  // 6,144
+constexpr int kT3StageVecs = kT3StageBytes / 16;   // 384
 constexpr int kT3Cap = 384;                        // candidate entries per wave (4 bytes each)
 constexpr int kT3Surv = 384;                       // survivor words per wave (4 bytes each)
 constexpr float kT3Alpha = 1.416015625f;           // bf16(3s) + bf16(s)
 constexpr float kT3Beta = 0.708984375f;            // bf16(3s) - bf16(s)
 constexpr float kT3S = 0.353515625f;               // bf16(s)
-static_assert(kT3StageVecs % kThreads == 0, "type-3 stage splits evenly over the block");
+static_assert(kT3StageVecs % 64 == 0, "type-3 stage splits into whole wave loads");
 static_assert(kT3Tiles % kT3ST == 0, "whole type-3 stages");
 
 __device__ __forceinline__ uint32_t t3_bucket(float v) { return (__float_as_uint(v) + 0x8000u) >> 16; }
@@ -563,7 +563,7 @@ __device__ __forceinline__ float t3_dot(const uint32_t *xr, uint32_t wb) {
 }
 
 template <int AT>
-__global__ __launch_bounds__(kThreads, 3) void t3_kernel(const uint4 *__restrict__ xb, int64_t n_atoms,
+__global__ __launch_bounds__(kThreads, 4) void t3_kernel(const uint4 *__restrict__ xb, int64_t n_atoms,
                                                          const uint8_t *__restrict__ t3_tiles,
                                                          const uint32_t *__restrict__ t3_words,
                                                          const uint32_t *__restrict__ t3_rows,
@@ -637,7 +637,8 @@ __global__ __launch_bounds__(kThreads, 3) void t3_kernel(const uint4 *__restrict
   auto stage_copy = [&](int g, int dst) {
     const int stage = g % kT3Stages;
 #pragma unroll
-    for (int i = 0; i < kT3StageVecs / kThreads; ++i) {
+    for (int i = 0; i < (kT3StageVecs + kThreads - 1) / kThreads; ++i) {
+      if (i * kThreads + wave * 64 >= kT3StageVecs) break;  // (wave-uniform)
       const uint4 *src = gsrc + static_cast<size_t>(stage) * kT3StageVecs + i * kThreads + tid;
       uint8_t *d = stg[dst] + (i * kThreads + wave * 64) * 16;
       __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)(src),
@@ -1390,10 +1391,11 @@ static_assert(kPairSweepTiles % (32 * kST) == 0, "every slice count holds whole 
 // t3_kernel: atom tiles per wave by launch size, so small launches still fill the chip.
 int t3_launch(const uint4 *xb, int64_t n_atoms, const DeviceTables *tab, const uint64_t *recs, int n_recs,
               uint4 *keys, hipStream_t s, int rows_by_sweep) {
-  // 4 atom tiles per wave from 131,072 atoms: 48 KB of LDS and 159 VGPRs, 3 blocks (12 waves) per CU.
-  // (8 tiles per wave, 2 blocks per CU, measured 14.9 against 12.5 ms on the config-4 launch; 2 tiles at
-  // 4 blocks per CU 13.0 ms; the representative words read from global memory instead of LDS is what
-  // fits the third block.)
+  // 4 atom tiles per wave from 131,072 atoms: 39 KB of LDS (8-tile stages) and 128 VGPRs, 4 blocks (16
+  // waves) per CU.  The evaluation is latency-bound, so occupancy decides: on the config-4 launch 8 tiles
+  // per wave at 2 blocks per CU measured 14.9 ms, 4 tiles at 3 blocks (16-tile stages) 12.5, 4 tiles at 4
+  // blocks 11.5, 2 tiles at 4 blocks 13.0; the representative words are read from global memory (L1 / L2)
+  // to leave the LDS to the stages and lists.
   const int AT = n_atoms >= 131072 ? 4 : n_atoms >= 32768 ? 2 : 1;
   const int64_t per_block = static_cast<int64_t>(kWaves) * AT * 16;
   const int64_t blocks = (n_atoms + per_block - 1) / per_block;
