@@ -5,9 +5,10 @@ is not a near-tie (oracle/nn.py classifies each disagreement).  Cases: the
 config-4 distribution at every launch size the scorer distinguishes (1, 2, 4
 and 8 atom tiles per wave), atoms dominated by one coordinate (whose
 candidate threshold falls to zero or below, so both signs of a word are
-listed), near-origin and zero atoms, ragged small launches, and atoms whose
+listed), near-origin and zero atoms, ragged small launches, atoms whose
 best code sits in the type-3 family by construction (scaled type-3 codes plus
-noise).
+noise), and integer atoms, whose scores are exact in any summation order, so
+both paths must agree on every atom through the exact ties between codes.
 """
 
 import numpy as np
@@ -113,3 +114,31 @@ def test_row_sweep_path_equals_survivor_path(dev):
     a = castor.quantize_indices(x, mode="bf16").cpu()
     b = castor.quantize_indices(x, mode="bf16-rows-sweep").cpu()
     assert torch.equal(a, b), int((a != b).sum())
+
+
+def test_integer_atoms_exact_ties(dev):
+    # integer coordinates: every score is an exact fp32 sum in any order (multiples of 2^-9 below 2^15),
+    # so the structured and the dense path see the same bf16 buckets and must pick the same lowest row
+    # on every atom -- including the many exact ties between codes -- and the oracle's answer wherever it
+    # is determined (exact bf16 midpoints, where the reference rounds to even, are its near-ties)
+    g = torch.Generator().manual_seed(16)
+    raw = torch.from_numpy(cb.codebook_int8().astype(np.float32))
+    n = 6_000
+    a = torch.randint(1, 196561, (n,), generator=g)
+    b = torch.randint(1, 196561, (n,), generator=g)
+    x = torch.cat([raw[a] + raw[b],                                    # sums of two codes
+                   torch.randint(-4, 5, (n, 24), generator=g).float(),  # small integer vectors
+                   2.0 * raw[a[: n // 2]],                              # scaled codes
+                   torch.randint(-1, 2, (n // 2, 24), generator=g).float()])
+    xs = x.to(dev)
+    s = castor.quantize_indices(xs, mode="bf16").long().cpu()
+    d = castor.quantize_indices(xs, mode="bf16-dense").long().cpu()
+    r = castor.quantize_indices(xs, mode="bf16-rows-sweep").long().cpu()
+    assert torch.equal(s, d), int((s != d).sum())
+    assert torch.equal(s, r), int((s != r).sum())
+    sub = torch.cat([torch.arange(k, k + 375) for k in (0, n, 2 * n, 2 * n + n // 2)])  # 375 of each kind
+    o = nn.quantize(x[sub].numpy(), "B")
+    ok = ~o["near_tie"]
+    print(f"[t3 integer atoms] {len(x)} atoms equal on both paths; oracle on {len(sub)}: "
+          f"{int((~ok).sum())} near-ties", flush=True)
+    assert np.array_equal(s[sub].numpy()[ok], o["idx"][ok])
