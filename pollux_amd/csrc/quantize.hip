@@ -507,27 +507,30 @@ __global__ __launch_bounds__(kThreads, MODE == kModeB ? 3 : 2) void nn_kernel(co
 // i.e. S(w) - x_p * (alpha = 1.416015625 where w_p = 0, beta = 0.708984375
 // where w_p = 1); both products are exact in fp32 (8 x 8 significant bits).
 // The best code of a word is S(w) + bonus(w) with bonus(w) = max_p of
-// -x_p (alpha or beta), which lies in [e_stop, e1]: e1 = max_p max(-alpha x_p,
-// -beta x_p) and e_stop = the smaller of the two at the p attaining e1 (every
-// word takes one of them there).  The Golay code holds the complement of
-// every word, S(~w) = -S(w), so one MFMA per 16 representative words scores
-// 32 words: 128 tiles instead of 6,144.
+// -x_p (alpha or beta) <= e1 = max_p max(-alpha x_p, -beta x_p).  The Golay
+// code holds the complement of every word, S(~w) = -S(w), so one MFMA per 16
+// representative words scores 32 words: 128 tiles instead of 6,144.
 // A block of 4 waves holds AT atom tiles of 16 atoms per wave as MFMA B
-// operands and streams the 128 pattern tiles through LDS three times:
-//   pass 0  the largest |S| per atom: the best type-3 score is at least
-//           S_max + e_stop, and no code below the best pair bucket (the pair
-//           records) or below 2.0 (the origin rule) can win;
+// operands and streams the 128 pattern tiles through LDS once (a second time
+// only if a survivor list overflows):
 //   pass 1  every lane whose four outputs hold a word that could reach the
-//           lowest bucket still possible (|S| >= lo(bucket) - e1 - margin)
+//           lowest bucket still possible -- the best pair bucket (the pair
+//           records), 2.0 (the origin rule) and the best type-3 bucket found
+//           so far, whichever is highest: |S| >= lo(bucket) - e1 - margin --
 //           appends one 4-byte entry (atom, tile, lane quarter, 4-bit mask of
-//           its outputs) to the wave's list in LDS; full lists are evaluated
-//           by the wave, one entry per lane: each flagged representative and
-//           its complement get S recomputed from the atom's bf16 coordinates
-//           and their 24 positions scored, and the best bucket M3 per atom is
-//           kept by an LDS atomic max;
-//   pass 2  the same for the words that could reach M3 (a handful): every
-//           (w, p) at bucket M3 gives its codebook row (t3_rows) and the
-//           lowest one is kept by an LDS atomic min.
+//           its outputs) to the wave's list in LDS; at every stage end (and
+//           when the list is full) the wave evaluates it, one entry per lane:
+//           each flagged representative and its complement get S recomputed
+//           from the atom's bf16 coordinates and their 24 positions scored,
+//           the best bucket M3 per atom is kept by an LDS atomic max, words
+//           at or above the running best go onto a survivor list, and the
+//           thresholds rise to the new best buckets;
+//   rows    every word at the final M3 was at or above the running best when
+//           it was evaluated, so the survivors give every (w, p) at bucket M3
+//           and its codebook row (t3_rows); the lowest is kept by an LDS
+//           atomic min;
+//   pass 2  (only after a survivor list overflowed) the same rows from a
+//           second sweep with the thresholds at M3.
 // The atom's key gets (M3 << 16, lowest row at M3), or 0 when no type-3 code
 // reaches 2.0; the resolve compares it with the pair region's candidates.
 // Buckets are taken by round-half-up like the dense sweep's, and every score
@@ -584,7 +587,7 @@ __global__ __launch_bounds__(kThreads, 4) void t3_kernel(const uint4 *__restrict
 
   if (lane == 0) surv_n[wave] = 0u;
   bf16x8 b[AT];
-  float e1[AT], es[AT];
+  float e1[AT], mg[AT];
 #pragma unroll
   for (int at = 0; at < AT; ++at) {
     const int64_t a = wave_atom0 + at * 16 + j;
@@ -592,31 +595,26 @@ __global__ __launch_bounds__(kThreads, 4) void t3_kernel(const uint4 *__restrict
     if (a < n_atoms && q < 3) w = xb[a * 3 + q];
     b[at] = __builtin_bit_cast(bf16x8, w);
     if (q < 3) *reinterpret_cast<uint4 *>(&xw[wave][at * 16 + j][4 * q]) = w;
-    // e1 / e_stop over this lane's 8 coordinates, then over the atom's 3 lanes
-    float hi = -__builtin_inff(), lo = -__builtin_inff();
+    // e1 = the largest position term max_p max(-alpha x_p, -beta x_p), and sum |x_p| (s * sum |x| bounds
+    // every |S|), over this lane's 8 coordinates, then over the atom's 3 lanes
+    float hi = -__builtin_inff(), ax = 0.f;
     if (q < 3) {
       const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const float x = __uint_as_float(e & 1 ? ww[e / 2] & 0xFFFF0000u : ww[e / 2] << 16);
-        const float v0 = -x * kT3Alpha, v1 = -x * kT3Beta;
-        const float h = fmaxf(v0, v1), l = fminf(v0, v1);
-        if (h > hi || (h == hi && l > lo)) {
-          hi = h;
-          lo = l;
-        }
+        hi = fmaxf(hi, fmaxf(-x * kT3Alpha, -x * kT3Beta));
+        ax += fabsf(x);
       }
     }
 #pragma unroll
     for (int sh = 16; sh <= 32; sh <<= 1) {
-      const float oh = __shfl_xor(hi, sh, 64), ol = __shfl_xor(lo, sh, 64);
-      if (oh > hi || (oh == hi && ol > lo)) {
-        hi = oh;
-        lo = ol;
-      }
+      hi = fmaxf(hi, __shfl_xor(hi, sh, 64));
+      ax += __shfl_xor(ax, sh, 64);
     }
     e1[at] = hi;
-    es[at] = lo;
+    // the margin for the MFMA's fp32 summation order of S and the score roundings
+    mg[at] = (ax * kT3S + fabsf(hi)) * 0x1p-14f;
   }
   for (int i = lane; i < NA; i += 64) {
     st_m[wave][i] = 0u;
@@ -707,33 +705,27 @@ __global__ __launch_bounds__(kThreads, 4) void t3_kernel(const uint4 *__restrict
     cnt = 0;
   };
 
-  float m[AT], thr[AT], mg[AT];
+  // The threshold on |S|: a word can reach bucket B only if |S| >= lo(B) - e1 - margin, and no bucket
+  // below the lowest that can still win counts: the best pair bucket (the pair records), 2.0 (the origin
+  // rule), and -- raised at every stage end -- the best type-3 bucket found so far.
+  float thr[AT];
+  auto set_thr = [&](int at, uint32_t mlow) {
+    mlow = max(mlow, max(mp[at], 0x4000u));
+    thr[at] = __uint_as_float((mlow << 16) - 0x8000u) - e1[at] - mg[at];
+    if (q == 0) st_t[wave][at * 16 + j] = thr[at] - mg[at];
+  };
 #pragma unroll
-  for (int at = 0; at < AT; ++at) m[at] = 0.f;
+  for (int at = 0; at < AT; ++at) set_thr(at, 0u);
 
   const int a_off = (q < 3 ? q : 0) * 256 + j * 16;
   stage_copy(0, 0);
   __syncthreads();
-  // passes 0 and 1; pass 2 only when some wave's survivor list overflowed
-  int g_end = 2 * kT3Stages;
+  // pass 1 (the candidates); pass 2 only when some wave's survivor list overflowed
+  int g_end = kT3Stages;
   for (int g = 0; g < g_end; ++g) {
-    const int pass = g / kT3Stages, buf = g & 1;
+    const int pass = 1 + g / kT3Stages, buf = g & 1;
     if (g + 1 < g_end) stage_copy(g + 1, buf ^ 1);  // (pass 2's first stage: after the decision below)
     if (g == kT3Stages) {
-      // pass 0 done: the lowest bucket that can still win, and the threshold on |S|
-#pragma unroll
-      for (int at = 0; at < AT; ++at) {
-        float sm = m[at];
-        sm = fmaxf(sm, __shfl_xor(sm, 16, 64));
-        sm = fmaxf(sm, __shfl_xor(sm, 32, 64));
-        mg[at] = (fabsf(sm) + fabsf(e1[at])) * 0x1p-14f;
-        const float lb = sm + es[at] - mg[at];
-        uint32_t mlow = lb > 0.f ? t3_bucket(lb) : 0u;
-        mlow = max(mlow, max(mp[at], 0x4000u));
-        thr[at] = __uint_as_float((mlow << 16) - 0x8000u) - e1[at] - mg[at];
-        if (q == 0) st_t[wave][at * 16 + j] = thr[at] - mg[at];
-      }
-    } else if (g == 2 * kT3Stages) {
       // pass 2 (the survivors overflowed): thresholds at the atoms' final best buckets
 #pragma unroll
       for (int at = 0; at < AT; ++at) {
@@ -750,14 +742,6 @@ __global__ __launch_bounds__(kThreads, 4) void t3_kernel(const uint4 *__restrict
 #pragma unroll
       for (int at = 0; at < AT; ++at)
         c[at] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b[at], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-      if (pass == 0) {
-#pragma unroll
-        for (int at = 0; at < AT; ++at) {
-          const float v = fmaxf(fmaxf(m[at], fabsf(c[at][0])), fabsf(c[at][1]));
-          m[at] = fmaxf(fmaxf(v, fabsf(c[at][2])), fabsf(c[at][3]));
-        }
-        continue;
-      }
 #pragma unroll
       for (int at = 0; at < AT; ++at) {
         // the lane's largest |S| against the atom's threshold (a word and its complement: one test)
@@ -780,12 +764,17 @@ __global__ __launch_bounds__(kThreads, 4) void t3_kernel(const uint4 *__restrict
       }
     }
     // every wave evaluates its list at the stage end, so no wave's evaluation holds the others at the barrier
-    if (pass > 0 && cnt > 0) flush(pass);
-    if (g == 2 * kT3Stages - 1) {
+    if (cnt > 0) flush(pass);
+    if (pass == 1) {
+      // the thresholds rise with the best buckets found so far (this wave's own atoms: no barrier needed)
+#pragma unroll
+      for (int at = 0; at < AT; ++at) set_thr(at, st_m[wave][at * 16 + j]);
+    }
+    if (g == kT3Stages - 1) {
       // pass 1 done: pass 2 only if a survivor list overflowed (all waves agree)
       // (rows_by_sweep: pass 2 always -- the path an overflow takes, for its tests)
       if (__syncthreads_or(rows_by_sweep != 0 || surv_n[wave] > static_cast<uint32_t>(kT3Surv))) {
-        g_end = 3 * kT3Stages;
+        g_end = 2 * kT3Stages;
         stage_copy(g + 1, buf ^ 1);  // buffer buf ^ 1 was last read in stage g - 1, before the barrier
         __syncthreads();
       }
@@ -793,7 +782,7 @@ __global__ __launch_bounds__(kThreads, 4) void t3_kernel(const uint4 *__restrict
       __syncthreads();
     }
   }
-  if (g_end == 2 * kT3Stages) {
+  if (g_end == kT3Stages) {
     // the lowest row at each atom's best bucket, from its survivors (every word that reached the final
     // best bucket was at or above the running best when it was evaluated)
     const int ns = static_cast<int>(surv_n[wave]);
