@@ -2,8 +2,8 @@
 
 Both compute NN-B (castor.py:544-557): indices must be equal on every atom that
 is not a near-tie (oracle/nn.py classifies each disagreement).  Cases: the
-config-4 distribution at every launch size the scorer distinguishes (1, 2, 4
-and 8 atom tiles per wave), atoms dominated by one coordinate (whose
+config-4 distribution at every launch size the scorer distinguishes (1, 2 and
+4 atom tiles per wave), atoms dominated by one coordinate (whose
 candidate threshold falls to zero or below, so both signs of a word are
 listed), near-origin and zero atoms, ragged small launches, atoms whose
 best code sits in the type-3 family by construction (scaled type-3 codes plus
@@ -101,7 +101,7 @@ def test_fixed_points_of_every_type3_code(dev):
 
 def test_row_sweep_path_equals_survivor_path(dev):
     # the lowest row at the best bucket comes from the per-wave survivor lists unless one overflows; the
-    # overflow path (a third sweep over the patterns) must give the same indices on every atom
+    # overflow path (a second sweep over the patterns) must give the same indices on every atom
     g = torch.Generator().manual_seed(14)
     n = 60_000
     spiky = torch.randn(n // 4, 24, generator=g) * 0.05
