@@ -10,14 +10,16 @@ input.  One step = ``castor.quantize_indices`` over all of them (fp32 atoms
 resident in HBM -> int32 codebook indices).
 
 The JSON line also carries
-  roofline      the dominant kernel of that launch, nn_kernel's sweep of the pair
-                region, against the dense bf16 MFMA peak: algorithmic flops
-                2*24*49,128 per atom (one dot product per type-1 / type-2
-                representative) over its HIP-event kernel time inside the timed
-                region (events recorded on the launch stream); traffic from
-                profiles/ (rocprofv3 --pmc); beside it t3_kernel's time (the
-                structured type-3 scorer);
-  dense_sweep_baseline  the same quantize with every code swept densely;
+  roofline      the dominant kernel of that launch, t3_kernel (the structured
+                type-3 scorer), against the dense bf16 MFMA peak: its
+                algorithmic MFMA flops 2*24*2,048 per atom (the representative
+                Golay sign-pattern sums) over its HIP-event kernel time inside
+                the timed region (events recorded on the launch stream); the
+                VALU issue fraction that binds it (rocprofv3 counters) and its
+                HBM traffic from profiles/; beside it t12_kernel's time (the
+                structured type-1/2 scorer);
+  dense_sweep_baseline  the same quantize with every code swept densely on
+                MFMA (nn_kernel: 2*24*196,560 flops per atom);
   dequant_gemv  the metric's second half: the fused dequant-GEMV at d=1920
                 (config 5, batch 1) in compressed-stream GB/s and as a fraction
                 of HBM peak;
@@ -53,14 +55,16 @@ FLOP_PER_ATOM = 2 * 24 * 196_560
 # type-3 codes, one representative per antipodal pair of the others, padding)
 # at K = 32 (24 coordinates + 8 zeros) -- 9,437,184.
 MFMA_FLOP_ISSUED_PER_ATOM = 2 * 32 * 9216 * 16
-# NN-B's default path: nn_kernel sweeps the pair region only -- 49,128 representatives
-# of the 98,256 type-1 / type-2 codes, whose antipodes' scores are the negations
-# (no products) -- 2 * 24 * 49,128 = 2,358,144 algorithmic flops per atom, issued as
-# 3,072 tiles at K = 32 (3,145,728); t3_kernel scores the 98,304 type-3 codes from
-# 128 tiles of Golay sign patterns plus per-candidate VALU work.
-PAIR_REPS = 49_128
-FLOP_PER_ATOM_PAIRS = 2 * 24 * PAIR_REPS
-MFMA_FLOP_ISSUED_PER_ATOM_PAIRS = 2 * 32 * 3072 * 16
+# NN-B's default path, the structured scorers: t12_kernel scores the 98,256 type-1 / type-2
+# codes from the 759 octad sums of |x| (2 * 24 * 759 = 36,432 algorithmic MFMA flops per
+# atom, issued as 48 tiles at K = 32: 49,152) and t3_kernel the 98,304 type-3 codes from
+# the 2,048 representative Golay sign-pattern sums (2 * 24 * 2,048 = 98,304 flops per atom,
+# issued as 128 tiles: 131,072); both evaluate their few candidate codes exactly on the VALU,
+# and that VALU work, not the MFMA, bounds them.
+T12_FLOP_PER_ATOM = 2 * 24 * 759
+T12_MFMA_ISSUED_PER_ATOM = 2 * 32 * 48 * 16
+T3_FLOP_PER_ATOM = 2 * 24 * 2048
+T3_MFMA_ISSUED_PER_ATOM = 2 * 32 * 128 * 16
 PEAK_BF16_FLOPS = 2.5e15  # MI355X dense bf16 MFMA
 PEAK_HBM_BPS = 8.0e12  # MI355X HBM3E
 C2_SHAPES = [(3456, 1152), (1152, 1152), (4608, 1152), (1152, 4608)]
@@ -459,13 +463,12 @@ def optim_extras(device, mats, iters=9, sets=3):
         optim.pollux_h24_step_many_(state, heat=heat, step=counter, width_inertia=inertia, scalars=sc)
         counter.add_(1)
 
-    t_f, nn_ms = _profiled(full_step, 3, 0, warmup=1)
+    t_f, kms = _scorer_profiled(full_step, 3, warmup=1)
     out["pollux1920_step"] = {
-        "atoms": atoms, "step_ms": t_f * 1e3, "atoms_per_s": atoms / t_f, "nn_kernel_ms": nn_ms,
-        "nn_kernel_mfma_frac": FLOP_PER_ATOM_PAIRS * atoms / (nn_ms / 1e3) / PEAK_BF16_FLOPS,
+        "atoms": atoms, "step_ms": t_f * 1e3, "atoms_per_s": atoms / t_f, **kms,
         "note": "plx_pollux_step_h24_batch over all 111 H24 tensors of Pollux-1920 (18 x q/k/v/o 1920x1920, "
                 "fc1 7680x1920, fc2 1920x7680; tok_emb and head 50688x1920; pos_emb 1024x1920): 111 update "
-                "passes and one scoring sweep; synthetic state (latent N(0, 0.02))"}
+                "passes and one pass of the structured scorers; synthetic state (latent N(0, 0.02))"}
     del state
     torch.cuda.empty_cache()
     return out
@@ -486,15 +489,20 @@ def pack_time_extras(mats, iters=5):
             "note": "quantize_h24_layer (NN-P + sigma16 + 18-bit pack) on the four config-2 weights"}
 
 
-def traffic_from_profiles(name="nn_kernel_c4_traffic.json"):
-    """HBM bytes per nn_kernel launch measured by two rocprofv3 --pmc runs (committed under profiles/)."""
+def json_from_profiles(name):
+    """A JSON summary committed under profiles/ (rocprofv3 counter runs), or {} when absent or unreadable."""
     p = ROOT / "profiles" / name
     if p.exists():
         try:
-            return json.loads(p.read_text()).get("hbm_bytes_per_launch")
+            return json.loads(p.read_text())
         except (ValueError, OSError):
-            return None
-    return None
+            return {}
+    return {}
+
+
+def traffic_from_profiles(name):
+    """HBM bytes per launch of a kernel measured by two rocprofv3 --pmc runs (committed under profiles/)."""
+    return json_from_profiles(name).get("hbm_bytes_per_launch")
 
 
 def make_c4(device, seed=404):
@@ -513,7 +521,8 @@ def make_c4(device, seed=404):
 def _profiled(fn, iters, kernel=0, warmup=0, rounds=1, warm_s=0.0):
     """(seconds per call, selected kernel's ms per launch) of fn, the kernel timed by HIP events.
 
-    kernel: a PLX_PROF_* id (0 = nn_kernel, 1 pack, 2 unpack, 3 dequant, 4 the optimiser update); the
+    kernel: a PLX_PROF_* id (0 = nn_kernel, 1 pack, 2 unpack, 3 dequant, 4 the optimiser update, 5 t3_kernel,
+    6 t12_kernel); the
     events are recorded on the kernel's launch stream around every launch of the timed calls.
     """
     import ctypes
@@ -535,9 +544,17 @@ def _profiled(fn, iters, kernel=0, warmup=0, rounds=1, warm_s=0.0):
     return t, tot_ms.value / max(1, launches.value)
 
 
-def _nn_profiled(fn, iters):
-    """(seconds per call, nn_kernel ms per launch) of fn over iters calls, nn_kernel timed by HIP events."""
-    return _profiled(fn, iters, 0)
+def _scorer_profiled(fn, iters, mode="bf16", warmup=0):
+    """(seconds per call, {kernel: ms per launch}) of fn over iters calls, the scoring kernels timed by HIP events:
+    NN-B's structured scorers (t3_kernel, t12_kernel), or nn_kernel (the dense sweep of the other modes)."""
+    from pollux_amd import _lib
+
+    if mode == "bf16":
+        t, t3 = _profiled(fn, iters, _lib.PROF_T3, warmup=warmup)
+        _, t12 = _profiled(fn, iters, _lib.PROF_T12)
+        return t, {"t3_kernel_ms_avg": t3, "t12_kernel_ms_avg": t12}
+    t, nn = _profiled(fn, iters, _lib.PROF_NN, warmup=warmup)
+    return t, {"nn_kernel_ms_avg": nn}
 
 
 def sweep_extras(device, mode="bf16", steps=10):
@@ -565,14 +582,12 @@ def sweep_extras(device, mode="bf16", steps=10):
             castor.requantize_h24(w, mode=mode)
 
     step2()
-    t, k_ms = _nn_profiled(step2, steps)
+    t, kms = _scorer_profiled(step2, steps, mode)
     out["config2_requantize"] = {
-        "atoms": atoms2, "ms_per_step": t * 1e3, "atoms_per_s": atoms2 / t, "nn_kernel_ms_avg": k_ms,
-        "nn_kernel_mfma_frac": FLOP_PER_ATOM_PAIRS * atoms2 / 4 / (k_ms / 1e3) / PEAK_BF16_FLOPS,
+        "atoms": atoms2, "ms_per_step": t * 1e3, "atoms_per_s": atoms2 / t, **kms,
         "note": "fused row scale + NN-B + pack + reconstructed weight of QKV 3456x1152, O 1152x1152, up 4608x1152, "
                 "down 1152x4608 (bf16-rounded N(0, 0.02) master weights), one requantize_h24 call per latent "
-                "(pollux.py:828-884); nn_kernel_mfma_frac: the pair sweep's algorithmic flops over the average of the "
-                "four launches"}
+                "(pollux.py:828-884); kernel times: the average over the four launches"}
     t_b = time_gpu(lambda: castor.requantize_h24_many(mats2, mode=mode), steps, 2)
     out["config2_requantize_batched"] = {
         "ms_per_step": t_b * 1e3, "atoms_per_s": atoms2 / t_b,
@@ -589,9 +604,9 @@ def sweep_extras(device, mode="bf16", steps=10):
             castor.requantize_h24(w, mode="bf16")
 
     step()
-    t, k_ms = _nn_profiled(step, 5)
+    t, kms = _scorer_profiled(step, 5)
     out["config3_requantize"] = {
-        "atoms": atoms, "ms_per_step": t * 1e3, "atoms_per_s": atoms / t, "nn_kernel_ms_avg": k_ms,
+        "atoms": atoms, "ms_per_step": t * 1e3, "atoms_per_s": atoms / t, **kms,
         "note": "fused row scale + NN-B + pack + reconstructed weight of QKV 5760x1920, O 1920x1920, up 7680x1920, "
                 "down 1920x7680 (bf16-rounded N(0, 0.02) master weights)"}
 
@@ -620,9 +635,9 @@ def sweep_extras(device, mode="bf16", steps=10):
     dirs = torch.randn(near_at.numel(), 24, generator=rng, device=device)
     x[near_at] = dirs / dirs.norm(dim=1, keepdim=True) * np.sqrt(2.0)
     castor.quantize_indices(x, mode="bf16")
-    t, k_ms = _nn_profiled(lambda: castor.quantize_indices(x, mode="bf16"), 5)
+    t, kms = _scorer_profiled(lambda: castor.quantize_indices(x, mode="bf16"), 5)
     out["config3_stress_quantize"] = {
-        "atoms": atoms, "ms": t * 1e3, "atoms_per_s": atoms / t, "nn_kernel_ms": k_ms,
+        "atoms": atoms, "ms": t * 1e3, "atoms_per_s": atoms / t, **kms,
         "note": "quantize_indices (NN-B) on the config-3 lattice atoms with 5% contact-pair midpoints and 5% "
                 "near-origin atoms (more near-ties for the exact rescoring pass)"}
     return out
@@ -1015,6 +1030,9 @@ def main() -> int:
     for _ in range(args.warmup):
         idx = step()
     torch.cuda.synchronize()
+    structured = args.mode == "bf16"
+    # the dominant kernel's launches are timed by HIP events on their stream inside the timed region
+    _lib.check(lib.plx_profile_select(_lib.PROF_T3 if structured else _lib.PROF_NN), "plx_profile_select")
     _lib.check(lib.plx_profile_begin(), "plx_profile_begin")
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -1026,46 +1044,57 @@ def main() -> int:
 
     tot_ms, launches = ctypes.c_double(), ctypes.c_int64()
     _lib.check(lib.plx_profile_end(ctypes.byref(tot_ms), ctypes.byref(launches)), "plx_profile_end")
+    _lib.check(lib.plx_profile_select(_lib.PROF_NN), "plx_profile_select")
     ms_per_step = elapsed / args.steps * 1e3
     value = atoms * args.steps / elapsed
     log(f"[bench] timed {args.steps} steps: {ms_per_step:.3f} ms/step, {value:.4g} atoms/s")
 
     kernel_s = tot_ms.value / 1e3
-    structured = args.mode == "bf16"
-    fpa = FLOP_PER_ATOM_PAIRS if structured else FLOP_PER_ATOM
-    issued = MFMA_FLOP_ISSUED_PER_ATOM_PAIRS if structured else MFMA_FLOP_ISSUED_PER_ATOM
+    kernel_avg_ms = tot_ms.value / max(1, launches.value)
+    fpa = T3_FLOP_PER_ATOM if structured else FLOP_PER_ATOM
+    issued = T3_MFMA_ISSUED_PER_ATOM if structured else MFMA_FLOP_ISSUED_PER_ATOM
     achieved = fpa * atoms * args.steps / kernel_s if kernel_s > 0 else 0.0
+    counters = json_from_profiles("quantize_c4_counters.json") if structured else {}
     roofline = {
         "bound": "mfma",
         "achieved": achieved / 1e12,
         "peak": PEAK_BF16_FLOPS / 1e12,
         "unit": "TFLOP/s",
         "frac": achieved / PEAK_BF16_FLOPS,
-        "traffic": traffic_from_profiles("nn_kernel_c4_traffic.json" if structured else "nn_kernel_c4_dense_traffic.json"),
-        "kernel": "nn_kernel (bf16 16x16x32 MFMA scoring + running max)"
-        + (": the pair sweep (type-1 / type-2 representatives, 3,072 tiles)" if structured else ""),
+        "traffic": traffic_from_profiles("t3_kernel_c4_traffic.json" if structured else "nn_kernel_c4_dense_traffic.json"),
+        "kernel": "t3_kernel (structured type-3 scorer: 128 Golay sign-pattern tiles on bf16 16x16x32 MFMA, the "
+        "candidate words' 24 positions on the VALU)" if structured else
+        "nn_kernel (bf16 16x16x32 MFMA scoring + running max over 9,216 tiles)",
         "kernel_launches": int(launches.value),
-        "kernel_avg_ms": tot_ms.value / max(1, launches.value),
+        "kernel_avg_ms": kernel_avg_ms,
         "flop_per_atom": fpa,
         "flop_per_launch": fpa * atoms,
         "mfma_issue_frac": issued * atoms * args.steps / kernel_s / PEAK_BF16_FLOPS if kernel_s > 0 else 0.0,
     }
     if structured:
-        # the rest of the scoring: the structured type-3 scorer, and the dense type-3 sweep it replaces
-        _, t3_ms = _profiled(step, 3, _lib.PROF_T3)
-        t_d, nn_d = _profiled(lambda: castor.quantize_indices(x, mode="bf16-dense"), 3, 0, warmup=1)
+        # the type-1/2 scorer, and the dense sweep the two structured scorers replace
+        _, t12_ms = _profiled(step, 3, _lib.PROF_T12)
+        t_d, nn_d = _profiled(lambda: castor.quantize_indices(x, mode="bf16-dense"), 3, _lib.PROF_NN, warmup=1)
         roofline["flop_per_atom_note"] = (
-            "2 * 24 flops per pair representative (49,128 per atom; an antipode's score is the negation, no "
-            "products); the type-3 codes are scored by t3_kernel, not counted here")
-        roofline["t3_kernel_avg_ms"] = t3_ms
-        roofline["t3_kernel_step_share"] = t3_ms / ms_per_step
+            "2 * 24 flops per representative Golay sign pattern (2,048 per atom; each also scores its "
+            "complement); the candidates' exact evaluation is VALU work, which binds the kernel: valu_issue_frac")
+        t3c = counters.get("t3_kernel", {})
+        if t3c:
+            roofline["valu_issue_frac"] = t3c.get("valu_issue_frac")
+            roofline["valu_note"] = counters.get("valu_note")
+        roofline["kernel_step_share"] = kernel_avg_ms / ms_per_step
+        roofline["t12_kernel_avg_ms"] = t12_ms
+        roofline["t12_kernel_step_share"] = t12_ms / ms_per_step
+        roofline["t12_kernel_mfma_frac"] = T12_FLOP_PER_ATOM * atoms / (t12_ms / 1e3) / PEAK_BF16_FLOPS
+        if counters.get("t12_kernel"):
+            roofline["t12_kernel_valu_issue_frac"] = counters["t12_kernel"].get("valu_issue_frac")
         result_dense = {
             "ms_per_step": t_d * 1e3, "atoms_per_s": atoms / t_d, "nn_kernel_avg_ms": nn_d,
             "nn_kernel_frac": FLOP_PER_ATOM * atoms / (nn_d / 1e3) / PEAK_BF16_FLOPS,
             "nn_kernel_mfma_issue_frac": MFMA_FLOP_ISSUED_PER_ATOM * atoms / (nn_d / 1e3) / PEAK_BF16_FLOPS,
             "note": "the same workload with every code swept densely (9,216 tiles, 2 * 24 * 196,560 flops per "
-                    "atom; castor mode 'bf16-dense', PLX_NN_DENSE_TYPE3): the baseline the structured type-3 "
-                    "scorer is measured against; identical indices off near-ties"}
+                    "atom; castor mode 'bf16-dense', PLX_NN_DENSE_TYPE3): the baseline the structured scorers "
+                    "are measured against; identical indices off near-ties"}
 
     result = {
         "metric": METRIC,
@@ -1085,8 +1114,8 @@ def main() -> int:
             "1920, the config's 16,777,216 rounded down to whole rows), directions uniform on S^23, radius "
             "U(0, 2) * sqrt(32), fed directly as quantizer input; fp32 atoms in HBM -> int32 indices",
             "atoms_per_step": atoms,
-            "call": "castor.quantize_indices (plx_quantize: operand prep, nn_kernel pair sweep, t3_kernel "
-            "structured type-3 scorer, resolve)" if structured else
+            "call": "castor.quantize_indices (plx_quantize: operand prep, t12_kernel structured type-1/2 scorer, "
+            "t3_kernel structured type-3 scorer, pick)" if structured else
             "castor.quantize_indices (plx_quantize: operand prep, nn_kernel scoring sweep, resolve)",
             "nn_mode": "NN-T (fp32 scores)" if args.mode == "fp32" else "NN-B (bf16 scores)",
             "seed": 404,

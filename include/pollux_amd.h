@@ -42,16 +42,18 @@ extern "C" {
  *       pack-time search, pack._quantize_h24_layer (pack.py:167-177). */
 #define PLX_NN_PACK_FP32 2
 /* Flag OR'ed into PLX_NN_BF16_SCORES (quantize / requantize entry points):
- * score the 98,304 type-3 codes densely on MFMA (one contraction per code)
- * instead of the default structured scorer, which scores the 2,048 Golay
- * sign-pattern pairs and evaluates the few candidate patterns exactly.  Both
- * have NN-B semantics (equal answers off near-ties); the dense sweep is kept
- * as the measured baseline of the structured one.  Ignored by the other modes. */
+ * score every code densely on MFMA (one contraction per type-3 code and per
+ * antipodal pair of type-1/2 codes) instead of the default structured
+ * scorers, which score the 759 octads' sums of |x| and the 2,048 Golay
+ * sign-pattern pairs and evaluate the few candidate codes exactly.  Both have
+ * NN-B semantics (equal answers off near-ties); the dense sweep is kept as
+ * the measured baseline of the structured one.  Ignored by the other modes. */
 #define PLX_NN_DENSE_TYPE3 0x100
 /* Flag OR'ed into PLX_NN_BF16_SCORES for plx_quantize (diagnostics): the
- * structured scorer finds the lowest row at the best bucket by a third sweep
- * over the patterns -- the path it takes when its per-wave list of surviving
- * words overflows -- instead of from that list.  Same results. */
+ * structured scorers find the lowest row at the best bucket by a second sweep
+ * over the octads and the patterns -- the path each takes when a per-wave list
+ * of surviving octads / words overflows -- instead of from those lists.  Same
+ * results. */
 #define PLX_NN_T3_ROWS_BY_SWEEP 0x200
 
 /* ---- element types of plx_gather_codebook's output -------------------- */
@@ -443,12 +445,13 @@ int plx_int8_embed(const int8_t *q, const uint16_t *mu16, int64_t vocab, int64_t
  * events and returns the summed kernel time (ms) and the number of
  * launches.  Used by bench.py for the roofline's per-launch kernel duration
  * and the HBM kernels' bandwidth. */
-#define PLX_PROF_NN 0      /* nn_kernel (plx_quantize / plx_requantize*) */
+#define PLX_PROF_NN 0      /* nn_kernel (the dense sweep of plx_quantize / plx_requantize*) */
 #define PLX_PROF_PACK 1    /* pack_kernel (plx_pack_indices) */
 #define PLX_PROF_UNPACK 2  /* unpack_kernel (plx_unpack_indices) */
 #define PLX_PROF_DEQUANT 3 /* dequant_kernel (plx_dequant_f16) */
 #define PLX_PROF_ADAM 4    /* adam_h24_kernel (plx_pollux_step_h24*) */
 #define PLX_PROF_T3 5      /* t3_kernel (the structured type-3 scorer of NN-B) */
+#define PLX_PROF_T12 6     /* t12_kernel (the structured type-1/2 scorer of NN-B) */
 int plx_profile_select(int kernel);
 int plx_profile_begin(void);
 int plx_profile_end(double *total_ms, int64_t *launches);

@@ -17,10 +17,10 @@ LIB_PATH = Path(__file__).resolve().parent / "lib" / "libpollux_amd.so"
 
 PLX_OK, PLX_EINVAL, PLX_EHIP, PLX_ENOMEM = 0, 1, 2, 3
 NN_BF16_SCORES, NN_FP32_SCORES, NN_PACK_FP32 = 0, 1, 2
-NN_DENSE_TYPE3 = 0x100  # flag on NN_BF16_SCORES: the dense type-3 sweep instead of the structured scorer
-NN_T3_ROWS_BY_SWEEP = 0x200  # flag on NN_BF16_SCORES (diagnostics): the structured scorer's overflow path
+NN_DENSE_TYPE3 = 0x100  # flag on NN_BF16_SCORES: the dense sweep of every code instead of the structured scorers
+NN_T3_ROWS_BY_SWEEP = 0x200  # flag on NN_BF16_SCORES (diagnostics): the structured scorers' overflow path
 DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
-PROF_NN, PROF_PACK, PROF_UNPACK, PROF_DEQUANT, PROF_ADAM, PROF_T3 = 0, 1, 2, 3, 4, 5  # plx_profile_select
+PROF_NN, PROF_PACK, PROF_UNPACK, PROF_DEQUANT, PROF_ADAM, PROF_T3, PROF_T12 = 0, 1, 2, 3, 4, 5, 6  # plx_profile_select
 
 _vp, _i64, _int, _sz = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_size_t
 

@@ -60,13 +60,13 @@ INDICES_PER_CHUNK = 4
 BYTES_PER_CHUNK = 9
 LEECH_SCALE: float = 1.0 / math.sqrt(8.0)
 
-# "bf16-dense": NN-B with every type-3 code scored densely on MFMA (the sweep the structured type-3
-# scorer replaces; same answers off near-ties), kept as the measured baseline
+# "bf16-dense": NN-B with every code scored densely on MFMA (the sweep the structured scorers
+# replace; same answers off near-ties), kept as the measured baseline
 _MODES = {"bf16": _lib.NN_BF16_SCORES, "fp32": _lib.NN_FP32_SCORES,
           "bf16-dense": _lib.NN_BF16_SCORES | _lib.NN_DENSE_TYPE3}
 # quantize_indices also takes "pack": the pack-time NN-P search (pack.py:167-177)
 _INDEX_MODES = {**_MODES, "pack": _lib.NN_PACK_FP32,
-                 # NN-B through the structured scorer's list-overflow path (its tests)
+                 # NN-B through the structured scorers' list-overflow path (their tests)
                  "bf16-rows-sweep": _lib.NN_BF16_SCORES | _lib.NN_T3_ROWS_BY_SWEEP}
 _mode_lock = threading.Lock()
 _nn_mode = os.environ.get("POLLUX_AMD_NN_MODE", "bf16")
@@ -76,7 +76,7 @@ if _nn_mode not in _MODES:
 
 def set_nn_mode(mode: str) -> None:
     """Select the quantizer semantics: "bf16" (NN-B, default), "fp32" (NN-T), or "bf16-dense" (NN-B with
-    the type-3 codes scored densely instead of by the structured scorer: the same answers off near-ties)."""
+    every code scored densely instead of by the structured scorers: the same answers off near-ties)."""
     global _nn_mode
     if mode not in _MODES:
         raise ValueError(f"nn mode must be one of {sorted(_MODES)}, got {mode!r}")
@@ -300,8 +300,8 @@ def _workspace(n_atoms: int, device: torch.device) -> torch.Tensor:
 def quantize_indices(x: torch.Tensor, mode: str | None = None) -> torch.Tensor:
     """int32 codebook indices of the atoms of ``x`` ([..., 24], any float dtype).
 
-    mode: "bf16" (NN-B), "bf16-dense" (NN-B, dense type-3 sweep), "fp32" (NN-T) or "pack" (NN-P);
-    default: the module mode.  ("bf16-rows-sweep": NN-B through the structured scorer's overflow path.)
+    mode: "bf16" (NN-B), "bf16-dense" (NN-B, dense sweep), "fp32" (NN-T) or "pack" (NN-P);
+    default: the module mode.  ("bf16-rows-sweep": NN-B through the structured scorers' overflow path.)
     """
     _lib.require_device(x, "quantize input")
     xf = x.reshape(-1, H24_DIM).float().contiguous()

@@ -47,6 +47,13 @@ constexpr int kT3Reps = 2048;
 constexpr int kT3Tiles = kT3Reps / kTileCodes;  // 128
 constexpr int kT3Words = 2 * kT3Reps;
 
+// Structured pair scoring (quantize.hip, NN-B): a type-2 code is +-2s on the
+// 8 positions of an octad (759 weight-8 Golay words) with an even number of
+// minus signs, a type-1 code +-4s on two positions.
+constexpr int kT2Octads = 759;
+constexpr int kT2Tiles = 48;  // 768 octad slots
+constexpr int kT2Subsets5 = 42504;  // C(24, 5): each in exactly one octad
+
 // fp32 constants of the reference (castor.py:47,50,68; castor.py:522; pack.py:164)
 constexpr uint32_t kLeechScaleBits = 0x3EB504F3u;  // fp32(1/sqrt 8)
 constexpr uint32_t kSLatticeBits = 0x3F3504F3u;    // fp32(1/sqrt 2)
@@ -72,6 +79,11 @@ struct DeviceTables {
   uint8_t *t3_tiles = nullptr;       // [kT3Tiles][3][16][8] bf16 sign patterns +-s of the representative words
   uint32_t *t3_words = nullptr;      // [4096] word of pattern id (representatives, then their complements)
   uint32_t *t3_rows = nullptr;       // [4096][24] codebook row of the type-3 code (word of id, -3 at position p)
+  uint8_t *t2_tiles = nullptr;       // [kT2Tiles][3][16][8] bf16 octad indicators times 2s
+  uint2 *t2_pos = nullptr;           // [kT2Tiles*16] the 8 positions of each octad, one byte each
+  uint32_t *t2_rows = nullptr;       // [759][128] codebook row of the octad code with sign pattern p
+  uint32_t *t1_rows = nullptr;       // [24][24][4] codebook row of the type-1 code at i < j, minus bits
+  uint16_t *t2_steiner = nullptr;    // [kT2Subsets5] the octad holding each 5-subset (colex rank)
 };
 
 // Plane tables (tables.cpp; host, built once): the codebook rows take only a

@@ -54,7 +54,7 @@ using namespace plx;
 extern "C" {
 
 int plx_profile_select(int kernel) {
-  if (kernel < PLX_PROF_NN || kernel > PLX_PROF_T3)
+  if (kernel < PLX_PROF_NN || kernel > PLX_PROF_T12)
     return fail(PLX_EINVAL, "plx_profile_select: unknown kernel id %d", kernel);
   Profile &p = prof();
   std::lock_guard<std::mutex> lock(p.mu);

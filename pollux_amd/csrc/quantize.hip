@@ -219,7 +219,7 @@ __global__ __launch_bounds__(kThreads, MODE == kModeB ? 3 : 2) void nn_kernel(co
                                                                              int64_t n_atoms,
                                                           const uint8_t *__restrict__ tiles, int n_slices,
                                                           int tiles_per_slice, uint4 *__restrict__ keys,
-                                                          uint64_t *__restrict__ recs, int s0, int t0_base) {
+                                                          uint64_t *__restrict__ recs, int s0) {
   __shared__ __align__(16) uint8_t lds[2][kStageBytes];
 
   const int slice = static_cast<int>(blockIdx.x % static_cast<unsigned>(n_slices));
@@ -257,7 +257,7 @@ __global__ __launch_bounds__(kThreads, MODE == kModeB ? 3 : 2) void nn_kernel(co
     }
   }
 
-  const int t0 = t0_base + slice * tiles_per_slice;  // t0_base: kType3Tiles when only the pair region is swept
+  const int t0 = slice * tiles_per_slice;
   const int n_stages = tiles_per_slice / kST;
   // stages [0, n_t) hold type-3 tiles, [n_t, n_stages) pair representatives
   // (the region boundary falls on a stage boundary)
@@ -515,7 +515,7 @@ __global__ __launch_bounds__(kThreads, MODE == kModeB ? 3 : 2) void nn_kernel(co
 // only if a survivor list overflows):
 //   pass 1  every lane whose four outputs hold a word that could reach the
 //           lowest bucket still possible -- the best pair bucket (the pair
-//           records), 2.0 (the origin rule) and the best type-3 bucket found
+//           key of t12_kernel), 2.0 (the origin rule) and the best type-3 bucket found
 //           so far, whichever is highest: |S| >= lo(bucket) - e1 - margin --
 //           appends one 4-byte entry (atom, tile, lane quarter, 4-bit mask of
 //           its outputs) to the wave's list in LDS; at every stage end (and
@@ -532,7 +532,7 @@ __global__ __launch_bounds__(kThreads, MODE == kModeB ? 3 : 2) void nn_kernel(co
 //   pass 2  (only after a survivor list overflowed) the same rows from a
 //           second sweep with the thresholds at M3.
 // The atom's key gets (M3 << 16, lowest row at M3), or 0 when no type-3 code
-// reaches 2.0; the resolve compares it with the pair region's candidates.
+// reaches 2.0; pick_kernel compares it with the pair key.
 // Buckets are taken by round-half-up like the dense sweep's, and every score
 // is an fp32 sum of exact products plus one rounding for the bonus, so the
 // answer equals the exact-score answer off near-ties (oracle/nn.py).
@@ -570,7 +570,6 @@ __global__ __launch_bounds__(kThreads, 4) void t3_kernel(const uint4 *__restrict
                                                          const uint8_t *__restrict__ t3_tiles,
                                                          const uint32_t *__restrict__ t3_words,
                                                          const uint32_t *__restrict__ t3_rows,
-                                                         const uint64_t *__restrict__ recs, int n_recs,
                                                          uint4 *__restrict__ keys, int rows_by_sweep) {
   constexpr int NA = AT * 16;  // atoms per wave
   static_assert(NA <= 128, "entry layout: 7 bits of atom");
@@ -620,14 +619,13 @@ __global__ __launch_bounds__(kThreads, 4) void t3_kernel(const uint4 *__restrict
     st_m[wave][i] = 0u;
     st_r[wave][i] = 0xFFFFFFFFu;
   }
-  // the best pair bucket of each atom (records of the pair sweep, which ran first)
+  // the best pair bucket of each atom (the pair key of t12_kernel, which ran first)
   uint32_t mp[AT];
 #pragma unroll
   for (int at = 0; at < AT; ++at) {
     const int64_t a = wave_atom0 + at * 16 + j;
     uint32_t m = 0u;
-    if (q == 0 && a < n_atoms)
-      for (int i = 0; i < n_recs; ++i) m = max(m, static_cast<uint32_t>(recs[static_cast<int64_t>(i) * n_atoms + a] >> 48));
+    if (q == 0 && a < n_atoms) m = keys[a].z >> 16;
     mp[at] = static_cast<uint32_t>(__shfl(static_cast<int>(m), j, 64));
   }
 
@@ -706,7 +704,7 @@ __global__ __launch_bounds__(kThreads, 4) void t3_kernel(const uint4 *__restrict
   };
 
   // The threshold on |S|: a word can reach bucket B only if |S| >= lo(B) - e1 - margin, and no bucket
-  // below the lowest that can still win counts: the best pair bucket (the pair records), 2.0 (the origin
+  // below the lowest that can still win counts: the best pair bucket (the pair key), 2.0 (the origin
   // rule), and -- raised at every stage end -- the best type-3 bucket found so far.
   float thr[AT];
   auto set_thr = [&](int at, uint32_t mlow) {
@@ -814,6 +812,431 @@ __global__ __launch_bounds__(kThreads, 4) void t3_kernel(const uint4 *__restrict
   }
 }
 
+// Structured pair scoring (NN-B; replaces the sweep's 3,072 pair tiles).
+//
+// A type-2 code is +-c2 on the 8 positions of an octad O (c2 = bf16(2s) =
+// 0.70703125) with an even number of minus signs; its score is
+// c2 sum_{i in O} e_i x_i (exact products, fp32 sums), at most
+// U(O) = c2 sum_{i in O} |x_i|.  Relative to the signs of x, a code flips a set
+// F of the octad's positions and scores c2 (sum_O |x_i| - 2 sum_F |x_i|), with
+// |F| of the parity of x's negative coordinates on O: the best code of an
+// octad flips nothing (even) or its smallest |x_i| (odd).  One MFMA with |x|
+// as the B operand gives U for 16 octads and 16 atoms: 48 tiles for the 759
+// octads.  A type-1 code is +-c1 on two positions (c1 = bf16(4s) =
+// 1.4140625); the best is c1 times the two largest |x_i|.
+// A block of 4 waves holds AT atom tiles of 16 atoms per wave as MFMA B
+// operands and streams the 48 octad tiles through LDS once (a second time
+// only if a survivor list overflows):
+//   set-up  one lane per atom scores the octad holding its 5 largest |x|
+//           (every 5 positions lie in exactly one octad, t2_steiner): usually
+//           at or near the atom's best octad, so the sweep starts from a high
+//           floor (~4 octads evaluated per atom instead of ~24);
+//   sweep   every lane whose outputs hold an octad with U >= lo(floor) - margin
+//           appends one 4-byte entry (atom, tile, quarter, output mask) to the
+//           wave's list; floor is the highest of 2.0 (the origin rule), the
+//           atom's best type-1 bucket and the best octad bucket found so far
+//           (raised at every stage end).  At every stage end (and when the list
+//           is full) the wave evaluates it, one entry per lane: the flagged
+//           octads' best codes scored exactly, the best bucket per atom kept by
+//           an LDS atomic max, octads at or above the running best onto a
+//           survivor list, which every stage end compacts to the octads at
+//           their atom's current best;
+//   rows    the survivors at the final best bucket M give every type-2 code at
+//           M: the flip sets F of the positions whose 2 c2 |x_i| fits in
+//           U - lo(M) are enumerated and scored exactly; type 1 the same way
+//           from the atom's coordinates when its best type-1 bucket is M; the
+//           lowest codebook row by LDS atomic min;
+//   pass 2  (only after a survivor list overflowed) the same rows from a
+//           second sweep with the thresholds at M.
+// The atom's key gets (M << 16, lowest row at M) in its upper 8 bytes, or 0
+// when no type-1/2 code reaches 2.0; t3_kernel takes M as its floor.
+// Buckets are taken by round-half-up like the dense sweep's, every score is
+// an fp32 sum of exact products in ascending position order, so the answer
+// equals the exact-score answer off near-ties (oracle/nn.py).
+constexpr int kT2ST = 8;                           // octad tiles per LDS stage
+constexpr int kT2Stages = kT2Tiles / kT2ST;        // 6
+constexpr int kT2StageBytes = kT2ST * kTileBytes;  // 6,144
+constexpr int kT2StageVecs = kT2StageBytes / 16;   // 384
+constexpr int kT2Cap = 384;                        // candidate entries per wave (4 bytes each)
+constexpr int kT2Surv = 256;                       // survivor entries per wave (4 bytes each)
+constexpr float kC1 = 1.4140625f;                  // bf16(4s)
+constexpr float kC2 = 0.70703125f;                 // bf16(2s)
+static_assert(kT2StageVecs % 64 == 0, "octad stage splits into whole wave loads");
+static_assert(kT2Tiles % kT2ST == 0 && kT2Tiles * kTileCodes >= kT2Octads && kT2Tiles <= 64, "whole octad stages");
+
+// |x| at octad o's 8 positions (pp: ascending, one byte each) of the atom whose bf16 coordinates are xr,
+// and the sign bits there (bit k: x negative at the k-th position).
+__device__ __forceinline__ uint32_t t2_load(const uint32_t *xr, uint2 pp, float *xa) {
+  const uint16_t *xh = reinterpret_cast<const uint16_t *>(xr);
+  uint32_t sg = 0u;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const uint32_t p = ((k < 4 ? pp.x : pp.y) >> (8 * (k & 3))) & 0xFFu;
+    const uint32_t h = xh[p];
+    xa[k] = __uint_as_float((h & 0x7FFFu) << 16);
+    sg |= (h >> 15) << k;
+  }
+  return sg;
+}
+
+// The exact score of the octad code with flips F (bit k: sign opposite to x's at the k-th position).
+__device__ __forceinline__ float t2_score(const float *xa, uint32_t F) {
+  float S = 0.f;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) S = fmaf(xa[k], ((F >> k) & 1u) ? -kC2 : kC2, S);
+  return S;
+}
+
+// The exact score of the octad's best code: no flip when x has an even number of negative coordinates there,
+// else its smallest |x| flipped.
+__device__ __forceinline__ float t2_best(const float *xa, uint32_t sg) {
+  float mn = xa[0];
+  int mi = 0;
+#pragma unroll
+  for (int k = 1; k < 8; ++k)
+    if (xa[k] < mn) {
+      mn = xa[k];
+      mi = k;
+    }
+  return t2_score(xa, (__popc(sg) & 1) ? 1u << mi : 0u);
+}
+
+// Colex rank of the 5-subset p0 < p1 < ... < p4 of the positions: C(p0,1) + C(p1,2) + ... + C(p4,5).
+__device__ __forceinline__ uint32_t subset5_rank(const uint32_t *p) {
+  return p[0] + p[1] * (p[1] - 1u) / 2u + p[2] * (p[2] - 1u) * (p[2] - 2u) / 6u +
+         p[3] * (p[3] - 1u) * (p[3] - 2u) * (p[3] - 3u) / 24u +
+         p[4] * (p[4] - 1u) * (p[4] - 2u) * (p[4] - 3u) * (p[4] - 4u) / 120u;
+}
+
+// The lowest row among octad o's codes at bucket M: every flip set of the parity of sg whose flipped |x|
+// can fit in U - lo(M) is scored.
+__device__ __forceinline__ uint32_t t2_rows_at(const float *xa, uint32_t sg, uint32_t o, uint32_t M,
+                                               const uint32_t *__restrict__ t2_rows) {
+  float U = 0.f;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) U = fmaf(xa[k], kC2, U);
+  const float room = (U - __uint_as_float((M << 16) - 0x8000u)) + U * 0x1p-14f;
+  uint32_t C = 0u;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) C |= (xa[k] * (2.f * kC2) <= room ? 1u : 0u) << k;
+  const uint32_t par = static_cast<uint32_t>(__popc(sg)) & 1u;
+  uint32_t rmin = 0xFFFFFFFFu;
+  for (uint32_t F = C;; F = (F - 1u) & C) {  // every subset of C, the empty one last
+    if ((static_cast<uint32_t>(__popc(F)) & 1u) == par) {
+      const float S = t2_score(xa, F);
+      if (S > 0.f && t3_bucket(S) == M) rmin = min(rmin, t2_rows[o * 128u + ((sg ^ F) & 0x7Fu)]);
+    }
+    if (F == 0u) break;
+  }
+  return rmin;
+}
+
+// The lowest row among the type-1 codes at bucket M of the atom whose bf16 coordinates are xr (v1: its
+// largest |x|): the positions i with c1 (|x_i| + v1) >= lo(M) - margin, every pair of them, all four signs.
+__device__ uint32_t t1_rows_at(const uint32_t *xr, float v1, uint32_t M, const uint32_t *__restrict__ t1_rows) {
+  const uint16_t *xh = reinterpret_cast<const uint16_t *>(xr);
+  const float lo = __uint_as_float((M << 16) - 0x8000u);
+  const float top = v1 * kC1;
+  const float need = lo - top - top * 0x1p-13f;
+  uint32_t C = 0u;
+  for (int i = 0; i < kDim; ++i) {
+    const float a = __uint_as_float((static_cast<uint32_t>(xh[i]) & 0x7FFFu) << 16);
+    C |= (a * kC1 >= need ? 1u : 0u) << i;
+  }
+  uint32_t rmin = 0xFFFFFFFFu;
+  for (uint32_t ci = C; ci != 0u; ci &= ci - 1u) {
+    const int i = __builtin_ctz(ci);
+    const float xi = __uint_as_float(static_cast<uint32_t>(xh[i]) << 16) * kC1;
+    for (uint32_t cj = ci & (ci - 1u); cj != 0u; cj &= cj - 1u) {
+      const int j = __builtin_ctz(cj);
+      const float xj = __uint_as_float(static_cast<uint32_t>(xh[j]) << 16) * kC1;
+#pragma unroll
+      for (uint32_t e = 0; e < 4; ++e) {
+        const float S = ((e & 1u) ? -xi : xi) + ((e & 2u) ? -xj : xj);
+        if (S > 0.f && t3_bucket(S) == M) rmin = min(rmin, t1_rows[(static_cast<uint32_t>(i) * kDim + j) * 4u + e]);
+      }
+    }
+  }
+  return rmin;
+}
+
+template <int AT>
+__global__ __launch_bounds__(kThreads, 4) void t12_kernel(const uint4 *__restrict__ xb, int64_t n_atoms,
+                                                          const uint8_t *__restrict__ t2_tiles,
+                                                          const uint2 *__restrict__ t2_pos,
+                                                          const uint32_t *__restrict__ t2_rows,
+                                                          const uint32_t *__restrict__ t1_rows,
+                                                          const uint16_t *__restrict__ t2_steiner,
+                                                          uint4 *__restrict__ keys, int rows_by_sweep) {
+  constexpr int NA = AT * 16;  // atoms per wave
+  static_assert(NA <= 128 && NA <= 64, "entry layout: 7 bits of atom; one lane per atom at set-up");
+  __shared__ __align__(16) uint8_t stg[2][kT2StageBytes];
+  __shared__ uint32_t cand[kWaves][kT2Cap];   // atom | tile << 7 | quarter << 13 | output mask << 16
+  __shared__ uint32_t surv[kWaves][kT2Surv];  // atom | octad << 7 | (bucket - 0x4000) << 17
+  __shared__ __align__(16) uint32_t xw[kWaves][NA][12];  // the atoms' bf16 coordinates (pairs)
+  __shared__ uint32_t st_m[kWaves][NA], st_r[kWaves][NA];
+  __shared__ uint32_t st_o[kWaves][NA];  // the octad of the atom's 5 largest |x| (scored at set-up)
+  __shared__ uint32_t surv_n[kWaves];
+
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, q = lane >> 4, j = lane & 15;
+  const int64_t wave_atom0 = static_cast<int64_t>(blockIdx.x) * (kWaves * NA) + static_cast<int64_t>(wave) * NA;
+
+  if (lane == 0) surv_n[wave] = 0u;
+  bf16x8 b[AT];
+  float mg[AT], v1[AT];
+  uint32_t m1b[AT];  // the best type-1 bucket (0 below 2.0)
+#pragma unroll
+  for (int at = 0; at < AT; ++at) {
+    const int64_t a = wave_atom0 + at * 16 + j;
+    uint4 w = make_uint4(0u, 0u, 0u, 0u);
+    if (a < n_atoms && q < 3) w = xb[a * 3 + q];
+    if (q < 3) *reinterpret_cast<uint4 *>(&xw[wave][at * 16 + j][4 * q]) = w;
+    const uint4 wa = make_uint4(w.x & 0x7FFF7FFFu, w.y & 0x7FFF7FFFu, w.z & 0x7FFF7FFFu, w.w & 0x7FFF7FFFu);
+    b[at] = __builtin_bit_cast(bf16x8, wa);
+    // the two largest |x| and sum |x| over this lane's 8 coordinates, then over the atom's lanes
+    float t1 = 0.f, t2 = 0.f, ax = 0.f;
+    const uint32_t ww[4] = {wa.x, wa.y, wa.z, wa.w};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float v = __uint_as_float(e & 1 ? ww[e / 2] & 0xFFFF0000u : ww[e / 2] << 16);
+      t2 = fmaxf(t2, fminf(t1, v));
+      t1 = fmaxf(t1, v);
+      ax += v;
+    }
+#pragma unroll
+    for (int sh = 16; sh <= 32; sh <<= 1) {
+      const float o1 = __shfl_xor(t1, sh, 64), o2 = __shfl_xor(t2, sh, 64);
+      t2 = fmaxf(fmaxf(t2, o2), fminf(t1, o1));
+      t1 = fmaxf(t1, o1);
+      ax += __shfl_xor(ax, sh, 64);
+    }
+    const float s1 = t1 * kC1 + t2 * kC1;  // exact products, one rounding
+    const uint32_t bk = s1 > 0.f ? t3_bucket(s1) : 0u;
+    m1b[at] = bk >= 0x4000u ? bk : 0u;
+    v1[at] = t1;
+    // the margin for the MFMA's fp32 summation order of U
+    mg[at] = ax * kC2 * 0x1p-14f;
+  }
+  for (int i = lane; i < NA; i += 64) st_r[wave][i] = 0xFFFFFFFFu;
+#pragma unroll
+  for (int at = 0; at < AT; ++at)
+    if (q == 0) st_m[wave][at * 16 + j] = m1b[at];
+
+  const uint4 *gsrc = reinterpret_cast<const uint4 *>(t2_tiles);
+  auto stage_copy = [&](int g, int dst) {
+    const int stage = g % kT2Stages;
+#pragma unroll
+    for (int i = 0; i < (kT2StageVecs + kThreads - 1) / kThreads; ++i) {
+      if (i * kThreads + wave * 64 >= kT2StageVecs) break;  // (wave-uniform)
+      const uint4 *src = gsrc + static_cast<size_t>(stage) * kT2StageVecs + i * kThreads + tid;
+      uint8_t *d = stg[dst] + (i * kThreads + wave * 64) * 16;
+      __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)(src),
+                                       (__attribute__((address_space(3))) void *)(d), 16, 0, 0);
+    }
+  };
+
+  int cnt = 0;  // entries in this wave's candidate list (wave-uniform)
+  // One entry per lane.  pass 1: each flagged octad's best code -> st_m (atomic max), and the octad onto
+  // the survivor list when it is at or above the atom's running best; pass 2: the lowest row at st_m -> st_r.
+  auto flush = [&](int pass) {
+    for (int i = lane; i < cnt; i += 64) {
+      const uint32_t ce = cand[wave][i];
+      const int al = static_cast<int>(ce & 0x7Fu);
+      const uint32_t o0 = ((ce >> 7) & 0x3Fu) * kTileCodes + 4u * ((ce >> 13) & 3u);
+      const uint32_t mask = (ce >> 16) & 0xFu;
+      const uint32_t *xr = xw[wave][al];
+      const uint32_t M = pass == 2 ? st_m[wave][al] : 0u;
+      const uint32_t o5 = pass == 1 ? st_o[wave][al] : 0xFFFFFFFFu;
+      uint32_t rmin = 0xFFFFFFFFu;
+      for (uint32_t mk = mask; mk != 0u; mk &= mk - 1u) {
+        const uint32_t o = o0 + static_cast<uint32_t>(__builtin_ctz(mk));
+        // (padding slots: U = 0 unless the margin is not finite; the set-up octad: scored already)
+        if (o >= static_cast<uint32_t>(kT2Octads) || o == o5) continue;
+        float xa[8];
+        const uint32_t sg = t2_load(xr, t2_pos[o], xa);
+        if (pass == 1) {
+          const float S = t2_best(xa, sg);
+          const uint32_t bk = S > 0.f ? t3_bucket(S) : 0u;
+          if (bk >= 0x4000u) {
+            const uint32_t old = atomicMax(&st_m[wave][al], bk);
+            if (bk >= old) {
+              const uint32_t slot = atomicAdd(&surv_n[wave], 1u);
+              if (slot < static_cast<uint32_t>(kT2Surv))
+                surv[wave][slot] = static_cast<uint32_t>(al) | o << 7 | (bk - 0x4000u) << 17;
+            }
+          }
+        } else {
+          rmin = min(rmin, t2_rows_at(xa, sg, o, M, t2_rows));
+        }
+      }
+      if (pass == 2 && rmin != 0xFFFFFFFFu) atomicMin(&st_r[wave][al], rmin);
+    }
+    cnt = 0;
+  };
+
+  // Keep only the survivors at their atom's current best bucket (none is lost while the list has not
+  // overflowed; after an overflow pass 2 gives the rows).
+  auto compact = [&]() {
+    const uint32_t n = surv_n[wave];
+    if (n > static_cast<uint32_t>(kT2Surv)) return;
+    uint32_t w = 0u;
+    for (uint32_t base = 0u; base < n; base += 64u) {
+      const uint32_t i = base + static_cast<uint32_t>(lane);
+      uint32_t e = 0u;
+      bool keep = false;
+      if (i < n) {
+        e = surv[wave][i];
+        keep = (e >> 17) + 0x4000u == st_m[wave][e & 0x7Fu];
+      }
+      const uint64_t msk = __ballot(keep);
+      // (in place: every lane read its entry before any writes, and w + rank <= i)
+      if (keep)
+        surv[wave][w + __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(msk >> 32),
+                                                 __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(msk), 0u))] = e;
+      w += static_cast<uint32_t>(__popcll(msk));
+    }
+    if (lane == 0) surv_n[wave] = w;
+  };
+
+  // The threshold on U: an octad can reach bucket B only if U >= lo(B) - margin; no bucket below the
+  // floor (2.0, the best type-1 bucket, the best octad bucket found so far) can win.
+  float thr[AT];
+  auto set_thr = [&](int at, uint32_t mlow) {
+    mlow = max(mlow, 0x4000u);
+    thr[at] = __uint_as_float((mlow << 16) - 0x8000u) - mg[at];
+  };
+
+  const int a_off = (q < 3 ? q : 0) * 256 + j * 16;
+  stage_copy(0, 0);
+  __syncthreads();
+  // The floor from one octad per atom, one lane per atom: the octad holding its 5 largest |x| (every 5
+  // positions lie in exactly one octad), usually at or near the atom's best octad, scored exactly and
+  // entered like a swept candidate.
+  if (lane < NA) {
+    const int al = lane;
+    const uint16_t *xh = reinterpret_cast<const uint16_t *>(xw[wave][al]);
+    float tv[5] = {-1.f, -1.f, -1.f, -1.f, -1.f};
+    uint32_t tp[5] = {0u, 1u, 2u, 3u, 4u};
+    for (int i = 0; i < kDim; ++i) {  // insertion into the top 5 (descending), branch-free
+      float cv = __uint_as_float((static_cast<uint32_t>(xh[i]) & 0x7FFFu) << 16);
+      uint32_t cp = static_cast<uint32_t>(i);
+#pragma unroll
+      for (int k = 0; k < 5; ++k) {
+        const bool sw = cv > tv[k];
+        const float t = tv[k];
+        const uint32_t u = tp[k];
+        tv[k] = sw ? cv : t;
+        tp[k] = sw ? cp : u;
+        cv = sw ? t : cv;
+        cp = sw ? u : cp;
+      }
+    }
+    // positions ascending (a 5-input sorting network), then the octad of that subset
+    constexpr int kNet[9][2] = {{0, 1}, {3, 4}, {2, 4}, {2, 3}, {0, 3}, {0, 2}, {1, 4}, {1, 3}, {1, 2}};
+#pragma unroll
+    for (int k = 0; k < 9; ++k) {
+      const uint32_t lo = min(tp[kNet[k][0]], tp[kNet[k][1]]), hi = max(tp[kNet[k][0]], tp[kNet[k][1]]);
+      tp[kNet[k][0]] = lo;
+      tp[kNet[k][1]] = hi;
+    }
+    // (a non-finite atom can leave a default position twice: clamp the rank into the table)
+    const uint32_t o = t2_steiner[min(subset5_rank(tp), static_cast<uint32_t>(kT2Subsets5 - 1))];
+    float xa[8];
+    const uint32_t sg = t2_load(xw[wave][al], t2_pos[o], xa);
+    const float S = t2_best(xa, sg);
+    const uint32_t bk = S > 0.f ? t3_bucket(S) : 0u;
+    st_o[wave][al] = o;
+    if (bk >= 0x4000u && bk >= st_m[wave][al]) {
+      st_m[wave][al] = bk;
+      const uint32_t slot = atomicAdd(&surv_n[wave], 1u);
+      if (slot < static_cast<uint32_t>(kT2Surv)) surv[wave][slot] = static_cast<uint32_t>(al) | o << 7 | (bk - 0x4000u) << 17;
+    }
+  }
+#pragma unroll
+  for (int at = 0; at < AT; ++at) set_thr(at, st_m[wave][at * 16 + j]);
+  int g_end = kT2Stages;
+  for (int g = 0; g < g_end; ++g) {
+    const int pass = 1 + g / kT2Stages, buf = g & 1;
+    if (g + 1 < g_end) stage_copy(g + 1, buf ^ 1);
+    if (g == kT2Stages) {
+#pragma unroll
+      for (int at = 0; at < AT; ++at) {
+        const uint32_t M = st_m[wave][at * 16 + j];
+        thr[at] = M >= 0x4000u ? __uint_as_float((M << 16) - 0x8000u) - mg[at] : __builtin_inff();
+      }
+    }
+    const uint8_t *L = stg[buf] + a_off;
+    const int tile0 = (g % kT2Stages) * kT2ST;
+    for (int k = 0; k < kT2ST; ++k) {
+      const bf16x8 a = *reinterpret_cast<const bf16x8 *>(L + k * kTileBytes);
+      f32x4 c[AT];
+#pragma unroll
+      for (int at = 0; at < AT; ++at)
+        c[at] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b[at], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+#pragma unroll
+      for (int at = 0; at < AT; ++at) {
+        const float m4 = fmaxf(fmaxf(c[at][0], c[at][1]), fmaxf(c[at][2], c[at][3]));
+        const bool hit = m4 >= thr[at];
+        const uint64_t msk = __ballot(hit);
+        if (msk == 0ull) continue;
+        if (cnt > kT2Cap - 64) flush(pass);
+        if (hit) {
+          const float T = thr[at];
+          const uint32_t mask = (c[at][0] >= T ? 1u : 0u) | (c[at][1] >= T ? 2u : 0u) | (c[at][2] >= T ? 4u : 0u) |
+                                (c[at][3] >= T ? 8u : 0u);
+          const uint32_t pos = static_cast<uint32_t>(cnt) +
+                               __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(msk >> 32),
+                                                         __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(msk), 0u));
+          cand[wave][pos] = static_cast<uint32_t>(at * 16 + j) | static_cast<uint32_t>(tile0 + k) << 7 |
+                            static_cast<uint32_t>(q) << 13 | mask << 16;
+        }
+        cnt += __popcll(msk);
+      }
+    }
+    if (cnt > 0) flush(pass);
+    if (pass == 1) {
+      compact();
+#pragma unroll
+      for (int at = 0; at < AT; ++at) set_thr(at, st_m[wave][at * 16 + j]);
+    }
+    if (g == kT2Stages - 1) {
+      if (__syncthreads_or(rows_by_sweep != 0 || surv_n[wave] > static_cast<uint32_t>(kT2Surv))) {
+        g_end = 2 * kT2Stages;
+        stage_copy(g + 1, buf ^ 1);  // buffer buf ^ 1 was last read in stage g - 1, before the barrier
+        __syncthreads();
+      }
+    } else {
+      __syncthreads();
+    }
+  }
+  if (g_end == kT2Stages) {
+    // the survivors are the octads at their atom's final best bucket (compacted at the last stage end)
+    const int ns = static_cast<int>(surv_n[wave]);
+    for (int i = lane; i < ns; i += 64) {
+      const uint32_t se = surv[wave][i];
+      const int al = static_cast<int>(se & 0x7Fu);
+      const uint32_t o = (se >> 7) & 0x3FFu;
+      float xa[8];
+      const uint32_t sg = t2_load(xw[wave][al], t2_pos[o], xa);
+      const uint32_t r = t2_rows_at(xa, sg, o, st_m[wave][al], t2_rows);
+      if (r != 0xFFFFFFFFu) atomicMin(&st_r[wave][al], r);
+    }
+  }
+  __syncthreads();  // (block-uniform: g_end is)
+  if (q == 0) {
+#pragma unroll
+    for (int at = 0; at < AT; ++at) {
+      const int64_t a = wave_atom0 + at * 16 + j;
+      if (a >= n_atoms) continue;
+      const uint32_t M = st_m[wave][at * 16 + j];
+      uint32_t r = st_r[wave][at * 16 + j];
+      if (M >= 0x4000u && m1b[at] == M) r = min(r, t1_rows_at(xw[wave][at * 16 + j], v1[at], M, t1_rows));
+      reinterpret_cast<uint2 *>(&keys[a])[1] =
+          M >= 0x4000u && r != 0xFFFFFFFFu ? make_uint2(M << 16, r) : make_uint2(0u, 0u);
+    }
+  }
+}
+
 // Resolve: per block 256 atoms.
 //   scan     thread per atom: its keys (type-3 region; pair region: NN-B the
 //            first and the last group at the best bucket, NN-T / NN-P the
@@ -864,9 +1287,28 @@ struct RsScore {  // per-candidate / per-atom running result
 // Sweep position (global, code granularity) of lane qq's code e in tile t of group g.
 __device__ __forceinline__ int sweep_pos(int g, int t, int qq, int e) { return (g * kG + t) * kTileCodes + 4 * qq + e; }
 
-// T3S (NN-B): the type-3 key is t3_kernel's (best bucket << 16, lowest row at
-// it) instead of the dense sweep's group key, so no type-3 group is rescanned.
-template <int MODE, bool FUSED, bool T3S = false>
+// The 256 indices of a block (ids, in LDS) as packed 9-byte groups of 4 atoms at packed_out (bytes: LDS
+// staging of 64 groups); every thread of the block calls it.
+__device__ __forceinline__ void store_packed_block(const int32_t *ids, uint8_t *bytes, int64_t a0, int64_t n_atoms,
+                                                   uint8_t *__restrict__ packed_out, int tid) {
+  const int64_t n_groups = (n_atoms + 3) / 4;
+  const int64_t g0 = a0 / 4;
+  const int64_t groups_here = min(static_cast<int64_t>(64), n_groups - g0);
+  if (tid < groups_here) {
+    const int i = tid * 4;
+    group_to_bytes(ids[i], ids[i + 1], ids[i + 2], ids[i + 3], bytes + tid * 9);
+  }
+  __syncthreads();
+  uint8_t *dst = packed_out + g0 * 9;
+  if (groups_here == 64 && aligned16(packed_out)) {
+    if (tid < 36) reinterpret_cast<uint4 *>(dst)[tid] = reinterpret_cast<const uint4 *>(bytes)[tid];
+  } else {
+    const int nb = static_cast<int>(groups_here * 9);
+    for (int i = tid; i < nb; i += 256) dst[i] = bytes[i];
+  }
+}
+
+template <int MODE, bool FUSED>
 __global__ __launch_bounds__(256) void resolve_kernel(const uint4 *__restrict__ keys, int64_t n_atoms,
                                                       const float *__restrict__ src,
                                                       const float *__restrict__ sigma, int64_t atoms_per_row,
@@ -913,7 +1355,6 @@ __global__ __launch_bounds__(256) void resolve_kernel(const uint4 *__restrict__ 
   // first group at the best |score| in [1]
   uint32_t M = 0, grp[5] = {0u, 0u, 0u, 0u, 0u}, lanes[5] = {0u, 0u, 0u, 0u, 0u};
   uint32_t span_g0 = 0, span_g1 = 0;  // NN-B: pair groups (span_g0, span_g1] to rescan for positive hits
-  uint32_t t3row = kNone;             // T3S: the lowest type-3 row at the best bucket
   bool many = false;
   bool active = false;
   if (a < n_atoms) {
@@ -940,12 +1381,8 @@ __global__ __launch_bounds__(256) void resolve_kernel(const uint4 *__restrict__ 
       many |= n_at > 2;  // a record between the two: its groups are not candidates
       M = max(MT, MP);
       if (M != 0u && MT == M) {
-        if constexpr (T3S) {
-          t3row = k.y;
-        } else {
-          grp[0] = 0x3FFu - ((k.x >> 6) & 0x3FFu);
-          lanes[0] = (k.x >> 2) & 0xFu;
-        }
+        grp[0] = 0x3FFu - ((k.x >> 6) & 0x3FFu);
+        lanes[0] = (k.x >> 2) & 0xFu;
       }
       if (M != 0u && MP == M) {
         const uint64_t rr[2] = {rF, rL};
@@ -998,12 +1435,12 @@ __global__ __launch_bounds__(256) void resolve_kernel(const uint4 *__restrict__ 
     }
     // NN-P's origin rule (pack.py:174): |x|_2 < fp32(1e-8); no scan needed
     const bool p_snap = MODE == kModeP && sqrt(nrm2) < static_cast<double>(__uint_as_float(kEpsBits));
-    active = M != 0u && ((lanes[0] | lanes[1] | lanes[2] | lanes[3] | lanes[4]) != 0u || t3row != kNone) && !p_snap;
+    active = M != 0u && (lanes[0] | lanes[1] | lanes[2] | lanes[3] | lanes[4]) != 0u && !p_snap;
   }
   Ms[tid] = M;
 
   // per-atom merge state
-  uint32_t fT = t3row, fPpos = kNone, fPneg = kNone;  // NN-B
+  uint32_t fT = kNone, fPpos = kNone, fPneg = kNone;  // NN-B
   bool pos_first = false;  // NN-B: a positive hit in the earliest pair group (then the lowest pair row is known)
   score_t best_v = -__builtin_inf();
   uint32_t best_code = kNone;
@@ -1280,7 +1717,7 @@ __global__ __launch_bounds__(256) void resolve_kernel(const uint4 *__restrict__ 
       const uint32_t found = min(fT, fS);
       const uint32_t bucket = found != kNone ? M : (__float_as_uint(static_cast<float>(best_v)) >> 16);
       row = found != kNone ? found : best_code;
-      // bf16 max below 2.0 (a row found at bucket M needs no rescanned score: T3S type-3 rows have none)
+      // bf16 max below 2.0
       snap = (found == kNone && !(best_v > 0.f)) || bucket < 0x4000u;
     } else {
       row = best_code;
@@ -1292,21 +1729,36 @@ __global__ __launch_bounds__(256) void resolve_kernel(const uint4 *__restrict__ 
   if (!packed_out) return;
   ids[tid] = id;
   __syncthreads();
-  const int64_t n_groups = (n_atoms + 3) / 4;
-  const int64_t g0 = a0 / 4;
-  const int64_t groups_here = min(static_cast<int64_t>(64), n_groups - g0);
-  if (tid < groups_here) {
-    const int i = tid * 4;
-    group_to_bytes(ids[i], ids[i + 1], ids[i + 2], ids[i + 3], bytes + tid * 9);
+  store_packed_block(ids, bytes, a0, n_atoms, packed_out, tid);
+}
+
+// NN-B with the structured scorers: the higher of the pair key (t12_kernel)
+// and the type-3 key (t3_kernel), the lower row on equal buckets, the origin
+// when neither reaches 2.0; then the int32 index and, optionally, the packed
+// 9-byte groups.
+__global__ __launch_bounds__(256) void pick_kernel(const uint4 *__restrict__ keys, int64_t n_atoms,
+                                                   int32_t *__restrict__ idx_out, uint8_t *__restrict__ packed_out) {
+  __shared__ int32_t ids[256];
+  __shared__ __align__(16) uint8_t bytes[64 * 9];
+  const int tid = threadIdx.x;
+  const int64_t a0 = static_cast<int64_t>(blockIdx.x) * 256;
+  const int64_t a = a0 + tid;
+  int32_t id = 0;
+  if (a < n_atoms) {
+    const uint4 k = keys[a];
+    const uint32_t M3 = k.x >> 16, M2 = k.z >> 16, M = max(M2, M3);
+    uint32_t row = kNone;
+    if (M >= 0x4000u) {
+      if (M3 == M) row = k.y;
+      if (M2 == M) row = min(row, k.w);
+    }
+    id = row == kNone ? 0 : static_cast<int32_t>(row);
+    if (idx_out) idx_out[a] = id;
   }
+  if (!packed_out) return;
+  ids[tid] = id;
   __syncthreads();
-  uint8_t *dst = packed_out + g0 * 9;
-  if (groups_here == 64 && aligned16(packed_out)) {
-    if (tid < 36) reinterpret_cast<uint4 *>(dst)[tid] = reinterpret_cast<const uint4 *>(bytes)[tid];
-  } else {
-    const int nb = static_cast<int>(groups_here * 9);
-    for (int i = tid; i < nb; i += 256) dst[i] = bytes[i];
-  }
+  store_packed_block(ids, bytes, a0, n_atoms, packed_out, tid);
 }
 
 // out[a*24 + c] = value(codebook[idx[a]][c]); SCALE: (v * sigma[row]) * fp32(1/sqrt 2).
@@ -1357,29 +1809,25 @@ int choose_slices(int64_t ablocks) {
 static_assert(kSweepTiles % (32 * kST) == 0, "every slice count holds whole stages");
 static_assert(kType3Tiles % kST == 0, "the pair region starts on a stage boundary");
 
-// per-atom key slots: 16 bytes (NN-B: the type-3 key; NN-T / NN-P: type-3
-// and pair keys of 64 bits)
+// per-atom key slots: 16 bytes (NN-B dense sweep: the type-3 key; NN-B
+// structured: the type-3 key (t3_kernel), then the pair key (t12_kernel);
+// NN-T / NN-P: type-3 and pair keys of 64 bits)
 size_t keys_bytes(int64_t n_atoms) { return (static_cast<size_t>(n_atoms) * 16 + 255) & ~static_cast<size_t>(255); }
 
 // First slice holding pair tiles, for a launch of n_slices slices.
 int first_pair_slice(int n_slices) { return kType3Tiles / (kSweepTiles / n_slices); }
 
-// NN-B pair records: 8 bytes per (atom, slice holding pair tiles) -- every
-// slice when the structured type-3 scorer runs (the sweep then covers the
-// pair region only), which is the larger of the two layouts
+// NN-B pair records of the dense sweep: 8 bytes per (atom, slice holding pair
+// tiles), sized for every slice
 size_t recs_bytes(int64_t n_atoms) {
   const int64_t ablocks = (n_atoms + kAtomsPerBlock - 1) / kAtomsPerBlock;
   const int n_slices = choose_slices(ablocks);
   return (static_cast<size_t>(n_atoms) * static_cast<size_t>(n_slices) * 8 + 255) & ~static_cast<size_t>(255);
 }
 
-// The pair region of the sweep: tiles [kType3Tiles, kSweepTiles), whole stages for every slice count.
-constexpr int kPairSweepTiles = kSweepTiles - kType3Tiles;  // 3,072
-static_assert(kPairSweepTiles % (32 * kST) == 0, "every slice count holds whole pair stages");
-
 // t3_kernel: atom tiles per wave by launch size, so small launches still fill the chip.
-int t3_launch(const uint4 *xb, int64_t n_atoms, const DeviceTables *tab, const uint64_t *recs, int n_recs,
-              uint4 *keys, hipStream_t s, int rows_by_sweep) {
+int t3_launch(const uint4 *xb, int64_t n_atoms, const DeviceTables *tab, uint4 *keys, hipStream_t s,
+              int rows_by_sweep) {
   // 4 atom tiles per wave from 131,072 atoms: 39 KB of LDS (8-tile stages) and 128 VGPRs, 4 blocks (16
   // waves) per CU.  The evaluation is latency-bound, so occupancy decides: on the config-4 launch 8 tiles
   // per wave at 2 blocks per CU measured 14.9 ms, 4 tiles at 3 blocks (16-tile stages) 12.5, 4 tiles at 4
@@ -1393,33 +1841,66 @@ int t3_launch(const uint4 *xb, int64_t n_atoms, const DeviceTables *tab, const u
   profile_before(s, PLX_PROF_T3);
   if (AT == 4)
     hipLaunchKernelGGL(t3_kernel<4>, g, dim3(kThreads), 0, s, xb, n_atoms, tab->t3_tiles, tab->t3_words, tab->t3_rows,
-                       recs, n_recs, keys, rows_by_sweep);
+                       keys, rows_by_sweep);
   else if (AT == 2)
     hipLaunchKernelGGL(t3_kernel<2>, g, dim3(kThreads), 0, s, xb, n_atoms, tab->t3_tiles, tab->t3_words, tab->t3_rows,
-                       recs, n_recs, keys, rows_by_sweep);
+                       keys, rows_by_sweep);
   else
     hipLaunchKernelGGL(t3_kernel<1>, g, dim3(kThreads), 0, s, xb, n_atoms, tab->t3_tiles, tab->t3_words, tab->t3_rows,
-                       recs, n_recs, keys, rows_by_sweep);
+                       keys, rows_by_sweep);
   profile_after(s, PLX_PROF_T3);
   return check_launch("t3_kernel");
 }
 
+// t12_kernel: atom tiles per wave by launch size, as t3_kernel (37 KB of LDS at 4 tiles per wave).
+int t12_launch(const uint4 *xb, int64_t n_atoms, const DeviceTables *tab, uint4 *keys, hipStream_t s,
+               int rows_by_sweep) {
+  const int AT = n_atoms >= 131072 ? 4 : n_atoms >= 32768 ? 2 : 1;
+  const int64_t per_block = static_cast<int64_t>(kWaves) * AT * 16;
+  const int64_t blocks = (n_atoms + per_block - 1) / per_block;
+  if (blocks > 0x7FFFFFFFll) return fail(PLX_EINVAL, "quantize: %lld atoms exceed one launch", static_cast<long long>(n_atoms));
+  const dim3 g(static_cast<unsigned>(blocks));
+  profile_before(s, PLX_PROF_T12);
+  if (AT == 4)
+    hipLaunchKernelGGL(t12_kernel<4>, g, dim3(kThreads), 0, s, xb, n_atoms, tab->t2_tiles, tab->t2_pos, tab->t2_rows,
+                       tab->t1_rows, tab->t2_steiner, keys, rows_by_sweep);
+  else if (AT == 2)
+    hipLaunchKernelGGL(t12_kernel<2>, g, dim3(kThreads), 0, s, xb, n_atoms, tab->t2_tiles, tab->t2_pos, tab->t2_rows,
+                       tab->t1_rows, tab->t2_steiner, keys, rows_by_sweep);
+  else
+    hipLaunchKernelGGL(t12_kernel<1>, g, dim3(kThreads), 0, s, xb, n_atoms, tab->t2_tiles, tab->t2_pos, tab->t2_rows,
+                       tab->t1_rows, tab->t2_steiner, keys, rows_by_sweep);
+  profile_after(s, PLX_PROF_T12);
+  return check_launch("t12_kernel");
+}
+
+// The structured NN-B path after prep_kernel: t12_kernel (types 1-2), t3_kernel (type 3), pick_kernel.
+int structured_launch(const uint4 *xb, int64_t n_atoms, const DeviceTables *tab, uint4 *keys, int32_t *idx_out,
+                      uint8_t *packed_out, hipStream_t s, int rows_by_sweep) {
+  int st;
+  if ((st = t12_launch(xb, n_atoms, tab, keys, s, rows_by_sweep)) != PLX_OK) return st;
+  if ((st = t3_launch(xb, n_atoms, tab, keys, s, rows_by_sweep)) != PLX_OK) return st;
+  hipLaunchKernelGGL(pick_kernel, dim3(static_cast<unsigned>((n_atoms + 255) / 256)), dim3(256), 0, s, keys, n_atoms,
+                     idx_out, packed_out);
+  return check_launch("pick_kernel");
+}
+
 // workspace = per-atom keys, the NN-B pair records, then (NN-B / NN-T) the bf16 planes.
-// T3S (NN-B): the sweep covers the pair region only and t3_kernel scores the
-// type-3 codes; otherwise every sweep code is scored densely.
-template <int MODE, bool FUSED, bool T3S = false>
+// STRUCT (NN-B): the structured scorers (t12_kernel, t3_kernel, pick_kernel);
+// otherwise every sweep code is scored densely (nn_kernel, resolve_kernel).
+template <int MODE, bool FUSED, bool STRUCT = false>
 int launch_mode(const float *x, const float *sigma, int64_t apr, int64_t n_atoms, const DeviceTables *tab,
                 int32_t *idx_out, uint8_t *packed_out, uint8_t *workspace, hipStream_t s, int rows_by_sweep = 0) {
-  static_assert(!T3S || MODE == kModeB, "the structured type-3 scorer has NN-B semantics");
+  static_assert(!STRUCT || MODE == kModeB, "the structured scorers have NN-B semantics");
   const int64_t ablocks = (n_atoms + kAtomsPerBlock - 1) / kAtomsPerBlock;
   const int n_slices = choose_slices(ablocks);
-  const int tiles_per_slice = (T3S ? kPairSweepTiles : kSweepTiles) / n_slices;
+  const int tiles_per_slice = kSweepTiles / n_slices;
   const int64_t grid = ablocks * n_slices;
   if (grid > 0x7FFFFFFFll) return fail(PLX_EINVAL, "quantize: %lld atoms exceed one launch", static_cast<long long>(n_atoms));
   uint4 *keys = reinterpret_cast<uint4 *>(workspace);
   uint64_t *recs = reinterpret_cast<uint64_t *>(workspace + keys_bytes(n_atoms));
   uint4 *xb = reinterpret_cast<uint4 *>(workspace + keys_bytes(n_atoms) + recs_bytes(n_atoms));
-  const int s0 = T3S ? 0 : first_pair_slice(n_slices);
+  const int s0 = first_pair_slice(n_slices);
   int st;
   if (MODE != kModeP) {
     hipLaunchKernelGGL((prep_kernel<FUSED>), dim3(static_cast<unsigned>((n_atoms * 3 + 255) / 256)), dim3(256), 0, s, x,
@@ -1430,17 +1911,15 @@ int launch_mode(const float *x, const float *sigma, int64_t apr, int64_t n_atoms
                        n_atoms);
     if ((st = check_launch("clear_keys_kernel")) != PLX_OK) return st;
   }
+  if constexpr (STRUCT) return structured_launch(xb, n_atoms, tab, keys, idx_out, packed_out, s, rows_by_sweep);
   profile_before(s);
   const uint8_t *tiles = MODE == kModeP ? tab->sw_raw_tiles : tab->sw_bf16_tiles;
   const void *operand = MODE == kModeP ? static_cast<const void *>(x) : static_cast<const void *>(xb);
   hipLaunchKernelGGL((nn_kernel<MODE>), dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0, s, operand, n_atoms, tiles,
-                     n_slices, tiles_per_slice, keys, recs, s0, T3S ? kType3Tiles : 0);
+                     n_slices, tiles_per_slice, keys, recs, s0);
   if ((st = check_launch("nn_kernel")) != PLX_OK) return st;
   profile_after(s);
-  if constexpr (T3S) {
-    if ((st = t3_launch(xb, n_atoms, tab, recs, n_slices, keys, s, rows_by_sweep)) != PLX_OK) return st;
-  }
-  hipLaunchKernelGGL((resolve_kernel<MODE, FUSED, T3S>), dim3(static_cast<unsigned>((n_atoms + 255) / 256)), dim3(256), 0, s,
+  hipLaunchKernelGGL((resolve_kernel<MODE, FUSED>), dim3(static_cast<unsigned>((n_atoms + 255) / 256)), dim3(256), 0, s,
                      keys, n_atoms, x, sigma, apr, xb, tab->sw_dq, tab->sw_idx, tab->sw_anti, tab->cb_raw,
                      tab->sw_bf16_tiles, static_cast<const uint64_t *>(recs), n_slices - s0, n_atoms, idx_out,
                      packed_out);
@@ -1508,26 +1987,28 @@ int launch_quantize(const float *x, const float *sigma, int64_t rows, int64_t co
 
 namespace {
 
-// Several latents in one scoring sweep: row scale and operand planes per
-// matrix, one nn_kernel launch over all their atoms (fewer codebook slices per
-// atom block and no per-matrix tail of the grid), then per matrix the resolve
-// (index + pack) and the scaled gather of the reconstructed weight.
-template <int MODE, bool T3S = false>
+// Several latents in one scoring pass: row scale and operand planes per
+// matrix, one launch of the scorers over all their atoms (STRUCT: t12_kernel
+// and t3_kernel; otherwise nn_kernel with fewer codebook slices per atom
+// block; no per-matrix tail of the grid either way), then per matrix the
+// index + pack (pick_kernel / resolve_kernel) and the scaled gather of the
+// reconstructed weight.
+template <int MODE, bool STRUCT = false>
 int launch_batch_mode(const RequantItem *items, int n_items, const DeviceTables *tab, uint8_t *workspace,
                       hipStream_t s) {
-  static_assert(!T3S || MODE == kModeB, "the structured type-3 scorer has NN-B semantics");
+  static_assert(!STRUCT || MODE == kModeB, "the structured scorers have NN-B semantics");
   int64_t total = 0;
   for (int i = 0; i < n_items; ++i) total += items[i].rows * (items[i].cols / kDim);
   if (total == 0) return PLX_OK;
   const int64_t ablocks = (total + kAtomsPerBlock - 1) / kAtomsPerBlock;
   const int n_slices = choose_slices(ablocks);
-  const int tiles_per_slice = (T3S ? kPairSweepTiles : kSweepTiles) / n_slices;
+  const int tiles_per_slice = kSweepTiles / n_slices;
   const int64_t grid = ablocks * n_slices;
   if (grid > 0x7FFFFFFFll) return fail(PLX_EINVAL, "requantize_batch: %lld atoms exceed one launch", static_cast<long long>(total));
   uint4 *keys = reinterpret_cast<uint4 *>(workspace);
   uint64_t *recs = reinterpret_cast<uint64_t *>(workspace + keys_bytes(total));
   uint4 *xb = reinterpret_cast<uint4 *>(workspace + keys_bytes(total) + recs_bytes(total));
-  const int s0 = T3S ? 0 : first_pair_slice(n_slices);
+  const int s0 = first_pair_slice(n_slices);
   int st;
   int64_t off = 0;
   for (int i = 0; i < n_items; ++i) {
@@ -1540,25 +2021,33 @@ int launch_batch_mode(const RequantItem *items, int n_items, const DeviceTables 
     if ((st = check_launch("prep_kernel")) != PLX_OK) return st;
     off += n;
   }
-  profile_before(s);
-  hipLaunchKernelGGL((nn_kernel<MODE>), dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0, s,
-                     static_cast<const void *>(xb), total, tab->sw_bf16_tiles, n_slices, tiles_per_slice, keys, recs, s0,
-                     T3S ? kType3Tiles : 0);
-  if ((st = check_launch("nn_kernel")) != PLX_OK) return st;
-  profile_after(s);
-  if constexpr (T3S) {
-    if ((st = t3_launch(xb, total, tab, recs, n_slices, keys, s, 0)) != PLX_OK) return st;
+  if constexpr (STRUCT) {
+    if ((st = t12_launch(xb, total, tab, keys, s, 0)) != PLX_OK) return st;
+    if ((st = t3_launch(xb, total, tab, keys, s, 0)) != PLX_OK) return st;
+  } else {
+    profile_before(s);
+    hipLaunchKernelGGL((nn_kernel<MODE>), dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0, s,
+                       static_cast<const void *>(xb), total, tab->sw_bf16_tiles, n_slices, tiles_per_slice, keys, recs,
+                       s0);
+    if ((st = check_launch("nn_kernel")) != PLX_OK) return st;
+    profile_after(s);
   }
   off = 0;
   for (int i = 0; i < n_items; ++i) {
     const RequantItem &it = items[i];
     const int64_t apr = it.cols / kDim, n = it.rows * apr;
     if (n == 0) continue;
-    hipLaunchKernelGGL((resolve_kernel<MODE, true, T3S>), dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s,
-                       keys + off, n, it.latent, it.sigma, apr, xb + off * 3, tab->sw_dq, tab->sw_idx, tab->sw_anti,
-                       tab->cb_raw, tab->sw_bf16_tiles, static_cast<const uint64_t *>(recs + off), n_slices - s0, total,
-                       it.idx, it.packed);
-    if ((st = check_launch("resolve_kernel")) != PLX_OK) return st;
+    if constexpr (STRUCT) {
+      hipLaunchKernelGGL(pick_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s, keys + off, n,
+                         it.idx, it.packed);
+      if ((st = check_launch("pick_kernel")) != PLX_OK) return st;
+    } else {
+      hipLaunchKernelGGL((resolve_kernel<MODE, true>), dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s,
+                         keys + off, n, it.latent, it.sigma, apr, xb + off * 3, tab->sw_dq, tab->sw_idx, tab->sw_anti,
+                         tab->cb_raw, tab->sw_bf16_tiles, static_cast<const uint64_t *>(recs + off), n_slices - s0,
+                         total, it.idx, it.packed);
+      if ((st = check_launch("resolve_kernel")) != PLX_OK) return st;
+    }
     if (it.weight) {
       hipLaunchKernelGGL((gather_kernel<0, true>), dim3(static_cast<unsigned>((n * 6 + 255) / 256)), dim3(256), 0, s,
                          it.idx, n, tab->cb_raw, it.sigma, apr, static_cast<void *>(it.weight));
@@ -1605,8 +2094,8 @@ int launch_requantize_batch(const RequantItem *items, int n_items, int mode, voi
 // needs nothing from the previous one, but calls that overlap on one device
 // (different streams at once) race on it.
 static_assert(PLX_NOALLOC_MAX_ATOMS > 0, "maximum atoms of the allocation-free entry point");
-// (at 2^20 atoms a launch uses 8 slices, each holding pair tiles: 16 B of
-// keys + 8 x 8 B of pair records + 48 B of operand planes per atom, the
+// (at 2^20 atoms a launch uses 8 slices, with pair-record slots for each: 16 B
+// of keys + 8 x 8 B of pair records + 48 B of operand planes per atom, the
 // largest workspace of any size up to the maximum, plus the 256-byte rounding
 // of its three parts; checked on every call)
 constexpr size_t kScratchBytes = static_cast<size_t>(PLX_NOALLOC_MAX_ATOMS) * (16 + 8 * 8 + 48) + 1024;

@@ -47,6 +47,21 @@
 //                complements (16,384 B);
 // t3_rows        the codebook row of the type-3 code with pattern id r and its
 //                -3 at position p, [4096][24] (393,216 B).
+// t2_tiles       the structured pair scorer's MFMA A operands: the 759 octads
+//                (ascending masks) with bf16(2s) = 0.70703125 on their 8
+//                positions, in the sweep tiles' layout (48 tiles, the last 9
+//                slots zero; 36,864 B);
+// t2_pos         each octad's 8 positions, ascending, one byte each (6,144 B);
+// t2_rows        the codebook row of the type-2 code on octad o whose minus
+//                signs on the octad's positions k = 0..6 (ascending) are the
+//                bits of p (the eighth sign: even parity), [759][128]
+//                (388,608 B);
+// t1_rows        the codebook row of the type-1 code with +-4 at positions
+//                i < j, [24][24][4] by minus at i | minus at j << 1 (9,216 B);
+// t2_steiner     the octad holding each 5-subset of the 24 positions (every
+//                5 positions lie in exactly one octad), by the subset's colex
+//                rank C(p0,1) + C(p1,2) + ... + C(p4,5), p0 < ... < p4
+//                (42,504 entries, 85,008 B).
 
 #include <algorithm>
 #include <cstring>
@@ -202,6 +217,87 @@ int build(int dev, DeviceTables *t) {
       t3rows[static_cast<size_t>(id) * kDim + pp] = it->second;
     }
 
+  // structured pair tables: the octads (from the type-2 rows' supports), their
+  // tiles and positions, and the row of every type-2 and type-1 code
+  std::vector<uint32_t> oct_masks;
+  for (int code = 1; code < kCodebook; ++code) {
+    const int8_t *r = raw + static_cast<size_t>(code) * kDim;
+    uint32_t m = 0;
+    int nz = 0;
+    for (int c = 0; c < kDim; ++c)
+      if (r[c] != 0) {
+        m |= 1u << c;
+        ++nz;
+      }
+    if (nz == 8) oct_masks.push_back(m);
+  }
+  std::sort(oct_masks.begin(), oct_masks.end());
+  oct_masks.erase(std::unique(oct_masks.begin(), oct_masks.end()), oct_masks.end());
+  if (static_cast<int>(oct_masks.size()) != kT2Octads) return fail(PLX_EINVAL, "%zu octads", oct_masks.size());
+  std::vector<uint16_t> t2_tiles(static_cast<size_t>(kT2Tiles) * (kTileBytes / 2), 0);
+  std::vector<uint8_t> t2_pos(static_cast<size_t>(kT2Tiles) * kTileCodes * 8, 0);
+  std::vector<uint32_t> t2_rows(static_cast<size_t>(kT2Octads) * 128, 0);
+  std::vector<uint32_t> t1_rows(static_cast<size_t>(kDim) * kDim * 4, 0);
+  for (int o = 0; o < kT2Octads; ++o) {
+    int k = 0;
+    for (int c = 0; c < kDim; ++c)
+      if ((oct_masks[o] >> c) & 1u) {
+        t2_tiles[static_cast<size_t>(o / kTileCodes) * 384 + (c / 8) * 128 + (o % kTileCodes) * 8 + c % 8] = bf_of[2 + 4];
+        t2_pos[static_cast<size_t>(o) * 8 + k++] = static_cast<uint8_t>(c);
+      }
+  }
+  std::vector<uint16_t> t2_steiner(static_cast<size_t>(kT2Subsets5), 0xFFFFu);
+  {
+    auto binom = [](int n, int k) {
+      long v = 1;
+      for (int i = 0; i < k; ++i) v = v * (n - i) / (i + 1);
+      return n < k ? 0L : v;
+    };
+    for (int o = 0; o < kT2Octads; ++o) {
+      const uint8_t *pp = t2_pos.data() + static_cast<size_t>(o) * 8;
+      for (int m = 0; m < 256; ++m) {
+        if (__builtin_popcount(m) != 5) continue;
+        long rank = 0;
+        int k = 0;
+        for (int b = 0; b < 8; ++b)
+          if ((m >> b) & 1) rank += binom(pp[b], ++k);
+        if (t2_steiner[static_cast<size_t>(rank)] != 0xFFFFu) return fail(PLX_EINVAL, "5 positions in two octads");
+        t2_steiner[static_cast<size_t>(rank)] = static_cast<uint16_t>(o);
+      }
+    }
+    for (uint16_t v : t2_steiner)
+      if (v == 0xFFFFu) return fail(PLX_EINVAL, "5 positions in no octad");
+  }
+  int n_t2 = 0, n_t1 = 0;
+  for (int code = 1; code < kCodebook; ++code) {
+    const int8_t *r = raw + static_cast<size_t>(code) * kDim;
+    uint32_t m = 0, minus = 0;
+    int nz = 0, lo = -1, hi = -1;
+    for (int c = 0; c < kDim; ++c)
+      if (r[c] != 0) {
+        if (r[c] < 0) minus |= 1u << nz;
+        m |= 1u << c;
+        lo = lo < 0 ? c : lo;
+        hi = c;
+        ++nz;
+      }
+    if (nz == 8) {
+      const int o = static_cast<int>(std::lower_bound(oct_masks.begin(), oct_masks.end(), m) - oct_masks.begin());
+      if (o >= kT2Octads || oct_masks[o] != m || (__builtin_popcount(minus) & 1) != 0)
+        return fail(PLX_EINVAL, "codebook row %d is no even-sign octad code", code);
+      uint32_t &slot = t2_rows[static_cast<size_t>(o) * 128 + (minus & 0x7Fu)];
+      if (slot != 0) return fail(PLX_EINVAL, "two octad codes share a sign pattern (row %d)", code);
+      slot = static_cast<uint32_t>(code);
+      ++n_t2;
+    } else if (nz == 2) {
+      uint32_t &slot = t1_rows[(static_cast<size_t>(lo) * kDim + hi) * 4 + minus];
+      if (slot != 0) return fail(PLX_EINVAL, "two type-1 codes share positions and signs (row %d)", code);
+      slot = static_cast<uint32_t>(code);
+      ++n_t1;
+    }
+  }
+  if (n_t2 != kT2Octads * 128 || n_t1 != 276 * 4) return fail(PLX_EINVAL, "%d type-2 and %d type-1 rows", n_t2, n_t1);
+
   // dequant-linear entries: 24 signed 4-bit coordinates, then type | pos << 8
   std::vector<uint32_t> gemv(static_cast<size_t>(kCodebook) * 4, 0);
   std::vector<uint32_t> dq(static_cast<size_t>(kCodebook) * 3, 0);
@@ -260,7 +356,8 @@ int build(int dev, DeviceTables *t) {
 
   void *dt = nullptr, *drt = nullptr, *dsq = nullptr, *dsi = nullptr, *dsa = nullptr, *dr = nullptr, *dg = nullptr,
        *dd = nullptr, *dk = nullptr, *dpi = nullptr, *dcp = nullptr, *dpn = nullptr, *d3t = nullptr, *d3w = nullptr,
-       *d3r = nullptr, *dgv = nullptr;
+       *d3r = nullptr, *dgv = nullptr, *d2t = nullptr, *d2p = nullptr, *d2r = nullptr, *d1r = nullptr,
+       *d2s = nullptr;
   const PlaneTables *pt = plane_tables_host();
   if (!pt) return fail(PLX_EINVAL, "the codebook rows take more than %d distinct planes", kMaxPlanes);
   std::vector<uint32_t> pl_pad(pt->ids);  // whole 16-byte vectors (the kernels stage it by uint4)
@@ -300,6 +397,11 @@ int build(int dev, DeviceTables *t) {
       {t3_tiles.data(), t3_tiles.size() * 2, &d3t},
       {t3w.data(), t3w.size() * 4, &d3w},
       {t3rows.data(), t3rows.size() * 4, &d3r},
+      {t2_tiles.data(), t2_tiles.size() * 2, &d2t},
+      {t2_pos.data(), t2_pos.size(), &d2p},
+      {t2_rows.data(), t2_rows.size() * 4, &d2r},
+      {t1_rows.data(), t1_rows.size() * 4, &d1r},
+      {t2_steiner.data(), t2_steiner.size() * 2, &d2s},
   };
   int st = PLX_OK;
   for (const Upload &u : ups) {
@@ -332,6 +434,11 @@ int build(int dev, DeviceTables *t) {
   t->t3_tiles = static_cast<uint8_t *>(d3t);
   t->t3_words = static_cast<uint32_t *>(d3w);
   t->t3_rows = static_cast<uint32_t *>(d3r);
+  t->t2_tiles = static_cast<uint8_t *>(d2t);
+  t->t2_pos = static_cast<uint2 *>(d2p);
+  t->t2_rows = static_cast<uint32_t *>(d2r);
+  t->t1_rows = static_cast<uint32_t *>(d1r);
+  t->t2_steiner = static_cast<uint16_t *>(d2s);
   t->device = dev;
   return PLX_OK;
 }
