@@ -507,21 +507,30 @@ __global__ __launch_bounds__(kThreads, MODE == kModeB ? 3 : 2) void nn_kernel(co
 // i.e. S(w) - x_p * (alpha = 1.416015625 where w_p = 0, beta = 0.708984375
 // where w_p = 1); both products are exact in fp32 (8 x 8 significant bits).
 // The best code of a word is S(w) + bonus(w) with bonus(w) = max_p of
-// -x_p (alpha or beta) <= e1 = max_p max(-alpha x_p, -beta x_p).  The Golay
-// code holds the complement of every word, S(~w) = -S(w), so one MFMA per 16
-// representative words scores 32 words: 128 tiles instead of 6,144.
+// -x_p (alpha or beta).  With p* the position of the largest term
+// t_p = max(-alpha x_p, -beta x_p) and m2 the largest off p*, bonus(w) <=
+// e0 = max(-alpha x_p*, m2) when w has a 0 at p* and <= e1 = max(-beta x_p*,
+// m2) when it has a 1: e(w) = eb + kap P_p*(w) with eb, kap the mean and
+// half-difference of e0, e1.  The MFMA's B operand is the atom with x_p*
+// raised by kap / s, so it gives T(w) = S(w) + kap P_p*(w), and S(w) + e(w)
+// = T(w) + eb: a test on T bounds each word by its own bit at p* (about 5x
+// fewer candidates than one bound e1 = max_p t_p for all words).  The Golay
+// code holds the complement of every word, S(~w) = -S(w) and T(~w) = -T(w),
+// so one MFMA per 16 representative words tests 32 words: 128 tiles instead
+// of 6,144.
 // A block of 4 waves holds AT atom tiles of 16 atoms per wave as MFMA B
 // operands and streams the 128 pattern tiles through LDS once (a second time
 // only if a survivor list overflows):
 //   pass 1  every lane whose four outputs hold a word that could reach the
 //           lowest bucket still possible -- the best pair bucket (the pair
-//           key of t12_kernel), 2.0 (the origin rule) and the best type-3 bucket found
-//           so far, whichever is highest: |S| >= lo(bucket) - e1 - margin --
-//           appends one 4-byte entry (atom, tile, lane quarter, 4-bit mask of
+//           key of t12_kernel), 2.0 (the origin rule) and the best type-3
+//           bucket found so far, whichever is highest: |T| >= lo(bucket) - eb
+//           - margin -- appends one 4-byte entry (atom, tile, lane quarter, 4-bit mask of
 //           its outputs) to the wave's list in LDS; at every stage end (and
 //           when the list is full) the wave evaluates it, one entry per lane:
-//           each flagged representative and its complement get S recomputed
-//           from the atom's bf16 coordinates and their 24 positions scored,
+//           each flagged representative gets S recomputed from the atom's
+//           bf16 coordinates, and it and its complement, each when its S +
+//           e(w) reaches the floor, get their 24 positions scored,
 //           the best bucket M3 per atom is kept by an LDS atomic max, words
 //           at or above the running best go onto a survivor list, and the
 //           thresholds rise to the new best buckets;
@@ -540,7 +549,7 @@ constexpr int kT3ST = 8;                           // pattern tiles per LDS stag
 constexpr int kT3Stages = kT3Tiles / kT3ST;        // 8 per pass
 constexpr int kT3StageBytes = kT3ST * kTileBytes;  // 6,144
 constexpr int kT3StageVecs = kT3StageBytes / 16;   // 384
-constexpr int kT3Cap = 384;                        // candidate entries per wave (4 bytes each)
+constexpr int kT3Cap = 256;                        // candidate entries per wave (4 bytes each)
 constexpr int kT3Surv = 384;                       // survivor words per wave (4 bytes each)
 constexpr float kT3Alpha = 1.416015625f;           // bf16(3s) + bf16(s)
 constexpr float kT3Beta = 0.708984375f;            // bf16(3s) - bf16(s)
@@ -578,7 +587,10 @@ __global__ __launch_bounds__(kThreads, 4) void t3_kernel(const uint4 *__restrict
   __shared__ uint32_t surv[kWaves][kT3Surv];  // atom | pattern id << 7: words at or above the atom's running best
   __shared__ __align__(16) uint32_t xw[kWaves][NA][12];  // the atoms' bf16 coordinates (pairs)
   __shared__ uint32_t st_m[kWaves][NA], st_r[kWaves][NA];
-  __shared__ float st_t[kWaves][NA];  // the atom's threshold on S less its margin (which signs to evaluate)
+  __shared__ float st_t[kWaves][NA];    // lo(floor) less twice the margin: which signs of a word to evaluate
+  __shared__ float st_m2[kWaves][NA];   // the second largest position term (the largest off p*)
+  __shared__ float st_mg[kWaves][NA];   // the atom's margin for summation orders
+  __shared__ uint8_t st_p[kWaves][NA];  // p*, the position of the largest position term
   __shared__ uint32_t surv_n[kWaves];
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, q = lane >> 4, j = lane & 15;
@@ -586,34 +598,70 @@ __global__ __launch_bounds__(kThreads, 4) void t3_kernel(const uint4 *__restrict
 
   if (lane == 0) surv_n[wave] = 0u;
   bf16x8 b[AT];
-  float e1[AT], mg[AT];
+  float offs[AT];  // eb, the raised coordinate's rounding and the margin: thr = lo(floor) - offs
 #pragma unroll
   for (int at = 0; at < AT; ++at) {
     const int64_t a = wave_atom0 + at * 16 + j;
     uint4 w = make_uint4(0u, 0u, 0u, 0u);
     if (a < n_atoms && q < 3) w = xb[a * 3 + q];
-    b[at] = __builtin_bit_cast(bf16x8, w);
     if (q < 3) *reinterpret_cast<uint4 *>(&xw[wave][at * 16 + j][4 * q]) = w;
-    // e1 = the largest position term max_p max(-alpha x_p, -beta x_p), and sum |x_p| (s * sum |x| bounds
-    // every |S|), over this lane's 8 coordinates, then over the atom's 3 lanes
-    float hi = -__builtin_inff(), ax = 0.f;
+    // the position terms t_p = max(-alpha x_p, -beta x_p): the largest (at p*, x there: x1) and the second
+    // largest, and sum |x_p| (s * sum |x| bounds every |S|), over this lane's 8 coordinates, then over the
+    // atom's 3 lanes (ties: the lowest position, so every lane of the atom agrees on p*)
+    uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+    float m1 = -__builtin_inff(), m2 = -__builtin_inff(), x1 = 0.f, ax = 0.f;
+    uint32_t p1 = 0u;
     if (q < 3) {
-      const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const float x = __uint_as_float(e & 1 ? ww[e / 2] & 0xFFFF0000u : ww[e / 2] << 16);
-        hi = fmaxf(hi, fmaxf(-x * kT3Alpha, -x * kT3Beta));
+        const float t = fmaxf(-x * kT3Alpha, -x * kT3Beta);
+        const bool up = t > m1;
+        m2 = up ? m1 : fmaxf(m2, t);
+        m1 = up ? t : m1;
+        x1 = up ? x : x1;
+        p1 = up ? static_cast<uint32_t>(8 * q + e) : p1;
         ax += fabsf(x);
       }
     }
 #pragma unroll
     for (int sh = 16; sh <= 32; sh <<= 1) {
-      hi = fmaxf(hi, __shfl_xor(hi, sh, 64));
+      const float om1 = __shfl_xor(m1, sh, 64), om2 = __shfl_xor(m2, sh, 64), ox1 = __shfl_xor(x1, sh, 64);
+      const uint32_t op1 = static_cast<uint32_t>(__shfl_xor(static_cast<int>(p1), sh, 64));
+      const bool take = om1 > m1 || (om1 == m1 && op1 < p1);
+      m2 = take ? fmaxf(m1, om2) : fmaxf(m2, om1);
+      m1 = take ? om1 : m1;
+      x1 = take ? ox1 : x1;
+      p1 = take ? op1 : p1;
       ax += __shfl_xor(ax, sh, 64);
     }
-    e1[at] = hi;
-    // the margin for the MFMA's fp32 summation order of S and the score roundings
-    mg[at] = (ax * kT3S + fabsf(hi)) * 0x1p-14f;
+    // A word w with bit 0 at p* has bonus(w) <= e0 = max(-alpha x1, m2), with bit 1 <= e1 = max(-beta x1, m2):
+    // e(w) = eb + kap P_p*(w) (P = +1 for bit 0).  The MFMA with x_p* raised by kap / s gives
+    // T(w) = S(w) + kap P_p*(w) (and T(~w) = -T(w)), so |T| >= lo(floor) - eb - margins flags every word
+    // whose S(w) + e(w) reaches the floor; dl: what the bf16 rounding of the raised coordinate adds.
+    const float e0 = fmaxf(-x1 * kT3Alpha, m2), e1 = fmaxf(-x1 * kT3Beta, m2);
+    const float kap = (e0 - e1) * 0.5f;
+    float dl = 0.f;
+    if (q < 3 && (p1 >> 3) == static_cast<uint32_t>(q)) {
+      const uint32_t h = bf16_rne_bits(x1 + kap / kT3S);
+      dl = fabsf((bf16_bits_to_float(h) - x1) * kT3S - kap);
+      const uint32_t e = p1 & 7u;
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        if (static_cast<uint32_t>(k) == (e >> 1))
+          ww[k] = (e & 1u) ? (ww[k] & 0xFFFFu) | (h << 16) : (ww[k] & 0xFFFF0000u) | h;
+    }
+#pragma unroll
+    for (int sh = 16; sh <= 32; sh <<= 1) dl = fmaxf(dl, __shfl_xor(dl, sh, 64));
+    b[at] = __builtin_bit_cast(bf16x8, make_uint4(ww[0], ww[1], ww[2], ww[3]));
+    // the margin for the MFMA's fp32 summation order of T and the score roundings
+    const float mg = (ax * kT3S + fabsf(m1)) * 0x1p-14f;
+    offs[at] = (e0 + e1) * 0.5f + dl + mg;
+    if (q == 0) {
+      st_m2[wave][at * 16 + j] = m2;
+      st_mg[wave][at * 16 + j] = mg;
+      st_p[wave][at * 16 + j] = static_cast<uint8_t>(p1);
+    }
   }
   for (int i = lane; i < NA; i += 64) {
     st_m[wave][i] = 0u;
@@ -667,18 +715,22 @@ __global__ __launch_bounds__(kThreads, 4) void t3_kernel(const uint4 *__restrict
       const uint32_t *xr = xw[wave][al];
       const uint32_t M = pass == 2 ? st_m[wave][al] : 0u;
       const float tlo = st_t[wave][al];
+      // the bounds on the bonus of a word by its bit at p* (as at set-up)
+      const uint32_t pst = st_p[wave][al];
+      const float m2v = st_m2[wave][al];
+      const float xps = __uint_as_float(static_cast<uint32_t>(reinterpret_cast<const uint16_t *>(xr)[pst]) << 16);
+      const float e0 = fmaxf(-xps * kT3Alpha, m2v), e1 = fmaxf(-xps * kT3Beta, m2v);
       uint32_t rmin = 0xFFFFFFFFu;
       // the flagged outputs one at a time (a wave iterates as often as its busiest lane needs)
       for (uint32_t mk = mask; mk != 0u; mk &= mk - 1u) {
         const uint32_t rep = rep0 + static_cast<uint32_t>(__builtin_ctz(mk));
         const uint32_t wr = t3_words[rep];
         const float D = t3_dot(xr, wr);
-        // the word whose S is |D| qualified (|S| passed the threshold); the other sign only when
-        // -|D| can reach the threshold too (an atom whose threshold is about 0 or below)
-        const int sg0 = D < 0.f ? 1 : 0;
-        const int nsg = -fabsf(D) >= tlo ? 2 : 1;
-        for (int u = 0; u < nsg; ++u) {
-          const int sg = sg0 ^ u;
+        const uint32_t bit = (wr >> pst) & 1u;
+        // each of the representative (S = D) and its complement (S = -D, the other bit at p*) whose
+        // S + e(word) can reach the floor
+        for (int sg = 0; sg < 2; ++sg) {
+          if ((sg ? -D : D) + (((bit ^ static_cast<uint32_t>(sg)) != 0u) ? e1 : e0) < tlo) continue;
           const uint32_t wid = rep + (sg ? static_cast<uint32_t>(kT3Reps) : 0u);
           if (pass == 1) {
             float best = -__builtin_inff();
@@ -703,14 +755,16 @@ __global__ __launch_bounds__(kThreads, 4) void t3_kernel(const uint4 *__restrict
     cnt = 0;
   };
 
-  // The threshold on |S|: a word can reach bucket B only if |S| >= lo(B) - e1 - margin, and no bucket
-  // below the lowest that can still win counts: the best pair bucket (the pair key), 2.0 (the origin
-  // rule), and -- raised at every stage end -- the best type-3 bucket found so far.
+  // The threshold on |T|: a word can reach bucket B only if S + e(w) >= lo(B) - margin, i.e.
+  // T >= lo(B) - eb - margin, and no bucket below the lowest that can still win counts: the best pair
+  // bucket (the pair key), 2.0 (the origin rule), and -- raised at every stage end -- the best type-3
+  // bucket found so far.
   float thr[AT];
   auto set_thr = [&](int at, uint32_t mlow) {
     mlow = max(mlow, max(mp[at], 0x4000u));
-    thr[at] = __uint_as_float((mlow << 16) - 0x8000u) - e1[at] - mg[at];
-    if (q == 0) st_t[wave][at * 16 + j] = thr[at] - mg[at];
+    const float lo = __uint_as_float((mlow << 16) - 0x8000u);
+    thr[at] = lo - offs[at];
+    if (q == 0) st_t[wave][at * 16 + j] = lo - 2.f * st_mg[wave][at * 16 + j];
   };
 #pragma unroll
   for (int at = 0; at < AT; ++at) set_thr(at, 0u);
@@ -728,8 +782,9 @@ __global__ __launch_bounds__(kThreads, 4) void t3_kernel(const uint4 *__restrict
 #pragma unroll
       for (int at = 0; at < AT; ++at) {
         const uint32_t M = st_m[wave][at * 16 + j];
-        thr[at] = M >= 0x4000u ? __uint_as_float((M << 16) - 0x8000u) - e1[at] - mg[at] : __builtin_inff();
-        if (q == 0) st_t[wave][at * 16 + j] = thr[at] - mg[at];
+        const float lo = M >= 0x4000u ? __uint_as_float((M << 16) - 0x8000u) : __builtin_inff();
+        thr[at] = lo - offs[at];
+        if (q == 0) st_t[wave][at * 16 + j] = lo - 2.f * st_mg[wave][at * 16 + j];
       }
     }
     const uint8_t *L = stg[buf] + a_off;
