@@ -507,28 +507,30 @@ __global__ __launch_bounds__(kThreads, MODE == kModeB ? 3 : 2) void nn_kernel(co
 // i.e. S(w) - x_p * (alpha = 1.416015625 where w_p = 0, beta = 0.708984375
 // where w_p = 1); both products are exact in fp32 (8 x 8 significant bits).
 // The best code of a word is S(w) + bonus(w) with bonus(w) = max_p of
-// -x_p (alpha or beta).  With p* the position of the largest term
-// t_p = max(-alpha x_p, -beta x_p) and m2 the largest off p*, bonus(w) <=
-// e0 = max(-alpha x_p*, m2) when w has a 0 at p* and <= e1 = max(-beta x_p*,
-// m2) when it has a 1: e(w) = eb + kap P_p*(w) with eb, kap the mean and
-// half-difference of e0, e1.  The MFMA's B operand is the atom with x_p*
-// raised by kap / s, so it gives T(w) = S(w) + kap P_p*(w), and S(w) + e(w)
-// = T(w) + eb: a test on T bounds each word by its own bit at p* (about 5x
-// fewer candidates than one bound e1 = max_p t_p for all words).  The Golay
-// code holds the complement of every word, S(~w) = -S(w) and T(~w) = -T(w),
-// so one MFMA per 16 representative words tests 32 words: 128 tiles instead
-// of 6,144.
+// -x_p (alpha or beta).  With p1, p2 the positions of the two largest terms
+// t_p = max(-alpha x_p, -beta x_p) and m3 the largest elsewhere, bonus(w) <=
+// e(b1, b2) = max(c1(b1), c2(b2), m3) for the word's bits b1, b2 at p1, p2
+// (c(0) = -alpha x, c(1) = -beta x there), and the least additive bound
+// eb + k1 P_p1(w) + k2 P_p2(w) >= e(b1, b2) is solved per atom.  The MFMA's
+// B operand is the atom with x_p1, x_p2 raised by k1 / s, k2 / s, so it gives
+// T(w) = S(w) + k1 P_p1(w) + k2 P_p2(w), and S(w) + e(w) <= T(w) + eb: a test
+// on T bounds each word by its own bits at p1, p2 (about 8x fewer candidates
+// than one bound max_p t_p for all words).  The Golay code holds the
+// complement of every word, S(~w) = -S(w) and T(~w) = -T(w), so one MFMA per
+// 16 representative words tests 32 words: 128 tiles instead of 6,144.
 // A block of 4 waves holds AT atom tiles of 16 atoms per wave as MFMA B
 // operands and streams the 128 pattern tiles through LDS once (a second time
 // only if a survivor list overflows):
 //   pass 1  every lane whose four outputs hold a word that could reach the
 //           lowest bucket still possible -- the best pair bucket (the pair
 //           key of t12_kernel), 2.0 (the origin rule) and the best type-3
-//           bucket found so far, whichever is highest: |T| >= lo(bucket) - eb
-//           - margin -- appends one 4-byte entry (atom, tile, lane quarter, 4-bit mask of
-//           its outputs) to the wave's list in LDS; at every stage end (and
-//           when the list is full) the wave evaluates it, one entry per lane:
-//           each flagged representative gets S recomputed from the atom's
+//           bucket found so far, whichever is highest: |T| >= lo(bucket) -
+//           eb - margin -- appends one 4-byte entry (atom, tile, lane
+//           quarter, 4-bit mask of its outputs) to the wave's list in LDS;
+//           at a stage end once the list holds a round of 64 entries, when
+//           it is full and at the end of the pass the wave evaluates it, one
+//           flagged word per lane per round (an entry with flagged words left
+//           goes back on the list): each flagged representative gets S recomputed from the atom's
 //           bf16 coordinates, and it and its complement, each when its S +
 //           e(w) reaches the floor, get their 24 positions scored,
 //           the best bucket M3 per atom is kept by an LDS atomic max, words
@@ -583,14 +585,14 @@ __global__ __launch_bounds__(kThreads, 4) void t3_kernel(const uint4 *__restrict
   constexpr int NA = AT * 16;  // atoms per wave
   static_assert(NA <= 128, "entry layout: 7 bits of atom");
   __shared__ __align__(16) uint8_t stg[2][kT3StageBytes];
-  __shared__ uint32_t cand[kWaves][kT3Cap];  // atom | tile << 7 | quarter << 14 | output mask << 16
+  __shared__ uint32_t cand[kWaves][kT3Cap];  // atom | tile << 7 | quarter << 14 | output mask << 16 | done << 20
   __shared__ uint32_t surv[kWaves][kT3Surv];  // atom | pattern id << 7: words at or above the atom's running best
   __shared__ __align__(16) uint32_t xw[kWaves][NA][12];  // the atoms' bf16 coordinates (pairs)
   __shared__ uint32_t st_m[kWaves][NA], st_r[kWaves][NA];
   __shared__ float st_t[kWaves][NA];    // lo(floor) less twice the margin: which signs of a word to evaluate
-  __shared__ float st_m2[kWaves][NA];   // the second largest position term (the largest off p*)
+  __shared__ float st_m3[kWaves][NA];   // the third largest position term (the largest off p1, p2)
   __shared__ float st_mg[kWaves][NA];   // the atom's margin for summation orders
-  __shared__ uint8_t st_p[kWaves][NA];  // p*, the position of the largest position term
+  __shared__ uint8_t st_p[kWaves][NA][2];  // p1, p2: the positions of the two largest position terms
   __shared__ uint32_t surv_n[kWaves];
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, q = lane >> 4, j = lane & 15;
@@ -605,75 +607,108 @@ __global__ __launch_bounds__(kThreads, 4) void t3_kernel(const uint4 *__restrict
     uint4 w = make_uint4(0u, 0u, 0u, 0u);
     if (a < n_atoms && q < 3) w = xb[a * 3 + q];
     if (q < 3) *reinterpret_cast<uint4 *>(&xw[wave][at * 16 + j][4 * q]) = w;
-    // the position terms t_p = max(-alpha x_p, -beta x_p): the largest (at p*, x there: x1) and the second
-    // largest, and sum |x_p| (s * sum |x| bounds every |S|), over this lane's 8 coordinates, then over the
-    // atom's 3 lanes (ties: the lowest position, so every lane of the atom agrees on p*)
+    // the position terms t_p = max(-alpha x_p, -beta x_p): the three largest (the first two at p1, p2, x
+    // there: x1, x2) and sum |x_p| (s * sum |x| bounds every |S|), over this lane's 8 coordinates, then over
+    // the atom's 3 lanes (ties: the lower position first, so every lane of the atom agrees on p1, p2)
     uint32_t ww[4] = {w.x, w.y, w.z, w.w};
-    float m1 = -__builtin_inff(), m2 = -__builtin_inff(), x1 = 0.f, ax = 0.f;
-    uint32_t p1 = 0u;
+    float m1 = -__builtin_inff(), m2 = -__builtin_inff(), m3 = -__builtin_inff(), x1 = 0.f, x2 = 0.f, ax = 0.f;
+    uint32_t p1 = 0u, p2 = 1u;
     if (q < 3) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const float x = __uint_as_float(e & 1 ? ww[e / 2] & 0xFFFF0000u : ww[e / 2] << 16);
         const float t = fmaxf(-x * kT3Alpha, -x * kT3Beta);
-        const bool up = t > m1;
-        m2 = up ? m1 : fmaxf(m2, t);
-        m1 = up ? t : m1;
-        x1 = up ? x : x1;
-        p1 = up ? static_cast<uint32_t>(8 * q + e) : p1;
+        const uint32_t p = static_cast<uint32_t>(8 * q + e);
+        const bool a1 = t > m1, a2 = t > m2;
+        m3 = a2 ? m2 : fmaxf(m3, t);
+        m2 = a1 ? m1 : (a2 ? t : m2);
+        x2 = a1 ? x1 : (a2 ? x : x2);
+        p2 = a1 ? p1 : (a2 ? p : p2);
+        m1 = a1 ? t : m1;
+        x1 = a1 ? x : x1;
+        p1 = a1 ? p : p1;
         ax += fabsf(x);
       }
     }
 #pragma unroll
     for (int sh = 16; sh <= 32; sh <<= 1) {
-      const float om1 = __shfl_xor(m1, sh, 64), om2 = __shfl_xor(m2, sh, 64), ox1 = __shfl_xor(x1, sh, 64);
-      const uint32_t op1 = static_cast<uint32_t>(__shfl_xor(static_cast<int>(p1), sh, 64));
-      const bool take = om1 > m1 || (om1 == m1 && op1 < p1);
-      m2 = take ? fmaxf(m1, om2) : fmaxf(m2, om1);
-      m1 = take ? om1 : m1;
-      x1 = take ? ox1 : x1;
-      p1 = take ? op1 : p1;
+      // merge this lane's top 3 with the partner's: (value, position) pairs ordered by value, then position
+      const float o1 = __shfl_xor(m1, sh, 64), o2 = __shfl_xor(m2, sh, 64), o3 = __shfl_xor(m3, sh, 64);
+      const float y1 = __shfl_xor(x1, sh, 64), y2 = __shfl_xor(x2, sh, 64);
+      const uint32_t q1 = static_cast<uint32_t>(__shfl_xor(static_cast<int>(p1), sh, 64));
+      const uint32_t q2 = static_cast<uint32_t>(__shfl_xor(static_cast<int>(p2), sh, 64));
+      auto before = [](float a, uint32_t pa, float b, uint32_t pb) { return a > b || (a == b && pa < pb); };
+      // the merged first: the better of the two firsts
+      const bool t1 = before(o1, q1, m1, p1);
+      const float n1 = t1 ? o1 : m1, r1x = t1 ? y1 : x1;
+      const uint32_t n1p = t1 ? q1 : p1;
+      // the rest of the winner's list and the loser's first compete for the second and third places
+      const float wa = t1 ? o2 : m2, wb = t1 ? o3 : m3, la = t1 ? m1 : o1, lb = t1 ? m2 : o2;
+      const float wax = t1 ? y2 : x2, lax = t1 ? x1 : y1;
+      const uint32_t wap = t1 ? q2 : p2, lap = t1 ? p1 : q1;
+      const bool t2 = before(wa, wap, la, lap);
+      const float n2 = t2 ? wa : la, n2x = t2 ? wax : lax;
+      const uint32_t n2p = t2 ? wap : lap;
+      const float n3 = t2 ? fmaxf(wb, la) : fmaxf(wa, lb);
+      m1 = n1; x1 = r1x; p1 = n1p;
+      m2 = n2; x2 = n2x; p2 = n2p;
+      m3 = n3;
       ax += __shfl_xor(ax, sh, 64);
     }
-    // A word w with bit 0 at p* has bonus(w) <= e0 = max(-alpha x1, m2), with bit 1 <= e1 = max(-beta x1, m2):
-    // e(w) = eb + kap P_p*(w) (P = +1 for bit 0).  The MFMA with x_p* raised by kap / s gives
-    // T(w) = S(w) + kap P_p*(w) (and T(~w) = -T(w)), so |T| >= lo(floor) - eb - margins flags every word
-    // whose S(w) + e(w) reaches the floor; dl: what the bf16 rounding of the raised coordinate adds.
-    const float e0 = fmaxf(-x1 * kT3Alpha, m2), e1 = fmaxf(-x1 * kT3Beta, m2);
-    const float kap = (e0 - e1) * 0.5f;
+    // A word w with bits b1, b2 at p1, p2 has bonus(w) <= e(b1, b2) = max(c1(b1), c2(b2), m3), c(0) =
+    // -alpha x, c(1) = -beta x there.  The additive bound eb + k1 P1(w) + k2 P2(w) >= e(b1, b2) (P = +1 for
+    // bit 0) with the least eb: eb = max((e00 + e11) / 2, (e01 + e10) / 2), k1 + k2 = (e00 - e11) / 2,
+    // k1 - k2 = (e01 - e10) / 2.  The MFMA with x_p1, x_p2 raised by k1 / s, k2 / s gives
+    // T(w) = S(w) + k1 P1(w) + k2 P2(w) (and T(~w) = -T(w)), so |T| >= lo(floor) - eb - margins flags
+    // every word whose S(w) + e(w) reaches the floor; dl: what the bf16 rounding of the raised coordinates
+    // adds.
+    const float a1 = -x1 * kT3Alpha, b1 = -x1 * kT3Beta, a2 = -x2 * kT3Alpha, b2 = -x2 * kT3Beta;
+    const float e00 = fmaxf(fmaxf(a1, a2), m3), e11 = fmaxf(fmaxf(b1, b2), m3);
+    const float e01 = fmaxf(fmaxf(a1, b2), m3), e10 = fmaxf(fmaxf(b1, a2), m3);
+    const float ebar = fmaxf((e00 + e11) * 0.5f, (e01 + e10) * 0.5f);
+    const float sgm = (e00 - e11) * 0.5f, dlt = (e01 - e10) * 0.5f;
+    const float k1 = (sgm + dlt) * 0.5f, k2 = (sgm - dlt) * 0.5f;
     float dl = 0.f;
-    if (q < 3 && (p1 >> 3) == static_cast<uint32_t>(q)) {
-      const uint32_t h = bf16_rne_bits(x1 + kap / kT3S);
-      dl = fabsf((bf16_bits_to_float(h) - x1) * kT3S - kap);
-      const uint32_t e = p1 & 7u;
 #pragma unroll
-      for (int k = 0; k < 4; ++k)
-        if (static_cast<uint32_t>(k) == (e >> 1))
-          ww[k] = (e & 1u) ? (ww[k] & 0xFFFFu) | (h << 16) : (ww[k] & 0xFFFF0000u) | h;
+    for (int r = 0; r < 2; ++r) {
+      const uint32_t pr = r ? p2 : p1;
+      const float xr0 = r ? x2 : x1, kr = r ? k2 : k1;
+      if (q < 3 && (pr >> 3) == static_cast<uint32_t>(q)) {
+        const uint32_t h = bf16_rne_bits(xr0 + kr / kT3S);
+        dl += fabsf((bf16_bits_to_float(h) - xr0) * kT3S - kr);
+        const uint32_t e = pr & 7u;
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+          if (static_cast<uint32_t>(k) == (e >> 1))
+            ww[k] = (e & 1u) ? (ww[k] & 0xFFFFu) | (h << 16) : (ww[k] & 0xFFFF0000u) | h;
+      }
     }
 #pragma unroll
-    for (int sh = 16; sh <= 32; sh <<= 1) dl = fmaxf(dl, __shfl_xor(dl, sh, 64));
+    for (int sh = 16; sh <= 32; sh <<= 1) dl += __shfl_xor(dl, sh, 64);
     b[at] = __builtin_bit_cast(bf16x8, make_uint4(ww[0], ww[1], ww[2], ww[3]));
     // the margin for the MFMA's fp32 summation order of T and the score roundings
     const float mg = (ax * kT3S + fabsf(m1)) * 0x1p-14f;
-    offs[at] = (e0 + e1) * 0.5f + dl + mg;
+    offs[at] = ebar + dl + mg;
     if (q == 0) {
-      st_m2[wave][at * 16 + j] = m2;
+      st_m3[wave][at * 16 + j] = m3;
       st_mg[wave][at * 16 + j] = mg;
-      st_p[wave][at * 16 + j] = static_cast<uint8_t>(p1);
+      st_p[wave][at * 16 + j][0] = static_cast<uint8_t>(p1);
+      st_p[wave][at * 16 + j][1] = static_cast<uint8_t>(p2);
     }
   }
-  for (int i = lane; i < NA; i += 64) {
-    st_m[wave][i] = 0u;
-    st_r[wave][i] = 0xFFFFFFFFu;
-  }
-  // the best pair bucket of each atom (the pair key of t12_kernel, which ran first)
+  // the best pair bucket of each atom (the pair key of t12_kernel, which ran first): the type-3 best starts
+  // there, so no word below it becomes a survivor (an atom whose type-3 codes all stay below it keeps no
+  // row and gets key 0)
   uint32_t mp[AT];
 #pragma unroll
   for (int at = 0; at < AT; ++at) {
     const int64_t a = wave_atom0 + at * 16 + j;
     uint32_t m = 0u;
     if (q == 0 && a < n_atoms) m = keys[a].z >> 16;
+    if (q == 0) {
+      st_m[wave][at * 16 + j] = m;
+      st_r[wave][at * 16 + j] = 0xFFFFFFFFu;
+    }
     mp[at] = static_cast<uint32_t>(__shfl(static_cast<int>(m), j, 64));
   }
 
@@ -703,34 +738,42 @@ __global__ __launch_bounds__(kThreads, 4) void t3_kernel(const uint4 *__restrict
   };
 
   int cnt = 0;  // entries in this wave's candidate list (wave-uniform)
-  // One entry per lane: each flagged output's representative word and (when it can qualify) its complement.
+  // One flagged word and sign per lane per round: the list is worked as a stack and an entry with work left
+  // goes back on it, so every lane is busy while 64 or more words are listed.
   // pass 1: the best bucket of each word -> st_m (atomic max), and the word onto the survivor list when it
   //         is at or above the atom's running best; pass 2: the lowest row at the atom's st_m -> st_r.
   auto flush = [&](int pass) {
-    for (int i = lane; i < cnt; i += 64) {
-      const uint32_t ce = cand[wave][i];
-      const int al = static_cast<int>(ce & 0x7Fu);
-      const uint32_t rep0 = ((ce >> 7) & 0x7Fu) * kTileCodes + 4 * ((ce >> 14) & 3u);
+    while (cnt > 0) {  // (wave-uniform)
+      const int n = min(cnt, 64);
+      cnt -= n;
+      const bool act = lane < n;
+      const uint32_t ce = act ? cand[wave][cnt + lane] : 0u;
       const uint32_t mask = (ce >> 16) & 0xFu;
-      const uint32_t *xr = xw[wave][al];
-      const uint32_t M = pass == 2 ? st_m[wave][al] : 0u;
-      const float tlo = st_t[wave][al];
-      // the bounds on the bonus of a word by its bit at p* (as at set-up)
-      const uint32_t pst = st_p[wave][al];
-      const float m2v = st_m2[wave][al];
-      const float xps = __uint_as_float(static_cast<uint32_t>(reinterpret_cast<const uint16_t *>(xr)[pst]) << 16);
-      const float e0 = fmaxf(-xps * kT3Alpha, m2v), e1 = fmaxf(-xps * kT3Beta, m2v);
-      uint32_t rmin = 0xFFFFFFFFu;
-      // the flagged outputs one at a time (a wave iterates as often as its busiest lane needs)
-      for (uint32_t mk = mask; mk != 0u; mk &= mk - 1u) {
-        const uint32_t rep = rep0 + static_cast<uint32_t>(__builtin_ctz(mk));
+      uint32_t back = 0u;  // the entry as it goes back on the list (0: done)
+      if (act) {
+        const int al = static_cast<int>(ce & 0x7Fu);
+        const uint32_t rep = ((ce >> 7) & 0x7Fu) * kTileCodes + 4 * ((ce >> 14) & 3u) +
+                             static_cast<uint32_t>(__builtin_ctz(mask));
+        const uint32_t *xr = xw[wave][al];
+        const float tlo = st_t[wave][al];
+        // the bound on the bonus of a word by its bits at p1, p2 (as at set-up)
+        const uint32_t pa = st_p[wave][al][0], pb = st_p[wave][al][1];
+        const float m3v = st_m3[wave][al];
+        const uint16_t *xh = reinterpret_cast<const uint16_t *>(xr);
+        const float xa1 = __uint_as_float(static_cast<uint32_t>(xh[pa]) << 16);
+        const float xa2 = __uint_as_float(static_cast<uint32_t>(xh[pb]) << 16);
         const uint32_t wr = t3_words[rep];
         const float D = t3_dot(xr, wr);
-        const uint32_t bit = (wr >> pst) & 1u;
-        // each of the representative (S = D) and its complement (S = -D, the other bit at p*) whose
-        // S + e(word) can reach the floor
-        for (int sg = 0; sg < 2; ++sg) {
-          if ((sg ? -D : D) + (((bit ^ static_cast<uint32_t>(sg)) != 0u) ? e1 : e0) < tlo) continue;
+        const uint32_t ba = (wr >> pa) & 1u, bb = (wr >> pb) & 1u;
+        // the representative (S = D) and its complement (S = -D, the other bits at p1, p2), each when its
+        // S + e(word) can reach the floor; one of them per round (bit 20: the representative is done)
+        const float ew0 = fmaxf(fmaxf(-xa1 * (ba ? kT3Beta : kT3Alpha), -xa2 * (bb ? kT3Beta : kT3Alpha)), m3v);
+        const float ew1 = fmaxf(fmaxf(-xa1 * (ba ? kT3Alpha : kT3Beta), -xa2 * (bb ? kT3Alpha : kT3Beta)), m3v);
+        const bool q0 = ((ce >> 20) & 1u) == 0u && D + ew0 >= tlo, q1 = -D + ew1 >= tlo;
+        const uint32_t rest = mask & (mask - 1u);
+        back = q0 && q1 ? ce | 1u << 20 : rest != 0u ? (ce & ~0x1F0000u) | rest << 16 : 0u;
+        if (q0 || q1) {
+          const int sg = q0 ? 0 : 1;
           const uint32_t wid = rep + (sg ? static_cast<uint32_t>(kT3Reps) : 0u);
           if (pass == 1) {
             float best = -__builtin_inff();
@@ -744,15 +787,22 @@ __global__ __launch_bounds__(kThreads, 4) void t3_kernel(const uint4 *__restrict
               }
             }
           } else {
+            const uint32_t M = st_m[wave][al];
+            uint32_t rmin = 0xFFFFFFFFu;
             word_scores(xr, wr, sg, D, [&](int p, float t) {
               if (t > 0.f && t3_bucket(t) == M) rmin = min(rmin, t3_rows[wid * kDim + p]);
             });
+            if (rmin != 0xFFFFFFFFu) atomicMin(&st_r[wave][al], rmin);
           }
         }
       }
-      if (pass == 2 && rmin != 0xFFFFFFFFu) atomicMin(&st_r[wave][al], rmin);
+      // the entries with work left go back on the list (every lane read its entry above)
+      const uint64_t bm = __ballot(back != 0u);
+      if (back != 0u)
+        cand[wave][cnt + __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(bm >> 32),
+                                                   __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(bm), 0u))] = back;
+      cnt += __popcll(bm);
     }
-    cnt = 0;
   };
 
   // The threshold on |T|: a word can reach bucket B only if S + e(w) >= lo(B) - margin, i.e.
@@ -797,16 +847,16 @@ __global__ __launch_bounds__(kThreads, 4) void t3_kernel(const uint4 *__restrict
         c[at] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b[at], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
 #pragma unroll
       for (int at = 0; at < AT; ++at) {
-        // the lane's largest |S| against the atom's threshold (a word and its complement: one test)
-        const float m4 = fmaxf(fmaxf(fabsf(c[at][0]), fabsf(c[at][1])), fmaxf(fabsf(c[at][2]), fabsf(c[at][3])));
-        const bool hit = m4 >= thr[at];
-        const uint64_t msk = __ballot(hit);
+        // each output's |T| against the atom's threshold (a word and its complement: one test), as four
+        // compares whose wave masks are OR'ed (no max over the outputs)
+        const bool h0 = fabsf(c[at][0]) >= thr[at], h1 = fabsf(c[at][1]) >= thr[at];
+        const bool h2 = fabsf(c[at][2]) >= thr[at], h3 = fabsf(c[at][3]) >= thr[at];
+        const uint64_t msk = __ballot(h0) | __ballot(h1) | __ballot(h2) | __ballot(h3);
         if (msk == 0ull) continue;
         if (cnt > kT3Cap - 64) flush(pass);
+        const bool hit = ((msk >> lane) & 1ull) != 0ull;
         if (hit) {
-          const float T = thr[at];
-          const uint32_t mask = (fabsf(c[at][0]) >= T ? 1u : 0u) | (fabsf(c[at][1]) >= T ? 2u : 0u) |
-                                (fabsf(c[at][2]) >= T ? 4u : 0u) | (fabsf(c[at][3]) >= T ? 8u : 0u);
+          const uint32_t mask = (h0 ? 1u : 0u) | (h1 ? 2u : 0u) | (h2 ? 4u : 0u) | (h3 ? 8u : 0u);
           const uint32_t pos = static_cast<uint32_t>(cnt) +
                                __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(msk >> 32),
                                                          __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(msk), 0u));
@@ -816,8 +866,8 @@ __global__ __launch_bounds__(kThreads, 4) void t3_kernel(const uint4 *__restrict
         cnt += __popcll(msk);
       }
     }
-    // every wave evaluates its list at the stage end, so no wave's evaluation holds the others at the barrier
-    if (cnt > 0) flush(pass);
+    // the list is evaluated once it fills a round of lanes, and at the end of each pass
+    if (cnt >= 64 || g == kT3Stages - 1 || g == 2 * kT3Stages - 1) flush(pass);
     if (pass == 1) {
       // the thresholds rise with the best buckets found so far (this wave's own atoms: no barrier needed)
 #pragma unroll
@@ -890,8 +940,9 @@ __global__ __launch_bounds__(kThreads, 4) void t3_kernel(const uint4 *__restrict
 //           appends one 4-byte entry (atom, tile, quarter, output mask) to the
 //           wave's list; floor is the highest of 2.0 (the origin rule), the
 //           atom's best type-1 bucket and the best octad bucket found so far
-//           (raised at every stage end).  At every stage end (and when the list
-//           is full) the wave evaluates it, one entry per lane: the flagged
+//           (raised at every stage end).  At a stage end once the list holds a
+//           round of 64 entries, when it is full and at the end of the pass the
+//           wave evaluates it, one flagged octad per lane per round: the
 //           octads' best codes scored exactly, the best bucket per atom kept by
 //           an LDS atomic max, octads at or above the running best onto a
 //           survivor list, which every stage end compacts to the octads at
@@ -1091,42 +1142,50 @@ __global__ __launch_bounds__(kThreads, 4) void t12_kernel(const uint4 *__restric
   };
 
   int cnt = 0;  // entries in this wave's candidate list (wave-uniform)
-  // One entry per lane.  pass 1: each flagged octad's best code -> st_m (atomic max), and the octad onto
-  // the survivor list when it is at or above the atom's running best; pass 2: the lowest row at st_m -> st_r.
+  // One flagged octad per lane per round (the list is worked as a stack: an entry with flagged octads left
+  // goes back on it).  pass 1: the octad's best code -> st_m (atomic max), and the octad onto the survivor
+  // list when it is at or above the atom's running best; pass 2: the lowest row at st_m -> st_r.
   auto flush = [&](int pass) {
-    for (int i = lane; i < cnt; i += 64) {
-      const uint32_t ce = cand[wave][i];
-      const int al = static_cast<int>(ce & 0x7Fu);
-      const uint32_t o0 = ((ce >> 7) & 0x3Fu) * kTileCodes + 4u * ((ce >> 13) & 3u);
+    while (cnt > 0) {  // (wave-uniform)
+      const int n = min(cnt, 64);
+      cnt -= n;
+      const bool act = lane < n;
+      const uint32_t ce = act ? cand[wave][cnt + lane] : 0u;
       const uint32_t mask = (ce >> 16) & 0xFu;
-      const uint32_t *xr = xw[wave][al];
-      const uint32_t M = pass == 2 ? st_m[wave][al] : 0u;
-      const uint32_t o5 = pass == 1 ? st_o[wave][al] : 0xFFFFFFFFu;
-      uint32_t rmin = 0xFFFFFFFFu;
-      for (uint32_t mk = mask; mk != 0u; mk &= mk - 1u) {
-        const uint32_t o = o0 + static_cast<uint32_t>(__builtin_ctz(mk));
+      const uint32_t rest = mask & (mask - 1u);
+      if (act) {
+        const int al = static_cast<int>(ce & 0x7Fu);
+        const uint32_t o = ((ce >> 7) & 0x3Fu) * kTileCodes + 4u * ((ce >> 13) & 3u) +
+                           static_cast<uint32_t>(__builtin_ctz(mask));
         // (padding slots: U = 0 unless the margin is not finite; the set-up octad: scored already)
-        if (o >= static_cast<uint32_t>(kT2Octads) || o == o5) continue;
-        float xa[8];
-        const uint32_t sg = t2_load(xr, t2_pos[o], xa);
-        if (pass == 1) {
-          const float S = t2_best(xa, sg);
-          const uint32_t bk = S > 0.f ? t3_bucket(S) : 0u;
-          if (bk >= 0x4000u) {
-            const uint32_t old = atomicMax(&st_m[wave][al], bk);
-            if (bk >= old) {
-              const uint32_t slot = atomicAdd(&surv_n[wave], 1u);
-              if (slot < static_cast<uint32_t>(kT2Surv))
-                surv[wave][slot] = static_cast<uint32_t>(al) | o << 7 | (bk - 0x4000u) << 17;
+        if (o < static_cast<uint32_t>(kT2Octads) && (pass == 2 || o != st_o[wave][al])) {
+          float xa[8];
+          const uint32_t sg = t2_load(xw[wave][al], t2_pos[o], xa);
+          if (pass == 1) {
+            const float S = t2_best(xa, sg);
+            const uint32_t bk = S > 0.f ? t3_bucket(S) : 0u;
+            if (bk >= 0x4000u) {
+              const uint32_t old = atomicMax(&st_m[wave][al], bk);
+              if (bk >= old) {
+                const uint32_t slot = atomicAdd(&surv_n[wave], 1u);
+                if (slot < static_cast<uint32_t>(kT2Surv))
+                  surv[wave][slot] = static_cast<uint32_t>(al) | o << 7 | (bk - 0x4000u) << 17;
+              }
             }
+          } else {
+            const uint32_t r = t2_rows_at(xa, sg, o, st_m[wave][al], t2_rows);
+            if (r != 0xFFFFFFFFu) atomicMin(&st_r[wave][al], r);
           }
-        } else {
-          rmin = min(rmin, t2_rows_at(xa, sg, o, M, t2_rows));
         }
       }
-      if (pass == 2 && rmin != 0xFFFFFFFFu) atomicMin(&st_r[wave][al], rmin);
+      // the entries with flagged octads left go back on the list (every lane read its entry above)
+      const uint64_t bm = __ballot(rest != 0u);
+      if (rest != 0u)
+        cand[wave][cnt + __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(bm >> 32),
+                                                   __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(bm), 0u))] =
+            (ce & ~0xF0000u) | rest << 16;
+      cnt += __popcll(bm);
     }
-    cnt = 0;
   };
 
   // Keep only the survivors at their atom's current best bucket (none is lost while the list has not
@@ -1230,15 +1289,15 @@ __global__ __launch_bounds__(kThreads, 4) void t12_kernel(const uint4 *__restric
         c[at] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b[at], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
 #pragma unroll
       for (int at = 0; at < AT; ++at) {
-        const float m4 = fmaxf(fmaxf(c[at][0], c[at][1]), fmaxf(c[at][2], c[at][3]));
-        const bool hit = m4 >= thr[at];
-        const uint64_t msk = __ballot(hit);
+        // each output against the atom's threshold, four compares whose wave masks are OR'ed
+        const bool h0 = c[at][0] >= thr[at], h1 = c[at][1] >= thr[at];
+        const bool h2 = c[at][2] >= thr[at], h3 = c[at][3] >= thr[at];
+        const uint64_t msk = __ballot(h0) | __ballot(h1) | __ballot(h2) | __ballot(h3);
         if (msk == 0ull) continue;
         if (cnt > kT2Cap - 64) flush(pass);
+        const bool hit = ((msk >> lane) & 1ull) != 0ull;
         if (hit) {
-          const float T = thr[at];
-          const uint32_t mask = (c[at][0] >= T ? 1u : 0u) | (c[at][1] >= T ? 2u : 0u) | (c[at][2] >= T ? 4u : 0u) |
-                                (c[at][3] >= T ? 8u : 0u);
+          const uint32_t mask = (h0 ? 1u : 0u) | (h1 ? 2u : 0u) | (h2 ? 4u : 0u) | (h3 ? 8u : 0u);
           const uint32_t pos = static_cast<uint32_t>(cnt) +
                                __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(msk >> 32),
                                                          __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(msk), 0u));
@@ -1248,7 +1307,8 @@ __global__ __launch_bounds__(kThreads, 4) void t12_kernel(const uint4 *__restric
         cnt += __popcll(msk);
       }
     }
-    if (cnt > 0) flush(pass);
+    // the list is evaluated once it fills a round of lanes, and at the end of each pass
+    if (cnt >= 64 || g == kT2Stages - 1 || g == 2 * kT2Stages - 1) flush(pass);
     if (pass == 1) {
       compact();
 #pragma unroll
