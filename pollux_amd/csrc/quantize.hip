@@ -820,6 +820,7 @@ __global__ __launch_bounds__(kThreads, 4) void t3_kernel(const uint4 *__restrict
   for (int at = 0; at < AT; ++at) set_thr(at, 0u);
 
   const int a_off = (q < 3 ? q : 0) * 256 + j * 16;
+  const uint32_t ebase = static_cast<uint32_t>(j) | static_cast<uint32_t>(q) << 14;  // the lane's entry bits
   stage_copy(0, 0);
   __syncthreads();
   // pass 1 (the candidates); pass 2 only when some wave's survivor list overflowed
@@ -854,14 +855,12 @@ __global__ __launch_bounds__(kThreads, 4) void t3_kernel(const uint4 *__restrict
         const uint64_t msk = __ballot(h0) | __ballot(h1) | __ballot(h2) | __ballot(h3);
         if (msk == 0ull) continue;
         if (cnt > kT3Cap - 64) flush(pass);
-        const bool hit = ((msk >> lane) & 1ull) != 0ull;
-        if (hit) {
+        if (h0 | h1 | h2 | h3) {  // (the compares' own lane masks: no per-lane test of msk)
           const uint32_t mask = (h0 ? 1u : 0u) | (h1 ? 2u : 0u) | (h2 ? 4u : 0u) | (h3 ? 8u : 0u);
           const uint32_t pos = static_cast<uint32_t>(cnt) +
                                __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(msk >> 32),
                                                          __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(msk), 0u));
-          cand[wave][pos] = static_cast<uint32_t>(at * 16 + j) | static_cast<uint32_t>(tile0 + k) << 7 |
-                            static_cast<uint32_t>(q) << 14 | mask << 16;
+          cand[wave][pos] = (ebase + static_cast<uint32_t>(at * 16)) | static_cast<uint32_t>(tile0 + k) << 7 | mask << 16;
         }
         cnt += __popcll(msk);
       }
@@ -1221,6 +1220,7 @@ __global__ __launch_bounds__(kThreads, 4) void t12_kernel(const uint4 *__restric
   };
 
   const int a_off = (q < 3 ? q : 0) * 256 + j * 16;
+  const uint32_t ebase = static_cast<uint32_t>(j) | static_cast<uint32_t>(q) << 13;  // the lane's entry bits
   stage_copy(0, 0);
   __syncthreads();
   // The floor from one octad per atom, one lane per atom: the octad holding its 5 largest |x| (every 5
@@ -1295,14 +1295,12 @@ __global__ __launch_bounds__(kThreads, 4) void t12_kernel(const uint4 *__restric
         const uint64_t msk = __ballot(h0) | __ballot(h1) | __ballot(h2) | __ballot(h3);
         if (msk == 0ull) continue;
         if (cnt > kT2Cap - 64) flush(pass);
-        const bool hit = ((msk >> lane) & 1ull) != 0ull;
-        if (hit) {
+        if (h0 | h1 | h2 | h3) {  // (the compares' own lane masks: no per-lane test of msk)
           const uint32_t mask = (h0 ? 1u : 0u) | (h1 ? 2u : 0u) | (h2 ? 4u : 0u) | (h3 ? 8u : 0u);
           const uint32_t pos = static_cast<uint32_t>(cnt) +
                                __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(msk >> 32),
                                                          __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(msk), 0u));
-          cand[wave][pos] = static_cast<uint32_t>(at * 16 + j) | static_cast<uint32_t>(tile0 + k) << 7 |
-                            static_cast<uint32_t>(q) << 13 | mask << 16;
+          cand[wave][pos] = (ebase + static_cast<uint32_t>(at * 16)) | static_cast<uint32_t>(tile0 + k) << 7 | mask << 16;
         }
         cnt += __popcll(msk);
       }
