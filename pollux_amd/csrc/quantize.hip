@@ -540,8 +540,9 @@ __global__ __launch_bounds__(kThreads, MODE == kModeB ? 3 : 2) void nn_kernel(co
 //           it was evaluated, so the survivors give every (w, p) at bucket M3
 //           and its codebook row (t3_rows); the lowest is kept by an LDS
 //           atomic min;
-//   pass 2  (only after a survivor list overflowed) the same rows from a
-//           second sweep with the thresholds at M3.
+//   pass 2  (only after a survivor list lost entries) the rows of the atoms
+//           whose entries were lost, from a second sweep with their
+//           thresholds at M3 (the other atoms' thresholds: +inf).
 // The atom's key gets (M3 << 16, lowest row at M3), or 0 when no type-3 code
 // reaches 2.0; pick_kernel compares it with the pair key.
 // Buckets are taken by round-half-up like the dense sweep's, and every score
@@ -594,10 +595,12 @@ __global__ __launch_bounds__(kThreads, 4) void t3_kernel(const uint4 *__restrict
   __shared__ float st_mg[kWaves][NA];   // the atom's margin for summation orders
   __shared__ uint8_t st_p[kWaves][NA][2];  // p1, p2: the positions of the two largest position terms
   __shared__ uint32_t surv_n[kWaves];
+  __shared__ uint32_t st_ovf[kWaves][2];   // atoms (bits) whose survivor list lost an entry: rows by pass 2
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, q = lane >> 4, j = lane & 15;
   const int64_t wave_atom0 = static_cast<int64_t>(blockIdx.x) * (kWaves * NA) + static_cast<int64_t>(wave) * NA;
 
+  if (lane < 2) st_ovf[wave][lane] = 0u;
   if (lane == 0) surv_n[wave] = 0u;
   bf16x8 b[AT];
   float offs[AT];  // eb, the raised coordinate's rounding and the margin: thr = lo(floor) - offs
@@ -783,7 +786,10 @@ __global__ __launch_bounds__(kThreads, 4) void t3_kernel(const uint4 *__restrict
               const uint32_t old = atomicMax(&st_m[wave][al], bk);
               if (bk >= old) {
                 const uint32_t slot = atomicAdd(&surv_n[wave], 1u);
-                if (slot < static_cast<uint32_t>(kT3Surv)) surv[wave][slot] = static_cast<uint32_t>(al) | wid << 7;
+                if (slot < static_cast<uint32_t>(kT3Surv))
+                  surv[wave][slot] = static_cast<uint32_t>(al) | wid << 7;
+                else
+                  atomicOr(&st_ovf[wave][al >> 5], 1u << (al & 31));
               }
             }
           } else {
@@ -829,11 +835,13 @@ __global__ __launch_bounds__(kThreads, 4) void t3_kernel(const uint4 *__restrict
     const int pass = 1 + g / kT3Stages, buf = g & 1;
     if (g + 1 < g_end) stage_copy(g + 1, buf ^ 1);  // (pass 2's first stage: after the decision below)
     if (g == kT3Stages) {
-      // pass 2 (the survivors overflowed): thresholds at the atoms' final best buckets
+      // pass 2 (a survivor list lost entries): thresholds at the final best buckets of the atoms concerned
 #pragma unroll
       for (int at = 0; at < AT; ++at) {
-        const uint32_t M = st_m[wave][at * 16 + j];
-        const float lo = M >= 0x4000u ? __uint_as_float((M << 16) - 0x8000u) : __builtin_inff();
+        const int al = at * 16 + j;
+        const bool redo = rows_by_sweep != 0 || ((st_ovf[wave][al >> 5] >> (al & 31)) & 1u) != 0u;
+        const uint32_t M = st_m[wave][al];
+        const float lo = redo && M >= 0x4000u ? __uint_as_float((M << 16) - 0x8000u) : __builtin_inff();
         thr[at] = lo - offs[at];
         if (q == 0) st_t[wave][at * 16 + j] = lo - 2.f * st_mg[wave][at * 16 + j];
       }
@@ -873,9 +881,9 @@ __global__ __launch_bounds__(kThreads, 4) void t3_kernel(const uint4 *__restrict
       for (int at = 0; at < AT; ++at) set_thr(at, st_m[wave][at * 16 + j]);
     }
     if (g == kT3Stages - 1) {
-      // pass 1 done: pass 2 only if a survivor list overflowed (all waves agree)
-      // (rows_by_sweep: pass 2 always -- the path an overflow takes, for its tests)
-      if (__syncthreads_or(rows_by_sweep != 0 || surv_n[wave] > static_cast<uint32_t>(kT3Surv))) {
+      // pass 1 done: pass 2 only if a survivor list lost entries (all waves agree), for those atoms
+      // (rows_by_sweep: pass 2 for every atom -- the path an overflow takes, for its tests)
+      if (__syncthreads_or(rows_by_sweep != 0 || (st_ovf[wave][0] | st_ovf[wave][1]) != 0u)) {
         g_end = 2 * kT3Stages;
         stage_copy(g + 1, buf ^ 1);  // buffer buf ^ 1 was last read in stage g - 1, before the barrier
         __syncthreads();
@@ -884,13 +892,14 @@ __global__ __launch_bounds__(kThreads, 4) void t3_kernel(const uint4 *__restrict
       __syncthreads();
     }
   }
-  if (g_end == kT3Stages) {
+  {
     // the lowest row at each atom's best bucket, from its survivors (every word that reached the final
-    // best bucket was at or above the running best when it was evaluated)
-    const int ns = static_cast<int>(surv_n[wave]);
+    // best bucket was at or above the running best when it was evaluated); pass 2 gave the others'
+    const int ns = static_cast<int>(min(surv_n[wave], static_cast<uint32_t>(kT3Surv)));
     for (int i = lane; i < ns; i += 64) {
       const uint32_t se = surv[wave][i];
       const int al = static_cast<int>(se & 0x7Fu);
+      if (rows_by_sweep != 0 || ((st_ovf[wave][al >> 5] >> (al & 31)) & 1u) != 0u) continue;
       const uint32_t wid = se >> 7;
       const uint32_t M = st_m[wave][al];
       const uint32_t *xr = xw[wave][al];
@@ -904,7 +913,7 @@ __global__ __launch_bounds__(kThreads, 4) void t3_kernel(const uint4 *__restrict
       if (rmin != 0xFFFFFFFFu) atomicMin(&st_r[wave][al], rmin);
     }
   }
-  __syncthreads();  // (block-uniform: g_end is)
+  __syncthreads();
   if (q == 0) {
 #pragma unroll
     for (int at = 0; at < AT; ++at) {
@@ -951,8 +960,9 @@ __global__ __launch_bounds__(kThreads, 4) void t3_kernel(const uint4 *__restrict
 //           U - lo(M) are enumerated and scored exactly; type 1 the same way
 //           from the atom's coordinates when its best type-1 bucket is M; the
 //           lowest codebook row by LDS atomic min;
-//   pass 2  (only after a survivor list overflowed) the same rows from a
-//           second sweep with the thresholds at M.
+//   pass 2  (only after a survivor list lost entries) the rows of the atoms
+//           whose entries were lost, from a second sweep with their
+//           thresholds at M (the other atoms' thresholds: +inf).
 // The atom's key gets (M << 16, lowest row at M) in its upper 8 bytes, or 0
 // when no type-1/2 code reaches 2.0; t3_kernel takes M as its floor.
 // Buckets are taken by round-half-up like the dense sweep's, every score is
@@ -1082,10 +1092,12 @@ __global__ __launch_bounds__(kThreads, 4) void t12_kernel(const uint4 *__restric
   __shared__ uint32_t st_m[kWaves][NA], st_r[kWaves][NA];
   __shared__ uint32_t st_o[kWaves][NA];  // the octad of the atom's 5 largest |x| (scored at set-up)
   __shared__ uint32_t surv_n[kWaves];
+  __shared__ uint32_t st_ovf[kWaves][2];  // atoms (bits) whose survivor list lost an entry: rows by pass 2
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, q = lane >> 4, j = lane & 15;
   const int64_t wave_atom0 = static_cast<int64_t>(blockIdx.x) * (kWaves * NA) + static_cast<int64_t>(wave) * NA;
 
+  if (lane < 2) st_ovf[wave][lane] = 0u;
   if (lane == 0) surv_n[wave] = 0u;
   bf16x8 b[AT];
   float mg[AT], v1[AT];
@@ -1169,6 +1181,8 @@ __global__ __launch_bounds__(kThreads, 4) void t12_kernel(const uint4 *__restric
                 const uint32_t slot = atomicAdd(&surv_n[wave], 1u);
                 if (slot < static_cast<uint32_t>(kT2Surv))
                   surv[wave][slot] = static_cast<uint32_t>(al) | o << 7 | (bk - 0x4000u) << 17;
+                else
+                  atomicOr(&st_ovf[wave][al >> 5], 1u << (al & 31));
               }
             }
           } else {
@@ -1187,11 +1201,10 @@ __global__ __launch_bounds__(kThreads, 4) void t12_kernel(const uint4 *__restric
     }
   };
 
-  // Keep only the survivors at their atom's current best bucket (none is lost while the list has not
-  // overflowed; after an overflow pass 2 gives the rows).
+  // Keep only the survivors at their atom's current best bucket (an atom that lost an entry to a full
+  // list is flagged in st_ovf, and pass 2 gives its rows).
   auto compact = [&]() {
-    const uint32_t n = surv_n[wave];
-    if (n > static_cast<uint32_t>(kT2Surv)) return;
+    const uint32_t n = min(surv_n[wave], static_cast<uint32_t>(kT2Surv));
     uint32_t w = 0u;
     for (uint32_t base = 0u; base < n; base += 64u) {
       const uint32_t i = base + static_cast<uint32_t>(lane);
@@ -1263,7 +1276,10 @@ __global__ __launch_bounds__(kThreads, 4) void t12_kernel(const uint4 *__restric
     if (bk >= 0x4000u && bk >= st_m[wave][al]) {
       st_m[wave][al] = bk;
       const uint32_t slot = atomicAdd(&surv_n[wave], 1u);
-      if (slot < static_cast<uint32_t>(kT2Surv)) surv[wave][slot] = static_cast<uint32_t>(al) | o << 7 | (bk - 0x4000u) << 17;
+      if (slot < static_cast<uint32_t>(kT2Surv))
+        surv[wave][slot] = static_cast<uint32_t>(al) | o << 7 | (bk - 0x4000u) << 17;
+      else
+        atomicOr(&st_ovf[wave][al >> 5], 1u << (al & 31));
     }
   }
 #pragma unroll
@@ -1273,10 +1289,13 @@ __global__ __launch_bounds__(kThreads, 4) void t12_kernel(const uint4 *__restric
     const int pass = 1 + g / kT2Stages, buf = g & 1;
     if (g + 1 < g_end) stage_copy(g + 1, buf ^ 1);
     if (g == kT2Stages) {
+      // pass 2 (a survivor list lost entries): thresholds at the final best buckets of the atoms concerned
 #pragma unroll
       for (int at = 0; at < AT; ++at) {
-        const uint32_t M = st_m[wave][at * 16 + j];
-        thr[at] = M >= 0x4000u ? __uint_as_float((M << 16) - 0x8000u) - mg[at] : __builtin_inff();
+        const int al = at * 16 + j;
+        const bool redo = rows_by_sweep != 0 || ((st_ovf[wave][al >> 5] >> (al & 31)) & 1u) != 0u;
+        const uint32_t M = st_m[wave][al];
+        thr[at] = redo && M >= 0x4000u ? __uint_as_float((M << 16) - 0x8000u) - mg[at] : __builtin_inff();
       }
     }
     const uint8_t *L = stg[buf] + a_off;
@@ -1313,7 +1332,7 @@ __global__ __launch_bounds__(kThreads, 4) void t12_kernel(const uint4 *__restric
       for (int at = 0; at < AT; ++at) set_thr(at, st_m[wave][at * 16 + j]);
     }
     if (g == kT2Stages - 1) {
-      if (__syncthreads_or(rows_by_sweep != 0 || surv_n[wave] > static_cast<uint32_t>(kT2Surv))) {
+      if (__syncthreads_or(rows_by_sweep != 0 || (st_ovf[wave][0] | st_ovf[wave][1]) != 0u)) {
         g_end = 2 * kT2Stages;
         stage_copy(g + 1, buf ^ 1);  // buffer buf ^ 1 was last read in stage g - 1, before the barrier
         __syncthreads();
@@ -1322,12 +1341,14 @@ __global__ __launch_bounds__(kThreads, 4) void t12_kernel(const uint4 *__restric
       __syncthreads();
     }
   }
-  if (g_end == kT2Stages) {
-    // the survivors are the octads at their atom's final best bucket (compacted at the last stage end)
-    const int ns = static_cast<int>(surv_n[wave]);
+  {
+    // the survivors are the octads at their atom's final best bucket (compacted at the last stage end);
+    // pass 2 gave the rows of the atoms whose list lost entries
+    const int ns = static_cast<int>(min(surv_n[wave], static_cast<uint32_t>(kT2Surv)));
     for (int i = lane; i < ns; i += 64) {
       const uint32_t se = surv[wave][i];
       const int al = static_cast<int>(se & 0x7Fu);
+      if (rows_by_sweep != 0 || ((st_ovf[wave][al >> 5] >> (al & 31)) & 1u) != 0u) continue;
       const uint32_t o = (se >> 7) & 0x3FFu;
       float xa[8];
       const uint32_t sg = t2_load(xw[wave][al], t2_pos[o], xa);
@@ -1335,7 +1356,7 @@ __global__ __launch_bounds__(kThreads, 4) void t12_kernel(const uint4 *__restric
       if (r != 0xFFFFFFFFu) atomicMin(&st_r[wave][al], r);
     }
   }
-  __syncthreads();  // (block-uniform: g_end is)
+  __syncthreads();
   if (q == 0) {
 #pragma unroll
     for (int at = 0; at < AT; ++at) {

@@ -142,3 +142,29 @@ def test_integer_atoms_exact_ties(dev):
     print(f"[t3 integer atoms] {len(x)} atoms equal on both paths; oracle on {len(sub)}: "
           f"{int((~ok).sum())} near-ties", flush=True)
     assert np.array_equal(s[sub].numpy()[ok], o["idx"][ok])
+
+
+def _contact_midpoints(n, seed):
+    # midpoints of code pairs at raw inner product 16 (the contact pairs) plus tiny noise: many codes tie at
+    # the best bucket there, so the scorers' per-wave survivor lists overflow for some atoms and not others
+    rng = np.random.default_rng(seed)
+    raw = cb.codebook_int8().astype(np.int64)
+    c32 = cb.codebook_f32()
+    a = rng.integers(1, 196561, 8 * n)
+    b = rng.integers(1, 196561, (8 * n, 64))
+    ip = (raw[b] * raw[a][:, None, :]).sum(-1)
+    ok = (ip == 16).any(1)
+    a, b, ip = a[ok][:n], b[ok][:n], ip[ok][:n]
+    bb = b[np.arange(len(a)), (ip == 16).argmax(1)]
+    return torch.from_numpy((0.5 * (c32[a] + c32[bb]) + rng.normal(0, 1e-3, (len(a), 24))).astype(np.float32))
+
+
+def test_midpoints_among_ordinary_atoms(dev):
+    # some waves lose survivors (their atoms' rows come from the second sweep), the rest keep theirs
+    mid = _contact_midpoints(3000, 17)
+    x = _c4_atoms(60_000, 18)
+    pos = torch.randperm(len(x), generator=torch.Generator().manual_seed(19))[: len(mid)]
+    x[pos] = mid
+    got = _compare(dev, x, "midpoints among c4 atoms", max_near=0.01)
+    r = castor.quantize_indices(x.to(dev), mode="bf16-rows-sweep").long().cpu()
+    assert torch.equal(got, r), int((got != r).sum())
