@@ -1075,8 +1075,12 @@ __device__ uint32_t t1_rows_at(const uint32_t *xr, float v1, uint32_t M, const u
   return rmin;
 }
 
-template <int AT>
-__global__ __launch_bounds__(kThreads, 4) void t12_kernel(const uint4 *__restrict__ xb, int64_t n_atoms,
+// LOAD: 0 the bf16 planes from prep_kernel (xb); 1 the fp32 atoms (src), rounded here and written to xb
+// for t3_kernel; 2 the same with the row scale applied first (src / sigma, as prep_kernel<true>).
+template <int AT, int LOAD>
+__global__ __launch_bounds__(kThreads, 4) void t12_kernel(uint4 *__restrict__ xb, const float *__restrict__ src,
+                                                          const float *__restrict__ sigma, int64_t atoms_per_row,
+                                                          int64_t n_atoms,
                                                           const uint8_t *__restrict__ t2_tiles,
                                                           const uint2 *__restrict__ t2_pos,
                                                           const uint32_t *__restrict__ t2_rows,
@@ -1106,7 +1110,17 @@ __global__ __launch_bounds__(kThreads, 4) void t12_kernel(const uint4 *__restric
   for (int at = 0; at < AT; ++at) {
     const int64_t a = wave_atom0 + at * 16 + j;
     uint4 w = make_uint4(0u, 0u, 0u, 0u);
-    if (a < n_atoms && q < 3) w = xb[a * 3 + q];
+    if constexpr (LOAD == 0) {
+      if (a < n_atoms && q < 3) w = xb[a * 3 + q];
+    } else {
+      float v[8];
+      load_coords8<LOAD == 2>(src, sigma, atoms_per_row, n_atoms, a, q, v);  // (zeros past the end, q == 3)
+      w.x = bf16_rne_bits(v[0]) | (bf16_rne_bits(v[1]) << 16);
+      w.y = bf16_rne_bits(v[2]) | (bf16_rne_bits(v[3]) << 16);
+      w.z = bf16_rne_bits(v[4]) | (bf16_rne_bits(v[5]) << 16);
+      w.w = bf16_rne_bits(v[6]) | (bf16_rne_bits(v[7]) << 16);
+      if (a < n_atoms && q < 3) xb[a * 3 + q] = w;
+    }
     if (q < 3) *reinterpret_cast<uint4 *>(&xw[wave][at * 16 + j][4 * q]) = w;
     const uint4 wa = make_uint4(w.x & 0x7FFF7FFFu, w.y & 0x7FFF7FFFu, w.z & 0x7FFF7FFFu, w.w & 0x7FFF7FFFu);
     b[at] = __builtin_bit_cast(bf16x8, wa);
@@ -1986,9 +2000,10 @@ int t3_launch(const uint4 *xb, int64_t n_atoms, const DeviceTables *tab, uint4 *
   return check_launch("t3_kernel");
 }
 
-// t12_kernel: atom tiles per wave by launch size, as t3_kernel (37 KB of LDS at 4 tiles per wave).
-int t12_launch(const uint4 *xb, int64_t n_atoms, const DeviceTables *tab, uint4 *keys, hipStream_t s,
-               int rows_by_sweep) {
+// t12_kernel: atom tiles per wave by launch size, as t3_kernel (38 KB of LDS at 4 tiles per wave).
+template <int LOAD>
+int t12_launch_load(uint4 *xb, const float *src, const float *sigma, int64_t apr, int64_t n_atoms,
+                    const DeviceTables *tab, uint4 *keys, hipStream_t s, int rows_by_sweep) {
   const int AT = n_atoms >= 131072 ? 4 : n_atoms >= 32768 ? 2 : 1;
   const int64_t per_block = static_cast<int64_t>(kWaves) * AT * 16;
   const int64_t blocks = (n_atoms + per_block - 1) / per_block;
@@ -1996,23 +2011,27 @@ int t12_launch(const uint4 *xb, int64_t n_atoms, const DeviceTables *tab, uint4 
   const dim3 g(static_cast<unsigned>(blocks));
   profile_before(s, PLX_PROF_T12);
   if (AT == 4)
-    hipLaunchKernelGGL(t12_kernel<4>, g, dim3(kThreads), 0, s, xb, n_atoms, tab->t2_tiles, tab->t2_pos, tab->t2_rows,
-                       tab->t1_rows, tab->t2_steiner, keys, rows_by_sweep);
+    hipLaunchKernelGGL((t12_kernel<4, LOAD>), g, dim3(kThreads), 0, s, xb, src, sigma, apr, n_atoms, tab->t2_tiles,
+                       tab->t2_pos, tab->t2_rows, tab->t1_rows, tab->t2_steiner, keys, rows_by_sweep);
   else if (AT == 2)
-    hipLaunchKernelGGL(t12_kernel<2>, g, dim3(kThreads), 0, s, xb, n_atoms, tab->t2_tiles, tab->t2_pos, tab->t2_rows,
-                       tab->t1_rows, tab->t2_steiner, keys, rows_by_sweep);
+    hipLaunchKernelGGL((t12_kernel<2, LOAD>), g, dim3(kThreads), 0, s, xb, src, sigma, apr, n_atoms, tab->t2_tiles,
+                       tab->t2_pos, tab->t2_rows, tab->t1_rows, tab->t2_steiner, keys, rows_by_sweep);
   else
-    hipLaunchKernelGGL(t12_kernel<1>, g, dim3(kThreads), 0, s, xb, n_atoms, tab->t2_tiles, tab->t2_pos, tab->t2_rows,
-                       tab->t1_rows, tab->t2_steiner, keys, rows_by_sweep);
+    hipLaunchKernelGGL((t12_kernel<1, LOAD>), g, dim3(kThreads), 0, s, xb, src, sigma, apr, n_atoms, tab->t2_tiles,
+                       tab->t2_pos, tab->t2_rows, tab->t1_rows, tab->t2_steiner, keys, rows_by_sweep);
   profile_after(s, PLX_PROF_T12);
   return check_launch("t12_kernel");
 }
 
-// The structured NN-B path after prep_kernel: t12_kernel (types 1-2), t3_kernel (type 3), pick_kernel.
-int structured_launch(const uint4 *xb, int64_t n_atoms, const DeviceTables *tab, uint4 *keys, int32_t *idx_out,
-                      uint8_t *packed_out, hipStream_t s, int rows_by_sweep) {
+// The structured NN-B path: t12_kernel (types 1-2; LOAD 1 / 2: it also rounds the atoms into xb, so no
+// prep_kernel runs), t3_kernel (type 3), pick_kernel.  Every atom's key halves are written by the two
+// scorers, so the keys need no clearing.
+template <int LOAD>
+int structured_launch(uint4 *xb, const float *src, const float *sigma, int64_t apr, int64_t n_atoms,
+                      const DeviceTables *tab, uint4 *keys, int32_t *idx_out, uint8_t *packed_out, hipStream_t s,
+                      int rows_by_sweep) {
   int st;
-  if ((st = t12_launch(xb, n_atoms, tab, keys, s, rows_by_sweep)) != PLX_OK) return st;
+  if ((st = t12_launch_load<LOAD>(xb, src, sigma, apr, n_atoms, tab, keys, s, rows_by_sweep)) != PLX_OK) return st;
   if ((st = t3_launch(xb, n_atoms, tab, keys, s, rows_by_sweep)) != PLX_OK) return st;
   hipLaunchKernelGGL(pick_kernel, dim3(static_cast<unsigned>((n_atoms + 255) / 256)), dim3(256), 0, s, keys, n_atoms,
                      idx_out, packed_out);
@@ -2035,6 +2054,8 @@ int launch_mode(const float *x, const float *sigma, int64_t apr, int64_t n_atoms
   uint64_t *recs = reinterpret_cast<uint64_t *>(workspace + keys_bytes(n_atoms));
   uint4 *xb = reinterpret_cast<uint4 *>(workspace + keys_bytes(n_atoms) + recs_bytes(n_atoms));
   const int s0 = first_pair_slice(n_slices);
+  if constexpr (STRUCT)
+    return structured_launch<FUSED ? 2 : 1>(xb, x, sigma, apr, n_atoms, tab, keys, idx_out, packed_out, s, rows_by_sweep);
   int st;
   if (MODE != kModeP) {
     hipLaunchKernelGGL((prep_kernel<FUSED>), dim3(static_cast<unsigned>((n_atoms * 3 + 255) / 256)), dim3(256), 0, s, x,
@@ -2045,7 +2066,6 @@ int launch_mode(const float *x, const float *sigma, int64_t apr, int64_t n_atoms
                        n_atoms);
     if ((st = check_launch("clear_keys_kernel")) != PLX_OK) return st;
   }
-  if constexpr (STRUCT) return structured_launch(xb, n_atoms, tab, keys, idx_out, packed_out, s, rows_by_sweep);
   profile_before(s);
   const uint8_t *tiles = MODE == kModeP ? tab->sw_raw_tiles : tab->sw_bf16_tiles;
   const void *operand = MODE == kModeP ? static_cast<const void *>(x) : static_cast<const void *>(xb);
@@ -2156,7 +2176,7 @@ int launch_batch_mode(const RequantItem *items, int n_items, const DeviceTables 
     off += n;
   }
   if constexpr (STRUCT) {
-    if ((st = t12_launch(xb, total, tab, keys, s, 0)) != PLX_OK) return st;
+    if ((st = t12_launch_load<0>(xb, nullptr, nullptr, 1, total, tab, keys, s, 0)) != PLX_OK) return st;
     if ((st = t3_launch(xb, total, tab, keys, s, 0)) != PLX_OK) return st;
   } else {
     profile_before(s);
