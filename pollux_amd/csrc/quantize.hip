@@ -527,10 +527,9 @@ __global__ __launch_bounds__(kThreads, MODE == kModeB ? 3 : 2) void nn_kernel(co
 //           bucket found so far, whichever is highest: |T| >= lo(bucket) -
 //           eb - margin -- appends one 4-byte entry (atom, tile, lane
 //           quarter, 4-bit mask of its outputs) to the wave's list in LDS;
-//           at a stage end once the list holds a round of 64 entries, when
-//           it is full and at the end of the pass the wave evaluates it, one
-//           flagged word per lane per round (an entry with flagged words left
-//           goes back on the list): each flagged representative gets S recomputed from the atom's
+//           when the list is nearly full and at the end of the pass the wave
+//           evaluates it, one flagged word per lane per round (an entry with
+//           work left goes back on the list): each flagged representative gets S recomputed from the atom's
 //           bf16 coordinates, and it and its complement, each when its S +
 //           e(w) reaches the floor, get their 24 positions scored,
 //           the best bucket M3 per atom is kept by an LDS atomic max, words
@@ -873,8 +872,11 @@ __global__ __launch_bounds__(kThreads, 4) void t3_kernel(const uint4 *__restrict
         cnt += __popcll(msk);
       }
     }
-    // the list is evaluated once it fills a round of lanes, and at the end of each pass
-    if (cnt >= 64 || g == kT3Stages - 1 || g == 2 * kT3Stages - 1) flush(pass);
+    // the list is evaluated when it is nearly full (in the tile loop) and at the end of each pass: the
+    // floor from the pair key leaves little for rising thresholds to gain, and fuller rounds keep the
+    // lanes busy and the block's waves in step at the barriers (4.93 -> 4.64 ms against a flush at
+    // every stage end holding 64 entries, config 4)
+    if (g == kT3Stages - 1 || g == 2 * kT3Stages - 1) flush(pass);
     if (pass == 1) {
       // the thresholds rise with the best buckets found so far (this wave's own atoms: no barrier needed)
 #pragma unroll
@@ -1256,22 +1258,21 @@ __global__ __launch_bounds__(kThreads, 4) void t12_kernel(uint4 *__restrict__ xb
   if (lane < NA) {
     const int al = lane;
     const uint16_t *xh = reinterpret_cast<const uint16_t *>(xw[wave][al]);
-    float tv[5] = {-1.f, -1.f, -1.f, -1.f, -1.f};
-    uint32_t tp[5] = {0u, 1u, 2u, 3u, 4u};
-    for (int i = 0; i < kDim; ++i) {  // insertion into the top 5 (descending), branch-free
-      float cv = __uint_as_float((static_cast<uint32_t>(xh[i]) & 0x7FFFu) << 16);
-      uint32_t cp = static_cast<uint32_t>(i);
+    // the 5 largest keys |x| bits << 5 | position (bf16 magnitudes order as integers; distinct keys), kept
+    // descending by a max / min pair per slot
+    uint32_t tk[5] = {0u, 0u, 0u, 0u, 0u};
+    for (int i = 0; i < kDim; ++i) {
+      uint32_t k = (static_cast<uint32_t>(xh[i]) & 0x7FFFu) << 5 | static_cast<uint32_t>(i);
 #pragma unroll
-      for (int k = 0; k < 5; ++k) {
-        const bool sw = cv > tv[k];
-        const float t = tv[k];
-        const uint32_t u = tp[k];
-        tv[k] = sw ? cv : t;
-        tp[k] = sw ? cp : u;
-        cv = sw ? t : cv;
-        cp = sw ? u : cp;
+      for (int t = 0; t < 5; ++t) {
+        const uint32_t hi = max(tk[t], k);
+        k = min(tk[t], k);
+        tk[t] = hi;
       }
     }
+    uint32_t tp[5];
+#pragma unroll
+    for (int t = 0; t < 5; ++t) tp[t] = tk[t] & 31u;
     // positions ascending (a 5-input sorting network), then the octad of that subset
     constexpr int kNet[9][2] = {{0, 1}, {3, 4}, {2, 4}, {2, 3}, {0, 3}, {0, 2}, {1, 4}, {1, 3}, {1, 2}};
 #pragma unroll
@@ -1280,7 +1281,7 @@ __global__ __launch_bounds__(kThreads, 4) void t12_kernel(uint4 *__restrict__ xb
       tp[kNet[k][0]] = lo;
       tp[kNet[k][1]] = hi;
     }
-    // (a non-finite atom can leave a default position twice: clamp the rank into the table)
+    // (the keys are distinct, so the positions are; the rank is clamped into the table all the same)
     const uint32_t o = t2_steiner[min(subset5_rank(tp), static_cast<uint32_t>(kT2Subsets5 - 1))];
     float xa[8];
     const uint32_t sg = t2_load(xw[wave][al], t2_pos[o], xa);
