@@ -1977,12 +1977,12 @@ size_t recs_bytes(int64_t n_atoms) {
 // t3_kernel: atom tiles per wave by launch size, so small launches still fill the chip.
 int t3_launch(const uint4 *xb, int64_t n_atoms, const DeviceTables *tab, uint4 *keys, hipStream_t s,
               int rows_by_sweep) {
-  // 4 atom tiles per wave from 131,072 atoms: 39 KB of LDS (8-tile stages) and 128 VGPRs, 4 blocks (16
-  // waves) per CU.  The evaluation is latency-bound, so occupancy decides: on the config-4 launch 8 tiles
-  // per wave at 2 blocks per CU measured 14.9 ms, 4 tiles at 3 blocks (16-tile stages) 12.5, 4 tiles at 4
-  // blocks 11.5, 2 tiles at 4 blocks 13.0; the representative words are read from global memory (L1 / L2)
-  // to leave the LDS to the stages and lists.
-  const int AT = n_atoms >= 131072 ? 4 : n_atoms >= 32768 ? 2 : 1;
+  // 4 atom tiles per wave from 131,072 atoms, 2 from 98,304, else 1 (measured per launch size: 55,296
+  // atoms take 35 + 42 us in t12 + t3 at 1 tile, 39 + 47 at 2; from 165,888 atoms 4 tiles are fastest).
+  // At 4 tiles: 40 KB of LDS (8-tile stages) and 128 VGPRs, 4 blocks (16 waves) per CU, which the
+  // kernel's stalls need (8 tiles per wave at 2 blocks per CU was 30% slower); the representative words
+  // are read from global memory (L1 / L2) to leave the LDS to the stages and lists.
+  const int AT = n_atoms >= 131072 ? 4 : n_atoms >= 98304 ? 2 : 1;
   const int64_t per_block = static_cast<int64_t>(kWaves) * AT * 16;
   const int64_t blocks = (n_atoms + per_block - 1) / per_block;
   if (blocks > 0x7FFFFFFFll) return fail(PLX_EINVAL, "quantize: %lld atoms exceed one launch", static_cast<long long>(n_atoms));
@@ -2005,7 +2005,7 @@ int t3_launch(const uint4 *xb, int64_t n_atoms, const DeviceTables *tab, uint4 *
 template <int LOAD>
 int t12_launch_load(uint4 *xb, const float *src, const float *sigma, int64_t apr, int64_t n_atoms,
                     const DeviceTables *tab, uint4 *keys, hipStream_t s, int rows_by_sweep) {
-  const int AT = n_atoms >= 131072 ? 4 : n_atoms >= 32768 ? 2 : 1;
+  const int AT = n_atoms >= 131072 ? 4 : n_atoms >= 98304 ? 2 : 1;
   const int64_t per_block = static_cast<int64_t>(kWaves) * AT * 16;
   const int64_t blocks = (n_atoms + per_block - 1) / per_block;
   if (blocks > 0x7FFFFFFFll) return fail(PLX_EINVAL, "quantize: %lld atoms exceed one launch", static_cast<long long>(n_atoms));
