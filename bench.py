@@ -1083,6 +1083,13 @@ def main() -> int:
             roofline["valu_issue_frac"] = t3c.get("valu_issue_frac")
             roofline["valu_note"] = counters.get("valu_note")
         roofline["kernel_step_share"] = kernel_avg_ms / ms_per_step
+        # the whole step priced on the dense contraction's work (2 * 24 * 196,560 flops per atom, the
+        # figure the dense sweep's roofline uses): above 1 means the step beats the dense MFMA roofline
+        roofline["dense_equivalent_frac"] = FLOP_PER_ATOM * atoms / (ms_per_step / 1e3) / PEAK_BF16_FLOPS
+        roofline["dense_equivalent_note"] = (
+            "the step's atoms/s x 9,434,880 flops per atom (every code's 24-term dot product) over the 2.5 PF "
+            "dense bf16 peak: the dense sweep's ceiling is 2.65e8 atoms/s, which the structured scorers exceed "
+            "because they skip ~99% of the codes exactly, not by computing faster")
         roofline["t12_kernel_avg_ms"] = t12_ms
         roofline["t12_kernel_step_share"] = t12_ms / ms_per_step
         roofline["t12_kernel_mfma_frac"] = T12_FLOP_PER_ATOM * atoms / (t12_ms / 1e3) / PEAK_BF16_FLOPS
