@@ -543,7 +543,9 @@ __global__ __launch_bounds__(kThreads, MODE == kModeB ? 3 : 2) void nn_kernel(co
 //           whose entries were lost, from a second sweep with their
 //           thresholds at M3 (the other atoms' thresholds: +inf).
 // The atom's key gets (M3 << 16, lowest row at M3), or 0 when no type-3 code
-// reaches 2.0; pick_kernel compares it with the pair key.
+// reaches 2.0; pick_kernel compares it with the pair key.  (An atom with a NaN
+// or infinite coordinate carries t12_kernel's marker pair key, whose NaN
+// threshold leaves it no candidates here.)
 // Buckets are taken by round-half-up like the dense sweep's, and every score
 // is an fp32 sum of exact products plus one rounding for the bonus, so the
 // answer equals the exact-score answer off near-ties (oracle/nn.py).
@@ -977,6 +979,7 @@ constexpr int kT2StageBytes = kT2ST * kTileBytes;  // 6,144
 constexpr int kT2StageVecs = kT2StageBytes / 16;   // 384
 constexpr int kT2Cap = 384;                        // candidate entries per wave (4 bytes each)
 constexpr int kT2Surv = 256;                       // survivor entries per wave (4 bytes each)
+constexpr uint32_t kNonFinite = 0xFFFFFFFFu;       // pair key of an atom with a NaN or infinite coordinate
 constexpr float kC1 = 1.4140625f;                  // bf16(4s)
 constexpr float kC2 = 0.70703125f;                 // bf16(2s)
 static_assert(kT2StageVecs % 64 == 0, "octad stage splits into whole wave loads");
@@ -1110,6 +1113,7 @@ __global__ __launch_bounds__(kThreads, 4) void t12_kernel(uint4 *__restrict__ xb
   bf16x8 b[AT];
   float mg[AT], v1[AT];
   uint32_t m1b[AT];  // the best type-1 bucket (0 below 2.0)
+  uint32_t nonfinite = 0u;  // bit at: the atom has a NaN or infinite coordinate, or sum |x| overflows fp32
 #pragma unroll
   for (int at = 0; at < AT; ++at) {
     const int64_t a = wave_atom0 + at * 16 + j;
@@ -1145,6 +1149,9 @@ __global__ __launch_bounds__(kThreads, 4) void t12_kernel(uint4 *__restrict__ xb
       t1 = fmaxf(t1, o1);
       ax += __shfl_xor(ax, sh, 64);
     }
+    // sum |x| is NaN or infinite exactly when a coordinate is (or the sum overflows fp32): such an atom
+    // goes to the origin
+    nonfinite |= (ax <= 3.402823466e38f ? 0u : 1u) << at;
     const float s1 = t1 * kC1 + t2 * kC1;  // exact products, one rounding
     const uint32_t bk = s1 > 0.f ? t3_bucket(s1) : 0u;
     m1b[at] = bk >= 0x4000u ? bk : 0u;
@@ -1396,8 +1403,11 @@ __global__ __launch_bounds__(kThreads, 4) void t12_kernel(uint4 *__restrict__ xb
       const uint32_t M = st_m[wave][at * 16 + j];
       uint32_t r = st_r[wave][at * 16 + j];
       if (M >= 0x4000u && m1b[at] == M) r = min(r, t1_rows_at(xw[wave][at * 16 + j], v1[at], M, t1_rows));
+      // (a non-finite atom: the marker kNonFinite, which pick_kernel maps to the origin as the dense sweep
+      // does; as a pair bucket it gives t3_kernel a NaN threshold, hence no candidates)
       reinterpret_cast<uint2 *>(&keys[a])[1] =
-          M >= 0x4000u && r != 0xFFFFFFFFu ? make_uint2(M << 16, r) : make_uint2(0u, 0u);
+          (nonfinite >> at) & 1u ? make_uint2(kNonFinite, 0u)
+                                 : M >= 0x4000u && r != 0xFFFFFFFFu ? make_uint2(M << 16, r) : make_uint2(0u, 0u);
     }
   }
 }
@@ -1584,6 +1594,7 @@ __global__ __launch_bounds__(256) void resolve_kernel(const uint4 *__restrict__ 
       }
     }
     double nrm2 = 0.0;
+    bool nonfinite = false;  // NN-B / NN-T: a NaN or infinite coordinate (its index is the origin)
 #pragma unroll
     for (int qq = 0; qq < 3; ++qq) {
       if constexpr (MODE == kModeP) {
@@ -1595,12 +1606,17 @@ __global__ __launch_bounds__(256) void resolve_kernel(const uint4 *__restrict__ 
           nrm2 = fma(static_cast<double>(v[e]), static_cast<double>(v[e]), nrm2);
         }
       } else {
-        *reinterpret_cast<uint4 *>(xs + tid * XW + 4 * qq) = xb[a * 3 + qq];  // bf16 pairs from prep_kernel
+        const uint4 w = xb[a * 3 + qq];  // bf16 pairs from prep_kernel
+        *reinterpret_cast<uint4 *>(xs + tid * XW + 4 * qq) = w;
+        const uint32_t wv[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+          nonfinite |= (wv[k] & 0x7F80u) == 0x7F80u || (wv[k] & 0x7F800000u) == 0x7F800000u;
       }
     }
     // NN-P's origin rule (pack.py:174): |x|_2 < fp32(1e-8); no scan needed
     const bool p_snap = MODE == kModeP && sqrt(nrm2) < static_cast<double>(__uint_as_float(kEpsBits));
-    active = M != 0u && (lanes[0] | lanes[1] | lanes[2] | lanes[3] | lanes[4]) != 0u && !p_snap;
+    active = M != 0u && (lanes[0] | lanes[1] | lanes[2] | lanes[3] | lanes[4]) != 0u && !p_snap && !nonfinite;
   }
   Ms[tid] = M;
 
@@ -1899,8 +1915,8 @@ __global__ __launch_bounds__(256) void resolve_kernel(const uint4 *__restrict__ 
 
 // NN-B with the structured scorers: the higher of the pair key (t12_kernel)
 // and the type-3 key (t3_kernel), the lower row on equal buckets, the origin
-// when neither reaches 2.0; then the int32 index and, optionally, the packed
-// 9-byte groups.
+// when neither reaches 2.0 or the atom has a NaN or infinite coordinate; then
+// the int32 index and, optionally, the packed 9-byte groups.
 __global__ __launch_bounds__(256) void pick_kernel(const uint4 *__restrict__ keys, int64_t n_atoms,
                                                    int32_t *__restrict__ idx_out, uint8_t *__restrict__ packed_out) {
   __shared__ int32_t ids[256];
@@ -1913,7 +1929,7 @@ __global__ __launch_bounds__(256) void pick_kernel(const uint4 *__restrict__ key
     const uint4 k = keys[a];
     const uint32_t M3 = k.x >> 16, M2 = k.z >> 16, M = max(M2, M3);
     uint32_t row = kNone;
-    if (M >= 0x4000u) {
+    if (M >= 0x4000u && k.z != kNonFinite) {  // (a non-finite atom: the origin)
       if (M3 == M) row = k.y;
       if (M2 == M) row = min(row, k.w);
     }

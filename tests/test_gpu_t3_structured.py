@@ -168,3 +168,21 @@ def test_midpoints_among_ordinary_atoms(dev):
     got = _compare(dev, x, "midpoints among c4 atoms", max_near=0.01)
     r = castor.quantize_indices(x.to(dev), mode="bf16-rows-sweep").long().cpu()
     assert torch.equal(got, r), int((got != r).sum())
+
+
+def test_non_finite_atoms_go_to_the_origin(dev):
+    # a NaN or infinite coordinate: both NN-B paths give the origin (the reference's torch ops give the first
+    # row whose score is NaN, outside any tested domain); the other atoms of the launch are unaffected
+    x = _c4_atoms(5000, 20)
+    ref = castor.quantize_indices(x.to(dev), mode="bf16").long().cpu()
+    bad = torch.arange(0, 5000, 97)
+    x[bad[0::3], 5] = float("nan")
+    x[bad[1::3], 7] = float("inf")
+    x[bad[2::3], 11] = -float("inf")
+    x[bad[:5]] = float("nan")
+    s = castor.quantize_indices(x.to(dev), mode="bf16").long().cpu()
+    d = castor.quantize_indices(x.to(dev), mode="bf16-dense").long().cpu()
+    assert torch.all(s[bad] == 0) and torch.all(d[bad] == 0)
+    keep = torch.ones(5000, dtype=torch.bool)
+    keep[bad] = False
+    assert torch.equal(s[keep], ref[keep])
