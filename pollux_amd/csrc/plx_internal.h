@@ -53,6 +53,7 @@ constexpr int kT3Words = 2 * kT3Reps;
 constexpr int kT2Octads = 759;
 constexpr int kT2Tiles = 48;  // 768 octad slots
 constexpr int kT2Subsets5 = 42504;  // C(24, 5): each in exactly one octad
+constexpr int kT3DecWords = 4096 + 12 + 24;  // Golay decoder: leaders by syndrome, basis, position syndromes
 
 // fp32 constants of the reference (castor.py:47,50,68; castor.py:522; pack.py:164)
 constexpr uint32_t kLeechScaleBits = 0x3EB504F3u;  // fp32(1/sqrt 8)
@@ -84,6 +85,7 @@ struct DeviceTables {
   uint32_t *t2_rows = nullptr;       // [759][128] codebook row of the octad code with sign pattern p
   uint32_t *t1_rows = nullptr;       // [24][24][4] codebook row of the type-1 code at i < j, minus bits
   uint16_t *t2_steiner = nullptr;    // [kT2Subsets5] the octad holding each 5-subset (colex rank)
+  uint32_t *t3_dec = nullptr;        // [kT3DecWords] Golay coset leaders by syndrome, basis words, position syndromes
 };
 
 // Plane tables (tables.cpp; host, built once): the codebook rows take only a

@@ -1092,6 +1092,7 @@ __global__ __launch_bounds__(kThreads, 4) void t12_kernel(uint4 *__restrict__ xb
                                                           const uint32_t *__restrict__ t2_rows,
                                                           const uint32_t *__restrict__ t1_rows,
                                                           const uint16_t *__restrict__ t2_steiner,
+                                                          const uint32_t *__restrict__ t3_dec,
                                                           uint4 *__restrict__ keys, int rows_by_sweep) {
   constexpr int NA = AT * 16;  // atoms per wave
   static_assert(NA <= 128 && NA <= 64, "entry layout: 7 bits of atom; one lane per atom at set-up");
@@ -1102,6 +1103,7 @@ __global__ __launch_bounds__(kThreads, 4) void t12_kernel(uint4 *__restrict__ xb
   __shared__ uint32_t st_m[kWaves][NA], st_r[kWaves][NA];
   __shared__ uint32_t st_o[kWaves][NA];  // the octad of the atom's 5 largest |x| (scored at set-up)
   __shared__ uint32_t st_o2[kWaves][NA];  // the octad of its 4 largest and its 6th largest |x| (set-up)
+  __shared__ uint32_t st_f[kWaves][NA];   // the type-3 floor: bucket of the best decoded type-3 code (or 0)
   __shared__ uint32_t surv_n[kWaves];
   __shared__ uint32_t st_ovf[kWaves][2];  // atoms (bits) whose survivor list lost an entry: rows by pass 2
 
@@ -1271,14 +1273,57 @@ __global__ __launch_bounds__(kThreads, 4) void t12_kernel(uint4 *__restrict__ xb
     // the 6 largest keys |x| bits << 5 | position (bf16 magnitudes order as integers; distinct keys), kept
     // descending by a max / min pair per slot
     uint32_t tk[6] = {0u, 0u, 0u, 0u, 0u, 0u};
+    uint32_t ysg = 0u, lk0 = 0xFFFFFFFFu, lk1 = 0xFFFFFFFFu;  // sign bits; the two smallest keys
     for (int i = 0; i < kDim; ++i) {
-      uint32_t k = (static_cast<uint32_t>(xh[i]) & 0x7FFFu) << 5 | static_cast<uint32_t>(i);
+      const uint32_t h = xh[i];
+      uint32_t k = (h & 0x7FFFu) << 5 | static_cast<uint32_t>(i);
+      ysg |= (h >> 15) << i;
+      lk1 = min(lk1, max(lk0, k));
+      lk0 = min(lk0, k);
 #pragma unroll
       for (int t = 0; t < 6; ++t) {
         const uint32_t hi = max(tk[t], k);
         k = min(tk[t], k);
         tk[t] = hi;
       }
+    }
+    // The type-3 floor (Chase decoding): the signs of x as a word, and that word with its least reliable
+    // position (smallest |x|), its second, or both flipped, each decoded to the nearest Golay word by
+    // syndrome (t3_dec); each word's type-3 codes with the -3 at one of the 6 largest |x| scored exactly
+    // as t3_kernel scores them (t3_dot, then one fma).  The best bucket is a type-3 code's, so the atom's
+    // type-3 best reaches it: octads below it cannot win (same answer, fewer candidates; config-4 atoms
+    // simulated: 0.58 -> 0.40 of the atom-tile x octad-tile steps hold a candidate), and t3_kernel
+    // starts from it (0.24 -> 0.19 of its steps).
+    {
+      uint32_t xr[12];
+#pragma unroll
+      for (int d = 0; d < 12; ++d) xr[d] = xw[wave][al][d];
+      uint32_t syn = 0u;
+#pragma unroll
+      for (int jj = 0; jj < 12; ++jj) syn |= static_cast<uint32_t>(__popc(ysg & t3_dec[4096 + jj]) & 1) << jj;
+      const uint32_t l0 = lk0 & 31u, l1 = lk1 & 31u;
+      const uint32_t c0 = t3_dec[4108 + l0], c1 = t3_dec[4108 + l1];
+      uint32_t tpos[6];
+      float xp[6];
+#pragma unroll
+      for (int c = 0; c < 6; ++c) {
+        tpos[c] = tk[c] & 31u;
+        xp[c] = __uint_as_float(static_cast<uint32_t>(xh[tpos[c]]) << 16);
+      }
+      float best = -__builtin_inff();
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const uint32_t fm = (t & 1 ? 1u << l0 : 0u) | (t & 2 ? 1u << l1 : 0u);
+        const uint32_t sy = syn ^ (t & 1 ? c0 : 0u) ^ (t & 2 ? c1 : 0u);
+        const uint32_t w = (ysg ^ fm ^ t3_dec[sy]) & 0xFFFFFFu;
+        const bool sg = (w >> 23) & 1u;
+        const float D = t3_dot(xr, sg ? w ^ 0xFFFFFFu : w);
+        const float S = sg ? -D : D;
+#pragma unroll
+        for (int c = 0; c < 6; ++c) best = fmaxf(best, fmaf(-xp[c], ((w >> tpos[c]) & 1u) ? kT3Beta : kT3Alpha, S));
+      }
+      const uint32_t f3 = best > 0.f ? t3_bucket(best) : 0u;
+      st_f[wave][al] = f3 >= 0x4000u ? f3 : 0u;
     }
     uint32_t tp[5], tq[5];
 #pragma unroll
@@ -1321,7 +1366,7 @@ __global__ __launch_bounds__(kThreads, 4) void t12_kernel(uint4 *__restrict__ xb
     }
   }
 #pragma unroll
-  for (int at = 0; at < AT; ++at) set_thr(at, st_m[wave][at * 16 + j]);
+  for (int at = 0; at < AT; ++at) set_thr(at, max(st_m[wave][at * 16 + j], st_f[wave][at * 16 + j]));
   int g_end = kT2Stages;
   for (int g = 0; g < g_end; ++g) {
     const int pass = 1 + g / kT2Stages, buf = g & 1;
@@ -1333,7 +1378,9 @@ __global__ __launch_bounds__(kThreads, 4) void t12_kernel(uint4 *__restrict__ xb
         const int al = at * 16 + j;
         const bool redo = rows_by_sweep != 0 || ((st_ovf[wave][al >> 5] >> (al & 31)) & 1u) != 0u;
         const uint32_t M = st_m[wave][al];
-        thr[at] = redo && M >= 0x4000u ? __uint_as_float((M << 16) - 0x8000u) - mg[at] : __builtin_inff();
+        // (an atom below its type-3 floor needs no pair rows)
+        thr[at] = redo && M >= 0x4000u && M >= st_f[wave][al] ? __uint_as_float((M << 16) - 0x8000u) - mg[at]
+                                                              : __builtin_inff();
       }
     }
     const uint8_t *L = stg[buf] + a_off;
@@ -1367,7 +1414,7 @@ __global__ __launch_bounds__(kThreads, 4) void t12_kernel(uint4 *__restrict__ xb
     if (pass == 1) {
       compact();
 #pragma unroll
-      for (int at = 0; at < AT; ++at) set_thr(at, st_m[wave][at * 16 + j]);
+      for (int at = 0; at < AT; ++at) set_thr(at, max(st_m[wave][at * 16 + j], st_f[wave][at * 16 + j]));
     }
     if (g == kT2Stages - 1) {
       if (__syncthreads_or(rows_by_sweep != 0 || (st_ovf[wave][0] | st_ovf[wave][1]) != 0u)) {
@@ -1387,6 +1434,7 @@ __global__ __launch_bounds__(kThreads, 4) void t12_kernel(uint4 *__restrict__ xb
       const uint32_t se = surv[wave][i];
       const int al = static_cast<int>(se & 0x7Fu);
       if (rows_by_sweep != 0 || ((st_ovf[wave][al >> 5] >> (al & 31)) & 1u) != 0u) continue;
+      if (st_m[wave][al] < st_f[wave][al]) continue;  // (below the type-3 floor: no pair rows needed)
       const uint32_t o = (se >> 7) & 0x3FFu;
       float xa[8];
       const uint32_t sg = t2_load(xw[wave][al], t2_pos[o], xa);
@@ -1400,14 +1448,18 @@ __global__ __launch_bounds__(kThreads, 4) void t12_kernel(uint4 *__restrict__ xb
     for (int at = 0; at < AT; ++at) {
       const int64_t a = wave_atom0 + at * 16 + j;
       if (a >= n_atoms) continue;
-      const uint32_t M = st_m[wave][at * 16 + j];
+      const uint32_t M = st_m[wave][at * 16 + j], F = st_f[wave][at * 16 + j];
       uint32_t r = st_r[wave][at * 16 + j];
-      if (M >= 0x4000u && m1b[at] == M) r = min(r, t1_rows_at(xw[wave][at * 16 + j], v1[at], M, t1_rows));
+      if (M >= 0x4000u && M >= F && m1b[at] == M) r = min(r, t1_rows_at(xw[wave][at * 16 + j], v1[at], M, t1_rows));
       // (a non-finite atom: the marker kNonFinite, which pick_kernel maps to the origin as the dense sweep
-      // does; as a pair bucket it gives t3_kernel a NaN threshold, hence no candidates)
+      // does; as a pair bucket it gives t3_kernel a NaN threshold, hence no candidates.  An atom whose
+      // type-3 floor is above its best pair bucket: the floor without a row, as t3_kernel's starting best,
+      // which its type-3 best reaches, so pick_kernel takes t3_kernel's row)
       reinterpret_cast<uint2 *>(&keys[a])[1] =
           (nonfinite >> at) & 1u ? make_uint2(kNonFinite, 0u)
-                                 : M >= 0x4000u && r != 0xFFFFFFFFu ? make_uint2(M << 16, r) : make_uint2(0u, 0u);
+          : F > M               ? make_uint2(F << 16, 0xFFFFFFFFu)
+          : M >= 0x4000u && r != 0xFFFFFFFFu ? make_uint2(M << 16, r)
+                                             : make_uint2(0u, 0u);
     }
   }
 }
@@ -2045,13 +2097,13 @@ int t12_launch_load(uint4 *xb, const float *src, const float *sigma, int64_t apr
   profile_before(s, PLX_PROF_T12);
   if (AT == 4)
     hipLaunchKernelGGL((t12_kernel<4, LOAD>), g, dim3(kThreads), 0, s, xb, src, sigma, apr, n_atoms, tab->t2_tiles,
-                       tab->t2_pos, tab->t2_rows, tab->t1_rows, tab->t2_steiner, keys, rows_by_sweep);
+                       tab->t2_pos, tab->t2_rows, tab->t1_rows, tab->t2_steiner, tab->t3_dec, keys, rows_by_sweep);
   else if (AT == 2)
     hipLaunchKernelGGL((t12_kernel<2, LOAD>), g, dim3(kThreads), 0, s, xb, src, sigma, apr, n_atoms, tab->t2_tiles,
-                       tab->t2_pos, tab->t2_rows, tab->t1_rows, tab->t2_steiner, keys, rows_by_sweep);
+                       tab->t2_pos, tab->t2_rows, tab->t1_rows, tab->t2_steiner, tab->t3_dec, keys, rows_by_sweep);
   else
     hipLaunchKernelGGL((t12_kernel<1, LOAD>), g, dim3(kThreads), 0, s, xb, src, sigma, apr, n_atoms, tab->t2_tiles,
-                       tab->t2_pos, tab->t2_rows, tab->t1_rows, tab->t2_steiner, keys, rows_by_sweep);
+                       tab->t2_pos, tab->t2_rows, tab->t1_rows, tab->t2_steiner, tab->t3_dec, keys, rows_by_sweep);
   profile_after(s, PLX_PROF_T12);
   return check_launch("t12_kernel");
 }

@@ -62,6 +62,14 @@
 //                5 positions lie in exactly one octad), by the subset's colex
 //                rank C(p0,1) + C(p1,2) + ... + C(p4,5), p0 < ... < p4
 //                (42,504 entries, 85,008 B).
+// t3_dec         a syndrome decoder of the extended Golay code for
+//                t12_kernel's type-3 floor: [0, 4096) the coset leader of
+//                each syndrome (a least-weight pattern, the first in order of
+//                weight, then colex order of its positions), [4096, 4108) the
+//                12 basis words whose parities with a pattern are its
+//                syndrome bits (the code is self-dual: every codeword has
+//                syndrome 0), [4108, 4132) the syndrome of each single
+//                position (16,528 B).
 
 #include <algorithm>
 #include <cstring>
@@ -268,6 +276,57 @@ int build(int dev, DeviceTables *t) {
     for (uint16_t v : t2_steiner)
       if (v == 0xFFFFu) return fail(PLX_EINVAL, "5 positions in no octad");
   }
+  std::vector<uint32_t> t3_dec(static_cast<size_t>(kT3DecWords), 0xFFFFFFFFu);
+  {
+    // basis: the first 12 words, in table order, independent of those before them
+    const uint32_t *golay = golay_words_host();
+    uint32_t basis[12];
+    int nb = 0;
+    std::vector<uint8_t> span(1u << 24, 0);
+    std::vector<uint32_t> members{0u};
+    span[0] = 1;
+    for (int m = 0; m < 4096 && nb < 12; ++m) {
+      const uint32_t w = golay[m];
+      if (span[w]) continue;
+      basis[nb++] = w;
+      const size_t k = members.size();
+      for (size_t i = 0; i < k; ++i) {
+        members.push_back(members[i] ^ w);
+        span[members[i] ^ w] = 1;
+      }
+    }
+    if (nb != 12) return fail(PLX_EINVAL, "Golay basis of %d words", nb);
+    auto syndrome = [&](uint32_t e) {
+      uint32_t sy = 0u;
+      for (int j = 0; j < 12; ++j) sy |= static_cast<uint32_t>(__builtin_popcount(e & basis[j]) & 1) << j;
+      return sy;
+    };
+    for (int m = 0; m < 4096; ++m)
+      if (syndrome(golay[m]) != 0u) return fail(PLX_EINVAL, "Golay word with a nonzero syndrome");
+    // leaders by weight 0..4, positions in colex order within a weight (the covering radius is 4)
+    int found = 0;
+    for (int wt = 0; wt <= 4 && found < 4096; ++wt) {
+      int pos[4] = {0, 1, 2, 3};
+      while (true) {
+        uint32_t e = 0u;
+        for (int k = 0; k < wt; ++k) e |= 1u << pos[k];
+        const uint32_t sy = syndrome(e);
+        if (t3_dec[sy] == 0xFFFFFFFFu) {
+          t3_dec[sy] = e;
+          ++found;
+        }
+        // next combination of wt positions in colex order
+        int k = 0;
+        while (k < wt && pos[k] + 1 == (k + 1 < wt ? pos[k + 1] : kDim)) ++k;
+        if (k == wt) break;
+        ++pos[k];
+        for (int i = 0; i < k; ++i) pos[i] = i;
+      }
+    }
+    if (found != 4096) return fail(PLX_EINVAL, "Golay syndromes without a leader of weight <= 4: %d", 4096 - found);
+    for (int j = 0; j < 12; ++j) t3_dec[4096 + j] = basis[j];
+    for (int c = 0; c < kDim; ++c) t3_dec[4108 + c] = syndrome(1u << c);
+  }
   int n_t2 = 0, n_t1 = 0;
   for (int code = 1; code < kCodebook; ++code) {
     const int8_t *r = raw + static_cast<size_t>(code) * kDim;
@@ -357,7 +416,7 @@ int build(int dev, DeviceTables *t) {
   void *dt = nullptr, *drt = nullptr, *dsq = nullptr, *dsi = nullptr, *dsa = nullptr, *dr = nullptr, *dg = nullptr,
        *dd = nullptr, *dk = nullptr, *dpi = nullptr, *dcp = nullptr, *dpn = nullptr, *d3t = nullptr, *d3w = nullptr,
        *d3r = nullptr, *dgv = nullptr, *d2t = nullptr, *d2p = nullptr, *d2r = nullptr, *d1r = nullptr,
-       *d2s = nullptr;
+       *d2s = nullptr, *d3d = nullptr;
   const PlaneTables *pt = plane_tables_host();
   if (!pt) return fail(PLX_EINVAL, "the codebook rows take more than %d distinct planes", kMaxPlanes);
   std::vector<uint32_t> pl_pad(pt->ids);  // whole 16-byte vectors (the kernels stage it by uint4)
@@ -402,6 +461,7 @@ int build(int dev, DeviceTables *t) {
       {t2_rows.data(), t2_rows.size() * 4, &d2r},
       {t1_rows.data(), t1_rows.size() * 4, &d1r},
       {t2_steiner.data(), t2_steiner.size() * 2, &d2s},
+      {t3_dec.data(), t3_dec.size() * 4, &d3d},
   };
   int st = PLX_OK;
   for (const Upload &u : ups) {
@@ -439,6 +499,7 @@ int build(int dev, DeviceTables *t) {
   t->t2_rows = static_cast<uint32_t *>(d2r);
   t->t1_rows = static_cast<uint32_t *>(d1r);
   t->t2_steiner = static_cast<uint16_t *>(d2s);
+  t->t3_dec = static_cast<uint32_t *>(d3d);
   t->device = dev;
   return PLX_OK;
 }
