@@ -518,12 +518,15 @@ __global__ __launch_bounds__(kThreads, MODE == kModeB ? 3 : 2) void nn_kernel(co
 // than one bound max_p t_p for all words).  The Golay code holds the
 // complement of every word, S(~w) = -S(w) and T(~w) = -T(w), so one MFMA per
 // 16 representative words tests 32 words: 128 tiles instead of 6,144.
+// p1, p2, the raised coordinates, m3, eb and the margin come per atom from
+// t12_kernel (T3Setup), which ran first.
 // A block of 4 waves holds AT atom tiles of 16 atoms per wave as MFMA B
 // operands and streams the 128 pattern tiles through LDS once (a second time
 // only if a survivor list overflows):
 //   pass 1  every lane whose four outputs hold a word that could reach the
-//           lowest bucket still possible -- the best pair bucket (the pair
-//           key of t12_kernel), 2.0 (the origin rule) and the best type-3
+//           lowest bucket still possible -- the pair key of t12_kernel (the
+//           best pair bucket, or a type-3 code's bucket above it), 2.0 (the
+//           origin rule) and the best type-3
 //           bucket found so far, whichever is highest: |T| >= lo(bucket) -
 //           eb - margin -- appends one 4-byte entry (atom, tile, lane
 //           quarter, 4-bit mask of its outputs) to the wave's list in LDS;
@@ -578,12 +581,59 @@ __device__ __forceinline__ float t3_dot(const uint32_t *xr, uint32_t wb) {
   return S;
 }
 
+// t3_kernel's per-atom set-up, made by t12_kernel (one lane per atom: 64 atoms per wave instruction
+// instead of t3_kernel's 16) and handed over as a 16-byte record.  Position terms t_p = max(-alpha x_p,
+// -beta x_p): the two largest at p1, p2 (ties: the lower position first), x there (x1, x2), the third
+// largest m3.  A word w with bits b1, b2 at p1, p2 has bonus(w) <= e(b1, b2) = max(c1(b1), c2(b2), m3),
+// c(0) = -alpha x, c(1) = -beta x there.  The additive bound eb + k1 P1(w) + k2 P2(w) >= e(b1, b2)
+// (P = +1 for bit 0) with the least eb: eb = max((e00 + e11) / 2, (e01 + e10) / 2), k1 + k2 = (e00 -
+// e11) / 2, k1 - k2 = (e01 - e10) / 2.  The MFMA with x_p1, x_p2 raised by k1 / s, k2 / s (rounded to
+// bf16: h1, h2) gives T(w) = S(w) + k1 P1(w) + k2 P2(w) (and T(~w) = -T(w)), so |T| >= lo(floor) - eb -
+// dl - mg flags every word whose S(w) + e(w) reaches the floor; dl: what the bf16 rounding of the raised
+// coordinates adds; mg = (s sum |x| + |t_p1|) 2^-14: the MFMA's fp32 summation order of T and the score
+// roundings.  Record: ra = (h1 | h2 << 16, p1 | p2 << 8 | mg's bf16 bits rounded up << 16) in the type-3
+// half of the atom's key (t3_kernel reads it, then writes its result there), rb = (m3, eb + dl).
+// add() takes the coordinates in ascending order, record() gives the record.
+struct T3Setup {
+  float m1 = -__builtin_inff(), m2 = -__builtin_inff(), m3 = -__builtin_inff(), x1 = 0.f, x2 = 0.f, ax = 0.f;
+  uint32_t p1 = 0u, p2 = 1u;
+  // coordinate i (ascending) of the atom
+  __device__ __forceinline__ void add(float x, uint32_t i) {
+    const float t = fmaxf(-x * kT3Alpha, -x * kT3Beta);
+    const bool a1 = t > m1, a2 = t > m2;
+    m3 = a2 ? m2 : fmaxf(m3, t);
+    m2 = a1 ? m1 : (a2 ? t : m2);
+    x2 = a1 ? x1 : (a2 ? x : x2);
+    p2 = a1 ? p1 : (a2 ? i : p2);
+    m1 = a1 ? t : m1;
+    x1 = a1 ? x : x1;
+    p1 = a1 ? i : p1;
+    ax += fabsf(x);
+  }
+  __device__ __forceinline__ void record(uint2 &ra, uint2 &rb) const {
+    const float a1 = -x1 * kT3Alpha, b1 = -x1 * kT3Beta, a2 = -x2 * kT3Alpha, b2 = -x2 * kT3Beta;
+    const float e00 = fmaxf(fmaxf(a1, a2), m3), e11 = fmaxf(fmaxf(b1, b2), m3);
+    const float e01 = fmaxf(fmaxf(a1, b2), m3), e10 = fmaxf(fmaxf(b1, a2), m3);
+    const float ebar = fmaxf((e00 + e11) * 0.5f, (e01 + e10) * 0.5f);
+    const float sgm = (e00 - e11) * 0.5f, dlt = (e01 - e10) * 0.5f;
+    const float k1 = (sgm + dlt) * 0.5f, k2 = (sgm - dlt) * 0.5f;
+    const uint32_t h1 = bf16_rne_bits(x1 + k1 / kT3S), h2 = bf16_rne_bits(x2 + k2 / kT3S);
+    const float dl =
+        fabsf((bf16_bits_to_float(h1) - x1) * kT3S - k1) + fabsf((bf16_bits_to_float(h2) - x2) * kT3S - k2);
+    const float mg = (ax * kT3S + fabsf(m1)) * 0x1p-14f;
+    const uint32_t mgb = (__float_as_uint(mg) + 0xFFFFu) >> 16;  // (mg >= 0: rounded up)
+    ra = make_uint2(h1 | h2 << 16, p1 | p2 << 8 | mgb << 16);
+    rb = make_uint2(__float_as_uint(m3), __float_as_uint(ebar + dl));
+  }
+};
+
 template <int AT>
 __global__ __launch_bounds__(kThreads, 4) void t3_kernel(const uint4 *__restrict__ xb, int64_t n_atoms,
                                                          const uint8_t *__restrict__ t3_tiles,
                                                          const uint32_t *__restrict__ t3_words,
                                                          const uint32_t *__restrict__ t3_rows,
-                                                         uint4 *__restrict__ keys, int rows_by_sweep) {
+                                                         uint4 *__restrict__ keys, const uint2 *__restrict__ rec,
+                                                         int rows_by_sweep) {
   constexpr int NA = AT * 16;  // atoms per wave
   static_assert(NA <= 128, "entry layout: 7 bits of atom");
   __shared__ __align__(16) uint8_t stg[2][kT3StageBytes];
@@ -611,75 +661,20 @@ __global__ __launch_bounds__(kThreads, 4) void t3_kernel(const uint4 *__restrict
     uint4 w = make_uint4(0u, 0u, 0u, 0u);
     if (a < n_atoms && q < 3) w = xb[a * 3 + q];
     if (q < 3) *reinterpret_cast<uint4 *>(&xw[wave][at * 16 + j][4 * q]) = w;
-    // the position terms t_p = max(-alpha x_p, -beta x_p): the three largest (the first two at p1, p2, x
-    // there: x1, x2) and sum |x_p| (s * sum |x| bounds every |S|), over this lane's 8 coordinates, then over
-    // the atom's 3 lanes (ties: the lower position first, so every lane of the atom agrees on p1, p2)
+    // The atom's set-up record from t12_kernel (T3Setup: positions p1, p2 of the two largest
+    // position terms, their raised bf16 coordinates, the third largest term m3, eb + dl and the margin);
+    // an atom past the end: the record of a zero atom (p1 = 0, p2 = 1, the rest 0)
+    uint2 ra = make_uint2(0u, 1u << 8), rb = make_uint2(0u, 0u);
+    if (a < n_atoms) {
+      ra = reinterpret_cast<const uint2 *>(&keys[a])[0];
+      rb = rec[a];
+    }
+    const uint32_t p1 = min(ra.y & 31u, 23u), p2 = min((ra.y >> 8) & 31u, 23u);
     uint32_t ww[4] = {w.x, w.y, w.z, w.w};
-    float m1 = -__builtin_inff(), m2 = -__builtin_inff(), m3 = -__builtin_inff(), x1 = 0.f, x2 = 0.f, ax = 0.f;
-    uint32_t p1 = 0u, p2 = 1u;
-    if (q < 3) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float x = __uint_as_float(e & 1 ? ww[e / 2] & 0xFFFF0000u : ww[e / 2] << 16);
-        const float t = fmaxf(-x * kT3Alpha, -x * kT3Beta);
-        const uint32_t p = static_cast<uint32_t>(8 * q + e);
-        const bool a1 = t > m1, a2 = t > m2;
-        m3 = a2 ? m2 : fmaxf(m3, t);
-        m2 = a1 ? m1 : (a2 ? t : m2);
-        x2 = a1 ? x1 : (a2 ? x : x2);
-        p2 = a1 ? p1 : (a2 ? p : p2);
-        m1 = a1 ? t : m1;
-        x1 = a1 ? x : x1;
-        p1 = a1 ? p : p1;
-        ax += fabsf(x);
-      }
-    }
-#pragma unroll
-    for (int sh = 16; sh <= 32; sh <<= 1) {
-      // merge this lane's top 3 with the partner's: (value, position) pairs ordered by value, then position
-      const float o1 = __shfl_xor(m1, sh, 64), o2 = __shfl_xor(m2, sh, 64), o3 = __shfl_xor(m3, sh, 64);
-      const float y1 = __shfl_xor(x1, sh, 64), y2 = __shfl_xor(x2, sh, 64);
-      const uint32_t q1 = static_cast<uint32_t>(__shfl_xor(static_cast<int>(p1), sh, 64));
-      const uint32_t q2 = static_cast<uint32_t>(__shfl_xor(static_cast<int>(p2), sh, 64));
-      auto before = [](float a, uint32_t pa, float b, uint32_t pb) { return a > b || (a == b && pa < pb); };
-      // the merged first: the better of the two firsts
-      const bool t1 = before(o1, q1, m1, p1);
-      const float n1 = t1 ? o1 : m1, r1x = t1 ? y1 : x1;
-      const uint32_t n1p = t1 ? q1 : p1;
-      // the rest of the winner's list and the loser's first compete for the second and third places
-      const float wa = t1 ? o2 : m2, wb = t1 ? o3 : m3, la = t1 ? m1 : o1, lb = t1 ? m2 : o2;
-      const float wax = t1 ? y2 : x2, lax = t1 ? x1 : y1;
-      const uint32_t wap = t1 ? q2 : p2, lap = t1 ? p1 : q1;
-      const bool t2 = before(wa, wap, la, lap);
-      const float n2 = t2 ? wa : la, n2x = t2 ? wax : lax;
-      const uint32_t n2p = t2 ? wap : lap;
-      const float n3 = t2 ? fmaxf(wb, la) : fmaxf(wa, lb);
-      m1 = n1; x1 = r1x; p1 = n1p;
-      m2 = n2; x2 = n2x; p2 = n2p;
-      m3 = n3;
-      ax += __shfl_xor(ax, sh, 64);
-    }
-    // A word w with bits b1, b2 at p1, p2 has bonus(w) <= e(b1, b2) = max(c1(b1), c2(b2), m3), c(0) =
-    // -alpha x, c(1) = -beta x there.  The additive bound eb + k1 P1(w) + k2 P2(w) >= e(b1, b2) (P = +1 for
-    // bit 0) with the least eb: eb = max((e00 + e11) / 2, (e01 + e10) / 2), k1 + k2 = (e00 - e11) / 2,
-    // k1 - k2 = (e01 - e10) / 2.  The MFMA with x_p1, x_p2 raised by k1 / s, k2 / s gives
-    // T(w) = S(w) + k1 P1(w) + k2 P2(w) (and T(~w) = -T(w)), so |T| >= lo(floor) - eb - margins flags
-    // every word whose S(w) + e(w) reaches the floor; dl: what the bf16 rounding of the raised coordinates
-    // adds.
-    const float a1 = -x1 * kT3Alpha, b1 = -x1 * kT3Beta, a2 = -x2 * kT3Alpha, b2 = -x2 * kT3Beta;
-    const float e00 = fmaxf(fmaxf(a1, a2), m3), e11 = fmaxf(fmaxf(b1, b2), m3);
-    const float e01 = fmaxf(fmaxf(a1, b2), m3), e10 = fmaxf(fmaxf(b1, a2), m3);
-    const float ebar = fmaxf((e00 + e11) * 0.5f, (e01 + e10) * 0.5f);
-    const float sgm = (e00 - e11) * 0.5f, dlt = (e01 - e10) * 0.5f;
-    const float k1 = (sgm + dlt) * 0.5f, k2 = (sgm - dlt) * 0.5f;
-    float dl = 0.f;
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
-      const uint32_t pr = r ? p2 : p1;
-      const float xr0 = r ? x2 : x1, kr = r ? k2 : k1;
+      const uint32_t pr = r ? p2 : p1, h = r ? ra.x >> 16 : ra.x & 0xFFFFu;
       if (q < 3 && (pr >> 3) == static_cast<uint32_t>(q)) {
-        const uint32_t h = bf16_rne_bits(xr0 + kr / kT3S);
-        dl += fabsf((bf16_bits_to_float(h) - xr0) * kT3S - kr);
         const uint32_t e = pr & 7u;
 #pragma unroll
         for (int k = 0; k < 4; ++k)
@@ -687,14 +682,11 @@ __global__ __launch_bounds__(kThreads, 4) void t3_kernel(const uint4 *__restrict
             ww[k] = (e & 1u) ? (ww[k] & 0xFFFFu) | (h << 16) : (ww[k] & 0xFFFF0000u) | h;
       }
     }
-#pragma unroll
-    for (int sh = 16; sh <= 32; sh <<= 1) dl += __shfl_xor(dl, sh, 64);
     b[at] = __builtin_bit_cast(bf16x8, make_uint4(ww[0], ww[1], ww[2], ww[3]));
-    // the margin for the MFMA's fp32 summation order of T and the score roundings
-    const float mg = (ax * kT3S + fabsf(m1)) * 0x1p-14f;
-    offs[at] = ebar + dl + mg;
+    const float mg = __uint_as_float(ra.y & 0xFFFF0000u);
+    offs[at] = __uint_as_float(rb.y) + mg;
     if (q == 0) {
-      st_m3[wave][at * 16 + j] = m3;
+      st_m3[wave][at * 16 + j] = __uint_as_float(rb.x);
       st_mg[wave][at * 16 + j] = mg;
       st_p[wave][at * 16 + j][0] = static_cast<uint8_t>(p1);
       st_p[wave][at * 16 + j][1] = static_cast<uint8_t>(p2);
@@ -1093,7 +1085,8 @@ __global__ __launch_bounds__(kThreads, 4) void t12_kernel(uint4 *__restrict__ xb
                                                           const uint32_t *__restrict__ t1_rows,
                                                           const uint16_t *__restrict__ t2_steiner,
                                                           const uint32_t *__restrict__ t3_dec,
-                                                          uint4 *__restrict__ keys, int rows_by_sweep) {
+                                                          uint4 *__restrict__ keys, uint2 *__restrict__ rec,
+                                                          int rows_by_sweep) {
   constexpr int NA = AT * 16;  // atoms per wave
   static_assert(NA <= 128 && NA <= 64, "entry layout: 7 bits of atom; one lane per atom at set-up");
   __shared__ __align__(16) uint8_t stg[2][kT2StageBytes];
@@ -1274,8 +1267,10 @@ __global__ __launch_bounds__(kThreads, 4) void t12_kernel(uint4 *__restrict__ xb
     // descending by a max / min pair per slot
     uint32_t tk[6] = {0u, 0u, 0u, 0u, 0u, 0u};
     uint32_t ysg = 0u, lk0 = 0xFFFFFFFFu, lk1 = 0xFFFFFFFFu;  // sign bits; the two smallest keys
+    T3Setup t3s;  // t3_kernel's set-up record
     for (int i = 0; i < kDim; ++i) {
       const uint32_t h = xh[i];
+      t3s.add(__uint_as_float(h << 16), static_cast<uint32_t>(i));
       uint32_t k = (h & 0x7FFFu) << 5 | static_cast<uint32_t>(i);
       ysg |= (h >> 15) << i;
       lk1 = min(lk1, max(lk0, k));
@@ -1324,6 +1319,15 @@ __global__ __launch_bounds__(kThreads, 4) void t12_kernel(uint4 *__restrict__ xb
       }
       const uint32_t f3 = best > 0.f ? t3_bucket(best) : 0u;
       st_f[wave][al] = f3 >= 0x4000u ? f3 : 0u;
+    }
+    {
+      uint2 ra, rb;
+      t3s.record(ra, rb);
+      const int64_t a = wave_atom0 + al;
+      if (a < n_atoms) {
+        reinterpret_cast<uint2 *>(&keys[a])[0] = ra;
+        rec[a] = rb;
+      }
     }
     uint32_t tp[5], tq[5];
 #pragma unroll
@@ -2059,8 +2063,8 @@ size_t recs_bytes(int64_t n_atoms) {
 }
 
 // t3_kernel: atom tiles per wave by launch size, so small launches still fill the chip.
-int t3_launch(const uint4 *xb, int64_t n_atoms, const DeviceTables *tab, uint4 *keys, hipStream_t s,
-              int rows_by_sweep) {
+int t3_launch(const uint4 *xb, int64_t n_atoms, const DeviceTables *tab, uint4 *keys, const uint2 *rec,
+              hipStream_t s, int rows_by_sweep) {
   // 4 atom tiles per wave from 131,072 atoms, 2 from 98,304, else 1 (measured per launch size: 55,296
   // atoms take 35 + 42 us in t12 + t3 at 1 tile, 39 + 47 at 2; from 165,888 atoms 4 tiles are fastest).
   // At 4 tiles: 40 KB of LDS (8-tile stages) and 128 VGPRs, 4 blocks (16 waves) per CU, which the
@@ -2074,13 +2078,13 @@ int t3_launch(const uint4 *xb, int64_t n_atoms, const DeviceTables *tab, uint4 *
   profile_before(s, PLX_PROF_T3);
   if (AT == 4)
     hipLaunchKernelGGL(t3_kernel<4>, g, dim3(kThreads), 0, s, xb, n_atoms, tab->t3_tiles, tab->t3_words, tab->t3_rows,
-                       keys, rows_by_sweep);
+                       keys, rec, rows_by_sweep);
   else if (AT == 2)
     hipLaunchKernelGGL(t3_kernel<2>, g, dim3(kThreads), 0, s, xb, n_atoms, tab->t3_tiles, tab->t3_words, tab->t3_rows,
-                       keys, rows_by_sweep);
+                       keys, rec, rows_by_sweep);
   else
     hipLaunchKernelGGL(t3_kernel<1>, g, dim3(kThreads), 0, s, xb, n_atoms, tab->t3_tiles, tab->t3_words, tab->t3_rows,
-                       keys, rows_by_sweep);
+                       keys, rec, rows_by_sweep);
   profile_after(s, PLX_PROF_T3);
   return check_launch("t3_kernel");
 }
@@ -2088,7 +2092,7 @@ int t3_launch(const uint4 *xb, int64_t n_atoms, const DeviceTables *tab, uint4 *
 // t12_kernel: atom tiles per wave by launch size, as t3_kernel (38 KB of LDS at 4 tiles per wave).
 template <int LOAD>
 int t12_launch_load(uint4 *xb, const float *src, const float *sigma, int64_t apr, int64_t n_atoms,
-                    const DeviceTables *tab, uint4 *keys, hipStream_t s, int rows_by_sweep) {
+                    const DeviceTables *tab, uint4 *keys, uint2 *rec, hipStream_t s, int rows_by_sweep) {
   const int AT = n_atoms >= 131072 ? 4 : n_atoms >= 98304 ? 2 : 1;
   const int64_t per_block = static_cast<int64_t>(kWaves) * AT * 16;
   const int64_t blocks = (n_atoms + per_block - 1) / per_block;
@@ -2097,13 +2101,13 @@ int t12_launch_load(uint4 *xb, const float *src, const float *sigma, int64_t apr
   profile_before(s, PLX_PROF_T12);
   if (AT == 4)
     hipLaunchKernelGGL((t12_kernel<4, LOAD>), g, dim3(kThreads), 0, s, xb, src, sigma, apr, n_atoms, tab->t2_tiles,
-                       tab->t2_pos, tab->t2_rows, tab->t1_rows, tab->t2_steiner, tab->t3_dec, keys, rows_by_sweep);
+                       tab->t2_pos, tab->t2_rows, tab->t1_rows, tab->t2_steiner, tab->t3_dec, keys, rec, rows_by_sweep);
   else if (AT == 2)
     hipLaunchKernelGGL((t12_kernel<2, LOAD>), g, dim3(kThreads), 0, s, xb, src, sigma, apr, n_atoms, tab->t2_tiles,
-                       tab->t2_pos, tab->t2_rows, tab->t1_rows, tab->t2_steiner, tab->t3_dec, keys, rows_by_sweep);
+                       tab->t2_pos, tab->t2_rows, tab->t1_rows, tab->t2_steiner, tab->t3_dec, keys, rec, rows_by_sweep);
   else
     hipLaunchKernelGGL((t12_kernel<1, LOAD>), g, dim3(kThreads), 0, s, xb, src, sigma, apr, n_atoms, tab->t2_tiles,
-                       tab->t2_pos, tab->t2_rows, tab->t1_rows, tab->t2_steiner, tab->t3_dec, keys, rows_by_sweep);
+                       tab->t2_pos, tab->t2_rows, tab->t1_rows, tab->t2_steiner, tab->t3_dec, keys, rec, rows_by_sweep);
   profile_after(s, PLX_PROF_T12);
   return check_launch("t12_kernel");
 }
@@ -2113,11 +2117,12 @@ int t12_launch_load(uint4 *xb, const float *src, const float *sigma, int64_t apr
 // scorers, so the keys need no clearing.
 template <int LOAD>
 int structured_launch(uint4 *xb, const float *src, const float *sigma, int64_t apr, int64_t n_atoms,
-                      const DeviceTables *tab, uint4 *keys, int32_t *idx_out, uint8_t *packed_out, hipStream_t s,
-                      int rows_by_sweep) {
+                      const DeviceTables *tab, uint4 *keys, uint2 *rec, int32_t *idx_out, uint8_t *packed_out,
+                      hipStream_t s, int rows_by_sweep) {
   int st;
-  if ((st = t12_launch_load<LOAD>(xb, src, sigma, apr, n_atoms, tab, keys, s, rows_by_sweep)) != PLX_OK) return st;
-  if ((st = t3_launch(xb, n_atoms, tab, keys, s, rows_by_sweep)) != PLX_OK) return st;
+  if ((st = t12_launch_load<LOAD>(xb, src, sigma, apr, n_atoms, tab, keys, rec, s, rows_by_sweep)) != PLX_OK)
+    return st;
+  if ((st = t3_launch(xb, n_atoms, tab, keys, rec, s, rows_by_sweep)) != PLX_OK) return st;
   hipLaunchKernelGGL(pick_kernel, dim3(static_cast<unsigned>((n_atoms + 255) / 256)), dim3(256), 0, s, keys, n_atoms,
                      idx_out, packed_out);
   return check_launch("pick_kernel");
@@ -2140,7 +2145,8 @@ int launch_mode(const float *x, const float *sigma, int64_t apr, int64_t n_atoms
   uint4 *xb = reinterpret_cast<uint4 *>(workspace + keys_bytes(n_atoms) + recs_bytes(n_atoms));
   const int s0 = first_pair_slice(n_slices);
   if constexpr (STRUCT)
-    return structured_launch<FUSED ? 2 : 1>(xb, x, sigma, apr, n_atoms, tab, keys, idx_out, packed_out, s, rows_by_sweep);
+    return structured_launch<FUSED ? 2 : 1>(xb, x, sigma, apr, n_atoms, tab, keys, reinterpret_cast<uint2 *>(recs),
+                                            idx_out, packed_out, s, rows_by_sweep);
   int st;
   if (MODE != kModeP) {
     hipLaunchKernelGGL((prep_kernel<FUSED>), dim3(static_cast<unsigned>((n_atoms * 3 + 255) / 256)), dim3(256), 0, s, x,
@@ -2261,8 +2267,10 @@ int launch_batch_mode(const RequantItem *items, int n_items, const DeviceTables 
     off += n;
   }
   if constexpr (STRUCT) {
-    if ((st = t12_launch_load<0>(xb, nullptr, nullptr, 1, total, tab, keys, s, 0)) != PLX_OK) return st;
-    if ((st = t3_launch(xb, total, tab, keys, s, 0)) != PLX_OK) return st;
+    if ((st = t12_launch_load<0>(xb, nullptr, nullptr, 1, total, tab, keys, reinterpret_cast<uint2 *>(recs), s, 0)) !=
+        PLX_OK)
+      return st;
+    if ((st = t3_launch(xb, total, tab, keys, reinterpret_cast<const uint2 *>(recs), s, 0)) != PLX_OK) return st;
   } else {
     profile_before(s);
     hipLaunchKernelGGL((nn_kernel<MODE>), dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0, s,
