@@ -746,7 +746,7 @@ __global__ __launch_bounds__(kThreads, 4) void t3_kernel(const uint4 *__restrict
       const uint32_t ce = act ? cand[wave][cnt + lane] : 0u;
       const uint32_t mask = (ce >> 16) & 0xFu;
       uint32_t back = 0u;  // the entry as it goes back on the list (0: done)
-      if (act) {
+      if (act && mask != 0u) {  // (every appended entry has an output bit; the test keeps rep in the table)
         const int al = static_cast<int>(ce & 0x7Fu);
         const uint32_t rep = ((ce >> 7) & 0x7Fu) * kTileCodes + 4 * ((ce >> 14) & 3u) +
                              static_cast<uint32_t>(__builtin_ctz(mask));
@@ -849,14 +849,18 @@ __global__ __launch_bounds__(kThreads, 4) void t3_kernel(const uint4 *__restrict
         c[at] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b[at], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
 #pragma unroll
       for (int at = 0; at < AT; ++at) {
-        // each output's |T| against the atom's threshold (a word and its complement: one test), as four
-        // compares whose wave masks are OR'ed (no max over the outputs)
-        const bool h0 = fabsf(c[at][0]) >= thr[at], h1 = fabsf(c[at][1]) >= thr[at];
-        const bool h2 = fabsf(c[at][2]) >= thr[at], h3 = fabsf(c[at][3]) >= thr[at];
-        const uint64_t msk = __ballot(h0) | __ballot(h1) | __ballot(h2) | __ballot(h3);
+        // each output's |T| against the atom's threshold (a word and its complement: one test): the
+        // largest of the four against it, one compare and one wave mask; the four compares only on a hit
+        // (IEEE maximum, v_maximum3_f32: a NaN output, only a non-finite atom's, makes the step a miss)
+        const float mx = __builtin_elementwise_maximum(__builtin_elementwise_maximum(fabsf(c[at][0]), fabsf(c[at][1])),
+                                                       __builtin_elementwise_maximum(fabsf(c[at][2]), fabsf(c[at][3])));
+        const bool hit = mx >= thr[at];
+        const uint64_t msk = __ballot(hit);
         if (msk == 0ull) continue;
         if (cnt > kT3Cap - 64) flush(pass);
-        if (h0 | h1 | h2 | h3) {  // (the compares' own lane masks: no per-lane test of msk)
+        if (hit) {
+          const bool h0 = fabsf(c[at][0]) >= thr[at], h1 = fabsf(c[at][1]) >= thr[at];
+          const bool h2 = fabsf(c[at][2]) >= thr[at], h3 = fabsf(c[at][3]) >= thr[at];
           const uint32_t mask = (h0 ? 1u : 0u) | (h1 ? 2u : 0u) | (h2 ? 4u : 0u) | (h3 ? 8u : 0u);
           const uint32_t pos = static_cast<uint32_t>(cnt) +
                                __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(msk >> 32),
@@ -1397,13 +1401,18 @@ __global__ __launch_bounds__(kThreads, 4) void t12_kernel(uint4 *__restrict__ xb
         c[at] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b[at], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
 #pragma unroll
       for (int at = 0; at < AT; ++at) {
-        // each output against the atom's threshold, four compares whose wave masks are OR'ed
-        const bool h0 = c[at][0] >= thr[at], h1 = c[at][1] >= thr[at];
-        const bool h2 = c[at][2] >= thr[at], h3 = c[at][3] >= thr[at];
-        const uint64_t msk = __ballot(h0) | __ballot(h1) | __ballot(h2) | __ballot(h3);
+        // each output against the atom's threshold: the largest of the four against it, one compare and
+        // one wave mask; the four compares only on a hit
+        // (IEEE maximum, v_maximum3_f32: a NaN output, only a non-finite atom's, makes the step a miss)
+        const float mx = __builtin_elementwise_maximum(__builtin_elementwise_maximum(c[at][0], c[at][1]),
+                                                       __builtin_elementwise_maximum(c[at][2], c[at][3]));
+        const bool hit = mx >= thr[at];
+        const uint64_t msk = __ballot(hit);
         if (msk == 0ull) continue;
         if (cnt > kT2Cap - 64) flush(pass);
-        if (h0 | h1 | h2 | h3) {  // (the compares' own lane masks: no per-lane test of msk)
+        if (hit) {
+          const bool h0 = c[at][0] >= thr[at], h1 = c[at][1] >= thr[at];
+          const bool h2 = c[at][2] >= thr[at], h3 = c[at][3] >= thr[at];
           const uint32_t mask = (h0 ? 1u : 0u) | (h1 ? 2u : 0u) | (h2 ? 4u : 0u) | (h3 ? 8u : 0u);
           const uint32_t pos = static_cast<uint32_t>(cnt) +
                                __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(msk >> 32),
