@@ -1180,7 +1180,9 @@ __global__ __launch_bounds__(kThreads, 4) void t12_kernel(uint4 *__restrict__ xb
   // One flagged octad per lane per round (the list is worked as a stack: an entry with flagged octads left
   // goes back on it).  pass 1: the octad's best code -> st_m (atomic max), and the octad onto the survivor
   // list when it is at or above the atom's running best; pass 2: the lowest row at st_m -> st_r.
+  bool flushed = false;  // (wave-uniform) a flush ran since the last compaction
   auto flush = [&](int pass) {
+    flushed |= cnt > 0;
     while (cnt > 0) {  // (wave-uniform)
       const int n = min(cnt, 64);
       cnt -= n;
@@ -1422,10 +1424,13 @@ __global__ __launch_bounds__(kThreads, 4) void t12_kernel(uint4 *__restrict__ xb
         cnt += __popcll(msk);
       }
     }
-    // the list is evaluated once it fills a round of lanes, and at the end of each pass
-    if (cnt >= 64 || g == kT2Stages - 1 || g == 2 * kT2Stages - 1) flush(pass);
-    if (pass == 1) {
+    // the list is evaluated when it is nearly full (in the tile loop) and at the end of each pass (with the
+    // type-3 floor, evaluating at stage ends once 64 entries were listed measured 4% slower); the best
+    // buckets change only then, so the survivors are compacted and the thresholds raised only after one
+    if (g == kT2Stages - 1 || g == 2 * kT2Stages - 1) flush(pass);
+    if (pass == 1 && flushed) {
       compact();
+      flushed = false;
 #pragma unroll
       for (int at = 0; at < AT; ++at) set_thr(at, max(st_m[wave][at * 16 + j], st_f[wave][at * 16 + j]));
     }
@@ -1440,7 +1445,8 @@ __global__ __launch_bounds__(kThreads, 4) void t12_kernel(uint4 *__restrict__ xb
     }
   }
   {
-    // the survivors are the octads at their atom's final best bucket (compacted at the last stage end);
+    // the survivors are the octads at their atom's final best bucket (compacted after the last flush; a
+    // set-up octad left below it has no code at the final bucket, so it gives no row);
     // pass 2 gave the rows of the atoms whose list lost entries
     const int ns = static_cast<int>(min(surv_n[wave], static_cast<uint32_t>(kT2Surv)));
     for (int i = lane; i < ns; i += 64) {
