@@ -8,7 +8,9 @@ candidate threshold falls to zero or below, so both signs of a word are
 listed), near-origin and zero atoms, ragged small launches, atoms whose
 best code sits in the type-3 family by construction (scaled type-3 codes plus
 noise), and integer atoms, whose scores are exact in any summation order, so
-both paths must agree on every atom through the exact ties between codes.
+both paths must agree on every atom through the exact ties between codes --
+among them sums of a type-3 and a type-2 code that tie at the best bucket, so
+that t12_kernel's type-3 floor meets its best pair bucket.
 """
 
 import numpy as np
@@ -186,3 +188,37 @@ def test_non_finite_atoms_go_to_the_origin(dev):
     keep = torch.ones(5000, dtype=torch.bool)
     keep[bad] = False
     assert torch.equal(s[keep], ref[keep])
+
+
+def test_pair_and_type3_ties(dev):
+    # x = c2 + c3 for a type-3 code c3 and a type-2 code c2 of largest c2.c3 (integer units): both codes
+    # score 32 + c2.c3, exactly in any summation order, so the best bucket usually holds both families and
+    # the answer is the lower row.  t12_kernel's Chase-decoded type-3 floor then equals its best pair
+    # bucket (the pair row must survive the tie) or exceeds it (the pair key carries the floor without a
+    # row); every atom must match the dense path and, where determined, the oracle
+    rng = np.random.default_rng(17)
+    raw = cb.codebook_int8().astype(np.float32)
+    nz = (raw != 0).sum(1)
+    t2 = np.nonzero(nz == 8)[0]
+    t3 = np.nonzero(nz == 24)[0]
+    c3 = rng.choice(t3, 3000)
+    c2 = np.empty_like(c3)
+    for k in range(0, len(c3), 250):
+        dots = raw[c3[k:k + 250]] @ raw[t2].T  # exact small integers
+        best = dots.max(1, keepdims=True)
+        for i, row in enumerate(dots == best):
+            c2[k + i] = t2[rng.choice(np.nonzero(row)[0])]
+    x = torch.from_numpy(raw[c2] + raw[c3])
+    xs = x.to(dev)
+    s = castor.quantize_indices(xs, mode="bf16").long().cpu()
+    d = castor.quantize_indices(xs, mode="bf16-dense").long().cpu()
+    assert torch.equal(s, d), int((s != d).sum())
+    # (the oracle on a sample: every answer is the lower of the two rows, c2 and c3 about equally often;
+    # a third code at the same bucket could take a few atoms)
+    lower = (s.numpy() == np.minimum(c2, c3)).mean()
+    print(f"[t3 pair/type-3 ties] {len(x)} atoms: answer is the lower of the two rows on {lower:.3f}", flush=True)
+    assert lower >= 0.99 and 0.3 < (s.numpy() == c2).mean() < 0.7
+    sub = np.arange(0, len(x), 5)
+    o = nn.quantize(x[sub].numpy(), "B")
+    ok = ~o["near_tie"]
+    assert np.array_equal(s[sub].numpy()[ok], o["idx"][ok])
