@@ -944,18 +944,19 @@ __global__ __launch_bounds__(kThreads, 4) void t3_kernel(const uint4 *__restrict
 //           and the one holding its 4 largest and 6th largest (every 5
 //           positions lie in exactly one octad, t2_steiner): usually at or
 //           near the atom's best octad, so the sweep starts from a high floor
-//           (~3 octads evaluated per atom instead of ~24);
+//           (~3 octads evaluated per atom instead of ~24); it also decodes a
+//           type-3 floor F3 (Chase decoding, t3_dec) and makes t3_kernel's
+//           per-atom set-up record (T3Setup);
 //   sweep   every lane whose outputs hold an octad with U >= lo(floor) - margin
 //           appends one 4-byte entry (atom, tile, quarter, output mask) to the
 //           wave's list; floor is the highest of 2.0 (the origin rule), the
-//           atom's best type-1 bucket and the best octad bucket found so far
-//           (raised at every stage end).  At a stage end once the list holds a
-//           round of 64 entries, when it is full and at the end of the pass the
+//           atom's best type-1 bucket, F3 and the best octad bucket found so
+//           far.  When the list is nearly full and at the end of the pass the
 //           wave evaluates it, one flagged octad per lane per round: the
 //           octads' best codes scored exactly, the best bucket per atom kept by
 //           an LDS atomic max, octads at or above the running best onto a
-//           survivor list, which every stage end compacts to the octads at
-//           their atom's current best;
+//           survivor list, which is compacted to the octads at their atom's
+//           current best (and the thresholds raised) at the next stage end;
 //   rows    the survivors at the final best bucket M give every type-2 code at
 //           M: the flip sets F of the positions whose 2 c2 |x_i| fits in
 //           U - lo(M) are enumerated and scored exactly; type 1 the same way
@@ -964,8 +965,9 @@ __global__ __launch_bounds__(kThreads, 4) void t3_kernel(const uint4 *__restrict
 //   pass 2  (only after a survivor list lost entries) the rows of the atoms
 //           whose entries were lost, from a second sweep with their
 //           thresholds at M (the other atoms' thresholds: +inf).
-// The atom's key gets (M << 16, lowest row at M) in its upper 8 bytes, or 0
-// when no type-1/2 code reaches 2.0; t3_kernel takes M as its floor.
+// The atom's key gets (M << 16, lowest row at M) in its upper 8 bytes, or
+// (F3 << 16, no row) when F3 is above M, or 0 when neither reaches 2.0;
+// t3_kernel takes that bucket as its floor.
 // Buckets are taken by round-half-up like the dense sweep's, every score is
 // an fp32 sum of exact products in ascending position order, so the answer
 // equals the exact-score answer off near-ties (oracle/nn.py).
