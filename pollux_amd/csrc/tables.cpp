@@ -278,22 +278,22 @@ int build(int dev, DeviceTables *t) {
   }
   std::vector<uint32_t> t3_dec(static_cast<size_t>(kT3DecWords), 0xFFFFFFFFu);
   {
-    // basis: the first 12 words, in table order, independent of those before them
+    // basis: the first 12 words, in table order, independent of those before them (GF(2) elimination:
+    // piv[b] holds a reduced word whose leading bit is b)
     const uint32_t *golay = golay_words_host();
-    uint32_t basis[12];
+    uint32_t basis[12], piv[kDim] = {};
     int nb = 0;
-    std::vector<uint8_t> span(1u << 24, 0);
-    std::vector<uint32_t> members{0u};
-    span[0] = 1;
     for (int m = 0; m < 4096 && nb < 12; ++m) {
-      const uint32_t w = golay[m];
-      if (span[w]) continue;
-      basis[nb++] = w;
-      const size_t k = members.size();
-      for (size_t i = 0; i < k; ++i) {
-        members.push_back(members[i] ^ w);
-        span[members[i] ^ w] = 1;
-      }
+      uint32_t r = golay[m];
+      for (int b = kDim - 1; b >= 0 && r != 0u; --b)
+        if (((r >> b) & 1u) != 0u) {
+          if (piv[b] == 0u) {
+            piv[b] = r;
+            basis[nb++] = golay[m];
+            break;
+          }
+          r ^= piv[b];
+        }
     }
     if (nb != 12) return fail(PLX_EINVAL, "Golay basis of %d words", nb);
     auto syndrome = [&](uint32_t e) {
