@@ -841,6 +841,8 @@ __global__ __launch_bounds__(kThreads, 4) void t3_kernel(const uint4 *__restrict
     }
     const uint8_t *L = stg[buf] + a_off;
     const int tile0 = (g % kT3Stages) * kT3ST;
+    // (unrolled: the A tiles' LDS offsets and the entries' tile bits become constants; 3.83 -> 3.75 ms)
+#pragma unroll 8
     for (int k = 0; k < kT3ST; ++k) {
       const bf16x8 a = *reinterpret_cast<const bf16x8 *>(L + k * kTileBytes);
       f32x4 c[AT];
@@ -1397,6 +1399,8 @@ __global__ __launch_bounds__(kThreads, 4) void t12_kernel(uint4 *__restrict__ xb
     }
     const uint8_t *L = stg[buf] + a_off;
     const int tile0 = (g % kT2Stages) * kT2ST;
+    // (unrolled: the A tiles' LDS offsets and the entries' tile bits become constants; 2.71 -> 2.65 ms)
+#pragma unroll 8
     for (int k = 0; k < kT2ST; ++k) {
       const bf16x8 a = *reinterpret_cast<const bf16x8 *>(L + k * kTileBytes);
       f32x4 c[AT];
