@@ -46,7 +46,8 @@ def _compare(dev, x, label, max_near=0.002):
     return got
 
 
-@pytest.mark.parametrize("n", [1000, 40_000, 140_000, 300_000])
+# (the scorers take 1 atom tile per wave below 98,304 atoms, 2 below 131,072, else 4)
+@pytest.mark.parametrize("n", [1000, 40_000, 98_304, 131_071, 140_000, 300_000])
 def test_structured_equals_dense_c4(dev, n):
     _compare(dev, _c4_atoms(n, n), f"c4 n={n}")
 
