@@ -738,7 +738,9 @@ __global__ __launch_bounds__(kThreads, 4) void t3_kernel(const uint4 *__restrict
   // goes back on it, so every lane is busy while 64 or more words are listed.
   // pass 1: the best bucket of each word -> st_m (atomic max), and the word onto the survivor list when it
   //         is at or above the atom's running best; pass 2: the lowest row at the atom's st_m -> st_r.
+  bool flushed = false;  // (wave-uniform) a flush ran since the thresholds were last set
   auto flush = [&](int pass) {
+    flushed |= cnt > 0;
     while (cnt > 0) {  // (wave-uniform)
       const int n = min(cnt, 64);
       cnt -= n;
@@ -877,8 +879,10 @@ __global__ __launch_bounds__(kThreads, 4) void t3_kernel(const uint4 *__restrict
     // lanes busy and the block's waves in step at the barriers (4.93 -> 4.64 ms against a flush at
     // every stage end holding 64 entries, config 4)
     if (g == kT3Stages - 1 || g == 2 * kT3Stages - 1) flush(pass);
-    if (pass == 1) {
-      // the thresholds rise with the best buckets found so far (this wave's own atoms: no barrier needed)
+    if (pass == 1 && flushed) {
+      // the thresholds rise with the best buckets found so far (this wave's own atoms: no barrier needed);
+      // the buckets change only in a flush
+      flushed = false;
 #pragma unroll
       for (int at = 0; at < AT; ++at) set_thr(at, st_m[wave][at * 16 + j]);
     }
