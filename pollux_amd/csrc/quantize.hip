@@ -552,11 +552,11 @@ __global__ __launch_bounds__(kThreads, MODE == kModeB ? 3 : 2) void nn_kernel(co
 // Buckets are taken by round-half-up like the dense sweep's, and every score
 // is an fp32 sum of exact products plus one rounding for the bonus, so the
 // answer equals the exact-score answer off near-ties (oracle/nn.py).
-constexpr int kT3ST = 8;                           // pattern tiles per LDS stage
+constexpr int kT3ST = 16;                          // pattern tiles per LDS stage (8: 3.47 -> 3.39 ms)
 constexpr int kT3Stages = kT3Tiles / kT3ST;        // 8 per pass
-constexpr int kT3StageBytes = kT3ST * kTileBytes;  // 6,144
-constexpr int kT3StageVecs = kT3StageBytes / 16;   // 384
-constexpr int kT3Cap = 256;                        // candidate entries per wave (4 bytes each)
+constexpr int kT3StageBytes = kT3ST * kTileBytes;  // 12,288
+constexpr int kT3StageVecs = kT3StageBytes / 16;   // 768
+constexpr int kT3Cap = 200;                        // candidate entries per wave (4 bytes each)
 constexpr int kT3Surv = 384;                       // survivor words per wave (4 bytes each)
 constexpr float kT3Alpha = 1.416015625f;           // bf16(3s) + bf16(s)
 constexpr float kT3Beta = 0.708984375f;            // bf16(3s) - bf16(s)
@@ -639,7 +639,7 @@ __global__ __launch_bounds__(kThreads, 4) void t3_kernel(const uint4 *__restrict
   __shared__ __align__(16) uint8_t stg[2][kT3StageBytes];
   __shared__ uint32_t cand[kWaves][kT3Cap];  // atom | tile << 7 | quarter << 14 | output mask << 16 | done << 20
   __shared__ uint32_t surv[kWaves][kT3Surv];  // atom | pattern id << 7: words at or above the atom's running best
-  __shared__ __align__(16) uint32_t xw[kWaves][NA][12];  // the atoms' bf16 coordinates (pairs)
+  __shared__ uint32_t st_x[kWaves][NA];  // x at p1 | x at p2 << 16 (bf16 bits)
   __shared__ uint32_t st_m[kWaves][NA], st_r[kWaves][NA];
   __shared__ float st_t[kWaves][NA];    // lo(floor) less twice the margin: which signs of a word to evaluate
   __shared__ float st_m3[kWaves][NA];   // the third largest position term (the largest off p1, p2)
@@ -660,7 +660,6 @@ __global__ __launch_bounds__(kThreads, 4) void t3_kernel(const uint4 *__restrict
     const int64_t a = wave_atom0 + at * 16 + j;
     uint4 w = make_uint4(0u, 0u, 0u, 0u);
     if (a < n_atoms && q < 3) w = xb[a * 3 + q];
-    if (q < 3) *reinterpret_cast<uint4 *>(&xw[wave][at * 16 + j][4 * q]) = w;
     // The atom's set-up record from t12_kernel (T3Setup: positions p1, p2 of the two largest
     // position terms, their raised bf16 coordinates, the third largest term m3, eb + dl and the margin);
     // an atom past the end: the record of a zero atom (p1 = 0, p2 = 1, the rest 0)
@@ -678,8 +677,11 @@ __global__ __launch_bounds__(kThreads, 4) void t3_kernel(const uint4 *__restrict
         const uint32_t e = pr & 7u;
 #pragma unroll
         for (int k = 0; k < 4; ++k)
-          if (static_cast<uint32_t>(k) == (e >> 1))
+          if (static_cast<uint32_t>(k) == (e >> 1)) {
+            reinterpret_cast<uint16_t *>(&st_x[wave][at * 16 + j])[r] =
+                static_cast<uint16_t>((e & 1u) ? ww[k] >> 16 : ww[k] & 0xFFFFu);
             ww[k] = (e & 1u) ? (ww[k] & 0xFFFFu) | (h << 16) : (ww[k] & 0xFFFF0000u) | h;
+          }
       }
     }
     b[at] = __builtin_bit_cast(bf16x8, make_uint4(ww[0], ww[1], ww[2], ww[3]));
@@ -752,14 +754,15 @@ __global__ __launch_bounds__(kThreads, 4) void t3_kernel(const uint4 *__restrict
         const int al = static_cast<int>(ce & 0x7Fu);
         const uint32_t rep = ((ce >> 7) & 0x7Fu) * kTileCodes + 4 * ((ce >> 14) & 3u) +
                              static_cast<uint32_t>(__builtin_ctz(mask));
-        const uint32_t *xr = xw[wave][al];
+        // (the atom's coordinates from its bf16 planes in global memory; an entry's atom is in range)
+        const uint32_t *xr = reinterpret_cast<const uint32_t *>(xb + min(wave_atom0 + al, n_atoms - 1) * 3);
         const float tlo = st_t[wave][al];
         // the bound on the bonus of a word by its bits at p1, p2 (as at set-up)
         const uint32_t pa = st_p[wave][al][0], pb = st_p[wave][al][1];
         const float m3v = st_m3[wave][al];
-        const uint16_t *xh = reinterpret_cast<const uint16_t *>(xr);
-        const float xa1 = __uint_as_float(static_cast<uint32_t>(xh[pa]) << 16);
-        const float xa2 = __uint_as_float(static_cast<uint32_t>(xh[pb]) << 16);
+        const uint32_t xab = st_x[wave][al];
+        const float xa1 = __uint_as_float(xab << 16);
+        const float xa2 = __uint_as_float(xab & 0xFFFF0000u);
         const uint32_t wr = t3_words[rep];
         const float D = t3_dot(xr, wr);
         const uint32_t ba = (wr >> pa) & 1u, bb = (wr >> pb) & 1u;
@@ -843,7 +846,8 @@ __global__ __launch_bounds__(kThreads, 4) void t3_kernel(const uint4 *__restrict
     }
     const uint8_t *L = stg[buf] + a_off;
     const int tile0 = (g % kT3Stages) * kT3ST;
-    // (unrolled: the A tiles' LDS offsets and the entries' tile bits become constants; 3.83 -> 3.75 ms)
+    // (unrolled by 8: the A tiles' LDS offsets and the entries' tile bits become constants; 3.83 -> 3.75
+    // ms with 8-tile stages)
 #pragma unroll 8
     for (int k = 0; k < kT3ST; ++k) {
       const bf16x8 a = *reinterpret_cast<const bf16x8 *>(L + k * kTileBytes);
@@ -908,7 +912,7 @@ __global__ __launch_bounds__(kThreads, 4) void t3_kernel(const uint4 *__restrict
       if (rows_by_sweep != 0 || ((st_ovf[wave][al >> 5] >> (al & 31)) & 1u) != 0u) continue;
       const uint32_t wid = se >> 7;
       const uint32_t M = st_m[wave][al];
-      const uint32_t *xr = xw[wave][al];
+      const uint32_t *xr = reinterpret_cast<const uint32_t *>(xb + min(wave_atom0 + al, n_atoms - 1) * 3);
       const uint32_t wr = t3_words[wid & (kT3Reps - 1)];
       const int sg = wid >= static_cast<uint32_t>(kT3Reps) ? 1 : 0;
       const float D = t3_dot(xr, wr);
@@ -2092,9 +2096,10 @@ int t3_launch(const uint4 *xb, int64_t n_atoms, const DeviceTables *tab, uint4 *
               hipStream_t s, int rows_by_sweep) {
   // 4 atom tiles per wave from 131,072 atoms, 2 from 98,304, else 1 (measured per launch size: 55,296
   // atoms take 35 + 42 us in t12 + t3 at 1 tile, 39 + 47 at 2; from 165,888 atoms 4 tiles are fastest).
-  // At 4 tiles: 40 KB of LDS (8-tile stages) and 128 VGPRs, 4 blocks (16 waves) per CU, which the
+  // At 4 tiles: 40 KB of LDS (16-tile stages) and 128 VGPRs, 4 blocks (16 waves) per CU, which the
   // kernel's stalls need (8 tiles per wave at 2 blocks per CU was 30% slower); the representative words
-  // are read from global memory (L1 / L2) to leave the LDS to the stages and lists.
+  // and, when a list is worked, the atoms' coordinates are read from global memory (L1 / L2) to leave
+  // the LDS to the stages and lists.
   const int AT = n_atoms >= 131072 ? 4 : n_atoms >= 98304 ? 2 : 1;
   const int64_t per_block = static_cast<int64_t>(kWaves) * AT * 16;
   const int64_t blocks = (n_atoms + per_block - 1) / per_block;
