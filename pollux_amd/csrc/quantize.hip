@@ -716,7 +716,9 @@ __global__ __launch_bounds__(kThreads, 4) void t3_kernel(const uint4 *__restrict
 #pragma unroll
     for (int i = 0; i < (kT3StageVecs + kThreads - 1) / kThreads; ++i) {
       if (i * kThreads + wave * 64 >= kT3StageVecs) break;  // (wave-uniform)
-      const uint4 *src = gsrc + static_cast<size_t>(stage) * kT3StageVecs + i * kThreads + tid;
+      int off = i * kThreads + tid;
+      asm volatile("" : "+v"(off));  // (computed here: a per-thread pointer kept across the loop spills)
+      const uint4 *src = gsrc + static_cast<size_t>(stage) * kT3StageVecs + off;
       uint8_t *d = stg[dst] + (i * kThreads + wave * 64) * 16;
       __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)(src),
                                        (__attribute__((address_space(3))) void *)(d), 16, 0, 0);
